@@ -1,0 +1,184 @@
+"""Benchmark of the MI355X PAM hot path (one JSON line on stdout).
+
+Workload ("config 2"): PAM chunked dual-form
+prefill forward, fp32 complex planar, B=8, T=2048, H=12, d=64, C=64.  A step
+is one scan forward over the whole batch (16384 tokens); `value` is tokens/s
+with inputs resident in HBM.  `roofline` covers the dominant kernel (the
+chunk-output MFMA kernel), timed live with HIP events recorded by the library
+on the launch stream around that kernel, against the fp32 MFMA peak.
+
+Secondary measurements (same line, under "extras"): config 4 ragged decode
+(256 slots, ~75% active, 1000 steps) in tokens/s and HBM GB/s; more configs
+as their kernels land.  `cpu_baseline` times the CPU restatement of the
+reference's chunk loop (oracle/pam.py: chunked_head) on a bounded sample of
+the same workload on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
+"""
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_FP32_PEAK = 157.3e12
+MFMA_BF16_PEAK = 2516.6e12
+HBM_PEAK = 8.0e12
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-steps", type=int, default=1000)
+    return ap.parse_args()
+
+
+def scan_inputs(B, H, T, d, M, seed, dtype, unit_qk=True, mu=3.0, mu_step=0.0):
+    import torch
+    from oracle.pam import make_scan_inputs
+    q, k, v, gamma = make_scan_inputs(B, H, T, d, seed, m_states=M, unit_qk=unit_qk, gamma_mu=mu,
+                                      gamma_mu_step=mu_step, dtype=torch.float32)
+    dev = torch.device("cuda")
+
+    def planes(x):
+        return x[..., 0].contiguous().to(dtype).to(dev), x[..., 1].contiguous().to(dtype).to(dev)
+
+    return planes(q), planes(k), planes(v), gamma.to(dev)
+
+
+def bench_scan_fwd(steps, warmup):
+    """Config 2: fp32 scan forward.  Returns (ms_per_step, kernel_ms, tokens)."""
+    import torch
+    from qllm2_amd import _lib, pam_scan
+    from oracle.pam import scan_flops
+    B, H, T, d, C = 8, 12, 2048, 64, 64
+    (qr, qi), (kr, ki), (vr, vi), gamma = scan_inputs(B, H, T, d, 1, 1002, torch.float32)
+
+    def step():
+        return pam_scan.scan_fwd_op(qr, qi, kr, ki, vr, vi, gamma, None, None, None, None, d ** -0.5, C)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    pairs = [_lib.EventPair() for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        pam_scan.set_profile_events(pairs[i])
+        step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    kms = statistics.mean(p.elapsed_ms() for p in pairs)
+    # dominant kernel algorithmic FLOPs: score + intra read + carried read (3 of the 4
+    # per-chunk complex GEMMs; the state write runs in chunk_state_kernel), carried
+    # read skipped on chunk 0
+    n = math.ceil(T / C)
+    kflops = B * H * (n * (8 * C * C * d * 2) + (n - 1) * 8 * C * d * d)
+    return dt * 1e3, kms, B * T, scan_flops(B, H, T, d, C), kflops
+
+
+def bench_decode(n_steps):
+    """Config 4: ragged decode over 256 slots x 16 layers x 12 heads, d=64."""
+    import torch
+    from qllm2_amd.decode import decode_step
+    S, L, H, d = 256, 16, 12, 64
+    G = L * H
+    dev = torch.device("cuda")
+    gen = torch.Generator().manual_seed(1004)
+    state = torch.empty(S, G, 1, d, d, 2, device=dev)
+    for sl in range(0, S, 32):  # fill in pieces to bound host memory
+        state[sl:sl + 32] = (torch.randn(32, G, 1, d, d, 2, generator=gen) * 0.01).to(dev)
+    q, k, v = (torch.randn(S, G, d, 2, generator=gen).to(dev) for _ in range(3))
+    gamma = torch.sigmoid(torch.randn(S, G, 1, generator=gen) + 3).to(dev)
+    masks = [torch.nonzero(torch.rand(S, generator=gen) < 0.75).flatten().to(torch.int32).to(dev)
+             for _ in range(16)]
+    counts = [int(m.numel()) for m in masks]
+    y = torch.zeros_like(q)
+    for i in range(20):
+        decode_step(state, q, k, v, gamma, active=masks[i % 16], q_scale=d ** -0.5, out=y)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(n_steps):
+        decode_step(state, q, k, v, gamma, active=masks[i % 16], q_scale=d ** -0.5, out=y)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n_steps
+    active = sum(counts[i % 16] for i in range(n_steps)) / n_steps
+    bytes_step = active * G * (2 * 32768 + 4 * 512 + 4)
+    return {"ms_per_step": ms, "tokens_per_s": active / (ms * 1e-3), "active_slots": active,
+            "hbm_GBps": bytes_step / (ms * 1e-3) / 1e9, "hbm_frac": bytes_step / (ms * 1e-3) / HBM_PEAK,
+            "bytes_per_step": bytes_step, "steps": n_steps}
+
+
+def cpu_baseline_scan():
+    """The reference's chunk loop restated on the CPU (oracle.pam.chunked_head),
+    fp32, on a bounded sample: 1 of the 8 batch rows (H=12, T=2048)."""
+    import torch
+    from oracle.pam import chunked_head, make_scan_inputs
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    q, k, v, gamma = make_scan_inputs(1, 12, 2048, 64, 1002, unit_qk=True, dtype=torch.float32)
+    chunked_head(q, k, v, gamma[0], 64, 64)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        chunked_head(q, k, v, gamma[0], 64, 64)
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    return {"value": 2048 / t, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": "oracle.pam.chunked_head fp32, B=1 of 8 (H=12, T=2048, d=64, C=64), median of 3"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every box has one GPU); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    ms, kms, tokens, flops, kflops = bench_scan_fwd(args.steps, args.warmup)
+    value = tokens / (ms * 1e-3)
+    achieved = kflops / (kms * 1e-3)
+    out = {
+        "metric": "PAM prefill tokens/s (config 2: chunked dual-form scan fwd, fp32)",
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic (seeded CPU draws, BASELINE.json config 2)",
+        "config": {"workload": "pam_scan_fwd config 2", "B": 8, "T": 2048, "H": 12, "d": 64, "C": 64,
+                   "layout": "planar re/im fp32"},
+        "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": MFMA_FP32_PEAK / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved / MFMA_FP32_PEAK, "traffic": None,
+                     "kernel": "chunk_output_kernel<float,64>", "kernel_ms": kms,
+                     "kernel_flops": kflops},
+        "scan_fwd_total": {"flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
+                           "mfma_fp32_frac": flops / (ms * 1e-3) / MFMA_FP32_PEAK},
+    }
+    if not args.no_extras:
+        out["extras"] = {"decode_config4": bench_decode(args.decode_steps)}
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline_scan()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,222 @@
+/*
+ * qpam.h -- C ABI of the MI355X (gfx950) Phase-Associative-Memory hot path.
+ *
+ * Plain C: POD argument structs of dimensions, strides (in elements) and
+ * device pointers; every entry point launches asynchronously on the HIP
+ * stream passed as `stream` (NULL = the null stream), performs no host
+ * synchronisation, allocates no device memory (the caller owns every buffer,
+ * workspaces included) and returns a qpam_status.  qpam_last_error() returns a
+ * thread-local message for the last non-zero status on the calling thread.
+ *
+ * Complex tensors are planar: separate real and imaginary planes that share
+ * one set of strides, innermost axis contiguous.  The decode state is the one
+ * exception: it keeps the reference's interleaved [..., d, d, 2] layout so the
+ * decode drop-in needs no conversion.
+ *
+ * Reference interfaces replaced (paths relative to gowrav-vishwakarma/qllm2):
+ *   qpam_decode_step    v11/model.py:927-965  V11PAMLayer._recur_step_additive
+ *                       v11/model.py:845-925  V11PAMLayer._recurrent (token
+ *                       step over K states with the e^{i phi} rotation)
+ *   qpam_scan_fwd       v11/model.py:378-417  _forward_chunked_head,
+ *                       v11/model.py:354-376  _dual_form_block (T <= C),
+ *                       v11/flash_pam.py:56-152 flash_pam_chunked_head,
+ *                       v11/model.py:657-781  _fused_chunk_step /
+ *                                             _forward_multistate_fused
+ *   qpam_scan_bwd       the autograd backward of the same functions (the
+ *                       reference differentiates them with torch autograd and
+ *                       v11/triton_kernels.py:447-480 for the decay matrix)
+ *   qpam_decay_matrix   v11/triton_kernels.py:570-573 fused_decay_matrix
+ *                       (forward, v11/triton_kernels.py:170-202, 420-445)
+ *   qpam_ce_fwd         v11/fused_ce.py:28-53   _FusedLinearCE.forward
+ *                       v11/fused_ce.py:98-141  linear_ce_per_token /
+ *                                               linear_ce_stats
+ *   qpam_ce_bwd         v11/fused_ce.py:56-82   _FusedLinearCE.backward
+ */
+#ifndef QPAM_H
+#define QPAM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    QPAM_OK = 0,
+    QPAM_ERR_ARG = 1,         /* invalid dimensions, strides or pointers */
+    QPAM_ERR_UNSUPPORTED = 2, /* valid request this build does not implement */
+    QPAM_ERR_HIP = 3,         /* a HIP runtime call failed */
+    QPAM_ERR_WORKSPACE = 4    /* workspace missing or too small */
+} qpam_status;
+
+typedef enum { QPAM_F32 = 0, QPAM_BF16 = 1 } qpam_dtype;
+
+/* Library version and the last error message of the calling thread. */
+int qpam_version(void);
+const char *qpam_last_error(void);
+
+/* Profiling helpers (no reference counterpart): timing events that the
+ * entry points with a prof_ev[2] field record around their dominant kernel,
+ * so a benchmark can time that kernel alone on the launch stream. */
+int qpam_event_create(void **ev);
+int qpam_event_destroy(void *ev);
+int qpam_event_elapsed_ms(void *ev0, void *ev1, float *ms);
+
+/* ---------------------------------------------------------------- decode --
+ * One O(1)/token recurrent step over a ragged pool of sequence slots.
+ * For every listed slot a and every group g (= layer*heads + head) and state m:
+ *     S[a,g,m] <- gamma[a,g,m] * S[a,g,m] + v[a,g] (x) conj(k[a,g])
+ *     y[a,g]    = sum_m rot[a,g,m] * (S[a,g,m] @ (q_scale * q[a,g]))
+ * (update before read, v11/model.py:948-964).  Slots not listed are neither
+ * read nor written; ids outside [0, n_slots) are skipped.  rot may be NULL
+ * (all ones).  S is interleaved complex fp32 [d][d][2]; q, k, v, y are
+ * interleaved [d][2]; rot is interleaved [2].  d in {16, 32, 64, 128}.
+ */
+typedef struct {
+    int32_t n_slots;        /* size of the slot axis of every operand */
+    int32_t n_active;       /* entries in `active` (or n_slots if active == NULL) */
+    const int32_t *active;  /* device list of slot ids, or NULL for all slots */
+    int32_t n_groups;       /* layers * heads per slot */
+    int32_t n_states;       /* M >= 1 matrix states per group */
+    int32_t d;              /* head dim */
+    float q_scale;          /* 1.0 when q is already scaled */
+    float *state;           /* updated in place */
+    int64_t st_slot, st_group, st_state;  /* float strides of S */
+    const float *q, *k, *v;
+    int64_t sq_slot, sq_group, sk_slot, sk_group, sv_slot, sv_group;
+    const float *gamma;
+    int64_t sg_slot, sg_group, sg_state;
+    const float *rot;       /* optional */
+    int64_t sr_slot, sr_group, sr_state;
+    float *y;
+    int64_t sy_slot, sy_group;
+} qpam_decode_args;
+
+int qpam_decode_step(const qpam_decode_args *a, void *stream);
+
+/* ------------------------------------------------------------------ scan --
+ * Chunked dual-form PAM scan with M >= 1 states per head (E3 when M > 1):
+ *     q~ = q_scale * q;  D_m, cum_m, total_m from c = cumsum(-log(gamma_m+1e-6))
+ *     Y[t]  = sum_{s<=t} (sum_m r_m[t] D_m[t,s]) (q~_t . k_s*) v_s
+ *           + sum_m r_m[t] cum_m[t] (S_m,in @ q~_t)
+ *     S_m  <- total_m S_m + sum_s D_m[C-1,s] v_s (x) k_s*
+ * q, k, v: planar [B,H,T,d] (strides s0=b, s1=h, s2=t), fp32 or bf16.
+ * gamma: fp32 [M,B,H,T]; rot (r_m, optional, NULL = 1): planar fp32 [M,B,H,T].
+ * s0: optional initial state, planar fp32 [M,B,H,d,d] contiguous.
+ * y: planar fp32 [B,H,T,d]; s_out: final state planar fp32 [M,B,H,d,d].
+ * The workspace keeps the state entering every chunk, planar fp32
+ * [M,B,H,n_chunks,d,d]; qpam_scan_bwd reads it.  d == 64, C in {16,32,64}.
+ */
+typedef struct {
+    const void *re, *im;
+    int64_t s0, s1, s2;
+} qpam_cview;
+
+typedef struct {
+    float *re, *im;
+    int64_t s0, s1, s2;
+} qpam_mview;
+
+typedef struct {
+    int32_t B, H, T, d, C, M;
+    int32_t dtype;          /* qpam_dtype of q, k, v (and of dq, dk, dv) */
+    float q_scale;
+    qpam_cview q, k, v;
+    const float *gamma;
+    int64_t sg_m, sg_b, sg_h, sg_t;
+    const float *rot_re, *rot_im;          /* optional */
+    int64_t sr_m, sr_b, sr_h, sr_t;
+    const float *s0_re, *s0_im;            /* optional */
+    qpam_mview y;
+    float *s_re, *s_im;
+    void *workspace;
+    size_t workspace_bytes;
+    void *prof_ev[2];       /* optional hipEvent_t pair recorded around the
+                               chunk-output kernel (the dominant launch) */
+} qpam_scan_args;
+
+size_t qpam_scan_workspace_size(const qpam_scan_args *a);
+int qpam_scan_fwd(const qpam_scan_args *a, void *stream);
+
+/* Backward of qpam_scan_fwd.  `fwd` must describe the same call whose
+ * workspace still holds the per-chunk states.  dy: planar fp32 [B,H,T,d];
+ * ds: optional gradient of the final state, planar fp32 [M,B,H,d,d].
+ * Outputs dq, dk, dv (dtype of q) planar [B,H,T,d]; dgamma fp32 [M,B,H,T]
+ * with the strides of gamma; drot (optional) planar fp32 with rot's strides;
+ * ds0 (optional) planar fp32 [M,B,H,d,d].  bwd_workspace holds per-chunk
+ * state gradients, size from qpam_scan_bwd_workspace_size. */
+typedef struct {
+    const qpam_scan_args *fwd;
+    qpam_cview dy;
+    const float *ds_re, *ds_im;            /* optional */
+    qpam_mview dq, dk, dv;
+    float *dgamma;
+    float *drot_re, *drot_im;              /* optional */
+    float *ds0_re, *ds0_im;                /* optional */
+    void *workspace;
+    size_t workspace_bytes;
+} qpam_scan_bwd_args;
+
+size_t qpam_scan_bwd_workspace_size(const qpam_scan_bwd_args *a);
+int qpam_scan_bwd(const qpam_scan_bwd_args *a, void *stream);
+
+/* Decay matrix of fused_decay_matrix: gamma [N, T] fp32 (row stride ldg) ->
+ * D [N, T, T] fp32 contiguous, D[t,s] = exp(min(c_s - c_t, 0)) for s <= t
+ * else 0, c = cumsum(-log(gamma + 1e-6)).  T <= 4096. */
+int qpam_decay_matrix(int32_t n, int32_t t, const float *gamma, int64_t ldg, float *out, void *stream);
+
+/* -------------------------------------------------------------------- CE --
+ * Tied complex LM-head cross-entropy over hidden rows H [N, D] and weights
+ * W [V, D] (row-major, leading dims ldh/ldw, bf16 or fp32), logits H W^T.
+ * Forward writes per-row lse [N] and per-row loss [N] (0 on ignored rows,
+ * times mask if given) and, if `stats` is non-NULL, the argmax-correct flag
+ * per row; loss_sum (device scalar, optional) receives sum(loss).
+ * Backward computes dH = G W, dW += G^T H with G = (softmax - onehot) *
+ * grad_scale[row] (grad_scale = g/denom * mask, 0 on ignored rows), processing
+ * `chunk` rows at a time through a bf16 G buffer in the workspace.
+ */
+typedef struct {
+    int32_t N, V, D;
+    int32_t dtype;                 /* of H and W */
+    const void *h; int64_t ldh;
+    const void *w; int64_t ldw;
+    const int64_t *targets;        /* [N] */
+    const float *mask;             /* optional [N] */
+    int64_t ignore_index;
+    float *lse;                    /* [N] */
+    float *loss;                   /* [N] */
+    float *correct;                /* optional [N], 1.0 where argmax == target */
+    float *loss_sum;               /* optional device scalar */
+    void *workspace;
+    size_t workspace_bytes;
+} qpam_ce_fwd_args;
+
+size_t qpam_ce_fwd_workspace_size(const qpam_ce_fwd_args *a);
+int qpam_ce_fwd(const qpam_ce_fwd_args *a, void *stream);
+
+typedef struct {
+    int32_t N, V, D;
+    int32_t dtype;
+    const void *h; int64_t ldh;
+    const void *w; int64_t ldw;
+    const int64_t *targets;
+    const float *mask;             /* optional */
+    int64_t ignore_index;
+    const float *lse;              /* from qpam_ce_fwd */
+    const float *grad_scale;       /* device scalar: grad_output / denom */
+    void *dh; int64_t lddh;        /* dtype of h */
+    float *dw; int64_t lddw;       /* fp32, accumulated (caller zeroes) */
+    int32_t chunk;                 /* rows per G buffer */
+    void *workspace;
+    size_t workspace_bytes;
+} qpam_ce_bwd_args;
+
+size_t qpam_ce_bwd_workspace_size(const qpam_ce_bwd_args *a);
+int qpam_ce_bwd(const qpam_ce_bwd_args *a, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QPAM_H */

@@ -1,0 +1,183 @@
+"""ctypes binding of the qpam C ABI (include/qpam.h).
+
+The library is loaded lazily, after torch (so the HIP runtime that torch
+bundles is the one the library binds to: both resolve the soname
+libamdhip64.so.7).  There is no fallback: if the library is missing or was
+built for another ABI version every entry point raises.
+"""
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must be loaded before the HIP library)
+
+LIB_NAME = "libqpam.so"
+ABI_VERSION = 1
+_HERE = os.path.dirname(os.path.abspath(__file__))
+
+QPAM_F32 = 0
+QPAM_BF16 = 1
+
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_ptr = ctypes.c_void_p
+c_f32 = ctypes.c_float
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("n_slots", c_i32), ("n_active", c_i32), ("active", c_ptr), ("n_groups", c_i32),
+        ("n_states", c_i32), ("d", c_i32), ("q_scale", c_f32),
+        ("state", c_ptr), ("st_slot", c_i64), ("st_group", c_i64), ("st_state", c_i64),
+        ("q", c_ptr), ("k", c_ptr), ("v", c_ptr),
+        ("sq_slot", c_i64), ("sq_group", c_i64), ("sk_slot", c_i64), ("sk_group", c_i64),
+        ("sv_slot", c_i64), ("sv_group", c_i64),
+        ("gamma", c_ptr), ("sg_slot", c_i64), ("sg_group", c_i64), ("sg_state", c_i64),
+        ("rot", c_ptr), ("sr_slot", c_i64), ("sr_group", c_i64), ("sr_state", c_i64),
+        ("y", c_ptr), ("sy_slot", c_i64), ("sy_group", c_i64),
+    ]
+
+
+class CView(ctypes.Structure):
+    _fields_ = [("re", c_ptr), ("im", c_ptr), ("s0", c_i64), ("s1", c_i64), ("s2", c_i64)]
+
+
+class MView(ctypes.Structure):
+    _fields_ = [("re", c_ptr), ("im", c_ptr), ("s0", c_i64), ("s1", c_i64), ("s2", c_i64)]
+
+
+class ScanArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_i32), ("H", c_i32), ("T", c_i32), ("d", c_i32), ("C", c_i32), ("M", c_i32),
+        ("dtype", c_i32), ("q_scale", c_f32),
+        ("q", CView), ("k", CView), ("v", CView),
+        ("gamma", c_ptr), ("sg_m", c_i64), ("sg_b", c_i64), ("sg_h", c_i64), ("sg_t", c_i64),
+        ("rot_re", c_ptr), ("rot_im", c_ptr), ("sr_m", c_i64), ("sr_b", c_i64), ("sr_h", c_i64), ("sr_t", c_i64),
+        ("s0_re", c_ptr), ("s0_im", c_ptr),
+        ("y", MView),
+        ("s_re", c_ptr), ("s_im", c_ptr),
+        ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+        ("prof_ev", c_ptr * 2),
+    ]
+
+
+class ScanBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", ctypes.POINTER(ScanArgs)),
+        ("dy", CView),
+        ("ds_re", c_ptr), ("ds_im", c_ptr),
+        ("dq", MView), ("dk", MView), ("dv", MView),
+        ("dgamma", c_ptr),
+        ("drot_re", c_ptr), ("drot_im", c_ptr),
+        ("ds0_re", c_ptr), ("ds0_im", c_ptr),
+        ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class CeFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("N", c_i32), ("V", c_i32), ("D", c_i32), ("dtype", c_i32),
+        ("h", c_ptr), ("ldh", c_i64), ("w", c_ptr), ("ldw", c_i64),
+        ("targets", c_ptr), ("mask", c_ptr), ("ignore_index", c_i64),
+        ("lse", c_ptr), ("loss", c_ptr), ("correct", c_ptr), ("loss_sum", c_ptr),
+        ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class CeBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("N", c_i32), ("V", c_i32), ("D", c_i32), ("dtype", c_i32),
+        ("h", c_ptr), ("ldh", c_i64), ("w", c_ptr), ("ldw", c_i64),
+        ("targets", c_ptr), ("mask", c_ptr), ("ignore_index", c_i64),
+        ("lse", c_ptr), ("grad_scale", c_ptr),
+        ("dh", c_ptr), ("lddh", c_i64), ("dw", c_ptr), ("lddw", c_i64),
+        ("chunk", c_i32),
+        ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+# symbol -> (restype, argtypes); every symbol include/qpam.h declares
+SIGNATURES = {
+    "qpam_version": (ctypes.c_int, []),
+    "qpam_last_error": (ctypes.c_char_p, []),
+    "qpam_event_create": (ctypes.c_int, [ctypes.POINTER(c_ptr)]),
+    "qpam_event_destroy": (ctypes.c_int, [c_ptr]),
+    "qpam_event_elapsed_ms": (ctypes.c_int, [c_ptr, c_ptr, ctypes.POINTER(c_f32)]),
+    "qpam_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_ptr]),
+    "qpam_scan_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(ScanArgs)]),
+    "qpam_scan_fwd": (ctypes.c_int, [ctypes.POINTER(ScanArgs), c_ptr]),
+    "qpam_scan_bwd_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(ScanBwdArgs)]),
+    "qpam_scan_bwd": (ctypes.c_int, [ctypes.POINTER(ScanBwdArgs), c_ptr]),
+    "qpam_decay_matrix": (ctypes.c_int, [c_i32, c_i32, c_ptr, c_i64, c_ptr, c_ptr]),
+    "qpam_ce_fwd_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(CeFwdArgs)]),
+    "qpam_ce_fwd": (ctypes.c_int, [ctypes.POINTER(CeFwdArgs), c_ptr]),
+    "qpam_ce_bwd_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(CeBwdArgs)]),
+    "qpam_ce_bwd": (ctypes.c_int, [ctypes.POINTER(CeBwdArgs), c_ptr]),
+}
+
+_LIB = None
+
+
+class QpamError(RuntimeError):
+    pass
+
+
+def lib_path():
+    return os.path.join(_HERE, LIB_NAME)
+
+
+def lib():
+    """Load (once) and return the ctypes library.  Raises if it is missing."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = lib_path()
+    if not os.path.exists(path):
+        raise QpamError(f"{path} is not built; run __graft_entry__.build() (hipcc --offload-arch=gfx950)")
+    handle = ctypes.CDLL(path)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    ver = handle.qpam_version()
+    if ver != ABI_VERSION:
+        raise QpamError(f"{path}: ABI version {ver}, expected {ABI_VERSION}; rebuild")
+    _LIB = handle
+    return _LIB
+
+
+def check(status, what):
+    if status != 0:
+        msg = lib().qpam_last_error().decode(errors="replace")
+        raise QpamError(f"{what} failed (status {status}): {msg}")
+
+
+def stream_ptr(device=None):
+    """Raw hipStream_t of torch's current stream on `device`."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+class EventPair:
+    """Two HIP timing events created by the library (for the prof_ev fields)."""
+
+    def __init__(self):
+        L = lib()
+        self.ev = [c_ptr(), c_ptr()]
+        for e in self.ev:
+            check(L.qpam_event_create(ctypes.byref(e)), "qpam_event_create")
+
+    def elapsed_ms(self):
+        ms = c_f32()
+        check(lib().qpam_event_elapsed_ms(self.ev[0], self.ev[1], ctypes.byref(ms)), "qpam_event_elapsed_ms")
+        return ms.value
+
+    def __del__(self):
+        try:
+            for e in self.ev:
+                lib().qpam_event_destroy(e)
+        except Exception:
+            pass

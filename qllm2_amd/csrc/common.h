@@ -1,0 +1,66 @@
+// Shared helpers of the qpam HIP library (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/qpam.h"
+
+namespace qpam {
+
+// ------------------------------------------------------------- errors ------
+std::string &last_error_slot();
+int fail(int code, const char *fmt, ...);
+
+#define QPAM_CHECK_HIP(expr)                                                    \
+    do {                                                                        \
+        hipError_t err__ = (expr);                                              \
+        if (err__ != hipSuccess)                                                \
+            return ::qpam::fail(QPAM_ERR_HIP, "%s failed: %s", #expr,           \
+                                hipGetErrorString(err__));                      \
+    } while (0)
+
+#define QPAM_REQUIRE(cond, ...)                                                 \
+    do {                                                                        \
+        if (!(cond)) return ::qpam::fail(QPAM_ERR_ARG, __VA_ARGS__);            \
+    } while (0)
+
+inline int launch_status(const char *what) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return fail(QPAM_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(err));
+    return QPAM_OK;
+}
+
+// ------------------------------------------------------------- vectors -----
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short ushortx8 __attribute__((ext_vector_type(8)));
+typedef unsigned short ushortx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(unsigned short u) {
+    return __uint_as_float(((unsigned int)u) << 16);
+}
+
+// round-to-nearest-even float -> bf16 bits (finite inputs)
+__device__ __forceinline__ unsigned short f32_to_bf16(float f) {
+    unsigned int u = __float_as_uint(f);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (unsigned short)(u >> 16);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+    __device__ __forceinline__ static float load(const float *p) { return *p; }
+};
+template <> struct Elem<unsigned short> {
+    __device__ __forceinline__ static float load(const unsigned short *p) { return bf16_to_f32(*p); }
+};
+
+}  // namespace qpam

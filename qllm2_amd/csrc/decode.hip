@@ -1,0 +1,179 @@
+// Ragged continuous-batching PAM decode step (HBM-bound streaming kernel).
+//
+// Reference semantics: V11PAMLayer._recur_step_additive (v11/model.py:927-965)
+// applied per state and phase-routed/summed as in _recurrent
+// (v11/model.py:874-906):
+//     S <- gamma S + v (x) conj(k);   y = sum_m r_m (S_m @ q~)
+//
+// Design: one workgroup per (listed slot, group).  The d x d interleaved
+// complex state of each of the M states is streamed once (16-byte loads and
+// stores, consecutive lanes on consecutive 16 bytes so every wave instruction
+// covers a contiguous 1 KiB).  Each lane owns a fixed pair of key columns, so
+// q~ and k are loaded once per lane; the row sums of S q~ are reduced across
+// the lanes of a row with a halving butterfly (each step halves the number of
+// live partial sums, 16 shuffles instead of 80 for d = 64).  Slots that are
+// not listed cost nothing: the grid is n_active * n_groups.
+#include "common.h"
+
+namespace qpam {
+namespace {
+
+template <int D>
+struct DecodeShape {
+    static constexpr int PAIRS = D / 2;                       // float4 per state row
+    static constexpr int THREADS = (D * D / 2) < 256 ? (D * D / 2) : 256;
+    static constexpr int ROWS_PER_IT = THREADS / PAIRS;       // rows covered per iteration
+    static constexpr int ITERS = D / ROWS_PER_IT;             // float4 per lane per state
+    static constexpr int NV = 2 * ITERS;                      // partial sums per lane (re, im per row)
+};
+
+// Reduce NV values across P aligned lanes by halving; on return the lane holds
+// `nv` complete sums for value indices [idx_base, idx_base + nv).
+template <int NV, int P>
+__device__ __forceinline__ void halving_reduce(float (&v)[NV], int lane, int &idx_base, int &nv_out) {
+    int nv = NV;
+    idx_base = 0;
+#pragma unroll
+    for (int off = P / 2; off >= 1; off >>= 1) {
+        if (nv > 1) {
+            const int half = nv / 2;
+            const bool up = (lane & off) != 0;
+#pragma unroll
+            for (int j = 0; j < NV / 2; ++j) {
+                if (j < half) {
+                    float send = up ? v[j] : v[j + half];
+                    float keep = up ? v[j + half] : v[j];
+                    v[j] = keep + __shfl_xor(send, off);
+                }
+            }
+            if (up) idx_base += half;
+            nv = half;
+        } else {
+            v[0] += __shfl_xor(v[0], off);
+        }
+    }
+    nv_out = nv;
+}
+
+template <int D>
+__global__ void __launch_bounds__(DecodeShape<D>::THREADS)
+decode_step_kernel(qpam_decode_args a) {
+    using S = DecodeShape<D>;
+    __shared__ float ys[D][2];
+
+    const int tid = threadIdx.x;
+    const int blk = blockIdx.x;
+    const int ai = blk / a.n_groups;
+    const int g = blk - ai * a.n_groups;
+    const int slot = a.active ? a.active[ai] : ai;
+    if (slot < 0 || slot >= a.n_slots) return;  // whole block exits together
+
+    const int cp = tid % S::PAIRS;      // this lane's key-column pair: j = 2cp, 2cp+1
+    const int r0 = tid / S::PAIRS;      // first row of this lane
+    const int lane = tid & 63;
+
+    const float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
+    const float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    const float q0r = qv.x * a.q_scale, q0i = qv.y * a.q_scale;
+    const float q1r = qv.z * a.q_scale, q1i = qv.w * a.q_scale;
+    const float *vrow = a.v + slot * a.sv_slot + g * a.sv_group;
+
+    float yacc_r = 0.f, yacc_i = 0.f;  // lanes tid < D accumulate row tid
+
+    for (int m = 0; m < a.n_states; ++m) {
+        float *st = a.state + slot * a.st_slot + g * a.st_group + m * a.st_state;
+        const float gam = a.gamma[slot * a.sg_slot + g * a.sg_group + m * a.sg_state];
+        float4 s[S::ITERS];
+#pragma unroll
+        for (int it = 0; it < S::ITERS; ++it)
+            s[it] = *reinterpret_cast<const float4 *>(st + 4 * (it * S::THREADS + tid));
+
+        float part[S::NV];
+#pragma unroll
+        for (int it = 0; it < S::ITERS; ++it) {
+            const int row = it * S::ROWS_PER_IT + r0;
+            const float2 vv = *reinterpret_cast<const float2 *>(vrow + 2 * row);
+            // v_i conj(k_j) for the two columns
+            const float o0r = vv.x * kv.x + vv.y * kv.y, o0i = vv.y * kv.x - vv.x * kv.y;
+            const float o1r = vv.x * kv.z + vv.y * kv.w, o1i = vv.y * kv.z - vv.x * kv.w;
+            float4 n;
+            n.x = gam * s[it].x + o0r;
+            n.y = gam * s[it].y + o0i;
+            n.z = gam * s[it].z + o1r;
+            n.w = gam * s[it].w + o1i;
+            *reinterpret_cast<float4 *>(st + 4 * (it * S::THREADS + tid)) = n;
+            part[2 * it] = n.x * q0r - n.y * q0i + n.z * q1r - n.w * q1i;
+            part[2 * it + 1] = n.x * q0i + n.y * q0r + n.z * q1i + n.w * q1r;
+        }
+
+        int base, nv;
+        halving_reduce<S::NV, S::PAIRS>(part, lane, base, nv);
+#pragma unroll
+        for (int j = 0; j < S::NV; ++j) {
+            if (j < nv) {
+                const int vi = base + j;
+                ys[(vi >> 1) * S::ROWS_PER_IT + r0][vi & 1] = part[j];
+            }
+        }
+        __syncthreads();
+        if (tid < D) {
+            const float yr = ys[tid][0], yi = ys[tid][1];
+            if (a.rot) {
+                const float *rp = a.rot + slot * a.sr_slot + g * a.sr_group + m * a.sr_state;
+                const float rr = rp[0], ri = rp[1];
+                yacc_r += rr * yr - ri * yi;
+                yacc_i += rr * yi + ri * yr;
+            } else {
+                yacc_r += yr;
+                yacc_i += yi;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < D) {
+        float *yp = a.y + slot * a.sy_slot + g * a.sy_group + 2 * tid;
+        *reinterpret_cast<float2 *>(yp) = make_float2(yacc_r, yacc_i);
+    }
+}
+
+template <int D>
+int launch_decode(const qpam_decode_args &a, hipStream_t stream) {
+    using S = DecodeShape<D>;
+    const long long blocks = (long long)a.n_active * a.n_groups;
+    if (blocks == 0) return QPAM_OK;
+    hipLaunchKernelGGL(decode_step_kernel<D>, dim3((unsigned)blocks), dim3(S::THREADS), 0, stream, a);
+    return launch_status("decode_step_kernel");
+}
+
+bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
+
+}  // namespace
+}  // namespace qpam
+
+extern "C" int qpam_decode_step(const qpam_decode_args *a, void *stream) {
+    using namespace qpam;
+    QPAM_REQUIRE(a != nullptr, "qpam_decode_step: null args");
+    QPAM_REQUIRE(a->n_slots >= 0 && a->n_active >= 0 && a->n_groups >= 1 && a->n_states >= 1,
+                 "qpam_decode_step: bad sizes (slots %d active %d groups %d states %d)", a->n_slots,
+                 a->n_active, a->n_groups, a->n_states);
+    QPAM_REQUIRE(a->active != nullptr || a->n_active <= a->n_slots,
+                 "qpam_decode_step: n_active > n_slots without an active list");
+    QPAM_REQUIRE(a->state && a->q && a->k && a->v && a->gamma && a->y, "qpam_decode_step: null pointer");
+    QPAM_REQUIRE((long long)a->n_active * a->n_groups < (1ll << 31), "qpam_decode_step: grid too large");
+    // 16-byte vector access of S, q, k and 8-byte access of v, y
+    QPAM_REQUIRE(aligned(a->state, 16) && aligned(a->q, 16) && aligned(a->k, 16) && aligned(a->v, 8) &&
+                     aligned(a->y, 8),
+                 "qpam_decode_step: misaligned operand");
+    QPAM_REQUIRE(a->st_slot % 4 == 0 && a->st_group % 4 == 0 && a->st_state % 4 == 0 && a->sq_slot % 4 == 0 &&
+                     a->sq_group % 4 == 0 && a->sk_slot % 4 == 0 && a->sk_group % 4 == 0 &&
+                     a->sv_slot % 2 == 0 && a->sv_group % 2 == 0 && a->sy_slot % 2 == 0 && a->sy_group % 2 == 0,
+                 "qpam_decode_step: strides must keep 16-byte (S, q, k) / 8-byte (v, y) alignment");
+    hipStream_t s = (hipStream_t)stream;
+    switch (a->d) {
+        case 16: return launch_decode<16>(*a, s);
+        case 32: return launch_decode<32>(*a, s);
+        case 64: return launch_decode<64>(*a, s);
+        case 128: return launch_decode<128>(*a, s);
+        default: return fail(QPAM_ERR_UNSUPPORTED, "qpam_decode_step: d=%d (supported 16, 32, 64, 128)", a->d);
+    }
+}

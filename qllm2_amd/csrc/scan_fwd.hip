@@ -1,0 +1,409 @@
+// Chunked dual-form PAM scan, forward (fp32 MFMA, d = 64).
+//
+// Reference semantics: V11PAMLayer._forward_chunked_head (v11/model.py:378-417)
+// for M = 1 and _fused_chunk_step/_forward_multistate_fused
+// (v11/model.py:657-781) for M states with rotations r_m = alpha e^{i phi}.
+//
+// The only sequential dependency of the scan is the d x d state carry, and the
+// state rows are independent, so the forward is split into three launches:
+//   1. chunk_state  (chunk-parallel, MFMA): per chunk c and state m the write
+//      dS_m,c = sum_s D_m[C-1,s] v_s (x) conj(k_s) and the chunk decay
+//      total_m,c -> workspace;
+//   2. state_scan   (elementwise, sequential over chunks): replaces dS_m,c by
+//      the state entering chunk c, S_in = prod-decayed prefix, and writes the
+//      final state;
+//   3. chunk_output (chunk-parallel, MFMA): Y_c = (W . D~) V + sum_m rho_m
+//      (Q~ S_in,m^T) with W = Q~ K^H, D~ = sum_m r_m D_m, rho_m = r_m cum_m.
+// Decay matrices are never materialised: each lane rebuilds D[t,s] from the
+// chunk's log-decay prefix sums held in LDS.  The score tile is computed
+// transposed (rows s, cols t) so the MFMA accumulator layout is directly the
+// A operand of the (W . D~) V product.
+#include "scan_common.h"
+
+namespace qpam {
+namespace scan {
+namespace {
+
+struct FwdParams {
+    qpam_scan_args a;
+    int n_chunks;
+    float *states;   // [M][B][H][n][2][64][64]
+    float *totals;   // [M][B][H][n]
+};
+
+__device__ __forceinline__ float *chunk_state_ptr(const FwdParams &p, int m, int b, int h, int c) {
+    const int64_t idx = (((int64_t)m * p.a.B + b) * p.a.H + h) * p.n_chunks + c;
+    return p.states + idx * (2 * D * D);
+}
+
+__device__ __forceinline__ float *chunk_total_ptr(const FwdParams &p, int m, int b, int h, int c) {
+    return p.totals + (((int64_t)m * p.a.B + b) * p.a.H + h) * p.n_chunks + c;
+}
+
+// ---------------------------------------------------------------- kernel 1 --
+template <typename Tin, int C>
+__global__ void __launch_bounds__(THREADS) chunk_state_kernel(FwdParams p) {
+    extern __shared__ float smem[];
+    float *sKr = smem, *sKi = sKr + C * P, *sVr = sKi + C * P, *sVi = sVr + C * P;
+    float *sDl = sVi + C * P;  // [MAX_M][64]
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * C;
+    const int valid = min(C, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+
+    const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+    const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+    load_tile<Tin>(sKr, (const Tin *)a.k.re + ko, a.k.s2, C, valid, 1.f);
+    load_tile<Tin>(sKi, (const Tin *)a.k.im + ko, a.k.s2, C, valid, 1.f);
+    load_tile<Tin>(sVr, (const Tin *)a.v.re + vo, a.v.s2, C, valid, 1.f);
+    load_tile<Tin>(sVi, (const Tin *)a.v.im + vo, a.v.s2, C, valid, 1.f);
+    if (w == 0) {
+        for (int m = 0; m < a.M; ++m) {
+            const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
+            const float L = chunk_log_prefix(gp, a.sg_t, valid, lane);
+            const float Llast = __shfl(L, valid - 1);
+            sDl[m * 64 + lane] = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
+            if (lane == 0) *chunk_total_ptr(p, m, b, h, c) = __expf(Llast);
+        }
+    }
+    __syncthreads();
+
+    // wave w owns value rows i in [16w, 16w+16); all 64 key columns j
+    for (int m = 0; m < a.M; ++m) {
+        floatx4 accR[4], accI[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
+#pragma unroll 4
+        for (int ks = 0; ks < C / 4; ++ks) {
+            const int s = 4 * ks + g;
+            const float dl = sDl[m * 64 + s];
+            const float vr = sVr[s * P + 16 * w + l16] * dl;
+            const float vi = sVi[s * P + 16 * w + l16] * dl;
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                const float kr = sKr[s * P + 16 * jt + l16];
+                const float ki = sKi[s * P + 16 * jt + l16];
+                accR[jt] = mfma4(vr, kr, accR[jt]);
+                accR[jt] = mfma4(vi, ki, accR[jt]);
+                accI[jt] = mfma4(vi, kr, accI[jt]);
+                accI[jt] = mfma4(vr, -ki, accI[jt]);
+            }
+        }
+        float *dst = chunk_state_ptr(p, m, b, h, c);
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * w + 4 * g + r, j = 16 * jt + l16;
+                dst[i * D + j] = accR[jt][r];
+                dst[D * D + i * D + j] = accI[jt][r];
+            }
+    }
+}
+
+// ---------------------------------------------------------------- kernel 2 --
+// One thread per 4 consecutive state floats of one (m, b, h); 2048 float4 per
+// state (re plane then im plane), 8 blocks per state.
+__global__ void __launch_bounds__(THREADS) state_scan_kernel(FwdParams p) {
+    const qpam_scan_args &a = p.a;
+    const int chain = blockIdx.x >> 3;
+    const int e4 = ((blockIdx.x & 7) << 8) + threadIdx.x;  // 0..2047
+    const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
+    const int b = bh / a.H, h = bh % a.H;
+    const int plane = e4 >> 10, off = (e4 & 1023) * 4;
+
+    float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
+    const int64_t so = (int64_t)chain * D * D + off;
+    if (a.s0_re) S = *reinterpret_cast<const float4 *>((plane ? a.s0_im : a.s0_re) + so);
+
+    float *base = chunk_state_ptr(p, m, b, h, 0) + plane * D * D + off;
+    const float *tot = chunk_total_ptr(p, m, b, h, 0);
+    const int n = p.n_chunks;
+    float4 nxt = *reinterpret_cast<const float4 *>(base);
+    for (int c = 0; c < n; ++c) {
+        const float4 ds = nxt;
+        if (c + 1 < n) nxt = *reinterpret_cast<const float4 *>(base + (int64_t)(c + 1) * 2 * D * D);
+        *reinterpret_cast<float4 *>(base + (int64_t)c * 2 * D * D) = S;
+        const float t = tot[c];
+        S.x = t * S.x + ds.x;
+        S.y = t * S.y + ds.y;
+        S.z = t * S.z + ds.z;
+        S.w = t * S.w + ds.w;
+    }
+    if (a.s_re) *reinterpret_cast<float4 *>((plane ? a.s_im : a.s_re) + so) = S;
+}
+
+// ---------------------------------------------------------------- kernel 3 --
+template <typename Tin, int C>
+__global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
+    extern __shared__ float smem[];
+    float *sQr = smem, *sQi = sQr + C * P;
+    float *sKr = sQi + C * P, *sKi = sKr + D * P;  // K tile, later the carried state S_m
+    float *sVr = sKi + D * P, *sVi = sVr + C * P;
+    float *sL = sVi + C * P;         // [MAX_M][64] log-decay prefix
+    float *sRr = sL + MAX_M * 64;    // [MAX_M][64] rotation
+    float *sRi = sRr + MAX_M * 64;
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * C;
+    const int valid = min(C, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const bool general = (a.M > 1) || (a.rot_re != nullptr);
+    const bool carry = (c > 0) || (a.s0_re != nullptr);
+
+    const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+    const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+    const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+    load_tile<Tin>(sQr, (const Tin *)a.q.re + qo, a.q.s2, C, valid, a.q_scale);
+    load_tile<Tin>(sQi, (const Tin *)a.q.im + qo, a.q.s2, C, valid, a.q_scale);
+    load_tile<Tin>(sKr, (const Tin *)a.k.re + ko, a.k.s2, C, valid, 1.f);
+    load_tile<Tin>(sKi, (const Tin *)a.k.im + ko, a.k.s2, C, valid, 1.f);
+    load_tile<Tin>(sVr, (const Tin *)a.v.re + vo, a.v.s2, C, valid, 1.f);
+    load_tile<Tin>(sVi, (const Tin *)a.v.im + vo, a.v.s2, C, valid, 1.f);
+    if (w == 0) {
+        for (int m = 0; m < a.M; ++m) {
+            const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
+            sL[m * 64 + lane] = chunk_log_prefix(gp, a.sg_t, valid, lane);
+            float rr = 1.f, ri = 0.f;
+            if (a.rot_re && lane < valid) {
+                const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + lane) * a.sr_t;
+                rr = a.rot_re[ro];
+                ri = a.rot_im[ro];
+            }
+            sRr[m * 64 + lane] = rr;
+            sRi[m * 64 + lane] = ri;
+        }
+    }
+    __syncthreads();
+
+    const int tt = w;                      // query rows t in [16tt, 16tt+16)
+    const bool active = tt < C / 16;
+    floatx4 yR[4], yI[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) yR[it] = yI[it] = zero4();
+
+    if (active) {
+        // ---- transposed score tiles W^T[s][t] for s-tiles st <= tt (causal)
+        floatx4 wr[4], wi[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) wr[st] = wi[st] = zero4();
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            // k-steps 4q4..4q4+3 use key/query columns j = 16 q4 + 4 g + kk
+            const float4 bq_r = *reinterpret_cast<const float4 *>(sQr + (16 * tt + l16) * P + 16 * q4 + 4 * g);
+            const float4 bq_i = *reinterpret_cast<const float4 *>(sQi + (16 * tt + l16) * P + 16 * q4 + 4 * g);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > tt || 16 * st >= C) continue;
+                const float4 ak_r = *reinterpret_cast<const float4 *>(sKr + (16 * st + l16) * P + 16 * q4 + 4 * g);
+                const float4 ak_i = *reinterpret_cast<const float4 *>(sKi + (16 * st + l16) * P + 16 * q4 + 4 * g);
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    wr[st] = mfma4(ak_r[kk], bq_r[kk], wr[st]);
+                    wr[st] = mfma4(ak_i[kk], bq_i[kk], wr[st]);
+                    wi[st] = mfma4(ak_r[kk], bq_i[kk], wi[st]);
+                    wi[st] = mfma4(-ak_i[kk], bq_r[kk], wi[st]);
+                }
+            }
+        }
+        // ---- apply the (complex) decay D~[t,s]; lane holds s = 16st+4g+r, t = 16tt+l16
+        const int t = 16 * tt + l16;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            if (st > tt || 16 * st >= C) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int s = 16 * st + 4 * g + r;
+                float dre = 0.f, dim = 0.f;
+                if (s <= t) {
+                    if (!general) {
+                        dre = __expf(fminf(sL[t] - sL[s], 0.f));
+                    } else {
+                        for (int m = 0; m < a.M; ++m) {
+                            const float dm = __expf(fminf(sL[m * 64 + t] - sL[m * 64 + s], 0.f));
+                            dre += sRr[m * 64 + t] * dm;
+                            dim += sRi[m * 64 + t] * dm;
+                        }
+                    }
+                }
+                const float xr = wr[st][r], xi = wi[st][r];
+                wr[st][r] = xr * dre - xi * dim;
+                wi[st][r] = xr * dim + xi * dre;
+            }
+        }
+        // ---- intra-chunk read  Y += (W . D~) V   (k = s, 4 k-steps per s-tile)
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            if (st > tt || 16 * st >= C) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int s = 16 * st + 4 * g + r;
+                const float ar = wr[st][r], ai = wi[st][r];
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const float vr = sVr[s * P + 16 * it + l16];
+                    const float vi = sVi[s * P + 16 * it + l16];
+                    yR[it] = mfma4(ar, vr, yR[it]);
+                    yR[it] = mfma4(-ai, vi, yR[it]);
+                    yI[it] = mfma4(ar, vi, yI[it]);
+                    yI[it] = mfma4(ai, vr, yI[it]);
+                }
+            }
+        }
+    }
+
+    // ---- carried read  Y += sum_m (rho_m . Q~) S_in,m^T
+    if (carry) {
+        for (int m = 0; m < a.M; ++m) {
+            __syncthreads();  // previous users of sK* are done
+            const float *src = chunk_state_ptr(p, m, b, h, c);
+            for (int idx = tid; idx < 2 * D * 16; idx += THREADS) {
+                const int pl = idx >> 10, r = (idx >> 4) & 63, c4 = idx & 15;
+                const float4 v = *reinterpret_cast<const float4 *>(src + pl * D * D + r * D + 4 * c4);
+                float *dst = (pl ? sKi : sKr) + r * P + 4 * c4;
+                dst[0] = v.x;
+                dst[1] = v.y;
+                dst[2] = v.z;
+                dst[3] = v.w;
+            }
+            __syncthreads();
+            if (active) {
+                const int t = 16 * tt + l16;
+                const float cum = __expf(sL[m * 64 + t]);
+                const float rho_r = sRr[m * 64 + t] * cum, rho_i = sRi[m * 64 + t] * cum;
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const float4 qr = *reinterpret_cast<const float4 *>(sQr + t * P + 16 * q4 + 4 * g);
+                    const float4 qi = *reinterpret_cast<const float4 *>(sQi + t * P + 16 * q4 + 4 * g);
+#pragma unroll
+                    for (int it = 0; it < 4; ++it) {
+                        const float4 sr = *reinterpret_cast<const float4 *>(sKr + (16 * it + l16) * P + 16 * q4 + 4 * g);
+                        const float4 si = *reinterpret_cast<const float4 *>(sKi + (16 * it + l16) * P + 16 * q4 + 4 * g);
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) {
+                            const float pr = rho_r * qr[kk] - rho_i * qi[kk];
+                            const float pi = rho_r * qi[kk] + rho_i * qr[kk];
+                            yR[it] = mfma4(pr, sr[kk], yR[it]);
+                            yR[it] = mfma4(-pi, si[kk], yR[it]);
+                            yI[it] = mfma4(pr, si[kk], yI[it]);
+                            yI[it] = mfma4(pi, sr[kk], yI[it]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    if (active) {
+        const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)c0 * a.y.s2;
+#pragma unroll
+        for (int it = 0; it < 4; ++it)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * tt + 4 * g + r;
+                if (t < valid) {
+                    a.y.re[yo + (int64_t)t * a.y.s2 + 16 * it + l16] = yR[it][r];
+                    a.y.im[yo + (int64_t)t * a.y.s2 + 16 * it + l16] = yI[it][r];
+                }
+            }
+    }
+}
+
+template <int C>
+size_t state_smem() { return (size_t)(4 * C * P + MAX_M * 64) * sizeof(float); }
+template <int C>
+size_t output_smem() { return (size_t)(4 * C * P + 2 * D * P + 3 * MAX_M * 64) * sizeof(float); }
+
+template <typename Tin, int C>
+int launch_fwd(const FwdParams &p, hipStream_t stream) {
+    const qpam_scan_args &a = p.a;
+    dim3 grid(p.n_chunks, a.H, a.B);
+    const size_t s1 = state_smem<C>(), s3 = output_smem<C>();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_state_kernel<Tin, C>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_kernel<Tin, C>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
+    hipLaunchKernelGGL((chunk_state_kernel<Tin, C>), grid, dim3(THREADS), s1, stream, p);
+    int st = launch_status("chunk_state_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(state_scan_kernel, dim3(a.M * a.B * a.H * 8), dim3(THREADS), 0, stream, p);
+    st = launch_status("state_scan_kernel");
+    if (st) return st;
+    if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));
+    hipLaunchKernelGGL((chunk_output_kernel<Tin, C>), grid, dim3(THREADS), s3, stream, p);
+    st = launch_status("chunk_output_kernel");
+    if (st) return st;
+    if (a.prof_ev[1]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[1], stream));
+    return QPAM_OK;
+}
+
+}  // namespace
+
+size_t fwd_workspace_bytes(const qpam_scan_args &a) {
+    const int64_t n = (a.T + a.C - 1) / a.C;
+    const int64_t chains = (int64_t)a.M * a.B * a.H;
+    return (size_t)(chains * n * 2 * D * D + chains * n) * sizeof(float);
+}
+
+int validate_scan(const qpam_scan_args *a, const char *who) {
+    QPAM_REQUIRE(a != nullptr, "%s: null args", who);
+    QPAM_REQUIRE(a->B >= 1 && a->H >= 1 && a->T >= 1 && a->M >= 1, "%s: bad sizes B=%d H=%d T=%d M=%d", who, a->B,
+                 a->H, a->T, a->M);
+    if (a->d != D) return fail(QPAM_ERR_UNSUPPORTED, "%s: head dim %d (this build supports 64)", who, a->d);
+    if (a->C != 16 && a->C != 32 && a->C != 64)
+        return fail(QPAM_ERR_UNSUPPORTED, "%s: chunk %d (supported 16, 32, 64)", who, a->C);
+    if (a->M > MAX_M) return fail(QPAM_ERR_UNSUPPORTED, "%s: %d states (max %d)", who, a->M, MAX_M);
+    QPAM_REQUIRE(a->dtype == QPAM_F32 || a->dtype == QPAM_BF16, "%s: dtype %d", who, a->dtype);
+    const qpam_cview *vs[3] = {&a->q, &a->k, &a->v};
+    const int vec = a->dtype == QPAM_F32 ? 4 : 8;  // elements per 16-byte load
+    for (const qpam_cview *v : vs) {
+        QPAM_REQUIRE(v->re && v->im, "%s: null q/k/v plane", who);
+        QPAM_REQUIRE(((uintptr_t)v->re % 16) == 0 && ((uintptr_t)v->im % 16) == 0,
+                     "%s: q/k/v planes must be 16-byte aligned", who);
+        QPAM_REQUIRE(v->s0 % vec == 0 && v->s1 % vec == 0 && v->s2 % vec == 0,
+                     "%s: q/k/v strides must be multiples of %d elements", who, vec);
+    }
+    QPAM_REQUIRE(a->gamma != nullptr, "%s: null gamma", who);
+    QPAM_REQUIRE((a->rot_re == nullptr) == (a->rot_im == nullptr), "%s: rot needs both planes", who);
+    QPAM_REQUIRE((a->s0_re == nullptr) == (a->s0_im == nullptr), "%s: s0 needs both planes", who);
+    QPAM_REQUIRE((a->s_re == nullptr) == (a->s_im == nullptr), "%s: s_out needs both planes", who);
+    QPAM_REQUIRE(a->y.re && a->y.im, "%s: null y", who);
+    const uintptr_t al = (uintptr_t)a->s0_re | (uintptr_t)a->s0_im | (uintptr_t)a->s_re | (uintptr_t)a->s_im;
+    QPAM_REQUIRE(al % 16 == 0, "%s: state buffers must be 16-byte aligned", who);
+    QPAM_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= fwd_workspace_bytes(*a) &&
+                     ((uintptr_t)a->workspace % 16) == 0,
+                 "%s: workspace needs %zu bytes (got %zu)", who, fwd_workspace_bytes(*a), a->workspace_bytes);
+    return QPAM_OK;
+}
+
+int scan_fwd(const qpam_scan_args *a, hipStream_t stream) {
+    int st = validate_scan(a, "qpam_scan_fwd");
+    if (st) return st;
+    FwdParams p;
+    p.a = *a;
+    p.n_chunks = (a->T + a->C - 1) / a->C;
+    const int64_t chains = (int64_t)a->M * a->B * a->H;
+    p.states = (float *)a->workspace;
+    p.totals = p.states + chains * p.n_chunks * 2 * D * D;
+    QPAM_REQUIRE(p.n_chunks <= 65535 && a->H <= 65535 && a->B <= 65535, "qpam_scan_fwd: grid too large");
+    const bool bf = a->dtype == QPAM_BF16;
+    switch (a->C) {
+        case 16: return bf ? launch_fwd<unsigned short, 16>(p, stream) : launch_fwd<float, 16>(p, stream);
+        case 32: return bf ? launch_fwd<unsigned short, 32>(p, stream) : launch_fwd<float, 32>(p, stream);
+        default: return bf ? launch_fwd<unsigned short, 64>(p, stream) : launch_fwd<float, 64>(p, stream);
+    }
+}
+
+}  // namespace scan
+}  // namespace qpam
+
+extern "C" size_t qpam_scan_workspace_size(const qpam_scan_args *a) {
+    return a ? qpam::scan::fwd_workspace_bytes(*a) : 0;
+}
+
+extern "C" int qpam_scan_fwd(const qpam_scan_args *a, void *stream) {
+    return qpam::scan::scan_fwd(a, (hipStream_t)stream);
+}

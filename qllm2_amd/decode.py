@@ -1,0 +1,101 @@
+"""O(1)/token recurrent PAM decode on the HIP kernel (qpam_decode_step).
+
+Reference: V11PAMLayer._recur_step_additive (v11/model.py:927-965) and the
+per-token state loop of V11PAMLayer._recurrent (v11/model.py:845-925).
+
+`decode_step` is the continuous-batching form: one call updates every listed
+slot of a state pool in place, all layers/heads/states at once.
+`recur_step_additive` keeps the reference method's signature and functional
+(non-mutating) semantics.
+"""
+
+import torch
+
+from . import _lib
+
+
+def _check_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("qpam decode: tensors must be on the GPU (no CPU path in this library)")
+
+
+def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, out=None):
+    """In-place ragged decode step over a slot pool.
+
+    state  [S, G, M, d, d, 2] fp32 (G = layers*heads, M states), updated in place
+    q,k,v  [S, G, d, 2] fp32 (q unscaled; multiplied by q_scale)
+    gamma  [S, G, M] fp32
+    active optional int32 [n] slot ids (others untouched); None = all slots
+    rot    optional [S, G, M, 2] fp32 complex rotation of each state's read
+    Returns y [S, G, d, 2] (rows of unlisted slots are left as in `out`/zero).
+    """
+    _check_cuda(state, q, k, v, gamma, active, rot)
+    if state.dim() != 6 or state.shape[-1] != 2 or state.shape[-2] != state.shape[-3]:
+        raise ValueError(f"state must be [S,G,M,d,d,2], got {tuple(state.shape)}")
+    n_slots, n_groups, n_states, d = state.shape[:4]
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if tuple(t.shape) != (n_slots, n_groups, d, 2):
+            raise ValueError(f"{name} must be [{n_slots},{n_groups},{d},2], got {tuple(t.shape)}")
+    if tuple(gamma.shape) != (n_slots, n_groups, n_states):
+        raise ValueError(f"gamma must be [{n_slots},{n_groups},{n_states}], got {tuple(gamma.shape)}")
+    for t in (state, q, k, v, gamma) + ((rot,) if rot is not None else ()):
+        if t.dtype != torch.float32:
+            raise ValueError("qpam decode works on fp32 tensors")
+    if state.stride()[-3:] != (2 * d, 2, 1):
+        raise ValueError("state matrices must be contiguous [d, d, 2]")
+    q, k, v = (t if t.stride()[-2:] == (2, 1) else t.contiguous() for t in (q, k, v))
+    if rot is not None:
+        if tuple(rot.shape) != (n_slots, n_groups, n_states, 2):
+            raise ValueError("rot must be [S,G,M,2]")
+        rot = rot if rot.stride(-1) == 1 else rot.contiguous()
+    y = out if out is not None else torch.zeros_like(q)
+    if active is not None:
+        if active.dtype != torch.int32:
+            active = active.to(torch.int32)
+        active = active.contiguous()
+        n_active = active.numel()
+    else:
+        n_active = n_slots
+    a = _lib.DecodeArgs()
+    a.n_slots, a.n_active, a.n_groups, a.n_states, a.d = n_slots, n_active, n_groups, n_states, d
+    a.active = active.data_ptr() if active is not None else None
+    a.q_scale = float(q_scale)
+    a.state = state.data_ptr()
+    a.st_slot, a.st_group, a.st_state = state.stride(0), state.stride(1), state.stride(2)
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.sq_slot, a.sq_group = q.stride(0), q.stride(1)
+    a.sk_slot, a.sk_group = k.stride(0), k.stride(1)
+    a.sv_slot, a.sv_group = v.stride(0), v.stride(1)
+    a.gamma = gamma.data_ptr()
+    a.sg_slot, a.sg_group, a.sg_state = gamma.stride()
+    if rot is not None:
+        a.rot = rot.data_ptr()
+        a.sr_slot, a.sr_group, a.sr_state = rot.stride(0), rot.stride(1), rot.stride(2)
+    a.y = y.data_ptr()
+    a.sy_slot, a.sy_group = y.stride(0), y.stride(1)
+    L = _lib.lib()
+    with torch.cuda.device(state.device):
+        _lib.check(L.qpam_decode_step(a, _lib.stream_ptr(state.device)), "qpam_decode_step")
+    return y
+
+
+def recur_step_additive(memory_state, decay_gamma, value_t, key_t, query_t):
+    """Drop-in for V11PAMLayer._recur_step_additive (v11/model.py:927-965),
+    head-scalar decay.  memory_state [..., d, d, 2], decay_gamma [...],
+    value_t/key_t/query_t [..., d, 2] (query already scaled).
+    Returns (output [..., d, 2], new memory_state); the input is not modified."""
+    if decay_gamma.dim() != memory_state.dim() - 3:
+        raise NotImplementedError("per-channel decay (E1) is not on the HIP decode path")
+    lead = memory_state.shape[:-3]
+    d = memory_state.shape[-2]
+    new_state = memory_state.to(torch.float32).contiguous().clone().view(-1, 1, 1, d, d, 2)
+    n = new_state.shape[0]
+
+    def flat(t):
+        return t.to(torch.float32).contiguous().view(n, 1, d, 2)
+
+    y = decode_step(new_state, flat(query_t), flat(key_t), flat(value_t),
+                    decay_gamma.to(torch.float32).contiguous().view(n, 1, 1), q_scale=1.0)
+    return (y.view(*lead, d, 2).to(memory_state.dtype),
+            new_state.view(*lead, d, d, 2).to(memory_state.dtype))

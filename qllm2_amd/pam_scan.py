@@ -1,0 +1,310 @@
+"""Chunked dual-form PAM scan on the HIP kernels (qpam_scan_fwd / qpam_scan_bwd).
+
+Planar API: every complex tensor is a pair of real planes.  q, k, v are
+[B, H, T, d] (any strides with d contiguous), fp32 or bf16; gamma is fp32
+[M, B, H, T]; optional rot (r_m = alpha_m e^{i phi_m}) is a pair of fp32
+[M, B, H, T] planes; optional s0 is a pair of fp32 [M, B, H, d, d] planes.
+Outputs Y (fp32 planes [B, H, T, d]) and the final state S (fp32 planes
+[M, B, H, d, d]).  Math: v11/model.py:378-417 (M = 1) and 657-781 (M > 1).
+
+The ops are registered with torch.library (custom_op + register_fake +
+register_autograd) so autograd and torch.compile see them as single nodes.
+
+Chunking: the kernels run chunks of 16, 32 or 64 steps.  With gamma + 1e-6 < 1
+the chunked result does not depend on the chunk length (every term is a
+product of (gamma + 1e-6) factors), so a reference chunk_size outside
+{16, 32} runs with 64-step chunks; see chunk_for().
+"""
+
+from typing import List, Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+KERNEL_CHUNKS = (16, 32, 64)
+
+# Optional EventPair whose events the next forward records around its
+# dominant (chunk-output) kernel; set by benchmarks, cleared after use.
+_PROFILE = {"fwd": None}
+
+
+def set_profile_events(pair):
+    """Arm a _lib.EventPair to be recorded around the next forward's
+    chunk-output kernel (benchmark instrumentation)."""
+    _PROFILE["fwd"] = pair
+
+
+def chunk_for(chunk_size: int, seq_len: int) -> int:
+    """Kernel chunk length used for a reference chunk_size."""
+    if chunk_size in (16, 32):
+        return chunk_size
+    return 64
+
+
+def _dtype_code(t):
+    if t.dtype == torch.float32:
+        return _lib.QPAM_F32
+    if t.dtype == torch.bfloat16:
+        return _lib.QPAM_BF16
+    raise ValueError(f"qpam scan: q/k/v must be fp32 or bf16, got {t.dtype}")
+
+
+def _aligned_plane(t):
+    vec = 4 if t.dtype == torch.float32 else 8
+    ok = t.stride(-1) == 1 and all(s % vec == 0 for s in t.stride()[:-1]) and t.data_ptr() % 16 == 0
+    return t if ok else t.contiguous()
+
+
+def _cview(re, im):
+    if re.stride() != im.stride():
+        im = im.contiguous() if re.is_contiguous() else im
+        re = re.contiguous()
+        im = im.contiguous()
+    v = _lib.CView()
+    v.re, v.im = re.data_ptr(), im.data_ptr()
+    v.s0, v.s1, v.s2 = re.stride(0), re.stride(1), re.stride(2)
+    return v, re, im
+
+
+def _mview(re, im):
+    v = _lib.MView()
+    v.re, v.im = re.data_ptr(), im.data_ptr()
+    v.s0, v.s1, v.s2 = re.stride(0), re.stride(1), re.stride(2)
+    return v
+
+
+def _fill_args(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk):
+    M, B, H, T = gamma.shape
+    d = q_re.shape[-1]
+    a = _lib.ScanArgs()
+    a.B, a.H, a.T, a.d, a.C, a.M = B, H, T, d, chunk, M
+    a.dtype = _dtype_code(q_re)
+    a.q_scale = float(q_scale)
+    keep = []
+    for name, (re, im) in (("q", (q_re, q_im)), ("k", (k_re, k_im)), ("v", (v_re, v_im))):
+        view, re, im = _cview(_aligned_plane(re), _aligned_plane(im))
+        keep += [re, im]
+        setattr(a, name, view)
+    a.gamma = gamma.data_ptr()
+    a.sg_m, a.sg_b, a.sg_h, a.sg_t = gamma.stride()
+    if rot_re is not None:
+        if rot_re.stride() != rot_im.stride():
+            rot_re, rot_im = rot_re.contiguous(), rot_im.contiguous()
+        keep += [rot_re, rot_im]
+        a.rot_re, a.rot_im = rot_re.data_ptr(), rot_im.data_ptr()
+        a.sr_m, a.sr_b, a.sr_h, a.sr_t = rot_re.stride()
+    if s0_re is not None:
+        s0_re, s0_im = s0_re.contiguous(), s0_im.contiguous()
+        keep += [s0_re, s0_im]
+        a.s0_re, a.s0_im = s0_re.data_ptr(), s0_im.data_ptr()
+    return a, keep
+
+
+def _validate(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, chunk):
+    if chunk not in KERNEL_CHUNKS:
+        raise ValueError(f"kernel chunk must be one of {KERNEL_CHUNKS}")
+    if gamma.dim() != 4:
+        raise ValueError("gamma must be [M, B, H, T]")
+    M, B, H, T = gamma.shape
+    for t in (q_re, q_im, k_re, k_im, v_re, v_im):
+        if t.dim() != 4 or tuple(t.shape[:3]) != (B, H, T):
+            raise ValueError(f"q/k/v planes must be [B={B}, H={H}, T={T}, d], got {tuple(t.shape)}")
+        if t.dtype != q_re.dtype:
+            raise ValueError("q, k, v must share one dtype")
+        if not t.is_cuda:
+            raise ValueError("qpam scan: tensors must be on the GPU (no CPU path in this library)")
+    if gamma.dtype != torch.float32:
+        raise ValueError("gamma must be fp32")
+    if q_re.shape[-1] != 64:
+        raise NotImplementedError("the HIP scan supports head_dim 64")
+    if M > 4:
+        raise NotImplementedError("the HIP scan supports up to 4 states")
+    for t in (rot_re, rot_im):
+        if t is not None and (tuple(t.shape) != (M, B, H, T) or t.dtype != torch.float32):
+            raise ValueError("rot planes must be fp32 [M, B, H, T]")
+    for t in (s0_re, s0_im):
+        if t is not None and (tuple(t.shape) != (M, B, H, 64, 64) or t.dtype != torch.float32):
+            raise ValueError("s0 planes must be fp32 [M, B, H, 64, 64]")
+
+
+@torch.library.custom_op("qpam::scan_fwd", mutates_args=())
+def scan_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Tensor, v_im: Tensor,
+                gamma: Tensor, rot_re: Optional[Tensor], rot_im: Optional[Tensor], s0_re: Optional[Tensor],
+                s0_im: Optional[Tensor], q_scale: float, chunk: int) -> List[Tensor]:
+    """Returns [y_re, y_im, s_re, s_im, workspace]; the workspace keeps the
+    per-chunk entering states for the backward."""
+    _validate(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, chunk)
+    M, B, H, T = gamma.shape
+    d = q_re.shape[-1]
+    dev = q_re.device
+    a, keep = _fill_args(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk)
+    y_re = torch.empty(B, H, T, d, device=dev, dtype=torch.float32)
+    y_im = torch.empty_like(y_re)
+    s_re = torch.empty(M, B, H, d, d, device=dev, dtype=torch.float32)
+    s_im = torch.empty_like(s_re)
+    a.y = _mview(y_re, y_im)
+    a.s_re, a.s_im = s_re.data_ptr(), s_im.data_ptr()
+    L = _lib.lib()
+    nbytes = L.qpam_scan_workspace_size(a)
+    ws = torch.empty((nbytes + 3) // 4, device=dev, dtype=torch.float32)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
+    prof = _PROFILE["fwd"]
+    if prof is not None:
+        a.prof_ev[0], a.prof_ev[1] = prof.ev[0], prof.ev[1]
+        _PROFILE["fwd"] = None
+    with torch.cuda.device(dev):
+        _lib.check(L.qpam_scan_fwd(a, _lib.stream_ptr(dev)), "qpam_scan_fwd")
+    del keep
+    return [y_re, y_im, s_re, s_im, ws]
+
+
+@scan_fwd_op.register_fake
+def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk):
+    M, B, H, T = gamma.shape
+    d = q_re.shape[-1]
+    n = (T + chunk - 1) // chunk
+    y = q_re.new_empty(B, H, T, d, dtype=torch.float32)
+    s = q_re.new_empty(M, B, H, d, d, dtype=torch.float32)
+    ws = q_re.new_empty(M * B * H * n * (2 * d * d + 1), dtype=torch.float32)
+    return [y, torch.empty_like(y), s, torch.empty_like(s), ws]
+
+
+@torch.library.custom_op("qpam::scan_bwd", mutates_args=())
+def scan_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Tensor, v_im: Tensor,
+                gamma: Tensor, rot_re: Optional[Tensor], rot_im: Optional[Tensor], s0_re: Optional[Tensor],
+                s0_im: Optional[Tensor], q_scale: float, chunk: int, ws: Tensor, dy_re: Tensor, dy_im: Tensor,
+                ds_re: Optional[Tensor], ds_im: Optional[Tensor]) -> List[Tensor]:
+    """Returns [dq_re, dq_im, dk_re, dk_im, dv_re, dv_im, dgamma, drot_re, drot_im, ds0_re, ds0_im]
+    (drot/ds0 are empty tensors when rot/s0 were not given)."""
+    M, B, H, T = gamma.shape
+    d = q_re.shape[-1]
+    dev = q_re.device
+    a, keep = _fill_args(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
+    bw = _lib.ScanBwdArgs()
+    bw.fwd = _lib.ctypes.pointer(a)
+    dy_re, dy_im = dy_re.contiguous(), dy_im.contiguous()
+    bw.dy, _, _ = _cview(dy_re, dy_im)
+    if ds_re is not None:
+        ds_re, ds_im = ds_re.contiguous(), ds_im.contiguous()
+        bw.ds_re, bw.ds_im = ds_re.data_ptr(), ds_im.data_ptr()
+    outs = [torch.empty(B, H, T, d, device=dev, dtype=q_re.dtype) for _ in range(6)]
+    bw.dq = _mview(outs[0], outs[1])
+    bw.dk = _mview(outs[2], outs[3])
+    bw.dv = _mview(outs[4], outs[5])
+    dgamma = torch.empty(M, B, H, T, device=dev, dtype=torch.float32)
+    bw.dgamma = dgamma.data_ptr()
+    if rot_re is not None:
+        drot_re = torch.empty(M, B, H, T, device=dev, dtype=torch.float32)
+        drot_im = torch.empty_like(drot_re)
+        bw.drot_re, bw.drot_im = drot_re.data_ptr(), drot_im.data_ptr()
+    else:
+        drot_re = drot_im = torch.empty(0, device=dev)
+    if s0_re is not None:
+        ds0_re = torch.empty(M, B, H, d, d, device=dev, dtype=torch.float32)
+        ds0_im = torch.empty_like(ds0_re)
+        bw.ds0_re, bw.ds0_im = ds0_re.data_ptr(), ds0_im.data_ptr()
+    else:
+        ds0_re = ds0_im = torch.empty(0, device=dev)
+    L = _lib.lib()
+    nbytes = L.qpam_scan_bwd_workspace_size(bw)
+    ws2 = torch.empty((nbytes + 3) // 4 + 1, device=dev, dtype=torch.float32)
+    bw.workspace, bw.workspace_bytes = ws2.data_ptr(), ws2.numel() * 4
+    with torch.cuda.device(dev):
+        _lib.check(L.qpam_scan_bwd(bw, _lib.stream_ptr(dev)), "qpam_scan_bwd")
+    del keep
+    return outs + [dgamma, drot_re, drot_im, ds0_re, ds0_im]
+
+
+@scan_bwd_op.register_fake
+def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk, ws, dy_re,
+      dy_im, ds_re, ds_im):
+    M, B, H, T = gamma.shape
+    d = q_re.shape[-1]
+    outs = [q_re.new_empty(B, H, T, d) for _ in range(6)]
+    dg = gamma.new_empty(M, B, H, T)
+    dr = [gamma.new_empty(M, B, H, T) if rot_re is not None else gamma.new_empty(0) for _ in range(2)]
+    d0 = [gamma.new_empty(M, B, H, d, d) if s0_re is not None else gamma.new_empty(0) for _ in range(2)]
+    return outs + [dg] + dr + d0
+
+
+def _setup_context(ctx, inputs, output):
+    (q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk) = inputs
+    ctx.save_for_backward(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, output[4])
+    ctx.q_scale, ctx.chunk = q_scale, chunk
+
+
+def _backward(ctx, grads):
+    (q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, ws) = ctx.saved_tensors
+    dy_re, dy_im, ds_re, ds_im = grads[0], grads[1], grads[2], grads[3]
+    if dy_re is None:
+        dy_re = torch.zeros_like(q_re, dtype=torch.float32)
+    if dy_im is None:
+        dy_im = torch.zeros_like(q_re, dtype=torch.float32)
+    if ds_re is None and ds_im is None:
+        ds_re_t = ds_im_t = None
+    else:
+        ds_re_t = ds_re if ds_re is not None else torch.zeros_like(ds_im)
+        ds_im_t = ds_im if ds_im is not None else torch.zeros_like(ds_re)
+    g = scan_bwd_op(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, ctx.q_scale,
+                    ctx.chunk, ws, dy_re, dy_im, ds_re_t, ds_im_t)
+    drot = (g[7], g[8]) if rot_re is not None else (None, None)
+    ds0 = (g[9], g[10]) if s0_re is not None else (None, None)
+    return (g[0], g[1], g[2], g[3], g[4], g[5], g[6], drot[0], drot[1], ds0[0], ds0[1], None, None)
+
+
+scan_fwd_op.register_autograd(_backward, setup_context=_setup_context)
+
+
+def pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, *, q_scale, chunk=64, rot=None, s0=None):
+    """Differentiable planar scan.  Returns (y_re, y_im, s_re, s_im).
+
+    Head dims below 64 are zero-padded to 64 (exact: padded key/query columns
+    add nothing to q.k*, padded value rows stay zero) and sliced back."""
+    rot_re, rot_im = rot if rot is not None else (None, None)
+    s0_re, s0_im = s0 if s0 is not None else (None, None)
+    d = q_re.shape[-1]
+    if d < 64:
+        if 64 % d:
+            raise NotImplementedError(f"head_dim {d}: the HIP scan pads head dims dividing 64")
+        pad = 64 - d
+        q_re, q_im, k_re, k_im, v_re, v_im = (torch.nn.functional.pad(x, (0, pad))
+                                              for x in (q_re, q_im, k_re, k_im, v_re, v_im))
+        if s0_re is not None:
+            s0_re, s0_im = (torch.nn.functional.pad(x, (0, pad, 0, pad)) for x in (s0_re, s0_im))
+    out = scan_fwd_op(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im,
+                      float(q_scale), int(chunk))
+    y_re, y_im, s_re, s_im = out[0], out[1], out[2], out[3]
+    if d < 64:
+        y_re, y_im = y_re[..., :d], y_im[..., :d]
+        s_re, s_im = s_re[..., :d, :d], s_im[..., :d, :d]
+    return y_re, y_im, s_re, s_im
+
+
+def _planes(z):
+    return z[..., 0], z[..., 1]
+
+
+def pam_scan_interleaved(queries, keys, values, gamma_all, head_dim, chunk_size, *, rot=None, s0=None,
+                         scale_queries=True):
+    """Split-real [..., d, 2] front end: queries/keys/values [B,H,T,d,2],
+    gamma_all [M,B,H,T]; rot optional (re, im) planes [M,B,H,T]; s0 optional
+    [M,B,H,d,d,2].  Returns (Y [B,H,T,d,2], S [M,B,H,d,d,2]) in the input dtype."""
+    dtype = queries.dtype
+    work = torch.bfloat16 if dtype == torch.bfloat16 else torch.float32
+    qr, qi = (x.to(work) for x in _planes(queries))
+    kr, ki = (x.to(work) for x in _planes(keys))
+    vr, vi = (x.to(work) for x in _planes(values))
+    s0p = None
+    if s0 is not None:
+        s0p = (s0[..., 0].float(), s0[..., 1].float())
+    rotp = (rot[0].float(), rot[1].float()) if rot is not None else None
+    t = queries.shape[2]
+    y_re, y_im, s_re, s_im = pam_scan_planar(
+        qr, qi, kr, ki, vr, vi, gamma_all.float(), q_scale=head_dim ** -0.5 if scale_queries else 1.0,
+        chunk=chunk_for(chunk_size, t), rot=rotp, s0=s0p)
+    y = torch.stack([y_re, y_im], dim=-1).to(dtype)
+    s = torch.stack([s_re, s_im], dim=-1).to(dtype)
+    return y, s

@@ -1,0 +1,80 @@
+"""CPU checks of the C ABI boundary: the built library loads (no GPU needed to
+dlopen it), exports every function include/qpam.h declares, the ctypes
+structures match the header's field lists, and the product path refuses CPU
+tensors instead of falling back."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from qllm2_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qpam.h")
+
+
+def _header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(qpam_\w+)\s*\(", text, flags=re.M)))
+
+
+def _header_struct_fields(name):
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    m = re.search(r"typedef struct \{([^{}]*)\}\s*" + name + ";", text)
+    assert m, name
+    fields = []
+    for decl in m.group(1).split(";"):
+        decl = decl.strip()
+        if not decl:
+            continue
+        decl = re.sub(r"^(const\s+)?\w+\s*", "", decl)
+        for part in decl.split(","):
+            part = part.strip().lstrip("*").strip()
+            part = re.sub(r"\[.*\]", "", part)
+            fields.append(part)
+    return fields
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = _header_functions()
+    assert "qpam_decode_step" in names and "qpam_scan_fwd" in names and "qpam_ce_fwd" in names
+    for n in names:
+        assert hasattr(lib, n), f"libqpam.so does not export {n}"
+        assert n in _lib.SIGNATURES, f"ctypes binding misses {n}"
+    assert set(_lib.SIGNATURES) == set(names)
+    assert lib.qpam_version() == _lib.ABI_VERSION
+
+
+@pytest.mark.parametrize("cname,pyname", [
+    ("qpam_decode_args", "DecodeArgs"), ("qpam_scan_args", "ScanArgs"), ("qpam_scan_bwd_args", "ScanBwdArgs"),
+    ("qpam_ce_fwd_args", "CeFwdArgs"), ("qpam_ce_bwd_args", "CeBwdArgs"),
+])
+def test_ctypes_structs_match_header(cname, pyname):
+    py = [f[0] for f in getattr(_lib, pyname)._fields_]
+    assert py == _header_struct_fields(cname)
+
+
+def test_errors_surface_as_exceptions_without_gpu():
+    lib = _lib.lib()
+    a = _lib.DecodeArgs()  # all zero: invalid sizes -> status, message, no launch
+    st = lib.qpam_decode_step(ctypes.byref(a), None)
+    assert st != 0
+    assert b"qpam_decode_step" in lib.qpam_last_error()
+    with pytest.raises(_lib.QpamError):
+        _lib.check(st, "qpam_decode_step")
+
+
+def test_cpu_tensors_are_refused():
+    from qllm2_amd import decode, pam_scan
+    s = torch.zeros(1, 1, 1, 4, 4, 2)
+    q = torch.zeros(1, 1, 4, 2)
+    with pytest.raises(ValueError, match="GPU"):
+        decode.decode_step(s, q, q, q, torch.zeros(1, 1, 1))
+    x = torch.zeros(1, 1, 8, 64)
+    with pytest.raises(ValueError, match="GPU"):
+        pam_scan.pam_scan_planar(x, x, x, x, x, x, torch.ones(1, 1, 1, 8), q_scale=0.125)

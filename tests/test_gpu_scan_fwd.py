@@ -1,0 +1,97 @@
+"""GPU parity of the chunked scan forward (qpam_scan_fwd) against the CPU oracle.
+
+Tolerances (north star): fp32 inputs rel <= 1e-4 on Y and S; bf16 inputs with
+fp32 state rel <= 2e-2.  The oracle runs in float64 on the same (rounded)
+inputs; for bf16 it consumes the bf16-rounded values.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import pam as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    return ((a.double() - b.double()).abs().max() / (b.double().abs().max() + 1e-30)).item()
+
+
+def _planes(x, dtype):
+    return x[..., 0].contiguous().to(dtype).cuda(), x[..., 1].contiguous().to(dtype).cuda()
+
+
+def _run(q, k, v, gamma, d, chunk, dtype=torch.float32, rot=None, s0=None):
+    from qllm2_amd.pam_scan import pam_scan_planar
+    qr, qi = _planes(q, dtype)
+    kr, ki = _planes(k, dtype)
+    vr, vi = _planes(v, dtype)
+    rotp = (rot[0].float().cuda(), rot[1].float().cuda()) if rot is not None else None
+    s0p = (s0[..., 0].float().cuda().contiguous(), s0[..., 1].float().cuda().contiguous()) if s0 is not None else None
+    y_re, y_im, s_re, s_im = pam_scan_planar(qr, qi, kr, ki, vr, vi, gamma.float().cuda(), q_scale=d ** -0.5,
+                                             chunk=chunk, rot=rotp, s0=s0p)
+    torch.cuda.synchronize()
+    return (torch.stack([y_re, y_im], -1).cpu(), torch.stack([s_re, s_im], -1).cpu())
+
+
+def test_config1_parity_chunked_and_recurrent(gpu_lib):
+    """Config 1: B=1, T=128, H=4, d=32, C=32, fp32; chunked oracle and the exact
+    recurrence (which differs from the chunked form by the reference's +1e-6)."""
+    B, H, T, d, C = 1, 4, 128, 32, 32
+    q, k, v, gamma = O.make_scan_inputs(B, H, T, d, 1001, qkv_std=1 / math.sqrt(2 * d), dtype=torch.float32)
+    y, s = _run(q, k, v, gamma, d, C)
+    y_ref, s_ref = O.chunked_head(q.double(), k.double(), v.double(), gamma[0].double(), d, C)
+    assert _rel(y, y_ref) < 1e-4 and _rel(s[0], s_ref) < 1e-4
+    yb, _ = O.brute_force_scan(O.to_complex(q), O.to_complex(k), O.to_complex(v), gamma[0].double().numpy(),
+                               d ** -0.5)
+    assert _rel(y, O.from_complex(yb)) < 1e-4
+
+
+@pytest.mark.parametrize("T,C", [(64, 64), (200, 64), (100, 32), (70, 16), (2048, 64)])
+def test_single_state_fp32(gpu_lib, T, C):
+    B, H, d = 2, 3, 64
+    q, k, v, gamma = O.make_scan_inputs(B, H, T, d, 2000 + T + C, unit_qk=True, dtype=torch.float32)
+    y, s = _run(q, k, v, gamma, d, C)
+    y_ref, s_ref = O.chunked_head(q.double(), k.double(), v.double(), gamma[0].double(), d, C)
+    assert _rel(y, y_ref) < 1e-4
+    assert _rel(s[0], s_ref) < 1e-4
+
+
+def test_multistate_rotation_and_initial_state_fp32(gpu_lib):
+    M, B, H, T, d, C = 3, 2, 2, 150, 64, 64
+    q, k, v, gamma = O.make_scan_inputs(B, H, T, d, 31, m_states=M, gamma_mu=2.0, gamma_mu_step=1.0,
+                                        unit_qk=True, dtype=torch.float32)
+    g = torch.Generator().manual_seed(5)
+    phase = torch.randn(M, B, H, T, generator=g)
+    routing = torch.rand(M, B, H, T, generator=g) + 0.5
+    s0 = torch.randn(M, B, H, d, d, 2, generator=g) * 0.1
+    rot = (routing * torch.cos(phase), routing * torch.sin(phase))
+    y, s = _run(q, k, v, gamma, d, C, rot=rot, s0=s0)
+    y_ref, s_ref = O.multistate_fused(q.double(), k.double(), v.double(), gamma.double(), phase.double(),
+                                      routing.double(), d, C, state=s0.double())
+    assert _rel(y, y_ref) < 1e-4 and _rel(s, s_ref) < 1e-4
+
+
+def test_config2_full_size_fp32(gpu_lib):
+    """Config 2: B=8, T=2048, H=12, d=64, C=64, unit-norm q,k, fp32 planar."""
+    B, H, T, d, C = 8, 12, 2048, 64, 64
+    q, k, v, gamma = O.make_scan_inputs(B, H, T, d, 1002, unit_qk=True, dtype=torch.float32)
+    y, s = _run(q, k, v, gamma, d, C)
+    y_ref, s_ref = O.chunked_head(q.double(), k.double(), v.double(), gamma[0].double(), d, C)
+    assert _rel(y, y_ref) < 1e-4
+    assert _rel(s[0], s_ref) < 1e-4
+
+
+def test_e3_bf16_inputs(gpu_lib):
+    """Config-3 shape family (smaller B): M=3, bf16 q/k/v, fp32 state, rel 2e-2."""
+    M, B, H, T, d, C = 3, 2, 2, 512, 64, 64
+    q, k, v, gamma = O.make_scan_inputs(B, H, T, d, 1003, m_states=M, gamma_mu=2.0, gamma_mu_step=1.0,
+                                        unit_qk=True, dtype=torch.float32)
+    qb, kb, vb = (x.to(torch.bfloat16) for x in (q, k, v))
+    y, s = _run(qb, kb, vb, gamma, d, C, dtype=torch.bfloat16)
+    ones, zeros = torch.ones_like(gamma), torch.zeros_like(gamma)
+    y_ref, s_ref = O.multistate_fused(qb.double(), kb.double(), vb.double(), gamma.double(), zeros.double(),
+                                      ones.double(), d, C)
+    assert _rel(y, y_ref) < 2e-2 and _rel(s, s_ref) < 2e-2

@@ -15,7 +15,15 @@ import torch
 
 from oracle import pam as O
 
-torch.set_default_dtype(torch.float64)
+
+
+@pytest.fixture(autouse=True)
+def _float64_default():
+    # the oracle pins run in float64; restore the default so other test modules are unaffected
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float64)
+    yield
+    torch.set_default_dtype(old)
 
 
 def _inputs(B, H, T, d, seed, **kw):

@@ -1,0 +1,824 @@
+// Chunked dual-form PAM scan, backward (fp32 MFMA, d = 64).
+//
+// The reference obtains these gradients with torch autograd through
+// _forward_chunked_head / _fused_chunk_step (v11/model.py:378-417, 657-737)
+// and the closed-form decay-matrix backward (v11/triton_kernels.py:447-480).
+// Per chunk, with G_Y = dL/dY, G'_m = dL/dS_m after the chunk, S_m the state
+// entering it, A = W . D~, rho_m = r_m cum_m:
+//   dA   = G_Y V^H                    gW = dA . conj(D~)   gD~ = dA . conj(W)
+//   dQ~ += gW K + sum_m conj(rho_m) (G_Y conj(S_m))
+//   dK  += gW^H Q~ + sum_m dl_m . (V conj(G'_m))
+//   dV  += A^H G_Y + sum_m dl_m . (K G'_m^T)
+//   dS_m = total_m G'_m + sum_t conj(rho_m[t]) G_Y[t] (x) conj(Q~[t])
+// and the log-decay gradient collects D (rows +, columns -), cum, total and
+// decay_last contributions before a reverse cumsum and 1/(gamma + 1e-6).
+//
+// Launches (mirroring the forward):
+//   1. grad_chunk_state (chunk-parallel): the per-chunk dS increment;
+//   2. grad_state_scan  (reverse, elementwise): dS after every chunk, dS0;
+//   3. query_side (chunk-parallel, wave = query tile): dQ, d rot, the decay
+//      gradient of D and cum -> partial dL/dL_t in the workspace;
+//   4. key_side (chunk-parallel, wave = key tile): dK, dV, the decay_last and
+//      total gradients, and the final d gamma of the chunk.
+#include "scan_common.h"
+
+namespace qpam {
+namespace scan {
+
+int validate_scan(const qpam_scan_args *a, const char *who, bool fwd_outputs);
+size_t fwd_workspace_bytes(const qpam_scan_args &a);
+
+namespace {
+
+struct BwdParams {
+    qpam_scan_args a;
+    qpam_cview dy;           // fp32
+    const float *ds_re, *ds_im;
+    qpam_mview dq, dk, dv;   // element type = input dtype
+    float *dgamma;
+    float *drot_re, *drot_im;
+    float *ds0_re, *ds0_im;
+    int n_chunks;
+    const float *states;     // forward: state entering each chunk
+    const float *totals;     // forward: chunk decay totals
+    float *gstates;          // dS increment per chunk -> dS after each chunk
+    float *gl;               // [M][B][H][n*C] partial dL/dL_t (query side)
+};
+
+__device__ __forceinline__ int64_t chain_idx(const BwdParams &p, int m, int b, int h) {
+    return ((int64_t)m * p.a.B + b) * p.a.H + h;
+}
+__device__ __forceinline__ const float *fstate(const BwdParams &p, int m, int b, int h, int c) {
+    return p.states + (chain_idx(p, m, b, h) * p.n_chunks + c) * (2 * D * D);
+}
+__device__ __forceinline__ float *gstate(const BwdParams &p, int m, int b, int h, int c) {
+    return p.gstates + (chain_idx(p, m, b, h) * p.n_chunks + c) * (2 * D * D);
+}
+__device__ __forceinline__ float ftotal(const BwdParams &p, int m, int b, int h, int c) {
+    return p.totals[chain_idx(p, m, b, h) * p.n_chunks + c];
+}
+
+template <typename T>
+__device__ __forceinline__ void store_elem(float *base, int64_t idx, float v);
+template <>
+__device__ __forceinline__ void store_elem<float>(float *base, int64_t idx, float v) {
+    base[idx] = v;
+}
+template <>
+__device__ __forceinline__ void store_elem<unsigned short>(float *base, int64_t idx, float v) {
+    reinterpret_cast<unsigned short *>(base)[idx] = f32_to_bf16(v);
+}
+
+// contiguous 64x64 fp32 plane -> LDS (pitch P)
+__device__ __forceinline__ void load_state_plane(float *lds, const float *src) {
+    for (int idx = threadIdx.x; idx < D * 16; idx += THREADS) {
+        const int r = idx >> 4, c4 = idx & 15;
+        const float4 v = *reinterpret_cast<const float4 *>(src + r * D + 4 * c4);
+        float *dst = lds + r * P + 4 * c4;
+        dst[0] = v.x;
+        dst[1] = v.y;
+        dst[2] = v.z;
+        dst[3] = v.w;
+    }
+}
+
+// Per-chunk prologue shared by the chunk-parallel backward kernels: log-decay
+// prefix sums and rotations of every state (wave 0).
+__device__ __forceinline__ void chunk_decay_prologue(const qpam_scan_args &a, int b, int h, int c0, int valid,
+                                                     float *sL, float *sRr, float *sRi) {
+    const int lane = threadIdx.x & 63;
+    for (int m = 0; m < a.M; ++m) {
+        const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
+        sL[m * 64 + lane] = chunk_log_prefix(gp, a.sg_t, valid, lane);
+        float rr = 1.f, ri = 0.f;
+        if (a.rot_re && lane < valid) {
+            const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + lane) * a.sr_t;
+            rr = a.rot_re[ro];
+            ri = a.rot_im[ro];
+        }
+        sRr[m * 64 + lane] = rr;
+        sRi[m * 64 + lane] = ri;
+    }
+}
+
+// ---------------------------------------------------------------- kernel 1 --
+// dS increment of chunk c: dG_m[i][j] = sum_t conj(rho_m[t]) G_Y[t][i] conj(Q~[t][j])
+template <typename Tin, int C>
+__global__ void __launch_bounds__(THREADS) grad_chunk_state_kernel(BwdParams p) {
+    extern __shared__ float smem[];
+    float *sGr = smem, *sGi = sGr + C * P, *sQr = sGi + C * P, *sQi = sQr + C * P;
+    float *sL = sQi + C * P, *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * C, valid = min(C, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+
+    if (c == 0 && a.s0_re == nullptr) {  // no initial state: chunk 0 carries nothing
+        for (int m = 0; m < a.M; ++m) {
+            float *dst = gstate(p, m, b, h, 0);
+            for (int e = tid; e < 2 * D * D / 4; e += THREADS)
+                reinterpret_cast<float4 *>(dst)[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        return;
+    }
+    const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
+    const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+    load_tile<float>(sGr, (const float *)p.dy.re + go, p.dy.s2, C, valid, 1.f);
+    load_tile<float>(sGi, (const float *)p.dy.im + go, p.dy.s2, C, valid, 1.f);
+    load_tile<Tin>(sQr, (const Tin *)a.q.re + qo, a.q.s2, C, valid, a.q_scale);
+    load_tile<Tin>(sQi, (const Tin *)a.q.im + qo, a.q.s2, C, valid, a.q_scale);
+    if (w == 0) chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
+    __syncthreads();
+
+    for (int m = 0; m < a.M; ++m) {
+        floatx4 accR[4], accI[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
+#pragma unroll 4
+        for (int ks = 0; ks < C / 4; ++ks) {
+            const int t = 4 * ks + g;
+            const float cum = (t < valid) ? __expf(sL[m * 64 + t]) : 0.f;
+            const float wr = sRr[m * 64 + t] * cum, wi = -sRi[m * 64 + t] * cum;  // conj(rho)
+            const float gr = sGr[t * P + 16 * w + l16], gi = sGi[t * P + 16 * w + l16];
+            const float vr = wr * gr - wi * gi, vi = wr * gi + wi * gr;
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                const float qr = sQr[t * P + 16 * jt + l16];
+                const float qi = sQi[t * P + 16 * jt + l16];
+                accR[jt] = mfma4(vr, qr, accR[jt]);
+                accR[jt] = mfma4(vi, qi, accR[jt]);
+                accI[jt] = mfma4(vi, qr, accI[jt]);
+                accI[jt] = mfma4(vr, -qi, accI[jt]);
+            }
+        }
+        float *dst = gstate(p, m, b, h, c);
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 16 * w + 4 * g + r, j = 16 * jt + l16;
+                dst[i * D + j] = accR[jt][r];
+                dst[D * D + i * D + j] = accI[jt][r];
+            }
+    }
+}
+
+// ---------------------------------------------------------------- kernel 2 --
+// Reverse scan: G = dS_final; for c = n-1..0: slot[c] <- G (dS after chunk c),
+// G = total_c G + increment_c.  At the end G = dS0.
+__global__ void __launch_bounds__(THREADS) grad_state_scan_kernel(BwdParams p) {
+    const qpam_scan_args &a = p.a;
+    const int chain = blockIdx.x >> 3;
+    const int e4 = ((blockIdx.x & 7) << 8) + threadIdx.x;
+    const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
+    const int b = bh / a.H, h = bh % a.H;
+    const int plane = e4 >> 10, off = (e4 & 1023) * 4;
+    const int64_t so = (int64_t)chain * D * D + off;
+
+    float4 G = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (p.ds_re) G = *reinterpret_cast<const float4 *>((plane ? p.ds_im : p.ds_re) + so);
+    float *base = gstate(p, m, b, h, 0) + plane * D * D + off;
+    const int n = p.n_chunks;
+    float4 nxt = *reinterpret_cast<const float4 *>(base + (int64_t)(n - 1) * 2 * D * D);
+    for (int c = n - 1; c >= 0; --c) {
+        const float4 inc = nxt;
+        if (c > 0) nxt = *reinterpret_cast<const float4 *>(base + (int64_t)(c - 1) * 2 * D * D);
+        *reinterpret_cast<float4 *>(base + (int64_t)c * 2 * D * D) = G;
+        const float t = ftotal(p, m, b, h, c);
+        G.x = t * G.x + inc.x;
+        G.y = t * G.y + inc.y;
+        G.z = t * G.z + inc.z;
+        G.w = t * G.w + inc.w;
+    }
+    if (p.ds0_re) *reinterpret_cast<float4 *>((plane ? p.ds0_im : p.ds0_re) + so) = G;
+}
+
+// ---------------------------------------------------------------- kernel 3 --
+template <typename Tin, int C>
+__global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
+    extern __shared__ float smem[];
+    float *sQr = smem, *sQi = sQr + C * P;
+    float *sKr = sQi + C * P, *sKi = sKr + C * P;
+    float *sVr = sKi + C * P, *sVi = sVr + D * P;  // V tile, later the state S_m
+    float *sGr = sVi + D * P, *sGi = sGr + C * P;
+    float *sL = sGi + C * P, *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+    float *sGL = sRi + MAX_M * 64, *sDRr = sGL + MAX_M * 64, *sDRi = sDRr + MAX_M * 64;
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * C, valid = min(C, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const bool carry = (c > 0) || (a.s0_re != nullptr);
+    const int M = a.M;
+
+    {
+        const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+        const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+        const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
+        load_tile<Tin>(sQr, (const Tin *)a.q.re + qo, a.q.s2, C, valid, a.q_scale);
+        load_tile<Tin>(sQi, (const Tin *)a.q.im + qo, a.q.s2, C, valid, a.q_scale);
+        load_tile<Tin>(sKr, (const Tin *)a.k.re + ko, a.k.s2, C, valid, 1.f);
+        load_tile<Tin>(sKi, (const Tin *)a.k.im + ko, a.k.s2, C, valid, 1.f);
+        load_tile<Tin>(sVr, (const Tin *)a.v.re + vo, a.v.s2, C, valid, 1.f);
+        load_tile<Tin>(sVi, (const Tin *)a.v.im + vo, a.v.s2, C, valid, 1.f);
+        load_tile<float>(sGr, (const float *)p.dy.re + go, p.dy.s2, C, valid, 1.f);
+        load_tile<float>(sGi, (const float *)p.dy.im + go, p.dy.s2, C, valid, 1.f);
+    }
+    if (w == 0) chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
+    for (int e = tid; e < 3 * MAX_M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
+    __syncthreads();
+
+    const int tt = w;
+    const bool active = tt < C / 16;
+    floatx4 gqR[4], gqI[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) gqR[jt] = gqI[jt] = zero4();
+
+    if (active) {
+        const int t = 16 * tt + l16;  // this lane's query row in the transposed tiles
+        floatx4 wr[4], wi[4], dr[4], di[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) wr[st] = wi[st] = dr[st] = di[st] = zero4();
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const float4 bq_r = *reinterpret_cast<const float4 *>(sQr + t * P + 16 * q4 + 4 * g);
+            const float4 bq_i = *reinterpret_cast<const float4 *>(sQi + t * P + 16 * q4 + 4 * g);
+            const float4 bg_r = *reinterpret_cast<const float4 *>(sGr + t * P + 16 * q4 + 4 * g);
+            const float4 bg_i = *reinterpret_cast<const float4 *>(sGi + t * P + 16 * q4 + 4 * g);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > tt || 16 * st >= C) continue;
+                const int s = 16 * st + l16;
+                const float4 ak_r = *reinterpret_cast<const float4 *>(sKr + s * P + 16 * q4 + 4 * g);
+                const float4 ak_i = *reinterpret_cast<const float4 *>(sKi + s * P + 16 * q4 + 4 * g);
+                const float4 av_r = *reinterpret_cast<const float4 *>(sVr + s * P + 16 * q4 + 4 * g);
+                const float4 av_i = *reinterpret_cast<const float4 *>(sVi + s * P + 16 * q4 + 4 * g);
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    // W^T[s][t] = sum_j q~[t,j] conj(k[s,j])
+                    wr[st] = mfma4(ak_r[kk], bq_r[kk], wr[st]);
+                    wr[st] = mfma4(ak_i[kk], bq_i[kk], wr[st]);
+                    wi[st] = mfma4(ak_r[kk], bq_i[kk], wi[st]);
+                    wi[st] = mfma4(-ak_i[kk], bq_r[kk], wi[st]);
+                    // dA^T[s][t] = sum_i G[t,i] conj(v[s,i])
+                    dr[st] = mfma4(av_r[kk], bg_r[kk], dr[st]);
+                    dr[st] = mfma4(av_i[kk], bg_i[kk], dr[st]);
+                    di[st] = mfma4(av_r[kk], bg_i[kk], di[st]);
+                    di[st] = mfma4(-av_i[kk], bg_r[kk], di[st]);
+                }
+            }
+        }
+        // elementwise decay algebra; lane holds s = 16st + 4g + r, t = 16tt + l16
+        float rowp[MAX_M], grr[MAX_M], gri[MAX_M];
+#pragma unroll
+        for (int m = 0; m < MAX_M; ++m) rowp[m] = grr[m] = gri[m] = 0.f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            if (st > tt || 16 * st >= C) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int s = 16 * st + 4 * g + r;
+                float gwr = 0.f, gwi = 0.f;
+                float colp[MAX_M];
+#pragma unroll
+                for (int m = 0; m < MAX_M; ++m) colp[m] = 0.f;
+                if (s <= t) {
+                    float Dm[MAX_M], nc[MAX_M];
+                    float dtr = 0.f, dti = 0.f;
+#pragma unroll
+                    for (int m = 0; m < MAX_M; ++m) {
+                        Dm[m] = nc[m] = 0.f;
+                        if (m < M) {
+                            const float x = sL[m * 64 + t] - sL[m * 64 + s];
+                            Dm[m] = __expf(fminf(x, 0.f));
+                            nc[m] = (x <= 0.f && s != t) ? 1.f : 0.f;  // diagonal: +g and -g cancel
+                            dtr += sRr[m * 64 + t] * Dm[m];
+                            dti += sRi[m * 64 + t] * Dm[m];
+                        }
+                    }
+                    const float Ar = dr[st][r], Ai = di[st][r];   // dA
+                    const float Wr = wr[st][r], Wi = wi[st][r];   // W
+                    gwr = Ar * dtr + Ai * dti;                    // dA conj(D~)
+                    gwi = Ai * dtr - Ar * dti;
+                    const float gdr = Ar * Wr + Ai * Wi;          // dA conj(W)
+                    const float gdi = Ai * Wr - Ar * Wi;
+#pragma unroll
+                    for (int m = 0; m < MAX_M; ++m) {
+                        if (m < M) {
+                            const float gdm = gdr * sRr[m * 64 + t] + gdi * sRi[m * 64 + t];
+                            const float gp = gdm * Dm[m] * nc[m];
+                            rowp[m] += gp;
+                            colp[m] = -gp;
+                            grr[m] += gdr * Dm[m];
+                            gri[m] += gdi * Dm[m];
+                        }
+                    }
+                }
+                // column sums over the 16 query rows of this tile (lanes sharing g)
+#pragma unroll
+                for (int m = 0; m < MAX_M; ++m) {
+                    if (m < M) {
+                        float x = colp[m];
+#pragma unroll
+                        for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off);
+                        if (l16 == 0) atomicAdd(&sGL[m * 64 + s], x);
+                    }
+                }
+                wr[st][r] = gwr;
+                wi[st][r] = gwi;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MAX_M; ++m) {
+            if (m < M) {
+                float x = rowp[m], yr = grr[m], yi = gri[m];
+                x += __shfl_xor(x, 16);
+                x += __shfl_xor(x, 32);
+                yr += __shfl_xor(yr, 16);
+                yr += __shfl_xor(yr, 32);
+                yi += __shfl_xor(yi, 16);
+                yi += __shfl_xor(yi, 32);
+                if (g == 0) {
+                    atomicAdd(&sGL[m * 64 + t], x);
+                    atomicAdd(&sDRr[m * 64 + t], yr);
+                    atomicAdd(&sDRi[m * 64 + t], yi);
+                }
+            }
+        }
+        // intra dQ~[t][j] += sum_s gW[t,s] K[s,j]
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            if (st > tt || 16 * st >= C) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int s = 16 * st + 4 * g + r;
+                const float ar = wr[st][r], ai = wi[st][r];
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) {
+                    const float kr = sKr[s * P + 16 * jt + l16];
+                    const float ki = sKi[s * P + 16 * jt + l16];
+                    gqR[jt] = mfma4(ar, kr, gqR[jt]);
+                    gqR[jt] = mfma4(-ai, ki, gqR[jt]);
+                    gqI[jt] = mfma4(ar, ki, gqI[jt]);
+                    gqI[jt] = mfma4(ai, kr, gqI[jt]);
+                }
+            }
+        }
+    }
+
+    // carried read: X_m = G_Y conj(S_m); dQ~ += conj(rho_m) X_m; g_rho_m[t] = sum_j conj(q~[t,j]) X_m[t,j]
+    if (carry) {
+        for (int m = 0; m < M; ++m) {
+            __syncthreads();
+            const float *src = fstate(p, m, b, h, c);
+            load_state_plane(sVr, src);
+            load_state_plane(sVi, src + D * D);
+            __syncthreads();
+            if (!active) continue;
+            const int t = 16 * tt + l16;
+            floatx4 xr[4], xi[4];
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) xr[jt] = xi[jt] = zero4();
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 ag_r = *reinterpret_cast<const float4 *>(sGr + t * P + 16 * q4 + 4 * g);
+                const float4 ag_i = *reinterpret_cast<const float4 *>(sGi + t * P + 16 * q4 + 4 * g);
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const int i = 16 * q4 + 4 * g + kk;
+#pragma unroll
+                    for (int jt = 0; jt < 4; ++jt) {
+                        const float sr = sVr[i * P + 16 * jt + l16], si = sVi[i * P + 16 * jt + l16];
+                        xr[jt] = mfma4(ag_r[kk], sr, xr[jt]);
+                        xr[jt] = mfma4(ag_i[kk], si, xr[jt]);
+                        xi[jt] = mfma4(ag_i[kk], sr, xi[jt]);
+                        xi[jt] = mfma4(-ag_r[kk], si, xi[jt]);
+                    }
+                }
+            }
+            // lane holds X[t' = 16tt + 4g + r][j = 16jt + l16]
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tr = 16 * tt + 4 * g + r;
+                const float cum = __expf(sL[m * 64 + tr]);
+                const float rr = sRr[m * 64 + tr], ri = sRi[m * 64 + tr];
+                const float rhr = rr * cum, rhi = ri * cum;
+                float pr = 0.f, pi = 0.f;
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) {
+                    const float x_r = xr[jt][r], x_i = xi[jt][r];
+                    gqR[jt][r] += rhr * x_r + rhi * x_i;  // conj(rho) X
+                    gqI[jt][r] += rhr * x_i - rhi * x_r;
+                    const float qr = sQr[tr * P + 16 * jt + l16], qi = sQi[tr * P + 16 * jt + l16];
+                    pr += qr * x_r + qi * x_i;  // conj(q~) X
+                    pi += qr * x_i - qi * x_r;
+                }
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) {
+                    pr += __shfl_xor(pr, off);
+                    pi += __shfl_xor(pi, off);
+                }
+                if (l16 == 0) {
+                    atomicAdd(&sDRr[m * 64 + tr], pr * cum);
+                    atomicAdd(&sDRi[m * 64 + tr], pi * cum);
+                    atomicAdd(&sGL[m * 64 + tr], (pr * rr + pi * ri) * cum);  // Re(g_rho conj(r)) cum
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    if (active) {
+        const int64_t qo = b * p.dq.s0 + h * p.dq.s1 + (int64_t)c0 * p.dq.s2;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * tt + 4 * g + r;
+                if (t < valid) {
+                    const int64_t o = qo + (int64_t)t * p.dq.s2 + 16 * jt + l16;
+                    store_elem<Tin>(p.dq.re, o, gqR[jt][r] * a.q_scale);
+                    store_elem<Tin>(p.dq.im, o, gqI[jt][r] * a.q_scale);
+                }
+            }
+    }
+    if (tid < 64 && tid < valid) {
+        for (int m = 0; m < M; ++m) {
+            p.gl[chain_idx(p, m, b, h) * (int64_t)p.n_chunks * C + c0 + tid] = sGL[m * 64 + tid];
+            if (p.drot_re) {
+                const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + tid) * a.sr_t;
+                p.drot_re[ro] = sDRr[m * 64 + tid];
+                p.drot_im[ro] = sDRi[m * 64 + tid];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- kernel 4 --
+template <typename Tin, int C>
+__global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
+    extern __shared__ float smem[];
+    float *sQr = smem, *sQi = sQr + D * P;           // Q~ tile, later G'_m
+    float *sKr = sQi + D * P, *sKi = sKr + C * P;
+    float *sVr = sKi + C * P, *sVi = sVr + C * P;
+    float *sGr = sVi + C * P, *sGi = sGr + D * P;    // G_Y tile, later S_m
+    float *sL = sGi + D * P, *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+    float *sGL = sRi + MAX_M * 64, *sDl = sGL + MAX_M * 64;
+    float *sRed = sDl + MAX_M * 64;                  // [4] wave partials
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * C, valid = min(C, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const bool carry = (c > 0) || (a.s0_re != nullptr);
+    const int M = a.M;
+
+    {
+        const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+        const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+        const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
+        load_tile<Tin>(sQr, (const Tin *)a.q.re + qo, a.q.s2, C, valid, a.q_scale);
+        load_tile<Tin>(sQi, (const Tin *)a.q.im + qo, a.q.s2, C, valid, a.q_scale);
+        load_tile<Tin>(sKr, (const Tin *)a.k.re + ko, a.k.s2, C, valid, 1.f);
+        load_tile<Tin>(sKi, (const Tin *)a.k.im + ko, a.k.s2, C, valid, 1.f);
+        load_tile<Tin>(sVr, (const Tin *)a.v.re + vo, a.v.s2, C, valid, 1.f);
+        load_tile<Tin>(sVi, (const Tin *)a.v.im + vo, a.v.s2, C, valid, 1.f);
+        load_tile<float>(sGr, (const float *)p.dy.re + go, p.dy.s2, C, valid, 1.f);
+        load_tile<float>(sGi, (const float *)p.dy.im + go, p.dy.s2, C, valid, 1.f);
+    }
+    if (w == 0) {
+        chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
+        for (int m = 0; m < M; ++m) {
+            const float L = sL[m * 64 + lane];
+            const float Llast = sL[m * 64 + valid - 1];
+            sDl[m * 64 + lane] = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
+            sGL[m * 64 + lane] =
+                (lane < valid) ? p.gl[chain_idx(p, m, b, h) * (int64_t)p.n_chunks * C + c0 + lane] : 0.f;
+        }
+    }
+    __syncthreads();
+
+    const int st = w;  // key rows s in [16st, 16st+16)
+    const bool active = st < C / 16;
+    floatx4 gvR[4], gvI[4], gkR[4], gkI[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) gvR[it] = gvI[it] = gkR[it] = gkI[it] = zero4();
+
+    if (active) {
+        const int s = 16 * st + l16;  // this lane's key row as MFMA B operand
+        floatx4 wr[4], wi[4], dr[4], di[4];  // W[t][s], dA[t][s] for t-tiles tt >= st
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) wr[tt] = wi[tt] = dr[tt] = di[tt] = zero4();
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const float4 bk_r = *reinterpret_cast<const float4 *>(sKr + s * P + 16 * q4 + 4 * g);
+            const float4 bk_i = *reinterpret_cast<const float4 *>(sKi + s * P + 16 * q4 + 4 * g);
+            const float4 bv_r = *reinterpret_cast<const float4 *>(sVr + s * P + 16 * q4 + 4 * g);
+            const float4 bv_i = *reinterpret_cast<const float4 *>(sVi + s * P + 16 * q4 + 4 * g);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                if (tt < st || 16 * tt >= C) continue;
+                const int t = 16 * tt + l16;
+                const float4 aq_r = *reinterpret_cast<const float4 *>(sQr + t * P + 16 * q4 + 4 * g);
+                const float4 aq_i = *reinterpret_cast<const float4 *>(sQi + t * P + 16 * q4 + 4 * g);
+                const float4 ag_r = *reinterpret_cast<const float4 *>(sGr + t * P + 16 * q4 + 4 * g);
+                const float4 ag_i = *reinterpret_cast<const float4 *>(sGi + t * P + 16 * q4 + 4 * g);
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    wr[tt] = mfma4(aq_r[kk], bk_r[kk], wr[tt]);
+                    wr[tt] = mfma4(aq_i[kk], bk_i[kk], wr[tt]);
+                    wi[tt] = mfma4(aq_i[kk], bk_r[kk], wi[tt]);
+                    wi[tt] = mfma4(-aq_r[kk], bk_i[kk], wi[tt]);
+                    dr[tt] = mfma4(ag_r[kk], bv_r[kk], dr[tt]);
+                    dr[tt] = mfma4(ag_i[kk], bv_i[kk], dr[tt]);
+                    di[tt] = mfma4(ag_i[kk], bv_r[kk], di[tt]);
+                    di[tt] = mfma4(-ag_r[kk], bv_i[kk], di[tt]);
+                }
+            }
+        }
+        // lane holds t = 16tt + 4g + r, s = 16st + l16: A = W D~ -> (wr, wi); gW = dA conj(D~) -> (dr, di)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            if (tt < st || 16 * tt >= C) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * tt + 4 * g + r;
+                float dtr = 0.f, dti = 0.f;
+                if (s <= t) {
+#pragma unroll
+                    for (int m = 0; m < MAX_M; ++m) {
+                        if (m < M) {
+                            const float Dm = __expf(fminf(sL[m * 64 + t] - sL[m * 64 + s], 0.f));
+                            dtr += sRr[m * 64 + t] * Dm;
+                            dti += sRi[m * 64 + t] * Dm;
+                        }
+                    }
+                }
+                const float Wr = wr[tt][r], Wi = wi[tt][r], Ar = dr[tt][r], Ai = di[tt][r];
+                wr[tt][r] = Wr * dtr - Wi * dti;
+                wi[tt][r] = Wr * dti + Wi * dtr;
+                dr[tt][r] = Ar * dtr + Ai * dti;
+                di[tt][r] = Ai * dtr - Ar * dti;
+            }
+        }
+        // dV[s][i] += sum_t conj(A[t,s]) G[t,i];  dK[s][j] += sum_t conj(gW[t,s]) Q~[t,j]
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            if (tt < st || 16 * tt >= C) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * tt + 4 * g + r;
+                const float ar = wr[tt][r], ai = wi[tt][r], gr_ = dr[tt][r], gi_ = di[tt][r];
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const float yr = sGr[t * P + 16 * it + l16], yi = sGi[t * P + 16 * it + l16];
+                    gvR[it] = mfma4(ar, yr, gvR[it]);
+                    gvR[it] = mfma4(ai, yi, gvR[it]);
+                    gvI[it] = mfma4(ar, yi, gvI[it]);
+                    gvI[it] = mfma4(-ai, yr, gvI[it]);
+                    const float qr = sQr[t * P + 16 * it + l16], qi = sQi[t * P + 16 * it + l16];
+                    gkR[it] = mfma4(gr_, qr, gkR[it]);
+                    gkR[it] = mfma4(gi_, qi, gkR[it]);
+                    gkI[it] = mfma4(gr_, qi, gkI[it]);
+                    gkI[it] = mfma4(-gi_, qr, gkI[it]);
+                }
+            }
+        }
+    }
+
+    // state-write gradients: G'_m = dS after this chunk
+    for (int m = 0; m < M; ++m) {
+        __syncthreads();
+        const float *gsrc = gstate(p, m, b, h, c);
+        load_state_plane(sQr, gsrc);
+        load_state_plane(sQi, gsrc + D * D);
+        if (carry) {
+            const float *ssrc = fstate(p, m, b, h, c);
+            load_state_plane(sGr, ssrc);
+            load_state_plane(sGi, ssrc + D * D);
+        }
+        __syncthreads();
+        // g_total = sum Re(conj(G') S)
+        if (carry) {
+            float part = 0.f;
+            for (int e = tid; e < D * D; e += THREADS) {
+                const int i = e >> 6, j = e & 63;
+                part += sQr[i * P + j] * sGr[i * P + j] + sQi[i * P + j] * sGi[i * P + j];
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+            if (lane == 0) sRed[w] = part;
+        }
+        if (active) {
+            const int s = 16 * st + l16;
+            const float dls = sDl[m * 64 + s];
+            // Z[s][i] = sum_j K[s,j] G'[i,j]
+            floatx4 zr[4], zi[4];
+#pragma unroll
+            for (int it = 0; it < 4; ++it) zr[it] = zi[it] = zero4();
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const float4 ak_r = *reinterpret_cast<const float4 *>(sKr + s * P + 16 * q4 + 4 * g);
+                const float4 ak_i = *reinterpret_cast<const float4 *>(sKi + s * P + 16 * q4 + 4 * g);
+                const float4 av_r = *reinterpret_cast<const float4 *>(sVr + s * P + 16 * q4 + 4 * g);
+                const float4 av_i = *reinterpret_cast<const float4 *>(sVi + s * P + 16 * q4 + 4 * g);
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const int i = 16 * it + l16;
+                    const float4 bg_r = *reinterpret_cast<const float4 *>(sQr + i * P + 16 * q4 + 4 * g);
+                    const float4 bg_i = *reinterpret_cast<const float4 *>(sQi + i * P + 16 * q4 + 4 * g);
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) {
+                        zr[it] = mfma4(ak_r[kk], bg_r[kk], zr[it]);
+                        zr[it] = mfma4(-ak_i[kk], bg_i[kk], zr[it]);
+                        zi[it] = mfma4(ak_r[kk], bg_i[kk], zi[it]);
+                        zi[it] = mfma4(ak_i[kk], bg_r[kk], zi[it]);
+                    }
+                }
+                // dK[s][j] += dl[s] sum_i V[s,i] conj(G'[i,j])  (i = 16 q4 + 4 g + kk)
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    const int i = 16 * q4 + 4 * g + kk;
+                    const float vr = av_r[kk] * dls, vi = av_i[kk] * dls;
+#pragma unroll
+                    for (int jt = 0; jt < 4; ++jt) {
+                        const float gr_ = sQr[i * P + 16 * jt + l16], gi_ = sQi[i * P + 16 * jt + l16];
+                        gkR[jt] = mfma4(vr, gr_, gkR[jt]);
+                        gkR[jt] = mfma4(vi, gi_, gkR[jt]);
+                        gkI[jt] = mfma4(vi, gr_, gkI[jt]);
+                        gkI[jt] = mfma4(-vr, gi_, gkI[jt]);
+                    }
+                }
+            }
+            // lane holds Z[s' = 16st + 4g + r][i = 16it + l16]
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int sr_ = 16 * st + 4 * g + r;
+                const float dl = sDl[m * 64 + sr_];
+                float gdl = 0.f;
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const float z_r = zr[it][r], z_i = zi[it][r];
+                    const float vr = sVr[sr_ * P + 16 * it + l16], vi = sVi[sr_ * P + 16 * it + l16];
+                    gdl += vr * z_r + vi * z_i;
+                    gvR[it][r] += dl * z_r;
+                    gvI[it][r] += dl * z_i;
+                }
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) gdl += __shfl_xor(gdl, off);
+                if (l16 == 0 && sr_ < valid) {
+                    const float x = sL[m * 64 + valid - 1] - sL[m * 64 + sr_];
+                    const float gp = (x <= 0.f) ? gdl * dl : 0.f;
+                    if (sr_ != valid - 1) {
+                        atomicAdd(&sGL[m * 64 + valid - 1], gp);
+                        atomicAdd(&sGL[m * 64 + sr_], -gp);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (tid == 0 && carry) {
+            const float gtot = sRed[0] + sRed[1] + sRed[2] + sRed[3];
+            sGL[m * 64 + valid - 1] += gtot * __expf(sL[m * 64 + valid - 1]);
+        }
+    }
+    __syncthreads();
+
+    if (active) {
+        const int64_t ko = b * p.dk.s0 + h * p.dk.s1 + (int64_t)c0 * p.dk.s2;
+        const int64_t vo = b * p.dv.s0 + h * p.dv.s1 + (int64_t)c0 * p.dv.s2;
+#pragma unroll
+        for (int it = 0; it < 4; ++it)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int s = 16 * st + 4 * g + r;
+                if (s < valid) {
+                    const int64_t o1 = ko + (int64_t)s * p.dk.s2 + 16 * it + l16;
+                    store_elem<Tin>(p.dk.re, o1, gkR[it][r]);
+                    store_elem<Tin>(p.dk.im, o1, gkI[it][r]);
+                    const int64_t o2 = vo + (int64_t)s * p.dv.s2 + 16 * it + l16;
+                    store_elem<Tin>(p.dv.re, o2, gvR[it][r]);
+                    store_elem<Tin>(p.dv.im, o2, gvI[it][r]);
+                }
+            }
+    }
+    // d gamma: reverse cumsum of dL/dL_t inside the chunk, then / (gamma + 1e-6)
+    if (w == 0) {
+        for (int m = 0; m < M; ++m) {
+            float x = (lane < valid) ? sGL[m * 64 + lane] : 0.f;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_down(x, off);
+                if (lane + off < 64) x += y;
+            }
+            if (lane < valid) {
+                const int64_t go = m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)(c0 + lane) * a.sg_t;
+                p.dgamma[go] = x / (a.gamma[go] + LOG_EPS);
+            }
+        }
+    }
+}
+
+template <int C>
+size_t gcs_smem() { return (size_t)(4 * C * P + 3 * MAX_M * 64) * sizeof(float); }
+template <int C>
+size_t qside_smem() { return (size_t)(6 * C * P + 2 * D * P + 6 * MAX_M * 64) * sizeof(float); }
+template <int C>
+size_t kside_smem() { return (size_t)(4 * C * P + 4 * D * P + 5 * MAX_M * 64 + 4) * sizeof(float); }
+
+template <typename Tin, int C>
+int launch_bwd(const BwdParams &p, hipStream_t stream) {
+    const qpam_scan_args &a = p.a;
+    dim3 grid(p.n_chunks, a.H, a.B);
+    const size_t s1 = gcs_smem<C>(), s3 = qside_smem<C>(), s4 = kside_smem<C>();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_chunk_state_kernel<Tin, C>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)query_side_kernel<Tin, C>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_kernel<Tin, C>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
+    hipLaunchKernelGGL((grad_chunk_state_kernel<Tin, C>), grid, dim3(THREADS), s1, stream, p);
+    int st = launch_status("grad_chunk_state_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * 8), dim3(THREADS), 0, stream, p);
+    st = launch_status("grad_state_scan_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL((query_side_kernel<Tin, C>), grid, dim3(THREADS), s3, stream, p);
+    st = launch_status("query_side_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL((key_side_kernel<Tin, C>), grid, dim3(THREADS), s4, stream, p);
+    return launch_status("key_side_kernel");
+}
+
+size_t bwd_workspace_bytes(const qpam_scan_args &a) {
+    const int64_t n = (a.T + a.C - 1) / a.C;
+    const int64_t chains = (int64_t)a.M * a.B * a.H;
+    return (size_t)(chains * n * 2 * D * D + chains * n * a.C) * sizeof(float);
+}
+
+}  // namespace
+
+int scan_bwd(const qpam_scan_bwd_args *bw, hipStream_t stream) {
+    QPAM_REQUIRE(bw != nullptr && bw->fwd != nullptr, "qpam_scan_bwd: null args");
+    const qpam_scan_args *a = bw->fwd;
+    int st = validate_scan(a, "qpam_scan_bwd", false);
+    if (st) return st;
+    QPAM_REQUIRE(bw->dy.re && bw->dy.im && ((uintptr_t)bw->dy.re % 16) == 0 && ((uintptr_t)bw->dy.im % 16) == 0 &&
+                     bw->dy.s0 % 4 == 0 && bw->dy.s1 % 4 == 0 && bw->dy.s2 % 4 == 0,
+                 "qpam_scan_bwd: dy must be 16-byte aligned fp32 planes with strides multiple of 4");
+    QPAM_REQUIRE(bw->dq.re && bw->dq.im && bw->dk.re && bw->dk.im && bw->dv.re && bw->dv.im && bw->dgamma,
+                 "qpam_scan_bwd: null output");
+    QPAM_REQUIRE((bw->ds_re == nullptr) == (bw->ds_im == nullptr), "qpam_scan_bwd: ds needs both planes");
+    QPAM_REQUIRE((bw->drot_re == nullptr) == (bw->drot_im == nullptr), "qpam_scan_bwd: drot needs both planes");
+    QPAM_REQUIRE(bw->drot_re == nullptr || a->rot_re != nullptr, "qpam_scan_bwd: drot without rot");
+    QPAM_REQUIRE((bw->ds0_re == nullptr) == (bw->ds0_im == nullptr), "qpam_scan_bwd: ds0 needs both planes");
+    const uintptr_t al = (uintptr_t)bw->ds_re | (uintptr_t)bw->ds_im | (uintptr_t)bw->ds0_re | (uintptr_t)bw->ds0_im;
+    QPAM_REQUIRE(al % 16 == 0, "qpam_scan_bwd: state gradients must be 16-byte aligned");
+    QPAM_REQUIRE(bw->workspace && bw->workspace_bytes >= bwd_workspace_bytes(*a) &&
+                     ((uintptr_t)bw->workspace % 16) == 0,
+                 "qpam_scan_bwd: workspace needs %zu bytes (got %zu)", bwd_workspace_bytes(*a),
+                 bw->workspace_bytes);
+    BwdParams p;
+    p.a = *a;
+    p.dy = bw->dy;
+    p.ds_re = bw->ds_re;
+    p.ds_im = bw->ds_im;
+    p.dq = bw->dq;
+    p.dk = bw->dk;
+    p.dv = bw->dv;
+    p.dgamma = bw->dgamma;
+    p.drot_re = bw->drot_re;
+    p.drot_im = bw->drot_im;
+    p.ds0_re = bw->ds0_re;
+    p.ds0_im = bw->ds0_im;
+    p.n_chunks = (a->T + a->C - 1) / a->C;
+    const int64_t chains = (int64_t)a->M * a->B * a->H;
+    p.states = (const float *)a->workspace;
+    p.totals = p.states + chains * p.n_chunks * 2 * D * D;
+    p.gstates = (float *)bw->workspace;
+    p.gl = p.gstates + chains * p.n_chunks * 2 * D * D;
+    const bool bf = a->dtype == QPAM_BF16;
+    switch (a->C) {
+        case 16: return bf ? launch_bwd<unsigned short, 16>(p, stream) : launch_bwd<float, 16>(p, stream);
+        case 32: return bf ? launch_bwd<unsigned short, 32>(p, stream) : launch_bwd<float, 32>(p, stream);
+        default: return bf ? launch_bwd<unsigned short, 64>(p, stream) : launch_bwd<float, 64>(p, stream);
+    }
+}
+
+size_t scan_bwd_workspace(const qpam_scan_bwd_args *bw) {
+    return (bw && bw->fwd) ? bwd_workspace_bytes(*bw->fwd) : 0;
+}
+
+}  // namespace scan
+}  // namespace qpam
+
+extern "C" size_t qpam_scan_bwd_workspace_size(const qpam_scan_bwd_args *a) {
+    return qpam::scan::scan_bwd_workspace(a);
+}
+
+extern "C" int qpam_scan_bwd(const qpam_scan_bwd_args *a, void *stream) {
+    return qpam::scan::scan_bwd(a, (hipStream_t)stream);
+}

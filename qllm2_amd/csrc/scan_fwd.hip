@@ -348,7 +348,7 @@ size_t fwd_workspace_bytes(const qpam_scan_args &a) {
     return (size_t)(chains * n * 2 * D * D + chains * n) * sizeof(float);
 }
 
-int validate_scan(const qpam_scan_args *a, const char *who) {
+int validate_scan(const qpam_scan_args *a, const char *who, bool fwd_outputs) {
     QPAM_REQUIRE(a != nullptr, "%s: null args", who);
     QPAM_REQUIRE(a->B >= 1 && a->H >= 1 && a->T >= 1 && a->M >= 1, "%s: bad sizes B=%d H=%d T=%d M=%d", who, a->B,
                  a->H, a->T, a->M);
@@ -370,7 +370,7 @@ int validate_scan(const qpam_scan_args *a, const char *who) {
     QPAM_REQUIRE((a->rot_re == nullptr) == (a->rot_im == nullptr), "%s: rot needs both planes", who);
     QPAM_REQUIRE((a->s0_re == nullptr) == (a->s0_im == nullptr), "%s: s0 needs both planes", who);
     QPAM_REQUIRE((a->s_re == nullptr) == (a->s_im == nullptr), "%s: s_out needs both planes", who);
-    QPAM_REQUIRE(a->y.re && a->y.im, "%s: null y", who);
+    QPAM_REQUIRE(!fwd_outputs || (a->y.re && a->y.im), "%s: null y", who);
     const uintptr_t al = (uintptr_t)a->s0_re | (uintptr_t)a->s0_im | (uintptr_t)a->s_re | (uintptr_t)a->s_im;
     QPAM_REQUIRE(al % 16 == 0, "%s: state buffers must be 16-byte aligned", who);
     QPAM_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= fwd_workspace_bytes(*a) &&
@@ -380,7 +380,7 @@ int validate_scan(const qpam_scan_args *a, const char *who) {
 }
 
 int scan_fwd(const qpam_scan_args *a, hipStream_t stream) {
-    int st = validate_scan(a, "qpam_scan_fwd");
+    int st = validate_scan(a, "qpam_scan_fwd", true);
     if (st) return st;
     FwdParams p;
     p.a = *a;

@@ -4,10 +4,6 @@
 
 using qpam::fail;
 
-extern "C" size_t qpam_scan_bwd_workspace_size(const qpam_scan_bwd_args *) { return 0; }
-extern "C" int qpam_scan_bwd(const qpam_scan_bwd_args *, void *) {
-    return fail(QPAM_ERR_UNSUPPORTED, "qpam_scan_bwd: not built yet");
-}
 extern "C" int qpam_decay_matrix(int32_t, int32_t, const float *, int64_t, float *, void *) {
     return fail(QPAM_ERR_UNSUPPORTED, "qpam_decay_matrix: not built yet");
 }

@@ -201,13 +201,13 @@ def scan_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
         drot_im = torch.empty_like(drot_re)
         bw.drot_re, bw.drot_im = drot_re.data_ptr(), drot_im.data_ptr()
     else:
-        drot_re = drot_im = torch.empty(0, device=dev)
+        drot_re, drot_im = torch.empty(0, device=dev), torch.empty(0, device=dev)
     if s0_re is not None:
         ds0_re = torch.empty(M, B, H, d, d, device=dev, dtype=torch.float32)
         ds0_im = torch.empty_like(ds0_re)
         bw.ds0_re, bw.ds0_im = ds0_re.data_ptr(), ds0_im.data_ptr()
     else:
-        ds0_re = ds0_im = torch.empty(0, device=dev)
+        ds0_re, ds0_im = torch.empty(0, device=dev), torch.empty(0, device=dev)
     L = _lib.lib()
     nbytes = L.qpam_scan_bwd_workspace_size(bw)
     ws2 = torch.empty((nbytes + 3) // 4 + 1, device=dev, dtype=torch.float32)

@@ -1,0 +1,125 @@
+"""GPU parity of the scan backward (qpam_scan_bwd through torch autograd)
+against autograd of the CPU oracle, the way the reference gets its gradients.
+
+Loss = sum(Y * dY) + sum(S * dS) with seeded dY, dS.  Tolerances (north
+star): fp32 inputs rel <= 1e-4 on every gradient (max-abs relative to the
+reference gradient); bf16 inputs with fp32 state rel <= 2e-2.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import pam as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    return ((a.double() - b.double()).abs().max() / (b.double().abs().max() + 1e-30)).item()
+
+
+def _case(M, B, H, T, d, seed, with_rot, with_s0, dtype):
+    q, k, v, gamma = O.make_scan_inputs(B, H, T, d, seed, m_states=M, gamma_mu=2.0 if M > 1 else 3.0,
+                                        gamma_mu_step=1.0 if M > 1 else 0.0, unit_qk=True, dtype=torch.float32)
+    q, k, v = (x.to(dtype).to(torch.float32) for x in (q, k, v))  # rounded values both sides see
+    g = torch.Generator().manual_seed(seed + 1)
+    dy = torch.randn(B, H, T, d, 2, generator=g)
+    ds = torch.randn(M, B, H, d, d, 2, generator=g) * 0.1
+    phase = torch.randn(M, B, H, T, generator=g) if with_rot else torch.zeros(M, B, H, T)
+    routing = (torch.rand(M, B, H, T, generator=g) + 0.5) if with_rot else torch.ones(M, B, H, T)
+    s0 = torch.randn(M, B, H, d, d, 2, generator=g) * 0.1 if with_s0 else None
+    return q, k, v, gamma, dy, ds, phase, routing, s0
+
+
+def _oracle_grads(q, k, v, gamma, dy, ds, phase, routing, s0, d, C):
+    xs = [x.double().clone().requires_grad_(True) for x in (q, k, v, gamma, phase, routing)]
+    s0d = s0.double().clone().requires_grad_(True) if s0 is not None else None
+    y, s = O.multistate_fused(xs[0], xs[1], xs[2], xs[3], xs[4], xs[5], d, C, state=s0d)
+    ((y * dy.double()).sum() + (s * ds.double()).sum()).backward()
+    out = [x.grad for x in xs]
+    out.append(s0d.grad if s0d is not None else None)
+    return out
+
+
+def _gpu_grads(q, k, v, gamma, dy, ds, phase, routing, s0, d, C, dtype, with_rot):
+    from qllm2_amd.pam_scan import pam_scan_planar
+    dev = torch.device("cuda")
+
+    def leaf(x):
+        return x.to(dev).requires_grad_(True)
+
+    planes = [leaf(x[..., i].contiguous().to(dtype)) for x in (q, k, v) for i in (0, 1)]
+    gam = leaf(gamma.float())
+    ph, ro = leaf(phase.float()), leaf(routing.float())
+    rot = (ro * torch.cos(ph), ro * torch.sin(ph)) if with_rot else None
+    s0p = None
+    if s0 is not None:
+        s0r, s0i = leaf(s0[..., 0].contiguous()), leaf(s0[..., 1].contiguous())
+        s0p = (s0r, s0i)
+    y_re, y_im, s_re, s_im = pam_scan_planar(*planes, gam, q_scale=d ** -0.5, chunk=C, rot=rot, s0=s0p)
+    dyd, dsd = dy.to(dev), ds.to(dev)
+    loss = ((y_re * dyd[..., 0]).sum() + (y_im * dyd[..., 1]).sum() + (s_re * dsd[..., 0]).sum()
+            + (s_im * dsd[..., 1]).sum())
+    loss.backward()
+    torch.cuda.synchronize()
+
+    def cpx(a, b):
+        return torch.stack([a.grad.float(), b.grad.float()], -1).cpu()
+
+    out = [cpx(planes[0], planes[1]), cpx(planes[2], planes[3]), cpx(planes[4], planes[5]), gam.grad.cpu()]
+    out += [ph.grad.cpu() if with_rot else None, ro.grad.cpu() if with_rot else None]
+    out.append(torch.stack([s0p[0].grad, s0p[1].grad], -1).cpu() if s0 is not None else None)
+    return out
+
+
+NAMES = ["dq", "dk", "dv", "dgamma", "dphase", "drouting", "ds0"]
+
+
+@pytest.mark.parametrize("M,T,C,with_rot,with_s0", [
+    (1, 64, 64, False, False), (1, 200, 64, False, False), (1, 100, 32, False, True),
+    (3, 150, 64, True, True), (2, 70, 16, True, False),
+])
+def test_scan_backward_fp32(gpu_lib, M, T, C, with_rot, with_s0):
+    B, H, d = 2, 2, 64
+    case = _case(M, B, H, T, d, 3000 + M * 7 + T + C, with_rot, with_s0, torch.float32)
+    ref = _oracle_grads(*case, d, C)
+    got = _gpu_grads(*case, d, C, torch.float32, with_rot)
+    for name, a, b in zip(NAMES, got, ref):
+        if a is None or b is None:
+            continue
+        assert _rel(a, b) < 1e-4, f"{name}: rel {_rel(a, b):.2e}"
+
+
+def test_scan_backward_bf16_e3(gpu_lib):
+    M, B, H, T, d, C = 3, 2, 2, 512, 64, 64
+    case = _case(M, B, H, T, d, 3303, False, False, torch.bfloat16)
+    ref = _oracle_grads(*case, d, C)
+    got = _gpu_grads(*case, d, C, torch.bfloat16, False)
+    for name, a, b in zip(NAMES, got, ref):
+        if a is None or b is None:
+            continue
+        assert _rel(a, b) < 2e-2, f"{name}: rel {_rel(a, b):.2e}"
+
+
+def test_scan_backward_config3_full_size(gpu_lib):
+    """Config 3: E3 M=3, B=8, T=2048, H=12, d=64, C=64, bf16 q/k/v, fp32 state,
+    dY complex N(0,1); oracle autograd in fp32 on the bf16-rounded inputs."""
+    M, B, H, T, d, C = 3, 8, 12, 2048, 64, 64
+    q, k, v, gamma = O.make_scan_inputs(B, H, T, d, 1003, m_states=M, gamma_mu=2.0, gamma_mu_step=1.0,
+                                        unit_qk=True, dtype=torch.float32)
+    q, k, v = (x.to(torch.bfloat16).to(torch.float32) for x in (q, k, v))
+    g = torch.Generator().manual_seed(1003 + 1)
+    dy = torch.randn(B, H, T, d, 2, generator=g)
+    ds = torch.zeros(M, B, H, d, d, 2)
+    phase, routing = torch.zeros(M, B, H, T), torch.ones(M, B, H, T)
+    xs = [x.clone().requires_grad_(True) for x in (q, k, v, gamma)]
+    y, s = O.multistate_fused(xs[0], xs[1], xs[2], xs[3], phase, routing, d, C)
+    (y * dy).sum().backward()
+    ref = [x.grad for x in xs]
+    del y, s
+    got = _gpu_grads(q, k, v, gamma, dy, ds, phase, routing, None, d, C, torch.bfloat16, False)
+    for name, a, b in zip(NAMES[:4], got[:4], ref):
+        assert _rel(a, b) < 2e-2, f"{name}: rel {_rel(a, b):.2e}"
+        assert math.isfinite(a.abs().sum().item())

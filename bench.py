@@ -121,6 +121,71 @@ def bench_decode(n_steps):
             "bytes_per_step": bytes_step, "steps": n_steps}
 
 
+def bench_e3_fwd_bwd(steps, warmup):
+    """Config 3: E3 M=3 scan forward + backward, bf16 q/k/v, fp32 state."""
+    import torch
+    from qllm2_amd.pam_scan import pam_scan_planar
+    from oracle.pam import scan_flops
+    M, B, H, T, d, C = 3, 8, 12, 2048, 64, 64
+    (qr, qi), (kr, ki), (vr, vi), gamma = scan_inputs(B, H, T, d, M, 1003, torch.bfloat16, mu=2.0, mu_step=1.0)
+    leaves = [x.requires_grad_(True) for x in (qr, qi, kr, ki, vr, vi, gamma)]
+    gen = torch.Generator().manual_seed(1004)
+    dy = torch.randn(B, H, T, d, 2, generator=gen)
+    dy_re, dy_im = dy[..., 0].contiguous().cuda(), dy[..., 1].contiguous().cuda()
+
+    def step():
+        y_re, y_im, _, _ = pam_scan_planar(*leaves, q_scale=d ** -0.5, chunk=C)
+        torch.autograd.backward([y_re, y_im], [dy_re, dy_im])
+        for x in leaves:
+            x.grad = None
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = scan_flops(B, H, T, d, C, M, backward=True)
+    return {"ms_per_step": ms, "tokens_per_s": B * T / (ms * 1e-3), "tflops": flops / (ms * 1e-3) / 1e12,
+            "bf16_mfma_frac": flops / (ms * 1e-3) / MFMA_BF16_PEAK, "flops": flops,
+            "config": "M=3 B=8 T=2048 H=12 d=64 C=64 bf16 in, fp32 state, fwd+bwd"}
+
+
+def bench_ce(steps, warmup):
+    """Config 5: tied complex LM-head CE fwd+bwd, N=16384, D=1024, V=50261, bf16."""
+    import torch
+    from qllm2_amd.fused_ce import fused_linear_cross_entropy
+    from oracle.ce import ce_flops, make_ce_inputs
+    N, d_model, V = 16384, 512, 50261
+    h, w, t = make_ce_inputs(N, d_model, V, 1005, dtype=torch.bfloat16)
+    h, w, t = h.cuda().requires_grad_(True), w.cuda().requires_grad_(True), t.cuda()
+
+    def step():
+        loss = fused_linear_cross_entropy(h, w, t)
+        loss.backward()
+        h.grad = None
+        w.grad = None
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = ce_flops(N, V, 2 * d_model)
+    return {"ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3), "tflops": flops / (ms * 1e-3) / 1e12,
+            "bf16_mfma_frac": flops / (ms * 1e-3) / MFMA_BF16_PEAK, "flops": flops,
+            "config": "N=16384 D=1024 V=50261 bf16, chunk=4096, fwd+bwd"}
+
+
 def cpu_baseline_scan():
     """The reference's chunk loop restated on the CPU (oracle.pam.chunked_head),
     fp32, on a bounded sample: 1 of the 8 batch rows (H=12, T=2048)."""
@@ -174,7 +239,9 @@ def main():
                            "mfma_fp32_frac": flops / (ms * 1e-3) / MFMA_FP32_PEAK},
     }
     if not args.no_extras:
-        out["extras"] = {"decode_config4": bench_decode(args.decode_steps)}
+        out["extras"] = {"decode_config4": bench_decode(args.decode_steps),
+                         "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 2),
+                         "ce_fwd_bwd_config5": bench_ce(max(3, args.steps // 4), 2)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_scan()
     print(json.dumps(out), flush=True)

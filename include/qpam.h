@@ -169,9 +169,12 @@ int qpam_decay_matrix(int32_t n, int32_t t, const float *gamma, int64_t ldg, flo
 /* -------------------------------------------------------------------- CE --
  * Tied complex LM-head cross-entropy over hidden rows H [N, D] and weights
  * W [V, D] (row-major, leading dims ldh/ldw, bf16 or fp32), logits H W^T.
- * Forward writes per-row lse [N] and per-row loss [N] (0 on ignored rows,
- * times mask if given) and, if `stats` is non-NULL, the argmax-correct flag
- * per row; loss_sum (device scalar, optional) receives sum(loss).
+ * Forward writes per-row lse [N] and per-row loss [N] (0 on ignored rows and
+ * on targets outside [0, V); times mask if given) and, if `correct` is
+ * non-NULL, the argmax == target flag per row; loss_sum (optional, device
+ * float[2]) receives {sum(loss), denominator}, the denominator being
+ * sum(mask) or the number of rows whose target != ignore_index.  D must be a
+ * multiple of 32.
  * Backward computes dH = G W, dW += G^T H with G = (softmax - onehot) *
  * grad_scale[row] (grad_scale = g/denom * mask, 0 on ignored rows), processing
  * `chunk` rows at a time through a bf16 G buffer in the workspace.
@@ -187,7 +190,7 @@ typedef struct {
     float *lse;                    /* [N] */
     float *loss;                   /* [N] */
     float *correct;                /* optional [N], 1.0 where argmax == target */
-    float *loss_sum;               /* optional device scalar */
+    float *loss_sum;               /* optional device float[2] */
     void *workspace;
     size_t workspace_bytes;
 } qpam_ce_fwd_args;

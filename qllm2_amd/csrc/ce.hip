@@ -1,0 +1,572 @@
+// Tied complex LM-head cross-entropy (fused GEMM + softmax statistics).
+//
+// Reference: _FusedLinearCE (v11/fused_ce.py:26-82), linear_ce_per_token and
+// linear_ce_stats (v11/fused_ce.py:98-141), called from V11LM.ce_from_lm
+// (v11/model.py:1175-1190) with H = [lm_r | lm_i], W = [E_r | E_i] so that
+// H W^T = Re(h conj(E)^T).
+//
+// Forward: one MFMA GEMM tile per (128 rows, 128 vocab) whose epilogue reduces
+// the tile to per-row (max, sum exp, argmax); logits never leave registers.
+// A per-row finalize merges the vocab tiles into lse, adds the target logit
+// (a direct dot product) and writes the per-row loss; a single-block reduction
+// produces the loss sum and the denominator.
+// Backward, per `chunk` rows: the same GEMM recomputes the logits tile and its
+// epilogue writes G = (softmax - onehot) * scale in the input dtype, both as
+// G [rows][vocab] and G^T [vocab][rows]; then two plain GEMMs dH = G W and
+// dW += G^T H run with K-contiguous operands (W^T and H^T are transposed once
+// into the workspace).  The G buffers hold `chunk` rows, the reference's own
+// memory bound (it keeps chunk x V fp32 logits and softmax alive).
+#include <algorithm>
+
+#include "common.h"
+
+namespace qpam {
+namespace ce {
+namespace {
+
+constexpr int THREADS = 256;
+constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int VT = 128;  // vocab tile
+
+template <typename T> struct Mma;
+
+// bf16 inputs: v_mfma_f32_16x16x32_bf16, lane supplies 8 consecutive k
+template <> struct Mma<unsigned short> {
+    static constexpr int PITCH = BK + 8;  // elements per LDS row (80 bytes)
+    static constexpr int ROW16 = BK * 2 / 16;  // 16-byte chunks per tile row
+    __device__ __forceinline__ static void step(const unsigned short *sA, const unsigned short *sB, int arow0,
+                                                int brow0, floatx4 (&acc)[4][4], int l16, int g) {
+        bf16x8 af[4], bfr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            af[i] = *reinterpret_cast<const bf16x8 *>(sA + (arow0 + 16 * i + l16) * PITCH + 8 * g);
+            bfr[i] = *reinterpret_cast<const bf16x8 *>(sB + (brow0 + 16 * i + l16) * PITCH + 8 * g);
+        }
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni)
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], bfr[ni], acc[mi][ni], 0, 0, 0);
+    }
+};
+
+// fp32 inputs: v_mfma_f32_16x16x4_f32, k-steps use k = 16q + 4g + kk
+template <> struct Mma<float> {
+    static constexpr int PITCH = BK + 4;
+    static constexpr int ROW16 = BK * 4 / 16;
+    __device__ __forceinline__ static void step(const float *sA, const float *sB, int arow0, int brow0,
+                                                floatx4 (&acc)[4][4], int l16, int g) {
+#pragma unroll
+        for (int q = 0; q < BK / 16; ++q) {
+            float4 af[4], bfr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                af[i] = *reinterpret_cast<const float4 *>(sA + (arow0 + 16 * i + l16) * PITCH + 16 * q + 4 * g);
+                bfr[i] = *reinterpret_cast<const float4 *>(sB + (brow0 + 16 * i + l16) * PITCH + 16 * q + 4 * g);
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+                for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+                    for (int ni = 0; ni < 4; ++ni)
+                        acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[mi][kk], bfr[ni][kk], acc[mi][ni], 0,
+                                                                           0, 0);
+        }
+    }
+};
+
+template <typename T>
+constexpr size_t gemm_smem() { return (size_t)2 * (BM + BN) * Mma<T>::PITCH * sizeof(T); }
+
+// C[m][n] = sum_k A[m][k] B[n][k] for one BM x BN tile; A and B point at the
+// tile's first row; rows beyond a_rows / b_rows read as zero; K % BK == 0.
+// Wave w owns rows 64*(w>>1).., cols 64*(w&1)..; acc[mi][ni] lane holds
+// C[64*(w>>1) + 16mi + 4g + r][64*(w&1) + 16ni + l16].
+template <typename T>
+__device__ __forceinline__ void gemm_tile(const T *A, int64_t lda, int a_rows, const T *B, int64_t ldb, int b_rows,
+                                          int K, floatx4 (&acc)[4][4], T *smem) {
+    using MM = Mma<T>;
+    constexpr int PITCH = MM::PITCH, R16 = MM::ROW16, EPC = 16 / sizeof(T);
+    constexpr int LOADS = BM * R16 / THREADS;  // 16-byte loads per thread per operand
+    T *sA[2] = {smem, smem + (BM + BN) * PITCH};
+    T *sB[2] = {smem + BM * PITCH, smem + (BM + BN) * PITCH + BM * PITCH};
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int arow0 = 64 * (w >> 1), brow0 = 64 * (w & 1);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    uint4 ra[LOADS], rb[LOADS];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int ci = tid + i * THREADS, row = ci / R16, c = ci % R16;
+            ra[i] = (row < a_rows) ? *reinterpret_cast<const uint4 *>(A + row * lda + k0 + c * EPC)
+                                   : make_uint4(0, 0, 0, 0);
+            rb[i] = (row < b_rows) ? *reinterpret_cast<const uint4 *>(B + row * ldb + k0 + c * EPC)
+                                   : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int ci = tid + i * THREADS, row = ci / R16, c = ci % R16;
+            *reinterpret_cast<uint4 *>(sA[buf] + row * PITCH + c * EPC) = ra[i];
+            *reinterpret_cast<uint4 *>(sB[buf] + row * PITCH + c * EPC) = rb[i];
+        }
+    };
+    const int KT = K / BK;
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < KT) gload((kt + 1) * BK);
+        MM::step(sA[buf], sB[buf], arow0, brow0, acc, l16, g);
+        if (kt + 1 < KT) lstore(buf ^ 1);
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------ forward -----
+struct FwdParams {
+    qpam_ce_fwd_args a;
+    int n_vt;
+    float *part_m, *part_s;  // [N][n_vt]
+    int *part_i;             // [N][n_vt] argmax
+    float *red;              // [2] loss sum, denominator
+};
+
+template <typename T>
+__global__ void __launch_bounds__(THREADS) ce_fwd_tile_kernel(FwdParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    T *smem = reinterpret_cast<T *>(smem_raw);
+    __shared__ float sM[2][BM], sS[2][BM];
+    __shared__ int sI[2][BM];
+    const qpam_ce_fwd_args &a = p.a;
+    const int vt = blockIdx.x, rt = blockIdx.y;
+    const int r0 = rt * BM, v0 = vt * VT;
+    floatx4 acc[4][4];
+    gemm_tile<T>((const T *)a.h + (int64_t)r0 * a.ldh, a.ldh, min(BM, a.N - r0), (const T *)a.w + (int64_t)v0 * a.ldw,
+                 a.ldw, min(BN, a.V - v0), a.D, acc, smem);
+
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float mx = -INFINITY;
+            int ix = 0x7fffffff;
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const int v = v0 + 64 * wn + 16 * ni + l16;
+                const float x = (v < a.V) ? acc[mi][ni][r] : -INFINITY;
+                if (x > mx) { mx = x; ix = v; }
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) {
+                const float om = __shfl_xor(mx, off);
+                const int oi = __shfl_xor(ix, off);
+                if (om > mx || (om == mx && oi < ix)) { mx = om; ix = oi; }
+            }
+            float s = 0.f;
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const int v = v0 + 64 * wn + 16 * ni + l16;
+                if (v < a.V) s += __expf(acc[mi][ni][r] - mx);
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
+            if (l16 == 0) {
+                const int row = 64 * wm + 16 * mi + 4 * g + r;
+                sM[wn][row] = mx;
+                sS[wn][row] = s;
+                sI[wn][row] = ix;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < BM && r0 + tid < a.N) {
+        const float m0 = sM[0][tid], m1 = sM[1][tid];
+        const float m = fmaxf(m0, m1);
+        float s = 0.f;
+        if (m0 > -INFINITY) s += sS[0][tid] * __expf(m0 - m);
+        if (m1 > -INFINITY) s += sS[1][tid] * __expf(m1 - m);
+        const int i = (m1 > m0 || (m1 == m0 && sI[1][tid] < sI[0][tid])) ? sI[1][tid] : sI[0][tid];
+        const int64_t o = (int64_t)(r0 + tid) * p.n_vt + vt;
+        p.part_m[o] = m;
+        p.part_s[o] = s;
+        p.part_i[o] = i;
+    }
+}
+
+// one wave per row: merge the vocab tiles, add the target logit
+template <typename T>
+__global__ void __launch_bounds__(THREADS) ce_fwd_finalize_kernel(FwdParams p) {
+    const qpam_ce_fwd_args &a = p.a;
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6);
+    if (row >= a.N) return;
+    float m = -INFINITY, s = 0.f;
+    int ix = 0x7fffffff;
+    for (int vt = lane; vt < p.n_vt; vt += 64) {
+        const int64_t o = (int64_t)row * p.n_vt + vt;
+        const float pm = p.part_m[o], ps = p.part_s[o];
+        const int pi = p.part_i[o];
+        if (pm > m || (pm == m && pi < ix)) ix = pi;
+        const float nm = fmaxf(m, pm);
+        s = (m > -INFINITY ? s * __expf(m - nm) : 0.f) + (pm > -INFINITY ? ps * __expf(pm - nm) : 0.f);
+        m = nm;
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float om = __shfl_xor(m, off), os = __shfl_xor(s, off);
+        const int oi = __shfl_xor(ix, off);
+        const float nm = fmaxf(m, om);
+        const float ns = (m > -INFINITY ? s * __expf(m - nm) : 0.f) + (om > -INFINITY ? os * __expf(om - nm) : 0.f);
+        if (om > m || (om == m && oi < ix)) ix = oi;
+        m = nm;
+        s = ns;
+    }
+    const float lse = m + __logf(s);
+    const int64_t t = a.targets[row];
+    const bool valid = (t != a.ignore_index) && t >= 0 && t < a.V;
+    float dot = 0.f;
+    if (valid) {
+        const T *hr = (const T *)a.h + (int64_t)row * a.ldh;
+        const T *wr = (const T *)a.w + t * a.ldw;
+        for (int k = lane; k < a.D; k += 64) dot += Elem<T>::load(hr + k) * Elem<T>::load(wr + k);
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) dot += __shfl_xor(dot, off);
+    if (lane == 0) {
+        float loss = valid ? (lse - dot) : 0.f;
+        if (a.mask) loss *= a.mask[row];
+        a.lse[row] = lse;
+        a.loss[row] = loss;
+        if (a.correct) a.correct[row] = (valid && ix == t) ? 1.f : 0.f;
+    }
+}
+
+// deterministic single-block sum: red[0] = sum loss, red[1] = denominator
+__global__ void __launch_bounds__(1024) ce_reduce_kernel(FwdParams p) {
+    const qpam_ce_fwd_args &a = p.a;
+    __shared__ float s1[32], s2[32];
+    float x = 0.f, y = 0.f;
+    for (int r = threadIdx.x; r < a.N; r += 1024) {
+        x += a.loss[r];
+        if (a.mask) {
+            y += a.mask[r];
+        } else {
+            const int64_t t = a.targets[r];
+            y += (t != a.ignore_index) ? 1.f : 0.f;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        x += __shfl_xor(x, off);
+        y += __shfl_xor(y, off);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s1[threadIdx.x >> 6] = x;
+        s2[threadIdx.x >> 6] = y;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float tx = 0.f, ty = 0.f;
+        for (int i = 0; i < 16; ++i) {
+            tx += s1[i];
+            ty += s2[i];
+        }
+        a.loss_sum[0] = tx;
+        a.loss_sum[1] = ty;
+    }
+}
+
+// ----------------------------------------------------------- backward -----
+struct BwdParams {
+    qpam_ce_bwd_args a;
+    int Vp;          // vocab padded to VT
+    int Rp;          // chunk rows padded to BK
+    int row0;        // first row of the chunk
+    int rows;        // rows in the chunk
+    void *wt;        // [D][Vp]
+    void *gbuf;      // [rows][Vp]
+    void *gtbuf;     // [Vp][Rp]
+    void *ht;        // [D][Rp]
+};
+
+// out[c][r] = in[r][c] for an R x Cc tile grid (64 x 64 LDS tiles); rows >= R
+// and cols >= Cc of the (padded) output are written as zero.
+template <typename T>
+__global__ void __launch_bounds__(THREADS) transpose_kernel(const T *in, int64_t ldi, int R, int Cc, T *out,
+                                                           int64_t ldo, int out_rows, int out_cols) {
+    __shared__ T tile[64][65];
+    const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+    for (int e = threadIdx.x; e < 64 * 64; e += THREADS) {
+        const int rr = e >> 6, cc = e & 63;
+        const int r = r0 + rr, c = c0 + cc;
+        tile[rr][cc] = (r < R && c < Cc) ? in[(int64_t)r * ldi + c] : T(0);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < 64 * 64; e += THREADS) {
+        const int cc = e >> 6, rr = e & 63;
+        const int orow = c0 + cc, ocol = r0 + rr;
+        if (orow < out_rows && ocol < out_cols) out[(int64_t)orow * ldo + ocol] = tile[rr][cc];
+    }
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ unsigned short from_f32<unsigned short>(float x) { return f32_to_bf16(x); }
+
+// G tile: recompute logits, G = (exp(x - lse) - [v == t]) * scale; write G and G^T
+template <typename T>
+__global__ void __launch_bounds__(THREADS) ce_grad_tile_kernel(BwdParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    T *smem = reinterpret_cast<T *>(smem_raw);
+    __shared__ float sLse[BM], sScale[BM];
+    __shared__ int sTgt[BM];
+    const qpam_ce_bwd_args &a = p.a;
+    const int vt = blockIdx.x, rt = blockIdx.y;
+    const int lr0 = rt * BM, v0 = vt * VT;          // chunk-local row
+    const int tid = threadIdx.x;
+    if (tid < BM) {
+        const int lr = lr0 + tid, row = p.row0 + lr;
+        float lse = 0.f, sc = 0.f;
+        int tg = -1;
+        if (lr < p.rows) {
+            const int64_t t = a.targets[row];
+            const bool valid = (t != a.ignore_index) && t >= 0 && t < a.V;
+            lse = a.lse[row];
+            sc = valid ? a.grad_scale[0] * (a.mask ? a.mask[row] : 1.f) : 0.f;
+            tg = valid ? (int)t : -1;
+        }
+        sLse[tid] = lse;
+        sScale[tid] = sc;
+        sTgt[tid] = tg;
+    }
+    floatx4 acc[4][4];
+    gemm_tile<T>((const T *)a.h + (int64_t)(p.row0 + lr0) * a.ldh, a.ldh, min(BM, p.rows - lr0),
+                 (const T *)a.w + (int64_t)v0 * a.ldw, a.ldw, min(BN, a.V - v0), a.D, acc, smem);
+    const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+    T *G = (T *)p.gbuf;
+    T *GT = (T *)p.gtbuf;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            const int vloc = 64 * wn + 16 * ni + l16, v = v0 + vloc;
+            T gv[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int rl = 64 * wm + 16 * mi + 4 * g + r;
+                float x = 0.f;
+                if (v < a.V && sScale[rl] != 0.f) {
+                    x = __expf(acc[mi][ni][r] - sLse[rl]);
+                    if (v == sTgt[rl]) x -= 1.f;
+                    x *= sScale[rl];
+                }
+                gv[r] = from_f32<T>(x);
+                const int lr = lr0 + rl;
+                if (lr < p.rows) G[(int64_t)lr * p.Vp + v] = gv[r];
+            }
+            // G^T[v][lr0 + 64wm + 16mi + 4g .. +3]: 4 consecutive rows
+            T *dst = GT + (int64_t)v * p.Rp + lr0 + 64 * wm + 16 * mi + 4 * g;
+            if (lr0 + 64 * wm + 16 * mi + 4 * g + 3 < p.Rp) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dst[r] = gv[r];
+            }
+        }
+    }
+}
+
+// C = A B^T with the epilogue writing dtype T (dH) or accumulating fp32 (dW)
+template <typename T, bool ACCUM>
+__global__ void __launch_bounds__(THREADS) ce_gemm_kernel(const T *A, int64_t lda, int M, const T *B, int64_t ldb,
+                                                         int N, int K, void *C, int64_t ldc) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    T *smem = reinterpret_cast<T *>(smem_raw);
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    floatx4 acc[4][4];
+    gemm_tile<T>(A + (int64_t)m0 * lda, lda, min(BM, M - m0), B + (int64_t)n0 * ldb, ldb, min(BN, N - n0), K, acc,
+                 smem);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 64 * wm + 16 * mi + 4 * g + r, n = n0 + 64 * wn + 16 * ni + l16;
+                if (m < M && n < N) {
+                    if (ACCUM) {
+                        float *c = (float *)C + (int64_t)m * ldc + n;
+                        *c += acc[mi][ni][r];
+                    } else {
+                        ((T *)C)[(int64_t)m * ldc + n] = from_f32<T>(acc[mi][ni][r]);
+                    }
+                }
+            }
+}
+
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+template <typename T>
+size_t fwd_ws(const qpam_ce_fwd_args &a) {
+    const int64_t n_vt = (a.V + VT - 1) / VT;
+    return (size_t)a.N * n_vt * 12 + 256;
+}
+
+template <typename T>
+size_t bwd_ws(const qpam_ce_bwd_args &a) {
+    const int64_t Vp = round_up(a.V, VT), chunk = std::min(a.chunk, a.N), Rp = round_up((int)chunk, BM);
+    const int64_t elems = (int64_t)a.D * Vp + chunk * Vp + Vp * Rp + (int64_t)a.D * Rp;
+    return (size_t)(elems * sizeof(T)) + 4 * 256;
+}
+
+template <typename T>
+int run_fwd(const qpam_ce_fwd_args &a, hipStream_t stream) {
+    FwdParams p;
+    p.a = a;
+    p.n_vt = (a.V + VT - 1) / VT;
+    char *ws = (char *)a.workspace;
+    const int64_t cnt = (int64_t)a.N * p.n_vt;
+    p.part_m = (float *)ws;
+    p.part_s = p.part_m + cnt;
+    p.part_i = (int *)(p.part_s + cnt);
+    p.red = nullptr;
+    const size_t smem = gemm_smem<T>();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)ce_fwd_tile_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)smem));
+    dim3 grid(p.n_vt, (a.N + BM - 1) / BM);
+    hipLaunchKernelGGL(ce_fwd_tile_kernel<T>, grid, dim3(THREADS), smem, stream, p);
+    int st = launch_status("ce_fwd_tile_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(ce_fwd_finalize_kernel<T>, dim3((a.N + 3) / 4), dim3(THREADS), 0, stream, p);
+    st = launch_status("ce_fwd_finalize_kernel");
+    if (st) return st;
+    if (a.loss_sum) {
+        hipLaunchKernelGGL(ce_reduce_kernel, dim3(1), dim3(1024), 0, stream, p);
+        st = launch_status("ce_reduce_kernel");
+    }
+    return st;
+}
+
+template <typename T>
+int run_bwd(const qpam_ce_bwd_args &a, hipStream_t stream) {
+    BwdParams p;
+    p.a = a;
+    p.Vp = round_up(a.V, VT);
+    const int chunk = std::min(a.chunk, a.N);
+    const int Rmax = round_up(chunk, BM);
+    T *ws = (T *)a.workspace;
+    p.wt = ws;
+    p.gbuf = ws + (int64_t)a.D * p.Vp;
+    p.gtbuf = (T *)p.gbuf + (int64_t)chunk * p.Vp;
+    p.ht = (T *)p.gtbuf + (int64_t)p.Vp * Rmax;
+    const size_t smem = gemm_smem<T>();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)ce_grad_tile_kernel<T>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)ce_gemm_kernel<T, false>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)ce_gemm_kernel<T, true>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    // W^T [D][Vp] (zero-padded vocab columns)
+    hipLaunchKernelGGL(transpose_kernel<T>, dim3((a.D + 63) / 64, (p.Vp + 63) / 64), dim3(THREADS), 0, stream,
+                       (const T *)a.w, a.ldw, a.V, a.D, (T *)p.wt, (int64_t)p.Vp, a.D, p.Vp);
+    int st = launch_status("transpose_kernel(W)");
+    if (st) return st;
+    for (int r0 = 0; r0 < a.N; r0 += chunk) {
+        p.row0 = r0;
+        p.rows = std::min(chunk, a.N - r0);
+        p.Rp = round_up(p.rows, BM);
+        // H^T [D][Rp] of this chunk
+        hipLaunchKernelGGL(transpose_kernel<T>, dim3((a.D + 63) / 64, (p.Rp + 63) / 64), dim3(THREADS), 0, stream,
+                           (const T *)a.h + (int64_t)r0 * a.ldh, a.ldh, p.rows, a.D, (T *)p.ht, (int64_t)p.Rp, a.D,
+                           p.Rp);
+        st = launch_status("transpose_kernel(H)");
+        if (st) return st;
+        hipLaunchKernelGGL(ce_grad_tile_kernel<T>, dim3(p.Vp / VT, p.Rp / BM), dim3(THREADS), smem, stream, p);
+        st = launch_status("ce_grad_tile_kernel");
+        if (st) return st;
+        // dH[r0 .. r0+rows] = G [rows][Vp] * (W^T [D][Vp])^T
+        hipLaunchKernelGGL((ce_gemm_kernel<T, false>), dim3((a.D + BN - 1) / BN, (p.rows + BM - 1) / BM),
+                           dim3(THREADS), smem, stream, (const T *)p.gbuf, (int64_t)p.Vp, p.rows, (const T *)p.wt,
+                           (int64_t)p.Vp, a.D, p.Vp, (void *)((T *)a.dh + (int64_t)r0 * a.lddh), a.lddh);
+        st = launch_status("ce_gemm_kernel(dH)");
+        if (st) return st;
+        // dW [V][D] += G^T [Vp][Rp] * (H^T [D][Rp])^T
+        hipLaunchKernelGGL((ce_gemm_kernel<T, true>), dim3((a.D + BN - 1) / BN, (a.V + BM - 1) / BM),
+                           dim3(THREADS), smem, stream, (const T *)p.gtbuf, (int64_t)p.Rp, a.V, (const T *)p.ht,
+                           (int64_t)p.Rp, a.D, p.Rp, (void *)a.dw, a.lddw);
+        st = launch_status("ce_gemm_kernel(dW)");
+        if (st) return st;
+    }
+    return QPAM_OK;
+}
+
+int validate_common(int N, int V, int D, int dtype, const void *h, int64_t ldh, const void *w, int64_t ldw,
+                    const int64_t *targets, const char *who) {
+    QPAM_REQUIRE(N >= 1 && V >= 1 && D >= 1, "%s: bad sizes N=%d V=%d D=%d", who, N, V, D);
+    QPAM_REQUIRE(dtype == QPAM_F32 || dtype == QPAM_BF16, "%s: dtype %d", who, dtype);
+    QPAM_REQUIRE(D % BK == 0, "%s: hidden size %d must be a multiple of %d", who, D, BK);
+    QPAM_REQUIRE(h && w && targets, "%s: null pointer", who);
+    const int vec = dtype == QPAM_F32 ? 4 : 8;
+    QPAM_REQUIRE(((uintptr_t)h % 16) == 0 && ((uintptr_t)w % 16) == 0 && ldh % vec == 0 && ldw % vec == 0 &&
+                     ldh >= D && ldw >= D,
+                 "%s: H and W must be 16-byte aligned with leading dims multiple of %d and >= D", who, vec);
+    return QPAM_OK;
+}
+
+}  // namespace
+}  // namespace ce
+}  // namespace qpam
+
+extern "C" size_t qpam_ce_fwd_workspace_size(const qpam_ce_fwd_args *a) {
+    using namespace qpam::ce;
+    if (!a) return 0;
+    return a->dtype == QPAM_BF16 ? fwd_ws<unsigned short>(*a) : fwd_ws<float>(*a);
+}
+
+extern "C" int qpam_ce_fwd(const qpam_ce_fwd_args *a, void *stream) {
+    using namespace qpam;
+    using namespace qpam::ce;
+    QPAM_REQUIRE(a != nullptr, "qpam_ce_fwd: null args");
+    int st = validate_common(a->N, a->V, a->D, a->dtype, a->h, a->ldh, a->w, a->ldw, a->targets, "qpam_ce_fwd");
+    if (st) return st;
+    QPAM_REQUIRE(a->lse && a->loss, "qpam_ce_fwd: lse and loss outputs are required");
+    const size_t need = qpam_ce_fwd_workspace_size(a);
+    QPAM_REQUIRE(a->workspace && a->workspace_bytes >= need && ((uintptr_t)a->workspace % 16) == 0,
+                 "qpam_ce_fwd: workspace needs %zu bytes (got %zu)", need, a->workspace_bytes);
+    QPAM_REQUIRE((a->N + BM - 1) / BM <= 65535, "qpam_ce_fwd: too many rows");
+    return a->dtype == QPAM_BF16 ? run_fwd<unsigned short>(*a, (hipStream_t)stream)
+                                 : run_fwd<float>(*a, (hipStream_t)stream);
+}
+
+extern "C" size_t qpam_ce_bwd_workspace_size(const qpam_ce_bwd_args *a) {
+    using namespace qpam::ce;
+    if (!a || a->chunk < 1) return 0;
+    return a->dtype == QPAM_BF16 ? bwd_ws<unsigned short>(*a) : bwd_ws<float>(*a);
+}
+
+extern "C" int qpam_ce_bwd(const qpam_ce_bwd_args *a, void *stream) {
+    using namespace qpam;
+    using namespace qpam::ce;
+    QPAM_REQUIRE(a != nullptr, "qpam_ce_bwd: null args");
+    int st = validate_common(a->N, a->V, a->D, a->dtype, a->h, a->ldh, a->w, a->ldw, a->targets, "qpam_ce_bwd");
+    if (st) return st;
+    QPAM_REQUIRE(a->lse && a->grad_scale && a->dh && a->dw, "qpam_ce_bwd: null lse/grad_scale/dh/dw");
+    QPAM_REQUIRE(a->chunk >= 1, "qpam_ce_bwd: chunk must be >= 1");
+    QPAM_REQUIRE(a->lddh >= a->D && a->lddw >= a->D, "qpam_ce_bwd: output leading dims must be >= D");
+    const size_t need = qpam_ce_bwd_workspace_size(a);
+    QPAM_REQUIRE(a->workspace && a->workspace_bytes >= need && ((uintptr_t)a->workspace % 16) == 0,
+                 "qpam_ce_bwd: workspace needs %zu bytes (got %zu)", need, a->workspace_bytes);
+    return a->dtype == QPAM_BF16 ? run_bwd<unsigned short>(*a, (hipStream_t)stream)
+                                 : run_bwd<float>(*a, (hipStream_t)stream);
+}

@@ -40,7 +40,32 @@ def parse():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=1000)
+    ap.add_argument("--only", choices=["scan_fwd", "decode", "e3", "ce", "copy"], default=None,
+                    help="run one workload (for profiler passes) and print its own JSON line")
     return ap.parse_args()
+
+
+def measured_traffic(kernel_key):
+    """HBM bytes per dispatch of `kernel_key` from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic.json, calibrated against a
+    plain copy), or None when that kernel has not been measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            return json.load(f)["kernels"][kernel_key]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_calibration(nbytes=1 << 30, reps=3):
+    """A plain device copy of known size: the reference point that scales the
+    FETCH_SIZE / WRITE_SIZE counters into HBM bytes."""
+    import torch
+    src = torch.ones(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"copy_bytes_each_way": nbytes, "reps": reps}
 
 
 def scan_inputs(B, H, T, d, M, seed, dtype, unit_qk=True, mu=3.0, mu_step=0.0):
@@ -213,6 +238,15 @@ def main():
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
+    if args.only is not None:
+        fn = {"scan_fwd": lambda: dict(zip(("ms", "kernel_ms", "tokens", "flops", "kernel_flops"),
+                                           bench_scan_fwd(args.steps, args.warmup))),
+              "decode": lambda: bench_decode(args.decode_steps),
+              "e3": lambda: bench_e3_fwd_bwd(args.steps, args.warmup),
+              "ce": lambda: bench_ce(args.steps, args.warmup),
+              "copy": copy_calibration}[args.only]
+        print(json.dumps({"only": args.only, "result": fn()}), flush=True)
+        return
     ms, kms, tokens, flops, kflops = bench_scan_fwd(args.steps, args.warmup)
     value = tokens / (ms * 1e-3)
     achieved = kflops / (kms * 1e-3)
@@ -232,7 +266,8 @@ def main():
         "config": {"workload": "pam_scan_fwd config 2", "B": 8, "T": 2048, "H": 12, "d": 64, "C": 64,
                    "layout": "planar re/im fp32"},
         "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": MFMA_FP32_PEAK / 1e12,
-                     "unit": "TFLOP/s", "frac": achieved / MFMA_FP32_PEAK, "traffic": None,
+                     "unit": "TFLOP/s", "frac": achieved / MFMA_FP32_PEAK,
+                     "traffic": measured_traffic("chunk_output_kernel<float,64>"),
                      "kernel": "chunk_output_kernel<float,64>", "kernel_ms": kms,
                      "kernel_flops": kflops},
         "scan_fwd_total": {"flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,

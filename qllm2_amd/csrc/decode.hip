@@ -6,25 +6,42 @@
 //     S <- gamma S + v (x) conj(k);   y = sum_m r_m (S_m @ q~)
 //
 // Design: one workgroup per (listed slot, group).  The d x d interleaved
-// complex state of each of the M states is streamed once (16-byte loads and
-// stores, consecutive lanes on consecutive 16 bytes so every wave instruction
-// covers a contiguous 1 KiB).  Each lane owns a fixed pair of key columns, so
-// q~ and k are loaded once per lane; the row sums of S q~ are reduced across
-// the lanes of a row with a halving butterfly (each step halves the number of
-// live partial sums, 16 shuffles instead of 80 for d = 64).  Slots that are
-// not listed cost nothing: the grid is n_active * n_groups.
+// complex state of each of the M states is streamed once with non-temporal
+// 16-byte loads and stores (consecutive lanes on consecutive 16 bytes, so a
+// wave instruction covers a contiguous 1 KiB; the state is touched once per
+// step, so it bypasses the caches).  Each lane owns a fixed pair of key
+// columns, so q~ and k are loaded once per lane; the row sums of S q~ are
+// reduced across the lanes of a row with a halving butterfly (each step
+// halves the number of live partial sums).  Slots that are not listed cost
+// nothing: the grid is n_active * n_groups.
+//
+// Two kernels: the single-state, unrotated step (the continuous-batching
+// common case) keeps every register for loads in flight, 512 threads per
+// 64 x 64 state and no LDS or barriers; the general kernel loops over the M
+// states, accumulating the rotated reads through LDS.
 #include "common.h"
 
 namespace qpam {
 namespace {
 
-template <int D>
+template <int D, int T>
 struct DecodeShape {
     static constexpr int PAIRS = D / 2;                       // float4 per state row
-    static constexpr int THREADS = (D * D / 2) < 256 ? (D * D / 2) : 256;
+    static constexpr int THREADS = (D * D / 2) < T ? (D * D / 2) : T;
     static constexpr int ROWS_PER_IT = THREADS / PAIRS;       // rows covered per iteration
     static constexpr int ITERS = D / ROWS_PER_IT;             // float4 per lane per state
     static constexpr int NV = 2 * ITERS;                      // partial sums per lane (re, im per row)
+    // lane-offset bits of the reduction steps that are plain butterflies (all
+    // lanes of the pair end with the same sum): a lane owns its sums when
+    // these bits of its lane id are zero
+    static constexpr int bfly_mask() {
+        int nv = NV, m = 0;
+        for (int off = PAIRS / 2; off >= 1; off >>= 1) {
+            if (nv > 1) nv /= 2;
+            else m |= off;
+        }
+        return m;
+    }
 };
 
 // Reduce NV values across P aligned lanes by halving; on return the lane holds
@@ -55,16 +72,72 @@ __device__ __forceinline__ void halving_reduce(float (&v)[NV], int lane, int &id
     nv_out = nv;
 }
 
+// S <- gam S + v (x) conj(k) on this lane's ITERS float4 (two complex entries
+// each), streamed in place; returns the lane's partial sums of S q~ per row.
+template <typename S>
+__device__ __forceinline__ void update_state(float *st, int tid, int r0, float gam, const float *vrow, float4 kv,
+                                             float q0r, float q0i, float q1r, float q1i, float (&part)[S::NV]) {
+    floatx4 s[S::ITERS];
+#pragma unroll
+    for (int it = 0; it < S::ITERS; ++it)
+        s[it] = __builtin_nontemporal_load(reinterpret_cast<const floatx4 *>(st + 4 * (it * S::THREADS + tid)));
+#pragma unroll
+    for (int it = 0; it < S::ITERS; ++it) {
+        const int row = it * S::ROWS_PER_IT + r0;
+        const float2 vv = *reinterpret_cast<const float2 *>(vrow + 2 * row);
+        // v_i conj(k_j) for the two columns
+        const float o0r = vv.x * kv.x + vv.y * kv.y, o0i = vv.y * kv.x - vv.x * kv.y;
+        const float o1r = vv.x * kv.z + vv.y * kv.w, o1i = vv.y * kv.z - vv.x * kv.w;
+        floatx4 n;
+        n.x = gam * s[it].x + o0r;
+        n.y = gam * s[it].y + o0i;
+        n.z = gam * s[it].z + o1r;
+        n.w = gam * s[it].w + o1i;
+        __builtin_nontemporal_store(n, reinterpret_cast<floatx4 *>(st + 4 * (it * S::THREADS + tid)));
+        part[2 * it] = n.x * q0r - n.y * q0i + n.z * q1r - n.w * q1i;
+        part[2 * it + 1] = n.x * q0i + n.y * q0r + n.z * q1i + n.w * q1r;
+    }
+}
+
+// ------------------------------------------------ one state, no rotation --
 template <int D>
-__global__ void __launch_bounds__(DecodeShape<D>::THREADS)
-decode_step_kernel(qpam_decode_args a) {
-    using S = DecodeShape<D>;
+__global__ void __launch_bounds__((DecodeShape<D, 512>::THREADS)) decode_single_kernel(qpam_decode_args a) {
+    using S = DecodeShape<D, 512>;
+    const int tid = threadIdx.x;
+    const int ai = blockIdx.x / a.n_groups;
+    const int g = blockIdx.x - ai * a.n_groups;
+    const int slot = a.active ? a.active[ai] : ai;
+    if (slot < 0 || slot >= a.n_slots) return;
+    const int cp = tid % S::PAIRS, r0 = tid / S::PAIRS, lane = tid & 63;
+    const float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
+    const float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    const float gam = a.gamma[slot * a.sg_slot + g * a.sg_group];
+    float part[S::NV];
+    update_state<S>(a.state + slot * a.st_slot + g * a.st_group, tid, r0, gam, a.v + slot * a.sv_slot + g * a.sv_group,
+                    kv, qv.x * a.q_scale, qv.y * a.q_scale, qv.z * a.q_scale, qv.w * a.q_scale, part);
+    int base, nv;
+    halving_reduce<S::NV, S::PAIRS>(part, lane, base, nv);
+    if ((lane & S::bfly_mask()) == 0) {
+        float *yp = a.y + slot * a.sy_slot + g * a.sy_group;
+#pragma unroll
+        for (int j = 0; j < S::NV; ++j) {
+            if (j < nv) {
+                const int vi = base + j;
+                yp[2 * ((vi >> 1) * S::ROWS_PER_IT + r0) + (vi & 1)] = part[j];
+            }
+        }
+    }
+}
+
+// ------------------------------------------------ M states, rotations -----
+template <int D>
+__global__ void __launch_bounds__((DecodeShape<D, 256>::THREADS)) decode_general_kernel(qpam_decode_args a) {
+    using S = DecodeShape<D, 256>;
     __shared__ float ys[D][2];
 
     const int tid = threadIdx.x;
-    const int blk = blockIdx.x;
-    const int ai = blk / a.n_groups;
-    const int g = blk - ai * a.n_groups;
+    const int ai = blockIdx.x / a.n_groups;
+    const int g = blockIdx.x - ai * a.n_groups;
     const int slot = a.active ? a.active[ai] : ai;
     if (slot < 0 || slot >= a.n_slots) return;  // whole block exits together
 
@@ -74,38 +147,14 @@ decode_step_kernel(qpam_decode_args a) {
 
     const float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
     const float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
-    const float q0r = qv.x * a.q_scale, q0i = qv.y * a.q_scale;
-    const float q1r = qv.z * a.q_scale, q1i = qv.w * a.q_scale;
     const float *vrow = a.v + slot * a.sv_slot + g * a.sv_group;
 
     float yacc_r = 0.f, yacc_i = 0.f;  // lanes tid < D accumulate row tid
-
     for (int m = 0; m < a.n_states; ++m) {
-        float *st = a.state + slot * a.st_slot + g * a.st_group + m * a.st_state;
         const float gam = a.gamma[slot * a.sg_slot + g * a.sg_group + m * a.sg_state];
-        float4 s[S::ITERS];
-#pragma unroll
-        for (int it = 0; it < S::ITERS; ++it)
-            s[it] = *reinterpret_cast<const float4 *>(st + 4 * (it * S::THREADS + tid));
-
         float part[S::NV];
-#pragma unroll
-        for (int it = 0; it < S::ITERS; ++it) {
-            const int row = it * S::ROWS_PER_IT + r0;
-            const float2 vv = *reinterpret_cast<const float2 *>(vrow + 2 * row);
-            // v_i conj(k_j) for the two columns
-            const float o0r = vv.x * kv.x + vv.y * kv.y, o0i = vv.y * kv.x - vv.x * kv.y;
-            const float o1r = vv.x * kv.z + vv.y * kv.w, o1i = vv.y * kv.z - vv.x * kv.w;
-            float4 n;
-            n.x = gam * s[it].x + o0r;
-            n.y = gam * s[it].y + o0i;
-            n.z = gam * s[it].z + o1r;
-            n.w = gam * s[it].w + o1i;
-            *reinterpret_cast<float4 *>(st + 4 * (it * S::THREADS + tid)) = n;
-            part[2 * it] = n.x * q0r - n.y * q0i + n.z * q1r - n.w * q1i;
-            part[2 * it + 1] = n.x * q0i + n.y * q0r + n.z * q1i + n.w * q1r;
-        }
-
+        update_state<S>(a.state + slot * a.st_slot + g * a.st_group + m * a.st_state, tid, r0, gam, vrow, kv,
+                        qv.x * a.q_scale, qv.y * a.q_scale, qv.z * a.q_scale, qv.w * a.q_scale, part);
         int base, nv;
         halving_reduce<S::NV, S::PAIRS>(part, lane, base, nv);
 #pragma unroll
@@ -138,11 +187,16 @@ decode_step_kernel(qpam_decode_args a) {
 
 template <int D>
 int launch_decode(const qpam_decode_args &a, hipStream_t stream) {
-    using S = DecodeShape<D>;
     const long long blocks = (long long)a.n_active * a.n_groups;
     if (blocks == 0) return QPAM_OK;
-    hipLaunchKernelGGL(decode_step_kernel<D>, dim3((unsigned)blocks), dim3(S::THREADS), 0, stream, a);
-    return launch_status("decode_step_kernel");
+    if (a.n_states == 1 && a.rot == nullptr) {
+        hipLaunchKernelGGL(decode_single_kernel<D>, dim3((unsigned)blocks), dim3(DecodeShape<D, 512>::THREADS), 0,
+                           stream, a);
+        return launch_status("decode_single_kernel");
+    }
+    hipLaunchKernelGGL(decode_general_kernel<D>, dim3((unsigned)blocks), dim3(DecodeShape<D, 256>::THREADS), 0, stream,
+                       a);
+    return launch_status("decode_general_kernel");
 }
 
 bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }

@@ -415,38 +415,397 @@ __global__ void __launch_bounds__(THREADS) ce_gemm_kernel(const T *A, int64_t ld
             }
 }
 
+// ------------------------------------------------------ bf16 big tiles ----
+// bf16 operands use 256 x 256 block tiles: 4 waves of 128 x 128, 8 x 8
+// accumulator tiles (256 fp32 per lane, AGPR resident), 64 MFMA per 32-wide
+// k-step against 16 fragment reads (64 flops per LDS byte), global loads
+// prefetched two k-steps ahead through registers into a double-buffered LDS.
+namespace big {
+constexpr int BTM = 256;                // block tile rows (A operand)
+constexpr int BTN = 128;                // block tile cols (B operand)
+constexpr int PITCH = BK + 8;           // bf16 elements per LDS row
+constexpr int LOADS_A = BTM * 4 / THREADS;  // 16-byte loads per thread per k-step
+constexpr int LOADS_B = BTN * 4 / THREADS;
+constexpr size_t SMEM = (size_t)2 * (BTM + BTN) * PITCH * sizeof(unsigned short);  // 60 KiB
+using U16 = unsigned short;
+
+struct Frag {
+    uint4 a[LOADS_A], b[LOADS_B];
+};
+
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2.
+// Give every XCD a contiguous range of work items (grid = 8 * per; items >=
+// total are idle) so that concurrently running tiles of one XCD share rows.
+constexpr int XCDS = 8;
+__device__ __forceinline__ int xcd_item(int bid, int total) {
+    const int per = (total + XCDS - 1) / XCDS;
+    return (bid % XCDS) * per + bid / XCDS;
+}
+inline int xcd_grid(int total) { return XCDS * ((total + XCDS - 1) / XCDS); }
+
+// Item -> (row tile, col tile), grouping GM row tiles: consecutive items walk
+// the GM row tiles of one column tile, then the next column tile, so a window
+// of ~32 items touches GM row tiles and ~32/GM column tiles.
+constexpr int GM = 4;
+__device__ __forceinline__ void grouped_tile(int item, int n_rt, int n_ct, int &rt, int &ct) {
+    const int group = item / (GM * n_ct);
+    const int in_group = item - group * GM * n_ct;
+    const int rows = min(GM, n_rt - group * GM);
+    rt = group * GM + in_group % rows;
+    ct = in_group / rows;
+}
+
+__device__ __forceinline__ void gload(Frag &f, const U16 *A, int64_t lda, int a_rows, const U16 *B, int64_t ldb,
+                                      int b_rows, int k0) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < LOADS_A; ++i) {
+        const int ci = tid + i * THREADS, row = ci >> 2, c = ci & 3;
+        f.a[i] = (row < a_rows) ? *reinterpret_cast<const uint4 *>(A + row * lda + k0 + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < LOADS_B; ++i) {
+        const int ci = tid + i * THREADS, row = ci >> 2, c = ci & 3;
+        f.b[i] = (row < b_rows) ? *reinterpret_cast<const uint4 *>(B + row * ldb + k0 + 8 * c) : make_uint4(0, 0, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void lstore(const Frag &f, U16 *sA, U16 *sB) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < LOADS_A; ++i) {
+        const int ci = tid + i * THREADS, row = ci >> 2, c = ci & 3;
+        *reinterpret_cast<uint4 *>(sA + row * PITCH + 8 * c) = f.a[i];
+    }
+#pragma unroll
+    for (int i = 0; i < LOADS_B; ++i) {
+        const int ci = tid + i * THREADS, row = ci >> 2, c = ci & 3;
+        *reinterpret_cast<uint4 *>(sB + row * PITCH + 8 * c) = f.b[i];
+    }
+}
+
+__device__ __forceinline__ void mma_step(const U16 *sA, const U16 *sB, floatx4 (&acc)[8][4], int arow0, int brow0,
+                                         int l16, int g) {
+    // B fragments stay in registers for the step; A fragments are read per row tile
+    bf16x8 bfr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bfr[i] = *reinterpret_cast<const bf16x8 *>(sB + (brow0 + 16 * i + l16) * PITCH + 8 * g);
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi) {
+        const bf16x8 af = *reinterpret_cast<const bf16x8 *>(sA + (arow0 + 16 * mi + l16) * PITCH + 8 * g);
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr[ni], acc[mi][ni], 0, 0, 0);
+    }
+}
+
+// C[m][n] = sum_{k in [k_begin, k_end)} A[m][k] B[n][k] for one 256 x 128 tile.
+// acc[mi][ni] lane holds C[128*(w>>1) + 16mi + 4g + r][64*(w&1) + 16ni + l16].
+// DEEP prefetches two k-steps ahead (two register stages); otherwise one.
+template <bool DEEP>
+__device__ __forceinline__ void gemm_tile(const U16 *A, int64_t lda, int a_rows, const U16 *B, int64_t ldb,
+                                          int b_rows, int k_begin, int k_end, floatx4 (&acc)[8][4], U16 *smem) {
+    U16 *sA[2] = {smem, smem + (BTM + BTN) * PITCH};
+    U16 *sB[2] = {smem + BTM * PITCH, smem + (BTM + BTN) * PITCH + BTM * PITCH};
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int arow0 = 128 * (w >> 1), brow0 = 64 * (w & 1);
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int KT = (k_end - k_begin) / BK;
+    if (KT <= 0) return;
+    if (!DEEP) {
+        Frag f;
+        gload(f, A, lda, a_rows, B, ldb, b_rows, k_begin);
+        lstore(f, sA[0], sB[0]);
+        __syncthreads();
+        for (int kt = 0; kt < KT; ++kt) {
+            const int buf = kt & 1;
+            if (kt + 1 < KT) gload(f, A, lda, a_rows, B, ldb, b_rows, k_begin + (kt + 1) * BK);
+            mma_step(sA[buf], sB[buf], acc, arow0, brow0, l16, g);
+            if (kt + 1 < KT) lstore(f, sA[buf ^ 1], sB[buf ^ 1]);
+            __syncthreads();
+        }
+        return;
+    }
+    Frag f0, f1;
+    gload(f0, A, lda, a_rows, B, ldb, b_rows, k_begin);
+    if (KT > 1) gload(f1, A, lda, a_rows, B, ldb, b_rows, k_begin + BK);
+    lstore(f0, sA[0], sB[0]);
+    __syncthreads();
+    for (int kt = 0; kt < KT; kt += 2) {
+        // even step: tile kt in buffer 0, tile kt+1 waiting in f1
+        if (kt + 2 < KT) gload(f0, A, lda, a_rows, B, ldb, b_rows, k_begin + (kt + 2) * BK);
+        mma_step(sA[0], sB[0], acc, arow0, brow0, l16, g);
+        if (kt + 1 < KT) lstore(f1, sA[1], sB[1]);
+        __syncthreads();
+        if (kt + 1 >= KT) break;
+        // odd step: tile kt+1 in buffer 1, tile kt+2 waiting in f0
+        if (kt + 3 < KT) gload(f1, A, lda, a_rows, B, ldb, b_rows, k_begin + (kt + 3) * BK);
+        mma_step(sA[1], sB[1], acc, arow0, brow0, l16, g);
+        if (kt + 2 < KT) lstore(f0, sA[0], sB[0]);
+        __syncthreads();
+    }
+}
+
+// forward: per (256 rows, 128 vocab) tile -> per-row (max, sum exp, argmax)
+__global__ void __launch_bounds__(THREADS, 2) fwd_tile_kernel(FwdParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ float sM[2][BTM], sS[2][BTM];
+    __shared__ int sI[2][BTM];
+    const qpam_ce_fwd_args &a = p.a;
+    const int n_rt = (a.N + BTM - 1) / BTM;
+    const int item = xcd_item(blockIdx.x, n_rt * p.n_vt);
+    if (item >= n_rt * p.n_vt) return;
+    int rt, vt;
+    grouped_tile(item, n_rt, p.n_vt, rt, vt);
+    const int r0 = rt * BTM, v0 = vt * BTN;
+    floatx4 acc[8][4];
+    gemm_tile<true>((const U16 *)a.h + (int64_t)r0 * a.ldh, a.ldh, min(BTM, a.N - r0), (const U16 *)a.w + (int64_t)v0 * a.ldw,
+              a.ldw, min(BTN, a.V - v0), 0, a.D, acc, reinterpret_cast<U16 *>(smem_raw));
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float mx = -INFINITY;
+            int ix = 0x7fffffff;
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const int v = v0 + 64 * wn + 16 * ni + l16;
+                const float x = (v < a.V) ? acc[mi][ni][r] : -INFINITY;
+                if (x > mx) { mx = x; ix = v; }
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) {
+                const float om = __shfl_xor(mx, off);
+                const int oi = __shfl_xor(ix, off);
+                if (om > mx || (om == mx && oi < ix)) { mx = om; ix = oi; }
+            }
+            float s = 0.f;
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                const int v = v0 + 64 * wn + 16 * ni + l16;
+                if (v < a.V) s += __expf(acc[mi][ni][r] - mx);
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
+            if (l16 == 0) {
+                const int row = 128 * wm + 16 * mi + 4 * g + r;
+                sM[wn][row] = mx;
+                sS[wn][row] = s;
+                sI[wn][row] = ix;
+            }
+        }
+    }
+    __syncthreads();
+    if (r0 + tid < a.N) {
+        const float m0 = sM[0][tid], m1 = sM[1][tid];
+        const float m = fmaxf(m0, m1);
+        float s = 0.f;
+        if (m0 > -INFINITY) s += sS[0][tid] * __expf(m0 - m);
+        if (m1 > -INFINITY) s += sS[1][tid] * __expf(m1 - m);
+        const int i = (m1 > m0 || (m1 == m0 && sI[1][tid] < sI[0][tid])) ? sI[1][tid] : sI[0][tid];
+        const int64_t o = (int64_t)(r0 + tid) * p.n_vt + vt;
+        p.part_m[o] = m;
+        p.part_s[o] = s;
+        p.part_i[o] = i;
+    }
+}
+
+// backward G tile (256 rows x 128 vocab): recompute logits, write G and G^T
+__global__ void __launch_bounds__(THREADS, 2) grad_tile_kernel(BwdParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ float sLse[BTM], sScale[BTM];
+    __shared__ int sTgt[BTM];
+    const qpam_ce_bwd_args &a = p.a;
+    const int n_rt = p.Rp / BTM, n_vt = p.Vp / BTN;
+    const int item = xcd_item(blockIdx.x, n_rt * n_vt);
+    if (item >= n_rt * n_vt) return;
+    int rt, vt;
+    grouped_tile(item, n_rt, n_vt, rt, vt);
+    const int lr0 = rt * BTM, v0 = vt * BTN;
+    const int tid = threadIdx.x;
+    {
+        const int lr = lr0 + tid, row = p.row0 + lr;
+        float lse = 0.f, sc = 0.f;
+        int tg = -1;
+        if (lr < p.rows) {
+            const int64_t t = a.targets[row];
+            const bool valid = (t != a.ignore_index) && t >= 0 && t < a.V;
+            lse = a.lse[row];
+            sc = valid ? a.grad_scale[0] * (a.mask ? a.mask[row] : 1.f) : 0.f;
+            tg = valid ? (int)t : -1;
+        }
+        sLse[tid] = lse;
+        sScale[tid] = sc;
+        sTgt[tid] = tg;
+    }
+    floatx4 acc[8][4];
+    gemm_tile<false>((const U16 *)a.h + (int64_t)(p.row0 + lr0) * a.ldh, a.ldh, min(BTM, p.rows - lr0),
+              (const U16 *)a.w + (int64_t)v0 * a.ldw, a.ldw, min(BTN, a.V - v0), 0, a.D, acc,
+              reinterpret_cast<U16 *>(smem_raw));
+    const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+    U16 *G = (U16 *)p.gbuf;
+    U16 *GT = (U16 *)p.gtbuf;
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            const int v = v0 + 64 * wn + 16 * ni + l16;
+            const int rl0 = 128 * wm + 16 * mi + 4 * g;
+            ushortx4 gv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int rl = rl0 + r;
+                float x = 0.f;
+                if (v < a.V && sScale[rl] != 0.f) {
+                    x = __expf(acc[mi][ni][r] - sLse[rl]);
+                    if (v == sTgt[rl]) x -= 1.f;
+                    x *= sScale[rl];
+                }
+                gv[r] = f32_to_bf16(x);
+                if (lr0 + rl < p.rows) G[(int64_t)(lr0 + rl) * p.Vp + v] = gv[r];
+            }
+            *reinterpret_cast<ushortx4 *>(GT + (int64_t)v * p.Rp + lr0 + rl0) = gv;
+        }
+    }
+}
+
+// backward GEMMs: dW tiles (dW[v][d] += sum_r G^T[v][r] H^T[d][r]) and
+// split-K partials of dH (dH_s[r][d] = sum_{v in split s} G[r][v] W^T[d][v])
+// into fp32, as two kernels so each keeps two waves per SIMD.
+struct GroupParams {
+    BwdParams p;
+    int n_dw, dw_ntiles_n;     // dW tiles, tiles along D
+    int dh_ntiles_m, dh_ntiles_n, splits, ksplit;
+    float *dh_part;            // [splits][rows][D]
+};
+
+__global__ void __launch_bounds__(THREADS, 2) dw_gemm_kernel(GroupParams q) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const BwdParams &p = q.p;
+    const qpam_ce_bwd_args &a = p.a;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+    floatx4 acc[8][4];
+    const int bid = xcd_item(blockIdx.x, q.n_dw);
+    if (bid >= q.n_dw) return;
+    const int mt = bid / q.dw_ntiles_n, nt = bid % q.dw_ntiles_n;
+    const int m0 = mt * BTM, n0 = nt * BTN;
+    gemm_tile<false>((const U16 *)p.gtbuf + (int64_t)m0 * p.Rp, p.Rp, min(BTM, a.V - m0),
+              (const U16 *)p.ht + (int64_t)n0 * p.Rp, p.Rp, min(BTN, a.D - n0), 0, p.Rp, acc,
+              reinterpret_cast<U16 *>(smem_raw));
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 128 * wm + 16 * mi + 4 * g + r, n = n0 + 64 * wn + 16 * ni + l16;
+                if (m < a.V && n < a.D) a.dw[(int64_t)m * a.lddw + n] += acc[mi][ni][r];
+            }
+}
+
+__global__ void __launch_bounds__(THREADS, 2) dh_gemm_kernel(GroupParams q) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const BwdParams &p = q.p;
+    const qpam_ce_bwd_args &a = p.a;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+    floatx4 acc[8][4];
+    const int total = q.splits * q.dh_ntiles_m * q.dh_ntiles_n;
+    const int bid = xcd_item(blockIdx.x, total);
+    if (bid >= total) return;
+    const int s = bid / (q.dh_ntiles_m * q.dh_ntiles_n);
+    const int t = bid % (q.dh_ntiles_m * q.dh_ntiles_n);
+    const int mt = t / q.dh_ntiles_n, nt = t % q.dh_ntiles_n;
+    const int m0 = mt * BTM, n0 = nt * BTN;
+    const int kb = s * q.ksplit, ke = min(p.Vp, kb + q.ksplit);
+    gemm_tile<false>((const U16 *)p.gbuf + (int64_t)m0 * p.Vp, p.Vp, min(BTM, p.rows - m0),
+              (const U16 *)p.wt + (int64_t)n0 * p.Vp, p.Vp, min(BTN, a.D - n0), kb, ke, acc,
+              reinterpret_cast<U16 *>(smem_raw));
+    float *dst = q.dh_part + (int64_t)s * p.rows * a.D;
+#pragma unroll
+    for (int mi = 0; mi < 8; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + 128 * wm + 16 * mi + 4 * g + r, n = n0 + 64 * wn + 16 * ni + l16;
+                if (m < p.rows && n < a.D) dst[(int64_t)m * a.D + n] = acc[mi][ni][r];
+            }
+}
+
+// dH rows of the chunk = sum of the split partials, written as bf16
+__global__ void __launch_bounds__(THREADS) dh_reduce_kernel(GroupParams q) {
+    const BwdParams &p = q.p;
+    const qpam_ce_bwd_args &a = p.a;
+    const int64_t n = (int64_t)p.rows * a.D;
+    for (int64_t e = blockIdx.x * (int64_t)THREADS + threadIdx.x; e < n; e += (int64_t)gridDim.x * THREADS) {
+        float x = 0.f;
+        for (int s = 0; s < q.splits; ++s) x += q.dh_part[s * n + e];
+        const int64_t r = e / a.D, c = e - r * a.D;
+        reinterpret_cast<U16 *>(a.dh)[(int64_t)(p.row0 + r) * a.lddh + c] = f32_to_bf16(x);
+    }
+}
+
+constexpr int DH_SPLITS = 8;
+}  // namespace big
+
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+template <typename T> constexpr bool is_bf() { return sizeof(T) == 2; }
+
+// vocab tile of the logits kernels: 256 on the bf16 big-tile path, 128 otherwise
+template <typename T> constexpr int vocab_tile() { return is_bf<T>() ? big::BTN : VT; }
+template <typename T> constexpr int row_tile() { return is_bf<T>() ? big::BTM : BM; }
 
 template <typename T>
 size_t fwd_ws(const qpam_ce_fwd_args &a) {
-    const int64_t n_vt = (a.V + VT - 1) / VT;
+    const int64_t n_vt = (a.V + vocab_tile<T>() - 1) / vocab_tile<T>();
     return (size_t)a.N * n_vt * 12 + 256;
 }
 
 template <typename T>
 size_t bwd_ws(const qpam_ce_bwd_args &a) {
-    const int64_t Vp = round_up(a.V, VT), chunk = std::min(a.chunk, a.N), Rp = round_up((int)chunk, BM);
+    const int64_t Vp = round_up(a.V, vocab_tile<T>()), chunk = std::min(a.chunk, a.N);
+    const int64_t Rp = round_up((int)chunk, row_tile<T>());
     const int64_t elems = (int64_t)a.D * Vp + chunk * Vp + Vp * Rp + (int64_t)a.D * Rp;
-    return (size_t)(elems * sizeof(T)) + 4 * 256;
+    size_t bytes = (size_t)(elems * sizeof(T)) + 4 * 256;
+    if (is_bf<T>()) bytes += (size_t)big::DH_SPLITS * chunk * a.D * sizeof(float) + 256;
+    return bytes;
 }
 
 template <typename T>
 int run_fwd(const qpam_ce_fwd_args &a, hipStream_t stream) {
     FwdParams p;
     p.a = a;
-    p.n_vt = (a.V + VT - 1) / VT;
+    p.n_vt = (a.V + vocab_tile<T>() - 1) / vocab_tile<T>();
     char *ws = (char *)a.workspace;
     const int64_t cnt = (int64_t)a.N * p.n_vt;
     p.part_m = (float *)ws;
     p.part_s = p.part_m + cnt;
     p.part_i = (int *)(p.part_s + cnt);
     p.red = nullptr;
-    const size_t smem = gemm_smem<T>();
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)ce_fwd_tile_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)smem));
-    dim3 grid(p.n_vt, (a.N + BM - 1) / BM);
-    hipLaunchKernelGGL(ce_fwd_tile_kernel<T>, grid, dim3(THREADS), smem, stream, p);
-    int st = launch_status("ce_fwd_tile_kernel");
+    int st;
+    if (is_bf<T>()) {
+        QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::fwd_tile_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)big::SMEM));
+        dim3 grid(big::xcd_grid(p.n_vt * ((a.N + big::BTM - 1) / big::BTM)));
+        hipLaunchKernelGGL(big::fwd_tile_kernel, grid, dim3(THREADS), big::SMEM, stream, p);
+        st = launch_status("ce fwd_tile_kernel (bf16)");
+    } else {
+        const size_t smem = gemm_smem<T>();
+        QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)ce_fwd_tile_kernel<T>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        dim3 grid(p.n_vt, (a.N + BM - 1) / BM);
+        hipLaunchKernelGGL(ce_fwd_tile_kernel<T>, grid, dim3(THREADS), smem, stream, p);
+        st = launch_status("ce_fwd_tile_kernel");
+    }
     if (st) return st;
     hipLaunchKernelGGL(ce_fwd_finalize_kernel<T>, dim3((a.N + 3) / 4), dim3(THREADS), 0, stream, p);
     st = launch_status("ce_fwd_finalize_kernel");
@@ -458,8 +817,68 @@ int run_fwd(const qpam_ce_fwd_args &a, hipStream_t stream) {
     return st;
 }
 
+int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
+    using U = unsigned short;
+    big::GroupParams q;
+    BwdParams &p = q.p;
+    p.a = a;
+    p.Vp = round_up(a.V, big::BTN);
+    const int chunk = std::min(a.chunk, a.N);
+    const int Rmax = round_up(chunk, big::BTM);
+    U *ws = (U *)a.workspace;
+    p.wt = ws;
+    p.gbuf = ws + (int64_t)a.D * p.Vp;
+    p.gtbuf = (U *)p.gbuf + (int64_t)chunk * p.Vp;
+    p.ht = (U *)p.gtbuf + (int64_t)p.Vp * Rmax;
+    uintptr_t part = (uintptr_t)((U *)p.ht + (int64_t)a.D * Rmax);
+    q.dh_part = (float *)((part + 255) & ~(uintptr_t)255);
+    const size_t smem = big::SMEM;
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::grad_tile_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::dw_gemm_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::dh_gemm_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    hipLaunchKernelGGL(transpose_kernel<U>, dim3((a.D + 63) / 64, (p.Vp + 63) / 64), dim3(THREADS), 0, stream,
+                       (const U *)a.w, a.ldw, a.V, a.D, (U *)p.wt, (int64_t)p.Vp, a.D, p.Vp);
+    int st = launch_status("transpose_kernel(W)");
+    if (st) return st;
+    q.dw_ntiles_n = (a.D + big::BTN - 1) / big::BTN;
+    q.n_dw = ((a.V + big::BTM - 1) / big::BTM) * q.dw_ntiles_n;
+    q.dh_ntiles_n = q.dw_ntiles_n;
+    q.splits = big::DH_SPLITS;
+    q.ksplit = round_up((p.Vp + q.splits - 1) / q.splits, BK);
+    for (int r0 = 0; r0 < a.N; r0 += chunk) {
+        p.row0 = r0;
+        p.rows = std::min(chunk, a.N - r0);
+        p.Rp = round_up(p.rows, big::BTM);
+        hipLaunchKernelGGL(transpose_kernel<U>, dim3((a.D + 63) / 64, (p.Rp + 63) / 64), dim3(THREADS), 0, stream,
+                           (const U *)a.h + (int64_t)r0 * a.ldh, a.ldh, p.rows, a.D, (U *)p.ht, (int64_t)p.Rp, a.D,
+                           p.Rp);
+        st = launch_status("transpose_kernel(H)");
+        if (st) return st;
+        hipLaunchKernelGGL(big::grad_tile_kernel, dim3(big::xcd_grid((p.Vp / big::BTN) * (p.Rp / big::BTM))),
+                           dim3(THREADS), smem, stream, p);
+        st = launch_status("ce grad_tile_kernel (bf16)");
+        if (st) return st;
+        q.dh_ntiles_m = (p.rows + big::BTM - 1) / big::BTM;
+        hipLaunchKernelGGL(big::dw_gemm_kernel, dim3(big::xcd_grid(q.n_dw)), dim3(THREADS), smem, stream, q);
+        st = launch_status("ce dw_gemm_kernel (bf16)");
+        if (st) return st;
+        hipLaunchKernelGGL(big::dh_gemm_kernel, dim3(big::xcd_grid(q.splits * q.dh_ntiles_m * q.dh_ntiles_n)),
+                           dim3(THREADS), smem, stream, q);
+        st = launch_status("ce dh_gemm_kernel (bf16)");
+        if (st) return st;
+        hipLaunchKernelGGL(big::dh_reduce_kernel, dim3(1024), dim3(THREADS), 0, stream, q);
+        st = launch_status("ce dh_reduce_kernel");
+        if (st) return st;
+    }
+    return QPAM_OK;
+}
+
 template <typename T>
 int run_bwd(const qpam_ce_bwd_args &a, hipStream_t stream) {
+    if (is_bf<T>()) return run_bwd_bf16(a, stream);
     BwdParams p;
     p.a = a;
     p.Vp = round_up(a.V, VT);

@@ -722,6 +722,602 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
     }
 }
 
+// ------------------------------------------------------ bf16 MFMA path ----
+// bf16 q/k/v with C = 64: the three chunk-parallel backward kernels on
+// v_mfma_f32_16x16x32_bf16 with bf16 LDS tiles (dY and the fp32 states are
+// rounded to bf16 when staged; accumulation stays fp32).  q is staged
+// unscaled; q_scale is applied where q~ enters an fp32 result.
+using U16 = unsigned short;
+
+__global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParams p) {
+    extern __shared__ float smem[];
+    U16 *sGtr = reinterpret_cast<U16 *>(smem), *sGti = sGtr + PLANE_B;
+    U16 *sQtr = sGti + PLANE_B, *sQti = sQtr + PLANE_B;
+    float *sL = reinterpret_cast<float *>(sQti + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+    float *sWr = sRi + MAX_M * 64, *sWi = sWr + MAX_M * 64;  // conj(rho) q_scale per step
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * 64, valid = min(64, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    if (c == 0 && a.s0_re == nullptr) {
+        for (int m = 0; m < a.M; ++m) {
+            float *dst = gstate(p, m, b, h, 0);
+            for (int e = tid; e < 2 * D * D / 4; e += THREADS)
+                reinterpret_cast<float4 *>(dst)[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        return;
+    }
+    const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
+    const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+    lds_from_f32<true>(sGtr, (const float *)p.dy.re + go, p.dy.s2, valid);
+    lds_from_f32<true>(sGti, (const float *)p.dy.im + go, p.dy.s2, valid);
+    lds_tr_bf(sQtr, (const U16 *)a.q.re + qo, a.q.s2, valid);
+    lds_tr_bf(sQti, (const U16 *)a.q.im + qo, a.q.s2, valid);
+    if (w == 0) {
+        chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
+        for (int m = 0; m < a.M; ++m) {
+            const float cum = (lane < valid) ? __expf(sL[m * 64 + lane]) * a.q_scale : 0.f;
+            sWr[m * 64 + lane] = sRr[m * 64 + lane] * cum;
+            sWi[m * 64 + lane] = -sRi[m * 64 + lane] * cum;
+        }
+    }
+    __syncthreads();
+
+    const int i = 16 * w + l16;
+    for (int m = 0; m < a.M; ++m) {
+        floatx4 accR[4], accI[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const int t0 = 32 * kp + 8 * g;
+            const floatx8 gr = to_f(ld8(sGtr + i * PB + t0)), gi = to_f(ld8(sGti + i * PB + t0));
+            floatx8 vr, vi;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float wr = sWr[m * 64 + t0 + e], wi = sWi[m * 64 + t0 + e];
+                vr[e] = wr * gr[e] - wi * gi[e];
+                vi[e] = wr * gi[e] + wi * gr[e];
+            }
+            const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                const bf16x8 qr = ld8(sQtr + (16 * jt + l16) * PB + t0), qi = ld8(sQti + (16 * jt + l16) * PB + t0);
+                accR[jt] = mfma_bf(ar, qr, accR[jt]);
+                accR[jt] = mfma_bf(ai, qi, accR[jt]);
+                accI[jt] = mfma_bf(ai, qr, accI[jt]);
+                accI[jt] = mfma_bf(nar, qi, accI[jt]);
+            }
+        }
+        float *dst = gstate(p, m, b, h, c);
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int ii = 16 * w + 4 * g + r, j = 16 * jt + l16;
+                dst[ii * D + j] = accR[jt][r];
+                dst[D * D + ii * D + j] = accI[jt][r];
+            }
+    }
+}
+
+__global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
+    extern __shared__ float smem[];
+    U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;
+    U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
+    U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;    // V tile, later S_m^T
+    U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;
+    U16 *sKtr = sGi + PLANE_B, *sKti = sKtr + PLANE_B;
+    float *sL = reinterpret_cast<float *>(sKti + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+    float *sGL = sRi + MAX_M * 64, *sDRr = sGL + MAX_M * 64, *sDRi = sDRr + MAX_M * 64;
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * 64, valid = min(64, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const bool carry = (c > 0) || (a.s0_re != nullptr);
+    const int M = a.M;
+    const float qs = a.q_scale;
+    {
+        const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+        const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+        const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
+        lds_nat_bf(sQr, (const U16 *)a.q.re + qo, a.q.s2, valid);
+        lds_nat_bf(sQi, (const U16 *)a.q.im + qo, a.q.s2, valid);
+        lds_nat_bf(sKr, (const U16 *)a.k.re + ko, a.k.s2, valid);
+        lds_nat_bf(sKi, (const U16 *)a.k.im + ko, a.k.s2, valid);
+        lds_nat_bf(sVr, (const U16 *)a.v.re + vo, a.v.s2, valid);
+        lds_nat_bf(sVi, (const U16 *)a.v.im + vo, a.v.s2, valid);
+        lds_from_f32<false>(sGr, (const float *)p.dy.re + go, p.dy.s2, valid);
+        lds_from_f32<false>(sGi, (const float *)p.dy.im + go, p.dy.s2, valid);
+        lds_tr_bf(sKtr, (const U16 *)a.k.re + ko, a.k.s2, valid);
+        lds_tr_bf(sKti, (const U16 *)a.k.im + ko, a.k.s2, valid);
+    }
+    if (w == 0) chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
+    for (int e = tid; e < 3 * MAX_M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
+    __syncthreads();
+
+    const int tt = w;
+    const int t = 16 * tt + l16;
+    floatx4 gqR[4], gqI[4];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) gqR[jt] = gqI[jt] = zero4();
+    {
+        floatx4 wr[4], wi[4], dr[4], di[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) wr[st] = wi[st] = dr[st] = di[st] = zero4();
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const int k0 = 32 * kp + 8 * g;
+            const bf16x8 bqr = ld8(sQr + t * PB + k0), bqi = ld8(sQi + t * PB + k0);
+            const bf16x8 bgr = ld8(sGr + t * PB + k0), bgi = ld8(sGi + t * PB + k0);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > tt) continue;
+                const int s = 16 * st + l16;
+                const bf16x8 akr = ld8(sKr + s * PB + k0), aki = ld8(sKi + s * PB + k0);
+                const bf16x8 avr = ld8(sVr + s * PB + k0), avi = ld8(sVi + s * PB + k0);
+                wr[st] = mfma_bf(akr, bqr, wr[st]);
+                wr[st] = mfma_bf(aki, bqi, wr[st]);
+                wi[st] = mfma_bf(akr, bqi, wi[st]);
+                wi[st] = mfma_bf(neg_bf(aki), bqr, wi[st]);
+                dr[st] = mfma_bf(avr, bgr, dr[st]);
+                dr[st] = mfma_bf(avi, bgi, dr[st]);
+                di[st] = mfma_bf(avr, bgi, di[st]);
+                di[st] = mfma_bf(neg_bf(avi), bgr, di[st]);
+            }
+        }
+        float rowp[MAX_M], grr[MAX_M], gri[MAX_M];
+#pragma unroll
+        for (int m = 0; m < MAX_M; ++m) rowp[m] = grr[m] = gri[m] = 0.f;
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            if (st > tt) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int s = 16 * st + 4 * g + r;
+                float gwr = 0.f, gwi = 0.f;
+                float colp[MAX_M];
+#pragma unroll
+                for (int m = 0; m < MAX_M; ++m) colp[m] = 0.f;
+                if (s <= t) {
+                    float Dm[MAX_M], nc[MAX_M];
+                    float dtr = 0.f, dti = 0.f;
+#pragma unroll
+                    for (int m = 0; m < MAX_M; ++m) {
+                        Dm[m] = nc[m] = 0.f;
+                        if (m < M) {
+                            const float x = sL[m * 64 + t] - sL[m * 64 + s];
+                            Dm[m] = __expf(fminf(x, 0.f));
+                            nc[m] = (x <= 0.f && s != t) ? 1.f : 0.f;
+                            dtr += sRr[m * 64 + t] * Dm[m];
+                            dti += sRi[m * 64 + t] * Dm[m];
+                        }
+                    }
+                    const float Ar = dr[st][r], Ai = di[st][r];
+                    const float Wr = wr[st][r] * qs, Wi = wi[st][r] * qs;
+                    gwr = Ar * dtr + Ai * dti;
+                    gwi = Ai * dtr - Ar * dti;
+                    const float gdr = Ar * Wr + Ai * Wi;
+                    const float gdi = Ai * Wr - Ar * Wi;
+#pragma unroll
+                    for (int m = 0; m < MAX_M; ++m) {
+                        if (m < M) {
+                            const float gdm = gdr * sRr[m * 64 + t] + gdi * sRi[m * 64 + t];
+                            const float gp = gdm * Dm[m] * nc[m];
+                            rowp[m] += gp;
+                            colp[m] = -gp;
+                            grr[m] += gdr * Dm[m];
+                            gri[m] += gdi * Dm[m];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < MAX_M; ++m) {
+                    if (m < M) {
+                        float x = colp[m];
+#pragma unroll
+                        for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off);
+                        if (l16 == 0) atomicAdd(&sGL[m * 64 + s], x);
+                    }
+                }
+                wr[st][r] = gwr;
+                wi[st][r] = gwi;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MAX_M; ++m) {
+            if (m < M) {
+                float x = rowp[m], yr = grr[m], yi = gri[m];
+                x += __shfl_xor(x, 16);
+                x += __shfl_xor(x, 32);
+                yr += __shfl_xor(yr, 16);
+                yr += __shfl_xor(yr, 32);
+                yi += __shfl_xor(yi, 16);
+                yi += __shfl_xor(yi, 32);
+                if (g == 0) {
+                    atomicAdd(&sGL[m * 64 + t], x);
+                    atomicAdd(&sDRr[m * 64 + t], yr);
+                    atomicAdd(&sDRi[m * 64 + t], yi);
+                }
+            }
+        }
+        // intra dQ~[t][j] += sum_s gW[t,s] K[s,j]  (registers x K^T)
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            if (2 * kp > tt) continue;
+            const bf16x8 ar = frag_from_acc(wr[2 * kp], wr[2 * kp + 1]);
+            const bf16x8 ai = frag_from_acc(wi[2 * kp], wi[2 * kp + 1]);
+            const bf16x8 nai = neg_bf(ai);
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                const int row = (16 * jt + l16) * PB + 32 * kp + 4 * g;
+                const bf16x8 kr = ld4x2(sKtr + row, sKtr + row + 16), ki = ld4x2(sKti + row, sKti + row + 16);
+                gqR[jt] = mfma_bf(ar, kr, gqR[jt]);
+                gqR[jt] = mfma_bf(nai, ki, gqR[jt]);
+                gqI[jt] = mfma_bf(ar, ki, gqI[jt]);
+                gqI[jt] = mfma_bf(ai, kr, gqI[jt]);
+            }
+        }
+    }
+
+    if (carry) {
+        for (int m = 0; m < M; ++m) {
+            __syncthreads();
+            const float *src = fstate(p, m, b, h, c);
+            lds_from_f32<true>(sVr, src, D, D);          // S^T
+            lds_from_f32<true>(sVi, src + D * D, D, D);
+            __syncthreads();
+            floatx4 xr[4], xi[4];
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) xr[jt] = xi[jt] = zero4();
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                const int k0 = 32 * kp + 8 * g;
+                const bf16x8 agr = ld8(sGr + t * PB + k0), agi = ld8(sGi + t * PB + k0), nagr = neg_bf(agr);
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) {
+                    const int row = (16 * jt + l16) * PB + k0;
+                    const bf16x8 sr = ld8(sVr + row), si = ld8(sVi + row);
+                    xr[jt] = mfma_bf(agr, sr, xr[jt]);
+                    xr[jt] = mfma_bf(agi, si, xr[jt]);
+                    xi[jt] = mfma_bf(agi, sr, xi[jt]);
+                    xi[jt] = mfma_bf(nagr, si, xi[jt]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tr = 16 * tt + 4 * g + r;
+                const float cum = __expf(sL[m * 64 + tr]);
+                const float rr = sRr[m * 64 + tr], ri = sRi[m * 64 + tr];
+                const float rhr = rr * cum, rhi = ri * cum;
+                float pr = 0.f, pi = 0.f;
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) {
+                    const float x_r = xr[jt][r], x_i = xi[jt][r];
+                    gqR[jt][r] += rhr * x_r + rhi * x_i;
+                    gqI[jt][r] += rhr * x_i - rhi * x_r;
+                    const float qr = bf16_to_f32(sQr[tr * PB + 16 * jt + l16]) * qs;
+                    const float qi = bf16_to_f32(sQi[tr * PB + 16 * jt + l16]) * qs;
+                    pr += qr * x_r + qi * x_i;
+                    pi += qr * x_i - qi * x_r;
+                }
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) {
+                    pr += __shfl_xor(pr, off);
+                    pi += __shfl_xor(pi, off);
+                }
+                if (l16 == 0) {
+                    atomicAdd(&sDRr[m * 64 + tr], pr * cum);
+                    atomicAdd(&sDRi[m * 64 + tr], pi * cum);
+                    atomicAdd(&sGL[m * 64 + tr], (pr * rr + pi * ri) * cum);
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    {
+        const int64_t qo = b * p.dq.s0 + h * p.dq.s1 + (int64_t)c0 * p.dq.s2;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tr = 16 * tt + 4 * g + r;
+                if (tr < valid) {
+                    const int64_t o = qo + (int64_t)tr * p.dq.s2 + 16 * jt + l16;
+                    store_elem<U16>(p.dq.re, o, gqR[jt][r] * qs);
+                    store_elem<U16>(p.dq.im, o, gqI[jt][r] * qs);
+                }
+            }
+    }
+    if (tid < 64 && tid < valid) {
+        for (int m = 0; m < M; ++m) {
+            p.gl[chain_idx(p, m, b, h) * (int64_t)p.n_chunks * 64 + c0 + tid] = sGL[m * 64 + tid];
+            if (p.drot_re) {
+                const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + tid) * a.sr_t;
+                p.drot_re[ro] = sDRr[m * 64 + tid];
+                p.drot_im[ro] = sDRi[m * 64 + tid];
+            }
+        }
+    }
+}
+
+__global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
+    extern __shared__ float smem[];
+    U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;   // q, later G'_m
+    U16 *sQtr = sQi + PLANE_B, *sQti = sQtr + PLANE_B;                 // q^T
+    U16 *sKr = sQti + PLANE_B, *sKi = sKr + PLANE_B;
+    U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
+    U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;                    // dY, later G'_m^T
+    U16 *sGtr = sGi + PLANE_B, *sGti = sGtr + PLANE_B;                 // dY^T
+    float *sL = reinterpret_cast<float *>(sGti + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+    float *sGL = sRi + MAX_M * 64, *sDl = sGL + MAX_M * 64;
+    float *sRed = sDl + MAX_M * 64;
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * 64, valid = min(64, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const bool carry = (c > 0) || (a.s0_re != nullptr);
+    const int M = a.M;
+    const float qs = a.q_scale;
+    {
+        const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+        const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+        const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
+        lds_nat_bf(sQr, (const U16 *)a.q.re + qo, a.q.s2, valid);
+        lds_nat_bf(sQi, (const U16 *)a.q.im + qo, a.q.s2, valid);
+        lds_tr_bf(sQtr, (const U16 *)a.q.re + qo, a.q.s2, valid);
+        lds_tr_bf(sQti, (const U16 *)a.q.im + qo, a.q.s2, valid);
+        lds_nat_bf(sKr, (const U16 *)a.k.re + ko, a.k.s2, valid);
+        lds_nat_bf(sKi, (const U16 *)a.k.im + ko, a.k.s2, valid);
+        lds_nat_bf(sVr, (const U16 *)a.v.re + vo, a.v.s2, valid);
+        lds_nat_bf(sVi, (const U16 *)a.v.im + vo, a.v.s2, valid);
+        lds_from_f32<false>(sGr, (const float *)p.dy.re + go, p.dy.s2, valid);
+        lds_from_f32<false>(sGi, (const float *)p.dy.im + go, p.dy.s2, valid);
+        lds_from_f32<true>(sGtr, (const float *)p.dy.re + go, p.dy.s2, valid);
+        lds_from_f32<true>(sGti, (const float *)p.dy.im + go, p.dy.s2, valid);
+    }
+    if (w == 0) {
+        chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
+        for (int m = 0; m < M; ++m) {
+            const float L = sL[m * 64 + lane];
+            const float Llast = sL[m * 64 + valid - 1];
+            sDl[m * 64 + lane] = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
+            sGL[m * 64 + lane] =
+                (lane < valid) ? p.gl[chain_idx(p, m, b, h) * (int64_t)p.n_chunks * 64 + c0 + lane] : 0.f;
+        }
+    }
+    __syncthreads();
+
+    const int st = w;
+    const int s = 16 * st + l16;
+    floatx4 gvR[4], gvI[4], gkR[4], gkI[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) gvR[it] = gvI[it] = gkR[it] = gkI[it] = zero4();
+    {
+        floatx4 wr[4], wi[4], dr[4], di[4];  // W[t][s], dA[t][s], t-tiles tt >= st
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) wr[tt] = wi[tt] = dr[tt] = di[tt] = zero4();
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const int k0 = 32 * kp + 8 * g;
+            const bf16x8 bkr = ld8(sKr + s * PB + k0), bki = ld8(sKi + s * PB + k0);
+            const bf16x8 bvr = ld8(sVr + s * PB + k0), bvi = ld8(sVi + s * PB + k0);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                if (tt < st) continue;
+                const int t = 16 * tt + l16;
+                const bf16x8 aqr = ld8(sQr + t * PB + k0), aqi = ld8(sQi + t * PB + k0);
+                const bf16x8 agr = ld8(sGr + t * PB + k0), agi = ld8(sGi + t * PB + k0);
+                wr[tt] = mfma_bf(aqr, bkr, wr[tt]);
+                wr[tt] = mfma_bf(aqi, bki, wr[tt]);
+                wi[tt] = mfma_bf(aqi, bkr, wi[tt]);
+                wi[tt] = mfma_bf(neg_bf(aqr), bki, wi[tt]);
+                dr[tt] = mfma_bf(agr, bvr, dr[tt]);
+                dr[tt] = mfma_bf(agi, bvi, dr[tt]);
+                di[tt] = mfma_bf(agi, bvr, di[tt]);
+                di[tt] = mfma_bf(neg_bf(agr), bvi, di[tt]);
+            }
+        }
+        // A = (q_scale W) D~ -> (wr, wi);  q_scale gW = q_scale dA conj(D~) -> (dr, di)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            if (tt < st) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * tt + 4 * g + r;
+                float dtr = 0.f, dti = 0.f;
+                if (s <= t) {
+#pragma unroll
+                    for (int m = 0; m < MAX_M; ++m) {
+                        if (m < M) {
+                            const float Dm = __expf(fminf(sL[m * 64 + t] - sL[m * 64 + s], 0.f));
+                            dtr += sRr[m * 64 + t] * Dm;
+                            dti += sRi[m * 64 + t] * Dm;
+                        }
+                    }
+                }
+                const float Wr = wr[tt][r] * qs, Wi = wi[tt][r] * qs, Ar = dr[tt][r] * qs, Ai = di[tt][r] * qs;
+                wr[tt][r] = Wr * dtr - Wi * dti;
+                wi[tt][r] = Wr * dti + Wi * dtr;
+                dr[tt][r] = Ar * dtr + Ai * dti;
+                di[tt][r] = Ai * dtr - Ar * dti;
+            }
+        }
+        // dV[s][i] += sum_t conj(A[t,s]) G[t,i];  dK[s][j] += sum_t conj(q_s gW[t,s]) q[t,j]
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            if (2 * kp + 1 < st) continue;
+            const bf16x8 ar = frag_from_acc(wr[2 * kp], wr[2 * kp + 1]);
+            const bf16x8 ai = frag_from_acc(wi[2 * kp], wi[2 * kp + 1]);
+            const bf16x8 gr_ = frag_from_acc(dr[2 * kp], dr[2 * kp + 1]);
+            const bf16x8 gi_ = frag_from_acc(di[2 * kp], di[2 * kp + 1]);
+            const bf16x8 nai = neg_bf(ai), ngi = neg_bf(gi_);
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int row = (16 * it + l16) * PB + 32 * kp + 4 * g;
+                const bf16x8 yr = ld4x2(sGtr + row, sGtr + row + 16), yi = ld4x2(sGti + row, sGti + row + 16);
+                gvR[it] = mfma_bf(ar, yr, gvR[it]);
+                gvR[it] = mfma_bf(ai, yi, gvR[it]);
+                gvI[it] = mfma_bf(ar, yi, gvI[it]);
+                gvI[it] = mfma_bf(nai, yr, gvI[it]);
+                const bf16x8 qr = ld4x2(sQtr + row, sQtr + row + 16), qi = ld4x2(sQti + row, sQti + row + 16);
+                gkR[it] = mfma_bf(gr_, qr, gkR[it]);
+                gkR[it] = mfma_bf(gi_, qi, gkR[it]);
+                gkI[it] = mfma_bf(gr_, qi, gkI[it]);
+                gkI[it] = mfma_bf(ngi, qr, gkI[it]);
+            }
+        }
+    }
+
+    // state-write gradients with G'_m = dS after this chunk
+    for (int m = 0; m < M; ++m) {
+        __syncthreads();
+        const float *gsrc = gstate(p, m, b, h, c);
+        lds_from_f32<false>(sQr, gsrc, D, D);            // G'
+        lds_from_f32<false>(sQi, gsrc + D * D, D, D);
+        lds_from_f32<true>(sGr, gsrc, D, D);             // G'^T
+        lds_from_f32<true>(sGi, gsrc + D * D, D, D);
+        if (carry) {  // g_total = sum Re(conj(G') S) straight from the fp32 workspace
+            const float *ssrc = fstate(p, m, b, h, c);
+            float part = 0.f;
+            for (int e = tid; e < 2 * D * D / 4; e += THREADS) {
+                const float4 x = reinterpret_cast<const float4 *>(gsrc)[e];
+                const float4 y = reinterpret_cast<const float4 *>(ssrc)[e];
+                part += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+            if (lane == 0) sRed[w] = part;
+        }
+        __syncthreads();
+        const float dls = sDl[m * 64 + s];
+        floatx4 zr[4], zi[4];
+#pragma unroll
+        for (int it = 0; it < 4; ++it) zr[it] = zi[it] = zero4();
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const int k0 = 32 * kp + 8 * g;
+            const bf16x8 akr = ld8(sKr + s * PB + k0), aki = ld8(sKi + s * PB + k0), naki = neg_bf(aki);
+            const floatx8 vrf = to_f(ld8(sVr + s * PB + k0)), vif = to_f(ld8(sVi + s * PB + k0));
+            const bf16x8 avr = to_bf(vrf * dls), avi = to_bf(vif * dls), navr = neg_bf(avr);
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int row = (16 * it + l16) * PB + k0;
+                // Z[s][i] = sum_j K[s,j] G'[i,j]
+                const bf16x8 gpr = ld8(sQr + row), gpi = ld8(sQi + row);
+                zr[it] = mfma_bf(akr, gpr, zr[it]);
+                zr[it] = mfma_bf(naki, gpi, zr[it]);
+                zi[it] = mfma_bf(akr, gpi, zi[it]);
+                zi[it] = mfma_bf(aki, gpr, zi[it]);
+                // dK[s][j] += dl[s] sum_i V[s,i] conj(G'[i,j])   (j = 16 it + l16, G'^T rows)
+                const bf16x8 gtr = ld8(sGr + row), gti = ld8(sGi + row);
+                gkR[it] = mfma_bf(avr, gtr, gkR[it]);
+                gkR[it] = mfma_bf(avi, gti, gkR[it]);
+                gkI[it] = mfma_bf(avi, gtr, gkI[it]);
+                gkI[it] = mfma_bf(navr, gti, gkI[it]);
+            }
+        }
+        // lane holds Z[s' = 16st + 4g + r][i = 16it + l16]
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int sr_ = 16 * st + 4 * g + r;
+            const float dl = sDl[m * 64 + sr_];
+            float gdl = 0.f;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const float z_r = zr[it][r], z_i = zi[it][r];
+                const float vr = bf16_to_f32(sVr[sr_ * PB + 16 * it + l16]);
+                const float vi = bf16_to_f32(sVi[sr_ * PB + 16 * it + l16]);
+                gdl += vr * z_r + vi * z_i;
+                gvR[it][r] += dl * z_r;
+                gvI[it][r] += dl * z_i;
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) gdl += __shfl_xor(gdl, off);
+            if (l16 == 0 && sr_ < valid) {
+                const float x = sL[m * 64 + valid - 1] - sL[m * 64 + sr_];
+                const float gp = (x <= 0.f) ? gdl * dl : 0.f;
+                if (sr_ != valid - 1) {
+                    atomicAdd(&sGL[m * 64 + valid - 1], gp);
+                    atomicAdd(&sGL[m * 64 + sr_], -gp);
+                }
+            }
+        }
+        __syncthreads();
+        if (tid == 0 && carry) {
+            const float gtot = sRed[0] + sRed[1] + sRed[2] + sRed[3];
+            sGL[m * 64 + valid - 1] += gtot * __expf(sL[m * 64 + valid - 1]);
+        }
+    }
+    __syncthreads();
+
+    {
+        const int64_t ko = b * p.dk.s0 + h * p.dk.s1 + (int64_t)c0 * p.dk.s2;
+        const int64_t vo = b * p.dv.s0 + h * p.dv.s1 + (int64_t)c0 * p.dv.s2;
+#pragma unroll
+        for (int it = 0; it < 4; ++it)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int sr_ = 16 * st + 4 * g + r;
+                if (sr_ < valid) {
+                    const int64_t o1 = ko + (int64_t)sr_ * p.dk.s2 + 16 * it + l16;
+                    store_elem<U16>(p.dk.re, o1, gkR[it][r]);
+                    store_elem<U16>(p.dk.im, o1, gkI[it][r]);
+                    const int64_t o2 = vo + (int64_t)sr_ * p.dv.s2 + 16 * it + l16;
+                    store_elem<U16>(p.dv.re, o2, gvR[it][r]);
+                    store_elem<U16>(p.dv.im, o2, gvI[it][r]);
+                }
+            }
+    }
+    if (w == 0) {
+        for (int m = 0; m < M; ++m) {
+            float x = (lane < valid) ? sGL[m * 64 + lane] : 0.f;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_down(x, off);
+                if (lane + off < 64) x += y;
+            }
+            if (lane < valid) {
+                const int64_t go = m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)(c0 + lane) * a.sg_t;
+                p.dgamma[go] = x / (a.gamma[go] + LOG_EPS);
+            }
+        }
+    }
+}
+
+constexpr size_t gcs_bf16_smem() { return (size_t)4 * PLANE_B * 2 + 5 * MAX_M * 64 * sizeof(float); }
+constexpr size_t qside_bf16_smem() { return (size_t)10 * PLANE_B * 2 + 6 * MAX_M * 64 * sizeof(float); }
+constexpr size_t kside_bf16_smem() { return (size_t)12 * PLANE_B * 2 + (5 * MAX_M * 64 + 4) * sizeof(float); }
+
+int launch_bwd_bf16(const BwdParams &p, hipStream_t stream) {
+    const qpam_scan_args &a = p.a;
+    dim3 grid(p.n_chunks, a.H, a.B);
+    const size_t s1 = gcs_bf16_smem(), s3 = qside_bf16_smem(), s4 = kside_bf16_smem();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_chunk_state_bf16_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)query_side_bf16_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_bf16_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
+    hipLaunchKernelGGL(grad_chunk_state_bf16_kernel, grid, dim3(THREADS), s1, stream, p);
+    int st = launch_status("grad_chunk_state_bf16_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * 8), dim3(THREADS), 0, stream, p);
+    st = launch_status("grad_state_scan_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(query_side_bf16_kernel, grid, dim3(THREADS), s3, stream, p);
+    st = launch_status("query_side_bf16_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(key_side_bf16_kernel, grid, dim3(THREADS), s4, stream, p);
+    return launch_status("key_side_bf16_kernel");
+}
+
 template <int C>
 size_t gcs_smem() { return (size_t)(4 * C * P + 3 * MAX_M * 64) * sizeof(float); }
 template <int C>
@@ -801,6 +1397,7 @@ int scan_bwd(const qpam_scan_bwd_args *bw, hipStream_t stream) {
     p.gstates = (float *)bw->workspace;
     p.gl = p.gstates + chains * p.n_chunks * 2 * D * D;
     const bool bf = a->dtype == QPAM_BF16;
+    if (bf && a->C == 64) return launch_bwd_bf16(p, stream);
     switch (a->C) {
         case 16: return bf ? launch_bwd<unsigned short, 16>(p, stream) : launch_bwd<float, 16>(p, stream);
         case 32: return bf ? launch_bwd<unsigned short, 32>(p, stream) : launch_bwd<float, 32>(p, stream);

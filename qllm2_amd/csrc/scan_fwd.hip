@@ -312,6 +312,255 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
     }
 }
 
+// ------------------------------------------------------ bf16 MFMA path ----
+// bf16 q/k/v with C = 64: the same two chunk-parallel kernels on
+// v_mfma_f32_16x16x32_bf16 with bf16 LDS tiles (fp32 accumulation, fp32
+// states in the workspace).  Operands whose MFMA k index is the time axis are
+// staged transposed in LDS; q is staged unscaled and q_scale is applied to the
+// fp32 results it enters.
+
+__global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) {
+    extern __shared__ float smem[];
+    unsigned short *sKtr = reinterpret_cast<unsigned short *>(smem), *sKti = sKtr + PLANE_B;
+    unsigned short *sVtr = sKti + PLANE_B, *sVti = sVtr + PLANE_B;
+    float *sDl = reinterpret_cast<float *>(sVti + PLANE_B);  // [MAX_M][64]
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * 64;
+    const int valid = min(64, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    using U = unsigned short;
+    const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+    const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+    lds_tr_bf(sKtr, (const U *)a.k.re + ko, a.k.s2, valid);
+    lds_tr_bf(sKti, (const U *)a.k.im + ko, a.k.s2, valid);
+    lds_tr_bf(sVtr, (const U *)a.v.re + vo, a.v.s2, valid);
+    lds_tr_bf(sVti, (const U *)a.v.im + vo, a.v.s2, valid);
+    if (w == 0) {
+        for (int m = 0; m < a.M; ++m) {
+            const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
+            const float L = chunk_log_prefix(gp, a.sg_t, valid, lane);
+            const float Llast = __shfl(L, valid - 1);
+            sDl[m * 64 + lane] = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
+            if (lane == 0) *chunk_total_ptr(p, m, b, h, c) = __expf(Llast);
+        }
+    }
+    __syncthreads();
+
+    const int i = 16 * w + l16;  // A-operand row (value index)
+    for (int m = 0; m < a.M; ++m) {
+        floatx4 accR[4], accI[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const int s0 = 32 * kp + 8 * g;
+            floatx8 vr = to_f(ld8(sVtr + i * PB + s0)), vi = to_f(ld8(sVti + i * PB + s0));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float dl = sDl[m * 64 + s0 + e];
+                vr[e] *= dl;
+                vi[e] *= dl;
+            }
+            const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                const bf16x8 kr = ld8(sKtr + (16 * jt + l16) * PB + s0);
+                const bf16x8 ki = ld8(sKti + (16 * jt + l16) * PB + s0);
+                accR[jt] = mfma_bf(ar, kr, accR[jt]);
+                accR[jt] = mfma_bf(ai, ki, accR[jt]);
+                accI[jt] = mfma_bf(ai, kr, accI[jt]);
+                accI[jt] = mfma_bf(nar, ki, accI[jt]);
+            }
+        }
+        float *dst = chunk_state_ptr(p, m, b, h, c);
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int ii = 16 * w + 4 * g + r, j = 16 * jt + l16;
+                dst[ii * D + j] = accR[jt][r];
+                dst[D * D + ii * D + j] = accI[jt][r];
+            }
+    }
+}
+
+__global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p) {
+    extern __shared__ float smem[];
+    using U = unsigned short;
+    U *sQr = reinterpret_cast<U *>(smem), *sQi = sQr + PLANE_B;
+    U *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;  // K tile, later the carried state S_m
+    U *sVtr = sKi + PLANE_B, *sVti = sVtr + PLANE_B;
+    float *sL = reinterpret_cast<float *>(sVti + PLANE_B);
+    float *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * 64;
+    const int valid = min(64, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const bool general = (a.M > 1) || (a.rot_re != nullptr);
+    const bool carry = (c > 0) || (a.s0_re != nullptr);
+    const float qs = a.q_scale;
+
+    const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+    const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+    const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+    lds_nat_bf(sQr, (const U *)a.q.re + qo, a.q.s2, valid);
+    lds_nat_bf(sQi, (const U *)a.q.im + qo, a.q.s2, valid);
+    lds_nat_bf(sKr, (const U *)a.k.re + ko, a.k.s2, valid);
+    lds_nat_bf(sKi, (const U *)a.k.im + ko, a.k.s2, valid);
+    lds_tr_bf(sVtr, (const U *)a.v.re + vo, a.v.s2, valid);
+    lds_tr_bf(sVti, (const U *)a.v.im + vo, a.v.s2, valid);
+    if (w == 0) {
+        for (int m = 0; m < a.M; ++m) {
+            const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
+            sL[m * 64 + lane] = chunk_log_prefix(gp, a.sg_t, valid, lane);
+            float rr = 1.f, ri = 0.f;
+            if (a.rot_re && lane < valid) {
+                const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + lane) * a.sr_t;
+                rr = a.rot_re[ro];
+                ri = a.rot_im[ro];
+            }
+            sRr[m * 64 + lane] = rr;
+            sRi[m * 64 + lane] = ri;
+        }
+    }
+    __syncthreads();
+
+    const int tt = w;
+    const int t = 16 * tt + l16;  // this lane's query row in the transposed score tiles
+    floatx4 yR[4], yI[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) yR[it] = yI[it] = zero4();
+    {
+        floatx4 wr[4], wi[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) wr[st] = wi[st] = zero4();
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const bf16x8 bqr = ld8(sQr + t * PB + 32 * kp + 8 * g), bqi = ld8(sQi + t * PB + 32 * kp + 8 * g);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > tt) continue;
+                const int s = 16 * st + l16;
+                const bf16x8 akr = ld8(sKr + s * PB + 32 * kp + 8 * g), aki = ld8(sKi + s * PB + 32 * kp + 8 * g);
+                wr[st] = mfma_bf(akr, bqr, wr[st]);
+                wr[st] = mfma_bf(aki, bqi, wr[st]);
+                wi[st] = mfma_bf(akr, bqi, wi[st]);
+                wi[st] = mfma_bf(neg_bf(aki), bqr, wi[st]);
+            }
+        }
+        // A = (q_scale W) . D~ ; lane holds s = 16st + 4g + r, t = 16tt + l16
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            if (st > tt) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int s = 16 * st + 4 * g + r;
+                float dre = 0.f, dim = 0.f;
+                if (s <= t) {
+                    if (!general) {
+                        dre = __expf(fminf(sL[t] - sL[s], 0.f));
+                    } else {
+                        for (int m = 0; m < a.M; ++m) {
+                            const float dm = __expf(fminf(sL[m * 64 + t] - sL[m * 64 + s], 0.f));
+                            dre += sRr[m * 64 + t] * dm;
+                            dim += sRi[m * 64 + t] * dm;
+                        }
+                    }
+                }
+                const float xr = wr[st][r] * qs, xi = wi[st][r] * qs;
+                wr[st][r] = xr * dre - xi * dim;
+                wi[st][r] = xr * dim + xi * dre;
+            }
+        }
+        // Y += A V: k-step kp covers s-tiles 2kp, 2kp+1 (registers), V^T rows give the matching k order
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            if (2 * kp > tt) continue;
+            const bf16x8 ar = frag_from_acc(wr[2 * kp], wr[2 * kp + 1]);
+            const bf16x8 ai = frag_from_acc(wi[2 * kp], wi[2 * kp + 1]);
+            const bf16x8 nai = neg_bf(ai);
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int row = (16 * it + l16) * PB + 32 * kp + 4 * g;
+                const bf16x8 vr = ld4x2(sVtr + row, sVtr + row + 16), vi = ld4x2(sVti + row, sVti + row + 16);
+                yR[it] = mfma_bf(ar, vr, yR[it]);
+                yR[it] = mfma_bf(nai, vi, yR[it]);
+                yI[it] = mfma_bf(ar, vi, yI[it]);
+                yI[it] = mfma_bf(ai, vr, yI[it]);
+            }
+        }
+    }
+
+    // carried read  Y += sum_m (rho_m q_scale q) S_in,m^T
+    if (carry) {
+        for (int m = 0; m < a.M; ++m) {
+            __syncthreads();
+            const float *src = chunk_state_ptr(p, m, b, h, c);
+            lds_from_f32<false>(sKr, src, D, D);
+            lds_from_f32<false>(sKi, src + D * D, D, D);
+            __syncthreads();
+            const float cum = __expf(sL[m * 64 + t]) * qs;
+            const float rhr = sRr[m * 64 + t] * cum, rhi = sRi[m * 64 + t] * cum;
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                const floatx8 qr = to_f(ld8(sQr + t * PB + 32 * kp + 8 * g));
+                const floatx8 qi = to_f(ld8(sQi + t * PB + 32 * kp + 8 * g));
+                const bf16x8 pr = to_bf(rhr * qr - rhi * qi), pi = to_bf(rhr * qi + rhi * qr), npi = neg_bf(pi);
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const int row = (16 * it + l16) * PB + 32 * kp + 8 * g;
+                    const bf16x8 sr = ld8(sKr + row), si = ld8(sKi + row);
+                    yR[it] = mfma_bf(pr, sr, yR[it]);
+                    yR[it] = mfma_bf(npi, si, yR[it]);
+                    yI[it] = mfma_bf(pr, si, yI[it]);
+                    yI[it] = mfma_bf(pi, sr, yI[it]);
+                }
+            }
+        }
+    }
+
+    const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)c0 * a.y.s2;
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tr = 16 * tt + 4 * g + r;
+            if (tr < valid) {
+                a.y.re[yo + (int64_t)tr * a.y.s2 + 16 * it + l16] = yR[it][r];
+                a.y.im[yo + (int64_t)tr * a.y.s2 + 16 * it + l16] = yI[it][r];
+            }
+        }
+}
+
+constexpr size_t state_bf16_smem() { return (size_t)4 * PLANE_B * 2 + MAX_M * 64 * sizeof(float); }
+constexpr size_t output_bf16_smem() { return (size_t)6 * PLANE_B * 2 + 3 * MAX_M * 64 * sizeof(float); }
+
+int launch_fwd_bf16(const FwdParams &p, hipStream_t stream) {
+    const qpam_scan_args &a = p.a;
+    dim3 grid(p.n_chunks, a.H, a.B);
+    const size_t s1 = state_bf16_smem(), s3 = output_bf16_smem();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_state_bf16_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_bf16_kernel,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
+    hipLaunchKernelGGL(chunk_state_bf16_kernel, grid, dim3(THREADS), s1, stream, p);
+    int st = launch_status("chunk_state_bf16_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(state_scan_kernel, dim3(a.M * a.B * a.H * 8), dim3(THREADS), 0, stream, p);
+    st = launch_status("state_scan_kernel");
+    if (st) return st;
+    if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));
+    hipLaunchKernelGGL(chunk_output_bf16_kernel, grid, dim3(THREADS), s3, stream, p);
+    st = launch_status("chunk_output_bf16_kernel");
+    if (st) return st;
+    if (a.prof_ev[1]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[1], stream));
+    return QPAM_OK;
+}
+
 template <int C>
 size_t state_smem() { return (size_t)(4 * C * P + MAX_M * 64) * sizeof(float); }
 template <int C>
@@ -390,6 +639,7 @@ int scan_fwd(const qpam_scan_args *a, hipStream_t stream) {
     p.totals = p.states + chains * p.n_chunks * 2 * D * D;
     QPAM_REQUIRE(p.n_chunks <= 65535 && a->H <= 65535 && a->B <= 65535, "qpam_scan_fwd: grid too large");
     const bool bf = a->dtype == QPAM_BF16;
+    if (bf && a->C == 64) return launch_fwd_bf16(p, stream);
     switch (a->C) {
         case 16: return bf ? launch_fwd<unsigned short, 16>(p, stream) : launch_fwd<float, 16>(p, stream);
         case 32: return bf ? launch_fwd<unsigned short, 32>(p, stream) : launch_fwd<float, 32>(p, stream);

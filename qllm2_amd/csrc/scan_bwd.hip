@@ -69,16 +69,43 @@ __device__ __forceinline__ void store_elem<unsigned short>(float *base, int64_t 
     reinterpret_cast<unsigned short *>(base)[idx] = f32_to_bf16(v);
 }
 
-// contiguous 64x64 fp32 plane -> LDS (pitch P)
-__device__ __forceinline__ void load_state_plane(float *lds, const float *src) {
-    for (int idx = threadIdx.x; idx < D * 16; idx += THREADS) {
-        const int r = idx >> 4, c4 = idx & 15;
-        const float4 v = *reinterpret_cast<const float4 *>(src + r * D + 4 * c4);
-        float *dst = lds + r * P + 4 * c4;
-        dst[0] = v.x;
-        dst[1] = v.y;
-        dst[2] = v.z;
-        dst[3] = v.w;
+// contiguous 64x64 fp32 planes (re, im) -> LDS (pitch P); both loads in flight together
+__device__ __forceinline__ void load_state_planes(float *lds_re, float *lds_im, const float *src) {
+    F32Tile<D> tr, ti;
+    tile_load<D>(tr, src, D, D);
+    tile_load<D>(ti, src + D * D, D, D);
+    tile_store<D>(lds_re, tr, 1.f);
+    tile_store<D>(lds_im, ti, 1.f);
+}
+
+// Stage the fp32 upstream-gradient tiles (NG of them) and the input tiles (NI)
+// of one chunk; with fp32 inputs all loads form one batch.
+template <typename Tin, int C, int NG, int NI>
+__device__ __forceinline__ void stage_grad_and_inputs(float *const (&gdst)[NG], const float *const (&gsrc)[NG],
+                                                      int64_t gst, float *const (&idst)[NI],
+                                                      const Tin *const (&isrc)[NI], const int64_t (&ist)[NI],
+                                                      const float (&isc)[NI], int valid) {
+    if constexpr (std::is_same<Tin, float>::value) {
+        float *dst[NG + NI];
+        const float *src[NG + NI];
+        int64_t st[NG + NI];
+        float sc[NG + NI];
+#pragma unroll
+        for (int i = 0; i < NI; ++i) dst[i] = idst[i], src[i] = isrc[i], st[i] = ist[i], sc[i] = isc[i];
+#pragma unroll
+        for (int i = 0; i < NG; ++i) dst[NI + i] = gdst[i], src[NI + i] = gsrc[i], st[NI + i] = gst, sc[NI + i] = 1.f;
+        F32Tile<C> t[NG + NI];
+#pragma unroll
+        for (int i = 0; i < NG + NI; ++i) tile_load<C>(t[i], src[i], st[i], valid);
+#pragma unroll
+        for (int i = 0; i < NG + NI; ++i) tile_store<C>(dst[i], t[i], sc[i]);
+    } else {
+        float gsc[NG];
+        int64_t gsts[NG];
+#pragma unroll
+        for (int i = 0; i < NG; ++i) gsc[i] = 1.f, gsts[i] = gst;
+        stage_tiles<float, C, NG>(gdst, gsrc, gsts, gsc, valid);
+        stage_tiles<Tin, C, NI>(idst, isrc, ist, isc, valid);
     }
 }
 
@@ -124,10 +151,15 @@ __global__ void __launch_bounds__(THREADS) grad_chunk_state_kernel(BwdParams p) 
     }
     const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
     const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
-    load_tile<float>(sGr, (const float *)p.dy.re + go, p.dy.s2, C, valid, 1.f);
-    load_tile<float>(sGi, (const float *)p.dy.im + go, p.dy.s2, C, valid, 1.f);
-    load_tile<Tin>(sQr, (const Tin *)a.q.re + qo, a.q.s2, C, valid, a.q_scale);
-    load_tile<Tin>(sQi, (const Tin *)a.q.im + qo, a.q.s2, C, valid, a.q_scale);
+    {
+        float *const gd[2] = {sGr, sGi};
+        const float *const gs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
+        float *const id[2] = {sQr, sQi};
+        const Tin *const is[2] = {(const Tin *)a.q.re + qo, (const Tin *)a.q.im + qo};
+        const int64_t ist[2] = {a.q.s2, a.q.s2};
+        const float isc[2] = {a.q_scale, a.q_scale};
+        stage_grad_and_inputs<Tin, C, 2, 2>(gd, gs, p.dy.s2, id, is, ist, isc, valid);
+    }
     if (w == 0) chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
     __syncthreads();
 
@@ -217,14 +249,14 @@ __global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
         const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
         const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
         const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-        load_tile<Tin>(sQr, (const Tin *)a.q.re + qo, a.q.s2, C, valid, a.q_scale);
-        load_tile<Tin>(sQi, (const Tin *)a.q.im + qo, a.q.s2, C, valid, a.q_scale);
-        load_tile<Tin>(sKr, (const Tin *)a.k.re + ko, a.k.s2, C, valid, 1.f);
-        load_tile<Tin>(sKi, (const Tin *)a.k.im + ko, a.k.s2, C, valid, 1.f);
-        load_tile<Tin>(sVr, (const Tin *)a.v.re + vo, a.v.s2, C, valid, 1.f);
-        load_tile<Tin>(sVi, (const Tin *)a.v.im + vo, a.v.s2, C, valid, 1.f);
-        load_tile<float>(sGr, (const float *)p.dy.re + go, p.dy.s2, C, valid, 1.f);
-        load_tile<float>(sGi, (const float *)p.dy.im + go, p.dy.s2, C, valid, 1.f);
+        float *const gd[2] = {sGr, sGi};
+        const float *const gs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
+        float *const id[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
+        const Tin *const is[6] = {(const Tin *)a.q.re + qo, (const Tin *)a.q.im + qo, (const Tin *)a.k.re + ko,
+                                  (const Tin *)a.k.im + ko, (const Tin *)a.v.re + vo, (const Tin *)a.v.im + vo};
+        const int64_t ist[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        const float isc[6] = {a.q_scale, a.q_scale, 1.f, 1.f, 1.f, 1.f};
+        stage_grad_and_inputs<Tin, C, 2, 6>(gd, gs, p.dy.s2, id, is, ist, isc, valid);
     }
     if (w == 0) chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
     for (int e = tid; e < 3 * MAX_M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
@@ -373,8 +405,7 @@ __global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
         for (int m = 0; m < M; ++m) {
             __syncthreads();
             const float *src = fstate(p, m, b, h, c);
-            load_state_plane(sVr, src);
-            load_state_plane(sVi, src + D * D);
+            load_state_planes(sVr, sVi, src);
             __syncthreads();
             if (!active) continue;
             const int t = 16 * tt + l16;
@@ -480,14 +511,14 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
         const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
         const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
         const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-        load_tile<Tin>(sQr, (const Tin *)a.q.re + qo, a.q.s2, C, valid, a.q_scale);
-        load_tile<Tin>(sQi, (const Tin *)a.q.im + qo, a.q.s2, C, valid, a.q_scale);
-        load_tile<Tin>(sKr, (const Tin *)a.k.re + ko, a.k.s2, C, valid, 1.f);
-        load_tile<Tin>(sKi, (const Tin *)a.k.im + ko, a.k.s2, C, valid, 1.f);
-        load_tile<Tin>(sVr, (const Tin *)a.v.re + vo, a.v.s2, C, valid, 1.f);
-        load_tile<Tin>(sVi, (const Tin *)a.v.im + vo, a.v.s2, C, valid, 1.f);
-        load_tile<float>(sGr, (const float *)p.dy.re + go, p.dy.s2, C, valid, 1.f);
-        load_tile<float>(sGi, (const float *)p.dy.im + go, p.dy.s2, C, valid, 1.f);
+        float *const gd[2] = {sGr, sGi};
+        const float *const gs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
+        float *const id[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
+        const Tin *const is[6] = {(const Tin *)a.q.re + qo, (const Tin *)a.q.im + qo, (const Tin *)a.k.re + ko,
+                                  (const Tin *)a.k.im + ko, (const Tin *)a.v.re + vo, (const Tin *)a.v.im + vo};
+        const int64_t ist[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        const float isc[6] = {a.q_scale, a.q_scale, 1.f, 1.f, 1.f, 1.f};
+        stage_grad_and_inputs<Tin, C, 2, 6>(gd, gs, p.dy.s2, id, is, ist, isc, valid);
     }
     if (w == 0) {
         chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
@@ -593,12 +624,19 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
     for (int m = 0; m < M; ++m) {
         __syncthreads();
         const float *gsrc = gstate(p, m, b, h, c);
-        load_state_plane(sQr, gsrc);
-        load_state_plane(sQi, gsrc + D * D);
         if (carry) {
             const float *ssrc = fstate(p, m, b, h, c);
-            load_state_plane(sGr, ssrc);
-            load_state_plane(sGi, ssrc + D * D);
+            F32Tile<D> t[4];
+            tile_load<D>(t[0], gsrc, D, D);
+            tile_load<D>(t[1], gsrc + D * D, D, D);
+            tile_load<D>(t[2], ssrc, D, D);
+            tile_load<D>(t[3], ssrc + D * D, D, D);
+            tile_store<D>(sQr, t[0], 1.f);
+            tile_store<D>(sQi, t[1], 1.f);
+            tile_store<D>(sGr, t[2], 1.f);
+            tile_store<D>(sGi, t[3], 1.f);
+        } else {
+            load_state_planes(sQr, sQi, gsrc);
         }
         __syncthreads();
         // g_total = sum Re(conj(G') S)
@@ -750,10 +788,15 @@ __global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParam
     }
     const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
     const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
-    lds_from_f32<true>(sGtr, (const float *)p.dy.re + go, p.dy.s2, valid);
-    lds_from_f32<true>(sGti, (const float *)p.dy.im + go, p.dy.s2, valid);
-    lds_tr_bf(sQtr, (const U16 *)a.q.re + qo, a.q.s2, valid);
-    lds_tr_bf(sQti, (const U16 *)a.q.im + qo, a.q.s2, valid);
+    {
+        U16 *const bd[2] = {sQtr, sQti};
+        const U16 *const bs[2] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo};
+        const int64_t bst[2] = {a.q.s2, a.q.s2};
+        U16 *const fd[2] = {sGtr, sGti};
+        const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
+        const int64_t fst[2] = {p.dy.s2, p.dy.s2};
+        stage_mixed<2, 0x3u, 2, 0x3u>(bd, bs, bst, fd, fs, fst, valid);
+    }
     if (w == 0) {
         chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
         for (int m = 0; m < a.M; ++m) {
@@ -824,16 +867,15 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
         const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
         const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
         const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-        lds_nat_bf(sQr, (const U16 *)a.q.re + qo, a.q.s2, valid);
-        lds_nat_bf(sQi, (const U16 *)a.q.im + qo, a.q.s2, valid);
-        lds_nat_bf(sKr, (const U16 *)a.k.re + ko, a.k.s2, valid);
-        lds_nat_bf(sKi, (const U16 *)a.k.im + ko, a.k.s2, valid);
-        lds_nat_bf(sVr, (const U16 *)a.v.re + vo, a.v.s2, valid);
-        lds_nat_bf(sVi, (const U16 *)a.v.im + vo, a.v.s2, valid);
-        lds_from_f32<false>(sGr, (const float *)p.dy.re + go, p.dy.s2, valid);
-        lds_from_f32<false>(sGi, (const float *)p.dy.im + go, p.dy.s2, valid);
-        lds_tr_bf(sKtr, (const U16 *)a.k.re + ko, a.k.s2, valid);
-        lds_tr_bf(sKti, (const U16 *)a.k.im + ko, a.k.s2, valid);
+        U16 *const bd[8] = {sQr, sQi, sKr, sKi, sVr, sVi, sKtr, sKti};
+        const U16 *const bs[8] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
+                                  (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo,
+                                  (const U16 *)a.k.re + ko, (const U16 *)a.k.im + ko};
+        const int64_t bst[8] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2, a.k.s2, a.k.s2};
+        U16 *const fd[2] = {sGr, sGi};
+        const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
+        const int64_t fst[2] = {p.dy.s2, p.dy.s2};
+        stage_mixed<8, 0xC0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
     }
     if (w == 0) chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
     for (int e = tid; e < 3 * MAX_M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
@@ -967,8 +1009,12 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
         for (int m = 0; m < M; ++m) {
             __syncthreads();
             const float *src = fstate(p, m, b, h, c);
-            lds_from_f32<true>(sVr, src, D, D);          // S^T
-            lds_from_f32<true>(sVi, src + D * D, D, D);
+            {  // S^T
+                U16 *const fd[2] = {sVr, sVi};
+                const float *const fs[2] = {src, src + D * D};
+                const int64_t fst[2] = {D, D};
+                stage_f32_as_bf<2, 0x3u>(fd, fs, fst, D);
+            }
             __syncthreads();
             floatx4 xr[4], xi[4];
 #pragma unroll
@@ -1069,18 +1115,16 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
         const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
         const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
         const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-        lds_nat_bf(sQr, (const U16 *)a.q.re + qo, a.q.s2, valid);
-        lds_nat_bf(sQi, (const U16 *)a.q.im + qo, a.q.s2, valid);
-        lds_tr_bf(sQtr, (const U16 *)a.q.re + qo, a.q.s2, valid);
-        lds_tr_bf(sQti, (const U16 *)a.q.im + qo, a.q.s2, valid);
-        lds_nat_bf(sKr, (const U16 *)a.k.re + ko, a.k.s2, valid);
-        lds_nat_bf(sKi, (const U16 *)a.k.im + ko, a.k.s2, valid);
-        lds_nat_bf(sVr, (const U16 *)a.v.re + vo, a.v.s2, valid);
-        lds_nat_bf(sVi, (const U16 *)a.v.im + vo, a.v.s2, valid);
-        lds_from_f32<false>(sGr, (const float *)p.dy.re + go, p.dy.s2, valid);
-        lds_from_f32<false>(sGi, (const float *)p.dy.im + go, p.dy.s2, valid);
-        lds_from_f32<true>(sGtr, (const float *)p.dy.re + go, p.dy.s2, valid);
-        lds_from_f32<true>(sGti, (const float *)p.dy.im + go, p.dy.s2, valid);
+        U16 *const bd[8] = {sQr, sQi, sQtr, sQti, sKr, sKi, sVr, sVi};
+        const U16 *const bs[8] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.q.re + qo,
+                                  (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko, (const U16 *)a.k.im + ko,
+                                  (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
+        const int64_t bst[8] = {a.q.s2, a.q.s2, a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        const float *const gre = (const float *)p.dy.re + go, *const gim = (const float *)p.dy.im + go;
+        U16 *const fd[4] = {sGr, sGi, sGtr, sGti};
+        const float *const fs[4] = {gre, gim, gre, gim};
+        const int64_t fst[4] = {p.dy.s2, p.dy.s2, p.dy.s2, p.dy.s2};
+        stage_mixed<8, 0x0Cu, 4, 0xCu>(bd, bs, bst, fd, fs, fst, valid);
     }
     if (w == 0) {
         chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
@@ -1179,10 +1223,12 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
     for (int m = 0; m < M; ++m) {
         __syncthreads();
         const float *gsrc = gstate(p, m, b, h, c);
-        lds_from_f32<false>(sQr, gsrc, D, D);            // G'
-        lds_from_f32<false>(sQi, gsrc + D * D, D, D);
-        lds_from_f32<true>(sGr, gsrc, D, D);             // G'^T
-        lds_from_f32<true>(sGi, gsrc + D * D, D, D);
+        {  // G' natural into sQ*, G'^T into sG*
+            U16 *const fd[4] = {sQr, sQi, sGr, sGi};
+            const float *const fs[4] = {gsrc, gsrc + D * D, gsrc, gsrc + D * D};
+            const int64_t fst[4] = {D, D, D, D};
+            stage_f32_as_bf<4, 0xCu>(fd, fs, fst, D);
+        }
         if (carry) {  // g_total = sum Re(conj(G') S) straight from the fp32 workspace
             const float *ssrc = fstate(p, m, b, h, c);
             float part = 0.f;

@@ -1,6 +1,8 @@
 // Shared pieces of the chunked PAM scan kernels (forward and backward).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace qpam {
@@ -51,6 +53,52 @@ __device__ __forceinline__ void load_tile<unsigned short>(float *lds, const unsi
         float *dst = lds + r * P + 8 * c8;
 #pragma unroll
         for (int e = 0; e < 8; ++e) dst[e] = bf16_to_f32(v[e]) * scale;
+    }
+}
+
+// Register-staged tile copies: every global load of a tile is issued before any
+// LDS store, so a block waits for one memory latency per batch of tiles rather
+// than one per load.  fp32 [ROWS x 64] tile: ROWS/16 float4 per thread.
+template <int ROWS>
+struct F32Tile {
+    float4 v[ROWS / 16];
+};
+
+template <int ROWS>
+__device__ __forceinline__ void tile_load(F32Tile<ROWS> &t, const float *base, int64_t st, int valid) {
+#pragma unroll
+    for (int i = 0; i < ROWS / 16; ++i) {
+        const int idx = threadIdx.x + i * THREADS, r = idx >> 4, c4 = idx & 15;
+        t.v[i] = (r < valid) ? *reinterpret_cast<const float4 *>(base + (int64_t)r * st + 4 * c4)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+template <int ROWS>
+__device__ __forceinline__ void tile_store(float *lds, const F32Tile<ROWS> &t, float scale) {
+#pragma unroll
+    for (int i = 0; i < ROWS / 16; ++i) {
+        const int idx = threadIdx.x + i * THREADS, r = idx >> 4, c4 = idx & 15;
+        float *dst = lds + r * P + 4 * c4;
+        *reinterpret_cast<float4 *>(dst) =
+            make_float4(t.v[i].x * scale, t.v[i].y * scale, t.v[i].z * scale, t.v[i].w * scale);
+    }
+}
+
+// Stage N [C x 64] tiles of element type Tin into fp32 LDS (pitch P), scaled.
+// fp32 sources are copied through registers with all loads in flight at once.
+template <typename Tin, int C, int N>
+__device__ __forceinline__ void stage_tiles(float *const (&dst)[N], const Tin *const (&src)[N],
+                                            const int64_t (&st)[N], const float (&scale)[N], int valid) {
+    if constexpr (std::is_same<Tin, float>::value) {
+        F32Tile<C> t[N];
+#pragma unroll
+        for (int i = 0; i < N; ++i) tile_load<C>(t[i], src[i], st[i], valid);
+#pragma unroll
+        for (int i = 0; i < N; ++i) tile_store<C>(dst[i], t[i], scale[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) load_tile<Tin>(dst[i], src[i], st[i], C, valid, scale[i]);
     }
 }
 
@@ -110,6 +158,126 @@ __device__ __forceinline__ bf16x8 ld4x2(const unsigned short *p0, const unsigned
 // fragment from two accumulator tiles lo/hi (fp32 -> bf16), same k order as ld4x2
 __device__ __forceinline__ bf16x8 frag_from_acc(floatx4 lo, floatx4 hi) {
     return to_bf(floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+}
+
+// Register-staged bf16 / fp32 -> bf16 tile copies (all loads of a batch are
+// issued before the LDS stores).  TR selects the thread -> element mapping that
+// suits the transposed store (consecutive lanes on consecutive rows).
+struct B16Regs {
+    uint4 v[2];
+};
+template <bool TR>
+__device__ __forceinline__ void regs_load_bf(B16Regs &t, const unsigned short *src, int64_t st, int valid) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int idx = threadIdx.x + i * THREADS;
+        const int r = TR ? (idx & 63) : (idx >> 3), c8 = TR ? (idx >> 6) : (idx & 7);
+        t.v[i] = (r < valid) ? *reinterpret_cast<const uint4 *>(src + (int64_t)r * st + 8 * c8) : make_uint4(0, 0, 0, 0);
+    }
+}
+template <bool TR>
+__device__ __forceinline__ void regs_store_bf(unsigned short *lds, const B16Regs &t) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int idx = threadIdx.x + i * THREADS;
+        const int r = TR ? (idx & 63) : (idx >> 3), c8 = TR ? (idx >> 6) : (idx & 7);
+        if (TR) {
+            const ushortx8 u = __builtin_bit_cast(ushortx8, t.v[i]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) lds[(8 * c8 + e) * PB + r] = u[e];
+        } else {
+            *reinterpret_cast<uint4 *>(lds + r * PB + 8 * c8) = t.v[i];
+        }
+    }
+}
+struct F32Regs {
+    float4 v[4];
+};
+template <bool TR>
+__device__ __forceinline__ void regs_load_f32(F32Regs &t, const float *src, int64_t st, int valid) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int idx = threadIdx.x + i * THREADS;
+        const int r = TR ? (idx & 63) : (idx >> 4), c4 = TR ? (idx >> 6) : (idx & 15);
+        t.v[i] = (r < valid) ? *reinterpret_cast<const float4 *>(src + (int64_t)r * st + 4 * c4)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+template <bool TR>
+__device__ __forceinline__ void regs_store_f32_as_bf(unsigned short *lds, const F32Regs &t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int idx = threadIdx.x + i * THREADS;
+        const int r = TR ? (idx & 63) : (idx >> 4), c4 = TR ? (idx >> 6) : (idx & 15);
+        const float f[4] = {t.v[i].x, t.v[i].y, t.v[i].z, t.v[i].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const unsigned short b = f32_to_bf16(f[e]);
+            if (TR) lds[(4 * c4 + e) * PB + r] = b;
+            else lds[r * PB + 4 * c4 + e] = b;
+        }
+    }
+}
+
+// Batched variants: N tiles, tile i stored transposed when bit i of TRMASK is set.
+template <int N, unsigned TRMASK>
+__device__ __forceinline__ void stage_bf(unsigned short *const (&dst)[N], const unsigned short *const (&src)[N],
+                                         const int64_t (&st)[N], int valid) {
+    B16Regs r[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if ((TRMASK >> i) & 1u) regs_load_bf<true>(r[i], src[i], st[i], valid);
+        else regs_load_bf<false>(r[i], src[i], st[i], valid);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if ((TRMASK >> i) & 1u) regs_store_bf<true>(dst[i], r[i]);
+        else regs_store_bf<false>(dst[i], r[i]);
+    }
+}
+template <int N, unsigned TRMASK>
+__device__ __forceinline__ void stage_f32_as_bf(unsigned short *const (&dst)[N], const float *const (&src)[N],
+                                                const int64_t (&st)[N], int valid) {
+    F32Regs r[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if ((TRMASK >> i) & 1u) regs_load_f32<true>(r[i], src[i], st[i], valid);
+        else regs_load_f32<false>(r[i], src[i], st[i], valid);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        if ((TRMASK >> i) & 1u) regs_store_f32_as_bf<true>(dst[i], r[i]);
+        else regs_store_f32_as_bf<false>(dst[i], r[i]);
+    }
+}
+
+// NB bf16 tiles and NF fp32 tiles (stored as bf16) in one batch of loads.
+template <int NB, unsigned TRB, int NF, unsigned TRF>
+__device__ __forceinline__ void stage_mixed(unsigned short *const (&bdst)[NB], const unsigned short *const (&bsrc)[NB],
+                                            const int64_t (&bst)[NB], unsigned short *const (&fdst)[NF],
+                                            const float *const (&fsrc)[NF], const int64_t (&fst)[NF], int valid) {
+    B16Regs rb[NB];
+    F32Regs rf[NF];
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+        if ((TRF >> i) & 1u) regs_load_f32<true>(rf[i], fsrc[i], fst[i], valid);
+        else regs_load_f32<false>(rf[i], fsrc[i], fst[i], valid);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if ((TRB >> i) & 1u) regs_load_bf<true>(rb[i], bsrc[i], bst[i], valid);
+        else regs_load_bf<false>(rb[i], bsrc[i], bst[i], valid);
+    }
+#pragma unroll
+    for (int i = 0; i < NF; ++i) {
+        if ((TRF >> i) & 1u) regs_store_f32_as_bf<true>(fdst[i], rf[i]);
+        else regs_store_f32_as_bf<false>(fdst[i], rf[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+        if ((TRB >> i) & 1u) regs_store_bf<true>(bdst[i], rb[i]);
+        else regs_store_bf<false>(bdst[i], rb[i]);
+    }
 }
 
 // [64 x 64] bf16 rows (row stride st, rows >= valid zero) -> LDS natural [r][c]

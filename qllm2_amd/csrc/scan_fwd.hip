@@ -55,10 +55,14 @@ __global__ void __launch_bounds__(THREADS) chunk_state_kernel(FwdParams p) {
 
     const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
     const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-    load_tile<Tin>(sKr, (const Tin *)a.k.re + ko, a.k.s2, C, valid, 1.f);
-    load_tile<Tin>(sKi, (const Tin *)a.k.im + ko, a.k.s2, C, valid, 1.f);
-    load_tile<Tin>(sVr, (const Tin *)a.v.re + vo, a.v.s2, C, valid, 1.f);
-    load_tile<Tin>(sVi, (const Tin *)a.v.im + vo, a.v.s2, C, valid, 1.f);
+    {
+        float *const dst[4] = {sKr, sKi, sVr, sVi};
+        const Tin *const src[4] = {(const Tin *)a.k.re + ko, (const Tin *)a.k.im + ko, (const Tin *)a.v.re + vo,
+                                   (const Tin *)a.v.im + vo};
+        const int64_t st[4] = {a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        const float sc[4] = {1.f, 1.f, 1.f, 1.f};
+        stage_tiles<Tin, C, 4>(dst, src, st, sc, valid);
+    }
     if (w == 0) {
         for (int m = 0; m < a.M; ++m) {
             const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
@@ -157,12 +161,14 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
     const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
     const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
     const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-    load_tile<Tin>(sQr, (const Tin *)a.q.re + qo, a.q.s2, C, valid, a.q_scale);
-    load_tile<Tin>(sQi, (const Tin *)a.q.im + qo, a.q.s2, C, valid, a.q_scale);
-    load_tile<Tin>(sKr, (const Tin *)a.k.re + ko, a.k.s2, C, valid, 1.f);
-    load_tile<Tin>(sKi, (const Tin *)a.k.im + ko, a.k.s2, C, valid, 1.f);
-    load_tile<Tin>(sVr, (const Tin *)a.v.re + vo, a.v.s2, C, valid, 1.f);
-    load_tile<Tin>(sVi, (const Tin *)a.v.im + vo, a.v.s2, C, valid, 1.f);
+    {
+        float *const dst[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
+        const Tin *const src[6] = {(const Tin *)a.q.re + qo, (const Tin *)a.q.im + qo, (const Tin *)a.k.re + ko,
+                                   (const Tin *)a.k.im + ko, (const Tin *)a.v.re + vo, (const Tin *)a.v.im + vo};
+        const int64_t st[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        const float sc[6] = {a.q_scale, a.q_scale, 1.f, 1.f, 1.f, 1.f};
+        stage_tiles<Tin, C, 6>(dst, src, st, sc, valid);
+    }
     if (w == 0) {
         for (int m = 0; m < a.M; ++m) {
             const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
@@ -260,14 +266,12 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
         for (int m = 0; m < a.M; ++m) {
             __syncthreads();  // previous users of sK* are done
             const float *src = chunk_state_ptr(p, m, b, h, c);
-            for (int idx = tid; idx < 2 * D * 16; idx += THREADS) {
-                const int pl = idx >> 10, r = (idx >> 4) & 63, c4 = idx & 15;
-                const float4 v = *reinterpret_cast<const float4 *>(src + pl * D * D + r * D + 4 * c4);
-                float *dst = (pl ? sKi : sKr) + r * P + 4 * c4;
-                dst[0] = v.x;
-                dst[1] = v.y;
-                dst[2] = v.z;
-                dst[3] = v.w;
+            {
+                F32Tile<D> sr, si;
+                tile_load<D>(sr, src, D, D);
+                tile_load<D>(si, src + D * D, D, D);
+                tile_store<D>(sKr, sr, 1.f);
+                tile_store<D>(sKi, si, 1.f);
             }
             __syncthreads();
             if (active) {
@@ -333,10 +337,13 @@ __global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) 
     using U = unsigned short;
     const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
     const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-    lds_tr_bf(sKtr, (const U *)a.k.re + ko, a.k.s2, valid);
-    lds_tr_bf(sKti, (const U *)a.k.im + ko, a.k.s2, valid);
-    lds_tr_bf(sVtr, (const U *)a.v.re + vo, a.v.s2, valid);
-    lds_tr_bf(sVti, (const U *)a.v.im + vo, a.v.s2, valid);
+    {
+        U *const dst[4] = {sKtr, sKti, sVtr, sVti};
+        const U *const src[4] = {(const U *)a.k.re + ko, (const U *)a.k.im + ko, (const U *)a.v.re + vo,
+                                 (const U *)a.v.im + vo};
+        const int64_t st[4] = {a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        stage_bf<4, 0xFu>(dst, src, st, valid);
+    }
     if (w == 0) {
         for (int m = 0; m < a.M; ++m) {
             const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
@@ -407,12 +414,13 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
     const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
     const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
     const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-    lds_nat_bf(sQr, (const U *)a.q.re + qo, a.q.s2, valid);
-    lds_nat_bf(sQi, (const U *)a.q.im + qo, a.q.s2, valid);
-    lds_nat_bf(sKr, (const U *)a.k.re + ko, a.k.s2, valid);
-    lds_nat_bf(sKi, (const U *)a.k.im + ko, a.k.s2, valid);
-    lds_tr_bf(sVtr, (const U *)a.v.re + vo, a.v.s2, valid);
-    lds_tr_bf(sVti, (const U *)a.v.im + vo, a.v.s2, valid);
+    {
+        U *const dst[6] = {sQr, sQi, sKr, sKi, sVtr, sVti};
+        const U *const src[6] = {(const U *)a.q.re + qo, (const U *)a.q.im + qo, (const U *)a.k.re + ko,
+                                 (const U *)a.k.im + ko, (const U *)a.v.re + vo, (const U *)a.v.im + vo};
+        const int64_t st[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        stage_bf<6, 0x30u>(dst, src, st, valid);
+    }
     if (w == 0) {
         for (int m = 0; m < a.M; ++m) {
             const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
@@ -500,8 +508,12 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
         for (int m = 0; m < a.M; ++m) {
             __syncthreads();
             const float *src = chunk_state_ptr(p, m, b, h, c);
-            lds_from_f32<false>(sKr, src, D, D);
-            lds_from_f32<false>(sKi, src + D * D, D, D);
+            {
+                U *const dst[2] = {sKr, sKi};
+                const float *const srcs[2] = {src, src + D * D};
+                const int64_t st[2] = {D, D};
+                stage_f32_as_bf<2, 0u>(dst, srcs, st, D);
+            }
             __syncthreads();
             const float cum = __expf(sL[m * 64 + t]) * qs;
             const float rhr = sRr[m * 64 + t] * cum, rhi = sRi[m * 64 + t] * cum;

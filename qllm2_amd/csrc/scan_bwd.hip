@@ -769,9 +769,9 @@ using U16 = unsigned short;
 
 __global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
-    U16 *sGtr = reinterpret_cast<U16 *>(smem), *sGti = sGtr + PLANE_B;
-    U16 *sQtr = sGti + PLANE_B, *sQti = sQtr + PLANE_B;
-    float *sL = reinterpret_cast<float *>(sQti + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+    U16 *sGr = reinterpret_cast<U16 *>(smem), *sGi = sGr + PLANE_B;
+    U16 *sQr = sGi + PLANE_B, *sQi = sQr + PLANE_B;
+    float *sL = reinterpret_cast<float *>(sQi + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
     float *sWr = sRi + MAX_M * 64, *sWi = sWr + MAX_M * 64;  // conj(rho) q_scale per step
 
     const qpam_scan_args &a = p.a;
@@ -789,13 +789,13 @@ __global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParam
     const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
     const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
     {
-        U16 *const bd[2] = {sQtr, sQti};
+        U16 *const bd[2] = {sQr, sQi};
         const U16 *const bs[2] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo};
         const int64_t bst[2] = {a.q.s2, a.q.s2};
-        U16 *const fd[2] = {sGtr, sGti};
+        U16 *const fd[2] = {sGr, sGi};
         const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
         const int64_t fst[2] = {p.dy.s2, p.dy.s2};
-        stage_mixed<2, 0x3u, 2, 0x3u>(bd, bs, bst, fd, fs, fst, valid);
+        stage_mixed<2, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
     }
     if (w == 0) {
         chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
@@ -807,7 +807,7 @@ __global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParam
     }
     __syncthreads();
 
-    const int i = 16 * w + l16;
+    const int i0 = 16 * w;  // this wave's value rows i0 + l16
     for (int m = 0; m < a.M; ++m) {
         floatx4 accR[4], accI[4];
 #pragma unroll
@@ -815,7 +815,7 @@ __global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParam
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             const int t0 = 32 * kp + 8 * g;
-            const floatx8 gr = to_f(ld8(sGtr + i * PB + t0)), gi = to_f(ld8(sGti + i * PB + t0));
+            const floatx8 gr = to_f(ld_tr(sGr, t0, t0 + 4, i0)), gi = to_f(ld_tr(sGi, t0, t0 + 4, i0));
             floatx8 vr, vi;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -826,7 +826,7 @@ __global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParam
             const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
 #pragma unroll
             for (int jt = 0; jt < 4; ++jt) {
-                const bf16x8 qr = ld8(sQtr + (16 * jt + l16) * PB + t0), qi = ld8(sQti + (16 * jt + l16) * PB + t0);
+                const bf16x8 qr = ld_tr(sQr, t0, t0 + 4, 16 * jt), qi = ld_tr(sQi, t0, t0 + 4, 16 * jt);
                 accR[jt] = mfma_bf(ar, qr, accR[jt]);
                 accR[jt] = mfma_bf(ai, qi, accR[jt]);
                 accI[jt] = mfma_bf(ai, qr, accI[jt]);
@@ -849,10 +849,9 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
     U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;
     U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
-    U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;    // V tile, later S_m^T
+    U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;    // V tile, later S_m
     U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;
-    U16 *sKtr = sGi + PLANE_B, *sKti = sKtr + PLANE_B;
-    float *sL = reinterpret_cast<float *>(sKti + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+    float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
     float *sGL = sRi + MAX_M * 64, *sDRr = sGL + MAX_M * 64, *sDRi = sDRr + MAX_M * 64;
 
     const qpam_scan_args &a = p.a;
@@ -867,15 +866,14 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
         const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
         const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
         const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-        U16 *const bd[8] = {sQr, sQi, sKr, sKi, sVr, sVi, sKtr, sKti};
-        const U16 *const bs[8] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
-                                  (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo,
-                                  (const U16 *)a.k.re + ko, (const U16 *)a.k.im + ko};
-        const int64_t bst[8] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2, a.k.s2, a.k.s2};
+        U16 *const bd[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
+        const U16 *const bs[6] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
+                                  (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
+        const int64_t bst[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
         U16 *const fd[2] = {sGr, sGi};
         const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
         const int64_t fst[2] = {p.dy.s2, p.dy.s2};
-        stage_mixed<8, 0xC0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
+        stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
     }
     if (w == 0) chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
     for (int e = tid; e < 3 * MAX_M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
@@ -986,7 +984,7 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
                 }
             }
         }
-        // intra dQ~[t][j] += sum_s gW[t,s] K[s,j]  (registers x K^T)
+        // intra dQ~[t][j] += sum_s gW[t,s] K[s,j]  (registers x transposed reads of K)
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             if (2 * kp > tt) continue;
@@ -995,8 +993,8 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
             const bf16x8 nai = neg_bf(ai);
 #pragma unroll
             for (int jt = 0; jt < 4; ++jt) {
-                const int row = (16 * jt + l16) * PB + 32 * kp + 4 * g;
-                const bf16x8 kr = ld4x2(sKtr + row, sKtr + row + 16), ki = ld4x2(sKti + row, sKti + row + 16);
+                const int r0 = 32 * kp + 4 * g;
+                const bf16x8 kr = ld_tr(sKr, r0, r0 + 16, 16 * jt), ki = ld_tr(sKi, r0, r0 + 16, 16 * jt);
                 gqR[jt] = mfma_bf(ar, kr, gqR[jt]);
                 gqR[jt] = mfma_bf(nai, ki, gqR[jt]);
                 gqI[jt] = mfma_bf(ar, ki, gqI[jt]);
@@ -1009,11 +1007,11 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
         for (int m = 0; m < M; ++m) {
             __syncthreads();
             const float *src = fstate(p, m, b, h, c);
-            {  // S^T
+            {  // S natural; read transposed below
                 U16 *const fd[2] = {sVr, sVi};
                 const float *const fs[2] = {src, src + D * D};
                 const int64_t fst[2] = {D, D};
-                stage_f32_as_bf<2, 0x3u>(fd, fs, fst, D);
+                stage_f32_as_bf<2, 0x0u>(fd, fs, fst, D);
             }
             __syncthreads();
             floatx4 xr[4], xi[4];
@@ -1025,8 +1023,7 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
                 const bf16x8 agr = ld8(sGr + t * PB + k0), agi = ld8(sGi + t * PB + k0), nagr = neg_bf(agr);
 #pragma unroll
                 for (int jt = 0; jt < 4; ++jt) {
-                    const int row = (16 * jt + l16) * PB + k0;
-                    const bf16x8 sr = ld8(sVr + row), si = ld8(sVi + row);
+                    const bf16x8 sr = ld_tr(sVr, k0, k0 + 4, 16 * jt), si = ld_tr(sVi, k0, k0 + 4, 16 * jt);
                     xr[jt] = mfma_bf(agr, sr, xr[jt]);
                     xr[jt] = mfma_bf(agi, si, xr[jt]);
                     xi[jt] = mfma_bf(agi, sr, xi[jt]);
@@ -1094,12 +1091,10 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
 __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
     U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;   // q, later G'_m
-    U16 *sQtr = sQi + PLANE_B, *sQti = sQtr + PLANE_B;                 // q^T
-    U16 *sKr = sQti + PLANE_B, *sKi = sKr + PLANE_B;
+    U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
     U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
-    U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;                    // dY, later G'_m^T
-    U16 *sGtr = sGi + PLANE_B, *sGti = sGtr + PLANE_B;                 // dY^T
-    float *sL = reinterpret_cast<float *>(sGti + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+    U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;                    // dY
+    float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
     float *sGL = sRi + MAX_M * 64, *sDl = sGL + MAX_M * 64;
     float *sRed = sDl + MAX_M * 64;
 
@@ -1115,16 +1110,14 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
         const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
         const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
         const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-        U16 *const bd[8] = {sQr, sQi, sQtr, sQti, sKr, sKi, sVr, sVi};
-        const U16 *const bs[8] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.q.re + qo,
-                                  (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko, (const U16 *)a.k.im + ko,
-                                  (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
-        const int64_t bst[8] = {a.q.s2, a.q.s2, a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        const float *const gre = (const float *)p.dy.re + go, *const gim = (const float *)p.dy.im + go;
-        U16 *const fd[4] = {sGr, sGi, sGtr, sGti};
-        const float *const fs[4] = {gre, gim, gre, gim};
-        const int64_t fst[4] = {p.dy.s2, p.dy.s2, p.dy.s2, p.dy.s2};
-        stage_mixed<8, 0x0Cu, 4, 0xCu>(bd, bs, bst, fd, fs, fst, valid);
+        U16 *const bd[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
+        const U16 *const bs[6] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
+                                  (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
+        const int64_t bst[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        U16 *const fd[2] = {sGr, sGi};
+        const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
+        const int64_t fst[2] = {p.dy.s2, p.dy.s2};
+        stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
     }
     if (w == 0) {
         chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
@@ -1204,13 +1197,13 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
             const bf16x8 nai = neg_bf(ai), ngi = neg_bf(gi_);
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
-                const int row = (16 * it + l16) * PB + 32 * kp + 4 * g;
-                const bf16x8 yr = ld4x2(sGtr + row, sGtr + row + 16), yi = ld4x2(sGti + row, sGti + row + 16);
+                const int r0 = 32 * kp + 4 * g;
+                const bf16x8 yr = ld_tr(sGr, r0, r0 + 16, 16 * it), yi = ld_tr(sGi, r0, r0 + 16, 16 * it);
                 gvR[it] = mfma_bf(ar, yr, gvR[it]);
                 gvR[it] = mfma_bf(ai, yi, gvR[it]);
                 gvI[it] = mfma_bf(ar, yi, gvI[it]);
                 gvI[it] = mfma_bf(nai, yr, gvI[it]);
-                const bf16x8 qr = ld4x2(sQtr + row, sQtr + row + 16), qi = ld4x2(sQti + row, sQti + row + 16);
+                const bf16x8 qr = ld_tr(sQr, r0, r0 + 16, 16 * it), qi = ld_tr(sQi, r0, r0 + 16, 16 * it);
                 gkR[it] = mfma_bf(gr_, qr, gkR[it]);
                 gkR[it] = mfma_bf(gi_, qi, gkR[it]);
                 gkI[it] = mfma_bf(gr_, qi, gkI[it]);
@@ -1223,11 +1216,11 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
     for (int m = 0; m < M; ++m) {
         __syncthreads();
         const float *gsrc = gstate(p, m, b, h, c);
-        {  // G' natural into sQ*, G'^T into sG*
-            U16 *const fd[4] = {sQr, sQi, sGr, sGi};
-            const float *const fs[4] = {gsrc, gsrc + D * D, gsrc, gsrc + D * D};
-            const int64_t fst[4] = {D, D, D, D};
-            stage_f32_as_bf<4, 0xCu>(fd, fs, fst, D);
+        {  // G' natural into sQ*
+            U16 *const fd[2] = {sQr, sQi};
+            const float *const fs[2] = {gsrc, gsrc + D * D};
+            const int64_t fst[2] = {D, D};
+            stage_f32_as_bf<2, 0x0u>(fd, fs, fst, D);
         }
         if (carry) {  // g_total = sum Re(conj(G') S) straight from the fp32 workspace
             const float *ssrc = fstate(p, m, b, h, c);
@@ -1261,8 +1254,8 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
                 zr[it] = mfma_bf(naki, gpi, zr[it]);
                 zi[it] = mfma_bf(akr, gpi, zi[it]);
                 zi[it] = mfma_bf(aki, gpr, zi[it]);
-                // dK[s][j] += dl[s] sum_i V[s,i] conj(G'[i,j])   (j = 16 it + l16, G'^T rows)
-                const bf16x8 gtr = ld8(sGr + row), gti = ld8(sGi + row);
+                // dK[s][j] += dl[s] sum_i V[s,i] conj(G'[i,j])   (j = 16 it + l16, transposed reads of G')
+                const bf16x8 gtr = ld_tr(sQr, k0, k0 + 4, 16 * it), gti = ld_tr(sQi, k0, k0 + 4, 16 * it);
                 gkR[it] = mfma_bf(avr, gtr, gkR[it]);
                 gkR[it] = mfma_bf(avi, gti, gkR[it]);
                 gkI[it] = mfma_bf(avi, gtr, gkI[it]);
@@ -1338,8 +1331,10 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
 }
 
 constexpr size_t gcs_bf16_smem() { return (size_t)4 * PLANE_B * 2 + 5 * MAX_M * 64 * sizeof(float); }
-constexpr size_t qside_bf16_smem() { return (size_t)10 * PLANE_B * 2 + 6 * MAX_M * 64 * sizeof(float); }
-constexpr size_t kside_bf16_smem() { return (size_t)12 * PLANE_B * 2 + (5 * MAX_M * 64 + 4) * sizeof(float); }
+// query/key side: 8 bf16 planes + per-step vectors < 80 KiB, so two blocks share a CU's 160 KiB LDS
+constexpr size_t qside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + 6 * MAX_M * 64 * sizeof(float); }
+constexpr size_t kside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (5 * MAX_M * 64 + 4) * sizeof(float); }
+static_assert(2 * qside_bf16_smem() <= 160 * 1024 && 2 * kside_bf16_smem() <= 160 * 1024, "LDS budget");
 
 int launch_bwd_bf16(const BwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;

@@ -160,6 +160,26 @@ __device__ __forceinline__ bf16x8 frag_from_acc(floatx4 lo, floatx4 hi) {
     return to_bf(floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
 }
 
+// gfx950 LDS transpose read (ds_read_b64_tr_b16).  Within each group of 16
+// lanes, lane 4a+b receives element b of the 8-byte chunks addressed by lanes
+// 4e+a (e = 0..3), so 16 lanes addressing a 4 x 16 block of a row-major bf16
+// tile receive its columns.
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ shortx4 lds_read_tr(const unsigned short *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) shortx4 *)p);
+}
+
+// MFMA operand fragment (8 k values per lane) of a natural row-major [k][n]
+// bf16 LDS tile (pitch PB) for a contraction over its rows: lane l16 of each
+// 16-lane group receives rows r0..r0+3 then r1..r1+3 of column col0 + l16.  The
+// caller folds the lane group into r0/r1; all 64 lanes must execute it.
+__device__ __forceinline__ bf16x8 ld_tr(const unsigned short *tile, int r0, int r1, int col0) {
+    const int l16 = threadIdx.x & 15;
+    const unsigned short *p = tile + (l16 >> 2) * PB + col0 + 4 * (l16 & 3);
+    const shortx4 lo = lds_read_tr(p + r0 * PB), hi = lds_read_tr(p + r1 * PB);
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // Register-staged bf16 / fp32 -> bf16 tile copies (all loads of a batch are
 // issued before the LDS stores).  TR selects the thread -> element mapping that
 // suits the transposed store (consecutive lanes on consecutive rows).
@@ -210,11 +230,12 @@ __device__ __forceinline__ void regs_store_f32_as_bf(unsigned short *lds, const 
         const int idx = threadIdx.x + i * THREADS;
         const int r = TR ? (idx & 63) : (idx >> 4), c4 = TR ? (idx >> 6) : (idx & 15);
         const float f[4] = {t.v[i].x, t.v[i].y, t.v[i].z, t.v[i].w};
+        if (TR) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const unsigned short b = f32_to_bf16(f[e]);
-            if (TR) lds[(4 * c4 + e) * PB + r] = b;
-            else lds[r * PB + 4 * c4 + e] = b;
+            for (int e = 0; e < 4; ++e) lds[(4 * c4 + e) * PB + r] = f32_to_bf16(f[e]);
+        } else {
+            const ushortx4 u = {f32_to_bf16(f[0]), f32_to_bf16(f[1]), f32_to_bf16(f[2]), f32_to_bf16(f[3])};
+            *reinterpret_cast<ushortx4 *>(lds + r * PB + 4 * c4) = u;
         }
     }
 }

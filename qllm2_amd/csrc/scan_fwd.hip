@@ -325,9 +325,9 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
 
 __global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) {
     extern __shared__ float smem[];
-    unsigned short *sKtr = reinterpret_cast<unsigned short *>(smem), *sKti = sKtr + PLANE_B;
-    unsigned short *sVtr = sKti + PLANE_B, *sVti = sVtr + PLANE_B;
-    float *sDl = reinterpret_cast<float *>(sVti + PLANE_B);  // [MAX_M][64]
+    unsigned short *sKr = reinterpret_cast<unsigned short *>(smem), *sKi = sKr + PLANE_B;
+    unsigned short *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
+    float *sDl = reinterpret_cast<float *>(sVi + PLANE_B);  // [MAX_M][64]
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -338,11 +338,11 @@ __global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) 
     const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
     const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
     {
-        U *const dst[4] = {sKtr, sKti, sVtr, sVti};
+        U *const dst[4] = {sKr, sKi, sVr, sVi};
         const U *const src[4] = {(const U *)a.k.re + ko, (const U *)a.k.im + ko, (const U *)a.v.re + vo,
                                  (const U *)a.v.im + vo};
         const int64_t st[4] = {a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        stage_bf<4, 0xFu>(dst, src, st, valid);
+        stage_bf<4, 0x0u>(dst, src, st, valid);
     }
     if (w == 0) {
         for (int m = 0; m < a.M; ++m) {
@@ -355,7 +355,7 @@ __global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) 
     }
     __syncthreads();
 
-    const int i = 16 * w + l16;  // A-operand row (value index)
+    const int i0 = 16 * w;  // this wave's A-operand rows (value index i0 + l16)
     for (int m = 0; m < a.M; ++m) {
         floatx4 accR[4], accI[4];
 #pragma unroll
@@ -363,7 +363,7 @@ __global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) 
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             const int s0 = 32 * kp + 8 * g;
-            floatx8 vr = to_f(ld8(sVtr + i * PB + s0)), vi = to_f(ld8(sVti + i * PB + s0));
+            floatx8 vr = to_f(ld_tr(sVr, s0, s0 + 4, i0)), vi = to_f(ld_tr(sVi, s0, s0 + 4, i0));
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float dl = sDl[m * 64 + s0 + e];
@@ -373,8 +373,8 @@ __global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) 
             const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
 #pragma unroll
             for (int jt = 0; jt < 4; ++jt) {
-                const bf16x8 kr = ld8(sKtr + (16 * jt + l16) * PB + s0);
-                const bf16x8 ki = ld8(sKti + (16 * jt + l16) * PB + s0);
+                const bf16x8 kr = ld_tr(sKr, s0, s0 + 4, 16 * jt);
+                const bf16x8 ki = ld_tr(sKi, s0, s0 + 4, 16 * jt);
                 accR[jt] = mfma_bf(ar, kr, accR[jt]);
                 accR[jt] = mfma_bf(ai, ki, accR[jt]);
                 accI[jt] = mfma_bf(ai, kr, accI[jt]);
@@ -398,8 +398,8 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
     using U = unsigned short;
     U *sQr = reinterpret_cast<U *>(smem), *sQi = sQr + PLANE_B;
     U *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;  // K tile, later the carried state S_m
-    U *sVtr = sKi + PLANE_B, *sVti = sVtr + PLANE_B;
-    float *sL = reinterpret_cast<float *>(sVti + PLANE_B);
+    U *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
+    float *sL = reinterpret_cast<float *>(sVi + PLANE_B);
     float *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
 
     const qpam_scan_args &a = p.a;
@@ -415,11 +415,11 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
     const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
     const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
     {
-        U *const dst[6] = {sQr, sQi, sKr, sKi, sVtr, sVti};
+        U *const dst[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
         const U *const src[6] = {(const U *)a.q.re + qo, (const U *)a.q.im + qo, (const U *)a.k.re + ko,
                                  (const U *)a.k.im + ko, (const U *)a.v.re + vo, (const U *)a.v.im + vo};
         const int64_t st[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        stage_bf<6, 0x30u>(dst, src, st, valid);
+        stage_bf<6, 0x0u>(dst, src, st, valid);
     }
     if (w == 0) {
         for (int m = 0; m < a.M; ++m) {
@@ -484,7 +484,8 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
                 wi[st][r] = xr * dim + xi * dre;
             }
         }
-        // Y += A V: k-step kp covers s-tiles 2kp, 2kp+1 (registers), V^T rows give the matching k order
+        // Y += A V: k-step kp covers s-tiles 2kp, 2kp+1 (registers); transposed reads of V give the
+        // matching k order
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             if (2 * kp > tt) continue;
@@ -493,8 +494,8 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
             const bf16x8 nai = neg_bf(ai);
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
-                const int row = (16 * it + l16) * PB + 32 * kp + 4 * g;
-                const bf16x8 vr = ld4x2(sVtr + row, sVtr + row + 16), vi = ld4x2(sVti + row, sVti + row + 16);
+                const int r0 = 32 * kp + 4 * g;
+                const bf16x8 vr = ld_tr(sVr, r0, r0 + 16, 16 * it), vi = ld_tr(sVi, r0, r0 + 16, 16 * it);
                 yR[it] = mfma_bf(ar, vr, yR[it]);
                 yR[it] = mfma_bf(nai, vi, yR[it]);
                 yI[it] = mfma_bf(ar, vi, yI[it]);

@@ -27,6 +27,8 @@ namespace scan {
 
 int validate_scan(const qpam_scan_args *a, const char *who, bool fwd_outputs);
 size_t fwd_workspace_bytes(const qpam_scan_args &a);
+bool uses_snapshots(const qpam_scan_args &a);
+size_t fwd_snapshot_offset(const qpam_scan_args &a);
 
 namespace {
 
@@ -43,6 +45,9 @@ struct BwdParams {
     const float *totals;     // forward: chunk decay totals
     float *gstates;          // dS increment per chunk -> dS after each chunk
     float *gl;               // [M][B][H][n*C] partial dL/dL_t (query side)
+    // bf16 path: entering states (forward snapshots) and dS after each chunk, bf16
+    const unsigned short *snap;
+    unsigned short *gsnap;
 };
 
 __device__ __forceinline__ int64_t chain_idx(const BwdParams &p, int m, int b, int h) {
@@ -53,6 +58,12 @@ __device__ __forceinline__ const float *fstate(const BwdParams &p, int m, int b,
 }
 __device__ __forceinline__ float *gstate(const BwdParams &p, int m, int b, int h, int c) {
     return p.gstates + (chain_idx(p, m, b, h) * p.n_chunks + c) * (2 * D * D);
+}
+__device__ __forceinline__ const unsigned short *fsnap(const BwdParams &p, int m, int b, int h, int c) {
+    return p.snap + (chain_idx(p, m, b, h) * p.n_chunks + c) * (2 * D * D);
+}
+__device__ __forceinline__ unsigned short *gsnap(const BwdParams &p, int m, int b, int h, int c) {
+    return p.gsnap + (chain_idx(p, m, b, h) * p.n_chunks + c) * (2 * D * D);
 }
 __device__ __forceinline__ float ftotal(const BwdParams &p, int m, int b, int h, int c) {
     return p.totals[chain_idx(p, m, b, h) * p.n_chunks + c];
@@ -211,12 +222,14 @@ __global__ void __launch_bounds__(THREADS) grad_state_scan_kernel(BwdParams p) {
     float4 G = make_float4(0.f, 0.f, 0.f, 0.f);
     if (p.ds_re) G = *reinterpret_cast<const float4 *>((plane ? p.ds_im : p.ds_re) + so);
     float *base = gstate(p, m, b, h, 0) + plane * D * D + off;
+    unsigned short *sbase = p.gsnap ? gsnap(p, m, b, h, 0) + plane * D * D + off : nullptr;
     const int n = p.n_chunks;
     float4 nxt = *reinterpret_cast<const float4 *>(base + (int64_t)(n - 1) * 2 * D * D);
     for (int c = n - 1; c >= 0; --c) {
         const float4 inc = nxt;
         if (c > 0) nxt = *reinterpret_cast<const float4 *>(base + (int64_t)(c - 1) * 2 * D * D);
-        *reinterpret_cast<float4 *>(base + (int64_t)c * 2 * D * D) = G;
+        if (sbase) *reinterpret_cast<ushortx4 *>(sbase + (int64_t)c * 2 * D * D) = to_bf16x4(G);
+        else *reinterpret_cast<float4 *>(base + (int64_t)c * 2 * D * D) = G;
         const float t = ftotal(p, m, b, h, c);
         G.x = t * G.x + inc.x;
         G.y = t * G.y + inc.y;
@@ -1006,12 +1019,12 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     if (carry) {
         for (int m = 0; m < M; ++m) {
             __syncthreads();
-            const float *src = fstate(p, m, b, h, c);
+            const U16 *src = fsnap(p, m, b, h, c);
             {  // S natural; read transposed below
-                U16 *const fd[2] = {sVr, sVi};
-                const float *const fs[2] = {src, src + D * D};
-                const int64_t fst[2] = {D, D};
-                stage_f32_as_bf<2, 0x0u>(fd, fs, fst, D);
+                U16 *const bd[2] = {sVr, sVi};
+                const U16 *const bs[2] = {src, src + D * D};
+                const int64_t bst[2] = {D, D};
+                stage_bf<2, 0x0u>(bd, bs, bst, D);
             }
             __syncthreads();
             floatx4 xr[4], xi[4];
@@ -1215,24 +1228,33 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
     // state-write gradients with G'_m = dS after this chunk
     for (int m = 0; m < M; ++m) {
         __syncthreads();
-        const float *gsrc = gstate(p, m, b, h, c);
-        {  // G' natural into sQ*
-            U16 *const fd[2] = {sQr, sQi};
-            const float *const fs[2] = {gsrc, gsrc + D * D};
-            const int64_t fst[2] = {D, D};
-            stage_f32_as_bf<2, 0x0u>(fd, fs, fst, D);
-        }
-        if (carry) {  // g_total = sum Re(conj(G') S) straight from the fp32 workspace
-            const float *ssrc = fstate(p, m, b, h, c);
-            float part = 0.f;
-            for (int e = tid; e < 2 * D * D / 4; e += THREADS) {
-                const float4 x = reinterpret_cast<const float4 *>(gsrc)[e];
-                const float4 y = reinterpret_cast<const float4 *>(ssrc)[e];
-                part += x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+        const U16 *gsrc = gsnap(p, m, b, h, c);
+        {  // G' natural into sQ*; with a carried state also this thread's share of S (registers)
+            B16Regs gr[2], sr[2];
+            regs_load_bf<false>(gr[0], gsrc, D, D);
+            regs_load_bf<false>(gr[1], gsrc + D * D, D, D);
+            if (carry) {
+                const U16 *ssrc = fsnap(p, m, b, h, c);
+                regs_load_bf<false>(sr[0], ssrc, D, D);
+                regs_load_bf<false>(sr[1], ssrc + D * D, D, D);
             }
+            regs_store_bf<false>(sQr, gr[0]);
+            regs_store_bf<false>(sQi, gr[1]);
+            if (carry) {  // g_total = sum Re(conj(G') S) over both planes, fp32 accumulation
+                float part = 0.f;
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
-            if (lane == 0) sRed[w] = part;
+                for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const ushortx8 x = __builtin_bit_cast(ushortx8, gr[pl].v[i]);
+                        const ushortx8 y = __builtin_bit_cast(ushortx8, sr[pl].v[i]);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) part += bf16_to_f32(x[e]) * bf16_to_f32(y[e]);
+                    }
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+                if (lane == 0) sRed[w] = part;
+            }
         }
         __syncthreads();
         const float dls = sDl[m * 64 + s];
@@ -1390,10 +1412,20 @@ int launch_bwd(const BwdParams &p, hipStream_t stream) {
     return launch_status("key_side_kernel");
 }
 
+// fp32 increments/gradient states, the partial log-decay gradient, then (bf16
+// path) the bf16 gradient-state snapshots at a 256-byte aligned offset.
+size_t bwd_snapshot_offset(const qpam_scan_args &a) {
+    const int64_t n = (a.T + a.C - 1) / a.C;
+    const int64_t chains = (int64_t)a.M * a.B * a.H;
+    return ((size_t)(chains * n * 2 * D * D + chains * n * a.C) * sizeof(float) + 255) & ~(size_t)255;
+}
+
 size_t bwd_workspace_bytes(const qpam_scan_args &a) {
     const int64_t n = (a.T + a.C - 1) / a.C;
     const int64_t chains = (int64_t)a.M * a.B * a.H;
-    return (size_t)(chains * n * 2 * D * D + chains * n * a.C) * sizeof(float);
+    size_t bytes = bwd_snapshot_offset(a);
+    if (uses_snapshots(a)) bytes += (size_t)chains * n * 2 * D * D * sizeof(unsigned short);
+    return bytes;
 }
 
 }  // namespace
@@ -1437,8 +1469,14 @@ int scan_bwd(const qpam_scan_bwd_args *bw, hipStream_t stream) {
     p.totals = p.states + chains * p.n_chunks * 2 * D * D;
     p.gstates = (float *)bw->workspace;
     p.gl = p.gstates + chains * p.n_chunks * 2 * D * D;
+    p.snap = nullptr;
+    p.gsnap = nullptr;
     const bool bf = a->dtype == QPAM_BF16;
-    if (bf && a->C == 64) return launch_bwd_bf16(p, stream);
+    if (uses_snapshots(*a)) {
+        p.snap = reinterpret_cast<const unsigned short *>((const char *)a->workspace + fwd_snapshot_offset(*a));
+        p.gsnap = reinterpret_cast<unsigned short *>((char *)bw->workspace + bwd_snapshot_offset(*a));
+        return launch_bwd_bf16(p, stream);
+    }
     switch (a->C) {
         case 16: return bf ? launch_bwd<unsigned short, 16>(p, stream) : launch_bwd<float, 16>(p, stream);
         case 32: return bf ? launch_bwd<unsigned short, 32>(p, stream) : launch_bwd<float, 32>(p, stream);

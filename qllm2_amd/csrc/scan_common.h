@@ -160,6 +160,10 @@ __device__ __forceinline__ bf16x8 frag_from_acc(floatx4 lo, floatx4 hi) {
     return to_bf(floatx8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
 }
 
+__device__ __forceinline__ ushortx4 to_bf16x4(float4 v) {
+    return ushortx4{f32_to_bf16(v.x), f32_to_bf16(v.y), f32_to_bf16(v.z), f32_to_bf16(v.w)};
+}
+
 // gfx950 LDS transpose read (ds_read_b64_tr_b16).  Within each group of 16
 // lanes, lane 4a+b receives element b of the 8-byte chunks addressed by lanes
 // 4e+a (e = 0..3), so 16 lanes addressing a 4 x 16 block of a row-major bf16

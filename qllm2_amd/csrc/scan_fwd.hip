@@ -27,13 +27,19 @@ namespace {
 struct FwdParams {
     qpam_scan_args a;
     int n_chunks;
-    float *states;   // [M][B][H][n][2][64][64]
-    float *totals;   // [M][B][H][n]
+    float *states;         // [M][B][H][n][2][64][64]
+    float *totals;         // [M][B][H][n]
+    unsigned short *snap;  // bf16 path: [M][B][H][n][2][64][64] bf16 entering states (else null)
 };
 
 __device__ __forceinline__ float *chunk_state_ptr(const FwdParams &p, int m, int b, int h, int c) {
     const int64_t idx = (((int64_t)m * p.a.B + b) * p.a.H + h) * p.n_chunks + c;
     return p.states + idx * (2 * D * D);
+}
+
+__device__ __forceinline__ unsigned short *chunk_snap_ptr(const FwdParams &p, int m, int b, int h, int c) {
+    const int64_t idx = (((int64_t)m * p.a.B + b) * p.a.H + h) * p.n_chunks + c;
+    return p.snap + idx * (2 * D * D);
 }
 
 __device__ __forceinline__ float *chunk_total_ptr(const FwdParams &p, int m, int b, int h, int c) {
@@ -109,7 +115,9 @@ __global__ void __launch_bounds__(THREADS) chunk_state_kernel(FwdParams p) {
 
 // ---------------------------------------------------------------- kernel 2 --
 // One thread per 4 consecutive state floats of one (m, b, h); 2048 float4 per
-// state (re plane then im plane), 8 blocks per state.
+// state (re plane then im plane), 8 blocks per state.  The running state stays
+// fp32; the entering state of every chunk goes either back over the increment
+// (fp32 path) or, rounded once, into the bf16 snapshot (bf16 path).
 __global__ void __launch_bounds__(THREADS) state_scan_kernel(FwdParams p) {
     const qpam_scan_args &a = p.a;
     const int chain = blockIdx.x >> 3;
@@ -123,13 +131,15 @@ __global__ void __launch_bounds__(THREADS) state_scan_kernel(FwdParams p) {
     if (a.s0_re) S = *reinterpret_cast<const float4 *>((plane ? a.s0_im : a.s0_re) + so);
 
     float *base = chunk_state_ptr(p, m, b, h, 0) + plane * D * D + off;
+    unsigned short *sbase = p.snap ? chunk_snap_ptr(p, m, b, h, 0) + plane * D * D + off : nullptr;
     const float *tot = chunk_total_ptr(p, m, b, h, 0);
     const int n = p.n_chunks;
     float4 nxt = *reinterpret_cast<const float4 *>(base);
     for (int c = 0; c < n; ++c) {
         const float4 ds = nxt;
         if (c + 1 < n) nxt = *reinterpret_cast<const float4 *>(base + (int64_t)(c + 1) * 2 * D * D);
-        *reinterpret_cast<float4 *>(base + (int64_t)c * 2 * D * D) = S;
+        if (sbase) *reinterpret_cast<ushortx4 *>(sbase + (int64_t)c * 2 * D * D) = to_bf16x4(S);
+        else *reinterpret_cast<float4 *>(base + (int64_t)c * 2 * D * D) = S;
         const float t = tot[c];
         S.x = t * S.x + ds.x;
         S.y = t * S.y + ds.y;
@@ -508,12 +518,12 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
     if (carry) {
         for (int m = 0; m < a.M; ++m) {
             __syncthreads();
-            const float *src = chunk_state_ptr(p, m, b, h, c);
+            const U *src = chunk_snap_ptr(p, m, b, h, c);
             {
                 U *const dst[2] = {sKr, sKi};
-                const float *const srcs[2] = {src, src + D * D};
+                const U *const srcs[2] = {src, src + D * D};
                 const int64_t st[2] = {D, D};
-                stage_f32_as_bf<2, 0u>(dst, srcs, st, D);
+                stage_bf<2, 0u>(dst, srcs, st, D);
             }
             __syncthreads();
             const float cum = __expf(sL[m * 64 + t]) * qs;
@@ -604,10 +614,22 @@ int launch_fwd(const FwdParams &p, hipStream_t stream) {
 
 }  // namespace
 
+bool uses_snapshots(const qpam_scan_args &a) { return a.dtype == QPAM_BF16 && a.C == 64; }
+
+// fp32 increments/states, chunk totals, then (bf16 path) the bf16 snapshots at a
+// 256-byte aligned offset.
+size_t fwd_snapshot_offset(const qpam_scan_args &a) {
+    const int64_t n = (a.T + a.C - 1) / a.C;
+    const int64_t chains = (int64_t)a.M * a.B * a.H;
+    return ((size_t)(chains * n * 2 * D * D + chains * n) * sizeof(float) + 255) & ~(size_t)255;
+}
+
 size_t fwd_workspace_bytes(const qpam_scan_args &a) {
     const int64_t n = (a.T + a.C - 1) / a.C;
     const int64_t chains = (int64_t)a.M * a.B * a.H;
-    return (size_t)(chains * n * 2 * D * D + chains * n) * sizeof(float);
+    size_t bytes = fwd_snapshot_offset(a);
+    if (uses_snapshots(a)) bytes += (size_t)chains * n * 2 * D * D * sizeof(unsigned short);
+    return bytes;
 }
 
 int validate_scan(const qpam_scan_args *a, const char *who, bool fwd_outputs) {
@@ -650,9 +672,12 @@ int scan_fwd(const qpam_scan_args *a, hipStream_t stream) {
     const int64_t chains = (int64_t)a->M * a->B * a->H;
     p.states = (float *)a->workspace;
     p.totals = p.states + chains * p.n_chunks * 2 * D * D;
+    p.snap = uses_snapshots(*a)
+                 ? reinterpret_cast<unsigned short *>((char *)a->workspace + fwd_snapshot_offset(*a))
+                 : nullptr;
     QPAM_REQUIRE(p.n_chunks <= 65535 && a->H <= 65535 && a->B <= 65535, "qpam_scan_fwd: grid too large");
     const bool bf = a->dtype == QPAM_BF16;
-    if (bf && a->C == 64) return launch_fwd_bf16(p, stream);
+    if (uses_snapshots(*a)) return launch_fwd_bf16(p, stream);
     switch (a->C) {
         case 16: return bf ? launch_fwd<unsigned short, 16>(p, stream) : launch_fwd<float, 16>(p, stream);
         case 32: return bf ? launch_fwd<unsigned short, 32>(p, stream) : launch_fwd<float, 32>(p, stream);

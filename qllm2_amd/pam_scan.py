@@ -160,14 +160,23 @@ def scan_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
     return [y_re, y_im, s_re, s_im, ws]
 
 
+def fwd_workspace_bytes(M, B, H, T, chunk, bf16, d=64):
+    """Forward workspace size, as qpam_scan_workspace_size computes it: fp32
+    per-chunk states and totals, then (bf16 inputs, chunk 64) bf16 snapshots of
+    the entering states at a 256-byte aligned offset."""
+    chains, n = M * B * H, (T + chunk - 1) // chunk
+    off = ((chains * n * 2 * d * d + chains * n) * 4 + 255) & ~255
+    return off + (chains * n * 2 * d * d * 2 if (bf16 and chunk == 64) else 0)
+
+
 @scan_fwd_op.register_fake
 def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk):
     M, B, H, T = gamma.shape
     d = q_re.shape[-1]
-    n = (T + chunk - 1) // chunk
     y = q_re.new_empty(B, H, T, d, dtype=torch.float32)
     s = q_re.new_empty(M, B, H, d, d, dtype=torch.float32)
-    ws = q_re.new_empty(M * B * H * n * (2 * d * d + 1), dtype=torch.float32)
+    nbytes = fwd_workspace_bytes(M, B, H, T, chunk, q_re.dtype == torch.bfloat16, d)
+    ws = q_re.new_empty((nbytes + 3) // 4, dtype=torch.float32)
     return [y, torch.empty_like(y), s, torch.empty_like(s), ws]
 
 
@@ -234,6 +243,9 @@ def _setup_context(ctx, inputs, output):
     (q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk) = inputs
     ctx.save_for_backward(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, output[4])
     ctx.q_scale, ctx.chunk = q_scale, chunk
+    # outputs without an incoming gradient arrive as None (the workspace output
+    # never has one): no zero-filled gradient buffers
+    ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, grads):

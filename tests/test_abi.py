@@ -78,3 +78,17 @@ def test_cpu_tensors_are_refused():
     x = torch.zeros(1, 1, 8, 64)
     with pytest.raises(ValueError, match="GPU"):
         pam_scan.pam_scan_planar(x, x, x, x, x, x, torch.ones(1, 1, 1, 8), q_scale=0.125)
+
+
+@pytest.mark.parametrize("M,B,H,T,chunk,bf16", [(3, 8, 12, 2048, 64, True), (1, 2, 3, 200, 64, False),
+                                                 (2, 1, 5, 70, 16, True), (1, 1, 1, 7, 32, False),
+                                                 (4, 3, 1, 129, 64, True)])
+def test_scan_workspace_size_matches_python_mirror(M, B, H, T, chunk, bf16):
+    """The fake (meta) kernel of qpam::scan_fwd sizes the workspace output with
+    the Python mirror of qpam_scan_workspace_size; both must agree."""
+    from qllm2_amd import pam_scan
+    a = _lib.ScanArgs()
+    a.B, a.H, a.T, a.d, a.M, a.C = B, H, T, 64, M, chunk
+    a.dtype = 1 if bf16 else 0
+    assert _lib.lib().qpam_scan_workspace_size(ctypes.byref(a)) == pam_scan.fwd_workspace_bytes(M, B, H, T, chunk,
+                                                                                                 bf16)

@@ -932,9 +932,6 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
             for (int r = 0; r < 4; ++r) {
                 const int s = 16 * st + 4 * g + r;
                 float gwr = 0.f, gwi = 0.f;
-                float colp[MAX_M];
-#pragma unroll
-                for (int m = 0; m < MAX_M; ++m) colp[m] = 0.f;
                 if (s <= t) {
                     float Dm[MAX_M], nc[MAX_M];
                     float dtr = 0.f, dti = 0.f;
@@ -959,21 +956,10 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
                     for (int m = 0; m < MAX_M; ++m) {
                         if (m < M) {
                             const float gdm = gdr * sRr[m * 64 + t] + gdi * sRi[m * 64 + t];
-                            const float gp = gdm * Dm[m] * nc[m];
-                            rowp[m] += gp;
-                            colp[m] = -gp;
+                            rowp[m] += gdm * Dm[m] * nc[m];  // the column part is summed by the key side
                             grr[m] += gdr * Dm[m];
                             gri[m] += gdi * Dm[m];
                         }
-                    }
-                }
-#pragma unroll
-                for (int m = 0; m < MAX_M; ++m) {
-                    if (m < M) {
-                        float x = colp[m];
-#pragma unroll
-                        for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off);
-                        if (l16 == 0) atomicAdd(&sGL[m * 64 + s], x);
                     }
                 }
                 wr[st][r] = gwr;
@@ -1174,29 +1160,48 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
                 di[tt] = mfma_bf(neg_bf(agr), bvi, di[tt]);
             }
         }
-        // A = (q_scale W) D~ -> (wr, wi);  q_scale gW = q_scale dA conj(D~) -> (dr, di)
+        // A = (q_scale W) D~ -> (wr, wi);  q_scale gW = q_scale dA conj(D~) -> (dr, di).
+        // Column part of the decay-matrix gradient: with gD~ = dA conj(q_scale W),
+        // dL_m[s] -= sum_t Re(gD~ conj(r_m[t])) D_m[t,s] over unclamped t > s.  This
+        // wave owns column tile st, so the sum runs over its registers and lane groups.
+        float colp[MAX_M];
+#pragma unroll
+        for (int m = 0; m < MAX_M; ++m) colp[m] = 0.f;
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
             if (tt < st) continue;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * tt + 4 * g + r;
+                const float Wr = wr[tt][r] * qs, Wi = wi[tt][r] * qs, Ar = dr[tt][r], Ai = di[tt][r];
+                const float gdr = Ar * Wr + Ai * Wi, gdi = Ai * Wr - Ar * Wi;
                 float dtr = 0.f, dti = 0.f;
                 if (s <= t) {
 #pragma unroll
                     for (int m = 0; m < MAX_M; ++m) {
                         if (m < M) {
-                            const float Dm = __expf(fminf(sL[m * 64 + t] - sL[m * 64 + s], 0.f));
-                            dtr += sRr[m * 64 + t] * Dm;
-                            dti += sRi[m * 64 + t] * Dm;
+                            const float x = sL[m * 64 + t] - sL[m * 64 + s];
+                            const float Dm = __expf(fminf(x, 0.f));
+                            const float rr = sRr[m * 64 + t], ri = sRi[m * 64 + t];
+                            dtr += rr * Dm;
+                            dti += ri * Dm;
+                            if (x <= 0.f && s != t) colp[m] += (gdr * rr + gdi * ri) * Dm;
                         }
                     }
                 }
-                const float Wr = wr[tt][r] * qs, Wi = wi[tt][r] * qs, Ar = dr[tt][r] * qs, Ai = di[tt][r] * qs;
                 wr[tt][r] = Wr * dtr - Wi * dti;
                 wi[tt][r] = Wr * dti + Wi * dtr;
-                dr[tt][r] = Ar * dtr + Ai * dti;
-                di[tt][r] = Ai * dtr - Ar * dti;
+                dr[tt][r] = (Ar * dtr + Ai * dti) * qs;
+                di[tt][r] = (Ai * dtr - Ar * dti) * qs;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MAX_M; ++m) {
+            if (m < M) {
+                float x = colp[m];
+                x += __shfl_xor(x, 16);
+                x += __shfl_xor(x, 32);
+                if (g == 0) sGL[m * 64 + s] -= x;
             }
         }
         // dV[s][i] += sum_t conj(A[t,s]) G[t,i];  dK[s][j] += sum_t conj(q_s gW[t,s]) q[t,j]

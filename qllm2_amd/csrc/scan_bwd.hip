@@ -139,6 +139,40 @@ __device__ __forceinline__ void chunk_decay_prologue(const qpam_scan_args &a, in
     }
 }
 
+// chunk_decay_prologue plus the factorised-decay tables of the bf16 kernels:
+// sF[m][t] = exp(-L_m[t]) and, when sPr is given, sPr/sPi[m][t] = r_m[t] exp(L_m[t]);
+// *sFast = 1 when every state of the chunk passes the factorisation test.
+template <int M>
+__device__ __forceinline__ void chunk_decay_prologue_f(const qpam_scan_args &a, int b, int h, int c0, int valid,
+                                                       float *sL, float *sRr, float *sRi, float *sF, float *sPr,
+                                                       float *sPi, int *sFast) {
+    const int lane = threadIdx.x & 63;
+    bool fast = true;
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
+        bool ok;
+        const float L = chunk_log_prefix_ok(gp, a.sg_t, valid, lane, ok);
+        fast = fast && ok;
+        float rr = 1.f, ri = 0.f;
+        if (a.rot_re && lane < valid) {
+            const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + lane) * a.sr_t;
+            rr = a.rot_re[ro];
+            ri = a.rot_im[ro];
+        }
+        sL[m * 64 + lane] = L;
+        sRr[m * 64 + lane] = rr;
+        sRi[m * 64 + lane] = ri;
+        sF[m * 64 + lane] = __expf(-L);  // unused (possibly inf) when the test fails
+        if (sPr) {
+            const float e = __expf(L);
+            sPr[m * 64 + lane] = rr * e;
+            sPi[m * 64 + lane] = ri * e;
+        }
+    }
+    if (lane == 0) *sFast = fast ? 1 : 0;
+}
+
 // ---------------------------------------------------------------- kernel 1 --
 // dS increment of chunk c: dG_m[i][j] = sum_t conj(rho_m[t]) G_Y[t][i] conj(Q~[t][j])
 template <typename Tin, int C>
@@ -858,21 +892,24 @@ __global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParam
     }
 }
 
+template <int M>
 __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
     U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;
     U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
     U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;    // V tile, later S_m
     U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;
-    float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
-    float *sGL = sRi + MAX_M * 64, *sDRr = sGL + MAX_M * 64, *sDRi = sDRr + MAX_M * 64;
+    // per-step vectors [M][64]
+    float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + M * 64, *sRi = sRr + M * 64;
+    float *sGL = sRi + M * 64, *sDRr = sGL + M * 64, *sDRi = sDRr + M * 64;
+    float *sF = sDRi + M * 64;
+    int *sFast = reinterpret_cast<int *>(sF + M * 64);
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int c0 = c * 64, valid = min(64, a.T - c0);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const bool carry = (c > 0) || (a.s0_re != nullptr);
-    const int M = a.M;
     const float qs = a.q_scale;
     {
         const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
@@ -888,8 +925,8 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
         const int64_t fst[2] = {p.dy.s2, p.dy.s2};
         stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
     }
-    if (w == 0) chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
-    for (int e = tid; e < 3 * MAX_M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
+    if (w == 0) chunk_decay_prologue_f<M>(a, b, h, c0, valid, sL, sRr, sRi, sF, nullptr, nullptr, sFast);
+    for (int e = tid; e < 3 * M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
     __syncthreads();
 
     const int tt = w;
@@ -925,6 +962,61 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
         float rowp[MAX_M], grr[MAX_M], gri[MAX_M];
 #pragma unroll
         for (int m = 0; m < MAX_M; ++m) rowp[m] = grr[m] = gri[m] = 0.f;
+        if (*sFast) {
+            // D_m[t,s] = E_m[t] F_m[s]: gW = dA conj(sum_m rho_m[t] F_m[s]); the row sums
+            // sum_s gD~ D_m over s < t are E_m[t] sum_s gD~ F_m[s]; D_m[t,t] = 1.
+            float Et[MAX_M], pr_t[MAX_M], pi_t[MAX_M], zr[MAX_M], zi[MAX_M];
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                Et[m] = __expf(sL[m * 64 + t]);
+                pr_t[m] = sRr[m * 64 + t] * Et[m];
+                pi_t[m] = sRi[m * 64 + t] * Et[m];
+                zr[m] = zi[m] = 0.f;
+            }
+            float dgr = 0.f, dgi = 0.f;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > tt) continue;
+                float4 F4[MAX_M];
+#pragma unroll
+                for (int m = 0; m < M; ++m) F4[m] = *reinterpret_cast<const float4 *>(sF + m * 64 + 16 * st + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int s = 16 * st + 4 * g + r;
+                    const float Ar = dr[st][r], Ai = di[st][r];
+                    const float Wr = wr[st][r] * qs, Wi = wi[st][r] * qs;
+                    const float gdr = Ar * Wr + Ai * Wi, gdi = Ai * Wr - Ar * Wi;
+                    float dtr = 0.f, dti = 0.f;
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const float f = r == 0 ? F4[m].x : r == 1 ? F4[m].y : r == 2 ? F4[m].z : F4[m].w;
+                        dtr += pr_t[m] * f;
+                        dti += pi_t[m] * f;
+                    }
+                    const bool keep = st < tt || s <= t, below = st < tt || s < t;
+                    wr[st][r] = keep ? Ar * dtr + Ai * dti : 0.f;
+                    wi[st][r] = keep ? Ai * dtr - Ar * dti : 0.f;
+                    const float gor = below ? gdr : 0.f, goi = below ? gdi : 0.f;
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const float f = r == 0 ? F4[m].x : r == 1 ? F4[m].y : r == 2 ? F4[m].z : F4[m].w;
+                        zr[m] += gor * f;
+                        zi[m] += goi * f;
+                    }
+                    if (st == tt) {
+                        dgr += s == t ? gdr : 0.f;
+                        dgi += s == t ? gdi : 0.f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float er = Et[m] * zr[m], ei = Et[m] * zi[m];
+                rowp[m] = sRr[m * 64 + t] * er + sRi[m * 64 + t] * ei;  // the column part is summed by the key side
+                grr[m] = er + dgr;
+                gri[m] = ei + dgi;
+            }
+        } else {
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             if (st > tt) continue;
@@ -965,6 +1057,7 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
                 wr[st][r] = gwr;
                 wi[st][r] = gwi;
             }
+        }
         }
 #pragma unroll
         for (int m = 0; m < MAX_M; ++m) {
@@ -1087,22 +1180,25 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     }
 }
 
+template <int M>
 __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
     U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;   // q, later G'_m
     U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
     U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
     U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;                    // dY
-    float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
-    float *sGL = sRi + MAX_M * 64, *sDl = sGL + MAX_M * 64;
-    float *sRed = sDl + MAX_M * 64;
+    // per-step vectors [M][64]
+    float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + M * 64, *sRi = sRr + M * 64;
+    float *sGL = sRi + M * 64, *sDl = sGL + M * 64;
+    float *sF = sDl + M * 64, *sPr = sF + M * 64, *sPi = sPr + M * 64;
+    float *sRed = sPi + M * 64;
+    int *sFast = reinterpret_cast<int *>(sRed + 4);
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int c0 = c * 64, valid = min(64, a.T - c0);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const bool carry = (c > 0) || (a.s0_re != nullptr);
-    const int M = a.M;
     const float qs = a.q_scale;
     {
         const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
@@ -1119,7 +1215,7 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
         stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
     }
     if (w == 0) {
-        chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
+        chunk_decay_prologue_f<M>(a, b, h, c0, valid, sL, sRr, sRi, sF, sPr, sPi, sFast);
         for (int m = 0; m < M; ++m) {
             const float L = sL[m * 64 + lane];
             const float Llast = sL[m * 64 + valid - 1];
@@ -1167,6 +1263,48 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
         float colp[MAX_M];
 #pragma unroll
         for (int m = 0; m < MAX_M; ++m) colp[m] = 0.f;
+        if (*sFast) {
+            // D_m[t,s] = E_m[t] F_m[s]: D~ = sum_m (r_m E_m)[t] F_m[s], and the column sums
+            // are F_m[s] sum_t Re(gD~ conj(r_m E_m)[t]) over t > s.
+            float Fs[MAX_M];
+#pragma unroll
+            for (int m = 0; m < M; ++m) Fs[m] = sF[m * 64 + s];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                if (tt < st) continue;
+                float4 P4r[MAX_M], P4i[MAX_M];
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    P4r[m] = *reinterpret_cast<const float4 *>(sPr + m * 64 + 16 * tt + 4 * g);
+                    P4i[m] = *reinterpret_cast<const float4 *>(sPi + m * 64 + 16 * tt + 4 * g);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * tt + 4 * g + r;
+                    const float Wr = wr[tt][r] * qs, Wi = wi[tt][r] * qs, Ar = dr[tt][r], Ai = di[tt][r];
+                    const float gdr = Ar * Wr + Ai * Wi, gdi = Ai * Wr - Ar * Wi;
+                    const bool keep = tt > st || s <= t, below = tt > st || s < t;
+                    const float gor = below ? gdr : 0.f, goi = below ? gdi : 0.f;
+                    float dtr = 0.f, dti = 0.f;
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const float pr = r == 0 ? P4r[m].x : r == 1 ? P4r[m].y : r == 2 ? P4r[m].z : P4r[m].w;
+                        const float pi = r == 0 ? P4i[m].x : r == 1 ? P4i[m].y : r == 2 ? P4i[m].z : P4i[m].w;
+                        dtr += pr * Fs[m];
+                        dti += pi * Fs[m];
+                        colp[m] += gor * pr + goi * pi;
+                    }
+                    dtr = keep ? dtr : 0.f;
+                    dti = keep ? dti : 0.f;
+                    wr[tt][r] = Wr * dtr - Wi * dti;
+                    wi[tt][r] = Wr * dti + Wi * dtr;
+                    dr[tt][r] = (Ar * dtr + Ai * dti) * qs;
+                    di[tt][r] = (Ai * dtr - Ar * dti) * qs;
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) colp[m] *= Fs[m];
+        } else {
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt) {
             if (tt < st) continue;
@@ -1194,6 +1332,7 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
                 dr[tt][r] = (Ar * dtr + Ai * dti) * qs;
                 di[tt][r] = (Ai * dtr - Ar * dti) * qs;
             }
+        }
         }
 #pragma unroll
         for (int m = 0; m < MAX_M; ++m) {
@@ -1359,19 +1498,22 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
 
 constexpr size_t gcs_bf16_smem() { return (size_t)4 * PLANE_B * 2 + 5 * MAX_M * 64 * sizeof(float); }
 // query/key side: 8 bf16 planes + per-step vectors < 80 KiB, so two blocks share a CU's 160 KiB LDS
-constexpr size_t qside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + 6 * MAX_M * 64 * sizeof(float); }
-constexpr size_t kside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (5 * MAX_M * 64 + 4) * sizeof(float); }
-static_assert(2 * qside_bf16_smem() <= 160 * 1024 && 2 * kside_bf16_smem() <= 160 * 1024, "LDS budget");
+template <int M>
+constexpr size_t qside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (7 * M * 64 + 4) * sizeof(float); }
+template <int M>
+constexpr size_t kside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (8 * M * 64 + 8) * sizeof(float); }
+static_assert(2 * qside_bf16_smem<3>() <= 160 * 1024 && 2 * kside_bf16_smem<3>() <= 160 * 1024, "LDS budget");
 
-int launch_bwd_bf16(const BwdParams &p, hipStream_t stream) {
+template <int M>
+int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;
     dim3 grid(p.n_chunks, a.H, a.B);
-    const size_t s1 = gcs_bf16_smem(), s3 = qside_bf16_smem(), s4 = kside_bf16_smem();
+    const size_t s1 = gcs_bf16_smem(), s3 = qside_bf16_smem<M>(), s4 = kside_bf16_smem<M>();
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_chunk_state_bf16_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)query_side_bf16_kernel,
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)query_side_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_bf16_kernel,
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
     hipLaunchKernelGGL(grad_chunk_state_bf16_kernel, grid, dim3(THREADS), s1, stream, p);
     int st = launch_status("grad_chunk_state_bf16_kernel");
@@ -1379,11 +1521,21 @@ int launch_bwd_bf16(const BwdParams &p, hipStream_t stream) {
     hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * 8), dim3(THREADS), 0, stream, p);
     st = launch_status("grad_state_scan_kernel");
     if (st) return st;
-    hipLaunchKernelGGL(query_side_bf16_kernel, grid, dim3(THREADS), s3, stream, p);
+    hipLaunchKernelGGL(query_side_bf16_kernel<M>, grid, dim3(THREADS), s3, stream, p);
     st = launch_status("query_side_bf16_kernel");
     if (st) return st;
-    hipLaunchKernelGGL(key_side_bf16_kernel, grid, dim3(THREADS), s4, stream, p);
+    hipLaunchKernelGGL(key_side_bf16_kernel<M>, grid, dim3(THREADS), s4, stream, p);
     return launch_status("key_side_bf16_kernel");
+}
+
+// The state count is a compile-time constant of the query/key-side kernels.
+int launch_bwd_bf16(const BwdParams &p, hipStream_t stream) {
+    switch (p.a.M) {
+        case 1: return launch_bwd_bf16_m<1>(p, stream);
+        case 2: return launch_bwd_bf16_m<2>(p, stream);
+        case 3: return launch_bwd_bf16_m<3>(p, stream);
+        default: return launch_bwd_bf16_m<4>(p, stream);
+    }
 }
 
 template <int C>

@@ -115,6 +115,26 @@ __device__ __forceinline__ float chunk_log_prefix(const float *g, int64_t gs, in
     return x;
 }
 
+// Factorised decay.  When every log(gamma + 1e-6) of a chunk is <= 0, the fp32
+// prefix sums L are non-increasing (rounding is monotone), so for s <= t
+// min(L_t - L_s, 0) = L_t - L_s and no entry is clamped; if also
+// L_last >= -FACTOR_RANGE, exp(L_t) and exp(-L_s) are finite and
+// D[t,s] = exp(L_t) exp(-L_s) needs no per-element exponential.
+constexpr float FACTOR_RANGE = 80.f;
+
+// chunk_log_prefix plus that test for one state (wave-uniform result).
+__device__ __forceinline__ float chunk_log_prefix_ok(const float *g, int64_t gs, int valid, int lane, bool &ok) {
+    float x = (lane < valid) ? logf(g[(int64_t)lane * gs] + LOG_EPS) : 0.f;
+    const bool pos = x > 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        float y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+    }
+    ok = !__any(pos) && __shfl(x, 63) >= -FACTOR_RANGE;
+    return x;
+}
+
 // ------------------------------------------------------------------------
 // bf16 MFMA helpers (v_mfma_f32_16x16x32_bf16).  Operand fragment: lane l
 // supplies 8 bf16 for row/col l % 16 and k-group g = l / 16.  Both operands of

@@ -403,21 +403,23 @@ __global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) 
     }
 }
 
+template <int M>
 __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p) {
     extern __shared__ float smem[];
     using U = unsigned short;
     U *sQr = reinterpret_cast<U *>(smem), *sQi = sQr + PLANE_B;
     U *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;  // K tile, later the carried state S_m
     U *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
-    float *sL = reinterpret_cast<float *>(sVi + PLANE_B);
-    float *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+    float *sL = reinterpret_cast<float *>(sVi + PLANE_B);  // per-step vectors [M][64]
+    float *sRr = sL + M * 64, *sRi = sRr + M * 64, *sF = sRi + M * 64;
+    int *sFast = reinterpret_cast<int *>(sF + M * 64);
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int c0 = c * 64;
     const int valid = min(64, a.T - c0);
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const bool general = (a.M > 1) || (a.rot_re != nullptr);
+    const bool general = (M > 1) || (a.rot_re != nullptr);
     const bool carry = (c > 0) || (a.s0_re != nullptr);
     const float qs = a.q_scale;
 
@@ -432,18 +434,25 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
         stage_bf<6, 0x0u>(dst, src, st, valid);
     }
     if (w == 0) {
-        for (int m = 0; m < a.M; ++m) {
+        bool fast = true;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
             const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
-            sL[m * 64 + lane] = chunk_log_prefix(gp, a.sg_t, valid, lane);
+            bool ok;
+            const float L = chunk_log_prefix_ok(gp, a.sg_t, valid, lane, ok);
+            fast = fast && ok;
             float rr = 1.f, ri = 0.f;
             if (a.rot_re && lane < valid) {
                 const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + lane) * a.sr_t;
                 rr = a.rot_re[ro];
                 ri = a.rot_im[ro];
             }
+            sL[m * 64 + lane] = L;
             sRr[m * 64 + lane] = rr;
             sRi[m * 64 + lane] = ri;
+            sF[m * 64 + lane] = __expf(-L);  // unused (possibly inf) when the test fails
         }
+        if (lane == 0) *sFast = fast ? 1 : 0;
     }
     __syncthreads();
 
@@ -471,6 +480,40 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
             }
         }
         // A = (q_scale W) . D~ ; lane holds s = 16st + 4g + r, t = 16tt + l16
+        if (*sFast) {
+            // D_m[t,s] = E_m[t] F_m[s]: D~ = sum_m (r_m E_m)[t] F_m[s]
+            float pr_t[MAX_M], pi_t[MAX_M];
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const float e = __expf(sL[m * 64 + t]) * qs;
+                pr_t[m] = sRr[m * 64 + t] * e;
+                pi_t[m] = sRi[m * 64 + t] * e;
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > tt) continue;
+                float4 F4[MAX_M];
+#pragma unroll
+                for (int m = 0; m < M; ++m) F4[m] = *reinterpret_cast<const float4 *>(sF + m * 64 + 16 * st + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int s = 16 * st + 4 * g + r;
+                    float dre = 0.f, dim = 0.f;
+#pragma unroll
+                    for (int m = 0; m < M; ++m) {
+                        const float f = r == 0 ? F4[m].x : r == 1 ? F4[m].y : r == 2 ? F4[m].z : F4[m].w;
+                        dre += pr_t[m] * f;
+                        dim += pi_t[m] * f;
+                    }
+                    const bool keep = st < tt || s <= t;
+                    dre = keep ? dre : 0.f;
+                    dim = keep ? dim : 0.f;
+                    const float xr = wr[st][r], xi = wi[st][r];
+                    wr[st][r] = xr * dre - xi * dim;
+                    wi[st][r] = xr * dim + xi * dre;
+                }
+            }
+        } else {
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             if (st > tt) continue;
@@ -482,7 +525,8 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
                     if (!general) {
                         dre = __expf(fminf(sL[t] - sL[s], 0.f));
                     } else {
-                        for (int m = 0; m < a.M; ++m) {
+#pragma unroll
+                        for (int m = 0; m < M; ++m) {
                             const float dm = __expf(fminf(sL[m * 64 + t] - sL[m * 64 + s], 0.f));
                             dre += sRr[m * 64 + t] * dm;
                             dim += sRi[m * 64 + t] * dm;
@@ -493,6 +537,7 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
                 wr[st][r] = xr * dre - xi * dim;
                 wi[st][r] = xr * dim + xi * dre;
             }
+        }
         }
         // Y += A V: k-step kp covers s-tiles 2kp, 2kp+1 (registers); transposed reads of V give the
         // matching k order
@@ -516,7 +561,7 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
 
     // carried read  Y += sum_m (rho_m q_scale q) S_in,m^T
     if (carry) {
-        for (int m = 0; m < a.M; ++m) {
+        for (int m = 0; m < M; ++m) {
             __syncthreads();
             const U *src = chunk_snap_ptr(p, m, b, h, c);
             {
@@ -560,15 +605,17 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
 }
 
 constexpr size_t state_bf16_smem() { return (size_t)4 * PLANE_B * 2 + MAX_M * 64 * sizeof(float); }
-constexpr size_t output_bf16_smem() { return (size_t)6 * PLANE_B * 2 + 3 * MAX_M * 64 * sizeof(float); }
+template <int M>
+constexpr size_t output_bf16_smem() { return (size_t)6 * PLANE_B * 2 + (4 * M * 64 + 4) * sizeof(float); }
 
-int launch_fwd_bf16(const FwdParams &p, hipStream_t stream) {
+template <int M>
+int launch_fwd_bf16_m(const FwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;
     dim3 grid(p.n_chunks, a.H, a.B);
-    const size_t s1 = state_bf16_smem(), s3 = output_bf16_smem();
+    const size_t s1 = state_bf16_smem(), s3 = output_bf16_smem<M>();
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_state_bf16_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_bf16_kernel,
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
     hipLaunchKernelGGL(chunk_state_bf16_kernel, grid, dim3(THREADS), s1, stream, p);
     int st = launch_status("chunk_state_bf16_kernel");
@@ -577,11 +624,21 @@ int launch_fwd_bf16(const FwdParams &p, hipStream_t stream) {
     st = launch_status("state_scan_kernel");
     if (st) return st;
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));
-    hipLaunchKernelGGL(chunk_output_bf16_kernel, grid, dim3(THREADS), s3, stream, p);
+    hipLaunchKernelGGL(chunk_output_bf16_kernel<M>, grid, dim3(THREADS), s3, stream, p);
     st = launch_status("chunk_output_bf16_kernel");
     if (st) return st;
     if (a.prof_ev[1]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[1], stream));
     return QPAM_OK;
+}
+
+// The state count is a compile-time constant of the output kernel.
+int launch_fwd_bf16(const FwdParams &p, hipStream_t stream) {
+    switch (p.a.M) {
+        case 1: return launch_fwd_bf16_m<1>(p, stream);
+        case 2: return launch_fwd_bf16_m<2>(p, stream);
+        case 3: return launch_fwd_bf16_m<3>(p, stream);
+        default: return launch_fwd_bf16_m<4>(p, stream);
+    }
 }
 
 template <int C>

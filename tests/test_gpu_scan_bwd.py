@@ -123,3 +123,40 @@ def test_scan_backward_config3_full_size(gpu_lib):
     for name, a, b in zip(NAMES[:4], got[:4], ref):
         assert _rel(a, b) < 2e-2, f"{name}: rel {_rel(a, b):.2e}"
         assert math.isfinite(a.abs().sum().item())
+
+
+def test_scan_bf16_e3_decay_regimes(gpu_lib):
+    """One E3 call whose chunks take both decay paths of the bf16 kernels: chunks
+    where every log(gamma + 1e-6) <= 0 with a moderate range (factorised decay)
+    and chunks that need the per-element exact form -- gamma = 1 (the clamp of
+    min(L_t - L_s, 0) is active) and gamma = 0.05 (cumulative decay beyond the
+    factorisation range).  Forward Y, S and every gradient against the oracle."""
+    from qllm2_amd.pam_scan import pam_scan_planar
+    M, B, H, T, d, C = 3, 1, 2, 320, 64, 64
+    case = list(_case(M, B, H, T, d, 3404, True, True, torch.bfloat16))
+    gamma = case[3].clone()
+    gamma[:, :, :, 64:128] = 1.0       # chunk 1: clamp regime in every state
+    gamma[:, :, 1, 128:192] = 0.05     # chunk 2, head 1: exp(-L) would overflow
+    gamma[0, :, 0, 192:256] = 1.0      # chunk 3, head 0: one state clamps, the others factorise
+    case[3] = gamma
+    ref = _oracle_grads(*case, d, C)
+    got = _gpu_grads(*case, d, C, torch.bfloat16, True)
+    for name, a, b in zip(NAMES, got, ref):
+        if a is None or b is None:
+            continue
+        assert math.isfinite(a.abs().sum().item()), name
+        assert _rel(a, b) < 2e-2, f"{name}: rel {_rel(a, b):.2e}"
+    q, k, v, gamma, dy, ds, phase, routing, s0 = case
+    y_ref, s_ref = O.multistate_fused(q.double(), k.double(), v.double(), gamma.double(), phase.double(),
+                                      routing.double(), d, C, state=s0.double())
+    dev = torch.device("cuda")
+    planes = [x[..., i].contiguous().to(torch.bfloat16).to(dev) for x in (q, k, v) for i in (0, 1)]
+    rot = ((routing * torch.cos(phase)).to(dev), (routing * torch.sin(phase)).to(dev))
+    s0p = (s0[..., 0].contiguous().to(dev), s0[..., 1].contiguous().to(dev))
+    with torch.no_grad():
+        y_re, y_im, s_re, s_im = pam_scan_planar(*planes, gamma.float().to(dev), q_scale=d ** -0.5, chunk=C,
+                                                 rot=rot, s0=s0p)
+    y = torch.stack([y_re, y_im], -1).cpu()
+    s = torch.stack([s_re, s_im], -1).cpu()
+    assert _rel(y, y_ref) < 2e-2, f"y: rel {_rel(y, y_ref):.2e}"
+    assert _rel(s, s_ref) < 2e-2, f"s: rel {_rel(s, s_ref):.2e}"

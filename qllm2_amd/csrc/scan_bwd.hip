@@ -243,34 +243,54 @@ __global__ void __launch_bounds__(THREADS) grad_chunk_state_kernel(BwdParams p) 
 
 // ---------------------------------------------------------------- kernel 2 --
 // Reverse scan: G = dS_final; for c = n-1..0: slot[c] <- G (dS after chunk c),
-// G = total_c G + increment_c.  At the end G = dS0.
+// G = total_c G + increment_c.  At the end G = dS0.  Thread layout and the
+// two-chunk prefetch as in the forward state scan.
 __global__ void __launch_bounds__(THREADS) grad_state_scan_kernel(BwdParams p) {
     const qpam_scan_args &a = p.a;
-    const int chain = blockIdx.x >> 3;
-    const int e4 = ((blockIdx.x & 7) << 8) + threadIdx.x;
+    const int chain = blockIdx.x / SCAN_BLOCKS;
     const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
-    const int plane = e4 >> 10, off = (e4 & 1023) * 4;
-    const int64_t so = (int64_t)chain * D * D + off;
-
-    float4 G = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (p.ds_re) G = *reinterpret_cast<const float4 *>((plane ? p.ds_im : p.ds_re) + so);
-    float *base = gstate(p, m, b, h, 0) + plane * D * D + off;
-    unsigned short *sbase = p.gsnap ? gsnap(p, m, b, h, 0) + plane * D * D + off : nullptr;
+    const int64_t cs = 2 * D * D;  // floats per chunk state
+    float *base = gstate(p, m, b, h, 0);
+    unsigned short *sbase = p.gsnap ? gsnap(p, m, b, h, 0) : nullptr;
     const int n = p.n_chunks;
-    float4 nxt = *reinterpret_cast<const float4 *>(base + (int64_t)(n - 1) * 2 * D * D);
-    for (int c = n - 1; c >= 0; --c) {
-        const float4 inc = nxt;
-        if (c > 0) nxt = *reinterpret_cast<const float4 *>(base + (int64_t)(c - 1) * 2 * D * D);
-        if (sbase) *reinterpret_cast<ushortx4 *>(sbase + (int64_t)c * 2 * D * D) = to_bf16x4(G);
-        else *reinterpret_cast<float4 *>(base + (int64_t)c * 2 * D * D) = G;
-        const float t = ftotal(p, m, b, h, c);
-        G.x = t * G.x + inc.x;
-        G.y = t * G.y + inc.y;
-        G.z = t * G.z + inc.z;
-        G.w = t * G.w + inc.w;
+
+    int off[SCAN_EPT];
+    float4 G[SCAN_EPT], b0[SCAN_EPT], b1[SCAN_EPT];
+#pragma unroll
+    for (int e = 0; e < SCAN_EPT; ++e) {
+        off[e] = 4 * ((blockIdx.x % SCAN_BLOCKS) * THREADS * SCAN_EPT + e * THREADS + threadIdx.x);
+        const int plane = off[e] >= D * D;
+        G[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (p.ds_re)
+            G[e] = *reinterpret_cast<const float4 *>((plane ? p.ds_im : p.ds_re) + (int64_t)chain * D * D +
+                                                     off[e] - plane * D * D);
+        b0[e] = *reinterpret_cast<const float4 *>(base + (n - 1) * cs + off[e]);
+        if (n > 1) b1[e] = *reinterpret_cast<const float4 *>(base + (n - 2) * cs + off[e]);
     }
-    if (p.ds0_re) *reinterpret_cast<float4 *>((plane ? p.ds0_im : p.ds0_re) + so) = G;
+    for (int c = n - 1; c >= 0; --c) {
+        const float t = ftotal(p, m, b, h, c);
+#pragma unroll
+        for (int e = 0; e < SCAN_EPT; ++e) {
+            const float4 inc = b0[e];
+            b0[e] = b1[e];
+            if (c >= 2) b1[e] = *reinterpret_cast<const float4 *>(base + (c - 2) * cs + off[e]);
+            if (sbase) *reinterpret_cast<ushortx4 *>(sbase + c * cs + off[e]) = to_bf16x4(G[e]);
+            else *reinterpret_cast<float4 *>(base + c * cs + off[e]) = G[e];
+            G[e].x = t * G[e].x + inc.x;
+            G[e].y = t * G[e].y + inc.y;
+            G[e].z = t * G[e].z + inc.z;
+            G[e].w = t * G[e].w + inc.w;
+        }
+    }
+    if (p.ds0_re) {
+#pragma unroll
+        for (int e = 0; e < SCAN_EPT; ++e) {
+            const int plane = off[e] >= D * D;
+            *reinterpret_cast<float4 *>((plane ? p.ds0_im : p.ds0_re) + (int64_t)chain * D * D + off[e] -
+                                        plane * D * D) = G[e];
+        }
+    }
 }
 
 // ---------------------------------------------------------------- kernel 3 --
@@ -1518,7 +1538,7 @@ int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
     hipLaunchKernelGGL(grad_chunk_state_bf16_kernel, grid, dim3(THREADS), s1, stream, p);
     int st = launch_status("grad_chunk_state_bf16_kernel");
     if (st) return st;
-    hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * 8), dim3(THREADS), 0, stream, p);
+    hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, stream, p);
     st = launch_status("grad_state_scan_kernel");
     if (st) return st;
     hipLaunchKernelGGL(query_side_bf16_kernel<M>, grid, dim3(THREADS), s3, stream, p);
@@ -1559,7 +1579,7 @@ int launch_bwd(const BwdParams &p, hipStream_t stream) {
     hipLaunchKernelGGL((grad_chunk_state_kernel<Tin, C>), grid, dim3(THREADS), s1, stream, p);
     int st = launch_status("grad_chunk_state_kernel");
     if (st) return st;
-    hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * 8), dim3(THREADS), 0, stream, p);
+    hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, stream, p);
     st = launch_status("grad_state_scan_kernel");
     if (st) return st;
     hipLaunchKernelGGL((query_side_kernel<Tin, C>), grid, dim3(THREADS), s3, stream, p);

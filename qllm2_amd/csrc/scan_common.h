@@ -115,6 +115,11 @@ __device__ __forceinline__ float chunk_log_prefix(const float *g, int64_t gs, in
     return x;
 }
 
+// Sequential state scans: float4 per thread and blocks per (m, b, h) state.
+constexpr int SCAN_EPT = 2;
+constexpr int SCAN_BLOCKS = (2 * 64 * 64 / 4) / (THREADS * SCAN_EPT);
+static_assert(SCAN_BLOCKS * THREADS * SCAN_EPT * 4 == 2 * 64 * 64, "scan tiling");
+
 // Factorised decay.  When every log(gamma + 1e-6) of a chunk is <= 0, the fp32
 // prefix sums L are non-increasing (rounding is monotone), so for s <= t
 // min(L_t - L_s, 0) = L_t - L_s and no entry is clamped; if also

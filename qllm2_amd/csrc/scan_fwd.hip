@@ -114,39 +114,58 @@ __global__ void __launch_bounds__(THREADS) chunk_state_kernel(FwdParams p) {
 }
 
 // ---------------------------------------------------------------- kernel 2 --
-// One thread per 4 consecutive state floats of one (m, b, h); 2048 float4 per
-// state (re plane then im plane), 8 blocks per state.  The running state stays
-// fp32; the entering state of every chunk goes either back over the increment
-// (fp32 path) or, rounded once, into the bf16 snapshot (bf16 path).
+// Each thread owns SCAN_EPT float4 of one (m, b, h) state (2048 float4: re
+// plane then im plane), SCAN_BLOCKS blocks per state, and keeps the increments
+// of the next two chunks in flight.  The running state stays fp32; the entering
+// state of every chunk goes either back over the increment (fp32 path) or,
+// rounded once, into the bf16 snapshot (bf16 path).
 __global__ void __launch_bounds__(THREADS) state_scan_kernel(FwdParams p) {
     const qpam_scan_args &a = p.a;
-    const int chain = blockIdx.x >> 3;
-    const int e4 = ((blockIdx.x & 7) << 8) + threadIdx.x;  // 0..2047
+    const int chain = blockIdx.x / SCAN_BLOCKS;
     const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
-    const int plane = e4 >> 10, off = (e4 & 1023) * 4;
-
-    float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
-    const int64_t so = (int64_t)chain * D * D + off;
-    if (a.s0_re) S = *reinterpret_cast<const float4 *>((plane ? a.s0_im : a.s0_re) + so);
-
-    float *base = chunk_state_ptr(p, m, b, h, 0) + plane * D * D + off;
-    unsigned short *sbase = p.snap ? chunk_snap_ptr(p, m, b, h, 0) + plane * D * D + off : nullptr;
+    const int64_t cs = 2 * D * D;  // floats per chunk state
+    float *base = chunk_state_ptr(p, m, b, h, 0);
+    unsigned short *sbase = p.snap ? chunk_snap_ptr(p, m, b, h, 0) : nullptr;
     const float *tot = chunk_total_ptr(p, m, b, h, 0);
     const int n = p.n_chunks;
-    float4 nxt = *reinterpret_cast<const float4 *>(base);
-    for (int c = 0; c < n; ++c) {
-        const float4 ds = nxt;
-        if (c + 1 < n) nxt = *reinterpret_cast<const float4 *>(base + (int64_t)(c + 1) * 2 * D * D);
-        if (sbase) *reinterpret_cast<ushortx4 *>(sbase + (int64_t)c * 2 * D * D) = to_bf16x4(S);
-        else *reinterpret_cast<float4 *>(base + (int64_t)c * 2 * D * D) = S;
-        const float t = tot[c];
-        S.x = t * S.x + ds.x;
-        S.y = t * S.y + ds.y;
-        S.z = t * S.z + ds.z;
-        S.w = t * S.w + ds.w;
+
+    int off[SCAN_EPT];  // float offset inside the [2][64][64] state
+    float4 S[SCAN_EPT], b0[SCAN_EPT], b1[SCAN_EPT];
+#pragma unroll
+    for (int e = 0; e < SCAN_EPT; ++e) {
+        off[e] = 4 * ((blockIdx.x % SCAN_BLOCKS) * THREADS * SCAN_EPT + e * THREADS + threadIdx.x);
+        const int plane = off[e] >= D * D;
+        S[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (a.s0_re)
+            S[e] = *reinterpret_cast<const float4 *>((plane ? a.s0_im : a.s0_re) + (int64_t)chain * D * D +
+                                                     off[e] - plane * D * D);
+        b0[e] = *reinterpret_cast<const float4 *>(base + off[e]);
+        if (n > 1) b1[e] = *reinterpret_cast<const float4 *>(base + cs + off[e]);
     }
-    if (a.s_re) *reinterpret_cast<float4 *>((plane ? a.s_im : a.s_re) + so) = S;
+    for (int c = 0; c < n; ++c) {
+        const float t = tot[c];
+#pragma unroll
+        for (int e = 0; e < SCAN_EPT; ++e) {
+            const float4 ds = b0[e];
+            b0[e] = b1[e];
+            if (c + 2 < n) b1[e] = *reinterpret_cast<const float4 *>(base + (c + 2) * cs + off[e]);
+            if (sbase) *reinterpret_cast<ushortx4 *>(sbase + c * cs + off[e]) = to_bf16x4(S[e]);
+            else *reinterpret_cast<float4 *>(base + c * cs + off[e]) = S[e];
+            S[e].x = t * S[e].x + ds.x;
+            S[e].y = t * S[e].y + ds.y;
+            S[e].z = t * S[e].z + ds.z;
+            S[e].w = t * S[e].w + ds.w;
+        }
+    }
+    if (a.s_re) {
+#pragma unroll
+        for (int e = 0; e < SCAN_EPT; ++e) {
+            const int plane = off[e] >= D * D;
+            *reinterpret_cast<float4 *>((plane ? a.s_im : a.s_re) + (int64_t)chain * D * D + off[e] - plane * D * D) =
+                S[e];
+        }
+    }
 }
 
 // ---------------------------------------------------------------- kernel 3 --
@@ -620,7 +639,7 @@ int launch_fwd_bf16_m(const FwdParams &p, hipStream_t stream) {
     hipLaunchKernelGGL(chunk_state_bf16_kernel, grid, dim3(THREADS), s1, stream, p);
     int st = launch_status("chunk_state_bf16_kernel");
     if (st) return st;
-    hipLaunchKernelGGL(state_scan_kernel, dim3(a.M * a.B * a.H * 8), dim3(THREADS), 0, stream, p);
+    hipLaunchKernelGGL(state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, stream, p);
     st = launch_status("state_scan_kernel");
     if (st) return st;
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));
@@ -658,7 +677,7 @@ int launch_fwd(const FwdParams &p, hipStream_t stream) {
     hipLaunchKernelGGL((chunk_state_kernel<Tin, C>), grid, dim3(THREADS), s1, stream, p);
     int st = launch_status("chunk_state_kernel");
     if (st) return st;
-    hipLaunchKernelGGL(state_scan_kernel, dim3(a.M * a.B * a.H * 8), dim3(THREADS), 0, stream, p);
+    hipLaunchKernelGGL(state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, stream, p);
     st = launch_status("state_scan_kernel");
     if (st) return st;
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));

@@ -1,0 +1,100 @@
+// Plain bf16 GEMMs through hipBLASLt (the two weight/hidden-gradient products
+// of the LM-head backward, which carry no fused epilogue).  One handle per
+// device and one cached plan (descriptors + heuristic algorithm) per shape.
+#include <hipblaslt/hipblaslt.h>
+
+#include <cstdlib>
+#include <map>
+#include <mutex>
+#include <tuple>
+
+#include "blas.h"
+#include "common.h"
+
+namespace qpam {
+namespace blas {
+namespace {
+
+struct Plan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, lc = nullptr;
+    hipblasLtMatmulAlgo_t algo;
+    size_t ws = 0;
+};
+
+using Key = std::tuple<int, int, int, int, int, int, int64_t, int64_t, int64_t, int, int, size_t>;
+
+std::mutex g_mu;
+std::map<int, hipblasLtHandle_t> g_handles;
+std::map<Key, Plan> g_plans;
+
+#define QPAM_CHECK_LT(expr)                                                                   \
+    do {                                                                                      \
+        hipblasStatus_t s_ = (expr);                                                          \
+        if (s_ != HIPBLAS_STATUS_SUCCESS) return fail(QPAM_ERR_HIP, "%s: hipBLASLt status %d", #expr, (int)s_); \
+    } while (0)
+
+int get_handle(int dev, hipblasLtHandle_t &h) {
+    auto it = g_handles.find(dev);
+    if (it != g_handles.end()) {
+        h = it->second;
+        return QPAM_OK;
+    }
+    QPAM_CHECK_LT(hipblasLtCreate(&h));
+    g_handles[dev] = h;
+    return QPAM_OK;
+}
+
+}  // namespace
+
+bool enabled() {
+    const char *e = std::getenv("QPAM_CE_GEMM");
+    return !(e && e[0] == 'h' && e[1] == 'i' && e[2] == 'p');  // QPAM_CE_GEMM=hip: hand-written kernels
+}
+
+int gemm_bf16(bool ta, bool tb, int m, int n, int k, const void *A, int64_t lda, const void *B, int64_t ldb,
+              float beta, void *C, int64_t ldc, bool c_f32, void *ws, size_t ws_bytes, hipStream_t stream) {
+    int dev = 0;
+    QPAM_CHECK_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_mu);
+    hipblasLtHandle_t h;
+    int st = get_handle(dev, h);
+    if (st) return st;
+    const Key key{dev, ta, tb, m, n, k, lda, ldb, ldc, c_f32, beta != 0.f, ws_bytes};
+    auto it = g_plans.find(key);
+    if (it == g_plans.end()) {
+        Plan p;
+        const hipDataType ct = c_f32 ? HIP_R_32F : HIP_R_16BF;
+        QPAM_CHECK_LT(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
+        const hipblasOperation_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+        QPAM_CHECK_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa)));
+        QPAM_CHECK_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb)));
+        // column-major layouts: op(A) is m x k, op(B) is k x n, C is m x n
+        QPAM_CHECK_LT(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, ta ? k : m, ta ? m : k, lda));
+        QPAM_CHECK_LT(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, tb ? n : k, tb ? k : n, ldb));
+        QPAM_CHECK_LT(hipblasLtMatrixLayoutCreate(&p.lc, ct, m, n, ldc));
+        hipblasLtMatmulPreference_t pref;
+        QPAM_CHECK_LT(hipblasLtMatmulPreferenceCreate(&pref));
+        const uint64_t wsb = ws_bytes;
+        QPAM_CHECK_LT(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
+                                                            sizeof(wsb)));
+        hipblasLtMatmulHeuristicResult_t res[1];
+        int count = 0;
+        const hipblasStatus_t hs =
+            hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, res, &count);
+        hipblasLtMatmulPreferenceDestroy(pref);
+        if (hs != HIPBLAS_STATUS_SUCCESS || count < 1)
+            return fail(QPAM_ERR_UNSUPPORTED, "hipBLASLt: no algorithm for %dx%dx%d (status %d)", m, n, k, (int)hs);
+        p.algo = res[0].algo;
+        p.ws = res[0].workspaceSize;
+        it = g_plans.emplace(key, p).first;
+    }
+    const Plan &p = it->second;
+    const float alpha = 1.f;
+    QPAM_CHECK_LT(hipblasLtMatmul(h, p.desc, &alpha, A, p.la, B, p.lb, &beta, C, p.lc, C, p.lc, &p.algo, ws,
+                                  ws_bytes, stream));
+    return QPAM_OK;
+}
+
+}  // namespace blas
+}  // namespace qpam

@@ -18,6 +18,7 @@
 // memory bound (it keeps chunk x V fp32 logits and softmax alive).
 #include <algorithm>
 
+#include "blas.h"
 #include "common.h"
 
 namespace qpam {
@@ -297,6 +298,7 @@ struct BwdParams {
     void *gbuf;      // [rows][Vp]
     void *gtbuf;     // [Vp][Rp]
     void *ht;        // [D][Rp]
+    int write_g;     // bf16 path: also write G (only the hand-written dH GEMM reads it)
 };
 
 // out[c][r] = in[r][c] for an R x Cc tile grid (64 x 64 LDS tiles); rows >= R
@@ -668,7 +670,7 @@ __global__ void __launch_bounds__(THREADS, 2) grad_tile_kernel(BwdParams p) {
                     x *= sScale[rl];
                 }
                 gv[r] = f32_to_bf16(x);
-                if (lr0 + rl < p.rows) G[(int64_t)(lr0 + rl) * p.Vp + v] = gv[r];
+                if (p.write_g && lr0 + rl < p.rows) G[(int64_t)(lr0 + rl) * p.Vp + v] = gv[r];
             }
             *reinterpret_cast<ushortx4 *>(GT + (int64_t)v * p.Rp + lr0 + rl0) = gv;
         }
@@ -776,7 +778,8 @@ size_t bwd_ws(const qpam_ce_bwd_args &a) {
     const int64_t Rp = round_up((int)chunk, row_tile<T>());
     const int64_t elems = (int64_t)a.D * Vp + chunk * Vp + Vp * Rp + (int64_t)a.D * Rp;
     size_t bytes = (size_t)(elems * sizeof(T)) + 4 * 256;
-    if (is_bf<T>()) bytes += (size_t)big::DH_SPLITS * chunk * a.D * sizeof(float) + 256;
+    // bf16: split-K partials of the hand-written dH GEMM, or the hipBLASLt workspace
+    if (is_bf<T>()) bytes += std::max((size_t)big::DH_SPLITS * chunk * a.D * sizeof(float), blas::WS_BYTES) + 256;
     return bytes;
 }
 
@@ -833,6 +836,33 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
     uintptr_t part = (uintptr_t)((U *)p.ht + (int64_t)a.D * Rmax);
     q.dh_part = (float *)((part + 255) & ~(uintptr_t)255);
     const size_t smem = big::SMEM;
+    if (blas::enabled()) {
+        // G^T [Vp][Rp] from the fused grad tiles, then two library GEMMs (column-major views):
+        //   dW^T[D][V] += H^T G^T-view   (m = D, n = V, k = rows)
+        //   dH^T[D][rows] = W^T G-view   (m = D, n = rows, k = V)
+        p.write_g = 0;
+        const size_t blas_ws = std::max((size_t)big::DH_SPLITS * chunk * a.D * sizeof(float), blas::WS_BYTES);
+        QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::grad_tile_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        for (int r0 = 0; r0 < a.N; r0 += chunk) {
+            p.row0 = r0;
+            p.rows = std::min(chunk, a.N - r0);
+            p.Rp = round_up(p.rows, big::BTM);
+            hipLaunchKernelGGL(big::grad_tile_kernel,
+                               dim3(big::xcd_grid((p.Vp / big::BTN) * (p.Rp / big::BTM))), dim3(THREADS), smem,
+                               stream, p);
+            int st = launch_status("ce grad_tile_kernel (bf16)");
+            if (st) return st;
+            st = blas::gemm_bf16(false, false, a.D, a.V, p.rows, (const U *)a.h + (int64_t)r0 * a.ldh, a.ldh,
+                                 p.gtbuf, p.Rp, 1.f, a.dw, a.lddw, true, q.dh_part, blas_ws, stream);
+            if (st) return st;
+            st = blas::gemm_bf16(false, true, a.D, p.rows, a.V, a.w, a.ldw, p.gtbuf, p.Rp, 0.f,
+                                 (U *)a.dh + (int64_t)r0 * a.lddh, a.lddh, false, q.dh_part, blas_ws, stream);
+            if (st) return st;
+        }
+        return QPAM_OK;
+    }
+    p.write_g = 1;
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::grad_tile_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::dw_gemm_kernel,
@@ -881,6 +911,7 @@ int run_bwd(const qpam_ce_bwd_args &a, hipStream_t stream) {
     if (is_bf<T>()) return run_bwd_bf16(a, stream);
     BwdParams p;
     p.a = a;
+    p.write_g = 1;
     p.Vp = round_up(a.V, VT);
     const int chunk = std::min(a.chunk, a.N);
     const int Rmax = round_up(chunk, BM);

@@ -66,7 +66,20 @@ def test_ce_all_rows_ignored(gpu_lib):
     assert loss.item() == 0.0 and torch.all(dh == 0) and torch.all(dw == 0)
 
 
-def test_ce_bf16(gpu_lib):
+# bf16 backward GEMMs: hipBLASLt (default) or the hand-written kernels (QPAM_CE_GEMM=hip)
+GEMM_PATHS = ["library", "hip"]
+
+
+def _select_gemm(monkeypatch, path):
+    if path == "hip":
+        monkeypatch.setenv("QPAM_CE_GEMM", "hip")
+    else:
+        monkeypatch.delenv("QPAM_CE_GEMM", raising=False)
+
+
+@pytest.mark.parametrize("path", GEMM_PATHS)
+def test_ce_bf16(gpu_lib, monkeypatch, path):
+    _select_gemm(monkeypatch, path)
     h, w, t = _data(1000, 128, 3000, 6, torch.bfloat16, e_std=0.1)
     t[::10] = -100
     loss, dh, dw = _gpu(h, w, t, chunk=384)
@@ -92,10 +105,12 @@ def test_ce_per_token_and_stats(gpu_lib):
     assert corr2 == tok2 == 150
 
 
-def test_ce_config5_full_size(gpu_lib):
+@pytest.mark.parametrize("path", GEMM_PATHS)
+def test_ce_config5_full_size(gpu_lib, monkeypatch, path):
     """Config 5: N=16384, d_model=512 (D=1024 real-concat), V=50261, bf16 h ~N(0,1),
     E ~N(0, 0.02^2), 10% ignore.  Loss checked on all rows, dH on 64 sampled
     rows, dW on 256 sampled vocab rows, against fp32 CPU math on the bf16 values."""
+    _select_gemm(monkeypatch, path)
     N, d_model, V = 16384, 512, 50261
     h, w, t = O.make_ce_inputs(N, d_model, V, 1005, dtype=torch.bfloat16)
     loss, dh, dw = _gpu(h, w, t)

@@ -169,6 +169,212 @@ __global__ void __launch_bounds__(THREADS) state_scan_kernel(FwdParams p) {
 }
 
 // ---------------------------------------------------------------- kernel 3 --
+// fp32 inputs.  Complex products take three real MFMAs (Gauss):
+//   a b       = (T1 - T2) + i (T3 - T1 - T2),  T1 = ar br, T2 = ai bi, T3 = (ar + ai)(br + bi)
+//   conj(a) b = (T1 + T2) + i (T3 - T1 + T2),  T3 = (ar - ai)(br + bi)
+// LDS holds Q and one 64-row tile that is K, then V, then each carried state
+// (about 72 KiB, two blocks per CU); V and the next state wait in registers.
+template <int C>
+__global__ void __launch_bounds__(THREADS) chunk_output_f32_kernel(FwdParams p) {
+    extern __shared__ float smem[];
+    float *sQr = smem, *sQi = sQr + C * P;
+    float *sXr = sQi + C * P, *sXi = sXr + D * P;  // K tile, then V, then S_m
+    float *sL = sXi + D * P;                        // [MAX_M][64] log-decay prefix
+    float *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
+
+    const qpam_scan_args &a = p.a;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int c0 = c * C;
+    const int valid = min(C, a.T - c0);
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const bool general = (a.M > 1) || (a.rot_re != nullptr);
+    const bool carry = (c > 0) || (a.s0_re != nullptr);
+
+    const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+    const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+    const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+    F32Tile<C> vrt, vit;
+    {
+        F32Tile<C> t4[4];
+        tile_load<C>(t4[0], (const float *)a.q.re + qo, a.q.s2, valid);
+        tile_load<C>(t4[1], (const float *)a.q.im + qo, a.q.s2, valid);
+        tile_load<C>(t4[2], (const float *)a.k.re + ko, a.k.s2, valid);
+        tile_load<C>(t4[3], (const float *)a.k.im + ko, a.k.s2, valid);
+        tile_load<C>(vrt, (const float *)a.v.re + vo, a.v.s2, valid);
+        tile_load<C>(vit, (const float *)a.v.im + vo, a.v.s2, valid);
+        tile_store<C>(sQr, t4[0], a.q_scale);
+        tile_store<C>(sQi, t4[1], a.q_scale);
+        tile_store<C>(sXr, t4[2], 1.f);
+        tile_store<C>(sXi, t4[3], 1.f);
+    }
+    if (w == 0) {
+        for (int m = 0; m < a.M; ++m) {
+            const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
+            sL[m * 64 + lane] = chunk_log_prefix(gp, a.sg_t, valid, lane);
+            float rr = 1.f, ri = 0.f;
+            if (a.rot_re && lane < valid) {
+                const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + lane) * a.sr_t;
+                rr = a.rot_re[ro];
+                ri = a.rot_im[ro];
+            }
+            sRr[m * 64 + lane] = rr;
+            sRi[m * 64 + lane] = ri;
+        }
+    }
+    __syncthreads();
+
+    const int tt = w;  // query rows t in [16tt, 16tt+16)
+    const bool active = tt < C / 16;
+    const int t = 16 * tt + l16;
+    floatx4 wr[4], wi[4];  // A = W . D~ per s-tile; lane holds s = 16st+4g+r, t
+    if (active) {
+        // ---- transposed score tiles W^T[s][t] = sum_j conj(K[s,j]) Q~[t,j], s-tiles st <= tt
+        floatx4 s1[4], s2[4], s3[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) s1[st] = s2[st] = s3[st] = zero4();
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const float4 qr = *reinterpret_cast<const float4 *>(sQr + t * P + 16 * q4 + 4 * g);
+            const float4 qi = *reinterpret_cast<const float4 *>(sQi + t * P + 16 * q4 + 4 * g);
+            const float4 qs4 = make_float4(qr.x + qi.x, qr.y + qi.y, qr.z + qi.z, qr.w + qi.w);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > tt || 16 * st >= C) continue;
+                const float4 kr = *reinterpret_cast<const float4 *>(sXr + (16 * st + l16) * P + 16 * q4 + 4 * g);
+                const float4 ki = *reinterpret_cast<const float4 *>(sXi + (16 * st + l16) * P + 16 * q4 + 4 * g);
+                const float kd[4] = {kr.x - ki.x, kr.y - ki.y, kr.z - ki.z, kr.w - ki.w};
+                const float krr[4] = {kr.x, kr.y, kr.z, kr.w}, kii[4] = {ki.x, ki.y, ki.z, ki.w};
+                const float qrr[4] = {qr.x, qr.y, qr.z, qr.w}, qii[4] = {qi.x, qi.y, qi.z, qi.w};
+                const float qss[4] = {qs4.x, qs4.y, qs4.z, qs4.w};
+#pragma unroll
+                for (int kk = 0; kk < 4; ++kk) {
+                    s1[st] = mfma4(krr[kk], qrr[kk], s1[st]);
+                    s2[st] = mfma4(kii[kk], qii[kk], s2[st]);
+                    s3[st] = mfma4(kd[kk], qss[kk], s3[st]);
+                }
+            }
+        }
+        // ---- W = conj(K) Q~, then the (complex) decay D~[t,s]
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            if (st > tt || 16 * st >= C) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int s = 16 * st + 4 * g + r;
+                const float xr = s1[st][r] + s2[st][r], xi = s3[st][r] - s1[st][r] + s2[st][r];
+                float dre = 0.f, dim = 0.f;
+                if (s <= t) {
+                    if (!general) {
+                        dre = __expf(fminf(sL[t] - sL[s], 0.f));
+                    } else {
+                        for (int m = 0; m < a.M; ++m) {
+                            const float dm = __expf(fminf(sL[m * 64 + t] - sL[m * 64 + s], 0.f));
+                            dre += sRr[m * 64 + t] * dm;
+                            dim += sRi[m * 64 + t] * dm;
+                        }
+                    }
+                }
+                wr[st][r] = xr * dre - xi * dim;
+                wi[st][r] = xr * dim + xi * dre;
+            }
+        }
+    }
+    // K is consumed: V takes its LDS tile; the first carried state waits in registers
+    F32Tile<D> nr, ni;
+    if (carry) {
+        const float *src = chunk_state_ptr(p, 0, b, h, c);
+        tile_load<D>(nr, src, D, D);
+        tile_load<D>(ni, src + D * D, D, D);
+    }
+    __syncthreads();
+    tile_store<C>(sXr, vrt, 1.f);
+    tile_store<C>(sXi, vit, 1.f);
+    __syncthreads();
+
+    floatx4 y1[4], y2[4], y3[4];  // Y = (y1 - y2) + i (y3 - y1 - y2)
+#pragma unroll
+    for (int it = 0; it < 4; ++it) y1[it] = y2[it] = y3[it] = zero4();
+    if (active) {
+        // ---- intra-chunk read  Y += A V   (k = s, 4 k-steps per s-tile)
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            if (st > tt || 16 * st >= C) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int s = 16 * st + 4 * g + r;
+                const float ar = wr[st][r], ai = wi[st][r], as = ar + ai;
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const float vr = sXr[s * P + 16 * it + l16];
+                    const float vi = sXi[s * P + 16 * it + l16];
+                    y1[it] = mfma4(ar, vr, y1[it]);
+                    y2[it] = mfma4(ai, vi, y2[it]);
+                    y3[it] = mfma4(as, vr + vi, y3[it]);
+                }
+            }
+        }
+    }
+
+    // ---- carried read  Y += sum_m (rho_m . Q~) S_in,m^T
+    if (carry) {
+        for (int m = 0; m < a.M; ++m) {
+            __syncthreads();  // previous readers of sX are done
+            tile_store<D>(sXr, nr, 1.f);
+            tile_store<D>(sXi, ni, 1.f);
+            if (m + 1 < a.M) {
+                const float *src = chunk_state_ptr(p, m + 1, b, h, c);
+                tile_load<D>(nr, src, D, D);
+                tile_load<D>(ni, src + D * D, D, D);
+            }
+            __syncthreads();
+            if (active) {
+                const float cum = __expf(sL[m * 64 + t]);
+                const float rho_r = sRr[m * 64 + t] * cum, rho_i = sRi[m * 64 + t] * cum;
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const float4 qr = *reinterpret_cast<const float4 *>(sQr + t * P + 16 * q4 + 4 * g);
+                    const float4 qi = *reinterpret_cast<const float4 *>(sQi + t * P + 16 * q4 + 4 * g);
+                    const float qrr[4] = {qr.x, qr.y, qr.z, qr.w}, qii[4] = {qi.x, qi.y, qi.z, qi.w};
+                    float pr[4], pi[4], ps[4];
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) {
+                        pr[kk] = rho_r * qrr[kk] - rho_i * qii[kk];
+                        pi[kk] = rho_r * qii[kk] + rho_i * qrr[kk];
+                        ps[kk] = pr[kk] + pi[kk];
+                    }
+#pragma unroll
+                    for (int it = 0; it < 4; ++it) {
+                        const float4 sr = *reinterpret_cast<const float4 *>(sXr + (16 * it + l16) * P + 16 * q4 + 4 * g);
+                        const float4 si = *reinterpret_cast<const float4 *>(sXi + (16 * it + l16) * P + 16 * q4 + 4 * g);
+                        const float srr[4] = {sr.x, sr.y, sr.z, sr.w}, sii[4] = {si.x, si.y, si.z, si.w};
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) {
+                            y1[it] = mfma4(pr[kk], srr[kk], y1[it]);
+                            y2[it] = mfma4(pi[kk], sii[kk], y2[it]);
+                            y3[it] = mfma4(ps[kk], srr[kk] + sii[kk], y3[it]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    if (active) {
+        const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)c0 * a.y.s2;
+#pragma unroll
+        for (int it = 0; it < 4; ++it)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tr = 16 * tt + 4 * g + r;
+                if (tr < valid) {
+                    a.y.re[yo + (int64_t)tr * a.y.s2 + 16 * it + l16] = y1[it][r] - y2[it][r];
+                    a.y.im[yo + (int64_t)tr * a.y.s2 + 16 * it + l16] = y3[it][r] - y1[it][r] - y2[it][r];
+                }
+            }
+    }
+}
+
+// Generic form (fp32 LDS tiles; used for bf16 inputs with 16- or 32-step chunks).
 template <typename Tin, int C>
 __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
     extern __shared__ float smem[];
@@ -664,16 +870,19 @@ template <int C>
 size_t state_smem() { return (size_t)(4 * C * P + MAX_M * 64) * sizeof(float); }
 template <int C>
 size_t output_smem() { return (size_t)(4 * C * P + 2 * D * P + 3 * MAX_M * 64) * sizeof(float); }
+template <int C>
+size_t output_f32_smem() { return (size_t)(2 * C * P + 2 * D * P + 3 * MAX_M * 64) * sizeof(float); }
 
 template <typename Tin, int C>
 int launch_fwd(const FwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;
     dim3 grid(p.n_chunks, a.H, a.B);
-    const size_t s1 = state_smem<C>(), s3 = output_smem<C>();
+    constexpr bool f32 = std::is_same<Tin, float>::value;
+    const void *out_kernel = f32 ? (const void *)chunk_output_f32_kernel<C> : (const void *)chunk_output_kernel<Tin, C>;
+    const size_t s1 = state_smem<C>(), s3 = f32 ? output_f32_smem<C>() : output_smem<C>();
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_state_kernel<Tin, C>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_kernel<Tin, C>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
+    QPAM_CHECK_HIP(hipFuncSetAttribute(out_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
     hipLaunchKernelGGL((chunk_state_kernel<Tin, C>), grid, dim3(THREADS), s1, stream, p);
     int st = launch_status("chunk_state_kernel");
     if (st) return st;
@@ -681,7 +890,8 @@ int launch_fwd(const FwdParams &p, hipStream_t stream) {
     st = launch_status("state_scan_kernel");
     if (st) return st;
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));
-    hipLaunchKernelGGL((chunk_output_kernel<Tin, C>), grid, dim3(THREADS), s3, stream, p);
+    if constexpr (f32) hipLaunchKernelGGL((chunk_output_f32_kernel<C>), grid, dim3(THREADS), s3, stream, p);
+    else hipLaunchKernelGGL((chunk_output_kernel<Tin, C>), grid, dim3(THREADS), s3, stream, p);
     st = launch_status("chunk_output_kernel");
     if (st) return st;
     if (a.prof_ev[1]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[1], stream));

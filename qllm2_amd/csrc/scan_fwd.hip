@@ -80,25 +80,27 @@ __global__ void __launch_bounds__(THREADS) chunk_state_kernel(FwdParams p) {
     }
     __syncthreads();
 
-    // wave w owns value rows i in [16w, 16w+16); all 64 key columns j
+    // wave w owns value rows i in [16w, 16w+16); all 64 key columns j.
+    // dS = sum_s dl_s v_s conj(k_s) with three MFMAs per complex product:
+    // re = T1 + T2, im = T3 - T1 + T2, T1 = vr kr, T2 = vi ki, T3 = (vr + vi)(kr - ki)
     for (int m = 0; m < a.M; ++m) {
-        floatx4 accR[4], accI[4];
+        floatx4 t1[4], t2[4], t3[4];
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
+        for (int jt = 0; jt < 4; ++jt) t1[jt] = t2[jt] = t3[jt] = zero4();
 #pragma unroll 4
         for (int ks = 0; ks < C / 4; ++ks) {
             const int s = 4 * ks + g;
             const float dl = sDl[m * 64 + s];
             const float vr = sVr[s * P + 16 * w + l16] * dl;
             const float vi = sVi[s * P + 16 * w + l16] * dl;
+            const float vs = vr + vi;
 #pragma unroll
             for (int jt = 0; jt < 4; ++jt) {
                 const float kr = sKr[s * P + 16 * jt + l16];
                 const float ki = sKi[s * P + 16 * jt + l16];
-                accR[jt] = mfma4(vr, kr, accR[jt]);
-                accR[jt] = mfma4(vi, ki, accR[jt]);
-                accI[jt] = mfma4(vi, kr, accI[jt]);
-                accI[jt] = mfma4(vr, -ki, accI[jt]);
+                t1[jt] = mfma4(vr, kr, t1[jt]);
+                t2[jt] = mfma4(vi, ki, t2[jt]);
+                t3[jt] = mfma4(vs, kr - ki, t3[jt]);
             }
         }
         float *dst = chunk_state_ptr(p, m, b, h, c);
@@ -107,8 +109,8 @@ __global__ void __launch_bounds__(THREADS) chunk_state_kernel(FwdParams p) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 16 * w + 4 * g + r, j = 16 * jt + l16;
-                dst[i * D + j] = accR[jt][r];
-                dst[D * D + i * D + j] = accI[jt][r];
+                dst[i * D + j] = t1[jt][r] + t2[jt][r];
+                dst[D * D + i * D + j] = t3[jt][r] - t1[jt][r] + t2[jt][r];
             }
     }
 }

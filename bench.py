@@ -251,7 +251,7 @@ def main():
     value = tokens / (ms * 1e-3)
     achieved = kflops / (kms * 1e-3)
     out = {
-        "metric": "PAM prefill tokens/s (config 2: chunked dual-form scan fwd, fp32)",
+        "metric": "PAM prefill tokens/s + MFMA %; ragged decode tokens/s + HBM GB/s (256 slots)",
         "value": value,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -263,12 +263,13 @@ def main():
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic (seeded CPU draws, BASELINE.json config 2)",
-        "config": {"workload": "pam_scan_fwd config 2", "B": 8, "T": 2048, "H": 12, "d": 64, "C": 64,
+        "config": {"workload": "config 2: PAM chunked dual-form scan forward (prefill), fp32 complex",
+                   "B": 8, "T": 2048, "H": 12, "d": 64, "C": 64,
                    "layout": "planar re/im fp32"},
         "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": MFMA_FP32_PEAK / 1e12,
                      "unit": "TFLOP/s", "frac": achieved / MFMA_FP32_PEAK,
-                     "traffic": measured_traffic("chunk_output_kernel<float,64>"),
-                     "kernel": "chunk_output_kernel<float,64>", "kernel_ms": kms,
+                     "traffic": measured_traffic("scan_fwd/chunk_output_f32_kernel<64>"),
+                     "kernel": "chunk_output_f32_kernel<64>", "kernel_ms": kms,
                      "kernel_flops": kflops},
         "scan_fwd_total": {"flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
                            "mfma_fp32_frac": flops / (ms * 1e-3) / MFMA_FP32_PEAK},

@@ -5,17 +5,20 @@
 // (v11/model.py:1175-1190) with H = [lm_r | lm_i], W = [E_r | E_i] so that
 // H W^T = Re(h conj(E)^T).
 //
-// Forward: one MFMA GEMM tile per (128 rows, 128 vocab) whose epilogue reduces
-// the tile to per-row (max, sum exp, argmax); logits never leave registers.
-// A per-row finalize merges the vocab tiles into lse, adds the target logit
-// (a direct dot product) and writes the per-row loss; a single-block reduction
-// produces the loss sum and the denominator.
+// Forward: one MFMA GEMM tile per (rows, vocab) block (256 x 128 for bf16,
+// 128 x 128 for fp32) whose epilogue reduces the tile to per-row (max, sum exp,
+// argmax); logits never leave registers.  A per-row finalize merges the vocab
+// tiles into lse, adds the target logit (a direct dot product) and writes the
+// per-row loss; a single-block reduction produces the loss sum and the
+// denominator.
 // Backward, per `chunk` rows: the same GEMM recomputes the logits tile and its
-// epilogue writes G = (softmax - onehot) * scale in the input dtype, both as
-// G [rows][vocab] and G^T [vocab][rows]; then two plain GEMMs dH = G W and
-// dW += G^T H run with K-contiguous operands (W^T and H^T are transposed once
-// into the workspace).  The G buffers hold `chunk` rows, the reference's own
-// memory bound (it keeps chunk x V fp32 logits and softmax alive).
+// epilogue writes G = (softmax - onehot) * scale in the input dtype as
+// G^T [vocab][rows] (and G [rows][vocab] where a hand-written GEMM reads it);
+// then the two plain GEMMs dW += G^T H and dH = G W run through hipBLASLt
+// (bf16, blas.hip) or through the hand-written K-contiguous GEMM kernels (W^T
+// and H^T transposed once into the workspace).  The G buffers hold `chunk`
+// rows, the reference's own memory bound (it keeps chunk x V fp32 logits and
+// softmax alive).
 #include <algorithm>
 
 #include "blas.h"

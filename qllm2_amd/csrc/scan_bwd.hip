@@ -947,6 +947,12 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     }
     if (w == 0) chunk_decay_prologue_f<M>(a, b, h, c0, valid, sL, sRr, sRi, sF, nullptr, nullptr, sFast);
     for (int e = tid; e < 3 * M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
+    B16Regs sn[2];  // carried state S_0, in flight during the intra-chunk phase
+    if (carry) {
+        const U16 *s0p = fsnap(p, 0, b, h, c);
+        regs_load_bf<false>(sn[0], s0p, D, D);
+        regs_load_bf<false>(sn[1], s0p + D * D, D, D);
+    }
     __syncthreads();
 
     const int tt = w;
@@ -1118,12 +1124,13 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     if (carry) {
         for (int m = 0; m < M; ++m) {
             __syncthreads();
-            const U16 *src = fsnap(p, m, b, h, c);
-            {  // S natural; read transposed below
-                U16 *const bd[2] = {sVr, sVi};
-                const U16 *const bs[2] = {src, src + D * D};
-                const int64_t bst[2] = {D, D};
-                stage_bf<2, 0x0u>(bd, bs, bst, D);
+            // S_m natural (read transposed below); S_{m+1} goes in flight meanwhile
+            regs_store_bf<false>(sVr, sn[0]);
+            regs_store_bf<false>(sVi, sn[1]);
+            if (m + 1 < M) {
+                const U16 *nx = fsnap(p, m + 1, b, h, c);
+                regs_load_bf<false>(sn[0], nx, D, D);
+                regs_load_bf<false>(sn[1], nx + D * D, D, D);
             }
             __syncthreads();
             floatx4 xr[4], xi[4];
@@ -1201,7 +1208,7 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
 }
 
 template <int M>
-__global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
+__global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
     U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;   // q, later G'_m
     U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
@@ -1245,6 +1252,21 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
         }
     }
     __syncthreads();
+
+    // snapshots of state m (dS after the chunk, and the entering state): state 0
+    // is in flight during the intra-chunk phase, state m+1 while m is processed
+    B16Regs gr[2], sr[2];
+    auto load_state = [&](int m) {
+        const U16 *gsrc = gsnap(p, m, b, h, c);
+        regs_load_bf<false>(gr[0], gsrc, D, D);
+        regs_load_bf<false>(gr[1], gsrc + D * D, D, D);
+        if (carry) {
+            const U16 *ssrc = fsnap(p, m, b, h, c);
+            regs_load_bf<false>(sr[0], ssrc, D, D);
+            regs_load_bf<false>(sr[1], ssrc + D * D, D, D);
+        }
+    };
+    load_state(0);
 
     const int st = w;
     const int s = 16 * st + l16;
@@ -1392,16 +1414,7 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
     // state-write gradients with G'_m = dS after this chunk
     for (int m = 0; m < M; ++m) {
         __syncthreads();
-        const U16 *gsrc = gsnap(p, m, b, h, c);
         {  // G' natural into sQ*; with a carried state also this thread's share of S (registers)
-            B16Regs gr[2], sr[2];
-            regs_load_bf<false>(gr[0], gsrc, D, D);
-            regs_load_bf<false>(gr[1], gsrc + D * D, D, D);
-            if (carry) {
-                const U16 *ssrc = fsnap(p, m, b, h, c);
-                regs_load_bf<false>(sr[0], ssrc, D, D);
-                regs_load_bf<false>(sr[1], ssrc + D * D, D, D);
-            }
             regs_store_bf<false>(sQr, gr[0]);
             regs_store_bf<false>(sQi, gr[1]);
             if (carry) {  // g_total = sum Re(conj(G') S) over both planes, fp32 accumulation
@@ -1420,6 +1433,7 @@ __global__ void __launch_bounds__(THREADS) key_side_bf16_kernel(BwdParams p) {
                 if (lane == 0) sRed[w] = part;
             }
         }
+        if (m + 1 < M) load_state(m + 1);
         __syncthreads();
         const float dls = sDl[m * 64 + s];
         floatx4 zr[4], zi[4];

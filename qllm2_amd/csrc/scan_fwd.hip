@@ -681,6 +681,12 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
         }
         if (lane == 0) *sFast = fast ? 1 : 0;
     }
+    B16Regs sn[2];  // snapshot of the first carried state, in flight during the intra-chunk phase
+    if (carry) {
+        const U *s0p = chunk_snap_ptr(p, 0, b, h, c);
+        regs_load_bf<false>(sn[0], s0p, D, D);
+        regs_load_bf<false>(sn[1], s0p + D * D, D, D);
+    }
     __syncthreads();
 
     const int tt = w;
@@ -790,12 +796,12 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
     if (carry) {
         for (int m = 0; m < M; ++m) {
             __syncthreads();
-            const U *src = chunk_snap_ptr(p, m, b, h, c);
-            {
-                U *const dst[2] = {sKr, sKi};
-                const U *const srcs[2] = {src, src + D * D};
-                const int64_t st[2] = {D, D};
-                stage_bf<2, 0u>(dst, srcs, st, D);
+            regs_store_bf<false>(sKr, sn[0]);
+            regs_store_bf<false>(sKi, sn[1]);
+            if (m + 1 < M) {  // the next state's snapshot is in flight while this one is used
+                const U *nx = chunk_snap_ptr(p, m + 1, b, h, c);
+                regs_load_bf<false>(sn[0], nx, D, D);
+                regs_load_bf<false>(sn[1], nx + D * D, D, D);
             }
             __syncthreads();
             const float cum = __expf(sL[m * 64 + t]) * qs;

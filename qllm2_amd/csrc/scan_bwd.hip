@@ -834,6 +834,182 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
 // unscaled; q_scale is applied where q~ enters an fp32 result.
 using U16 = unsigned short;
 
+// Gradient-state pass (reverse): one block per (state m, b, h, half of the value
+// rows) walks the chunks from last to first with the running dS in registers
+// (fp32, accumulator layout).  Per chunk: bf16 snapshot of dS after the chunk,
+// then dS <- total dS + sum_t conj(rho_m[t]) q_scale dY_t (x) conj(q_t) on MFMA.
+// dS0 is written when requested.  Chunk c-2's dY (fp32 -> bf16), Q and gamma /
+// rotation are loaded while chunk c is processed; the snapshot of chunk c is
+// staged in LDS and stored during the next chunk.
+constexpr size_t gpass_bf16_smem() {
+    return (size_t)2 * 2 * PLANE_B * 2           // Q [buf][plane][64][PB]
+           + (size_t)2 * 2 * 64 * PBH * 2        // dY columns of this half (bf16) [buf][plane][64][PBH]
+           + (size_t)2 * 2 * PASS_ROWS * PB * 2  // snapshot staging [buf][plane][32][PB]
+           + (size_t)2 * 128 * sizeof(float);    // conj(rho) q_scale (re[64], im[64]) per buffer
+}
+
+__global__ void __launch_bounds__(THREADS) grad_pass_bf16_kernel(BwdParams p) {
+    extern __shared__ float smem[];
+    U16 *sQ = reinterpret_cast<U16 *>(smem);     // + (buf * 2 + plane) * PLANE_B
+    U16 *sG = sQ + 4 * PLANE_B;                  // + (buf * 2 + plane) * 64 * PBH
+    U16 *sS = sG + 4 * 64 * PBH;                 // + (buf * 2 + plane) * PASS_ROWS * PB
+    float *sW = reinterpret_cast<float *>(sS + 4 * PASS_ROWS * PB);  // + buf * 128: re[64], im[64]
+
+    const qpam_scan_args &a = p.a;
+    const int part = blockIdx.x % PASS_SPLIT, chain = blockIdx.x / PASS_SPLIT;
+    const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
+    const int b = bh / a.H, h = bh % a.H;
+    const int i0 = part * PASS_ROWS;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int it = w >> 1, jh = w & 1;
+    const int n = p.n_chunks;
+    const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
+    const float *rbr = a.rot_re ? a.rot_re + m * a.sr_m + b * a.sr_b + h * a.sr_h : nullptr;
+    const float *rbi = a.rot_im ? a.rot_im + m * a.sr_m + b * a.sr_b + h * a.sr_h : nullptr;
+    const U16 *qre = (const U16 *)a.q.re + b * a.q.s0 + h * a.q.s1, *qim = (const U16 *)a.q.im + b * a.q.s0 + h * a.q.s1;
+    const float *yre = (const float *)p.dy.re + b * p.dy.s0 + h * p.dy.s1;
+    const float *yim = (const float *)p.dy.im + b * p.dy.s0 + h * p.dy.s1;
+    const bool need_ds0 = p.ds0_re != nullptr;
+
+    floatx4 gR[2], gI[2];  // dS[i][j], rows i0 + 16it + 4g + r, cols 16(2jh + jj) + l16
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        gR[jj] = gI[jj] = zero4();
+        if (p.ds_re) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(i0 + 16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                gR[jj][r] = p.ds_re[o];
+                gI[jj][r] = p.ds_im[o];
+            }
+        }
+    }
+
+    struct ChunkRegs {
+        B16Regs qr, qi;
+        F32Half yr, yi;
+        float gam, rr, ri;
+    };
+    ChunkRegs cr[2];
+    auto load_chunk = [&](int c, ChunkRegs &x) {
+        const int c0 = c * 64, valid = min(64, a.T - c0);
+        const int64_t qo = (int64_t)c0 * a.q.s2, yo = (int64_t)c0 * p.dy.s2;
+        regs_load_bf<false>(x.qr, qre + qo, a.q.s2, valid);
+        regs_load_bf<false>(x.qi, qim + qo, a.q.s2, valid);
+        x.yr = half_tile_load_f32(yre + yo, p.dy.s2, i0, valid);
+        x.yi = half_tile_load_f32(yim + yo, p.dy.s2, i0, valid);
+        const bool lv = w == 0 && lane < valid;
+        x.gam = lv ? gbase[(int64_t)(c0 + lane) * a.sg_t] : 1.f;
+        x.rr = (lv && rbr) ? rbr[(int64_t)(c0 + lane) * a.sr_t] : 1.f;
+        x.ri = (lv && rbi) ? rbi[(int64_t)(c0 + lane) * a.sr_t] : 0.f;
+    };
+    auto stage_chunk = [&](int c, int buf, const ChunkRegs &x) {
+        regs_store_bf<false>(sQ + (buf * 2) * PLANE_B, x.qr);
+        regs_store_bf<false>(sQ + (buf * 2 + 1) * PLANE_B, x.qi);
+        half_tile_store_f32_as_bf(sG + (buf * 2) * 64 * PBH, x.yr);
+        half_tile_store_f32_as_bf(sG + (buf * 2 + 1) * 64 * PBH, x.yi);
+        if (w == 0) {  // conj(rho[t]) q_scale = conj(r[t]) cum[t] q_scale
+            const int valid = min(64, a.T - c * 64);
+            float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_up(L, off);
+                if (lane >= off) L += y;
+            }
+            const float cum = (lane < valid) ? __expf(L) * a.q_scale : 0.f;
+            sW[buf * 128 + lane] = x.rr * cum;
+            sW[buf * 128 + 64 + lane] = -x.ri * cum;
+        }
+    };
+    auto store_snapshot = [&](int c, int buf) {
+        U16 *dst = gsnap(p, m, b, h, c);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int idx = tid + q * THREADS;
+            const int pl = idx >> 8, r = (idx >> 3) & 31, c8 = idx & 7;
+            const uint4 v = *reinterpret_cast<const uint4 *>(sS + (buf * 2 + pl) * PASS_ROWS * PB + r * PB + 8 * c8);
+            *reinterpret_cast<uint4 *>(dst + pl * D * D + (int64_t)(i0 + r) * D + 8 * c8) = v;
+        }
+    };
+
+    // reverse order: step k handles chunk c = n-1-k with LDS buffer k & 1
+    auto step = [&](int k, ChunkRegs &mine, ChunkRegs &next) {
+        const int c = n - 1 - k, buf = k & 1;
+        if (k + 2 < n) load_chunk(c - 2, mine);
+        if (k > 0) store_snapshot(c + 1, buf ^ 1);
+        // snapshot of dS after chunk c
+        U16 *snr = sS + (buf * 2) * PASS_ROWS * PB, *sni = sS + (buf * 2 + 1) * PASS_ROWS * PB;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * it + 4 * g + r, col = 16 * (2 * jh + jj) + l16;
+                snr[row * PB + col] = f32_to_bf16(gR[jj][r]);
+                sni[row * PB + col] = f32_to_bf16(gI[jj][r]);
+            }
+        if (c > 0 || need_ds0) {
+            // dG rows (value i) x cols (key j): A = (conj(rho) q_scale dY)^T, B = Q (k = t)
+            floatx4 accR[2], accI[2];
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
+            const U16 *Qr = sQ + (buf * 2) * PLANE_B, *Qi = sQ + (buf * 2 + 1) * PLANE_B;
+            const U16 *Gr = sG + (buf * 2) * 64 * PBH, *Gi = sG + (buf * 2 + 1) * 64 * PBH;
+            const float *wre = sW + buf * 128, *wim = wre + 64;
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                const int t0 = 32 * kp + 8 * g;
+                const floatx8 gr = to_f(ld_tr(Gr, t0, t0 + 4, 16 * it, PBH)), gi = to_f(ld_tr(Gi, t0, t0 + 4, 16 * it, PBH));
+                floatx8 vr, vi;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float wr = wre[t0 + e], wi = wim[t0 + e];
+                    vr[e] = wr * gr[e] - wi * gi[e];
+                    vi[e] = wr * gi[e] + wi * gr[e];
+                }
+                const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int jt = 2 * jh + jj;
+                    const bf16x8 qr = ld_tr(Qr, t0, t0 + 4, 16 * jt), qi = ld_tr(Qi, t0, t0 + 4, 16 * jt);
+                    accR[jj] = mfma_bf(ar, qr, accR[jj]);
+                    accR[jj] = mfma_bf(ai, qi, accR[jj]);
+                    accI[jj] = mfma_bf(ai, qr, accI[jj]);
+                    accI[jj] = mfma_bf(nar, qi, accI[jj]);
+                }
+            }
+            const float tot = ftotal(p, m, b, h, c);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    gR[jj][r] = tot * gR[jj][r] + accR[jj][r];
+                    gI[jj][r] = tot * gI[jj][r] + accI[jj][r];
+                }
+        }
+        if (k + 1 < n) stage_chunk(c - 1, buf ^ 1, next);
+        __syncthreads();
+    };
+    load_chunk(n - 1, cr[0]);
+    if (n > 1) load_chunk(n - 2, cr[1]);
+    stage_chunk(n - 1, 0, cr[0]);
+    __syncthreads();
+    for (int k = 0; k < n; k += 2) {
+        step(k, cr[0], cr[1]);
+        if (k + 1 < n) step(k + 1, cr[1], cr[0]);
+    }
+    store_snapshot(0, (n - 1) & 1);
+    if (need_ds0) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(i0 + 16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                p.ds0_re[o] = gR[jj][r];
+                p.ds0_im[o] = gI[jj][r];
+            }
+    }
+}
+
 __global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
     U16 *sGr = reinterpret_cast<U16 *>(smem), *sGi = sGr + PLANE_B;
@@ -1542,18 +1718,15 @@ template <int M>
 int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;
     dim3 grid(p.n_chunks, a.H, a.B);
-    const size_t s1 = gcs_bf16_smem(), s3 = qside_bf16_smem<M>(), s4 = kside_bf16_smem<M>();
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_chunk_state_bf16_kernel,
+    const size_t s1 = gpass_bf16_smem(), s3 = qside_bf16_smem<M>(), s4 = kside_bf16_smem<M>();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)query_side_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
-    hipLaunchKernelGGL(grad_chunk_state_bf16_kernel, grid, dim3(THREADS), s1, stream, p);
-    int st = launch_status("grad_chunk_state_bf16_kernel");
-    if (st) return st;
-    hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, stream, p);
-    st = launch_status("grad_state_scan_kernel");
+    hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(a.M * a.B * a.H * PASS_SPLIT), dim3(THREADS), s1, stream, p);
+    int st = launch_status("grad_pass_bf16_kernel");
     if (st) return st;
     hipLaunchKernelGGL(query_side_bf16_kernel<M>, grid, dim3(THREADS), s3, stream, p);
     st = launch_status("query_side_bf16_kernel");

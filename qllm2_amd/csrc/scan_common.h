@@ -202,11 +202,47 @@ __device__ __forceinline__ shortx4 lds_read_tr(const unsigned short *p) {
 // bf16 LDS tile (pitch PB) for a contraction over its rows: lane l16 of each
 // 16-lane group receives rows r0..r0+3 then r1..r1+3 of column col0 + l16.  The
 // caller folds the lane group into r0/r1; all 64 lanes must execute it.
-__device__ __forceinline__ bf16x8 ld_tr(const unsigned short *tile, int r0, int r1, int col0) {
+__device__ __forceinline__ bf16x8 ld_tr(const unsigned short *tile, int r0, int r1, int col0, int pitch = PB) {
     const int l16 = threadIdx.x & 15;
-    const unsigned short *p = tile + (l16 >> 2) * PB + col0 + 4 * (l16 & 3);
-    const shortx4 lo = lds_read_tr(p + r0 * PB), hi = lds_read_tr(p + r1 * PB);
+    const unsigned short *p = tile + (l16 >> 2) * pitch + col0 + 4 * (l16 & 3);
+    const shortx4 lo = lds_read_tr(p + r0 * pitch), hi = lds_read_tr(p + r1 * pitch);
     return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// State passes (one block per state and half of its value rows walks the chunks).
+constexpr int PASS_ROWS = 32;  // value rows per block
+constexpr int PASS_SPLIT = D / PASS_ROWS;
+constexpr int PBH = 40;        // LDS pitch (bf16) of 32-column tiles
+
+// [64 rows x 32 cols] bf16 sub-tile (columns col0..col0+31): one 16-byte load per thread
+__device__ __forceinline__ uint4 half_tile_load(const unsigned short *src, int64_t st, int col0, int valid) {
+    const int r = threadIdx.x >> 2, c8 = threadIdx.x & 3;
+    return (r < valid) ? *reinterpret_cast<const uint4 *>(src + (int64_t)r * st + col0 + 8 * c8)
+                       : make_uint4(0, 0, 0, 0);
+}
+__device__ __forceinline__ void half_tile_store(unsigned short *lds, uint4 v) {
+    const int r = threadIdx.x >> 2, c8 = threadIdx.x & 3;
+    *reinterpret_cast<uint4 *>(lds + r * PBH + 8 * c8) = v;
+}
+// the same sub-tile of an fp32 source, kept as two float4 per thread
+struct F32Half {
+    float4 lo, hi;
+};
+__device__ __forceinline__ F32Half half_tile_load_f32(const float *src, int64_t st, int col0, int valid) {
+    const int r = threadIdx.x >> 2, c8 = threadIdx.x & 3;
+    F32Half x{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+    if (r < valid) {
+        const float *q = src + (int64_t)r * st + col0 + 8 * c8;
+        x.lo = *reinterpret_cast<const float4 *>(q);
+        x.hi = *reinterpret_cast<const float4 *>(q + 4);
+    }
+    return x;
+}
+__device__ __forceinline__ void half_tile_store_f32_as_bf(unsigned short *lds, const F32Half &x) {
+    const int r = threadIdx.x >> 2, c8 = threadIdx.x & 3;
+    const ushortx8 u = {f32_to_bf16(x.lo.x), f32_to_bf16(x.lo.y), f32_to_bf16(x.lo.z), f32_to_bf16(x.lo.w),
+                        f32_to_bf16(x.hi.x), f32_to_bf16(x.hi.y), f32_to_bf16(x.hi.z), f32_to_bf16(x.hi.w)};
+    *reinterpret_cast<ushortx8 *>(lds + r * PBH + 8 * c8) = u;
 }
 
 // Register-staged bf16 / fp32 -> bf16 tile copies (all loads of a batch are

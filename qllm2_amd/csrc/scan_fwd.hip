@@ -554,11 +554,182 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
 }
 
 // ------------------------------------------------------ bf16 MFMA path ----
-// bf16 q/k/v with C = 64: the same two chunk-parallel kernels on
-// v_mfma_f32_16x16x32_bf16 with bf16 LDS tiles (fp32 accumulation, fp32
-// states in the workspace).  Operands whose MFMA k index is the time axis are
-// staged transposed in LDS; q is staged unscaled and q_scale is applied to the
-// fp32 results it enters.
+// bf16 q/k/v with C = 64 on v_mfma_f32_16x16x32_bf16 with bf16 LDS tiles and
+// fp32 accumulation; q is staged unscaled and q_scale is applied to the fp32
+// results it enters.
+//
+// State pass: one block per (state m, b, h, half of the value rows) walks the
+// chunks in order.  Per chunk it forms dS = sum_s dl_s v_s (x) conj(k_s) on
+// MFMA (rows i of its half, all key columns j) and updates the running state
+// S <- total S + dS, which never leaves registers (fp32, accumulator layout).
+// Only the bf16 snapshot of the state entering each chunk, the chunk totals and
+// the final state reach HBM.  Chunk c+1's K and V tiles and gamma are loaded
+// while chunk c is processed (double-buffered LDS, one barrier per chunk); the
+// snapshot of chunk c is staged in LDS and stored during chunk c+1.
+constexpr size_t pass_bf16_smem() {
+    return (size_t)2 * 2 * PLANE_B * 2     // K [buf][plane][64][PB]
+           + (size_t)2 * 2 * 64 * PBH * 2  // V columns of this half [buf][plane][64][PBH]
+           + (size_t)2 * 2 * PASS_ROWS * PB * 2  // snapshot staging [buf][plane][32][PB]
+           + (size_t)2 * 68 * sizeof(float);     // dl[64] + total per buffer
+}
+
+__global__ void __launch_bounds__(THREADS) state_pass_bf16_kernel(FwdParams p) {
+    extern __shared__ float smem[];
+    using U = unsigned short;
+    U *sK = reinterpret_cast<U *>(smem);         // + (buf * 2 + plane) * PLANE_B
+    U *sV = sK + 4 * PLANE_B;                    // + (buf * 2 + plane) * 64 * PBH
+    U *sS = sV + 4 * 64 * PBH;                   // + (buf * 2 + plane) * PASS_ROWS * PB
+    float *sDl = reinterpret_cast<float *>(sS + 4 * PASS_ROWS * PB);  // + buf * 68; [64] = total
+
+    const qpam_scan_args &a = p.a;
+    const int part = blockIdx.x % PASS_SPLIT, chain = blockIdx.x / PASS_SPLIT;
+    const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
+    const int b = bh / a.H, h = bh % a.H;
+    const int i0 = part * PASS_ROWS;  // first value row of this block
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int it = w >> 1, jh = w & 1;  // wave: rows 16it.. of the half, key-column tiles 2jh, 2jh+1
+    const int n = p.n_chunks;
+    const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
+    const U *kre = (const U *)a.k.re + b * a.k.s0 + h * a.k.s1, *kim = (const U *)a.k.im + b * a.k.s0 + h * a.k.s1;
+    const U *vre = (const U *)a.v.re + b * a.v.s0 + h * a.v.s1, *vim = (const U *)a.v.im + b * a.v.s0 + h * a.v.s1;
+
+    // running state S[i][j] for rows i0 + 16it + 4g + r, cols 16(2jh + jj) + l16
+    floatx4 sR[2], sI[2];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        sR[jj] = sI[jj] = zero4();
+        if (a.s0_re) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(i0 + 16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                sR[jj][r] = a.s0_re[o];
+                sI[jj][r] = a.s0_im[o];
+            }
+        }
+    }
+
+    // chunk inputs in registers, two register sets (chunk c in set c & 1): K (2 planes x
+    // 2 uint4), V half (2 planes x 1 uint4), gamma (wave 0).  Sets are selected by
+    // compile-time index only (the chunk loop is unrolled by two).
+    struct ChunkRegs {
+        B16Regs kr, ki;
+        uint4 vr, vi;
+        float gam;
+    };
+    ChunkRegs cr[2];
+    auto load_chunk = [&](int c, ChunkRegs &x) {
+        const int c0 = c * 64, valid = min(64, a.T - c0);
+        const int64_t ko = (int64_t)c0 * a.k.s2, vo = (int64_t)c0 * a.v.s2;
+        regs_load_bf<false>(x.kr, kre + ko, a.k.s2, valid);
+        regs_load_bf<false>(x.ki, kim + ko, a.k.s2, valid);
+        x.vr = half_tile_load(vre + vo, a.v.s2, i0, valid);
+        x.vi = half_tile_load(vim + vo, a.v.s2, i0, valid);
+        x.gam = (w == 0 && lane < valid) ? gbase[(int64_t)(c0 + lane) * a.sg_t] : 1.f;
+    };
+    // registers -> LDS buffer `buf`; wave 0 turns gamma into dl and the chunk total
+    auto stage_chunk = [&](int c, int buf, const ChunkRegs &x) {
+        regs_store_bf<false>(sK + (buf * 2) * PLANE_B, x.kr);
+        regs_store_bf<false>(sK + (buf * 2 + 1) * PLANE_B, x.ki);
+        half_tile_store(sV + (buf * 2) * 64 * PBH, x.vr);
+        half_tile_store(sV + (buf * 2 + 1) * 64 * PBH, x.vi);
+        if (w == 0) {
+            const int valid = min(64, a.T - c * 64);
+            float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_up(L, off);
+                if (lane >= off) L += y;
+            }
+            const float Llast = __shfl(L, valid - 1);
+            sDl[buf * 68 + lane] = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
+            if (lane == 0) {
+                const float tot = __expf(Llast);
+                sDl[buf * 68 + 64] = tot;
+                if (part == 0) *chunk_total_ptr(p, m, b, h, c) = tot;
+            }
+        }
+    };
+    // LDS snapshot staging `buf` -> chunk c's bf16 snapshot rows i0.. (two 16-byte stores per thread)
+    auto store_snapshot = [&](int c, int buf) {
+        U *dst = chunk_snap_ptr(p, m, b, h, c);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const int idx = tid + q * THREADS;  // 0..511: plane, row, 16-byte chunk
+            const int pl = idx >> 8, r = (idx >> 3) & 31, c8 = idx & 7;
+            const uint4 v = *reinterpret_cast<const uint4 *>(sS + (buf * 2 + pl) * PASS_ROWS * PB + r * PB + 8 * c8);
+            *reinterpret_cast<uint4 *>(dst + pl * D * D + (int64_t)(i0 + r) * D + 8 * c8) = v;
+        }
+    };
+
+    // chunk c uses LDS buffer c & 1; chunk c + 2 is loaded into register set c & 1
+    // during chunk c and staged at the end of chunk c + 1 (two chunks of latency cover)
+    auto step = [&](int c, ChunkRegs &mine, ChunkRegs &next) {
+        const int buf = c & 1;
+        if (c + 2 < n) load_chunk(c + 2, mine);
+        if (c > 0) store_snapshot(c - 1, buf ^ 1);
+        // dS rows (value i) x cols (key j): A = dl-scaled V^T (transposed reads of the V half), B = K
+        floatx4 accR[2], accI[2];
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
+        const U *Kr = sK + (buf * 2) * PLANE_B, *Ki = sK + (buf * 2 + 1) * PLANE_B;
+        const U *Vr = sV + (buf * 2) * 64 * PBH, *Vi = sV + (buf * 2 + 1) * 64 * PBH;
+        const float *dl = sDl + buf * 68;
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            const int s0 = 32 * kp + 8 * g;
+            floatx8 vr = to_f(ld_tr(Vr, s0, s0 + 4, 16 * it, PBH)), vi = to_f(ld_tr(Vi, s0, s0 + 4, 16 * it, PBH));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                vr[e] *= dl[s0 + e];
+                vi[e] *= dl[s0 + e];
+            }
+            const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int jt = 2 * jh + jj;
+                const bf16x8 kr = ld_tr(Kr, s0, s0 + 4, 16 * jt), ki = ld_tr(Ki, s0, s0 + 4, 16 * jt);
+                accR[jj] = mfma_bf(ar, kr, accR[jj]);
+                accR[jj] = mfma_bf(ai, ki, accR[jj]);
+                accI[jj] = mfma_bf(ai, kr, accI[jj]);
+                accI[jj] = mfma_bf(nar, ki, accI[jj]);
+            }
+        }
+        // snapshot of the entering state, then S <- total S + dS
+        const float tot = dl[64];
+        U *snr = sS + (buf * 2) * PASS_ROWS * PB, *sni = sS + (buf * 2 + 1) * PASS_ROWS * PB;
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = 16 * it + 4 * g + r, col = 16 * (2 * jh + jj) + l16;
+                snr[row * PB + col] = f32_to_bf16(sR[jj][r]);
+                sni[row * PB + col] = f32_to_bf16(sI[jj][r]);
+                sR[jj][r] = tot * sR[jj][r] + accR[jj][r];
+                sI[jj][r] = tot * sI[jj][r] + accI[jj][r];
+            }
+        if (c + 1 < n) stage_chunk(c + 1, buf ^ 1, next);
+        __syncthreads();
+    };
+    load_chunk(0, cr[0]);
+    if (n > 1) load_chunk(1, cr[1]);
+    stage_chunk(0, 0, cr[0]);
+    __syncthreads();
+    for (int c = 0; c < n; c += 2) {
+        step(c, cr[0], cr[1]);
+        if (c + 1 < n) step(c + 1, cr[1], cr[0]);
+    }
+    store_snapshot(n - 1, (n - 1) & 1);
+    if (a.s_re) {
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(i0 + 16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                a.s_re[o] = sR[jj][r];
+                a.s_im[o] = sI[jj][r];
+            }
+    }
+}
 
 __global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) {
     extern __shared__ float smem[];
@@ -845,16 +1016,13 @@ template <int M>
 int launch_fwd_bf16_m(const FwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;
     dim3 grid(p.n_chunks, a.H, a.B);
-    const size_t s1 = state_bf16_smem(), s3 = output_bf16_smem<M>();
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_state_bf16_kernel,
+    const size_t s1 = pass_bf16_smem(), s3 = output_bf16_smem<M>();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)state_pass_bf16_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
-    hipLaunchKernelGGL(chunk_state_bf16_kernel, grid, dim3(THREADS), s1, stream, p);
-    int st = launch_status("chunk_state_bf16_kernel");
-    if (st) return st;
-    hipLaunchKernelGGL(state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, stream, p);
-    st = launch_status("state_scan_kernel");
+    hipLaunchKernelGGL(state_pass_bf16_kernel, dim3(a.M * a.B * a.H * PASS_SPLIT), dim3(THREADS), s1, stream, p);
+    int st = launch_status("state_pass_bf16_kernel");
     if (st) return st;
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));
     hipLaunchKernelGGL(chunk_output_bf16_kernel<M>, grid, dim3(THREADS), s3, stream, p);

@@ -29,6 +29,7 @@ int validate_scan(const qpam_scan_args *a, const char *who, bool fwd_outputs);
 size_t fwd_workspace_bytes(const qpam_scan_args &a);
 bool uses_snapshots(const qpam_scan_args &a);
 size_t fwd_snapshot_offset(const qpam_scan_args &a);
+int64_t fwd_totals_offset(const qpam_scan_args &a);
 
 namespace {
 
@@ -834,34 +835,31 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
 // unscaled; q_scale is applied where q~ enters an fp32 result.
 using U16 = unsigned short;
 
-// Gradient-state pass (reverse): one block per (state m, b, h, half of the value
-// rows) walks the chunks from last to first with the running dS in registers
-// (fp32, accumulator layout).  Per chunk: bf16 snapshot of dS after the chunk,
-// then dS <- total dS + sum_t conj(rho_m[t]) q_scale dY_t (x) conj(q_t) on MFMA.
-// dS0 is written when requested.  Chunk c-2's dY (fp32 -> bf16), Q and gamma /
-// rotation are loaded while chunk c is processed; the snapshot of chunk c is
-// staged in LDS and stored during the next chunk.
+// Gradient-state pass (reverse): one block per (state m, b, h) walks the chunks
+// from last to first with the running dS in registers (fp32, accumulator layout;
+// wave w owns value rows 16w..16w+15).  Per chunk: bf16 snapshot of dS after the
+// chunk, then dS <- total dS + sum_t conj(rho_m[t]) q_scale dY_t (x) conj(q_t) on
+// MFMA.  dS0 is written when requested.  Chunk c-2's Q and gamma / rotation and
+// chunk c-1's dY (fp32, rounded to bf16 when staged) are loaded while chunk c is
+// processed.
 constexpr size_t gpass_bf16_smem() {
-    return (size_t)2 * 2 * PLANE_B * 2           // Q [buf][plane][64][PB]
-           + (size_t)2 * 2 * 64 * PBH * 2        // dY columns of this half (bf16) [buf][plane][64][PBH]
-           + (size_t)2 * 2 * PASS_ROWS * PB * 2  // snapshot staging [buf][plane][32][PB]
-           + (size_t)2 * 128 * sizeof(float);    // conj(rho) q_scale (re[64], im[64]) per buffer
+    return (size_t)2 * 2 * PLANE_B * 2         // Q [buf][plane][64][PB]
+           + (size_t)2 * 2 * PLANE_B * 2       // dY (bf16) [buf][plane][64][PB]
+           + (size_t)2 * 128 * sizeof(float);  // conj(rho) q_scale (re[64], im[64]) per buffer
 }
 
-__global__ void __launch_bounds__(THREADS) grad_pass_bf16_kernel(BwdParams p) {
+__global__ void __launch_bounds__(THREADS, 2) grad_pass_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
-    U16 *sQ = reinterpret_cast<U16 *>(smem);     // + (buf * 2 + plane) * PLANE_B
-    U16 *sG = sQ + 4 * PLANE_B;                  // + (buf * 2 + plane) * 64 * PBH
-    U16 *sS = sG + 4 * 64 * PBH;                 // + (buf * 2 + plane) * PASS_ROWS * PB
-    float *sW = reinterpret_cast<float *>(sS + 4 * PASS_ROWS * PB);  // + buf * 128: re[64], im[64]
+    U16 *sQ = reinterpret_cast<U16 *>(smem);  // + (buf * 2 + plane) * PLANE_B
+    U16 *sG = sQ + 4 * PLANE_B;               // + (buf * 2 + plane) * PLANE_B
+    float *sW = reinterpret_cast<float *>(sG + 4 * PLANE_B);  // + buf * 128: re[64], im[64]
 
     const qpam_scan_args &a = p.a;
-    const int part = blockIdx.x % PASS_SPLIT, chain = blockIdx.x / PASS_SPLIT;
+    const int chain = blockIdx.x;
     const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
-    const int i0 = part * PASS_ROWS;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int it = w >> 1, jh = w & 1;
+    const int it = w;
     const int n = p.n_chunks;
     const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
     const float *rbr = a.rot_re ? a.rot_re + m * a.sr_m + b * a.sr_b + h * a.sr_h : nullptr;
@@ -871,33 +869,37 @@ __global__ void __launch_bounds__(THREADS) grad_pass_bf16_kernel(BwdParams p) {
     const float *yim = (const float *)p.dy.im + b * p.dy.s0 + h * p.dy.s1;
     const bool need_ds0 = p.ds0_re != nullptr;
 
-    floatx4 gR[2], gI[2];  // dS[i][j], rows i0 + 16it + 4g + r, cols 16(2jh + jj) + l16
+    floatx4 gR[4], gI[4];  // dS[i][j], rows 16it + 4g + r, cols 16jt + l16
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-        gR[jj] = gI[jj] = zero4();
+    for (int jt = 0; jt < 4; ++jt) {
+        gR[jt] = gI[jt] = zero4();
         if (p.ds_re) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(i0 + 16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                gR[jj][r] = p.ds_re[o];
-                gI[jj][r] = p.ds_im[o];
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
+                gR[jt][r] = p.ds_re[o];
+                gI[jt][r] = p.ds_im[o];
             }
         }
     }
 
     struct ChunkRegs {
         B16Regs qr, qi;
-        F32Half yr, yi;
         float gam, rr, ri;
     };
     ChunkRegs cr[2];
+    F32Regs yr, yi;  // dY of the next chunk (one set: fp32 tiles are twice the size)
+    auto load_dy = [&](int c) {
+        const int c0 = c * 64, valid = min(64, a.T - c0);
+        const int64_t yo = (int64_t)c0 * p.dy.s2;
+        regs_load_f32<false>(yr, yre + yo, p.dy.s2, valid);
+        regs_load_f32<false>(yi, yim + yo, p.dy.s2, valid);
+    };
     auto load_chunk = [&](int c, ChunkRegs &x) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
-        const int64_t qo = (int64_t)c0 * a.q.s2, yo = (int64_t)c0 * p.dy.s2;
+        const int64_t qo = (int64_t)c0 * a.q.s2;
         regs_load_bf<false>(x.qr, qre + qo, a.q.s2, valid);
         regs_load_bf<false>(x.qi, qim + qo, a.q.s2, valid);
-        x.yr = half_tile_load_f32(yre + yo, p.dy.s2, i0, valid);
-        x.yi = half_tile_load_f32(yim + yo, p.dy.s2, i0, valid);
         const bool lv = w == 0 && lane < valid;
         x.gam = lv ? gbase[(int64_t)(c0 + lane) * a.sg_t] : 1.f;
         x.rr = (lv && rbr) ? rbr[(int64_t)(c0 + lane) * a.sr_t] : 1.f;
@@ -906,8 +908,8 @@ __global__ void __launch_bounds__(THREADS) grad_pass_bf16_kernel(BwdParams p) {
     auto stage_chunk = [&](int c, int buf, const ChunkRegs &x) {
         regs_store_bf<false>(sQ + (buf * 2) * PLANE_B, x.qr);
         regs_store_bf<false>(sQ + (buf * 2 + 1) * PLANE_B, x.qi);
-        half_tile_store_f32_as_bf(sG + (buf * 2) * 64 * PBH, x.yr);
-        half_tile_store_f32_as_bf(sG + (buf * 2 + 1) * 64 * PBH, x.yi);
+        regs_store_f32_as_bf<false>(sG + (buf * 2) * PLANE_B, yr);
+        regs_store_f32_as_bf<false>(sG + (buf * 2 + 1) * PLANE_B, yi);
         if (w == 0) {  // conj(rho[t]) q_scale = conj(r[t]) cum[t] q_scale
             const int valid = min(64, a.T - c * 64);
             float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
@@ -921,44 +923,29 @@ __global__ void __launch_bounds__(THREADS) grad_pass_bf16_kernel(BwdParams p) {
             sW[buf * 128 + 64 + lane] = -x.ri * cum;
         }
     };
-    auto store_snapshot = [&](int c, int buf) {
-        U16 *dst = gsnap(p, m, b, h, c);
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int idx = tid + q * THREADS;
-            const int pl = idx >> 8, r = (idx >> 3) & 31, c8 = idx & 7;
-            const uint4 v = *reinterpret_cast<const uint4 *>(sS + (buf * 2 + pl) * PASS_ROWS * PB + r * PB + 8 * c8);
-            *reinterpret_cast<uint4 *>(dst + pl * D * D + (int64_t)(i0 + r) * D + 8 * c8) = v;
-        }
-    };
 
     // reverse order: step k handles chunk c = n-1-k with LDS buffer k & 1
     auto step = [&](int k, ChunkRegs &mine, ChunkRegs &next) {
         const int c = n - 1 - k, buf = k & 1;
         if (k + 2 < n) load_chunk(c - 2, mine);
-        if (k > 0) store_snapshot(c + 1, buf ^ 1);
-        // snapshot of dS after chunk c
-        U16 *snr = sS + (buf * 2) * PASS_ROWS * PB, *sni = sS + (buf * 2 + 1) * PASS_ROWS * PB;
+        if (k + 1 < n) load_dy(c - 1);
+        {  // bf16 snapshot of dS after chunk c
+            U16 *dst = gsnap(p, m, b, h, c);
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = 16 * it + 4 * g + r, col = 16 * (2 * jh + jj) + l16;
-                snr[row * PB + col] = f32_to_bf16(gR[jj][r]);
-                sni[row * PB + col] = f32_to_bf16(gI[jj][r]);
-            }
+            for (int jt = 0; jt < 4; ++jt) acc_store_bf_pairs(dst, dst + D * D, gR[jt], gI[jt], 16 * it, 16 * jt);
+        }
         if (c > 0 || need_ds0) {
             // dG rows (value i) x cols (key j): A = (conj(rho) q_scale dY)^T, B = Q (k = t)
-            floatx4 accR[2], accI[2];
+            floatx4 accR[4], accI[4];
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
+            for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
             const U16 *Qr = sQ + (buf * 2) * PLANE_B, *Qi = sQ + (buf * 2 + 1) * PLANE_B;
-            const U16 *Gr = sG + (buf * 2) * 64 * PBH, *Gi = sG + (buf * 2 + 1) * 64 * PBH;
+            const U16 *Gr = sG + (buf * 2) * PLANE_B, *Gi = sG + (buf * 2 + 1) * PLANE_B;
             const float *wre = sW + buf * 128, *wim = wre + 64;
 #pragma unroll
             for (int kp = 0; kp < 2; ++kp) {
                 const int t0 = 32 * kp + 8 * g;
-                const floatx8 gr = to_f(ld_tr(Gr, t0, t0 + 4, 16 * it, PBH)), gi = to_f(ld_tr(Gi, t0, t0 + 4, 16 * it, PBH));
+                const floatx8 gr = to_f(ld_tr(Gr, t0, t0 + 4, 16 * it)), gi = to_f(ld_tr(Gi, t0, t0 + 4, 16 * it));
                 floatx8 vr, vi;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -968,28 +955,28 @@ __global__ void __launch_bounds__(THREADS) grad_pass_bf16_kernel(BwdParams p) {
                 }
                 const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
 #pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    const int jt = 2 * jh + jj;
+                for (int jt = 0; jt < 4; ++jt) {
                     const bf16x8 qr = ld_tr(Qr, t0, t0 + 4, 16 * jt), qi = ld_tr(Qi, t0, t0 + 4, 16 * jt);
-                    accR[jj] = mfma_bf(ar, qr, accR[jj]);
-                    accR[jj] = mfma_bf(ai, qi, accR[jj]);
-                    accI[jj] = mfma_bf(ai, qr, accI[jj]);
-                    accI[jj] = mfma_bf(nar, qi, accI[jj]);
+                    accR[jt] = mfma_bf(ar, qr, accR[jt]);
+                    accR[jt] = mfma_bf(ai, qi, accR[jt]);
+                    accI[jt] = mfma_bf(ai, qr, accI[jt]);
+                    accI[jt] = mfma_bf(nar, qi, accI[jt]);
                 }
             }
             const float tot = ftotal(p, m, b, h, c);
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
+            for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    gR[jj][r] = tot * gR[jj][r] + accR[jj][r];
-                    gI[jj][r] = tot * gI[jj][r] + accI[jj][r];
+                    gR[jt][r] = tot * gR[jt][r] + accR[jt][r];
+                    gI[jt][r] = tot * gI[jt][r] + accI[jt][r];
                 }
         }
         if (k + 1 < n) stage_chunk(c - 1, buf ^ 1, next);
         __syncthreads();
     };
     load_chunk(n - 1, cr[0]);
+    load_dy(n - 1);
     if (n > 1) load_chunk(n - 2, cr[1]);
     stage_chunk(n - 1, 0, cr[0]);
     __syncthreads();
@@ -997,93 +984,14 @@ __global__ void __launch_bounds__(THREADS) grad_pass_bf16_kernel(BwdParams p) {
         step(k, cr[0], cr[1]);
         if (k + 1 < n) step(k + 1, cr[1], cr[0]);
     }
-    store_snapshot(0, (n - 1) & 1);
     if (need_ds0) {
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(i0 + 16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                p.ds0_re[o] = gR[jj][r];
-                p.ds0_im[o] = gI[jj][r];
-            }
-    }
-}
-
-__global__ void __launch_bounds__(THREADS) grad_chunk_state_bf16_kernel(BwdParams p) {
-    extern __shared__ float smem[];
-    U16 *sGr = reinterpret_cast<U16 *>(smem), *sGi = sGr + PLANE_B;
-    U16 *sQr = sGi + PLANE_B, *sQi = sQr + PLANE_B;
-    float *sL = reinterpret_cast<float *>(sQi + PLANE_B), *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
-    float *sWr = sRi + MAX_M * 64, *sWi = sWr + MAX_M * 64;  // conj(rho) q_scale per step
-
-    const qpam_scan_args &a = p.a;
-    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int c0 = c * 64, valid = min(64, a.T - c0);
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    if (c == 0 && a.s0_re == nullptr) {
-        for (int m = 0; m < a.M; ++m) {
-            float *dst = gstate(p, m, b, h, 0);
-            for (int e = tid; e < 2 * D * D / 4; e += THREADS)
-                reinterpret_cast<float4 *>(dst)[e] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        return;
-    }
-    const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-    const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
-    {
-        U16 *const bd[2] = {sQr, sQi};
-        const U16 *const bs[2] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo};
-        const int64_t bst[2] = {a.q.s2, a.q.s2};
-        U16 *const fd[2] = {sGr, sGi};
-        const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
-        const int64_t fst[2] = {p.dy.s2, p.dy.s2};
-        stage_mixed<2, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
-    }
-    if (w == 0) {
-        chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
-        for (int m = 0; m < a.M; ++m) {
-            const float cum = (lane < valid) ? __expf(sL[m * 64 + lane]) * a.q_scale : 0.f;
-            sWr[m * 64 + lane] = sRr[m * 64 + lane] * cum;
-            sWi[m * 64 + lane] = -sRi[m * 64 + lane] * cum;
-        }
-    }
-    __syncthreads();
-
-    const int i0 = 16 * w;  // this wave's value rows i0 + l16
-    for (int m = 0; m < a.M; ++m) {
-        floatx4 accR[4], accI[4];
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
-#pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-            const int t0 = 32 * kp + 8 * g;
-            const floatx8 gr = to_f(ld_tr(sGr, t0, t0 + 4, i0)), gi = to_f(ld_tr(sGi, t0, t0 + 4, i0));
-            floatx8 vr, vi;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float wr = sWr[m * 64 + t0 + e], wi = sWi[m * 64 + t0 + e];
-                vr[e] = wr * gr[e] - wi * gi[e];
-                vi[e] = wr * gi[e] + wi * gr[e];
-            }
-            const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                const bf16x8 qr = ld_tr(sQr, t0, t0 + 4, 16 * jt), qi = ld_tr(sQi, t0, t0 + 4, 16 * jt);
-                accR[jt] = mfma_bf(ar, qr, accR[jt]);
-                accR[jt] = mfma_bf(ai, qi, accR[jt]);
-                accI[jt] = mfma_bf(ai, qr, accI[jt]);
-                accI[jt] = mfma_bf(nar, qi, accI[jt]);
-            }
-        }
-        float *dst = gstate(p, m, b, h, c);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int ii = 16 * w + 4 * g + r, j = 16 * jt + l16;
-                dst[ii * D + j] = accR[jt][r];
-                dst[D * D + ii * D + j] = accI[jt][r];
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
+                p.ds0_re[o] = gR[jt][r];
+                p.ds0_im[o] = gI[jt][r];
             }
     }
 }
@@ -1706,7 +1614,6 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
     }
 }
 
-constexpr size_t gcs_bf16_smem() { return (size_t)4 * PLANE_B * 2 + 5 * MAX_M * 64 * sizeof(float); }
 // query/key side: 8 bf16 planes + per-step vectors < 80 KiB, so two blocks share a CU's 160 KiB LDS
 template <int M>
 constexpr size_t qside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (7 * M * 64 + 4) * sizeof(float); }
@@ -1725,7 +1632,7 @@ int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
-    hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(a.M * a.B * a.H * PASS_SPLIT), dim3(THREADS), s1, stream, p);
+    hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(THREADS), s1, stream, p);
     int st = launch_status("grad_pass_bf16_kernel");
     if (st) return st;
     hipLaunchKernelGGL(query_side_bf16_kernel<M>, grid, dim3(THREADS), s3, stream, p);
@@ -1778,10 +1685,18 @@ int launch_bwd(const BwdParams &p, hipStream_t stream) {
 
 // fp32 increments/gradient states, the partial log-decay gradient, then (bf16
 // path) the bf16 gradient-state snapshots at a 256-byte aligned offset.
+// Workspace: fp32 per-chunk gradient states (fp32 path only), the fp32 per-token
+// log-decay gradients, then at a 256-byte aligned offset the bf16 gradient-state
+// snapshots (snapshot path only).
+int64_t bwd_gl_offset(const qpam_scan_args &a) {  // in floats
+    const int64_t n = (a.T + a.C - 1) / a.C;
+    return uses_snapshots(a) ? 0 : (int64_t)a.M * a.B * a.H * n * 2 * D * D;
+}
+
 size_t bwd_snapshot_offset(const qpam_scan_args &a) {
     const int64_t n = (a.T + a.C - 1) / a.C;
     const int64_t chains = (int64_t)a.M * a.B * a.H;
-    return ((size_t)(chains * n * 2 * D * D + chains * n * a.C) * sizeof(float) + 255) & ~(size_t)255;
+    return ((size_t)(bwd_gl_offset(a) + chains * n * a.C) * sizeof(float) + 255) & ~(size_t)255;
 }
 
 size_t bwd_workspace_bytes(const qpam_scan_args &a) {
@@ -1828,11 +1743,10 @@ int scan_bwd(const qpam_scan_bwd_args *bw, hipStream_t stream) {
     p.ds0_re = bw->ds0_re;
     p.ds0_im = bw->ds0_im;
     p.n_chunks = (a->T + a->C - 1) / a->C;
-    const int64_t chains = (int64_t)a->M * a->B * a->H;
-    p.states = (const float *)a->workspace;
-    p.totals = p.states + chains * p.n_chunks * 2 * D * D;
-    p.gstates = (float *)bw->workspace;
-    p.gl = p.gstates + chains * p.n_chunks * 2 * D * D;
+    p.states = uses_snapshots(*a) ? nullptr : (const float *)a->workspace;
+    p.totals = (const float *)a->workspace + fwd_totals_offset(*a);
+    p.gstates = uses_snapshots(*a) ? nullptr : (float *)bw->workspace;
+    p.gl = (float *)bw->workspace + bwd_gl_offset(*a);
     p.snap = nullptr;
     p.gsnap = nullptr;
     const bool bf = a->dtype == QPAM_BF16;

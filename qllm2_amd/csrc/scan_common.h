@@ -209,40 +209,26 @@ __device__ __forceinline__ bf16x8 ld_tr(const unsigned short *tile, int r0, int 
     return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// State passes (one block per state and half of its value rows walks the chunks).
-constexpr int PASS_ROWS = 32;  // value rows per block
-constexpr int PASS_SPLIT = D / PASS_ROWS;
-constexpr int PBH = 40;        // LDS pitch (bf16) of 32-column tiles
-
-// [64 rows x 32 cols] bf16 sub-tile (columns col0..col0+31): one 16-byte load per thread
-__device__ __forceinline__ uint4 half_tile_load(const unsigned short *src, int64_t st, int col0, int valid) {
-    const int r = threadIdx.x >> 2, c8 = threadIdx.x & 3;
-    return (r < valid) ? *reinterpret_cast<const uint4 *>(src + (int64_t)r * st + col0 + 8 * c8)
-                       : make_uint4(0, 0, 0, 0);
-}
-__device__ __forceinline__ void half_tile_store(unsigned short *lds, uint4 v) {
-    const int r = threadIdx.x >> 2, c8 = threadIdx.x & 3;
-    *reinterpret_cast<uint4 *>(lds + r * PBH + 8 * c8) = v;
-}
-// the same sub-tile of an fp32 source, kept as two float4 per thread
-struct F32Half {
-    float4 lo, hi;
-};
-__device__ __forceinline__ F32Half half_tile_load_f32(const float *src, int64_t st, int col0, int valid) {
-    const int r = threadIdx.x >> 2, c8 = threadIdx.x & 3;
-    F32Half x{make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
-    if (r < valid) {
-        const float *q = src + (int64_t)r * st + col0 + 8 * c8;
-        x.lo = *reinterpret_cast<const float4 *>(q);
-        x.hi = *reinterpret_cast<const float4 *>(q + 4);
+// One 16x16 accumulator tile of a complex matrix (element (4g + r, l16) of lane
+// 16g + l16) -> rows row0.., columns col0.. of two bf16 planes with row pitch D.
+// Adjacent lanes swap one row pair element (DPP quad_perm [1,0,3,2]) so that
+// each lane writes two consecutive columns of one row: a 4-byte store per plane
+// instead of two 2-byte stores.
+__device__ __forceinline__ void acc_store_bf_pairs(unsigned short *dre, unsigned short *dim, const floatx4 &re,
+                                                   const floatx4 &im, int row0, int col0) {
+    const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+    const bool odd = l16 & 1;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const unsigned p0 = f32_to_bf16(re[2 * q]) | ((unsigned)f32_to_bf16(im[2 * q]) << 16);
+        const unsigned p1 = f32_to_bf16(re[2 * q + 1]) | ((unsigned)f32_to_bf16(im[2 * q + 1]) << 16);
+        const unsigned keep = odd ? p1 : p0, send = odd ? p0 : p1;
+        const unsigned recv = (unsigned)__builtin_amdgcn_update_dpp(0, (int)send, 0xB1, 0xF, 0xF, false);
+        const unsigned lo = odd ? recv : keep, hi = odd ? keep : recv;  // columns (l16 & ~1) and +1
+        const int row = row0 + 4 * g + 2 * q + (odd ? 1 : 0), col = col0 + (l16 & ~1);
+        *reinterpret_cast<unsigned *>(dre + row * D + col) = (lo & 0xFFFFu) | (hi << 16);
+        *reinterpret_cast<unsigned *>(dim + row * D + col) = (lo >> 16) | (hi & 0xFFFF0000u);
     }
-    return x;
-}
-__device__ __forceinline__ void half_tile_store_f32_as_bf(unsigned short *lds, const F32Half &x) {
-    const int r = threadIdx.x >> 2, c8 = threadIdx.x & 3;
-    const ushortx8 u = {f32_to_bf16(x.lo.x), f32_to_bf16(x.lo.y), f32_to_bf16(x.lo.z), f32_to_bf16(x.lo.w),
-                        f32_to_bf16(x.hi.x), f32_to_bf16(x.hi.y), f32_to_bf16(x.hi.z), f32_to_bf16(x.hi.w)};
-    *reinterpret_cast<ushortx8 *>(lds + r * PBH + 8 * c8) = u;
 }
 
 // Register-staged bf16 / fp32 -> bf16 tile copies (all loads of a batch are

@@ -567,53 +567,50 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
 // while chunk c is processed (double-buffered LDS, one barrier per chunk); the
 // snapshot of chunk c is staged in LDS and stored during chunk c+1.
 constexpr size_t pass_bf16_smem() {
-    return (size_t)2 * 2 * PLANE_B * 2     // K [buf][plane][64][PB]
-           + (size_t)2 * 2 * 64 * PBH * 2  // V columns of this half [buf][plane][64][PBH]
-           + (size_t)2 * 2 * PASS_ROWS * PB * 2  // snapshot staging [buf][plane][32][PB]
-           + (size_t)2 * 68 * sizeof(float);     // dl[64] + total per buffer
+    return (size_t)2 * 2 * PLANE_B * 2    // K [buf][plane][64][PB]
+           + (size_t)2 * 2 * PLANE_B * 2  // V [buf][plane][64][PB]
+           + (size_t)2 * 68 * sizeof(float);  // dl[64] + total per buffer
 }
 
 __global__ void __launch_bounds__(THREADS) state_pass_bf16_kernel(FwdParams p) {
     extern __shared__ float smem[];
     using U = unsigned short;
-    U *sK = reinterpret_cast<U *>(smem);         // + (buf * 2 + plane) * PLANE_B
-    U *sV = sK + 4 * PLANE_B;                    // + (buf * 2 + plane) * 64 * PBH
-    U *sS = sV + 4 * 64 * PBH;                   // + (buf * 2 + plane) * PASS_ROWS * PB
-    float *sDl = reinterpret_cast<float *>(sS + 4 * PASS_ROWS * PB);  // + buf * 68; [64] = total
+    U *sK = reinterpret_cast<U *>(smem);  // + (buf * 2 + plane) * PLANE_B
+    U *sV = sK + 4 * PLANE_B;             // + (buf * 2 + plane) * PLANE_B
+    float *sDl = reinterpret_cast<float *>(sV + 4 * PLANE_B);  // + buf * 68; [64] = total
 
     const qpam_scan_args &a = p.a;
-    const int part = blockIdx.x % PASS_SPLIT, chain = blockIdx.x / PASS_SPLIT;
+    const int chain = blockIdx.x;
     const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
-    const int i0 = part * PASS_ROWS;  // first value row of this block
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int it = w >> 1, jh = w & 1;  // wave: rows 16it.. of the half, key-column tiles 2jh, 2jh+1
+    const int it = w;  // wave: value rows 16it.., all four key-column tiles
     const int n = p.n_chunks;
     const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
     const U *kre = (const U *)a.k.re + b * a.k.s0 + h * a.k.s1, *kim = (const U *)a.k.im + b * a.k.s0 + h * a.k.s1;
     const U *vre = (const U *)a.v.re + b * a.v.s0 + h * a.v.s1, *vim = (const U *)a.v.im + b * a.v.s0 + h * a.v.s1;
+    U *snap0 = chunk_snap_ptr(p, m, b, h, 0);
 
-    // running state S[i][j] for rows i0 + 16it + 4g + r, cols 16(2jh + jj) + l16
-    floatx4 sR[2], sI[2];
+    // running state S[i][j] for rows 16it + 4g + r, cols 16jt + l16
+    floatx4 sR[4], sI[4];
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-        sR[jj] = sI[jj] = zero4();
+    for (int jt = 0; jt < 4; ++jt) {
+        sR[jt] = sI[jt] = zero4();
         if (a.s0_re) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(i0 + 16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                sR[jj][r] = a.s0_re[o];
-                sI[jj][r] = a.s0_im[o];
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
+                sR[jt][r] = a.s0_re[o];
+                sI[jt][r] = a.s0_im[o];
             }
         }
     }
 
-    // chunk inputs in registers, two register sets (chunk c in set c & 1): K (2 planes x
-    // 2 uint4), V half (2 planes x 1 uint4), gamma (wave 0).  Sets are selected by
-    // compile-time index only (the chunk loop is unrolled by two).
+    // chunk inputs in registers, two register sets (chunk c in set c & 1): K and V
+    // (2 planes x 2 uint4 each), gamma (wave 0).  Sets are selected by compile-time
+    // index only (the chunk loop is unrolled by two).
     struct ChunkRegs {
-        B16Regs kr, ki;
-        uint4 vr, vi;
+        B16Regs kr, ki, vr, vi;
         float gam;
     };
     ChunkRegs cr[2];
@@ -622,16 +619,16 @@ __global__ void __launch_bounds__(THREADS) state_pass_bf16_kernel(FwdParams p) {
         const int64_t ko = (int64_t)c0 * a.k.s2, vo = (int64_t)c0 * a.v.s2;
         regs_load_bf<false>(x.kr, kre + ko, a.k.s2, valid);
         regs_load_bf<false>(x.ki, kim + ko, a.k.s2, valid);
-        x.vr = half_tile_load(vre + vo, a.v.s2, i0, valid);
-        x.vi = half_tile_load(vim + vo, a.v.s2, i0, valid);
+        regs_load_bf<false>(x.vr, vre + vo, a.v.s2, valid);
+        regs_load_bf<false>(x.vi, vim + vo, a.v.s2, valid);
         x.gam = (w == 0 && lane < valid) ? gbase[(int64_t)(c0 + lane) * a.sg_t] : 1.f;
     };
     // registers -> LDS buffer `buf`; wave 0 turns gamma into dl and the chunk total
     auto stage_chunk = [&](int c, int buf, const ChunkRegs &x) {
         regs_store_bf<false>(sK + (buf * 2) * PLANE_B, x.kr);
         regs_store_bf<false>(sK + (buf * 2 + 1) * PLANE_B, x.ki);
-        half_tile_store(sV + (buf * 2) * 64 * PBH, x.vr);
-        half_tile_store(sV + (buf * 2 + 1) * 64 * PBH, x.vi);
+        regs_store_bf<false>(sV + (buf * 2) * PLANE_B, x.vr);
+        regs_store_bf<false>(sV + (buf * 2 + 1) * PLANE_B, x.vi);
         if (w == 0) {
             const int valid = min(64, a.T - c * 64);
             float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
@@ -645,19 +642,8 @@ __global__ void __launch_bounds__(THREADS) state_pass_bf16_kernel(FwdParams p) {
             if (lane == 0) {
                 const float tot = __expf(Llast);
                 sDl[buf * 68 + 64] = tot;
-                if (part == 0) *chunk_total_ptr(p, m, b, h, c) = tot;
+                *chunk_total_ptr(p, m, b, h, c) = tot;
             }
-        }
-    };
-    // LDS snapshot staging `buf` -> chunk c's bf16 snapshot rows i0.. (two 16-byte stores per thread)
-    auto store_snapshot = [&](int c, int buf) {
-        U *dst = chunk_snap_ptr(p, m, b, h, c);
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int idx = tid + q * THREADS;  // 0..511: plane, row, 16-byte chunk
-            const int pl = idx >> 8, r = (idx >> 3) & 31, c8 = idx & 7;
-            const uint4 v = *reinterpret_cast<const uint4 *>(sS + (buf * 2 + pl) * PASS_ROWS * PB + r * PB + 8 * c8);
-            *reinterpret_cast<uint4 *>(dst + pl * D * D + (int64_t)(i0 + r) * D + 8 * c8) = v;
         }
     };
 
@@ -666,18 +652,23 @@ __global__ void __launch_bounds__(THREADS) state_pass_bf16_kernel(FwdParams p) {
     auto step = [&](int c, ChunkRegs &mine, ChunkRegs &next) {
         const int buf = c & 1;
         if (c + 2 < n) load_chunk(c + 2, mine);
-        if (c > 0) store_snapshot(c - 1, buf ^ 1);
-        // dS rows (value i) x cols (key j): A = dl-scaled V^T (transposed reads of the V half), B = K
-        floatx4 accR[2], accI[2];
+        // bf16 snapshot of the entering state (rows 16it.. of chunk c's snapshot)
+        {
+            U *dst = snap0 + (int64_t)c * 2 * D * D;
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
+            for (int jt = 0; jt < 4; ++jt) acc_store_bf_pairs(dst, dst + D * D, sR[jt], sI[jt], 16 * it, 16 * jt);
+        }
+        // dS rows (value i) x cols (key j): A = dl-scaled V^T (transposed reads of V), B = K
+        floatx4 accR[4], accI[4];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
         const U *Kr = sK + (buf * 2) * PLANE_B, *Ki = sK + (buf * 2 + 1) * PLANE_B;
-        const U *Vr = sV + (buf * 2) * 64 * PBH, *Vi = sV + (buf * 2 + 1) * 64 * PBH;
+        const U *Vr = sV + (buf * 2) * PLANE_B, *Vi = sV + (buf * 2 + 1) * PLANE_B;
         const float *dl = sDl + buf * 68;
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             const int s0 = 32 * kp + 8 * g;
-            floatx8 vr = to_f(ld_tr(Vr, s0, s0 + 4, 16 * it, PBH)), vi = to_f(ld_tr(Vi, s0, s0 + 4, 16 * it, PBH));
+            floatx8 vr = to_f(ld_tr(Vr, s0, s0 + 4, 16 * it)), vi = to_f(ld_tr(Vi, s0, s0 + 4, 16 * it));
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 vr[e] *= dl[s0 + e];
@@ -685,27 +676,22 @@ __global__ void __launch_bounds__(THREADS) state_pass_bf16_kernel(FwdParams p) {
             }
             const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const int jt = 2 * jh + jj;
+            for (int jt = 0; jt < 4; ++jt) {
                 const bf16x8 kr = ld_tr(Kr, s0, s0 + 4, 16 * jt), ki = ld_tr(Ki, s0, s0 + 4, 16 * jt);
-                accR[jj] = mfma_bf(ar, kr, accR[jj]);
-                accR[jj] = mfma_bf(ai, ki, accR[jj]);
-                accI[jj] = mfma_bf(ai, kr, accI[jj]);
-                accI[jj] = mfma_bf(nar, ki, accI[jj]);
+                accR[jt] = mfma_bf(ar, kr, accR[jt]);
+                accR[jt] = mfma_bf(ai, ki, accR[jt]);
+                accI[jt] = mfma_bf(ai, kr, accI[jt]);
+                accI[jt] = mfma_bf(nar, ki, accI[jt]);
             }
         }
-        // snapshot of the entering state, then S <- total S + dS
+        // S <- total S + dS
         const float tot = dl[64];
-        U *snr = sS + (buf * 2) * PASS_ROWS * PB, *sni = sS + (buf * 2 + 1) * PASS_ROWS * PB;
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
+        for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = 16 * it + 4 * g + r, col = 16 * (2 * jh + jj) + l16;
-                snr[row * PB + col] = f32_to_bf16(sR[jj][r]);
-                sni[row * PB + col] = f32_to_bf16(sI[jj][r]);
-                sR[jj][r] = tot * sR[jj][r] + accR[jj][r];
-                sI[jj][r] = tot * sI[jj][r] + accI[jj][r];
+                sR[jt][r] = tot * sR[jt][r] + accR[jt][r];
+                sI[jt][r] = tot * sI[jt][r] + accI[jt][r];
             }
         if (c + 1 < n) stage_chunk(c + 1, buf ^ 1, next);
         __syncthreads();
@@ -718,85 +704,14 @@ __global__ void __launch_bounds__(THREADS) state_pass_bf16_kernel(FwdParams p) {
         step(c, cr[0], cr[1]);
         if (c + 1 < n) step(c + 1, cr[1], cr[0]);
     }
-    store_snapshot(n - 1, (n - 1) & 1);
     if (a.s_re) {
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(i0 + 16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                a.s_re[o] = sR[jj][r];
-                a.s_im[o] = sI[jj][r];
-            }
-    }
-}
-
-__global__ void __launch_bounds__(THREADS) chunk_state_bf16_kernel(FwdParams p) {
-    extern __shared__ float smem[];
-    unsigned short *sKr = reinterpret_cast<unsigned short *>(smem), *sKi = sKr + PLANE_B;
-    unsigned short *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
-    float *sDl = reinterpret_cast<float *>(sVi + PLANE_B);  // [MAX_M][64]
-
-    const qpam_scan_args &a = p.a;
-    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int c0 = c * 64;
-    const int valid = min(64, a.T - c0);
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    using U = unsigned short;
-    const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
-    const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-    {
-        U *const dst[4] = {sKr, sKi, sVr, sVi};
-        const U *const src[4] = {(const U *)a.k.re + ko, (const U *)a.k.im + ko, (const U *)a.v.re + vo,
-                                 (const U *)a.v.im + vo};
-        const int64_t st[4] = {a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        stage_bf<4, 0x0u>(dst, src, st, valid);
-    }
-    if (w == 0) {
-        for (int m = 0; m < a.M; ++m) {
-            const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
-            const float L = chunk_log_prefix(gp, a.sg_t, valid, lane);
-            const float Llast = __shfl(L, valid - 1);
-            sDl[m * 64 + lane] = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
-            if (lane == 0) *chunk_total_ptr(p, m, b, h, c) = __expf(Llast);
-        }
-    }
-    __syncthreads();
-
-    const int i0 = 16 * w;  // this wave's A-operand rows (value index i0 + l16)
-    for (int m = 0; m < a.M; ++m) {
-        floatx4 accR[4], accI[4];
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
-#pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-            const int s0 = 32 * kp + 8 * g;
-            floatx8 vr = to_f(ld_tr(sVr, s0, s0 + 4, i0)), vi = to_f(ld_tr(sVi, s0, s0 + 4, i0));
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float dl = sDl[m * 64 + s0 + e];
-                vr[e] *= dl;
-                vi[e] *= dl;
-            }
-            const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                const bf16x8 kr = ld_tr(sKr, s0, s0 + 4, 16 * jt);
-                const bf16x8 ki = ld_tr(sKi, s0, s0 + 4, 16 * jt);
-                accR[jt] = mfma_bf(ar, kr, accR[jt]);
-                accR[jt] = mfma_bf(ai, ki, accR[jt]);
-                accI[jt] = mfma_bf(ai, kr, accI[jt]);
-                accI[jt] = mfma_bf(nar, ki, accI[jt]);
-            }
-        }
-        float *dst = chunk_state_ptr(p, m, b, h, c);
 #pragma unroll
         for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int ii = 16 * w + 4 * g + r, j = 16 * jt + l16;
-                dst[ii * D + j] = accR[jt][r];
-                dst[D * D + ii * D + j] = accI[jt][r];
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
+                a.s_re[o] = sR[jt][r];
+                a.s_im[o] = sI[jt][r];
             }
     }
 }
@@ -1008,7 +923,6 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
         }
 }
 
-constexpr size_t state_bf16_smem() { return (size_t)4 * PLANE_B * 2 + MAX_M * 64 * sizeof(float); }
 template <int M>
 constexpr size_t output_bf16_smem() { return (size_t)6 * PLANE_B * 2 + (4 * M * 64 + 4) * sizeof(float); }
 
@@ -1021,7 +935,7 @@ int launch_fwd_bf16_m(const FwdParams &p, hipStream_t stream) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
-    hipLaunchKernelGGL(state_pass_bf16_kernel, dim3(a.M * a.B * a.H * PASS_SPLIT), dim3(THREADS), s1, stream, p);
+    hipLaunchKernelGGL(state_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(THREADS), s1, stream, p);
     int st = launch_status("state_pass_bf16_kernel");
     if (st) return st;
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));
@@ -1080,10 +994,17 @@ bool uses_snapshots(const qpam_scan_args &a) { return a.dtype == QPAM_BF16 && a.
 
 // fp32 increments/states, chunk totals, then (bf16 path) the bf16 snapshots at a
 // 256-byte aligned offset.
+// Workspace: fp32 per-chunk states (fp32 path only), fp32 chunk totals, then at a
+// 256-byte aligned offset the bf16 entering-state snapshots (snapshot path only).
+int64_t fwd_totals_offset(const qpam_scan_args &a) {  // in floats
+    const int64_t n = (a.T + a.C - 1) / a.C;
+    return uses_snapshots(a) ? 0 : (int64_t)a.M * a.B * a.H * n * 2 * D * D;
+}
+
 size_t fwd_snapshot_offset(const qpam_scan_args &a) {
     const int64_t n = (a.T + a.C - 1) / a.C;
     const int64_t chains = (int64_t)a.M * a.B * a.H;
-    return ((size_t)(chains * n * 2 * D * D + chains * n) * sizeof(float) + 255) & ~(size_t)255;
+    return ((size_t)(fwd_totals_offset(a) + chains * n) * sizeof(float) + 255) & ~(size_t)255;
 }
 
 size_t fwd_workspace_bytes(const qpam_scan_args &a) {
@@ -1131,9 +1052,8 @@ int scan_fwd(const qpam_scan_args *a, hipStream_t stream) {
     FwdParams p;
     p.a = *a;
     p.n_chunks = (a->T + a->C - 1) / a->C;
-    const int64_t chains = (int64_t)a->M * a->B * a->H;
-    p.states = (float *)a->workspace;
-    p.totals = p.states + chains * p.n_chunks * 2 * D * D;
+    p.states = uses_snapshots(*a) ? nullptr : (float *)a->workspace;
+    p.totals = (float *)a->workspace + fwd_totals_offset(*a);
     p.snap = uses_snapshots(*a)
                  ? reinterpret_cast<unsigned short *>((char *)a->workspace + fwd_snapshot_offset(*a))
                  : nullptr;

@@ -835,31 +835,35 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
 // unscaled; q_scale is applied where q~ enters an fp32 result.
 using U16 = unsigned short;
 
-// Gradient-state pass (reverse): one block per (state m, b, h) walks the chunks
-// from last to first with the running dS in registers (fp32, accumulator layout;
-// wave w owns value rows 16w..16w+15).  Per chunk: bf16 snapshot of dS after the
+// Gradient-state pass (reverse): one block of PASS_THREADS (8 waves) per (state m,
+// b, h) walks the chunks from last to first with the running dS in registers
+// (fp32, accumulator layout; wave w owns value rows 16(w & 3).. and key-column
+// tiles 2(w >> 2), 2(w >> 2) + 1).  Per chunk: bf16 snapshot of dS after the
 // chunk, then dS <- total dS + sum_t conj(rho_m[t]) q_scale dY_t (x) conj(q_t) on
 // MFMA.  dS0 is written when requested.  Chunk c-2's Q and gamma / rotation and
-// chunk c-1's dY (fp32, rounded to bf16 when staged) are loaded while chunk c is
-// processed.
+// chunk c-1's dY (fp32; one register set) are loaded while chunk c is processed.
+// Every wave forms the chunk's weights conj(rho_m[t]) q_scale itself, and dY is
+// staged already weighted (fp32 product rounded once to bf16), so the MFMA
+// operands come straight from LDS.  Rows past the end of the sequence re-read its
+// last row: their weights are zero.
 constexpr size_t gpass_bf16_smem() {
-    return (size_t)2 * 2 * PLANE_B * 2         // Q [buf][plane][64][PB]
-           + (size_t)2 * 2 * PLANE_B * 2       // dY (bf16) [buf][plane][64][PB]
-           + (size_t)2 * 128 * sizeof(float);  // conj(rho) q_scale (re[64], im[64]) per buffer
+    return (size_t)2 * 2 * PLANE_B * 2     // Q [buf][plane][64][PB]
+           + (size_t)2 * 2 * PLANE_B * 2;  // weighted dY (bf16) [buf][plane][64][PB]
 }
 
-__global__ void __launch_bounds__(THREADS, 2) grad_pass_bf16_kernel(BwdParams p) {
+__global__ void __launch_bounds__(PASS_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
+grad_pass_bf16_kernel(BwdParams p) {
+    constexpr int NT = PASS_THREADS;
     extern __shared__ float smem[];
     U16 *sQ = reinterpret_cast<U16 *>(smem);  // + (buf * 2 + plane) * PLANE_B
     U16 *sG = sQ + 4 * PLANE_B;               // + (buf * 2 + plane) * PLANE_B
-    float *sW = reinterpret_cast<float *>(sG + 4 * PLANE_B);  // + buf * 128: re[64], im[64]
 
     const qpam_scan_args &a = p.a;
     const int chain = blockIdx.x;
     const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int it = w;
+    const int it = w & 3, jh = w >> 2;
     const int n = p.n_chunks;
     const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
     const float *rbr = a.rot_re ? a.rot_re + m * a.sr_m + b * a.sr_b + h * a.sr_h : nullptr;
@@ -868,130 +872,134 @@ __global__ void __launch_bounds__(THREADS, 2) grad_pass_bf16_kernel(BwdParams p)
     const float *yre = (const float *)p.dy.re + b * p.dy.s0 + h * p.dy.s1;
     const float *yim = (const float *)p.dy.im + b * p.dy.s0 + h * p.dy.s1;
     const bool need_ds0 = p.ds0_re != nullptr;
+    // rotations are read from gamma when absent (and replaced by 1 + 0i when staged)
+    const float *rsrc_r = rbr ? rbr : gbase, *rsrc_i = rbi ? rbi : gbase;
+    const int64_t rst_r = rbr ? a.sr_t : a.sg_t, rst_i = rbi ? a.sr_t : a.sg_t;
 
-    floatx4 gR[4], gI[4];  // dS[i][j], rows 16it + 4g + r, cols 16jt + l16
+    floatx4 gR[2], gI[2];  // dS[i][j], rows 16it + 4g + r, cols 16(2jh + jj) + l16
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        gR[jt] = gI[jt] = zero4();
+    for (int jj = 0; jj < 2; ++jj) {
+        gR[jj] = gI[jj] = zero4();
         if (p.ds_re) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
-                gR[jt][r] = p.ds_re[o];
-                gI[jt][r] = p.ds_im[o];
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                gR[jj][r] = p.ds_re[o];
+                gI[jj][r] = p.ds_im[o];
             }
         }
     }
 
     struct ChunkRegs {
-        B16Regs qr, qi;
+        BfTileRegs<NT> qr, qi;
         float gam, rr, ri;
     };
-    ChunkRegs cr[2];
-    F32Regs yr, yi;  // dY of the next chunk (one set: fp32 tiles are twice the size)
+    ChunkRegs cr0, cr1;
+    F32TileRegs<NT> yr, yi;  // dY of the next chunk (one set: fp32 tiles are twice the size)
     auto load_dy = [&](int c) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
         const int64_t yo = (int64_t)c0 * p.dy.s2;
-        regs_load_f32<false>(yr, yre + yo, p.dy.s2, valid);
-        regs_load_f32<false>(yi, yim + yo, p.dy.s2, valid);
+        tile_load_f32<NT>(yr, yre + yo, p.dy.s2, valid);
+        tile_load_f32<NT>(yi, yim + yo, p.dy.s2, valid);
     };
     auto load_chunk = [&](int c, ChunkRegs &x) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
         const int64_t qo = (int64_t)c0 * a.q.s2;
-        regs_load_bf<false>(x.qr, qre + qo, a.q.s2, valid);
-        regs_load_bf<false>(x.qi, qim + qo, a.q.s2, valid);
-        const bool lv = w == 0 && lane < valid;
-        x.gam = lv ? gbase[(int64_t)(c0 + lane) * a.sg_t] : 1.f;
-        x.rr = (lv && rbr) ? rbr[(int64_t)(c0 + lane) * a.sr_t] : 1.f;
-        x.ri = (lv && rbi) ? rbi[(int64_t)(c0 + lane) * a.sr_t] : 0.f;
+        tile_load_bf<NT>(x.qr, qre + qo, a.q.s2, valid);
+        tile_load_bf<NT>(x.qi, qim + qo, a.q.s2, valid);
+        const int64_t t = c0 + min(lane, valid - 1);
+        x.gam = gbase[t * a.sg_t];
+        x.rr = rsrc_r[t * rst_r];
+        x.ri = rsrc_i[t * rst_i];
     };
     auto stage_chunk = [&](int c, int buf, const ChunkRegs &x) {
-        regs_store_bf<false>(sQ + (buf * 2) * PLANE_B, x.qr);
-        regs_store_bf<false>(sQ + (buf * 2 + 1) * PLANE_B, x.qi);
-        regs_store_f32_as_bf<false>(sG + (buf * 2) * PLANE_B, yr);
-        regs_store_f32_as_bf<false>(sG + (buf * 2 + 1) * PLANE_B, yi);
-        if (w == 0) {  // conj(rho[t]) q_scale = conj(r[t]) cum[t] q_scale
-            const int valid = min(64, a.T - c * 64);
-            float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
+        // conj(rho[t]) q_scale = conj(r[t]) cum[t] q_scale, lane t
+        const int valid = min(64, a.T - c * 64);
+        float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_up(L, off);
-                if (lane >= off) L += y;
-            }
-            const float cum = (lane < valid) ? __expf(L) * a.q_scale : 0.f;
-            sW[buf * 128 + lane] = x.rr * cum;
-            sW[buf * 128 + 64 + lane] = -x.ri * cum;
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(L, off);
+            if (lane >= off) L += y;
         }
+        const float cum = (lane < valid) ? __expf(L) * a.q_scale : 0.f;
+        tile_store_bf<NT>(sQ + (buf * 2) * PLANE_B, x.qr);
+        tile_store_bf<NT>(sQ + (buf * 2 + 1) * PLANE_B, x.qi);
+        tile_store_f32_cmul_as_bf<NT>(sG + (buf * 2) * PLANE_B, sG + (buf * 2 + 1) * PLANE_B, yr, yi,
+                                      (rbr ? x.rr : 1.f) * cum, -(rbi ? x.ri : 0.f) * cum);
     };
 
-    // reverse order: step k handles chunk c = n-1-k with LDS buffer k & 1
+    // reverse order: step k handles chunk c = n-1-k with LDS buffer k & 1; chunk
+    // c - 2 is loaded into register set k & 1 and staged at the end of step k + 1
     auto step = [&](int k, ChunkRegs &mine, ChunkRegs &next) {
         const int c = n - 1 - k, buf = k & 1;
-        if (k + 2 < n) load_chunk(c - 2, mine);
-        if (k + 1 < n) load_dy(c - 1);
+        // unconditional (chunk 0 is re-read near the end): the same memory operation
+        // count on every path keeps the compiler's waits for the staged set exact.
+        // dY first: the stage at the end of this step waits for it, and the memory
+        // counter completes in order, so Q behind it stays in flight
+        load_dy(max(c - 1, 0));
+        load_chunk(max(c - 2, 0), mine);
         {  // bf16 snapshot of dS after chunk c
             U16 *dst = gsnap(p, m, b, h, c);
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) acc_store_bf_pairs(dst, dst + D * D, gR[jt], gI[jt], 16 * it, 16 * jt);
+            for (int jj = 0; jj < 2; ++jj)
+                acc_store_bf_pairs(dst, dst + D * D, gR[jj], gI[jj], 16 * it, 16 * (2 * jh + jj));
         }
         if (c > 0 || need_ds0) {
             // dG rows (value i) x cols (key j): A = (conj(rho) q_scale dY)^T, B = Q (k = t)
-            floatx4 accR[4], accI[4];
+            floatx4 accR[2], accI[2];
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
+            for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
             const U16 *Qr = sQ + (buf * 2) * PLANE_B, *Qi = sQ + (buf * 2 + 1) * PLANE_B;
             const U16 *Gr = sG + (buf * 2) * PLANE_B, *Gi = sG + (buf * 2 + 1) * PLANE_B;
-            const float *wre = sW + buf * 128, *wim = wre + 64;
 #pragma unroll
             for (int kp = 0; kp < 2; ++kp) {
                 const int t0 = 32 * kp + 8 * g;
-                const floatx8 gr = to_f(ld_tr(Gr, t0, t0 + 4, 16 * it)), gi = to_f(ld_tr(Gi, t0, t0 + 4, 16 * it));
-                floatx8 vr, vi;
+                const bf16x8 ar = ld_tr(Gr, t0, t0 + 4, 16 * it), ai = ld_tr(Gi, t0, t0 + 4, 16 * it),
+                             nar = neg_bf(ar);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float wr = wre[t0 + e], wi = wim[t0 + e];
-                    vr[e] = wr * gr[e] - wi * gi[e];
-                    vi[e] = wr * gi[e] + wi * gr[e];
-                }
-                const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
-#pragma unroll
-                for (int jt = 0; jt < 4; ++jt) {
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int jt = 2 * jh + jj;
                     const bf16x8 qr = ld_tr(Qr, t0, t0 + 4, 16 * jt), qi = ld_tr(Qi, t0, t0 + 4, 16 * jt);
-                    accR[jt] = mfma_bf(ar, qr, accR[jt]);
-                    accR[jt] = mfma_bf(ai, qi, accR[jt]);
-                    accI[jt] = mfma_bf(ai, qr, accI[jt]);
-                    accI[jt] = mfma_bf(nar, qi, accI[jt]);
+                    accR[jj] = mfma_bf(ar, qr, accR[jj]);
+                    accR[jj] = mfma_bf(ai, qi, accR[jj]);
+                    accI[jj] = mfma_bf(ai, qr, accI[jj]);
+                    accI[jj] = mfma_bf(nar, qi, accI[jj]);
                 }
             }
             const float tot = ftotal(p, m, b, h, c);
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt)
+            for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    gR[jt][r] = tot * gR[jt][r] + accR[jt][r];
-                    gI[jt][r] = tot * gI[jt][r] + accI[jt][r];
+                    gR[jj][r] = tot * gR[jj][r] + accR[jj][r];
+                    gI[jj][r] = tot * gI[jj][r] + accI[jj][r];
                 }
         }
-        if (k + 1 < n) stage_chunk(c - 1, buf ^ 1, next);
+        // also unconditional: past the end, chunk 0 (which `next` and the dY registers
+        // then hold) is staged again into the unused buffer
+        stage_chunk(max(c - 1, 0), buf ^ 1, next);
         __syncthreads();
     };
-    load_chunk(n - 1, cr[0]);
+    load_chunk(n - 1, cr0);
     load_dy(n - 1);
-    if (n > 1) load_chunk(n - 2, cr[1]);
-    stage_chunk(n - 1, 0, cr[0]);
+    load_chunk(max(n - 2, 0), cr1);
+    stage_chunk(n - 1, 0, cr0);
     __syncthreads();
-    for (int k = 0; k < n; k += 2) {
-        step(k, cr[0], cr[1]);
-        if (k + 1 < n) step(k + 1, cr[1], cr[0]);
+    // pairs of steps without conditions inside the loop, odd tail after it
+    int k = 0;
+    for (; k + 1 < n; k += 2) {
+        step(k, cr0, cr1);
+        step(k + 1, cr1, cr0);
     }
+    if (k < n) step(k, cr0, cr1);
     if (need_ds0) {
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
+        for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
-                p.ds0_re[o] = gR[jt][r];
-                p.ds0_im[o] = gI[jt][r];
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                p.ds0_re[o] = gR[jj][r];
+                p.ds0_im[o] = gI[jj][r];
             }
     }
 }
@@ -1632,7 +1640,7 @@ int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
-    hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(THREADS), s1, stream, p);
+    hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(PASS_THREADS), s1, stream, p);
     int st = launch_status("grad_pass_bf16_kernel");
     if (st) return st;
     hipLaunchKernelGGL(query_side_bf16_kernel<M>, grid, dim3(THREADS), s3, stream, p);

@@ -209,6 +209,11 @@ __device__ __forceinline__ bf16x8 ld_tr(const unsigned short *tile, int r0, int 
     return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// (lo, hi) -> two bf16 in one dword (hardware round-to-nearest-even conversion)
+__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{lo, hi}, bf16x2));
+}
+
 // One 16x16 accumulator tile of a complex matrix (element (4g + r, l16) of lane
 // 16g + l16) -> rows row0.., columns col0.. of two bf16 planes with row pitch D.
 // Adjacent lanes swap one row pair element (DPP quad_perm [1,0,3,2]) so that
@@ -220,14 +225,94 @@ __device__ __forceinline__ void acc_store_bf_pairs(unsigned short *dre, unsigned
     const bool odd = l16 & 1;
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-        const unsigned p0 = f32_to_bf16(re[2 * q]) | ((unsigned)f32_to_bf16(im[2 * q]) << 16);
-        const unsigned p1 = f32_to_bf16(re[2 * q + 1]) | ((unsigned)f32_to_bf16(im[2 * q + 1]) << 16);
+        const unsigned p0 = pack_bf16x2(re[2 * q], im[2 * q]), p1 = pack_bf16x2(re[2 * q + 1], im[2 * q + 1]);
         const unsigned keep = odd ? p1 : p0, send = odd ? p0 : p1;
         const unsigned recv = (unsigned)__builtin_amdgcn_update_dpp(0, (int)send, 0xB1, 0xF, 0xF, false);
         const unsigned lo = odd ? recv : keep, hi = odd ? keep : recv;  // columns (l16 & ~1) and +1
         const int row = row0 + 4 * g + 2 * q + (odd ? 1 : 0), col = col0 + (l16 & ~1);
-        *reinterpret_cast<unsigned *>(dre + row * D + col) = (lo & 0xFFFFu) | (hi << 16);
-        *reinterpret_cast<unsigned *>(dim + row * D + col) = (lo >> 16) | (hi & 0xFFFF0000u);
+        *reinterpret_cast<unsigned *>(dre + row * D + col) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        *reinterpret_cast<unsigned *>(dim + row * D + col) = __builtin_amdgcn_perm(hi, lo, 0x07060302u);
+    }
+}
+
+// State passes: blocks of PASS_THREADS threads (8 waves) walk the chunks of one
+// state; 64 x 64 chunk tiles travel global -> registers -> LDS in natural layout
+// (thread idx: row idx >> 3 and 16-byte column chunk idx & 7 for bf16, row idx >> 4
+// and float4 chunk idx & 15 for fp32).  Loads clamp rows at and beyond `valid` to
+// row valid-1, for consumers that weight those rows by zero: with no conditional
+// register initialisation, a load in a software pipeline does not wait for the
+// previous load into the same registers.  (Clang vector types: a uint4 / float4
+// struct copy from memory would keep the register sets in scratch.)
+constexpr int PASS_THREADS = 512;
+template <int NT>
+struct BfTileRegs {
+    uintx4 v[512 / NT];
+};
+template <int NT>
+struct F32TileRegs {
+    floatx4 v[1024 / NT];
+};
+template <int NT>
+__device__ __forceinline__ void tile_load_bf(BfTileRegs<NT> &t, const unsigned short *src, int64_t st, int valid) {
+#pragma unroll
+    for (int i = 0; i < 512 / NT; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        const int r = min(idx >> 3, valid - 1), c8 = idx & 7;
+        t.v[i] = *reinterpret_cast<const uintx4 *>(src + (int64_t)r * st + 8 * c8);
+    }
+}
+template <int NT>
+__device__ __forceinline__ void tile_store_bf(unsigned short *lds, const BfTileRegs<NT> &t) {
+#pragma unroll
+    for (int i = 0; i < 512 / NT; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        *reinterpret_cast<uintx4 *>(lds + (idx >> 3) * PB + 8 * (idx & 7)) = t.v[i];
+    }
+}
+// The same store with row r scaled by lane r's `row_scale` (of the calling wave),
+// in fp32, rounded once to bf16.
+template <int NT>
+__device__ __forceinline__ void tile_store_bf_rowscaled(unsigned short *lds, const BfTileRegs<NT> &t, float row_scale) {
+#pragma unroll
+    for (int i = 0; i < 512 / NT; ++i) {
+        const int idx = threadIdx.x + i * NT, r = idx >> 3;
+        const float f = __shfl(row_scale, r);
+        const floatx8 x = to_f(__builtin_bit_cast(bf16x8, t.v[i])) * f;
+        *reinterpret_cast<bf16x8 *>(lds + r * PB + 8 * (idx & 7)) = to_bf(x);
+    }
+}
+template <int NT>
+__device__ __forceinline__ void tile_load_f32(F32TileRegs<NT> &t, const float *src, int64_t st, int valid) {
+#pragma unroll
+    for (int i = 0; i < 1024 / NT; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        const int r = min(idx >> 4, valid - 1), c4 = idx & 15;
+        t.v[i] = *reinterpret_cast<const floatx4 *>(src + (int64_t)r * st + 4 * c4);
+    }
+}
+// A complex fp32 tile (two planes) times a per-row complex weight (lane r of the
+// calling wave holds row r's (w_re, w_im)) -> two bf16 planes, rounded once.
+template <int NT>
+__device__ __forceinline__ void tile_store_f32_cmul_as_bf(unsigned short *lre, unsigned short *lim,
+                                                         const F32TileRegs<NT> &xr, const F32TileRegs<NT> &xi,
+                                                         float w_re, float w_im) {
+#pragma unroll
+    for (int i = 0; i < 1024 / NT; ++i) {
+        const int idx = threadIdx.x + i * NT, r = idx >> 4;
+        const float wr = __shfl(w_re, r), wi = __shfl(w_im, r);
+        const floatx4 yr = wr * xr.v[i] - wi * xi.v[i], yi = wr * xi.v[i] + wi * xr.v[i];
+        const int o = r * PB + 4 * (idx & 15);
+        *reinterpret_cast<uint2 *>(lre + o) = make_uint2(pack_bf16x2(yr[0], yr[1]), pack_bf16x2(yr[2], yr[3]));
+        *reinterpret_cast<uint2 *>(lim + o) = make_uint2(pack_bf16x2(yi[0], yi[1]), pack_bf16x2(yi[2], yi[3]));
+    }
+}
+template <int NT>
+__device__ __forceinline__ void tile_store_f32_as_bf(unsigned short *lds, const F32TileRegs<NT> &t) {
+#pragma unroll
+    for (int i = 0; i < 1024 / NT; ++i) {
+        const int idx = threadIdx.x + i * NT;
+        const uint2 u = make_uint2(pack_bf16x2(t.v[i][0], t.v[i][1]), pack_bf16x2(t.v[i][2], t.v[i][3]));
+        *reinterpret_cast<uint2 *>(lds + (idx >> 4) * PB + 4 * (idx & 15)) = u;
     }
 }
 

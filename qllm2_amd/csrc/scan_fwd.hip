@@ -558,160 +558,166 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
 // fp32 accumulation; q is staged unscaled and q_scale is applied to the fp32
 // results it enters.
 //
-// State pass: one block per (state m, b, h, half of the value rows) walks the
-// chunks in order.  Per chunk it forms dS = sum_s dl_s v_s (x) conj(k_s) on
-// MFMA (rows i of its half, all key columns j) and updates the running state
-// S <- total S + dS, which never leaves registers (fp32, accumulator layout).
-// Only the bf16 snapshot of the state entering each chunk, the chunk totals and
-// the final state reach HBM.  Chunk c+1's K and V tiles and gamma are loaded
-// while chunk c is processed (double-buffered LDS, one barrier per chunk); the
-// snapshot of chunk c is staged in LDS and stored during chunk c+1.
+// State pass: one block of PASS_THREADS (8 waves) per (state m, b, h) walks the
+// chunks in order; wave w owns value rows 16(w & 3).. and key-column tiles
+// 2(w >> 2), 2(w >> 2) + 1 (two waves per SIMD, so one wave's loads, stores and
+// MFMA chain overlap the other's).  Per chunk it forms dS = sum_s dl_s v_s (x)
+// conj(k_s) on MFMA and updates the running state S <- total S + dS, which never
+// leaves registers (fp32, accumulator layout).  Only the bf16 snapshot of the
+// state entering each chunk (stored straight from registers), the chunk totals
+// and the final state reach HBM.  Chunk c+2's K and V tiles and gamma are loaded
+// into registers while chunk c is processed and staged into LDS at the end of
+// chunk c+1 (double-buffered LDS, one barrier per chunk); every wave forms the
+// chunk's decay prefix itself and V is staged already scaled by dl_s, so the
+// MFMA operands come straight from LDS.  Rows past the end of the sequence
+// re-read its last row: their decay weights dl are zero.
 constexpr size_t pass_bf16_smem() {
-    return (size_t)2 * 2 * PLANE_B * 2    // K [buf][plane][64][PB]
-           + (size_t)2 * 2 * PLANE_B * 2  // V [buf][plane][64][PB]
-           + (size_t)2 * 68 * sizeof(float);  // dl[64] + total per buffer
+    return (size_t)2 * 2 * PLANE_B * 2     // K [buf][plane][64][PB]
+           + (size_t)2 * 2 * PLANE_B * 2;  // dl-scaled V [buf][plane][64][PB]
 }
 
-__global__ void __launch_bounds__(THREADS) state_pass_bf16_kernel(FwdParams p) {
+__global__ void __launch_bounds__(PASS_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
+state_pass_bf16_kernel(FwdParams p) {
+    constexpr int NT = PASS_THREADS;
     extern __shared__ float smem[];
     using U = unsigned short;
     U *sK = reinterpret_cast<U *>(smem);  // + (buf * 2 + plane) * PLANE_B
     U *sV = sK + 4 * PLANE_B;             // + (buf * 2 + plane) * PLANE_B
-    float *sDl = reinterpret_cast<float *>(sV + 4 * PLANE_B);  // + buf * 68; [64] = total
 
     const qpam_scan_args &a = p.a;
     const int chain = blockIdx.x;
     const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int it = w;  // wave: value rows 16it.., all four key-column tiles
+    const int it = w & 3, jh = w >> 2;  // value rows 16it.., key-column tiles 2jh + jj
     const int n = p.n_chunks;
     const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
     const U *kre = (const U *)a.k.re + b * a.k.s0 + h * a.k.s1, *kim = (const U *)a.k.im + b * a.k.s0 + h * a.k.s1;
     const U *vre = (const U *)a.v.re + b * a.v.s0 + h * a.v.s1, *vim = (const U *)a.v.im + b * a.v.s0 + h * a.v.s1;
     U *snap0 = chunk_snap_ptr(p, m, b, h, 0);
 
-    // running state S[i][j] for rows 16it + 4g + r, cols 16jt + l16
-    floatx4 sR[4], sI[4];
+    // running state S[i][j] for rows 16it + 4g + r, cols 16(2jh + jj) + l16
+    floatx4 sR[2], sI[2];
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        sR[jt] = sI[jt] = zero4();
+    for (int jj = 0; jj < 2; ++jj) {
+        sR[jj] = sI[jj] = zero4();
         if (a.s0_re) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
-                sR[jt][r] = a.s0_re[o];
-                sI[jt][r] = a.s0_im[o];
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                sR[jj][r] = a.s0_re[o];
+                sI[jj][r] = a.s0_im[o];
             }
         }
     }
 
     // chunk inputs in registers, two register sets (chunk c in set c & 1): K and V
-    // (2 planes x 2 uint4 each), gamma (wave 0).  Sets are selected by compile-time
-    // index only (the chunk loop is unrolled by two).
+    // planes, gamma.  Sets are selected by compile-time index only (the chunk loop
+    // is unrolled by two).
     struct ChunkRegs {
-        B16Regs kr, ki, vr, vi;
+        BfTileRegs<NT> kr, ki, vr, vi;
         float gam;
     };
-    ChunkRegs cr[2];
+    ChunkRegs cr0, cr1;
     auto load_chunk = [&](int c, ChunkRegs &x) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
         const int64_t ko = (int64_t)c0 * a.k.s2, vo = (int64_t)c0 * a.v.s2;
-        regs_load_bf<false>(x.kr, kre + ko, a.k.s2, valid);
-        regs_load_bf<false>(x.ki, kim + ko, a.k.s2, valid);
-        regs_load_bf<false>(x.vr, vre + vo, a.v.s2, valid);
-        regs_load_bf<false>(x.vi, vim + vo, a.v.s2, valid);
-        x.gam = (w == 0 && lane < valid) ? gbase[(int64_t)(c0 + lane) * a.sg_t] : 1.f;
+        tile_load_bf<NT>(x.kr, kre + ko, a.k.s2, valid);
+        tile_load_bf<NT>(x.ki, kim + ko, a.k.s2, valid);
+        tile_load_bf<NT>(x.vr, vre + vo, a.v.s2, valid);
+        tile_load_bf<NT>(x.vi, vim + vo, a.v.s2, valid);
+        x.gam = gbase[(int64_t)(c0 + min(lane, valid - 1)) * a.sg_t];
     };
-    // registers -> LDS buffer `buf`; wave 0 turns gamma into dl and the chunk total
+    // registers -> LDS buffer `buf`: K as loaded, V scaled by dl_s = D[C-1, s]; each
+    // wave forms the decay prefix from gamma itself and keeps the chunk total
+    float tot_staged = 1.f;  // decay total of the chunk in the most recently staged buffer
     auto stage_chunk = [&](int c, int buf, const ChunkRegs &x) {
-        regs_store_bf<false>(sK + (buf * 2) * PLANE_B, x.kr);
-        regs_store_bf<false>(sK + (buf * 2 + 1) * PLANE_B, x.ki);
-        regs_store_bf<false>(sV + (buf * 2) * PLANE_B, x.vr);
-        regs_store_bf<false>(sV + (buf * 2 + 1) * PLANE_B, x.vi);
-        if (w == 0) {
-            const int valid = min(64, a.T - c * 64);
-            float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
+        const int valid = min(64, a.T - c * 64);
+        float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_up(L, off);
-                if (lane >= off) L += y;
-            }
-            const float Llast = __shfl(L, valid - 1);
-            sDl[buf * 68 + lane] = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
-            if (lane == 0) {
-                const float tot = __expf(Llast);
-                sDl[buf * 68 + 64] = tot;
-                *chunk_total_ptr(p, m, b, h, c) = tot;
-            }
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(L, off);
+            if (lane >= off) L += y;
         }
+        const float Llast = __shfl(L, valid - 1);
+        const float dl = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
+        tot_staged = __expf(Llast);
+        if (tid == 0) *chunk_total_ptr(p, m, b, h, c) = tot_staged;
+        tile_store_bf<NT>(sK + (buf * 2) * PLANE_B, x.kr);
+        tile_store_bf<NT>(sK + (buf * 2 + 1) * PLANE_B, x.ki);
+        tile_store_bf_rowscaled<NT>(sV + (buf * 2) * PLANE_B, x.vr, dl);
+        tile_store_bf_rowscaled<NT>(sV + (buf * 2 + 1) * PLANE_B, x.vi, dl);
     };
 
     // chunk c uses LDS buffer c & 1; chunk c + 2 is loaded into register set c & 1
     // during chunk c and staged at the end of chunk c + 1 (two chunks of latency cover)
     auto step = [&](int c, ChunkRegs &mine, ChunkRegs &next) {
         const int buf = c & 1;
-        if (c + 2 < n) load_chunk(c + 2, mine);
-        // bf16 snapshot of the entering state (rows 16it.. of chunk c's snapshot)
+        // unconditional (the last chunk is re-read near the end): the same memory
+        // operation count on every path keeps the compiler's waits for the staged
+        // set exact
+        load_chunk(min(c + 2, n - 1), mine);
+        // bf16 snapshot of the entering state (this wave's tiles of chunk c's snapshot)
         {
             U *dst = snap0 + (int64_t)c * 2 * D * D;
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) acc_store_bf_pairs(dst, dst + D * D, sR[jt], sI[jt], 16 * it, 16 * jt);
+            for (int jj = 0; jj < 2; ++jj)
+                acc_store_bf_pairs(dst, dst + D * D, sR[jj], sI[jj], 16 * it, 16 * (2 * jh + jj));
         }
-        // dS rows (value i) x cols (key j): A = dl-scaled V^T (transposed reads of V), B = K
-        floatx4 accR[4], accI[4];
+        // dS rows (value i) x cols (key j): A = dl-scaled V^T (transposed reads), B = K
+        floatx4 accR[2], accI[2];
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt) accR[jt] = accI[jt] = zero4();
+        for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
         const U *Kr = sK + (buf * 2) * PLANE_B, *Ki = sK + (buf * 2 + 1) * PLANE_B;
         const U *Vr = sV + (buf * 2) * PLANE_B, *Vi = sV + (buf * 2 + 1) * PLANE_B;
-        const float *dl = sDl + buf * 68;
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             const int s0 = 32 * kp + 8 * g;
-            floatx8 vr = to_f(ld_tr(Vr, s0, s0 + 4, 16 * it)), vi = to_f(ld_tr(Vi, s0, s0 + 4, 16 * it));
+            const bf16x8 ar = ld_tr(Vr, s0, s0 + 4, 16 * it), ai = ld_tr(Vi, s0, s0 + 4, 16 * it), nar = neg_bf(ar);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                vr[e] *= dl[s0 + e];
-                vi[e] *= dl[s0 + e];
-            }
-            const bf16x8 ar = to_bf(vr), ai = to_bf(vi), nar = neg_bf(ar);
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
+            for (int jj = 0; jj < 2; ++jj) {
+                const int jt = 2 * jh + jj;
                 const bf16x8 kr = ld_tr(Kr, s0, s0 + 4, 16 * jt), ki = ld_tr(Ki, s0, s0 + 4, 16 * jt);
-                accR[jt] = mfma_bf(ar, kr, accR[jt]);
-                accR[jt] = mfma_bf(ai, ki, accR[jt]);
-                accI[jt] = mfma_bf(ai, kr, accI[jt]);
-                accI[jt] = mfma_bf(nar, ki, accI[jt]);
+                accR[jj] = mfma_bf(ar, kr, accR[jj]);
+                accR[jj] = mfma_bf(ai, ki, accR[jj]);
+                accI[jj] = mfma_bf(ai, kr, accI[jj]);
+                accI[jj] = mfma_bf(nar, ki, accI[jj]);
             }
         }
         // S <- total S + dS
-        const float tot = dl[64];
+        const float tot = tot_staged;
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
+        for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                sR[jt][r] = tot * sR[jt][r] + accR[jt][r];
-                sI[jt][r] = tot * sI[jt][r] + accI[jt][r];
+                sR[jj][r] = tot * sR[jj][r] + accR[jj][r];
+                sI[jj][r] = tot * sI[jj][r] + accI[jj][r];
             }
-        if (c + 1 < n) stage_chunk(c + 1, buf ^ 1, next);
+        // also unconditional: past the end, chunk n-1 (which `next` then holds) is
+        // staged again into the unused buffer
+        stage_chunk(min(c + 1, n - 1), buf ^ 1, next);
         __syncthreads();
     };
-    load_chunk(0, cr[0]);
-    if (n > 1) load_chunk(1, cr[1]);
-    stage_chunk(0, 0, cr[0]);
+    load_chunk(0, cr0);
+    load_chunk(min(1, n - 1), cr1);
+    stage_chunk(0, 0, cr0);
     __syncthreads();
-    for (int c = 0; c < n; c += 2) {
-        step(c, cr[0], cr[1]);
-        if (c + 1 < n) step(c + 1, cr[1], cr[0]);
+    // pairs of steps without conditions inside the loop (no path on which the
+    // compiler would see fewer memory operations), odd tail after it
+    int c = 0;
+    for (; c + 1 < n; c += 2) {
+        step(c, cr0, cr1);
+        step(c + 1, cr1, cr0);
     }
+    if (c < n) step(c, cr0, cr1);
     if (a.s_re) {
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
+        for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
-                a.s_re[o] = sR[jt][r];
-                a.s_im[o] = sI[jt][r];
+                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                a.s_re[o] = sR[jj][r];
+                a.s_im[o] = sI[jj][r];
             }
     }
 }
@@ -935,7 +941,7 @@ int launch_fwd_bf16_m(const FwdParams &p, hipStream_t stream) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
-    hipLaunchKernelGGL(state_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(THREADS), s1, stream, p);
+    hipLaunchKernelGGL(state_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(PASS_THREADS), s1, stream, p);
     int st = launch_status("state_pass_bf16_kernel");
     if (st) return st;
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));

@@ -103,6 +103,27 @@ def test_scan_backward_bf16_e3(gpu_lib):
         assert _rel(a, b) < 2e-2, f"{name}: rel {_rel(a, b):.2e}"
 
 
+@pytest.mark.parametrize("M,T,with_rot,with_s0", [
+    (3, 40, True, True),     # one partial chunk
+    (3, 150, True, True),    # odd chunk count, ragged last chunk
+    (1, 200, False, False),  # even chunk count, ragged last chunk, no rotation
+    (2, 128, True, False),   # two full chunks
+])
+def test_scan_backward_bf16_ragged(gpu_lib, M, T, with_rot, with_s0):
+    """bf16 inputs (the state-pass kernels) at sequence lengths that are not a
+    multiple of the chunk and chunk counts of 1, 2, odd and even: every gradient
+    against oracle autograd."""
+    B, H, d, C = 2, 2, 64, 64
+    case = _case(M, B, H, T, d, 3500 + M * 11 + T, with_rot, with_s0, torch.bfloat16)
+    ref = _oracle_grads(*case, d, C)
+    got = _gpu_grads(*case, d, C, torch.bfloat16, with_rot)
+    for name, a, b in zip(NAMES, got, ref):
+        if a is None or b is None:
+            continue
+        assert math.isfinite(a.abs().sum().item()), name
+        assert _rel(a, b) < 2e-2, f"{name}: rel {_rel(a, b):.2e}"
+
+
 def test_scan_backward_config3_full_size(gpu_lib):
     """Config 3: E3 M=3, B=8, T=2048, H=12, d=64, C=64, bf16 q/k/v, fp32 state,
     dY complex N(0,1); oracle autograd in fp32 on the bf16-rounded inputs."""

@@ -761,12 +761,261 @@ __global__ void __launch_bounds__(THREADS) dh_reduce_kernel(GroupParams q) {
 constexpr int DH_SPLITS = 8;
 }  // namespace big
 
+// 256 x 256 tiles for the bf16 logits GEMMs (hidden size a multiple of 64): one
+// block of 4 waves per tile, each wave a 128 x 128 quadrant (64 accumulator
+// tiles, one wave per SIMD), k-steps of 64 through double-buffered LDS (72 KiB
+// per stage) with the next stage's global loads in flight in registers.  Rows
+// past the end of an operand re-read its last row (the epilogues mask them), so
+// the pipelined loads carry no conditional register initialisation.
+namespace wide {
+constexpr int TM = 256, TN = 256, WK = 64;
+constexpr int WTHREADS = 512;   // 8 waves: 4 row groups x 2 column groups, 64 x 128 each
+constexpr int WPITCH = WK + 8;  // bf16 elements per LDS row (144 bytes: conflict-free 16-byte reads)
+constexpr int WLOADS = TM * WK / 8 / WTHREADS;  // 16-byte loads per thread per operand per k-step (4)
+constexpr size_t WSMEM = (size_t)2 * (TM + TN) * WPITCH * sizeof(unsigned short);  // 144 KiB
+using U16 = unsigned short;
+
+struct WFrag {
+    uintx4 a[WLOADS], b[WLOADS];
+};
+
+// Rows past the end of an operand re-read its last row (the epilogues mask them).
+// Addresses are a wave-uniform base plus a 32-bit byte offset per load.
+__device__ __forceinline__ void wgload(WFrag &f, const U16 *A, int64_t lda, int a_rows, const U16 *B, int64_t ldb,
+                                       int b_rows, int k0) {
+    const int tid = threadIdx.x, c8 = 8 * (tid & 7);
+    const char *ab = reinterpret_cast<const char *>(A + k0), *bb = reinterpret_cast<const char *>(B + k0);
+#pragma unroll
+    for (int i = 0; i < WLOADS; ++i) {
+        const int row = (tid >> 3) + 64 * i;
+        const unsigned ao = 2u * (unsigned)(min(row, a_rows - 1) * (int)lda + c8);
+        const unsigned bo = 2u * (unsigned)(min(row, b_rows - 1) * (int)ldb + c8);
+        f.a[i] = *reinterpret_cast<const uintx4 *>(ab + ao);
+        f.b[i] = *reinterpret_cast<const uintx4 *>(bb + bo);
+    }
+}
+
+__device__ __forceinline__ void wlstore(const WFrag &f, U16 *sA, U16 *sB) {
+    const int tid = threadIdx.x, c8 = 8 * (tid & 7);
+#pragma unroll
+    for (int i = 0; i < WLOADS; ++i) {
+        const int row = (tid >> 3) + 64 * i;
+        *reinterpret_cast<uintx4 *>(sA + row * WPITCH + c8) = f.a[i];
+        *reinterpret_cast<uintx4 *>(sB + row * WPITCH + c8) = f.b[i];
+    }
+}
+
+// One k-step (64) of the wave's 64 x 128 block: per 32-wide half, the four A
+// fragments stay in registers while the eight B fragments stream through (each
+// feeds four MFMAs).
+__device__ __forceinline__ void wmma_stage(const U16 *sA, const U16 *sB, floatx4 (&acc)[4][8], int arow0, int brow0,
+                                           int l16, int g) {
+#pragma unroll
+    for (int ks = 0; ks < WK / 32; ++ks) {
+        bf16x8 af[4];
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+            af[mi] = *reinterpret_cast<const bf16x8 *>(sA + (arow0 + 16 * mi + l16) * WPITCH + 32 * ks + 8 * g);
+#pragma unroll
+        for (int ni = 0; ni < 8; ++ni) {
+            const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(sB + (brow0 + 16 * ni + l16) * WPITCH + 32 * ks + 8 * g);
+#pragma unroll
+            for (int mi = 0; mi < 4; ++mi)
+                acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], bfr, acc[mi][ni], 0, 0, 0);
+        }
+    }
+}
+
+// C[m][n] = sum_k A[m][k] B[n][k] (k in [0, K), K a multiple of 64) for one 256 x 256
+// tile; acc[mi][ni] lane holds C[64*(w>>1) + 16mi + 4g + r][128*(w&1) + 16ni + l16].
+// The global loads of k-step kt + 1 are issued (and pinned) before the MFMAs of
+// k-step kt and reach the other LDS buffer after them; the second wave on each
+// SIMD covers the rest of their latency.
+__device__ __forceinline__ void wgemm_tile(const U16 *A, int64_t lda, int a_rows, const U16 *B, int64_t ldb,
+                                           int b_rows, int K, floatx4 (&acc)[4][8], U16 *smem) {
+    U16 *sA0 = smem, *sB0 = smem + TM * WPITCH;
+    U16 *sA1 = smem + (TM + TN) * WPITCH, *sB1 = sA1 + TM * WPITCH;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int arow0 = 64 * (w >> 1), brow0 = 128 * (w & 1);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int KT = K / WK;
+    WFrag f;
+    wgload(f, A, lda, a_rows, B, ldb, b_rows, 0);
+    wlstore(f, sA0, sB0);
+    __syncthreads();
+    // two k-steps per iteration (buffers by compile-time index); the loads are
+    // unconditional (past the end they re-read the last k-step) so that every path
+    // has the same memory operations
+    int kt = 0;
+    for (; kt + 1 < KT; kt += 2) {
+        wgload(f, A, lda, a_rows, B, ldb, b_rows, (kt + 1) * WK);
+        __builtin_amdgcn_sched_barrier(0);
+        wmma_stage(sA0, sB0, acc, arow0, brow0, l16, g);
+        __builtin_amdgcn_sched_barrier(0);
+        wlstore(f, sA1, sB1);
+        __syncthreads();
+        wgload(f, A, lda, a_rows, B, ldb, b_rows, min(kt + 2, KT - 1) * WK);
+        __builtin_amdgcn_sched_barrier(0);
+        wmma_stage(sA1, sB1, acc, arow0, brow0, l16, g);
+        __builtin_amdgcn_sched_barrier(0);
+        wlstore(f, sA0, sB0);
+        __syncthreads();
+    }
+    if (kt < KT) wmma_stage(sA0, sB0, acc, arow0, brow0, l16, g);
+}
+
+__device__ __forceinline__ int xcd_item(int bid, int total) { return big::xcd_item(bid, total); }
+
+// forward: per (256 rows, 256 vocab) tile -> per-row (max, sum exp, argmax)
+__global__ void __launch_bounds__(WTHREADS) fwd_tile_kernel(FwdParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ float sM[2][TM], sS[2][TM];
+    __shared__ int sI[2][TM];
+    const qpam_ce_fwd_args &a = p.a;
+    const int n_rt = (a.N + TM - 1) / TM;
+    const int item = xcd_item(blockIdx.x, n_rt * p.n_vt);
+    if (item >= n_rt * p.n_vt) return;
+    int rt, vt;
+    big::grouped_tile(item, n_rt, p.n_vt, rt, vt);
+    const int r0 = rt * TM, v0 = vt * TN;
+    floatx4 acc[4][8];
+    wgemm_tile((const U16 *)a.h + (int64_t)r0 * a.ldh, a.ldh, min(TM, a.N - r0), (const U16 *)a.w + (int64_t)v0 * a.ldw,
+               a.ldw, min(TN, a.V - v0), a.D, acc, reinterpret_cast<U16 *>(smem_raw));
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float mx = -INFINITY;
+            int ix = 0x7fffffff;
+#pragma unroll
+            for (int ni = 0; ni < 8; ++ni) {
+                const int v = v0 + 128 * wn + 16 * ni + l16;
+                const float x = (v < a.V) ? acc[mi][ni][r] : -INFINITY;
+                if (x > mx) { mx = x; ix = v; }
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) {
+                const float om = __shfl_xor(mx, off);
+                const int oi = __shfl_xor(ix, off);
+                if (om > mx || (om == mx && oi < ix)) { mx = om; ix = oi; }
+            }
+            float s = 0.f;
+#pragma unroll
+            for (int ni = 0; ni < 8; ++ni) {
+                const int v = v0 + 128 * wn + 16 * ni + l16;
+                if (v < a.V) s += __expf(acc[mi][ni][r] - mx);
+            }
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
+            if (l16 == 0) {
+                const int row = 64 * wm + 16 * mi + 4 * g + r;
+                sM[wn][row] = mx;
+                sS[wn][row] = s;
+                sI[wn][row] = ix;
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < TM && r0 + tid < a.N) {
+        const float m0 = sM[0][tid], m1 = sM[1][tid];
+        const float m = fmaxf(m0, m1);
+        float s = 0.f;
+        if (m0 > -INFINITY) s += sS[0][tid] * __expf(m0 - m);
+        if (m1 > -INFINITY) s += sS[1][tid] * __expf(m1 - m);
+        const int i = (m1 > m0 || (m1 == m0 && sI[1][tid] < sI[0][tid])) ? sI[1][tid] : sI[0][tid];
+        const int64_t o = (int64_t)(r0 + tid) * p.n_vt + vt;
+        p.part_m[o] = m;
+        p.part_s[o] = s;
+        p.part_i[o] = i;
+    }
+}
+
+// backward G tile (256 rows x 256 vocab): recompute logits, write G^T [Vp][Rp]
+// (and G [rows][Vp] when write_g)
+__global__ void __launch_bounds__(WTHREADS) grad_tile_kernel(BwdParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ float sLse[TM], sScale[TM];
+    __shared__ int sTgt[TM];
+    const qpam_ce_bwd_args &a = p.a;
+    const int n_rt = p.Rp / TM, n_vt = p.Vp / TN;
+    const int item = xcd_item(blockIdx.x, n_rt * n_vt);
+    if (item >= n_rt * n_vt) return;
+    int rt, vt;
+    big::grouped_tile(item, n_rt, n_vt, rt, vt);
+    const int lr0 = rt * TM, v0 = vt * TN;
+    const int tid = threadIdx.x;
+    if (tid < TM) {
+        const int lr = lr0 + tid, row = p.row0 + lr;
+        float lse = 0.f, sc = 0.f;
+        int tg = -1;
+        if (lr < p.rows) {
+            const int64_t t = a.targets[row];
+            const bool valid = (t != a.ignore_index) && t >= 0 && t < a.V;
+            lse = a.lse[row];
+            sc = valid ? a.grad_scale[0] * (a.mask ? a.mask[row] : 1.f) : 0.f;
+            tg = valid ? (int)t : -1;
+        }
+        sLse[tid] = lse;
+        sScale[tid] = sc;
+        sTgt[tid] = tg;
+    }
+    floatx4 acc[4][8];
+    wgemm_tile((const U16 *)a.h + (int64_t)(p.row0 + lr0) * a.ldh, a.ldh, min(TM, p.rows - lr0),
+               (const U16 *)a.w + (int64_t)v0 * a.ldw, a.ldw, min(TN, a.V - v0), a.D, acc,
+               reinterpret_cast<U16 *>(smem_raw));
+    const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int wm = w >> 1, wn = w & 1;
+    U16 *G = (U16 *)p.gbuf;
+    U16 *GT = (U16 *)p.gtbuf;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+#pragma unroll
+        for (int ni = 0; ni < 8; ++ni) {
+            const int v = v0 + 128 * wn + 16 * ni + l16;
+            const int rl0 = 64 * wm + 16 * mi + 4 * g;
+            float x[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int rl = rl0 + r;
+                x[r] = 0.f;
+                if (v < a.V && sScale[rl] != 0.f) {
+                    x[r] = __expf(acc[mi][ni][r] - sLse[rl]);
+                    if (v == sTgt[rl]) x[r] -= 1.f;
+                    x[r] *= sScale[rl];
+                }
+            }
+            const unsigned lo = pack_bf16x2(x[0], x[1]), hi = pack_bf16x2(x[2], x[3]);
+            if (p.write_g) {
+                const unsigned short gb[4] = {(unsigned short)(lo & 0xFFFFu), (unsigned short)(lo >> 16),
+                                              (unsigned short)(hi & 0xFFFFu), (unsigned short)(hi >> 16)};
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (lr0 + rl0 + r < p.rows) G[(int64_t)(lr0 + rl0 + r) * p.Vp + v] = gb[r];
+            }
+            *reinterpret_cast<uint2 *>(GT + (int64_t)v * p.Rp + lr0 + rl0) = make_uint2(lo, hi);
+        }
+    }
+}
+}  // namespace wide
+
 int round_up(int x, int m) { return (x + m - 1) / m * m; }
 
 template <typename T> constexpr bool is_bf() { return sizeof(T) == 2; }
 
-// vocab tile of the logits kernels: 256 on the bf16 big-tile path, 128 otherwise
+// bf16 with a hidden size that is a multiple of 64 takes the 256 x 256 tiles
+bool use_wide(int D) { return D % wide::WK == 0; }
+
+// vocab tile of the forward logits kernel (128 on the fp32 and narrow bf16 paths:
+// the larger partial count, used to size the workspace)
 template <typename T> constexpr int vocab_tile() { return is_bf<T>() ? big::BTN : VT; }
+// vocab / row padding of the backward G buffers (one value per dtype, whichever
+// bf16 tile runs: 256 is a multiple of both bf16 tile widths)
+template <typename T> constexpr int vocab_pad() { return is_bf<T>() ? wide::TN : VT; }
 template <typename T> constexpr int row_tile() { return is_bf<T>() ? big::BTM : BM; }
 
 template <typename T>
@@ -777,7 +1026,7 @@ size_t fwd_ws(const qpam_ce_fwd_args &a) {
 
 template <typename T>
 size_t bwd_ws(const qpam_ce_bwd_args &a) {
-    const int64_t Vp = round_up(a.V, vocab_tile<T>()), chunk = std::min(a.chunk, a.N);
+    const int64_t Vp = round_up(a.V, vocab_pad<T>()), chunk = std::min(a.chunk, a.N);
     const int64_t Rp = round_up((int)chunk, row_tile<T>());
     const int64_t elems = (int64_t)a.D * Vp + chunk * Vp + Vp * Rp + (int64_t)a.D * Rp;
     size_t bytes = (size_t)(elems * sizeof(T)) + 4 * 256;
@@ -790,7 +1039,8 @@ template <typename T>
 int run_fwd(const qpam_ce_fwd_args &a, hipStream_t stream) {
     FwdParams p;
     p.a = a;
-    p.n_vt = (a.V + vocab_tile<T>() - 1) / vocab_tile<T>();
+    const bool wide_tiles = is_bf<T>() && use_wide(a.D);
+    p.n_vt = wide_tiles ? (a.V + wide::TN - 1) / wide::TN : (a.V + vocab_tile<T>() - 1) / vocab_tile<T>();
     char *ws = (char *)a.workspace;
     const int64_t cnt = (int64_t)a.N * p.n_vt;
     p.part_m = (float *)ws;
@@ -798,7 +1048,13 @@ int run_fwd(const qpam_ce_fwd_args &a, hipStream_t stream) {
     p.part_i = (int *)(p.part_s + cnt);
     p.red = nullptr;
     int st;
-    if (is_bf<T>()) {
+    if (wide_tiles) {
+        QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)wide::fwd_tile_kernel,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide::WSMEM));
+        dim3 grid(big::xcd_grid(p.n_vt * ((a.N + wide::TM - 1) / wide::TM)));
+        hipLaunchKernelGGL(wide::fwd_tile_kernel, grid, dim3(wide::WTHREADS), wide::WSMEM, stream, p);
+        st = launch_status("ce fwd_tile_kernel (bf16, 256 x 256)");
+    } else if (is_bf<T>()) {
         QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::fwd_tile_kernel,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)big::SMEM));
         dim3 grid(big::xcd_grid(p.n_vt * ((a.N + big::BTM - 1) / big::BTM)));
@@ -828,9 +1084,22 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
     big::GroupParams q;
     BwdParams &p = q.p;
     p.a = a;
-    p.Vp = round_up(a.V, big::BTN);
+    p.Vp = round_up(a.V, vocab_pad<U>());
     const int chunk = std::min(a.chunk, a.N);
     const int Rmax = round_up(chunk, big::BTM);
+    const bool wide_tiles = use_wide(a.D);
+    // the G-tile kernel: 256 x 256 tiles, or 256 x 128 for hidden sizes that are not
+    // a multiple of 64 (Vp and Rp are multiples of both)
+    const void *gkern = wide_tiles ? (const void *)wide::grad_tile_kernel : (const void *)big::grad_tile_kernel;
+    const size_t gsmem = wide_tiles ? wide::WSMEM : big::SMEM;
+    auto launch_grad = [&]() {
+        const int tiles = (p.Vp / (wide_tiles ? wide::TN : big::BTN)) * (p.Rp / big::BTM);
+        if (wide_tiles)
+            hipLaunchKernelGGL(wide::grad_tile_kernel, dim3(big::xcd_grid(tiles)), dim3(wide::WTHREADS), gsmem, stream, p);
+        else
+            hipLaunchKernelGGL(big::grad_tile_kernel, dim3(big::xcd_grid(tiles)), dim3(THREADS), gsmem, stream, p);
+        return launch_status(wide_tiles ? "ce grad_tile_kernel (bf16, 256 x 256)" : "ce grad_tile_kernel (bf16)");
+    };
     U *ws = (U *)a.workspace;
     p.wt = ws;
     p.gbuf = ws + (int64_t)a.D * p.Vp;
@@ -845,16 +1114,12 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
         //   dH^T[D][rows] = W^T G-view   (m = D, n = rows, k = V)
         p.write_g = 0;
         const size_t blas_ws = std::max((size_t)big::DH_SPLITS * chunk * a.D * sizeof(float), blas::WS_BYTES);
-        QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::grad_tile_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        QPAM_CHECK_HIP(hipFuncSetAttribute(gkern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsmem));
         for (int r0 = 0; r0 < a.N; r0 += chunk) {
             p.row0 = r0;
             p.rows = std::min(chunk, a.N - r0);
             p.Rp = round_up(p.rows, big::BTM);
-            hipLaunchKernelGGL(big::grad_tile_kernel,
-                               dim3(big::xcd_grid((p.Vp / big::BTN) * (p.Rp / big::BTM))), dim3(THREADS), smem,
-                               stream, p);
-            int st = launch_status("ce grad_tile_kernel (bf16)");
+            int st = launch_grad();
             if (st) return st;
             st = blas::gemm_bf16(false, false, a.D, a.V, p.rows, (const U *)a.h + (int64_t)r0 * a.ldh, a.ldh,
                                  p.gtbuf, p.Rp, 1.f, a.dw, a.lddw, true, q.dh_part, blas_ws, stream);
@@ -866,8 +1131,7 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
         return QPAM_OK;
     }
     p.write_g = 1;
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::grad_tile_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    QPAM_CHECK_HIP(hipFuncSetAttribute(gkern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsmem));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::dw_gemm_kernel,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::dh_gemm_kernel,
@@ -890,9 +1154,7 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
                            p.Rp);
         st = launch_status("transpose_kernel(H)");
         if (st) return st;
-        hipLaunchKernelGGL(big::grad_tile_kernel, dim3(big::xcd_grid((p.Vp / big::BTN) * (p.Rp / big::BTM))),
-                           dim3(THREADS), smem, stream, p);
-        st = launch_status("ce grad_tile_kernel (bf16)");
+        st = launch_grad();
         if (st) return st;
         q.dh_ntiles_m = (p.rows + big::BTM - 1) / big::BTM;
         hipLaunchKernelGGL(big::dw_gemm_kernel, dim3(big::xcd_grid(q.n_dw)), dim3(THREADS), smem, stream, q);

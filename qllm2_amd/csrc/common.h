@@ -57,6 +57,11 @@ __device__ __forceinline__ unsigned short f32_to_bf16(float f) {
     return (unsigned short)(u >> 16);
 }
 
+// (lo, hi) -> two bf16 in one dword (hardware round-to-nearest-even conversion)
+__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
+    return __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{lo, hi}, bf16x2));
+}
+
 template <typename T> struct Elem;
 template <> struct Elem<float> {
     __device__ __forceinline__ static float load(const float *p) { return *p; }

@@ -209,11 +209,6 @@ __device__ __forceinline__ bf16x8 ld_tr(const unsigned short *tile, int r0, int 
     return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// (lo, hi) -> two bf16 in one dword (hardware round-to-nearest-even conversion)
-__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
-    return __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{lo, hi}, bf16x2));
-}
-
 // One 16x16 accumulator tile of a complex matrix (element (4g + r, l16) of lane
 // 16g + l16) -> rows row0.., columns col0.. of two bf16 planes with row pitch D.
 // Adjacent lanes swap one row pair element (DPP quad_perm [1,0,3,2]) so that

@@ -90,6 +90,27 @@ def test_ce_bf16(gpu_lib, monkeypatch, path):
     assert _rel(dh, rdh) < 2e-2 and _rel(dw, rdw) < 2e-2
 
 
+@pytest.mark.parametrize("d", [128, 96])
+def test_ce_bf16_tile_paths(gpu_lib, monkeypatch, d):
+    """bf16 hidden sizes that take the 256 x 256 logits tiles (d % 64 == 0) and the
+    256 x 128 tiles (d = 96): loss, gradients through the hand-written backward
+    GEMMs, per-token losses and the argmax-based accuracy counts."""
+    from qllm2_amd.fused_ce import linear_ce_per_token, linear_ce_stats
+    _select_gemm(monkeypatch, "hip")
+    h, w, t = _data(300, d, 700, 11 + d, torch.bfloat16, e_std=0.1)
+    t[::9] = -100
+    loss, dh, dw = _gpu(h, w, t, chunk=256)
+    ref, denom = O.ce_forward(h.double(), w.double(), t, chunk=256)
+    rdh, rdw = O.ce_backward(h.double(), w.double(), t, denom, chunk=256)
+    assert _rel(loss, ref) < 2e-2
+    assert _rel(dh, rdh) < 2e-2 and _rel(dw, rdw) < 2e-2
+    per = linear_ce_per_token(h.cuda(), w.cuda(), t.cuda()).float().cpu()
+    assert _rel(per, O.ce_per_token(h.double(), w.double(), t)) < 2e-2
+    t2 = (h.float() @ w.float().T).argmax(-1)
+    _, corr, tok = linear_ce_stats(h.cuda(), w.cuda(), t2.cuda())
+    assert tok == 300 and corr >= 297  # bf16 logits may reorder near-ties
+
+
 def test_ce_per_token_and_stats(gpu_lib):
     from qllm2_amd.fused_ce import linear_ce_per_token, linear_ce_stats
     h, w, t = _data(150, 64, 400, 7, torch.float32)

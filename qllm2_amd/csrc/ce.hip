@@ -867,6 +867,91 @@ __device__ __forceinline__ void wgemm_tile(const U16 *A, int64_t lda, int a_rows
     if (kt < KT) wmma_stage(sA0, sB0, acc, arow0, brow0, l16, g);
 }
 
+// The same tile product with the operands streamed global -> LDS by direct
+// (no register) loads: four LDS stages of k = 32 (128 KiB), the loads of k-step
+// kt + 3 issued when k-step kt starts, so each load has three k-steps to land.
+// Each direct load writes 64 lanes x 16 bytes = 16 rows x 64 bytes contiguously;
+// the 16-byte chunks of a row are XOR-swizzled (chunk c of row r at c ^ ((r >> 1) & 3))
+// so that the fragment reads (16 rows, one chunk) hit distinct banks.  Separate
+// arrays per stage let the compiler's memory-counter tracking tell the stages apart;
+// the wait before each barrier is explicit: every k-step issues exactly four
+// direct loads per wave (past the end they re-read the last k-step into a free
+// stage), so "own loads of the next k-step done" is vmcnt <= 8.
+constexpr int DK = 32, DSTAGES = 4;
+constexpr bool USE_DMA = true;                  // direct-load mainloop (else register-staged)
+constexpr size_t KSMEM = USE_DMA ? 0 : WSMEM;   // dynamic LDS of the tile kernels
+__device__ __forceinline__ int swz(int row, int c) { return c ^ ((row >> 1) & 3); }
+
+template <int S>
+__device__ __forceinline__ void dma_stage(U16 (&sA)[TM * DK], U16 (&sB)[TN * DK], const U16 *A, int64_t lda,
+                                          int a_rows, const U16 *B, int64_t ldb, int b_rows, int k0) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int r0 = 32 * w + 16 * j, row = r0 + (lane >> 2), c = swz(row, lane & 3);
+        __builtin_amdgcn_global_load_lds(A + (int64_t)min(row, a_rows - 1) * lda + k0 + 8 * c, &sA[r0 * DK], 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(B + (int64_t)min(row, b_rows - 1) * ldb + k0 + 8 * c, &sB[r0 * DK], 16, 0, 0);
+    }
+}
+
+__device__ __forceinline__ void dma_mma(const U16 *sA, const U16 *sB, floatx4 (&acc)[4][8], int arow0, int brow0,
+                                        int l16, int g) {
+    bf16x8 af[4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+        const int row = arow0 + 16 * mi + l16;
+        af[mi] = *reinterpret_cast<const bf16x8 *>(sA + row * DK + 8 * swz(row, g));
+    }
+#pragma unroll
+    for (int ni = 0; ni < 8; ++ni) {
+        const int row = brow0 + 16 * ni + l16;
+        const bf16x8 bfr = *reinterpret_cast<const bf16x8 *>(sB + row * DK + 8 * swz(row, g));
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+            acc[mi][ni] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mi], bfr, acc[mi][ni], 0, 0, 0);
+    }
+}
+
+// s_waitcnt with vmcnt <= 8 and the other counters unconstrained
+constexpr int WAIT_VM8 = 8 | 0x70 | 0xF00;
+
+__device__ __forceinline__ void wgemm_tile_dma(const U16 *A, int64_t lda, int a_rows, const U16 *B, int64_t ldb,
+                                               int b_rows, int K, floatx4 (&acc)[4][8]) {
+    __shared__ __align__(16) U16 sA0[TM * DK], sA1[TM * DK], sA2[TM * DK], sA3[TM * DK];
+    __shared__ __align__(16) U16 sB0[TN * DK], sB1[TN * DK], sB2[TN * DK], sB3[TN * DK];
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int arow0 = 64 * (w >> 1), brow0 = 128 * (w & 1);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 8; ++ni) acc[mi][ni] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int KT = K / DK;
+    dma_stage<0>(sA0, sB0, A, lda, a_rows, B, ldb, b_rows, 0);
+    dma_stage<1>(sA1, sB1, A, lda, a_rows, B, ldb, b_rows, min(1, KT - 1) * DK);
+    dma_stage<2>(sA2, sB2, A, lda, a_rows, B, ldb, b_rows, min(2, KT - 1) * DK);
+    __builtin_amdgcn_s_waitcnt(WAIT_VM8);
+    __builtin_amdgcn_s_barrier();
+#define QPAM_DMA_STEP(KT_, CUR_A, CUR_B, NXT_A, NXT_B, NS)                                                    \
+    dma_stage<NS>(NXT_A, NXT_B, A, lda, a_rows, B, ldb, b_rows, min((KT_) + 3, KT - 1) * DK);                 \
+    __builtin_amdgcn_sched_barrier(0);                                                                         \
+    dma_mma(CUR_A, CUR_B, acc, arow0, brow0, l16, g);                                                          \
+    __builtin_amdgcn_s_waitcnt(WAIT_VM8);                                                                      \
+    __builtin_amdgcn_s_barrier();
+    int kt = 0;
+    for (; kt + 3 < KT; kt += 4) {
+        QPAM_DMA_STEP(kt, sA0, sB0, sA3, sB3, 3)
+        QPAM_DMA_STEP(kt + 1, sA1, sB1, sA0, sB0, 0)
+        QPAM_DMA_STEP(kt + 2, sA2, sB2, sA1, sB1, 1)
+        QPAM_DMA_STEP(kt + 3, sA3, sB3, sA2, sB2, 2)
+    }
+    if (kt < KT) { QPAM_DMA_STEP(kt, sA0, sB0, sA3, sB3, 3) }
+    if (kt + 1 < KT) { QPAM_DMA_STEP(kt + 1, sA1, sB1, sA0, sB0, 0) }
+    if (kt + 2 < KT) { QPAM_DMA_STEP(kt + 2, sA2, sB2, sA1, sB1, 1) }
+#undef QPAM_DMA_STEP
+    // drain the direct loads still in flight before the LDS is reused or the wave ends
+    __builtin_amdgcn_s_waitcnt(0 | 0x70 | 0xF00);
+}
+
 __device__ __forceinline__ int xcd_item(int bid, int total) { return big::xcd_item(bid, total); }
 
 // forward: per (256 rows, 256 vocab) tile -> per-row (max, sum exp, argmax)
@@ -882,8 +967,13 @@ __global__ void __launch_bounds__(WTHREADS) fwd_tile_kernel(FwdParams p) {
     big::grouped_tile(item, n_rt, p.n_vt, rt, vt);
     const int r0 = rt * TM, v0 = vt * TN;
     floatx4 acc[4][8];
-    wgemm_tile((const U16 *)a.h + (int64_t)r0 * a.ldh, a.ldh, min(TM, a.N - r0), (const U16 *)a.w + (int64_t)v0 * a.ldw,
-               a.ldw, min(TN, a.V - v0), a.D, acc, reinterpret_cast<U16 *>(smem_raw));
+    if constexpr (USE_DMA)
+        wgemm_tile_dma((const U16 *)a.h + (int64_t)r0 * a.ldh, a.ldh, min(TM, a.N - r0),
+                       (const U16 *)a.w + (int64_t)v0 * a.ldw, a.ldw, min(TN, a.V - v0), a.D, acc);
+    else
+        wgemm_tile((const U16 *)a.h + (int64_t)r0 * a.ldh, a.ldh, min(TM, a.N - r0),
+                   (const U16 *)a.w + (int64_t)v0 * a.ldw, a.ldw, min(TN, a.V - v0), a.D, acc,
+                   reinterpret_cast<U16 *>(smem_raw));
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const int wm = w >> 1, wn = w & 1;
 #pragma unroll
@@ -965,9 +1055,13 @@ __global__ void __launch_bounds__(WTHREADS) grad_tile_kernel(BwdParams p) {
         sTgt[tid] = tg;
     }
     floatx4 acc[4][8];
-    wgemm_tile((const U16 *)a.h + (int64_t)(p.row0 + lr0) * a.ldh, a.ldh, min(TM, p.rows - lr0),
-               (const U16 *)a.w + (int64_t)v0 * a.ldw, a.ldw, min(TN, a.V - v0), a.D, acc,
-               reinterpret_cast<U16 *>(smem_raw));
+    if constexpr (USE_DMA)
+        wgemm_tile_dma((const U16 *)a.h + (int64_t)(p.row0 + lr0) * a.ldh, a.ldh, min(TM, p.rows - lr0),
+                       (const U16 *)a.w + (int64_t)v0 * a.ldw, a.ldw, min(TN, a.V - v0), a.D, acc);
+    else
+        wgemm_tile((const U16 *)a.h + (int64_t)(p.row0 + lr0) * a.ldh, a.ldh, min(TM, p.rows - lr0),
+                   (const U16 *)a.w + (int64_t)v0 * a.ldw, a.ldw, min(TN, a.V - v0), a.D, acc,
+                   reinterpret_cast<U16 *>(smem_raw));
     const int w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const int wm = w >> 1, wn = w & 1;
     U16 *G = (U16 *)p.gbuf;
@@ -1050,9 +1144,9 @@ int run_fwd(const qpam_ce_fwd_args &a, hipStream_t stream) {
     int st;
     if (wide_tiles) {
         QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)wide::fwd_tile_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide::WSMEM));
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide::KSMEM));
         dim3 grid(big::xcd_grid(p.n_vt * ((a.N + wide::TM - 1) / wide::TM)));
-        hipLaunchKernelGGL(wide::fwd_tile_kernel, grid, dim3(wide::WTHREADS), wide::WSMEM, stream, p);
+        hipLaunchKernelGGL(wide::fwd_tile_kernel, grid, dim3(wide::WTHREADS), wide::KSMEM, stream, p);
         st = launch_status("ce fwd_tile_kernel (bf16, 256 x 256)");
     } else if (is_bf<T>()) {
         QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::fwd_tile_kernel,
@@ -1091,7 +1185,7 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
     // the G-tile kernel: 256 x 256 tiles, or 256 x 128 for hidden sizes that are not
     // a multiple of 64 (Vp and Rp are multiples of both)
     const void *gkern = wide_tiles ? (const void *)wide::grad_tile_kernel : (const void *)big::grad_tile_kernel;
-    const size_t gsmem = wide_tiles ? wide::WSMEM : big::SMEM;
+    const size_t gsmem = wide_tiles ? wide::KSMEM : big::SMEM;
     auto launch_grad = [&]() {
         const int tiles = (p.Vp / (wide_tiles ? wide::TN : big::BTN)) * (p.Rp / big::BTM);
         if (wide_tiles)

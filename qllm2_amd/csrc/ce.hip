@@ -219,7 +219,7 @@ __global__ void __launch_bounds__(THREADS) ce_fwd_finalize_kernel(FwdParams p) {
     for (int vt = lane; vt < p.n_vt; vt += 64) {
         const int64_t o = (int64_t)row * p.n_vt + vt;
         const float pm = p.part_m[o], ps = p.part_s[o];
-        const int pi = p.part_i[o];
+        const int pi = a.correct ? p.part_i[o] : 0;  // tile argmax, written only when requested
         if (pm > m || (pm == m && pi < ix)) ix = pi;
         const float nm = fmaxf(m, pm);
         s = (m > -INFINITY ? s * __expf(m - nm) : 0.f) + (pm > -INFINITY ? ps * __expf(pm - nm) : 0.f);
@@ -954,7 +954,11 @@ __device__ __forceinline__ void wgemm_tile_dma(const U16 *A, int64_t lda, int a_
 
 __device__ __forceinline__ int xcd_item(int bid, int total) { return big::xcd_item(bid, total); }
 
-// forward: per (256 rows, 256 vocab) tile -> per-row (max, sum exp, argmax)
+// forward: per (256 rows, 256 vocab) tile -> per-row (max, sum exp[, argmax]).
+// Row statistics over a wave's 128 columns: per lane over its 8 columns, then
+// across the 16 lanes that hold the row (DPP); the argmax (first column at the
+// maximum) only when accuracy counts are requested.
+template <bool ARGMAX>
 __global__ void __launch_bounds__(WTHREADS) fwd_tile_kernel(FwdParams p) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     __shared__ float sM[2][TM], sS[2][TM];
@@ -976,37 +980,34 @@ __global__ void __launch_bounds__(WTHREADS) fwd_tile_kernel(FwdParams p) {
                    reinterpret_cast<U16 *>(smem_raw));
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const int wm = w >> 1, wn = w & 1;
+    const int vl = v0 + 128 * wn + l16;  // this lane's column in tile ni: vl + 16 ni
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            float mx = -INFINITY;
-            int ix = 0x7fffffff;
+            float lm = -INFINITY;
 #pragma unroll
-            for (int ni = 0; ni < 8; ++ni) {
-                const int v = v0 + 128 * wn + 16 * ni + l16;
-                const float x = (v < a.V) ? acc[mi][ni][r] : -INFINITY;
-                if (x > mx) { mx = x; ix = v; }
-            }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) {
-                const float om = __shfl_xor(mx, off);
-                const int oi = __shfl_xor(ix, off);
-                if (om > mx || (om == mx && oi < ix)) { mx = om; ix = oi; }
-            }
+            for (int ni = 0; ni < 8; ++ni)
+                if (vl + 16 * ni < a.V) lm = fmaxf(lm, acc[mi][ni][r]);
+            const float mx = row16_max(lm);
             float s = 0.f;
+            int ix = 0x7fffffff;
+            if (mx > -INFINITY) {
 #pragma unroll
-            for (int ni = 0; ni < 8; ++ni) {
-                const int v = v0 + 128 * wn + 16 * ni + l16;
-                if (v < a.V) s += __expf(acc[mi][ni][r] - mx);
+                for (int ni = 0; ni < 8; ++ni)
+                    if (vl + 16 * ni < a.V) {
+                        const float x = acc[mi][ni][r];
+                        s += __expf(x - mx);
+                        if (ARGMAX && x == mx) ix = min(ix, vl + 16 * ni);
+                    }
             }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
+            s = row16_sum(s);
+            if (ARGMAX) ix = row16_min(ix);
             if (l16 == 0) {
                 const int row = 64 * wm + 16 * mi + 4 * g + r;
                 sM[wn][row] = mx;
                 sS[wn][row] = s;
-                sI[wn][row] = ix;
+                if (ARGMAX) sI[wn][row] = ix;
             }
         }
     }
@@ -1017,11 +1018,10 @@ __global__ void __launch_bounds__(WTHREADS) fwd_tile_kernel(FwdParams p) {
         float s = 0.f;
         if (m0 > -INFINITY) s += sS[0][tid] * __expf(m0 - m);
         if (m1 > -INFINITY) s += sS[1][tid] * __expf(m1 - m);
-        const int i = (m1 > m0 || (m1 == m0 && sI[1][tid] < sI[0][tid])) ? sI[1][tid] : sI[0][tid];
         const int64_t o = (int64_t)(r0 + tid) * p.n_vt + vt;
         p.part_m[o] = m;
         p.part_s[o] = s;
-        p.part_i[o] = i;
+        if (ARGMAX) p.part_i[o] = (m1 > m0 || (m1 == m0 && sI[1][tid] < sI[0][tid])) ? sI[1][tid] : sI[0][tid];
     }
 }
 
@@ -1143,10 +1143,14 @@ int run_fwd(const qpam_ce_fwd_args &a, hipStream_t stream) {
     p.red = nullptr;
     int st;
     if (wide_tiles) {
-        QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)wide::fwd_tile_kernel,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide::KSMEM));
+        // the argmax (accuracy counts) only when requested
+        const void *kern = a.correct ? (const void *)wide::fwd_tile_kernel<true> : (const void *)wide::fwd_tile_kernel<false>;
+        QPAM_CHECK_HIP(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)wide::KSMEM));
         dim3 grid(big::xcd_grid(p.n_vt * ((a.N + wide::TM - 1) / wide::TM)));
-        hipLaunchKernelGGL(wide::fwd_tile_kernel, grid, dim3(wide::WTHREADS), wide::KSMEM, stream, p);
+        if (a.correct)
+            hipLaunchKernelGGL(wide::fwd_tile_kernel<true>, grid, dim3(wide::WTHREADS), wide::KSMEM, stream, p);
+        else
+            hipLaunchKernelGGL(wide::fwd_tile_kernel<false>, grid, dim3(wide::WTHREADS), wide::KSMEM, stream, p);
         st = launch_status("ce fwd_tile_kernel (bf16, 256 x 256)");
     } else if (is_bf<T>()) {
         QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::fwd_tile_kernel,

@@ -62,6 +62,36 @@ __device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(unsigned, __builtin_convertvector(floatx2{lo, hi}, bf16x2));
 }
 
+// DPP lane permutations (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror,
+// row_mirror) and reductions over the 16 lanes of a DPP row: every lane of the
+// row ends with the result.  Four steps: pairs, quads, halves, rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f<0xB1>(x));
+    x = fmaxf(x, dpp_f<0x4E>(x));
+    x = fmaxf(x, dpp_f<0x141>(x));
+    return fmaxf(x, dpp_f<0x140>(x));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f<0xB1>(x);
+    x += dpp_f<0x4E>(x);
+    x += dpp_f<0x141>(x);
+    return x + dpp_f<0x140>(x);
+}
+__device__ __forceinline__ int row16_min(int x) {
+    x = min(x, dpp_i<0xB1>(x));
+    x = min(x, dpp_i<0x4E>(x));
+    x = min(x, dpp_i<0x141>(x));
+    return min(x, dpp_i<0x140>(x));
+}
+
 template <typename T> struct Elem;
 template <> struct Elem<float> {
     __device__ __forceinline__ static float load(const float *p) { return *p; }

@@ -1,4 +1,6 @@
 // Error plumbing and version of the qpam C ABI.
+#include <map>
+
 #include "common.h"
 
 namespace qpam {
@@ -18,6 +20,29 @@ int fail(int code, const char *fmt, ...) {
     return code;
 }
 
+}  // namespace qpam
+
+namespace qpam {
+std::mutex &side_stream_mutex() {
+    static std::mutex mu;
+    return mu;
+}
+
+int side_stream(SideStream *&out) {
+    static std::map<int, SideStream> streams;  // guarded by side_stream_mutex()
+    int dev = 0;
+    QPAM_CHECK_HIP(hipGetDevice(&dev));
+    auto it = streams.find(dev);
+    if (it == streams.end()) {
+        SideStream s;
+        QPAM_CHECK_HIP(hipStreamCreateWithFlags(&s.side, hipStreamNonBlocking));
+        QPAM_CHECK_HIP(hipEventCreateWithFlags(&s.fork, hipEventDisableTiming));
+        QPAM_CHECK_HIP(hipEventCreateWithFlags(&s.join, hipEventDisableTiming));
+        it = streams.emplace(dev, s).first;
+    }
+    out = &it->second;
+    return QPAM_OK;
+}
 }  // namespace qpam
 
 extern "C" int qpam_version(void) { return 1; }

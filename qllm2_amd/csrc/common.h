@@ -9,6 +9,8 @@
 #include <cstdio>
 #include <string>
 
+#include <mutex>
+
 #include "../../include/qpam.h"
 
 namespace qpam {
@@ -30,11 +32,44 @@ int fail(int code, const char *fmt, ...);
         if (!(cond)) return ::qpam::fail(QPAM_ERR_ARG, __VA_ARGS__);            \
     } while (0)
 
+// Fork / join of two independent launch sequences of one call: `side` is an
+// extra stream of the current device (non-blocking, default priority) created on
+// first use and kept until the process ends, with a pair of events.  The caller
+// holds `lock()` from the fork until the join is enqueued, so concurrent callers
+// do not interleave their event records.
+struct SideStream {
+    hipStream_t side;
+    hipEvent_t fork, join;
+};
+int side_stream(SideStream *&out);
+std::mutex &side_stream_mutex();
+
 inline int launch_status(const char *what) {
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return fail(QPAM_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(err));
     return QPAM_OK;
 }
+
+// Runs on_side(side) and on_main(stream) concurrently, both after the work already
+// queued on `stream`; `stream` continues after both (event fork / join, which HIP
+// graph capture of `stream` follows).  Each callable enqueues launches and
+// returns a status.
+template <typename FS, typename FM>
+int fork_join(hipStream_t stream, FS &&on_side, FM &&on_main) {
+    std::lock_guard<std::mutex> lock(side_stream_mutex());
+    SideStream *ss = nullptr;
+    int st = side_stream(ss);
+    if (st) return st;
+    if (hipEventRecord(ss->fork, stream) != hipSuccess || hipStreamWaitEvent(ss->side, ss->fork, 0) != hipSuccess)
+        return fail(QPAM_ERR_HIP, "fork_join: fork failed");
+    const int st_side = on_side(ss->side);
+    const int st_main = on_main(stream);
+    // join even after a failed launch, so `stream` never runs ahead of side work
+    if (hipEventRecord(ss->join, ss->side) != hipSuccess || hipStreamWaitEvent(stream, ss->join, 0) != hipSuccess)
+        return fail(QPAM_ERR_HIP, "fork_join: join failed");
+    return st_side ? st_side : st_main;
+}
+
 
 // ------------------------------------------------------------- vectors -----
 typedef float floatx4 __attribute__((ext_vector_type(4)));

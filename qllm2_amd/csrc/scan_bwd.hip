@@ -1640,11 +1640,19 @@ int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
-    hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(PASS_THREADS), s1, stream, p);
-    int st = launch_status("grad_pass_bf16_kernel");
-    if (st) return st;
-    hipLaunchKernelGGL(query_side_bf16_kernel<M>, grid, dim3(THREADS), s3, stream, p);
-    st = launch_status("query_side_bf16_kernel");
+    // the gradient-state pass (a sequential chain over 288-ish blocks) and the query
+    // side (reads only forward snapshots) are independent: run them concurrently;
+    // the key side needs both
+    int st = fork_join(
+        stream,
+        [&](hipStream_t s) {
+            hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(PASS_THREADS), s1, s, p);
+            return launch_status("grad_pass_bf16_kernel");
+        },
+        [&](hipStream_t s) {
+            hipLaunchKernelGGL(query_side_bf16_kernel<M>, grid, dim3(THREADS), s3, s, p);
+            return launch_status("query_side_bf16_kernel");
+        });
     if (st) return st;
     hipLaunchKernelGGL(key_side_bf16_kernel<M>, grid, dim3(THREADS), s4, stream, p);
     return launch_status("key_side_bf16_kernel");
@@ -1678,14 +1686,20 @@ int launch_bwd(const BwdParams &p, hipStream_t stream) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_kernel<Tin, C>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
-    hipLaunchKernelGGL((grad_chunk_state_kernel<Tin, C>), grid, dim3(THREADS), s1, stream, p);
-    int st = launch_status("grad_chunk_state_kernel");
-    if (st) return st;
-    hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, stream, p);
-    st = launch_status("grad_state_scan_kernel");
-    if (st) return st;
-    hipLaunchKernelGGL((query_side_kernel<Tin, C>), grid, dim3(THREADS), s3, stream, p);
-    st = launch_status("query_side_kernel");
+    // gradient-state chain and query side concurrently (independent); key side after both
+    int st = fork_join(
+        stream,
+        [&](hipStream_t s) {
+            hipLaunchKernelGGL((grad_chunk_state_kernel<Tin, C>), grid, dim3(THREADS), s1, s, p);
+            int r = launch_status("grad_chunk_state_kernel");
+            if (r) return r;
+            hipLaunchKernelGGL(grad_state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, s, p);
+            return launch_status("grad_state_scan_kernel");
+        },
+        [&](hipStream_t s) {
+            hipLaunchKernelGGL((query_side_kernel<Tin, C>), grid, dim3(THREADS), s3, s, p);
+            return launch_status("query_side_kernel");
+        });
     if (st) return st;
     hipLaunchKernelGGL((key_side_kernel<Tin, C>), grid, dim3(THREADS), s4, stream, p);
     return launch_status("key_side_kernel");

@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=1000)
-    ap.add_argument("--only", choices=["scan_fwd", "decode", "e3", "ce", "copy"], default=None,
+    ap.add_argument("--only", choices=["scan_fwd", "decode", "e3", "ce", "cplx", "copy"], default=None,
                     help="run one workload (for profiler passes) and print its own JSON line")
     return ap.parse_args()
 
@@ -211,6 +211,48 @@ def bench_ce(steps, warmup):
             "config": "N=16384 D=1024 V=50261 bf16, chunk=4096, fwd+bwd"}
 
 
+def bench_complex_ops(steps, warmup):
+    """Complex elementwise layers (ComplexNorm, ModSwish, CGU gate), forward +
+    backward, on [16384, 1024] complex bf16 rows (a 16k-token batch at dim 1024).
+    HBM-bound: algorithmic bytes per call are the complex tensors read and
+    written (2 bytes per real), parameters aside."""
+    import torch
+    from qllm2_amd import triton_kernels as tk
+    rows, dim = 16384, 1024
+    g = torch.Generator(device="cuda").manual_seed(9)
+    z = torch.randn(rows, dim, 2, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    up = torch.randn(rows, dim, 2, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    gout = torch.randn(rows, dim, 2, device="cuda", generator=g).to(torch.bfloat16)
+    scale = torch.ones(dim, device="cuda", requires_grad=True)
+    bias = torch.zeros(dim, device="cuda", requires_grad=True)
+    beta = torch.ones(dim, device="cuda", requires_grad=True)
+    el = rows * dim * 2 * 2  # bytes of one complex bf16 tensor
+    cases = {
+        # forward reads z (+ up), writes out; backward reads z (+ up) and gout, writes gz (+ gup)
+        "complex_norm": (lambda: tk.fused_complex_norm(z, scale), (z, scale), 2 * el + 3 * el),
+        "mod_swish": (lambda: tk.fused_mod_swish(z, bias, beta), (z, bias, beta), 2 * el + 3 * el),
+        "cgu_gate": (lambda: tk.fused_cgu_gate(z, up), (z, up), 3 * el + 5 * el),
+    }
+    res = {}
+    for name, (fn, inputs, nbytes) in cases.items():
+        def step():
+            torch.autograd.grad(fn(), inputs, gout)  # no .grad accumulation in the timed loop
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        res[name] = {"ms_fwd_bwd": ms, "GBps": nbytes / (ms * 1e-3) / 1e9,
+                     "hbm_frac": nbytes / (ms * 1e-3) / HBM_PEAK, "bytes": nbytes}
+    res["config"] = "rows=16384 dim=1024 complex bf16, fwd+bwd"
+    return res
+
+
 def cpu_baseline_scan():
     """The reference's chunk loop restated on the CPU (oracle.pam.chunked_head),
     fp32, on a bounded sample: 1 of the 8 batch rows (H=12, T=2048)."""
@@ -244,6 +286,7 @@ def main():
               "decode": lambda: bench_decode(args.decode_steps),
               "e3": lambda: bench_e3_fwd_bwd(args.steps, args.warmup),
               "ce": lambda: bench_ce(args.steps, args.warmup),
+              "cplx": lambda: bench_complex_ops(args.steps, args.warmup),
               "copy": copy_calibration}[args.only]
         print(json.dumps({"only": args.only, "result": fn()}), flush=True)
         return
@@ -277,7 +320,8 @@ def main():
     if not args.no_extras:
         out["extras"] = {"decode_config4": bench_decode(args.decode_steps),
                          "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 2),
-                         "ce_fwd_bwd_config5": bench_ce(max(3, args.steps // 4), 2)}
+                         "ce_fwd_bwd_config5": bench_ce(max(3, args.steps // 4), 2),
+                         "complex_elementwise": bench_complex_ops(max(3, args.steps // 2), 2)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_scan()
     print(json.dumps(out), flush=True)

@@ -27,6 +27,10 @@
  *                       v11/triton_kernels.py:447-480 for the decay matrix)
  *   qpam_decay_matrix   v11/triton_kernels.py:570-573 fused_decay_matrix
  *                       (forward, v11/triton_kernels.py:170-202, 420-445)
+ *   qpam_cplx_fwd       v11/triton_kernels.py:489-520 public fused_complex_norm,
+ *                       fused_mod_swish, fused_mod_relu, fused_cgu_gate
+ *                       (forward kernels :48-166)
+ *   qpam_cplx_bwd       their autograd backward (v11/triton_kernels.py:209-395)
  *   qpam_ce_fwd         v11/fused_ce.py:28-53   _FusedLinearCE.forward
  *                       v11/fused_ce.py:98-141  linear_ce_per_token /
  *                                               linear_ce_stats
@@ -165,6 +169,41 @@ int qpam_scan_bwd(const qpam_scan_bwd_args *a, void *stream);
  * D [N, T, T] fp32 contiguous, D[t,s] = exp(min(c_s - c_t, 0)) for s <= t
  * else 0, c = cumsum(-log(gamma + 1e-6)).  T <= 4096. */
 int qpam_decay_matrix(int32_t n, int32_t t, const float *gamma, int64_t ldg, float *out, void *stream);
+
+/* ------------------------------------------------ complex elementwise -----
+ * Split-real complex tensors [rows, dim, 2] (interleaved re/im, contiguous),
+ * fp32 or bf16; per-column parameters fp32 [dim].  Ops (z = gate for the CGU):
+ *   NORM       out = z/(|z|+1e-8) * (|z|/rms) * scale, rms = sqrt(mean|z|^2 + eps)
+ *   MOD_SWISH  out = z/(|z|+1e-8) * |z| sigmoid(beta |z| + bias)
+ *   MOD_RELU   out = z/(|z|+1e-8) * relu(|z| + bias)
+ *   CGU_GATE   out = sigmoid(|z|) * (z/(|z|+1e-8)) * up
+ * with |z| = sqrt(re^2 + im^2 + 1e-8).  The backward writes gz (and gup), and
+ * the parameter gradients gp0 (scale / bias) and gp1 (beta) as fp32 column
+ * sums (deterministic: per-block partials in the workspace, summed in order).
+ * dim * (number of parameters) <= 8192. */
+enum { QPAM_CPLX_NORM = 0, QPAM_CPLX_MOD_SWISH = 1, QPAM_CPLX_MOD_RELU = 2, QPAM_CPLX_CGU_GATE = 3 };
+
+typedef struct {
+    int32_t op;            /* QPAM_CPLX_* */
+    int32_t dtype;         /* of z, up, out and the tensor gradients */
+    int64_t rows;
+    int32_t dim;
+    float eps;             /* NORM */
+    const void *z;         /* [rows][dim][2] (the gate of CGU_GATE) */
+    const void *up;        /* CGU_GATE */
+    const float *p0;       /* NORM: scale; MOD_*: bias */
+    const float *p1;       /* MOD_SWISH: beta */
+    void *out;             /* forward output */
+    const void *gout;      /* backward: gradient of out */
+    void *gz, *gup;        /* backward: gradients of z / up */
+    float *gp0, *gp1;      /* backward: parameter gradients [dim] */
+    void *workspace;       /* backward: qpam_cplx_workspace_size bytes */
+    size_t workspace_bytes;
+} qpam_cplx_args;
+
+size_t qpam_cplx_workspace_size(const qpam_cplx_args *a);
+int qpam_cplx_fwd(const qpam_cplx_args *a, void *stream);
+int qpam_cplx_bwd(const qpam_cplx_args *a, void *stream);
 
 /* -------------------------------------------------------------------- CE --
  * Tied complex LM-head cross-entropy over hidden rows H [N, D] and weights

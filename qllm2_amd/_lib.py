@@ -96,6 +96,18 @@ class CeBwdArgs(ctypes.Structure):
     ]
 
 
+QPAM_CPLX_NORM, QPAM_CPLX_MOD_SWISH, QPAM_CPLX_MOD_RELU, QPAM_CPLX_CGU_GATE = 0, 1, 2, 3
+
+
+class CplxArgs(ctypes.Structure):
+    _fields_ = [
+        ("op", c_i32), ("dtype", c_i32), ("rows", c_i64), ("dim", c_i32), ("eps", c_f32),
+        ("z", c_ptr), ("up", c_ptr), ("p0", c_ptr), ("p1", c_ptr), ("out", c_ptr),
+        ("gout", c_ptr), ("gz", c_ptr), ("gup", c_ptr), ("gp0", c_ptr), ("gp1", c_ptr),
+        ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 # symbol -> (restype, argtypes); every symbol include/qpam.h declares
 SIGNATURES = {
     "qpam_version": (ctypes.c_int, []),
@@ -113,6 +125,9 @@ SIGNATURES = {
     "qpam_ce_fwd": (ctypes.c_int, [ctypes.POINTER(CeFwdArgs), c_ptr]),
     "qpam_ce_bwd_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(CeBwdArgs)]),
     "qpam_ce_bwd": (ctypes.c_int, [ctypes.POINTER(CeBwdArgs), c_ptr]),
+    "qpam_cplx_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(CplxArgs)]),
+    "qpam_cplx_fwd": (ctypes.c_int, [ctypes.POINTER(CplxArgs), c_ptr]),
+    "qpam_cplx_bwd": (ctypes.c_int, [ctypes.POINTER(CplxArgs), c_ptr]),
 }
 
 _LIB = None

@@ -1,0 +1,797 @@
+// Complex elementwise layers on split-real [rows, dim, 2] tensors (interleaved
+// re/im), forward and backward.
+//
+// Reference: the public API of v11/triton_kernels.py — fused_complex_norm
+// (forward kernel :48-79, autograd backward :209-260), fused_mod_swish
+// (:83-108, :263-304), fused_mod_relu (:112-135, :307-345), fused_cgu_gate
+// (:139-166, :348-395); the PyTorch forms they replace are :489-520.  The
+// backward formulas here are the closed forms of those autograd Functions.
+//
+// Layout and parallelism: every op is HBM-bound (a few flops per 8-byte complex
+// element).  Forward elementwise ops run a flat grid-stride loop of complex
+// elements (8-byte fp32 / 4-byte bf16 accesses, consecutive lanes on consecutive
+// columns).  ComplexNorm (a row reduction) and the backward of the ops with
+// per-column parameters run one wave per row, lanes over columns: the row sums
+// use a wave reduction, and the parameter gradients (column sums over rows)
+// accumulate in a per-wave LDS slice that each block folds in fixed order into
+// a [block][dim] partial, summed over blocks by a second kernel — deterministic,
+// no atomics.
+#include <algorithm>
+
+#include "common.h"
+
+namespace qpam {
+namespace cplx {
+namespace {
+
+constexpr int THREADS = 256;  // 4 waves
+constexpr int WAVES = THREADS / 64;
+constexpr int MAX_BLOCKS = 2048;  // row-kernel blocks (and column partials)
+constexpr float MAG_EPS = 1e-8f;  // inside the sqrt and added to the magnitude, as the reference
+
+// V consecutive complex elements starting at complex index e: V = 4 moves 16
+// bytes (bf16) or 2 x 16 bytes (fp32) per lane; V = 1 for dims that are not a
+// multiple of 4.
+template <typename T, int V> struct CVec;
+template <int V> struct CVec<float, V> {
+    __device__ __forceinline__ static void load(const float *p, int64_t e, float (&re)[V], float (&im)[V]) {
+        if constexpr (V == 4) {
+            const float4 a = *reinterpret_cast<const float4 *>(p + 2 * e), b = *reinterpret_cast<const float4 *>(p + 2 * e + 4);
+            re[0] = a.x, im[0] = a.y, re[1] = a.z, im[1] = a.w, re[2] = b.x, im[2] = b.y, re[3] = b.z, im[3] = b.w;
+        } else {
+            const float2 a = *reinterpret_cast<const float2 *>(p + 2 * e);
+            re[0] = a.x, im[0] = a.y;
+        }
+    }
+    __device__ __forceinline__ static void store(float *p, int64_t e, const float (&re)[V], const float (&im)[V]) {
+        if constexpr (V == 4) {
+            *reinterpret_cast<float4 *>(p + 2 * e) = make_float4(re[0], im[0], re[1], im[1]);
+            *reinterpret_cast<float4 *>(p + 2 * e + 4) = make_float4(re[2], im[2], re[3], im[3]);
+        } else {
+            *reinterpret_cast<float2 *>(p + 2 * e) = make_float2(re[0], im[0]);
+        }
+    }
+};
+template <int V> struct CVec<unsigned short, V> {
+    __device__ __forceinline__ static void load(const unsigned short *p, int64_t e, float (&re)[V], float (&im)[V]) {
+        if constexpr (V == 4) {
+            const uint4 a = *reinterpret_cast<const uint4 *>(p + 2 * e);
+            const unsigned u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) re[k] = __uint_as_float(u[k] << 16), im[k] = __uint_as_float(u[k] & 0xFFFF0000u);
+        } else {
+            const unsigned u = *reinterpret_cast<const unsigned *>(p + 2 * e);
+            re[0] = __uint_as_float(u << 16), im[0] = __uint_as_float(u & 0xFFFF0000u);
+        }
+    }
+    __device__ __forceinline__ static void store(unsigned short *p, int64_t e, const float (&re)[V],
+                                                 const float (&im)[V]) {
+        if constexpr (V == 4) {
+            *reinterpret_cast<uint4 *>(p + 2 * e) = make_uint4(pack_bf16x2(re[0], im[0]), pack_bf16x2(re[1], im[1]),
+                                                               pack_bf16x2(re[2], im[2]), pack_bf16x2(re[3], im[3]));
+        } else {
+            *reinterpret_cast<unsigned *>(p + 2 * e) = pack_bf16x2(re[0], im[0]);
+        }
+    }
+};
+
+__device__ __forceinline__ float wave_sum(float x) {
+    x = row16_sum(x);
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
+}
+
+// hardware square root / reciprocal (1 ulp): the magnitude is >= 1e-4, so no
+// denormal operands reach them
+__device__ __forceinline__ float magnitude(float re, float im) {
+    return __builtin_amdgcn_sqrtf(re * re + im * im + MAG_EPS);
+}
+__device__ __forceinline__ float rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sigmoidf(float x) { return rcp(1.f + __expf(-x)); }
+
+struct Params {
+    int64_t rows;
+    int dim;
+    float eps;
+    const void *z, *up;
+    const float *p0, *p1;
+    void *out;
+    const void *gout;
+    void *gz, *gup;
+    float *part;  // backward: [blocks][n_params][dim] column partials
+};
+
+// ------------------------------------------------------------------ forward --
+template <typename T, int V>
+__global__ void __launch_bounds__(THREADS) norm_fwd_kernel(Params p) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const T *z = (const T *)p.z;
+    T *out = (T *)p.out;
+    const int groups = p.dim / V;
+    for (int64_t row = (int64_t)blockIdx.x * WAVES + w; row < p.rows; row += (int64_t)gridDim.x * WAVES) {
+        const int64_t e0 = row * p.dim;
+        float ss = 0.f;
+        for (int j = lane; j < groups; j += 64) {
+            float re[V], im[V];
+            CVec<T, V>::load(z, e0 + V * j, re, im);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const float m = magnitude(re[k], im[k]);
+                ss += m * m;
+            }
+        }
+        const float rms = sqrtf(wave_sum(ss) / p.dim + p.eps);
+        for (int j = lane; j < groups; j += 64) {
+            float re[V], im[V];
+            CVec<T, V>::load(z, e0 + V * j, re, im);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const float m = magnitude(re[k], im[k]);
+                const float f = (m / rms) * p.p0[V * j + k] / (m + MAG_EPS);
+                re[k] *= f;
+                im[k] *= f;
+            }
+            CVec<T, V>::store(out, e0 + V * j, re, im);
+        }
+    }
+}
+
+// OP 1: mod swish, 2: mod relu, 3: CGU gate (elementwise)
+template <typename T, int V, int OP>
+__global__ void __launch_bounds__(THREADS) pointwise_fwd_kernel(Params p) {
+    const T *z = (const T *)p.z;
+    T *out = (T *)p.out;
+    const int64_t n = p.rows * p.dim / V;  // groups
+    for (int64_t j = (int64_t)blockIdx.x * THREADS + threadIdx.x; j < n; j += (int64_t)gridDim.x * THREADS) {
+        float re[V], im[V];
+        CVec<T, V>::load(z, V * j, re, im);
+        if constexpr (OP == 3) {
+            float ur[V], ui[V];
+            CVec<T, V>::load((const T *)p.up, V * j, ur, ui);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const float m = magnitude(re[k], im[k]), inv = rcp(m + MAG_EPS), gm = sigmoidf(m);
+                const float pr = re[k] * inv, pi = im[k] * inv;
+                re[k] = (pr * ur[k] - pi * ui[k]) * gm;
+                im[k] = (pr * ui[k] + pi * ur[k]) * gm;
+            }
+        } else {
+            const int c0 = (int)((V * j) % p.dim);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const float m = magnitude(re[k], im[k]), inv = rcp(m + MAG_EPS);
+                const int c = c0 + k;
+                const float act = OP == 1 ? m * sigmoidf(p.p1[c] * m + p.p0[c]) : fmaxf(m + p.p0[c], 0.f);
+                re[k] *= inv * act;
+                im[k] *= inv * act;
+            }
+        }
+        CVec<T, V>::store(out, V * j, re, im);
+    }
+}
+
+// ----------------------------------------------------------------- backward --
+// Rows of this block: [r0, r1); wave w takes r0 + w, r0 + w + WAVES, ...
+__device__ __forceinline__ void block_rows(const Params &p, int64_t &r0, int64_t &r1) {
+    const int64_t per = (p.rows + gridDim.x - 1) / gridDim.x;
+    r0 = (int64_t)blockIdx.x * per;
+    r1 = r0 + per < p.rows ? r0 + per : p.rows;
+}
+
+// fold the per-wave LDS slices [WAVES][NP][dim] into this block's partial
+template <int NP>
+__device__ __forceinline__ void write_partials(const Params &p, const float *acc) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < NP * p.dim; i += THREADS) {
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) s += acc[w * NP * p.dim + i];
+        p.part[(int64_t)blockIdx.x * NP * p.dim + i] = s;
+    }
+}
+
+template <typename T, int V>
+__global__ void __launch_bounds__(THREADS) norm_bwd_kernel(Params p) {
+    extern __shared__ float acc[];  // [WAVES][1][dim]
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float *my = acc + w * p.dim;
+    for (int c = lane; c < p.dim; c += 64) my[c] = 0.f;
+    const T *z = (const T *)p.z, *go = (const T *)p.gout;
+    T *gz = (T *)p.gz;
+    const int groups = p.dim / V;
+    int64_t r0, r1;
+    block_rows(p, r0, r1);
+    for (int64_t row = r0 + w; row < r1; row += WAVES) {
+        const int64_t e0 = row * p.dim;
+        // row sums: sum |z|^2 (the rms) and sum (g . unit) scale |z|
+        float ss = 0.f, sg = 0.f;
+        for (int j = lane; j < groups; j += 64) {
+            float zr[V], zi[V], gr[V], gi[V];
+            CVec<T, V>::load(z, e0 + V * j, zr, zi);
+            CVec<T, V>::load(go, e0 + V * j, gr, gi);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const float m = magnitude(zr[k], zi[k]), inv = rcp(m + MAG_EPS);
+                ss += m * m;
+                sg += (gr[k] * zr[k] * inv + gi[k] * zi[k] * inv) * p.p0[V * j + k] * m;
+            }
+        }
+        ss = wave_sum(ss);
+        sg = wave_sum(sg);
+        const float rms = sqrtf(ss / p.dim + p.eps), inv_rms = 1.f / rms;
+        const float grad_rms = -sg * inv_rms * inv_rms;
+        for (int j = lane; j < groups; j += 64) {
+            float zr[V], zi[V], gr[V], gi[V];
+            CVec<T, V>::load(z, e0 + V * j, zr, zi);
+            CVec<T, V>::load(go, e0 + V * j, gr, gi);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const int c = V * j + k;
+                const float m = magnitude(zr[k], zi[k]), inv = rcp(m + MAG_EPS);
+                const float ur = zr[k] * inv, ui = zi[k] * inv, sc = p.p0[c];
+                const float gs = gr[k] * ur + gi[k] * ui;
+                my[c] += gs * m * inv_rms;
+                const float gmag = gs * sc * inv_rms + grad_rms * m / (p.dim * rms);
+                const float smag = m * inv_rms * sc;
+                const float pr = gr[k] * smag, pi = gi[k] * smag, dot = pr * ur + pi * ui;
+                const float zrk = zr[k], zik = zi[k];
+                zr[k] = (pr - ur * dot) * inv + gmag * zrk / m;
+                zi[k] = (pi - ui * dot) * inv + gmag * zik / m;
+            }
+            CVec<T, V>::store(gz, e0 + V * j, zr, zi);
+        }
+    }
+    write_partials<1>(p, acc);
+}
+
+// OP 1: mod swish (partials d bias, d beta), 2: mod relu (d bias)
+template <typename T, int V, int OP>
+__global__ void __launch_bounds__(THREADS) act_bwd_kernel(Params p) {
+    constexpr int NP = OP == 1 ? 2 : 1;
+    extern __shared__ float acc[];  // [WAVES][NP][dim]
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float *my = acc + w * NP * p.dim;
+    for (int c = lane; c < NP * p.dim; c += 64) my[c] = 0.f;
+    const T *z = (const T *)p.z, *go = (const T *)p.gout;
+    T *gz = (T *)p.gz;
+    const int groups = p.dim / V;
+    int64_t r0, r1;
+    block_rows(p, r0, r1);
+    for (int64_t row = r0 + w; row < r1; row += WAVES) {
+        const int64_t e0 = row * p.dim;
+        for (int j = lane; j < groups; j += 64) {
+            float zr[V], zi[V], gr[V], gi[V];
+            CVec<T, V>::load(z, e0 + V * j, zr, zi);
+            CVec<T, V>::load(go, e0 + V * j, gr, gi);
+#pragma unroll
+            for (int k = 0; k < V; ++k) {
+                const int c = V * j + k;
+                const float m = magnitude(zr[k], zi[k]), inv = rcp(m + MAG_EPS);
+                const float ur = zr[k] * inv, ui = zi[k] * inv;
+                const float da = gr[k] * ur + gi[k] * ui;  // d activated
+                float act, dmag;
+                if constexpr (OP == 1) {
+                    const float beta = p.p1[c], s = sigmoidf(beta * m + p.p0[c]), sd = s * (1.f - s);
+                    act = m * s;
+                    dmag = da * (s + m * beta * sd);
+                    my[c] += da * m * sd;
+                    my[p.dim + c] += da * m * m * sd;
+                } else {
+                    const float x = m + p.p0[c];
+                    act = fmaxf(x, 0.f);
+                    dmag = x > 0.f ? da : 0.f;
+                    my[c] += dmag;
+                }
+                const float pr = gr[k] * act, pi = gi[k] * act, dot = pr * ur + pi * ui;
+                const float zrk = zr[k], zik = zi[k];
+                zr[k] = (pr - ur * dot) * inv + dmag * zrk / m;
+                zi[k] = (pi - ui * dot) * inv + dmag * zik / m;
+            }
+            CVec<T, V>::store(gz, e0 + V * j, zr, zi);
+        }
+    }
+    write_partials<NP>(p, acc);
+}
+
+template <typename T, int V>
+__global__ void __launch_bounds__(THREADS) cgu_bwd_kernel(Params p) {
+    const T *gt = (const T *)p.z, *up = (const T *)p.up, *go = (const T *)p.gout;
+    T *dg = (T *)p.gz, *du = (T *)p.gup;
+    const int64_t n = p.rows * p.dim / V;
+    for (int64_t j = (int64_t)blockIdx.x * THREADS + threadIdx.x; j < n; j += (int64_t)gridDim.x * THREADS) {
+        float vr[V], vi[V], ur[V], ui[V], gr[V], gi[V];
+        CVec<T, V>::load(gt, V * j, vr, vi);
+        CVec<T, V>::load(up, V * j, ur, ui);
+        CVec<T, V>::load(go, V * j, gr, gi);
+#pragma unroll
+        for (int k = 0; k < V; ++k) {
+            const float m = magnitude(vr[k], vi[k]), inv = rcp(m + MAG_EPS), gm = sigmoidf(m);
+            const float pr = vr[k] * inv, pi = vi[k] * inv;
+            const float cr = pr * ur[k] - pi * ui[k], ci = pr * ui[k] + pi * ur[k];
+            const float dgm = (gr[k] * cr + gi[k] * ci) * gm * (1.f - gm);
+            const float dcr = gr[k] * gm, dci = gi[k] * gm;
+            const float dpr = dcr * ur[k] + dci * ui[k], dpi = -dcr * ui[k] + dci * ur[k];
+            const float dot = dpr * pr + dpi * pi;
+            ur[k] = dcr * pr + dci * pi;  // d up
+            ui[k] = -dcr * pi + dci * pr;
+            const float vrk = vr[k], vik = vi[k];
+            vr[k] = (dpr - pr * dot) * inv + dgm * vrk / m;  // d gate
+            vi[k] = (dpi - pi * dot) * inv + dgm * vik / m;
+        }
+        CVec<T, V>::store(du, V * j, ur, ui);
+        CVec<T, V>::store(dg, V * j, vr, vi);
+    }
+}
+
+// Row kernels with the row in registers: four columns per 16-byte group, up to G
+// groups per lane (dim <= 256 G), so the second pass over a row re-reads nothing
+// and the parameter-gradient column sums stay in registers across the wave's
+// rows (lane l owns columns 4(l + 64 g) .. +3).
+template <typename T, int G>
+__global__ void __launch_bounds__(THREADS) norm_fwd_reg_kernel(Params p) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const T *z = (const T *)p.z;
+    T *out = (T *)p.out;
+    const int groups = p.dim / 4;
+    float sc[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int j = lane + 64 * g;
+        const float4 s4 = j < groups ? *reinterpret_cast<const float4 *>(p.p0 + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+        sc[g][0] = s4.x, sc[g][1] = s4.y, sc[g][2] = s4.z, sc[g][3] = s4.w;
+    }
+    for (int64_t row = (int64_t)blockIdx.x * WAVES + w; row < p.rows; row += (int64_t)gridDim.x * WAVES) {
+        const int64_t e0 = row * p.dim;
+        float re[G][4], im[G][4], m[G][4];
+        float ss = 0.f;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int j = lane + 64 * g;
+            if (j < groups) CVec<T, 4>::load(z, e0 + 4 * j, re[g], im[g]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                m[g][k] = magnitude(re[g][k], im[g][k]);
+                if (j < groups) ss += m[g][k] * m[g][k];
+            }
+        }
+        const float inv_rms = rcp(sqrtf(wave_sum(ss) / p.dim + p.eps));
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int j = lane + 64 * g;
+            if (j >= groups) continue;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float f = m[g][k] * inv_rms * sc[g][k] * rcp(m[g][k] + MAG_EPS);
+                re[g][k] *= f;
+                im[g][k] *= f;
+            }
+            CVec<T, 4>::store(out, e0 + 4 * j, re[g], im[g]);
+        }
+    }
+}
+
+// mod swish (OP 1) / mod relu (OP 2) forward over register-resident parameters
+template <typename T, int G, int OP>
+__global__ void __launch_bounds__(THREADS) act_fwd_reg_kernel(Params p) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const T *z = (const T *)p.z;
+    T *out = (T *)p.out;
+    const int groups = p.dim / 4;
+    float b0[G][4], b1[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int j = lane + 64 * g;
+        const float4 x0 = j < groups ? *reinterpret_cast<const float4 *>(p.p0 + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 x1 = (OP == 1 && j < groups) ? *reinterpret_cast<const float4 *>(p.p1 + 4 * j)
+                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        b0[g][0] = x0.x, b0[g][1] = x0.y, b0[g][2] = x0.z, b0[g][3] = x0.w;
+        b1[g][0] = x1.x, b1[g][1] = x1.y, b1[g][2] = x1.z, b1[g][3] = x1.w;
+    }
+    for (int64_t row = (int64_t)blockIdx.x * WAVES + w; row < p.rows; row += (int64_t)gridDim.x * WAVES) {
+        const int64_t e0 = row * p.dim;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int j = lane + 64 * g;
+            if (j >= groups) continue;
+            float re[4], im[4];
+            CVec<T, 4>::load(z, e0 + 4 * j, re, im);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float m = magnitude(re[k], im[k]), inv = rcp(m + MAG_EPS);
+                const float act = OP == 1 ? m * sigmoidf(b1[g][k] * m + b0[g][k]) : fmaxf(m + b0[g][k], 0.f);
+                re[k] *= inv * act;
+                im[k] *= inv * act;
+            }
+            CVec<T, 4>::store(out, e0 + 4 * j, re, im);
+        }
+    }
+}
+
+// fold per-lane register column sums (NP parameters x G groups x 4 columns)
+// across the block's waves in fixed order into this block's partial
+template <int NP, int G>
+__device__ __forceinline__ void write_partials_reg(const Params &p, const float (&acc)[NP][G][4], float *lds) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, groups = p.dim / 4;
+#pragma unroll
+    for (int q = 0; q < NP; ++q)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int j = lane + 64 * g;
+            if (j < groups)
+                *reinterpret_cast<float4 *>(lds + (w * NP + q) * p.dim + 4 * j) =
+                    make_float4(acc[q][g][0], acc[q][g][1], acc[q][g][2], acc[q][g][3]);
+        }
+    write_partials<NP>(p, lds);
+}
+
+template <typename T, int G>
+__global__ void __launch_bounds__(THREADS) norm_bwd_reg_kernel(Params p) {
+    extern __shared__ float lds[];  // [WAVES][1][dim], used once at the end
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const T *z = (const T *)p.z, *go = (const T *)p.gout;
+    T *gz = (T *)p.gz;
+    const int groups = p.dim / 4;
+    float sc[G][4], acc[1][G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int j = lane + 64 * g;
+        const float4 s4 = j < groups ? *reinterpret_cast<const float4 *>(p.p0 + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+        sc[g][0] = s4.x, sc[g][1] = s4.y, sc[g][2] = s4.z, sc[g][3] = s4.w;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[0][g][k] = 0.f;
+    }
+    int64_t r0, r1;
+    block_rows(p, r0, r1);
+    for (int64_t row = r0 + w; row < r1; row += WAVES) {
+        const int64_t e0 = row * p.dim;
+        float zr[G][4], zi[G][4], gr[G][4], gi[G][4];
+        float ss = 0.f, sg = 0.f;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int j = lane + 64 * g;
+            if (j >= groups) continue;
+            CVec<T, 4>::load(z, e0 + 4 * j, zr[g], zi[g]);
+            CVec<T, 4>::load(go, e0 + 4 * j, gr[g], gi[g]);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float m = magnitude(zr[g][k], zi[g][k]), inv = rcp(m + MAG_EPS);
+                ss += m * m;
+                sg += (gr[g][k] * zr[g][k] + gi[g][k] * zi[g][k]) * inv * sc[g][k] * m;
+            }
+        }
+        ss = wave_sum(ss);
+        sg = wave_sum(sg);
+        const float rms = sqrtf(ss / p.dim + p.eps), inv_rms = rcp(rms);
+        const float grad_rms = -sg * inv_rms * inv_rms, rms_term = grad_rms * rcp(p.dim * rms);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int j = lane + 64 * g;
+            if (j >= groups) continue;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float m = magnitude(zr[g][k], zi[g][k]), inv = rcp(m + MAG_EPS), rm = rcp(m);
+                const float ur = zr[g][k] * inv, ui = zi[g][k] * inv;
+                const float gs = gr[g][k] * ur + gi[g][k] * ui;
+                acc[0][g][k] += gs * m * inv_rms;
+                const float gmag = gs * sc[g][k] * inv_rms + rms_term * m;
+                const float smag = m * inv_rms * sc[g][k];
+                const float pr = gr[g][k] * smag, pi = gi[g][k] * smag, dot = pr * ur + pi * ui;
+                const float a = zr[g][k], b = zi[g][k];
+                zr[g][k] = (pr - ur * dot) * inv + gmag * a * rm;
+                zi[g][k] = (pi - ui * dot) * inv + gmag * b * rm;
+            }
+            CVec<T, 4>::store(gz, e0 + 4 * j, zr[g], zi[g]);
+        }
+    }
+    write_partials_reg<1, G>(p, acc, lds);
+}
+
+template <typename T, int G, int OP>
+__global__ void __launch_bounds__(THREADS) act_bwd_reg_kernel(Params p) {
+    constexpr int NP = OP == 1 ? 2 : 1;
+    extern __shared__ float lds[];  // [WAVES][NP][dim], used once at the end
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const T *z = (const T *)p.z, *go = (const T *)p.gout;
+    T *gz = (T *)p.gz;
+    const int groups = p.dim / 4;
+    float b0[G][4], b1[G][4], acc[NP][G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int j = lane + 64 * g;
+        const float4 x0 = j < groups ? *reinterpret_cast<const float4 *>(p.p0 + 4 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 x1 = (OP == 1 && j < groups) ? *reinterpret_cast<const float4 *>(p.p1 + 4 * j)
+                                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        b0[g][0] = x0.x, b0[g][1] = x0.y, b0[g][2] = x0.z, b0[g][3] = x0.w;
+        b1[g][0] = x1.x, b1[g][1] = x1.y, b1[g][2] = x1.z, b1[g][3] = x1.w;
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[q][g][k] = 0.f;
+    }
+    int64_t r0, r1;
+    block_rows(p, r0, r1);
+    for (int64_t row = r0 + w; row < r1; row += WAVES) {
+        const int64_t e0 = row * p.dim;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int j = lane + 64 * g;
+            if (j >= groups) continue;
+            float zr[4], zi[4], gr[4], gi[4];
+            CVec<T, 4>::load(z, e0 + 4 * j, zr, zi);
+            CVec<T, 4>::load(go, e0 + 4 * j, gr, gi);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float m = magnitude(zr[k], zi[k]), inv = rcp(m + MAG_EPS), rm = rcp(m);
+                const float ur = zr[k] * inv, ui = zi[k] * inv;
+                const float da = gr[k] * ur + gi[k] * ui;
+                float act, dmag;
+                if constexpr (OP == 1) {
+                    const float beta = b1[g][k], sg = sigmoidf(beta * m + b0[g][k]), sd = sg * (1.f - sg);
+                    act = m * sg;
+                    dmag = da * (sg + m * beta * sd);
+                    acc[0][g][k] += da * m * sd;
+                    acc[NP - 1][g][k] += OP == 1 ? da * m * m * sd : 0.f;
+                } else {
+                    const float x = m + b0[g][k];
+                    act = fmaxf(x, 0.f);
+                    dmag = x > 0.f ? da : 0.f;
+                    acc[0][g][k] += dmag;
+                }
+                const float pr = gr[k] * act, pi = gi[k] * act, dot = pr * ur + pi * ui;
+                const float a = zr[k], b = zi[k];
+                zr[k] = (pr - ur * dot) * inv + dmag * a * rm;
+                zi[k] = (pi - ui * dot) * inv + dmag * b * rm;
+            }
+            CVec<T, 4>::store(gz, e0 + 4 * j, zr, zi);
+        }
+    }
+    write_partials_reg<NP, G>(p, acc, lds);
+}
+
+// out[i] = sum over blocks of part[b][i], in a fixed order: 16 waves each sum
+// the blocks b = w, w + 16, ... (eight loads in flight), then wave 0 adds the 16
+constexpr int SUM_THREADS = 1024;
+__global__ void __launch_bounds__(SUM_THREADS) partial_sum_kernel(const float *part, int blocks, int n, float *o0,
+                                                                  float *o1, int dim) {
+    __shared__ float red[SUM_THREADS / 64][64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i = blockIdx.x * 64 + lane;
+    float s = 0.f;
+    if (i < n) {
+        float acc8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        int b = w;
+        for (; b + 7 * (SUM_THREADS / 64) < blocks; b += 8 * (SUM_THREADS / 64)) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc8[k] += part[(int64_t)(b + k * (SUM_THREADS / 64)) * n + i];
+        }
+        for (; b < blocks; b += SUM_THREADS / 64) acc8[0] += part[(int64_t)b * n + i];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s += acc8[k];
+    }
+    red[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && i < n) {
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < SUM_THREADS / 64; ++k) t += red[k][lane];
+        if (i < dim) o0[i] = t;
+        else o1[i - dim] = t;
+    }
+}
+
+int n_params(int op) { return op == QPAM_CPLX_NORM || op == QPAM_CPLX_MOD_RELU ? 1 : op == QPAM_CPLX_MOD_SWISH ? 2 : 0; }
+
+int row_blocks(int64_t rows) { return (int)std::min<int64_t>((rows + WAVES - 1) / WAVES, MAX_BLOCKS); }
+int flat_blocks(int64_t n) { return (int)std::min<int64_t>((n + THREADS - 1) / THREADS, 4 * MAX_BLOCKS); }
+
+int validate(const qpam_cplx_args *a, const char *who, bool bwd) {
+    QPAM_REQUIRE(a != nullptr, "%s: null args", who);
+    QPAM_REQUIRE(a->op >= QPAM_CPLX_NORM && a->op <= QPAM_CPLX_CGU_GATE, "%s: unknown op %d", who, a->op);
+    QPAM_REQUIRE(a->dtype == QPAM_F32 || a->dtype == QPAM_BF16, "%s: dtype %d", who, a->dtype);
+    QPAM_REQUIRE(a->rows >= 0 && a->dim >= 1, "%s: bad sizes rows=%lld dim=%d", who, (long long)a->rows, a->dim);
+    const int np = n_params(a->op);
+    QPAM_REQUIRE(a->dim * np <= 8192, "%s: dim %d too large for the parameter-gradient slices (max %d)", who, a->dim,
+                 np ? 8192 / np : 0);
+    if (a->rows == 0) {  // nothing to read or write but the (zero) parameter gradients
+        QPAM_REQUIRE(!bwd || np < 1 || a->gp0 != nullptr, "%s: missing parameter gradient", who);
+        QPAM_REQUIRE(!bwd || np < 2 || a->gp1 != nullptr, "%s: missing beta gradient", who);
+        return QPAM_OK;
+    }
+    QPAM_REQUIRE(a->z != nullptr, "%s: null z", who);
+    QPAM_REQUIRE(a->op != QPAM_CPLX_CGU_GATE || a->up != nullptr, "%s: CGU gate needs up", who);
+    QPAM_REQUIRE(np < 1 || a->p0 != nullptr, "%s: missing parameter", who);
+    QPAM_REQUIRE(np < 2 || a->p1 != nullptr, "%s: missing beta", who);
+    if (!bwd) {
+        QPAM_REQUIRE(a->out != nullptr, "%s: null out", who);
+    } else {
+        QPAM_REQUIRE(a->gout && a->gz, "%s: null gradient pointers", who);
+        QPAM_REQUIRE(a->op != QPAM_CPLX_CGU_GATE || a->gup != nullptr, "%s: CGU gate needs gup", who);
+        QPAM_REQUIRE(np < 1 || a->gp0 != nullptr, "%s: missing parameter gradient", who);
+        QPAM_REQUIRE(np < 2 || a->gp1 != nullptr, "%s: missing beta gradient", who);
+        QPAM_REQUIRE(np == 0 || (a->workspace != nullptr && a->workspace_bytes >= qpam_cplx_workspace_size(a)),
+                     "%s: workspace needs %zu bytes (got %zu)", who, qpam_cplx_workspace_size(a), a->workspace_bytes);
+    }
+    return QPAM_OK;
+}
+
+Params params(const qpam_cplx_args *a) {
+    Params p;
+    p.rows = a->rows;
+    p.dim = a->dim;
+    p.eps = a->eps;
+    p.z = a->z;
+    p.up = a->up;
+    p.p0 = a->p0;
+    p.p1 = a->p1;
+    p.out = a->out;
+    p.gout = a->gout;
+    p.gz = a->gz;
+    p.gup = a->gup;
+    p.part = (float *)a->workspace;
+    return p;
+}
+
+// groups of 4 columns per lane for the register-row kernels: 1, 2, 4 or 8 (dim <= 2048); 0 = use the
+// LDS-accumulating kernels
+int reg_groups(int dim) {
+    const int g = (dim / 4 + 63) / 64;
+    return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : g <= 8 ? 8 : 0;
+}
+
+template <typename T, int OP>
+int launch_act_fwd_reg(int g, int64_t rows, hipStream_t stream, const Params &p) {
+    const dim3 grid(row_blocks(rows));
+    switch (g) {
+        case 1: hipLaunchKernelGGL((act_fwd_reg_kernel<T, 1, OP>), grid, dim3(THREADS), 0, stream, p); break;
+        case 2: hipLaunchKernelGGL((act_fwd_reg_kernel<T, 2, OP>), grid, dim3(THREADS), 0, stream, p); break;
+        case 4: hipLaunchKernelGGL((act_fwd_reg_kernel<T, 4, OP>), grid, dim3(THREADS), 0, stream, p); break;
+        default: hipLaunchKernelGGL((act_fwd_reg_kernel<T, 8, OP>), grid, dim3(THREADS), 0, stream, p);
+    }
+    return launch_status("qpam_cplx_fwd");
+}
+
+template <typename T, int G>
+int launch_bwd_reg_g(int op, int blocks, size_t smem, hipStream_t stream, const Params &p) {
+    const void *k = op == QPAM_CPLX_NORM ? (const void *)norm_bwd_reg_kernel<T, G>
+                    : op == QPAM_CPLX_MOD_SWISH ? (const void *)act_bwd_reg_kernel<T, G, 1>
+                                                : (const void *)act_bwd_reg_kernel<T, G, 2>;
+    QPAM_CHECK_HIP(hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    if (op == QPAM_CPLX_NORM)
+        hipLaunchKernelGGL((norm_bwd_reg_kernel<T, G>), dim3(blocks), dim3(THREADS), smem, stream, p);
+    else if (op == QPAM_CPLX_MOD_SWISH)
+        hipLaunchKernelGGL((act_bwd_reg_kernel<T, G, 1>), dim3(blocks), dim3(THREADS), smem, stream, p);
+    else
+        hipLaunchKernelGGL((act_bwd_reg_kernel<T, G, 2>), dim3(blocks), dim3(THREADS), smem, stream, p);
+    return launch_status("qpam_cplx_bwd");
+}
+
+template <typename T>
+int launch_bwd_reg(int op, int g, int blocks, size_t smem, hipStream_t stream, const Params &p) {
+    switch (g) {
+        case 1: return launch_bwd_reg_g<T, 1>(op, blocks, smem, stream, p);
+        case 2: return launch_bwd_reg_g<T, 2>(op, blocks, smem, stream, p);
+        case 4: return launch_bwd_reg_g<T, 4>(op, blocks, smem, stream, p);
+        default: return launch_bwd_reg_g<T, 8>(op, blocks, smem, stream, p);
+    }
+}
+
+template <typename T, int V>
+int fwd(const qpam_cplx_args *a, hipStream_t stream) {
+    const Params p = params(a);
+    const int64_t n = a->rows * (int64_t)a->dim / V;
+    switch (a->op) {
+        case QPAM_CPLX_NORM:
+            if (V == 4 && reg_groups(a->dim)) {
+                const dim3 grid(row_blocks(a->rows));
+                switch (reg_groups(a->dim)) {
+                    case 1: hipLaunchKernelGGL((norm_fwd_reg_kernel<T, 1>), grid, dim3(THREADS), 0, stream, p); break;
+                    case 2: hipLaunchKernelGGL((norm_fwd_reg_kernel<T, 2>), grid, dim3(THREADS), 0, stream, p); break;
+                    case 4: hipLaunchKernelGGL((norm_fwd_reg_kernel<T, 4>), grid, dim3(THREADS), 0, stream, p); break;
+                    default: hipLaunchKernelGGL((norm_fwd_reg_kernel<T, 8>), grid, dim3(THREADS), 0, stream, p);
+                }
+                break;
+            }
+            hipLaunchKernelGGL((norm_fwd_kernel<T, V>), dim3(row_blocks(a->rows)), dim3(THREADS), 0, stream, p);
+            break;
+        case QPAM_CPLX_MOD_SWISH:
+            if (V == 4 && reg_groups(a->dim)) return launch_act_fwd_reg<T, 1>(reg_groups(a->dim), a->rows, stream, p);
+            hipLaunchKernelGGL((pointwise_fwd_kernel<T, V, 1>), dim3(flat_blocks(n)), dim3(THREADS), 0, stream, p);
+            break;
+        case QPAM_CPLX_MOD_RELU:
+            if (V == 4 && reg_groups(a->dim)) return launch_act_fwd_reg<T, 2>(reg_groups(a->dim), a->rows, stream, p);
+            hipLaunchKernelGGL((pointwise_fwd_kernel<T, V, 2>), dim3(flat_blocks(n)), dim3(THREADS), 0, stream, p);
+            break;
+        default:
+            hipLaunchKernelGGL((pointwise_fwd_kernel<T, V, 3>), dim3(flat_blocks(n)), dim3(THREADS), 0, stream, p);
+    }
+    return launch_status("qpam_cplx_fwd");
+}
+
+template <typename T, int V>
+int bwd(const qpam_cplx_args *a, hipStream_t stream) {
+    const Params p = params(a);
+    const int np = n_params(a->op);
+    const int blocks = row_blocks(a->rows);
+    const size_t smem = (size_t)WAVES * np * a->dim * sizeof(float);
+    if (V == 4 && reg_groups(a->dim) && a->op != QPAM_CPLX_CGU_GATE) {
+        int st = launch_bwd_reg<T>(a->op, reg_groups(a->dim), blocks, smem, stream, p);
+        if (st) return st;
+        const int n = np * a->dim;
+        hipLaunchKernelGGL(partial_sum_kernel, dim3((n + 63) / 64), dim3(SUM_THREADS), 0, stream,
+                           (const float *)a->workspace, blocks, n, a->gp0, a->gp1, a->dim);
+        return launch_status("qpam_cplx_bwd (parameter gradients)");
+    }
+    switch (a->op) {
+        case QPAM_CPLX_NORM:
+            QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)norm_bwd_kernel<T, V>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+            hipLaunchKernelGGL((norm_bwd_kernel<T, V>), dim3(blocks), dim3(THREADS), smem, stream, p);
+            break;
+        case QPAM_CPLX_MOD_SWISH:
+            QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)act_bwd_kernel<T, V, 1>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+            hipLaunchKernelGGL((act_bwd_kernel<T, V, 1>), dim3(blocks), dim3(THREADS), smem, stream, p);
+            break;
+        case QPAM_CPLX_MOD_RELU:
+            QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)act_bwd_kernel<T, V, 2>,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+            hipLaunchKernelGGL((act_bwd_kernel<T, V, 2>), dim3(blocks), dim3(THREADS), smem, stream, p);
+            break;
+        default:
+            hipLaunchKernelGGL((cgu_bwd_kernel<T, V>), dim3(flat_blocks(a->rows * (int64_t)a->dim / V)),
+                               dim3(THREADS), 0, stream, p);
+            return launch_status("qpam_cplx_bwd (CGU gate)");
+    }
+    int st = launch_status("qpam_cplx_bwd");
+    if (st) return st;
+    const int n = np * a->dim;
+    hipLaunchKernelGGL(partial_sum_kernel, dim3((n + 63) / 64), dim3(SUM_THREADS), 0, stream,
+                       (const float *)a->workspace, blocks, n, a->gp0, a->gp1, a->dim);
+    return launch_status("qpam_cplx_bwd (parameter gradients)");
+}
+
+// 16-byte vectors of four complex elements when every row starts 16-byte aligned
+bool vec4(const qpam_cplx_args *a) {
+    const uintptr_t m = (uintptr_t)a->z | (uintptr_t)a->up | (uintptr_t)a->out | (uintptr_t)a->gout |
+                        (uintptr_t)a->gz | (uintptr_t)a->gup | (uintptr_t)a->p0 | (uintptr_t)a->p1;
+    return a->dim % 4 == 0 && (m & 15) == 0;
+}
+
+template <typename T>
+int fwd_t(const qpam_cplx_args *a, hipStream_t stream) { return vec4(a) ? fwd<T, 4>(a, stream) : fwd<T, 1>(a, stream); }
+template <typename T>
+int bwd_t(const qpam_cplx_args *a, hipStream_t stream) { return vec4(a) ? bwd<T, 4>(a, stream) : bwd<T, 1>(a, stream); }
+
+}  // namespace
+}  // namespace cplx
+}  // namespace qpam
+
+extern "C" size_t qpam_cplx_workspace_size(const qpam_cplx_args *a) {
+    using namespace qpam::cplx;
+    if (!a || a->rows <= 0 || a->dim <= 0) return 0;
+    return (size_t)row_blocks(a->rows) * n_params(a->op) * a->dim * sizeof(float);
+}
+
+extern "C" int qpam_cplx_fwd(const qpam_cplx_args *a, void *stream) {
+    using namespace qpam::cplx;
+    int st = validate(a, "qpam_cplx_fwd", false);
+    if (st) return st;
+    if (a->rows == 0) return QPAM_OK;
+    return a->dtype == QPAM_BF16 ? fwd_t<unsigned short>(a, (hipStream_t)stream) : fwd_t<float>(a, (hipStream_t)stream);
+}
+
+extern "C" int qpam_cplx_bwd(const qpam_cplx_args *a, void *stream) {
+    using namespace qpam::cplx;
+    int st = validate(a, "qpam_cplx_bwd", true);
+    if (st) return st;
+    if (a->rows == 0) {
+        // no rows: parameter gradients are zero (a sum over zero blocks; a kernel,
+        // not a memset, so that the call can be captured in a HIP graph)
+        const int n = n_params(a->op) * a->dim;
+        if (n > 0)
+            hipLaunchKernelGGL(partial_sum_kernel, dim3((n + 63) / 64), dim3(SUM_THREADS), 0, (hipStream_t)stream,
+                               (const float *)nullptr, 0, n, a->gp0, a->gp1, a->dim);
+        return n > 0 ? qpam::launch_status("qpam_cplx_bwd (zero parameter gradients)") : QPAM_OK;
+    }
+    return a->dtype == QPAM_BF16 ? bwd_t<unsigned short>(a, (hipStream_t)stream) : bwd_t<float>(a, (hipStream_t)stream);
+}

@@ -52,7 +52,7 @@ def test_library_loads_and_exports_every_declared_symbol():
 
 @pytest.mark.parametrize("cname,pyname", [
     ("qpam_decode_args", "DecodeArgs"), ("qpam_scan_args", "ScanArgs"), ("qpam_scan_bwd_args", "ScanBwdArgs"),
-    ("qpam_ce_fwd_args", "CeFwdArgs"), ("qpam_ce_bwd_args", "CeBwdArgs"),
+    ("qpam_ce_fwd_args", "CeFwdArgs"), ("qpam_ce_bwd_args", "CeBwdArgs"), ("qpam_cplx_args", "CplxArgs"),
 ])
 def test_ctypes_structs_match_header(cname, pyname):
     py = [f[0] for f in getattr(_lib, pyname)._fields_]
@@ -67,6 +67,21 @@ def test_errors_surface_as_exceptions_without_gpu():
     assert b"qpam_decode_step" in lib.qpam_last_error()
     with pytest.raises(_lib.QpamError):
         _lib.check(st, "qpam_decode_step")
+
+
+def test_complex_op_argument_errors_without_gpu():
+    """Bad op, missing parameter and oversized dim come back as errors before any launch."""
+    lib = _lib.lib()
+    a = _lib.CplxArgs()
+    a.op, a.dtype, a.rows, a.dim = 7, _lib.QPAM_F32, 4, 8
+    assert lib.qpam_cplx_fwd(ctypes.byref(a), None) != 0 and b"unknown op" in lib.qpam_last_error()
+    a.op = _lib.QPAM_CPLX_MOD_SWISH
+    a.z, a.out, a.p0 = 16, 16, 16  # p1 (beta) missing
+    assert lib.qpam_cplx_fwd(ctypes.byref(a), None) != 0 and b"beta" in lib.qpam_last_error()
+    a.op, a.dim = _lib.QPAM_CPLX_NORM, 9000
+    assert lib.qpam_cplx_fwd(ctypes.byref(a), None) != 0 and b"too large" in lib.qpam_last_error()
+    a.dim = 8
+    assert lib.qpam_cplx_workspace_size(ctypes.byref(a)) == 1 * 1 * 8 * 4  # one block, one parameter
 
 
 def test_cpu_tensors_are_refused():

@@ -157,4 +157,15 @@ def install(model_module=None):
         parent = sys.modules.get(pkg)
         if parent is not None:
             setattr(parent, sub, m)
+    # v11.complex_ops bound the four elementwise ops from v11.triton_kernels at its
+    # own import (v11/complex_ops.py:19-24); its layers look them up at call time
+    cops = sys.modules.get(f"{pkg}.complex_ops")
+    if cops is not None:
+        for name in _COMPLEX_OPS:
+            if hasattr(cops, name):
+                _ORIGINALS.setdefault(f"complex_ops.{name}", getattr(cops, name))
+                setattr(cops, name, getattr(_tk, name))
     return dict(_ORIGINALS)
+
+
+_COMPLEX_OPS = ("fused_complex_norm", "fused_mod_swish", "fused_mod_relu", "fused_cgu_gate")

@@ -1,6 +1,7 @@
 """CPU check of install(): it rebinds the V11PAMLayer hot-path methods of a
-v11.model-like module, replaces the module-level fused_decay_matrix name and
-aliases the v11.flash_pam / triton_kernels / fused_ce modules (no GPU call)."""
+v11.model-like module, replaces the module-level fused_decay_matrix name,
+aliases the v11.flash_pam / triton_kernels / fused_ce modules and rebinds the
+elementwise ops v11.complex_ops imported (no GPU call)."""
 
 import sys
 import types
@@ -34,8 +35,12 @@ def test_install_rebinds_methods_and_aliases():
 
     mod.V11PAMLayer = V11PAMLayer
     mod.fused_decay_matrix = lambda *a: "orig"
+    cops = types.ModuleType("v11x.complex_ops")  # imported the ops by name before install()
+    for name in ("fused_complex_norm", "fused_mod_swish", "fused_mod_relu", "fused_cgu_gate"):
+        setattr(cops, name, lambda *a: "orig")
     sys.modules["v11x"] = pkg
     sys.modules["v11x.model"] = mod
+    sys.modules["v11x.complex_ops"] = cops
     saved = dict(pam_layer._ORIGINALS)
     pam_layer._ORIGINALS.clear()
     try:
@@ -52,8 +57,10 @@ def test_install_rebinds_methods_and_aliases():
         assert sys.modules["v11x.fused_ce"] is fused_ce
         assert pkg.fused_ce is fused_ce
         assert set(originals) >= {"_forward_chunked_head", "_recurrent", "_dual_form_block"}
+        for name in ("fused_complex_norm", "fused_mod_swish", "fused_mod_relu", "fused_cgu_gate"):
+            assert getattr(cops, name) is getattr(triton_kernels, name)
     finally:
         pam_layer._ORIGINALS.clear()
         pam_layer._ORIGINALS.update(saved)
-        for k in ("v11x", "v11x.model", "v11x.flash_pam", "v11x.triton_kernels", "v11x.fused_ce"):
+        for k in ("v11x", "v11x.model", "v11x.flash_pam", "v11x.triton_kernels", "v11x.fused_ce", "v11x.complex_ops"):
             sys.modules.pop(k, None)

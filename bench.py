@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=1000)
-    ap.add_argument("--only", choices=["scan_fwd", "decode", "e3", "ce", "cplx", "copy"], default=None,
+    ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "e3", "ce", "cplx", "copy"], default=None,
                     help="run one workload (for profiler passes) and print its own JSON line")
     return ap.parse_args()
 
@@ -141,6 +141,52 @@ def bench_decode(n_steps):
     ms = e0.elapsed_time(e1) / n_steps
     active = sum(counts[i % 16] for i in range(n_steps)) / n_steps
     bytes_step = active * G * (2 * 32768 + 4 * 512 + 4)
+    return {"ms_per_step": ms, "tokens_per_s": active / (ms * 1e-3), "active_slots": active,
+            "hbm_GBps": bytes_step / (ms * 1e-3) / 1e9, "hbm_frac": bytes_step / (ms * 1e-3) / HBM_PEAK,
+            "bytes_per_step": bytes_step, "steps": n_steps}
+
+
+def bench_decode_e3_rope(n_steps):
+    """Continuous-batching decode of an E3 model: 256 slots x 16 layers x 12 heads,
+    3 states per head with per-state read rotation, d=64, per-slot RoPE positions,
+    ~75% of slots active per step (one launch per step for all layers)."""
+    import torch
+    from qllm2_amd.decode import build_rope_cache, decode_step
+    S, L, H, M, d = 256, 16, 12, 3, 64
+    G = L * H
+    dev = torch.device("cuda")
+    gen = torch.Generator().manual_seed(1014)
+    state = torch.empty(S, G, M, d, d, 2, device=dev)
+    for sl in range(0, S, 16):
+        state[sl:sl + 16] = (torch.randn(16, G, M, d, d, 2, generator=gen) * 0.01).to(dev)
+    q, k, v = (torch.randn(S, G, d, 2, generator=gen).to(dev) for _ in range(3))
+    gamma = torch.sigmoid(torch.randn(S, G, M, generator=gen) + 3).to(dev)
+    rot = torch.randn(S, G, M, 2, generator=gen).to(dev)
+    rope = build_rope_cache(8192, d, device=dev)
+    pos = torch.randint(0, 8192, (S,), generator=gen, dtype=torch.int32).to(dev)
+    masks = [torch.nonzero(torch.rand(S, generator=gen) < 0.75).flatten().to(torch.int32).to(dev)
+             for _ in range(16)]
+    counts = [int(m.numel()) for m in masks]
+    y = torch.zeros_like(q)
+
+    def step(i):
+        decode_step(state, q, k, v, gamma, active=masks[i % 16], rot=rot, q_scale=d ** -0.5, out=y,
+                    rope=rope, pos=pos)
+
+    for i in range(10):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(n_steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n_steps
+    active = sum(counts[i % 16] for i in range(n_steps)) / n_steps
+    # per active (slot, group): M states read+written (2 x 32 KiB each), q, k, v, y
+    # rows (4 x 512 B), gamma + rotation per state (12 B); one rope row per slot
+    bytes_step = active * G * (M * 2 * 32768 + 4 * 512 + M * 12) + active * 512
     return {"ms_per_step": ms, "tokens_per_s": active / (ms * 1e-3), "active_slots": active,
             "hbm_GBps": bytes_step / (ms * 1e-3) / 1e9, "hbm_frac": bytes_step / (ms * 1e-3) / HBM_PEAK,
             "bytes_per_step": bytes_step, "steps": n_steps}
@@ -284,6 +330,7 @@ def main():
         fn = {"scan_fwd": lambda: dict(zip(("ms", "kernel_ms", "tokens", "flops", "kernel_flops"),
                                            bench_scan_fwd(args.steps, args.warmup))),
               "decode": lambda: bench_decode(args.decode_steps),
+              "decode_e3": lambda: bench_decode_e3_rope(max(50, args.decode_steps // 5)),
               "e3": lambda: bench_e3_fwd_bwd(args.steps, args.warmup),
               "ce": lambda: bench_ce(args.steps, args.warmup),
               "cplx": lambda: bench_complex_ops(args.steps, args.warmup),
@@ -319,6 +366,7 @@ def main():
     }
     if not args.no_extras:
         out["extras"] = {"decode_config4": bench_decode(args.decode_steps),
+                         "decode_e3_rope_slots": bench_decode_e3_rope(max(50, args.decode_steps // 5)),
                          "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 2),
                          "ce_fwd_bwd_config5": bench_ce(max(3, args.steps // 4), 2),
                          "complex_elementwise": bench_complex_ops(max(3, args.steps // 2), 2)}

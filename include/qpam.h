@@ -95,6 +95,15 @@ typedef struct {
     int64_t sr_slot, sr_group, sr_state;
     float *y;
     int64_t sy_slot, sy_group;
+    /* optional per-slot rotary position (the reference's _project rotation,
+     * v11/model.py:290-301, with one offset per slot instead of one step_offset):
+     * q and k of slot a are multiplied, feature by feature, by the complex
+     * rope[pos[a]][j] before the update; rope is [rope_len][d][2] fp32 (the
+     * build_rope_cache table, v11/complex_ops.py:261-266), positions are clamped
+     * to [0, rope_len). */
+    const float *rope;      /* NULL = no rotation */
+    const int32_t *pos;     /* [n_slots] device positions */
+    int32_t rope_len;
 } qpam_decode_args;
 
 int qpam_decode_step(const qpam_decode_args *a, void *stream);

@@ -326,12 +326,24 @@ def recurrent(queries, keys, protected_values, gamma_all, head_dim, phase=None, 
     return torch.stack(ys, dim=2), state
 
 
-def decode_slots(state, active, q, k, v, gamma, q_scale, rot=None):
+def rope_table(max_len, head_dim):
+    """e^{i m theta_j}, theta_j = 10000^(-j/head_dim), [max_len, head_dim, 2] in
+    float64 (v11/complex_ops.py:261-266 computes the same angles in fp32)."""
+    j = np.arange(head_dim, dtype=np.float64)
+    inv = 1.0 / (10000.0 ** (j / head_dim))
+    ang = np.arange(max_len, dtype=np.float64)[:, None] * inv[None, :]
+    return torch.from_numpy(np.stack([np.cos(ang), np.sin(ang)], -1))
+
+
+def decode_slots(state, active, q, k, v, gamma, q_scale, rot=None, rope=None, pos=None):
     """One continuous-batching decode step over a slot pool (config 4 semantics).
 
     state [S, G, M, d, d, 2] (G = layers*heads groups, M states), active: 1-D
     int tensor of slot ids, q/k/v [S, G, d, 2] (q unscaled), gamma [S, G, M],
-    rot optional [S, G, M, 2].  For every active slot and group applies
+    rot optional [S, G, M, 2].  With rope [P, d, 2] and pos [S], q and k of
+    slot a are first multiplied by rope[pos[a]] (the reference's
+    cmul(queries, rope_cache[step_offset]), v11/model.py:290-301, with one
+    offset per slot).  For every active slot and group applies
     recur_step_additive per state, rotates, sums over M.  Returns (y [S,G,d,2]
     with zeros for inactive slots, new state) -- inactive slots untouched.
     """
@@ -339,8 +351,12 @@ def decode_slots(state, active, q, k, v, gamma, q_scale, rot=None):
     y = torch.zeros_like(q)
     for sl in active.tolist():
         acc = None
+        qs, ks = q[sl], k[sl]
+        if rope is not None:
+            r = rope[int(pos[sl])].to(q.dtype)
+            qs, ks = cmul(qs, r), cmul(ks, r)
         for m in range(state.shape[2]):
-            ym, st = recur_step_additive(state[sl, :, m], gamma[sl, :, m], v[sl], k[sl], q[sl] * q_scale)
+            ym, st = recur_step_additive(state[sl, :, m], gamma[sl, :, m], v[sl], ks, qs * q_scale)
             state[sl, :, m] = st
             if rot is not None:
                 ym = cmul(ym, rot[sl, :, m].unsqueeze(-2))

@@ -15,10 +15,15 @@
 // halves the number of live partial sums).  Slots that are not listed cost
 // nothing: the grid is n_active * n_groups.
 //
-// Two kernels: the single-state, unrotated step (the continuous-batching
-// common case) keeps every register for loads in flight, 512 threads per
-// 64 x 64 state and no LDS or barriers; the general kernel loops over the M
-// states, accumulating the rotated reads through LDS.
+// Optional per-slot rotary positions rotate q and k as they are loaded.
+//
+// Kernels: the single-state, unrotated step (the continuous-batching common
+// case) keeps every register for loads in flight, 512 threads per 64 x 64
+// state and no LDS or barriers; up to 4 states (E3 models use 3), with or
+// without read rotations, take the multi-state kernel, which loads every state
+// up front and folds the rotations into the lane partials (d = 128: one
+// state); more states take the general kernel, which loops over them
+// through LDS.
 #include "common.h"
 
 namespace qpam {
@@ -43,6 +48,17 @@ struct DecodeShape {
         return m;
     }
 };
+
+// q and k of the slot times rope[pos[slot]] (two complex features per float4)
+template <int D>
+__device__ __forceinline__ void apply_rope(const qpam_decode_args &a, int slot, int cp, float4 &qv, float4 &kv) {
+    if (!a.rope) return;
+    const int p = min(max(a.pos[slot], 0), a.rope_len - 1);
+    const float4 r = *reinterpret_cast<const float4 *>(a.rope + (int64_t)p * 2 * D + 4 * cp);
+    const float4 q = qv, k = kv;
+    qv = make_float4(q.x * r.x - q.y * r.y, q.x * r.y + q.y * r.x, q.z * r.z - q.w * r.w, q.z * r.w + q.w * r.z);
+    kv = make_float4(k.x * r.x - k.y * r.y, k.x * r.y + k.y * r.x, k.z * r.z - k.w * r.w, k.z * r.w + k.w * r.z);
+}
 
 // Reduce NV values across P aligned lanes by halving; on return the lane holds
 // `nv` complete sums for value indices [idx_base, idx_base + nv).
@@ -109,8 +125,9 @@ __global__ void __launch_bounds__((DecodeShape<D, 512>::THREADS)) decode_single_
     const int slot = a.active ? a.active[ai] : ai;
     if (slot < 0 || slot >= a.n_slots) return;
     const int cp = tid % S::PAIRS, r0 = tid / S::PAIRS, lane = tid & 63;
-    const float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
-    const float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
+    float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    apply_rope<D>(a, slot, cp, qv, kv);
     const float gam = a.gamma[slot * a.sg_slot + g * a.sg_group];
     float part[S::NV];
     update_state<S>(a.state + slot * a.st_slot + g * a.st_group, tid, r0, gam, a.v + slot * a.sv_slot + g * a.sv_group,
@@ -129,10 +146,87 @@ __global__ void __launch_bounds__((DecodeShape<D, 512>::THREADS)) decode_single_
     }
 }
 
+// ------------------------------- 1..4 states, rotations, all loads in flight --
+// Every state of the (slot, group) is loaded before any is updated, so the M
+// state streams overlap; each state's lane partials of S_m q~ are rotated by
+// r_m and summed in registers, and one halving reduction produces y (no LDS).
+template <int D>
+constexpr int multi_threads() { return D >= 128 ? 1024 : 512; }
+
+template <int D, int MS>
+__global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS)) decode_multi_kernel(qpam_decode_args a) {
+    using S = DecodeShape<D, multi_threads<D>()>;
+    const int tid = threadIdx.x;
+    const int ai = blockIdx.x / a.n_groups;
+    const int g = blockIdx.x - ai * a.n_groups;
+    const int slot = a.active ? a.active[ai] : ai;
+    if (slot < 0 || slot >= a.n_slots) return;
+    const int cp = tid % S::PAIRS, r0 = tid / S::PAIRS, lane = tid & 63;
+    float *st0 = a.state + slot * a.st_slot + g * a.st_group;
+    floatx4 s[MS][S::ITERS];
+#pragma unroll
+    for (int m = 0; m < MS; ++m)
+#pragma unroll
+        for (int it = 0; it < S::ITERS; ++it)
+            s[m][it] = __builtin_nontemporal_load(
+                reinterpret_cast<const floatx4 *>(st0 + m * a.st_state + 4 * (it * S::THREADS + tid)));
+    float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
+    float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    apply_rope<D>(a, slot, cp, qv, kv);
+    const float q0r = qv.x * a.q_scale, q0i = qv.y * a.q_scale, q1r = qv.z * a.q_scale, q1i = qv.w * a.q_scale;
+    const float *vrow = a.v + slot * a.sv_slot + g * a.sv_group;
+    float2 vv[S::ITERS];
+#pragma unroll
+    for (int it = 0; it < S::ITERS; ++it) vv[it] = *reinterpret_cast<const float2 *>(vrow + 2 * (it * S::ROWS_PER_IT + r0));
+    float tot[S::NV];
+#pragma unroll
+    for (int j = 0; j < S::NV; ++j) tot[j] = 0.f;
+#pragma unroll
+    for (int m = 0; m < MS; ++m) {
+        const float gam = a.gamma[slot * a.sg_slot + g * a.sg_group + m * a.sg_state];
+        float rr = 1.f, ri = 0.f;
+        if (a.rot) {
+            const float *rp = a.rot + slot * a.sr_slot + g * a.sr_group + m * a.sr_state;
+            rr = rp[0];
+            ri = rp[1];
+        }
+#pragma unroll
+        for (int it = 0; it < S::ITERS; ++it) {
+            const float o0r = vv[it].x * kv.x + vv[it].y * kv.y, o0i = vv[it].y * kv.x - vv[it].x * kv.y;
+            const float o1r = vv[it].x * kv.z + vv[it].y * kv.w, o1i = vv[it].y * kv.z - vv[it].x * kv.w;
+            floatx4 n;
+            n.x = gam * s[m][it].x + o0r;
+            n.y = gam * s[m][it].y + o0i;
+            n.z = gam * s[m][it].z + o1r;
+            n.w = gam * s[m][it].w + o1i;
+            __builtin_nontemporal_store(n, reinterpret_cast<floatx4 *>(st0 + m * a.st_state + 4 * (it * S::THREADS + tid)));
+            const float pr = n.x * q0r - n.y * q0i + n.z * q1r - n.w * q1i;
+            const float pi = n.x * q0i + n.y * q0r + n.z * q1i + n.w * q1r;
+            tot[2 * it] += rr * pr - ri * pi;
+            tot[2 * it + 1] += rr * pi + ri * pr;
+        }
+    }
+    int base, nv;
+    halving_reduce<S::NV, S::PAIRS>(tot, lane, base, nv);
+    if ((lane & S::bfly_mask()) == 0) {
+        float *yp = a.y + slot * a.sy_slot + g * a.sy_group;
+#pragma unroll
+        for (int j = 0; j < S::NV; ++j) {
+            if (j < nv) {
+                const int vi = base + j;
+                yp[2 * ((vi >> 1) * S::ROWS_PER_IT + r0) + (vi & 1)] = tot[j];
+            }
+        }
+    }
+}
+
 // ------------------------------------------------ M states, rotations -----
 template <int D>
-__global__ void __launch_bounds__((DecodeShape<D, 256>::THREADS)) decode_general_kernel(qpam_decode_args a) {
-    using S = DecodeShape<D, 256>;
+constexpr int general_threads() { return D >= 128 ? 1024 : 256; }  // 8 float4 of state per lane at d = 64, 128
+
+template <int D>
+__global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS)) decode_general_kernel(qpam_decode_args a) {
+    using S = DecodeShape<D, general_threads<D>()>;
     __shared__ float ys[D][2];
 
     const int tid = threadIdx.x;
@@ -145,8 +239,9 @@ __global__ void __launch_bounds__((DecodeShape<D, 256>::THREADS)) decode_general
     const int r0 = tid / S::PAIRS;      // first row of this lane
     const int lane = tid & 63;
 
-    const float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
-    const float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
+    float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    apply_rope<D>(a, slot, cp, qv, kv);
     const float *vrow = a.v + slot * a.sv_slot + g * a.sv_group;
 
     float yacc_r = 0.f, yacc_i = 0.f;  // lanes tid < D accumulate row tid
@@ -194,7 +289,36 @@ int launch_decode(const qpam_decode_args &a, hipStream_t stream) {
                            stream, a);
         return launch_status("decode_single_kernel");
     }
-    hipLaunchKernelGGL(decode_general_kernel<D>, dim3((unsigned)blocks), dim3(DecodeShape<D, 256>::THREADS), 0, stream,
+    constexpr int MT = DecodeShape<D, multi_threads<D>()>::THREADS;
+    // the multi-state kernel holds M x ITERS float4 of state per lane: up to 4
+    // states of a 64 x 64 state, one of a 128 x 128 state (more would spill)
+    constexpr int MAX_MS = D >= 128 ? 1 : 4;
+    switch (a.n_states) {
+        case 1:
+            hipLaunchKernelGGL((decode_multi_kernel<D, 1>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
+            return launch_status("decode_multi_kernel<1>");
+        case 2:
+            if constexpr (MAX_MS >= 2) {
+                hipLaunchKernelGGL((decode_multi_kernel<D, 2>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
+                return launch_status("decode_multi_kernel<2>");
+            }
+            break;
+        case 3:
+            if constexpr (MAX_MS >= 3) {
+                hipLaunchKernelGGL((decode_multi_kernel<D, 3>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
+                return launch_status("decode_multi_kernel<3>");
+            }
+            break;
+        case 4:
+            if constexpr (MAX_MS >= 4) {
+                hipLaunchKernelGGL((decode_multi_kernel<D, 4>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
+                return launch_status("decode_multi_kernel<4>");
+            }
+            break;
+        default:
+            break;
+    }
+    hipLaunchKernelGGL(decode_general_kernel<D>, dim3((unsigned)blocks), dim3(DecodeShape<D, general_threads<D>()>::THREADS), 0, stream,
                        a);
     return launch_status("decode_general_kernel");
 }
@@ -213,6 +337,8 @@ extern "C" int qpam_decode_step(const qpam_decode_args *a, void *stream) {
     QPAM_REQUIRE(a->active != nullptr || a->n_active <= a->n_slots,
                  "qpam_decode_step: n_active > n_slots without an active list");
     QPAM_REQUIRE(a->state && a->q && a->k && a->v && a->gamma && a->y, "qpam_decode_step: null pointer");
+    QPAM_REQUIRE(a->rope == nullptr || (a->pos != nullptr && a->rope_len >= 1 && aligned(a->rope, 16)),
+                 "qpam_decode_step: rope needs positions, rope_len >= 1 and a 16-byte aligned table");
     QPAM_REQUIRE((long long)a->n_active * a->n_groups < (1ll << 31), "qpam_decode_step: grid too large");
     // 16-byte vector access of S, q, k and 8-byte access of v, y
     QPAM_REQUIRE(aligned(a->state, 16) && aligned(a->q, 16) && aligned(a->k, 16) && aligned(a->v, 8) &&

@@ -4,7 +4,10 @@ Reference: V11PAMLayer._recur_step_additive (v11/model.py:927-965) and the
 per-token state loop of V11PAMLayer._recurrent (v11/model.py:845-925).
 
 `decode_step` is the continuous-batching form: one call updates every listed
-slot of a state pool in place, all layers/heads/states at once.
+slot of a state pool in place, all layers/heads/states at once, optionally
+rotating q and k by each slot's own RoPE position.  `SlotPool` is the decode
+engine around it (V11LM.generate, v11/model.py:1207-1245, without the batch-1
+loop): per-layer states of many sequences, joined and released between steps.
 `recur_step_additive` keeps the reference method's signature and functional
 (non-mutating) semantics.
 """
@@ -20,7 +23,7 @@ def _check_cuda(*ts):
             raise ValueError("qpam decode: tensors must be on the GPU (no CPU path in this library)")
 
 
-def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, out=None):
+def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, out=None, rope=None, pos=None):
     """In-place ragged decode step over a slot pool.
 
     state  [S, G, M, d, d, 2] fp32 (G = layers*heads, M states), updated in place
@@ -28,9 +31,11 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     gamma  [S, G, M] fp32
     active optional int32 [n] slot ids (others untouched); None = all slots
     rot    optional [S, G, M, 2] fp32 complex rotation of each state's read
+    rope   optional [P, d, 2] fp32 rotary table (build_rope_cache) with
+    pos    int32 [S] per-slot positions: q and k of slot a are rotated by rope[pos[a]]
     Returns y [S, G, d, 2] (rows of unlisted slots are left as in `out`/zero).
     """
-    _check_cuda(state, q, k, v, gamma, active, rot)
+    _check_cuda(state, q, k, v, gamma, active, rot, rope, pos)
     if state.dim() != 6 or state.shape[-1] != 2 or state.shape[-2] != state.shape[-3]:
         raise ValueError(f"state must be [S,G,M,d,d,2], got {tuple(state.shape)}")
     n_slots, n_groups, n_states, d = state.shape[:4]
@@ -74,6 +79,16 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
         a.sr_slot, a.sr_group, a.sr_state = rot.stride(0), rot.stride(1), rot.stride(2)
     a.y = y.data_ptr()
     a.sy_slot, a.sy_group = y.stride(0), y.stride(1)
+    if rope is not None:
+        if pos is None:
+            raise ValueError("rope needs per-slot positions `pos`")
+        if rope.dtype != torch.float32 or tuple(rope.shape[1:]) != (d, 2):
+            raise ValueError(f"rope must be fp32 [P, {d}, 2], got {rope.dtype} {tuple(rope.shape)}")
+        rope = rope.contiguous()
+        pos = pos.to(torch.int32).contiguous()
+        if pos.numel() != n_slots:
+            raise ValueError(f"pos must hold one position per slot ({n_slots}), got {pos.numel()}")
+        a.rope, a.pos, a.rope_len = rope.data_ptr(), pos.data_ptr(), rope.shape[0]
     L = _lib.lib()
     with torch.cuda.device(state.device):
         _lib.check(L.qpam_decode_step(a, _lib.stream_ptr(state.device)), "qpam_decode_step")
@@ -99,3 +114,86 @@ def recur_step_additive(memory_state, decay_gamma, value_t, key_t, query_t):
                     decay_gamma.to(torch.float32).contiguous().view(n, 1, 1), q_scale=1.0)
     return (y.view(*lead, d, 2).to(memory_state.dtype),
             new_state.view(*lead, d, d, 2).to(memory_state.dtype))
+
+
+def build_rope_cache(max_len, head_dim, device=None):
+    """Complex RoPE table e^{i m theta_j} [max_len, head_dim, 2] fp32, the
+    reference's build_rope_cache (v11/complex_ops.py:261-266):
+    theta_j = 10000^(-j / head_dim), computed in fp32 as there."""
+    inverse_freqs = 1.0 / (10000.0 ** (torch.arange(head_dim, device=device).float() / head_dim))
+    positions = torch.arange(max_len, device=device).float()
+    angles = positions.unsqueeze(1) * inverse_freqs.unsqueeze(0)
+    return torch.stack([angles.cos(), angles.sin()], dim=-1)
+
+
+class SlotPool:
+    """PAM state of a continuous-batching decode: `n_slots` sequence slots, each
+    with per-layer fp32 states [layers, heads, states, d, d, 2] and its own
+    position for the rotary offset.
+
+    Replaces the per-sequence state lists and the single step_offset of the
+    reference's batch loop (V11LM.generate, v11/model.py:1207-1245): sequences
+    join (acquire, optionally with the states a prefill produced) and leave
+    (release) between steps, and one `step` per layer updates every listed slot
+    with one kernel launch (qpam_decode_step with per-slot RoPE); `advance`
+    moves the listed slots' positions by one token.
+    """
+
+    def __init__(self, n_slots, n_layers, n_heads, head_dim, n_states=1, device="cuda", max_len=4096):
+        self.n_slots, self.n_layers, self.n_heads, self.head_dim, self.n_states = (
+            n_slots, n_layers, n_heads, head_dim, n_states)
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise ValueError("qpam SlotPool: the pool lives on the GPU (no CPU path in this library)")
+        self.state = torch.zeros(n_slots, n_layers, n_heads, n_states, head_dim, head_dim, 2,
+                                 device=self.device, dtype=torch.float32)
+        self.pos = torch.zeros(n_slots, device=self.device, dtype=torch.int32)
+        self.rope = build_rope_cache(max_len, head_dim, device=self.device)
+        self._free = list(range(n_slots - 1, -1, -1))
+        self.live = set()
+
+    def acquire(self, position=0, states=None):
+        """Take a free slot for a sequence whose next token is at `position`.
+        states: optional per-layer prefill states, each [n_states, n_heads, d, d, 2]
+        (the reference's [K, B=1, H, d, d, 2] with the batch axis dropped) or
+        [n_heads, d, d, 2] when n_states == 1.  Returns the slot id."""
+        if not self._free:
+            raise RuntimeError("SlotPool: no free slot")
+        slot = self._free.pop()
+        self.live.add(slot)
+        self.pos[slot] = int(position)
+        if states is None:
+            self.state[slot].zero_()
+        else:
+            for layer, st in enumerate(states):
+                st = st.to(self.device, torch.float32)
+                if st.dim() == 4:
+                    st = st.unsqueeze(0)
+                # [M, H, d, d, 2] -> [H, M, d, d, 2]
+                self.state[slot, layer].copy_(st.permute(1, 0, 2, 3, 4))
+        return slot
+
+    def release(self, slot):
+        self.live.discard(slot)
+        self._free.append(slot)
+
+    def layer_state(self, layer):
+        """View [n_slots, n_heads, n_states, d, d, 2] of one layer (no copy)."""
+        return self.state[:, layer]
+
+    def ensure_len(self, max_pos):
+        """Grow the rotary table (doubling, as the reference's rope cache) to cover max_pos."""
+        if max_pos >= self.rope.shape[0]:
+            self.rope = build_rope_cache(2 * (max_pos + 1), self.head_dim, device=self.device)
+
+    def step(self, layer, q, k, v, gamma, active, rot=None, q_scale=None, out=None):
+        """One token for the listed slots on one layer: q, k, v [n_slots, heads, d, 2]
+        (rows of unlisted slots ignored; q unscaled), gamma [n_slots, heads, states],
+        rot optional [n_slots, heads, states, 2].  RoPE at each slot's position."""
+        scale = self.head_dim ** -0.5 if q_scale is None else q_scale
+        return decode_step(self.layer_state(layer), q, k, v, gamma, active=active, rot=rot, q_scale=scale,
+                           out=out, rope=self.rope, pos=self.pos)
+
+    def advance(self, active):
+        self.pos[active.long()] += 1
+

@@ -28,7 +28,7 @@ def _pool(S, G, M, d, seed):
 
 
 @pytest.mark.parametrize("d", [16, 32, 64, 128])
-@pytest.mark.parametrize("M,use_rot", [(1, False), (3, True)])
+@pytest.mark.parametrize("M,use_rot", [(1, False), (1, True), (2, True), (3, True), (4, False), (5, True)])
 def test_decode_step_matches_oracle(gpu_lib, d, M, use_rot):
     S, G = 6, 5
     state, q, k, v, gamma, rot = _pool(S, G, M, d, 100 + d + M)
@@ -107,3 +107,74 @@ def test_decode_config4_full_pool_properties(gpu_lib):
         assert _rel(y[sl].cpu(), ys) < REL
     del before
     assert math.isfinite(y.abs().sum().item())
+
+
+@pytest.mark.parametrize("d", [16, 64, 128])
+@pytest.mark.parametrize("M,use_rot", [(1, False), (3, True)])
+def test_decode_rope_per_slot(gpu_lib, d, M, use_rot):
+    """Per-slot rotary positions inside the decode kernel against the oracle's
+    cmul(q, rope[pos]), cmul(k, rope[pos]) (one offset per slot)."""
+    from qllm2_amd.decode import decode_step
+    S, G = 7, 4
+    state, q, k, v, gamma, rot = _pool(S, G, M, d, 300 + d + M)
+    rope = O.rope_table(1000, d)
+    pos = torch.tensor([0, 999, 5, 123, 77, 1, 640], dtype=torch.int32)
+    active = torch.tensor([6, 0, 1, 3, 4], dtype=torch.int32)
+    scale = d ** -0.5
+    y_ref, s_ref = O.decode_slots(state.double(), active.long(), q.double(), k.double(), v.double(),
+                                  gamma.double(), scale, rot.double() if use_rot else None, rope=rope, pos=pos)
+    st = state.cuda()
+    y = decode_step(st, q.cuda(), k.cuda(), v.cuda(), gamma.cuda(), active=active.cuda(),
+                    rot=rot.cuda() if use_rot else None, q_scale=scale, rope=rope.float().cuda(), pos=pos.cuda())
+    torch.cuda.synchronize()
+    st, y = st.cpu(), y.cpu()
+    for sl in (2, 5):
+        assert torch.equal(st[sl], state[sl]) and torch.all(y[sl] == 0)
+    for sl in (0, 1, 3, 4, 6):
+        assert _rel(st[sl], s_ref[sl]) < REL
+        assert _rel(y[sl], y_ref[sl]) < REL
+
+
+def test_slot_pool_e3_continuous_batching(gpu_lib):
+    """SlotPool over 2 layers x 3 heads x 3 states, d=64: sequences join with a
+    prefill state at their own position, leave, and their slots are reused, over
+    12 steps.  Every live sequence's outputs and states are checked each step
+    against its own oracle decode (per-sequence state, per-sequence position)."""
+    from qllm2_amd.decode import SlotPool
+    L, H, M, d, S = 2, 3, 3, 64, 5
+    pool = SlotPool(S, L, H, d, n_states=M, max_len=256)
+    g = torch.Generator().manual_seed(77)
+    scale = d ** -0.5
+    rope = O.rope_table(256, d)
+    seqs = {}  # seq id -> dict(slot, pos, states [L] of [H, M, d, d, 2] float64)
+    schedule = {0: [("join", 0, 10), ("join", 1, 0), ("join", 2, 50)], 3: [("leave", 1), ("join", 3, 7)],
+                5: [("join", 4, 200), ("join", 5, 3)], 7: [("leave", 0), ("leave", 4)], 8: [("join", 6, 1)]}
+    for step in range(12):
+        for ev in schedule.get(step, []):
+            if ev[0] == "join":
+                _, sid, p0 = ev
+                pre = [torch.randn(M, H, d, d, 2, generator=g) * 0.02 for _ in range(L)]
+                slot = pool.acquire(position=p0, states=pre)
+                seqs[sid] = dict(slot=slot, pos=p0, st=[x.permute(1, 0, 2, 3, 4).double() for x in pre])
+            else:
+                pool.release(seqs.pop(ev[1])["slot"])
+        active = torch.tensor(sorted(s["slot"] for s in seqs.values()), dtype=torch.int32)
+        for layer in range(L):
+            q, k, v = (torch.randn(S, H, d, 2, generator=g) for _ in range(3))
+            gamma = torch.sigmoid(torch.randn(S, H, M, generator=g) + 2)
+            rot = torch.randn(S, H, M, 2, generator=g)
+            y = pool.step(layer, q.cuda(), k.cuda(), v.cuda(), gamma.cuda(), active.cuda(), rot=rot.cuda())
+            y = y.cpu()
+            for sid, s in seqs.items():
+                sl = s["slot"]
+                yr, sr = O.decode_slots(s["st"][layer][None], torch.tensor([0]), q[sl:sl + 1].double(),
+                                        k[sl:sl + 1].double(), v[sl:sl + 1].double(), gamma[sl:sl + 1].double(),
+                                        scale, rot[sl:sl + 1].double(), rope=rope, pos=torch.tensor([s["pos"]]))
+                s["st"][layer] = sr[0]
+                assert _rel(y[sl], yr[0]) < REL, (step, layer, sid)
+                assert _rel(pool.state[sl, layer].cpu(), sr[0]) < REL, (step, layer, sid)
+        pool.advance(active.cuda())
+        for s in seqs.values():
+            s["pos"] += 1
+        assert pool.pos.cpu()[active.long()].tolist() == [
+            s["pos"] for s in sorted(seqs.values(), key=lambda s: s["slot"])]

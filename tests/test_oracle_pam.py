@@ -236,3 +236,64 @@ def test_multistate_grads_match_recurrence_autograd():
     g2 = grads(lambda a, b, c, g, p, r: O.recurrent(a, b, c, g + O.EPS, d, p, r))
     for a, b in zip(g1, g2):
         assert (a - b).abs().max() <= 1e-10 * (b.abs().max() + 1e-30)
+
+
+def test_rope_table_closed_form():
+    """RoPE table: rope[0] = 1, unit modulus, band 0 turns 1 rad per position,
+    band d/2 turns 10000^(-1/2) = 0.01 rad, and rope[a + b] = rope[a] * rope[b]
+    (angles linear in the position)."""
+    d, P = 64, 300
+    r = O.rope_table(P, d)
+    assert torch.allclose(r[0], torch.stack([torch.ones(d), torch.zeros(d)], -1), atol=0)
+    assert torch.allclose(r.square().sum(-1), torch.ones(P, d), atol=1e-14)
+    m = torch.arange(P, dtype=torch.float64)
+    assert torch.allclose(r[:, 0, 0], torch.cos(m)) and torch.allclose(r[:, 0, 1], torch.sin(m))
+    assert torch.allclose(r[:, d // 2, 1], torch.sin(0.01 * m), atol=1e-13)
+    for a, b in ((3, 5), (17, 200), (0, 99)):
+        assert torch.allclose(r[a + b], O.cmul(r[a], r[b]), atol=1e-12)
+
+
+def test_build_rope_cache_matches_table():
+    """The library's fp32 table (computed as the reference does, in fp32) against
+    the float64 closed form: angle error bounded by fp32 rounding of m * theta."""
+    from qllm2_amd.decode import build_rope_cache
+    P, d = 4096, 64
+    got = build_rope_cache(P, d)
+    assert got.dtype == torch.float32 and tuple(got.shape) == (P, d, 2)
+    ref = O.rope_table(P, d)
+    assert (got.double() - ref).abs().max() < 2e-3
+    assert (got.double()[:64] - ref[:64]).abs().max() < 1e-5
+
+
+def test_decode_rope_is_relative():
+    """PAM reads S q with S = sum gamma^.. v k*: with q and k rotated by the same
+    per-position phases the output depends only on position differences, so
+    decoding a sequence at offset 0 and at offset 37 gives the same outputs
+    from a zero state.  A rotation of only q (or a missing conjugate on k)
+    breaks this.  Position 0 is the identity rotation."""
+    S, G, M, d, T = 2, 3, 2, 8, 6
+    g = torch.Generator().manual_seed(21)
+    rope = O.rope_table(64, d)
+    seq = [tuple(torch.randn(S, G, d, 2, generator=g) for _ in range(3)) for _ in range(T)]
+    gamma = torch.rand(S, G, M, generator=g)
+    rot = torch.randn(S, G, M, 2, generator=g)
+    active = torch.arange(S)
+
+    def run(off, q_only=False):
+        st = torch.zeros(S, G, M, d, d, 2)
+        ys = []
+        for t, (q, k, v) in enumerate(seq):
+            if q_only:
+                y, st = O.decode_slots(st, active, O.cmul(q, rope[off + t]), k, v, gamma, 0.3, rot)
+            else:
+                y, st = O.decode_slots(st, active, q, k, v, gamma, 0.3, rot, rope=rope, pos=torch.full((S,), off + t))
+            ys.append(y)
+        return torch.stack(ys)
+
+    assert torch.allclose(run(0), run(37), atol=1e-12)
+    assert not torch.allclose(run(0, True), run(37, True), atol=1e-3)
+    st0 = torch.randn(S, G, M, d, d, 2, generator=g)
+    q, k, v = seq[0]
+    a = O.decode_slots(st0, active, q, k, v, gamma, 0.3, rot, rope=rope, pos=torch.zeros(S, dtype=torch.long))
+    b = O.decode_slots(st0, active, q, k, v, gamma, 0.3, rot)
+    assert torch.allclose(a[0], b[0], atol=1e-14) and torch.allclose(a[1], b[1], atol=1e-14)

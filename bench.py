@@ -90,7 +90,7 @@ def bench_scan_fwd(steps, warmup):
     (qr, qi), (kr, ki), (vr, vi), gamma = scan_inputs(B, H, T, d, 1, 1002, torch.float32)
 
     def step():
-        return pam_scan.scan_fwd_op(qr, qi, kr, ki, vr, vi, gamma, None, None, None, None, d ** -0.5, C)
+        return pam_scan.scan_fwd_op(qr, qi, kr, ki, vr, vi, gamma, None, None, None, None, d ** -0.5, C, False)
 
     for _ in range(warmup):
         step()

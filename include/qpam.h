@@ -35,6 +35,13 @@
  *                       v11/fused_ce.py:98-141  linear_ce_per_token /
  *                                               linear_ce_stats
  *   qpam_ce_bwd         v11/fused_ce.py:56-82   _FusedLinearCE.backward
+ *   qpam_prologue_fwd   the elementwise steps of V11PAMLayer between the
+ *                       projections and the scan: _project's RoPE / qk-norm
+ *                       (v11/model.py:290-305), _gamma_all_and_vprime /
+ *                       _gamma_and_vprime (:630-655, :309-347, floor :193-201)
+ *                       and the rotations of _phase_and_alpha (:230-257,
+ *                       consumed at :741-746)
+ *   qpam_prologue_bwd   their autograd backward
  */
 #ifndef QPAM_H
 #define QPAM_H
@@ -178,6 +185,71 @@ int qpam_scan_bwd(const qpam_scan_bwd_args *a, void *stream);
  * D [N, T, T] fp32 contiguous, D[t,s] = exp(min(c_s - c_t, 0)) for s <= t
  * else 0, c = cumsum(-log(gamma + 1e-6)).  T <= 4096. */
 int qpam_decay_matrix(int32_t n, int32_t t, const float *gamma, int64_t ldg, float *out, void *stream);
+
+/* ------------------------------------------------ PAM layer prologue -----
+ * One pass from the layer's projections to the scan's inputs:
+ *   q' = nrm(q * rope[rope_offset + t]),  k' = nrm(k * rope[rope_offset + t])
+ *   p  = sigmoid(protect[b,t,h])                     (GSP; p = 0 without it)
+ *   base_m = exp(-softplus(dt[b,t,h] + dt_bias[h] + state_offset[m]))
+ *   base_m <- floor + (1 - floor) base_m             (only when floor > 0)
+ *   gamma[m,b,h,t] = base_m (1 - p) + p,   v' = v (1 - p)
+ *   rot[m,b,h,t] = routing[b,t,h,m] e^{i phase[b,t,h,m]}
+ * with complex products per element, nrm(z) = z / sqrt(re^2 + im^2 + 1e-8)
+ * when qk_norm (else the identity), softplus(x) = x for x > 20 else
+ * log(1 + e^x).  q, k, v: planar views [B,T,H,d] (strides sx_b, sx_t, sx_h
+ * shared by the six planes, d contiguous; a fused QKV projection's planes
+ * [B,T,3,H,d] give them without copies), in_dtype.  q', k', v': planar
+ * [B,H,T,d] contiguous in out_dtype -- the scan's q, k, v.  gamma, rot: fp32
+ * [M,B,H,T] contiguous -- the scan's gamma and rot.  d == 64, 1 <= M <= 4.
+ * Rope rows past rope_len - 1 are clamped to the last row (size the table to
+ * cover rope_offset + T).
+ */
+typedef struct {
+    int32_t B, T, H, d, M;
+    int32_t in_dtype, out_dtype;        /* qpam_dtype */
+    int32_t qk_norm;
+    float gamma_floor;
+    int32_t rope_offset, rope_len;
+    const float *rope;                  /* [rope_len][d][2], optional (NULL = none) */
+    const void *q_re, *q_im, *k_re, *k_im, *v_re, *v_im;
+    int64_t sx_b, sx_t, sx_h;
+    const float *dt;                    /* [B,T,H] pre-bias decay logits */
+    int64_t sd_b, sd_t, sd_h;
+    const float *dt_bias;               /* [H] */
+    const float *state_offset;          /* [M], optional (NULL = 0) */
+    const float *protect;               /* [B,T,H] protect-gate logits, optional */
+    int64_t sp_b, sp_t, sp_h;
+    const float *phase;                 /* [B,T,H,M], optional (NULL = no rot) */
+    const float *routing;               /* [B,T,H,M], optional (NULL = 1) */
+    int64_t sr_b, sr_t, sr_h, sr_m;     /* shared by phase and routing */
+    void *oq_re, *oq_im, *ok_re, *ok_im, *ov_re, *ov_im;
+    float *gamma;
+    float *rot_re, *rot_im;             /* required when phase is given */
+} qpam_prologue_args;
+
+int qpam_prologue_fwd(const qpam_prologue_args *a, void *stream);
+
+/* Backward of qpam_prologue_fwd (`fwd` describes the forward call; its
+ * outputs are not read).  In: gradients of q', k', v' ([B,H,T,d] contiguous,
+ * out_dtype), of gamma and (when phase) rot ([M,B,H,T] fp32).  Out: the
+ * gradients of the projections q, k, v (planar views [B,T,H,d] with strides
+ * sg_b, sg_t, sg_h, in_dtype); dpre [M,B,H,T] = dL/d(dt + dt_bias +
+ * state_offset_m) (dt's gradient is its sum over m, dt_bias's and
+ * state_offset's the sums over the other axes); dprotect [B,H,T] (when
+ * protect); dphase and, optionally, drouting [M,B,H,T] (when phase). */
+typedef struct {
+    const qpam_prologue_args *fwd;
+    const void *gq_re, *gq_im, *gk_re, *gk_im, *gv_re, *gv_im;
+    const float *ggamma;
+    const float *grot_re, *grot_im;     /* required when phase is given */
+    void *dq_re, *dq_im, *dk_re, *dk_im, *dv_re, *dv_im;
+    int64_t sg_b, sg_t, sg_h;
+    float *dpre;
+    float *dprotect;
+    float *dphase, *drouting;
+} qpam_prologue_bwd_args;
+
+int qpam_prologue_bwd(const qpam_prologue_bwd_args *a, void *stream);
 
 /* ------------------------------------------------ complex elementwise -----
  * Split-real complex tensors [rows, dim, 2] (interleaved re/im, contiguous),

@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -110,6 +110,33 @@ class CplxArgs(ctypes.Structure):
 
 
 # symbol -> (restype, argtypes); every symbol include/qpam.h declares
+class PrologueArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_i32), ("T", c_i32), ("H", c_i32), ("d", c_i32), ("M", c_i32),
+        ("in_dtype", c_i32), ("out_dtype", c_i32), ("qk_norm", c_i32), ("gamma_floor", c_f32),
+        ("rope_offset", c_i32), ("rope_len", c_i32), ("rope", c_ptr),
+        ("q_re", c_ptr), ("q_im", c_ptr), ("k_re", c_ptr), ("k_im", c_ptr), ("v_re", c_ptr), ("v_im", c_ptr),
+        ("sx_b", c_i64), ("sx_t", c_i64), ("sx_h", c_i64),
+        ("dt", c_ptr), ("sd_b", c_i64), ("sd_t", c_i64), ("sd_h", c_i64),
+        ("dt_bias", c_ptr), ("state_offset", c_ptr),
+        ("protect", c_ptr), ("sp_b", c_i64), ("sp_t", c_i64), ("sp_h", c_i64),
+        ("phase", c_ptr), ("routing", c_ptr), ("sr_b", c_i64), ("sr_t", c_i64), ("sr_h", c_i64), ("sr_m", c_i64),
+        ("oq_re", c_ptr), ("oq_im", c_ptr), ("ok_re", c_ptr), ("ok_im", c_ptr), ("ov_re", c_ptr), ("ov_im", c_ptr),
+        ("gamma", c_ptr), ("rot_re", c_ptr), ("rot_im", c_ptr),
+    ]
+
+
+class PrologueBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", ctypes.POINTER(PrologueArgs)),
+        ("gq_re", c_ptr), ("gq_im", c_ptr), ("gk_re", c_ptr), ("gk_im", c_ptr), ("gv_re", c_ptr), ("gv_im", c_ptr),
+        ("ggamma", c_ptr), ("grot_re", c_ptr), ("grot_im", c_ptr),
+        ("dq_re", c_ptr), ("dq_im", c_ptr), ("dk_re", c_ptr), ("dk_im", c_ptr), ("dv_re", c_ptr), ("dv_im", c_ptr),
+        ("sg_b", c_i64), ("sg_t", c_i64), ("sg_h", c_i64),
+        ("dpre", c_ptr), ("dprotect", c_ptr), ("dphase", c_ptr), ("drouting", c_ptr),
+    ]
+
+
 SIGNATURES = {
     "qpam_version": (ctypes.c_int, []),
     "qpam_last_error": (ctypes.c_char_p, []),
@@ -129,6 +156,8 @@ SIGNATURES = {
     "qpam_cplx_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(CplxArgs)]),
     "qpam_cplx_fwd": (ctypes.c_int, [ctypes.POINTER(CplxArgs), c_ptr]),
     "qpam_cplx_bwd": (ctypes.c_int, [ctypes.POINTER(CplxArgs), c_ptr]),
+    "qpam_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(PrologueArgs), c_ptr]),
+    "qpam_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(PrologueBwdArgs), c_ptr]),
 }
 
 _LIB = None

@@ -1,0 +1,337 @@
+// PAM layer prologue: projections -> scan inputs in one HBM pass, and its
+// backward.
+//
+// Reference semantics (v11/model.py): _project's RoPE product and optional
+// qk-norm (:290-305), the decay / GSP blend of _gamma_all_and_vprime and
+// _gamma_and_vprime (:630-655, :309-347, gamma floor :193-201), and the state
+// rotations routing * e^{i phase} of _phase_and_alpha (:230-257) that
+// _forward_multistate_fused hands to the chunk loop (:741-746).  The reference
+// runs these as separate elementwise passes plus the [B,T,H] -> [B,H,T]
+// transposes; here one kernel reads each projection element once and writes
+// the scan's planar [B,H,T,d] operands, the decays and the rotations.
+//
+// Layout: one block of 4 waves per (b, h, 64 consecutive tokens).  The per-token
+// scalars (decays of the M states, protect gate, rotations) take one thread per
+// (state, token), so their [M,B,H,T] rows are written as 256-byte runs.  For
+// the vectors a token row of d = 64 complex elements is one DPP row of 16 lanes
+// (4 elements each: one 16-byte fp32 or 8-byte bf16 access per plane), a wave
+// covers 4 tokens per step and 16 per block slice.
+#include "common.h"
+
+namespace qpam {
+namespace {
+
+constexpr int D = 64;
+constexpr int PT = 64;        // tokens per block
+constexpr int PTHREADS = 256;
+
+struct Bf16 {};
+
+template <typename T> struct Io;
+template <> struct Io<float> {
+    __device__ __forceinline__ static void load4(const void *base, int64_t off, float (&o)[4]) {
+        const floatx4 v = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(base) + off);
+        o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
+    }
+    __device__ __forceinline__ static void store4(void *base, int64_t off, const float (&v)[4]) {
+        *reinterpret_cast<floatx4 *>(static_cast<float *>(base) + off) = floatx4{v[0], v[1], v[2], v[3]};
+    }
+};
+template <> struct Io<Bf16> {
+    __device__ __forceinline__ static void load4(const void *base, int64_t off, float (&o)[4]) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const unsigned short *>(base) + off);
+        o[0] = __uint_as_float(v.x << 16), o[1] = __uint_as_float(v.x & 0xffff0000u);
+        o[2] = __uint_as_float(v.y << 16), o[3] = __uint_as_float(v.y & 0xffff0000u);
+    }
+    __device__ __forceinline__ static void store4(void *base, int64_t off, const float (&v)[4]) {
+        *reinterpret_cast<uint2 *>(static_cast<unsigned short *>(base) + off) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+};
+
+__device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+
+// decay logit of state m: dt + dt_bias + state_offset
+__device__ __forceinline__ float pre_sum(const qpam_prologue_args &a, int b, int t, int h, int m) {
+    return a.dt[b * a.sd_b + (int64_t)t * a.sd_t + h * a.sd_h] + a.dt_bias[h] + (a.state_offset ? a.state_offset[m] : 0.f);
+}
+
+// exp(-softplus(pre)) lifted onto [floor, 1) when floor > 0
+__device__ __forceinline__ float lifted_decay(const qpam_prologue_args &a, float pre) {
+    const float base = expf(-softplus(pre));
+    return a.gamma_floor > 0.f ? a.gamma_floor + (1.f - a.gamma_floor) * base : base;
+}
+
+__device__ __forceinline__ float protect_prob(const qpam_prologue_args &a, int b, int t, int h) {
+    return a.protect ? sigmoid(a.protect[b * a.sp_b + (int64_t)t * a.sp_t + h * a.sp_h]) : 0.f;
+}
+
+// this lane's 4 rope factors (c, s) for the token at position rope_offset + t
+__device__ __forceinline__ void rope4(const qpam_prologue_args &a, int t, int c4, float (&c)[4], float (&s)[4]) {
+    const int p = min(max(a.rope_offset + t, 0), a.rope_len - 1);
+    const floatx4 *rp = reinterpret_cast<const floatx4 *>(a.rope + ((int64_t)p * D + c4) * 2);
+    const floatx4 r0 = rp[0], r1 = rp[1];
+    c[0] = r0.x, s[0] = r0.y, c[1] = r0.z, s[1] = r0.w, c[2] = r1.x, s[2] = r1.y, c[3] = r1.z, s[3] = r1.w;
+}
+
+__device__ __forceinline__ int64_t tile_count(const qpam_prologue_args &a) { return (a.T + PT - 1) / PT; }
+
+template <typename TI, typename TO>
+__global__ void __launch_bounds__(PTHREADS) prologue_fwd_kernel(qpam_prologue_args a) {
+    __shared__ float s_keep[PT];
+    const int nt = (int)tile_count(a);
+    const int bh = blockIdx.x / nt, tile = blockIdx.x - bh * nt;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int t0 = tile * PT, tid = threadIdx.x;
+
+    {   // scalars: thread = (state m, token)
+        const int tt = tid & (PT - 1), m = tid / PT, t = t0 + tt;
+        if (t < a.T) {
+            const float p = protect_prob(a, b, t, h);
+            if (m == 0) s_keep[tt] = 1.f - p;
+            if (m < a.M) {
+                const float base = lifted_decay(a, pre_sum(a, b, t, h, m));
+                const int64_t o = (((int64_t)m * a.B + b) * a.H + h) * a.T + t;
+                a.gamma[o] = base * (1.f - p) + p;
+                if (a.phase) {
+                    const int64_t po = b * a.sr_b + (int64_t)t * a.sr_t + h * a.sr_h + m * a.sr_m;
+                    const float r = a.routing ? a.routing[po] : 1.f;
+                    float sn, cs;
+                    sincosf(a.phase[po], &sn, &cs);
+                    a.rot_re[o] = r * cs;
+                    a.rot_im[o] = r * sn;
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    const int w = tid >> 6, lane = tid & 63, c4 = (lane & 15) * 4;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int tt = w * 16 + it * 4 + (lane >> 4), t = t0 + tt;
+        if (t >= a.T) continue;
+        const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
+        float qr[4], qi[4], kr[4], ki[4], vr[4], vi[4];
+        Io<TI>::load4(a.q_re, xo, qr), Io<TI>::load4(a.q_im, xo, qi);
+        Io<TI>::load4(a.k_re, xo, kr), Io<TI>::load4(a.k_im, xo, ki);
+        Io<TI>::load4(a.v_re, xo, vr), Io<TI>::load4(a.v_im, xo, vi);
+        if (a.rope) {
+            float c[4], s[4];
+            rope4(a, t, c4, c, s);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float q0 = qr[j], k0 = kr[j];
+                qr[j] = q0 * c[j] - qi[j] * s[j], qi[j] = q0 * s[j] + qi[j] * c[j];
+                kr[j] = k0 * c[j] - ki[j] * s[j], ki[j] = k0 * s[j] + ki[j] * c[j];
+            }
+        }
+        if (a.qk_norm) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float iq = 1.f / sqrtf(qr[j] * qr[j] + qi[j] * qi[j] + 1e-8f);
+                const float ik = 1.f / sqrtf(kr[j] * kr[j] + ki[j] * ki[j] + 1e-8f);
+                qr[j] *= iq, qi[j] *= iq, kr[j] *= ik, ki[j] *= ik;
+            }
+        }
+        const float keep = s_keep[tt];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vr[j] *= keep, vi[j] *= keep;
+        const int64_t oo = (((int64_t)b * a.H + h) * a.T + t) * D + c4;
+        Io<TO>::store4(a.oq_re, oo, qr), Io<TO>::store4(a.oq_im, oo, qi);
+        Io<TO>::store4(a.ok_re, oo, kr), Io<TO>::store4(a.ok_im, oo, ki);
+        Io<TO>::store4(a.ov_re, oo, vr), Io<TO>::store4(a.ov_im, oo, vi);
+    }
+}
+
+// Backward of z -> nrm(z * r) for one element: g is dL/d(output); returns
+// dL/dz.  With u = z r (|r| = 1), nrm(u) = u / m, m = sqrt(|u|^2 + 1e-8):
+// du = g / m - u (g.u) / m^3, then dz = du * conj(r).
+__device__ __forceinline__ void rope_norm_bwd(float zr, float zi, float c, float s, bool rope, bool norm, float &gr,
+                                              float &gi) {
+    if (norm) {
+        const float ur = rope ? zr * c - zi * s : zr, ui = rope ? zr * s + zi * c : zi;
+        const float im = 1.f / sqrtf(ur * ur + ui * ui + 1e-8f);
+        const float dot = (gr * ur + gi * ui) * im * im;
+        gr = (gr - ur * dot) * im;
+        gi = (gi - ui * dot) * im;
+    }
+    if (rope) {
+        const float r0 = gr;
+        gr = r0 * c + gi * s;
+        gi = gi * c - r0 * s;
+    }
+}
+
+template <typename TI, typename TO>
+__global__ void __launch_bounds__(PTHREADS) prologue_bwd_kernel(qpam_prologue_bwd_args g, qpam_prologue_args a) {
+    __shared__ float s_keep[PT], s_gvv[PT];
+    const int nt = (int)tile_count(a);
+    const int bh = blockIdx.x / nt, tile = blockIdx.x - bh * nt;
+    const int b = bh / a.H, h = bh - b * a.H;
+    const int t0 = tile * PT, tid = threadIdx.x;
+    if (tid < PT) s_keep[tid] = t0 + tid < a.T ? 1.f - protect_prob(a, b, t0 + tid, h) : 1.f;
+    __syncthreads();
+
+    const int w = tid >> 6, lane = tid & 63, c4 = (lane & 15) * 4;
+    const bool rope = a.rope != nullptr, norm = a.qk_norm != 0;
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int tt = w * 16 + it * 4 + (lane >> 4), t = t0 + tt;
+        // whole DPP rows share t, so a row is either all in or all out of range
+        if (t >= a.T) continue;
+        const int64_t oo = (((int64_t)b * a.H + h) * a.T + t) * D + c4;
+        const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
+        const int64_t go = b * g.sg_b + (int64_t)t * g.sg_t + h * g.sg_h + c4;
+        float gqr[4], gqi[4], gkr[4], gki[4], gvr[4], gvi[4], vr[4], vi[4];
+        Io<TO>::load4(g.gq_re, oo, gqr), Io<TO>::load4(g.gq_im, oo, gqi);
+        Io<TO>::load4(g.gk_re, oo, gkr), Io<TO>::load4(g.gk_im, oo, gki);
+        Io<TO>::load4(g.gv_re, oo, gvr), Io<TO>::load4(g.gv_im, oo, gvi);
+        Io<TI>::load4(a.v_re, xo, vr), Io<TI>::load4(a.v_im, xo, vi);
+        if (rope || norm) {
+            float c[4] = {1.f, 1.f, 1.f, 1.f}, s[4] = {0.f, 0.f, 0.f, 0.f};
+            if (rope) rope4(a, t, c4, c, s);
+            float qr[4], qi[4], kr[4], ki[4];
+            if (norm) {
+                Io<TI>::load4(a.q_re, xo, qr), Io<TI>::load4(a.q_im, xo, qi);
+                Io<TI>::load4(a.k_re, xo, kr), Io<TI>::load4(a.k_im, xo, ki);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                rope_norm_bwd(norm ? qr[j] : 0.f, norm ? qi[j] : 0.f, c[j], s[j], rope, norm, gqr[j], gqi[j]);
+                rope_norm_bwd(norm ? kr[j] : 0.f, norm ? ki[j] : 0.f, c[j], s[j], rope, norm, gkr[j], gki[j]);
+            }
+        }
+        const float keep = s_keep[tt];
+        float dot = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            dot += gvr[j] * vr[j] + gvi[j] * vi[j];
+            gvr[j] *= keep, gvi[j] *= keep;
+        }
+        dot = row16_sum(dot);
+        if ((lane & 15) == 0) s_gvv[tt] = dot;
+        Io<TI>::store4(g.dq_re, go, gqr), Io<TI>::store4(g.dq_im, go, gqi);
+        Io<TI>::store4(g.dk_re, go, gkr), Io<TI>::store4(g.dk_im, go, gki);
+        Io<TI>::store4(g.dv_re, go, gvr), Io<TI>::store4(g.dv_im, go, gvi);
+    }
+    __syncthreads();
+
+    {   // scalars: thread = (state m, token)
+        const int tt = tid & (PT - 1), m = tid / PT, t = t0 + tt;
+        if (t < a.T && m < a.M) {
+            const float p = 1.f - s_keep[tt];
+            const int64_t o = (((int64_t)m * a.B + b) * a.H + h) * a.T + t;
+            // d gamma / d pre = (1 - p) (1 - floor) (-exp(-softplus(pre))) softplus'(pre)
+            const float pre = pre_sum(a, b, t, h, m);
+            const float raw = expf(-softplus(pre));
+            const float dsp = pre > 20.f ? 1.f : sigmoid(pre);
+            const float lift = a.gamma_floor > 0.f ? 1.f - a.gamma_floor : 1.f;
+            g.dpre[o] = -g.ggamma[o] * (1.f - p) * lift * raw * dsp;
+            if (a.phase) {
+                const int64_t po = b * a.sr_b + (int64_t)t * a.sr_t + h * a.sr_h + m * a.sr_m;
+                const float r = a.routing ? a.routing[po] : 1.f;
+                float sn, cs;
+                sincosf(a.phase[po], &sn, &cs);
+                const float gr = g.grot_re[o], gi = g.grot_im[o];
+                g.dphase[o] = r * (gi * cs - gr * sn);
+                if (g.drouting) g.drouting[o] = gr * cs + gi * sn;
+            }
+            if (m == 0 && a.protect) {
+                // d gamma_m / d p = 1 - base_m;  d v' / d p = -v
+                float dp = -s_gvv[tt];
+                for (int mm = 0; mm < a.M; ++mm)
+                    dp += g.ggamma[(((int64_t)mm * a.B + b) * a.H + h) * a.T + t] *
+                          (1.f - lifted_decay(a, pre_sum(a, b, t, h, mm)));
+                g.dprotect[((int64_t)b * a.H + h) * a.T + t] = dp * p * (1.f - p);
+            }
+        }
+    }
+}
+
+bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
+
+// everything the backward reads of the forward description (not its outputs)
+int validate_inputs(const qpam_prologue_args *a) {
+    QPAM_REQUIRE(a != nullptr, "qpam_prologue: null arguments");
+    QPAM_REQUIRE(a->B >= 0 && a->T >= 0 && a->H >= 1 && a->M >= 1 && a->M <= 4,
+                 "qpam_prologue: invalid sizes B=%d T=%d H=%d M=%d (1 <= M <= 4)", a->B, a->T, a->H, a->M);
+    QPAM_REQUIRE(a->d == D, "qpam_prologue: head_dim %d unsupported (64 only)", a->d);
+    QPAM_REQUIRE((a->in_dtype == QPAM_F32 || a->in_dtype == QPAM_BF16) &&
+                     (a->out_dtype == QPAM_F32 || a->out_dtype == QPAM_BF16),
+                 "qpam_prologue: dtypes must be QPAM_F32 or QPAM_BF16");
+    const int vin = a->in_dtype == QPAM_F32 ? 16 : 8;
+    QPAM_REQUIRE(a->q_re && a->q_im && a->k_re && a->k_im && a->v_re && a->v_im && a->dt && a->dt_bias,
+                 "qpam_prologue: q, k, v, dt and dt_bias are required");
+    QPAM_REQUIRE(aligned(a->q_re, vin) && aligned(a->q_im, vin) && aligned(a->k_re, vin) && aligned(a->k_im, vin) &&
+                     aligned(a->v_re, vin) && aligned(a->v_im, vin) && a->sx_b % 4 == 0 && a->sx_t % 4 == 0 &&
+                     a->sx_h % 4 == 0,
+                 "qpam_prologue: projection planes need %d-byte aligned rows (strides multiple of 4)", vin);
+    QPAM_REQUIRE(a->rope == nullptr || (a->rope_len >= 1 && aligned(a->rope, 16)),
+                 "qpam_prologue: rope needs rope_len >= 1 and a 16-byte aligned table");
+    QPAM_REQUIRE(a->routing == nullptr || a->phase, "qpam_prologue: routing needs phase");
+    return QPAM_OK;
+}
+
+int validate_outputs(const qpam_prologue_args *a) {
+    const int vout = a->out_dtype == QPAM_F32 ? 16 : 8;
+    QPAM_REQUIRE(a->oq_re && a->oq_im && a->ok_re && a->ok_im && a->ov_re && a->ov_im && a->gamma &&
+                     aligned(a->oq_re, vout) && aligned(a->oq_im, vout) && aligned(a->ok_re, vout) &&
+                     aligned(a->ok_im, vout) && aligned(a->ov_re, vout) && aligned(a->ov_im, vout),
+                 "qpam_prologue: outputs q', k', v' (%d-byte aligned) and gamma required", vout);
+    QPAM_REQUIRE(a->phase == nullptr || (a->rot_re && a->rot_im), "qpam_prologue: phase given without rot outputs");
+    return QPAM_OK;
+}
+
+}  // namespace
+}  // namespace qpam
+
+using namespace qpam;
+
+extern "C" int qpam_prologue_fwd(const qpam_prologue_args *a, void *stream) {
+    int st = validate_inputs(a);
+    if (!st) st = validate_outputs(a);
+    if (st) return st;
+    const long long blocks = (long long)a->B * a->H * ((a->T + PT - 1) / PT);
+    if (blocks == 0) return QPAM_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)blocks), block(PTHREADS);
+    const bool fi = a->in_dtype == QPAM_F32, fo = a->out_dtype == QPAM_F32;
+    if (fi && fo) hipLaunchKernelGGL((prologue_fwd_kernel<float, float>), grid, block, 0, s, *a);
+    else if (fi) hipLaunchKernelGGL((prologue_fwd_kernel<float, Bf16>), grid, block, 0, s, *a);
+    else if (fo) hipLaunchKernelGGL((prologue_fwd_kernel<Bf16, float>), grid, block, 0, s, *a);
+    else hipLaunchKernelGGL((prologue_fwd_kernel<Bf16, Bf16>), grid, block, 0, s, *a);
+    return launch_status("prologue_fwd_kernel");
+}
+
+extern "C" int qpam_prologue_bwd(const qpam_prologue_bwd_args *g, void *stream) {
+    QPAM_REQUIRE(g != nullptr && g->fwd != nullptr, "qpam_prologue_bwd: null arguments");
+    const qpam_prologue_args &a = *g->fwd;
+    int st = validate_inputs(&a);
+    if (st) return st;
+    const int vin = a.in_dtype == QPAM_F32 ? 16 : 8, vout = a.out_dtype == QPAM_F32 ? 16 : 8;
+    QPAM_REQUIRE(g->gq_re && g->gq_im && g->gk_re && g->gk_im && g->gv_re && g->gv_im && g->ggamma &&
+                     aligned(g->gq_re, vout) && aligned(g->gq_im, vout) && aligned(g->gk_re, vout) &&
+                     aligned(g->gk_im, vout) && aligned(g->gv_re, vout) && aligned(g->gv_im, vout),
+                 "qpam_prologue_bwd: gradients of q', k', v' and gamma required, %d-byte aligned", vout);
+    QPAM_REQUIRE(g->dq_re && g->dq_im && g->dk_re && g->dk_im && g->dv_re && g->dv_im && aligned(g->dq_re, vin) &&
+                     aligned(g->dq_im, vin) && aligned(g->dk_re, vin) && aligned(g->dk_im, vin) &&
+                     aligned(g->dv_re, vin) && aligned(g->dv_im, vin) && g->sg_b % 4 == 0 && g->sg_t % 4 == 0 &&
+                     g->sg_h % 4 == 0,
+                 "qpam_prologue_bwd: projection gradients required, %d-byte aligned rows", vin);
+    QPAM_REQUIRE(g->dpre != nullptr, "qpam_prologue_bwd: dpre required");
+    QPAM_REQUIRE(a.protect == nullptr || g->dprotect != nullptr, "qpam_prologue_bwd: dprotect required with protect");
+    QPAM_REQUIRE(a.phase == nullptr || (g->grot_re && g->grot_im && g->dphase),
+                 "qpam_prologue_bwd: rot gradients and dphase required with phase");
+    const long long blocks = (long long)a.B * a.H * ((a.T + PT - 1) / PT);
+    if (blocks == 0) return QPAM_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)blocks), block(PTHREADS);
+    const bool fi = a.in_dtype == QPAM_F32, fo = a.out_dtype == QPAM_F32;
+    if (fi && fo) hipLaunchKernelGGL((prologue_bwd_kernel<float, float>), grid, block, 0, s, *g, a);
+    else if (fi) hipLaunchKernelGGL((prologue_bwd_kernel<float, Bf16>), grid, block, 0, s, *g, a);
+    else if (fo) hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, float>), grid, block, 0, s, *g, a);
+    else hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, Bf16>), grid, block, 0, s, *g, a);
+    return launch_status("prologue_bwd_kernel");
+}

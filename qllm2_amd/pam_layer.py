@@ -10,21 +10,32 @@ Reference methods replaced (v11/model.py):
   _recurrent                845-925  (decode token loop; all K states of a
                                       token in one kernel launch)
 
-Every replacement keeps the layer's own projections/gates (_phase_and_alpha,
-_gamma_all_and_vprime, _gamma_and_vprime) and replaces only the PAM math.
-Modes outside the hot path (E1 per-channel decay, E2 delta write) keep the
-reference methods: install() leaves them reachable as the saved originals.
+  forward                   785-843  prefill of the production modes (head
+                                      decay, additive write, E3 fused or one
+                                      state, head_dim 64): projections as
+                                      planar GEMMs, one prologue kernel, the
+                                      scan writing Y head-merged, o_proj on the
+                                      planar Y; other calls go to the original
+
+The method replacements keep the layer's own projections/gates
+(_phase_and_alpha, _gamma_all_and_vprime, _gamma_and_vprime) and replace only
+the PAM math; the forward replacement fuses those elementwise steps into the
+prologue kernel (qpam_prologue_fwd).  Modes outside the hot path (E1
+per-channel decay, E2 delta write) keep the reference methods: install()
+leaves them reachable as the saved originals.
 """
 
 import sys
 
 import torch
+import torch.nn.functional as F
 
 from . import decode as _decode
 from . import fused_ce as _fused_ce
 from . import flash_pam as _flash_pam
 from . import triton_kernels as _tk
-from .pam_scan import pam_scan_interleaved
+from .pam_prologue import pam_prologue
+from .pam_scan import chunk_for, pam_scan_interleaved, pam_scan_planar
 
 
 def _cat_rot(phase, routing):
@@ -120,9 +131,91 @@ def recurrent(self, x, queries, keys, values, state, head_dim):
     return out, (new_state if k_states > 1 else new_state[0])
 
 
+def _complex_linear_planar(mod, xr, xi):
+    """ComplexLinear.forward (v11/complex_ops.py:165-172) on planar input,
+    returning the planar (re, im) pair instead of the stacked [..., 2]."""
+    wr, wi = mod.weight_real, mod.weight_imag
+    re = F.linear(xr, wr) - F.linear(xi, wi)
+    im = F.linear(xr, wi) + F.linear(xi, wr)
+    if getattr(mod, "bias_real", None) is not None:
+        re, im = re + mod.bias_real, im + mod.bias_imag
+    return re, im
+
+
+def _fused_prefill(self, x, state):
+    return (state is None and x.dim() == 4 and x.shape[1] > 1 and x.is_cuda
+            and getattr(self, "decay_mode", "head") != "per_channel" and self.write_mode == "additive"
+            and self.head_dim == 64 and 1 <= self.n_states <= 4
+            and (self.n_states == 1 or getattr(self, "fused_e3", True)))
+
+
+def forward(self, x, state=None, step_offset: int = 0):
+    """V11PAMLayer.forward (v11/model.py:785-843) for a prefill of the
+    production modes; everything else runs the original forward.
+
+    x [B,T,dim,2] -> (out [B,T,dim,2], state [K,B,H,d,d,2] or [B,H,d,d,2]).
+    The QKV projection runs as planar GEMMs (no interleave, no transposes),
+    qpam_prologue_fwd turns its planes, the decay / gate / phase logits and the
+    RoPE table into the scan's operands in one pass, the scan writes Y as
+    [B,T,H,d] planes (the head-merged layout of :834-835) and o_proj reads them
+    as they are."""
+    if not _fused_prefill(self, x, state):
+        return _ORIGINALS["forward"](self, x, state, step_offset)
+    b, t = x.shape[0], x.shape[1]
+    h, d, m = self.num_heads, self.head_dim, self.n_states
+    xr, xi = x[..., 0], x[..., 1]
+    if self.fused_qkv:
+        qkv_re, qkv_im = _complex_linear_planar(self.qkv_proj, xr, xi)
+        qkv_re, qkv_im = qkv_re.view(b, t, 3, h, d), qkv_im.view(b, t, 3, h, d)
+    else:
+        parts = [_complex_linear_planar(p, xr, xi) for p in (self.q_proj, self.k_proj, self.v_proj)]
+        qkv_re = torch.stack([p[0].view(b, t, h, d) for p in parts], 2)
+        qkv_im = torch.stack([p[1].view(b, t, h, d) for p in parts], 2)
+    if qkv_re.dtype not in (torch.float32, torch.bfloat16):
+        qkv_re, qkv_im = qkv_re.float(), qkv_im.float()
+    rope = None
+    if self.use_rope:
+        end = step_offset + t
+        if end > self.rope_cache.shape[0]:  # grown as the reference does (v11/model.py:291-297)
+            self.register_buffer("rope_cache", _decode.build_rope_cache(end * 2, d, device=x.device),
+                                 persistent=False)
+        rope = self.rope_cache.float()
+    x_flat = torch.cat([xr, xi], dim=-1)
+    dt = self.dt_proj(x_flat)                                            # [B,T,H]
+    protect = None
+    if self.use_gsp:
+        gate_in = x_flat if self.gate_content_aware else torch.sqrt(xr.square() + xi.square() + 1e-8)
+        protect = self.protect_gate(gate_in)                             # [B,T,H]
+        if self.gate_surprisal_lambda > 0 and self.training:
+            self._gate_prob_bt = torch.sigmoid(protect).mean(dim=2)      # [B,T]
+    phase = routing = offsets = None
+    if m > 1:
+        phase, routing_w = self._phase_and_alpha(x)                      # [B,T,H,K]
+        self._route_aux = self._route_balance_loss(routing_w)
+        routing = routing_w if self.state_compete else None
+        offsets = self.state_dt_offset
+    (qr, qi), (kr, ki), (vr, vi), gamma, rot = pam_prologue(
+        qkv_re, qkv_im, dt, self.dt_bias, n_states=m, state_offset=offsets, protect=protect, phase=phase,
+        routing=routing, rope=rope, rope_offset=step_offset, qk_norm=self.qk_norm,
+        gamma_floor=self.gamma_floor or 0.0)
+    y_re, y_im, s_re, s_im = pam_scan_planar(qr, qi, kr, ki, vr, vi, gamma, q_scale=d ** -0.5,
+                                             chunk=chunk_for(self.chunk_size, t), rot=rot, y_layout="bthd")
+    if x.dtype != torch.float32:
+        y_re, y_im = y_re.to(x.dtype), y_im.to(x.dtype)
+    out_re, out_im = _complex_linear_planar(self.o_proj, y_re.view(b, t, h * d), y_im.view(b, t, h * d))
+    if self.training:
+        # one keep-mask per complex value (as_complex_dropout_mask, v11/complex_ops.py:59-66)
+        mask = self.dropout(torch.ones(out_re.shape, device=out_re.device, dtype=out_re.dtype))
+        out_re, out_im = out_re * mask, out_im * mask
+    out = torch.stack([out_re, out_im], dim=-1)
+    new_state = torch.stack([s_re, s_im], dim=-1).to(x.dtype)
+    return out, (new_state if m > 1 else new_state[0])
+
+
 _ORIGINALS = {}
 
 _METHODS = {
+    "forward": forward,
     "_forward_chunked_head": forward_chunked_head,
     "_fused_chunk_step": fused_chunk_step,
     "_forward_multistate_fused": forward_multistate_fused,

@@ -14,6 +14,9 @@ def test_install_rebinds_methods_and_aliases():
     mod = types.ModuleType("v11x.model")
 
     class V11PAMLayer:
+        def forward(self, *a):
+            return "orig"
+
         @staticmethod
         def _dual_form_block(*a):
             return "orig"
@@ -45,6 +48,7 @@ def test_install_rebinds_methods_and_aliases():
     pam_layer._ORIGINALS.clear()
     try:
         originals = pam_layer.install(mod)
+        assert V11PAMLayer.forward is pam_layer.forward
         assert V11PAMLayer._forward_chunked_head is pam_layer.forward_chunked_head
         assert V11PAMLayer._fused_chunk_step is pam_layer.fused_chunk_step
         assert V11PAMLayer._forward_multistate_fused is pam_layer.forward_multistate_fused
@@ -56,7 +60,7 @@ def test_install_rebinds_methods_and_aliases():
         assert sys.modules["v11x.triton_kernels"] is triton_kernels
         assert sys.modules["v11x.fused_ce"] is fused_ce
         assert pkg.fused_ce is fused_ce
-        assert set(originals) >= {"_forward_chunked_head", "_recurrent", "_dual_form_block"}
+        assert set(originals) >= {"forward", "_forward_chunked_head", "_recurrent", "_dual_form_block"}
         for name in ("fused_complex_norm", "fused_mod_swish", "fused_mod_relu", "fused_cgu_gate"):
             assert getattr(cops, name) is getattr(triton_kernels, name)
     finally:

@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=1000)
-    ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "e3", "ce", "cplx", "copy"], default=None,
+    ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "e3", "ce", "cplx", "layer", "copy"], default=None,
                     help="run one workload (for profiler passes) and print its own JSON line")
     return ap.parse_args()
 
@@ -90,7 +90,7 @@ def bench_scan_fwd(steps, warmup):
     (qr, qi), (kr, ki), (vr, vi), gamma = scan_inputs(B, H, T, d, 1, 1002, torch.float32)
 
     def step():
-        return pam_scan.scan_fwd_op(qr, qi, kr, ki, vr, vi, gamma, None, None, None, None, d ** -0.5, C, False)
+        return pam_scan.scan_fwd_op(qr, qi, kr, ki, vr, vi, gamma, None, None, None, None, d ** -0.5, C, 0)
 
     for _ in range(warmup):
         step()
@@ -299,6 +299,160 @@ def bench_complex_ops(steps, warmup):
     return res
 
 
+class _BenchPamLayer:
+    """Parameters and attributes of a V11PAMLayer in the production E3 setting
+    (fused QKV, RoPE, GSP gate on |x|, K phase-routed states, head decay,
+    additive write), random-initialised, for timing the layer forward+backward
+    two ways: the fused path (qllm2_amd.pam_layer.forward) and the reference's
+    sequence of elementwise torch steps around the same scan kernels."""
+
+    def __init__(self, dim, H, d, M, T, dtype, seed=21):
+        import torch
+        from qllm2_amd.decode import build_rope_cache
+        g = torch.Generator().manual_seed(seed)
+        inner = H * d
+
+        def prm(*shape, std):
+            return torch.nn.Parameter((torch.randn(*shape, generator=g) * std).to("cuda", dtype))
+
+        mod = torch.nn.Module()
+        mod.num_heads, mod.head_dim, mod.n_states, mod.inner_dim = H, d, M, inner
+        mod.chunk_size, mod.use_rope, mod.use_gsp, mod.qk_norm, mod.fused_qkv = 256, True, True, False, True
+        mod.gamma_floor, mod.gate_content_aware, mod.routing_content_aware, mod.state_compete = 0.0, False, False, False
+        mod.decay_mode, mod.write_mode, mod.fused_e3, mod.gate_surprisal_lambda = "head", "additive", True, 0.0
+        for name, o, i in (("qkv_proj", 3 * inner, dim), ("o_proj", dim, inner)):
+            lin = torch.nn.Module()
+            lin.weight_real, lin.weight_imag, lin.bias_real = prm(o, i, std=i ** -0.5), prm(o, i, std=i ** -0.5), None
+            setattr(mod, name, lin)
+        mod.dt_proj = torch.nn.Linear(2 * dim, H).to("cuda", dtype)
+        mod.dt_bias = prm(H, std=0.5)
+        mod.protect_gate = torch.nn.Linear(dim, H).to("cuda", dtype)
+        mod.state_dt_offset = prm(M, std=1.0)
+        mod.phase_proj = torch.nn.Linear(dim, H * M).to("cuda", dtype)
+        mod.register_buffer("rope_cache", build_rope_cache(2 * T, d, device="cuda"), persistent=False)
+        mod.dropout = torch.nn.Dropout(0.0)
+        mod.training = False
+
+        def phase_and_alpha(x):
+            b, t = x.shape[:2]
+            phase = mod.phase_proj(torch.sqrt(x[..., 0].square() + x[..., 1].square() + 1e-8)).view(b, t, H, M)
+            return phase, torch.ones_like(phase)
+        mod._phase_and_alpha = phase_and_alpha
+        mod._route_balance_loss = lambda w: None
+        self.mod = mod
+
+    def fused(self, x):
+        from qllm2_amd import pam_layer
+        return pam_layer.forward(self.mod, x, None, 0)
+
+    def unfused(self, x):
+        """The reference's forward steps (v11/model.py:271-306, 630-655,
+        739-781, 834-836) as separate torch passes, the scan itself on the
+        same HIP kernels."""
+        import torch
+        import torch.nn.functional as F
+        from qllm2_amd.pam_scan import pam_scan_interleaved
+        m = self.mod
+        b, t = x.shape[:2]
+        H, d, M = m.num_heads, m.head_dim, m.n_states
+
+        def clin(lin, z):
+            re = F.linear(z[..., 0], lin.weight_real) - F.linear(z[..., 1], lin.weight_imag)
+            im = F.linear(z[..., 0], lin.weight_imag) + F.linear(z[..., 1], lin.weight_real)
+            return torch.stack([re, im], -1)
+
+        def cmul(a, r):
+            return torch.stack([a[..., 0] * r[..., 0] - a[..., 1] * r[..., 1],
+                                a[..., 0] * r[..., 1] + a[..., 1] * r[..., 0]], -1)
+
+        qkv = clin(m.qkv_proj, x).view(b, t, 3, H, d, 2)
+        q, k, v = (qkv[:, :, i].transpose(1, 2).contiguous() for i in range(3))
+        rope = m.rope_cache[:t].to(x.dtype)
+        q, k = cmul(q, rope), cmul(k, rope)
+        phase, routing = m._phase_and_alpha(x)
+        phase, routing = phase.permute(3, 0, 2, 1), routing.permute(3, 0, 2, 1)
+        x_flat = torch.cat([x[..., 0], x[..., 1]], -1)
+        sp = F.softplus(m.dt_proj(x_flat) + m.dt_bias + m.state_dt_offset.view(M, 1, 1, 1))
+        base = torch.exp(-sp.permute(0, 1, 3, 2).contiguous())
+        p = torch.sigmoid(m.protect_gate(torch.sqrt(x[..., 0].square() + x[..., 1].square() + 1e-8))).transpose(1, 2)
+        gamma = base * (1 - p) + p
+        v = v * (1 - p)[..., None, None]
+        rot = (routing * torch.cos(phase), routing * torch.sin(phase))
+        y, s = pam_scan_interleaved(q, k, v, gamma, d, m.chunk_size, rot=rot)
+        y = y.transpose(1, 2).contiguous().view(b, t, H * d, 2)
+        return clin(m.o_proj, y), s
+
+
+def bench_pam_layer(steps, warmup):
+    """PAM layer forward + backward at the config-3 shape (E3 M=3, B=8, T=2048,
+    H=12, d=64, dim=768, bf16 parameters and activations): the fused path
+    against the reference's unfused elementwise steps around the same scan,
+    and the prologue kernels alone (HBM-bound: algorithmic bytes are the six
+    projection planes read and the six scan operand planes written, plus the
+    per-token scalars)."""
+    import torch
+    from qllm2_amd import pam_prologue as PP
+    B, T, H, d, M, dim = 8, 2048, 12, 64, 3, 768
+    lay = _BenchPamLayer(dim, H, d, M, T, torch.bfloat16)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(B, T, dim, 2, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
+    dy = torch.randn(B, T, dim, 2, device="cuda", generator=g).to(torch.bfloat16)
+    params = [p for p in lay.mod.parameters()]
+    res = {"config": "E3 M=3, B=8, T=2048, H=12, d=64, dim=768, bf16, fwd+bwd"}
+    for name, fn in (("fused", lay.fused), ("unfused_reference_steps", lay.unfused)):
+        def step():
+            out, _ = fn(x)
+            torch.autograd.grad(out, [x] + params, dy)
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name + "_ms"] = e0.elapsed_time(e1) / steps
+    res["speedup"] = res["unfused_reference_steps_ms"] / res["fused_ms"]
+    # the prologue kernels alone, fed the layer's own tensors
+    from qllm2_amd import pam_layer as PL
+    m = lay.mod
+    with torch.no_grad():
+        cols = PP.proj_columns(H)
+        w_in, b_in = PL._in_weight(m, H, d, cols)
+        proj = torch.nn.functional.linear(x.detach().view(B, T, 2 * dim), w_in, b_in)
+        mag = torch.sqrt(x.detach().square().sum(-1) + 1e-8)
+        prot = m.protect_gate(mag)
+        phase = m.phase_proj(mag).view(B, T, H, M)
+    args = (proj, prot, phase, None, m.dt_bias.detach().float(), m.state_dt_offset.detach().float(), m.rope_cache,
+            H, M, 0, False, 0.0)
+    outs = PP.prologue_fwd_op(*args)
+    grads = [torch.randn_like(o) if o.numel() else o for o in outs]
+    plane = B * T * H * d * 2                  # bytes of one bf16 plane
+    tok = B * T * H * 4                        # one fp32 value per (token, head)
+    tok2 = B * T * H * 2                       # one bf16 value per (token, head)
+    # forward: 6 projection planes in, 6 operand planes out; dt, protect, M phases in (bf16); gamma, rot out (fp32)
+    fwd_bytes = 12 * plane + (2 + M) * tok2 + 3 * M * tok
+    # backward: 6 gradient planes and the 2 v planes in, 6 projection-gradient planes out; the logits in again;
+    # dgamma, drot in; dpre, dphase, dprotect out (fp32), ddt out (bf16)
+    bwd_bytes = 14 * plane + (2 + M) * tok2 + 3 * M * tok + (2 * M + 1) * tok + tok2
+    for name, fn, nbytes in (("prologue_fwd", lambda: PP.prologue_fwd_op(*args), fwd_bytes),
+                             ("prologue_bwd", lambda: PP.prologue_bwd_op(*args, grads), bwd_bytes)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(20):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 20
+        res[name] = {"ms": ms, "bytes": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9,
+                     "hbm_frac": nbytes / (ms * 1e-3) / HBM_PEAK}
+    return res
+
+
 def cpu_baseline_scan():
     """The reference's chunk loop restated on the CPU (oracle.pam.chunked_head),
     fp32, on a bounded sample: 1 of the 8 batch rows (H=12, T=2048)."""
@@ -334,6 +488,7 @@ def main():
               "e3": lambda: bench_e3_fwd_bwd(args.steps, args.warmup),
               "ce": lambda: bench_ce(args.steps, args.warmup),
               "cplx": lambda: bench_complex_ops(args.steps, args.warmup),
+              "layer": lambda: bench_pam_layer(args.steps, args.warmup),
               "copy": copy_calibration}[args.only]
         print(json.dumps({"only": args.only, "result": fn()}), flush=True)
         return
@@ -369,7 +524,8 @@ def main():
                          "decode_e3_rope_slots": bench_decode_e3_rope(max(50, args.decode_steps // 5)),
                          "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 2),
                          "ce_fwd_bwd_config5": bench_ce(max(3, args.steps // 4), 2),
-                         "complex_elementwise": bench_complex_ops(max(3, args.steps // 2), 2)}
+                         "complex_elementwise": bench_complex_ops(max(3, args.steps // 2), 2),
+                         "pam_layer_config3": bench_pam_layer(max(3, args.steps // 2), 2)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_scan()
     print(json.dumps(out), flush=True)

@@ -42,6 +42,8 @@
  *                       and the rotations of _phase_and_alpha (:230-257,
  *                       consumed at :741-746)
  *   qpam_prologue_bwd   their autograd backward
+ *   qpam_cabs_fwd/_bwd  cabs (v11/complex_ops.py:86-87) feeding the gate and
+ *                       phase projections (v11/model.py:228, 646)
  */
 #ifndef QPAM_H
 #define QPAM_H
@@ -197,12 +199,13 @@ int qpam_decay_matrix(int32_t n, int32_t t, const float *gamma, int64_t ldg, flo
  * with complex products per element, nrm(z) = z / sqrt(re^2 + im^2 + 1e-8)
  * when qk_norm (else the identity), softplus(x) = x for x > 20 else
  * log(1 + e^x).  q, k, v: planar views [B,T,H,d] (strides sx_b, sx_t, sx_h
- * shared by the six planes, d contiguous; a fused QKV projection's planes
- * [B,T,3,H,d] give them without copies), in_dtype.  q', k', v': planar
- * [B,H,T,d] contiguous in out_dtype -- the scan's q, k, v.  gamma, rot: fp32
- * [M,B,H,T] contiguous -- the scan's gamma and rot.  d == 64, 1 <= M <= 4.
- * Rope rows past rope_len - 1 are clamped to the last row (size the table to
- * cover rope_offset + T).
+ * shared by the six planes, d contiguous; the columns of one projection GEMM
+ * [B*T, (re|im) x (q|k|v) x H x d] give them without copies), in_dtype; the
+ * logits dt, protect, phase and routing are in in_dtype too (any strides).
+ * q', k', v': planar [B,H,T,d] contiguous in out_dtype -- the scan's q, k, v.
+ * gamma, rot: fp32 [M,B,H,T] contiguous -- the scan's gamma and rot.
+ * d == 64, 1 <= M <= 4.  Rope rows past rope_len - 1 are clamped to the last
+ * row (size the table to cover rope_offset + T).
  */
 typedef struct {
     int32_t B, T, H, d, M;
@@ -213,14 +216,14 @@ typedef struct {
     const float *rope;                  /* [rope_len][d][2], optional (NULL = none) */
     const void *q_re, *q_im, *k_re, *k_im, *v_re, *v_im;
     int64_t sx_b, sx_t, sx_h;
-    const float *dt;                    /* [B,T,H] pre-bias decay logits */
+    const void *dt;                     /* [B,T,H] pre-bias decay logits */
     int64_t sd_b, sd_t, sd_h;
-    const float *dt_bias;               /* [H] */
-    const float *state_offset;          /* [M], optional (NULL = 0) */
-    const float *protect;               /* [B,T,H] protect-gate logits, optional */
+    const float *dt_bias;               /* [H] fp32 */
+    const float *state_offset;          /* [M] fp32, optional (NULL = 0) */
+    const void *protect;                /* [B,T,H] protect-gate logits, optional */
     int64_t sp_b, sp_t, sp_h;
-    const float *phase;                 /* [B,T,H,M], optional (NULL = no rot) */
-    const float *routing;               /* [B,T,H,M], optional (NULL = 1) */
+    const void *phase;                  /* [B,T,H,M], optional (NULL = no rot) */
+    const void *routing;                /* [B,T,H,M], optional (NULL = 1) */
     int64_t sr_b, sr_t, sr_h, sr_m;     /* shared by phase and routing */
     void *oq_re, *oq_im, *ok_re, *ok_im, *ov_re, *ov_im;
     float *gamma;
@@ -233,10 +236,11 @@ int qpam_prologue_fwd(const qpam_prologue_args *a, void *stream);
  * outputs are not read).  In: gradients of q', k', v' ([B,H,T,d] contiguous,
  * out_dtype), of gamma and (when phase) rot ([M,B,H,T] fp32).  Out: the
  * gradients of the projections q, k, v (planar views [B,T,H,d] with strides
- * sg_b, sg_t, sg_h, in_dtype); dpre [M,B,H,T] = dL/d(dt + dt_bias +
- * state_offset_m) (dt's gradient is its sum over m, dt_bias's and
- * state_offset's the sums over the other axes); dprotect [B,H,T] (when
- * protect); dphase and, optionally, drouting [M,B,H,T] (when phase). */
+ * sg_b, sg_t, sg_h, in_dtype); dpre [M,B,H,T] fp32 = dL/d(dt + dt_bias +
+ * state_offset_m) (dt_bias's and state_offset's gradients are its sums over
+ * the other axes); optionally ddt [B,T,H] (strides sdd_*, in_dtype) = the sum
+ * of dpre over m, dt's gradient; dprotect [B,H,T] fp32 (when protect); dphase
+ * and, optionally, drouting [M,B,H,T] fp32 (when phase). */
 typedef struct {
     const qpam_prologue_args *fwd;
     const void *gq_re, *gq_im, *gk_re, *gk_im, *gv_re, *gv_im;
@@ -245,11 +249,21 @@ typedef struct {
     void *dq_re, *dq_im, *dk_re, *dk_im, *dv_re, *dv_im;
     int64_t sg_b, sg_t, sg_h;
     float *dpre;
+    void *ddt;                          /* optional */
+    int64_t sdd_b, sdd_t, sdd_h;
     float *dprotect;
     float *dphase, *drouting;
 } qpam_prologue_bwd_args;
 
 int qpam_prologue_bwd(const qpam_prologue_bwd_args *a, void *stream);
+
+/* cabs (v11/complex_ops.py:86-87), the magnitudes the layer's gates read
+ * (v11/model.py:228, 646): mag[i] = sqrt(z[i][0]^2 + z[i][1]^2 + 1e-8) over n
+ * interleaved complex elements (n a multiple of 4, buffers 16-byte aligned
+ * for fp32, 8-byte for bf16; mag in the dtype of z); the backward writes
+ * gz[i] = gmag[i] z[i] / mag[i]. */
+int qpam_cabs_fwd(int32_t dtype, int64_t n, const void *z, void *mag, void *stream);
+int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void *mag, const void *gmag, void *gz, void *stream);
 
 /* ------------------------------------------------ complex elementwise -----
  * Split-real complex tensors [rows, dim, 2] (interleaved re/im, contiguous),

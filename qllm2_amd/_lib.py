@@ -133,7 +133,8 @@ class PrologueBwdArgs(ctypes.Structure):
         ("ggamma", c_ptr), ("grot_re", c_ptr), ("grot_im", c_ptr),
         ("dq_re", c_ptr), ("dq_im", c_ptr), ("dk_re", c_ptr), ("dk_im", c_ptr), ("dv_re", c_ptr), ("dv_im", c_ptr),
         ("sg_b", c_i64), ("sg_t", c_i64), ("sg_h", c_i64),
-        ("dpre", c_ptr), ("dprotect", c_ptr), ("dphase", c_ptr), ("drouting", c_ptr),
+        ("dpre", c_ptr), ("ddt", c_ptr), ("sdd_b", c_i64), ("sdd_t", c_i64), ("sdd_h", c_i64),
+        ("dprotect", c_ptr), ("dphase", c_ptr), ("drouting", c_ptr),
     ]
 
 
@@ -158,6 +159,8 @@ SIGNATURES = {
     "qpam_cplx_bwd": (ctypes.c_int, [ctypes.POINTER(CplxArgs), c_ptr]),
     "qpam_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(PrologueArgs), c_ptr]),
     "qpam_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(PrologueBwdArgs), c_ptr]),
+    "qpam_cabs_fwd": (ctypes.c_int, [c_i32, c_i64, c_ptr, c_ptr, c_ptr]),
+    "qpam_cabs_bwd": (ctypes.c_int, [c_i32, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
 }
 
 _LIB = None

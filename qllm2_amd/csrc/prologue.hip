@@ -29,6 +29,12 @@ struct Bf16 {};
 
 template <typename T> struct Io;
 template <> struct Io<float> {
+    __device__ __forceinline__ static float load1(const void *base, int64_t off) {
+        return static_cast<const float *>(base)[off];
+    }
+    __device__ __forceinline__ static void store1(void *base, int64_t off, float v) {
+        static_cast<float *>(base)[off] = v;
+    }
     __device__ __forceinline__ static void load4(const void *base, int64_t off, float (&o)[4]) {
         const floatx4 v = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(base) + off);
         o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
@@ -38,6 +44,12 @@ template <> struct Io<float> {
     }
 };
 template <> struct Io<Bf16> {
+    __device__ __forceinline__ static float load1(const void *base, int64_t off) {
+        return bf16_to_f32(static_cast<const unsigned short *>(base)[off]);
+    }
+    __device__ __forceinline__ static void store1(void *base, int64_t off, float v) {
+        static_cast<unsigned short *>(base)[off] = f32_to_bf16(v);
+    }
     __device__ __forceinline__ static void load4(const void *base, int64_t off, float (&o)[4]) {
         const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const unsigned short *>(base) + off);
         o[0] = __uint_as_float(v.x << 16), o[1] = __uint_as_float(v.x & 0xffff0000u);
@@ -53,8 +65,10 @@ __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1p
 __device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
 
 // decay logit of state m: dt + dt_bias + state_offset
+template <typename TI>
 __device__ __forceinline__ float pre_sum(const qpam_prologue_args &a, int b, int t, int h, int m) {
-    return a.dt[b * a.sd_b + (int64_t)t * a.sd_t + h * a.sd_h] + a.dt_bias[h] + (a.state_offset ? a.state_offset[m] : 0.f);
+    return Io<TI>::load1(a.dt, b * a.sd_b + (int64_t)t * a.sd_t + h * a.sd_h) + a.dt_bias[h] +
+           (a.state_offset ? a.state_offset[m] : 0.f);
 }
 
 // exp(-softplus(pre)) lifted onto [floor, 1) when floor > 0
@@ -63,8 +77,18 @@ __device__ __forceinline__ float lifted_decay(const qpam_prologue_args &a, float
     return a.gamma_floor > 0.f ? a.gamma_floor + (1.f - a.gamma_floor) * base : base;
 }
 
+template <typename TI>
 __device__ __forceinline__ float protect_prob(const qpam_prologue_args &a, int b, int t, int h) {
-    return a.protect ? sigmoid(a.protect[b * a.sp_b + (int64_t)t * a.sp_t + h * a.sp_h]) : 0.f;
+    return a.protect ? sigmoid(Io<TI>::load1(a.protect, b * a.sp_b + (int64_t)t * a.sp_t + h * a.sp_h)) : 0.f;
+}
+
+// routing weight and e^{i phase} of state m at (b, t, h)
+template <typename TI>
+__device__ __forceinline__ void rotation(const qpam_prologue_args &a, int b, int t, int h, int m, float &r, float &cs,
+                                         float &sn) {
+    const int64_t po = b * a.sr_b + (int64_t)t * a.sr_t + h * a.sr_h + m * a.sr_m;
+    r = a.routing ? Io<TI>::load1(a.routing, po) : 1.f;
+    sincosf(Io<TI>::load1(a.phase, po), &sn, &cs);
 }
 
 // this lane's 4 rope factors (c, s) for the token at position rope_offset + t
@@ -88,17 +112,15 @@ __global__ void __launch_bounds__(PTHREADS) prologue_fwd_kernel(qpam_prologue_ar
     {   // scalars: thread = (state m, token)
         const int tt = tid & (PT - 1), m = tid / PT, t = t0 + tt;
         if (t < a.T) {
-            const float p = protect_prob(a, b, t, h);
+            const float p = protect_prob<TI>(a, b, t, h);
             if (m == 0) s_keep[tt] = 1.f - p;
             if (m < a.M) {
-                const float base = lifted_decay(a, pre_sum(a, b, t, h, m));
+                const float base = lifted_decay(a, pre_sum<TI>(a, b, t, h, m));
                 const int64_t o = (((int64_t)m * a.B + b) * a.H + h) * a.T + t;
                 a.gamma[o] = base * (1.f - p) + p;
                 if (a.phase) {
-                    const int64_t po = b * a.sr_b + (int64_t)t * a.sr_t + h * a.sr_h + m * a.sr_m;
-                    const float r = a.routing ? a.routing[po] : 1.f;
-                    float sn, cs;
-                    sincosf(a.phase[po], &sn, &cs);
+                    float r, cs, sn;
+                    rotation<TI>(a, b, t, h, m, r, cs, sn);
                     a.rot_re[o] = r * cs;
                     a.rot_im[o] = r * sn;
                 }
@@ -171,7 +193,7 @@ __global__ void __launch_bounds__(PTHREADS) prologue_bwd_kernel(qpam_prologue_bw
     const int bh = blockIdx.x / nt, tile = blockIdx.x - bh * nt;
     const int b = bh / a.H, h = bh - b * a.H;
     const int t0 = tile * PT, tid = threadIdx.x;
-    if (tid < PT) s_keep[tid] = t0 + tid < a.T ? 1.f - protect_prob(a, b, t0 + tid, h) : 1.f;
+    if (tid < PT) s_keep[tid] = t0 + tid < a.T ? 1.f - protect_prob<TI>(a, b, t0 + tid, h) : 1.f;
     __syncthreads();
 
     const int w = tid >> 6, lane = tid & 63, c4 = (lane & 15) * 4;
@@ -218,36 +240,75 @@ __global__ void __launch_bounds__(PTHREADS) prologue_bwd_kernel(qpam_prologue_bw
     }
     __syncthreads();
 
-    {   // scalars: thread = (state m, token)
+    // scalars: thread = (state m, token); the sums over the states (dt's
+    // gradient, the protect gate's) are taken in a fixed order afterwards
+    __shared__ float s_dpre[4][PT], s_dpm[4][PT];
+    {
         const int tt = tid & (PT - 1), m = tid / PT, t = t0 + tt;
+        float dpre = 0.f, dpm = 0.f;
         if (t < a.T && m < a.M) {
             const float p = 1.f - s_keep[tt];
             const int64_t o = (((int64_t)m * a.B + b) * a.H + h) * a.T + t;
             // d gamma / d pre = (1 - p) (1 - floor) (-exp(-softplus(pre))) softplus'(pre)
-            const float pre = pre_sum(a, b, t, h, m);
+            const float pre = pre_sum<TI>(a, b, t, h, m);
             const float raw = expf(-softplus(pre));
             const float dsp = pre > 20.f ? 1.f : sigmoid(pre);
             const float lift = a.gamma_floor > 0.f ? 1.f - a.gamma_floor : 1.f;
-            g.dpre[o] = -g.ggamma[o] * (1.f - p) * lift * raw * dsp;
+            const float gg = g.ggamma[o];
+            dpre = -gg * (1.f - p) * lift * raw * dsp;
+            g.dpre[o] = dpre;
+            dpm = gg * (1.f - lifted_decay(a, pre));  // d gamma_m / d p = 1 - base_m
             if (a.phase) {
-                const int64_t po = b * a.sr_b + (int64_t)t * a.sr_t + h * a.sr_h + m * a.sr_m;
-                const float r = a.routing ? a.routing[po] : 1.f;
-                float sn, cs;
-                sincosf(a.phase[po], &sn, &cs);
+                float r, cs, sn;
+                rotation<TI>(a, b, t, h, m, r, cs, sn);
                 const float gr = g.grot_re[o], gi = g.grot_im[o];
                 g.dphase[o] = r * (gi * cs - gr * sn);
                 if (g.drouting) g.drouting[o] = gr * cs + gi * sn;
             }
-            if (m == 0 && a.protect) {
-                // d gamma_m / d p = 1 - base_m;  d v' / d p = -v
-                float dp = -s_gvv[tt];
-                for (int mm = 0; mm < a.M; ++mm)
-                    dp += g.ggamma[(((int64_t)mm * a.B + b) * a.H + h) * a.T + t] *
-                          (1.f - lifted_decay(a, pre_sum(a, b, t, h, mm)));
-                g.dprotect[((int64_t)b * a.H + h) * a.T + t] = dp * p * (1.f - p);
-            }
+        }
+        s_dpre[m][tt] = dpre;
+        s_dpm[m][tt] = dpm;
+    }
+    __syncthreads();
+    const int t = t0 + tid;
+    if (tid < PT && t < a.T) {
+        float ddt = 0.f, dp = -s_gvv[tid];       // d v' / d p = -v
+        for (int m = 0; m < a.M; ++m) ddt += s_dpre[m][tid], dp += s_dpm[m][tid];
+        if (g.ddt) Io<TI>::store1(g.ddt, b * g.sdd_b + (int64_t)t * g.sdd_t + h * g.sdd_h, ddt);
+        if (a.protect) {
+            const float p = 1.f - s_keep[tid];
+            g.dprotect[((int64_t)b * a.H + h) * a.T + t] = dp * p * (1.f - p);
         }
     }
+}
+
+// |z| = sqrt(re^2 + im^2 + 1e-8) of interleaved complex elements, four per
+// thread, and its backward dz = g z / |z|
+template <typename T>
+__global__ void __launch_bounds__(256) cabs_fwd_kernel(int64_t n4, const void *z, void *mag) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    float a[4], b[4], m[4];
+    Io<T>::load4(z, 8 * i, a), Io<T>::load4(z, 8 * i + 4, b);
+    m[0] = sqrtf(a[0] * a[0] + a[1] * a[1] + 1e-8f), m[1] = sqrtf(a[2] * a[2] + a[3] * a[3] + 1e-8f);
+    m[2] = sqrtf(b[0] * b[0] + b[1] * b[1] + 1e-8f), m[3] = sqrtf(b[2] * b[2] + b[3] * b[3] + 1e-8f);
+    Io<T>::store4(mag, 4 * i, m);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(256) cabs_bwd_kernel(int64_t n4, const void *z, const void *mag, const void *gmag,
+                                                       void *gz) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    float a[4], b[4], m[4], g[4];
+    Io<T>::load4(z, 8 * i, a), Io<T>::load4(z, 8 * i + 4, b);
+    Io<T>::load4(mag, 4 * i, m), Io<T>::load4(gmag, 4 * i, g);
+    float s[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = g[j] / m[j];
+    a[0] *= s[0], a[1] *= s[0], a[2] *= s[1], a[3] *= s[1];
+    b[0] *= s[2], b[1] *= s[2], b[2] *= s[3], b[3] *= s[3];
+    Io<T>::store4(gz, 8 * i, a), Io<T>::store4(gz, 8 * i + 4, b);
 }
 
 bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
@@ -334,4 +395,35 @@ extern "C" int qpam_prologue_bwd(const qpam_prologue_bwd_args *g, void *stream) 
     else if (fo) hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, float>), grid, block, 0, s, *g, a);
     else hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, Bf16>), grid, block, 0, s, *g, a);
     return launch_status("prologue_bwd_kernel");
+}
+
+extern "C" int qpam_cabs_fwd(int32_t dtype, int64_t n, const void *z, void *mag, void *stream) {
+    QPAM_REQUIRE(dtype == QPAM_F32 || dtype == QPAM_BF16, "qpam_cabs_fwd: dtype must be QPAM_F32 or QPAM_BF16");
+    QPAM_REQUIRE(n >= 0 && n % 4 == 0, "qpam_cabs_fwd: element count %lld must be a multiple of 4", (long long)n);
+    const int va = dtype == QPAM_F32 ? 16 : 8;
+    QPAM_REQUIRE(n == 0 || (z && mag && aligned(z, va) && aligned(mag, va)), "qpam_cabs_fwd: %d-byte aligned z, mag required", va);
+    if (n == 0) return QPAM_OK;
+    const int64_t n4 = n / 4;
+    const dim3 grid((unsigned)((n4 + 255) / 256)), block(256);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == QPAM_F32) hipLaunchKernelGGL(cabs_fwd_kernel<float>, grid, block, 0, s, n4, z, mag);
+    else hipLaunchKernelGGL(cabs_fwd_kernel<Bf16>, grid, block, 0, s, n4, z, mag);
+    return launch_status("cabs_fwd_kernel");
+}
+
+extern "C" int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void *mag, const void *gmag, void *gz,
+                             void *stream) {
+    QPAM_REQUIRE(dtype == QPAM_F32 || dtype == QPAM_BF16, "qpam_cabs_bwd: dtype must be QPAM_F32 or QPAM_BF16");
+    QPAM_REQUIRE(n >= 0 && n % 4 == 0, "qpam_cabs_bwd: element count %lld must be a multiple of 4", (long long)n);
+    const int va = dtype == QPAM_F32 ? 16 : 8;
+    QPAM_REQUIRE(n == 0 || (z && mag && gmag && gz && aligned(z, va) && aligned(mag, va) && aligned(gmag, va) &&
+                            aligned(gz, va)),
+                 "qpam_cabs_bwd: %d-byte aligned buffers required", va);
+    if (n == 0) return QPAM_OK;
+    const int64_t n4 = n / 4;
+    const dim3 grid((unsigned)((n4 + 255) / 256)), block(256);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == QPAM_F32) hipLaunchKernelGGL(cabs_bwd_kernel<float>, grid, block, 0, s, n4, z, mag, gmag, gz);
+    else hipLaunchKernelGGL(cabs_bwd_kernel<Bf16>, grid, block, 0, s, n4, z, mag, gmag, gz);
+    return launch_status("cabs_bwd_kernel");
 }

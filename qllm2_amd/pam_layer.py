@@ -34,7 +34,7 @@ from . import decode as _decode
 from . import fused_ce as _fused_ce
 from . import flash_pam as _flash_pam
 from . import triton_kernels as _tk
-from .pam_prologue import pam_prologue
+from .pam_prologue import cabs, pam_prologue, proj_columns
 from .pam_scan import chunk_for, pam_scan_interleaved, pam_scan_planar
 
 
@@ -131,15 +131,44 @@ def recurrent(self, x, queries, keys, values, state, head_dim):
     return out, (new_state if k_states > 1 else new_state[0])
 
 
-def _complex_linear_planar(mod, xr, xi):
-    """ComplexLinear.forward (v11/complex_ops.py:165-172) on planar input,
-    returning the planar (re, im) pair instead of the stacked [..., 2]."""
+def _in_weight(self, h, d, cols):
+    """Weight [cols, 2 dim] and bias [cols] (None when the QKV projection
+    has none) of the one GEMM that maps the interleaved input x.view(N, 2 dim)
+    (re, im per feature) to `proj`: the real planes of q, k, v
+    (ComplexLinear: re = Wr xr - Wi xi, v11/complex_ops.py:165-172), their
+    imaginary planes (im = Wi xr + Wr xi), dt_proj's logits without its bias
+    (v11/model.py:636, its [xr | xi] columns reordered to the interleaved
+    input), zero padding."""
+    if self.fused_qkv:
+        mods = [self.qkv_proj]
+    else:
+        mods = [self.q_proj, self.k_proj, self.v_proj]
+    wr = torch.cat([m.weight_real for m in mods], 0) if len(mods) > 1 else mods[0].weight_real
+    wi = torch.cat([m.weight_imag for m in mods], 0) if len(mods) > 1 else mods[0].weight_imag
+    rows, dim = wr.shape
+    w_dt = self.dt_proj.weight.view(h, 2, dim).transpose(1, 2).reshape(h, 2 * dim)
+    pad = cols - 2 * rows - h
+    parts = [torch.stack([wr, -wi], -1).view(rows, 2 * dim), torch.stack([wi, wr], -1).view(rows, 2 * dim), w_dt]
+    if pad:
+        parts.append(w_dt.new_zeros(pad, 2 * dim))
+    w = torch.cat(parts, 0)
+    if all(getattr(m, "bias_real", None) is None for m in mods):
+        return w, None      # dt_proj's bias joins dt_bias in the prologue instead
+    br = torch.cat([m.bias_real if m.bias_real is not None else wr.new_zeros(m.weight_real.shape[0]) for m in mods])
+    bi = torch.cat([m.bias_imag if m.bias_imag is not None else wr.new_zeros(m.weight_real.shape[0]) for m in mods])
+    return w, torch.cat([br, bi, wr.new_zeros(h + pad)])
+
+
+def _out_weight(mod):
+    """Weight [2 dim, 2 inner] (and bias) of the o_proj GEMM from the
+    per-token [y_re | y_im] planes to the interleaved output (re_o, im_o)."""
     wr, wi = mod.weight_real, mod.weight_imag
-    re = F.linear(xr, wr) - F.linear(xi, wi)
-    im = F.linear(xr, wi) + F.linear(xi, wr)
+    dim = wr.shape[0]
+    w = torch.stack([torch.cat([wr, -wi], 1), torch.cat([wi, wr], 1)], 1).view(2 * dim, -1)
+    bias = None
     if getattr(mod, "bias_real", None) is not None:
-        re, im = re + mod.bias_real, im + mod.bias_imag
-    return re, im
+        bias = torch.stack([mod.bias_real, mod.bias_imag], 1).view(2 * dim)
+    return w, bias
 
 
 def _fused_prefill(self, x, state):
@@ -154,25 +183,23 @@ def forward(self, x, state=None, step_offset: int = 0):
     production modes; everything else runs the original forward.
 
     x [B,T,dim,2] -> (out [B,T,dim,2], state [K,B,H,d,d,2] or [B,H,d,d,2]).
-    The QKV projection runs as planar GEMMs (no interleave, no transposes),
-    qpam_prologue_fwd turns its planes, the decay / gate / phase logits and the
-    RoPE table into the scan's operands in one pass, the scan writes Y as
-    [B,T,H,d] planes (the head-merged layout of :834-835) and o_proj reads them
-    as they are."""
+    Three GEMMs and two HIP launches instead of the reference's chain of
+    elementwise passes: (1) one GEMM from x viewed as [N, 2 dim] (no copy) to
+    the q, k, v planes and the decay logits; (2) one GEMM from |x| to the
+    protect-gate and phase logits; qpam_prologue_fwd turns those and the RoPE
+    table into the scan's operands; the scan writes Y as [B,T,2,H,d]; (3) one
+    GEMM from Y viewed as [N, 2 H d] straight to the interleaved output."""
     if not _fused_prefill(self, x, state):
         return _ORIGINALS["forward"](self, x, state, step_offset)
-    b, t = x.shape[0], x.shape[1]
+    b, t, dim = x.shape[0], x.shape[1], x.shape[2]
     h, d, m = self.num_heads, self.head_dim, self.n_states
-    xr, xi = x[..., 0], x[..., 1]
-    if self.fused_qkv:
-        qkv_re, qkv_im = _complex_linear_planar(self.qkv_proj, xr, xi)
-        qkv_re, qkv_im = qkv_re.view(b, t, 3, h, d), qkv_im.view(b, t, 3, h, d)
-    else:
-        parts = [_complex_linear_planar(p, xr, xi) for p in (self.q_proj, self.k_proj, self.v_proj)]
-        qkv_re = torch.stack([p[0].view(b, t, h, d) for p in parts], 2)
-        qkv_im = torch.stack([p[1].view(b, t, h, d) for p in parts], 2)
-    if qkv_re.dtype not in (torch.float32, torch.bfloat16):
-        qkv_re, qkv_im = qkv_re.float(), qkv_im.float()
+    n = b * t
+    xc = x if x.is_contiguous() else x.contiguous()
+    cols = proj_columns(h)
+    w_in, b_in = _in_weight(self, h, d, cols)
+    proj = F.linear(xc.view(b, t, 2 * dim), w_in, b_in)                 # [B,T,cols]
+    if proj.dtype not in (torch.float32, torch.bfloat16):
+        proj = proj.float()
     rope = None
     if self.use_rope:
         end = step_offset + t
@@ -180,34 +207,52 @@ def forward(self, x, state=None, step_offset: int = 0):
             self.register_buffer("rope_cache", _decode.build_rope_cache(end * 2, d, device=x.device),
                                  persistent=False)
         rope = self.rope_cache.float()
-    x_flat = torch.cat([xr, xi], dim=-1)
-    dt = self.dt_proj(x_flat)                                            # [B,T,H]
-    protect = None
+    mag = None
+    if (self.use_gsp and not self.gate_content_aware) or (m > 1 and not (self.routing_content_aware
+                                                                         or self.state_compete)):
+        mag = cabs(xc)                                                   # [B,T,dim]
+    protect = phase = routing = offsets = None
+    g_w, g_b, g_parts = [], [], []
     if self.use_gsp:
-        gate_in = x_flat if self.gate_content_aware else torch.sqrt(xr.square() + xi.square() + 1e-8)
-        protect = self.protect_gate(gate_in)                             # [B,T,H]
-        if self.gate_surprisal_lambda > 0 and self.training:
-            self._gate_prob_bt = torch.sigmoid(protect).mean(dim=2)      # [B,T]
-    phase = routing = offsets = None
+        if self.gate_content_aware:
+            protect = self.protect_gate(torch.cat([xc[..., 0], xc[..., 1]], -1))
+        else:
+            g_w.append(self.protect_gate.weight), g_b.append(self.protect_gate.bias), g_parts.append("protect")
     if m > 1:
-        phase, routing_w = self._phase_and_alpha(x)                      # [B,T,H,K]
-        self._route_aux = self._route_balance_loss(routing_w)
-        routing = routing_w if self.state_compete else None
         offsets = self.state_dt_offset
+        if self.routing_content_aware or self.state_compete:
+            phase, routing_w = self._phase_and_alpha(x)                  # [B,T,H,K]
+            self._route_aux = self._route_balance_loss(routing_w)
+            routing = routing_w if self.state_compete else None
+        else:
+            g_w.append(self.phase_proj.weight), g_b.append(self.phase_proj.bias), g_parts.append("phase")
+            self._route_aux = self._route_balance_loss(x.new_ones(1, 1, 1, 1).expand(b, t, h, m))
+    if g_parts:
+        gl = F.linear(mag, torch.cat(g_w, 0), torch.cat(g_b, 0))          # [B,T,H (+H K)]
+        col = 0
+        for part in g_parts:
+            if part == "protect":
+                protect, col = gl[..., col:col + h], col + h
+            else:
+                phase, col = gl[..., col:col + h * m].view(b, t, h, m), col + h * m
+    if protect is not None and self.gate_surprisal_lambda > 0 and self.training:
+        self._gate_prob_bt = torch.sigmoid(protect.float()).mean(dim=2)  # [B,T]
+    dt_bias = self.dt_bias if self.dt_proj.bias is None else self.dt_bias + self.dt_proj.bias
     (qr, qi), (kr, ki), (vr, vi), gamma, rot = pam_prologue(
-        qkv_re, qkv_im, dt, self.dt_bias, n_states=m, state_offset=offsets, protect=protect, phase=phase,
+        proj, dt_bias, n_heads=h, n_states=m, state_offset=offsets, protect=protect, phase=phase,
         routing=routing, rope=rope, rope_offset=step_offset, qk_norm=self.qk_norm,
         gamma_floor=self.gamma_floor or 0.0)
-    y_re, y_im, s_re, s_im = pam_scan_planar(qr, qi, kr, ki, vr, vi, gamma, q_scale=d ** -0.5,
-                                             chunk=chunk_for(self.chunk_size, t), rot=rot, y_layout="bthd")
-    if x.dtype != torch.float32:
-        y_re, y_im = y_re.to(x.dtype), y_im.to(x.dtype)
-    out_re, out_im = _complex_linear_planar(self.o_proj, y_re.view(b, t, h * d), y_im.view(b, t, h * d))
+    y, _, s_re, s_im = pam_scan_planar(qr, qi, kr, ki, vr, vi, gamma, q_scale=d ** -0.5,
+                                       chunk=chunk_for(self.chunk_size, t), rot=rot, y_layout="bt2hd")
+    w_out, b_out = _out_weight(self.o_proj)
+    y = y.view(b, t, 2 * h * d)
+    if w_out.dtype != torch.float32 and not torch.is_autocast_enabled():
+        y = y.to(w_out.dtype)
+    out = F.linear(y, w_out, b_out).view(b, t, dim, 2)
     if self.training:
         # one keep-mask per complex value (as_complex_dropout_mask, v11/complex_ops.py:59-66)
-        mask = self.dropout(torch.ones(out_re.shape, device=out_re.device, dtype=out_re.dtype))
-        out_re, out_im = out_re * mask, out_im * mask
-    out = torch.stack([out_re, out_im], dim=-1)
+        mask = self.dropout(torch.ones(out.shape[:-1], device=out.device, dtype=out.dtype))
+        out = out * mask.unsqueeze(-1)
     new_state = torch.stack([s_re, s_im], dim=-1).to(x.dtype)
     return out, (new_state if m > 1 else new_state[0])
 

@@ -132,20 +132,27 @@ def _validate(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, 
 @torch.library.custom_op("qpam::scan_fwd", mutates_args=())
 def scan_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Tensor, v_im: Tensor,
                 gamma: Tensor, rot_re: Optional[Tensor], rot_im: Optional[Tensor], s0_re: Optional[Tensor],
-                s0_im: Optional[Tensor], q_scale: float, chunk: int, y_bthd: bool) -> List[Tensor]:
+                s0_im: Optional[Tensor], q_scale: float, chunk: int, y_layout: int) -> List[Tensor]:
     """Returns [y_re, y_im, s_re, s_im, workspace]; the workspace keeps the
-    per-chunk entering states for the backward.  y is [B,H,T,d], or [B,T,H,d]
-    when y_bthd (the head-merged layout the output projection reads)."""
+    per-chunk entering states for the backward.  y_layout 0: y planes
+    [B,H,T,d]; 1: [B,T,H,d] (head-merged); 2: one tensor [B,T,2,H,d] in the
+    y_re slot (re and im planes of a token side by side, the [N, 2 H d] input
+    of one output-projection GEMM) and an empty y_im."""
     _validate(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, chunk)
     M, B, H, T = gamma.shape
     d = q_re.shape[-1]
     dev = q_re.device
     a, keep = _fill_args(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk)
-    y_re = torch.empty((B, T, H, d) if y_bthd else (B, H, T, d), device=dev, dtype=torch.float32)
-    y_im = torch.empty_like(y_re)
+    if y_layout == 2:
+        y_re = torch.empty(B, T, 2, H, d, device=dev, dtype=torch.float32)
+        y_im = y_re.new_empty(0)
+        a.y = _mview(y_re[:, :, 0].transpose(1, 2), y_re[:, :, 1].transpose(1, 2))
+    else:
+        y_re = torch.empty((B, T, H, d) if y_layout == 1 else (B, H, T, d), device=dev, dtype=torch.float32)
+        y_im = torch.empty_like(y_re)
+        a.y = _mview(y_re.transpose(1, 2), y_im.transpose(1, 2)) if y_layout == 1 else _mview(y_re, y_im)
     s_re = torch.empty(M, B, H, d, d, device=dev, dtype=torch.float32)
     s_im = torch.empty_like(s_re)
-    a.y = _mview(y_re.transpose(1, 2), y_im.transpose(1, 2)) if y_bthd else _mview(y_re, y_im)
     a.s_re, a.s_im = s_re.data_ptr(), s_im.data_ptr()
     L = _lib.lib()
     nbytes = L.qpam_scan_workspace_size(a)
@@ -172,13 +179,16 @@ def fwd_workspace_bytes(M, B, H, T, chunk, bf16, d=64):
 
 
 @scan_fwd_op.register_fake
-def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk, y_bthd):
+def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk, y_layout):
     M, B, H, T = gamma.shape
     d = q_re.shape[-1]
-    y = q_re.new_empty((B, T, H, d) if y_bthd else (B, H, T, d), dtype=torch.float32)
     s = q_re.new_empty(M, B, H, d, d, dtype=torch.float32)
     nbytes = fwd_workspace_bytes(M, B, H, T, chunk, q_re.dtype == torch.bfloat16, d)
     ws = q_re.new_empty((nbytes + 3) // 4, dtype=torch.float32)
+    if y_layout == 2:
+        return [q_re.new_empty(B, T, 2, H, d, dtype=torch.float32), q_re.new_empty(0, dtype=torch.float32), s,
+                torch.empty_like(s), ws]
+    y = q_re.new_empty((B, T, H, d) if y_layout == 1 else (B, H, T, d), dtype=torch.float32)
     return [y, torch.empty_like(y), s, torch.empty_like(s), ws]
 
 
@@ -186,7 +196,7 @@ def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q
 def scan_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Tensor, v_im: Tensor,
                 gamma: Tensor, rot_re: Optional[Tensor], rot_im: Optional[Tensor], s0_re: Optional[Tensor],
                 s0_im: Optional[Tensor], q_scale: float, chunk: int, ws: Tensor, dy_re: Tensor, dy_im: Tensor,
-                ds_re: Optional[Tensor], ds_im: Optional[Tensor], y_bthd: bool) -> List[Tensor]:
+                ds_re: Optional[Tensor], ds_im: Optional[Tensor], y_layout: int) -> List[Tensor]:
     """Returns [dq_re, dq_im, dk_re, dk_im, dv_re, dv_im, dgamma, drot_re, drot_im, ds0_re, ds0_im]
     (drot/ds0 are empty tensors when rot/s0 were not given); dy in y's layout."""
     M, B, H, T = gamma.shape
@@ -196,9 +206,13 @@ def scan_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     bw = _lib.ScanBwdArgs()
     bw.fwd = _lib.ctypes.pointer(a)
-    dy_re, dy_im = dy_re.contiguous(), dy_im.contiguous()
-    if y_bthd:
-        dy_re, dy_im = dy_re.transpose(1, 2), dy_im.transpose(1, 2)
+    if y_layout == 2:      # one [B,T,2,H,d] gradient in dy_re
+        dy = dy_re.contiguous()
+        dy_re, dy_im = dy[:, :, 0].transpose(1, 2), dy[:, :, 1].transpose(1, 2)
+    else:
+        dy_re, dy_im = dy_re.contiguous(), dy_im.contiguous()
+        if y_layout == 1:
+            dy_re, dy_im = dy_re.transpose(1, 2), dy_im.transpose(1, 2)
     bw.dy, _, _ = _cview(dy_re, dy_im)
     if ds_re is not None:
         ds_re, ds_im = ds_re.contiguous(), ds_im.contiguous()
@@ -233,7 +247,7 @@ def scan_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
 
 @scan_bwd_op.register_fake
 def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk, ws, dy_re,
-      dy_im, ds_re, ds_im, y_bthd):
+      dy_im, ds_re, ds_im, y_layout):
     M, B, H, T = gamma.shape
     d = q_re.shape[-1]
     outs = [q_re.new_empty(B, H, T, d) for _ in range(6)]
@@ -244,9 +258,9 @@ def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q
 
 
 def _setup_context(ctx, inputs, output):
-    (q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk, y_bthd) = inputs
+    (q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk, y_layout) = inputs
     ctx.save_for_backward(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, output[4])
-    ctx.q_scale, ctx.chunk, ctx.y_bthd = q_scale, chunk, y_bthd
+    ctx.q_scale, ctx.chunk, ctx.y_layout = q_scale, chunk, y_layout
     # outputs without an incoming gradient arrive as None (the workspace output
     # never has one): no zero-filled gradient buffers
     ctx.set_materialize_grads(False)
@@ -255,18 +269,24 @@ def _setup_context(ctx, inputs, output):
 def _backward(ctx, grads):
     (q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, ws) = ctx.saved_tensors
     dy_re, dy_im, ds_re, ds_im = grads[0], grads[1], grads[2], grads[3]
-    yshape = q_re.transpose(1, 2).shape if ctx.y_bthd else q_re.shape
-    if dy_re is None:
-        dy_re = q_re.new_zeros(yshape, dtype=torch.float32)
-    if dy_im is None:
-        dy_im = q_re.new_zeros(yshape, dtype=torch.float32)
+    B, H, T, d = q_re.shape
+    if ctx.y_layout == 2:
+        if dy_re is None:
+            dy_re = q_re.new_zeros((B, T, 2, H, d), dtype=torch.float32)
+        dy_im = dy_re
+    else:
+        yshape = (B, T, H, d) if ctx.y_layout == 1 else (B, H, T, d)
+        if dy_re is None:
+            dy_re = q_re.new_zeros(yshape, dtype=torch.float32)
+        if dy_im is None:
+            dy_im = q_re.new_zeros(yshape, dtype=torch.float32)
     if ds_re is None and ds_im is None:
         ds_re_t = ds_im_t = None
     else:
         ds_re_t = ds_re if ds_re is not None else torch.zeros_like(ds_im)
         ds_im_t = ds_im if ds_im is not None else torch.zeros_like(ds_re)
     g = scan_bwd_op(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, ctx.q_scale,
-                    ctx.chunk, ws, dy_re, dy_im, ds_re_t, ds_im_t, ctx.y_bthd)
+                    ctx.chunk, ws, dy_re, dy_im, ds_re_t, ds_im_t, ctx.y_layout)
     drot = (g[7], g[8]) if rot_re is not None else (None, None)
     ds0 = (g[9], g[10]) if s0_re is not None else (None, None)
     return (g[0], g[1], g[2], g[3], g[4], g[5], g[6], drot[0], drot[1], ds0[0], ds0[1], None, None, None)
@@ -278,13 +298,15 @@ scan_fwd_op.register_autograd(_backward, setup_context=_setup_context)
 def pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, *, q_scale, chunk=64, rot=None, s0=None,
                     y_layout="bhtd"):
     """Differentiable planar scan.  Returns (y_re, y_im, s_re, s_im); y is
-    [B,H,T,d], or [B,T,H,d] with y_layout="bthd" (written in that layout by
-    the kernel, and its gradient read in it: no transposes).
+    [B,H,T,d], or [B,T,H,d] with y_layout="bthd", or with y_layout="bt2hd"
+    one tensor [B,T,2,H,d] returned as y_re (y_im None): the kernel writes y
+    in that layout and reads its gradient in it, no transposes.
 
     Head dims below 64 are zero-padded to 64 (exact: padded key/query columns
     add nothing to q.k*, padded value rows stay zero) and sliced back."""
-    if y_layout not in ("bhtd", "bthd"):
-        raise ValueError("y_layout must be 'bhtd' or 'bthd'")
+    layouts = {"bhtd": 0, "bthd": 1, "bt2hd": 2}
+    if y_layout not in layouts:
+        raise ValueError(f"y_layout must be one of {list(layouts)}")
     rot_re, rot_im = rot if rot is not None else (None, None)
     s0_re, s0_im = s0 if s0 is not None else (None, None)
     d = q_re.shape[-1]
@@ -297,8 +319,12 @@ def pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, *, q_scale, chunk
         if s0_re is not None:
             s0_re, s0_im = (torch.nn.functional.pad(x, (0, pad, 0, pad)) for x in (s0_re, s0_im))
     out = scan_fwd_op(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im,
-                      float(q_scale), int(chunk), y_layout == "bthd")
+                      float(q_scale), int(chunk), layouts[y_layout])
     y_re, y_im, s_re, s_im = out[0], out[1], out[2], out[3]
+    if y_layout == "bt2hd":
+        if d < 64:
+            raise NotImplementedError("y_layout 'bt2hd' needs head_dim 64")
+        return y_re, None, s_re, s_im
     if d < 64:
         y_re, y_im = y_re[..., :d], y_im[..., :d]
         s_re, s_im = s_re[..., :d, :d], s_im[..., :d, :d]

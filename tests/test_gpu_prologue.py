@@ -58,19 +58,28 @@ def _oracle(qkv, dt, bias, off, prot, ph, ro, rope, offset, qk_norm, floor):
 @pytest.mark.parametrize("case", CASES)
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_prologue_matches_oracle(gpu_lib, case, dtype):
+    """The prologue op on a projection matrix [B,T,C] (q, k, v re planes, im
+    planes, dt, padding) against the oracle's prologue: outputs, and the
+    gradients of the projection matrix (its padding columns zero), dt_bias,
+    the state offsets, protect, phase and routing."""
     from qllm2_amd.decode import build_rope_cache
-    from qllm2_amd.pam_prologue import pam_prologue
+    from qllm2_amd.pam_prologue import pam_prologue, proj_columns
     M, offset, gsp, phase, routing, qk_norm, floor, T = case
+    B, H, d = 2, 3, 64
     qkv, dt, bias, off, prot, ph, ro = _inputs(M, offset is not None, gsp, phase, routing, T, 500 + M + T)
-    qkv = qkv.to(dtype).float()                         # values both sides see
+    rnd = (lambda t: t.to(dtype).float() if t is not None else None)
+    qkv, dt, prot, ph, ro = rnd(qkv), rnd(dt), rnd(prot), rnd(ph), rnd(ro)   # values both sides see
     rope = build_rope_cache(offset + T + 3, 64) if offset is not None else None
     leaves, ref = _oracle(qkv, dt, bias, off, prot, ph, ro, rope, offset or 0, qk_norm, floor)
     dev = torch.device("cuda")
-    gl = [x.to(dev).requires_grad_(True) if x is not None else None for x in (dt, bias, off, prot, ph, ro)]
-    qkv_re = qkv[..., 0].contiguous().to(dtype).to(dev).requires_grad_(True)
-    qkv_im = qkv[..., 1].contiguous().to(dtype).to(dev).requires_grad_(True)
-    q, k, v, gamma, rot = pam_prologue(qkv_re, qkv_im, gl[0], gl[1], n_states=M, state_offset=gl[2], protect=gl[3],
-                                       phase=gl[4], routing=gl[5], rope=rope.to(dev) if rope is not None else None,
+    C = proj_columns(H)
+    proj = torch.cat([qkv[..., 0].reshape(B, T, 3 * H * d), qkv[..., 1].reshape(B, T, 3 * H * d), dt,
+                      torch.zeros(B, T, C - 6 * H * d - H)], -1)
+    proj = proj.to(dtype).to(dev).requires_grad_(True)
+    gl = [x.to(dev).to(dtype if i >= 2 else torch.float32).requires_grad_(True) if x is not None else None
+          for i, x in enumerate((bias, off, prot, ph, ro))]
+    q, k, v, gamma, rot = pam_prologue(proj, gl[0], n_heads=H, n_states=M, state_offset=gl[1], protect=gl[2],
+                                       phase=gl[3], routing=gl[4], rope=rope.to(dev) if rope is not None else None,
                                        rope_offset=offset or 0, qk_norm=qk_norm, gamma_floor=floor)
     tol_f = 1e-5 if dtype == torch.float32 else 2e-2
     tol_g = 1e-4 if dtype == torch.float32 else 2e-2
@@ -94,14 +103,18 @@ def test_prologue_matches_oracle(gpu_lib, case, dtype):
         loss = loss + (rot[0] * cr[0].to(dev).float()).sum() + (rot[1] * cr[1].to(dev).float()).sum()
     loss_ref.backward()
     loss.backward()
-    got_qkv = torch.stack([qkv_re.grad.float(), qkv_im.grad.float()], -1)
-    assert qkv_re.grad.dtype == dtype
+    dp = proj.grad.float().cpu()
+    assert proj.grad.dtype == dtype
+    n = 3 * H * d
+    got_qkv = torch.stack([dp[..., :n].reshape(B, T, 3, H, d), dp[..., n:2 * n].reshape(B, T, 3, H, d)], -1)
     assert _rel(got_qkv, leaves[0].grad) < tol_g, "dqkv"
-    names = ["ddt", "dbias", "doffset", "dprotect", "dphase", "drouting"]
-    for name, a, b in zip(names, gl, leaves[1:]):
+    assert _rel(dp[..., 2 * n:2 * n + H], leaves[1].grad) < tol_g, "ddt"
+    assert torch.all(dp[..., 2 * n + H:] == 0), "padding columns"
+    names = ["dbias", "doffset", "dprotect", "dphase", "drouting"]
+    for name, a, b in zip(names, gl, leaves[2:]):
         if a is None:
             continue
-        assert math.isfinite(a.grad.abs().sum().item()), name
+        assert math.isfinite(a.grad.float().abs().sum().item()), name
         assert _rel(a.grad, b.grad) < tol_g, f"{name}: {_rel(a.grad, b.grad):.2e}"
 
 
@@ -240,3 +253,25 @@ def test_fused_layer_bf16(gpu_lib):
     for name in ("qkv_proj.weight_real", "o_proj.weight_imag", "dt_bias", "state_dt_offset", "phase_proj.weight",
                  "protect_gate.weight"):
         assert _rel(params[name].grad, pr[name].grad) < 2e-2, name
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_cabs_matches_oracle(gpu_lib, dtype):
+    """The cabs kernel (|z| with the reference's +1e-8) and its backward
+    against the oracle's cabs under float64 autograd; a zero element keeps a
+    finite gradient (|z| >= 1e-4)."""
+    from qllm2_amd.pam_prologue import cabs
+    g = torch.Generator().manual_seed(31)
+    z = torch.randn(3, 50, 16, 2, generator=g).to(dtype).float()
+    z[0, 0, 0] = 0.0
+    gm = torch.randn(3, 50, 16, generator=g)
+    zr = z.double().requires_grad_(True)
+    mr = L.cabs(zr)
+    (mr * gm.double()).sum().backward()
+    zc = z.to(dtype).cuda().requires_grad_(True)
+    m = cabs(zc)
+    (m.float() * gm.cuda()).sum().backward()
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    assert m.dtype == dtype and _rel(m, mr) < tol
+    assert zc.grad.dtype == dtype and _rel(zc.grad, zr.grad) < tol
+    assert torch.isfinite(zc.grad.float()).all()

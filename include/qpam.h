@@ -236,11 +236,12 @@ int qpam_prologue_fwd(const qpam_prologue_args *a, void *stream);
  * outputs are not read).  In: gradients of q', k', v' ([B,H,T,d] contiguous,
  * out_dtype), of gamma and (when phase) rot ([M,B,H,T] fp32).  Out: the
  * gradients of the projections q, k, v (planar views [B,T,H,d] with strides
- * sg_b, sg_t, sg_h, in_dtype); dpre [M,B,H,T] fp32 = dL/d(dt + dt_bias +
+ * sg_b, sg_t, sg_h, in_dtype); dpre [B,T,H,M] fp32 = dL/d(dt + dt_bias +
  * state_offset_m) (dt_bias's and state_offset's gradients are its sums over
  * the other axes); optionally ddt [B,T,H] (strides sdd_*, in_dtype) = the sum
- * of dpre over m, dt's gradient; dprotect [B,H,T] fp32 (when protect); dphase
- * and, optionally, drouting [M,B,H,T] fp32 (when phase). */
+ * of dpre over m, dt's gradient; dprotect [B,T,H] fp32 (when protect); dphase
+ * and, optionally, drouting [B,T,H,M] fp32 (when phase) -- the layouts of the
+ * logits they are the gradients of.  16 * H * (2 + 4 M) * 4 <= 65536. */
 typedef struct {
     const qpam_prologue_args *fwd;
     const void *gq_re, *gq_im, *gk_re, *gk_im, *gv_re, *gv_im;

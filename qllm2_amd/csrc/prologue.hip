@@ -10,7 +10,10 @@
 // transposes; here one kernel reads each projection element once and writes
 // the scan's planar [B,H,T,d] operands, the decays and the rotations.
 //
-// Layout: one block of 4 waves per (b, h, 64 consecutive tokens).  The per-token
+// Layout: one block of 4 waves per (b, h, 64 consecutive tokens); the
+// operand planes are written with non-temporal stores (read next by other
+// kernels, not by this one: keeping them out of the caches measured 25% faster
+// than ordinary stores, which compete with the projection reads).  The per-token
 // scalars (decays of the M states, protect gate, rotations) take one thread per
 // (state, token), so their [M,B,H,T] rows are written as 256-byte runs.  For
 // the vectors a token row of d = 64 complex elements is one DPP row of 16 lanes
@@ -28,7 +31,16 @@ constexpr int PTHREADS = 256;
 struct Bf16 {};
 
 template <typename T> struct Io;
+typedef unsigned uintx2 __attribute__((ext_vector_type(2)));
+
 template <> struct Io<float> {
+    typedef floatx4 Raw;    // four elements as loaded
+    __device__ __forceinline__ static Raw load_raw(const void *base, int64_t off) {
+        return *reinterpret_cast<const floatx4 *>(static_cast<const float *>(base) + off);
+    }
+    __device__ __forceinline__ static void unpack(const Raw &v, float (&o)[4]) {
+        o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
+    }
     __device__ __forceinline__ static float load1(const void *base, int64_t off) {
         return static_cast<const float *>(base)[off];
     }
@@ -40,10 +52,19 @@ template <> struct Io<float> {
         o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
     }
     __device__ __forceinline__ static void store4(void *base, int64_t off, const float (&v)[4]) {
-        *reinterpret_cast<floatx4 *>(static_cast<float *>(base) + off) = floatx4{v[0], v[1], v[2], v[3]};
+        __builtin_nontemporal_store(floatx4{v[0], v[1], v[2], v[3]},
+                                    reinterpret_cast<floatx4 *>(static_cast<float *>(base) + off));
     }
 };
 template <> struct Io<Bf16> {
+    typedef uintx2 Raw;
+    __device__ __forceinline__ static Raw load_raw(const void *base, int64_t off) {
+        return *reinterpret_cast<const uintx2 *>(static_cast<const unsigned short *>(base) + off);
+    }
+    __device__ __forceinline__ static void unpack(const Raw &v, float (&o)[4]) {
+        o[0] = __uint_as_float(v.x << 16), o[1] = __uint_as_float(v.x & 0xffff0000u);
+        o[2] = __uint_as_float(v.y << 16), o[3] = __uint_as_float(v.y & 0xffff0000u);
+    }
     __device__ __forceinline__ static float load1(const void *base, int64_t off) {
         return bf16_to_f32(static_cast<const unsigned short *>(base)[off]);
     }
@@ -56,8 +77,8 @@ template <> struct Io<Bf16> {
         o[2] = __uint_as_float(v.y << 16), o[3] = __uint_as_float(v.y & 0xffff0000u);
     }
     __device__ __forceinline__ static void store4(void *base, int64_t off, const float (&v)[4]) {
-        *reinterpret_cast<uint2 *>(static_cast<unsigned short *>(base) + off) =
-            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        const uintx2 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+        __builtin_nontemporal_store(w, reinterpret_cast<uintx2 *>(static_cast<unsigned short *>(base) + off));
     }
 };
 
@@ -108,6 +129,20 @@ __global__ void __launch_bounds__(PTHREADS) prologue_fwd_kernel(qpam_prologue_ar
     const int bh = blockIdx.x / nt, tile = blockIdx.x - bh * nt;
     const int b = bh / a.H, h = bh - b * a.H;
     const int t0 = tile * PT, tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, c4 = (lane & 15) * 4;
+
+    // this lane's projection elements of its 4 tokens, loaded before the
+    // scalar work so the loads overlap it (rows past T re-read row T - 1 and
+    // are not stored)
+    typename Io<TI>::Raw raw[4][6];
+    const void *planes[6] = {a.q_re, a.q_im, a.k_re, a.k_im, a.v_re, a.v_im};
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+        const int t = min(t0 + w * 16 + it * 4 + (lane >> 4), a.T - 1);
+        const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
+#pragma unroll
+        for (int pl = 0; pl < 6; ++pl) raw[it][pl] = Io<TI>::load_raw(planes[pl], xo);
+    }
 
     {   // scalars: thread = (state m, token)
         const int tt = tid & (PT - 1), m = tid / PT, t = t0 + tt;
@@ -129,16 +164,14 @@ __global__ void __launch_bounds__(PTHREADS) prologue_fwd_kernel(qpam_prologue_ar
     }
     __syncthreads();
 
-    const int w = tid >> 6, lane = tid & 63, c4 = (lane & 15) * 4;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
         const int tt = w * 16 + it * 4 + (lane >> 4), t = t0 + tt;
         if (t >= a.T) continue;
-        const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
         float qr[4], qi[4], kr[4], ki[4], vr[4], vi[4];
-        Io<TI>::load4(a.q_re, xo, qr), Io<TI>::load4(a.q_im, xo, qi);
-        Io<TI>::load4(a.k_re, xo, kr), Io<TI>::load4(a.k_im, xo, ki);
-        Io<TI>::load4(a.v_re, xo, vr), Io<TI>::load4(a.v_im, xo, vi);
+        Io<TI>::unpack(raw[it][0], qr), Io<TI>::unpack(raw[it][1], qi);
+        Io<TI>::unpack(raw[it][2], kr), Io<TI>::unpack(raw[it][3], ki);
+        Io<TI>::unpack(raw[it][4], vr), Io<TI>::unpack(raw[it][5], vi);
         if (a.rope) {
             float c[4], s[4];
             rope4(a, t, c4, c, s);
@@ -186,101 +219,142 @@ __device__ __forceinline__ void rope_norm_bwd(float zr, float zi, float c, float
     }
 }
 
+// Backward layout: one block of 4 waves per (b, 16 consecutive tokens) and all
+// heads, so the projection gradients are written as whole rows of the
+// projection matrix (writes of 128-byte pieces spread over the rows, as a
+// per-head block would make them, measured twice as slow).  A (token, head)
+// row of 64 complex elements is one DPP row of 16 lanes; 16 rows per pass,
+// four passes' loads issued before their arithmetic.  The per-(token, head,
+// state) scalars are computed in token order (coalesced reads of the [M,B,H,T]
+// gradients), kept in LDS, and written state-fastest to the [B,T,H,M] outputs.
+constexpr int BT = 16;
+
 template <typename TI, typename TO>
 __global__ void __launch_bounds__(PTHREADS) prologue_bwd_kernel(qpam_prologue_bwd_args g, qpam_prologue_args a) {
-    __shared__ float s_keep[PT], s_gvv[PT];
-    const int nt = (int)tile_count(a);
-    const int bh = blockIdx.x / nt, tile = blockIdx.x - bh * nt;
-    const int b = bh / a.H, h = bh - b * a.H;
-    const int t0 = tile * PT, tid = threadIdx.x;
-    if (tid < PT) s_keep[tid] = t0 + tid < a.T ? 1.f - protect_prob<TI>(a, b, t0 + tid, h) : 1.f;
-    __syncthreads();
+    extern __shared__ float lds[];
+    const int rows = BT * a.H, M = a.M;
+    float *s_keep = lds, *s_gvv = lds + rows;
+    float *s_dpre = lds + 2 * rows, *s_dpm = s_dpre + M * rows, *s_dph = s_dpm + M * rows, *s_dro = s_dph + M * rows;
+    const int ntile = (a.T + BT - 1) / BT;
+    const int b = blockIdx.x / ntile, t0 = (blockIdx.x - b * ntile) * BT;
+    const int tid = threadIdx.x, lane = tid & 63, c4 = (lane & 15) * 4, slot = tid >> 4;
 
-    const int w = tid >> 6, lane = tid & 63, c4 = (lane & 15) * 4;
-    const bool rope = a.rope != nullptr, norm = a.qk_norm != 0;
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int tt = w * 16 + it * 4 + (lane >> 4), t = t0 + tt;
-        // whole DPP rows share t, so a row is either all in or all out of range
-        if (t >= a.T) continue;
-        const int64_t oo = (((int64_t)b * a.H + h) * a.T + t) * D + c4;
-        const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
-        const int64_t go = b * g.sg_b + (int64_t)t * g.sg_t + h * g.sg_h + c4;
-        float gqr[4], gqi[4], gkr[4], gki[4], gvr[4], gvi[4], vr[4], vi[4];
-        Io<TO>::load4(g.gq_re, oo, gqr), Io<TO>::load4(g.gq_im, oo, gqi);
-        Io<TO>::load4(g.gk_re, oo, gkr), Io<TO>::load4(g.gk_im, oo, gki);
-        Io<TO>::load4(g.gv_re, oo, gvr), Io<TO>::load4(g.gv_im, oo, gvi);
-        Io<TI>::load4(a.v_re, xo, vr), Io<TI>::load4(a.v_im, xo, vi);
-        if (rope || norm) {
-            float c[4] = {1.f, 1.f, 1.f, 1.f}, s[4] = {0.f, 0.f, 0.f, 0.f};
-            if (rope) rope4(a, t, c4, c, s);
-            float qr[4], qi[4], kr[4], ki[4];
-            if (norm) {
-                Io<TI>::load4(a.q_re, xo, qr), Io<TI>::load4(a.q_im, xo, qi);
-                Io<TI>::load4(a.k_re, xo, kr), Io<TI>::load4(a.k_im, xo, ki);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                rope_norm_bwd(norm ? qr[j] : 0.f, norm ? qi[j] : 0.f, c[j], s[j], rope, norm, gqr[j], gqi[j]);
-                rope_norm_bwd(norm ? kr[j] : 0.f, norm ? ki[j] : 0.f, c[j], s[j], rope, norm, gkr[j], gki[j]);
-            }
-        }
-        const float keep = s_keep[tt];
-        float dot = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            dot += gvr[j] * vr[j] + gvi[j] * vi[j];
-            gvr[j] *= keep, gvi[j] *= keep;
-        }
-        dot = row16_sum(dot);
-        if ((lane & 15) == 0) s_gvv[tt] = dot;
-        Io<TI>::store4(g.dq_re, go, gqr), Io<TI>::store4(g.dq_im, go, gqi);
-        Io<TI>::store4(g.dk_re, go, gkr), Io<TI>::store4(g.dk_im, go, gki);
-        Io<TI>::store4(g.dv_re, go, gvr), Io<TI>::store4(g.dv_im, go, gvi);
+    for (int r = tid; r < rows; r += PTHREADS) {  // row r = token-in-tile * H + head
+        const int tt = r / a.H, h = r - tt * a.H, t = t0 + tt;
+        s_keep[r] = t < a.T ? 1.f - protect_prob<TI>(a, b, t, h) : 1.f;
     }
     __syncthreads();
 
-    // scalars: thread = (state m, token); the sums over the states (dt's
-    // gradient, the protect gate's) are taken in a fixed order afterwards
-    __shared__ float s_dpre[4][PT], s_dpm[4][PT];
-    {
-        const int tt = tid & (PT - 1), m = tid / PT, t = t0 + tt;
-        float dpre = 0.f, dpm = 0.f;
-        if (t < a.T && m < a.M) {
-            const float p = 1.f - s_keep[tt];
+    const bool rope = a.rope != nullptr, norm = a.qk_norm != 0;
+    const void *gplanes[6] = {g.gq_re, g.gq_im, g.gk_re, g.gk_im, g.gv_re, g.gv_im};
+    for (int r0 = 0; r0 < rows; r0 += 64) {
+        typename Io<TO>::Raw graw[4][6];
+        typename Io<TI>::Raw vraw[4][2];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {   // rows past the tile re-read a valid row and are not stored
+            const int r = min(r0 + 16 * k + slot, rows - 1);
+            const int tt = r / a.H, h = r - tt * a.H, t = min(t0 + tt, a.T - 1);
+            const int64_t oo = (((int64_t)b * a.H + h) * a.T + t) * D + c4;
+            const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
+#pragma unroll
+            for (int pl = 0; pl < 6; ++pl) graw[k][pl] = Io<TO>::load_raw(gplanes[pl], oo);
+            vraw[k][0] = Io<TI>::load_raw(a.v_re, xo);
+            vraw[k][1] = Io<TI>::load_raw(a.v_im, xo);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int r = r0 + 16 * k + slot;
+            const int tt = r / a.H, h = r - tt * a.H, t = t0 + tt;
+            // a DPP row (16 lanes) shares r, so it is either all in or all out
+            if (r >= rows || t >= a.T) continue;
+            const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
+            const int64_t go = b * g.sg_b + (int64_t)t * g.sg_t + h * g.sg_h + c4;
+            float gqr[4], gqi[4], gkr[4], gki[4], gvr[4], gvi[4], vr[4], vi[4];
+            Io<TO>::unpack(graw[k][0], gqr), Io<TO>::unpack(graw[k][1], gqi);
+            Io<TO>::unpack(graw[k][2], gkr), Io<TO>::unpack(graw[k][3], gki);
+            Io<TO>::unpack(graw[k][4], gvr), Io<TO>::unpack(graw[k][5], gvi);
+            Io<TI>::unpack(vraw[k][0], vr), Io<TI>::unpack(vraw[k][1], vi);
+            if (rope || norm) {
+                float c[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
+                if (rope) rope4(a, t, c4, c, sn);
+                float qr[4], qi[4], kr[4], ki[4];
+                if (norm) {
+                    Io<TI>::load4(a.q_re, xo, qr), Io<TI>::load4(a.q_im, xo, qi);
+                    Io<TI>::load4(a.k_re, xo, kr), Io<TI>::load4(a.k_im, xo, ki);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    rope_norm_bwd(norm ? qr[j] : 0.f, norm ? qi[j] : 0.f, c[j], sn[j], rope, norm, gqr[j], gqi[j]);
+                    rope_norm_bwd(norm ? kr[j] : 0.f, norm ? ki[j] : 0.f, c[j], sn[j], rope, norm, gkr[j], gki[j]);
+                }
+            }
+            const float keep = s_keep[r];
+            float dot = 0.f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                dot += gvr[j] * vr[j] + gvi[j] * vi[j];
+                gvr[j] *= keep, gvi[j] *= keep;
+            }
+            dot = row16_sum(dot);
+            if ((lane & 15) == 0) s_gvv[r] = dot;
+            Io<TI>::store4(g.dq_re, go, gqr), Io<TI>::store4(g.dq_im, go, gqi);
+            Io<TI>::store4(g.dk_re, go, gkr), Io<TI>::store4(g.dk_im, go, gki);
+            Io<TI>::store4(g.dv_re, go, gvr), Io<TI>::store4(g.dv_im, go, gvi);
+        }
+    }
+
+    // scalars, token-fastest over (state, head, token)
+    const int items = M * rows;
+    const float lift = a.gamma_floor > 0.f ? 1.f - a.gamma_floor : 1.f;
+    for (int i = tid; i < items; i += PTHREADS) {
+        const int tt = i % BT, mh = i / BT, h = mh % a.H, m = mh / a.H, t = t0 + tt;
+        const int r = tt * a.H + h;
+        float dpre = 0.f, dpm = 0.f, dph = 0.f, dro = 0.f;
+        if (t < a.T) {
             const int64_t o = (((int64_t)m * a.B + b) * a.H + h) * a.T + t;
+            const float p = 1.f - s_keep[r];
             // d gamma / d pre = (1 - p) (1 - floor) (-exp(-softplus(pre))) softplus'(pre)
             const float pre = pre_sum<TI>(a, b, t, h, m);
             const float raw = expf(-softplus(pre));
             const float dsp = pre > 20.f ? 1.f : sigmoid(pre);
-            const float lift = a.gamma_floor > 0.f ? 1.f - a.gamma_floor : 1.f;
             const float gg = g.ggamma[o];
             dpre = -gg * (1.f - p) * lift * raw * dsp;
-            g.dpre[o] = dpre;
             dpm = gg * (1.f - lifted_decay(a, pre));  // d gamma_m / d p = 1 - base_m
             if (a.phase) {
-                float r, cs, sn;
-                rotation<TI>(a, b, t, h, m, r, cs, sn);
+                float rr, cs, sn;
+                rotation<TI>(a, b, t, h, m, rr, cs, sn);
                 const float gr = g.grot_re[o], gi = g.grot_im[o];
-                g.dphase[o] = r * (gi * cs - gr * sn);
-                if (g.drouting) g.drouting[o] = gr * cs + gi * sn;
+                dph = rr * (gi * cs - gr * sn);
+                dro = gr * cs + gi * sn;
             }
         }
-        s_dpre[m][tt] = dpre;
-        s_dpm[m][tt] = dpm;
+        s_dpre[m * rows + r] = dpre, s_dpm[m * rows + r] = dpm, s_dph[m * rows + r] = dph, s_dro[m * rows + r] = dro;
     }
     __syncthreads();
-    const int t = t0 + tid;
-    if (tid < PT && t < a.T) {
-        float ddt = 0.f, dp = -s_gvv[tid];       // d v' / d p = -v
-        for (int m = 0; m < a.M; ++m) ddt += s_dpre[m][tid], dp += s_dpm[m][tid];
+    for (int i = tid; i < items; i += PTHREADS) {   // state-fastest: contiguous [B,T,H,M] rows
+        const int m = i % M, r = i / M, tt = r / a.H, h = r - tt * a.H, t = t0 + tt;
+        if (t >= a.T) continue;
+        const int64_t o = (((int64_t)b * a.T + t) * a.H + h) * M + m;
+        g.dpre[o] = s_dpre[m * rows + r];
+        if (a.phase) {
+            g.dphase[o] = s_dph[m * rows + r];
+            if (g.drouting) g.drouting[o] = s_dro[m * rows + r];
+        }
+    }
+    for (int r = tid; r < rows; r += PTHREADS) {
+        const int tt = r / a.H, h = r - tt * a.H, t = t0 + tt;
+        if (t >= a.T) continue;
+        float ddt = 0.f, dp = -s_gvv[r];             // d v' / d p = -v
+        for (int m = 0; m < M; ++m) ddt += s_dpre[m * rows + r], dp += s_dpm[m * rows + r];
         if (g.ddt) Io<TI>::store1(g.ddt, b * g.sdd_b + (int64_t)t * g.sdd_t + h * g.sdd_h, ddt);
         if (a.protect) {
-            const float p = 1.f - s_keep[tid];
-            g.dprotect[((int64_t)b * a.H + h) * a.T + t] = dp * p * (1.f - p);
+            const float p = 1.f - s_keep[r];
+            g.dprotect[((int64_t)b * a.T + t) * a.H + h] = dp * p * (1.f - p);
         }
     }
 }
+
+size_t bwd_lds_bytes(const qpam_prologue_args &a) { return (size_t)(2 + 4 * a.M) * BT * a.H * sizeof(float); }
 
 // |z| = sqrt(re^2 + im^2 + 1e-8) of interleaved complex elements, four per
 // thread, and its backward dz = g z / |z|
@@ -385,15 +459,17 @@ extern "C" int qpam_prologue_bwd(const qpam_prologue_bwd_args *g, void *stream) 
     QPAM_REQUIRE(a.protect == nullptr || g->dprotect != nullptr, "qpam_prologue_bwd: dprotect required with protect");
     QPAM_REQUIRE(a.phase == nullptr || (g->grot_re && g->grot_im && g->dphase),
                  "qpam_prologue_bwd: rot gradients and dphase required with phase");
-    const long long blocks = (long long)a.B * a.H * ((a.T + PT - 1) / PT);
+    const size_t lds = bwd_lds_bytes(a);
+    QPAM_REQUIRE(lds <= 64 * 1024, "qpam_prologue_bwd: H=%d, M=%d need %zu bytes of LDS (64 KiB max)", a.H, a.M, lds);
+    const long long blocks = (long long)a.B * ((a.T + BT - 1) / BT);
     if (blocks == 0) return QPAM_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid((unsigned)blocks), block(PTHREADS);
     const bool fi = a.in_dtype == QPAM_F32, fo = a.out_dtype == QPAM_F32;
-    if (fi && fo) hipLaunchKernelGGL((prologue_bwd_kernel<float, float>), grid, block, 0, s, *g, a);
-    else if (fi) hipLaunchKernelGGL((prologue_bwd_kernel<float, Bf16>), grid, block, 0, s, *g, a);
-    else if (fo) hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, float>), grid, block, 0, s, *g, a);
-    else hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, Bf16>), grid, block, 0, s, *g, a);
+    if (fi && fo) hipLaunchKernelGGL((prologue_bwd_kernel<float, float>), grid, block, lds, s, *g, a);
+    else if (fi) hipLaunchKernelGGL((prologue_bwd_kernel<float, Bf16>), grid, block, lds, s, *g, a);
+    else if (fo) hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, float>), grid, block, lds, s, *g, a);
+    else hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, Bf16>), grid, block, lds, s, *g, a);
     return launch_status("prologue_bwd_kernel");
 }
 

@@ -17,7 +17,8 @@ the GEMM's backward without assembling slices.
 
 `pam_prologue` is differentiable (torch.library custom op with a registered
 autograd formula); the gradients of dt_bias and the state offsets are sums of
-the kernel's per-element dpre over the broadcast axes.
+the kernel's per-element dpre over the broadcast axes.  The backward writes
+the logits' gradients in the logits' own [B,T,H(,M)] layouts.
 """
 
 from typing import List, Optional
@@ -134,8 +135,8 @@ def prologue_bwd_op(proj: Tensor, protect: Optional[Tensor], phase: Optional[Ten
                     dt_bias: Tensor, state_offset: Optional[Tensor], rope: Optional[Tensor], H: int, M: int,
                     rope_offset: int, qk_norm: bool, gamma_floor: float, grads: List[Tensor]) -> List[Tensor]:
     """grads: the 9 output gradients (rot's empty without phase).  Returns
-    [dproj ([B,T,C], padding columns zero), dpre [M,B,H,T], dprotect [B,H,T],
-    dphase, drouting [M,B,H,T]] (fp32, empty where not applicable)."""
+    [dproj ([B,T,C], padding columns zero), dpre [B,T,H,M], dprotect [B,T,H],
+    dphase, drouting [B,T,H,M]] (fp32, empty where not applicable)."""
     a, keep = _fill(proj, protect, phase, routing, dt_bias, state_offset, rope, H, M, rope_offset, qk_norm,
                     gamma_floor)
     B, T, C = proj.shape
@@ -157,10 +158,10 @@ def prologue_bwd_op(proj: Tensor, protect: Optional[Tensor], phase: Optional[Ten
     g.sg_b, g.sg_t, g.sg_h = dproj.stride(0), dproj.stride(1), HEAD_DIM
     g.ddt = base + 6 * plane * es
     g.sdd_b, g.sdd_t, g.sdd_h = dproj.stride(0), dproj.stride(1), 1
-    dpre = torch.empty(M, B, H, T, device=dev, dtype=torch.float32)
+    dpre = torch.empty(B, T, H, M, device=dev, dtype=torch.float32)
     g.dpre = dpre.data_ptr()
     # distinct (never aliased) empty tensors stand for the gradients that do not apply
-    dprotect = torch.empty(B, H, T, device=dev, dtype=torch.float32) if protect is not None else dpre.new_empty(0)
+    dprotect = torch.empty(B, T, H, device=dev, dtype=torch.float32) if protect is not None else dpre.new_empty(0)
     if protect is not None:
         g.dprotect = dprotect.data_ptr()
     dphase = torch.empty_like(dpre) if phase is not None else dpre.new_empty(0)
@@ -178,10 +179,10 @@ def prologue_bwd_op(proj: Tensor, protect: Optional[Tensor], phase: Optional[Ten
 @prologue_bwd_op.register_fake
 def _(proj, protect, phase, routing, dt_bias, state_offset, rope, H, M, rope_offset, qk_norm, gamma_floor, grads):
     B, T, C = proj.shape
-    dpre = dt_bias.new_empty(M, B, H, T)
-    dprotect = dt_bias.new_empty(B, H, T) if protect is not None else dt_bias.new_empty(0)
-    dphase = dt_bias.new_empty(M, B, H, T) if phase is not None else dt_bias.new_empty(0)
-    drouting = dt_bias.new_empty(M, B, H, T) if routing is not None else dt_bias.new_empty(0)
+    dpre = dt_bias.new_empty(B, T, H, M)
+    dprotect = dt_bias.new_empty(B, T, H) if protect is not None else dt_bias.new_empty(0)
+    dphase = dt_bias.new_empty(B, T, H, M) if phase is not None else dt_bias.new_empty(0)
+    drouting = dt_bias.new_empty(B, T, H, M) if routing is not None else dt_bias.new_empty(0)
     return [proj.new_empty(B, T, C), dpre, dprotect, dphase, drouting]
 
 
@@ -209,12 +210,12 @@ def _backward(ctx, grads):
             full.append(torch.empty(0, device=dev))
     dproj, dpre, dprotect, dphase, drouting = prologue_bwd_op(
         proj, protect, phase, routing, dt_bias, state_offset, rope, H, M, rope_offset, qk_norm, gamma_floor, full)
-    per_head = dpre.sum(-1)                                              # [M,B,H], contiguous reduction
-    d_bias = per_head.sum((0, 1))
-    d_off = per_head.sum((1, 2)) if state_offset is not None else None
-    d_protect = dprotect.transpose(1, 2).to(protect.dtype) if protect is not None else None
-    d_phase = dphase.permute(1, 3, 2, 0).to(phase.dtype) if phase is not None else None      # [B,T,H,M]
-    d_routing = drouting.permute(1, 3, 2, 0).to(routing.dtype) if routing is not None else None
+    per_state = dpre.view(B * T, H * M).sum(0).view(H, M)               # column sums of [B*T, H*M]
+    d_bias = per_state.sum(1)
+    d_off = per_state.sum(0) if state_offset is not None else None
+    d_protect = dprotect.to(protect.dtype) if protect is not None else None
+    d_phase = dphase.to(phase.dtype) if phase is not None else None
+    d_routing = drouting.to(routing.dtype) if routing is not None else None
     return (dproj, d_protect, d_phase, d_routing, d_bias, d_off, None, None, None, None, None, None)
 
 

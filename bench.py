@@ -259,12 +259,13 @@ def bench_ce(steps, warmup):
 
 def bench_complex_ops(steps, warmup):
     """Complex elementwise layers (ComplexNorm, ModSwish, CGU gate), forward +
-    backward, on [16384, 1024] complex bf16 rows (a 16k-token batch at dim 1024).
-    HBM-bound: algorithmic bytes per call are the complex tensors read and
-    written (2 bytes per real), parameters aside."""
+    backward, on [65536, 1024] complex bf16 rows (4 batches of 16k tokens at dim
+    1024: large enough that the kernels, not the Python launches, set the
+    time).  HBM-bound: algorithmic bytes per call are the complex tensors read
+    and written (2 bytes per real), parameters aside."""
     import torch
     from qllm2_amd import triton_kernels as tk
-    rows, dim = 16384, 1024
+    rows, dim = 65536, 1024
     g = torch.Generator(device="cuda").manual_seed(9)
     z = torch.randn(rows, dim, 2, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
     up = torch.randn(rows, dim, 2, device="cuda", generator=g).to(torch.bfloat16).requires_grad_(True)
@@ -295,7 +296,7 @@ def bench_complex_ops(steps, warmup):
         ms = e0.elapsed_time(e1) / steps
         res[name] = {"ms_fwd_bwd": ms, "GBps": nbytes / (ms * 1e-3) / 1e9,
                      "hbm_frac": nbytes / (ms * 1e-3) / HBM_PEAK, "bytes": nbytes}
-    res["config"] = "rows=16384 dim=1024 complex bf16, fwd+bwd"
+    res["config"] = "rows=65536 dim=1024 complex bf16, fwd+bwd"
     return res
 
 

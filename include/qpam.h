@@ -42,6 +42,10 @@
  *                       and the rotations of _phase_and_alpha (:230-257,
  *                       consumed at :741-746)
  *   qpam_prologue_bwd   their autograd backward
+ *   qpam_delta_fwd      v11/model.py:491-576  V11PAMLayer._forward_delta (E2
+ *                       delta write; its solve v11/model.py:1005-1016) and
+ *                       v11/model.py:967-1002 _recur_step_delta
+ *   qpam_delta_bwd      their autograd backward
  *   qpam_cabs_fwd/_bwd  cabs (v11/complex_ops.py:86-87) feeding the gate and
  *                       phase projections (v11/model.py:228, 646)
  */
@@ -265,6 +269,54 @@ int qpam_prologue_bwd(const qpam_prologue_bwd_args *a, void *stream);
  * gz[i] = gmag[i] z[i] / mag[i]. */
 int qpam_cabs_fwd(int32_t dtype, int64_t n, const void *z, void *mag, void *stream);
 int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void *mag, const void *gmag, void *gz, void *stream);
+
+/* ---------------------------------------------------------- E2 delta rule --
+ * Gated delta-rule write, per (b, h) over t (one state, head-scalar decay):
+ *   S <- (gamma_t + gamma_eps) S;  u = beta_t (v_t - S k_t);
+ *   S <- S + u (x) conj(k_t);      y_t = S (q_scale q_t)
+ * -- the result of _forward_delta's chunked UT solve with gamma_eps = 1e-6
+ * (its per-step factor gamma + 1e-6), of _recur_step_delta with 0.  q, k, v
+ * fp32 planar [B,H,T,d] (strides b, h, t); gamma, beta fp32 [B,H,T] sharing
+ * strides sg_*; s0 optional fp32 planar [B,H,d,d] contiguous; y fp32 planar
+ * [B,H,T,d]; s_re/s_im the final state [B,H,d,d].  The workspace (size from
+ * qpam_delta_workspace_size, or NULL when no backward follows) keeps the state
+ * before every 16th token.  d == 64.
+ */
+typedef struct {
+    int32_t B, H, T, d;
+    float q_scale;
+    float gamma_eps;
+    qpam_cview q, k, v;
+    const float *gamma, *beta;
+    int64_t sg_b, sg_h, sg_t;
+    const float *s0_re, *s0_im;            /* optional */
+    qpam_mview y;
+    float *s_re, *s_im;
+    void *workspace;
+    size_t workspace_bytes;
+} qpam_delta_args;
+
+size_t qpam_delta_workspace_size(const qpam_delta_args *a);
+int qpam_delta_fwd(const qpam_delta_args *a, void *stream);
+
+/* Backward of qpam_delta_fwd (`fwd` describes the forward call; its
+ * workspace still holds the checkpoints).  dy fp32 planar [B,H,T,d]; ds
+ * optional gradient of the final state.  Out: dq, dk, dv planar fp32; dgamma,
+ * dbeta [B,H,T] with the strides of gamma; ds0 optional [B,H,d,d].
+ * Deterministic (fixed-order reductions). */
+typedef struct {
+    const qpam_delta_args *fwd;
+    qpam_cview dy;
+    const float *ds_re, *ds_im;            /* optional */
+    qpam_mview dq, dk, dv;
+    float *dgamma, *dbeta;
+    float *ds0_re, *ds0_im;                /* optional */
+    void *workspace;
+    size_t workspace_bytes;
+} qpam_delta_bwd_args;
+
+size_t qpam_delta_bwd_workspace_size(const qpam_delta_bwd_args *a);
+int qpam_delta_bwd(const qpam_delta_bwd_args *a, void *stream);
 
 /* ------------------------------------------------ complex elementwise -----
  * Split-real complex tensors [rows, dim, 2] (interleaved re/im, contiguous),

@@ -110,6 +110,24 @@ class CplxArgs(ctypes.Structure):
 
 
 # symbol -> (restype, argtypes); every symbol include/qpam.h declares
+class DeltaArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_i32), ("H", c_i32), ("T", c_i32), ("d", c_i32), ("q_scale", c_f32), ("gamma_eps", c_f32),
+        ("q", CView), ("k", CView), ("v", CView),
+        ("gamma", c_ptr), ("beta", c_ptr), ("sg_b", c_i64), ("sg_h", c_i64), ("sg_t", c_i64),
+        ("s0_re", c_ptr), ("s0_im", c_ptr), ("y", MView), ("s_re", c_ptr), ("s_im", c_ptr),
+        ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+class DeltaBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", ctypes.POINTER(DeltaArgs)), ("dy", CView), ("ds_re", c_ptr), ("ds_im", c_ptr),
+        ("dq", MView), ("dk", MView), ("dv", MView), ("dgamma", c_ptr), ("dbeta", c_ptr),
+        ("ds0_re", c_ptr), ("ds0_im", c_ptr), ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
 class PrologueArgs(ctypes.Structure):
     _fields_ = [
         ("B", c_i32), ("T", c_i32), ("H", c_i32), ("d", c_i32), ("M", c_i32),
@@ -160,6 +178,10 @@ SIGNATURES = {
     "qpam_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(PrologueArgs), c_ptr]),
     "qpam_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(PrologueBwdArgs), c_ptr]),
     "qpam_cabs_fwd": (ctypes.c_int, [c_i32, c_i64, c_ptr, c_ptr, c_ptr]),
+    "qpam_delta_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(DeltaArgs)]),
+    "qpam_delta_fwd": (ctypes.c_int, [ctypes.POINTER(DeltaArgs), c_ptr]),
+    "qpam_delta_bwd_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(DeltaBwdArgs)]),
+    "qpam_delta_bwd": (ctypes.c_int, [ctypes.POINTER(DeltaBwdArgs), c_ptr]),
     "qpam_cabs_bwd": (ctypes.c_int, [c_i32, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
 }
 

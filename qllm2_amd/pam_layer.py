@@ -9,6 +9,9 @@ Reference methods replaced (v11/model.py):
   _recur_step_additive      927-965  (one decode step)
   _recurrent                845-925  (decode token loop; all K states of a
                                       token in one kernel launch)
+  _forward_delta            491-576  (E2 delta write; HIP token recurrence
+                                      instead of the per-chunk solve)
+  _recur_step_delta         967-1002 (one E2 decode token)
 
   forward                   785-843  prefill of the production modes (head
                                       decay, additive write, E3 fused or one
@@ -20,9 +23,9 @@ Reference methods replaced (v11/model.py):
 The method replacements keep the layer's own projections/gates
 (_phase_and_alpha, _gamma_all_and_vprime, _gamma_and_vprime) and replace only
 the PAM math; the forward replacement fuses those elementwise steps into the
-prologue kernel (qpam_prologue_fwd).  Modes outside the hot path (E1
-per-channel decay, E2 delta write) keep the reference methods: install()
-leaves them reachable as the saved originals.
+prologue kernel (qpam_prologue_fwd).  The E1 per-channel decay mode keeps
+the reference methods: install() leaves them reachable as the saved
+originals.
 """
 
 import sys
@@ -31,6 +34,7 @@ import torch
 import torch.nn.functional as F
 
 from . import decode as _decode
+from . import pam_delta as _delta
 from . import fused_ce as _fused_ce
 from . import flash_pam as _flash_pam
 from . import triton_kernels as _tk
@@ -87,6 +91,22 @@ def forward_multistate_fused(self, x, queries, keys, values, head_dim):
     chunk = self.chunk_size if self.chunk_size > 0 else x.shape[1]
     return pam_scan_interleaved(queries, keys, protected_values, decay_gamma_all, head_dim, chunk,
                                 rot=_cat_rot(retrieval_phase, routing_weights))
+
+
+def forward_delta(self, queries, keys, protected_values, decay_gamma, write_beta, head_dim):
+    """V11PAMLayer._forward_delta (E2 delta write, head-scalar decay): the HIP
+    delta-rule kernels; per-channel decay or other head dims keep the original."""
+    if decay_gamma.dim() != 3 or head_dim != 64 or not queries.is_cuda:
+        return _ORIGINALS["_forward_delta"](self, queries, keys, protected_values, decay_gamma, write_beta, head_dim)
+    return _delta.forward_delta(queries, keys, protected_values, decay_gamma, write_beta, head_dim)
+
+
+def recur_step_delta(self, memory_state, decay_gamma, value_t, key_t, query_t, write_beta_t):
+    """V11PAMLayer._recur_step_delta (one decode token of the E2 write)."""
+    if decay_gamma.dim() != 2 or memory_state.shape[-2] != 64 or not memory_state.is_cuda:
+        return _ORIGINALS["_recur_step_delta"](self, memory_state, decay_gamma, value_t, key_t, query_t,
+                                               write_beta_t)
+    return _delta.recur_step_delta(memory_state, decay_gamma, value_t, key_t, query_t, write_beta_t)
 
 
 def recur_step_additive(self, memory_state, decay_gamma, value_t, key_t, query_t):
@@ -265,6 +285,8 @@ _METHODS = {
     "_fused_chunk_step": fused_chunk_step,
     "_forward_multistate_fused": forward_multistate_fused,
     "_recur_step_additive": recur_step_additive,
+    "_forward_delta": forward_delta,
+    "_recur_step_delta": recur_step_delta,
     "_recurrent": recurrent,
 }
 

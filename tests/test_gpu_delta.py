@@ -1,0 +1,109 @@
+"""GPU parity of the E2 delta-rule kernels (qpam_delta_fwd / qpam_delta_bwd)
+against the CPU oracle (oracle/delta.py: the reference's chunked UT-transform
+form and its token recurrence) in float64, fp32 rel <= 1e-4 on Y, S and every
+gradient (dq, dk, dv, dgamma, dbeta, ds0)."""
+
+import math
+
+import pytest
+import torch
+
+from oracle import delta as D
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).abs().max() / (b.abs().max() + 1e-30)).item()
+
+
+def _run(q, k, v, g, b, s0, dy, ds, eps):
+    from qllm2_amd.pam_delta import delta_planar
+    dev = torch.device("cuda")
+    planes = [x[..., i].contiguous().float().to(dev).requires_grad_(True) for x in (q, k, v) for i in (0, 1)]
+    gg, bb = g.float().to(dev).requires_grad_(True), b.float().to(dev).requires_grad_(True)
+    s0p = None
+    if s0 is not None:
+        s0p = tuple(s0[..., i].contiguous().float().to(dev).requires_grad_(True) for i in (0, 1))
+    y_re, y_im, s_re, s_im = delta_planar(*planes, gg, bb, q_scale=64 ** -0.5, gamma_eps=eps, s0=s0p)
+    loss = (y_re * dy[..., 0].to(dev)).sum() + (y_im * dy[..., 1].to(dev)).sum()
+    if ds is not None:
+        loss = loss + (s_re * ds[..., 0].to(dev)).sum() + (s_im * ds[..., 1].to(dev)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    cpx = (lambda a, b: torch.stack([a.grad, b.grad], -1).cpu())
+    grads = [cpx(planes[0], planes[1]), cpx(planes[2], planes[3]), cpx(planes[4], planes[5]), gg.grad.cpu(),
+             bb.grad.cpu(), cpx(*s0p) if s0p is not None else None]
+    return torch.stack([y_re, y_im], -1).detach().cpu(), torch.stack([s_re, s_im], -1).detach().cpu(), grads
+
+
+def _ref(q, k, v, g, b, s0, dy, ds, chunked):
+    xs = [x.double().clone().requires_grad_(True) for x in (q, k, v, g, b)]
+    s0r = s0.double().clone().requires_grad_(True) if s0 is not None else None
+    if chunked:
+        y, s = D.delta_chunked(*xs, 64, 64, state=s0r)
+    else:
+        y, s = D.delta_recurrent(*xs, 64, state=s0r, eps=0.0)
+    loss = (y * dy.double()).sum() + ((s * ds.double()).sum() if ds is not None else 0)
+    loss.backward()
+    return y.detach(), s.detach(), [x.grad for x in xs] + [s0r.grad if s0r is not None else None]
+
+
+NAMES = ["dq", "dk", "dv", "dgamma", "dbeta", "ds0"]
+
+
+@pytest.mark.parametrize("T,with_s0,with_ds", [(64, False, False), (100, True, True), (37, False, True),
+                                               (1, True, False), (16, False, False), (130, True, False)])
+def test_delta_matches_chunked_oracle(gpu_lib, T, with_s0, with_ds):
+    """The reference's chunked UT-transform form (delta_chunk 64) in float64
+    against the kernels with gamma + 1e-6: outputs, final state, all gradients;
+    ragged T (not a multiple of the 16-token checkpoint or 4-token sub-group)."""
+    B, H, d = 2, 3, 64
+    q, k, v, g, b = D.make_delta_inputs(B, H, T, d, 600 + T)
+    gen = torch.Generator().manual_seed(601 + T)
+    s0 = torch.randn(B, H, d, d, 2, generator=gen, dtype=torch.float64) * 0.05 if with_s0 else None
+    dy = torch.randn(B, H, T, d, 2, generator=gen, dtype=torch.float64)
+    ds = torch.randn(B, H, d, d, 2, generator=gen, dtype=torch.float64) * 0.1 if with_ds else None
+    y, s, grads = _run(q, k, v, g, b, s0, dy, ds, 1e-6)
+    yr, sr, rgrads = _ref(q, k, v, g, b, s0, dy, ds, chunked=True)
+    assert _rel(y, yr) < 1e-4, f"y {_rel(y, yr):.2e}"
+    assert _rel(s, sr) < 1e-4, f"s {_rel(s, sr):.2e}"
+    for name, a, r in zip(NAMES, grads, rgrads):
+        if a is None or r is None:
+            continue
+        assert math.isfinite(a.abs().sum().item()), name
+        assert _rel(a, r) < 1e-4, f"{name}: {_rel(a, r):.2e}"
+
+
+def test_delta_step_matches_reference_step(gpu_lib):
+    """recur_step_delta (the decode drop-in, gamma without the chunked form's
+    1e-6) against the reference step, several tokens in a row."""
+    from qllm2_amd.pam_delta import recur_step_delta
+    B, H, d = 2, 2, 64
+    q, k, v, g, b = D.make_delta_inputs(B, H, 5, d, 650)
+    s = torch.randn(B, H, d, d, 2, generator=torch.Generator().manual_seed(651), dtype=torch.float64) * 0.1
+    sc = s.float().cuda()
+    for t in range(5):
+        qt = q[:, :, t] * d ** -0.5
+        yr, s = D.recur_step_delta(s, g[:, :, t], v[:, :, t], k[:, :, t], qt, b[:, :, t])
+        y, sc = recur_step_delta(sc, g[:, :, t].float().cuda(), v[:, :, t].float().cuda(), k[:, :, t].float().cuda(),
+                                 qt.float().cuda(), b[:, :, t].float().cuda())
+        assert _rel(y, yr) < 1e-4 and _rel(sc, s) < 1e-4
+
+
+def test_delta_long_sequence_properties(gpu_lib):
+    """T = 2048 (the config-3 length, 128 checkpoint groups), B=1, H=4: output
+    and final state of the first head against the oracle's token recurrence."""
+    from qllm2_amd.pam_delta import delta_planar
+    B, H, T, d = 1, 4, 2048, 64
+    q, k, v, g, b = D.make_delta_inputs(B, H, T, d, 660, dtype=torch.float32)
+    dev = torch.device("cuda")
+    planes = [x[..., i].contiguous().to(dev) for x in (q, k, v) for i in (0, 1)]
+    with torch.no_grad():
+        y_re, y_im, s_re, s_im = delta_planar(*planes, g.to(dev), b.to(dev), q_scale=d ** -0.5, gamma_eps=1e-6)
+    yr, sr = D.delta_recurrent(q[:, :1].double(), k[:, :1].double(), v[:, :1].double(), g[:, :1].double(),
+                               b[:, :1].double(), d)
+    y = torch.stack([y_re, y_im], -1)[:, :1].cpu()
+    assert _rel(y, yr) < 1e-4
+    assert _rel(torch.stack([s_re, s_im], -1)[:, :1].cpu(), sr) < 1e-4

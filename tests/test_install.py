@@ -36,6 +36,12 @@ def test_install_rebinds_methods_and_aliases():
         def _recurrent(self, *a):
             return "orig"
 
+        def _forward_delta(self, *a):
+            return "orig"
+
+        def _recur_step_delta(self, *a):
+            return "orig"
+
     mod.V11PAMLayer = V11PAMLayer
     mod.fused_decay_matrix = lambda *a: "orig"
     cops = types.ModuleType("v11x.complex_ops")  # imported the ops by name before install()
@@ -54,6 +60,8 @@ def test_install_rebinds_methods_and_aliases():
         assert V11PAMLayer._forward_multistate_fused is pam_layer.forward_multistate_fused
         assert V11PAMLayer._recur_step_additive is pam_layer.recur_step_additive
         assert V11PAMLayer._recurrent is pam_layer.recurrent
+        assert V11PAMLayer._forward_delta is pam_layer.forward_delta
+        assert V11PAMLayer._recur_step_delta is pam_layer.recur_step_delta
         assert V11PAMLayer._dual_form_block is pam_layer.dual_form_block  # staticmethod unwraps
         assert mod.fused_decay_matrix is triton_kernels.fused_decay_matrix
         assert sys.modules["v11x.flash_pam"] is flash_pam

@@ -40,7 +40,8 @@ def parse():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=1000)
-    ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "e3", "ce", "cplx", "layer", "copy"], default=None,
+    ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "e3", "ce", "cplx", "layer", "delta",
+                                       "copy"], default=None,
                     help="run one workload (for profiler passes) and print its own JSON line")
     return ap.parse_args()
 
@@ -454,6 +455,109 @@ def bench_pam_layer(steps, warmup):
     return res
 
 
+def _delta_reference_steps(q, k, v, gamma, beta, d, chunk):
+    """The reference's chunked E2 forward (v11/model.py:491-576) as torch
+    steps on the GPU -- decay matrix, Gram and mass matrices, the 2C x 2C real
+    block solve, dual-form and carried reads, state write -- for timing
+    against the kernels.  Planar fp32 inputs [B,H,T,d]."""
+    import torch
+    (qr, qi), (kr, ki), (vr, vi) = q, k, v
+    B, H, T, _ = qr.shape
+    scale = d ** -0.5
+    sr = qr.new_zeros(B, H, d, d)
+    si = qr.new_zeros(B, H, d, d)
+    ys = []
+    for c0 in range(0, T, chunk):
+        c1 = min(c0 + chunk, T)
+        n = c1 - c0
+        g, bt = gamma[:, :, c0:c1], beta[:, :, c0:c1]
+        lg = torch.log(g + 1e-6)
+        cum = torch.cumsum(lg, -1)
+        diff = cum.unsqueeze(-1) - cum.unsqueeze(-2)
+        dmat = torch.exp(torch.clamp(diff.masked_fill(torch.ones(n, n, device=g.device).triu(1).bool(), -1e4),
+                                     max=0)) * torch.ones(n, n, device=g.device).tril()
+        alpha = torch.exp(cum)
+        k_r, k_i, q_r, q_i = kr[:, :, c0:c1], ki[:, :, c0:c1], qr[:, :, c0:c1], qi[:, :, c0:c1]
+        gram_r = k_r @ k_r.transpose(-1, -2) + k_i @ k_i.transpose(-1, -2)
+        gram_i = k_i @ k_r.transpose(-1, -2) - k_r @ k_i.transpose(-1, -2)
+        strict = torch.ones(n, n, device=g.device).tril(-1)
+        m_r, m_i = bt.unsqueeze(-1) * dmat * strict * gram_r, bt.unsqueeze(-1) * dmat * strict * gram_i
+        sk_r = (k_r @ sr.transpose(-1, -2) - k_i @ si.transpose(-1, -2)) * alpha.unsqueeze(-1)
+        sk_i = (k_r @ si.transpose(-1, -2) + k_i @ sr.transpose(-1, -2)) * alpha.unsqueeze(-1)
+        w_r, w_i = bt.unsqueeze(-1) * (vr[:, :, c0:c1] - sk_r), bt.unsqueeze(-1) * (vi[:, :, c0:c1] - sk_i)
+        eye = torch.eye(n, device=g.device)
+        sysm = torch.cat([torch.cat([eye + m_r, -m_i], -1), torch.cat([m_i, eye + m_r], -1)], -2)
+        sol = torch.linalg.solve(sysm, torch.cat([w_r, w_i], -2))
+        u_r, u_i = sol[..., :n, :], sol[..., n:, :]
+        qk_r = q_r @ k_r.transpose(-1, -2) + q_i @ k_i.transpose(-1, -2)
+        qk_i = q_i @ k_r.transpose(-1, -2) - q_r @ k_i.transpose(-1, -2)
+        p_r, p_i = dmat * qk_r, dmat * qk_i
+        sq_r, sq_i = q_r * scale * alpha.unsqueeze(-1), q_i * scale * alpha.unsqueeze(-1)
+        y_r = (p_r @ u_r - p_i @ u_i) * scale + sq_r @ sr.transpose(-1, -2) - sq_i @ si.transpose(-1, -2)
+        y_i = (p_r @ u_i + p_i @ u_r) * scale + sq_r @ si.transpose(-1, -2) + sq_i @ sr.transpose(-1, -2)
+        ys.append(torch.stack([y_r, y_i], -1))
+        tail = (alpha[:, :, -1:] / (alpha + 1e-12)).unsqueeze(-1)
+        ud_r, ud_i = u_r * tail, u_i * tail
+        total = alpha[:, :, -1:].unsqueeze(-1)
+        sr, si = (sr * total + ud_r.transpose(-1, -2) @ k_r + ud_i.transpose(-1, -2) @ k_i,
+                  si * total + ud_i.transpose(-1, -2) @ k_r - ud_r.transpose(-1, -2) @ k_i)
+    return torch.cat(ys, 2), (sr, si)
+
+
+def bench_delta(steps, warmup):
+    """E2 delta rule forward + backward at the config-3 shape (one state: B=8,
+    T=2048, H=12, d=64, fp32): the HIP kernels against the reference's chunked
+    UT-transform steps (delta_chunk 64) run in torch on the same GPU.  The
+    kernels are a sequential recurrence per (b, h) chain: `us_per_token` is
+    the forward's time per token step, the bound that matters; achieved HBM
+    traffic (inputs, outputs, checkpoints) is reported beside it."""
+    import torch
+    from qllm2_amd.pam_delta import delta_planar
+    B, H, T, d = 8, 12, 2048, 64
+    gen = torch.Generator(device="cuda").manual_seed(31)
+    planes = [torch.randn(B, H, T, d, device="cuda", generator=gen) for _ in range(6)]
+    nrm = (planes[2].square() + planes[3].square()).sum(-1, keepdim=True).sqrt()
+    planes[2], planes[3] = planes[2] / nrm, planes[3] / nrm
+    gamma = 0.5 + 0.5 * torch.sigmoid(torch.randn(B, H, T, device="cuda", generator=gen) + 2)
+    beta = torch.sigmoid(torch.randn(B, H, T, device="cuda", generator=gen))
+    leaves = [x.requires_grad_(True) for x in planes + [gamma, beta]]
+    dy = [torch.randn(B, H, T, d, device="cuda", generator=gen) for _ in range(2)]
+
+    def timed(fn, n):
+        for _ in range(min(warmup, n)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    def fused():
+        y_re, y_im, _, _ = delta_planar(*leaves[:6], leaves[6], leaves[7], q_scale=d ** -0.5)
+        torch.autograd.grad([y_re, y_im], leaves, dy)
+
+    def fwd_only():
+        with torch.no_grad():
+            delta_planar(*planes, gamma, beta, q_scale=d ** -0.5)
+
+    def reference():
+        y, _ = _delta_reference_steps((leaves[0], leaves[1]), (leaves[2], leaves[3]), (leaves[4], leaves[5]),
+                                      leaves[6], leaves[7], d, 64)
+        torch.autograd.grad([y[..., 0], y[..., 1]], leaves, dy)
+
+    ms = timed(fused, steps)
+    fwd_ms = timed(fwd_only, steps)
+    ref_ms = timed(reference, max(2, steps // 5))
+    fwd_bytes = 6 * B * H * T * d * 4 + 2 * B * H * T * 4 + 2 * B * H * T * d * 4 + B * H * (T // 16) * 2 * d * d * 4
+    return {"config": "E2 delta write, B=8 T=2048 H=12 d=64 fp32, fwd+bwd", "ms_fwd_bwd": ms, "ms_fwd": fwd_ms,
+            "reference_steps_ms_fwd_bwd": ref_ms, "speedup": ref_ms / ms, "tokens_per_s": B * T / (ms * 1e-3),
+            "us_per_token_fwd": fwd_ms * 1e3 / T, "fwd_bytes": fwd_bytes,
+            "fwd_hbm_frac": fwd_bytes / (fwd_ms * 1e-3) / HBM_PEAK}
+
+
 def cpu_baseline_scan():
     """The reference's chunk loop restated on the CPU (oracle.pam.chunked_head),
     fp32, on a bounded sample: 1 of the 8 batch rows (H=12, T=2048)."""
@@ -490,6 +594,7 @@ def main():
               "ce": lambda: bench_ce(args.steps, args.warmup),
               "cplx": lambda: bench_complex_ops(args.steps, args.warmup),
               "layer": lambda: bench_pam_layer(args.steps, args.warmup),
+              "delta": lambda: bench_delta(args.steps, args.warmup),
               "copy": copy_calibration}[args.only]
         print(json.dumps({"only": args.only, "result": fn()}), flush=True)
         return
@@ -526,7 +631,8 @@ def main():
                          "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 2),
                          "ce_fwd_bwd_config5": bench_ce(max(3, args.steps // 4), 2),
                          "complex_elementwise": bench_complex_ops(max(3, args.steps // 2), 2),
-                         "pam_layer_config3": bench_pam_layer(max(3, args.steps // 2), 2)}
+                         "pam_layer_config3": bench_pam_layer(max(3, args.steps // 2), 2),
+                         "delta_e2_config3_shape": bench_delta(max(3, args.steps // 4), 1)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_scan()
     print(json.dumps(out), flush=True)

@@ -9,82 +9,146 @@
 // v11/model.py:967-1002, is the same step with g~ = gamma).
 //
 // Design: the rows of S are independent under the recurrence (row i reads
-// only k, q, v_i, gamma, beta), so one block of 8 waves owns one (b, h) chain
-// and each lane owns 2 rows x 4 columns of the 64 x 64 complex state in
-// registers; the per-row dot products S k and S q~ are DPP reductions over the
-// 16 lanes of a row group, and no other communication happens in the forward.
-// A token costs ~100 dependent VALU/DPP operations and no solve; the chunked
-// form's O(C^2 d + C^3) per-chunk work (the Gram matrix, the 2C x 2C real
-// solve, the dual-form products) is not needed on a GPU whose state fits in
-// the registers of one block.  The forward stores the state before every
-// 16th token (the backward's checkpoints).
+// only k, q, v_i, gamma, beta).  A (b, h) chain's 64 x 64 complex state is
+// split over 16 waves of 4 rows; a lane owns 1 row x 4 columns in registers,
+// and the per-row dot products S k and S q~ are DPP reductions over the 16
+// lanes of a row group.  The forward needs no other communication, so each
+// wave is its own workgroup (B*H*16 of them, spread over every CU).  A token
+// costs ~100 VALU/DPP operations per wave and no solve; the chunked form's
+// O(C^2 d + C^3) per-chunk work (the Gram matrix, the 2C x 2C real solve, the
+// dual-form products) is not needed on a GPU whose state fits in registers.
+// The forward stores the state before every 16th token (the backward's
+// checkpoints).
 //
-// Backward: blocks walk the chains' 16-token groups in reverse; each group is
-// recomputed from its checkpoint with the state before every 4th token kept in
-// a per-block scratch, then each 4-token sub-group is recomputed into
-// registers and differentiated in reverse.  Gradients of k, q, gamma and beta
-// are sums over the 64 rows: lanes -> row groups by shuffles, waves through
-// LDS once per sub-group, in a fixed order (deterministic).
+// Backward: four workgroups of 4 waves (16 rows each) per chain walk its
+// 16-token groups in reverse; each group is recomputed from its checkpoint
+// with the state before every 4th token kept in a scratch, then each 4-token
+// sub-group is recomputed into registers and differentiated in reverse.
+// Gradients of k, q, gamma and beta are sums over the 64 rows: lanes -> row
+// groups by shuffles, waves through LDS every 2 tokens, workgroups through
+// per-part partial sums that a second kernel adds in a fixed order
+// (deterministic).
 #include "common.h"
 
 namespace qpam {
 namespace {
 
 constexpr int D = 64;
-constexpr int DTHREADS = 512;   // 8 waves x 8 rows
-constexpr int GROUP = 16;       // tokens per forward checkpoint
-constexpr int SUB = 4;          // tokens per backward sub-group
+constexpr int RPL = 1;               // rows per lane
+constexpr int NW = D / (4 * RPL);    // waves per chain (16)
+constexpr int GROUP = 16;            // tokens per forward checkpoint
+constexpr int SUB = 4;               // tokens per backward sub-group
 constexpr int SUBS = GROUP / SUB;
+constexpr int FL = 2;                // tokens per backward cross-wave reduction
+constexpr int PARTS = 4;             // backward workgroups per chain
+constexpr int PW = NW / PARTS;       // waves per backward workgroup
+constexpr int PROWS = 4 * RPL * PW;  // rows per backward workgroup
+constexpr int BWD_THREADS = 64 * PW;
 
 struct Lane {
-    int w, rg, cg, r0;   // wave, row group (0..3), column group (0..15), first row
-    __device__ Lane(int tid) {
-        w = tid >> 6;
-        const int lane = tid & 63;
-        rg = lane >> 4, cg = lane & 15;
-        r0 = 8 * w + 2 * rg;
+    int w, lane, rg, cg, r0;   // wave of the chain, lane, row group (0..3), column group (0..15), first row
+    __device__ Lane(int wave, int ln) {
+        w = wave, lane = ln;
+        rg = ln >> 4, cg = ln & 15;
+        r0 = (4 * w + rg) * RPL;
     }
+    __device__ int slot() const { return w * 64 + lane; }   // thread-private state slot of the chain
 };
 
 // one token's inputs as this lane sees them
 struct Tok {
     float kr[4], ki[4], qr[4], qi[4];  // the lane's 4 columns (q already scaled)
-    float vr[2], vi[2];                // the lane's 2 rows
+    float vr[RPL], vi[RPL];            // the lane's rows
     float g, b;                        // gamma + eps, beta
 };
 
 struct State {
-    float r[2][4], i[2][4];
+    float r[RPL][4], i[RPL][4];
 };
 
-__device__ __forceinline__ Tok load_tok(const qpam_delta_args &a, int b, int h, int t, const Lane &L) {
+// The inputs of NT consecutive tokens staged in LDS: the k and q planes of
+// every column (q scaled), v of the ROWS rows the workgroup owns, gamma + eps
+// and beta.  Global loads go to registers first (fetch) and to LDS later
+// (commit), so a span's loads overlap the previous span's arithmetic.
+template <int NT, int ROWS>
+struct Span {
+    floatx4 kq[NT][4][16];   // [token][k re, k im, q re, q im][column / 4]
+    float v[NT][2][ROWS];
+    float gb[NT][2];
+};
+
+template <int NT, int ROWS, int NTHR>
+struct SpanRegs {
+    static constexpr int KQ = NT * 64 / NTHR;                 // float4 per thread
+    static constexpr int VV = (NT * 2 * ROWS + NTHR - 1) / NTHR;
+    static_assert(KQ >= 1 && KQ * NTHR == NT * 64, "span shape");
+    floatx4 kq[KQ];
+    float v[VV];
+    float gb;
+
+    // rows past T re-read row T - 1 (their results are not stored)
+    __device__ __forceinline__ void fetch(const qpam_delta_args &a, int b, int h, int t0, int row0, int tid) {
+#pragma unroll
+        for (int k = 0; k < KQ; ++k) {
+            const int i = tid + k * NTHR, tok = i >> 6, pl = (i >> 4) & 3, c4 = i & 15;
+            const int t = min(t0 + tok, a.T - 1);
+            const qpam_cview &v = pl < 2 ? a.k : a.q;
+            const float *base = static_cast<const float *>((pl & 1) ? v.im : v.re);
+            kq[k] = *reinterpret_cast<const floatx4 *>(base + b * v.s0 + h * v.s1 + (int64_t)t * v.s2 + 4 * c4);
+            if (pl >= 2) kq[k] *= a.q_scale;
+        }
+#pragma unroll
+        for (int k = 0; k < VV; ++k) {
+            const int i = min(tid + k * NTHR, NT * 2 * ROWS - 1);
+            const int tok = i / (2 * ROWS), rem = i - tok * 2 * ROWS, ri = rem / ROWS, r = rem - ri * ROWS;
+            const int t = min(t0 + tok, a.T - 1);
+            const float *base = static_cast<const float *>(ri ? a.v.im : a.v.re);
+            v[k] = base[b * a.v.s0 + h * a.v.s1 + (int64_t)t * a.v.s2 + row0 + r];
+        }
+        const int i = min(tid, 2 * NT - 1), t = min(t0 + (i >> 1), a.T - 1);
+        const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)t * a.sg_t;
+        gb = (i & 1) ? a.beta[go] : a.gamma[go] + a.gamma_eps;
+    }
+
+    __device__ __forceinline__ void commit(Span<NT, ROWS> &sp, int tid) const {
+#pragma unroll
+        for (int k = 0; k < KQ; ++k) {
+            const int i = tid + k * NTHR;
+            sp.kq[i >> 6][(i >> 4) & 3][i & 15] = kq[k];
+        }
+#pragma unroll
+        for (int k = 0; k < VV; ++k) {
+            const int i = tid + k * NTHR;
+            if (i < NT * 2 * ROWS) {
+                const int tok = i / (2 * ROWS), rem = i - tok * 2 * ROWS, ri = rem / ROWS, r = rem - ri * ROWS;
+                sp.v[tok][ri][r] = v[k];
+            }
+        }
+        if (tid < 2 * NT) sp.gb[tid >> 1][tid & 1] = gb;
+    }
+};
+
+// token j of a span as this lane sees it; `row` = the lane's first row in the span's rows
+template <int NT, int ROWS>
+__device__ __forceinline__ Tok span_tok(const Span<NT, ROWS> &sp, int j, int cg, int row) {
     Tok x;
-    const int64_t kq = b * a.k.s0 + h * a.k.s1 + (int64_t)t * a.k.s2 + 4 * L.cg;
-    const int64_t qq = b * a.q.s0 + h * a.q.s1 + (int64_t)t * a.q.s2 + 4 * L.cg;
-    const int64_t vv = b * a.v.s0 + h * a.v.s1 + (int64_t)t * a.v.s2 + L.r0;
-    const floatx4 kr = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(a.k.re) + kq);
-    const floatx4 ki = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(a.k.im) + kq);
-    const floatx4 qr = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(a.q.re) + qq);
-    const floatx4 qi = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(a.q.im) + qq);
-    const floatx2 vr = *reinterpret_cast<const floatx2 *>(static_cast<const float *>(a.v.re) + vv);
-    const floatx2 vi = *reinterpret_cast<const floatx2 *>(static_cast<const float *>(a.v.im) + vv);
+    const floatx4 kr = sp.kq[j][0][cg], ki = sp.kq[j][1][cg], qr = sp.kq[j][2][cg], qi = sp.kq[j][3][cg];
     x.kr[0] = kr.x, x.kr[1] = kr.y, x.kr[2] = kr.z, x.kr[3] = kr.w;
     x.ki[0] = ki.x, x.ki[1] = ki.y, x.ki[2] = ki.z, x.ki[3] = ki.w;
-    x.qr[0] = qr.x * a.q_scale, x.qr[1] = qr.y * a.q_scale, x.qr[2] = qr.z * a.q_scale, x.qr[3] = qr.w * a.q_scale;
-    x.qi[0] = qi.x * a.q_scale, x.qi[1] = qi.y * a.q_scale, x.qi[2] = qi.z * a.q_scale, x.qi[3] = qi.w * a.q_scale;
-    x.vr[0] = vr.x, x.vr[1] = vr.y, x.vi[0] = vi.x, x.vi[1] = vi.y;
-    const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)t * a.sg_t;
-    x.g = a.gamma[go] + a.gamma_eps;
-    x.b = a.beta[go];
+    x.qr[0] = qr.x, x.qr[1] = qr.y, x.qr[2] = qr.z, x.qr[3] = qr.w;
+    x.qi[0] = qi.x, x.qi[1] = qi.y, x.qi[2] = qi.z, x.qi[3] = qi.w;
+#pragma unroll
+    for (int rr = 0; rr < RPL; ++rr) x.vr[rr] = sp.v[j][0][row + rr], x.vi[rr] = sp.v[j][1][row + rr];
+    x.g = sp.gb[j][0], x.b = sp.gb[j][1];
     return x;
 }
 
 // One token: S <- g S + u (x) k*, u = b (v - g S k); returns y = S q~ for the
 // lane's 2 rows (complete in every lane of the row group).
-__device__ __forceinline__ void fwd_step(State &s, const Tok &x, float (&yr)[2], float (&yi)[2]) {
-    float pkr[2], pki[2], pqr[2], pqi[2];
+__device__ __forceinline__ void fwd_step(State &s, const Tok &x, float (&yr)[RPL], float (&yi)[RPL]) {
+    float pkr[RPL], pki[RPL], pqr[RPL], pqi[RPL];
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
+    for (int rr = 0; rr < RPL; ++rr) {
         float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -105,7 +169,7 @@ __device__ __forceinline__ void fwd_step(State &s, const Tok &x, float (&yr)[2],
     }
     cr = row16_sum(cr), ci = row16_sum(ci);
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
+    for (int rr = 0; rr < RPL; ++rr) {
         const float ur = x.b * (x.vr[rr] - x.g * pkr[rr]), ui = x.b * (x.vi[rr] - x.g * pki[rr]);
         yr[rr] = x.g * pqr[rr] + ur * cr - ui * ci;
         yi[rr] = x.g * pqi[rr] + ur * ci + ui * cr;
@@ -121,59 +185,90 @@ __device__ __forceinline__ void fwd_step(State &s, const Tok &x, float (&yr)[2],
 
 __device__ __forceinline__ int chain_groups(int T) { return (T + GROUP - 1) / GROUP; }
 
-// per-thread 16 floats of state at [chain][slot][tid], float4-coalesced
-__device__ __forceinline__ void store_state(float *base, const State &s, int tid) {
-    floatx4 *p = reinterpret_cast<floatx4 *>(base) + 4 * tid;
-    p[0] = floatx4{s.r[0][0], s.r[0][1], s.r[0][2], s.r[0][3]};
-    p[1] = floatx4{s.i[0][0], s.i[0][1], s.i[0][2], s.i[0][3]};
-    p[2] = floatx4{s.r[1][0], s.r[1][1], s.r[1][2], s.r[1][3]};
-    p[3] = floatx4{s.i[1][0], s.i[1][1], s.i[1][2], s.i[1][3]};
+// a thread's 8 RPL floats of state at [chain][checkpoint][slot], float4-coalesced
+__device__ __forceinline__ void store_state(float *base, const State &s, int slot) {
+    floatx4 *p = reinterpret_cast<floatx4 *>(base) + 2 * RPL * slot;
+#pragma unroll
+    for (int rr = 0; rr < RPL; ++rr) {
+        p[2 * rr] = floatx4{s.r[rr][0], s.r[rr][1], s.r[rr][2], s.r[rr][3]};
+        p[2 * rr + 1] = floatx4{s.i[rr][0], s.i[rr][1], s.i[rr][2], s.i[rr][3]};
+    }
 }
-__device__ __forceinline__ void load_state(const float *base, State &s, int tid) {
-    const floatx4 *p = reinterpret_cast<const floatx4 *>(base) + 4 * tid;
-    const floatx4 a = p[0], b = p[1], c = p[2], d = p[3];
-    s.r[0][0] = a.x, s.r[0][1] = a.y, s.r[0][2] = a.z, s.r[0][3] = a.w;
-    s.i[0][0] = b.x, s.i[0][1] = b.y, s.i[0][2] = b.z, s.i[0][3] = b.w;
-    s.r[1][0] = c.x, s.r[1][1] = c.y, s.r[1][2] = c.z, s.r[1][3] = c.w;
-    s.i[1][0] = d.x, s.i[1][1] = d.y, s.i[1][2] = d.z, s.i[1][3] = d.w;
+__device__ __forceinline__ void load_state(const float *base, State &s, int slot) {
+    const floatx4 *p = reinterpret_cast<const floatx4 *>(base) + 2 * RPL * slot;
+#pragma unroll
+    for (int rr = 0; rr < RPL; ++rr) {
+        const floatx4 a = p[2 * rr], b = p[2 * rr + 1];
+        s.r[rr][0] = a.x, s.r[rr][1] = a.y, s.r[rr][2] = a.z, s.r[rr][3] = a.w;
+        s.i[rr][0] = b.x, s.i[rr][1] = b.y, s.i[rr][2] = b.z, s.i[rr][3] = b.w;
+    }
+}
+
+__device__ __forceinline__ void init_state(State &s, const float *re, const float *im, int64_t chain, const Lane &L) {
+#pragma unroll
+    for (int rr = 0; rr < RPL; ++rr) {
+        if (re) {
+            const int64_t o = chain * D * D + (L.r0 + rr) * D + 4 * L.cg;
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(re + o), b = *reinterpret_cast<const floatx4 *>(im + o);
+            s.r[rr][0] = a.x, s.r[rr][1] = a.y, s.r[rr][2] = a.z, s.r[rr][3] = a.w;
+            s.i[rr][0] = b.x, s.i[rr][1] = b.y, s.i[rr][2] = b.z, s.i[rr][3] = b.w;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) s.r[rr][c] = 0.f, s.i[rr][c] = 0.f;
+        }
+    }
+}
+
+__device__ __forceinline__ void write_state(float *re, float *im, const State &s, int64_t chain, const Lane &L) {
+#pragma unroll
+    for (int rr = 0; rr < RPL; ++rr) {
+        const int64_t o = chain * D * D + (L.r0 + rr) * D + 4 * L.cg;
+        *reinterpret_cast<floatx4 *>(re + o) = floatx4{s.r[rr][0], s.r[rr][1], s.r[rr][2], s.r[rr][3]};
+        *reinterpret_cast<floatx4 *>(im + o) = floatx4{s.i[rr][0], s.i[rr][1], s.i[rr][2], s.i[rr][3]};
+    }
 }
 constexpr int STATE_FLOATS = 2 * D * D;   // one chain's state, thread-private layout
 
-__global__ void __launch_bounds__(DTHREADS) delta_fwd_kernel(qpam_delta_args a) {
-    const int chain = blockIdx.x, b = chain / a.H, h = chain - b * a.H, tid = threadIdx.x;
-    const Lane L(tid);
+// backward workspace: sub-group states [chain][SUBS][state], then the parts' partial sums
+__host__ __device__ __forceinline__ size_t bwd_sub_bytes(const qpam_delta_args &a) {
+    return (size_t)a.B * a.H * SUBS * STATE_FLOATS * sizeof(float);
+}
+
+constexpr int FNT = 8;   // tokens per forward span
+
+__global__ void __launch_bounds__(64) delta_fwd_kernel(qpam_delta_args a) {
+    __shared__ Span<FNT, 4 * RPL> sp[2];
+    const int chain = blockIdx.x / NW, b = chain / a.H, h = chain - b * a.H, tid = threadIdx.x;
+    const Lane L(blockIdx.x - chain * NW, tid);
     State s;
+    init_state(s, a.s0_re, a.s0_im, chain, L);
+    float *ckpt = static_cast<float *>(a.workspace);
+    if (ckpt) ckpt += (int64_t)chain * chain_groups(a.T) * STATE_FLOATS;
+    const int row0 = 4 * RPL * L.w;   // the wave's first row
+    SpanRegs<FNT, 4 * RPL, 64> regs;
+    regs.fetch(a, b, h, 0, row0, tid);
+    regs.commit(sp[0], tid);
+    __syncthreads();
+    for (int t0 = 0, buf = 0; t0 < a.T; t0 += FNT, buf ^= 1) {
+        const bool more = t0 + FNT < a.T;
+        if (more) regs.fetch(a, b, h, t0 + FNT, row0, tid);
+        const int n = min(FNT, a.T - t0);
+        for (int j = 0; j < n; ++j) {
+            const int t = t0 + j;
+            if (t % GROUP == 0 && ckpt) store_state(ckpt + (int64_t)(t / GROUP) * STATE_FLOATS, s, L.slot());
+            const Tok x = span_tok(sp[buf], j, L.cg, L.rg * RPL);
+            float yr[RPL], yi[RPL];
+            fwd_step(s, x, yr, yi);
+            if (L.cg == 0) {
+                const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)t * a.y.s2 + L.r0;
 #pragma unroll
-    for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            if (a.s0_re) {
-                const int64_t o = (int64_t)chain * D * D + (L.r0 + rr) * D + 4 * L.cg + c;
-                s.r[rr][c] = a.s0_re[o], s.i[rr][c] = a.s0_im[o];
-            } else {
-                s.r[rr][c] = 0.f, s.i[rr][c] = 0.f;
+                for (int rr = 0; rr < RPL; ++rr) a.y.re[yo + rr] = yr[rr], a.y.im[yo + rr] = yi[rr];
             }
         }
-    float *ckpt = static_cast<float *>(a.workspace) + (int64_t)chain * chain_groups(a.T) * STATE_FLOATS;
-    Tok cur = load_tok(a, b, h, 0, L);
-    for (int t = 0; t < a.T; ++t) {
-        const Tok nxt = load_tok(a, b, h, min(t + 1, a.T - 1), L);
-        if (t % GROUP == 0 && ckpt) store_state(ckpt + (int64_t)(t / GROUP) * STATE_FLOATS, s, tid);
-        float yr[2], yi[2];
-        fwd_step(s, cur, yr, yi);
-        if (L.cg == 0) {
-            const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)t * a.y.s2 + L.r0;
-            *reinterpret_cast<floatx2 *>(a.y.re + yo) = floatx2{yr[0], yr[1]};
-            *reinterpret_cast<floatx2 *>(a.y.im + yo) = floatx2{yi[0], yi[1]};
-        }
-        cur = nxt;
+        if (more) regs.commit(sp[buf ^ 1], tid);
+        __syncthreads();
     }
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr) {
-        const int64_t o = (int64_t)chain * D * D + (L.r0 + rr) * D + 4 * L.cg;
-        *reinterpret_cast<floatx4 *>(a.s_re + o) = floatx4{s.r[rr][0], s.r[rr][1], s.r[rr][2], s.r[rr][3]};
-        *reinterpret_cast<floatx4 *>(a.s_im + o) = floatx4{s.i[rr][0], s.i[rr][1], s.i[rr][2], s.i[rr][3]};
-    }
+    write_state(a.s_re, a.s_im, s, chain, L);
 }
 
 // sum over the 4 row groups of a wave (lanes cg, cg+16, cg+32, cg+48)
@@ -182,173 +277,219 @@ __device__ __forceinline__ float rows4_sum(float x) {
     return x + __shfl_xor(x, 32);
 }
 
-__global__ void __launch_bounds__(DTHREADS) delta_bwd_kernel(qpam_delta_bwd_args g, qpam_delta_args a) {
-    // per sub-group: [token][wave][column][dq re, dq im, dk re, dk im] and
-    // [token][wave * 4 + row group][dgamma, dbeta]
-    __shared__ floatx4 red[SUB][8][D];
-    __shared__ floatx2 sred[SUB][32];
-    const int chain = blockIdx.x, b = chain / a.H, h = chain - b * a.H, tid = threadIdx.x;
-    const Lane L(tid);
+// Per-workgroup partial sums over its rows, [part][chain][t]: (dq~ re, dq~ im,
+// dk re, dk im) per column and (dgamma, dbeta); summed over the parts in a
+// fixed order by delta_reduce_kernel.
+__global__ void __launch_bounds__(BWD_THREADS) delta_bwd_kernel(qpam_delta_bwd_args g, qpam_delta_args a) {
+    // per flush: [token][wave][column] = (dq~ re, dq~ im, dk re, dk im) and
+    // [token][wave * 4 + row group] = (dgamma, dbeta)
+    __shared__ floatx4 red[FL][PW][D];
+    __shared__ floatx2 sred[FL][4 * PW];
+    __shared__ Span<GROUP, PROWS> sp;          // the group's token inputs for this workgroup's rows
+    __shared__ float sdy[GROUP][2][PROWS];     // and output gradients
+    const int chain = blockIdx.x / PARTS, part = blockIdx.x - chain * PARTS;
+    const int b = chain / a.H, h = chain - b * a.H, tid = threadIdx.x;
+    const Lane L(part * PW + (tid >> 6), tid & 63);
+    const int row0 = part * PROWS;
+    const int64_t nbht = (int64_t)a.B * a.H * a.T;
+    floatx4 *pcol = reinterpret_cast<floatx4 *>(static_cast<char *>(g.workspace) + bwd_sub_bytes(a)) +
+                    ((int64_t)part * a.B * a.H + chain) * a.T * D;
+    floatx2 *pscal = reinterpret_cast<floatx2 *>(reinterpret_cast<floatx4 *>(static_cast<char *>(g.workspace) +
+                                                                             bwd_sub_bytes(a)) + PARTS * nbht * D) +
+                     ((int64_t)part * a.B * a.H + chain) * a.T;
     const int ng = chain_groups(a.T);
     const float *ckpt = static_cast<const float *>(a.workspace) + (int64_t)chain * ng * STATE_FLOATS;
     float *sub = static_cast<float *>(g.workspace) + (int64_t)chain * SUBS * STATE_FLOATS;
 
     State gs;   // adjoint of the state after the current token
-#pragma unroll
-    for (int rr = 0; rr < 2; ++rr)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            if (g.ds_re) {
-                const int64_t o = (int64_t)chain * D * D + (L.r0 + rr) * D + 4 * L.cg + c;
-                gs.r[rr][c] = g.ds_re[o], gs.i[rr][c] = g.ds_im[o];
-            } else {
-                gs.r[rr][c] = 0.f, gs.i[rr][c] = 0.f;
-            }
-        }
+    init_state(gs, g.ds_re, g.ds_im, chain, L);
 
     for (int grp = ng - 1; grp >= 0; --grp) {
         const int t0 = grp * GROUP, tn = min(t0 + GROUP, a.T);
+        {   // stage the group's inputs and output gradients
+            SpanRegs<GROUP, PROWS, BWD_THREADS> regs;
+            regs.fetch(a, b, h, t0, row0, tid);
+            constexpr int NDY = GROUP * 2 * PROWS / BWD_THREADS;
+            float dyv[NDY];
+#pragma unroll
+            for (int k = 0; k < NDY; ++k) {
+                const int i = tid + k * BWD_THREADS, tok = i / (2 * PROWS), rem = i - tok * 2 * PROWS;
+                const int ri = rem / PROWS, r = rem - ri * PROWS;
+                const int t = min(t0 + tok, a.T - 1);
+                dyv[k] = static_cast<const float *>(ri ? g.dy.im : g.dy.re)[b * g.dy.s0 + h * g.dy.s1 +
+                                                                            (int64_t)t * g.dy.s2 + row0 + r];
+            }
+            __syncthreads();   // the previous group's readers are done
+            regs.commit(sp, tid);
+#pragma unroll
+            for (int k = 0; k < NDY; ++k) {
+                const int i = tid + k * BWD_THREADS, tok = i / (2 * PROWS), rem = i - tok * 2 * PROWS;
+                const int ri = rem / PROWS, r = rem - ri * PROWS;
+                sdy[tok][ri][r] = dyv[k];
+            }
+            __syncthreads();
+        }
         // recompute the group, keeping the state before every SUB-th token
         State s;
-        load_state(ckpt + (int64_t)grp * STATE_FLOATS, s, tid);
+        load_state(ckpt + (int64_t)grp * STATE_FLOATS, s, L.slot());
         for (int t = t0; t < tn; ++t) {
-            if ((t - t0) % SUB == 0) store_state(sub + (int64_t)((t - t0) / SUB) * STATE_FLOATS, s, tid);
-            const Tok x = load_tok(a, b, h, t, L);
-            float yr[2], yi[2];
+            if ((t - t0) % SUB == 0) store_state(sub + (int64_t)((t - t0) / SUB) * STATE_FLOATS, s, L.slot());
+            const Tok x = span_tok(sp, t - t0, L.cg, L.r0 - row0);
+            float yr[RPL], yi[RPL];
             fwd_step(s, x, yr, yi);
         }
         for (int sg = (tn - t0 - 1) / SUB; sg >= 0; --sg) {
             const int s0 = t0 + sg * SUB, n = min(SUB, tn - s0);
             // states before each token of the sub-group
             State prev[SUB];
-            load_state(sub + (int64_t)sg * STATE_FLOATS, prev[0], tid);
+            load_state(sub + (int64_t)sg * STATE_FLOATS, prev[0], L.slot());
 #pragma unroll
             for (int j = 1; j < SUB; ++j) {
                 prev[j] = prev[j - 1];
                 if (j < n) {
-                    const Tok x = load_tok(a, b, h, s0 + j - 1, L);
-                    float yr[2], yi[2];
+                    const Tok x = span_tok(sp, s0 + j - 1 - t0, L.cg, L.r0 - row0);
+                    float yr[RPL], yi[RPL];
                     fwd_step(prev[j], x, yr, yi);
                 }
             }
 #pragma unroll
             for (int j = SUB - 1; j >= 0; --j) {
-                if (j >= n) continue;
-                const int t = s0 + j;
-                const Tok x = load_tok(a, b, h, t, L);
-                const int64_t dyo = b * g.dy.s0 + h * g.dy.s1 + (int64_t)t * g.dy.s2 + L.r0;
-                const floatx2 dyr = *reinterpret_cast<const floatx2 *>(static_cast<const float *>(g.dy.re) + dyo);
-                const floatx2 dyi = *reinterpret_cast<const floatx2 *>(static_cast<const float *>(g.dy.im) + dyo);
-                const float gyr[2] = {dyr.x, dyr.y}, gyi[2] = {dyi.x, dyi.y};
-                const State &sp = prev[j];
-                // forward quantities of this token
-                float ar[2][4], ai[2][4], pr[2], pi[2], ur[2], ui[2];
+                if (j < n) {
+                    const int t = s0 + j;
+                    const Tok x = span_tok(sp, t - t0, L.cg, L.r0 - row0);
+                    float gyr[RPL], gyi[RPL];
 #pragma unroll
-                for (int rr = 0; rr < 2; ++rr) {
-                    float p0 = 0.f, p1 = 0.f;
+                    for (int rr = 0; rr < RPL; ++rr)
+                        gyr[rr] = sdy[t - t0][0][L.r0 - row0 + rr], gyi[rr] = sdy[t - t0][1][L.r0 - row0 + rr];
+                    const State &sp = prev[j];
+                    // forward quantities of this token
+                    float ar[RPL][4], ai[RPL][4], pr[RPL], pi[RPL], ur[RPL], ui[RPL];
+#pragma unroll
+                    for (int rr = 0; rr < RPL; ++rr) {
+                        float p0 = 0.f, p1 = 0.f;
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            ar[rr][c] = x.g * sp.r[rr][c], ai[rr][c] = x.g * sp.i[rr][c];
+                            p0 += ar[rr][c] * x.kr[c] - ai[rr][c] * x.ki[c];
+                            p1 += ar[rr][c] * x.ki[c] + ai[rr][c] * x.kr[c];
+                        }
+                        pr[rr] = row16_sum(p0), pi[rr] = row16_sum(p1);
+                        ur[rr] = x.b * (x.vr[rr] - pr[rr]), ui[rr] = x.b * (x.vi[rr] - pi[rr]);
+                    }
+                    float gq[4][2] = {}, gk[4][2] = {};
+                    float ggam = 0.f, gbet = 0.f;
+                    float gur[RPL], gui[RPL];
+#pragma unroll
+                    for (int rr = 0; rr < RPL; ++rr) {
+                        float u0 = 0.f, u1 = 0.f;
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            // s = a + u conj(k) (the state after the token)
+                            const float sr = ar[rr][c] + ur[rr] * x.kr[c] + ui[rr] * x.ki[c];
+                            const float si = ai[rr][c] + ui[rr] * x.kr[c] - ur[rr] * x.ki[c];
+                            // y = s . q~:  g_s += conj(q~) g_y;  g_q~ += conj(s) g_y
+                            gs.r[rr][c] += x.qr[c] * gyr[rr] + x.qi[c] * gyi[rr];
+                            gs.i[rr][c] += x.qr[c] * gyi[rr] - x.qi[c] * gyr[rr];
+                            gq[c][0] += sr * gyr[rr] + si * gyi[rr];
+                            gq[c][1] += sr * gyi[rr] - si * gyr[rr];
+                            // g_u = sum_c k_c g_s_c
+                            u0 += x.kr[c] * gs.r[rr][c] - x.ki[c] * gs.i[rr][c];
+                            u1 += x.kr[c] * gs.i[rr][c] + x.ki[c] * gs.r[rr][c];
+                            // g_k_c += u conj(g_s_c)
+                            gk[c][0] += ur[rr] * gs.r[rr][c] + ui[rr] * gs.i[rr][c];
+                            gk[c][1] += ui[rr] * gs.r[rr][c] - ur[rr] * gs.i[rr][c];
+                        }
+                        gur[rr] = row16_sum(u0), gui[rr] = row16_sum(u1);
+                    }
+#pragma unroll
+                    for (int rr = 0; rr < RPL; ++rr) {
+                        // u = beta (v - p)
+                        gbet += (x.vr[rr] - pr[rr]) * gur[rr] + (x.vi[rr] - pi[rr]) * gui[rr];
+                        const float gpr = -x.b * gur[rr], gpi = -x.b * gui[rr];
+                        float gg = 0.f;
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            // p = sum_c a_c k_c:  g_a += conj(k) g_p;  g_k += conj(a) g_p
+                            const float gar = gs.r[rr][c] + x.kr[c] * gpr + x.ki[c] * gpi;
+                            const float gai = gs.i[rr][c] + x.kr[c] * gpi - x.ki[c] * gpr;
+                            gk[c][0] += ar[rr][c] * gpr + ai[rr][c] * gpi;
+                            gk[c][1] += ar[rr][c] * gpi - ai[rr][c] * gpr;
+                            // a = g~ s_prev:  g_g~ += Re(conj(s_prev) g_a);  g_s_prev = g~ g_a
+                            gg += sp.r[rr][c] * gar + sp.i[rr][c] * gai;
+                            gs.r[rr][c] = x.g * gar;
+                            gs.i[rr][c] = x.g * gai;
+                        }
+                        ggam += gg;
+                    }
+                    if (L.cg == 0) {
+                        const int64_t vo = b * g.dv.s0 + h * g.dv.s1 + (int64_t)t * g.dv.s2 + L.r0;
+#pragma unroll
+                        for (int rr = 0; rr < RPL; ++rr) g.dv.re[vo + rr] = x.b * gur[rr], g.dv.im[vo + rr] = x.b * gui[rr];
+                    }
+                    // column sums over the wave's rows, then one slot per wave
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        ar[rr][c] = x.g * sp.r[rr][c], ai[rr][c] = x.g * sp.i[rr][c];
-                        p0 += ar[rr][c] * x.kr[c] - ai[rr][c] * x.ki[c];
-                        p1 += ar[rr][c] * x.ki[c] + ai[rr][c] * x.kr[c];
+                        gq[c][0] = rows4_sum(gq[c][0]), gq[c][1] = rows4_sum(gq[c][1]);
+                        gk[c][0] = rows4_sum(gk[c][0]), gk[c][1] = rows4_sum(gk[c][1]);
                     }
-                    pr[rr] = row16_sum(p0), pi[rr] = row16_sum(p1);
-                    ur[rr] = x.b * (x.vr[rr] - pr[rr]), ui[rr] = x.b * (x.vi[rr] - pi[rr]);
-                }
-                float gq[4][2] = {}, gk[4][2] = {};
-                float ggam = 0.f, gbet = 0.f;
-                float gur[2], gui[2];
+                    if (L.rg == 0) {
 #pragma unroll
-                for (int rr = 0; rr < 2; ++rr) {
-                    float u0 = 0.f, u1 = 0.f;
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        // s = a + u conj(k) (the state after the token)
-                        const float sr = ar[rr][c] + ur[rr] * x.kr[c] + ui[rr] * x.ki[c];
-                        const float si = ai[rr][c] + ui[rr] * x.kr[c] - ur[rr] * x.ki[c];
-                        // y = s . q~:  g_s += conj(q~) g_y;  g_q~ += conj(s) g_y
-                        gs.r[rr][c] += x.qr[c] * gyr[rr] + x.qi[c] * gyi[rr];
-                        gs.i[rr][c] += x.qr[c] * gyi[rr] - x.qi[c] * gyr[rr];
-                        gq[c][0] += sr * gyr[rr] + si * gyi[rr];
-                        gq[c][1] += sr * gyi[rr] - si * gyr[rr];
-                        // g_u = sum_c k_c g_s_c
-                        u0 += x.kr[c] * gs.r[rr][c] - x.ki[c] * gs.i[rr][c];
-                        u1 += x.kr[c] * gs.i[rr][c] + x.ki[c] * gs.r[rr][c];
-                        // g_k_c += u conj(g_s_c)
-                        gk[c][0] += ur[rr] * gs.r[rr][c] + ui[rr] * gs.i[rr][c];
-                        gk[c][1] += ui[rr] * gs.r[rr][c] - ur[rr] * gs.i[rr][c];
+                        for (int c = 0; c < 4; ++c)
+                            red[j % FL][L.w - part * PW][4 * L.cg + c] = floatx4{gq[c][0], gq[c][1], gk[c][0], gk[c][1]};
                     }
-                    gur[rr] = row16_sum(u0), gui[rr] = row16_sum(u1);
+                    // ggam holds this lane's columns; gbet is already the row group's value
+                    ggam = row16_sum(ggam);
+                    if (L.cg == 0) sred[j % FL][4 * (L.w - part * PW) + L.rg] = floatx2{ggam, gbet};
                 }
+                if (j % FL == 0) {
+                    __syncthreads();
+                    // tokens j .. j + FL - 1 of the sub-group: reduce the wave slots in a fixed order
+                    const int m = min(FL, n - j);
+                    for (int i = tid; i < m * D; i += BWD_THREADS) {
+                        const int jj = i / D, c = i - jj * D, t = s0 + j + jj;
+                        floatx4 acc = red[jj][0][c];
 #pragma unroll
-                for (int rr = 0; rr < 2; ++rr) {
-                    // u = beta (v - p)
-                    gbet += (x.vr[rr] - pr[rr]) * gur[rr] + (x.vi[rr] - pi[rr]) * gui[rr];
-                    const float gpr = -x.b * gur[rr], gpi = -x.b * gui[rr];
-                    float gg = 0.f;
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        // p = sum_c a_c k_c:  g_a += conj(k) g_p;  g_k += conj(a) g_p
-                        const float gar = gs.r[rr][c] + x.kr[c] * gpr + x.ki[c] * gpi;
-                        const float gai = gs.i[rr][c] + x.kr[c] * gpi - x.ki[c] * gpr;
-                        gk[c][0] += ar[rr][c] * gpr + ai[rr][c] * gpi;
-                        gk[c][1] += ar[rr][c] * gpi - ai[rr][c] * gpr;
-                        // a = g~ s_prev:  g_g~ += Re(conj(s_prev) g_a);  g_s_prev = g~ g_a
-                        gg += sp.r[rr][c] * gar + sp.i[rr][c] * gai;
-                        gs.r[rr][c] = x.g * gar;
-                        gs.i[rr][c] = x.g * gai;
+                        for (int w = 1; w < PW; ++w) acc += red[jj][w][c];
+                        pcol[(int64_t)t * D + c] = acc;
                     }
-                    ggam += gg;
+                    if (tid < m) {
+                        floatx2 acc = sred[tid][0];
+                        for (int k = 1; k < 4 * PW; ++k) acc += sred[tid][k];
+                        pscal[s0 + j + tid] = acc;
+                    }
+                    __syncthreads();
                 }
-                if (L.cg == 0) {
-                    const int64_t vo = b * g.dv.s0 + h * g.dv.s1 + (int64_t)t * g.dv.s2 + L.r0;
-                    *reinterpret_cast<floatx2 *>(g.dv.re + vo) = floatx2{x.b * gur[0], x.b * gur[1]};
-                    *reinterpret_cast<floatx2 *>(g.dv.im + vo) = floatx2{x.b * gui[0], x.b * gui[1]};
-                }
-                // column sums over the wave's 8 rows, then one slot per wave
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    gq[c][0] = rows4_sum(gq[c][0]), gq[c][1] = rows4_sum(gq[c][1]);
-                    gk[c][0] = rows4_sum(gk[c][0]), gk[c][1] = rows4_sum(gk[c][1]);
-                }
-                if (L.rg == 0) {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c)
-                        red[j][L.w][4 * L.cg + c] = floatx4{gq[c][0], gq[c][1], gk[c][0], gk[c][1]};
-                }
-                // ggam holds this lane's columns; gbet is already the row group's value
-                ggam = row16_sum(ggam);
-                if (L.cg == 0) sred[j][4 * L.w + L.rg] = floatx2{ggam, gbet};
             }
-            __syncthreads();
-            // reduce the 8 wave slots of each (token, column) in a fixed order
-            for (int i = tid; i < n * D; i += DTHREADS) {
-                const int j = i / D, c = i - j * D, t = s0 + j;
-                floatx4 acc = red[j][0][c];
-#pragma unroll
-                for (int w = 1; w < 8; ++w) acc += red[j][w][c];
-                const int64_t qo = b * g.dq.s0 + h * g.dq.s1 + (int64_t)t * g.dq.s2 + c;
-                const int64_t ko = b * g.dk.s0 + h * g.dk.s1 + (int64_t)t * g.dk.s2 + c;
-                g.dq.re[qo] = acc.x * a.q_scale, g.dq.im[qo] = acc.y * a.q_scale;
-                g.dk.re[ko] = acc.z, g.dk.im[ko] = acc.w;
-            }
-            if (tid < n) {
-                floatx2 acc = sred[tid][0];
-                for (int k = 1; k < 32; ++k) acc += sred[tid][k];
-                const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)(s0 + tid) * a.sg_t;
-                g.dgamma[go] = acc.x;
-                g.dbeta[go] = acc.y;
-            }
-            __syncthreads();
         }
     }
-    if (g.ds0_re) {
+    if (g.ds0_re) write_state(g.ds0_re, g.ds0_im, gs, chain, L);
+}
+
+// dq = q_scale * sum of the parts' dq~, dk, dgamma, dbeta: one thread per (chain, t, column)
+__global__ void __launch_bounds__(256) delta_reduce_kernel(qpam_delta_bwd_args g, qpam_delta_args a) {
+    const int64_t nbht = (int64_t)a.B * a.H * a.T;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nbht * D) return;
+    const int64_t ct = i / D;
+    const int c = (int)(i - ct * D);
+    const int chain = (int)(ct / a.T), t = (int)(ct - (int64_t)chain * a.T);
+    const int b = chain / a.H, h = chain - b * a.H;
+    const floatx4 *pcol = reinterpret_cast<const floatx4 *>(static_cast<const char *>(g.workspace) + bwd_sub_bytes(a));
+    floatx4 acc = pcol[i];
 #pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-            const int64_t o = (int64_t)chain * D * D + (L.r0 + rr) * D + 4 * L.cg;
-            *reinterpret_cast<floatx4 *>(g.ds0_re + o) = floatx4{gs.r[rr][0], gs.r[rr][1], gs.r[rr][2], gs.r[rr][3]};
-            *reinterpret_cast<floatx4 *>(g.ds0_im + o) = floatx4{gs.i[rr][0], gs.i[rr][1], gs.i[rr][2], gs.i[rr][3]};
-        }
+    for (int p = 1; p < PARTS; ++p) acc += pcol[p * nbht * D + i];
+    const int64_t qo = b * g.dq.s0 + h * g.dq.s1 + (int64_t)t * g.dq.s2 + c;
+    const int64_t ko = b * g.dk.s0 + h * g.dk.s1 + (int64_t)t * g.dk.s2 + c;
+    g.dq.re[qo] = acc.x * a.q_scale, g.dq.im[qo] = acc.y * a.q_scale;
+    g.dk.re[ko] = acc.z, g.dk.im[ko] = acc.w;
+    if (c == 0) {
+        const floatx2 *pscal = reinterpret_cast<const floatx2 *>(pcol + PARTS * nbht * D);
+        floatx2 sacc = pscal[ct];
+#pragma unroll
+        for (int p = 1; p < PARTS; ++p) sacc += pscal[p * nbht + ct];
+        const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)t * a.sg_t;
+        g.dgamma[go] = sacc.x;
+        g.dbeta[go] = sacc.y;
     }
 }
 
@@ -364,7 +505,10 @@ bool mview_ok(const qpam_mview &v) {
 size_t fwd_ws(const qpam_delta_args &a) {
     return (size_t)a.B * a.H * ((a.T + GROUP - 1) / GROUP) * STATE_FLOATS * sizeof(float);
 }
-size_t bwd_ws(const qpam_delta_args &a) { return (size_t)a.B * a.H * SUBS * STATE_FLOATS * sizeof(float); }
+size_t bwd_ws(const qpam_delta_args &a) {
+    const size_t nbht = (size_t)a.B * a.H * a.T;
+    return bwd_sub_bytes(a) + PARTS * nbht * (D * sizeof(floatx4) + sizeof(floatx2));
+}
 
 int validate(const qpam_delta_args *a) {
     QPAM_REQUIRE(a != nullptr, "qpam_delta: null arguments");
@@ -395,7 +539,7 @@ extern "C" int qpam_delta_fwd(const qpam_delta_args *a, void *stream) {
                  "qpam_delta_fwd: workspace of %zu bytes needed (or NULL without a backward)", fwd_ws(*a));
     if (a->B == 0) return QPAM_OK;
     QPAM_REQUIRE(a->T >= 1, "qpam_delta_fwd: T must be >= 1");
-    hipLaunchKernelGGL(delta_fwd_kernel, dim3(a->B * a->H), dim3(DTHREADS), 0, static_cast<hipStream_t>(stream), *a);
+    hipLaunchKernelGGL(delta_fwd_kernel, dim3(a->B * a->H * NW), dim3(64), 0, static_cast<hipStream_t>(stream), *a);
     return launch_status("delta_fwd_kernel");
 }
 
@@ -418,6 +562,11 @@ extern "C" int qpam_delta_bwd(const qpam_delta_bwd_args *g, void *stream) {
     QPAM_REQUIRE((g->ds_re == nullptr) == (g->ds_im == nullptr) && (g->ds0_re == nullptr) == (g->ds0_im == nullptr),
                  "qpam_delta_bwd: ds / ds0 need both planes");
     if (a.B == 0 || a.T == 0) return QPAM_OK;
-    hipLaunchKernelGGL(delta_bwd_kernel, dim3(a.B * a.H), dim3(DTHREADS), 0, static_cast<hipStream_t>(stream), *g, a);
-    return launch_status("delta_bwd_kernel");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(delta_bwd_kernel, dim3(a.B * a.H * PARTS), dim3(BWD_THREADS), 0, s, *g, a);
+    st = launch_status("delta_bwd_kernel");
+    if (st) return st;
+    const int64_t n = (int64_t)a.B * a.H * a.T * D;
+    hipLaunchKernelGGL(delta_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, *g, a);
+    return launch_status("delta_reduce_kernel");
 }

@@ -45,6 +45,44 @@ int get_handle(int dev, hipblasLtHandle_t &h) {
     return QPAM_OK;
 }
 
+// QPAM_BLAS_TUNE=1: on the first call of each shape, time up to 16 of the
+// heuristic's candidates on the stream (a one-time host synchronisation) and
+// keep the fastest; otherwise the heuristic's first choice, with no sync.
+bool tune_enabled() {
+    const char *e = std::getenv("QPAM_BLAS_TUNE");
+    return e && e[0] == '1';
+}
+
+int pick_fastest(hipblasLtHandle_t h, Plan &p, const hipblasLtMatmulHeuristicResult_t *res, int count, const void *A,
+                 const void *B, float beta, void *C, void *ws, size_t ws_bytes, hipStream_t stream) {
+    hipEvent_t e0, e1;
+    QPAM_CHECK_HIP(hipEventCreate(&e0));
+    QPAM_CHECK_HIP(hipEventCreate(&e1));
+    float best = 1e30f;
+    int best_i = 0;
+    const float alpha = 1.f;
+    for (int i = 0; i < count; ++i) {
+        if (res[i].workspaceSize > ws_bytes) continue;
+        float ms = 0.f;
+        bool ok = true;
+        for (int rep = 0; rep < 2 && ok; ++rep) {   // first run warms up, second is timed
+            hipEventRecord(e0, stream);
+            ok = hipblasLtMatmul(h, p.desc, &alpha, A, p.la, B, p.lb, &beta, C, p.lc, C, p.lc, &res[i].algo, ws,
+                                 ws_bytes, stream) == HIPBLAS_STATUS_SUCCESS;
+            hipEventRecord(e1, stream);
+        }
+        if (!ok) continue;
+        hipEventSynchronize(e1);
+        hipEventElapsedTime(&ms, e0, e1);
+        if (ms < best) best = ms, best_i = i;
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    p.algo = res[best_i].algo;
+    p.ws = res[best_i].workspaceSize;
+    return QPAM_OK;
+}
+
 }  // namespace
 
 bool enabled() {
@@ -78,15 +116,24 @@ int gemm_bf16(bool ta, bool tb, int m, int n, int k, const void *A, int64_t lda,
         const uint64_t wsb = ws_bytes;
         QPAM_CHECK_LT(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
                                                             sizeof(wsb)));
-        hipblasLtMatmulHeuristicResult_t res[1];
+        const bool tune = tune_enabled();
+        hipblasLtMatmulHeuristicResult_t res[16];
         int count = 0;
         const hipblasStatus_t hs =
-            hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, 1, res, &count);
+            hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, tune ? 16 : 1, res, &count);
         hipblasLtMatmulPreferenceDestroy(pref);
         if (hs != HIPBLAS_STATUS_SUCCESS || count < 1)
             return fail(QPAM_ERR_UNSUPPORTED, "hipBLASLt: no algorithm for %dx%dx%d (status %d)", m, n, k, (int)hs);
         p.algo = res[0].algo;
         p.ws = res[0].workspaceSize;
+        if (tune && count > 1) {
+            // the candidates write C: tune on a beta = 0 copy of the problem only when C is
+            // not accumulated into (beta != 0 would double-count), else keep the first choice
+            if (beta == 0.f) {
+                st = pick_fastest(h, p, res, count, A, B, beta, C, ws, ws_bytes, stream);
+                if (st) return st;
+            }
+        }
         it = g_plans.emplace(key, p).first;
     }
     const Plan &p = it->second;

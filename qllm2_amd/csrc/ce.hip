@@ -1066,11 +1066,18 @@ __global__ void __launch_bounds__(WTHREADS) grad_tile_kernel(BwdParams p) {
     const int wm = w >> 1, wn = w & 1;
     U16 *G = (U16 *)p.gbuf;
     U16 *GT = (U16 *)p.gtbuf;
+    // G^T rows (one per vocab entry) hold the tile's rows contiguously: each
+    // 16-wide vocab slab of a wave's 64 x 128 tile goes through LDS so that it
+    // leaves as 128-byte runs (the accumulator layout alone would write 32-byte
+    // pieces).
+    constexpr int GT_LD = 72;   // bf16 per staged vocab row: 64 tile rows + padding against bank conflicts
+    __shared__ __align__(16) U16 sEpi[8 * 16 * GT_LD];
+    U16 *tw = sEpi + w * 16 * GT_LD;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
+    for (int ni = 0; ni < 8; ++ni) {
+        const int vb = v0 + 128 * wn + 16 * ni, v = vb + l16;
 #pragma unroll
-        for (int ni = 0; ni < 8; ++ni) {
-            const int v = v0 + 128 * wn + 16 * ni + l16;
+        for (int mi = 0; mi < 4; ++mi) {
             const int rl0 = 64 * wm + 16 * mi + 4 * g;
             float x[4];
 #pragma unroll
@@ -1091,8 +1098,18 @@ __global__ void __launch_bounds__(WTHREADS) grad_tile_kernel(BwdParams p) {
                 for (int r = 0; r < 4; ++r)
                     if (lr0 + rl0 + r < p.rows) G[(int64_t)(lr0 + rl0 + r) * p.Vp + v] = gb[r];
             }
-            *reinterpret_cast<uint2 *>(GT + (int64_t)v * p.Rp + lr0 + rl0) = make_uint2(lo, hi);
+            *reinterpret_cast<uint2 *>(tw + l16 * GT_LD + 16 * mi + 4 * g) = make_uint2(lo, hi);
         }
+        __syncthreads();
+        {   // lane -> (vocab row lane / 4, 16 tile rows (lane % 4) * 16 ..): 32 bytes each
+            const int vl = lane >> 2, part = lane & 3;
+            const uint4 *src = reinterpret_cast<const uint4 *>(tw + vl * GT_LD + 16 * part);
+            const uint4 d0 = src[0], d1 = src[1];
+            uint4 *dst = reinterpret_cast<uint4 *>(GT + (int64_t)(vb + vl) * p.Rp + lr0 + 64 * wm + 16 * part);
+            dst[0] = d0;
+            dst[1] = d1;
+        }
+        __syncthreads();
     }
 }
 }  // namespace wide

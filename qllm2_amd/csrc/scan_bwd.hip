@@ -835,10 +835,11 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
 // unscaled; q_scale is applied where q~ enters an fp32 result.
 using U16 = unsigned short;
 
-// Gradient-state pass (reverse): one block of PASS_THREADS (8 waves) per (state m,
-// b, h) walks the chunks from last to first with the running dS in registers
-// (fp32, accumulator layout; wave w owns value rows 16(w & 3).. and key-column
-// tiles 2(w >> 2), 2(w >> 2) + 1).  Per chunk: bf16 snapshot of dS after the
+// Gradient-state pass (reverse): PASS_SPLIT blocks of PASS_THREADS (4 waves) per
+// (state m, b, h) walk the chunks from last to first with the running dS in
+// registers (fp32, accumulator layout; block `half` owns value rows 32 half.. (dY
+// columns 32 half..), its wave w the rows 16 it.., it = 2 half + (w & 1), and
+// key-column tiles 2(w >> 1), 2(w >> 1) + 1).  Per chunk: bf16 snapshot of dS after the
 // chunk, then dS <- total dS + sum_t conj(rho_m[t]) q_scale dY_t (x) conj(q_t) on
 // MFMA.  dS0 is written when requested.  Chunk c-2's Q and gamma / rotation and
 // chunk c-1's dY (fp32; one register set) are loaded while chunk c is processed.
@@ -847,23 +848,26 @@ using U16 = unsigned short;
 // operands come straight from LDS.  Rows past the end of the sequence re-read its
 // last row: their weights are zero.
 constexpr size_t gpass_bf16_smem() {
-    return (size_t)2 * 2 * PLANE_B * 2     // Q [buf][plane][64][PB]
-           + (size_t)2 * 2 * PLANE_B * 2;  // weighted dY (bf16) [buf][plane][64][PB]
+    return (size_t)2 * PLANE_B * 2     // Q [plane][64][PB]
+           + (size_t)2 * PLANE_B * 2;  // weighted dY (bf16) [plane][64][PB] (this block's columns)
 }
 
-__global__ void __launch_bounds__(PASS_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(PASS_THREADS) __attribute__((amdgpu_waves_per_eu(3)))
 grad_pass_bf16_kernel(BwdParams p) {
     constexpr int NT = PASS_THREADS;
     extern __shared__ float smem[];
-    U16 *sQ = reinterpret_cast<U16 *>(smem);  // + (buf * 2 + plane) * PLANE_B
-    U16 *sG = sQ + 4 * PLANE_B;               // + (buf * 2 + plane) * PLANE_B
+    U16 *sQ = reinterpret_cast<U16 *>(smem);  // + plane * PLANE_B
+    U16 *sG = sQ + 2 * PLANE_B;               // + plane * PLANE_B
 
     const qpam_scan_args &a = p.a;
-    const int chain = blockIdx.x;
+    // the halves of a chain are n_chains blocks apart (same XCD when 8 | B H)
+    const int n_chains = a.M * a.B * a.H;
+    const int chain = blockIdx.x % n_chains, half = blockIdx.x / n_chains;
     const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int it = w & 3, jh = w >> 2;
+    const int it = 2 * half + (w & 1), jh = w >> 1;
+    const int yc0 = 32 * half;  // dY columns of this block's value rows
     const int n = p.n_chunks;
     const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
     const float *rbr = a.rot_re ? a.rot_re + m * a.sr_m + b * a.sr_b + h * a.sr_h : nullptr;
@@ -895,12 +899,12 @@ grad_pass_bf16_kernel(BwdParams p) {
         float gam, rr, ri;
     };
     ChunkRegs cr0, cr1;
-    F32TileRegs<NT> yr, yi;  // dY of the next chunk (one set: fp32 tiles are twice the size)
+    F32TileRegs<NT, 32> yr, yi;  // this block's dY columns of the next chunk (one set)
     auto load_dy = [&](int c) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
         const int64_t yo = (int64_t)c0 * p.dy.s2;
-        tile_load_f32<NT>(yr, yre + yo, p.dy.s2, valid);
-        tile_load_f32<NT>(yi, yim + yo, p.dy.s2, valid);
+        tile_load_f32<NT, 32>(yr, yre + yo, p.dy.s2, valid, yc0);
+        tile_load_f32<NT, 32>(yi, yim + yo, p.dy.s2, valid, yc0);
     };
     auto load_chunk = [&](int c, ChunkRegs &x) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
@@ -912,7 +916,12 @@ grad_pass_bf16_kernel(BwdParams p) {
         x.rr = rsrc_r[t * rst_r];
         x.ri = rsrc_i[t * rst_i];
     };
-    auto stage_chunk = [&](int c, int buf, const ChunkRegs &x) {
+    auto stage_chunk = [&](int c, const ChunkRegs &x) {
+        // nothing of the staging moves above this point: its first use of the staged
+        // register set is where the compiler waits for that set's loads, and the
+        // memory counter completes in order, so a use hoisted to the top of the step
+        // would also wait for everything loaded one step earlier
+        __builtin_amdgcn_sched_barrier(0);
         // conj(rho[t]) q_scale = conj(r[t]) cum[t] q_scale, lane t
         const int valid = min(64, a.T - c * 64);
         float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
@@ -922,16 +931,17 @@ grad_pass_bf16_kernel(BwdParams p) {
             if (lane >= off) L += y;
         }
         const float cum = (lane < valid) ? __expf(L) * a.q_scale : 0.f;
-        tile_store_bf<NT>(sQ + (buf * 2) * PLANE_B, x.qr);
-        tile_store_bf<NT>(sQ + (buf * 2 + 1) * PLANE_B, x.qi);
-        tile_store_f32_cmul_as_bf<NT>(sG + (buf * 2) * PLANE_B, sG + (buf * 2 + 1) * PLANE_B, yr, yi,
-                                      (rbr ? x.rr : 1.f) * cum, -(rbi ? x.ri : 0.f) * cum);
+        tile_store_bf<NT>(sQ, x.qr);
+        tile_store_bf<NT>(sQ + PLANE_B, x.qi);
+        tile_store_f32_cmul_as_bf<NT, 32>(sG, sG + PLANE_B, yr, yi,
+                                          (rbr ? x.rr : 1.f) * cum, -(rbi ? x.ri : 0.f) * cum, yc0);
     };
 
-    // reverse order: step k handles chunk c = n-1-k with LDS buffer k & 1; chunk
-    // c - 2 is loaded into register set k & 1 and staged at the end of step k + 1
+    // reverse order: step k handles chunk c = n-1-k; chunk c - 2 is loaded into
+    // register set k & 1 and staged at the end of step k + 1 (one LDS buffer, staged
+    // between two barriers)
     auto step = [&](int k, ChunkRegs &mine, ChunkRegs &next) {
-        const int c = n - 1 - k, buf = k & 1;
+        const int c = n - 1 - k;
         // unconditional (chunk 0 is re-read near the end): the same memory operation
         // count on every path keeps the compiler's waits for the staged set exact.
         // dY first: the stage at the end of this step waits for it, and the memory
@@ -949,8 +959,8 @@ grad_pass_bf16_kernel(BwdParams p) {
             floatx4 accR[2], accI[2];
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
-            const U16 *Qr = sQ + (buf * 2) * PLANE_B, *Qi = sQ + (buf * 2 + 1) * PLANE_B;
-            const U16 *Gr = sG + (buf * 2) * PLANE_B, *Gi = sG + (buf * 2 + 1) * PLANE_B;
+            const U16 *Qr = sQ, *Qi = sQ + PLANE_B;
+            const U16 *Gr = sG, *Gi = sG + PLANE_B;
 #pragma unroll
             for (int kp = 0; kp < 2; ++kp) {
                 const int t0 = 32 * kp + 8 * g;
@@ -976,14 +986,15 @@ grad_pass_bf16_kernel(BwdParams p) {
                 }
         }
         // also unconditional: past the end, chunk 0 (which `next` and the dY registers
-        // then hold) is staged again into the unused buffer
-        stage_chunk(max(c - 1, 0), buf ^ 1, next);
+        // then hold) is staged again
+        __syncthreads();
+        stage_chunk(max(c - 1, 0), next);
         __syncthreads();
     };
     load_chunk(n - 1, cr0);
     load_dy(n - 1);
     load_chunk(max(n - 2, 0), cr1);
-    stage_chunk(n - 1, 0, cr0);
+    stage_chunk(n - 1, cr0);
     __syncthreads();
     // pairs of steps without conditions inside the loop, odd tail after it
     int k = 0;
@@ -1646,7 +1657,8 @@ int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
     int st = fork_join(
         stream,
         [&](hipStream_t s) {
-            hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(PASS_THREADS), s1, s, p);
+            hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(PASS_SPLIT * a.M * a.B * a.H), dim3(PASS_THREADS), s1, s,
+                               p);
             return launch_status("grad_pass_bf16_kernel");
         },
         [&](hipStream_t s) {

@@ -230,73 +230,81 @@ __device__ __forceinline__ void acc_store_bf_pairs(unsigned short *dre, unsigned
     }
 }
 
-// State passes: blocks of PASS_THREADS threads (8 waves) walk the chunks of one
-// state; 64 x 64 chunk tiles travel global -> registers -> LDS in natural layout
-// (thread idx: row idx >> 3 and 16-byte column chunk idx & 7 for bf16, row idx >> 4
-// and float4 chunk idx & 15 for fp32).  Loads clamp rows at and beyond `valid` to
+// State passes: blocks of PASS_THREADS threads (4 waves) walk the chunks of one
+// state; the state's 64 value rows are split over PASS_SPLIT blocks (rows of the
+// recurrence are independent, so a chain's halves never exchange data).  Chunk
+// tiles travel global -> registers -> LDS in natural layout (thread idx: row
+// idx / (CW / 8) and 16-byte column chunk idx % (CW / 8) for bf16, float4 chunks
+// for fp32).  Loads clamp rows at and beyond `valid` to
 // row valid-1, for consumers that weight those rows by zero: with no conditional
 // register initialisation, a load in a software pipeline does not wait for the
 // previous load into the same registers.  (Clang vector types: a uint4 / float4
 // struct copy from memory would keep the register sets in scratch.)
-constexpr int PASS_THREADS = 512;
-template <int NT>
+constexpr int PASS_THREADS = 256;
+constexpr int PASS_SPLIT = 2;
+// 64-row tiles of CW columns (64, or a 32-column half at column c0) held in
+// registers, NT threads of the block; 16-byte loads along the row.
+template <int NT, int CW = 64>
 struct BfTileRegs {
-    uintx4 v[512 / NT];
+    uintx4 v[8 * CW / NT];
 };
-template <int NT>
+template <int NT, int CW = 64>
 struct F32TileRegs {
-    floatx4 v[1024 / NT];
+    floatx4 v[16 * CW / NT];
 };
-template <int NT>
-__device__ __forceinline__ void tile_load_bf(BfTileRegs<NT> &t, const unsigned short *src, int64_t st, int valid) {
+template <int NT, int CW = 64>
+__device__ __forceinline__ void tile_load_bf(BfTileRegs<NT, CW> &t, const unsigned short *src, int64_t st, int valid,
+                                             int c0 = 0) {
 #pragma unroll
-    for (int i = 0; i < 512 / NT; ++i) {
+    for (int i = 0; i < 8 * CW / NT; ++i) {
         const int idx = threadIdx.x + i * NT;
-        const int r = min(idx >> 3, valid - 1), c8 = idx & 7;
-        t.v[i] = *reinterpret_cast<const uintx4 *>(src + (int64_t)r * st + 8 * c8);
+        const int r = min(idx / (CW / 8), valid - 1), c8 = idx % (CW / 8);
+        t.v[i] = *reinterpret_cast<const uintx4 *>(src + (int64_t)r * st + c0 + 8 * c8);
     }
 }
-template <int NT>
-__device__ __forceinline__ void tile_store_bf(unsigned short *lds, const BfTileRegs<NT> &t) {
+template <int NT, int CW = 64>
+__device__ __forceinline__ void tile_store_bf(unsigned short *lds, const BfTileRegs<NT, CW> &t, int c0 = 0) {
 #pragma unroll
-    for (int i = 0; i < 512 / NT; ++i) {
+    for (int i = 0; i < 8 * CW / NT; ++i) {
         const int idx = threadIdx.x + i * NT;
-        *reinterpret_cast<uintx4 *>(lds + (idx >> 3) * PB + 8 * (idx & 7)) = t.v[i];
+        *reinterpret_cast<uintx4 *>(lds + (idx / (CW / 8)) * PB + c0 + 8 * (idx % (CW / 8))) = t.v[i];
     }
 }
 // The same store with row r scaled by lane r's `row_scale` (of the calling wave),
 // in fp32, rounded once to bf16.
-template <int NT>
-__device__ __forceinline__ void tile_store_bf_rowscaled(unsigned short *lds, const BfTileRegs<NT> &t, float row_scale) {
+template <int NT, int CW = 64>
+__device__ __forceinline__ void tile_store_bf_rowscaled(unsigned short *lds, const BfTileRegs<NT, CW> &t,
+                                                        float row_scale, int c0 = 0) {
 #pragma unroll
-    for (int i = 0; i < 512 / NT; ++i) {
-        const int idx = threadIdx.x + i * NT, r = idx >> 3;
+    for (int i = 0; i < 8 * CW / NT; ++i) {
+        const int idx = threadIdx.x + i * NT, r = idx / (CW / 8);
         const float f = __shfl(row_scale, r);
         const floatx8 x = to_f(__builtin_bit_cast(bf16x8, t.v[i])) * f;
-        *reinterpret_cast<bf16x8 *>(lds + r * PB + 8 * (idx & 7)) = to_bf(x);
+        *reinterpret_cast<bf16x8 *>(lds + r * PB + c0 + 8 * (idx % (CW / 8))) = to_bf(x);
     }
 }
-template <int NT>
-__device__ __forceinline__ void tile_load_f32(F32TileRegs<NT> &t, const float *src, int64_t st, int valid) {
+template <int NT, int CW = 64>
+__device__ __forceinline__ void tile_load_f32(F32TileRegs<NT, CW> &t, const float *src, int64_t st, int valid,
+                                              int c0 = 0) {
 #pragma unroll
-    for (int i = 0; i < 1024 / NT; ++i) {
+    for (int i = 0; i < 16 * CW / NT; ++i) {
         const int idx = threadIdx.x + i * NT;
-        const int r = min(idx >> 4, valid - 1), c4 = idx & 15;
-        t.v[i] = *reinterpret_cast<const floatx4 *>(src + (int64_t)r * st + 4 * c4);
+        const int r = min(idx / (CW / 4), valid - 1), c4 = idx % (CW / 4);
+        t.v[i] = *reinterpret_cast<const floatx4 *>(src + (int64_t)r * st + c0 + 4 * c4);
     }
 }
 // A complex fp32 tile (two planes) times a per-row complex weight (lane r of the
 // calling wave holds row r's (w_re, w_im)) -> two bf16 planes, rounded once.
-template <int NT>
+template <int NT, int CW = 64>
 __device__ __forceinline__ void tile_store_f32_cmul_as_bf(unsigned short *lre, unsigned short *lim,
-                                                         const F32TileRegs<NT> &xr, const F32TileRegs<NT> &xi,
-                                                         float w_re, float w_im) {
+                                                         const F32TileRegs<NT, CW> &xr, const F32TileRegs<NT, CW> &xi,
+                                                         float w_re, float w_im, int c0 = 0) {
 #pragma unroll
-    for (int i = 0; i < 1024 / NT; ++i) {
-        const int idx = threadIdx.x + i * NT, r = idx >> 4;
+    for (int i = 0; i < 16 * CW / NT; ++i) {
+        const int idx = threadIdx.x + i * NT, r = idx / (CW / 4);
         const float wr = __shfl(w_re, r), wi = __shfl(w_im, r);
         const floatx4 yr = wr * xr.v[i] - wi * xi.v[i], yi = wr * xi.v[i] + wi * xr.v[i];
-        const int o = r * PB + 4 * (idx & 15);
+        const int o = r * PB + c0 + 4 * (idx % (CW / 4));
         *reinterpret_cast<uint2 *>(lre + o) = make_uint2(pack_bf16x2(yr[0], yr[1]), pack_bf16x2(yr[2], yr[3]));
         *reinterpret_cast<uint2 *>(lim + o) = make_uint2(pack_bf16x2(yi[0], yi[1]), pack_bf16x2(yi[2], yi[3]));
     }

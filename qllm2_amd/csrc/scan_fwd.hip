@@ -558,38 +558,42 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
 // fp32 accumulation; q is staged unscaled and q_scale is applied to the fp32
 // results it enters.
 //
-// State pass: one block of PASS_THREADS (8 waves) per (state m, b, h) walks the
-// chunks in order; wave w owns value rows 16(w & 3).. and key-column tiles
-// 2(w >> 2), 2(w >> 2) + 1 (two waves per SIMD, so one wave's loads, stores and
-// MFMA chain overlap the other's).  Per chunk it forms dS = sum_s dl_s v_s (x)
+// State pass: PASS_SPLIT blocks of PASS_THREADS (4 waves) per (state m, b, h) walk
+// the chunks in order; block `half` owns value rows 32 half.. (V columns 32 half..)
+// and its wave w the rows 16 it.., it = 2 half + (w & 1), and key-column tiles
+// 2(w >> 1), 2(w >> 1) + 1.  Per chunk it forms dS = sum_s dl_s v_s (x)
 // conj(k_s) on MFMA and updates the running state S <- total S + dS, which never
 // leaves registers (fp32, accumulator layout).  Only the bf16 snapshot of the
 // state entering each chunk (stored straight from registers), the chunk totals
 // and the final state reach HBM.  Chunk c+2's K and V tiles and gamma are loaded
 // into registers while chunk c is processed and staged into LDS at the end of
-// chunk c+1 (double-buffered LDS, one barrier per chunk); every wave forms the
+// chunk c+1 (one LDS buffer, two barriers per chunk); every wave forms the
 // chunk's decay prefix itself and V is staged already scaled by dl_s, so the
 // MFMA operands come straight from LDS.  Rows past the end of the sequence
 // re-read its last row: their decay weights dl are zero.
 constexpr size_t pass_bf16_smem() {
-    return (size_t)2 * 2 * PLANE_B * 2     // K [buf][plane][64][PB]
-           + (size_t)2 * 2 * PLANE_B * 2;  // dl-scaled V [buf][plane][64][PB]
+    return (size_t)2 * PLANE_B * 2     // K [plane][64][PB]
+           + (size_t)2 * PLANE_B * 2;  // dl-scaled V [plane][64][PB] (this block's columns)
 }
 
-__global__ void __launch_bounds__(PASS_THREADS) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ void __launch_bounds__(PASS_THREADS) __attribute__((amdgpu_waves_per_eu(3)))
 state_pass_bf16_kernel(FwdParams p) {
     constexpr int NT = PASS_THREADS;
     extern __shared__ float smem[];
     using U = unsigned short;
-    U *sK = reinterpret_cast<U *>(smem);  // + (buf * 2 + plane) * PLANE_B
-    U *sV = sK + 4 * PLANE_B;             // + (buf * 2 + plane) * PLANE_B
+    U *sK = reinterpret_cast<U *>(smem);  // + plane * PLANE_B
+    U *sV = sK + 2 * PLANE_B;             // + plane * PLANE_B
 
     const qpam_scan_args &a = p.a;
-    const int chain = blockIdx.x;
+    // the halves of a chain are n_chains blocks apart: a multiple of 8 (the XCD
+    // count) when B H is, so both read K through the same L2
+    const int n_chains = a.M * a.B * a.H;
+    const int chain = blockIdx.x % n_chains, half = blockIdx.x / n_chains;
     const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
     const int b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int it = w & 3, jh = w >> 2;  // value rows 16it.., key-column tiles 2jh + jj
+    const int it = 2 * half + (w & 1), jh = w >> 1;  // value rows 16it.., key-column tiles 2jh + jj
+    const int vc0 = 32 * half;                       // V columns of this block's value rows
     const int n = p.n_chunks;
     const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
     const U *kre = (const U *)a.k.re + b * a.k.s0 + h * a.k.s1, *kim = (const U *)a.k.im + b * a.k.s0 + h * a.k.s1;
@@ -615,7 +619,8 @@ state_pass_bf16_kernel(FwdParams p) {
     // planes, gamma.  Sets are selected by compile-time index only (the chunk loop
     // is unrolled by two).
     struct ChunkRegs {
-        BfTileRegs<NT> kr, ki, vr, vi;
+        BfTileRegs<NT> kr, ki;
+        BfTileRegs<NT, 32> vr, vi;
         float gam;
     };
     ChunkRegs cr0, cr1;
@@ -624,14 +629,19 @@ state_pass_bf16_kernel(FwdParams p) {
         const int64_t ko = (int64_t)c0 * a.k.s2, vo = (int64_t)c0 * a.v.s2;
         tile_load_bf<NT>(x.kr, kre + ko, a.k.s2, valid);
         tile_load_bf<NT>(x.ki, kim + ko, a.k.s2, valid);
-        tile_load_bf<NT>(x.vr, vre + vo, a.v.s2, valid);
-        tile_load_bf<NT>(x.vi, vim + vo, a.v.s2, valid);
+        tile_load_bf<NT, 32>(x.vr, vre + vo, a.v.s2, valid, vc0);
+        tile_load_bf<NT, 32>(x.vi, vim + vo, a.v.s2, valid, vc0);
         x.gam = gbase[(int64_t)(c0 + min(lane, valid - 1)) * a.sg_t];
     };
-    // registers -> LDS buffer `buf`: K as loaded, V scaled by dl_s = D[C-1, s]; each
-    // wave forms the decay prefix from gamma itself and keeps the chunk total
-    float tot_staged = 1.f;  // decay total of the chunk in the most recently staged buffer
-    auto stage_chunk = [&](int c, int buf, const ChunkRegs &x) {
+    // registers -> LDS: K as loaded, V scaled by dl_s = D[C-1, s]; each wave forms
+    // the decay prefix from gamma itself and keeps the chunk total
+    float tot_staged = 1.f;  // decay total of the chunk in LDS
+    auto stage_chunk = [&](int c, const ChunkRegs &x) {
+        // nothing of the staging moves above this point: its first use of the staged
+        // register set is where the compiler waits for that set's loads, and the
+        // memory counter completes in order, so a use hoisted to the top of the step
+        // would also wait for everything loaded one step earlier
+        __builtin_amdgcn_sched_barrier(0);
         const int valid = min(64, a.T - c * 64);
         float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
 #pragma unroll
@@ -642,17 +652,17 @@ state_pass_bf16_kernel(FwdParams p) {
         const float Llast = __shfl(L, valid - 1);
         const float dl = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
         tot_staged = __expf(Llast);
-        if (tid == 0) *chunk_total_ptr(p, m, b, h, c) = tot_staged;
-        tile_store_bf<NT>(sK + (buf * 2) * PLANE_B, x.kr);
-        tile_store_bf<NT>(sK + (buf * 2 + 1) * PLANE_B, x.ki);
-        tile_store_bf_rowscaled<NT>(sV + (buf * 2) * PLANE_B, x.vr, dl);
-        tile_store_bf_rowscaled<NT>(sV + (buf * 2 + 1) * PLANE_B, x.vi, dl);
+        if (tid == 0 && half == 0) *chunk_total_ptr(p, m, b, h, c) = tot_staged;
+        tile_store_bf<NT>(sK, x.kr);
+        tile_store_bf<NT>(sK + PLANE_B, x.ki);
+        tile_store_bf_rowscaled<NT, 32>(sV, x.vr, dl, vc0);
+        tile_store_bf_rowscaled<NT, 32>(sV + PLANE_B, x.vi, dl, vc0);
     };
 
-    // chunk c uses LDS buffer c & 1; chunk c + 2 is loaded into register set c & 1
-    // during chunk c and staged at the end of chunk c + 1 (two chunks of latency cover)
+    // chunk c + 2 is loaded into register set c & 1 during chunk c and staged at the
+    // end of chunk c + 1 (two chunks of latency cover); one LDS buffer, staged
+    // between two barriers
     auto step = [&](int c, ChunkRegs &mine, ChunkRegs &next) {
-        const int buf = c & 1;
         // unconditional (the last chunk is re-read near the end): the same memory
         // operation count on every path keeps the compiler's waits for the staged
         // set exact
@@ -668,8 +678,8 @@ state_pass_bf16_kernel(FwdParams p) {
         floatx4 accR[2], accI[2];
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
-        const U *Kr = sK + (buf * 2) * PLANE_B, *Ki = sK + (buf * 2 + 1) * PLANE_B;
-        const U *Vr = sV + (buf * 2) * PLANE_B, *Vi = sV + (buf * 2 + 1) * PLANE_B;
+        const U *Kr = sK, *Ki = sK + PLANE_B;
+        const U *Vr = sV, *Vi = sV + PLANE_B;
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             const int s0 = 32 * kp + 8 * g;
@@ -694,13 +704,14 @@ state_pass_bf16_kernel(FwdParams p) {
                 sI[jj][r] = tot * sI[jj][r] + accI[jj][r];
             }
         // also unconditional: past the end, chunk n-1 (which `next` then holds) is
-        // staged again into the unused buffer
-        stage_chunk(min(c + 1, n - 1), buf ^ 1, next);
+        // staged again
+        __syncthreads();
+        stage_chunk(min(c + 1, n - 1), next);
         __syncthreads();
     };
     load_chunk(0, cr0);
     load_chunk(min(1, n - 1), cr1);
-    stage_chunk(0, 0, cr0);
+    stage_chunk(0, cr0);
     __syncthreads();
     // pairs of steps without conditions inside the loop (no path on which the
     // compiler would see fewer memory operations), odd tail after it
@@ -941,7 +952,7 @@ int launch_fwd_bf16_m(const FwdParams &p, hipStream_t stream) {
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_bf16_kernel<M>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
-    hipLaunchKernelGGL(state_pass_bf16_kernel, dim3(a.M * a.B * a.H), dim3(PASS_THREADS), s1, stream, p);
+    hipLaunchKernelGGL(state_pass_bf16_kernel, dim3(PASS_SPLIT * a.M * a.B * a.H), dim3(PASS_THREADS), s1, stream, p);
     int st = launch_status("state_pass_bf16_kernel");
     if (st) return st;
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));

@@ -330,7 +330,7 @@ __global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
     for (int e = tid; e < 3 * MAX_M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
     __syncthreads();
 
-    const int tt = w;
+    const int tt = causal_tile(w);
     const bool active = tt < C / 16;
     floatx4 gqR[4], gqI[4];
 #pragma unroll
@@ -600,7 +600,7 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
     }
     __syncthreads();
 
-    const int st = w;  // key rows s in [16st, 16st+16)
+    const int st = causal_tile(w);  // key rows s in [16st, 16st+16)
     const bool active = st < C / 16;
     floatx4 gvR[4], gvI[4], gkR[4], gkI[4];
 #pragma unroll
@@ -1058,7 +1058,7 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     }
     __syncthreads();
 
-    const int tt = w;
+    const int tt = causal_tile(w);
     const int t = 16 * tt + l16;
     floatx4 gqR[4], gqI[4];
 #pragma unroll
@@ -1371,7 +1371,7 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
     };
     load_state(0);
 
-    const int st = w;
+    const int st = causal_tile(w);
     const int s = 16 * st + l16;
     floatx4 gvR[4], gvI[4], gkR[4], gkI[4];
 #pragma unroll

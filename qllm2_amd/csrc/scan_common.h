@@ -241,6 +241,17 @@ __device__ __forceinline__ void acc_store_bf_pairs(unsigned short *dre, unsigned
 // previous load into the same registers.  (Clang vector types: a uint4 / float4
 // struct copy from memory would keep the register sets in scratch.)
 constexpr int PASS_THREADS = 256;
+
+// The 16-row tile wave w of a 4-wave chunk block works on.  Causal tiles differ
+// in cost (the last query tile of a chunk does four times the score work of the
+// first, and the reverse for key tiles) and a CU holds two such blocks, typically
+// of adjacent dispatch rounds of 256 blocks: alternate rounds take the tiles a
+// half-turn apart, so the heavy tiles of the two blocks do not share a SIMD.
+// Every tile is computed the same way whichever wave takes it.
+__device__ __forceinline__ int causal_tile(int w) {
+    const int lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    return (w + 2 * ((lin >> 8) & 1)) & 3;
+}
 constexpr int PASS_SPLIT = 2;
 // 64-row tiles of CW columns (64, or a 32-column half at column c0) held in
 // registers, NT threads of the block; 16-byte loads along the row.

@@ -225,7 +225,7 @@ __global__ void __launch_bounds__(THREADS) chunk_output_f32_kernel(FwdParams p) 
     }
     __syncthreads();
 
-    const int tt = w;  // query rows t in [16tt, 16tt+16)
+    const int tt = causal_tile(w);  // query rows t in [16tt, 16tt+16)
     const bool active = tt < C / 16;
     const int t = 16 * tt + l16;
     floatx4 wr[4], wi[4];  // A = W . D~ per s-tile; lane holds s = 16st+4g+r, t
@@ -422,7 +422,7 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
     }
     __syncthreads();
 
-    const int tt = w;                      // query rows t in [16tt, 16tt+16)
+    const int tt = causal_tile(w);  // query rows t in [16tt, 16tt+16)
     const bool active = tt < C / 16;
     floatx4 yR[4], yI[4];
 #pragma unroll
@@ -792,7 +792,7 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
     }
     __syncthreads();
 
-    const int tt = w;
+    const int tt = causal_tile(w);
     const int t = 16 * tt + l16;  // this lane's query row in the transposed score tiles
     floatx4 yR[4], yI[4];
 #pragma unroll

@@ -198,6 +198,54 @@ def _fused_prefill(self, x, state):
             and (self.n_states == 1 or getattr(self, "fused_e3", True)))
 
 
+class _TallKLinear(torch.autograd.Function):
+    """F.linear whose weight gradient g^T x contracts over all N = B T rows in
+    row slices: one batched product [S, in, N/S] x [S, N/S, out] and a sum of
+    the S partial products (in fp32 for 16-bit weights).  A weight gradient with a small output (the
+    gate logits: out = H or H + H K) or a square one (o_proj) gives the library
+    GEMM a few hundred output tiles at most for a K of N; the slices give it
+    S times as many."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, splits):
+        ctx.save_for_backward(x, w)
+        ctx.splits, ctx.has_bias = splits, b is not None
+        return F.linear(x, w, b)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, w = ctx.saved_tensors
+        gx = gw = gb = None
+        g2 = gy.reshape(-1, w.shape[0])
+        acc = torch.float32 if w.dtype in (torch.float16, torch.bfloat16) else w.dtype
+        if ctx.needs_input_grad[0]:
+            gx = (g2 @ w).view(x.shape)
+        if ctx.needs_input_grad[1]:
+            x2, n, s = x.reshape(-1, w.shape[1]), g2.shape[0], ctx.splits
+            # g^T x as (x^T g)^T: the right operand of the batched product stays a
+            # contiguous slice (no copy of either operand)
+            gwt = torch.bmm(x2.view(s, n // s, -1).transpose(1, 2), g2.view(s, n // s, -1))
+            gw = gwt.sum(0, dtype=acc).t().contiguous().to(w.dtype)
+        if ctx.has_bias and ctx.needs_input_grad[2]:
+            gb = g2.sum(0, dtype=acc).to(w.dtype)
+        return gx, gw, gb, None
+
+
+def _linear_tall_k(x, w, b):
+    """F.linear for N = x.numel() / in rows with the sliced weight gradient when
+    the library GEMM would see few output tiles (fewer than 512 of 128 x 128) and
+    N splits into slices of at least 512 rows; plain F.linear otherwise (and
+    under autocast or mixed dtypes)."""
+    n = x.numel() // w.shape[1]
+    tiles = -(-w.shape[0] // 128) * -(-w.shape[1] // 128)
+    s = 1
+    while s * tiles < 512 and n % (2 * s) == 0 and n // (2 * s) >= 512:
+        s *= 2
+    if s == 1 or torch.is_autocast_enabled() or x.dtype != w.dtype or not torch.is_grad_enabled():
+        return F.linear(x, w, b)
+    return _TallKLinear.apply(x if x.is_contiguous() else x.contiguous(), w, b, s)
+
+
 def forward(self, x, state=None, step_offset: int = 0):
     """V11PAMLayer.forward (v11/model.py:785-843) for a prefill of the
     production modes; everything else runs the original forward.
@@ -248,7 +296,7 @@ def forward(self, x, state=None, step_offset: int = 0):
             g_w.append(self.phase_proj.weight), g_b.append(self.phase_proj.bias), g_parts.append("phase")
             self._route_aux = self._route_balance_loss(x.new_ones(1, 1, 1, 1).expand(b, t, h, m))
     if g_parts:
-        gl = F.linear(mag, torch.cat(g_w, 0), torch.cat(g_b, 0))          # [B,T,H (+H K)]
+        gl = _linear_tall_k(mag, torch.cat(g_w, 0), torch.cat(g_b, 0))    # [B,T,H (+H K)]
         col = 0
         for part in g_parts:
             if part == "protect":
@@ -268,7 +316,7 @@ def forward(self, x, state=None, step_offset: int = 0):
     y = y.view(b, t, 2 * h * d)
     if w_out.dtype != torch.float32 and not torch.is_autocast_enabled():
         y = y.to(w_out.dtype)
-    out = F.linear(y, w_out, b_out).view(b, t, dim, 2)
+    out = _linear_tall_k(y, w_out, b_out).view(b, t, dim, 2)
     if self.training:
         # one keep-mask per complex value (as_complex_dropout_mask, v11/complex_ops.py:59-66)
         mask = self.dropout(torch.ones(out.shape[:-1], device=out.device, dtype=out.dtype))

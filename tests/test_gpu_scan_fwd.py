@@ -95,3 +95,23 @@ def test_e3_bf16_inputs(gpu_lib):
     y_ref, s_ref = O.multistate_fused(qb.double(), kb.double(), vb.double(), gamma.double(), zeros.double(),
                                       ones.double(), d, C)
     assert _rel(y, y_ref) < 2e-2 and _rel(s, s_ref) < 2e-2
+
+
+@pytest.mark.parametrize("B,T", [(2, 0), (0, 16)])
+def test_empty_batch_or_sequence_raises(gpu_lib, B, T):
+    """The reference's chunk loop concatenates an empty list at T = 0 and
+    raises (v11/model.py:385, 417); the HIP scan rejects zero sizes with an
+    error too, before any launch."""
+    from qllm2_amd._lib import QpamError
+    from qllm2_amd.pam_scan import pam_scan_planar
+
+    def call(b, t):
+        z = torch.zeros(b, 2, t, 64, device="cuda")
+        return pam_scan_planar(z, z, z, z, z, z, torch.full((1, b, 2, t), 0.9, device="cuda"), q_scale=0.125,
+                               chunk=16)
+
+    y_re = call(2, 16)[0]  # the same arguments at a nonzero size are accepted
+    assert y_re.shape == (2, 2, 16, 64)
+    with pytest.raises((QpamError, ValueError, RuntimeError)):
+        call(B, T)
+    torch.cuda.synchronize()

@@ -55,8 +55,9 @@ template <int V> struct CVec<float, V> {
 template <int V> struct CVec<unsigned short, V> {
     __device__ __forceinline__ static void load(const unsigned short *p, int64_t e, float (&re)[V], float (&im)[V]) {
         if constexpr (V == 4) {
-            const uint4 a = *reinterpret_cast<const uint4 *>(p + 2 * e);
-            const unsigned u[4] = {a.x, a.y, a.z, a.w};
+            // rows are streamed once: nontemporal 16-byte loads and stores
+            const uintx4 a = __builtin_nontemporal_load(reinterpret_cast<const uintx4 *>(p + 2 * e));
+            const unsigned u[4] = {a[0], a[1], a[2], a[3]};
 #pragma unroll
             for (int k = 0; k < 4; ++k) re[k] = __uint_as_float(u[k] << 16), im[k] = __uint_as_float(u[k] & 0xFFFF0000u);
         } else {
@@ -67,8 +68,9 @@ template <int V> struct CVec<unsigned short, V> {
     __device__ __forceinline__ static void store(unsigned short *p, int64_t e, const float (&re)[V],
                                                  const float (&im)[V]) {
         if constexpr (V == 4) {
-            *reinterpret_cast<uint4 *>(p + 2 * e) = make_uint4(pack_bf16x2(re[0], im[0]), pack_bf16x2(re[1], im[1]),
-                                                               pack_bf16x2(re[2], im[2]), pack_bf16x2(re[3], im[3]));
+            const uintx4 v = {pack_bf16x2(re[0], im[0]), pack_bf16x2(re[1], im[1]), pack_bf16x2(re[2], im[2]),
+                              pack_bf16x2(re[3], im[3])};
+            __builtin_nontemporal_store(v, reinterpret_cast<uintx4 *>(p + 2 * e));
         } else {
             *reinterpret_cast<unsigned *>(p + 2 * e) = pack_bf16x2(re[0], im[0]);
         }

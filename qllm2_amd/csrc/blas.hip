@@ -55,29 +55,30 @@ bool tune_enabled() {
 
 int pick_fastest(hipblasLtHandle_t h, Plan &p, const hipblasLtMatmulHeuristicResult_t *res, int count, const void *A,
                  const void *B, float beta, void *C, void *ws, size_t ws_bytes, hipStream_t stream) {
-    hipEvent_t e0, e1;
-    QPAM_CHECK_HIP(hipEventCreate(&e0));
-    QPAM_CHECK_HIP(hipEventCreate(&e1));
-    float best = 1e30f;
-    int best_i = 0;
-    const float alpha = 1.f;
-    for (int i = 0; i < count; ++i) {
-        if (res[i].workspaceSize > ws_bytes) continue;
-        float ms = 0.f;
-        bool ok = true;
-        for (int rep = 0; rep < 2 && ok; ++rep) {   // first run warms up, second is timed
-            hipEventRecord(e0, stream);
-            ok = hipblasLtMatmul(h, p.desc, &alpha, A, p.la, B, p.lb, &beta, C, p.lc, C, p.lc, &res[i].algo, ws,
-                                 ws_bytes, stream) == HIPBLAS_STATUS_SUCCESS;
-            hipEventRecord(e1, stream);
+    // timing is best effort: any failed event or matmul call skips that candidate,
+    // and the heuristic's first candidate stays the choice when none is timed
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    int best_i = -1;
+    if (hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess) {
+        float best = 1e30f;
+        const float alpha = 1.f;
+        for (int i = 0; i < count; ++i) {
+            if (res[i].workspaceSize > ws_bytes) continue;
+            bool ok = true;
+            for (int rep = 0; rep < 2 && ok; ++rep)  // first run warms up, second is timed
+                ok = hipEventRecord(e0, stream) == hipSuccess &&
+                     hipblasLtMatmul(h, p.desc, &alpha, A, p.la, B, p.lb, &beta, C, p.lc, C, p.lc, &res[i].algo, ws,
+                                     ws_bytes, stream) == HIPBLAS_STATUS_SUCCESS &&
+                     hipEventRecord(e1, stream) == hipSuccess;
+            float ms = 0.f;
+            if (ok && hipEventSynchronize(e1) == hipSuccess && hipEventElapsedTime(&ms, e0, e1) == hipSuccess &&
+                ms < best)
+                best = ms, best_i = i;
         }
-        if (!ok) continue;
-        hipEventSynchronize(e1);
-        hipEventElapsedTime(&ms, e0, e1);
-        if (ms < best) best = ms, best_i = i;
     }
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    if (best_i < 0) best_i = 0;
     p.algo = res[best_i].algo;
     p.ws = res[best_i].workspaceSize;
     return QPAM_OK;

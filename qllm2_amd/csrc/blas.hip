@@ -84,6 +84,53 @@ int pick_fastest(hipblasLtHandle_t h, Plan &p, const hipblasLtMatmulHeuristicRes
     return QPAM_OK;
 }
 
+void destroy_plan(Plan &p) {
+    if (p.la) (void)hipblasLtMatrixLayoutDestroy(p.la);
+    if (p.lb) (void)hipblasLtMatrixLayoutDestroy(p.lb);
+    if (p.lc) (void)hipblasLtMatrixLayoutDestroy(p.lc);
+    if (p.desc) (void)hipblasLtMatmulDescDestroy(p.desc);
+    p = Plan{};
+}
+
+// The matmul descriptor, layouts and algorithm of one GEMM shape; on failure the
+// caller destroys what `p` holds.
+int build_plan(hipblasLtHandle_t h, Plan &p, bool ta, bool tb, int m, int n, int k, const void *A, int64_t lda,
+               const void *B, int64_t ldb, float beta, void *C, int64_t ldc, bool c_f32, void *ws, size_t ws_bytes,
+               hipStream_t stream) {
+    const hipDataType ct = c_f32 ? HIP_R_32F : HIP_R_16BF;
+    QPAM_CHECK_LT(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
+    const hipblasOperation_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
+    QPAM_CHECK_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa)));
+    QPAM_CHECK_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb)));
+    // column-major layouts: op(A) is m x k, op(B) is k x n, C is m x n
+    QPAM_CHECK_LT(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, ta ? k : m, ta ? m : k, lda));
+    QPAM_CHECK_LT(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, tb ? n : k, tb ? k : n, ldb));
+    QPAM_CHECK_LT(hipblasLtMatrixLayoutCreate(&p.lc, ct, m, n, ldc));
+    struct Pref {  // destroyed on every path
+        hipblasLtMatmulPreference_t v = nullptr;
+        ~Pref() {
+            if (v) (void)hipblasLtMatmulPreferenceDestroy(v);
+        }
+    } pref;
+    QPAM_CHECK_LT(hipblasLtMatmulPreferenceCreate(&pref.v));
+    const uint64_t wsb = ws_bytes;
+    QPAM_CHECK_LT(
+        hipblasLtMatmulPreferenceSetAttribute(pref.v, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof(wsb)));
+    const bool tune = tune_enabled();
+    hipblasLtMatmulHeuristicResult_t res[16];
+    int count = 0;
+    const hipblasStatus_t hs =
+        hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref.v, tune ? 16 : 1, res, &count);
+    if (hs != HIPBLAS_STATUS_SUCCESS || count < 1)
+        return fail(QPAM_ERR_UNSUPPORTED, "hipBLASLt: no algorithm for %dx%dx%d (status %d)", m, n, k, (int)hs);
+    p.algo = res[0].algo;
+    p.ws = res[0].workspaceSize;
+    // the candidates write C: tune only when C is not accumulated into (beta != 0
+    // would double-count), else keep the first choice
+    if (tune && count > 1 && beta == 0.f) return pick_fastest(h, p, res, count, A, B, beta, C, ws, ws_bytes, stream);
+    return QPAM_OK;
+}
+
 }  // namespace
 
 bool enabled() {
@@ -103,37 +150,10 @@ int gemm_bf16(bool ta, bool tb, int m, int n, int k, const void *A, int64_t lda,
     auto it = g_plans.find(key);
     if (it == g_plans.end()) {
         Plan p;
-        const hipDataType ct = c_f32 ? HIP_R_32F : HIP_R_16BF;
-        QPAM_CHECK_LT(hipblasLtMatmulDescCreate(&p.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F));
-        const hipblasOperation_t opa = ta ? HIPBLAS_OP_T : HIPBLAS_OP_N, opb = tb ? HIPBLAS_OP_T : HIPBLAS_OP_N;
-        QPAM_CHECK_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa)));
-        QPAM_CHECK_LT(hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb)));
-        // column-major layouts: op(A) is m x k, op(B) is k x n, C is m x n
-        QPAM_CHECK_LT(hipblasLtMatrixLayoutCreate(&p.la, HIP_R_16BF, ta ? k : m, ta ? m : k, lda));
-        QPAM_CHECK_LT(hipblasLtMatrixLayoutCreate(&p.lb, HIP_R_16BF, tb ? n : k, tb ? k : n, ldb));
-        QPAM_CHECK_LT(hipblasLtMatrixLayoutCreate(&p.lc, ct, m, n, ldc));
-        hipblasLtMatmulPreference_t pref;
-        QPAM_CHECK_LT(hipblasLtMatmulPreferenceCreate(&pref));
-        const uint64_t wsb = ws_bytes;
-        QPAM_CHECK_LT(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
-                                                            sizeof(wsb)));
-        const bool tune = tune_enabled();
-        hipblasLtMatmulHeuristicResult_t res[16];
-        int count = 0;
-        const hipblasStatus_t hs =
-            hipblasLtMatmulAlgoGetHeuristic(h, p.desc, p.la, p.lb, p.lc, p.lc, pref, tune ? 16 : 1, res, &count);
-        hipblasLtMatmulPreferenceDestroy(pref);
-        if (hs != HIPBLAS_STATUS_SUCCESS || count < 1)
-            return fail(QPAM_ERR_UNSUPPORTED, "hipBLASLt: no algorithm for %dx%dx%d (status %d)", m, n, k, (int)hs);
-        p.algo = res[0].algo;
-        p.ws = res[0].workspaceSize;
-        if (tune && count > 1) {
-            // the candidates write C: tune on a beta = 0 copy of the problem only when C is
-            // not accumulated into (beta != 0 would double-count), else keep the first choice
-            if (beta == 0.f) {
-                st = pick_fastest(h, p, res, count, A, B, beta, C, ws, ws_bytes, stream);
-                if (st) return st;
-            }
+        st = build_plan(h, p, ta, tb, m, n, k, A, lda, B, ldb, beta, C, ldc, c_f32, ws, ws_bytes, stream);
+        if (st) {
+            destroy_plan(p);
+            return st;
         }
         it = g_plans.emplace(key, p).first;
     }

@@ -130,7 +130,7 @@ int qpam_decode_step(const qpam_decode_args *a, void *stream);
  * q, k, v: planar [B,H,T,d] (strides s0=b, s1=h, s2=t), fp32 or bf16.
  * gamma: fp32 [M,B,H,T]; rot (r_m, optional, NULL = 1): planar fp32 [M,B,H,T].
  * s0: optional initial state, planar fp32 [M,B,H,d,d] contiguous.
- * y: planar fp32 [B,H,T,d]; s_out: final state planar fp32 [M,B,H,d,d].
+ * y: planar fp32 (or bf16, y_dtype) [B,H,T,d]; s_out: final state planar fp32 [M,B,H,d,d].
  * The workspace keeps the state entering every chunk, planar fp32
  * [M,B,H,n_chunks,d,d]; qpam_scan_bwd reads it.  d == 64, C in {16,32,64}.
  */
@@ -148,6 +148,9 @@ typedef struct {
     int32_t B, H, T, d, C, M;
     int32_t dtype;          /* qpam_dtype of q, k, v (and of dq, dk, dv) */
     float q_scale;
+    int32_t y_dtype;        /* qpam_dtype of y: QPAM_F32, or QPAM_BF16 for bf16 inputs with C == 64
+                               (y rounded once from the fp32 result) */
+    int32_t reserved0;
     qpam_cview q, k, v;
     const float *gamma;
     int64_t sg_m, sg_b, sg_h, sg_t;
@@ -166,7 +169,7 @@ size_t qpam_scan_workspace_size(const qpam_scan_args *a);
 int qpam_scan_fwd(const qpam_scan_args *a, void *stream);
 
 /* Backward of qpam_scan_fwd.  `fwd` must describe the same call whose
- * workspace still holds the per-chunk states.  dy: planar fp32 [B,H,T,d];
+ * workspace still holds the per-chunk states.  dy: planar fp32 (or bf16, dy_dtype) [B,H,T,d];
  * ds: optional gradient of the final state, planar fp32 [M,B,H,d,d].
  * Outputs dq, dk, dv (dtype of q) planar [B,H,T,d]; dgamma fp32 [M,B,H,T]
  * with the strides of gamma; drot (optional) planar fp32 with rot's strides;
@@ -175,6 +178,8 @@ int qpam_scan_fwd(const qpam_scan_args *a, void *stream);
 typedef struct {
     const qpam_scan_args *fwd;
     qpam_cview dy;
+    int32_t dy_dtype;       /* qpam_dtype of dy: QPAM_F32, or QPAM_BF16 for bf16 inputs with C == 64 */
+    int32_t reserved0;
     const float *ds_re, *ds_im;            /* optional */
     qpam_mview dq, dk, dv;
     float *dgamma;

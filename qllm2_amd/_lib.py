@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -50,7 +50,7 @@ class MView(ctypes.Structure):
 class ScanArgs(ctypes.Structure):
     _fields_ = [
         ("B", c_i32), ("H", c_i32), ("T", c_i32), ("d", c_i32), ("C", c_i32), ("M", c_i32),
-        ("dtype", c_i32), ("q_scale", c_f32),
+        ("dtype", c_i32), ("q_scale", c_f32), ("y_dtype", c_i32), ("reserved0", c_i32),
         ("q", CView), ("k", CView), ("v", CView),
         ("gamma", c_ptr), ("sg_m", c_i64), ("sg_b", c_i64), ("sg_h", c_i64), ("sg_t", c_i64),
         ("rot_re", c_ptr), ("rot_im", c_ptr), ("sr_m", c_i64), ("sr_b", c_i64), ("sr_h", c_i64), ("sr_t", c_i64),
@@ -65,7 +65,7 @@ class ScanArgs(ctypes.Structure):
 class ScanBwdArgs(ctypes.Structure):
     _fields_ = [
         ("fwd", ctypes.POINTER(ScanArgs)),
-        ("dy", CView),
+        ("dy", CView), ("dy_dtype", c_i32), ("reserved0", c_i32),
         ("ds_re", c_ptr), ("ds_im", c_ptr),
         ("dq", MView), ("dk", MView), ("dv", MView),
         ("dgamma", c_ptr),

@@ -20,6 +20,8 @@
 //      gradient of D and cum -> partial dL/dL_t in the workspace;
 //   4. key_side (chunk-parallel, wave = key tile): dK, dV, the decay_last and
 //      total gradients, and the final d gamma of the chunk.
+#include <type_traits>
+
 #include "scan_common.h"
 
 namespace qpam {
@@ -49,6 +51,7 @@ struct BwdParams {
     // bf16 path: entering states (forward snapshots) and dS after each chunk, bf16
     const unsigned short *snap;
     unsigned short *gsnap;
+    int dy_bf16;             // dy planes are bf16 (bf16 path only)
 };
 
 __device__ __forceinline__ int64_t chain_idx(const BwdParams &p, int m, int b, int h) {
@@ -852,6 +855,7 @@ constexpr size_t gpass_bf16_smem() {
            + (size_t)2 * PLANE_B * 2;  // weighted dY (bf16) [plane][64][PB] (this block's columns)
 }
 
+template <bool DYBF>
 __global__ void __launch_bounds__(PASS_THREADS) __attribute__((amdgpu_waves_per_eu(3)))
 grad_pass_bf16_kernel(BwdParams p) {
     constexpr int NT = PASS_THREADS;
@@ -873,8 +877,10 @@ grad_pass_bf16_kernel(BwdParams p) {
     const float *rbr = a.rot_re ? a.rot_re + m * a.sr_m + b * a.sr_b + h * a.sr_h : nullptr;
     const float *rbi = a.rot_im ? a.rot_im + m * a.sr_m + b * a.sr_b + h * a.sr_h : nullptr;
     const U16 *qre = (const U16 *)a.q.re + b * a.q.s0 + h * a.q.s1, *qim = (const U16 *)a.q.im + b * a.q.s0 + h * a.q.s1;
-    const float *yre = (const float *)p.dy.re + b * p.dy.s0 + h * p.dy.s1;
-    const float *yim = (const float *)p.dy.im + b * p.dy.s0 + h * p.dy.s1;
+    // dY planes: fp32, or bf16 when DYBF (the same element offsets)
+    using YT = typename std::conditional<DYBF, U16, float>::type;
+    const YT *yre = (const YT *)p.dy.re + b * p.dy.s0 + h * p.dy.s1;
+    const YT *yim = (const YT *)p.dy.im + b * p.dy.s0 + h * p.dy.s1;
     const bool need_ds0 = p.ds0_re != nullptr;
     // rotations are read from gamma when absent (and replaced by 1 + 0i when staged)
     const float *rsrc_r = rbr ? rbr : gbase, *rsrc_i = rbi ? rbi : gbase;
@@ -899,12 +905,18 @@ grad_pass_bf16_kernel(BwdParams p) {
         float gam, rr, ri;
     };
     ChunkRegs cr0, cr1;
-    F32TileRegs<NT, 32> yr, yi;  // this block's dY columns of the next chunk (one set)
+    // this block's dY columns of the next chunk (one set)
+    typename std::conditional<DYBF, BfTileRegs<NT, 32>, F32TileRegs<NT, 32>>::type yr, yi;
     auto load_dy = [&](int c) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
         const int64_t yo = (int64_t)c0 * p.dy.s2;
-        tile_load_f32<NT, 32>(yr, yre + yo, p.dy.s2, valid, yc0);
-        tile_load_f32<NT, 32>(yi, yim + yo, p.dy.s2, valid, yc0);
+        if constexpr (DYBF) {
+            tile_load_bf<NT, 32>(yr, yre + yo, p.dy.s2, valid, yc0);
+            tile_load_bf<NT, 32>(yi, yim + yo, p.dy.s2, valid, yc0);
+        } else {
+            tile_load_f32<NT, 32>(yr, yre + yo, p.dy.s2, valid, yc0);
+            tile_load_f32<NT, 32>(yi, yim + yo, p.dy.s2, valid, yc0);
+        }
     };
     auto load_chunk = [&](int c, ChunkRegs &x) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
@@ -933,8 +945,12 @@ grad_pass_bf16_kernel(BwdParams p) {
         const float cum = (lane < valid) ? __expf(L) * a.q_scale : 0.f;
         tile_store_bf<NT>(sQ, x.qr);
         tile_store_bf<NT>(sQ + PLANE_B, x.qi);
-        tile_store_f32_cmul_as_bf<NT, 32>(sG, sG + PLANE_B, yr, yi,
-                                          (rbr ? x.rr : 1.f) * cum, -(rbi ? x.ri : 0.f) * cum, yc0);
+        if constexpr (DYBF)
+            tile_store_bf_cmul_as_bf<NT, 32>(sG, sG + PLANE_B, yr, yi, (rbr ? x.rr : 1.f) * cum,
+                                             -(rbi ? x.ri : 0.f) * cum, yc0);
+        else
+            tile_store_f32_cmul_as_bf<NT, 32>(sG, sG + PLANE_B, yr, yi, (rbr ? x.rr : 1.f) * cum,
+                                              -(rbi ? x.ri : 0.f) * cum, yc0);
     };
 
     // reverse order: step k handles chunk c = n-1-k; chunk c - 2 is loaded into
@@ -1015,7 +1031,7 @@ grad_pass_bf16_kernel(BwdParams p) {
     }
 }
 
-template <int M>
+template <int M, bool DYBF>
 __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
     U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;
@@ -1043,10 +1059,18 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
         const U16 *const bs[6] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
                                   (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
         const int64_t bst[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        U16 *const fd[2] = {sGr, sGi};
-        const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
-        const int64_t fst[2] = {p.dy.s2, p.dy.s2};
-        stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
+        if constexpr (DYBF) {
+            U16 *const bd8[8] = {bd[0], bd[1], bd[2], bd[3], bd[4], bd[5], sGr, sGi};
+            const U16 *const bs8[8] = {bs[0], bs[1], bs[2], bs[3], bs[4], bs[5], (const U16 *)p.dy.re + go,
+                                       (const U16 *)p.dy.im + go};
+            const int64_t bst8[8] = {bst[0], bst[1], bst[2], bst[3], bst[4], bst[5], p.dy.s2, p.dy.s2};
+            stage_bf<8, 0x0u>(bd8, bs8, bst8, valid);
+        } else {
+            U16 *const fd[2] = {sGr, sGi};
+            const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
+            const int64_t fst[2] = {p.dy.s2, p.dy.s2};
+            stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
+        }
     }
     if (w == 0) chunk_decay_prologue_f<M>(a, b, h, c0, valid, sL, sRr, sRi, sF, nullptr, nullptr, sFast);
     for (int e = tid; e < 3 * M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
@@ -1310,7 +1334,7 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     }
 }
 
-template <int M>
+template <int M, bool DYBF>
 __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
     U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;   // q, later G'_m
@@ -1339,10 +1363,18 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
         const U16 *const bs[6] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
                                   (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
         const int64_t bst[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        U16 *const fd[2] = {sGr, sGi};
-        const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
-        const int64_t fst[2] = {p.dy.s2, p.dy.s2};
-        stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
+        if constexpr (DYBF) {
+            U16 *const bd8[8] = {bd[0], bd[1], bd[2], bd[3], bd[4], bd[5], sGr, sGi};
+            const U16 *const bs8[8] = {bs[0], bs[1], bs[2], bs[3], bs[4], bs[5], (const U16 *)p.dy.re + go,
+                                       (const U16 *)p.dy.im + go};
+            const int64_t bst8[8] = {bst[0], bst[1], bst[2], bst[3], bst[4], bst[5], p.dy.s2, p.dy.s2};
+            stage_bf<8, 0x0u>(bd8, bs8, bst8, valid);
+        } else {
+            U16 *const fd[2] = {sGr, sGi};
+            const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
+            const int64_t fst[2] = {p.dy.s2, p.dy.s2};
+            stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
+        }
     }
     if (w == 0) {
         chunk_decay_prologue_f<M>(a, b, h, c0, valid, sL, sRr, sRi, sF, sPr, sPi, sFast);
@@ -1645,12 +1677,15 @@ int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;
     dim3 grid(p.n_chunks, a.H, a.B);
     const size_t s1 = gpass_bf16_smem(), s3 = qside_bf16_smem<M>(), s4 = kside_bf16_smem<M>();
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel,
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel<false>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)query_side_bf16_kernel<M>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)key_side_bf16_kernel<M>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel<true>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
+    const void *qk = p.dy_bf16 ? (const void *)query_side_bf16_kernel<M, true>
+                               : (const void *)query_side_bf16_kernel<M, false>;
+    const void *kk = p.dy_bf16 ? (const void *)key_side_bf16_kernel<M, true> : (const void *)key_side_bf16_kernel<M, false>;
+    QPAM_CHECK_HIP(hipFuncSetAttribute(qk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
+    QPAM_CHECK_HIP(hipFuncSetAttribute(kk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
     // the gradient-state pass (sequential chains, latency-bound) and the query side
     // (reads only forward snapshots) are independent: run them concurrently, the
     // chains launched first (measured faster than either the reverse order or one
@@ -1658,16 +1693,19 @@ int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
     int st = fork_join(
         stream,
         [&](hipStream_t s) {
-            hipLaunchKernelGGL(grad_pass_bf16_kernel, dim3(PASS_SPLIT * a.M * a.B * a.H), dim3(PASS_THREADS), s1, s,
-                               p);
+            const dim3 pg(PASS_SPLIT * a.M * a.B * a.H);
+            if (p.dy_bf16) hipLaunchKernelGGL(grad_pass_bf16_kernel<true>, pg, dim3(PASS_THREADS), s1, s, p);
+            else hipLaunchKernelGGL(grad_pass_bf16_kernel<false>, pg, dim3(PASS_THREADS), s1, s, p);
             return launch_status("grad_pass_bf16_kernel");
         },
         [&](hipStream_t s) {
-            hipLaunchKernelGGL(query_side_bf16_kernel<M>, grid, dim3(THREADS), s3, s, p);
+            if (p.dy_bf16) hipLaunchKernelGGL((query_side_bf16_kernel<M, true>), grid, dim3(THREADS), s3, s, p);
+            else hipLaunchKernelGGL((query_side_bf16_kernel<M, false>), grid, dim3(THREADS), s3, s, p);
             return launch_status("query_side_bf16_kernel");
         });
     if (st) return st;
-    hipLaunchKernelGGL(key_side_bf16_kernel<M>, grid, dim3(THREADS), s4, stream, p);
+    if (p.dy_bf16) hipLaunchKernelGGL((key_side_bf16_kernel<M, true>), grid, dim3(THREADS), s4, stream, p);
+    else hipLaunchKernelGGL((key_side_bf16_kernel<M, false>), grid, dim3(THREADS), s4, stream, p);
     return launch_status("key_side_bf16_kernel");
 }
 
@@ -1752,6 +1790,11 @@ int scan_bwd(const qpam_scan_bwd_args *bw, hipStream_t stream) {
     QPAM_REQUIRE(bw->dy.re && bw->dy.im && ((uintptr_t)bw->dy.re % 16) == 0 && ((uintptr_t)bw->dy.im % 16) == 0 &&
                      bw->dy.s0 % 4 == 0 && bw->dy.s1 % 4 == 0 && bw->dy.s2 % 4 == 0,
                  "qpam_scan_bwd: dy must be 16-byte aligned fp32 planes with strides multiple of 4");
+    QPAM_REQUIRE(bw->dy_dtype == QPAM_F32 ||
+                     (bw->dy_dtype == QPAM_BF16 && a->dtype == QPAM_BF16 && a->C == 64 && bw->dy.s0 % 8 == 0 &&
+                      bw->dy.s1 % 8 == 0 && bw->dy.s2 % 8 == 0),
+                 "qpam_scan_bwd: dy_dtype %d (bf16 dy needs bf16 inputs, chunk 64 and strides multiple of 8)",
+                 bw->dy_dtype);
     QPAM_REQUIRE(bw->dq.re && bw->dq.im && bw->dk.re && bw->dk.im && bw->dv.re && bw->dv.im && bw->dgamma,
                  "qpam_scan_bwd: null output");
     QPAM_REQUIRE((bw->ds_re == nullptr) == (bw->ds_im == nullptr), "qpam_scan_bwd: ds needs both planes");
@@ -1784,6 +1827,7 @@ int scan_bwd(const qpam_scan_bwd_args *bw, hipStream_t stream) {
     p.gl = (float *)bw->workspace + bwd_gl_offset(*a);
     p.snap = nullptr;
     p.gsnap = nullptr;
+    p.dy_bf16 = bw->dy_dtype == QPAM_BF16 ? 1 : 0;
     const bool bf = a->dtype == QPAM_BF16;
     if (uses_snapshots(*a)) {
         p.snap = reinterpret_cast<const unsigned short *>((const char *)a->workspace + fwd_snapshot_offset(*a));

@@ -320,6 +320,22 @@ __device__ __forceinline__ void tile_store_f32_cmul_as_bf(unsigned short *lre, u
         *reinterpret_cast<uint2 *>(lim + o) = make_uint2(pack_bf16x2(yi[0], yi[1]), pack_bf16x2(yi[2], yi[3]));
     }
 }
+// The same product for a complex bf16 tile (two planes as loaded by tile_load_bf):
+// widened to fp32, multiplied, rounded once to bf16.
+template <int NT, int CW = 64>
+__device__ __forceinline__ void tile_store_bf_cmul_as_bf(unsigned short *lre, unsigned short *lim,
+                                                        const BfTileRegs<NT, CW> &xr, const BfTileRegs<NT, CW> &xi,
+                                                        float w_re, float w_im, int c0 = 0) {
+#pragma unroll
+    for (int i = 0; i < 8 * CW / NT; ++i) {
+        const int idx = threadIdx.x + i * NT, r = idx / (CW / 8);
+        const float wr = __shfl(w_re, r), wi = __shfl(w_im, r);
+        const floatx8 a = to_f(__builtin_bit_cast(bf16x8, xr.v[i])), b = to_f(__builtin_bit_cast(bf16x8, xi.v[i]));
+        const int o = r * PB + c0 + 8 * (idx % (CW / 8));
+        *reinterpret_cast<bf16x8 *>(lre + o) = to_bf(wr * a - wi * b);
+        *reinterpret_cast<bf16x8 *>(lim + o) = to_bf(wr * b + wi * a);
+    }
+}
 template <int NT>
 __device__ __forceinline__ void tile_store_f32_as_bf(unsigned short *lds, const F32TileRegs<NT> &t) {
 #pragma unroll

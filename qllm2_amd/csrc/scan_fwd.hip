@@ -934,8 +934,14 @@ __global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p)
         for (int r = 0; r < 4; ++r) {
             const int tr = 16 * tt + 4 * g + r;
             if (tr < valid) {
-                a.y.re[yo + (int64_t)tr * a.y.s2 + 16 * it + l16] = yR[it][r];
-                a.y.im[yo + (int64_t)tr * a.y.s2 + 16 * it + l16] = yI[it][r];
+                const int64_t o = yo + (int64_t)tr * a.y.s2 + 16 * it + l16;
+                if (a.y_dtype == QPAM_BF16) {
+                    reinterpret_cast<U *>(a.y.re)[o] = f32_to_bf16(yR[it][r]);
+                    reinterpret_cast<U *>(a.y.im)[o] = f32_to_bf16(yI[it][r]);
+                } else {
+                    a.y.re[o] = yR[it][r];
+                    a.y.im[o] = yI[it][r];
+                }
             }
         }
 }
@@ -1055,6 +1061,8 @@ int validate_scan(const qpam_scan_args *a, const char *who, bool fwd_outputs) {
     QPAM_REQUIRE((a->s0_re == nullptr) == (a->s0_im == nullptr), "%s: s0 needs both planes", who);
     QPAM_REQUIRE((a->s_re == nullptr) == (a->s_im == nullptr), "%s: s_out needs both planes", who);
     QPAM_REQUIRE(!fwd_outputs || (a->y.re && a->y.im), "%s: null y", who);
+    QPAM_REQUIRE(a->y_dtype == QPAM_F32 || (a->y_dtype == QPAM_BF16 && a->dtype == QPAM_BF16 && a->C == 64),
+                 "%s: y_dtype %d (bf16 y needs bf16 inputs and chunk 64)", who, a->y_dtype);
     const uintptr_t al = (uintptr_t)a->s0_re | (uintptr_t)a->s0_im | (uintptr_t)a->s_re | (uintptr_t)a->s_im;
     QPAM_REQUIRE(al % 16 == 0, "%s: state buffers must be 16-byte aligned", who);
     QPAM_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= fwd_workspace_bytes(*a) &&

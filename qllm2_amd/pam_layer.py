@@ -310,9 +310,13 @@ def forward(self, x, state=None, step_offset: int = 0):
         proj, dt_bias, n_heads=h, n_states=m, state_offset=offsets, protect=protect, phase=phase,
         routing=routing, rope=rope, rope_offset=step_offset, qk_norm=self.qk_norm,
         gamma_floor=self.gamma_floor or 0.0)
-    y, _, s_re, s_im = pam_scan_planar(qr, qi, kr, ki, vr, vi, gamma, q_scale=d ** -0.5,
-                                       chunk=chunk_for(self.chunk_size, t), rot=rot, y_layout="bt2hd")
     w_out, b_out = _out_weight(self.o_proj)
+    ck = chunk_for(self.chunk_size, t)
+    # bf16 o_proj: the scan writes Y in bf16 itself (and reads its gradient in bf16)
+    y_bf16 = (qr.dtype == torch.bfloat16 and ck == 64 and w_out.dtype == torch.bfloat16
+              and not torch.is_autocast_enabled())
+    y, _, s_re, s_im = pam_scan_planar(qr, qi, kr, ki, vr, vi, gamma, q_scale=d ** -0.5, chunk=ck, rot=rot,
+                                       y_layout="bt2hd_bf16" if y_bf16 else "bt2hd")
     y = y.view(b, t, 2 * h * d)
     if w_out.dtype != torch.float32 and not torch.is_autocast_enabled():
         y = y.to(w_out.dtype)

@@ -137,16 +137,18 @@ def scan_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
     per-chunk entering states for the backward.  y_layout 0: y planes
     [B,H,T,d]; 1: [B,T,H,d] (head-merged); 2: one tensor [B,T,2,H,d] in the
     y_re slot (re and im planes of a token side by side, the [N, 2 H d] input
-    of one output-projection GEMM) and an empty y_im."""
+    of one output-projection GEMM) and an empty y_im; 3: layout 2 in bf16 (bf16
+    inputs, chunk 64: the kernel rounds y once from its fp32 result)."""
     _validate(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, chunk)
     M, B, H, T = gamma.shape
     d = q_re.shape[-1]
     dev = q_re.device
     a, keep = _fill_args(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk)
-    if y_layout == 2:
-        y_re = torch.empty(B, T, 2, H, d, device=dev, dtype=torch.float32)
+    if y_layout in (2, 3):
+        y_re = torch.empty(B, T, 2, H, d, device=dev, dtype=torch.bfloat16 if y_layout == 3 else torch.float32)
         y_im = y_re.new_empty(0)
         a.y = _mview(y_re[:, :, 0].transpose(1, 2), y_re[:, :, 1].transpose(1, 2))
+        a.y_dtype = 1 if y_layout == 3 else 0
     else:
         y_re = torch.empty((B, T, H, d) if y_layout == 1 else (B, H, T, d), device=dev, dtype=torch.float32)
         y_im = torch.empty_like(y_re)
@@ -185,9 +187,9 @@ def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q
     s = q_re.new_empty(M, B, H, d, d, dtype=torch.float32)
     nbytes = fwd_workspace_bytes(M, B, H, T, chunk, q_re.dtype == torch.bfloat16, d)
     ws = q_re.new_empty((nbytes + 3) // 4, dtype=torch.float32)
-    if y_layout == 2:
-        return [q_re.new_empty(B, T, 2, H, d, dtype=torch.float32), q_re.new_empty(0, dtype=torch.float32), s,
-                torch.empty_like(s), ws]
+    if y_layout in (2, 3):
+        yd = torch.bfloat16 if y_layout == 3 else torch.float32
+        return [q_re.new_empty(B, T, 2, H, d, dtype=yd), q_re.new_empty(0, dtype=yd), s, torch.empty_like(s), ws]
     y = q_re.new_empty((B, T, H, d) if y_layout == 1 else (B, H, T, d), dtype=torch.float32)
     return [y, torch.empty_like(y), s, torch.empty_like(s), ws]
 
@@ -206,8 +208,9 @@ def scan_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     bw = _lib.ScanBwdArgs()
     bw.fwd = _lib.ctypes.pointer(a)
-    if y_layout == 2:      # one [B,T,2,H,d] gradient in dy_re
+    if y_layout in (2, 3):  # one [B,T,2,H,d] gradient in dy_re (bf16 for layout 3)
         dy = dy_re.contiguous()
+        bw.dy_dtype = 1 if y_layout == 3 else 0
         dy_re, dy_im = dy[:, :, 0].transpose(1, 2), dy[:, :, 1].transpose(1, 2)
     else:
         dy_re, dy_im = dy_re.contiguous(), dy_im.contiguous()
@@ -270,9 +273,9 @@ def _backward(ctx, grads):
     (q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, ws) = ctx.saved_tensors
     dy_re, dy_im, ds_re, ds_im = grads[0], grads[1], grads[2], grads[3]
     B, H, T, d = q_re.shape
-    if ctx.y_layout == 2:
+    if ctx.y_layout in (2, 3):
         if dy_re is None:
-            dy_re = q_re.new_zeros((B, T, 2, H, d), dtype=torch.float32)
+            dy_re = q_re.new_zeros((B, T, 2, H, d), dtype=torch.bfloat16 if ctx.y_layout == 3 else torch.float32)
         dy_im = dy_re
     else:
         yshape = (B, T, H, d) if ctx.y_layout == 1 else (B, H, T, d)
@@ -301,12 +304,17 @@ def pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, *, q_scale, chunk
     [B,H,T,d], or [B,T,H,d] with y_layout="bthd", or with y_layout="bt2hd"
     one tensor [B,T,2,H,d] returned as y_re (y_im None): the kernel writes y
     in that layout and reads its gradient in it, no transposes.
+    y_layout="bt2hd_bf16" is the same tensor in bf16 (bf16 q, k, v and chunk
+    64): y is rounded once from the fp32 result and the gradient is read in
+    bf16, which equals rounding an fp32 y afterwards and widening a bf16 dy.
 
     Head dims below 64 are zero-padded to 64 (exact: padded key/query columns
     add nothing to q.k*, padded value rows stay zero) and sliced back."""
-    layouts = {"bhtd": 0, "bthd": 1, "bt2hd": 2}
+    layouts = {"bhtd": 0, "bthd": 1, "bt2hd": 2, "bt2hd_bf16": 3}
     if y_layout not in layouts:
         raise ValueError(f"y_layout must be one of {list(layouts)}")
+    if y_layout == "bt2hd_bf16" and (q_re.dtype != torch.bfloat16 or chunk != 64):
+        raise ValueError("y_layout 'bt2hd_bf16' needs bf16 q, k, v and chunk 64")
     rot_re, rot_im = rot if rot is not None else (None, None)
     s0_re, s0_im = s0 if s0 is not None else (None, None)
     d = q_re.shape[-1]
@@ -321,9 +329,9 @@ def pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, *, q_scale, chunk
     out = scan_fwd_op(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im,
                       float(q_scale), int(chunk), layouts[y_layout])
     y_re, y_im, s_re, s_im = out[0], out[1], out[2], out[3]
-    if y_layout == "bt2hd":
+    if y_layout in ("bt2hd", "bt2hd_bf16"):
         if d < 64:
-            raise NotImplementedError("y_layout 'bt2hd' needs head_dim 64")
+            raise NotImplementedError(f"y_layout '{y_layout}' needs head_dim 64")
         return y_re, None, s_re, s_im
     if d < 64:
         y_re, y_im = y_re[..., :d], y_im[..., :d]

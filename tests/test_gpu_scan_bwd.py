@@ -181,3 +181,36 @@ def test_scan_bf16_e3_decay_regimes(gpu_lib):
     s = torch.stack([s_re, s_im], -1).cpu()
     assert _rel(y, y_ref) < 2e-2, f"y: rel {_rel(y, y_ref):.2e}"
     assert _rel(s, s_ref) < 2e-2, f"s: rel {_rel(s, s_ref):.2e}"
+
+
+@pytest.mark.parametrize("T", [200, 2048])
+def test_bf16_head_merged_y_equals_rounded_fp32(gpu_lib, T):
+    """y_layout 'bt2hd_bf16' (E3, bf16 inputs, chunk 64): y is the fp32
+    result rounded once, so it equals the 'bt2hd' fp32 y rounded to bf16 bit
+    for bit; a bf16 dy gives the gradients of the same dy widened to fp32 (the
+    backward's LDS partial sums may add in another order: rel 1e-6)."""
+    from qllm2_amd.pam_scan import pam_scan_planar
+    g = torch.Generator().manual_seed(31 + T)
+    M, B, H, d = 3, 2, 2, 64
+    planes = [(torch.randn(B, H, T, d, generator=g) * 0.5).to(torch.bfloat16).cuda() for _ in range(6)]
+    gamma = (0.8 + 0.19 * torch.rand(M, B, H, T, generator=g)).cuda()
+    rot = tuple(torch.randn(M, B, H, T, generator=g).cuda() for _ in range(2))
+    dy = (torch.randn(B, T, 2, H, d, generator=g)).to(torch.bfloat16).cuda()
+
+    def run(layout, dy_in):
+        ins = [p.clone().requires_grad_(True) for p in planes]
+        gm = gamma.clone().requires_grad_(True)
+        rr = [r.clone().requires_grad_(True) for r in rot]
+        y, _, s_re, s_im = pam_scan_planar(*ins, gm, q_scale=d ** -0.5, chunk=64, rot=tuple(rr), y_layout=layout)
+        grads = torch.autograd.grad(y, ins + [gm] + rr, dy_in)
+        torch.cuda.synchronize()
+        return y, s_re, grads
+
+    y32, s32, g32 = run("bt2hd", dy.float())
+    y16, s16, g16 = run("bt2hd_bf16", dy)
+    assert y16.dtype == torch.bfloat16 and y16.shape == (B, T, 2, H, d)
+    assert torch.equal(y16, y32.to(torch.bfloat16))
+    assert torch.equal(s16, s32)
+    for a, b in zip(g16, g32):
+        assert a.dtype == b.dtype
+        assert _rel(a, b) < 1e-6

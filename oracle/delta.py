@@ -27,7 +27,7 @@ def _csolve_unit_lower(m_re, m_im, w_re, w_im):
     does it: the real 2C x 2C block system [[I+Mr, -Mi], [Mi, I+Mr]] through
     torch.linalg.solve in float (v11/model.py:1005-1016)."""
     c = m_re.shape[-1]
-    eye = torch.eye(c, dtype=m_re.dtype)
+    eye = torch.eye(c, dtype=m_re.dtype, device=m_re.device)
     top = torch.cat([eye + m_re, -m_im], dim=-1)
     bot = torch.cat([m_im, eye + m_re], dim=-1)
     sol = torch.linalg.solve(torch.cat([top, bot], dim=-2), torch.cat([w_re, w_im], dim=-2))
@@ -54,7 +54,7 @@ def delta_chunked(queries, keys, values, gamma, beta, head_dim, chunk_size, stat
         kr, ki, qr, qi = k[..., 0], k[..., 1], q[..., 0], q[..., 1]
         gram_r = kr @ kr.transpose(-1, -2) + ki @ ki.transpose(-1, -2)
         gram_i = ki @ kr.transpose(-1, -2) - kr @ ki.transpose(-1, -2)
-        strict = torch.tril(torch.ones(n, n, dtype=q.dtype), -1)
+        strict = torch.tril(torch.ones(n, n, dtype=q.dtype, device=q.device), -1)
         m_re = bt.unsqueeze(-1) * dmat * strict * gram_r
         m_im = bt.unsqueeze(-1) * dmat * strict * gram_i
         vr, vi = v[..., 0], v[..., 1]
@@ -68,7 +68,7 @@ def delta_chunked(queries, keys, values, gamma, beta, head_dim, chunk_size, stat
         u_re, u_im = _csolve_unit_lower(m_re, m_im, w_re, w_im)
         qk_r = qr @ kr.transpose(-1, -2) + qi @ ki.transpose(-1, -2)
         qk_i = qi @ kr.transpose(-1, -2) - qr @ ki.transpose(-1, -2)
-        causal = torch.tril(torch.ones(n, n, dtype=q.dtype))
+        causal = torch.tril(torch.ones(n, n, dtype=q.dtype, device=q.device))
         p_r, p_i = dmat * causal * qk_r, dmat * causal * qk_i
         y = torch.stack([(p_r @ u_re - p_i @ u_im) * scale, (p_r @ u_im + p_i @ u_re) * scale], -1)
         if c0 > 0 or has_state:

@@ -72,7 +72,7 @@ def decay_matrices(decay_gamma, chunk_len=None):
     log_decay = torch.log(decay_gamma.to(compute_dtype) + EPS)
     cum_neg = torch.cumsum(-log_decay, dim=-1)
     log_d = (cum_neg.unsqueeze(-1) - cum_neg.unsqueeze(-2)).transpose(-1, -2)
-    causal = torch.tril(torch.ones(chunk_len, chunk_len, dtype=compute_dtype))
+    causal = torch.tril(torch.ones(chunk_len, chunk_len, dtype=compute_dtype, device=decay_gamma.device))
     log_d = log_d * causal + (1 - causal) * (-1e4)
     d_mat = torch.exp(log_d.clamp(max=0.0))
     cum = torch.exp(torch.cumsum(log_decay, dim=-1))
@@ -146,6 +146,52 @@ def forward_head(queries, keys, protected_values, decay_gamma, head_dim, chunk_s
     if chunk_size > 0 and t > chunk_size:
         return chunked_head(queries, keys, protected_values, decay_gamma, head_dim, chunk_size)
     return dual_form_block(queries * head_dim ** -0.5, keys, protected_values, decay_gamma)
+
+
+# ------------------------------------------ E1: per-channel decay ------------
+
+def chunked_perchannel(queries, keys, protected_values, decay_gamma, head_dim, chunk_size):
+    """V11PAMLayer._forward_chunked_perchannel (v11/model.py:421-489).
+
+    decay_gamma [B,H,T,d]: one decay per key channel j, S[i,j] <- g_j S[i,j]
+    + v_i conj(k_j).  Per chunk the decay is folded into the operands: with
+    L = max(cumsum(log max(g, 1e-6)), -30) (inclusive), queries carry e^{L}
+    and keys e^{-L}, so the masked score (q e^L)(k e^-L)* is the decayed
+    score; the carried read is (q e^L) S^T, and the state update weights each
+    key by e^{L_last - L} and decays S's columns by e^{L_last}.  Queries are
+    unscaled on entry (scaled by head_dim**-0.5 here)."""
+    b, h, t = queries.shape[:3]
+    scale = head_dim ** -0.5
+    state = queries.new_zeros(b, h, head_dim, head_dim, 2)
+    outs = []
+    for c0 in range(0, t, chunk_size):
+        c1 = min(c0 + chunk_size, t)
+        n = c1 - c0
+        q_c, k_c, v_c = queries[:, :, c0:c1], keys[:, :, c0:c1], protected_values[:, :, c0:c1]
+        lg = torch.log(decay_gamma[:, :, c0:c1].clamp_min(1e-6)).float()
+        cl = torch.cumsum(lg, dim=2).clamp(min=-30.0)                     # [B,H,n,d]
+        a = torch.exp(cl).to(queries.dtype)
+        inv = torch.exp(-cl).to(queries.dtype)
+        tail = torch.exp(cl[:, :, -1:] - cl).to(queries.dtype)
+        a_tot = torch.exp(cl[:, :, -1]).to(queries.dtype)                 # [B,H,d]
+        fq = q_c * (a * scale).unsqueeze(-1)
+        fk = k_c * inv.unsqueeze(-1)
+        w_r = _re(fq) @ _re(fk).transpose(-1, -2) + _im(fq) @ _im(fk).transpose(-1, -2)
+        w_i = _im(fq) @ _re(fk).transpose(-1, -2) - _re(fq) @ _im(fk).transpose(-1, -2)
+        mask = torch.tril(torch.ones(n, n, dtype=w_r.dtype, device=w_r.device))
+        w_r, w_i = w_r * mask, w_i * mask
+        vr, vi = _re(v_c), _im(v_c)
+        out = _stack(w_r @ vr - w_i @ vi, w_r @ vi + w_i @ vr)
+        if c0 > 0:
+            sr, si = _re(state), _im(state)
+            out = out + _stack(_re(fq) @ sr.transpose(-1, -2) - _im(fq) @ si.transpose(-1, -2),
+                               _re(fq) @ si.transpose(-1, -2) + _im(fq) @ sr.transpose(-1, -2))
+        outs.append(out)
+        dk = k_c * tail.unsqueeze(-1)
+        s_r = vr.transpose(-1, -2) @ _re(dk) + vi.transpose(-1, -2) @ _im(dk)
+        s_i = vi.transpose(-1, -2) @ _re(dk) - vr.transpose(-1, -2) @ _im(dk)
+        state = state * a_tot[:, :, None, :, None] + _stack(s_r, s_i)
+    return torch.cat(outs, dim=2), state
 
 
 # ------------------------------------------ a4: flash_pam_chunked_head -------
@@ -281,15 +327,20 @@ def multistate_loop(queries, keys, protected_values, gamma_all, phase, routing, 
 # ------------------------------------------ a7: recurrent decode -------------
 
 def recur_step_additive(state, decay_gamma, value_t, key_t, query_t):
-    """V11PAMLayer._recur_step_additive (v11/model.py:927-965), head-scalar gamma.
+    """V11PAMLayer._recur_step_additive (v11/model.py:927-965).
 
-    state [..., d, d, 2]; decay_gamma [...]; value_t/key_t/query_t [..., d, 2]
-    (query already scaled).  S <- gamma*S + v (x) k*;  y = S q  (update before read).
+    state [..., d, d, 2]; decay_gamma [...] (head scalar) or [..., d] (E1: one
+    decay per key channel j, v11/model.py:948-954); value_t/key_t/query_t
+    [..., d, 2] (query already scaled).  S <- gamma*S + v (x) k*;  y = S q
+    (update before read).
     """
     kc = _stack(_re(key_t), -_im(key_t)).unsqueeze(-3)
     vr, vi = _re(value_t).unsqueeze(-1), _im(value_t).unsqueeze(-1)
     outer = _stack(vr * _re(kc) - vi * _im(kc), vr * _im(kc) + vi * _re(kc))
-    state = state * decay_gamma[..., None, None, None] + outer
+    if decay_gamma.dim() == state.dim() - 3:
+        state = state * decay_gamma[..., None, None, None] + outer
+    else:
+        state = state * decay_gamma[..., None, :, None] + outer
     qr, qi = _re(query_t).unsqueeze(-2), _im(query_t).unsqueeze(-2)
     y = _stack((_re(state) * qr - _im(state) * qi).sum(-1), (_re(state) * qi + _im(state) * qr).sum(-1))
     return y, state
@@ -381,6 +432,23 @@ def brute_force_scan(q, k, v, gamma, scale, eps=0.0, state0=None):
     y = np.zeros_like(q)
     for ti in range(t):
         s = g[..., ti, None, None] * s + v[..., ti, :, None] * np.conj(k[..., ti, None, :])
+        y[..., ti, :] = np.einsum('...ij,...j->...i', s, scale * q[..., ti, :])
+    return y, s
+
+
+def brute_force_perchannel(q, k, v, gamma, scale):
+    """E1 textbook recurrence in complex128 numpy: one decay per key channel,
+        S_t[i, j] = gamma_t[j] S_{t-1}[i, j] + v_t[i] conj(k_t[j]),  y_t = S_t (scale q_t).
+    q,k,v complex [..., T, d]; gamma [..., T, d].  Returns (y, S_T)."""
+    q = np.asarray(q, dtype=np.complex128)
+    k = np.asarray(k, dtype=np.complex128)
+    v = np.asarray(v, dtype=np.complex128)
+    g = np.asarray(gamma, dtype=np.float64)
+    t, d = q.shape[-2], q.shape[-1]
+    s = np.zeros(q.shape[:-2] + (d, d), np.complex128)
+    y = np.zeros_like(q)
+    for ti in range(t):
+        s = g[..., ti, None, :] * s + v[..., ti, :, None] * np.conj(k[..., ti, None, :])
         y[..., ti, :] = np.einsum('...ij,...j->...i', s, scale * q[..., ti, :])
     return y, s
 

@@ -148,6 +148,7 @@ class SlotPool:
         self.state = torch.zeros(n_slots, n_layers, n_heads, n_states, head_dim, head_dim, 2,
                                  device=self.device, dtype=torch.float32)
         self.pos = torch.zeros(n_slots, device=self.device, dtype=torch.int32)
+        self._host_pos = [0] * n_slots       # host copy of pos: the table is grown before a step needs it
         self.rope = build_rope_cache(max_len, head_dim, device=self.device)
         self._free = list(range(n_slots - 1, -1, -1))
         self.live = set()
@@ -162,6 +163,7 @@ class SlotPool:
         slot = self._free.pop()
         self.live.add(slot)
         self.pos[slot] = int(position)
+        self._host_pos[slot] = int(position)
         if states is None:
             self.state[slot].zero_()
         else:
@@ -189,11 +191,19 @@ class SlotPool:
     def step(self, layer, q, k, v, gamma, active, rot=None, q_scale=None, out=None):
         """One token for the listed slots on one layer: q, k, v [n_slots, heads, d, 2]
         (rows of unlisted slots ignored; q unscaled), gamma [n_slots, heads, states],
-        rot optional [n_slots, heads, states, 2].  RoPE at each slot's position."""
+        rot optional [n_slots, heads, states, 2].  RoPE at each slot's position; the
+        table is grown first (doubling) when a live slot's position passes its end."""
         scale = self.head_dim ** -0.5 if q_scale is None else q_scale
+        if self.live:
+            self.ensure_len(max(self._host_pos[s] for s in self.live))
         return decode_step(self.layer_state(layer), q, k, v, gamma, active=active, rot=rot, q_scale=scale,
                            out=out, rope=self.rope, pos=self.pos)
 
     def advance(self, active):
-        self.pos[active.long()] += 1
+        """Move the listed slots (an int tensor or a list of slot ids) one token on."""
+        ids = active.tolist() if torch.is_tensor(active) else list(active)
+        for s in ids:
+            self._host_pos[int(s)] += 1
+        idx = active.long() if torch.is_tensor(active) else torch.tensor(ids, dtype=torch.long)
+        self.pos[idx.to(self.device)] += 1
 

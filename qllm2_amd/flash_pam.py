@@ -16,6 +16,7 @@ identical either way.
 
 import torch
 
+from . import _reference
 from .pam_scan import pam_scan_interleaved
 from .triton_kernels import fused_decay_matrix
 
@@ -26,6 +27,9 @@ def _chunk_decay_matrices(decay_gamma_batch, chunk_len):
     """[N, C] -> (decay_matrix [N,C,C], cumulative_decay [N,C], total_decay [N],
     decay_last [N,C]) as v11/flash_pam.py:32-53.  The matrix comes from the
     HIP decay-matrix kernel; bf16/fp16 gamma is computed in fp32."""
+    if not decay_gamma_batch.is_cuda:
+        return _reference.on_cpu("flash_pam._chunk_decay_matrices", "_chunk_decay_matrices", decay_gamma_batch,
+                                 chunk_len)
     compute = torch.float32 if decay_gamma_batch.dtype in (torch.bfloat16, torch.float16) else decay_gamma_batch.dtype
     g = decay_gamma_batch.to(compute)
     d_mat = fused_decay_matrix(g, chunk_len)
@@ -35,5 +39,8 @@ def _chunk_decay_matrices(decay_gamma_batch, chunk_len):
 
 def flash_pam_chunked_head(queries, keys, protected_values, decay_gamma, head_dim, chunk_size):
     """Chunk-parallel PAM scan, head-scalar decay (v11/flash_pam.py:56-152)."""
+    if not queries.is_cuda:
+        return _reference.on_cpu("flash_pam.flash_pam_chunked_head", "flash_pam_chunked_head", queries, keys,
+                                 protected_values, decay_gamma, head_dim, chunk_size)
     y, s = pam_scan_interleaved(queries, keys, protected_values, decay_gamma.unsqueeze(0), head_dim, chunk_size)
     return y, s[0]

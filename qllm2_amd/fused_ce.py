@@ -11,7 +11,9 @@ Precision: if either operand is bf16 the GEMMs run on bf16 MFMA with fp32
 accumulation (the other operand is cast to bf16); two fp32 operands run on
 fp32 MFMA.  dW is accumulated in fp32 and cast to the weight dtype; dH is
 written in the hidden dtype.  Targets outside [0, V) that are not
-ignore_index contribute zero loss (the reference raises for them).
+ignore_index contribute zero loss (the reference raises for them).  CPU
+tensors raise, except after pam_layer.install(), which keeps the reference's
+own functions for them.
 """
 
 from typing import List, Optional
@@ -19,7 +21,7 @@ from typing import List, Optional
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, _reference
 
 __all__ = ["fused_linear_cross_entropy", "linear_ce_per_token", "linear_ce_stats"]
 
@@ -159,12 +161,18 @@ def fused_linear_cross_entropy(hidden_rows: Tensor, weight_matrix: Tensor, targe
     """Mean cross-entropy of (hidden_rows @ weight_matrix.T) vs targets
     (v11/fused_ce.py:85-94).  `chunk` bounds the rows whose softmax gradient
     is alive at once in the backward."""
+    if not hidden_rows.is_cuda:
+        return _reference.on_cpu("fused_ce.fused_linear_cross_entropy", "fused_linear_cross_entropy", hidden_rows,
+                                 weight_matrix, targets, mask=mask, chunk=chunk, ignore_index=ignore_index)
     return _FusedLinearCE.apply(hidden_rows, weight_matrix, targets, mask, chunk, ignore_index)
 
 
 @torch.no_grad()
 def linear_ce_per_token(hidden_rows, weight_matrix, targets, chunk: int = 4096, ignore_index: int = -100):
     """Per-row cross-entropy [N], 0.0 on ignore rows (v11/fused_ce.py:98-115)."""
+    if not hidden_rows.is_cuda:
+        return _reference.on_cpu("fused_ce.linear_ce_per_token", "linear_ce_per_token", hidden_rows, weight_matrix,
+                                 targets, chunk=chunk, ignore_index=ignore_index)
     h, w, dtype = _operands(hidden_rows, weight_matrix)
     targets, _ = _prep_targets(targets, None, h.shape[0])
     _, loss, _, _ = _run_fwd(h, w, dtype, targets, None, ignore_index, False)
@@ -174,6 +182,9 @@ def linear_ce_per_token(hidden_rows, weight_matrix, targets, chunk: int = 4096, 
 @torch.no_grad()
 def linear_ce_stats(hidden_rows, weight_matrix, targets, mask=None, chunk: int = 4096, ignore_index: int = -100):
     """(loss_sum, correct, tokens) as Python floats (v11/fused_ce.py:118-141)."""
+    if not hidden_rows.is_cuda:
+        return _reference.on_cpu("fused_ce.linear_ce_stats", "linear_ce_stats", hidden_rows, weight_matrix, targets,
+                                 mask=mask, chunk=chunk, ignore_index=ignore_index)
     h, w, dtype = _operands(hidden_rows, weight_matrix)
     targets, maskf = _prep_targets(targets, mask, h.shape[0])
     _, loss, correct, _ = _run_fwd(h, w, dtype, targets, None, ignore_index, True)

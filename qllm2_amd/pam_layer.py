@@ -23,16 +23,32 @@ Reference methods replaced (v11/model.py):
 The method replacements keep the layer's own projections/gates
 (_phase_and_alpha, _gamma_all_and_vprime, _gamma_and_vprime) and replace only
 the PAM math; the forward replacement fuses those elementwise steps into the
-prologue kernel (qpam_prologue_fwd).  The E1 per-channel decay mode keeps
-the reference methods: install() leaves them reachable as the saved
-originals.
+prologue kernel (qpam_prologue_fwd).
+
+install() keeps the class's own methods as `_qpam_originals` on that class,
+and every replacement hands a call to the saved method when the kernels do
+not cover it, so the installed layer computes what the reference computes in
+every mode:
+  * CPU tensors (the reference computes on CPU through its torch code);
+  * E1 per-channel decay (decay_gamma [..., d]): the reference's
+    _forward_chunked_perchannel is not replaced, and its decode steps go to
+    the saved _recur_step_additive / _recurrent;
+  * decode steps whose inputs need gradients (a T = 1 forward in training, a
+    state-carrying call under grad mode): the reference step is differentiable
+    torch code, the HIP decode step updates the state in place;
+  * head dims and state counts the scan kernels do not take (head_dim not
+    dividing 64, more than 4 states).
+The HIP library itself has no CPU path: the replacements raise for GPU
+tensors if it cannot load.
 """
 
+import importlib
 import sys
 
 import torch
 import torch.nn.functional as F
 
+from . import _reference
 from . import decode as _decode
 from . import pam_delta as _delta
 from . import fused_ce as _fused_ce
@@ -47,6 +63,30 @@ def _cat_rot(phase, routing):
     return routing * torch.cos(phase), routing * torch.sin(phase)
 
 
+def _originals(owner):
+    """The methods install() saved from `owner`'s class (or the class itself)."""
+    cls = owner if isinstance(owner, type) else type(owner)
+    table = getattr(cls, "_qpam_originals", None)
+    if table is None:
+        raise RuntimeError(f"qpam: {cls.__name__} was not set up by qllm2_amd.pam_layer.install(), so a call "
+                           "the HIP kernels do not cover has no reference method to run")
+    return table
+
+
+def _original(self, name):
+    return _originals(self)[name]
+
+
+def _scan_covers(t, head_dim, n_states=1):
+    """True when the HIP scan takes this call: GPU tensor, head_dim dividing 64
+    (smaller ones are zero-padded), at most 4 states."""
+    return t.is_cuda and head_dim <= 64 and 64 % head_dim == 0 and n_states <= 4
+
+
+def _needs_grad(*ts):
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
 def dual_form_block(scaled_queries, keys, protected_values, decay_gamma, causal_mask=None):
     """V11PAMLayer._dual_form_block: one block with zero incoming state; queries
     already scaled.  Returns (output [B,H,C,d,2], chunk state [B,H,d,d,2])."""
@@ -56,8 +96,23 @@ def dual_form_block(scaled_queries, keys, protected_values, decay_gamma, causal_
     return y, s[0]
 
 
+def _dual_form_block_for(original):
+    """The static _dual_form_block install() binds: the HIP block, or the saved
+    reference block for calls the scan does not take."""
+    def _dual_form_block(scaled_queries, keys, protected_values, decay_gamma, causal_mask=None):
+        if not _scan_covers(scaled_queries, scaled_queries.shape[-2]) and original is not None:
+            return original(scaled_queries, keys, protected_values, decay_gamma, causal_mask)
+        return dual_form_block(scaled_queries, keys, protected_values, decay_gamma, causal_mask)
+    _dual_form_block.__doc__ = dual_form_block.__doc__
+    _dual_form_block.__wrapped__ = dual_form_block
+    return _dual_form_block
+
+
 def forward_chunked_head(self, queries, keys, protected_values, decay_gamma, head_dim):
     """V11PAMLayer._forward_chunked_head (queries unscaled)."""
+    if not _scan_covers(queries, head_dim):
+        return _original(self, "_forward_chunked_head")(self, queries, keys, protected_values, decay_gamma,
+                                                        head_dim)
     y, s = pam_scan_interleaved(queries, keys, protected_values, decay_gamma.unsqueeze(0), head_dim,
                                 self.chunk_size)
     return y, s[0]
@@ -68,6 +123,10 @@ def fused_chunk_step(self, queries_chunk, keys_chunk, protected_values_chunk, de
     """V11PAMLayer._fused_chunk_step: queries scaled; decay/phase/routing
     [K,B,H,C]; memory_state [K,B,H,d,d,2] (ignored when is_first_chunk)."""
     d = queries_chunk.shape[-2]
+    if not _scan_covers(queries_chunk, d, decay_gamma_chunk.shape[0]):
+        return _original(self, "_fused_chunk_step")(
+            self, queries_chunk, keys_chunk, protected_values_chunk, decay_gamma_chunk, retrieval_phase_chunk,
+            routing_weights_chunk, memory_state, is_first_chunk)
     rot = _cat_rot(retrieval_phase_chunk, routing_weights_chunk)
     s0 = None if is_first_chunk else memory_state
     y, s = pam_scan_interleaved(queries_chunk, keys_chunk, protected_values_chunk, decay_gamma_chunk, d,
@@ -83,6 +142,8 @@ def fused_chunk_step(self, queries_chunk, keys_chunk, protected_values_chunk, de
 def forward_multistate_fused(self, x, queries, keys, values, head_dim):
     """V11PAMLayer._forward_multistate_fused: the layer's own prologue, then
     one E3 scan over every chunk.  Returns (output, state [K,B,H,d,d,2])."""
+    if not _scan_covers(queries, head_dim, self.n_states):
+        return _original(self, "_forward_multistate_fused")(self, x, queries, keys, values, head_dim)
     retrieval_phase, routing_weights = self._phase_and_alpha(x)
     retrieval_phase = retrieval_phase.permute(3, 0, 2, 1)
     routing_weights = routing_weights.permute(3, 0, 2, 1)
@@ -97,28 +158,43 @@ def forward_delta(self, queries, keys, protected_values, decay_gamma, write_beta
     """V11PAMLayer._forward_delta (E2 delta write, head-scalar decay): the HIP
     delta-rule kernels; per-channel decay or other head dims keep the original."""
     if decay_gamma.dim() != 3 or head_dim != 64 or not queries.is_cuda:
-        return _ORIGINALS["_forward_delta"](self, queries, keys, protected_values, decay_gamma, write_beta, head_dim)
+        return _original(self, "_forward_delta")(self, queries, keys, protected_values, decay_gamma, write_beta,
+                                                 head_dim)
     return _delta.forward_delta(queries, keys, protected_values, decay_gamma, write_beta, head_dim)
 
 
 def recur_step_delta(self, memory_state, decay_gamma, value_t, key_t, query_t, write_beta_t):
-    """V11PAMLayer._recur_step_delta (one decode token of the E2 write)."""
+    """V11PAMLayer._recur_step_delta (one decode token of the E2 write; the HIP
+    step is differentiable)."""
     if decay_gamma.dim() != 2 or memory_state.shape[-2] != 64 or not memory_state.is_cuda:
-        return _ORIGINALS["_recur_step_delta"](self, memory_state, decay_gamma, value_t, key_t, query_t,
-                                               write_beta_t)
+        return _original(self, "_recur_step_delta")(self, memory_state, decay_gamma, value_t, key_t, query_t,
+                                                    write_beta_t)
     return _delta.recur_step_delta(memory_state, decay_gamma, value_t, key_t, query_t, write_beta_t)
 
 
+_DECODE_DIMS = (16, 32, 64, 128)
+
+
 def recur_step_additive(self, memory_state, decay_gamma, value_t, key_t, query_t):
-    """V11PAMLayer._recur_step_additive (head-scalar decay)."""
+    """V11PAMLayer._recur_step_additive: the HIP decode step for head-scalar
+    decay without gradients; per-channel decay (decay_gamma [..., d]), inputs
+    that need gradients, CPU tensors and head dims outside 16/32/64/128 run the
+    saved reference step (v11/model.py:927-965, differentiable torch code)."""
+    if (not memory_state.is_cuda or decay_gamma.dim() != memory_state.dim() - 3
+            or memory_state.shape[-2] not in _DECODE_DIMS
+            or _needs_grad(memory_state, decay_gamma, value_t, key_t, query_t)):
+        return _original(self, "_recur_step_additive")(self, memory_state, decay_gamma, value_t, key_t, query_t)
     return _decode.recur_step_additive(memory_state, decay_gamma, value_t, key_t, query_t)
 
 
 def recurrent(self, x, queries, keys, values, state, head_dim):
     """V11PAMLayer._recurrent for the additive head-decay write: per token one
-    qpam_decode_step launch updates all K states and sums the rotated reads."""
-    if self.write_mode != 'additive' or self.decay_mode == 'per_channel' or torch.is_grad_enabled():
-        return _ORIGINALS['_recurrent'](self, x, queries, keys, values, state, head_dim)
+    qpam_decode_step launch updates all K states and sums the rotated reads.
+    The E1 / E2 modes, grad mode, CPU tensors and other head dims run the saved
+    reference loop (which then calls the replaced steps where they apply)."""
+    if (self.write_mode != 'additive' or self.decay_mode == 'per_channel' or torch.is_grad_enabled()
+            or not x.is_cuda or head_dim not in _DECODE_DIMS):
+        return _original(self, "_recurrent")(self, x, queries, keys, values, state, head_dim)
     b, t = x.shape[0], x.shape[1]
     h, k_states, d = self.num_heads, self.n_states, head_dim
     scale = head_dim ** -0.5
@@ -258,7 +334,7 @@ def forward(self, x, state=None, step_offset: int = 0):
     table into the scan's operands; the scan writes Y as [B,T,2,H,d]; (3) one
     GEMM from Y viewed as [N, 2 H d] straight to the interleaved output."""
     if not _fused_prefill(self, x, state):
-        return _ORIGINALS["forward"](self, x, state, step_offset)
+        return _original(self, "forward")(self, x, state, step_offset)
     b, t, dim = x.shape[0], x.shape[1], x.shape[2]
     h, d, m = self.num_heads, self.head_dim, self.n_states
     n = b * t
@@ -329,8 +405,6 @@ def forward(self, x, state=None, step_offset: int = 0):
     return out, (new_state if m > 1 else new_state[0])
 
 
-_ORIGINALS = {}
-
 _METHODS = {
     "forward": forward,
     "_forward_chunked_head": forward_chunked_head,
@@ -342,29 +416,58 @@ _METHODS = {
     "_recurrent": recurrent,
 }
 
+# module-level functions of the reference's v11 package that this package
+# replaces, kept for CPU calls (qllm2_amd/_reference.py)
+_MODULE_FUNCS = {
+    "flash_pam": ("flash_pam_chunked_head", "_chunk_decay_matrices"),
+    "triton_kernels": ("fused_decay_matrix", "fused_complex_norm", "fused_mod_swish", "fused_mod_relu",
+                       "fused_cgu_gate"),
+    "fused_ce": ("fused_linear_cross_entropy", "linear_ce_per_token", "linear_ce_stats"),
+}
+
+_COMPLEX_OPS = ("fused_complex_norm", "fused_mod_swish", "fused_mod_relu", "fused_cgu_gate")
+
 
 def install(model_module=None):
     """Bind the HIP implementations into the reference's v11 package.
 
     model_module: the imported v11.model module (default: sys.modules['v11.model']).
-    Rebinds the V11PAMLayer methods above (and the static _dual_form_block),
-    replaces the module-level fused_decay_matrix name v11/model.py:40 bound at
-    import, and aliases v11.flash_pam / v11.triton_kernels / v11.fused_ce to this
+    Rebinds the V11PAMLayer methods above (and the static _dual_form_block)
+    after keeping the class's own methods as V11PAMLayer._qpam_originals (the
+    replacements hand them the calls the kernels do not cover), replaces the
+    module-level fused_decay_matrix name v11/model.py:40 bound at import, and
+    aliases v11.flash_pam / v11.triton_kernels / v11.fused_ce to this
     package's modules so later imports (v11/model.py:1182, v7/train.py:301,350)
-    resolve here.  Returns the dict of replaced originals."""
+    resolve here; the reference functions they replace are kept for CPU
+    tensors.  Calling it again is harmless.  Returns the saved originals."""
     mod = model_module if model_module is not None else sys.modules["v11.model"]
     layer = mod.V11PAMLayer
+    table = layer.__dict__.get("_qpam_originals")
+    if table is None:
+        table = {name: getattr(layer, name) for name in _METHODS if hasattr(layer, name)}
+        if hasattr(layer, "_dual_form_block"):
+            table["_dual_form_block"] = getattr(layer, "_dual_form_block")   # the static function itself
+        layer._qpam_originals = table
     for name, fn in _METHODS.items():
-        if name not in _ORIGINALS and hasattr(layer, name):
-            _ORIGINALS[name] = getattr(layer, name)
-        setattr(layer, name, fn)
-    if "_dual_form_block" not in _ORIGINALS and hasattr(layer, "_dual_form_block"):
-        _ORIGINALS["_dual_form_block"] = layer.__dict__.get("_dual_form_block", layer._dual_form_block)
-    layer._dual_form_block = staticmethod(dual_form_block)
+        if name in table:
+            setattr(layer, name, fn)
+    layer._dual_form_block = staticmethod(_dual_form_block_for(table.get("_dual_form_block")))
     if hasattr(mod, "fused_decay_matrix"):
+        _reference.save("triton_kernels.fused_decay_matrix", mod.fused_decay_matrix)
         mod.fused_decay_matrix = _tk.fused_decay_matrix
     pkg = mod.__name__.rsplit(".", 1)[0] if "." in mod.__name__ else "v11"
-    for sub, m in (("flash_pam", _flash_pam), ("triton_kernels", _tk), ("fused_ce", _fused_ce)):
+    ours = {"flash_pam": _flash_pam, "triton_kernels": _tk, "fused_ce": _fused_ce}
+    saved = dict(table)
+    for sub, m in ours.items():
+        ref = sys.modules.get(f"{pkg}.{sub}")
+        if ref is None:
+            try:
+                ref = importlib.import_module(f"{pkg}.{sub}")
+            except ImportError:
+                ref = None
+        if ref is not None and ref is not m:
+            for name in _MODULE_FUNCS[sub]:
+                _reference.save(f"{sub}.{name}", getattr(ref, name, None))
         sys.modules[f"{pkg}.{sub}"] = m
         parent = sys.modules.get(pkg)
         if parent is not None:
@@ -375,9 +478,12 @@ def install(model_module=None):
     if cops is not None:
         for name in _COMPLEX_OPS:
             if hasattr(cops, name):
-                _ORIGINALS.setdefault(f"complex_ops.{name}", getattr(cops, name))
+                if _reference.saved(f"triton_kernels.{name}") is None:
+                    _reference.save(f"triton_kernels.{name}", getattr(cops, name))
                 setattr(cops, name, getattr(_tk, name))
-    return dict(_ORIGINALS)
-
-
-_COMPLEX_OPS = ("fused_complex_norm", "fused_mod_swish", "fused_mod_relu", "fused_cgu_gate")
+    for sub, names in _MODULE_FUNCS.items():
+        for name in names:
+            fn = _reference.saved(f"{sub}.{name}")
+            if fn is not None:
+                saved[f"{sub}.{name}"] = fn
+    return saved

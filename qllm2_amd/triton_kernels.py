@@ -16,7 +16,9 @@ tensors; other floating dtypes are computed in fp32 and cast back.
 set_triton_enabled / triton_enabled keep their names; they switch the HIP
 kernels on or off (off = the reference's PyTorch formulas, its `_pt_*`
 functions, v11/triton_kernels.py:489-520, on the GPU).  HAS_TRITON is False:
-this module has no Triton.
+this module has no Triton.  CPU tensors raise, except after
+pam_layer.install(), which keeps the reference's own functions for them
+(the reference computes on CPU through its `_pt_*` forms).
 """
 
 import ctypes
@@ -26,7 +28,7 @@ import torch
 import torch.nn.functional as F
 from torch import Tensor
 
-from . import _lib
+from . import _lib, _reference
 
 __all__ = ["fused_decay_matrix", "fused_complex_norm", "fused_mod_swish", "fused_mod_relu", "fused_cgu_gate",
            "set_triton_enabled", "triton_enabled", "HAS_TRITON", "HAS_HIP"]
@@ -125,11 +127,13 @@ decay_matrix_op.register_autograd(_decay_backward, setup_context=_decay_setup)
 def fused_decay_matrix(decay_gamma: Tensor, seq_len: int, block: int = 64) -> Tensor:
     """D[t,s] = exp(min(c_s - c_t, 0)) for s <= t else 0, c = cumsum(-log(gamma+1e-6)),
     gamma [N, T] -> [N, T, T] in gamma's dtype (v11/triton_kernels.py:570-573)."""
-    if decay_gamma.is_cuda and _use_hip and not torch.compiler.is_compiling():
+    if not decay_gamma.is_cuda:
+        return _reference.on_cpu("triton_kernels.fused_decay_matrix", "fused_decay_matrix", decay_gamma, seq_len,
+                                 block)
+    if _use_hip:
+        # a registered custom op (fake + autograd): torch.compile traces it as one node
         return decay_matrix_op(decay_gamma, seq_len).to(decay_gamma.dtype)
-    if decay_gamma.is_cuda or torch.compiler.is_compiling():
-        return _pt_decay_matrix(decay_gamma, seq_len)
-    raise ValueError("qpam fused_decay_matrix: tensors must be on the GPU (no CPU path in this library)")
+    return _pt_decay_matrix(decay_gamma, seq_len)
 
 
 # ---------------------------------------------------------------- complex elementwise ops (HIP)
@@ -240,33 +244,35 @@ def _run_cplx(op, z, up=None, p0=None, p1=None, eps=0.0):
 
 def fused_complex_norm(z: Tensor, scale: Tensor, eps: float = 1e-6) -> Tensor:
     """ComplexNorm forward (v11/triton_kernels.py:48-79, backward :209-260)."""
+    if not z.is_cuda:
+        return _reference.on_cpu("triton_kernels.fused_complex_norm", "fused_complex_norm", z, scale, eps)
     if _use_hip:
         return _run_cplx(_lib.QPAM_CPLX_NORM, z, p0=scale, eps=eps)
-    return _gpu_only(_pt_complex_norm, z, scale, eps)
+    return _pt_complex_norm(z, scale, eps)
 
 
 def fused_mod_swish(z: Tensor, bias: Tensor, beta: Tensor) -> Tensor:
     """ModSwish forward (v11/triton_kernels.py:83-108, backward :263-304)."""
+    if not z.is_cuda:
+        return _reference.on_cpu("triton_kernels.fused_mod_swish", "fused_mod_swish", z, bias, beta)
     if _use_hip:
         return _run_cplx(_lib.QPAM_CPLX_MOD_SWISH, z, p0=bias, p1=beta)
-    return _gpu_only(_pt_mod_swish, z, bias, beta)
+    return _pt_mod_swish(z, bias, beta)
 
 
 def fused_mod_relu(z: Tensor, bias: Tensor) -> Tensor:
     """ModReLU forward (v11/triton_kernels.py:112-135, backward :307-345)."""
+    if not z.is_cuda:
+        return _reference.on_cpu("triton_kernels.fused_mod_relu", "fused_mod_relu", z, bias)
     if _use_hip:
         return _run_cplx(_lib.QPAM_CPLX_MOD_RELU, z, p0=bias)
-    return _gpu_only(_pt_mod_relu, z, bias)
+    return _pt_mod_relu(z, bias)
 
 
 def fused_cgu_gate(gate: Tensor, up: Tensor) -> Tensor:
     """CGU gate sigmoid(|g|) * phase(g) * up (v11/triton_kernels.py:139-166, backward :348-395)."""
+    if not gate.is_cuda:
+        return _reference.on_cpu("triton_kernels.fused_cgu_gate", "fused_cgu_gate", gate, up)
     if _use_hip:
         return _run_cplx(_lib.QPAM_CPLX_CGU_GATE, gate, up=up)
-    return _gpu_only(_pt_cgu_gate, gate, up)
-
-
-def _gpu_only(fn, z, *args):
-    if not z.is_cuda:
-        raise ValueError("qpam complex ops: tensors must be on the GPU (no CPU path in this library)")
-    return fn(z, *args)
+    return _pt_cgu_gate(gate, up)

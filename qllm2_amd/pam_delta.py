@@ -118,6 +118,9 @@ def delta_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: T
                  ds_im: Optional[Tensor]) -> List[Tensor]:
     """Returns [dq_re, dq_im, dk_re, dk_im, dv_re, dv_im, dgamma, dbeta, ds0_re, ds0_im]
     (ds0 empty without s0)."""
+    # the kernels write dgamma and dbeta with gamma's strides: contiguous planes,
+    # matching the gradients allocated below
+    gamma, beta = gamma.contiguous(), beta.contiguous()
     a, keep = _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps)
     B, H, T, d = q_re.shape
     dev = q_re.device
@@ -146,7 +149,6 @@ def delta_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: T
     with torch.cuda.device(dev):
         _lib.check(L.qpam_delta_bwd(g, _lib.stream_ptr(dev)), "qpam_delta_bwd")
     del keep
-    # dgamma/dbeta follow gamma's strides; _fill may have used contiguous copies
     return outs + [dgamma, dbeta] + ds0
 
 

@@ -204,6 +204,11 @@ def scan_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
     M, B, H, T = gamma.shape
     d = q_re.shape[-1]
     dev = q_re.device
+    # the kernels write dgamma and drot with the strides of gamma and rot: hand
+    # them contiguous planes so those strides match the gradients allocated here
+    gamma = gamma.contiguous()
+    if rot_re is not None:
+        rot_re, rot_im = rot_re.contiguous(), rot_im.contiguous()
     a, keep = _fill_args(q_re, q_im, k_re, k_im, v_re, v_im, gamma, rot_re, rot_im, s0_re, s0_im, q_scale, chunk)
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
     bw = _lib.ScanBwdArgs()

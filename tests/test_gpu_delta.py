@@ -76,6 +76,27 @@ def test_delta_matches_chunked_oracle(gpu_lib, T, with_s0, with_ds):
         assert _rel(a, r) < 1e-4, f"{name}: {_rel(a, r):.2e}"
 
 
+def test_delta_strided_gamma_and_beta(gpu_lib):
+    """gamma and beta as transposed views of [B,T,H] tensors with equal strides
+    (the layout of the reference's write_beta, v11/model.py:807): dgamma and
+    dbeta against the chunked oracle."""
+    from qllm2_amd.pam_delta import delta_planar
+    B, H, T, d = 2, 3, 50, 64
+    q, k, v, g, b = D.make_delta_inputs(B, H, T, d, 640)
+    dy = torch.randn(B, H, T, d, 2, generator=torch.Generator().manual_seed(641), dtype=torch.float64)
+    _, _, rgrads = _ref(q, k, v, g, b, None, dy, None, chunked=True)
+    dev = torch.device("cuda")
+    planes = [x[..., i].contiguous().float().to(dev) for x in (q, k, v) for i in (0, 1)]
+    gt = g.transpose(1, 2).contiguous().float().to(dev).requires_grad_(True)   # [B,T,H] storage
+    bt = b.transpose(1, 2).contiguous().float().to(dev).requires_grad_(True)
+    gv, bv = gt.transpose(1, 2), bt.transpose(1, 2)
+    assert not gv.is_contiguous() and gv.stride() == bv.stride()
+    y_re, y_im, _, _ = delta_planar(*planes, gv, bv, q_scale=64 ** -0.5, gamma_eps=1e-6)
+    ((y_re * dy[..., 0].to(dev)).sum() + (y_im * dy[..., 1].to(dev)).sum()).backward()
+    assert _rel(gt.grad.transpose(1, 2), rgrads[3]) < 1e-4, "dgamma"
+    assert _rel(bt.grad.transpose(1, 2), rgrads[4]) < 1e-4, "dbeta"
+
+
 def test_delta_step_matches_reference_step(gpu_lib):
     """recur_step_delta (the decode drop-in, gamma without the chunked form's
     1e-6) against the reference step, several tokens in a row."""

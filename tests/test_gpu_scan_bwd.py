@@ -92,6 +92,35 @@ def test_scan_backward_fp32(gpu_lib, M, T, C, with_rot, with_s0):
         assert _rel(a, b) < 1e-4, f"{name}: rel {_rel(a, b):.2e}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_scan_backward_strided_gamma_and_rot(gpu_lib, dtype):
+    """gamma and the rotation planes as permuted views of [B,T,H,M] tensors (the
+    layout V11PAMLayer._forward_multistate_fused hands over, v11/model.py:746-748):
+    dgamma, dphase and drouting against oracle autograd."""
+    M, B, H, T, d, C = 2, 2, 3, 40, 64, 64
+    case = list(_case(M, B, H, T, d, 3400, True, False, dtype))
+    ref = _oracle_grads(*case, d, C)
+    from qllm2_amd.pam_scan import pam_scan_planar
+    dev = torch.device("cuda")
+    q, k, v, gamma, dy, ds, phase, routing, _ = case
+    planes = [x[..., i].contiguous().to(dtype).to(dev).requires_grad_(True) for x in (q, k, v) for i in (0, 1)]
+    # [B,T,H,M] storage, [M,B,H,T] views
+    gam = gamma.permute(1, 3, 2, 0).contiguous().to(dev).requires_grad_(True)
+    ph = phase.permute(1, 3, 2, 0).contiguous().to(dev).requires_grad_(True)
+    ro = routing.permute(1, 3, 2, 0).contiguous().to(dev).requires_grad_(True)
+    g4, p4, r4 = (x.permute(3, 0, 2, 1) for x in (gam, ph, ro))
+    assert not g4.is_contiguous()
+    rot = (r4 * torch.cos(p4), r4 * torch.sin(p4))
+    y_re, y_im, s_re, s_im = pam_scan_planar(*planes, g4, q_scale=d ** -0.5, chunk=C, rot=rot)
+    dyd, dsd = dy.to(dev), ds.to(dev)
+    ((y_re * dyd[..., 0]).sum() + (y_im * dyd[..., 1]).sum() + (s_re * dsd[..., 0]).sum()
+     + (s_im * dsd[..., 1]).sum()).backward()
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    for name, got, want in (("dgamma", gam.grad, ref[3]), ("dphase", ph.grad, ref[4]), ("drouting", ro.grad, ref[5])):
+        got = got.permute(3, 0, 2, 1).cpu()
+        assert _rel(got, want) < tol, f"{name}: rel {_rel(got, want):.2e}"
+
+
 def test_scan_backward_bf16_e3(gpu_lib):
     M, B, H, T, d, C = 3, 2, 2, 512, 64, 64
     case = _case(M, B, H, T, d, 3303, False, False, torch.bfloat16)

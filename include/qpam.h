@@ -168,6 +168,22 @@ typedef struct {
 size_t qpam_scan_workspace_size(const qpam_scan_args *a);
 int qpam_scan_fwd(const qpam_scan_args *a, void *stream);
 
+/* Allocation-free variant of qpam_scan_fwd.  It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results as qpam_scan_fwd, except that
+ * `workspace` / `workspace_bytes` are ignored: the per-chunk states live in a
+ * device array of QPAM_SCAN_FWD_NOALLOC_MAX_BYTES bytes inside the library
+ * (one per GPU, held until the process ends).  A call whose states need more
+ * (qpam_scan_workspace_size) fails with QPAM_ERR_WORKSPACE before any launch;
+ * 64 MiB covers one 2048-token sequence of 12 heads with up to 4 fp32 states.
+ * Every call on a GPU shares that GPU's array and it keeps only the last
+ * call's states: calls that overlap on one GPU (two streams or threads) race,
+ * and no qpam_scan_bwd can follow (training uses qpam_scan_fwd).  The call
+ * allocates nothing (no hipMalloc, no library allocation). */
+#define QPAM_SCAN_FWD_NOALLOC_MAX_BYTES (64u << 20)
+int qpam_scan_fwd_noalloc(const qpam_scan_args *a, void *stream);
+
 /* Backward of qpam_scan_fwd.  `fwd` must describe the same call whose
  * workspace still holds the per-chunk states.  dy: planar fp32 (or bf16, dy_dtype) [B,H,T,d];
  * ds: optional gradient of the final state, planar fp32 [M,B,H,d,d].

@@ -17,6 +17,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
 QPAM_BF16 = 1
+QPAM_ERR_WORKSPACE = 4
+QPAM_SCAN_FWD_NOALLOC_MAX_BYTES = 64 << 20
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -165,6 +167,7 @@ SIGNATURES = {
     "qpam_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_ptr]),
     "qpam_scan_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(ScanArgs)]),
     "qpam_scan_fwd": (ctypes.c_int, [ctypes.POINTER(ScanArgs), c_ptr]),
+    "qpam_scan_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(ScanArgs), c_ptr]),
     "qpam_scan_bwd_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(ScanBwdArgs)]),
     "qpam_scan_bwd": (ctypes.c_int, [ctypes.POINTER(ScanBwdArgs), c_ptr]),
     "qpam_decay_matrix": (ctypes.c_int, [c_i32, c_i32, c_ptr, c_i64, c_ptr, c_ptr]),

@@ -18,6 +18,9 @@
 // chunk's log-decay prefix sums held in LDS.  The score tile is computed
 // transposed (rows s, cols t) so the MFMA accumulator layout is directly the
 // A operand of the (W . D~) V product.
+#include <map>
+#include <mutex>
+
 #include "scan_common.h"
 
 namespace qpam {
@@ -1101,4 +1104,54 @@ extern "C" size_t qpam_scan_workspace_size(const qpam_scan_args *a) {
 
 extern "C" int qpam_scan_fwd(const qpam_scan_args *a, void *stream) {
     return qpam::scan::scan_fwd(a, (hipStream_t)stream);
+}
+
+// ------------------------------------------------ allocation-free entry --
+// qpam_scan_fwd with the per-chunk states in `scratch`, a device array of the
+// library (one copy per GPU, alive until the process ends), instead of a
+// caller workspace.  Host code never passes the array's name to a kernel (on
+// the host it is only a stand-in for the symbol): the device address comes
+// from hipGetSymbolAddress, once per device, kept in scratch_ptr's table.
+// The forward kernels overwrite every workspace word they later read, so no
+// part of the array has to start at zero.
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[QPAM_SCAN_FWD_NOALLOC_MAX_BYTES];
+
+int scratch_ptr(void **out) {
+    static std::mutex mu;
+    static std::map<int, void *> ptrs;
+    int dev = 0;
+    QPAM_CHECK_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = ptrs.find(dev);
+    if (it == ptrs.end()) {
+        void *p = nullptr;
+        QPAM_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        QPAM_REQUIRE(p != nullptr && ((uintptr_t)p % 256) == 0, "qpam_scan_fwd_noalloc: bad scratch address");
+        it = ptrs.emplace(dev, p).first;
+    }
+    *out = it->second;
+    return QPAM_OK;
+}
+
+}  // namespace
+
+extern "C" int qpam_scan_fwd_noalloc(const qpam_scan_args *a, void *stream) {
+    QPAM_REQUIRE(a != nullptr, "qpam_scan_fwd_noalloc: null args");
+    QPAM_REQUIRE(a->B >= 1 && a->H >= 1 && a->T >= 1 && a->M >= 1 && a->C >= 1,
+                 "qpam_scan_fwd_noalloc: bad sizes B=%d H=%d T=%d M=%d C=%d", a->B, a->H, a->T, a->M, a->C);
+    const size_t need = qpam::scan::fwd_workspace_bytes(*a);
+    if (need > (size_t)QPAM_SCAN_FWD_NOALLOC_MAX_BYTES)
+        return qpam::fail(QPAM_ERR_WORKSPACE,
+                          "qpam_scan_fwd_noalloc: this call needs %zu bytes of scan state, the library's scratch "
+                          "holds %zu (use qpam_scan_fwd with a caller workspace)",
+                          need, (size_t)QPAM_SCAN_FWD_NOALLOC_MAX_BYTES);
+    void *ptr = nullptr;
+    int st = scratch_ptr(&ptr);
+    if (st) return st;
+    qpam_scan_args b = *a;
+    b.workspace = ptr;
+    b.workspace_bytes = (size_t)QPAM_SCAN_FWD_NOALLOC_MAX_BYTES;
+    return qpam::scan::scan_fwd(&b, (hipStream_t)stream);
 }

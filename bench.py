@@ -40,8 +40,8 @@ def parse():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=1000)
-    ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "e3", "ce", "cplx", "layer", "delta",
-                                       "copy"], default=None,
+    ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "engine", "e3", "ce", "cplx", "layer",
+                                       "delta", "copy"], default=None,
                     help="run one workload (for profiler passes) and print its own JSON line")
     return ap.parse_args()
 
@@ -191,6 +191,43 @@ def bench_decode_e3_rope(n_steps):
     return {"ms_per_step": ms, "tokens_per_s": active / (ms * 1e-3), "active_slots": active,
             "hbm_GBps": bytes_step / (ms * 1e-3) / 1e9, "hbm_frac": bytes_step / (ms * 1e-3) / HBM_PEAK,
             "bytes_per_step": bytes_step, "steps": n_steps}
+
+
+def bench_engine(steps, warmup):
+    """Model-level continuous-batching decode (qllm2_amd.engine.DecodeEngine):
+    16 E3 PAM layers (M=3, H=12, d=64, dim=768, fp32, RoPE, GSP, phase-routed
+    states) over 256 slots, ~75% of them live per step.  A step runs every
+    layer on the live rows: projection GEMM, gate GEMMs, the prologue kernel,
+    one decode launch with per-slot RoPE, the o_proj GEMM."""
+    import torch
+    from qllm2_amd.engine import DecodeEngine
+    S, L, H, d, M, dim = 256, 16, 12, 64, 3, 768
+    layers = [_BenchPamLayer(dim, H, d, M, 16, torch.float32, seed=40 + i).mod for i in range(L)]
+    engine = DecodeEngine(layers, n_slots=S, max_len=8192)
+    gen = torch.Generator().manual_seed(1015)
+    for s_ in range(S):
+        engine.admit(int(torch.randint(1, 4096, (1,), generator=gen)))
+    engine.pool.state.normal_(0.0, 0.01, generator=torch.Generator(device="cuda").manual_seed(1016))
+    hosts = [torch.nonzero(torch.rand(S, generator=gen) < 0.75).flatten().tolist() for _ in range(16)]
+    masks = [torch.tensor(h, dtype=torch.int32).cuda() for h in hosts]
+    xs = [torch.randn(len(h), dim, 2, generator=gen).cuda() for h in hosts]
+
+    def step(i):
+        engine.step(xs[i % 16], masks[i % 16], host_slots=hosts[i % 16])
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    active = sum(len(hosts[i % 16]) for i in range(steps)) / steps
+    return {"config": "16 PAM layers E3 M=3, H=12, d=64, dim=768, fp32, 256 slots (~75% live)",
+            "ms_per_step": ms, "tokens_per_s": active / (ms * 1e-3), "active_slots": active, "steps": steps}
 
 
 def bench_e3_fwd_bwd(steps, warmup):
@@ -590,6 +627,7 @@ def main():
                                            bench_scan_fwd(args.steps, args.warmup))),
               "decode": lambda: bench_decode(args.decode_steps),
               "decode_e3": lambda: bench_decode_e3_rope(max(50, args.decode_steps // 5)),
+              "engine": lambda: bench_engine(args.steps, args.warmup),
               "e3": lambda: bench_e3_fwd_bwd(args.steps, args.warmup),
               "ce": lambda: bench_ce(args.steps, args.warmup),
               "cplx": lambda: bench_complex_ops(args.steps, args.warmup),
@@ -628,6 +666,7 @@ def main():
     if not args.no_extras:
         out["extras"] = {"decode_config4": bench_decode(args.decode_steps),
                          "decode_e3_rope_slots": bench_decode_e3_rope(max(50, args.decode_steps // 5)),
+                         "decode_engine_e3_16_layers": bench_engine(20, 5),
                          # five untimed warmup steps: after two, the first timed steps still run
                          # slow (E3 0.69 vs 0.66 ms per step)
                          "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 5),

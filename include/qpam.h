@@ -117,6 +117,10 @@ typedef struct {
     const float *rope;      /* NULL = no rotation */
     const int32_t *pos;     /* [n_slots] device positions */
     int32_t rope_len;
+    /* 0: q, k, v, gamma, rot, y are indexed by slot id (rows of unlisted slots
+     * are ignored / left alone).  1: they are compact, row i belonging to the
+     * slot active[i] (n_active rows); S and pos stay indexed by slot id. */
+    int32_t vec_by_rank;
 } qpam_decode_args;
 
 int qpam_decode_step(const qpam_decode_args *a, void *stream);

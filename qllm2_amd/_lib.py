@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -37,7 +37,7 @@ class DecodeArgs(ctypes.Structure):
         ("gamma", c_ptr), ("sg_slot", c_i64), ("sg_group", c_i64), ("sg_state", c_i64),
         ("rot", c_ptr), ("sr_slot", c_i64), ("sr_group", c_i64), ("sr_state", c_i64),
         ("y", c_ptr), ("sy_slot", c_i64), ("sy_group", c_i64),
-        ("rope", c_ptr), ("pos", c_ptr), ("rope_len", c_i32),
+        ("rope", c_ptr), ("pos", c_ptr), ("rope_len", c_i32), ("vec_by_rank", c_i32),
     ]
 
 

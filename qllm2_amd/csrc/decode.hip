@@ -15,7 +15,11 @@
 // halves the number of live partial sums).  Slots that are not listed cost
 // nothing: the grid is n_active * n_groups.
 //
-// Optional per-slot rotary positions rotate q and k as they are loaded.
+// Optional per-slot rotary positions rotate q and k as they are loaded.  With
+// vec_by_rank the per-token operands (q, k, v, gamma, rot, y) are the compact
+// rows of the listed slots (row i for active[i]): a continuous-batching engine
+// projects only its live sequences and needs no scatter into slot-sized
+// buffers; states and positions stay indexed by slot.
 //
 // Kernels: the single-state, unrotated step (the continuous-batching common
 // case) keeps every register for loads in flight, 512 threads per 64 x 64
@@ -124,18 +128,19 @@ __global__ void __launch_bounds__((DecodeShape<D, 512>::THREADS)) decode_single_
     const int g = blockIdx.x - ai * a.n_groups;
     const int slot = a.active ? a.active[ai] : ai;
     if (slot < 0 || slot >= a.n_slots) return;
+    const int vr = a.vec_by_rank ? ai : slot;   // row of q, k, v, gamma, rot, y
     const int cp = tid % S::PAIRS, r0 = tid / S::PAIRS, lane = tid & 63;
-    float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
-    float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    float4 qv = *reinterpret_cast<const float4 *>(a.q + vr * a.sq_slot + g * a.sq_group + 4 * cp);
+    float4 kv = *reinterpret_cast<const float4 *>(a.k + vr * a.sk_slot + g * a.sk_group + 4 * cp);
     apply_rope<D>(a, slot, cp, qv, kv);
-    const float gam = a.gamma[slot * a.sg_slot + g * a.sg_group];
+    const float gam = a.gamma[vr * a.sg_slot + g * a.sg_group];
     float part[S::NV];
-    update_state<S>(a.state + slot * a.st_slot + g * a.st_group, tid, r0, gam, a.v + slot * a.sv_slot + g * a.sv_group,
+    update_state<S>(a.state + slot * a.st_slot + g * a.st_group, tid, r0, gam, a.v + vr * a.sv_slot + g * a.sv_group,
                     kv, qv.x * a.q_scale, qv.y * a.q_scale, qv.z * a.q_scale, qv.w * a.q_scale, part);
     int base, nv;
     halving_reduce<S::NV, S::PAIRS>(part, lane, base, nv);
     if ((lane & S::bfly_mask()) == 0) {
-        float *yp = a.y + slot * a.sy_slot + g * a.sy_group;
+        float *yp = a.y + vr * a.sy_slot + g * a.sy_group;
 #pragma unroll
         for (int j = 0; j < S::NV; ++j) {
             if (j < nv) {
@@ -161,6 +166,7 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
     const int g = blockIdx.x - ai * a.n_groups;
     const int slot = a.active ? a.active[ai] : ai;
     if (slot < 0 || slot >= a.n_slots) return;
+    const int vr = a.vec_by_rank ? ai : slot;   // row of q, k, v, gamma, rot, y
     const int cp = tid % S::PAIRS, r0 = tid / S::PAIRS, lane = tid & 63;
     float *st0 = a.state + slot * a.st_slot + g * a.st_group;
     floatx4 s[MS][S::ITERS];
@@ -170,11 +176,11 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
         for (int it = 0; it < S::ITERS; ++it)
             s[m][it] = __builtin_nontemporal_load(
                 reinterpret_cast<const floatx4 *>(st0 + m * a.st_state + 4 * (it * S::THREADS + tid)));
-    float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
-    float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    float4 qv = *reinterpret_cast<const float4 *>(a.q + vr * a.sq_slot + g * a.sq_group + 4 * cp);
+    float4 kv = *reinterpret_cast<const float4 *>(a.k + vr * a.sk_slot + g * a.sk_group + 4 * cp);
     apply_rope<D>(a, slot, cp, qv, kv);
     const float q0r = qv.x * a.q_scale, q0i = qv.y * a.q_scale, q1r = qv.z * a.q_scale, q1i = qv.w * a.q_scale;
-    const float *vrow = a.v + slot * a.sv_slot + g * a.sv_group;
+    const float *vrow = a.v + vr * a.sv_slot + g * a.sv_group;
     float2 vv[S::ITERS];
 #pragma unroll
     for (int it = 0; it < S::ITERS; ++it) vv[it] = *reinterpret_cast<const float2 *>(vrow + 2 * (it * S::ROWS_PER_IT + r0));
@@ -183,10 +189,10 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
     for (int j = 0; j < S::NV; ++j) tot[j] = 0.f;
 #pragma unroll
     for (int m = 0; m < MS; ++m) {
-        const float gam = a.gamma[slot * a.sg_slot + g * a.sg_group + m * a.sg_state];
+        const float gam = a.gamma[vr * a.sg_slot + g * a.sg_group + m * a.sg_state];
         float rr = 1.f, ri = 0.f;
         if (a.rot) {
-            const float *rp = a.rot + slot * a.sr_slot + g * a.sr_group + m * a.sr_state;
+            const float *rp = a.rot + vr * a.sr_slot + g * a.sr_group + m * a.sr_state;
             rr = rp[0];
             ri = rp[1];
         }
@@ -209,7 +215,7 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
     int base, nv;
     halving_reduce<S::NV, S::PAIRS>(tot, lane, base, nv);
     if ((lane & S::bfly_mask()) == 0) {
-        float *yp = a.y + slot * a.sy_slot + g * a.sy_group;
+        float *yp = a.y + vr * a.sy_slot + g * a.sy_group;
 #pragma unroll
         for (int j = 0; j < S::NV; ++j) {
             if (j < nv) {
@@ -234,19 +240,20 @@ __global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS
     const int g = blockIdx.x - ai * a.n_groups;
     const int slot = a.active ? a.active[ai] : ai;
     if (slot < 0 || slot >= a.n_slots) return;  // whole block exits together
+    const int vr = a.vec_by_rank ? ai : slot;   // row of q, k, v, gamma, rot, y
 
     const int cp = tid % S::PAIRS;      // this lane's key-column pair: j = 2cp, 2cp+1
     const int r0 = tid / S::PAIRS;      // first row of this lane
     const int lane = tid & 63;
 
-    float4 qv = *reinterpret_cast<const float4 *>(a.q + slot * a.sq_slot + g * a.sq_group + 4 * cp);
-    float4 kv = *reinterpret_cast<const float4 *>(a.k + slot * a.sk_slot + g * a.sk_group + 4 * cp);
+    float4 qv = *reinterpret_cast<const float4 *>(a.q + vr * a.sq_slot + g * a.sq_group + 4 * cp);
+    float4 kv = *reinterpret_cast<const float4 *>(a.k + vr * a.sk_slot + g * a.sk_group + 4 * cp);
     apply_rope<D>(a, slot, cp, qv, kv);
-    const float *vrow = a.v + slot * a.sv_slot + g * a.sv_group;
+    const float *vrow = a.v + vr * a.sv_slot + g * a.sv_group;
 
     float yacc_r = 0.f, yacc_i = 0.f;  // lanes tid < D accumulate row tid
     for (int m = 0; m < a.n_states; ++m) {
-        const float gam = a.gamma[slot * a.sg_slot + g * a.sg_group + m * a.sg_state];
+        const float gam = a.gamma[vr * a.sg_slot + g * a.sg_group + m * a.sg_state];
         float part[S::NV];
         update_state<S>(a.state + slot * a.st_slot + g * a.st_group + m * a.st_state, tid, r0, gam, vrow, kv,
                         qv.x * a.q_scale, qv.y * a.q_scale, qv.z * a.q_scale, qv.w * a.q_scale, part);
@@ -263,7 +270,7 @@ __global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS
         if (tid < D) {
             const float yr = ys[tid][0], yi = ys[tid][1];
             if (a.rot) {
-                const float *rp = a.rot + slot * a.sr_slot + g * a.sr_group + m * a.sr_state;
+                const float *rp = a.rot + vr * a.sr_slot + g * a.sr_group + m * a.sr_state;
                 const float rr = rp[0], ri = rp[1];
                 yacc_r += rr * yr - ri * yi;
                 yacc_i += rr * yi + ri * yr;
@@ -275,7 +282,7 @@ __global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS
         __syncthreads();
     }
     if (tid < D) {
-        float *yp = a.y + slot * a.sy_slot + g * a.sy_group + 2 * tid;
+        float *yp = a.y + vr * a.sy_slot + g * a.sy_group + 2 * tid;
         *reinterpret_cast<float2 *>(yp) = make_float2(yacc_r, yacc_i);
     }
 }

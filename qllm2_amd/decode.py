@@ -23,27 +23,34 @@ def _check_cuda(*ts):
             raise ValueError("qpam decode: tensors must be on the GPU (no CPU path in this library)")
 
 
-def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, out=None, rope=None, pos=None):
+def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, out=None, rope=None, pos=None,
+                compact=False):
     """In-place ragged decode step over a slot pool.
 
     state  [S, G, M, d, d, 2] fp32 (G = layers*heads, M states), updated in place
-    q,k,v  [S, G, d, 2] fp32 (q unscaled; multiplied by q_scale)
-    gamma  [S, G, M] fp32
+    q,k,v  [R, G, d, 2] fp32 (q unscaled; multiplied by q_scale)
+    gamma  [R, G, M] fp32 (any strides)
     active optional int32 [n] slot ids (others untouched); None = all slots
-    rot    optional [S, G, M, 2] fp32 complex rotation of each state's read
+    rot    optional [R, G, M, 2] fp32 complex rotation of each state's read
     rope   optional [P, d, 2] fp32 rotary table (build_rope_cache) with
     pos    int32 [S] per-slot positions: q and k of slot a are rotated by rope[pos[a]]
-    Returns y [S, G, d, 2] (rows of unlisted slots are left as in `out`/zero).
+    compact False: R = S, row a of q, k, v, gamma, rot, y belongs to slot a
+           True:  R = n, row i belongs to slot active[i] (the live batch of an engine)
+    Returns y [R, G, d, 2] (without `compact`, rows of unlisted slots are left
+    as in `out` / zero).
     """
     _check_cuda(state, q, k, v, gamma, active, rot, rope, pos)
     if state.dim() != 6 or state.shape[-1] != 2 or state.shape[-2] != state.shape[-3]:
         raise ValueError(f"state must be [S,G,M,d,d,2], got {tuple(state.shape)}")
     n_slots, n_groups, n_states, d = state.shape[:4]
+    if compact and active is None:
+        raise ValueError("compact rows need the active slot list")
+    rows = active.numel() if compact else n_slots
     for name, t in (("q", q), ("k", k), ("v", v)):
-        if tuple(t.shape) != (n_slots, n_groups, d, 2):
-            raise ValueError(f"{name} must be [{n_slots},{n_groups},{d},2], got {tuple(t.shape)}")
-    if tuple(gamma.shape) != (n_slots, n_groups, n_states):
-        raise ValueError(f"gamma must be [{n_slots},{n_groups},{n_states}], got {tuple(gamma.shape)}")
+        if tuple(t.shape) != (rows, n_groups, d, 2):
+            raise ValueError(f"{name} must be [{rows},{n_groups},{d},2], got {tuple(t.shape)}")
+    if tuple(gamma.shape) != (rows, n_groups, n_states):
+        raise ValueError(f"gamma must be [{rows},{n_groups},{n_states}], got {tuple(gamma.shape)}")
     for t in (state, q, k, v, gamma) + ((rot,) if rot is not None else ()):
         if t.dtype != torch.float32:
             raise ValueError("qpam decode works on fp32 tensors")
@@ -51,8 +58,8 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
         raise ValueError("state matrices must be contiguous [d, d, 2]")
     q, k, v = (t if t.stride()[-2:] == (2, 1) else t.contiguous() for t in (q, k, v))
     if rot is not None:
-        if tuple(rot.shape) != (n_slots, n_groups, n_states, 2):
-            raise ValueError("rot must be [S,G,M,2]")
+        if tuple(rot.shape) != (rows, n_groups, n_states, 2):
+            raise ValueError(f"rot must be [{rows},{n_groups},{n_states},2]")
         rot = rot if rot.stride(-1) == 1 else rot.contiguous()
     y = out if out is not None else torch.zeros_like(q)
     if active is not None:
@@ -64,6 +71,7 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
         n_active = n_slots
     a = _lib.DecodeArgs()
     a.n_slots, a.n_active, a.n_groups, a.n_states, a.d = n_slots, n_active, n_groups, n_states, d
+    a.vec_by_rank = int(bool(compact))
     a.active = active.data_ptr() if active is not None else None
     a.q_scale = float(q_scale)
     a.state = state.data_ptr()
@@ -188,22 +196,29 @@ class SlotPool:
         if max_pos >= self.rope.shape[0]:
             self.rope = build_rope_cache(2 * (max_pos + 1), self.head_dim, device=self.device)
 
-    def step(self, layer, q, k, v, gamma, active, rot=None, q_scale=None, out=None):
+    def step(self, layer, q, k, v, gamma, active, rot=None, q_scale=None, out=None, compact=False):
         """One token for the listed slots on one layer: q, k, v [n_slots, heads, d, 2]
         (rows of unlisted slots ignored; q unscaled), gamma [n_slots, heads, states],
-        rot optional [n_slots, heads, states, 2].  RoPE at each slot's position; the
+        rot optional [n_slots, heads, states, 2]; with `compact` the rows are those of
+        the listed slots in order ([n_active, ...]).  RoPE at each slot's position; the
         table is grown first (doubling) when a live slot's position passes its end."""
         scale = self.head_dim ** -0.5 if q_scale is None else q_scale
         if self.live:
             self.ensure_len(max(self._host_pos[s] for s in self.live))
         return decode_step(self.layer_state(layer), q, k, v, gamma, active=active, rot=rot, q_scale=scale,
-                           out=out, rope=self.rope, pos=self.pos)
+                           out=out, rope=self.rope, pos=self.pos, compact=compact)
 
-    def advance(self, active):
-        """Move the listed slots (an int tensor or a list of slot ids) one token on."""
-        ids = active.tolist() if torch.is_tensor(active) else list(active)
-        for s in ids:
+    def advance(self, active, host_ids=None):
+        """Move the listed slots one token on.  active: an int tensor or a list
+        of slot ids; host_ids: the same ids as a host list when `active` is a
+        device tensor (saves reading it back, a host synchronisation)."""
+        if host_ids is None:
+            host_ids = active.tolist() if torch.is_tensor(active) else list(active)
+        for s in host_ids:
             self._host_pos[int(s)] += 1
-        idx = active.long() if torch.is_tensor(active) else torch.tensor(ids, dtype=torch.long)
-        self.pos[idx.to(self.device)] += 1
+        if torch.is_tensor(active):
+            idx = active.to(self.device, torch.long)
+        else:
+            idx = torch.tensor(host_ids, dtype=torch.long).to(self.device)
+        self.pos[idx] += 1
 

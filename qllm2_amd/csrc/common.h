@@ -44,6 +44,11 @@ struct SideStream {
 int side_stream(SideStream *&out);
 std::mutex &side_stream_mutex();
 
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector-memory
+// operations are outstanding and leaves the other counters unconstrained:
+// vmcnt is split over bits [3:0] and [15:14], expcnt is bits [6:4], lgkmcnt [11:8]
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
+
 inline int launch_status(const char *what) {
     hipError_t err = hipGetLastError();
     if (err != hipSuccess) return fail(QPAM_ERR_HIP, "%s launch failed: %s", what, hipGetErrorString(err));

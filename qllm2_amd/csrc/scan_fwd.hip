@@ -5,14 +5,16 @@
 // (v11/model.py:657-781) for M states with rotations r_m = alpha e^{i phi}.
 //
 // The only sequential dependency of the scan is the d x d state carry, and the
-// state rows are independent, so the forward is split into three launches:
-//   1. chunk_state  (chunk-parallel, MFMA): per chunk c and state m the write
-//      dS_m,c = sum_s D_m[C-1,s] v_s (x) conj(k_s) and the chunk decay
-//      total_m,c -> workspace;
-//   2. state_scan   (elementwise, sequential over chunks): replaces dS_m,c by
-//      the state entering chunk c, S_in = prod-decayed prefix, and writes the
-//      final state;
-//   3. chunk_output (chunk-parallel, MFMA): Y_c = (W . D~) V + sum_m rho_m
+// state rows are independent, so the forward is split into a state pass and a
+// chunk-parallel output pass:
+//   fp32 inputs: state_pass_f32 (sequential over chunks, MFMA, the state in
+//      registers): per chain (m, b, h) the state entering every chunk -> workspace,
+//      S_m <- total_m,c S_m + dS_m,c with dS_m,c = sum_s D_m[C-1,s] v_s (x) conj(k_s),
+//      chunk totals, the final state;
+//   bf16 inputs with 16- or 32-step chunks: chunk_state (chunk-parallel increments
+//      dS_m,c -> workspace) then state_scan (the prefix over chunks, in place);
+//   bf16 inputs with 64-step chunks: state_pass_bf16 (bf16 snapshots);
+//   then chunk_output (chunk-parallel, MFMA): Y_c = (W . D~) V + sum_m rho_m
 //      (Q~ S_in,m^T) with W = Q~ K^H, D~ = sum_m r_m D_m, rho_m = r_m cum_m.
 // Decay matrices are never materialised: each lane rebuilds D[t,s] from the
 // chunk's log-decay prefix sums held in LDS.  The score tile is computed
@@ -33,6 +35,7 @@ struct FwdParams {
     float *states;         // [M][B][H][n][2][64][64]
     float *totals;         // [M][B][H][n]
     unsigned short *snap;  // bf16 path: [M][B][H][n][2][64][64] bf16 entering states (else null)
+    float *dlast;          // fp32 64-step path: [M][B][H][n][64] D[C-1, s] of every chunk (else null)
 };
 
 __device__ __forceinline__ float *chunk_state_ptr(const FwdParams &p, int m, int b, int h, int c) {
@@ -378,6 +381,195 @@ __global__ void __launch_bounds__(THREADS) chunk_output_f32_kernel(FwdParams p) 
             }
     }
 }
+
+// ---------------------------------------------------- fp32 state pass --
+// fp32 inputs: the carried state of every chain (m, b, h) walks its chunks in
+// registers, one launch for what chunk_state + state_scan do in two with the
+// per-chunk increments written to HBM and read back.  Block rb of a chain owns
+// value rows [16 rb, 16 rb + 16) (rows of the recurrence are independent); of
+// its 8 waves, wave (half, w) owns key columns [16 w, 16 w + 16) and half of
+// the chunk's tokens, so the first-half wave keeps a 4 x 1 piece of S per
+// plane.  Per chunk: store the entering state (the output kernel and the
+// backward read it), form both halves' products for dS = sum_s D[C-1,s] v_s
+// conj(k_s) on MFMA (operands straight from global memory in MFMA layout, the
+// next two chunks' loads in flight), add the second half's through LDS,
+// S <- total S + dS.  The pass is a dependency chain over the chunks, so its
+// speed is the latency of one step: eight waves per block halve each wave's
+// MFMA chain and give the SIMDs twice the waves to switch between.
+// Measured alternative not kept: one launch in which each chunk's block hands
+// the state to the next one through device memory (release / acquire flags)
+// costs 7-9 us per hand-off alone and 16-21 us with 96 chains in flight on
+// MI355X, so a 32-chunk chain took 0.89 ms against 0.31 ms for three launches.
+constexpr int PASS32_SPLIT = 2;      // row blocks per chain (32 value rows each)
+constexpr int PASS32_THREADS = 512;  // 8 waves: 2 row tiles x 4 column tiles of 16 x 16
+
+// One LDS stage of the pass, one flat array (the compiler's tracking of
+// direct-to-LDS loads tells whole arrays apart, so each stage is one object):
+// the chunk's K tile [64 tokens][64 columns] per plane at P32_KR / P32_KI, the
+// block's V slice [64 tokens][32 value rows] per plane at P32_VR / P32_VI,
+// fp32, and the chunk's 64 gammas at P32_G + 64 wv (each wave loads its own copy,
+// so every wave issues the same memory operations).  Rows are stored as 16-byte chunks
+// XOR-swizzled so that the MFMA-layout reads (16 lanes along a row, four rows
+// s = 4 ks + g) hit 64 distinct banks: K chunk c of row r at c ^ ((r & 3) << 2),
+// V chunk c of row r at c ^ (((r >> 1) & 1) << 2).
+constexpr int P32_KR = 0, P32_KI = 64 * 64, P32_VR = 2 * 64 * 64, P32_VI = P32_VR + 64 * 32,
+              P32_DL = P32_VI + 64 * 32, P32_TOT = P32_DL + 8 * 64, P32_STAGE = P32_TOT + 8 * 64;
+
+__device__ __forceinline__ float pass32_k(const float *plane, int s, int col) {
+    return plane[s * 64 + 4 * ((col >> 2) ^ ((s & 3) << 2)) + (col & 3)];
+}
+
+__device__ __forceinline__ float pass32_v(const float *plane, int s, int col) {
+    return plane[s * 32 + 4 * ((col >> 2) ^ (((s >> 1) & 1) << 2)) + (col & 3)];
+}
+
+// Direct global -> LDS loads of chunk c (tokens from c0 = 64 c) into stage `st`:
+// six 1 KiB loads per wave (K: 16 rows of 64 floats per load, V: 32 rows of 32
+// floats per two loads) and the wave's copies of the chunk's decay weights and
+// total (`drow`, `tot`: this chain's entries of the pre-pass outputs); rows
+// beyond the sequence re-read row T-1 (their decay weight is zero).
+__device__ __forceinline__ void pass32_dma(float *st, const qpam_scan_args &a, const float *kre, const float *kim,
+                                           const float *vre, const float *vim, const float *drow, const float *tot,
+                                           int c, int i0, int wv, int lane) {
+    const int last = a.T - 1, c0 = 64 * c;
+    __builtin_amdgcn_global_load_lds(drow + 64 * (int64_t)c + lane, st + P32_DL + 64 * wv, 4, 0, 0);
+    __builtin_amdgcn_global_load_lds(tot + c, st + P32_TOT + 64 * wv, 4, 0, 0);
+#pragma unroll
+    for (int q2 = 0; q2 < 2; ++q2) {
+        const int q = 2 * wv + q2;                  // K load q: rows 4q .. 4q+3
+        const int r = 4 * q + (lane >> 4), slot = lane & 15;
+        const int c = slot ^ ((r & 3) << 2);
+        const int64_t o = (int64_t)min(c0 + r, last) * a.k.s2 + 4 * c;
+        __builtin_amdgcn_global_load_lds(kre + o, st + P32_KR + q * 256, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(kim + o, st + P32_KI + q * 256, 16, 0, 0);
+    }
+    {
+        const int r = 8 * wv + (lane >> 3), slot = lane & 7;  // V load wv: rows 8wv .. 8wv+7
+        const int c = slot ^ (((r >> 1) & 1) << 2);
+        const int64_t o = (int64_t)min(c0 + r, last) * a.v.s2 + i0 + 4 * c;
+        __builtin_amdgcn_global_load_lds(vre + o, st + P32_VR + wv * 256, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vim + o, st + P32_VI + wv * 256, 16, 0, 0);
+    }
+}
+
+// s_waitcnt vmcnt(16), the other counters unconstrained.  Every wave issues the
+// same operations per step: eight direct loads, then eight state stores; at
+// most 16 operations issued after the previous step's last direct load may
+// still run, and memory operations complete in order, so that step's loads
+// have landed.
+constexpr int PASS32_WAIT = waitcnt_vm(16);
+
+// Decay weights of every (chain, chunk) for the state pass, all chunks at once
+// (a wave per chunk): D[C-1, s] = exp(min(L_last - L_s, 0)) (0 beyond the
+// chunk) and the chunk's total decay exp(L_last), L the inclusive prefix of
+// log(gamma + 1e-6).  The sequential pass then does no scan of its own.
+__global__ void __launch_bounds__(THREADS) chunk_decay_f32_kernel(FwdParams p) {
+    const qpam_scan_args &a = p.a;
+    const int lane = threadIdx.x & 63;
+    const int64_t item = (int64_t)blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6);
+    const int n = p.n_chunks;
+    if (item >= (int64_t)a.M * a.B * a.H * n) return;  // whole waves exit together
+    const int c = (int)(item % n);
+    const int64_t chain = item / n;
+    const int bh = (int)(chain % (a.B * a.H)), m = (int)(chain / (a.B * a.H));
+    const int b = bh / a.H, h = bh % a.H;
+    const int c0 = c * 64, valid = min(64, a.T - c0);
+    const float L = chunk_log_prefix(a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t, a.sg_t,
+                                     valid, lane);
+    const float Llast = __shfl(L, valid - 1);
+    p.dlast[item * 64 + lane] = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
+    if (lane == 0) p.totals[item] = __expf(Llast);
+}
+
+__device__ __forceinline__ void state_pass_f32_body(const FwdParams &p) {
+    __shared__ __align__(16) float st0[P32_STAGE], st1[P32_STAGE], st2[P32_STAGE];
+    const qpam_scan_args &a = p.a;
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int rt = wv >> 2, w = wv & 3;  // row tile, column tile
+    const int rb = blockIdx.x % PASS32_SPLIT, chain = blockIdx.x / PASS32_SPLIT;
+    const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
+    const int b = bh / a.H, h = bh % a.H;
+    const int n = p.n_chunks;
+    const int i0 = 32 * rb;                                  // the block's value rows
+    const int ri = i0 + 16 * rt + 4 * g, j = 16 * w + l16;   // this lane's S rows ri + r, column j
+    const float *kre = (const float *)a.k.re + b * a.k.s0 + h * a.k.s1;
+    const float *kim = (const float *)a.k.im + b * a.k.s0 + h * a.k.s1;
+    const float *vre = (const float *)a.v.re + b * a.v.s0 + h * a.v.s1;
+    const float *vim = (const float *)a.v.im + b * a.v.s0 + h * a.v.s1;
+    const float *drow = p.dlast + (int64_t)chain * n * 64;   // this chain's decay weights
+    const float *tot = p.totals + (int64_t)chain * n;
+
+    float sr[4], si[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int64_t o = (int64_t)chain * D * D + (ri + r) * D + j;
+        sr[r] = a.s0_re ? a.s0_re[o] : 0.f;
+        si[r] = a.s0_re ? a.s0_im[o] : 0.f;
+    }
+    pass32_dma(st0, a, kre, kim, vre, vim, drow, tot, 0, i0, wv, lane);
+    pass32_dma(st1, a, kre, kim, vre, vim, drow, tot, min(1, n - 1), i0, wv, lane);
+    // chunk 0's loads are the oldest: wait for them (chunk 1's eight may still run)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
+    __builtin_amdgcn_s_barrier();
+
+    // one chunk: stream chunk c+2 into NXT, store S_in(c), dS from CUR, S <- total S + dS
+    // (the stages rotate through three unrolled steps)
+#define QPAM_PASS32_STEP(CUR, NXT)                                                                     \
+    {                                                                                                  \
+        pass32_dma(NXT, a, kre, kim, vre, vim, drow, tot, min(c + 2, n - 1), i0, wv, lane);            \
+        float *dst = chunk_state_ptr(p, m, b, h, c);                                                   \
+        _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                                \
+            dst[(ri + r) * D + j] = sr[r];                                                             \
+            dst[D * D + (ri + r) * D + j] = si[r];                                                     \
+        }                                                                                              \
+        __builtin_amdgcn_sched_barrier(0);                                                             \
+        float d_[16], vr_[16], vi_[16], kr_[16], ki_[16];                                              \
+        _Pragma("unroll") for (int ks = 0; ks < 16; ++ks) {                                            \
+            const int s_ = 4 * ks + g;                                                                 \
+            d_[ks] = CUR[P32_DL + 64 * wv + s_];                                                       \
+            vr_[ks] = pass32_v(CUR + P32_VR, s_, 16 * rt + l16);                                       \
+            vi_[ks] = pass32_v(CUR + P32_VI, s_, 16 * rt + l16);                                       \
+            kr_[ks] = pass32_k(CUR + P32_KR, s_, j);                                                   \
+            ki_[ks] = pass32_k(CUR + P32_KI, s_, j);                                                   \
+        }                                                                                              \
+        const float tc = CUR[P32_TOT + 64 * wv + lane];                                                \
+        floatx4 u1 = zero4(), u2 = zero4(), u3 = zero4();                                              \
+        _Pragma("unroll") for (int ks = 0; ks < 16; ++ks) {                                            \
+            const float vr = vr_[ks] * d_[ks], vi = vi_[ks] * d_[ks];                                  \
+            u1 = mfma4(vr, kr_[ks], u1);                                                               \
+            u2 = mfma4(vi, ki_[ks], u2);                                                               \
+            u3 = mfma4(vr + vi, kr_[ks] - ki_[ks], u3);                                                \
+        }                                                                                              \
+        _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                                \
+            sr[r] = tc * sr[r] + (u1[r] + u2[r]);                                                      \
+            si[r] = tc * si[r] + (u3[r] - u1[r] + u2[r]);                                              \
+        }                                                                                              \
+        __builtin_amdgcn_s_waitcnt(PASS32_WAIT);                                                       \
+        __builtin_amdgcn_s_barrier();                                                                  \
+        ++c;                                                                                           \
+    }
+    int c = 0;
+    while (c + 3 <= n) {
+        QPAM_PASS32_STEP(st0, st2)
+        QPAM_PASS32_STEP(st1, st0)
+        QPAM_PASS32_STEP(st2, st1)
+    }
+    if (c < n) QPAM_PASS32_STEP(st0, st2)
+    if (c < n) QPAM_PASS32_STEP(st1, st0)
+#undef QPAM_PASS32_STEP
+    // drain the direct loads still in flight before the wave ends
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    if (a.s_re) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t o = (int64_t)chain * D * D + (ri + r) * D + j;
+            a.s_re[o] = sr[r];
+            a.s_im[o] = si[r];
+        }
+    }
+}
+
+__global__ void __launch_bounds__(PASS32_THREADS) state_pass_f32_kernel(FwdParams p) { state_pass_f32_body(p); }
 
 // Generic form (fp32 LDS tiles; used for bf16 inputs with 16- or 32-step chunks).
 template <typename Tin, int C>
@@ -996,15 +1188,28 @@ int launch_fwd(const FwdParams &p, hipStream_t stream) {
     constexpr bool f32 = std::is_same<Tin, float>::value;
     const void *out_kernel = f32 ? (const void *)chunk_output_f32_kernel<C> : (const void *)chunk_output_kernel<Tin, C>;
     const size_t s1 = state_smem<C>(), s3 = f32 ? output_f32_smem<C>() : output_smem<C>();
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_state_kernel<Tin, C>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
     QPAM_CHECK_HIP(hipFuncSetAttribute(out_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
-    hipLaunchKernelGGL((chunk_state_kernel<Tin, C>), grid, dim3(THREADS), s1, stream, p);
-    int st = launch_status("chunk_state_kernel");
-    if (st) return st;
-    hipLaunchKernelGGL(state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, stream, p);
-    st = launch_status("state_scan_kernel");
-    if (st) return st;
+    int st;
+    if constexpr (f32 && C == 64) {
+        const long long blocks = (long long)a.M * a.B * a.H * PASS32_SPLIT;
+        QPAM_REQUIRE(blocks < (1ll << 31), "qpam_scan_fwd: grid too large");
+        const long long items = (long long)a.M * a.B * a.H * p.n_chunks;
+        hipLaunchKernelGGL(chunk_decay_f32_kernel, dim3((unsigned)((items + 3) / 4)), dim3(THREADS), 0, stream, p);
+        st = launch_status("chunk_decay_f32_kernel");
+        if (st) return st;
+        hipLaunchKernelGGL(state_pass_f32_kernel, dim3((unsigned)blocks), dim3(PASS32_THREADS), 0, stream, p);
+        st = launch_status("state_pass_f32_kernel");
+        if (st) return st;
+    } else {
+        QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_state_kernel<Tin, C>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
+        hipLaunchKernelGGL((chunk_state_kernel<Tin, C>), grid, dim3(THREADS), s1, stream, p);
+        st = launch_status("chunk_state_kernel");
+        if (st) return st;
+        hipLaunchKernelGGL(state_scan_kernel, dim3(a.M * a.B * a.H * SCAN_BLOCKS), dim3(THREADS), 0, stream, p);
+        st = launch_status("state_scan_kernel");
+        if (st) return st;
+    }
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));
     if constexpr (f32) hipLaunchKernelGGL((chunk_output_f32_kernel<C>), grid, dim3(THREADS), s3, stream, p);
     else hipLaunchKernelGGL((chunk_output_kernel<Tin, C>), grid, dim3(THREADS), s3, stream, p);
@@ -1033,11 +1238,16 @@ size_t fwd_snapshot_offset(const qpam_scan_args &a) {
     return ((size_t)(fwd_totals_offset(a) + chains * n) * sizeof(float) + 255) & ~(size_t)255;
 }
 
+// fp32 path with 64-step chunks: the state pass's decay weights sit where the
+// snapshot path keeps its snapshots
+bool uses_dlast(const qpam_scan_args &a) { return a.dtype == QPAM_F32 && a.C == 64; }
+
 size_t fwd_workspace_bytes(const qpam_scan_args &a) {
     const int64_t n = (a.T + a.C - 1) / a.C;
     const int64_t chains = (int64_t)a.M * a.B * a.H;
     size_t bytes = fwd_snapshot_offset(a);
     if (uses_snapshots(a)) bytes += (size_t)chains * n * 2 * D * D * sizeof(unsigned short);
+    if (uses_dlast(a)) bytes += (size_t)chains * n * 64 * sizeof(float);
     return bytes;
 }
 
@@ -1085,6 +1295,7 @@ int scan_fwd(const qpam_scan_args *a, hipStream_t stream) {
     p.snap = uses_snapshots(*a)
                  ? reinterpret_cast<unsigned short *>((char *)a->workspace + fwd_snapshot_offset(*a))
                  : nullptr;
+    p.dlast = uses_dlast(*a) ? reinterpret_cast<float *>((char *)a->workspace + fwd_snapshot_offset(*a)) : nullptr;
     QPAM_REQUIRE(p.n_chunks <= 65535 && a->H <= 65535 && a->B <= 65535, "qpam_scan_fwd: grid too large");
     const bool bf = a->dtype == QPAM_BF16;
     if (uses_snapshots(*a)) return launch_fwd_bf16(p, stream);

@@ -172,12 +172,15 @@ def scan_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
 
 def fwd_workspace_bytes(M, B, H, T, chunk, bf16, d=64):
     """Forward workspace size, as qpam_scan_workspace_size computes it: fp32
-    per-chunk states (fp32 path) and chunk totals, then (bf16 inputs, chunk 64)
-    bf16 snapshots of the entering states at a 256-byte aligned offset."""
+    per-chunk states (fp32 path) and chunk totals, then at a 256-byte aligned
+    offset either (bf16 inputs, chunk 64) bf16 snapshots of the entering states
+    or (fp32 inputs, chunk 64) the state pass's per-chunk decay weights."""
     chains, n = M * B * H, (T + chunk - 1) // chunk
     snap = bf16 and chunk == 64
     off = (((0 if snap else chains * n * 2 * d * d) + chains * n) * 4 + 255) & ~255
-    return off + (chains * n * 2 * d * d * 2 if snap else 0)
+    if snap:
+        return off + chains * n * 2 * d * d * 2
+    return off + (chains * n * 64 * 4 if chunk == 64 else 0)
 
 
 @scan_fwd_op.register_fake

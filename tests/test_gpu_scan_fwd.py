@@ -115,3 +115,52 @@ def test_empty_batch_or_sequence_raises(gpu_lib, B, T):
     with pytest.raises((QpamError, ValueError, RuntimeError)):
         call(B, T)
     torch.cuda.synchronize()
+
+
+def _rel_per_chain(a, b):
+    """Max over (b, h) chains of that chain's max error over its max reference
+    value: a chain with small values cannot hide behind another's scale."""
+    a, b = a.double().flatten(0, 1).flatten(1), b.double().flatten(0, 1).flatten(1)
+    return ((a - b).abs().max(1).values / (b.abs().max(1).values + 1e-30)).max().item()
+
+
+@pytest.mark.parametrize("T,C,with_s0", [(64 * 37 + 13, 64, True), (64 * 37 + 13, 64, False), (40, 64, True),
+                                         (64, 64, False), (32 * 9 + 5, 32, True), (16 * 7, 16, False)])
+def test_fp32_state_pass_entering_states(gpu_lib, T, C, with_s0):
+    """fp32, one state: the state pass (the carried state of each chain walking
+    its chunks in registers) and the output kernel.  Y and the final state per
+    (b, h) chain against the oracle (with an initial state through the fused-E3
+    restatement, M = 1, no rotation), and the state entering every sampled chunk
+    -- what the output kernel and the backward read -- against the oracle's
+    state after that prefix."""
+    from qllm2_amd import pam_scan
+    B, H, d = 2, 3, 64
+    q, k, v, gamma = O.make_scan_inputs(B, H, T, d, 4100 + T, unit_qk=True, dtype=torch.float32)
+    g = torch.Generator().manual_seed(4101)
+    s0 = torch.randn(1, B, H, d, d, 2, generator=g) * 0.1 if with_s0 else None
+    pl = [x[..., i].contiguous().cuda() for x in (q, k, v) for i in (0, 1)]
+    s0p = (s0[..., 0].contiguous().cuda(), s0[..., 1].contiguous().cuda()) if with_s0 else (None, None)
+    out = pam_scan.scan_fwd_op(*pl, gamma.cuda(), None, None, *s0p, d ** -0.5, C, 0)
+    torch.cuda.synchronize()
+    y = torch.stack([out[0], out[1]], -1).cpu()
+    s = torch.stack([out[2], out[3]], -1).cpu()[0]
+    ws = out[4]
+
+    def oracle(t_end):
+        zero = torch.zeros(1, B, H, t_end)
+        return O.multistate_fused(q[:, :, :t_end].double(), k[:, :, :t_end].double(), v[:, :, :t_end].double(),
+                                  gamma[:, :, :, :t_end].double(), zero.double(), (zero + 1).double(), d, C,
+                                  state=s0.double() if with_s0 else None)
+
+    y_ref, s_ref = oracle(T)
+    assert _rel_per_chain(y, y_ref) < 1e-4, f"y {_rel_per_chain(y, y_ref):.2e}"
+    assert _rel_per_chain(s, s_ref[0]) < 1e-4, f"s {_rel_per_chain(s, s_ref[0]):.2e}"
+    n = (T + C - 1) // C
+    states = ws[:B * H * n * 2 * d * d].view(B, H, n, 2, d, d).cpu()
+    for c in sorted({1, 2, n // 2, n - 1} & set(range(1, n))):
+        _, s_c = oracle(c * C)
+        got = torch.stack([states[:, :, c, 0], states[:, :, c, 1]], -1)
+        assert _rel_per_chain(got, s_c[0]) < 1e-4, f"entering state of chunk {c}"
+    if with_s0:
+        got = torch.stack([states[:, :, 0, 0], states[:, :, 0, 1]], -1)
+        assert torch.equal(got, s0[0]), "the state entering chunk 0 is s0"

@@ -210,10 +210,11 @@ __device__ __forceinline__ bf16x8 ld_tr(const unsigned short *tile, int r0, int 
 }
 
 // One 16x16 accumulator tile of a complex matrix (element (4g + r, l16) of lane
-// 16g + l16) -> rows row0.., columns col0.. of two bf16 planes with row pitch D.
-// Adjacent lanes swap one row pair element (DPP quad_perm [1,0,3,2]) so that
-// each lane writes two consecutive columns of one row: a 4-byte store per plane
-// instead of two 2-byte stores.
+// 16g + l16) -> rows row0.., columns col0.. of two bf16 planes with row pitch
+// PITCH (D in global memory, PB in LDS).  Adjacent lanes swap one row pair
+// element (DPP quad_perm [1,0,3,2]) so that each lane writes two consecutive
+// columns of one row: a 4-byte store per plane instead of two 2-byte stores.
+template <int PITCH = D>
 __device__ __forceinline__ void acc_store_bf_pairs(unsigned short *dre, unsigned short *dim, const floatx4 &re,
                                                    const floatx4 &im, int row0, int col0) {
     const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
@@ -225,8 +226,8 @@ __device__ __forceinline__ void acc_store_bf_pairs(unsigned short *dre, unsigned
         const unsigned recv = (unsigned)__builtin_amdgcn_update_dpp(0, (int)send, 0xB1, 0xF, 0xF, false);
         const unsigned lo = odd ? recv : keep, hi = odd ? keep : recv;  // columns (l16 & ~1) and +1
         const int row = row0 + 4 * g + 2 * q + (odd ? 1 : 0), col = col0 + (l16 & ~1);
-        *reinterpret_cast<unsigned *>(dre + row * D + col) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-        *reinterpret_cast<unsigned *>(dim + row * D + col) = __builtin_amdgcn_perm(hi, lo, 0x07060302u);
+        *reinterpret_cast<unsigned *>(dre + row * PITCH + col) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        *reinterpret_cast<unsigned *>(dim + row * PITCH + col) = __builtin_amdgcn_perm(hi, lo, 0x07060302u);
     }
 }
 
@@ -253,6 +254,21 @@ __device__ __forceinline__ int causal_tile(int w) {
     return (w + 2 * ((lin >> 8) & 1)) & 3;
 }
 constexpr int PASS_SPLIT = 2;
+
+// bf16 path with 64-step chunks: the chunks of a chain are grouped in segments
+// of SEG chunks.  Segment increments are formed chunk-parallel, a short
+// elementwise scan links the segments, and the chunk kernels carry the state
+// (or its gradient) through the chunks of one segment in registers.
+constexpr int SEG = 4;
+constexpr int SEG_THREADS = 512;  // 8 waves per segment block
+
+// Forward-workspace offsets (in floats) of the segment data: segment totals
+// [chains][n_segs], weights wfwd and wbwd [chains][n * 64].
+struct SegLayout {
+    int n_segs;
+    int64_t segtot, wfwd, wbwd;
+};
+SegLayout seg_layout(const qpam_scan_args &a);
 // 64-row tiles of CW columns (64, or a 32-column half at column c0) held in
 // registers, NT threads of the block; 16-byte loads along the row.
 template <int NT, int CW = 64>

@@ -36,6 +36,12 @@ struct FwdParams {
     float *totals;         // [M][B][H][n]
     unsigned short *snap;  // bf16 path: [M][B][H][n][2][64][64] bf16 entering states (else null)
     float *dlast;          // fp32 64-step path: [M][B][H][n][64] D[C-1, s] of every chunk (else null)
+    // bf16 64-step path (segments of SEG chunks, else null):
+    int n_segs;
+    float *segs;    // [M][B][H][n_segs][2][64][64]: segment increments, then the state entering each segment
+    float *segtot;  // [M][B][H][n_segs] decay total of each segment
+    float *wfwd;    // [M][B][H][n*64] weight of step t in its segment's end state
+    float *wbwd;    // [M][B][H][n*64] decay from its segment's start through step t
 };
 
 __device__ __forceinline__ float *chunk_state_ptr(const FwdParams &p, int m, int b, int h, int c) {
@@ -753,418 +759,569 @@ __global__ void __launch_bounds__(THREADS) chunk_output_kernel(FwdParams p) {
 // fp32 accumulation; q is staged unscaled and q_scale is applied to the fp32
 // results it enters.
 //
-// State pass: PASS_SPLIT blocks of PASS_THREADS (4 waves) per (state m, b, h) walk
-// the chunks in order; block `half` owns value rows 32 half.. (V columns 32 half..)
-// and its wave w the rows 16 it.., it = 2 half + (w & 1), and key-column tiles
-// 2(w >> 1), 2(w >> 1) + 1.  Per chunk it forms dS = sum_s dl_s v_s (x)
-// conj(k_s) on MFMA and updates the running state S <- total S + dS, which never
-// leaves registers (fp32, accumulator layout).  Only the bf16 snapshot of the
-// state entering each chunk (stored straight from registers), the chunk totals
-// and the final state reach HBM.  Chunk c+2's K and V tiles and gamma are loaded
-// into registers while chunk c is processed and staged into LDS at the end of
-// chunk c+1 (one LDS buffer, two barriers per chunk); every wave forms the
-// chunk's decay prefix itself and V is staged already scaled by dl_s, so the
-// MFMA operands come straight from LDS.  Rows past the end of the sequence
-// re-read its last row: their decay weights dl are zero.
-constexpr size_t pass_bf16_smem() {
-    return (size_t)2 * PLANE_B * 2     // K [plane][64][PB]
-           + (size_t)2 * PLANE_B * 2;  // dl-scaled V [plane][64][PB] (this block's columns)
+// The chunks of a chain are grouped in segments of SEG chunks, so the only
+// sequential work is an elementwise scan over the segments:
+//   seg_decay (a wave per chunk): log-decay prefix of the chunk, chunk totals,
+//      segment totals and two per-step weights: wfwd[t], the weight of step t's
+//      write in its segment's end state (D[C-1, t] of its chunk times the totals
+//      of the segment's later chunks), and wbwd[t], the decay from the segment's
+//      start through t (used by the backward);
+//   seg_state (a block per (b, h, segment), all M states): the segment's
+//      increment dS_m = sum_t wfwd_m[t] v_t (x) conj(k_t) on MFMA;
+//   seg_scan (elementwise): S entering segment g+1 = total_g S_g + dS_g, in place
+//      over the increments, and the final state;
+//   seg_output (a block per (b, h, segment)): walks the segment's chunks with
+//      the carried states S_m in registers (fp32): Y_c = (W . D~) V + sum_m rho_m
+//      (Q~ S_m^T) with the bf16 copy of S_m in LDS, the bf16 snapshot of S_m for
+//      the backward, and S_m <- total_m S_m + sum_s D_m[C-1,s] v_s (x) conj(k_s)
+//      before the next chunk.
+// A chain's chunk totals multiply in the same order as a chunk-by-chunk pass
+// only up to fp32 rounding: the segment weights are exponentials of sums of
+// log-decays rather than products of per-chunk exponentials.
+
+// One wave per chunk: wave q of block (chain, g) takes chunk SEG g + q.
+__global__ void __launch_bounds__(THREADS) seg_decay_kernel(FwdParams p) {
+    static_assert(SEG * 64 == THREADS, "a wave per chunk of the segment");
+    __shared__ float s_last[SEG];
+    const qpam_scan_args &a = p.a;
+    const int64_t chain = blockIdx.x / p.n_segs;
+    const int sg = blockIdx.x % p.n_segs;
+    const int bh = (int)(chain % (a.B * a.H)), m = (int)(chain / (a.B * a.H));
+    const int b = bh / a.H, h = bh % a.H;
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = sg * SEG + w;
+    const bool live = c < p.n_chunks;
+    float L = 0.f, Llast = 0.f;
+    int valid = 0;
+    if (live) {
+        valid = min(64, a.T - c * 64);
+        const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c * 64 * a.sg_t;
+        L = chunk_log_prefix(gp, a.sg_t, valid, lane);
+        Llast = __shfl(L, valid - 1);
+    }
+    if (lane == 0) s_last[w] = Llast;  // 0 past the end of the sequence
+    __syncthreads();
+    float before = 0.f, after = 0.f, total = 0.f;
+#pragma unroll
+    for (int q = 0; q < SEG; ++q) {
+        const float x = s_last[q];
+        total += x;
+        before += q < w ? x : 0.f;
+        after += q > w ? x : 0.f;
+    }
+    if (live) {
+        const int64_t o = chain * p.n_chunks * 64 + (int64_t)c * 64 + lane;
+        p.wfwd[o] = lane < valid ? __expf(fminf(Llast - L, 0.f) + after) : 0.f;
+        p.wbwd[o] = lane < valid ? __expf(L + before) : 0.f;
+        if (lane == 0) *chunk_total_ptr(p, m, b, h, c) = __expf(Llast);
+    }
+    if (threadIdx.x == 0) p.segtot[chain * p.n_segs + sg] = __expf(total);
 }
 
-__global__ void __launch_bounds__(PASS_THREADS) __attribute__((amdgpu_waves_per_eu(3)))
-state_pass_bf16_kernel(FwdParams p) {
-    constexpr int NT = PASS_THREADS;
+__device__ __forceinline__ int64_t seg_chain(const qpam_scan_args &a, int m, int b, int h) {
+    return ((int64_t)m * a.B + b) * a.H + h;
+}
+
+// Segment increments.  Wave w owns value-row tile it = w & 3 and key-column tiles
+// 2 jh, 2 jh + 1 (jh = w >> 2) of every state's increment.  Per chunk: K in LDS
+// as loaded, V once per state with row t scaled by wfwd_m[t] (fp32 product,
+// rounded once); the next chunk's tiles and weights are in flight meanwhile.
+template <int M>
+constexpr size_t seg_state_smem() { return (size_t)(2 + 2 * M) * PLANE_B * 2; }
+
+template <int M>
+__global__ void __launch_bounds__(SEG_THREADS) seg_state_kernel(FwdParams p) {
+    constexpr int NT = SEG_THREADS;
     extern __shared__ float smem[];
     using U = unsigned short;
-    U *sK = reinterpret_cast<U *>(smem);  // + plane * PLANE_B
-    U *sV = sK + 2 * PLANE_B;             // + plane * PLANE_B
-
+    U *sK = reinterpret_cast<U *>(smem);  // [plane][64][PB]
+    U *sV = sK + 2 * PLANE_B;             // [m][plane][64][PB]
     const qpam_scan_args &a = p.a;
-    // the halves of a chain are n_chains blocks apart: a multiple of 8 (the XCD
-    // count) when B H is, so both read K through the same L2
-    const int n_chains = a.M * a.B * a.H;
-    const int chain = blockIdx.x % n_chains, half = blockIdx.x / n_chains;
-    const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
-    const int b = bh / a.H, h = bh % a.H;
+    const int sg = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int it = 2 * half + (w & 1), jh = w >> 1;  // value rows 16it.., key-column tiles 2jh + jj
-    const int vc0 = 32 * half;                       // V columns of this block's value rows
-    const int n = p.n_chunks;
-    const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
+    const int it = w & 3, jh = w >> 2;
+    const int c_begin = sg * SEG, c_end = min(c_begin + SEG, p.n_chunks);
     const U *kre = (const U *)a.k.re + b * a.k.s0 + h * a.k.s1, *kim = (const U *)a.k.im + b * a.k.s0 + h * a.k.s1;
     const U *vre = (const U *)a.v.re + b * a.v.s0 + h * a.v.s1, *vim = (const U *)a.v.im + b * a.v.s0 + h * a.v.s1;
-    U *snap0 = chunk_snap_ptr(p, m, b, h, 0);
 
-    // running state S[i][j] for rows 16it + 4g + r, cols 16(2jh + jj) + l16
-    floatx4 sR[2], sI[2];
-#pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-        sR[jj] = sI[jj] = zero4();
-        if (a.s0_re) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                sR[jj][r] = a.s0_re[o];
-                sI[jj][r] = a.s0_im[o];
-            }
-        }
-    }
-
-    // chunk inputs in registers, two register sets (chunk c in set c & 1): K and V
-    // planes, gamma.  Sets are selected by compile-time index only (the chunk loop
-    // is unrolled by two).
     struct ChunkRegs {
-        BfTileRegs<NT> kr, ki;
-        BfTileRegs<NT, 32> vr, vi;
-        float gam;
+        BfTileRegs<NT> kr, ki, vr, vi;
+        float wm[M];
     };
-    ChunkRegs cr0, cr1;
     auto load_chunk = [&](int c, ChunkRegs &x) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
-        const int64_t ko = (int64_t)c0 * a.k.s2, vo = (int64_t)c0 * a.v.s2;
-        tile_load_bf<NT>(x.kr, kre + ko, a.k.s2, valid);
-        tile_load_bf<NT>(x.ki, kim + ko, a.k.s2, valid);
-        tile_load_bf<NT, 32>(x.vr, vre + vo, a.v.s2, valid, vc0);
-        tile_load_bf<NT, 32>(x.vi, vim + vo, a.v.s2, valid, vc0);
-        x.gam = gbase[(int64_t)(c0 + min(lane, valid - 1)) * a.sg_t];
-    };
-    // registers -> LDS: K as loaded, V scaled by dl_s = D[C-1, s]; each wave forms
-    // the decay prefix from gamma itself and keeps the chunk total
-    float tot_staged = 1.f;  // decay total of the chunk in LDS
-    auto stage_chunk = [&](int c, const ChunkRegs &x) {
-        // nothing of the staging moves above this point: its first use of the staged
-        // register set is where the compiler waits for that set's loads, and the
-        // memory counter completes in order, so a use hoisted to the top of the step
-        // would also wait for everything loaded one step earlier
-        __builtin_amdgcn_sched_barrier(0);
-        const int valid = min(64, a.T - c * 64);
-        float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
+        tile_load_bf<NT>(x.kr, kre + (int64_t)c0 * a.k.s2, a.k.s2, valid);
+        tile_load_bf<NT>(x.ki, kim + (int64_t)c0 * a.k.s2, a.k.s2, valid);
+        tile_load_bf<NT>(x.vr, vre + (int64_t)c0 * a.v.s2, a.v.s2, valid);
+        tile_load_bf<NT>(x.vi, vim + (int64_t)c0 * a.v.s2, a.v.s2, valid);
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float y = __shfl_up(L, off);
-            if (lane >= off) L += y;
-        }
-        const float Llast = __shfl(L, valid - 1);
-        const float dl = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
-        tot_staged = __expf(Llast);
-        if (tid == 0 && half == 0) *chunk_total_ptr(p, m, b, h, c) = tot_staged;
+        for (int m = 0; m < M; ++m) x.wm[m] = p.wfwd[seg_chain(a, m, b, h) * p.n_chunks * 64 + c0 + lane];
+    };
+    auto stage_chunk = [&](const ChunkRegs &x) {
         tile_store_bf<NT>(sK, x.kr);
         tile_store_bf<NT>(sK + PLANE_B, x.ki);
-        tile_store_bf_rowscaled<NT, 32>(sV, x.vr, dl, vc0);
-        tile_store_bf_rowscaled<NT, 32>(sV + PLANE_B, x.vi, dl, vc0);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            tile_store_bf_rowscaled<NT>(sV + 2 * m * PLANE_B, x.vr, x.wm[m]);
+            tile_store_bf_rowscaled<NT>(sV + (2 * m + 1) * PLANE_B, x.vi, x.wm[m]);
+        }
     };
 
-    // chunk c + 2 is loaded into register set c & 1 during chunk c and staged at the
-    // end of chunk c + 1 (two chunks of latency cover); one LDS buffer, staged
-    // between two barriers
-    auto step = [&](int c, ChunkRegs &mine, ChunkRegs &next) {
-        // unconditional (the last chunk is re-read near the end): the same memory
-        // operation count on every path keeps the compiler's waits for the staged
-        // set exact
-        load_chunk(min(c + 2, n - 1), mine);
-        // bf16 snapshot of the entering state (this wave's tiles of chunk c's snapshot)
-        {
-            U *dst = snap0 + (int64_t)c * 2 * D * D;
+    floatx4 accR[M][2], accI[M][2];
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-                acc_store_bf_pairs(dst, dst + D * D, sR[jj], sI[jj], 16 * it, 16 * (2 * jh + jj));
-        }
-        // dS rows (value i) x cols (key j): A = dl-scaled V^T (transposed reads), B = K
-        floatx4 accR[2], accI[2];
+    for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
-        const U *Kr = sK, *Ki = sK + PLANE_B;
-        const U *Vr = sV, *Vi = sV + PLANE_B;
+        for (int jj = 0; jj < 2; ++jj) accR[m][jj] = accI[m][jj] = zero4();
+    ChunkRegs cr;
+    load_chunk(c_begin, cr);
+    for (int c = c_begin; c < c_end; ++c) {
+        __syncthreads();
+        stage_chunk(cr);
+        __syncthreads();
+        if (c + 1 < c_end) load_chunk(c + 1, cr);
+        // dS_m[i][j] += sum_s (w_m V)[s,i] conj(K[s,j]): A = weighted V^T, B = K (k = s)
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             const int s0 = 32 * kp + 8 * g;
-            const bf16x8 ar = ld_tr(Vr, s0, s0 + 4, 16 * it), ai = ld_tr(Vi, s0, s0 + 4, 16 * it), nar = neg_bf(ar);
+            bf16x8 kr[2], ki[2];
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
-                const int jt = 2 * jh + jj;
-                const bf16x8 kr = ld_tr(Kr, s0, s0 + 4, 16 * jt), ki = ld_tr(Ki, s0, s0 + 4, 16 * jt);
-                accR[jj] = mfma_bf(ar, kr, accR[jj]);
-                accR[jj] = mfma_bf(ai, ki, accR[jj]);
-                accI[jj] = mfma_bf(ai, kr, accI[jj]);
-                accI[jj] = mfma_bf(nar, ki, accI[jj]);
+                kr[jj] = ld_tr(sK, s0, s0 + 4, 16 * (2 * jh + jj));
+                ki[jj] = ld_tr(sK + PLANE_B, s0, s0 + 4, 16 * (2 * jh + jj));
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const bf16x8 ar = ld_tr(sV + 2 * m * PLANE_B, s0, s0 + 4, 16 * it);
+                const bf16x8 ai = ld_tr(sV + (2 * m + 1) * PLANE_B, s0, s0 + 4, 16 * it);
+                const bf16x8 nar = neg_bf(ar);
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    accR[m][jj] = mfma_bf(ar, kr[jj], accR[m][jj]);
+                    accR[m][jj] = mfma_bf(ai, ki[jj], accR[m][jj]);
+                    accI[m][jj] = mfma_bf(ai, kr[jj], accI[m][jj]);
+                    accI[m][jj] = mfma_bf(nar, ki[jj], accI[m][jj]);
+                }
             }
         }
-        // S <- total S + dS
-        const float tot = tot_staged;
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                sR[jj][r] = tot * sR[jj][r] + accR[jj][r];
-                sI[jj][r] = tot * sI[jj][r] + accI[jj][r];
-            }
-        // also unconditional: past the end, chunk n-1 (which `next` then holds) is
-        // staged again
-        __syncthreads();
-        stage_chunk(min(c + 1, n - 1), next);
-        __syncthreads();
-    };
-    load_chunk(0, cr0);
-    load_chunk(min(1, n - 1), cr1);
-    stage_chunk(0, cr0);
-    __syncthreads();
-    // pairs of steps without conditions inside the loop (no path on which the
-    // compiler would see fewer memory operations), odd tail after it
-    int c = 0;
-    for (; c + 1 < n; c += 2) {
-        step(c, cr0, cr1);
-        step(c + 1, cr1, cr0);
     }
-    if (c < n) step(c, cr0, cr1);
-    if (a.s_re) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float *dst = p.segs + (seg_chain(a, m, b, h) * p.n_segs + sg) * (2 * D * D);
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                a.s_re[o] = sR[jj][r];
-                a.s_im[o] = sI[jj][r];
+                const int o = (16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                dst[o] = accR[m][jj][r];
+                dst[D * D + o] = accI[m][jj][r];
             }
     }
 }
 
+// Elementwise scan over the segments of every chain, in place: the increment of
+// segment g is replaced by the state entering it (s0, or zero, for g = 0); the
+// state after the last segment is the final state.  A thread per float4 of a
+// chain's two 64 x 64 planes; a batch of segments' loads in flight at once.
+constexpr int SEG_SCAN_BATCH = 8;
+__global__ void __launch_bounds__(THREADS) seg_scan_fwd_kernel(FwdParams p) {
+    const qpam_scan_args &a = p.a;
+    const int64_t chain = blockIdx.x >> 3;
+    const int e = ((blockIdx.x & 7) << 8) + threadIdx.x;  // float4 index in [2][64][64]
+    const int plane = e >> 10, off = (e & 1023) * 4;
+    float4 *buf = reinterpret_cast<float4 *>(p.segs + chain * p.n_segs * (2 * D * D)) + e;
+    const float *tot = p.segtot + chain * p.n_segs;
+    float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (a.s0_re) S = *reinterpret_cast<const float4 *>((plane ? a.s0_im : a.s0_re) + chain * D * D + off);
+    for (int g0 = 0; g0 < p.n_segs; g0 += SEG_SCAN_BATCH) {
+        const int nb = min(SEG_SCAN_BATCH, p.n_segs - g0);
+        float4 d[SEG_SCAN_BATCH];
+#pragma unroll
+        for (int i = 0; i < SEG_SCAN_BATCH; ++i)
+            if (i < nb) d[i] = buf[(int64_t)(g0 + i) * (2 * D * D / 4)];
+#pragma unroll
+        for (int i = 0; i < SEG_SCAN_BATCH; ++i) {
+            if (i < nb) {
+                buf[(int64_t)(g0 + i) * (2 * D * D / 4)] = S;
+                const float t = tot[g0 + i];
+                S = make_float4(t * S.x + d[i].x, t * S.y + d[i].y, t * S.z + d[i].z, t * S.w + d[i].w);
+            }
+        }
+    }
+    if (a.s_re) *reinterpret_cast<float4 *>((plane ? a.s_im : a.s_re) + chain * D * D + off) = S;
+}
+
+// Output pass over one segment.  Wave roles (w = 0..7; waves w and w + 4 share a
+// SIMD):
+//   output: query tile tt = w (w < 4) or 7 - w, value tiles 2 ih, 2 ih + 1
+//     (ih = w >> 2): the causal score tiles of tt (both waves of a tt form them),
+//     so each SIMD holds one light and one heavy query tile;
+//   state: value-row tile iu = w & 3 and key-column tiles 2 jh, 2 jh + 1 of every
+//     carried state S_m.
+// LDS: Q, K, V tiles of the chunk, the bf16 copy of each S_m, the per-step decay
+// vectors of each state.  The next chunk's tiles, gamma and rotation are loaded
+// into registers while the chunk is processed.
 template <int M>
-__global__ void __launch_bounds__(THREADS) chunk_output_bf16_kernel(FwdParams p) {
+constexpr size_t seg_output_smem() {
+    return (size_t)(6 + 2 * M) * PLANE_B * 2 + (7 * M * 64 + 2 * MAX_M) * sizeof(float);
+}
+
+template <int M>
+__global__ void __launch_bounds__(SEG_THREADS) seg_output_kernel(FwdParams p) {
+    constexpr int NT = SEG_THREADS;
     extern __shared__ float smem[];
     using U = unsigned short;
     U *sQr = reinterpret_cast<U *>(smem), *sQi = sQr + PLANE_B;
-    U *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;  // K tile, later the carried state S_m
+    U *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
     U *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
-    float *sL = reinterpret_cast<float *>(sVi + PLANE_B);  // per-step vectors [M][64]
-    float *sRr = sL + M * 64, *sRi = sRr + M * 64, *sF = sRi + M * 64;
-    int *sFast = reinterpret_cast<int *>(sF + M * 64);
+    U *sS = sVi + PLANE_B;  // [m][plane][64][PB] bf16 state entering the chunk
+    float *sL = reinterpret_cast<float *>(sS + 2 * M * PLANE_B);  // per-step vectors [M][64]
+    float *sRr = sL + M * 64, *sRi = sRr + M * 64, *sF = sRi + M * 64, *sDl = sF + M * 64;
+    float *sPr = sDl + M * 64, *sPi = sPr + M * 64;           // rho_m q_scale
+    float *sTot = sPi + M * 64;                               // [MAX_M]
+    int *sFast = reinterpret_cast<int *>(sTot + MAX_M);       // [MAX_M]
 
     const qpam_scan_args &a = p.a;
-    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int c0 = c * 64;
-    const int valid = min(64, a.T - c0);
+    const int sg = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int c_begin = sg * SEG, c_end = min(c_begin + SEG, p.n_chunks);
     const bool general = (M > 1) || (a.rot_re != nullptr);
-    const bool carry = (c > 0) || (a.s0_re != nullptr);
     const float qs = a.q_scale;
+    const int tt = w < 4 ? w : 7 - w, ih = w >> 2;
+    const int iu = w & 3, jh = w >> 2;
+    const int64_t qb = b * a.q.s0 + h * a.q.s1, kb = b * a.k.s0 + h * a.k.s1, vb = b * a.v.s0 + h * a.v.s1;
 
-    const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
-    const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
-    const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-    {
-        U *const dst[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
-        const U *const src[6] = {(const U *)a.q.re + qo, (const U *)a.q.im + qo, (const U *)a.k.re + ko,
-                                 (const U *)a.k.im + ko, (const U *)a.v.re + vo, (const U *)a.v.im + vo};
-        const int64_t st[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        stage_bf<6, 0x0u>(dst, src, st, valid);
-    }
-    if (w == 0) {
-        bool fast = true;
+    struct ChunkRegs {
+        BfTileRegs<NT> qr, qi, kr, ki, vr, vi;
+        float gam, rr, ri;
+    };
+    auto load_chunk = [&](int c, ChunkRegs &x) {
+        const int c0 = c * 64, valid = min(64, a.T - c0);
+        tile_load_bf<NT>(x.qr, (const U *)a.q.re + qb + (int64_t)c0 * a.q.s2, a.q.s2, valid);
+        tile_load_bf<NT>(x.qi, (const U *)a.q.im + qb + (int64_t)c0 * a.q.s2, a.q.s2, valid);
+        tile_load_bf<NT>(x.kr, (const U *)a.k.re + kb + (int64_t)c0 * a.k.s2, a.k.s2, valid);
+        tile_load_bf<NT>(x.ki, (const U *)a.k.im + kb + (int64_t)c0 * a.k.s2, a.k.s2, valid);
+        tile_load_bf<NT>(x.vr, (const U *)a.v.re + vb + (int64_t)c0 * a.v.s2, a.v.s2, valid);
+        tile_load_bf<NT>(x.vi, (const U *)a.v.im + vb + (int64_t)c0 * a.v.s2, a.v.s2, valid);
+        x.gam = 1.f;
+        x.rr = 1.f;
+        x.ri = 0.f;
+        if (w < M) {  // wave m forms state m's decay vectors
+            const int64_t t = c0 + min(lane, valid - 1);
+            x.gam = a.gamma[w * a.sg_m + b * a.sg_b + h * a.sg_h + t * a.sg_t];
+            if (a.rot_re) {
+                const int64_t ro = w * a.sr_m + b * a.sr_b + h * a.sr_h + t * a.sr_t;
+                x.rr = a.rot_re[ro];
+                x.ri = a.rot_im[ro];
+            }
+        }
+    };
+    auto stage_chunk = [&](int c, const ChunkRegs &x) {
+        tile_store_bf<NT>(sQr, x.qr);
+        tile_store_bf<NT>(sQi, x.qi);
+        tile_store_bf<NT>(sKr, x.kr);
+        tile_store_bf<NT>(sKi, x.ki);
+        tile_store_bf<NT>(sVr, x.vr);
+        tile_store_bf<NT>(sVi, x.vi);
+        if (w < M) {
+            const int valid = min(64, a.T - c * 64);
+            float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
+            const bool pos = L > 0.f;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_up(L, off);
+                if (lane >= off) L += y;
+            }
+            const bool ok = !__any(pos) && __shfl(L, 63) >= -FACTOR_RANGE;
+            const float Llast = __shfl(L, valid - 1);
+            const float rr = lane < valid ? x.rr : 1.f, ri = lane < valid ? x.ri : 0.f;
+            const float cum = __expf(L) * a.q_scale;
+            sL[w * 64 + lane] = L;
+            sRr[w * 64 + lane] = rr;
+            sRi[w * 64 + lane] = ri;
+            sPr[w * 64 + lane] = rr * cum;
+            sPi[w * 64 + lane] = ri * cum;
+            sF[w * 64 + lane] = __expf(-L);  // unused (possibly inf) when the test fails
+            sDl[w * 64 + lane] = lane < valid ? __expf(fminf(Llast - L, 0.f)) : 0.f;
+            if (lane == 0) {
+                sTot[w] = __expf(Llast);
+                sFast[w] = ok ? 1 : 0;
+            }
+        }
+    };
+    // carried state S_m of this wave's tiles (fp32) -> bf16 LDS copy and the snapshot of chunk c
+    floatx4 sR[M][2], sI[M][2];
+    auto publish_state = [&](int c) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            const float *gp = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)c0 * a.sg_t;
-            bool ok;
-            const float L = chunk_log_prefix_ok(gp, a.sg_t, valid, lane, ok);
-            fast = fast && ok;
-            float rr = 1.f, ri = 0.f;
-            if (a.rot_re && lane < valid) {
-                const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + lane) * a.sr_t;
-                rr = a.rot_re[ro];
-                ri = a.rot_im[ro];
+            U *snap = chunk_snap_ptr(p, m, b, h, c);
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                acc_store_bf_pairs<PB>(sS + 2 * m * PLANE_B, sS + (2 * m + 1) * PLANE_B, sR[m][jj], sI[m][jj], 16 * iu,
+                                       16 * (2 * jh + jj));
+                acc_store_bf_pairs(snap, snap + D * D, sR[m][jj], sI[m][jj], 16 * iu, 16 * (2 * jh + jj));
             }
-            sL[m * 64 + lane] = L;
-            sRr[m * 64 + lane] = rr;
-            sRi[m * 64 + lane] = ri;
-            sF[m * 64 + lane] = __expf(-L);  // unused (possibly inf) when the test fails
         }
-        if (lane == 0) *sFast = fast ? 1 : 0;
-    }
-    B16Regs sn[2];  // snapshot of the first carried state, in flight during the intra-chunk phase
-    if (carry) {
-        const U *s0p = chunk_snap_ptr(p, 0, b, h, c);
-        regs_load_bf<false>(sn[0], s0p, D, D);
-        regs_load_bf<false>(sn[1], s0p + D * D, D, D);
-    }
-    __syncthreads();
+    };
 
-    const int tt = causal_tile(w);
-    const int t = 16 * tt + l16;  // this lane's query row in the transposed score tiles
-    floatx4 yR[4], yI[4];
+    ChunkRegs cr;
+    load_chunk(c_begin, cr);
 #pragma unroll
-    for (int it = 0; it < 4; ++it) yR[it] = yI[it] = zero4();
-    {
-        floatx4 wr[4], wi[4];
+    for (int m = 0; m < M; ++m) {
+        const float *src = p.segs + (seg_chain(a, m, b, h) * p.n_segs + sg) * (2 * D * D);
 #pragma unroll
-        for (int st = 0; st < 4; ++st) wr[st] = wi[st] = zero4();
-#pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-            const bf16x8 bqr = ld8(sQr + t * PB + 32 * kp + 8 * g), bqi = ld8(sQi + t * PB + 32 * kp + 8 * g);
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                if (st > tt) continue;
-                const int s = 16 * st + l16;
-                const bf16x8 akr = ld8(sKr + s * PB + 32 * kp + 8 * g), aki = ld8(sKi + s * PB + 32 * kp + 8 * g);
-                wr[st] = mfma_bf(akr, bqr, wr[st]);
-                wr[st] = mfma_bf(aki, bqi, wr[st]);
-                wi[st] = mfma_bf(akr, bqi, wi[st]);
-                wi[st] = mfma_bf(neg_bf(aki), bqr, wi[st]);
-            }
-        }
-        // A = (q_scale W) . D~ ; lane holds s = 16st + 4g + r, t = 16tt + l16
-        if (*sFast) {
-            // D_m[t,s] = E_m[t] F_m[s]: D~ = sum_m (r_m E_m)[t] F_m[s]
-            float pr_t[MAX_M], pi_t[MAX_M];
-#pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const float e = __expf(sL[m * 64 + t]) * qs;
-                pr_t[m] = sRr[m * 64 + t] * e;
-                pi_t[m] = sRi[m * 64 + t] * e;
-            }
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                if (st > tt) continue;
-                float4 F4[MAX_M];
-#pragma unroll
-                for (int m = 0; m < M; ++m) F4[m] = *reinterpret_cast<const float4 *>(sF + m * 64 + 16 * st + 4 * g);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int s = 16 * st + 4 * g + r;
-                    float dre = 0.f, dim = 0.f;
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const float f = r == 0 ? F4[m].x : r == 1 ? F4[m].y : r == 2 ? F4[m].z : F4[m].w;
-                        dre += pr_t[m] * f;
-                        dim += pi_t[m] * f;
-                    }
-                    const bool keep = st < tt || s <= t;
-                    dre = keep ? dre : 0.f;
-                    dim = keep ? dim : 0.f;
-                    const float xr = wr[st][r], xi = wi[st][r];
-                    wr[st][r] = xr * dre - xi * dim;
-                    wi[st][r] = xr * dim + xi * dre;
-                }
-            }
-        } else {
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            if (st > tt) continue;
+        for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int s = 16 * st + 4 * g + r;
-                float dre = 0.f, dim = 0.f;
-                if (s <= t) {
-                    if (!general) {
-                        dre = __expf(fminf(sL[t] - sL[s], 0.f));
-                    } else {
+                const int o = (16 * iu + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
+                sR[m][jj][r] = src[o];
+                sI[m][jj][r] = src[D * D + o];
+            }
+    }
+    publish_state(c_begin);
+    stage_chunk(c_begin, cr);
+    __syncthreads();
+
+    for (int c = c_begin; c < c_end; ++c) {
+        const int c0 = c * 64, valid = min(64, a.T - c0);
+        const bool more = c + 1 < c_end;
+        const bool carry = (c > 0) || (a.s0_re != nullptr);
+        bool fast = true;
+#pragma unroll
+        for (int m = 0; m < M; ++m) fast = fast && sFast[m];
+        const int t = 16 * tt + l16;  // this lane's query row in the transposed score tiles
+        floatx4 yR[2], yI[2];
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) yR[ii] = yI[ii] = zero4();
+        {
+            floatx4 wr[4], wi[4];
+#pragma unroll
+            for (int st = 0; st < 4; ++st) wr[st] = wi[st] = zero4();
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                const bf16x8 bqr = ld8(sQr + t * PB + 32 * kp + 8 * g), bqi = ld8(sQi + t * PB + 32 * kp + 8 * g);
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    if (st > tt) continue;
+                    const int s = 16 * st + l16;
+                    const bf16x8 akr = ld8(sKr + s * PB + 32 * kp + 8 * g), aki = ld8(sKi + s * PB + 32 * kp + 8 * g);
+                    wr[st] = mfma_bf(akr, bqr, wr[st]);
+                    wr[st] = mfma_bf(aki, bqi, wr[st]);
+                    wi[st] = mfma_bf(akr, bqi, wi[st]);
+                    wi[st] = mfma_bf(neg_bf(aki), bqr, wi[st]);
+                }
+            }
+            // A = (q_scale W) . D~ ; lane holds s = 16st + 4g + r, t = 16tt + l16
+            if (fast) {
+                // D_m[t,s] = E_m[t] F_m[s]: D~ = sum_m (r_m E_m)[t] F_m[s]
+                float pr_t[MAX_M], pi_t[MAX_M];
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    pr_t[m] = sPr[m * 64 + t];
+                    pi_t[m] = sPi[m * 64 + t];
+                }
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    if (st > tt) continue;
+                    float4 F4[MAX_M];
+#pragma unroll
+                    for (int m = 0; m < M; ++m) F4[m] = *reinterpret_cast<const float4 *>(sF + m * 64 + 16 * st + 4 * g);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int s = 16 * st + 4 * g + r;
+                        float dre = 0.f, dim = 0.f;
 #pragma unroll
                         for (int m = 0; m < M; ++m) {
-                            const float dm = __expf(fminf(sL[m * 64 + t] - sL[m * 64 + s], 0.f));
-                            dre += sRr[m * 64 + t] * dm;
-                            dim += sRi[m * 64 + t] * dm;
+                            const float f = r == 0 ? F4[m].x : r == 1 ? F4[m].y : r == 2 ? F4[m].z : F4[m].w;
+                            dre += pr_t[m] * f;
+                            dim += pi_t[m] * f;
+                        }
+                        const bool keep = st < tt || s <= t;
+                        dre = keep ? dre : 0.f;
+                        dim = keep ? dim : 0.f;
+                        const float xr = wr[st][r], xi = wi[st][r];
+                        wr[st][r] = xr * dre - xi * dim;
+                        wi[st][r] = xr * dim + xi * dre;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    if (st > tt) continue;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int s = 16 * st + 4 * g + r;
+                        float dre = 0.f, dim = 0.f;
+                        if (s <= t) {
+                            if (!general) {
+                                dre = __expf(fminf(sL[t] - sL[s], 0.f));
+                            } else {
+#pragma unroll
+                                for (int m = 0; m < M; ++m) {
+                                    const float dm = __expf(fminf(sL[m * 64 + t] - sL[m * 64 + s], 0.f));
+                                    dre += sRr[m * 64 + t] * dm;
+                                    dim += sRi[m * 64 + t] * dm;
+                                }
+                            }
+                        }
+                        const float xr = wr[st][r] * qs, xi = wi[st][r] * qs;
+                        wr[st][r] = xr * dre - xi * dim;
+                        wi[st][r] = xr * dim + xi * dre;
+                    }
+                }
+            }
+            // Y += A V: k-step kp covers s-tiles 2kp, 2kp+1 (registers); transposed reads of V
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                if (2 * kp > tt) continue;
+                const bf16x8 ar = frag_from_acc(wr[2 * kp], wr[2 * kp + 1]);
+                const bf16x8 ai = frag_from_acc(wi[2 * kp], wi[2 * kp + 1]);
+                const bf16x8 nai = neg_bf(ai);
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii) {
+                    const int it = 2 * ih + ii, r0 = 32 * kp + 4 * g;
+                    const bf16x8 vr = ld_tr(sVr, r0, r0 + 16, 16 * it), vi = ld_tr(sVi, r0, r0 + 16, 16 * it);
+                    yR[ii] = mfma_bf(ar, vr, yR[ii]);
+                    yR[ii] = mfma_bf(nai, vi, yR[ii]);
+                    yI[ii] = mfma_bf(ar, vi, yI[ii]);
+                    yI[ii] = mfma_bf(ai, vr, yI[ii]);
+                }
+            }
+        }
+        // carried read  Y[t,i] += rho_m[t] q_scale U_m[t,i],  U_m = Q S_m^T on MFMA (operands straight
+        // from LDS, shared Q fragments); rho is applied to the fp32 product
+        if (carry) {
+            bf16x8 aqr[2], aqi[2], naqi[2];
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                aqr[kp] = ld8(sQr + t * PB + 32 * kp + 8 * g);
+                aqi[kp] = ld8(sQi + t * PB + 32 * kp + 8 * g);
+                naqi[kp] = neg_bf(aqi[kp]);
+            }
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const U *Sr = sS + 2 * m * PLANE_B, *Si = Sr + PLANE_B;
+                floatx4 uR[2], uI[2];
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii) uR[ii] = uI[ii] = zero4();
+#pragma unroll
+                for (int kp = 0; kp < 2; ++kp) {
+#pragma unroll
+                    for (int ii = 0; ii < 2; ++ii) {
+                        const int row = (16 * (2 * ih + ii) + l16) * PB + 32 * kp + 8 * g;
+                        const bf16x8 sr = ld8(Sr + row), si = ld8(Si + row);
+                        uR[ii] = mfma_bf(aqr[kp], sr, uR[ii]);
+                        uR[ii] = mfma_bf(naqi[kp], si, uR[ii]);
+                        uI[ii] = mfma_bf(aqr[kp], si, uI[ii]);
+                        uI[ii] = mfma_bf(aqi[kp], sr, uI[ii]);
+                    }
+                }
+                const float4 pr4 = *reinterpret_cast<const float4 *>(sPr + m * 64 + 16 * tt + 4 * g);
+                const float4 pi4 = *reinterpret_cast<const float4 *>(sPi + m * 64 + 16 * tt + 4 * g);
+                const float prv[4] = {pr4.x, pr4.y, pr4.z, pr4.w}, piv[4] = {pi4.x, pi4.y, pi4.z, pi4.w};
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        yR[ii][r] += prv[r] * uR[ii][r] - piv[r] * uI[ii][r];
+                        yI[ii][r] += prv[r] * uI[ii][r] + piv[r] * uR[ii][r];
+                    }
+            }
+        }
+        {
+            const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)c0 * a.y.s2;
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int tr = 16 * tt + 4 * g + r;
+                    if (tr < valid) {
+                        const int64_t o = yo + (int64_t)tr * a.y.s2 + 16 * (2 * ih + ii) + l16;
+                        if (a.y_dtype == QPAM_BF16) {
+                            reinterpret_cast<U *>(a.y.re)[o] = f32_to_bf16(yR[ii][r]);
+                            reinterpret_cast<U *>(a.y.im)[o] = f32_to_bf16(yI[ii][r]);
+                        } else {
+                            a.y.re[o] = yR[ii][r];
+                            a.y.im[o] = yI[ii][r];
                         }
                     }
                 }
-                const float xr = wr[st][r] * qs, xi = wi[st][r] * qs;
-                wr[st][r] = xr * dre - xi * dim;
-                wi[st][r] = xr * dim + xi * dre;
-            }
         }
-        }
-        // Y += A V: k-step kp covers s-tiles 2kp, 2kp+1 (registers); transposed reads of V give the
-        // matching k order
+        if (!more) break;
+        load_chunk(c + 1, cr);
+        // S_m <- total_m S_m + sum_s D_m[C-1,s] v_s (x) conj(k_s): the scaled state is the MFMA
+        // accumulator; A = dl-weighted V^T, B = K (k = s)
+        {
 #pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-            if (2 * kp > tt) continue;
-            const bf16x8 ar = frag_from_acc(wr[2 * kp], wr[2 * kp + 1]);
-            const bf16x8 ai = frag_from_acc(wi[2 * kp], wi[2 * kp + 1]);
-            const bf16x8 nai = neg_bf(ai);
+            for (int m = 0; m < M; ++m) {
+                const float tot = sTot[m];
 #pragma unroll
-            for (int it = 0; it < 4; ++it) {
-                const int r0 = 32 * kp + 4 * g;
-                const bf16x8 vr = ld_tr(sVr, r0, r0 + 16, 16 * it), vi = ld_tr(sVi, r0, r0 + 16, 16 * it);
-                yR[it] = mfma_bf(ar, vr, yR[it]);
-                yR[it] = mfma_bf(nai, vi, yR[it]);
-                yI[it] = mfma_bf(ar, vi, yI[it]);
-                yI[it] = mfma_bf(ai, vr, yI[it]);
+                for (int jj = 0; jj < 2; ++jj) {
+                    sR[m][jj] *= tot;
+                    sI[m][jj] *= tot;
+                }
             }
-        }
-    }
-
-    // carried read  Y += sum_m (rho_m q_scale q) S_in,m^T
-    if (carry) {
-        for (int m = 0; m < M; ++m) {
-            __syncthreads();
-            regs_store_bf<false>(sKr, sn[0]);
-            regs_store_bf<false>(sKi, sn[1]);
-            if (m + 1 < M) {  // the next state's snapshot is in flight while this one is used
-                const U *nx = chunk_snap_ptr(p, m + 1, b, h, c);
-                regs_load_bf<false>(sn[0], nx, D, D);
-                regs_load_bf<false>(sn[1], nx + D * D, D, D);
-            }
-            __syncthreads();
-            const float cum = __expf(sL[m * 64 + t]) * qs;
-            const float rhr = sRr[m * 64 + t] * cum, rhi = sRi[m * 64 + t] * cum;
 #pragma unroll
             for (int kp = 0; kp < 2; ++kp) {
-                const floatx8 qr = to_f(ld8(sQr + t * PB + 32 * kp + 8 * g));
-                const floatx8 qi = to_f(ld8(sQi + t * PB + 32 * kp + 8 * g));
-                const bf16x8 pr = to_bf(rhr * qr - rhi * qi), pi = to_bf(rhr * qi + rhi * qr), npi = neg_bf(pi);
+                const int s0 = 32 * kp + 8 * g;
+                bf16x8 kr[2], ki[2];
 #pragma unroll
-                for (int it = 0; it < 4; ++it) {
-                    const int row = (16 * it + l16) * PB + 32 * kp + 8 * g;
-                    const bf16x8 sr = ld8(sKr + row), si = ld8(sKi + row);
-                    yR[it] = mfma_bf(pr, sr, yR[it]);
-                    yR[it] = mfma_bf(npi, si, yR[it]);
-                    yI[it] = mfma_bf(pr, si, yI[it]);
-                    yI[it] = mfma_bf(pi, sr, yI[it]);
+                for (int jj = 0; jj < 2; ++jj) {
+                    kr[jj] = ld_tr(sKr, s0, s0 + 4, 16 * (2 * jh + jj));
+                    ki[jj] = ld_tr(sKi, s0, s0 + 4, 16 * (2 * jh + jj));
+                }
+                const floatx8 vr = to_f(ld_tr(sVr, s0, s0 + 4, 16 * iu)), vi = to_f(ld_tr(sVi, s0, s0 + 4, 16 * iu));
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float4 d0 = *reinterpret_cast<const float4 *>(sDl + m * 64 + s0);
+                    const float4 d1 = *reinterpret_cast<const float4 *>(sDl + m * 64 + s0 + 4);
+                    const floatx8 dl = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+                    const bf16x8 ar = to_bf(vr * dl), ai = to_bf(vi * dl), nar = neg_bf(ar);
+#pragma unroll
+                    for (int jj = 0; jj < 2; ++jj) {
+                        sR[m][jj] = mfma_bf(ar, kr[jj], sR[m][jj]);
+                        sR[m][jj] = mfma_bf(ai, ki[jj], sR[m][jj]);
+                        sI[m][jj] = mfma_bf(ai, kr[jj], sI[m][jj]);
+                        sI[m][jj] = mfma_bf(nar, ki[jj], sI[m][jj]);
+                    }
                 }
             }
         }
+        __syncthreads();  // every read of this chunk's LDS tiles and states is done
+        publish_state(c + 1);
+        stage_chunk(c + 1, cr);
+        __syncthreads();
     }
-
-    const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)c0 * a.y.s2;
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int tr = 16 * tt + 4 * g + r;
-            if (tr < valid) {
-                const int64_t o = yo + (int64_t)tr * a.y.s2 + 16 * it + l16;
-                if (a.y_dtype == QPAM_BF16) {
-                    reinterpret_cast<U *>(a.y.re)[o] = f32_to_bf16(yR[it][r]);
-                    reinterpret_cast<U *>(a.y.im)[o] = f32_to_bf16(yI[it][r]);
-                } else {
-                    a.y.re[o] = yR[it][r];
-                    a.y.im[o] = yI[it][r];
-                }
-            }
-        }
 }
-
-template <int M>
-constexpr size_t output_bf16_smem() { return (size_t)6 * PLANE_B * 2 + (4 * M * 64 + 4) * sizeof(float); }
 
 template <int M>
 int launch_fwd_bf16_m(const FwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;
-    dim3 grid(p.n_chunks, a.H, a.B);
-    const size_t s1 = pass_bf16_smem(), s3 = output_bf16_smem<M>();
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)state_pass_bf16_kernel,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)chunk_output_bf16_kernel<M>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
-    hipLaunchKernelGGL(state_pass_bf16_kernel, dim3(PASS_SPLIT * a.M * a.B * a.H), dim3(PASS_THREADS), s1, stream, p);
-    int st = launch_status("state_pass_bf16_kernel");
+    const int64_t chains = (int64_t)a.M * a.B * a.H;
+    QPAM_REQUIRE(chains * p.n_segs < (1ll << 31) && chains * 8 < (1ll << 31), "qpam_scan_fwd: grid too large");
+    const dim3 grid(p.n_segs, a.H, a.B);
+    const size_t s_state = seg_state_smem<M>(), s_out = seg_output_smem<M>();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)seg_state_kernel<M>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)s_state));
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)seg_output_kernel<M>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)s_out));
+    hipLaunchKernelGGL(seg_decay_kernel, dim3((unsigned)(chains * p.n_segs)), dim3(THREADS), 0, stream, p);
+    int st = launch_status("seg_decay_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(seg_state_kernel<M>, grid, dim3(SEG_THREADS), s_state, stream, p);
+    st = launch_status("seg_state_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(seg_scan_fwd_kernel, dim3((unsigned)(chains * 8)), dim3(THREADS), 0, stream, p);
+    st = launch_status("seg_scan_fwd_kernel");
     if (st) return st;
     if (a.prof_ev[0]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[0], stream));
-    hipLaunchKernelGGL(chunk_output_bf16_kernel<M>, grid, dim3(THREADS), s3, stream, p);
-    st = launch_status("chunk_output_bf16_kernel");
+    hipLaunchKernelGGL(seg_output_kernel<M>, grid, dim3(SEG_THREADS), s_out, stream, p);
+    st = launch_status("seg_output_kernel");
     if (st) return st;
     if (a.prof_ev[1]) QPAM_CHECK_HIP(hipEventRecord((hipEvent_t)a.prof_ev[1], stream));
     return QPAM_OK;
 }
 
-// The state count is a compile-time constant of the output kernel.
+// The state count is a compile-time constant of the segment kernels.
 int launch_fwd_bf16(const FwdParams &p, hipStream_t stream) {
     switch (p.a.M) {
         case 1: return launch_fwd_bf16_m<1>(p, stream);
@@ -1223,19 +1380,37 @@ int launch_fwd(const FwdParams &p, hipStream_t stream) {
 
 bool uses_snapshots(const qpam_scan_args &a) { return a.dtype == QPAM_BF16 && a.C == 64; }
 
-// fp32 increments/states, chunk totals, then (bf16 path) the bf16 snapshots at a
-// 256-byte aligned offset.
-// Workspace: fp32 per-chunk states (fp32 path only), fp32 chunk totals, then at a
-// 256-byte aligned offset the bf16 entering-state snapshots (snapshot path only).
+// Workspace: fp32 per-chunk states (fp32 inputs), fp32 chunk totals, then (bf16 path with 64-step chunks) the segment totals and the
+// two per-step segment weights; at a 256-byte aligned offset either the bf16
+// entering-state snapshots followed by the fp32 segment states (bf16, 64-step
+// chunks) or the fp32 state pass's decay weights (fp32, 64-step chunks).
 int64_t fwd_totals_offset(const qpam_scan_args &a) {  // in floats
     const int64_t n = (a.T + a.C - 1) / a.C;
     return uses_snapshots(a) ? 0 : (int64_t)a.M * a.B * a.H * n * 2 * D * D;
 }
 
+SegLayout seg_layout(const qpam_scan_args &a) {
+    const int64_t n = (a.T + a.C - 1) / a.C, n_segs = (n + SEG - 1) / SEG;
+    const int64_t chains = (int64_t)a.M * a.B * a.H;
+    SegLayout l;
+    l.n_segs = (int)n_segs;
+    l.segtot = fwd_totals_offset(a) + chains * n;
+    l.wfwd = l.segtot + chains * n_segs;
+    l.wbwd = l.wfwd + chains * n * 64;
+    return l;
+}
+
 size_t fwd_snapshot_offset(const qpam_scan_args &a) {
     const int64_t n = (a.T + a.C - 1) / a.C;
     const int64_t chains = (int64_t)a.M * a.B * a.H;
-    return ((size_t)(fwd_totals_offset(a) + chains * n) * sizeof(float) + 255) & ~(size_t)255;
+    const int64_t floats = uses_snapshots(a) ? seg_layout(a).wbwd + chains * n * 64 : fwd_totals_offset(a) + chains * n;
+    return ((size_t)floats * sizeof(float) + 255) & ~(size_t)255;
+}
+
+size_t fwd_segs_offset(const qpam_scan_args &a) {
+    const int64_t n = (a.T + a.C - 1) / a.C;
+    const int64_t chains = (int64_t)a.M * a.B * a.H;
+    return fwd_snapshot_offset(a) + (size_t)chains * n * 2 * D * D * sizeof(unsigned short);
 }
 
 // fp32 path with 64-step chunks: the state pass's decay weights sit where the
@@ -1245,8 +1420,8 @@ bool uses_dlast(const qpam_scan_args &a) { return a.dtype == QPAM_F32 && a.C == 
 size_t fwd_workspace_bytes(const qpam_scan_args &a) {
     const int64_t n = (a.T + a.C - 1) / a.C;
     const int64_t chains = (int64_t)a.M * a.B * a.H;
+    if (uses_snapshots(a)) return fwd_segs_offset(a) + (size_t)chains * seg_layout(a).n_segs * 2 * D * D * sizeof(float);
     size_t bytes = fwd_snapshot_offset(a);
-    if (uses_snapshots(a)) bytes += (size_t)chains * n * 2 * D * D * sizeof(unsigned short);
     if (uses_dlast(a)) bytes += (size_t)chains * n * 64 * sizeof(float);
     return bytes;
 }
@@ -1296,6 +1471,16 @@ int scan_fwd(const qpam_scan_args *a, hipStream_t stream) {
                  ? reinterpret_cast<unsigned short *>((char *)a->workspace + fwd_snapshot_offset(*a))
                  : nullptr;
     p.dlast = uses_dlast(*a) ? reinterpret_cast<float *>((char *)a->workspace + fwd_snapshot_offset(*a)) : nullptr;
+    p.n_segs = 0;
+    p.segs = p.segtot = p.wfwd = p.wbwd = nullptr;
+    if (uses_snapshots(*a)) {
+        const SegLayout l = seg_layout(*a);
+        p.n_segs = l.n_segs;
+        p.segtot = (float *)a->workspace + l.segtot;
+        p.wfwd = (float *)a->workspace + l.wfwd;
+        p.wbwd = (float *)a->workspace + l.wbwd;
+        p.segs = reinterpret_cast<float *>((char *)a->workspace + fwd_segs_offset(*a));
+    }
     QPAM_REQUIRE(p.n_chunks <= 65535 && a->H <= 65535 && a->B <= 65535, "qpam_scan_fwd: grid too large");
     const bool bf = a->dtype == QPAM_BF16;
     if (uses_snapshots(*a)) return launch_fwd_bf16(p, stream);

@@ -24,6 +24,7 @@ from torch import Tensor
 from . import _lib
 
 KERNEL_CHUNKS = (16, 32, 64)
+SEG = 4  # 64-step chunks per segment of the bf16 kernels (workspace layout)
 
 # Optional EventPair whose events the next forward records around its
 # dominant (chunk-output) kernel; set by benchmarks, cleared after use.
@@ -172,14 +173,19 @@ def scan_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
 
 def fwd_workspace_bytes(M, B, H, T, chunk, bf16, d=64):
     """Forward workspace size, as qpam_scan_workspace_size computes it: fp32
-    per-chunk states (fp32 path) and chunk totals, then at a 256-byte aligned
-    offset either (bf16 inputs, chunk 64) bf16 snapshots of the entering states
-    or (fp32 inputs, chunk 64) the state pass's per-chunk decay weights."""
+    per-chunk states (fp32 inputs) and chunk totals; with bf16 inputs and chunk
+    64 also the segment totals and two per-step segment weights, then at a
+    256-byte aligned offset the bf16 snapshots of the entering states and the
+    fp32 segment states; with fp32 inputs and chunk 64, at that offset the
+    state pass's per-chunk decay weights."""
     chains, n = M * B * H, (T + chunk - 1) // chunk
     snap = bf16 and chunk == 64
-    off = (((0 if snap else chains * n * 2 * d * d) + chains * n) * 4 + 255) & ~255
     if snap:
-        return off + chains * n * 2 * d * d * 2
+        n_segs = (n + SEG - 1) // SEG
+        floats = chains * n + chains * n_segs + 2 * chains * n * 64
+        off = (floats * 4 + 255) & ~255
+        return off + chains * n * 2 * d * d * 2 + chains * n_segs * 2 * d * d * 4
+    off = ((chains * n * 2 * d * d + chains * n) * 4 + 255) & ~255
     return off + (chains * n * 64 * 4 if chunk == 64 else 0)
 
 

@@ -7,11 +7,18 @@ with inputs resident in HBM.  `roofline` covers the dominant kernel (the
 chunk-output MFMA kernel), timed live with HIP events recorded by the library
 on the launch stream around that kernel, against the fp32 MFMA peak.
 
+`roofline.frac_causal` counts the score and intra-read products over the
+causal half of each chunk only; `traffic` (HBM bytes per launch) comes from
+profiles/traffic.json, whose `build` hash is reported beside the current one.
+
 Secondary measurements (same line, under "extras"): config 4 ragged decode
-(256 slots, ~75% active, 1000 steps) in tokens/s and HBM GB/s; more configs
-as their kernels land.  `cpu_baseline` times the CPU restatement of the
-reference's chunk loop (oracle/pam.py: chunked_head) on a bounded sample of
-the same workload on the host cores.
+(256 slots, ~75% active, 1000 steps) in tokens/s and HBM GB/s, the E3 decode
+engine, config 3 E3 fwd+bwd, config 5 CE fwd+bwd, complex elementwise ops,
+the fused layer and the E2 delta rule.  `cpu_baseline` times the CPU
+restatement of the reference's chunk loop (oracle/pam.py: chunked_head) on a
+bounded sample of the same workload on the host cores; `cpu_baselines` does
+the same for configs 3, 4 and 5 (oracle restatements, bounded samples, with
+the host's CPU model and torch version).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras] [--no-cpu]
 """
@@ -41,20 +48,64 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "engine", "e3", "ce", "cplx", "layer",
-                                       "delta", "copy"], default=None,
+                                       "delta", "delta_ref", "copy"], default=None,
                     help="run one workload (for profiler passes) and print its own JSON line")
     return ap.parse_args()
 
 
+def source_hash():
+    """16 hex digits of the SHA-256 of the library's sources (every .hip / .h
+    under qllm2_amd/csrc and include/qpam.h, in name order): the build a
+    measurement belongs to."""
+    import hashlib
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "qllm2_amd", "csrc")
+    files = sorted(os.path.join(csrc, f) for f in os.listdir(csrc) if f.endswith((".hip", ".h")))
+    for path in files + [os.path.join(ROOT, "include", "qpam.h")]:
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(kernel_key):
-    """HBM bytes per dispatch of `kernel_key` from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (profiles/traffic.json, calibrated against a
-    plain copy), or None when that kernel has not been measured."""
+    """(HBM bytes per dispatch of `kernel_key`, build hash of that measurement)
+    from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (profiles/traffic.json, calibrated against a plain copy); bytes None when
+    that kernel has not been measured."""
     try:
         with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
-            return json.load(f)["kernels"][kernel_key]["hbm_bytes"]
-    except (OSError, KeyError, ValueError):
-        return None
+            doc = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    entry = doc.get("kernels", {}).get(kernel_key)
+    return (entry["hbm_bytes"] if entry else None), doc.get("build")
+
+
+def cpu_threads():
+    """Threads for the CPU baselines: the CPUs this process may run on, capped
+    at OMP_NUM_THREADS when it is set (the GPU boxes set it to their CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def host_info(threads):
+    import platform
+    import torch
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cores": threads, "host_cpus": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "cpu_model": model, "torch": torch.__version__}
 
 
 def copy_calibration(nbytes=1 << 30, reps=3):
@@ -110,7 +161,9 @@ def bench_scan_fwd(steps, warmup):
     # read skipped on chunk 0
     n = math.ceil(T / C)
     kflops = B * H * (n * (8 * C * C * d * 2) + (n - 1) * 8 * C * d * d)
-    return dt * 1e3, kms, B * T, scan_flops(B, H, T, d, C), kflops
+    # the same with the score and intra read counted over the causal half (C (C + 1) / 2 of C^2 pairs)
+    kflops_causal = B * H * (n * (8 * (C * (C + 1) // 2) * d * 2) + (n - 1) * 8 * C * d * d)
+    return dt * 1e3, kms, B * T, scan_flops(B, H, T, d, C), kflops, kflops_causal
 
 
 def bench_decode(n_steps):
@@ -541,7 +594,7 @@ def _delta_reference_steps(q, k, v, gamma, beta, d, chunk):
     return torch.cat(ys, 2), (sr, si)
 
 
-def bench_delta(steps, warmup):
+def bench_delta(steps, warmup, reference=True):
     """E2 delta rule forward + backward at the config-3 shape (one state: B=8,
     T=2048, H=12, d=64, fp32): the HIP kernels against the reference's chunked
     UT-transform steps (delta_chunk 64) run in torch on the same GPU.  The
@@ -580,19 +633,34 @@ def bench_delta(steps, warmup):
         with torch.no_grad():
             delta_planar(*planes, gamma, beta, q_scale=d ** -0.5)
 
-    def reference():
+    def reference_steps():
         y, _ = _delta_reference_steps((leaves[0], leaves[1]), (leaves[2], leaves[3]), (leaves[4], leaves[5]),
                                       leaves[6], leaves[7], d, 64)
         torch.autograd.grad([y[..., 0], y[..., 1]], leaves, dy)
 
+    if reference == "only":  # the torch reference steps alone (never under a counter pass)
+        ref_ms = timed(reference_steps, max(2, steps // 5))
+        return {"config": "E2 reference steps, B=8 T=2048 H=12 d=64 fp32, fwd+bwd", "ms_fwd_bwd": ref_ms}
     ms = timed(fused, steps)
     fwd_ms = timed(fwd_only, steps)
-    ref_ms = timed(reference, max(2, steps // 5))
     fwd_bytes = 6 * B * H * T * d * 4 + 2 * B * H * T * 4 + 2 * B * H * T * d * 4 + B * H * (T // 16) * 2 * d * d * 4
-    return {"config": "E2 delta write, B=8 T=2048 H=12 d=64 fp32, fwd+bwd", "ms_fwd_bwd": ms, "ms_fwd": fwd_ms,
-            "reference_steps_ms_fwd_bwd": ref_ms, "speedup": ref_ms / ms, "tokens_per_s": B * T / (ms * 1e-3),
-            "us_per_token_fwd": fwd_ms * 1e3 / T, "fwd_bytes": fwd_bytes,
-            "fwd_hbm_frac": fwd_bytes / (fwd_ms * 1e-3) / HBM_PEAK}
+    out = {"config": "E2 delta write, B=8 T=2048 H=12 d=64 fp32, fwd+bwd", "ms_fwd_bwd": ms, "ms_fwd": fwd_ms,
+           "tokens_per_s": B * T / (ms * 1e-3), "us_per_token_fwd": fwd_ms * 1e3 / T, "fwd_bytes": fwd_bytes,
+           "fwd_hbm_frac": fwd_bytes / (fwd_ms * 1e-3) / HBM_PEAK}
+    if reference:
+        out["reference_steps_ms_fwd_bwd"] = timed(reference_steps, max(2, steps // 5))
+        out["speedup"] = out["reference_steps_ms_fwd_bwd"] / ms
+    return out
+
+
+def _median_time(fn, reps):
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
 
 
 def cpu_baseline_scan():
@@ -600,7 +668,7 @@ def cpu_baseline_scan():
     fp32, on a bounded sample: 1 of the 8 batch rows (H=12, T=2048)."""
     import torch
     from oracle.pam import chunked_head, make_scan_inputs
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     q, k, v, gamma = make_scan_inputs(1, 12, 2048, 64, 1002, unit_qk=True, dtype=torch.float32)
     chunked_head(q, k, v, gamma[0], 64, 64)
@@ -610,8 +678,86 @@ def cpu_baseline_scan():
         chunked_head(q, k, v, gamma[0], 64, 64)
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
-    return {"value": 2048 / t, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": "oracle.pam.chunked_head fp32, B=1 of 8 (H=12, T=2048, d=64, C=64), median of 3"}
+    out = {"value": 2048 / t, "unit": "tokens/s", "cores": threads, "kind": "port",
+           "sample": "oracle.pam.chunked_head fp32, B=1 of 8 (H=12, T=2048, d=64, C=64), median of 3"}
+    out.update(host_info(threads))
+    return out
+
+
+def cpu_baseline_e3():
+    """Config 3 on the CPU: the reference's fused E3 chunk loop restated in torch
+    (oracle.pam.multistate_fused, v11/model.py:657-781), fp32 forward plus
+    autograd backward on the bf16-rounded inputs, 1 of the 8 batch rows."""
+    import torch
+    from oracle import pam as O
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    M, B, H, T, d, C = 3, 1, 12, 2048, 64, 64
+    q, k, v, gamma = O.make_scan_inputs(B, H, T, d, 1003, m_states=M, gamma_mu=2.0, gamma_mu_step=1.0,
+                                        unit_qk=True, dtype=torch.float32)
+    q, k, v = (x.to(torch.bfloat16).to(torch.float32) for x in (q, k, v))
+    dy = torch.randn(B, H, T, d, 2, generator=torch.Generator().manual_seed(1004))
+    phase, routing = torch.zeros(M, B, H, T), torch.ones(M, B, H, T)
+
+    def step():
+        xs = [x.clone().requires_grad_(True) for x in (q, k, v, gamma)]
+        y, _ = O.multistate_fused(xs[0], xs[1], xs[2], xs[3], phase, routing, d, C)
+        (y * dy).sum().backward()
+
+    t = _median_time(step, 3)
+    out = {"value": B * T / t, "unit": "tokens/s", "kind": "port",
+           "sample": "oracle.pam.multistate_fused fp32 forward + autograd backward, M=3, B=1 of 8 "
+                     "(H=12, T=2048, d=64, C=64), median of 3"}
+    out.update(host_info(threads))
+    return out
+
+
+def cpu_baseline_decode(steps=20):
+    """Config 4 on the CPU: the reference's token step (oracle.pam.recur_step_additive,
+    v11/model.py:927-965) over 16 layers x 12 heads for a sample of 16 live
+    slots, `steps` consecutive tokens, fp32."""
+    import torch
+    from oracle import pam as O
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    S, G, d = 16, 16 * 12, 64
+    gen = torch.Generator().manual_seed(1004)
+    state = torch.randn(S, G, d, d, 2, generator=gen) * 0.01
+    gamma = torch.sigmoid(torch.randn(S, G, generator=gen) + 3)
+    qkv = [torch.randn(3, S, G, d, 2, generator=gen) for _ in range(steps)]
+    O.recur_step_additive(state, gamma, qkv[0][2], qkv[0][1], qkv[0][0] * d ** -0.5)
+    t0 = time.perf_counter()
+    for x in qkv:
+        _, state = O.recur_step_additive(state, gamma, x[2], x[1], x[0] * d ** -0.5)
+    t = time.perf_counter() - t0
+    out = {"value": S * steps / t, "unit": "tokens/s", "kind": "port",
+           "sample": f"oracle.pam.recur_step_additive fp32, 16 live slots x 16 layers x 12 heads (d=64), "
+                     f"{steps} consecutive steps"}
+    out.update(host_info(threads))
+    return out
+
+
+def cpu_baseline_ce():
+    """Config 5 on the CPU: the reference's chunked fused CE restated in torch
+    (oracle.ce ce_forward / ce_backward, v11/fused_ce.py:28-82), fp32 on the
+    bf16-rounded inputs, 512 of the 16384 rows against the full vocabulary."""
+    import torch
+    from oracle.ce import ce_backward, ce_forward, make_ce_inputs
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    N, d_model, V = 512, 512, 50261
+    h, w, tgt = make_ce_inputs(N, d_model, V, 1005, dtype=torch.bfloat16)
+    h, w = h.float(), w.float()
+
+    def step():
+        _, denom = ce_forward(h, w, tgt, chunk=N)
+        ce_backward(h, w, tgt, denom, chunk=N)
+
+    t = _median_time(step, 3)
+    out = {"value": N / t, "unit": "tokens/s", "kind": "port",
+           "sample": "oracle.ce ce_forward + ce_backward fp32, 512 of 16384 rows, V=50261, D=1024, median of 3"}
+    out.update(host_info(threads))
+    return out
 
 
 def main():
@@ -623,7 +769,7 @@ def main():
     import torch
     assert torch.cuda.is_available(), "bench.py needs the MI355X"
     if args.only is not None:
-        fn = {"scan_fwd": lambda: dict(zip(("ms", "kernel_ms", "tokens", "flops", "kernel_flops"),
+        fn = {"scan_fwd": lambda: dict(zip(("ms", "kernel_ms", "tokens", "flops", "kernel_flops", "kernel_flops_causal"),
                                            bench_scan_fwd(args.steps, args.warmup))),
               "decode": lambda: bench_decode(args.decode_steps),
               "decode_e3": lambda: bench_decode_e3_rope(max(50, args.decode_steps // 5)),
@@ -632,13 +778,15 @@ def main():
               "ce": lambda: bench_ce(args.steps, args.warmup),
               "cplx": lambda: bench_complex_ops(args.steps, args.warmup),
               "layer": lambda: bench_pam_layer(args.steps, args.warmup),
-              "delta": lambda: bench_delta(args.steps, args.warmup),
+              "delta": lambda: bench_delta(args.steps, args.warmup, reference=False),
+              "delta_ref": lambda: bench_delta(args.steps, args.warmup, reference="only"),
               "copy": copy_calibration}[args.only]
         print(json.dumps({"only": args.only, "result": fn()}), flush=True)
         return
-    ms, kms, tokens, flops, kflops = bench_scan_fwd(args.steps, args.warmup)
+    ms, kms, tokens, flops, kflops, kflops_causal = bench_scan_fwd(args.steps, args.warmup)
     value = tokens / (ms * 1e-3)
     achieved = kflops / (kms * 1e-3)
+    traffic, traffic_build = measured_traffic("scan_fwd/chunk_output_f32_kernel<64>")
     out = {
         "metric": "PAM prefill tokens/s + MFMA %; ragged decode tokens/s + HBM GB/s (256 slots)",
         "value": value,
@@ -648,7 +796,6 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": ms,
         "higher_is_better": True,
-        "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic (seeded CPU draws, BASELINE.json config 2)",
@@ -657,9 +804,10 @@ def main():
                    "layout": "planar re/im fp32"},
         "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": MFMA_FP32_PEAK / 1e12,
                      "unit": "TFLOP/s", "frac": achieved / MFMA_FP32_PEAK,
-                     "traffic": measured_traffic("scan_fwd/chunk_output_f32_kernel<64>"),
+                     "frac_causal": kflops_causal / (kms * 1e-3) / MFMA_FP32_PEAK,
+                     "traffic": traffic, "traffic_build": traffic_build, "build": source_hash(),
                      "kernel": "chunk_output_f32_kernel<64>", "kernel_ms": kms,
-                     "kernel_flops": kflops},
+                     "kernel_flops": kflops, "kernel_flops_causal": kflops_causal},
         "scan_fwd_total": {"flops": flops, "tflops": flops / (ms * 1e-3) / 1e12,
                            "mfma_fp32_frac": flops / (ms * 1e-3) / MFMA_FP32_PEAK},
     }
@@ -676,6 +824,8 @@ def main():
                          "delta_e2_config3_shape": bench_delta(max(3, args.steps // 4), 1)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_scan()
+        out["cpu_baselines"] = {"config3_e3_fwd_bwd": cpu_baseline_e3(), "config4_decode": cpu_baseline_decode(),
+                                "config5_ce_fwd_bwd": cpu_baseline_ce()}
     print(json.dumps(out), flush=True)
 
 

@@ -20,6 +20,30 @@ def _rel(a, b):
     return ((a.double() - b.double()).abs().max() / (b.double().abs().max() + 1e-30)).item()
 
 
+def _rel_heads(a, b, lead):
+    """Largest per-head relative error: max |a - b| / max |b| within each slice
+    over the first `lead` dimensions ((b, h) or (m, b, h)), then the max over
+    slices."""
+    a, b = a.double(), b.double()
+    err = (a - b).abs().flatten(lead).amax(-1)
+    ref = b.abs().flatten(lead).amax(-1)
+    return (err / (ref + 1e-30)).max().item()
+
+
+# leading (per-head) dimensions of each gradient: dq, dk, dv [B,H,T,d,2];
+# dgamma, dphase, drouting [M,B,H,T]; ds0 [M,B,H,d,d,2]
+LEAD = [2, 2, 2, 3, 3, 3, 3]
+
+
+def _check(got, ref, tol, names=None):
+    for name, lead, a, b in zip(names or NAMES, LEAD, got, ref):
+        if a is None or b is None:
+            continue
+        assert math.isfinite(a.abs().sum().item()), name
+        assert _rel(a, b) < tol, f"{name}: rel {_rel(a, b):.2e}"
+        assert _rel_heads(a, b, lead) < tol, f"{name}: worst head rel {_rel_heads(a, b, lead):.2e}"
+
+
 def _case(M, B, H, T, d, seed, with_rot, with_s0, dtype):
     q, k, v, gamma = O.make_scan_inputs(B, H, T, d, seed, m_states=M, gamma_mu=2.0 if M > 1 else 3.0,
                                         gamma_mu_step=1.0 if M > 1 else 0.0, unit_qk=True, dtype=torch.float32)
@@ -43,7 +67,7 @@ def _oracle_grads(q, k, v, gamma, dy, ds, phase, routing, s0, d, C):
     return out
 
 
-def _gpu_grads(q, k, v, gamma, dy, ds, phase, routing, s0, d, C, dtype, with_rot):
+def _gpu_grads(q, k, v, gamma, dy, ds, phase, routing, s0, d, C, dtype, with_rot, outs=None):
     from qllm2_amd.pam_scan import pam_scan_planar
     dev = torch.device("cuda")
 
@@ -59,6 +83,9 @@ def _gpu_grads(q, k, v, gamma, dy, ds, phase, routing, s0, d, C, dtype, with_rot
         s0r, s0i = leaf(s0[..., 0].contiguous()), leaf(s0[..., 1].contiguous())
         s0p = (s0r, s0i)
     y_re, y_im, s_re, s_im = pam_scan_planar(*planes, gam, q_scale=d ** -0.5, chunk=C, rot=rot, s0=s0p)
+    if outs is not None:
+        outs["y"] = torch.stack([y_re, y_im], -1).detach().float().cpu()
+        outs["s"] = torch.stack([s_re, s_im], -1).detach().float().cpu()
     dyd, dsd = dy.to(dev), ds.to(dev)
     loss = ((y_re * dyd[..., 0]).sum() + (y_im * dyd[..., 1]).sum() + (s_re * dsd[..., 0]).sum()
             + (s_im * dsd[..., 1]).sum())
@@ -86,10 +113,7 @@ def test_scan_backward_fp32(gpu_lib, M, T, C, with_rot, with_s0):
     case = _case(M, B, H, T, d, 3000 + M * 7 + T + C, with_rot, with_s0, torch.float32)
     ref = _oracle_grads(*case, d, C)
     got = _gpu_grads(*case, d, C, torch.float32, with_rot)
-    for name, a, b in zip(NAMES, got, ref):
-        if a is None or b is None:
-            continue
-        assert _rel(a, b) < 1e-4, f"{name}: rel {_rel(a, b):.2e}"
+    _check(got, ref, 1e-4)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -126,10 +150,7 @@ def test_scan_backward_bf16_e3(gpu_lib):
     case = _case(M, B, H, T, d, 3303, False, False, torch.bfloat16)
     ref = _oracle_grads(*case, d, C)
     got = _gpu_grads(*case, d, C, torch.bfloat16, False)
-    for name, a, b in zip(NAMES, got, ref):
-        if a is None or b is None:
-            continue
-        assert _rel(a, b) < 2e-2, f"{name}: rel {_rel(a, b):.2e}"
+    _check(got, ref, 2e-2)
 
 
 @pytest.mark.parametrize("M,T,with_rot,with_s0", [
@@ -137,20 +158,19 @@ def test_scan_backward_bf16_e3(gpu_lib):
     (3, 150, True, True),    # odd chunk count, ragged last chunk
     (1, 200, False, False),  # even chunk count, ragged last chunk, no rotation
     (2, 128, True, False),   # two full chunks
+    (3, 64 * 6 + 10, True, True),  # seven chunks: a full segment of four, then a segment of three
+    (2, 64 * 9, True, True),       # nine chunks: the last segment holds one chunk
 ])
 def test_scan_backward_bf16_ragged(gpu_lib, M, T, with_rot, with_s0):
-    """bf16 inputs (the state-pass kernels) at sequence lengths that are not a
-    multiple of the chunk and chunk counts of 1, 2, odd and even: every gradient
+    """bf16 inputs (the segment kernels, four 64-step chunks per segment) at
+    sequence lengths that are not a multiple of the chunk, chunk counts of 1, 2,
+    odd and even, and segment counts with a partial last segment: every gradient
     against oracle autograd."""
     B, H, d, C = 2, 2, 64, 64
     case = _case(M, B, H, T, d, 3500 + M * 11 + T, with_rot, with_s0, torch.bfloat16)
     ref = _oracle_grads(*case, d, C)
     got = _gpu_grads(*case, d, C, torch.bfloat16, with_rot)
-    for name, a, b in zip(NAMES, got, ref):
-        if a is None or b is None:
-            continue
-        assert math.isfinite(a.abs().sum().item()), name
-        assert _rel(a, b) < 2e-2, f"{name}: rel {_rel(a, b):.2e}"
+    _check(got, ref, 2e-2)
 
 
 def test_scan_backward_config3_full_size(gpu_lib):
@@ -168,11 +188,13 @@ def test_scan_backward_config3_full_size(gpu_lib):
     y, s = O.multistate_fused(xs[0], xs[1], xs[2], xs[3], phase, routing, d, C)
     (y * dy).sum().backward()
     ref = [x.grad for x in xs]
+    y_ref, s_ref = y.detach(), s.detach()
     del y, s
-    got = _gpu_grads(q, k, v, gamma, dy, ds, phase, routing, None, d, C, torch.bfloat16, False)
-    for name, a, b in zip(NAMES[:4], got[:4], ref):
-        assert _rel(a, b) < 2e-2, f"{name}: rel {_rel(a, b):.2e}"
-        assert math.isfinite(a.abs().sum().item())
+    outs = {}
+    got = _gpu_grads(q, k, v, gamma, dy, ds, phase, routing, None, d, C, torch.bfloat16, False, outs)
+    assert _rel(outs["y"], y_ref) < 2e-2 and _rel_heads(outs["y"], y_ref, 2) < 2e-2
+    assert _rel(outs["s"], s_ref) < 2e-2 and _rel_heads(outs["s"], s_ref, 3) < 2e-2
+    _check(got[:4], ref, 2e-2, NAMES[:4])
 
 
 def test_scan_bf16_e3_decay_regimes(gpu_lib):

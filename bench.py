@@ -317,13 +317,16 @@ def bench_e3_fwd_bwd(steps, warmup):
             "config": "M=3 B=8 T=2048 H=12 d=64 C=64 bf16 in, fp32 state, fwd+bwd"}
 
 
-def bench_ce(steps, warmup):
-    """Config 5: tied complex LM-head CE fwd+bwd, N=16384, D=1024, V=50261, bf16."""
+def bench_ce(steps, warmup, master_fp32=False):
+    """Config 5: tied complex LM-head CE fwd+bwd, N=16384, D=1024, V=50261, bf16
+    (master_fp32: an fp32 master E, run on its bf16 copy, fp32 dE)."""
     import torch
     from qllm2_amd.fused_ce import fused_linear_cross_entropy
     from oracle.ce import ce_flops, make_ce_inputs
     N, d_model, V = 16384, 512, 50261
     h, w, t = make_ce_inputs(N, d_model, V, 1005, dtype=torch.bfloat16)
+    if master_fp32:
+        w = w.float()
     h, w, t = h.cuda().requires_grad_(True), w.cuda().requires_grad_(True), t.cuda()
 
     def step():
@@ -345,7 +348,7 @@ def bench_ce(steps, warmup):
     flops = ce_flops(N, V, 2 * d_model)
     return {"ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3), "tflops": flops / (ms * 1e-3) / 1e12,
             "bf16_mfma_frac": flops / (ms * 1e-3) / MFMA_BF16_PEAK, "flops": flops,
-            "config": "N=16384 D=1024 V=50261 bf16, chunk=4096, fwd+bwd"}
+            "config": "N=16384 D=1024 V=50261 bf16" + (", fp32 master E" if master_fp32 else "") + ", chunk=4096, fwd+bwd"}
 
 
 def bench_complex_ops(steps, warmup):
@@ -819,6 +822,7 @@ def main():
                          # slow (E3 0.69 vs 0.66 ms per step)
                          "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 5),
                          "ce_fwd_bwd_config5": bench_ce(max(3, args.steps // 4), 3),
+                         "ce_fwd_bwd_config5_fp32_master_e": bench_ce(max(3, args.steps // 4), 3, master_fp32=True),
                          "complex_elementwise": bench_complex_ops(max(3, args.steps // 2), 5),
                          "pam_layer_config3": bench_pam_layer(max(3, args.steps // 2), 5),
                          "delta_e2_config3_shape": bench_delta(max(3, args.steps // 4), 1)}

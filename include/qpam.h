@@ -422,7 +422,11 @@ typedef struct {
     const float *grad_scale;       /* device scalar: grad_output / denom */
     void *dh; int64_t lddh;        /* dtype of h */
     float *dw; int64_t lddw;       /* fp32, accumulated (caller zeroes) */
-    int32_t chunk;                 /* rows per G buffer */
+    int32_t chunk;                 /* the reference's row chunk: one pass covers as many rows
+                                      as fit the bytes the reference keeps alive for `chunk`
+                                      rows (fp32 logits and softmax): 4 chunk rows with bf16
+                                      inputs and the library GEMMs (G^T only), 2 chunk rows
+                                      with the hand-written GEMMs (G and G^T), chunk rows fp32 */
     void *workspace;
     size_t workspace_bytes;
 } qpam_ce_bwd_args;

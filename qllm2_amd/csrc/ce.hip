@@ -1135,13 +1135,25 @@ size_t fwd_ws(const qpam_ce_fwd_args &a) {
     return (size_t)a.N * n_vt * 12 + 256;
 }
 
+// Rows of one backward pass.  The reference keeps the fp32 logits and softmax of
+// `chunk` rows alive (8 bytes per row and vocabulary entry); a pass here covers
+// as many rows as fit those bytes: bf16 G^T alone (library GEMMs) takes 2 bytes,
+// bf16 G and G^T (hand-written GEMMs) 4 bytes, fp32 G and G^T 8 bytes.
+int pass_rows(const qpam_ce_bwd_args &a) {
+    const int64_t factor = a.dtype == QPAM_BF16 ? (blas::enabled() ? 4 : 2) : 1;
+    return (int)std::min<int64_t>((int64_t)a.chunk * factor, a.N);
+}
+
 template <typename T>
 size_t bwd_ws(const qpam_ce_bwd_args &a) {
-    const int64_t Vp = round_up(a.V, vocab_pad<T>()), chunk = std::min(a.chunk, a.N);
+    const int64_t Vp = round_up(a.V, vocab_pad<T>()), chunk = pass_rows(a);
     const int64_t Rp = round_up((int)chunk, row_tile<T>());
+    if (is_bf<T>() && blas::enabled())  // G^T and the library GEMMs' workspace
+        return (size_t)(Vp * Rp * sizeof(T)) + 4 * 256 +
+               std::max((size_t)big::DH_SPLITS * chunk * a.D * sizeof(float), blas::WS_BYTES) + 256;
     const int64_t elems = (int64_t)a.D * Vp + chunk * Vp + Vp * Rp + (int64_t)a.D * Rp;
     size_t bytes = (size_t)(elems * sizeof(T)) + 4 * 256;
-    // bf16: split-K partials of the hand-written dH GEMM, or the hipBLASLt workspace
+    // bf16: split-K partials of the hand-written dH GEMM
     if (is_bf<T>()) bytes += std::max((size_t)big::DH_SPLITS * chunk * a.D * sizeof(float), blas::WS_BYTES) + 256;
     return bytes;
 }
@@ -1200,7 +1212,7 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
     BwdParams &p = q.p;
     p.a = a;
     p.Vp = round_up(a.V, vocab_pad<U>());
-    const int chunk = std::min(a.chunk, a.N);
+    const int chunk = pass_rows(a);
     const int Rmax = round_up(chunk, big::BTM);
     const bool wide_tiles = use_wide(a.D);
     // the G-tile kernel: 256 x 256 tiles, or 256 x 128 for hidden sizes that are not
@@ -1216,14 +1228,11 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
         return launch_status(wide_tiles ? "ce grad_tile_kernel (bf16, 256 x 256)" : "ce grad_tile_kernel (bf16)");
     };
     U *ws = (U *)a.workspace;
-    p.wt = ws;
-    p.gbuf = ws + (int64_t)a.D * p.Vp;
-    p.gtbuf = (U *)p.gbuf + (int64_t)chunk * p.Vp;
-    p.ht = (U *)p.gtbuf + (int64_t)p.Vp * Rmax;
-    uintptr_t part = (uintptr_t)((U *)p.ht + (int64_t)a.D * Rmax);
-    q.dh_part = (float *)((part + 255) & ~(uintptr_t)255);
     const size_t smem = big::SMEM;
     if (blas::enabled()) {
+        p.wt = p.gbuf = p.ht = nullptr;
+        p.gtbuf = ws;
+        q.dh_part = (float *)(((uintptr_t)(ws + (int64_t)p.Vp * Rmax) + 255) & ~(uintptr_t)255);
         // G^T [Vp][Rp] from the fused grad tiles, then two library GEMMs (column-major views):
         //   dW^T[D][V] += H^T G^T-view   (m = D, n = V, k = rows)
         //   dH^T[D][rows] = W^T G-view   (m = D, n = rows, k = V)
@@ -1245,6 +1254,11 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
         }
         return QPAM_OK;
     }
+    p.wt = ws;
+    p.gbuf = ws + (int64_t)a.D * p.Vp;
+    p.gtbuf = (U *)p.gbuf + (int64_t)chunk * p.Vp;
+    p.ht = (U *)p.gtbuf + (int64_t)p.Vp * Rmax;
+    q.dh_part = (float *)(((uintptr_t)((U *)p.ht + (int64_t)a.D * Rmax) + 255) & ~(uintptr_t)255);
     p.write_g = 1;
     QPAM_CHECK_HIP(hipFuncSetAttribute(gkern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)gsmem));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)big::dw_gemm_kernel,
@@ -1293,7 +1307,7 @@ int run_bwd(const qpam_ce_bwd_args &a, hipStream_t stream) {
     p.a = a;
     p.write_g = 1;
     p.Vp = round_up(a.V, VT);
-    const int chunk = std::min(a.chunk, a.N);
+    const int chunk = pass_rows(a);
     const int Rmax = round_up(chunk, BM);
     T *ws = (T *)a.workspace;
     p.wt = ws;

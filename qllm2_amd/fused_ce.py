@@ -159,8 +159,13 @@ def fused_linear_cross_entropy(hidden_rows: Tensor, weight_matrix: Tensor, targe
                                mask: Optional[Tensor] = None, chunk: int = 4096,
                                ignore_index: int = -100) -> Tensor:
     """Mean cross-entropy of (hidden_rows @ weight_matrix.T) vs targets
-    (v11/fused_ce.py:85-94).  `chunk` bounds the rows whose softmax gradient
-    is alive at once in the backward."""
+    (v11/fused_ce.py:85-94).  `chunk` bounds the backward's live gradient
+    memory as in the reference (fp32 logits and softmax of `chunk` rows, 8
+    bytes per row and vocabulary entry): with bf16 operands one pass holds a
+    bf16 gradient of 4 x chunk rows (2 x chunk with QPAM_CE_GEMM=hip), the
+    same bytes.  An fp32 weight_matrix with bf16 hidden_rows (fp32 master
+    embedding) runs on a bf16 copy of the weights and returns an fp32
+    gradient."""
     if not hidden_rows.is_cuda:
         return _reference.on_cpu("fused_ce.fused_linear_cross_entropy", "fused_linear_cross_entropy", hidden_rows,
                                  weight_matrix, targets, mask=mask, chunk=chunk, ignore_index=ignore_index)

@@ -78,14 +78,36 @@ def _select_gemm(monkeypatch, path):
 
 
 @pytest.mark.parametrize("path", GEMM_PATHS)
-def test_ce_bf16(gpu_lib, monkeypatch, path):
+@pytest.mark.parametrize("chunk", [384, 64])
+def test_ce_bf16(gpu_lib, monkeypatch, path, chunk):
+    """bf16 operands; chunk 64 makes the backward take several passes (256 rows
+    each on the library GEMMs, 128 on the hand-written ones)."""
     _select_gemm(monkeypatch, path)
     h, w, t = _data(1000, 128, 3000, 6, torch.bfloat16, e_std=0.1)
     t[::10] = -100
-    loss, dh, dw = _gpu(h, w, t, chunk=384)
+    loss, dh, dw = _gpu(h, w, t, chunk=chunk)
     ref, denom = O.ce_forward(h.double(), w.double(), t, chunk=384)
     rdh, rdw = O.ce_backward(h.double(), w.double(), t, denom, chunk=384)
     assert dh.dtype == torch.bfloat16 and dw.dtype == torch.bfloat16
+    assert _rel(loss, ref) < 2e-2
+    assert _rel(dh, rdh) < 2e-2 and _rel(dw, rdw) < 2e-2
+
+
+@pytest.mark.parametrize("path", GEMM_PATHS)
+def test_ce_fp32_master_weight(gpu_lib, monkeypatch, path):
+    """bf16 hidden rows with an fp32 master embedding (config 5's E): the GEMMs run
+    on a bf16 copy of E, the loss and dH match the oracle on the bf16-rounded
+    values, and dE comes back in fp32 (the gradient of the bf16 copy), over
+    several backward passes."""
+    _select_gemm(monkeypatch, path)
+    h, w, t = _data(1000, 128, 3000, 16, torch.bfloat16, e_std=0.1)
+    w = w.float() + torch.randn(w.shape, generator=torch.Generator().manual_seed(17)) * 1e-3  # not bf16-exact
+    t[::10] = -100
+    loss, dh, dw = _gpu(h, w, t, chunk=64)
+    wb = w.to(torch.bfloat16).double()
+    ref, denom = O.ce_forward(h.double(), wb, t, chunk=384)
+    rdh, rdw = O.ce_backward(h.double(), wb, t, denom, chunk=384)
+    assert dh.dtype == torch.bfloat16 and dw.dtype == torch.float32
     assert _rel(loss, ref) < 2e-2
     assert _rel(dh, rdh) < 2e-2 and _rel(dw, rdw) < 2e-2
 

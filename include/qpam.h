@@ -319,9 +319,13 @@ typedef struct {
     float *s_re, *s_im;
     void *workspace;
     size_t workspace_bytes;
+    void *scratch;                         /* qpam_delta_scratch_size bytes: the forward's per-chunk
+                                              products (always required by qpam_delta_fwd) */
+    size_t scratch_bytes;
 } qpam_delta_args;
 
 size_t qpam_delta_workspace_size(const qpam_delta_args *a);
+size_t qpam_delta_scratch_size(const qpam_delta_args *a);
 int qpam_delta_fwd(const qpam_delta_args *a, void *stream);
 
 /* Backward of qpam_delta_fwd (`fwd` describes the forward call; its

@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -119,6 +119,7 @@ class DeltaArgs(ctypes.Structure):
         ("gamma", c_ptr), ("beta", c_ptr), ("sg_b", c_i64), ("sg_h", c_i64), ("sg_t", c_i64),
         ("s0_re", c_ptr), ("s0_im", c_ptr), ("y", MView), ("s_re", c_ptr), ("s_im", c_ptr),
         ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+        ("scratch", c_ptr), ("scratch_bytes", ctypes.c_size_t),
     ]
 
 
@@ -182,6 +183,7 @@ SIGNATURES = {
     "qpam_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(PrologueBwdArgs), c_ptr]),
     "qpam_cabs_fwd": (ctypes.c_int, [c_i32, c_i64, c_ptr, c_ptr, c_ptr]),
     "qpam_delta_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(DeltaArgs)]),
+    "qpam_delta_scratch_size": (ctypes.c_size_t, [ctypes.POINTER(DeltaArgs)]),
     "qpam_delta_fwd": (ctypes.c_int, [ctypes.POINTER(DeltaArgs), c_ptr]),
     "qpam_delta_bwd_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(DeltaBwdArgs)]),
     "qpam_delta_bwd": (ctypes.c_int, [ctypes.POINTER(DeltaBwdArgs), c_ptr]),

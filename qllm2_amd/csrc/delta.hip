@@ -234,41 +234,508 @@ __host__ __device__ __forceinline__ size_t bwd_sub_bytes(const qpam_delta_args &
     return (size_t)a.B * a.H * SUBS * STATE_FLOATS * sizeof(float);
 }
 
-constexpr int FNT = 8;   // tokens per forward span
+// ---------------------------------------------------------------------------
+// Forward over 64-step chunks on fp32 MFMA (v_mfma_f32_16x16x4f32).  Unrolled
+// over a chunk, the recurrence is the reference's UT form: with L_t the
+// inclusive prefix of log(gamma + eps) from the chunk's start, alpha_t = e^{L_t},
+// D[t,s] = e^{L_t - L_s} and S_0 the state entering the chunk,
+//     (I + M) U = W,   M[t,s] = beta_t D[t,s] (k_t . conj(k_s))  (s < t),
+//     W_t = beta_t (v_t - alpha_t S_0 k_t),
+//     y_t = alpha_t S_0 q~_t + sum_{s<=t} D[t,s] (q~_t . conj(k_s)) u_s,
+//     S_end = alpha_last S_0 + sum_s D[last,s] u_s (x) conj(k_s).
+// delta_prep_kernel (chunk-parallel, a block per (b, h, chunk)) forms everything
+// that does not depend on S: the Gram and query-key products, T = (I + M)^{-1}
+// (diagonal 16 x 16 blocks by forward substitution, the blocks below them as
+// T_bc = -T_bb sum_k M_bk T_kc) and Ahat[t,s] = D[t,s] (q~_t . conj(k_s)), stored
+// per chunk in the MFMA A-operand order.  delta_chunk_kernel then walks the
+// chunks of one (b, h) for 16 value rows (rows of the recurrence are
+// independent: four blocks per chain) with S^T in LDS: W = beta (V - alpha K S^T),
+// U = T W, the state update in four 16-step quarters (each quarter's end state is
+// the backward's checkpoint before the next 16 steps), then Y = Ahat U + alpha
+// Q~ S^T with the chunk's entering state.
+constexpr int CH = 64;                 // steps per chunk
+constexpr int ROW_BLOCKS = 4;          // blocks per chain in the chunk pass (16 value rows each)
+constexpr int KP = CH + 4;             // LDS pitch of [64][64] fp32 tiles read element-wise
+constexpr int SP = 16;                 // LDS pitch of [64][16] fp32 tiles
+constexpr int NBLK = 10;               // 16 x 16 blocks on and below the diagonal of a 64 x 64 matrix
+constexpr int BLK = 2 * 256;           // floats of one complex 16 x 16 block (re plane, then im)
+constexpr int PREP_T = 0, PREP_A = NBLK * BLK, PREP_L = 2 * NBLK * BLK;
+constexpr int PREP_FLOATS = PREP_L + CH;  // per chunk: T blocks, Ahat blocks, L
 
-__global__ void __launch_bounds__(64) delta_fwd_kernel(qpam_delta_args a) {
-    __shared__ Span<FNT, 4 * RPL> sp[2];
-    const int chain = blockIdx.x / NW, b = chain / a.H, h = chain - b * a.H, tid = threadIdx.x;
-    const Lane L(blockIdx.x - chain * NW, tid);
-    State s;
-    init_state(s, a.s0_re, a.s0_im, chain, L);
-    float *ckpt = static_cast<float *>(a.workspace);
-    if (ckpt) ckpt += (int64_t)chain * chain_groups(a.T) * STATE_FLOATS;
-    const int row0 = 4 * RPL * L.w;   // the wave's first row
-    SpanRegs<FNT, 4 * RPL, 64> regs;
-    regs.fetch(a, b, h, 0, row0, tid);
-    regs.commit(sp[0], tid);
-    __syncthreads();
-    for (int t0 = 0, buf = 0; t0 < a.T; t0 += FNT, buf ^= 1) {
-        const bool more = t0 + FNT < a.T;
-        if (more) regs.fetch(a, b, h, t0 + FNT, row0, tid);
-        const int n = min(FNT, a.T - t0);
-        for (int j = 0; j < n; ++j) {
-            const int t = t0 + j;
-            if (t % GROUP == 0 && ckpt) store_state(ckpt + (int64_t)(t / GROUP) * STATE_FLOATS, s, L.slot());
-            const Tok x = span_tok(sp[buf], j, L.cg, L.rg * RPL);
-            float yr[RPL], yi[RPL];
-            fwd_step(s, x, yr, yi);
-            if (L.cg == 0) {
-                const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)t * a.y.s2 + L.r0;
+__device__ __forceinline__ int blk(int b, int c) { return b * (b + 1) / 2 + c; }  // c <= b
+
+__device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void blk_store(float *dst, const floatx4 &cr, const floatx4 &ci, int l16, int g) {
 #pragma unroll
-                for (int rr = 0; rr < RPL; ++rr) a.y.re[yo + rr] = yr[rr], a.y.im[yo + rr] = yi[rr];
+    for (int r = 0; r < 4; ++r) {
+        dst[(4 * g + r) * 16 + l16] = cr[r];
+        dst[256 + (4 * g + r) * 16 + l16] = ci[r];
+    }
+}
+
+__device__ __forceinline__ int64_t chunk_prep(int64_t chain, int n_chunks, int c) {
+    return (chain * n_chunks + c) * PREP_FLOATS;
+}
+
+// LDS block [16][16] (re, im) -> global in A-operand order: lane (l16 = row, g)
+// reads float4 {A[row][4 ks + g], ks = 0..3} at (g * 16 + row) * 4 (per plane)
+__device__ __forceinline__ void blk_export(float *dst, const float *src, int tid, int nthreads) {
+    for (int e = tid; e < 512; e += nthreads) {
+        const int pl = e >> 8, idx = e & 255, ln = idx >> 2, ks = idx & 3;
+        const int row = ln & 15, gg = ln >> 4;
+        dst[e] = src[pl * 256 + row * 16 + 4 * ks + gg];
+    }
+}
+
+// Gauss accumulation of a complex product over k: t1 += ar br, t2 += ai bi,
+// t3 += (ar + ai)(br + bi); then re = t1 - t2, im = t3 - t1 - t2.  Three real
+// MFMAs per complex product instead of four.
+struct Gauss {
+    floatx4 t1, t2, t3;
+};
+__device__ __forceinline__ void gz(Gauss &x) {
+    x.t1 = x.t2 = x.t3 = floatx4{0.f, 0.f, 0.f, 0.f};
+}
+__device__ __forceinline__ void gstep(Gauss &x, float ar, float ai, float br, float bi) {
+    x.t1 = mfma4(ar, br, x.t1);
+    x.t2 = mfma4(ai, bi, x.t2);
+    x.t3 = mfma4(ar + ai, br + bi, x.t3);
+}
+__device__ __forceinline__ floatx4 gre(const Gauss &x) { return x.t1 - x.t2; }
+__device__ __forceinline__ floatx4 gim(const Gauss &x) { return x.t3 - x.t1 - x.t2; }
+
+// C = A B for complex 16 x 16 LDS blocks (Gauss)
+__device__ __forceinline__ void blk_mul_g(Gauss &x, const float *A, const float *B, int l16, int g) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        const int k = 4 * ks + g;
+        gstep(x, A[l16 * 16 + k], A[256 + l16 * 16 + k], B[k * 16 + l16], B[256 + k * 16 + l16]);
+    }
+}
+// element (4g + r, l16) of an LDS block, re and im
+__device__ __forceinline__ float blk_re(const float *A, int g, int r, int l16) { return A[(4 * g + r) * 16 + l16]; }
+__device__ __forceinline__ float blk_im(const float *A, int g, int r, int l16) {
+    return A[256 + (4 * g + r) * 16 + l16];
+}
+
+// The prep block's LDS: K and q_scale Q of the chunk while the Gram and
+// query-key products run; the same bytes then hold M, T and each wave's four
+// scratch blocks of the diagonal inversion, whose first three blocks later hold
+// the partial sums of the blocks below the diagonal (two blocks per CU).
+constexpr int PREP_KQ = 4 * CH * KP;
+constexpr int PREP_INV = NBLK * BLK * 2 + 16 * BLK;
+constexpr size_t PREP_SMEM = (size_t)((PREP_KQ > PREP_INV ? PREP_KQ : PREP_INV) + 2 * CH) * sizeof(float);
+
+__global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, float *prep, int n_chunks) {
+    extern __shared__ float sm[];
+    float *sKr = sm, *sKi = sKr + CH * KP, *sQr = sKi + CH * KP, *sQi = sQr + CH * KP;
+    float *sM = sm;                // after the products: M blocks [blk][re | im][16][16] (diagonal included)
+    float *sT = sM + NBLK * BLK;   // T blocks
+    float *sX = sT + NBLK * BLK;   // four scratch blocks per wave
+    float *sR = sX;                // after the inversion: three partial sums
+    const int big = PREP_KQ > PREP_INV ? PREP_KQ : PREP_INV;
+    float *sL = sm + big, *sB = sL + CH;
+    const int chain = blockIdx.x / n_chunks, c = blockIdx.x % n_chunks;
+    const int b = chain / a.H, h = chain % a.H;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int t0 = c * CH, valid = min(CH, a.T - t0);
+    {  // K and q_scale Q, rows past the end zero
+        const float *kre = static_cast<const float *>(a.k.re) + b * a.k.s0 + h * a.k.s1;
+        const float *kim = static_cast<const float *>(a.k.im) + b * a.k.s0 + h * a.k.s1;
+        const float *qre = static_cast<const float *>(a.q.re) + b * a.q.s0 + h * a.q.s1;
+        const float *qim = static_cast<const float *>(a.q.im) + b * a.q.s0 + h * a.q.s1;
+        for (int idx = tid; idx < CH * 16; idx += 256) {
+            const int r = idx >> 4, c4 = 4 * (idx & 15);
+            floatx4 kr = {0.f, 0.f, 0.f, 0.f}, ki = kr, qr = kr, qi = kr;
+            if (r < valid) {
+                const int64_t tk = (int64_t)(t0 + r) * a.k.s2 + c4, tq = (int64_t)(t0 + r) * a.q.s2 + c4;
+                kr = *reinterpret_cast<const floatx4 *>(kre + tk);
+                ki = *reinterpret_cast<const floatx4 *>(kim + tk);
+                qr = *reinterpret_cast<const floatx4 *>(qre + tq) * a.q_scale;
+                qi = *reinterpret_cast<const floatx4 *>(qim + tq) * a.q_scale;
+            }
+            *reinterpret_cast<floatx4 *>(sKr + r * KP + c4) = kr;
+            *reinterpret_cast<floatx4 *>(sKi + r * KP + c4) = ki;
+            *reinterpret_cast<floatx4 *>(sQr + r * KP + c4) = qr;
+            *reinterpret_cast<floatx4 *>(sQi + r * KP + c4) = qi;
+        }
+    }
+    if (w == 0) {  // inclusive prefix of log(gamma + eps); held past the end
+        const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)(t0 + min(lane, valid - 1)) * a.sg_t;
+        float x = lane < valid ? logf(a.gamma[go] + a.gamma_eps) : 0.f;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(x, off);
+            if (lane >= off) x += y;
+        }
+        sL[lane] = x;
+        sB[lane] = lane < valid ? a.beta[go] : 0.f;
+        prep[chunk_prep(chain, n_chunks, c) + PREP_L + lane] = x;
+    }
+    __syncthreads();
+    // 20 products (10 blocks on and below the diagonal, Gram G[t,s] = k_t . conj(k_s) and
+    // query-key P[t,s] = q~_t . conj(k_s)), five per wave: items w, w + 4, ..., w + 16
+    // (item i: kind i & 1, block i >> 1)
+    Gauss acc[5];
+#pragma unroll
+    for (int it = 0; it < 5; ++it) {
+        const int item = w + 4 * it, kind = item & 1, bk = item >> 1;
+        const int bb = (bk >= 1) + (bk >= 3) + (bk >= 6), cc = bk - bb * (bb + 1) / 2;
+        const float *Ar = kind ? sQr : sKr, *Ai = kind ? sQi : sKi;
+        const int ra = (16 * bb + l16) * KP, rb = (16 * cc + l16) * KP;
+        gz(acc[it]);
+#pragma unroll 4
+        for (int ks = 0; ks < 16; ++ks) {
+            const int j = 4 * ks + g;
+            gstep(acc[it], Ar[ra + j], Ai[ra + j], sKr[rb + j], -sKi[rb + j]);  // times conj(k_s)
+        }
+    }
+    __syncthreads();  // K and Q no longer read: their bytes become M, T and scratch
+#pragma unroll
+    for (int it = 0; it < 5; ++it) {
+        const int item = w + 4 * it, kind = item & 1, bk = item >> 1;
+        const int bb = (bk >= 1) + (bk >= 3) + (bk >= 6), cc = bk - bb * (bb + 1) / 2;
+        const floatx4 xr = gre(acc[it]), xi = gim(acc[it]);
+        if (kind == 0) {
+            float *Mb = sM + bk * BLK;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * bb + 4 * g + r, s = 16 * cc + l16;
+                const float m = s < t ? sB[t] * __expf(sL[t] - sL[s]) : 0.f;
+                Mb[(4 * g + r) * 16 + l16] = m * xr[r];
+                Mb[256 + (4 * g + r) * 16 + l16] = m * xi[r];
+            }
+        } else {
+            // Ahat in A-operand order: element (row 4g + r, col l16) -> lane (col % 4) * 16 + row, slot col / 4
+            float *dst = prep + chunk_prep(chain, n_chunks, c) + PREP_A + bk * BLK;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * bb + 4 * g + r, s = 16 * cc + l16;
+                const float dts = s <= t ? __expf(sL[t] - sL[s]) : 0.f;
+                const int ln = (l16 & 3) * 16 + 4 * g + r, ks = l16 >> 2;
+                dst[ln * 4 + ks] = dts * xr[r];
+                dst[256 + ln * 4 + ks] = dts * xi[r];
             }
         }
-        if (more) regs.commit(sp[buf ^ 1], tid);
+    }
+    __syncthreads();
+    {  // T_bb = (I + N)^{-1} = (I - N)(I + N^2)(I + N^4)(I + N^8), N = M_bb nilpotent (N^16 = 0); wave b
+        const float *N = sM + blk(w, w) * BLK;
+        float *X = sX + w * 4 * BLK;  // N^2, N^4, N^8, P1 (then P2 over N^2)
+        Gauss x;
+        gz(x);
+        blk_mul_g(x, N, N, l16, g);
+        blk_store(X, gre(x), gim(x), l16, g);
+        gz(x);
+        blk_mul_g(x, X, X, l16, g);
+        blk_store(X + BLK, gre(x), gim(x), l16, g);
+        gz(x);
+        blk_mul_g(x, X + BLK, X + BLK, l16, g);
+        blk_store(X + 2 * BLK, gre(x), gim(x), l16, g);
+        // P1 = I - N + N^2 - N N^2
+        gz(x);
+        blk_mul_g(x, N, X, l16, g);
+        {
+            floatx4 pr = -gre(x), pi = -gim(x);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[r] += (4 * g + r == l16 ? 1.f : 0.f) - blk_re(N, g, r, l16) + blk_re(X, g, r, l16);
+                pi[r] += -blk_im(N, g, r, l16) + blk_im(X, g, r, l16);
+            }
+            blk_store(X + 3 * BLK, pr, pi, l16, g);
+        }
+        // P2 = P1 + P1 N^4 (over N^2)
+        gz(x);
+        blk_mul_g(x, X + 3 * BLK, X + BLK, l16, g);
+        {
+            floatx4 pr = gre(x), pi = gim(x);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[r] += blk_re(X + 3 * BLK, g, r, l16);
+                pi[r] += blk_im(X + 3 * BLK, g, r, l16);
+            }
+            blk_store(X, pr, pi, l16, g);
+        }
+        // T = P2 + P2 N^8
+        gz(x);
+        blk_mul_g(x, X, X + 2 * BLK, l16, g);
+        {
+            floatx4 pr = gre(x), pi = gim(x);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[r] += blk_re(X, g, r, l16);
+                pi[r] += blk_im(X, g, r, l16);
+            }
+            blk_store(sT + blk(w, w) * BLK, pr, pi, l16, g);
+        }
+    }
+    __syncthreads();
+    // blocks below the diagonal by distance: T_bc = -T_bb sum_{k=c}^{b-1} M_bk T_kc
+    for (int dist = 1; dist < 4; ++dist) {
+        const bool mine = w + dist < 4;
+        const int bb = w + dist, cc = w;
+        if (mine) {
+            Gauss x;
+            gz(x);
+            for (int k = cc; k < bb; ++k) blk_mul_g(x, sM + blk(bb, k) * BLK, sT + blk(k, cc) * BLK, l16, g);
+            blk_store(sR + w * BLK, gre(x), gim(x), l16, g);
+        }
+        __syncthreads();
+        if (mine) {
+            Gauss x;
+            gz(x);
+            blk_mul_g(x, sT + blk(bb, bb) * BLK, sR + w * BLK, l16, g);
+            blk_store(sT + blk(bb, cc) * BLK, -gre(x), -gim(x), l16, g);
+        }
         __syncthreads();
     }
-    write_state(a.s_re, a.s_im, s, chain, L);
+    for (int k = 0; k < NBLK; ++k)
+        blk_export(prep + chunk_prep(chain, n_chunks, c) + PREP_T + k * BLK, sT + k * BLK, tid, 256);
+}
+
+// a [64][64] fp32 complex tile of the chunk (rows past the end zero) in registers:
+// thread tid owns row tid / 4, columns 16 (tid % 4) .. + 15
+struct TileRegs {
+    floatx4 re[4], im[4];
+};
+__device__ __forceinline__ void tile_fetch(TileRegs &x, const qpam_cview &v, int b, int h, int t0, int valid, int tid,
+                                           float scale) {
+    const int r = tid >> 2, c0 = 16 * (tid & 3);
+    const float *re = static_cast<const float *>(v.re) + b * v.s0 + h * v.s1 + (int64_t)(t0 + min(r, valid - 1)) * v.s2 + c0;
+    const float *im = static_cast<const float *>(v.im) + b * v.s0 + h * v.s1 + (int64_t)(t0 + min(r, valid - 1)) * v.s2 + c0;
+    const float f = r < valid ? scale : 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        x.re[e] = *reinterpret_cast<const floatx4 *>(re + 4 * e) * f;
+        x.im[e] = *reinterpret_cast<const floatx4 *>(im + 4 * e) * f;
+    }
+}
+__device__ __forceinline__ void tile_put(float *sr, float *si, const TileRegs &x, int tid) {
+    const int r = tid >> 2, c0 = 16 * (tid & 3);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        *reinterpret_cast<floatx4 *>(sr + r * KP + c0 + 4 * e) = x.re[e];
+        *reinterpret_cast<floatx4 *>(si + r * KP + c0 + 4 * e) = x.im[e];
+    }
+}
+// the A-operand blocks (w, 0..w) of one prepared matrix: 4 k-elements per lane and plane
+struct OpRegs {
+    floatx4 re[4], im[4];
+};
+__device__ __forceinline__ void ops_fetch(OpRegs &x, const float *base, int w, int lane) {
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        if (cc <= w) {
+            const float *p = base + blk(w, cc) * BLK;
+            x.re[cc] = *reinterpret_cast<const floatx4 *>(p + lane * 4);
+            x.im[cc] = *reinterpret_cast<const floatx4 *>(p + 256 + lane * 4);
+        }
+    }
+}
+
+// the chain's checkpoint layout (the backward's): float (slot * 8 + plane * 4 + j % 4) of
+// group state, slot = (i / 4) * 64 + (i % 4) * 16 + j / 4
+__device__ __forceinline__ void ckpt_store(float *dst, int i, int j4, const floatx4 &re, const floatx4 &im) {
+    const int slot = (i >> 2) * 64 + (i & 3) * 16 + j4;
+    *reinterpret_cast<floatx4 *>(dst + slot * 8) = re;
+    *reinterpret_cast<floatx4 *>(dst + slot * 8 + 4) = im;
+}
+
+__global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, const float *prep, int n_chunks) {
+    __shared__ __align__(16) float sKQr[CH * KP], sKQi[CH * KP];   // K, then q_scale Q, of the chunk
+    __shared__ __align__(16) float sUr[CH * SP], sUi[CH * SP];     // W, then U  [t][i]
+    __shared__ __align__(16) float sSr[2][CH * SP], sSi[2][CH * SP];  // S^T [j][i], entering / next
+    __shared__ float sL[CH], sBt[CH];
+    const int n_chains = a.B * a.H;
+    const int chain = blockIdx.x % n_chains, rblk = blockIdx.x / n_chains;  // a chain's blocks share an XCD
+    const int b = chain / a.H, h = chain % a.H;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int i0 = 16 * rblk;  // the block's value rows
+    const int n_groups = (a.T + 15) / 16;
+    float *ckpt = a.workspace ? static_cast<float *>(a.workspace) + (int64_t)chain * n_groups * (2 * D * D) : nullptr;
+
+    for (int idx = tid; idx < CH * 16; idx += 256) {  // S0^T
+        const int i = idx & 15, j = idx >> 4;
+        const int64_t o = (int64_t)chain * D * D + (i0 + i) * D + j;
+        sSr[0][j * SP + i] = a.s0_re ? a.s0_re[o] : 0.f;
+        sSi[0][j * SP + i] = a.s0_re ? a.s0_im[o] : 0.f;
+    }
+    TileRegs xr;
+    tile_fetch(xr, a.k, b, h, 0, min(CH, a.T), tid, 1.f);
+    float lnext = prep[chunk_prep(chain, n_chunks, 0) + PREP_L + lane];
+    float bnext = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)min(lane, a.T - 1) * a.sg_t];
+    int cur = 0;
+    __syncthreads();
+    if (ckpt) {  // group 0: the entering state
+        floatx4 er, ei;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            er[r] = sSr[0][(16 * w + 4 * g + r) * SP + l16];
+            ei[r] = sSi[0][(16 * w + 4 * g + r) * SP + l16];
+        }
+        ckpt_store(ckpt, i0 + l16, 4 * w + g, er, ei);
+    }
+    for (int c = 0; c < n_chunks; ++c) {
+        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        const int64_t pc = chunk_prep(chain, n_chunks, c);
+        tile_put(sKQr, sKQi, xr, tid);
+        if (w == 0) {
+            sL[lane] = lnext;
+            sBt[lane] = lane < valid ? bnext : 0.f;
+        }
+        __syncthreads();
+        tile_fetch(xr, a.q, b, h, t0, valid, tid, a.q_scale);  // in flight through the state work
+        OpRegs ops;
+        ops_fetch(ops, prep + pc + PREP_T, w, lane);
+        float vr4[4], vi4[4];  // V of this lane's W elements
+        {
+            const float *vre = static_cast<const float *>(a.v.re) + b * a.v.s0 + h * a.v.s1 + i0 + l16;
+            const float *vim = static_cast<const float *>(a.v.im) + b * a.v.s0 + h * a.v.s1 + i0 + l16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t o = (int64_t)(t0 + min(16 * w + 4 * g + r, valid - 1)) * a.v.s2;
+                vr4[r] = vre[o];
+                vi4[r] = vim[o];
+            }
+        }
+        const int t = 16 * w + l16;  // this lane's row in A-operand reads
+        // W[t][i] = beta_t (v_t[i] - alpha_t (K S^T)[t][i]), row tile w
+        floatx4 ar, ai;
+        {
+            Gauss x;
+            gz(x);
+#pragma unroll 4
+            for (int ks = 0; ks < 16; ++ks) {
+                const int j = 4 * ks + g;
+                gstep(x, sKQr[t * KP + j], sKQi[t * KP + j], sSr[cur][j * SP + l16], sSi[cur][j * SP + l16]);
+            }
+            ar = gre(x);
+            ai = gim(x);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int tr = 16 * w + 4 * g + r;
+            const float al = __expf(sL[tr]), bt = sBt[tr];
+            sUr[tr * SP + l16] = bt * (vr4[r] - al * ar[r]);
+            sUi[tr * SP + l16] = bt * (vi4[r] - al * ai[r]);
+        }
+        __syncthreads();
+        // U = T W, row tile w: sum over column tiles cc <= w
+        floatx4 ur, ui;
+        {
+            Gauss x;
+            gz(x);
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                if (cc > w) continue;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int s = 16 * cc + 4 * ks + g;
+                    gstep(x, ops.re[cc][ks], ops.im[cc][ks], sUr[s * SP + l16], sUi[s * SP + l16]);
+                }
+            }
+            ur = gre(x);
+            ui = gim(x);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sUr[(16 * w + 4 * g + r) * SP + l16] = ur[r];
+            sUi[(16 * w + 4 * g + r) * SP + l16] = ui[r];
+        }
+        __syncthreads();
+        const int wy = 3 - w;  // Y row tile: the wave with the most T blocks gets the fewest Ahat blocks
+        ops_fetch(ops, prep + pc + PREP_A, wy, lane);  // Ahat, in flight through the state update
+        // state update, row tile w of S^T (j = 16 w + 4 g + r, i = l16), in four 16-step quarters
+        {
+            floatx4 sr, si;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sr[r] = sSr[cur][(16 * w + 4 * g + r) * SP + l16];
+                si[r] = sSi[cur][(16 * w + 4 * g + r) * SP + l16];
+            }
+            float Lprev = 0.f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float Lq = sL[16 * q + 15];
+                const float f = __expf(Lq - Lprev);
+                sr *= f;
+                si *= f;
+                Gauss x;
+                gz(x);
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int s = 16 * q + 4 * ks + g;
+                    const float wq = __expf(Lq - sL[s]);
+                    // conj(K)^T [j][s] (A) times (D U)[s][i] (B)
+                    gstep(x, sKQr[s * KP + 16 * w + l16], -sKQi[s * KP + 16 * w + l16], sUr[s * SP + l16] * wq,
+                          sUi[s * SP + l16] * wq);
+                }
+                sr += gre(x);
+                si += gim(x);
+                Lprev = Lq;
+                const int grp = 4 * c + q + 1;  // the state before step 16 grp
+                if (ckpt && 16 * grp < a.T) ckpt_store(ckpt + (int64_t)grp * (2 * D * D), i0 + l16, 4 * w + g, sr, si);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                sSr[cur ^ 1][(16 * w + 4 * g + r) * SP + l16] = sr[r];
+                sSi[cur ^ 1][(16 * w + 4 * g + r) * SP + l16] = si[r];
+            }
+        }
+        __syncthreads();  // K no longer read
+        tile_put(sKQr, sKQi, xr, tid);
+        if (c + 1 < n_chunks) {
+            const int v1 = min(CH, a.T - t0 - CH);
+            tile_fetch(xr, a.k, b, h, t0 + CH, v1, tid, 1.f);
+            lnext = prep[chunk_prep(chain, n_chunks, c + 1) + PREP_L + lane];
+            bnext = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)(t0 + CH + min(lane, v1 - 1)) * a.sg_t];
+        }
+        __syncthreads();
+        // Y = Ahat U + alpha Q~ S^T (entering state), row tile w
+        {
+            Gauss x;
+            gz(x);
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                if (cc > wy) continue;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int s = 16 * cc + 4 * ks + g;
+                    gstep(x, ops.re[cc][ks], ops.im[cc][ks], sUr[s * SP + l16], sUi[s * SP + l16]);
+                }
+            }
+            const int ty = 16 * wy + l16;
+            const float al = __expf(sL[ty]);
+#pragma unroll 4
+            for (int ks = 0; ks < 16; ++ks) {
+                const int j = 4 * ks + g;
+                gstep(x, al * sKQr[ty * KP + j], al * sKQi[ty * KP + j], sSr[cur][j * SP + l16], sSi[cur][j * SP + l16]);
+            }
+            const floatx4 yr = gre(x), yi = gim(x);
+            float *yre = a.y.re + b * a.y.s0 + h * a.y.s1 + i0 + l16;
+            float *yim = a.y.im + b * a.y.s0 + h * a.y.s1 + i0 + l16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tr = 16 * wy + 4 * g + r;
+                if (tr < valid) {
+                    yre[(int64_t)(t0 + tr) * a.y.s2] = yr[r];
+                    yim[(int64_t)(t0 + tr) * a.y.s2] = yi[r];
+                }
+            }
+        }
+        __syncthreads();  // before the next chunk's tiles replace Q and U
+        cur ^= 1;
+    }
+    for (int idx = tid; idx < CH * 16; idx += 256) {  // final state from S^T
+        const int j = idx & 63, i = idx >> 6;
+        const int64_t o = (int64_t)chain * D * D + (i0 + i) * D + j;
+        a.s_re[o] = sSr[cur][j * SP + i];
+        a.s_im[o] = sSi[cur][j * SP + i];
+    }
 }
 
 // sum over the 4 row groups of a wave (lanes cg, cg+16, cg+32, cg+48)
@@ -505,6 +972,9 @@ bool mview_ok(const qpam_mview &v) {
 size_t fwd_ws(const qpam_delta_args &a) {
     return (size_t)a.B * a.H * ((a.T + GROUP - 1) / GROUP) * STATE_FLOATS * sizeof(float);
 }
+size_t prep_bytes(const qpam_delta_args &a) {
+    return (size_t)a.B * a.H * ((a.T + CH - 1) / CH) * PREP_FLOATS * sizeof(float);
+}
 size_t bwd_ws(const qpam_delta_args &a) {
     const size_t nbht = (size_t)a.B * a.H * a.T;
     return bwd_sub_bytes(a) + PARTS * nbht * (D * sizeof(floatx4) + sizeof(floatx2));
@@ -530,6 +1000,8 @@ using namespace qpam;
 
 extern "C" size_t qpam_delta_workspace_size(const qpam_delta_args *a) { return a ? fwd_ws(*a) : 0; }
 
+extern "C" size_t qpam_delta_scratch_size(const qpam_delta_args *a) { return a ? prep_bytes(*a) : 0; }
+
 extern "C" int qpam_delta_fwd(const qpam_delta_args *a, void *stream) {
     int st = validate(a);
     if (st) return st;
@@ -539,8 +1011,21 @@ extern "C" int qpam_delta_fwd(const qpam_delta_args *a, void *stream) {
                  "qpam_delta_fwd: workspace of %zu bytes needed (or NULL without a backward)", fwd_ws(*a));
     if (a->B == 0) return QPAM_OK;
     QPAM_REQUIRE(a->T >= 1, "qpam_delta_fwd: T must be >= 1");
-    hipLaunchKernelGGL(delta_fwd_kernel, dim3(a->B * a->H * NW), dim3(64), 0, static_cast<hipStream_t>(stream), *a);
-    return launch_status("delta_fwd_kernel");
+    QPAM_REQUIRE(a->scratch && aligned(a->scratch, 16) && a->scratch_bytes >= prep_bytes(*a),
+                 "qpam_delta_fwd: scratch of %zu bytes needed", prep_bytes(*a));
+    const int n_chunks = (a->T + CH - 1) / CH;
+    const int64_t items = (int64_t)a->B * a->H * n_chunks;
+    QPAM_REQUIRE(items < (1ll << 31) && (int64_t)a->B * a->H * ROW_BLOCKS < (1ll << 31), "qpam_delta_fwd: grid too large");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)delta_prep_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)PREP_SMEM));
+    float *prep = static_cast<float *>(a->scratch);
+    hipLaunchKernelGGL(delta_prep_kernel, dim3((unsigned)items), dim3(256), PREP_SMEM, s, *a, prep, n_chunks);
+    st = launch_status("delta_prep_kernel");
+    if (st) return st;
+    hipLaunchKernelGGL(delta_chunk_kernel, dim3((unsigned)(a->B * a->H * ROW_BLOCKS)), dim3(256), 0, s, *a,
+                       (const float *)prep, n_chunks);
+    return launch_status("delta_chunk_kernel");
 }
 
 extern "C" size_t qpam_delta_bwd_workspace_size(const qpam_delta_bwd_args *g) {

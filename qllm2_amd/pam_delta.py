@@ -86,8 +86,13 @@ def delta_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: T
     else:
         ws = torch.empty(0, device=dev, dtype=torch.float32)
     if T > 0 and B > 0:
+        # the forward's per-chunk products (freed when the call returns; the
+        # caching allocator keeps the block for the next call)
+        scratch = torch.empty((L.qpam_delta_scratch_size(a) + 3) // 4, device=dev, dtype=torch.float32)
+        a.scratch, a.scratch_bytes = scratch.data_ptr(), scratch.numel() * 4
         with torch.cuda.device(dev):
             _lib.check(L.qpam_delta_fwd(a, _lib.stream_ptr(dev)), "qpam_delta_fwd")
+        del scratch
     else:
         y_re.zero_(), y_im.zero_()
         if s0_re is not None:

@@ -8,18 +8,16 @@
 // exactly this recurrence unrolled over the chunk; _recur_step_delta,
 // v11/model.py:967-1002, is the same step with g~ = gamma).
 //
-// Design: the rows of S are independent under the recurrence (row i reads
-// only k, q, v_i, gamma, beta).  A (b, h) chain's 64 x 64 complex state is
-// split over 16 waves of 4 rows; a lane owns 1 row x 4 columns in registers,
-// and the per-row dot products S k and S q~ are DPP reductions over the 16
-// lanes of a row group.  The forward needs no other communication, so each
-// wave is its own workgroup (B*H*16 of them, spread over every CU).  A token
-// costs ~100 VALU/DPP operations per wave and no solve; the chunked form's
-// O(C^2 d + C^3) per-chunk work (the Gram matrix, the 2C x 2C real solve, the
-// dual-form products) is not needed on a GPU whose state fits in registers.
-// The forward stores the state before every 16th token (the backward's
-// checkpoints).
+// Forward: the chunked form on fp32 MFMA (delta_prep_kernel, chunk-parallel,
+// then delta_chunk_kernel along the chunks; described at the kernels), with
+// the state before every 16th token stored as the backward's checkpoints.
+// The rows of S are independent under the recurrence (row i reads only k, q,
+// v_i, gamma, beta), so the chunk pass splits a chain's 64 value rows over four
+// blocks.
 //
+// Backward (token recurrence in registers): a lane owns 1 row x 4 columns of
+// S, and the per-row dot products S k and S q~ are DPP reductions over the 16
+// lanes of a row group.
 // Backward: four workgroups of 4 waves (16 rows each) per chain walk its
 // 16-token groups in reverse; each group is recomputed from its checkpoint
 // with the state before every 4th token kept in a scratch, then each 4-token

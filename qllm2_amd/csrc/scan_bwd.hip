@@ -1031,18 +1031,98 @@ grad_pass_bf16_kernel(BwdParams p) {
     }
 }
 
+// Decay inputs of state m of a chunk for one wave (lane = step): gamma and the
+// rotation, loaded at kernel entry so that their latency overlaps the tile loads.
+struct DecayIn {
+    float gam, rr, ri;
+};
+__device__ __forceinline__ DecayIn decay_load(const qpam_scan_args &a, int m, int b, int h, int c0, int valid) {
+    const int lane = threadIdx.x & 63;
+    DecayIn d{1.f, 1.f, 0.f};
+    if (lane < valid) {
+        d.gam = a.gamma[m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)(c0 + lane) * a.sg_t];
+        if (a.rot_re) {
+            const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + lane) * a.sr_t;
+            d.rr = a.rot_re[ro];
+            d.ri = a.rot_im[ro];
+        }
+    }
+    return d;
+}
+// The chunk tables of state m (one wave): L = the log-decay prefix sums (as
+// chunk_log_prefix_ok forms them), the rotations, F = exp(-L) and P = r exp(L);
+// returns the factorisation test of the state.
+__device__ __forceinline__ bool decay_tables(const DecayIn &d, int m, int valid, float *sL, float *sRr, float *sRi,
+                                             float *sF, float *sPr, float *sPi) {
+    const int lane = threadIdx.x & 63;
+    float x = (lane < valid) ? logf(d.gam + LOG_EPS) : 0.f;
+    const bool pos = x > 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+    }
+    const bool ok = !__any(pos) && __shfl(x, 63) >= -FACTOR_RANGE;
+    sL[m * 64 + lane] = x;
+    sRr[m * 64 + lane] = d.rr;
+    sRi[m * 64 + lane] = d.ri;
+    sF[m * 64 + lane] = __expf(-x);  // unused (possibly inf) when the test fails
+    const float e = __expf(x);
+    sPr[m * 64 + lane] = d.rr * e;
+    sPi[m * 64 + lane] = d.ri * e;
+    return ok;
+}
+
+// Own-row operands of the chunk kernels: lane (g, l16) of a wave that owns 16
+// rows of the chunk reads row l16 of them straight from global memory, either
+// columns 32 kp + 8 g .. +7 (an MFMA operand fragment) or the four columns
+// 16 jt + 4 g .. +3 that the transposed accumulators of the wave hold; rows at
+// or past `valid` read as zero.
+__device__ __forceinline__ bf16x8 own_frag(const U16 *row, int kp, bool ok) {
+    const int g = (threadIdx.x & 63) >> 4;
+    return ok ? *reinterpret_cast<const bf16x8 *>(row + 32 * kp + 8 * g) : __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+}
+__device__ __forceinline__ bf16x8 own_frag_f32(const float *row, int kp, bool ok) {
+    const int g = (threadIdx.x & 63) >> 4;
+    if (!ok) return __builtin_bit_cast(bf16x8, make_uint4(0, 0, 0, 0));
+    const floatx4 x0 = *reinterpret_cast<const floatx4 *>(row + 32 * kp + 8 * g);
+    const floatx4 x1 = *reinterpret_cast<const floatx4 *>(row + 32 * kp + 8 * g + 4);
+    return to_bf(floatx8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]});
+}
+__device__ __forceinline__ uint2 own_quad(const U16 *row, int jt, bool ok) {
+    const int g = (threadIdx.x & 63) >> 4;
+    return ok ? *reinterpret_cast<const uint2 *>(row + 16 * jt + 4 * g) : make_uint2(0u, 0u);
+}
+// element r of four bf16 held in two dwords
+__device__ __forceinline__ float quad_elem(uint2 u, int r) {
+    const unsigned x = (r < 2) ? u.x : u.y;
+    return __uint_as_float((r & 1) ? (x & 0xffff0000u) : (x << 16));
+}
+// scale * v -> bf16, columns 16 jt + 4 g .. +3 of `row` (one 8-byte store)
+__device__ __forceinline__ void store_quad(U16 *row, int jt, const floatx4 &v, float scale) {
+    const int g = (threadIdx.x & 63) >> 4;
+    *reinterpret_cast<uint2 *>(row + 16 * jt + 4 * g) =
+        make_uint2(pack_bf16x2(v[0] * scale, v[1] * scale), pack_bf16x2(v[2] * scale, v[3] * scale));
+}
+
+// Query side, bf16 operands and chunk 64.  Wave = 16 query rows t, whose q and
+// dY rows stay in registers; K and V (later the carried states) are staged in
+// LDS.  The score tiles are transposed (lane: row t = l16, key s = 4g + r), so
+// per-row quantities are per-lane scalars, and dQ~ accumulates transposed
+// (lane: row t, columns 16 jt + 4 g + r) and leaves as 8-byte runs.  With the
+// factorised decay D_m[t,s] = E_m[t] F_m[s] the decay factor
+// D~[t,s] = sum_m P_m[t] F_m[s] (P_m = r_m E_m) and the row sums
+// Z_m[t] = sum_{s<t} gD~[t,s] F_m[s] are fp32 MFMA products (k = m, resp. k = s).
 template <int M, bool DYBF>
-__global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
+__global__ void __launch_bounds__(THREADS, 2) query_side_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
-    U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;
-    U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
-    U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;    // V tile, later S_m
-    U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;
-    // per-step vectors [M][64]
-    float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + M * 64, *sRi = sRr + M * 64;
-    float *sGL = sRi + M * 64, *sDRr = sGL + M * 64, *sDRi = sDRr + M * 64;
-    float *sF = sDRi + M * 64;
-    int *sFast = reinterpret_cast<int *>(sF + M * 64);
+    U16 *sKr = reinterpret_cast<U16 *>(smem), *sKi = sKr + PLANE_B;
+    U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;  // V tile, later S_m
+    // per-step vectors [M][64]; sGq, sDq*: this chunk's row results (each wave its own rows)
+    float *sL = reinterpret_cast<float *>(sVi + PLANE_B), *sRr = sL + M * 64, *sRi = sRr + M * 64;
+    float *sF = sRi + M * 64, *sPr = sF + M * 64, *sPi = sPr + M * 64;
+    float *sGq = sPi + M * 64, *sDqr = sGq + M * 64, *sDqi = sDqr + M * 64;
+    int *sFast = reinterpret_cast<int *>(sDqi + M * 64);  // [M] factorisation tests
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -1050,171 +1130,196 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const bool carry = (c > 0) || (a.s0_re != nullptr);
     const float qs = a.q_scale;
+    // global loads first: decay inputs of state m = w, the wave's own q and dY
+    // rows, the K and V tiles and the carried state S_0
+    DecayIn din;
+    if (w < M) din = decay_load(a, w, b, h, c0, valid);
+    const int tt = causal_tile(w);
+    const int t = 16 * tt + l16;
+    const bool tv = t < valid;
+    const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)(c0 + min(t, valid - 1)) * a.q.s2;
+    const U16 *qrr = (const U16 *)a.q.re + qo, *qri = (const U16 *)a.q.im + qo;
+    bf16x8 bq[2][2], bg[2][2];  // [kp][re, im] of q and dY, rows t
     {
-        const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
-        const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
-        const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-        U16 *const bd[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
-        const U16 *const bs[6] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
-                                  (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
-        const int64_t bst[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        if constexpr (DYBF) {
-            U16 *const bd8[8] = {bd[0], bd[1], bd[2], bd[3], bd[4], bd[5], sGr, sGi};
-            const U16 *const bs8[8] = {bs[0], bs[1], bs[2], bs[3], bs[4], bs[5], (const U16 *)p.dy.re + go,
-                                       (const U16 *)p.dy.im + go};
-            const int64_t bst8[8] = {bst[0], bst[1], bst[2], bst[3], bst[4], bst[5], p.dy.s2, p.dy.s2};
-            stage_bf<8, 0x0u>(bd8, bs8, bst8, valid);
-        } else {
-            U16 *const fd[2] = {sGr, sGi};
-            const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
-            const int64_t fst[2] = {p.dy.s2, p.dy.s2};
-            stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
+        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)(c0 + min(t, valid - 1)) * p.dy.s2;
+#pragma unroll
+        for (int kp = 0; kp < 2; ++kp) {
+            bq[kp][0] = own_frag(qrr, kp, tv);
+            bq[kp][1] = own_frag(qri, kp, tv);
+            if constexpr (DYBF) {
+                bg[kp][0] = own_frag((const U16 *)p.dy.re + go, kp, tv);
+                bg[kp][1] = own_frag((const U16 *)p.dy.im + go, kp, tv);
+            } else {
+                bg[kp][0] = own_frag_f32((const float *)p.dy.re + go, kp, tv);
+                bg[kp][1] = own_frag_f32((const float *)p.dy.im + go, kp, tv);
+            }
         }
     }
-    if (w == 0) chunk_decay_prologue_f<M>(a, b, h, c0, valid, sL, sRr, sRi, sF, nullptr, nullptr, sFast);
-    for (int e = tid; e < 3 * M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
+    B16Regs stg[4];
+    {
+        const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+        const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+        regs_load_bf<false>(stg[0], (const U16 *)a.k.re + ko, a.k.s2, valid);
+        regs_load_bf<false>(stg[1], (const U16 *)a.k.im + ko, a.k.s2, valid);
+        regs_load_bf<false>(stg[2], (const U16 *)a.v.re + vo, a.v.s2, valid);
+        regs_load_bf<false>(stg[3], (const U16 *)a.v.im + vo, a.v.s2, valid);
+    }
     B16Regs sn[2];  // carried state S_0, in flight during the intra-chunk phase
     if (carry) {
         const U16 *s0p = fsnap(p, 0, b, h, c);
         regs_load_bf<false>(sn[0], s0p, D, D);
         regs_load_bf<false>(sn[1], s0p + D * D, D, D);
     }
+    if (w < M) {
+        const bool ok = decay_tables(din, w, valid, sL, sRr, sRi, sF, sPr, sPi);
+        if (lane == 0) sFast[w] = ok ? 1 : 0;
+    }
+    regs_store_bf<false>(sKr, stg[0]);
+    regs_store_bf<false>(sKi, stg[1]);
+    regs_store_bf<false>(sVr, stg[2]);
+    regs_store_bf<false>(sVi, stg[3]);
     __syncthreads();
 
-    const int tt = causal_tile(w);
-    const int t = 16 * tt + l16;
+    bool fast = true;
+#pragma unroll
+    for (int m = 0; m < M; ++m) fast = fast && sFast[m] != 0;
     floatx4 gqR[4], gqI[4];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) gqR[jt] = gqI[jt] = zero4();
     {
-        floatx4 wr[4], wi[4], dr[4], di[4];
-#pragma unroll
-        for (int st = 0; st < 4; ++st) wr[st] = wi[st] = dr[st] = di[st] = zero4();
-#pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-            const int k0 = 32 * kp + 8 * g;
-            const bf16x8 bqr = ld8(sQr + t * PB + k0), bqi = ld8(sQi + t * PB + k0);
-            const bf16x8 bgr = ld8(sGr + t * PB + k0), bgi = ld8(sGi + t * PB + k0);
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                if (st > tt) continue;
-                const int s = 16 * st + l16;
-                const bf16x8 akr = ld8(sKr + s * PB + k0), aki = ld8(sKi + s * PB + k0);
-                const bf16x8 avr = ld8(sVr + s * PB + k0), avi = ld8(sVi + s * PB + k0);
-                wr[st] = mfma_bf(akr, bqr, wr[st]);
-                wr[st] = mfma_bf(aki, bqi, wr[st]);
-                wi[st] = mfma_bf(akr, bqi, wi[st]);
-                wi[st] = mfma_bf(neg_bf(aki), bqr, wi[st]);
-                dr[st] = mfma_bf(avr, bgr, dr[st]);
-                dr[st] = mfma_bf(avi, bgi, dr[st]);
-                di[st] = mfma_bf(avr, bgi, di[st]);
-                di[st] = mfma_bf(neg_bf(avi), bgr, di[st]);
-            }
-        }
+        // fast path: Z_m[t] in element m of lanes g == 0 (fp32 MFMA, rows m); gD~[t][t]
+        floatx4 zR = zero4(), zI = zero4();
+        float dgr = 0.f, dgi = 0.f;
+        // general path: per-lane partial row sums
         float rowp[MAX_M], grr[MAX_M], gri[MAX_M];
 #pragma unroll
         for (int m = 0; m < MAX_M; ++m) rowp[m] = grr[m] = gri[m] = 0.f;
-        if (*sFast) {
-            // D_m[t,s] = E_m[t] F_m[s]: gW = dA conj(sum_m rho_m[t] F_m[s]); the row sums
-            // sum_s gD~ D_m over s < t are E_m[t] sum_s gD~ F_m[s]; D_m[t,t] = 1.
-            float Et[MAX_M], pr_t[MAX_M], pi_t[MAX_M], zr[MAX_M], zi[MAX_M];
+        // B operand of the decay-factor product: lane (g = m, l16) holds P_m[t]
+        const float pbr = (g < M) ? sPr[g * 64 + t] : 0.f, pbi = (g < M) ? sPi[g * 64 + t] : 0.f;
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                Et[m] = __expf(sL[m * 64 + t]);
-                pr_t[m] = sRr[m * 64 + t] * Et[m];
-                pi_t[m] = sRi[m * 64 + t] * Et[m];
-                zr[m] = zi[m] = 0.f;
-            }
-            float dgr = 0.f, dgi = 0.f;
+        for (int kp = 0; kp < 2; ++kp) {
+            if (2 * kp > tt) continue;
+            floatx4 gwr[2], gwi[2];  // gW^T tiles st = 2 kp, 2 kp + 1
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int st = 2 * kp + h2;
+                gwr[h2] = gwi[h2] = zero4();
                 if (st > tt) continue;
-                float4 F4[MAX_M];
+                const int s = 16 * st + l16;
+                // W^T[s][t] = sum_j conj(k[s,j]) q[t,j],  dA^T[s][t] = sum_i conj(v[s,i]) dY[t,i]
+                floatx4 wr = zero4(), wi = zero4(), dr = zero4(), di = zero4();
 #pragma unroll
-                for (int m = 0; m < M; ++m) F4[m] = *reinterpret_cast<const float4 *>(sF + m * 64 + 16 * st + 4 * g);
+                for (int kq = 0; kq < 2; ++kq) {
+                    const int k0 = 32 * kq + 8 * g;
+                    const bf16x8 akr = ld8(sKr + s * PB + k0), aki = ld8(sKi + s * PB + k0);
+                    const bf16x8 avr = ld8(sVr + s * PB + k0), avi = ld8(sVi + s * PB + k0);
+                    wr = mfma_bf(akr, bq[kq][0], wr);
+                    wr = mfma_bf(aki, bq[kq][1], wr);
+                    wi = mfma_bf(akr, bq[kq][1], wi);
+                    wi = mfma_bf(neg_bf(aki), bq[kq][0], wi);
+                    dr = mfma_bf(avr, bg[kq][0], dr);
+                    dr = mfma_bf(avi, bg[kq][1], dr);
+                    di = mfma_bf(avr, bg[kq][1], di);
+                    di = mfma_bf(neg_bf(avi), bg[kq][0], di);
+                }
+                if (fast) {
+                    // D~^T[s][t] = sum_m F_m[s] P_m[t]: A lane (g = m, l16) holds F_m[16 st + l16]
+                    const float fa = (g < M) ? sF[g * 64 + s] : 0.f;
+                    const floatx4 Dr = mfma4(fa, pbr, zero4()), Di = mfma4(fa, pbi, zero4());
+                    floatx4 gdr, gdi;  // gD~ = dA conj(W), q_scale applied to the row sums
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int s = 16 * st + 4 * g + r;
-                    const float Ar = dr[st][r], Ai = di[st][r];
-                    const float Wr = wr[st][r] * qs, Wi = wi[st][r] * qs;
-                    const float gdr = Ar * Wr + Ai * Wi, gdi = Ai * Wr - Ar * Wi;
-                    float dtr = 0.f, dti = 0.f;
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const float f = r == 0 ? F4[m].x : r == 1 ? F4[m].y : r == 2 ? F4[m].z : F4[m].w;
-                        dtr += pr_t[m] * f;
-                        dti += pi_t[m] * f;
+                    for (int r = 0; r < 4; ++r) {
+                        gwr[h2][r] = dr[r] * Dr[r] + di[r] * Di[r];
+                        gwi[h2][r] = di[r] * Dr[r] - dr[r] * Di[r];
+                        gdr[r] = dr[r] * wr[r] + di[r] * wi[r];
+                        gdi[r] = di[r] * wr[r] - dr[r] * wi[r];
                     }
-                    const bool keep = st < tt || s <= t, below = st < tt || s < t;
-                    wr[st][r] = keep ? Ar * dtr + Ai * dti : 0.f;
-                    wi[st][r] = keep ? Ai * dtr - Ar * dti : 0.f;
-                    const float gor = below ? gdr : 0.f, goi = below ? gdi : 0.f;
+                    if (st == tt) {  // diagonal tile: gW on s <= t, row sums over s < t, gD~[t][t] apart
 #pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const float f = r == 0 ? F4[m].x : r == 1 ? F4[m].y : r == 2 ? F4[m].z : F4[m].w;
-                        zr[m] += gor * f;
-                        zi[m] += goi * f;
+                        for (int r = 0; r < 4; ++r) {
+                            const int si = 4 * g + r;
+                            if (si == l16) dgr = gdr[r], dgi = gdi[r];
+                            gwr[h2][r] = (si <= l16) ? gwr[h2][r] : 0.f;
+                            gwi[h2][r] = (si <= l16) ? gwi[h2][r] : 0.f;
+                            gdr[r] = (si < l16) ? gdr[r] : 0.f;
+                            gdi[r] = (si < l16) ? gdi[r] : 0.f;
+                        }
                     }
-                    if (st == tt) {
-                        dgr += s == t ? gdr : 0.f;
-                        dgi += s == t ? gdi : 0.f;
+                    // Z_m[t] += sum_s F_m[s] gD~[t][s]: A lane (g, l16 = m) holds F_m[16 st + 4 g + r]
+                    floatx4 fz = zero4();
+                    if (l16 < M) fz = *reinterpret_cast<const floatx4 *>(sF + l16 * 64 + 16 * st + 4 * g);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        zR = mfma4(fz[r], gdr[r], zR);
+                        zI = mfma4(fz[r], gdi[r], zI);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int sr = 16 * st + 4 * g + r;
+                        if (sr > t) continue;
+                        float Dm[MAX_M], nc[MAX_M];
+                        float dtr = 0.f, dti = 0.f;
+#pragma unroll
+                        for (int m = 0; m < MAX_M; ++m) {
+                            Dm[m] = nc[m] = 0.f;
+                            if (m < M) {
+                                const float x = sL[m * 64 + t] - sL[m * 64 + sr];
+                                Dm[m] = __expf(fminf(x, 0.f));
+                                nc[m] = (x <= 0.f && sr != t) ? 1.f : 0.f;
+                                dtr += sRr[m * 64 + t] * Dm[m];
+                                dti += sRi[m * 64 + t] * Dm[m];
+                            }
+                        }
+                        const float Ar = dr[r], Ai = di[r];
+                        const float Wr = wr[r] * qs, Wi = wi[r] * qs;
+                        gwr[h2][r] = Ar * dtr + Ai * dti;
+                        gwi[h2][r] = Ai * dtr - Ar * dti;
+                        const float gdr = Ar * Wr + Ai * Wi, gdi = Ai * Wr - Ar * Wi;
+#pragma unroll
+                        for (int m = 0; m < MAX_M; ++m) {
+                            if (m < M) {
+                                const float gdm = gdr * sRr[m * 64 + t] + gdi * sRi[m * 64 + t];
+                                rowp[m] += gdm * Dm[m] * nc[m];  // the column part is summed by the key side
+                                grr[m] += gdr * Dm[m];
+                                gri[m] += gdi * Dm[m];
+                            }
+                        }
                     }
                 }
             }
+            // dQ~^T[j][t] += sum_s K[s][j] gW[t][s]  (transposed reads of K x register gW)
+            const bf16x8 ar = frag_from_acc(gwr[0], gwr[1]), ai = frag_from_acc(gwi[0], gwi[1]);
+            const bf16x8 nai = neg_bf(ai);
 #pragma unroll
-            for (int m = 0; m < M; ++m) {
-                const float er = Et[m] * zr[m], ei = Et[m] * zi[m];
-                rowp[m] = sRr[m * 64 + t] * er + sRi[m * 64 + t] * ei;  // the column part is summed by the key side
-                grr[m] = er + dgr;
-                gri[m] = ei + dgi;
+            for (int jt = 0; jt < 4; ++jt) {
+                const int r0 = 32 * kp + 4 * g;
+                const bf16x8 kr = ld_tr(sKr, r0, r0 + 16, 16 * jt), ki = ld_tr(sKi, r0, r0 + 16, 16 * jt);
+                gqR[jt] = mfma_bf(kr, ar, gqR[jt]);
+                gqR[jt] = mfma_bf(ki, nai, gqR[jt]);
+                gqI[jt] = mfma_bf(ki, ar, gqI[jt]);
+                gqI[jt] = mfma_bf(kr, ai, gqI[jt]);
+            }
+        }
+        // row results of the intra-chunk part -> sGq / sDq* (lanes g == 0; each wave its own rows)
+        if (fast) {
+            dgr += __shfl_xor(dgr, 16);  // one lane of the column holds gD~[t][t], the others 0
+            dgr += __shfl_xor(dgr, 32);
+            dgi += __shfl_xor(dgi, 16);
+            dgi += __shfl_xor(dgi, 32);
+            if (g == 0) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) {
+                    const float e = __expf(sL[m * 64 + t]) * qs;
+                    const float er = zR[m] * e, ei = zI[m] * e;
+                    sGq[m * 64 + t] = sRr[m * 64 + t] * er + sRi[m * 64 + t] * ei;
+                    sDqr[m * 64 + t] = er + qs * dgr;
+                    sDqi[m * 64 + t] = ei + qs * dgi;
+                }
             }
         } else {
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            if (st > tt) continue;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int s = 16 * st + 4 * g + r;
-                float gwr = 0.f, gwi = 0.f;
-                if (s <= t) {
-                    float Dm[MAX_M], nc[MAX_M];
-                    float dtr = 0.f, dti = 0.f;
-#pragma unroll
-                    for (int m = 0; m < MAX_M; ++m) {
-                        Dm[m] = nc[m] = 0.f;
-                        if (m < M) {
-                            const float x = sL[m * 64 + t] - sL[m * 64 + s];
-                            Dm[m] = __expf(fminf(x, 0.f));
-                            nc[m] = (x <= 0.f && s != t) ? 1.f : 0.f;
-                            dtr += sRr[m * 64 + t] * Dm[m];
-                            dti += sRi[m * 64 + t] * Dm[m];
-                        }
-                    }
-                    const float Ar = dr[st][r], Ai = di[st][r];
-                    const float Wr = wr[st][r] * qs, Wi = wi[st][r] * qs;
-                    gwr = Ar * dtr + Ai * dti;
-                    gwi = Ai * dtr - Ar * dti;
-                    const float gdr = Ar * Wr + Ai * Wi;
-                    const float gdi = Ai * Wr - Ar * Wi;
-#pragma unroll
-                    for (int m = 0; m < MAX_M; ++m) {
-                        if (m < M) {
-                            const float gdm = gdr * sRr[m * 64 + t] + gdi * sRi[m * 64 + t];
-                            rowp[m] += gdm * Dm[m] * nc[m];  // the column part is summed by the key side
-                            grr[m] += gdr * Dm[m];
-                            gri[m] += gdi * Dm[m];
-                        }
-                    }
-                }
-                wr[st][r] = gwr;
-                wi[st][r] = gwi;
-            }
-        }
-        }
-#pragma unroll
-        for (int m = 0; m < MAX_M; ++m) {
-            if (m < M) {
+            for (int m = 0; m < M; ++m) {
                 float x = rowp[m], yr = grr[m], yi = gri[m];
                 x += __shfl_xor(x, 16);
                 x += __shfl_xor(x, 32);
@@ -1223,32 +1328,22 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
                 yi += __shfl_xor(yi, 16);
                 yi += __shfl_xor(yi, 32);
                 if (g == 0) {
-                    atomicAdd(&sGL[m * 64 + t], x);
-                    atomicAdd(&sDRr[m * 64 + t], yr);
-                    atomicAdd(&sDRi[m * 64 + t], yi);
+                    sGq[m * 64 + t] = x;
+                    sDqr[m * 64 + t] = yr;
+                    sDqi[m * 64 + t] = yi;
                 }
-            }
-        }
-        // intra dQ~[t][j] += sum_s gW[t,s] K[s,j]  (registers x transposed reads of K)
-#pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-            if (2 * kp > tt) continue;
-            const bf16x8 ar = frag_from_acc(wr[2 * kp], wr[2 * kp + 1]);
-            const bf16x8 ai = frag_from_acc(wi[2 * kp], wi[2 * kp + 1]);
-            const bf16x8 nai = neg_bf(ai);
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) {
-                const int r0 = 32 * kp + 4 * g;
-                const bf16x8 kr = ld_tr(sKr, r0, r0 + 16, 16 * jt), ki = ld_tr(sKi, r0, r0 + 16, 16 * jt);
-                gqR[jt] = mfma_bf(ar, kr, gqR[jt]);
-                gqR[jt] = mfma_bf(nai, ki, gqR[jt]);
-                gqI[jt] = mfma_bf(ar, ki, gqI[jt]);
-                gqI[jt] = mfma_bf(ai, kr, gqI[jt]);
             }
         }
     }
 
     if (carry) {
+        // q of row t in the transposed accumulator layout, unscaled
+        uint2 qq[4][2];
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            qq[jt][0] = own_quad(qrr, jt, tv);
+            qq[jt][1] = own_quad(qri, jt, tv);
+        }
         for (int m = 0; m < M; ++m) {
             __syncthreads();
             // S_m natural (read transposed below); S_{m+1} goes in flight meanwhile
@@ -1260,93 +1355,96 @@ __global__ void __launch_bounds__(THREADS) query_side_bf16_kernel(BwdParams p) {
                 regs_load_bf<false>(sn[1], nx + D * D, D, D);
             }
             __syncthreads();
-            floatx4 xr[4], xi[4];
+            // X^T[j][t] = sum_k conj(S_m[k][j]) dY[t][k], two column tiles jt at a time;
+            // dQ~ += conj(rho_m[t]) X (rho_m = P_m); d rho_m[t] = sum_j q~[t][j] conj(X[t][j])
+            const float rhr = sPr[m * 64 + t], rhi = sPi[m * 64 + t];
+            float pr = 0.f, pi = 0.f;
 #pragma unroll
-            for (int jt = 0; jt < 4; ++jt) xr[jt] = xi[jt] = zero4();
+            for (int jh = 0; jh < 2; ++jh) {
+                floatx4 xr[2], xi[2];
 #pragma unroll
-            for (int kp = 0; kp < 2; ++kp) {
-                const int k0 = 32 * kp + 8 * g;
-                const bf16x8 agr = ld8(sGr + t * PB + k0), agi = ld8(sGi + t * PB + k0), nagr = neg_bf(agr);
+                for (int jj = 0; jj < 2; ++jj) xr[jj] = xi[jj] = zero4();
 #pragma unroll
-                for (int jt = 0; jt < 4; ++jt) {
-                    const bf16x8 sr = ld_tr(sVr, k0, k0 + 4, 16 * jt), si = ld_tr(sVi, k0, k0 + 4, 16 * jt);
-                    xr[jt] = mfma_bf(agr, sr, xr[jt]);
-                    xr[jt] = mfma_bf(agi, si, xr[jt]);
-                    xi[jt] = mfma_bf(agi, sr, xi[jt]);
-                    xi[jt] = mfma_bf(nagr, si, xi[jt]);
+                for (int kp = 0; kp < 2; ++kp) {
+                    const int k0 = 32 * kp + 8 * g;
+                    const bf16x8 ngr = neg_bf(bg[kp][0]);
+#pragma unroll
+                    for (int jj = 0; jj < 2; ++jj) {
+                        const int jt = 2 * jh + jj;
+                        const bf16x8 sr = ld_tr(sVr, k0, k0 + 4, 16 * jt), si = ld_tr(sVi, k0, k0 + 4, 16 * jt);
+                        xr[jj] = mfma_bf(sr, bg[kp][0], xr[jj]);
+                        xr[jj] = mfma_bf(si, bg[kp][1], xr[jj]);
+                        xi[jj] = mfma_bf(sr, bg[kp][1], xi[jj]);
+                        xi[jj] = mfma_bf(si, ngr, xi[jj]);
+                    }
                 }
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int jt = 2 * jh + jj;
+                        const float x_r = xr[jj][r], x_i = xi[jj][r];
+                        gqR[jt][r] += rhr * x_r + rhi * x_i;
+                        gqI[jt][r] += rhr * x_i - rhi * x_r;
+                        const float qr = quad_elem(qq[jt][0], r), qi = quad_elem(qq[jt][1], r);
+                        pr += qr * x_r + qi * x_i;
+                        pi += qr * x_i - qi * x_r;
+                    }
             }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tr = 16 * tt + 4 * g + r;
-                const float cum = __expf(sL[m * 64 + tr]);
-                const float rr = sRr[m * 64 + tr], ri = sRi[m * 64 + tr];
-                const float rhr = rr * cum, rhi = ri * cum;
-                float pr = 0.f, pi = 0.f;
-#pragma unroll
-                for (int jt = 0; jt < 4; ++jt) {
-                    const float x_r = xr[jt][r], x_i = xi[jt][r];
-                    gqR[jt][r] += rhr * x_r + rhi * x_i;
-                    gqI[jt][r] += rhr * x_i - rhi * x_r;
-                    const float qr = bf16_to_f32(sQr[tr * PB + 16 * jt + l16]) * qs;
-                    const float qi = bf16_to_f32(sQi[tr * PB + 16 * jt + l16]) * qs;
-                    pr += qr * x_r + qi * x_i;
-                    pi += qr * x_i - qi * x_r;
-                }
-#pragma unroll
-                for (int off = 1; off < 16; off <<= 1) {
-                    pr += __shfl_xor(pr, off);
-                    pi += __shfl_xor(pi, off);
-                }
-                if (l16 == 0) {
-                    atomicAdd(&sDRr[m * 64 + tr], pr * cum);
-                    atomicAdd(&sDRi[m * 64 + tr], pi * cum);
-                    atomicAdd(&sGL[m * 64 + tr], (pr * rr + pi * ri) * cum);
-                }
+            pr += __shfl_xor(pr, 16);
+            pr += __shfl_xor(pr, 32);
+            pi += __shfl_xor(pi, 16);
+            pi += __shfl_xor(pi, 32);
+            if (g == 0) {
+                const float cum = __expf(sL[m * 64 + t]) * qs;
+                sDqr[m * 64 + t] += pr * cum;
+                sDqi[m * 64 + t] += pi * cum;
+                sGq[m * 64 + t] += (pr * sRr[m * 64 + t] + pi * sRi[m * 64 + t]) * cum;
             }
         }
     }
-    __syncthreads();
 
-    {
-        const int64_t qo = b * p.dq.s0 + h * p.dq.s1 + (int64_t)c0 * p.dq.s2;
+    if (tv) {
+        const int64_t o = b * p.dq.s0 + h * p.dq.s1 + (int64_t)(c0 + t) * p.dq.s2;
+        U16 *dre = (U16 *)p.dq.re + o, *dim = (U16 *)p.dq.im + o;
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int tr = 16 * tt + 4 * g + r;
-                if (tr < valid) {
-                    const int64_t o = qo + (int64_t)tr * p.dq.s2 + 16 * jt + l16;
-                    store_elem<U16>(p.dq.re, o, gqR[jt][r] * qs);
-                    store_elem<U16>(p.dq.im, o, gqI[jt][r] * qs);
+        for (int jt = 0; jt < 4; ++jt) {
+            store_quad(dre, jt, gqR[jt], qs);
+            store_quad(dim, jt, gqI[jt], qs);
+        }
+        if (g == 0) {
+            for (int m = 0; m < M; ++m) {
+                p.gl[chain_idx(p, m, b, h) * (int64_t)p.n_chunks * 64 + c0 + t] = sGq[m * 64 + t];
+                if (p.drot_re) {
+                    const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + t) * a.sr_t;
+                    p.drot_re[ro] = sDqr[m * 64 + t];
+                    p.drot_im[ro] = sDqi[m * 64 + t];
                 }
-            }
-    }
-    if (tid < 64 && tid < valid) {
-        for (int m = 0; m < M; ++m) {
-            p.gl[chain_idx(p, m, b, h) * (int64_t)p.n_chunks * 64 + c0 + tid] = sGL[m * 64 + tid];
-            if (p.drot_re) {
-                const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + tid) * a.sr_t;
-                p.drot_re[ro] = sDRr[m * 64 + tid];
-                p.drot_im[ro] = sDRi[m * 64 + tid];
             }
         }
     }
 }
 
+// Key side, bf16 operands and chunk 64.  Wave = 16 key rows s; q (later G'_m),
+// k, v and dY are staged in LDS, and the wave's own k and v rows are held as
+// MFMA operands while it forms its score tiles.  Score tiles
+// in natural orientation (lane: key s = l16, row t = 4g + r) so that per-key
+// quantities are per-lane scalars; dK and dV accumulate transposed (lane: key
+// s, columns 16 it + 4 g + r) and leave as 8-byte runs.  Fast path: D~ and the
+// column sums sum_{t>s} Re(gD~[t,s] conj(P_m[t])) are fp32 MFMA products.
 template <int M, bool DYBF>
 __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
-    U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;   // q, later G'_m
+    U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;  // q, later G'_m
     U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
     U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
-    U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;                    // dY
+    U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;                   // dY
     // per-step vectors [M][64]
     float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + M * 64, *sRi = sRr + M * 64;
     float *sGL = sRi + M * 64, *sDl = sGL + M * 64;
     float *sF = sDl + M * 64, *sPr = sF + M * 64, *sPi = sPr + M * 64;
     float *sRed = sPi + M * 64;
-    int *sFast = reinterpret_cast<int *>(sRed + 4);
+    int *sFast = reinterpret_cast<int *>(sRed + 4);  // [M] factorisation tests
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -1354,40 +1452,17 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const bool carry = (c > 0) || (a.s0_re != nullptr);
     const float qs = a.q_scale;
-    {
-        const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
-        const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
-        const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-        U16 *const bd[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
-        const U16 *const bs[6] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
-                                  (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
-        const int64_t bst[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        if constexpr (DYBF) {
-            U16 *const bd8[8] = {bd[0], bd[1], bd[2], bd[3], bd[4], bd[5], sGr, sGi};
-            const U16 *const bs8[8] = {bs[0], bs[1], bs[2], bs[3], bs[4], bs[5], (const U16 *)p.dy.re + go,
-                                       (const U16 *)p.dy.im + go};
-            const int64_t bst8[8] = {bst[0], bst[1], bst[2], bst[3], bst[4], bst[5], p.dy.s2, p.dy.s2};
-            stage_bf<8, 0x0u>(bd8, bs8, bst8, valid);
-        } else {
-            U16 *const fd[2] = {sGr, sGi};
-            const float *const fs[2] = {(const float *)p.dy.re + go, (const float *)p.dy.im + go};
-            const int64_t fst[2] = {p.dy.s2, p.dy.s2};
-            stage_mixed<6, 0x0u, 2, 0x0u>(bd, bs, bst, fd, fs, fst, valid);
-        }
+    // global loads first: decay inputs and row part of the decay gradient of
+    // state m = w, the Q, K, V, dY tiles and the state-0 snapshots
+    DecayIn din;
+    float glv = 0.f;
+    if (w < M) {
+        din = decay_load(a, w, b, h, c0, valid);
+        if (lane < valid) glv = p.gl[chain_idx(p, w, b, h) * (int64_t)p.n_chunks * 64 + c0 + lane];
     }
-    if (w == 0) {
-        chunk_decay_prologue_f<M>(a, b, h, c0, valid, sL, sRr, sRi, sF, sPr, sPi, sFast);
-        for (int m = 0; m < M; ++m) {
-            const float L = sL[m * 64 + lane];
-            const float Llast = sL[m * 64 + valid - 1];
-            sDl[m * 64 + lane] = (lane < valid) ? __expf(fminf(Llast - L, 0.f)) : 0.f;
-            sGL[m * 64 + lane] =
-                (lane < valid) ? p.gl[chain_idx(p, m, b, h) * (int64_t)p.n_chunks * 64 + c0 + lane] : 0.f;
-        }
-    }
-    __syncthreads();
-
+    const int st = causal_tile(w);
+    const int s = 16 * st + l16;
+    const bool sv = s < valid;
     // snapshots of state m (dS after the chunk, and the entering state): state 0
     // is in flight during the intra-chunk phase, state m+1 while m is processed
     B16Regs gr[2], sr[2];
@@ -1401,147 +1476,193 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
             regs_load_bf<false>(sr[1], ssrc + D * D, D, D);
         }
     };
-    load_state(0);
+    {
+        const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
+        const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
+        const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
+        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
+        U16 *const bd[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
+        const U16 *const bs[6] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
+                                  (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
+        const int64_t bst[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        B16Regs rb[8];
+        F32Regs rf[2];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) regs_load_bf<false>(rb[i], bs[i], bst[i], valid);
+        if constexpr (DYBF) {
+            regs_load_bf<false>(rb[6], (const U16 *)p.dy.re + go, p.dy.s2, valid);
+            regs_load_bf<false>(rb[7], (const U16 *)p.dy.im + go, p.dy.s2, valid);
+        } else {
+            regs_load_f32<false>(rf[0], (const float *)p.dy.re + go, p.dy.s2, valid);
+            regs_load_f32<false>(rf[1], (const float *)p.dy.im + go, p.dy.s2, valid);
+        }
+        load_state(0);
+        if (w < M) {
+            const bool ok = decay_tables(din, w, valid, sL, sRr, sRi, sF, sPr, sPi);
+            if (lane == 0) sFast[w] = ok ? 1 : 0;
+            const float Llast = __shfl(sL[w * 64 + lane], valid - 1);
+            sDl[w * 64 + lane] = (lane < valid) ? __expf(fminf(Llast - sL[w * 64 + lane], 0.f)) : 0.f;
+            sGL[w * 64 + lane] = glv;
+        }
+#pragma unroll
+        for (int i = 0; i < 6; ++i) regs_store_bf<false>(bd[i], rb[i]);
+        if constexpr (DYBF) {
+            regs_store_bf<false>(sGr, rb[6]);
+            regs_store_bf<false>(sGi, rb[7]);
+        } else {
+            regs_store_f32_as_bf<false>(sGr, rf[0]);
+            regs_store_f32_as_bf<false>(sGi, rf[1]);
+        }
+    }
+    __syncthreads();
 
-    const int st = causal_tile(w);
-    const int s = 16 * st + l16;
+    bool fast = true;
+#pragma unroll
+    for (int m = 0; m < M; ++m) fast = fast && sFast[m] != 0;
     floatx4 gvR[4], gvI[4], gkR[4], gkI[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it) gvR[it] = gvI[it] = gkR[it] = gkI[it] = zero4();
     {
-        floatx4 wr[4], wi[4], dr[4], di[4];  // W[t][s], dA[t][s], t-tiles tt >= st
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) wr[tt] = wi[tt] = dr[tt] = di[tt] = zero4();
-#pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-            const int k0 = 32 * kp + 8 * g;
-            const bf16x8 bkr = ld8(sKr + s * PB + k0), bki = ld8(sKi + s * PB + k0);
-            const bf16x8 bvr = ld8(sVr + s * PB + k0), bvi = ld8(sVi + s * PB + k0);
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                if (tt < st) continue;
-                const int t = 16 * tt + l16;
-                const bf16x8 aqr = ld8(sQr + t * PB + k0), aqi = ld8(sQi + t * PB + k0);
-                const bf16x8 agr = ld8(sGr + t * PB + k0), agi = ld8(sGi + t * PB + k0);
-                wr[tt] = mfma_bf(aqr, bkr, wr[tt]);
-                wr[tt] = mfma_bf(aqi, bki, wr[tt]);
-                wi[tt] = mfma_bf(aqi, bkr, wi[tt]);
-                wi[tt] = mfma_bf(neg_bf(aqr), bki, wi[tt]);
-                dr[tt] = mfma_bf(agr, bvr, dr[tt]);
-                dr[tt] = mfma_bf(agi, bvi, dr[tt]);
-                di[tt] = mfma_bf(agi, bvr, di[tt]);
-                di[tt] = mfma_bf(neg_bf(agr), bvi, di[tt]);
-            }
-        }
-        // A = (q_scale W) D~ -> (wr, wi);  q_scale gW = q_scale dA conj(D~) -> (dr, di).
-        // Column part of the decay-matrix gradient: with gD~ = dA conj(q_scale W),
-        // dL_m[s] -= sum_t Re(gD~ conj(r_m[t])) D_m[t,s] over unclamped t > s.  This
-        // wave owns column tile st, so the sum runs over its registers and lane groups.
-        float colp[MAX_M];
+        // fast path: the column sums C[m][s] in element m of lanes g == 0 (fp32 MFMA)
+        floatx4 cR = zero4();
+        float colp[MAX_M];  // general path, per-lane partials
 #pragma unroll
         for (int m = 0; m < MAX_M; ++m) colp[m] = 0.f;
-        if (*sFast) {
-            // D_m[t,s] = E_m[t] F_m[s]: D~ = sum_m (r_m E_m)[t] F_m[s], and the column sums
-            // are F_m[s] sum_t Re(gD~ conj(r_m E_m)[t]) over t > s.
-            float Fs[MAX_M];
+        // B operand of the decay-factor product: lane (g = m, l16) holds q_scale F_m[s]
+        const float fb = (g < M) ? sF[g * 64 + s] * qs : 0.f;
+        bf16x8 bk[2][2], bv[2][2];  // [k half][re, im] of k and v, rows s
 #pragma unroll
-            for (int m = 0; m < M; ++m) Fs[m] = sF[m * 64 + s];
-#pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                if (tt < st) continue;
-                float4 P4r[MAX_M], P4i[MAX_M];
-#pragma unroll
-                for (int m = 0; m < M; ++m) {
-                    P4r[m] = *reinterpret_cast<const float4 *>(sPr + m * 64 + 16 * tt + 4 * g);
-                    P4i[m] = *reinterpret_cast<const float4 *>(sPi + m * 64 + 16 * tt + 4 * g);
-                }
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int t = 16 * tt + 4 * g + r;
-                    const float Wr = wr[tt][r] * qs, Wi = wi[tt][r] * qs, Ar = dr[tt][r], Ai = di[tt][r];
-                    const float gdr = Ar * Wr + Ai * Wi, gdi = Ai * Wr - Ar * Wi;
-                    const bool keep = tt > st || s <= t, below = tt > st || s < t;
-                    const float gor = below ? gdr : 0.f, goi = below ? gdi : 0.f;
-                    float dtr = 0.f, dti = 0.f;
-#pragma unroll
-                    for (int m = 0; m < M; ++m) {
-                        const float pr = r == 0 ? P4r[m].x : r == 1 ? P4r[m].y : r == 2 ? P4r[m].z : P4r[m].w;
-                        const float pi = r == 0 ? P4i[m].x : r == 1 ? P4i[m].y : r == 2 ? P4i[m].z : P4i[m].w;
-                        dtr += pr * Fs[m];
-                        dti += pi * Fs[m];
-                        colp[m] += gor * pr + goi * pi;
-                    }
-                    dtr = keep ? dtr : 0.f;
-                    dti = keep ? dti : 0.f;
-                    wr[tt][r] = Wr * dtr - Wi * dti;
-                    wi[tt][r] = Wr * dti + Wi * dtr;
-                    dr[tt][r] = (Ar * dtr + Ai * dti) * qs;
-                    di[tt][r] = (Ai * dtr - Ar * dti) * qs;
-                }
-            }
-#pragma unroll
-            for (int m = 0; m < M; ++m) colp[m] *= Fs[m];
-        } else {
-#pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
-            if (tt < st) continue;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = 16 * tt + 4 * g + r;
-                const float Wr = wr[tt][r] * qs, Wi = wi[tt][r] * qs, Ar = dr[tt][r], Ai = di[tt][r];
-                const float gdr = Ar * Wr + Ai * Wi, gdi = Ai * Wr - Ar * Wi;
-                float dtr = 0.f, dti = 0.f;
-                if (s <= t) {
-#pragma unroll
-                    for (int m = 0; m < MAX_M; ++m) {
-                        if (m < M) {
-                            const float x = sL[m * 64 + t] - sL[m * 64 + s];
-                            const float Dm = __expf(fminf(x, 0.f));
-                            const float rr = sRr[m * 64 + t], ri = sRi[m * 64 + t];
-                            dtr += rr * Dm;
-                            dti += ri * Dm;
-                            if (x <= 0.f && s != t) colp[m] += (gdr * rr + gdi * ri) * Dm;
-                        }
-                    }
-                }
-                wr[tt][r] = Wr * dtr - Wi * dti;
-                wi[tt][r] = Wr * dti + Wi * dtr;
-                dr[tt][r] = (Ar * dtr + Ai * dti) * qs;
-                di[tt][r] = (Ai * dtr - Ar * dti) * qs;
-            }
+        for (int kq = 0; kq < 2; ++kq) {
+            const int k0 = 32 * kq + 8 * g;
+            bk[kq][0] = ld8(sKr + s * PB + k0);
+            bk[kq][1] = ld8(sKi + s * PB + k0);
+            bv[kq][0] = ld8(sVr + s * PB + k0);
+            bv[kq][1] = ld8(sVi + s * PB + k0);
         }
-        }
-#pragma unroll
-        for (int m = 0; m < MAX_M; ++m) {
-            if (m < M) {
-                float x = colp[m];
-                x += __shfl_xor(x, 16);
-                x += __shfl_xor(x, 32);
-                if (g == 0) sGL[m * 64 + s] -= x;
-            }
-        }
-        // dV[s][i] += sum_t conj(A[t,s]) G[t,i];  dK[s][j] += sum_t conj(q_s gW[t,s]) q[t,j]
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             if (2 * kp + 1 < st) continue;
-            const bf16x8 ar = frag_from_acc(wr[2 * kp], wr[2 * kp + 1]);
-            const bf16x8 ai = frag_from_acc(wi[2 * kp], wi[2 * kp + 1]);
-            const bf16x8 gr_ = frag_from_acc(dr[2 * kp], dr[2 * kp + 1]);
-            const bf16x8 gi_ = frag_from_acc(di[2 * kp], di[2 * kp + 1]);
+            floatx4 aR[2], aI[2], gR[2], gI[2];  // A' = q_scale W D~ and gA = q_scale dA conj(D~), t tiles 2kp + h2
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const int tt = 2 * kp + h2;
+                aR[h2] = aI[h2] = gR[h2] = gI[h2] = zero4();
+                if (tt < st) continue;
+                const int t = 16 * tt + l16;
+                // W[t][s] = sum_j q[t,j] conj(k[s,j]),  dA[t][s] = sum_i dY[t,i] conj(v[s,i])
+                floatx4 wr = zero4(), wi = zero4(), dr = zero4(), di = zero4();
+#pragma unroll
+                for (int kq = 0; kq < 2; ++kq) {
+                    const int k0 = 32 * kq + 8 * g;
+                    const bf16x8 aqr = ld8(sQr + t * PB + k0), aqi = ld8(sQi + t * PB + k0);
+                    const bf16x8 agr = ld8(sGr + t * PB + k0), agi = ld8(sGi + t * PB + k0);
+                    wr = mfma_bf(aqr, bk[kq][0], wr);
+                    wr = mfma_bf(aqi, bk[kq][1], wr);
+                    wi = mfma_bf(aqi, bk[kq][0], wi);
+                    wi = mfma_bf(neg_bf(aqr), bk[kq][1], wi);
+                    dr = mfma_bf(agr, bv[kq][0], dr);
+                    dr = mfma_bf(agi, bv[kq][1], dr);
+                    di = mfma_bf(agi, bv[kq][0], di);
+                    di = mfma_bf(neg_bf(agr), bv[kq][1], di);
+                }
+                if (fast) {
+                    // q_scale D~[t][s] = sum_m P_m[t] q_scale F_m[s]: A lane (g = m, l16) holds P_m[16 tt + l16]
+                    const float par = (g < M) ? sPr[g * 64 + t] : 0.f, pai = (g < M) ? sPi[g * 64 + t] : 0.f;
+                    floatx4 Dr = mfma4(par, fb, zero4()), Di = mfma4(pai, fb, zero4());
+                    if (tt == st) {  // diagonal tile: A' and gA on t >= s
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            Dr[r] = (4 * g + r >= l16) ? Dr[r] : 0.f;
+                            Di[r] = (4 * g + r >= l16) ? Di[r] : 0.f;
+                        }
+                    }
+                    floatx4 gdr, gdi;  // gD~ = dA conj(W), q_scale applied to the column sums
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        aR[h2][r] = wr[r] * Dr[r] - wi[r] * Di[r];
+                        aI[h2][r] = wr[r] * Di[r] + wi[r] * Dr[r];
+                        gR[h2][r] = dr[r] * Dr[r] + di[r] * Di[r];
+                        gI[h2][r] = di[r] * Dr[r] - dr[r] * Di[r];
+                        gdr[r] = dr[r] * wr[r] + di[r] * wi[r];
+                        gdi[r] = di[r] * wr[r] - dr[r] * wi[r];
+                    }
+                    if (tt == st) {  // column sums over t > s
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            gdr[r] = (4 * g + r > l16) ? gdr[r] : 0.f;
+                            gdi[r] = (4 * g + r > l16) ? gdi[r] : 0.f;
+                        }
+                    }
+                    // C[m][s] += sum_t Re(gD~[t][s] conj(P_m[t])): A lane (g, l16 = m) holds P_m[16 tt + 4 g + r]
+                    floatx4 p4r = zero4(), p4i = zero4();
+                    if (l16 < M) {
+                        p4r = *reinterpret_cast<const floatx4 *>(sPr + l16 * 64 + 16 * tt + 4 * g);
+                        p4i = *reinterpret_cast<const floatx4 *>(sPi + l16 * 64 + 16 * tt + 4 * g);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        cR = mfma4(p4r[r], gdr[r], cR);
+                        cR = mfma4(p4i[r], gdi[r], cR);
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int tr = 16 * tt + 4 * g + r;
+                        const float Wr = wr[r] * qs, Wi = wi[r] * qs, Ar = dr[r], Ai = di[r];
+                        const float gdr = Ar * Wr + Ai * Wi, gdi = Ai * Wr - Ar * Wi;
+                        float dtr = 0.f, dti = 0.f;
+                        if (s <= tr) {
+#pragma unroll
+                            for (int m = 0; m < MAX_M; ++m) {
+                                if (m < M) {
+                                    const float x = sL[m * 64 + tr] - sL[m * 64 + s];
+                                    const float Dm = __expf(fminf(x, 0.f));
+                                    const float rr = sRr[m * 64 + tr], ri = sRi[m * 64 + tr];
+                                    dtr += rr * Dm;
+                                    dti += ri * Dm;
+                                    if (x <= 0.f && s != tr) colp[m] += (gdr * rr + gdi * ri) * Dm;
+                                }
+                            }
+                        }
+                        aR[h2][r] = Wr * dtr - Wi * dti;
+                        aI[h2][r] = Wr * dti + Wi * dtr;
+                        gR[h2][r] = (Ar * dtr + Ai * dti) * qs;
+                        gI[h2][r] = (Ai * dtr - Ar * dti) * qs;
+                    }
+                }
+            }
+            // dV^T[i][s] += sum_t dY[t][i] conj(A'[t][s]);  dK^T[j][s] += sum_t q[t][j] conj(gA[t][s])
+            const bf16x8 ar = frag_from_acc(aR[0], aR[1]), ai = frag_from_acc(aI[0], aI[1]);
+            const bf16x8 gr_ = frag_from_acc(gR[0], gR[1]), gi_ = frag_from_acc(gI[0], gI[1]);
             const bf16x8 nai = neg_bf(ai), ngi = neg_bf(gi_);
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
                 const int r0 = 32 * kp + 4 * g;
                 const bf16x8 yr = ld_tr(sGr, r0, r0 + 16, 16 * it), yi = ld_tr(sGi, r0, r0 + 16, 16 * it);
-                gvR[it] = mfma_bf(ar, yr, gvR[it]);
-                gvR[it] = mfma_bf(ai, yi, gvR[it]);
-                gvI[it] = mfma_bf(ar, yi, gvI[it]);
-                gvI[it] = mfma_bf(nai, yr, gvI[it]);
+                gvR[it] = mfma_bf(yr, ar, gvR[it]);
+                gvR[it] = mfma_bf(yi, ai, gvR[it]);
+                gvI[it] = mfma_bf(yi, ar, gvI[it]);
+                gvI[it] = mfma_bf(yr, nai, gvI[it]);
                 const bf16x8 qr = ld_tr(sQr, r0, r0 + 16, 16 * it), qi = ld_tr(sQi, r0, r0 + 16, 16 * it);
-                gkR[it] = mfma_bf(gr_, qr, gkR[it]);
-                gkR[it] = mfma_bf(gi_, qi, gkR[it]);
-                gkI[it] = mfma_bf(gr_, qi, gkI[it]);
-                gkI[it] = mfma_bf(ngi, qr, gkI[it]);
+                gkR[it] = mfma_bf(qr, gr_, gkR[it]);
+                gkR[it] = mfma_bf(qi, gi_, gkR[it]);
+                gkI[it] = mfma_bf(qi, gr_, gkI[it]);
+                gkI[it] = mfma_bf(qr, ngi, gkI[it]);
+            }
+        }
+        // column part of the decay-matrix gradient: dL_m[s] -= F_m[s] C[m][s] (this wave's keys)
+        if (fast) {
+            if (g == 0) {
+#pragma unroll
+                for (int m = 0; m < M; ++m) sGL[m * 64 + s] -= cR[m] * sF[m * 64 + s] * qs;
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                float x = colp[m];
+                x += __shfl_xor(x, 16);
+                x += __shfl_xor(x, 32);
+                if (g == 0) sGL[m * 64 + s] -= x;
             }
         }
     }
@@ -1549,19 +1670,24 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
     // state-write gradients with G'_m = dS after this chunk
     for (int m = 0; m < M; ++m) {
         __syncthreads();
-        {  // G' natural into sQ*; with a carried state also this thread's share of S (registers)
+        {  // G' natural into sQ*; with a carried state also this thread's share of Re<G', S>
             regs_store_bf<false>(sQr, gr[0]);
             regs_store_bf<false>(sQi, gr[1]);
-            if (carry) {  // g_total = sum Re(conj(G') S) over both planes, fp32 accumulation
+            if (carry) {
                 float part = 0.f;
 #pragma unroll
                 for (int pl = 0; pl < 2; ++pl)
 #pragma unroll
                     for (int i = 0; i < 2; ++i) {
-                        const ushortx8 x = __builtin_bit_cast(ushortx8, gr[pl].v[i]);
-                        const ushortx8 y = __builtin_bit_cast(ushortx8, sr[pl].v[i]);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) part += bf16_to_f32(x[e]) * bf16_to_f32(y[e]);
+                        const uint4 x = gr[pl].v[i], y = sr[pl].v[i];
+                        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.x),
+                                                               __builtin_bit_cast(bf16x2, y.x), part, false);
+                        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.y),
+                                                               __builtin_bit_cast(bf16x2, y.y), part, false);
+                        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.z),
+                                                               __builtin_bit_cast(bf16x2, y.z), part, false);
+                        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.w),
+                                                               __builtin_bit_cast(bf16x2, y.w), part, false);
                     }
 #pragma unroll
                 for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
@@ -1577,50 +1703,48 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             const int k0 = 32 * kp + 8 * g;
-            const bf16x8 akr = ld8(sKr + s * PB + k0), aki = ld8(sKi + s * PB + k0), naki = neg_bf(aki);
-            const floatx8 vrf = to_f(ld8(sVr + s * PB + k0)), vif = to_f(ld8(sVi + s * PB + k0));
-            const bf16x8 avr = to_bf(vrf * dls), avi = to_bf(vif * dls), navr = neg_bf(avr);
+            const bf16x8 akr = ld8(sKr + s * PB + k0), aki = ld8(sKi + s * PB + k0), nki = neg_bf(aki);
+            const bf16x8 avr = to_bf(to_f(ld8(sVr + s * PB + k0)) * dls), avi = to_bf(to_f(ld8(sVi + s * PB + k0)) * dls);
+            const bf16x8 navr = neg_bf(avr);
 #pragma unroll
             for (int it = 0; it < 4; ++it) {
+                // Z^T[i][s] = sum_j G'[i][j] k[s][j]
                 const int row = (16 * it + l16) * PB + k0;
-                // Z[s][i] = sum_j K[s,j] G'[i,j]
                 const bf16x8 gpr = ld8(sQr + row), gpi = ld8(sQi + row);
-                zr[it] = mfma_bf(akr, gpr, zr[it]);
-                zr[it] = mfma_bf(naki, gpi, zr[it]);
-                zi[it] = mfma_bf(akr, gpi, zi[it]);
-                zi[it] = mfma_bf(aki, gpr, zi[it]);
-                // dK[s][j] += dl[s] sum_i V[s,i] conj(G'[i,j])   (j = 16 it + l16, transposed reads of G')
+                zr[it] = mfma_bf(gpr, akr, zr[it]);
+                zr[it] = mfma_bf(gpi, nki, zr[it]);
+                zi[it] = mfma_bf(gpi, akr, zi[it]);
+                zi[it] = mfma_bf(gpr, aki, zi[it]);
+                // dK^T[j][s] += dl[s] sum_i conj(G'[i][j]) v[s][i]   (transposed reads of G')
                 const bf16x8 gtr = ld_tr(sQr, k0, k0 + 4, 16 * it), gti = ld_tr(sQi, k0, k0 + 4, 16 * it);
-                gkR[it] = mfma_bf(avr, gtr, gkR[it]);
-                gkR[it] = mfma_bf(avi, gti, gkR[it]);
-                gkI[it] = mfma_bf(avi, gtr, gkI[it]);
-                gkI[it] = mfma_bf(navr, gti, gkI[it]);
+                gkR[it] = mfma_bf(gtr, avr, gkR[it]);
+                gkR[it] = mfma_bf(gti, avi, gkR[it]);
+                gkI[it] = mfma_bf(gtr, avi, gkI[it]);
+                gkI[it] = mfma_bf(gti, navr, gkI[it]);
             }
         }
-        // lane holds Z[s' = 16st + 4g + r][i = 16it + l16]
+        // dV += dl Z; the dl gradient sum_i Re(v[s][i] conj(Z[s][i]))
+        float gdl = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int sr_ = 16 * st + 4 * g + r;
-            const float dl = sDl[m * 64 + sr_];
-            float gdl = 0.f;
+        for (int it = 0; it < 4; ++it) {
+            const uint2 vr4 = *reinterpret_cast<const uint2 *>(sVr + s * PB + 16 * it + 4 * g);
+            const uint2 vi4 = *reinterpret_cast<const uint2 *>(sVi + s * PB + 16 * it + 4 * g);
 #pragma unroll
-            for (int it = 0; it < 4; ++it) {
+            for (int r = 0; r < 4; ++r) {
                 const float z_r = zr[it][r], z_i = zi[it][r];
-                const float vr = bf16_to_f32(sVr[sr_ * PB + 16 * it + l16]);
-                const float vi = bf16_to_f32(sVi[sr_ * PB + 16 * it + l16]);
-                gdl += vr * z_r + vi * z_i;
-                gvR[it][r] += dl * z_r;
-                gvI[it][r] += dl * z_i;
+                gvR[it][r] += dls * z_r;
+                gvI[it][r] += dls * z_i;
+                gdl += quad_elem(vr4, r) * z_r + quad_elem(vi4, r) * z_i;
             }
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) gdl += __shfl_xor(gdl, off);
-            if (l16 == 0 && sr_ < valid) {
-                const float x = sL[m * 64 + valid - 1] - sL[m * 64 + sr_];
-                const float gp = (x <= 0.f) ? gdl * dl : 0.f;
-                if (sr_ != valid - 1) {
-                    atomicAdd(&sGL[m * 64 + valid - 1], gp);
-                    atomicAdd(&sGL[m * 64 + sr_], -gp);
-                }
+        }
+        gdl += __shfl_xor(gdl, 16);
+        gdl += __shfl_xor(gdl, 32);
+        if (g == 0 && sv) {
+            const float x = sL[m * 64 + valid - 1] - sL[m * 64 + s];
+            const float gp = (x <= 0.f) ? gdl * dls : 0.f;
+            if (s != valid - 1) {
+                atomicAdd(&sGL[m * 64 + valid - 1], gp);
+                atomicAdd(&sGL[m * 64 + s], -gp);
             }
         }
         __syncthreads();
@@ -1631,23 +1755,18 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
     }
     __syncthreads();
 
-    {
-        const int64_t ko = b * p.dk.s0 + h * p.dk.s1 + (int64_t)c0 * p.dk.s2;
-        const int64_t vo = b * p.dv.s0 + h * p.dv.s1 + (int64_t)c0 * p.dv.s2;
+    if (sv) {
+        const int64_t ok_ = b * p.dk.s0 + h * p.dk.s1 + (int64_t)(c0 + s) * p.dk.s2;
+        const int64_t ov_ = b * p.dv.s0 + h * p.dv.s1 + (int64_t)(c0 + s) * p.dv.s2;
+        U16 *kre = (U16 *)p.dk.re + ok_, *kim = (U16 *)p.dk.im + ok_;
+        U16 *vre = (U16 *)p.dv.re + ov_, *vim = (U16 *)p.dv.im + ov_;
 #pragma unroll
-        for (int it = 0; it < 4; ++it)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int sr_ = 16 * st + 4 * g + r;
-                if (sr_ < valid) {
-                    const int64_t o1 = ko + (int64_t)sr_ * p.dk.s2 + 16 * it + l16;
-                    store_elem<U16>(p.dk.re, o1, gkR[it][r]);
-                    store_elem<U16>(p.dk.im, o1, gkI[it][r]);
-                    const int64_t o2 = vo + (int64_t)sr_ * p.dv.s2 + 16 * it + l16;
-                    store_elem<U16>(p.dv.re, o2, gvR[it][r]);
-                    store_elem<U16>(p.dv.im, o2, gvI[it][r]);
-                }
-            }
+        for (int it = 0; it < 4; ++it) {
+            store_quad(kre, it, gkR[it], 1.f);
+            store_quad(kim, it, gkI[it], 1.f);
+            store_quad(vre, it, gvR[it], 1.f);
+            store_quad(vim, it, gvI[it], 1.f);
+        }
     }
     if (w == 0) {
         for (int m = 0; m < M; ++m) {
@@ -1665,12 +1784,13 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
     }
 }
 
-// query/key side: 8 bf16 planes + per-step vectors < 80 KiB, so two blocks share a CU's 160 KiB LDS
+// query side: 4 bf16 planes + 9 per-step vectors; key side: 8 planes + 8
+// vectors (two blocks share a CU's 160 KiB LDS)
 template <int M>
-constexpr size_t qside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (7 * M * 64 + 4) * sizeof(float); }
+constexpr size_t qside_bf16_smem() { return (size_t)4 * PLANE_B * 2 + (9 * M * 64 + 4) * sizeof(float); }
 template <int M>
 constexpr size_t kside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (8 * M * 64 + 8) * sizeof(float); }
-static_assert(2 * qside_bf16_smem<3>() <= 160 * 1024 && 2 * kside_bf16_smem<3>() <= 160 * 1024, "LDS budget");
+static_assert(2 * qside_bf16_smem<MAX_M>() <= 160 * 1024 && 2 * kside_bf16_smem<3>() <= 160 * 1024, "LDS budget");
 
 template <int M>
 int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
@@ -1803,6 +1923,13 @@ int scan_bwd(const qpam_scan_bwd_args *bw, hipStream_t stream) {
     QPAM_REQUIRE((bw->ds0_re == nullptr) == (bw->ds0_im == nullptr), "qpam_scan_bwd: ds0 needs both planes");
     const uintptr_t al = (uintptr_t)bw->ds_re | (uintptr_t)bw->ds_im | (uintptr_t)bw->ds0_re | (uintptr_t)bw->ds0_im;
     QPAM_REQUIRE(al % 16 == 0, "qpam_scan_bwd: state gradients must be 16-byte aligned");
+    if (uses_snapshots(*a)) {  // the bf16 chunk-64 kernels store dq/dk/dv rows in 8-byte runs
+        const qpam_mview *os[3] = {&bw->dq, &bw->dk, &bw->dv};
+        for (const qpam_mview *o : os)
+            QPAM_REQUIRE(((uintptr_t)o->re % 8) == 0 && ((uintptr_t)o->im % 8) == 0 && o->s0 % 4 == 0 &&
+                             o->s1 % 4 == 0 && o->s2 % 4 == 0,
+                         "qpam_scan_bwd: bf16 dq/dk/dv planes must be 8-byte aligned with strides multiple of 4");
+    }
     QPAM_REQUIRE(bw->workspace && bw->workspace_bytes >= bwd_workspace_bytes(*a) &&
                      ((uintptr_t)bw->workspace % 16) == 0,
                  "qpam_scan_bwd: workspace needs %zu bytes (got %zu)", bwd_workspace_bytes(*a),

@@ -194,7 +194,9 @@ int qpam_scan_fwd_noalloc(const qpam_scan_args *a, void *stream);
  * Outputs dq, dk, dv (dtype of q) planar [B,H,T,d]; dgamma fp32 [M,B,H,T]
  * with the strides of gamma; drot (optional) planar fp32 with rot's strides;
  * ds0 (optional) planar fp32 [M,B,H,d,d].  bwd_workspace holds per-chunk
- * state gradients, size from qpam_scan_bwd_workspace_size. */
+ * state gradients, size from qpam_scan_bwd_workspace_size.  With bf16 q/k/v
+ * and C == 64, dq/dk/dv planes must be 8-byte aligned with strides that are
+ * multiples of 4 elements (their rows are stored in 8-byte runs). */
 typedef struct {
     const qpam_scan_args *fwd;
     qpam_cview dy;

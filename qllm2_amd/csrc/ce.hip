@@ -954,6 +954,15 @@ __device__ __forceinline__ void wgemm_tile_dma(const U16 *A, int64_t lda, int a_
 
 __device__ __forceinline__ int xcd_item(int bid, int total) { return big::xcd_item(bid, total); }
 
+// Order a wave's LDS accesses around a point: its earlier LDS operations are
+// complete (lgkmcnt 0) and no LDS access moves across it.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt unconstrained
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // forward: per (256 rows, 256 vocab) tile -> per-row (max, sum exp[, argmax]).
 // Row statistics over a wave's 128 columns: per lane over its 8 columns, then
 // across the 16 lanes that hold the row (DPP); the argmax (first column at the
@@ -1100,7 +1109,9 @@ __global__ void __launch_bounds__(WTHREADS) grad_tile_kernel(BwdParams p) {
             }
             *reinterpret_cast<uint2 *>(tw + l16 * GT_LD + 16 * mi + 4 * g) = make_uint2(lo, hi);
         }
-        __syncthreads();
+        // the slab is this wave's own: its LDS writes complete before its reads
+        // (and the reads before the next slab's writes) without a block barrier
+        wave_lds_sync();
         {   // lane -> (vocab row lane / 4, 16 tile rows (lane % 4) * 16 ..): 32 bytes each
             const int vl = lane >> 2, part = lane & 3;
             const uint4 *src = reinterpret_cast<const uint4 *>(tw + vl * GT_LD + 16 * part);
@@ -1109,7 +1120,7 @@ __global__ void __launch_bounds__(WTHREADS) grad_tile_kernel(BwdParams p) {
             dst[0] = d0;
             dst[1] = d1;
         }
-        __syncthreads();
+        wave_lds_sync();
     }
 }
 }  // namespace wide

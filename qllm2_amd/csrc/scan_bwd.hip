@@ -1105,24 +1105,31 @@ __device__ __forceinline__ void store_quad(U16 *row, int jt, const floatx4 &v, f
         make_uint2(pack_bf16x2(v[0] * scale, v[1] * scale), pack_bf16x2(v[2] * scale, v[3] * scale));
 }
 
-// Query side, bf16 operands and chunk 64.  Wave = 16 query rows t, whose q and
-// dY rows stay in registers; K and V (later the carried states) are staged in
-// LDS.  The score tiles are transposed (lane: row t = l16, key s = 4g + r), so
-// per-row quantities are per-lane scalars, and dQ~ accumulates transposed
-// (lane: row t, columns 16 jt + 4 g + r) and leaves as 8-byte runs.  With the
-// factorised decay D_m[t,s] = E_m[t] F_m[s] the decay factor
-// D~[t,s] = sum_m P_m[t] F_m[s] (P_m = r_m E_m) and the row sums
-// Z_m[t] = sum_{s<t} gD~[t,s] F_m[s] are fp32 MFMA products (k = m, resp. k = s).
+// Query and key sides of a chunk in one pass (bf16 operands, chunk 64): the
+// chunk's q, k, v and dY tiles are staged once and each state's snapshots are
+// read once.  Wave w takes the query tile and the key tile of the same index i
+// (causal work (i + 1) + (4 - i) = 5 tile pairs on every wave).  Phases: the
+// query side's score tiles (dQ~ intra, decay-gradient row sums), the key side's
+// (dV and dK intra, column sums), then per state the carried read (S_m staged in
+// the q tile) and the state write (G'_m, dS after the chunk, in the same tile).
+// The score phases are the query- and key-side kernels' own: transposed score
+// tiles with the factorised decay D~ and its row / column sums on fp32 MFMA,
+// dQ~, dK, dV accumulated transposed and stored as 8-byte runs.
 template <int M, bool DYBF>
-__global__ void __launch_bounds__(THREADS, 2) query_side_bf16_kernel(BwdParams p) {
+__global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
-    U16 *sKr = reinterpret_cast<U16 *>(smem), *sKi = sKr + PLANE_B;
-    U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;  // V tile, later S_m
-    // per-step vectors [M][64]; sGq, sDq*: this chunk's row results (each wave its own rows)
-    float *sL = reinterpret_cast<float *>(sVi + PLANE_B), *sRr = sL + M * 64, *sRi = sRr + M * 64;
+    U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;  // q, then S_m and G'_m
+    U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
+    U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
+    U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;  // dY
+    // per-step vectors [M][64]: decay tables; the query rows' results (each wave
+    // its own rows); the key side's decay-gradient terms
+    float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + M * 64, *sRi = sRr + M * 64;
     float *sF = sRi + M * 64, *sPr = sF + M * 64, *sPi = sPr + M * 64;
     float *sGq = sPi + M * 64, *sDqr = sGq + M * 64, *sDqi = sDqr + M * 64;
-    int *sFast = reinterpret_cast<int *>(sDqi + M * 64);  // [M] factorisation tests
+    float *sGL = sDqi + M * 64;
+    float *sRed = sGL + M * 64;
+    int *sFast = reinterpret_cast<int *>(sRed + 4);  // [M] factorisation tests
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -1130,59 +1137,77 @@ __global__ void __launch_bounds__(THREADS, 2) query_side_bf16_kernel(BwdParams p
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const bool carry = (c > 0) || (a.s0_re != nullptr);
     const float qs = a.q_scale;
-    // global loads first: decay inputs of state m = w, the wave's own q and dY
-    // rows, the K and V tiles and the carried state S_0
+    // global loads first: decay inputs of state m = w, the Q, K, V, dY tiles and
+    // the state-0 snapshots
     DecayIn din;
     if (w < M) din = decay_load(a, w, b, h, c0, valid);
-    const int tt = causal_tile(w);
-    const int t = 16 * tt + l16;
-    const bool tv = t < valid;
-    const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)(c0 + min(t, valid - 1)) * a.q.s2;
-    const U16 *qrr = (const U16 *)a.q.re + qo, *qri = (const U16 *)a.q.im + qo;
-    bf16x8 bq[2][2], bg[2][2];  // [kp][re, im] of q and dY, rows t
-    {
-        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)(c0 + min(t, valid - 1)) * p.dy.s2;
-#pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-            bq[kp][0] = own_frag(qrr, kp, tv);
-            bq[kp][1] = own_frag(qri, kp, tv);
-            if constexpr (DYBF) {
-                bg[kp][0] = own_frag((const U16 *)p.dy.re + go, kp, tv);
-                bg[kp][1] = own_frag((const U16 *)p.dy.im + go, kp, tv);
-            } else {
-                bg[kp][0] = own_frag_f32((const float *)p.dy.re + go, kp, tv);
-                bg[kp][1] = own_frag_f32((const float *)p.dy.im + go, kp, tv);
-            }
+    const int tt = causal_tile(w), st = tt;  // query tile and key tile of this wave
+    const int t = 16 * tt + l16, s = 16 * st + l16;
+    const bool tv = t < valid, sv = s < valid;
+    // snapshots of state m (dS after the chunk, and the entering state): state 0
+    // is in flight during the score phases, state m+1 while m is processed
+    B16Regs gr[2], sr[2];
+    auto load_state = [&](int m) {
+        const U16 *gsrc = gsnap(p, m, b, h, c);
+        regs_load_bf<false>(gr[0], gsrc, D, D);
+        regs_load_bf<false>(gr[1], gsrc + D * D, D, D);
+        if (carry) {
+            const U16 *ssrc = fsnap(p, m, b, h, c);
+            regs_load_bf<false>(sr[0], ssrc, D, D);
+            regs_load_bf<false>(sr[1], ssrc + D * D, D, D);
         }
-    }
-    B16Regs stg[4];
+    };
     {
+        const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
         const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
         const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-        regs_load_bf<false>(stg[0], (const U16 *)a.k.re + ko, a.k.s2, valid);
-        regs_load_bf<false>(stg[1], (const U16 *)a.k.im + ko, a.k.s2, valid);
-        regs_load_bf<false>(stg[2], (const U16 *)a.v.re + vo, a.v.s2, valid);
-        regs_load_bf<false>(stg[3], (const U16 *)a.v.im + vo, a.v.s2, valid);
+        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
+        U16 *const bd[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
+        const U16 *const bs[6] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
+                                  (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
+        const int64_t bst[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
+        B16Regs rb[8];
+        F32Regs rf[2];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) regs_load_bf<false>(rb[i], bs[i], bst[i], valid);
+        if constexpr (DYBF) {
+            regs_load_bf<false>(rb[6], (const U16 *)p.dy.re + go, p.dy.s2, valid);
+            regs_load_bf<false>(rb[7], (const U16 *)p.dy.im + go, p.dy.s2, valid);
+        } else {
+            regs_load_f32<false>(rf[0], (const float *)p.dy.re + go, p.dy.s2, valid);
+            regs_load_f32<false>(rf[1], (const float *)p.dy.im + go, p.dy.s2, valid);
+        }
+        load_state(0);
+        if (w < M) {
+            const bool ok = decay_tables(din, w, valid, sL, sRr, sRi, sF, sPr, sPi);
+            if (lane == 0) sFast[w] = ok ? 1 : 0;
+            sGL[w * 64 + lane] = 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 6; ++i) regs_store_bf<false>(bd[i], rb[i]);
+        if constexpr (DYBF) {
+            regs_store_bf<false>(sGr, rb[6]);
+            regs_store_bf<false>(sGi, rb[7]);
+        } else {
+            regs_store_f32_as_bf<false>(sGr, rf[0]);
+            regs_store_f32_as_bf<false>(sGi, rf[1]);
+        }
     }
-    B16Regs sn[2];  // carried state S_0, in flight during the intra-chunk phase
-    if (carry) {
-        const U16 *s0p = fsnap(p, 0, b, h, c);
-        regs_load_bf<false>(sn[0], s0p, D, D);
-        regs_load_bf<false>(sn[1], s0p + D * D, D, D);
-    }
-    if (w < M) {
-        const bool ok = decay_tables(din, w, valid, sL, sRr, sRi, sF, sPr, sPi);
-        if (lane == 0) sFast[w] = ok ? 1 : 0;
-    }
-    regs_store_bf<false>(sKr, stg[0]);
-    regs_store_bf<false>(sKi, stg[1]);
-    regs_store_bf<false>(sVr, stg[2]);
-    regs_store_bf<false>(sVi, stg[3]);
     __syncthreads();
 
     bool fast = true;
 #pragma unroll
     for (int m = 0; m < M; ++m) fast = fast && sFast[m] != 0;
+    // q and dY rows t as MFMA operand fragments
+    bf16x8 bq[2][2], bg[2][2];  // [kp][re, im]
+#pragma unroll
+    for (int kp = 0; kp < 2; ++kp) {
+        const int k0 = 32 * kp + 8 * g;
+        bq[kp][0] = ld8(sQr + t * PB + k0);
+        bq[kp][1] = ld8(sQi + t * PB + k0);
+        bg[kp][0] = ld8(sGr + t * PB + k0);
+        bg[kp][1] = ld8(sGi + t * PB + k0);
+    }
     floatx4 gqR[4], gqI[4];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) gqR[jt] = gqI[jt] = zero4();
@@ -1336,189 +1361,6 @@ __global__ void __launch_bounds__(THREADS, 2) query_side_bf16_kernel(BwdParams p
         }
     }
 
-    if (carry) {
-        // q of row t in the transposed accumulator layout, unscaled
-        uint2 qq[4][2];
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-            qq[jt][0] = own_quad(qrr, jt, tv);
-            qq[jt][1] = own_quad(qri, jt, tv);
-        }
-        for (int m = 0; m < M; ++m) {
-            __syncthreads();
-            // S_m natural (read transposed below); S_{m+1} goes in flight meanwhile
-            regs_store_bf<false>(sVr, sn[0]);
-            regs_store_bf<false>(sVi, sn[1]);
-            if (m + 1 < M) {
-                const U16 *nx = fsnap(p, m + 1, b, h, c);
-                regs_load_bf<false>(sn[0], nx, D, D);
-                regs_load_bf<false>(sn[1], nx + D * D, D, D);
-            }
-            __syncthreads();
-            // X^T[j][t] = sum_k conj(S_m[k][j]) dY[t][k], two column tiles jt at a time;
-            // dQ~ += conj(rho_m[t]) X (rho_m = P_m); d rho_m[t] = sum_j q~[t][j] conj(X[t][j])
-            const float rhr = sPr[m * 64 + t], rhi = sPi[m * 64 + t];
-            float pr = 0.f, pi = 0.f;
-#pragma unroll
-            for (int jh = 0; jh < 2; ++jh) {
-                floatx4 xr[2], xi[2];
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj) xr[jj] = xi[jj] = zero4();
-#pragma unroll
-                for (int kp = 0; kp < 2; ++kp) {
-                    const int k0 = 32 * kp + 8 * g;
-                    const bf16x8 ngr = neg_bf(bg[kp][0]);
-#pragma unroll
-                    for (int jj = 0; jj < 2; ++jj) {
-                        const int jt = 2 * jh + jj;
-                        const bf16x8 sr = ld_tr(sVr, k0, k0 + 4, 16 * jt), si = ld_tr(sVi, k0, k0 + 4, 16 * jt);
-                        xr[jj] = mfma_bf(sr, bg[kp][0], xr[jj]);
-                        xr[jj] = mfma_bf(si, bg[kp][1], xr[jj]);
-                        xi[jj] = mfma_bf(sr, bg[kp][1], xi[jj]);
-                        xi[jj] = mfma_bf(si, ngr, xi[jj]);
-                    }
-                }
-#pragma unroll
-                for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int jt = 2 * jh + jj;
-                        const float x_r = xr[jj][r], x_i = xi[jj][r];
-                        gqR[jt][r] += rhr * x_r + rhi * x_i;
-                        gqI[jt][r] += rhr * x_i - rhi * x_r;
-                        const float qr = quad_elem(qq[jt][0], r), qi = quad_elem(qq[jt][1], r);
-                        pr += qr * x_r + qi * x_i;
-                        pi += qr * x_i - qi * x_r;
-                    }
-            }
-            pr += __shfl_xor(pr, 16);
-            pr += __shfl_xor(pr, 32);
-            pi += __shfl_xor(pi, 16);
-            pi += __shfl_xor(pi, 32);
-            if (g == 0) {
-                const float cum = __expf(sL[m * 64 + t]) * qs;
-                sDqr[m * 64 + t] += pr * cum;
-                sDqi[m * 64 + t] += pi * cum;
-                sGq[m * 64 + t] += (pr * sRr[m * 64 + t] + pi * sRi[m * 64 + t]) * cum;
-            }
-        }
-    }
-
-    if (tv) {
-        const int64_t o = b * p.dq.s0 + h * p.dq.s1 + (int64_t)(c0 + t) * p.dq.s2;
-        U16 *dre = (U16 *)p.dq.re + o, *dim = (U16 *)p.dq.im + o;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-            store_quad(dre, jt, gqR[jt], qs);
-            store_quad(dim, jt, gqI[jt], qs);
-        }
-        if (g == 0) {
-            for (int m = 0; m < M; ++m) {
-                p.gl[chain_idx(p, m, b, h) * (int64_t)p.n_chunks * 64 + c0 + t] = sGq[m * 64 + t];
-                if (p.drot_re) {
-                    const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + t) * a.sr_t;
-                    p.drot_re[ro] = sDqr[m * 64 + t];
-                    p.drot_im[ro] = sDqi[m * 64 + t];
-                }
-            }
-        }
-    }
-}
-
-// Key side, bf16 operands and chunk 64.  Wave = 16 key rows s; q (later G'_m),
-// k, v and dY are staged in LDS, and the wave's own k and v rows are held as
-// MFMA operands while it forms its score tiles.  Score tiles
-// in natural orientation (lane: key s = l16, row t = 4g + r) so that per-key
-// quantities are per-lane scalars; dK and dV accumulate transposed (lane: key
-// s, columns 16 it + 4 g + r) and leave as 8-byte runs.  Fast path: D~ and the
-// column sums sum_{t>s} Re(gD~[t,s] conj(P_m[t])) are fp32 MFMA products.
-template <int M, bool DYBF>
-__global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) {
-    extern __shared__ float smem[];
-    U16 *sQr = reinterpret_cast<U16 *>(smem), *sQi = sQr + PLANE_B;  // q, later G'_m
-    U16 *sKr = sQi + PLANE_B, *sKi = sKr + PLANE_B;
-    U16 *sVr = sKi + PLANE_B, *sVi = sVr + PLANE_B;
-    U16 *sGr = sVi + PLANE_B, *sGi = sGr + PLANE_B;                   // dY
-    // per-step vectors [M][64]
-    float *sL = reinterpret_cast<float *>(sGi + PLANE_B), *sRr = sL + M * 64, *sRi = sRr + M * 64;
-    float *sGL = sRi + M * 64, *sDl = sGL + M * 64;
-    float *sF = sDl + M * 64, *sPr = sF + M * 64, *sPi = sPr + M * 64;
-    float *sRed = sPi + M * 64;
-    int *sFast = reinterpret_cast<int *>(sRed + 4);  // [M] factorisation tests
-
-    const qpam_scan_args &a = p.a;
-    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-    const int c0 = c * 64, valid = min(64, a.T - c0);
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const bool carry = (c > 0) || (a.s0_re != nullptr);
-    const float qs = a.q_scale;
-    // global loads first: decay inputs and row part of the decay gradient of
-    // state m = w, the Q, K, V, dY tiles and the state-0 snapshots
-    DecayIn din;
-    float glv = 0.f;
-    if (w < M) {
-        din = decay_load(a, w, b, h, c0, valid);
-        if (lane < valid) glv = p.gl[chain_idx(p, w, b, h) * (int64_t)p.n_chunks * 64 + c0 + lane];
-    }
-    const int st = causal_tile(w);
-    const int s = 16 * st + l16;
-    const bool sv = s < valid;
-    // snapshots of state m (dS after the chunk, and the entering state): state 0
-    // is in flight during the intra-chunk phase, state m+1 while m is processed
-    B16Regs gr[2], sr[2];
-    auto load_state = [&](int m) {
-        const U16 *gsrc = gsnap(p, m, b, h, c);
-        regs_load_bf<false>(gr[0], gsrc, D, D);
-        regs_load_bf<false>(gr[1], gsrc + D * D, D, D);
-        if (carry) {
-            const U16 *ssrc = fsnap(p, m, b, h, c);
-            regs_load_bf<false>(sr[0], ssrc, D, D);
-            regs_load_bf<false>(sr[1], ssrc + D * D, D, D);
-        }
-    };
-    {
-        const int64_t qo = b * a.q.s0 + h * a.q.s1 + (int64_t)c0 * a.q.s2;
-        const int64_t ko = b * a.k.s0 + h * a.k.s1 + (int64_t)c0 * a.k.s2;
-        const int64_t vo = b * a.v.s0 + h * a.v.s1 + (int64_t)c0 * a.v.s2;
-        const int64_t go = b * p.dy.s0 + h * p.dy.s1 + (int64_t)c0 * p.dy.s2;
-        U16 *const bd[6] = {sQr, sQi, sKr, sKi, sVr, sVi};
-        const U16 *const bs[6] = {(const U16 *)a.q.re + qo, (const U16 *)a.q.im + qo, (const U16 *)a.k.re + ko,
-                                  (const U16 *)a.k.im + ko, (const U16 *)a.v.re + vo, (const U16 *)a.v.im + vo};
-        const int64_t bst[6] = {a.q.s2, a.q.s2, a.k.s2, a.k.s2, a.v.s2, a.v.s2};
-        B16Regs rb[8];
-        F32Regs rf[2];
-#pragma unroll
-        for (int i = 0; i < 6; ++i) regs_load_bf<false>(rb[i], bs[i], bst[i], valid);
-        if constexpr (DYBF) {
-            regs_load_bf<false>(rb[6], (const U16 *)p.dy.re + go, p.dy.s2, valid);
-            regs_load_bf<false>(rb[7], (const U16 *)p.dy.im + go, p.dy.s2, valid);
-        } else {
-            regs_load_f32<false>(rf[0], (const float *)p.dy.re + go, p.dy.s2, valid);
-            regs_load_f32<false>(rf[1], (const float *)p.dy.im + go, p.dy.s2, valid);
-        }
-        load_state(0);
-        if (w < M) {
-            const bool ok = decay_tables(din, w, valid, sL, sRr, sRi, sF, sPr, sPi);
-            if (lane == 0) sFast[w] = ok ? 1 : 0;
-            const float Llast = __shfl(sL[w * 64 + lane], valid - 1);
-            sDl[w * 64 + lane] = (lane < valid) ? __expf(fminf(Llast - sL[w * 64 + lane], 0.f)) : 0.f;
-            sGL[w * 64 + lane] = glv;
-        }
-#pragma unroll
-        for (int i = 0; i < 6; ++i) regs_store_bf<false>(bd[i], rb[i]);
-        if constexpr (DYBF) {
-            regs_store_bf<false>(sGr, rb[6]);
-            regs_store_bf<false>(sGi, rb[7]);
-        } else {
-            regs_store_f32_as_bf<false>(sGr, rf[0]);
-            regs_store_f32_as_bf<false>(sGi, rf[1]);
-        }
-    }
-    __syncthreads();
-
-    bool fast = true;
-#pragma unroll
-    for (int m = 0; m < M; ++m) fast = fast && sFast[m] != 0;
     floatx4 gvR[4], gvI[4], gkR[4], gkI[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it) gvR[it] = gvI[it] = gkR[it] = gkI[it] = zero4();
@@ -1667,36 +1509,100 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
         }
     }
 
-    // state-write gradients with G'_m = dS after this chunk
+    // q of row t in the transposed accumulator layout (unscaled), read before
+    // the q tile is overwritten
+    uint2 qq[4][2];
+#pragma unroll
+    for (int jt = 0; jt < 4; ++jt) {
+        qq[jt][0] = *reinterpret_cast<const uint2 *>(sQr + t * PB + 16 * jt + 4 * g);
+        qq[jt][1] = *reinterpret_cast<const uint2 *>(sQi + t * PB + 16 * jt + 4 * g);
+    }
     for (int m = 0; m < M; ++m) {
-        __syncthreads();
-        {  // G' natural into sQ*; with a carried state also this thread's share of Re<G', S>
-            regs_store_bf<false>(sQr, gr[0]);
-            regs_store_bf<false>(sQi, gr[1]);
-            if (carry) {
-                float part = 0.f;
+        __syncthreads();  // nothing reads the q tile (m = 0) or G'_{m-1} any more
+        if (carry) {  // S_m natural into the q tile; this thread's share of Re<G'_m, S_m>
+            regs_store_bf<false>(sQr, sr[0]);
+            regs_store_bf<false>(sQi, sr[1]);
+            float part = 0.f;
 #pragma unroll
-                for (int pl = 0; pl < 2; ++pl)
+            for (int pl = 0; pl < 2; ++pl)
 #pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        const uint4 x = gr[pl].v[i], y = sr[pl].v[i];
-                        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.x),
-                                                               __builtin_bit_cast(bf16x2, y.x), part, false);
-                        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.y),
-                                                               __builtin_bit_cast(bf16x2, y.y), part, false);
-                        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.z),
-                                                               __builtin_bit_cast(bf16x2, y.z), part, false);
-                        part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.w),
-                                                               __builtin_bit_cast(bf16x2, y.w), part, false);
-                    }
+                for (int i = 0; i < 2; ++i) {
+                    const uint4 x = gr[pl].v[i], y = sr[pl].v[i];
+                    part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.x),
+                                                           __builtin_bit_cast(bf16x2, y.x), part, false);
+                    part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.y),
+                                                           __builtin_bit_cast(bf16x2, y.y), part, false);
+                    part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.z),
+                                                           __builtin_bit_cast(bf16x2, y.z), part, false);
+                    part = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x.w),
+                                                           __builtin_bit_cast(bf16x2, y.w), part, false);
+                }
 #pragma unroll
-                for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
-                if (lane == 0) sRed[w] = part;
-            }
+            for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+            if (lane == 0) sRed[w] = part;
         }
+        __syncthreads();
+        if (carry) {
+#pragma unroll
+            for (int kp = 0; kp < 2; ++kp) {
+                const int k0 = 32 * kp + 8 * g;
+                bg[kp][0] = ld8(sGr + t * PB + k0);
+                bg[kp][1] = ld8(sGi + t * PB + k0);
+            }
+                // X^T[j][t] = sum_k conj(S_m[k][j]) dY[t][k], two column tiles jt at a time;
+                // dQ~ += conj(rho_m[t]) X (rho_m = P_m); d rho_m[t] = sum_j q~[t][j] conj(X[t][j])
+                const float rhr = sPr[m * 64 + t], rhi = sPi[m * 64 + t];
+                float pr = 0.f, pi = 0.f;
+    #pragma unroll
+                for (int jh = 0; jh < 2; ++jh) {
+                    floatx4 xr[2], xi[2];
+    #pragma unroll
+                    for (int jj = 0; jj < 2; ++jj) xr[jj] = xi[jj] = zero4();
+    #pragma unroll
+                    for (int kp = 0; kp < 2; ++kp) {
+                        const int k0 = 32 * kp + 8 * g;
+                        const bf16x8 ngr = neg_bf(bg[kp][0]);
+    #pragma unroll
+                        for (int jj = 0; jj < 2; ++jj) {
+                            const int jt = 2 * jh + jj;
+                            const bf16x8 sr = ld_tr(sQr, k0, k0 + 4, 16 * jt), si = ld_tr(sQi, k0, k0 + 4, 16 * jt);
+                            xr[jj] = mfma_bf(sr, bg[kp][0], xr[jj]);
+                            xr[jj] = mfma_bf(si, bg[kp][1], xr[jj]);
+                            xi[jj] = mfma_bf(sr, bg[kp][1], xi[jj]);
+                            xi[jj] = mfma_bf(si, ngr, xi[jj]);
+                        }
+                    }
+    #pragma unroll
+                    for (int jj = 0; jj < 2; ++jj)
+    #pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int jt = 2 * jh + jj;
+                            const float x_r = xr[jj][r], x_i = xi[jj][r];
+                            gqR[jt][r] += rhr * x_r + rhi * x_i;
+                            gqI[jt][r] += rhr * x_i - rhi * x_r;
+                            const float qr = quad_elem(qq[jt][0], r), qi = quad_elem(qq[jt][1], r);
+                            pr += qr * x_r + qi * x_i;
+                            pi += qr * x_i - qi * x_r;
+                        }
+                }
+                pr += __shfl_xor(pr, 16);
+                pr += __shfl_xor(pr, 32);
+                pi += __shfl_xor(pi, 16);
+                pi += __shfl_xor(pi, 32);
+                if (g == 0) {
+                    const float cum = __expf(sL[m * 64 + t]) * qs;
+                    sDqr[m * 64 + t] += pr * cum;
+                    sDqi[m * 64 + t] += pi * cum;
+                    sGq[m * 64 + t] += (pr * sRr[m * 64 + t] + pi * sRi[m * 64 + t]) * cum;
+                }
+
+        }
+        __syncthreads();  // S_m is no longer read: G'_m natural into the q tile
+        regs_store_bf<false>(sQr, gr[0]);
+        regs_store_bf<false>(sQi, gr[1]);
         if (m + 1 < M) load_state(m + 1);
         __syncthreads();
-        const float dls = sDl[m * 64 + s];
+        const float dls = sv ? __expf(fminf(sL[m * 64 + valid - 1] - sL[m * 64 + s], 0.f)) : 0.f;
         floatx4 zr[4], zi[4];
 #pragma unroll
         for (int it = 0; it < 4; ++it) zr[it] = zi[it] = zero4();
@@ -1755,6 +1661,22 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
     }
     __syncthreads();
 
+    if (tv) {
+        const int64_t o = b * p.dq.s0 + h * p.dq.s1 + (int64_t)(c0 + t) * p.dq.s2;
+        U16 *dre = (U16 *)p.dq.re + o, *dim = (U16 *)p.dq.im + o;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            store_quad(dre, jt, gqR[jt], qs);
+            store_quad(dim, jt, gqI[jt], qs);
+        }
+        if (g == 0 && p.drot_re) {
+            for (int m = 0; m < M; ++m) {
+                const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c0 + t) * a.sr_t;
+                p.drot_re[ro] = sDqr[m * 64 + t];
+                p.drot_im[ro] = sDqi[m * 64 + t];
+            }
+        }
+    }
     if (sv) {
         const int64_t ok_ = b * p.dk.s0 + h * p.dk.s1 + (int64_t)(c0 + s) * p.dk.s2;
         const int64_t ov_ = b * p.dv.s0 + h * p.dv.s1 + (int64_t)(c0 + s) * p.dv.s2;
@@ -1768,9 +1690,9 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
             store_quad(vim, it, gvI[it], 1.f);
         }
     }
-    if (w == 0) {
+    if (w == 0) {  // row part + column part + state terms -> reverse cumsum -> d gamma
         for (int m = 0; m < M; ++m) {
-            float x = (lane < valid) ? sGL[m * 64 + lane] : 0.f;
+            float x = (lane < valid) ? sGL[m * 64 + lane] + sGq[m * 64 + lane] : 0.f;
 #pragma unroll
             for (int off = 1; off < 64; off <<= 1) {
                 const float y = __shfl_down(x, off);
@@ -1784,52 +1706,36 @@ __global__ void __launch_bounds__(THREADS, 2) key_side_bf16_kernel(BwdParams p) 
     }
 }
 
-// query side: 4 bf16 planes + 9 per-step vectors; key side: 8 planes + 8
-// vectors (two blocks share a CU's 160 KiB LDS)
+// 8 bf16 planes + 10 per-step vectors: two blocks share a CU's 160 KiB LDS up to M = 3
 template <int M>
-constexpr size_t qside_bf16_smem() { return (size_t)4 * PLANE_B * 2 + (9 * M * 64 + 4) * sizeof(float); }
-template <int M>
-constexpr size_t kside_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (8 * M * 64 + 8) * sizeof(float); }
-static_assert(2 * qside_bf16_smem<MAX_M>() <= 160 * 1024 && 2 * kside_bf16_smem<3>() <= 160 * 1024, "LDS budget");
+constexpr size_t chunk_grad_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (10 * M * 64 + 8) * sizeof(float); }
+static_assert(2 * chunk_grad_bf16_smem<3>() <= 160 * 1024, "LDS budget");
 
 template <int M>
 int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;
     dim3 grid(p.n_chunks, a.H, a.B);
-    const size_t s1 = gpass_bf16_smem(), s3 = qside_bf16_smem<M>(), s4 = kside_bf16_smem<M>();
+    const size_t s1 = gpass_bf16_smem(), s3 = chunk_grad_bf16_smem<M>();
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel<false>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
     QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel<true>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
-    const void *qk = p.dy_bf16 ? (const void *)query_side_bf16_kernel<M, true>
-                               : (const void *)query_side_bf16_kernel<M, false>;
-    const void *kk = p.dy_bf16 ? (const void *)key_side_bf16_kernel<M, true> : (const void *)key_side_bf16_kernel<M, false>;
-    QPAM_CHECK_HIP(hipFuncSetAttribute(qk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
-    QPAM_CHECK_HIP(hipFuncSetAttribute(kk, hipFuncAttributeMaxDynamicSharedMemorySize, (int)s4));
-    // the gradient-state pass (sequential chains, latency-bound) and the query side
-    // (reads only forward snapshots) are independent: run them concurrently, the
-    // chains launched first (measured faster than either the reverse order or one
-    // stream); the key side needs both
-    int st = fork_join(
-        stream,
-        [&](hipStream_t s) {
-            const dim3 pg(PASS_SPLIT * a.M * a.B * a.H);
-            if (p.dy_bf16) hipLaunchKernelGGL(grad_pass_bf16_kernel<true>, pg, dim3(PASS_THREADS), s1, s, p);
-            else hipLaunchKernelGGL(grad_pass_bf16_kernel<false>, pg, dim3(PASS_THREADS), s1, s, p);
-            return launch_status("grad_pass_bf16_kernel");
-        },
-        [&](hipStream_t s) {
-            if (p.dy_bf16) hipLaunchKernelGGL((query_side_bf16_kernel<M, true>), grid, dim3(THREADS), s3, s, p);
-            else hipLaunchKernelGGL((query_side_bf16_kernel<M, false>), grid, dim3(THREADS), s3, s, p);
-            return launch_status("query_side_bf16_kernel");
-        });
+    const void *ck = p.dy_bf16 ? (const void *)chunk_grad_bf16_kernel<M, true>
+                               : (const void *)chunk_grad_bf16_kernel<M, false>;
+    QPAM_CHECK_HIP(hipFuncSetAttribute(ck, hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
+    // the gradient-state pass (sequential chains) writes dS after every chunk;
+    // the chunk pass then forms every gradient of the chunk
+    const dim3 pg(PASS_SPLIT * a.M * a.B * a.H);
+    if (p.dy_bf16) hipLaunchKernelGGL(grad_pass_bf16_kernel<true>, pg, dim3(PASS_THREADS), s1, stream, p);
+    else hipLaunchKernelGGL(grad_pass_bf16_kernel<false>, pg, dim3(PASS_THREADS), s1, stream, p);
+    int st = launch_status("grad_pass_bf16_kernel");
     if (st) return st;
-    if (p.dy_bf16) hipLaunchKernelGGL((key_side_bf16_kernel<M, true>), grid, dim3(THREADS), s4, stream, p);
-    else hipLaunchKernelGGL((key_side_bf16_kernel<M, false>), grid, dim3(THREADS), s4, stream, p);
-    return launch_status("key_side_bf16_kernel");
+    if (p.dy_bf16) hipLaunchKernelGGL((chunk_grad_bf16_kernel<M, true>), grid, dim3(THREADS), s3, stream, p);
+    else hipLaunchKernelGGL((chunk_grad_bf16_kernel<M, false>), grid, dim3(THREADS), s3, stream, p);
+    return launch_status("chunk_grad_bf16_kernel");
 }
 
-// The state count is a compile-time constant of the query/key-side kernels.
+// The state count is a compile-time constant of the chunk-gradient kernel.
 int launch_bwd_bf16(const BwdParams &p, hipStream_t stream) {
     switch (p.a.M) {
         case 1: return launch_bwd_bf16_m<1>(p, stream);

@@ -850,9 +850,11 @@ using U16 = unsigned short;
 // staged already weighted (fp32 product rounded once to bf16), so the MFMA
 // operands come straight from LDS.  Rows past the end of the sequence re-read its
 // last row: their weights are zero.
+constexpr int GSNAP_ROWS = 64 / PASS_SPLIT;  // dS rows of one block
 constexpr size_t gpass_bf16_smem() {
-    return (size_t)2 * PLANE_B * 2     // Q [plane][64][PB]
-           + (size_t)2 * PLANE_B * 2;  // weighted dY (bf16) [plane][64][PB] (this block's columns)
+    return (size_t)2 * PLANE_B * 2                 // Q [plane][64][PB]
+           + (size_t)2 * PLANE_B * 2               // weighted dY (bf16) [plane][64][PB] (this block's columns)
+           + (size_t)2 * GSNAP_ROWS * PB * 2;      // bf16 snapshot of the block's dS rows [plane][32][PB]
 }
 
 template <bool DYBF>
@@ -862,6 +864,7 @@ grad_pass_bf16_kernel(BwdParams p) {
     extern __shared__ float smem[];
     U16 *sQ = reinterpret_cast<U16 *>(smem);  // + plane * PLANE_B
     U16 *sG = sQ + 2 * PLANE_B;               // + plane * PLANE_B
+    U16 *sS = sG + 2 * PLANE_B;               // + plane * GSNAP_ROWS * PB
 
     const qpam_scan_args &a = p.a;
     // the halves of a chain are n_chains blocks apart (same XCD when 8 | B H)
@@ -902,9 +905,10 @@ grad_pass_bf16_kernel(BwdParams p) {
 
     struct ChunkRegs {
         BfTileRegs<NT> qr, qi;
-        float gam, rr, ri;
+        float gam, rr, ri, tot;
     };
     ChunkRegs cr0, cr1;
+    float tot_cur = 1.f;  // total decay of the chunk staged last (the one the next step processes)
     // this block's dY columns of the next chunk (one set)
     typename std::conditional<DYBF, BfTileRegs<NT, 32>, F32TileRegs<NT, 32>>::type yr, yi;
     auto load_dy = [&](int c) {
@@ -927,6 +931,10 @@ grad_pass_bf16_kernel(BwdParams p) {
         x.gam = gbase[t * a.sg_t];
         x.rr = rsrc_r[t * rst_r];
         x.ri = rsrc_i[t * rst_i];
+        // a vector load (lane-dependent address; lane 0's value is taken when the
+        // chunk is staged): a scalar load would share the LDS counter, and the next
+        // LDS wait would wait for it too
+        x.tot = p.totals[chain_idx(p, m, b, h) * p.n_chunks + max(c - (lane & 1), 0)];
     };
     auto stage_chunk = [&](int c, const ChunkRegs &x) {
         // nothing of the staging moves above this point: its first use of the staged
@@ -936,6 +944,7 @@ grad_pass_bf16_kernel(BwdParams p) {
         __builtin_amdgcn_sched_barrier(0);
         // conj(rho[t]) q_scale = conj(r[t]) cum[t] q_scale, lane t
         const int valid = min(64, a.T - c * 64);
+        tot_cur = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x.tot)));
         float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -964,12 +973,11 @@ grad_pass_bf16_kernel(BwdParams p) {
         // counter completes in order, so Q behind it stays in flight
         load_dy(max(c - 1, 0));
         load_chunk(max(c - 2, 0), mine);
-        {  // bf16 snapshot of dS after chunk c
-            U16 *dst = gsnap(p, m, b, h, c);
+        // bf16 snapshot of dS after chunk c: into LDS now, to global memory as
+        // 16-byte row pieces after the next barrier
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-                acc_store_bf_pairs(dst, dst + D * D, gR[jj], gI[jj], 16 * it, 16 * (2 * jh + jj));
-        }
+        for (int jj = 0; jj < 2; ++jj)
+            acc_store_bf_pairs<PB>(sS, sS + GSNAP_ROWS * PB, gR[jj], gI[jj], 16 * (w & 1), 16 * (2 * jh + jj));
         if (c > 0 || need_ds0) {
             // dG rows (value i) x cols (key j): A = (conj(rho) q_scale dY)^T, B = Q (k = t)
             floatx4 accR[2], accI[2];
@@ -992,7 +1000,7 @@ grad_pass_bf16_kernel(BwdParams p) {
                     accI[jj] = mfma_bf(nar, qi, accI[jj]);
                 }
             }
-            const float tot = ftotal(p, m, b, h, c);
+            const float tot = tot_cur;  // chunk c's total, loaded two steps ahead
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
@@ -1004,6 +1012,15 @@ grad_pass_bf16_kernel(BwdParams p) {
         // also unconditional: past the end, chunk 0 (which `next` and the dY registers
         // then hold) is staged again
         __syncthreads();
+        {  // the snapshot rows: 32 bytes per thread
+            const int pl = tid >> 7, row = (tid & 127) >> 2, q = tid & 3;
+            const uint4 *src = reinterpret_cast<const uint4 *>(sS + pl * GSNAP_ROWS * PB + row * PB + 16 * q);
+            const uint4 v0 = src[0], v1 = src[1];
+            uint4 *dst = reinterpret_cast<uint4 *>(gsnap(p, m, b, h, c) + pl * D * D + (GSNAP_ROWS * half + row) * D +
+                                                   16 * q);
+            dst[0] = v0;
+            dst[1] = v1;
+        }
         stage_chunk(max(c - 1, 0), next);
         __syncthreads();
     };

@@ -1048,18 +1048,27 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_output_kernel(FwdParams p) {
             }
         }
     };
-    // carried state S_m of this wave's tiles (fp32) -> bf16 LDS copy and the snapshot of chunk c
+    // carried state S_m of this wave's tiles (fp32) -> bf16 LDS copy
     floatx4 sR[M][2], sI[M][2];
     auto publish_state = [&](int c) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            U *snap = chunk_snap_ptr(p, m, b, h, c);
+        for (int m = 0; m < M; ++m)
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
+            for (int jj = 0; jj < 2; ++jj)
                 acc_store_bf_pairs<PB>(sS + 2 * m * PLANE_B, sS + (2 * m + 1) * PLANE_B, sR[m][jj], sI[m][jj], 16 * iu,
                                        16 * (2 * jh + jj));
-                acc_store_bf_pairs(snap, snap + D * D, sR[m][jj], sI[m][jj], 16 * iu, 16 * (2 * jh + jj));
-            }
+    };
+    // the published copy -> the backward's snapshot of chunk c, as 16-byte row
+    // pieces (32 bytes per thread and state), after the barrier that follows it
+    auto copy_snapshot = [&](int c) {
+        const int pl = tid >> 8, row = (tid & 255) >> 2, q = tid & 3;
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const uint4 *src = reinterpret_cast<const uint4 *>(sS + (2 * m + pl) * PLANE_B + row * PB + 16 * q);
+            const uint4 v0 = src[0], v1 = src[1];
+            uint4 *dst = reinterpret_cast<uint4 *>(chunk_snap_ptr(p, m, b, h, c) + pl * D * D + row * D + 16 * q);
+            dst[0] = v0;
+            dst[1] = v1;
         }
     };
 
@@ -1080,6 +1089,7 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_output_kernel(FwdParams p) {
     publish_state(c_begin);
     stage_chunk(c_begin, cr);
     __syncthreads();
+    copy_snapshot(c_begin);
 
     for (int c = c_begin; c < c_end; ++c) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
@@ -1290,6 +1300,7 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_output_kernel(FwdParams p) {
         publish_state(c + 1);
         stage_chunk(c + 1, cr);
         __syncthreads();
+        copy_snapshot(c + 1);
     }
 }
 

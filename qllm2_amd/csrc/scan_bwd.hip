@@ -1707,18 +1707,17 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
             store_quad(vim, it, gvI[it], 1.f);
         }
     }
-    if (w == 0) {  // row part + column part + state terms -> reverse cumsum -> d gamma
-        for (int m = 0; m < M; ++m) {
-            float x = (lane < valid) ? sGL[m * 64 + lane] + sGq[m * 64 + lane] : 0.f;
+    if (w < M) {  // state w: row part + column part + state terms -> reverse cumsum -> d gamma
+        const int m = w;
+        float x = (lane < valid) ? sGL[m * 64 + lane] + sGq[m * 64 + lane] : 0.f;
 #pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_down(x, off);
-                if (lane + off < 64) x += y;
-            }
-            if (lane < valid) {
-                const int64_t go = m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)(c0 + lane) * a.sg_t;
-                p.dgamma[go] = x / (a.gamma[go] + LOG_EPS);
-            }
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_down(x, off);
+            if (lane + off < 64) x += y;
+        }
+        if (lane < valid) {
+            const int64_t go = m * a.sg_m + b * a.sg_b + h * a.sg_h + (int64_t)(c0 + lane) * a.sg_t;
+            p.dgamma[go] = x / (din.gam + LOG_EPS);  // din: gamma of state w, loaded at entry
         }
     }
 }

@@ -879,7 +879,7 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_state_kernel(FwdParams p) {
         stage_chunk(cr);
         __syncthreads();
         if (c + 1 < c_end) load_chunk(c + 1, cr);
-        // dS_m[i][j] += sum_s (w_m V)[s,i] conj(K[s,j]): A = weighted V^T, B = K (k = s)
+        // dS_m[i][j] += sum_s (w_m V)[s,i] conj(K[s,j]), accumulated transposed (A = K, B = weighted V; k = s)
 #pragma unroll
         for (int kp = 0; kp < 2; ++kp) {
             const int s0 = 32 * kp + 8 * g;
@@ -895,11 +895,11 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_state_kernel(FwdParams p) {
                 const bf16x8 ai = ld_tr(sV + (2 * m + 1) * PLANE_B, s0, s0 + 4, 16 * it);
                 const bf16x8 nar = neg_bf(ar);
 #pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    accR[m][jj] = mfma_bf(ar, kr[jj], accR[m][jj]);
-                    accR[m][jj] = mfma_bf(ai, ki[jj], accR[m][jj]);
-                    accI[m][jj] = mfma_bf(ai, kr[jj], accI[m][jj]);
-                    accI[m][jj] = mfma_bf(nar, ki[jj], accI[m][jj]);
+                for (int jj = 0; jj < 2; ++jj) {  // transposed: lane holds row i = 16 it + l16, columns 4g + r
+                    accR[m][jj] = mfma_bf(kr[jj], ar, accR[m][jj]);
+                    accR[m][jj] = mfma_bf(ki[jj], ai, accR[m][jj]);
+                    accI[m][jj] = mfma_bf(kr[jj], ai, accI[m][jj]);
+                    accI[m][jj] = mfma_bf(ki[jj], nar, accI[m][jj]);
                 }
             }
         }
@@ -908,13 +908,11 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_state_kernel(FwdParams p) {
     for (int m = 0; m < M; ++m) {
         float *dst = p.segs + (seg_chain(a, m, b, h) * p.n_segs + sg) * (2 * D * D);
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int o = (16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                dst[o] = accR[m][jj][r];
-                dst[D * D + o] = accI[m][jj][r];
-            }
+        for (int jj = 0; jj < 2; ++jj) {
+            const int o = (16 * it + l16) * D + 16 * (2 * jh + jj) + 4 * g;
+            *reinterpret_cast<floatx4 *>(dst + o) = accR[m][jj];
+            *reinterpret_cast<floatx4 *>(dst + D * D + o) = accI[m][jj];
+        }
     }
 }
 

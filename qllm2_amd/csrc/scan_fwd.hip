@@ -1046,15 +1046,20 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_output_kernel(FwdParams p) {
             }
         }
     };
-    // carried state S_m of this wave's tiles (fp32) -> bf16 LDS copy
+    // carried state S_m of this wave's tiles (fp32, accumulated transposed: lane holds
+    // row i = 16 iu + l16, columns 16 (2 jh + jj) + 4 g .. +3) -> bf16 LDS copy
     floatx4 sR[M][2], sI[M][2];
     auto publish_state = [&](int c) {
 #pragma unroll
         for (int m = 0; m < M; ++m)
 #pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
-                acc_store_bf_pairs<PB>(sS + 2 * m * PLANE_B, sS + (2 * m + 1) * PLANE_B, sR[m][jj], sI[m][jj], 16 * iu,
-                                       16 * (2 * jh + jj));
+            for (int jj = 0; jj < 2; ++jj) {
+                const int o = (16 * iu + l16) * PB + 16 * (2 * jh + jj) + 4 * g;
+                *reinterpret_cast<uint2 *>(sS + 2 * m * PLANE_B + o) =
+                    make_uint2(pack_bf16x2(sR[m][jj][0], sR[m][jj][1]), pack_bf16x2(sR[m][jj][2], sR[m][jj][3]));
+                *reinterpret_cast<uint2 *>(sS + (2 * m + 1) * PLANE_B + o) =
+                    make_uint2(pack_bf16x2(sI[m][jj][0], sI[m][jj][1]), pack_bf16x2(sI[m][jj][2], sI[m][jj][3]));
+            }
     };
     // the published copy -> the backward's snapshot of chunk c, as 16-byte row
     // pieces (32 bytes per thread and state), after the barrier that follows it
@@ -1076,13 +1081,11 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_output_kernel(FwdParams p) {
     for (int m = 0; m < M; ++m) {
         const float *src = p.segs + (seg_chain(a, m, b, h) * p.n_segs + sg) * (2 * D * D);
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int o = (16 * iu + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                sR[m][jj][r] = src[o];
-                sI[m][jj][r] = src[D * D + o];
-            }
+        for (int jj = 0; jj < 2; ++jj) {
+            const int o = (16 * iu + l16) * D + 16 * (2 * jh + jj) + 4 * g;
+            sR[m][jj] = *reinterpret_cast<const floatx4 *>(src + o);
+            sI[m][jj] = *reinterpret_cast<const floatx4 *>(src + D * D + o);
+        }
     }
     publish_state(c_begin);
     stage_chunk(c_begin, cr);
@@ -1285,11 +1288,11 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_output_kernel(FwdParams p) {
                     const floatx8 dl = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
                     const bf16x8 ar = to_bf(vr * dl), ai = to_bf(vi * dl), nar = neg_bf(ar);
 #pragma unroll
-                    for (int jj = 0; jj < 2; ++jj) {
-                        sR[m][jj] = mfma_bf(ar, kr[jj], sR[m][jj]);
-                        sR[m][jj] = mfma_bf(ai, ki[jj], sR[m][jj]);
-                        sI[m][jj] = mfma_bf(ai, kr[jj], sI[m][jj]);
-                        sI[m][jj] = mfma_bf(nar, ki[jj], sI[m][jj]);
+                    for (int jj = 0; jj < 2; ++jj) {  // transposed (A = K, B = weighted V)
+                        sR[m][jj] = mfma_bf(kr[jj], ar, sR[m][jj]);
+                        sR[m][jj] = mfma_bf(ki[jj], ai, sR[m][jj]);
+                        sI[m][jj] = mfma_bf(kr[jj], ai, sI[m][jj]);
+                        sI[m][jj] = mfma_bf(ki[jj], nar, sI[m][jj]);
                     }
                 }
             }

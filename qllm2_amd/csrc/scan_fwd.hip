@@ -1188,13 +1188,13 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_output_kernel(FwdParams p) {
                 const bf16x8 ai = frag_from_acc(wi[2 * kp], wi[2 * kp + 1]);
                 const bf16x8 nai = neg_bf(ai);
 #pragma unroll
-                for (int ii = 0; ii < 2; ++ii) {
+                for (int ii = 0; ii < 2; ++ii) {  // Y accumulates transposed: lane holds row t, columns 4g + r
                     const int it = 2 * ih + ii, r0 = 32 * kp + 4 * g;
                     const bf16x8 vr = ld_tr(sVr, r0, r0 + 16, 16 * it), vi = ld_tr(sVi, r0, r0 + 16, 16 * it);
-                    yR[ii] = mfma_bf(ar, vr, yR[ii]);
-                    yR[ii] = mfma_bf(nai, vi, yR[ii]);
-                    yI[ii] = mfma_bf(ar, vi, yI[ii]);
-                    yI[ii] = mfma_bf(ai, vr, yI[ii]);
+                    yR[ii] = mfma_bf(vr, ar, yR[ii]);
+                    yR[ii] = mfma_bf(vi, nai, yR[ii]);
+                    yI[ii] = mfma_bf(vi, ar, yI[ii]);
+                    yI[ii] = mfma_bf(vr, ai, yI[ii]);
                 }
             }
         }
@@ -1220,42 +1220,35 @@ __global__ void __launch_bounds__(SEG_THREADS) seg_output_kernel(FwdParams p) {
                     for (int ii = 0; ii < 2; ++ii) {
                         const int row = (16 * (2 * ih + ii) + l16) * PB + 32 * kp + 8 * g;
                         const bf16x8 sr = ld8(Sr + row), si = ld8(Si + row);
-                        uR[ii] = mfma_bf(aqr[kp], sr, uR[ii]);
-                        uR[ii] = mfma_bf(naqi[kp], si, uR[ii]);
-                        uI[ii] = mfma_bf(aqr[kp], si, uI[ii]);
-                        uI[ii] = mfma_bf(aqi[kp], sr, uI[ii]);
+                        uR[ii] = mfma_bf(sr, aqr[kp], uR[ii]);
+                        uR[ii] = mfma_bf(si, naqi[kp], uR[ii]);
+                        uI[ii] = mfma_bf(si, aqr[kp], uI[ii]);
+                        uI[ii] = mfma_bf(sr, aqi[kp], uI[ii]);
                     }
                 }
-                const float4 pr4 = *reinterpret_cast<const float4 *>(sPr + m * 64 + 16 * tt + 4 * g);
-                const float4 pi4 = *reinterpret_cast<const float4 *>(sPi + m * 64 + 16 * tt + 4 * g);
-                const float prv[4] = {pr4.x, pr4.y, pr4.z, pr4.w}, piv[4] = {pi4.x, pi4.y, pi4.z, pi4.w};
+                const float prv = sPr[m * 64 + t], piv = sPi[m * 64 + t];  // rho_m q_scale of row t
 #pragma unroll
-                for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        yR[ii][r] += prv[r] * uR[ii][r] - piv[r] * uI[ii][r];
-                        yI[ii][r] += prv[r] * uI[ii][r] + piv[r] * uR[ii][r];
-                    }
+                for (int ii = 0; ii < 2; ++ii) {
+                    yR[ii] += prv * uR[ii] - piv * uI[ii];
+                    yI[ii] += prv * uI[ii] + piv * uR[ii];
+                }
             }
         }
-        {
-            const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)c0 * a.y.s2;
+        if (t < valid) {  // row t, columns 16 (2 ih + ii) + 4 g .. +3: 16-byte (fp32) or 8-byte (bf16) runs
+            const int64_t yo = b * a.y.s0 + h * a.y.s1 + (int64_t)(c0 + t) * a.y.s2;
 #pragma unroll
-            for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int tr = 16 * tt + 4 * g + r;
-                    if (tr < valid) {
-                        const int64_t o = yo + (int64_t)tr * a.y.s2 + 16 * (2 * ih + ii) + l16;
-                        if (a.y_dtype == QPAM_BF16) {
-                            reinterpret_cast<U *>(a.y.re)[o] = f32_to_bf16(yR[ii][r]);
-                            reinterpret_cast<U *>(a.y.im)[o] = f32_to_bf16(yI[ii][r]);
-                        } else {
-                            a.y.re[o] = yR[ii][r];
-                            a.y.im[o] = yI[ii][r];
-                        }
-                    }
+            for (int ii = 0; ii < 2; ++ii) {
+                const int64_t o = yo + 16 * (2 * ih + ii) + 4 * g;
+                if (a.y_dtype == QPAM_BF16) {
+                    *reinterpret_cast<uint2 *>(reinterpret_cast<U *>(a.y.re) + o) =
+                        make_uint2(pack_bf16x2(yR[ii][0], yR[ii][1]), pack_bf16x2(yR[ii][2], yR[ii][3]));
+                    *reinterpret_cast<uint2 *>(reinterpret_cast<U *>(a.y.im) + o) =
+                        make_uint2(pack_bf16x2(yI[ii][0], yI[ii][1]), pack_bf16x2(yI[ii][2], yI[ii][3]));
+                } else {
+                    *reinterpret_cast<floatx4 *>(a.y.re + o) = yR[ii];
+                    *reinterpret_cast<floatx4 *>(a.y.im + o) = yI[ii];
                 }
+            }
         }
         if (!more) break;
         load_chunk(c + 1, cr);
@@ -1465,6 +1458,13 @@ int validate_scan(const qpam_scan_args *a, const char *who, bool fwd_outputs) {
                  "%s: y_dtype %d (bf16 y needs bf16 inputs and chunk 64)", who, a->y_dtype);
     const uintptr_t al = (uintptr_t)a->s0_re | (uintptr_t)a->s0_im | (uintptr_t)a->s_re | (uintptr_t)a->s_im;
     QPAM_REQUIRE(al % 16 == 0, "%s: state buffers must be 16-byte aligned", who);
+    if (fwd_outputs && uses_snapshots(*a)) {  // Y rows leave in 16-byte (fp32) / 8-byte (bf16) runs
+        const uintptr_t ya = (uintptr_t)a->y.re | (uintptr_t)a->y.im;
+        QPAM_REQUIRE(ya % (a->y_dtype == QPAM_BF16 ? 8 : 16) == 0 && a->y.s0 % 4 == 0 && a->y.s1 % 4 == 0 &&
+                         a->y.s2 % 4 == 0,
+                     "%s: y planes must be %d-byte aligned with strides multiple of 4", who,
+                     a->y_dtype == QPAM_BF16 ? 8 : 16);
+    }
     QPAM_REQUIRE(a->workspace != nullptr && a->workspace_bytes >= fwd_workspace_bytes(*a) &&
                      ((uintptr_t)a->workspace % 16) == 0,
                  "%s: workspace needs %zu bytes (got %zu)", who, fwd_workspace_bytes(*a), a->workspace_bytes);

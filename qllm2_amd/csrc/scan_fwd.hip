@@ -395,8 +395,9 @@ __global__ void __launch_bounds__(THREADS) chunk_output_f32_kernel(FwdParams p) 
 // value rows [16 rb, 16 rb + 16) (rows of the recurrence are independent); of
 // its 8 waves, wave (half, w) owns key columns [16 w, 16 w + 16) and half of
 // the chunk's tokens, so the first-half wave keeps a 4 x 1 piece of S per
-// plane.  Per chunk: store the entering state (the output kernel and the
-// backward read it), form both halves' products for dS = sum_s D[C-1,s] v_s
+// plane.  Per chunk: store the entering state (accumulated transposed, a lane
+// holds one row and four consecutive columns, so it leaves in 16-byte stores;
+// the output kernel and the backward read it), form both halves' products for dS = sum_s D[C-1,s] v_s
 // conj(k_s) on MFMA (operands straight from global memory in MFMA layout, the
 // next two chunks' loads in flight), add the second half's through LDS,
 // S <- total S + dS.  The pass is a dependency chain over the chunks, so its
@@ -497,7 +498,9 @@ __device__ __forceinline__ void state_pass_f32_body(const FwdParams &p) {
     const int b = bh / a.H, h = bh % a.H;
     const int n = p.n_chunks;
     const int i0 = 32 * rb;                                  // the block's value rows
-    const int ri = i0 + 16 * rt + 4 * g, j = 16 * w + l16;   // this lane's S rows ri + r, column j
+    // S accumulates transposed: this lane holds row ri, columns j0 .. j0 + 3; its MFMA
+    // operands are K column j and V column 16 rt + l16
+    const int ri = i0 + 16 * rt + l16, j0 = 16 * w + 4 * g, j = 16 * w + l16;
     const float *kre = (const float *)a.k.re + b * a.k.s0 + h * a.k.s1;
     const float *kim = (const float *)a.k.im + b * a.k.s0 + h * a.k.s1;
     const float *vre = (const float *)a.v.re + b * a.v.s0 + h * a.v.s1;
@@ -505,12 +508,11 @@ __device__ __forceinline__ void state_pass_f32_body(const FwdParams &p) {
     const float *drow = p.dlast + (int64_t)chain * n * 64;   // this chain's decay weights
     const float *tot = p.totals + (int64_t)chain * n;
 
-    float sr[4], si[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int64_t o = (int64_t)chain * D * D + (ri + r) * D + j;
-        sr[r] = a.s0_re ? a.s0_re[o] : 0.f;
-        si[r] = a.s0_re ? a.s0_im[o] : 0.f;
+    floatx4 sr = zero4(), si = zero4();
+    if (a.s0_re) {
+        const int64_t o = (int64_t)chain * D * D + ri * D + j0;
+        sr = *reinterpret_cast<const floatx4 *>(a.s0_re + o);
+        si = *reinterpret_cast<const floatx4 *>(a.s0_im + o);
     }
     pass32_dma(st0, a, kre, kim, vre, vim, drow, tot, 0, i0, wv, lane);
     pass32_dma(st1, a, kre, kim, vre, vim, drow, tot, min(1, n - 1), i0, wv, lane);
@@ -524,10 +526,8 @@ __device__ __forceinline__ void state_pass_f32_body(const FwdParams &p) {
     {                                                                                                  \
         pass32_dma(NXT, a, kre, kim, vre, vim, drow, tot, min(c + 2, n - 1), i0, wv, lane);            \
         float *dst = chunk_state_ptr(p, m, b, h, c);                                                   \
-        _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                                \
-            dst[(ri + r) * D + j] = sr[r];                                                             \
-            dst[D * D + (ri + r) * D + j] = si[r];                                                     \
-        }                                                                                              \
+        *reinterpret_cast<floatx4 *>(dst + ri * D + j0) = sr;                                          \
+        *reinterpret_cast<floatx4 *>(dst + D * D + ri * D + j0) = si;                                  \
         __builtin_amdgcn_sched_barrier(0);                                                             \
         float d_[16], vr_[16], vi_[16], kr_[16], ki_[16];                                              \
         _Pragma("unroll") for (int ks = 0; ks < 16; ++ks) {                                            \
@@ -542,14 +542,12 @@ __device__ __forceinline__ void state_pass_f32_body(const FwdParams &p) {
         floatx4 u1 = zero4(), u2 = zero4(), u3 = zero4();                                              \
         _Pragma("unroll") for (int ks = 0; ks < 16; ++ks) {                                            \
             const float vr = vr_[ks] * d_[ks], vi = vi_[ks] * d_[ks];                                  \
-            u1 = mfma4(vr, kr_[ks], u1);                                                               \
-            u2 = mfma4(vi, ki_[ks], u2);                                                               \
-            u3 = mfma4(vr + vi, kr_[ks] - ki_[ks], u3);                                                \
+            u1 = mfma4(kr_[ks], vr, u1);                                                               \
+            u2 = mfma4(ki_[ks], vi, u2);                                                               \
+            u3 = mfma4(kr_[ks] - ki_[ks], vr + vi, u3);                                                \
         }                                                                                              \
-        _Pragma("unroll") for (int r = 0; r < 4; ++r) {                                                \
-            sr[r] = tc * sr[r] + (u1[r] + u2[r]);                                                      \
-            si[r] = tc * si[r] + (u3[r] - u1[r] + u2[r]);                                              \
-        }                                                                                              \
+        sr = tc * sr + (u1 + u2);                                                                      \
+        si = tc * si + (u3 - u1 + u2);                                                                 \
         __builtin_amdgcn_s_waitcnt(PASS32_WAIT);                                                       \
         __builtin_amdgcn_s_barrier();                                                                  \
         ++c;                                                                                           \
@@ -566,12 +564,9 @@ __device__ __forceinline__ void state_pass_f32_body(const FwdParams &p) {
     // drain the direct loads still in flight before the wave ends
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     if (a.s_re) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int64_t o = (int64_t)chain * D * D + (ri + r) * D + j;
-            a.s_re[o] = sr[r];
-            a.s_im[o] = si[r];
-        }
+        const int64_t o = (int64_t)chain * D * D + ri * D + j0;
+        *reinterpret_cast<floatx4 *>(a.s_re + o) = sr;
+        *reinterpret_cast<floatx4 *>(a.s_im + o) = si;
     }
 }
 

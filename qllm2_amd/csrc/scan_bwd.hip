@@ -20,6 +20,9 @@
 //      gradient of D and cum -> partial dL/dL_t in the workspace;
 //   4. key_side (chunk-parallel, wave = key tile): dK, dV, the decay_last and
 //      total gradients, and the final d gamma of the chunk.
+// bf16 inputs with 64-step chunks: grad_pass_bf16 (the sequential dS chain,
+// writing a bf16 snapshot of dS after every chunk), then chunk_grad_bf16 (the
+// query and key sides of a chunk in one block).
 #include <type_traits>
 
 #include "scan_common.h"

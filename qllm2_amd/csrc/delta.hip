@@ -9,228 +9,24 @@
 // v11/model.py:967-1002, is the same step with g~ = gamma).
 //
 // Forward: the chunked form on fp32 MFMA (delta_prep_kernel, chunk-parallel,
-// then delta_chunk_kernel along the chunks; described at the kernels), with
-// the state before every 16th token stored as the backward's checkpoints.
+// then delta_chunk_kernel along the chunks; described at the kernels).
 // The rows of S are independent under the recurrence (row i reads only k, q,
 // v_i, gamma, beta), so the chunk pass splits a chain's 64 value rows over four
 // blocks.
 //
-// Backward (token recurrence in registers): a lane owns 1 row x 4 columns of
-// S, and the per-row dot products S k and S q~ are DPP reductions over the 16
-// lanes of a row group.
-// Backward: four workgroups of 4 waves (16 rows each) per chain walk its
-// 16-token groups in reverse; each group is recomputed from its checkpoint
-// with the state before every 4th token kept in a scratch, then each 4-token
-// sub-group is recomputed into registers and differentiated in reverse.
-// Gradients of k, q, gamma and beta are sums over the 64 rows: lanes -> row
-// groups by shuffles, waves through LDS every 2 tokens, workgroups through
-// per-part partial sums that a second kernel adds in a fixed order
-// (deterministic).
+// Backward: the same chunked form differentiated, on fp32 MFMA in three
+// launches (described at the kernels): a reverse pass along the chunks for the
+// gradient of the state (rows of it are independent again: four blocks per
+// chain), then two chunk-parallel kernels for the score-matrix gradients and
+// for dq, dk, dgamma, dbeta.  The forward leaves what they need in its
+// workspace: the state entering every chunk, U, and the chunk's products in the
+// orders the backward reads them.
 #include "common.h"
 
 namespace qpam {
 namespace {
 
 constexpr int D = 64;
-constexpr int RPL = 1;               // rows per lane
-constexpr int NW = D / (4 * RPL);    // waves per chain (16)
-constexpr int GROUP = 16;            // tokens per forward checkpoint
-constexpr int SUB = 4;               // tokens per backward sub-group
-constexpr int SUBS = GROUP / SUB;
-constexpr int FL = 2;                // tokens per backward cross-wave reduction
-constexpr int PARTS = 4;             // backward workgroups per chain
-constexpr int PW = NW / PARTS;       // waves per backward workgroup
-constexpr int PROWS = 4 * RPL * PW;  // rows per backward workgroup
-constexpr int BWD_THREADS = 64 * PW;
-
-struct Lane {
-    int w, lane, rg, cg, r0;   // wave of the chain, lane, row group (0..3), column group (0..15), first row
-    __device__ Lane(int wave, int ln) {
-        w = wave, lane = ln;
-        rg = ln >> 4, cg = ln & 15;
-        r0 = (4 * w + rg) * RPL;
-    }
-    __device__ int slot() const { return w * 64 + lane; }   // thread-private state slot of the chain
-};
-
-// one token's inputs as this lane sees them
-struct Tok {
-    float kr[4], ki[4], qr[4], qi[4];  // the lane's 4 columns (q already scaled)
-    float vr[RPL], vi[RPL];            // the lane's rows
-    float g, b;                        // gamma + eps, beta
-};
-
-struct State {
-    float r[RPL][4], i[RPL][4];
-};
-
-// The inputs of NT consecutive tokens staged in LDS: the k and q planes of
-// every column (q scaled), v of the ROWS rows the workgroup owns, gamma + eps
-// and beta.  Global loads go to registers first (fetch) and to LDS later
-// (commit), so a span's loads overlap the previous span's arithmetic.
-template <int NT, int ROWS>
-struct Span {
-    floatx4 kq[NT][4][16];   // [token][k re, k im, q re, q im][column / 4]
-    float v[NT][2][ROWS];
-    float gb[NT][2];
-};
-
-template <int NT, int ROWS, int NTHR>
-struct SpanRegs {
-    static constexpr int KQ = NT * 64 / NTHR;                 // float4 per thread
-    static constexpr int VV = (NT * 2 * ROWS + NTHR - 1) / NTHR;
-    static_assert(KQ >= 1 && KQ * NTHR == NT * 64, "span shape");
-    floatx4 kq[KQ];
-    float v[VV];
-    float gb;
-
-    // rows past T re-read row T - 1 (their results are not stored)
-    __device__ __forceinline__ void fetch(const qpam_delta_args &a, int b, int h, int t0, int row0, int tid) {
-#pragma unroll
-        for (int k = 0; k < KQ; ++k) {
-            const int i = tid + k * NTHR, tok = i >> 6, pl = (i >> 4) & 3, c4 = i & 15;
-            const int t = min(t0 + tok, a.T - 1);
-            const qpam_cview &v = pl < 2 ? a.k : a.q;
-            const float *base = static_cast<const float *>((pl & 1) ? v.im : v.re);
-            kq[k] = *reinterpret_cast<const floatx4 *>(base + b * v.s0 + h * v.s1 + (int64_t)t * v.s2 + 4 * c4);
-            if (pl >= 2) kq[k] *= a.q_scale;
-        }
-#pragma unroll
-        for (int k = 0; k < VV; ++k) {
-            const int i = min(tid + k * NTHR, NT * 2 * ROWS - 1);
-            const int tok = i / (2 * ROWS), rem = i - tok * 2 * ROWS, ri = rem / ROWS, r = rem - ri * ROWS;
-            const int t = min(t0 + tok, a.T - 1);
-            const float *base = static_cast<const float *>(ri ? a.v.im : a.v.re);
-            v[k] = base[b * a.v.s0 + h * a.v.s1 + (int64_t)t * a.v.s2 + row0 + r];
-        }
-        const int i = min(tid, 2 * NT - 1), t = min(t0 + (i >> 1), a.T - 1);
-        const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)t * a.sg_t;
-        gb = (i & 1) ? a.beta[go] : a.gamma[go] + a.gamma_eps;
-    }
-
-    __device__ __forceinline__ void commit(Span<NT, ROWS> &sp, int tid) const {
-#pragma unroll
-        for (int k = 0; k < KQ; ++k) {
-            const int i = tid + k * NTHR;
-            sp.kq[i >> 6][(i >> 4) & 3][i & 15] = kq[k];
-        }
-#pragma unroll
-        for (int k = 0; k < VV; ++k) {
-            const int i = tid + k * NTHR;
-            if (i < NT * 2 * ROWS) {
-                const int tok = i / (2 * ROWS), rem = i - tok * 2 * ROWS, ri = rem / ROWS, r = rem - ri * ROWS;
-                sp.v[tok][ri][r] = v[k];
-            }
-        }
-        if (tid < 2 * NT) sp.gb[tid >> 1][tid & 1] = gb;
-    }
-};
-
-// token j of a span as this lane sees it; `row` = the lane's first row in the span's rows
-template <int NT, int ROWS>
-__device__ __forceinline__ Tok span_tok(const Span<NT, ROWS> &sp, int j, int cg, int row) {
-    Tok x;
-    const floatx4 kr = sp.kq[j][0][cg], ki = sp.kq[j][1][cg], qr = sp.kq[j][2][cg], qi = sp.kq[j][3][cg];
-    x.kr[0] = kr.x, x.kr[1] = kr.y, x.kr[2] = kr.z, x.kr[3] = kr.w;
-    x.ki[0] = ki.x, x.ki[1] = ki.y, x.ki[2] = ki.z, x.ki[3] = ki.w;
-    x.qr[0] = qr.x, x.qr[1] = qr.y, x.qr[2] = qr.z, x.qr[3] = qr.w;
-    x.qi[0] = qi.x, x.qi[1] = qi.y, x.qi[2] = qi.z, x.qi[3] = qi.w;
-#pragma unroll
-    for (int rr = 0; rr < RPL; ++rr) x.vr[rr] = sp.v[j][0][row + rr], x.vi[rr] = sp.v[j][1][row + rr];
-    x.g = sp.gb[j][0], x.b = sp.gb[j][1];
-    return x;
-}
-
-// One token: S <- g S + u (x) k*, u = b (v - g S k); returns y = S q~ for the
-// lane's 2 rows (complete in every lane of the row group).
-__device__ __forceinline__ void fwd_step(State &s, const Tok &x, float (&yr)[RPL], float (&yi)[RPL]) {
-    float pkr[RPL], pki[RPL], pqr[RPL], pqi[RPL];
-#pragma unroll
-    for (int rr = 0; rr < RPL; ++rr) {
-        float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const float sr = s.r[rr][c], si = s.i[rr][c];
-            a0 += sr * x.kr[c] - si * x.ki[c];
-            a1 += sr * x.ki[c] + si * x.kr[c];
-            b0 += sr * x.qr[c] - si * x.qi[c];
-            b1 += sr * x.qi[c] + si * x.qr[c];
-        }
-        pkr[rr] = row16_sum(a0), pki[rr] = row16_sum(a1), pqr[rr] = row16_sum(b0), pqi[rr] = row16_sum(b1);
-    }
-    // k^H q~ over all columns
-    float cr = 0.f, ci = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-        cr += x.kr[c] * x.qr[c] + x.ki[c] * x.qi[c];
-        ci += x.kr[c] * x.qi[c] - x.ki[c] * x.qr[c];
-    }
-    cr = row16_sum(cr), ci = row16_sum(ci);
-#pragma unroll
-    for (int rr = 0; rr < RPL; ++rr) {
-        const float ur = x.b * (x.vr[rr] - x.g * pkr[rr]), ui = x.b * (x.vi[rr] - x.g * pki[rr]);
-        yr[rr] = x.g * pqr[rr] + ur * cr - ui * ci;
-        yi[rr] = x.g * pqi[rr] + ur * ci + ui * cr;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            // u conj(k_c)
-            const float or_ = ur * x.kr[c] + ui * x.ki[c], oi = ui * x.kr[c] - ur * x.ki[c];
-            s.r[rr][c] = x.g * s.r[rr][c] + or_;
-            s.i[rr][c] = x.g * s.i[rr][c] + oi;
-        }
-    }
-}
-
-__device__ __forceinline__ int chain_groups(int T) { return (T + GROUP - 1) / GROUP; }
-
-// a thread's 8 RPL floats of state at [chain][checkpoint][slot], float4-coalesced
-__device__ __forceinline__ void store_state(float *base, const State &s, int slot) {
-    floatx4 *p = reinterpret_cast<floatx4 *>(base) + 2 * RPL * slot;
-#pragma unroll
-    for (int rr = 0; rr < RPL; ++rr) {
-        p[2 * rr] = floatx4{s.r[rr][0], s.r[rr][1], s.r[rr][2], s.r[rr][3]};
-        p[2 * rr + 1] = floatx4{s.i[rr][0], s.i[rr][1], s.i[rr][2], s.i[rr][3]};
-    }
-}
-__device__ __forceinline__ void load_state(const float *base, State &s, int slot) {
-    const floatx4 *p = reinterpret_cast<const floatx4 *>(base) + 2 * RPL * slot;
-#pragma unroll
-    for (int rr = 0; rr < RPL; ++rr) {
-        const floatx4 a = p[2 * rr], b = p[2 * rr + 1];
-        s.r[rr][0] = a.x, s.r[rr][1] = a.y, s.r[rr][2] = a.z, s.r[rr][3] = a.w;
-        s.i[rr][0] = b.x, s.i[rr][1] = b.y, s.i[rr][2] = b.z, s.i[rr][3] = b.w;
-    }
-}
-
-__device__ __forceinline__ void init_state(State &s, const float *re, const float *im, int64_t chain, const Lane &L) {
-#pragma unroll
-    for (int rr = 0; rr < RPL; ++rr) {
-        if (re) {
-            const int64_t o = chain * D * D + (L.r0 + rr) * D + 4 * L.cg;
-            const floatx4 a = *reinterpret_cast<const floatx4 *>(re + o), b = *reinterpret_cast<const floatx4 *>(im + o);
-            s.r[rr][0] = a.x, s.r[rr][1] = a.y, s.r[rr][2] = a.z, s.r[rr][3] = a.w;
-            s.i[rr][0] = b.x, s.i[rr][1] = b.y, s.i[rr][2] = b.z, s.i[rr][3] = b.w;
-        } else {
-#pragma unroll
-            for (int c = 0; c < 4; ++c) s.r[rr][c] = 0.f, s.i[rr][c] = 0.f;
-        }
-    }
-}
-
-__device__ __forceinline__ void write_state(float *re, float *im, const State &s, int64_t chain, const Lane &L) {
-#pragma unroll
-    for (int rr = 0; rr < RPL; ++rr) {
-        const int64_t o = chain * D * D + (L.r0 + rr) * D + 4 * L.cg;
-        *reinterpret_cast<floatx4 *>(re + o) = floatx4{s.r[rr][0], s.r[rr][1], s.r[rr][2], s.r[rr][3]};
-        *reinterpret_cast<floatx4 *>(im + o) = floatx4{s.i[rr][0], s.i[rr][1], s.i[rr][2], s.i[rr][3]};
-    }
-}
-constexpr int STATE_FLOATS = 2 * D * D;   // one chain's state, thread-private layout
-
-// backward workspace: sub-group states [chain][SUBS][state], then the parts' partial sums
-__host__ __device__ __forceinline__ size_t bwd_sub_bytes(const qpam_delta_args &a) {
-    return (size_t)a.B * a.H * SUBS * STATE_FLOATS * sizeof(float);
-}
 
 // ---------------------------------------------------------------------------
 // Forward over 64-step chunks on fp32 MFMA (v_mfma_f32_16x16x4f32).  Unrolled
@@ -248,8 +44,7 @@ __host__ __device__ __forceinline__ size_t bwd_sub_bytes(const qpam_delta_args &
 // per chunk in the MFMA A-operand order.  delta_chunk_kernel then walks the
 // chunks of one (b, h) for 16 value rows (rows of the recurrence are
 // independent: four blocks per chain) with S^T in LDS: W = beta (V - alpha K S^T),
-// U = T W, the state update in four 16-step quarters (each quarter's end state is
-// the backward's checkpoint before the next 16 steps), then Y = Ahat U + alpha
+// U = T W, the state update in four 16-step quarters, then Y = Ahat U + alpha
 // Q~ S^T with the chunk's entering state.
 constexpr int CH = 64;                 // steps per chunk
 constexpr int ROW_BLOCKS = 4;          // blocks per chain in the chunk pass (16 value rows each)
@@ -259,6 +54,26 @@ constexpr int NBLK = 10;               // 16 x 16 blocks on and below the diagon
 constexpr int BLK = 2 * 256;           // floats of one complex 16 x 16 block (re plane, then im)
 constexpr int PREP_T = 0, PREP_A = NBLK * BLK, PREP_L = 2 * NBLK * BLK;
 constexpr int PREP_FLOATS = PREP_L + CH;  // per chunk: T blocks, Ahat blocks, L
+
+// The forward's workspace (kept for the backward), one record per (b, h, chunk):
+// the entering state S [plane][i][j] and U [plane][t][i] (row-major), then the
+// chunk's products in the orders the backward reads them: T^H and Ahat^H in
+// A-operand order (T^H block (rows a, cols b >= a) at index blk(b, a), likewise
+// Ahat^H), and Ahat and D.Gk (D[t,s] k_t.conj(k_s) for s < t) in accumulator
+// order (block (bt, bs), lane (l16, g), element r <-> t = 16 bt + 4 g + r,
+// s = 16 bs + l16, float4 per lane and plane), and L.
+constexpr int WS_S = 0, WS_U = 2 * D * D, WS_TH = 4 * D * D, WS_AH = WS_TH + NBLK * BLK,
+              WS_AA = WS_AH + NBLK * BLK, WS_GA = WS_AA + NBLK * BLK, WS_L = WS_GA + NBLK * BLK,
+              WS_REC = WS_L + CH;
+// The backward's workspace, one record per (b, h, chunk): G (the gradient of the
+// state after the chunk) [plane][i][j], dW [plane][t][i], dP = D.dAhat and
+// dGk = beta D.dM in two layouts each (x_Q: transposed accumulator order, lane
+// (l16, g), r <-> t = 16 bt + l16, s = 16 bs + 4 g + r; x_K: accumulator order),
+// and two per-step vectors: the score part of the log-decay gradient and the
+// beta gradient through M.
+constexpr int BW_G = 0, BW_W = 2 * D * D, BW_PQ = 4 * D * D, BW_PK = BW_PQ + NBLK * BLK,
+              BW_GQ = BW_PK + NBLK * BLK, BW_GK = BW_GQ + NBLK * BLK, BW_V = BW_GK + NBLK * BLK,
+              BW_REC = BW_V + 2 * CH;
 
 __device__ __forceinline__ int blk(int b, int c) { return b * (b + 1) / 2 + c; }  // c <= b
 
@@ -340,6 +155,8 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
     const int b = chain / a.H, h = chain % a.H;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const int t0 = c * CH, valid = min(CH, a.T - t0);
+    // the backward's record of this chunk (when a backward follows)
+    float *wrec = a.workspace ? static_cast<float *>(a.workspace) + ((int64_t)chain * n_chunks + c) * WS_REC : nullptr;
     {  // K and q_scale Q, rows past the end zero
         const float *kre = static_cast<const float *>(a.k.re) + b * a.k.s0 + h * a.k.s1;
         const float *kim = static_cast<const float *>(a.k.im) + b * a.k.s0 + h * a.k.s1;
@@ -372,6 +189,7 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
         sL[lane] = x;
         sB[lane] = lane < valid ? a.beta[go] : 0.f;
         prep[chunk_prep(chain, n_chunks, c) + PREP_L + lane] = x;
+        if (wrec) wrec[WS_L + lane] = x;
     }
     __syncthreads();
     // 20 products (10 blocks on and below the diagonal, Gram G[t,s] = k_t . conj(k_s) and
@@ -399,23 +217,47 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
         const floatx4 xr = gre(acc[it]), xi = gim(acc[it]);
         if (kind == 0) {
             float *Mb = sM + bk * BLK;
+            floatx4 gr, gi;  // D.Gk for the backward
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * bb + 4 * g + r, s = 16 * cc + l16;
-                const float m = s < t ? sB[t] * __expf(sL[t] - sL[s]) : 0.f;
+                const float dts = s < t ? __expf(sL[t] - sL[s]) : 0.f;
+                const float m = sB[t] * dts;
                 Mb[(4 * g + r) * 16 + l16] = m * xr[r];
                 Mb[256 + (4 * g + r) * 16 + l16] = m * xi[r];
+                gr[r] = dts * xr[r];
+                gi[r] = dts * xi[r];
+            }
+            if (wrec) {
+                float *dst = wrec + WS_GA + bk * BLK + (g * 16 + l16) * 4;
+                *reinterpret_cast<floatx4 *>(dst) = gr;
+                *reinterpret_cast<floatx4 *>(dst + 256) = gi;
             }
         } else {
             // Ahat in A-operand order: element (row 4g + r, col l16) -> lane (col % 4) * 16 + row, slot col / 4
             float *dst = prep + chunk_prep(chain, n_chunks, c) + PREP_A + bk * BLK;
+            floatx4 ar, ai;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * bb + 4 * g + r, s = 16 * cc + l16;
                 const float dts = s <= t ? __expf(sL[t] - sL[s]) : 0.f;
                 const int ln = (l16 & 3) * 16 + 4 * g + r, ks = l16 >> 2;
-                dst[ln * 4 + ks] = dts * xr[r];
-                dst[256 + ln * 4 + ks] = dts * xi[r];
+                ar[r] = dts * xr[r];
+                ai[r] = dts * xi[r];
+                dst[ln * 4 + ks] = ar[r];
+                dst[256 + ln * 4 + ks] = ai[r];
+            }
+            if (wrec) {
+                // Ahat in accumulator order; Ahat^H in A-operand order (rows s: lane (l16, r), slot g)
+                float *da = wrec + WS_AA + bk * BLK + (g * 16 + l16) * 4;
+                *reinterpret_cast<floatx4 *>(da) = ar;
+                *reinterpret_cast<floatx4 *>(da + 256) = ai;
+                float *dh = wrec + WS_AH + bk * BLK;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    dh[(r * 16 + l16) * 4 + g] = ar[r];
+                    dh[256 + (r * 16 + l16) * 4 + g] = -ai[r];
+                }
             }
         }
     }
@@ -492,6 +334,16 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
     }
     for (int k = 0; k < NBLK; ++k)
         blk_export(prep + chunk_prep(chain, n_chunks, c) + PREP_T + k * BLK, sT + k * BLK, tid, 256);
+    if (wrec) {
+        // T^H in A-operand order: block (rows cc, cols bb) of T^H, element (x, 4 ks + g) =
+        // conj(T_(bb, cc)[4 ks + g][x]), stored at T's block index
+        for (int e = tid; e < NBLK * BLK; e += 256) {
+            const int k = e >> 9, pl = (e >> 8) & 1, idx = e & 255, ln = idx >> 2, ks = idx & 3;
+            const int row = ln & 15, gg = ln >> 4;
+            const float v = sT[k * BLK + pl * 256 + (4 * ks + gg) * 16 + row];
+            wrec[WS_TH + e] = pl ? -v : v;
+        }
+    }
 }
 
 // a [64][64] fp32 complex tile of the chunk (rows past the end zero) in registers:
@@ -534,14 +386,6 @@ __device__ __forceinline__ void ops_fetch(OpRegs &x, const float *base, int w, i
     }
 }
 
-// the chain's checkpoint layout (the backward's): float (slot * 8 + plane * 4 + j % 4) of
-// group state, slot = (i / 4) * 64 + (i % 4) * 16 + j / 4
-__device__ __forceinline__ void ckpt_store(float *dst, int i, int j4, const floatx4 &re, const floatx4 &im) {
-    const int slot = (i >> 2) * 64 + (i & 3) * 16 + j4;
-    *reinterpret_cast<floatx4 *>(dst + slot * 8) = re;
-    *reinterpret_cast<floatx4 *>(dst + slot * 8 + 4) = im;
-}
-
 __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, const float *prep, int n_chunks) {
     __shared__ __align__(16) float sKQr[CH * KP], sKQi[CH * KP];   // K, then q_scale Q, of the chunk
     __shared__ __align__(16) float sUr[CH * SP], sUi[CH * SP];     // W, then U  [t][i]
@@ -552,8 +396,8 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
     const int b = chain / a.H, h = chain % a.H;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const int i0 = 16 * rblk;  // the block's value rows
-    const int n_groups = (a.T + 15) / 16;
-    float *ckpt = a.workspace ? static_cast<float *>(a.workspace) + (int64_t)chain * n_groups * (2 * D * D) : nullptr;
+    // the backward's records of this chain: entering states and U
+    float *wrec = a.workspace ? static_cast<float *>(a.workspace) + (int64_t)chain * n_chunks * WS_REC : nullptr;
 
     for (int idx = tid; idx < CH * 16; idx += 256) {  // S0^T
         const int i = idx & 15, j = idx >> 4;
@@ -567,15 +411,6 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
     float bnext = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)min(lane, a.T - 1) * a.sg_t];
     int cur = 0;
     __syncthreads();
-    if (ckpt) {  // group 0: the entering state
-        floatx4 er, ei;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            er[r] = sSr[0][(16 * w + 4 * g + r) * SP + l16];
-            ei[r] = sSi[0][(16 * w + 4 * g + r) * SP + l16];
-        }
-        ckpt_store(ckpt, i0 + l16, 4 * w + g, er, ei);
-    }
     for (int c = 0; c < n_chunks; ++c) {
         const int t0 = c * CH, valid = min(CH, a.T - t0);
         const int64_t pc = chunk_prep(chain, n_chunks, c);
@@ -644,6 +479,14 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
             sUr[(16 * w + 4 * g + r) * SP + l16] = ur[r];
             sUi[(16 * w + 4 * g + r) * SP + l16] = ui[r];
         }
+        if (wrec) {  // U [t][i] of the block's rows
+            float *du = wrec + (int64_t)c * WS_REC + WS_U + i0 + l16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                du[(16 * w + 4 * g + r) * D] = ur[r];
+                du[D * D + (16 * w + 4 * g + r) * D] = ui[r];
+            }
+        }
         __syncthreads();
         const int wy = 3 - w;  // Y row tile: the wave with the most T blocks gets the fewest Ahat blocks
         ops_fetch(ops, prep + pc + PREP_A, wy, lane);  // Ahat, in flight through the state update
@@ -654,6 +497,11 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
             for (int r = 0; r < 4; ++r) {
                 sr[r] = sSr[cur][(16 * w + 4 * g + r) * SP + l16];
                 si[r] = sSi[cur][(16 * w + 4 * g + r) * SP + l16];
+            }
+            if (wrec) {  // entering state: S[i0 + l16][16 w + 4 g + r], 16-byte pieces
+                float *ds = wrec + (int64_t)c * WS_REC + WS_S + (i0 + l16) * D + 16 * w + 4 * g;
+                *reinterpret_cast<floatx4 *>(ds) = sr;
+                *reinterpret_cast<floatx4 *>(ds + D * D) = si;
             }
             float Lprev = 0.f;
 #pragma unroll
@@ -675,8 +523,6 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
                 sr += gre(x);
                 si += gim(x);
                 Lprev = Lq;
-                const int grp = 4 * c + q + 1;  // the state before step 16 grp
-                if (ckpt && 16 * grp < a.T) ckpt_store(ckpt + (int64_t)grp * (2 * D * D), i0 + l16, 4 * w + g, sr, si);
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -736,225 +582,699 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
     }
 }
 
-// sum over the 4 row groups of a wave (lanes cg, cg+16, cg+32, cg+48)
-__device__ __forceinline__ float rows4_sum(float x) {
-    x += __shfl_xor(x, 16);
-    return x + __shfl_xor(x, 32);
+// ---------------------------------------------------------------------------
+// Backward over the same 64-step chunks.  With G the gradient of the state after
+// a chunk and S the state entering it, the chunk's forward above differentiates to
+//     dU = Ahat^H dY + diag(dl) K G^T,   dW = T^H dU,   dv = diag(beta) dW,
+//     G_before = A_C G + (diag(alpha) dY)^T conj(Q~) - (diag(alpha beta) dW)^T conj(K)
+// (dl_s = D[last, s], A_C = e^{L_last}) and
+//     dAhat = dY U^H on s <= t,   dM = -dW U^H on s < t,   dP = D.dAhat,   dGk = beta_t D.dM,
+//     dq~ = dP K + diag(alpha) dY conj(S),
+//     dk  = dP^H Q~ + dGk K + dGk^H K - diag(alpha beta) dW conj(S) + diag(dl) U conj(G),
+//     dbeta_t  = Re sum_i conj(v_ti) dW_ti - alpha_t Re sum_j conj(k_tj) (dW conj S)_tj
+//                + Re sum_s conj(D.Gk)_ts dM_ts,
+//     dalpha_t = Re sum_j conj(q~_tj) (dY conj S)_tj - beta_t Re sum_j conj(k_tj) (dW conj S)_tj,
+//     ddl_s = Re sum_j k_sj conj(U conj G)_sj,   dA_C = Re <S, G>,
+// and the log-decay gradient dL_t = sum_s E_ts - sum_s E_st + dalpha_t alpha_t - ddl_t dl_t,
+// E = Re(conj(Ahat) dAhat) + beta_t Re(conj(D.Gk) dM), the chunk's last step also taking
+// sum_s ddl_s dl_s + dA_C A_C; dgamma_t = sum_{t' >= t} dL_t' / (gamma_t + eps).
+
+// the A-operand blocks (w, bb >= w) of an upper-triangular product (T^H, Ahat^H:
+// block (rows w, cols bb) stored at index blk(bb, w))
+__device__ __forceinline__ void ops_fetch_up(OpRegs &x, const float *base, int w, int lane) {
+#pragma unroll
+    for (int bb = 0; bb < 4; ++bb) {
+        if (bb >= w) {
+            const float *p = base + blk(bb, w) * BLK;
+            x.re[bb] = *reinterpret_cast<const floatx4 *>(p + lane * 4);
+            x.im[bb] = *reinterpret_cast<const floatx4 *>(p + 256 + lane * 4);
+        }
+    }
 }
 
-// Per-workgroup partial sums over its rows, [part][chain][t]: (dq~ re, dq~ im,
-// dk re, dk im) per column and (dgamma, dbeta); summed over the parts in a
-// fixed order by delta_reduce_kernel.
-__global__ void __launch_bounds__(BWD_THREADS) delta_bwd_kernel(qpam_delta_bwd_args g, qpam_delta_args a) {
-    // per flush: [token][wave][column] = (dq~ re, dq~ im, dk re, dk im) and
-    // [token][wave * 4 + row group] = (dgamma, dbeta)
-    __shared__ floatx4 red[FL][PW][D];
-    __shared__ floatx2 sred[FL][4 * PW];
-    __shared__ Span<GROUP, PROWS> sp;          // the group's token inputs for this workgroup's rows
-    __shared__ float sdy[GROUP][2][PROWS];     // and output gradients
-    const int chain = blockIdx.x / PARTS, part = blockIdx.x - chain * PARTS;
-    const int b = chain / a.H, h = chain - b * a.H, tid = threadIdx.x;
-    const Lane L(part * PW + (tid >> 6), tid & 63);
-    const int row0 = part * PROWS;
-    const int64_t nbht = (int64_t)a.B * a.H * a.T;
-    floatx4 *pcol = reinterpret_cast<floatx4 *>(static_cast<char *>(g.workspace) + bwd_sub_bytes(a)) +
-                    ((int64_t)part * a.B * a.H + chain) * a.T * D;
-    floatx2 *pscal = reinterpret_cast<floatx2 *>(reinterpret_cast<floatx4 *>(static_cast<char *>(g.workspace) +
-                                                                             bwd_sub_bytes(a)) + PARTS * nbht * D) +
-                     ((int64_t)part * a.B * a.H + chain) * a.T;
-    const int ng = chain_groups(a.T);
-    const float *ckpt = static_cast<const float *>(a.workspace) + (int64_t)chain * ng * STATE_FLOATS;
-    float *sub = static_cast<float *>(g.workspace) + (int64_t)chain * SUBS * STATE_FLOATS;
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0), vmcnt / expcnt unconstrained
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
-    State gs;   // adjoint of the state after the current token
-    init_state(gs, g.ds_re, g.ds_im, chain, L);
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
 
-    for (int grp = ng - 1; grp >= 0; --grp) {
-        const int t0 = grp * GROUP, tn = min(t0 + GROUP, a.T);
-        {   // stage the group's inputs and output gradients
-            SpanRegs<GROUP, PROWS, BWD_THREADS> regs;
-            regs.fetch(a, b, h, t0, row0, tid);
-            constexpr int NDY = GROUP * 2 * PROWS / BWD_THREADS;
-            float dyv[NDY];
-#pragma unroll
-            for (int k = 0; k < NDY; ++k) {
-                const int i = tid + k * BWD_THREADS, tok = i / (2 * PROWS), rem = i - tok * 2 * PROWS;
-                const int ri = rem / PROWS, r = rem - ri * PROWS;
-                const int t = min(t0 + tok, a.T - 1);
-                dyv[k] = static_cast<const float *>(ri ? g.dy.im : g.dy.re)[b * g.dy.s0 + h * g.dy.s1 +
-                                                                            (int64_t)t * g.dy.s2 + row0 + r];
-            }
-            __syncthreads();   // the previous group's readers are done
-            regs.commit(sp, tid);
-#pragma unroll
-            for (int k = 0; k < NDY; ++k) {
-                const int i = tid + k * BWD_THREADS, tok = i / (2 * PROWS), rem = i - tok * 2 * PROWS;
-                const int ri = rem / PROWS, r = rem - ri * PROWS;
-                sdy[tok][ri][r] = dyv[k];
-            }
-            __syncthreads();
+// delta_bwd_chain_kernel: the first two lines above along the chunks in reverse,
+// a block per (b, h) and 16 value rows (rows of G are independent as those of S
+// are; a chain's four blocks share an XCD), G^T [j][i] in LDS and each wave's
+// column tile of it in registers.  Per chunk: G leaves as the chunk's record,
+// X^T = conj(Q~)^T (alpha dY) is formed while K arrives, dU (row tile w) = dl K G^T
+// + Ahat^H dY, dW (row tile w) = T^H dU -> the record and dv, then
+// G^T <- A_C G^T + X^T - conj(K)^T (alpha beta dW).  The previous chunk's q~, dY,
+// L and beta are in flight from the middle of the step.
+__global__ void __launch_bounds__(256, 2) delta_bwd_chain_kernel(qpam_delta_bwd_args bw, qpam_delta_args a,
+                                                                 int n_chunks) {
+    __shared__ __align__(16) float sKQr[CH * KP], sKQi[CH * KP];  // q~, then K, of the chunk
+    __shared__ __align__(16) float sYr[CH * SP], sYi[CH * SP];    // dY [t][i] (the block's rows)
+    __shared__ __align__(16) float sUr[CH * SP], sUi[CH * SP];    // dU, then alpha beta dW  [t][i]
+    __shared__ __align__(16) float sGr[CH * SP], sGi[CH * SP];    // G^T [j][i]
+    __shared__ float sL[CH], sA[CH], sBt[CH];
+    const int n_chains = a.B * a.H;
+    const int chain = blockIdx.x % n_chains, rblk = blockIdx.x / n_chains;
+    const int b = chain / a.H, h = chain % a.H;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int i0 = 16 * rblk;
+    const float *wsf = static_cast<const float *>(a.workspace) + (int64_t)chain * n_chunks * WS_REC;
+    float *bws = static_cast<float *>(bw.workspace) + (int64_t)chain * n_chunks * BW_REC;
+    const int n = n_chunks;
+
+    // G^T column tile w: lane holds G[i0 + l16][16 w + 4 g + r]
+    floatx4 gR = {0.f, 0.f, 0.f, 0.f}, gI = gR;
+    if (bw.ds_re) {
+        const int64_t o = (int64_t)chain * D * D + (i0 + l16) * D + 16 * w + 4 * g;
+        gR = *reinterpret_cast<const floatx4 *>(bw.ds_re + o);
+        gI = *reinterpret_cast<const floatx4 *>(bw.ds_im + o);
+    }
+    // dY of a chunk for the block's rows: thread -> step tid / 4, columns i0 + 4 (tid % 4) ..
+    const int yt = tid >> 2, yc = 4 * (tid & 3);
+    floatx4 dyr, dyi;
+    auto fetch_dy = [&](int c) {
+        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        const int64_t o = b * bw.dy.s0 + h * bw.dy.s1 + (int64_t)(t0 + min(yt, valid - 1)) * bw.dy.s2 + i0 + yc;
+        const float f = yt < valid ? 1.f : 0.f;
+        dyr = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(bw.dy.re) + o) * f;
+        dyi = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(bw.dy.im) + o) * f;
+    };
+    float lnext = 0.f, bnext = 0.f;
+    auto fetch_lb = [&](int c) {  // wave 0: L and beta of chunk c (beta 0 past the end)
+        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        lnext = wsf[(int64_t)c * WS_REC + WS_L + lane];
+        const float bt = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)(t0 + min(lane, valid - 1)) * a.sg_t];
+        bnext = lane < valid ? bt : 0.f;
+    };
+    TileRegs xr;
+    auto stage = [&]() {
+        tile_put(sKQr, sKQi, xr, tid);
+        *reinterpret_cast<floatx4 *>(sYr + yt * SP + yc) = dyr;
+        *reinterpret_cast<floatx4 *>(sYi + yt * SP + yc) = dyi;
+        if (w == 0) {
+            sL[lane] = lnext;
+            sA[lane] = __expf(lnext);
+            sBt[lane] = bnext;
         }
-        // recompute the group, keeping the state before every SUB-th token
-        State s;
-        load_state(ckpt + (int64_t)grp * STATE_FLOATS, s, L.slot());
-        for (int t = t0; t < tn; ++t) {
-            if ((t - t0) % SUB == 0) store_state(sub + (int64_t)((t - t0) / SUB) * STATE_FLOATS, s, L.slot());
-            const Tok x = span_tok(sp, t - t0, L.cg, L.r0 - row0);
-            float yr[RPL], yi[RPL];
-            fwd_step(s, x, yr, yi);
-        }
-        for (int sg = (tn - t0 - 1) / SUB; sg >= 0; --sg) {
-            const int s0 = t0 + sg * SUB, n = min(SUB, tn - s0);
-            // states before each token of the sub-group
-            State prev[SUB];
-            load_state(sub + (int64_t)sg * STATE_FLOATS, prev[0], L.slot());
+    };
+    {
+        const int t0 = (n - 1) * CH;
+        tile_fetch(xr, a.q, b, h, t0, min(CH, a.T - t0), tid, a.q_scale);
+        fetch_dy(n - 1);
+        if (w == 0) fetch_lb(n - 1);
+    }
 #pragma unroll
-            for (int j = 1; j < SUB; ++j) {
-                prev[j] = prev[j - 1];
-                if (j < n) {
-                    const Tok x = span_tok(sp, s0 + j - 1 - t0, L.cg, L.r0 - row0);
-                    float yr[RPL], yi[RPL];
-                    fwd_step(prev[j], x, yr, yi);
+    for (int r = 0; r < 4; ++r) {
+        sGr[(16 * w + 4 * g + r) * SP + l16] = gR[r];
+        sGi[(16 * w + 4 * g + r) * SP + l16] = gI[r];
+    }
+    stage();
+    __syncthreads();
+
+    for (int c = n - 1; c >= 0; --c) {
+        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        const float *rec = wsf + (int64_t)c * WS_REC;
+        float *brec = bws + (int64_t)c * BW_REC;
+        {  // G after this chunk -> the record (16-byte pieces of rows i0 + l16)
+            float *dg = brec + BW_G + (i0 + l16) * D + 16 * w + 4 * g;
+            *reinterpret_cast<floatx4 *>(dg) = gR;
+            *reinterpret_cast<floatx4 *>(dg + D * D) = gI;
+        }
+        tile_fetch(xr, a.k, b, h, t0, valid, tid, 1.f);  // K, in flight through X
+        OpRegs ah, th;
+        ops_fetch_up(ah, rec + WS_AH, w, lane);
+        ops_fetch_up(th, rec + WS_TH, w, lane);
+        // X^T[j][i] = sum_t conj(q~_t[j]) alpha_t dY[t][i], column tile w
+        Gauss xq;
+        gz(xq);
+#pragma unroll 4
+        for (int ks = 0; ks < 16; ++ks) {
+            const int t = 4 * ks + g;
+            const float al = sA[t];
+            gstep(xq, sKQr[t * KP + 16 * w + l16], -sKQi[t * KP + 16 * w + l16], al * sYr[t * SP + l16],
+                  al * sYi[t * SP + l16]);
+        }
+        __syncthreads();  // q~ no longer read
+        tile_put(sKQr, sKQi, xr, tid);
+        if (c > 0) {  // the previous (full) chunk's q~, dY, L and beta, in flight through the rest
+            tile_fetch(xr, a.q, b, h, t0 - CH, CH, tid, a.q_scale);
+            fetch_dy(c - 1);
+            if (w == 0) fetch_lb(c - 1);
+        }
+        __syncthreads();
+        const float Llast = sL[CH - 1];
+        // dU[s][i] = dl_s sum_j K[s][j] G^T[j][i] + sum_{t >= s} conj(Ahat[t][s]) dY[t][i], row tile w
+        {
+            Gauss x;
+            gz(x);
+#pragma unroll 4
+            for (int ks = 0; ks < 16; ++ks) {
+                const int j = 4 * ks + g;
+                gstep(x, sKQr[(16 * w + l16) * KP + j], sKQi[(16 * w + l16) * KP + j], sGr[j * SP + l16],
+                      sGi[j * SP + l16]);
+            }
+            floatx4 ur = gre(x), ui = gim(x);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float dl = __expf(Llast - sL[16 * w + 4 * g + r]);
+                ur[r] *= dl;
+                ui[r] *= dl;
+            }
+            Gauss y;
+            gz(y);
+#pragma unroll
+            for (int bt = 0; bt < 4; ++bt) {
+                if (bt < w) continue;
+#pragma unroll
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int t = 16 * bt + 4 * ks + g;
+                    gstep(y, ah.re[bt][ks], ah.im[bt][ks], sYr[t * SP + l16], sYi[t * SP + l16]);
                 }
             }
+            ur += gre(y);
+            ui += gim(y);
 #pragma unroll
-            for (int j = SUB - 1; j >= 0; --j) {
-                if (j < n) {
-                    const int t = s0 + j;
-                    const Tok x = span_tok(sp, t - t0, L.cg, L.r0 - row0);
-                    float gyr[RPL], gyi[RPL];
+            for (int r = 0; r < 4; ++r) {
+                sUr[(16 * w + 4 * g + r) * SP + l16] = ur[r];
+                sUi[(16 * w + 4 * g + r) * SP + l16] = ui[r];
+            }
+        }
+        __syncthreads();
+        // dW[t][i] = sum_{s >= t} conj(T[s][t]) dU[s][i], row tile w
+        floatx4 wr, wi;
+        {
+            Gauss x;
+            gz(x);
 #pragma unroll
-                    for (int rr = 0; rr < RPL; ++rr)
-                        gyr[rr] = sdy[t - t0][0][L.r0 - row0 + rr], gyi[rr] = sdy[t - t0][1][L.r0 - row0 + rr];
-                    const State &sp = prev[j];
-                    // forward quantities of this token
-                    float ar[RPL][4], ai[RPL][4], pr[RPL], pi[RPL], ur[RPL], ui[RPL];
+            for (int bs = 0; bs < 4; ++bs) {
+                if (bs < w) continue;
 #pragma unroll
-                    for (int rr = 0; rr < RPL; ++rr) {
-                        float p0 = 0.f, p1 = 0.f;
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            ar[rr][c] = x.g * sp.r[rr][c], ai[rr][c] = x.g * sp.i[rr][c];
-                            p0 += ar[rr][c] * x.kr[c] - ai[rr][c] * x.ki[c];
-                            p1 += ar[rr][c] * x.ki[c] + ai[rr][c] * x.kr[c];
-                        }
-                        pr[rr] = row16_sum(p0), pi[rr] = row16_sum(p1);
-                        ur[rr] = x.b * (x.vr[rr] - pr[rr]), ui[rr] = x.b * (x.vi[rr] - pi[rr]);
-                    }
-                    float gq[4][2] = {}, gk[4][2] = {};
-                    float ggam = 0.f, gbet = 0.f;
-                    float gur[RPL], gui[RPL];
-#pragma unroll
-                    for (int rr = 0; rr < RPL; ++rr) {
-                        float u0 = 0.f, u1 = 0.f;
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            // s = a + u conj(k) (the state after the token)
-                            const float sr = ar[rr][c] + ur[rr] * x.kr[c] + ui[rr] * x.ki[c];
-                            const float si = ai[rr][c] + ui[rr] * x.kr[c] - ur[rr] * x.ki[c];
-                            // y = s . q~:  g_s += conj(q~) g_y;  g_q~ += conj(s) g_y
-                            gs.r[rr][c] += x.qr[c] * gyr[rr] + x.qi[c] * gyi[rr];
-                            gs.i[rr][c] += x.qr[c] * gyi[rr] - x.qi[c] * gyr[rr];
-                            gq[c][0] += sr * gyr[rr] + si * gyi[rr];
-                            gq[c][1] += sr * gyi[rr] - si * gyr[rr];
-                            // g_u = sum_c k_c g_s_c
-                            u0 += x.kr[c] * gs.r[rr][c] - x.ki[c] * gs.i[rr][c];
-                            u1 += x.kr[c] * gs.i[rr][c] + x.ki[c] * gs.r[rr][c];
-                            // g_k_c += u conj(g_s_c)
-                            gk[c][0] += ur[rr] * gs.r[rr][c] + ui[rr] * gs.i[rr][c];
-                            gk[c][1] += ui[rr] * gs.r[rr][c] - ur[rr] * gs.i[rr][c];
-                        }
-                        gur[rr] = row16_sum(u0), gui[rr] = row16_sum(u1);
-                    }
-#pragma unroll
-                    for (int rr = 0; rr < RPL; ++rr) {
-                        // u = beta (v - p)
-                        gbet += (x.vr[rr] - pr[rr]) * gur[rr] + (x.vi[rr] - pi[rr]) * gui[rr];
-                        const float gpr = -x.b * gur[rr], gpi = -x.b * gui[rr];
-                        float gg = 0.f;
-#pragma unroll
-                        for (int c = 0; c < 4; ++c) {
-                            // p = sum_c a_c k_c:  g_a += conj(k) g_p;  g_k += conj(a) g_p
-                            const float gar = gs.r[rr][c] + x.kr[c] * gpr + x.ki[c] * gpi;
-                            const float gai = gs.i[rr][c] + x.kr[c] * gpi - x.ki[c] * gpr;
-                            gk[c][0] += ar[rr][c] * gpr + ai[rr][c] * gpi;
-                            gk[c][1] += ar[rr][c] * gpi - ai[rr][c] * gpr;
-                            // a = g~ s_prev:  g_g~ += Re(conj(s_prev) g_a);  g_s_prev = g~ g_a
-                            gg += sp.r[rr][c] * gar + sp.i[rr][c] * gai;
-                            gs.r[rr][c] = x.g * gar;
-                            gs.i[rr][c] = x.g * gai;
-                        }
-                        ggam += gg;
-                    }
-                    if (L.cg == 0) {
-                        const int64_t vo = b * g.dv.s0 + h * g.dv.s1 + (int64_t)t * g.dv.s2 + L.r0;
-#pragma unroll
-                        for (int rr = 0; rr < RPL; ++rr) g.dv.re[vo + rr] = x.b * gur[rr], g.dv.im[vo + rr] = x.b * gui[rr];
-                    }
-                    // column sums over the wave's rows, then one slot per wave
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        gq[c][0] = rows4_sum(gq[c][0]), gq[c][1] = rows4_sum(gq[c][1]);
-                        gk[c][0] = rows4_sum(gk[c][0]), gk[c][1] = rows4_sum(gk[c][1]);
-                    }
-                    if (L.rg == 0) {
-#pragma unroll
-                        for (int c = 0; c < 4; ++c)
-                            red[j % FL][L.w - part * PW][4 * L.cg + c] = floatx4{gq[c][0], gq[c][1], gk[c][0], gk[c][1]};
-                    }
-                    // ggam holds this lane's columns; gbet is already the row group's value
-                    ggam = row16_sum(ggam);
-                    if (L.cg == 0) sred[j % FL][4 * (L.w - part * PW) + L.rg] = floatx2{ggam, gbet};
+                for (int ks = 0; ks < 4; ++ks) {
+                    const int s = 16 * bs + 4 * ks + g;
+                    gstep(x, th.re[bs][ks], th.im[bs][ks], sUr[s * SP + l16], sUi[s * SP + l16]);
                 }
-                if (j % FL == 0) {
-                    __syncthreads();
-                    // tokens j .. j + FL - 1 of the sub-group: reduce the wave slots in a fixed order
-                    const int m = min(FL, n - j);
-                    for (int i = tid; i < m * D; i += BWD_THREADS) {
-                        const int jj = i / D, c = i - jj * D, t = s0 + j + jj;
-                        floatx4 acc = red[jj][0][c];
+            }
+            wr = gre(x);
+            wi = gim(x);
+        }
+        {  // dW -> the record; dv = beta dW
+            float *dw = brec + BW_W + i0 + l16;
+            float *dvr = bw.dv.re + b * bw.dv.s0 + h * bw.dv.s1 + i0 + l16;
+            float *dvi = bw.dv.im + b * bw.dv.s0 + h * bw.dv.s1 + i0 + l16;
 #pragma unroll
-                        for (int w = 1; w < PW; ++w) acc += red[jj][w][c];
-                        pcol[(int64_t)t * D + c] = acc;
-                    }
-                    if (tid < m) {
-                        floatx2 acc = sred[tid][0];
-                        for (int k = 1; k < 4 * PW; ++k) acc += sred[tid][k];
-                        pscal[s0 + j + tid] = acc;
-                    }
-                    __syncthreads();
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * w + 4 * g + r;
+                dw[t * D] = wr[r];
+                dw[D * D + t * D] = wi[r];
+                if (t < valid) {
+                    const float bt = sBt[t];
+                    dvr[(int64_t)(t0 + t) * bw.dv.s2] = bt * wr[r];
+                    dvi[(int64_t)(t0 + t) * bw.dv.s2] = bt * wi[r];
                 }
+            }
+        }
+        __syncthreads();  // dU no longer read
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 16 * w + 4 * g + r;
+            const float ab = sA[t] * sBt[t];
+            sUr[t * SP + l16] = ab * wr[r];
+            sUi[t * SP + l16] = ab * wi[r];
+        }
+        __syncthreads();
+        // G^T <- A_C G^T + X^T - sum_t conj(k_t[j]) alpha_t beta_t dW[t][i], column tile w
+        {
+            Gauss x;
+            gz(x);
+#pragma unroll 4
+            for (int ks = 0; ks < 16; ++ks) {
+                const int t = 4 * ks + g;
+                gstep(x, sKQr[t * KP + 16 * w + l16], -sKQi[t * KP + 16 * w + l16], sUr[t * SP + l16],
+                      sUi[t * SP + l16]);
+            }
+            const float ac = __expf(Llast);
+            gR = ac * gR + gre(xq) - gre(x);
+            gI = ac * gI + gim(xq) - gim(x);
+        }
+        __syncthreads();  // K, dY, alpha beta dW and the old G^T no longer read
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            sGr[(16 * w + 4 * g + r) * SP + l16] = gR[r];
+            sGi[(16 * w + 4 * g + r) * SP + l16] = gI[r];
+        }
+        if (c > 0) stage();
+        __syncthreads();
+    }
+    if (bw.ds0_re) {
+        const int64_t o = (int64_t)chain * D * D + (i0 + l16) * D + 16 * w + 4 * g;
+        *reinterpret_cast<floatx4 *>(bw.ds0_re + o) = gR;
+        *reinterpret_cast<floatx4 *>(bw.ds0_im + o) = gI;
+    }
+}
+
+// delta_bwd_score_kernel: the score-matrix gradients of one chunk (a block per
+// (b, h, chunk), 4 waves).  U is staged in LDS; wave w forms dAhat on query tile
+// w and dM on query tile 3 - w (five 16 x 16 blocks either way), its dY and dW
+// rows straight from global memory as MFMA operands (k = i in the order
+// 16 q + 4 g + r: 16-byte loads), U rows as 16-byte LDS reads.  dP and dGk leave
+// in both layouts (a 16 x 16 LDS transpose per block and wave); E's row sums and
+// the beta part complete in the wave, its column sums per block through LDS,
+// added in a fixed order.
+__global__ void __launch_bounds__(256) delta_bwd_score_kernel(qpam_delta_bwd_args bw, qpam_delta_args a,
+                                                              int n_chunks) {
+    __shared__ __align__(16) float sUr[CH * KP], sUi[CH * KP];  // U [s][i]
+    __shared__ float sX[4][2][16 * 17];                         // each wave's transpose of one block
+    __shared__ float sRow[2][CH], sCol[2][4][CH], sDb[CH], sL[CH], sBt[CH];
+    const int chain = blockIdx.x / n_chunks, c = blockIdx.x % n_chunks;
+    const int b = chain / a.H, h = chain % a.H;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int t0 = c * CH, valid = min(CH, a.T - t0);
+    const float *rec = static_cast<const float *>(a.workspace) + ((int64_t)chain * n_chunks + c) * WS_REC;
+    float *brec = static_cast<float *>(bw.workspace) + ((int64_t)chain * n_chunks + c) * BW_REC;
+    // this lane's MFMA A rows: dY of step 16 w + l16, dW of step 16 (3 - w) + l16;
+    // element (q, r) is column 16 q + 4 g + r
+    floatx4 opr[2][4], opi[2][4];
+    {
+        const int t = 16 * w + l16;
+        const float f = t < valid ? 1.f : 0.f;
+        const int64_t o = b * bw.dy.s0 + h * bw.dy.s1 + (int64_t)(t0 + min(t, valid - 1)) * bw.dy.s2 + 4 * g;
+        const float *dw = brec + BW_W + (16 * (3 - w) + l16) * D + 4 * g;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            opr[0][q] = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(bw.dy.re) + o + 16 * q) * f;
+            opi[0][q] = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(bw.dy.im) + o + 16 * q) * f;
+            opr[1][q] = *reinterpret_cast<const floatx4 *>(dw + 16 * q);
+            opi[1][q] = *reinterpret_cast<const floatx4 *>(dw + D * D + 16 * q);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {  // U -> LDS, 16-byte pieces
+        const int e = tid + 256 * k, pl = e >> 10, row = (e >> 4) & 63, c4 = 4 * (e & 15);
+        const floatx4 v = *reinterpret_cast<const floatx4 *>(rec + WS_U + pl * D * D + row * D + c4);
+        *reinterpret_cast<floatx4 *>((pl ? sUi : sUr) + row * KP + c4) = v;
+    }
+    if (w == 0) {
+        sL[lane] = rec[WS_L + lane];
+        const float bt = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)(t0 + min(lane, valid - 1)) * a.sg_t];
+        sBt[lane] = lane < valid ? bt : 0.f;
+    }
+    __syncthreads();
+
+    float rowacc[2][4], db2[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rowacc[0][r] = rowacc[1][r] = db2[r] = 0.f;
+    float *X = sX[w][0], *Xi = sX[w][1];
+#pragma unroll
+    for (int kind = 0; kind < 2; ++kind) {
+        const int tt = kind ? 3 - w : w;  // query tile of this product
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            if (st > tt) continue;
+            const int s = 16 * st + l16;
+            // acc[t = 16 tt + 4 g + r][s] = sum_i A[t][i] conj(U[s][i])
+            Gauss x;
+            gz(x);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const floatx4 ur4 = *reinterpret_cast<const floatx4 *>(sUr + s * KP + 16 * q + 4 * g);
+                const floatx4 ui4 = *reinterpret_cast<const floatx4 *>(sUi + s * KP + 16 * q + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) gstep(x, opr[kind][q][r], opi[kind][q][r], ur4[r], -ui4[r]);
+            }
+            const floatx4 dr = gre(x), di = gim(x);
+            const float *src = rec + (kind ? WS_GA : WS_AA) + blk(tt, st) * BLK + lane * 4;
+            const floatx4 xr4 = *reinterpret_cast<const floatx4 *>(src);       // Ahat or D.Gk
+            const floatx4 xi4 = *reinterpret_cast<const floatx4 *>(src + 256);
+            const float Ls = sL[s];
+            floatx4 pr, pi;
+            float cs = 0.f;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 16 * tt + 4 * g + r;
+                const bool keep = kind ? (s < t) : (s <= t);
+                const float Dv = keep ? __expf(sL[t] - Ls) : 0.f;
+                float e;
+                if (kind == 0) {  // dP = D dAhat; E = Re(conj(Ahat) dAhat)
+                    pr[r] = Dv * dr[r];
+                    pi[r] = Dv * di[r];
+                    e = xr4[r] * dr[r] + xi4[r] * di[r];
+                } else {  // dM = -acc; dGk = beta D dM; E = beta Re(conj(D.Gk) dM)
+                    const float bt = sBt[t];
+                    const float e2 = -(xr4[r] * dr[r] + xi4[r] * di[r]);
+                    pr[r] = -bt * Dv * dr[r];
+                    pi[r] = -bt * Dv * di[r];
+                    e = bt * e2;
+                    db2[r] += e2;
+                }
+                rowacc[kind][r] += e;
+                cs += e;
+            }
+            cs += __shfl_xor(cs, 16);
+            cs += __shfl_xor(cs, 32);
+            if (g == 0) sCol[kind][tt][s] = cs;
+            // x_K layout: the accumulator order
+            float *dk_ = brec + (kind ? BW_GK : BW_PK) + blk(tt, st) * BLK + lane * 4;
+            *reinterpret_cast<floatx4 *>(dk_) = pr;
+            *reinterpret_cast<floatx4 *>(dk_ + 256) = pi;
+            // x_Q layout: lane (l16 = t, g), r <-> s = 4 g + r, through the wave's LDS block
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                X[(4 * g + r) * 17 + l16] = pr[r];
+                Xi[(4 * g + r) * 17 + l16] = pi[r];
+            }
+            wave_lds_sync();
+            floatx4 qr4, qi4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                qr4[r] = X[l16 * 17 + 4 * g + r];
+                qi4[r] = Xi[l16 * 17 + 4 * g + r];
+            }
+            float *dq_ = brec + (kind ? BW_GQ : BW_PQ) + blk(tt, st) * BLK + lane * 4;
+            *reinterpret_cast<floatx4 *>(dq_) = qr4;
+            *reinterpret_cast<floatx4 *>(dq_ + 256) = qi4;
+            wave_lds_sync();
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float v0 = row16_sum(rowacc[0][r]), v1 = row16_sum(rowacc[1][r]), vb = row16_sum(db2[r]);
+        if (l16 == 0) {
+            sRow[0][16 * w + 4 * g + r] = v0;
+            sRow[1][16 * (3 - w) + 4 * g + r] = v1;
+            sDb[16 * (3 - w) + 4 * g + r] = vb;
+        }
+    }
+    __syncthreads();
+    if (tid < CH) {
+        const int t = tid;
+        float col = 0.f;
+#pragma unroll
+        for (int kind = 0; kind < 2; ++kind)
+            for (int tt = t >> 4; tt < 4; ++tt) col += sCol[kind][tt][t];
+        brec[BW_V + t] = sRow[0][t] + sRow[1][t] - col;
+        brec[BW_V + CH + t] = sDb[t];
+    }
+}
+
+// delta_bwd_grad_kernel: dq, dk, dgamma and dbeta of one chunk (a block per
+// (b, h, chunk), 8 waves).  K, q~, S and G are staged in LDS (pitch KP: the
+// MFMA reads of rows 4 g + r, 16 consecutive columns, hit distinct banks); waves
+// 0-3 take query tile w: dq~ = dP K + alpha dY conj(S) and the t-side part of dk,
+// dGk K - alpha beta dW conj(S); waves 4-7 key tile w: dP^H q~ + dGk^H K +
+// dl U conj(G).  Outputs accumulate transposed (a lane holds one step and four
+// consecutive columns, so rows leave as 16-byte pieces), with the lane's own
+// operands (dP, dGk blocks in the matching layout, dY, dW, U rows) straight from
+// global memory.  The key side stores its part of dk and the query side adds
+// its own after a barrier; the per-step sums (dalpha, dbeta, ddl) and Re<S, G>
+// meet in LDS, and wave 4 forms dL, its reverse cumsum and dgamma.
+constexpr int G2_TILE = 2 * CH * KP;
+constexpr size_t G2_SMEM = (size_t)(4 * G2_TILE + 7 * CH + 8) * sizeof(float);
+
+__global__ void __launch_bounds__(512) delta_bwd_grad_kernel(qpam_delta_bwd_args bw, qpam_delta_args a,
+                                                             int n_chunks) {
+    extern __shared__ __align__(16) float sm[];
+    float *sK = sm, *sQ = sK + G2_TILE, *sS = sQ + G2_TILE, *sG = sS + G2_TILE;  // [plane][row][KP]
+    float *sL = sG + G2_TILE, *sBt = sL + CH, *sLp = sBt + CH, *sDb2 = sLp + CH;
+    float *sDa = sDb2 + CH, *sDb = sDa + CH, *sDdl = sDb + CH, *sRed = sDdl + CH;
+    const int chain = blockIdx.x / n_chunks, c = blockIdx.x % n_chunks;
+    const int b = chain / a.H, h = chain % a.H;
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+    const int w = wv & 3;
+    const bool qside = wv < 4;
+    const int t0 = c * CH, valid = min(CH, a.T - t0);
+    const float *rec = static_cast<const float *>(a.workspace) + ((int64_t)chain * n_chunks + c) * WS_REC;
+    const float *brec = static_cast<const float *>(bw.workspace) + ((int64_t)chain * n_chunks + c) * BW_REC;
+    constexpr int PL = CH * KP;  // offset of the im plane in a staged tile
+    // stage K, q~ (rows past the end zero), S and G: 16 16-byte pieces per thread
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int e = tid + 512 * k, m = e >> 11, pl = (e >> 10) & 1, row = (e >> 4) & 63, c4 = 4 * (e & 15);
+        floatx4 v;
+        if (m < 2) {
+            const qpam_cview &x = m ? a.q : a.k;
+            const float *base = static_cast<const float *>(pl ? x.im : x.re);
+            const float f = row < valid ? (m ? a.q_scale : 1.f) : 0.f;
+            v = *reinterpret_cast<const floatx4 *>(base + b * x.s0 + h * x.s1 +
+                                                   (int64_t)(t0 + min(row, valid - 1)) * x.s2 + c4) * f;
+        } else {
+            const float *src = (m == 2 ? rec + WS_S : brec + BW_G) + pl * D * D;
+            v = *reinterpret_cast<const floatx4 *>(src + row * D + c4);
+        }
+        *reinterpret_cast<floatx4 *>(sm + m * G2_TILE + pl * PL + row * KP + c4) = v;
+    }
+    if (wv == 0) {
+        sL[lane] = rec[WS_L + lane];
+        const float bt = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)(t0 + min(lane, valid - 1)) * a.sg_t];
+        sBt[lane] = lane < valid ? bt : 0.f;
+        sLp[lane] = brec[BW_V + lane];
+        sDb2[lane] = brec[BW_V + CH + lane];
+    }
+    __syncthreads();
+    {  // Re<S, G>: this thread's 8 elements, summed per wave
+        float part = 0.f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int e = tid + 512 * k, row = e >> 6, col = e & 63;
+            part += sS[row * KP + col] * sG[row * KP + col] + sS[PL + row * KP + col] * sG[PL + row * KP + col];
+        }
+        part = wave_sum(part);
+        if (lane == 0) sRed[wv] = part;
+    }
+
+    floatx4 xkr[4], xki[4];  // the query side's part of dk, [column tile]
+    if (qside) {
+        const int t = 16 * w + l16;  // this lane's step
+        const float al = __expf(sL[t]), bt = sBt[t];
+        const float *opbase;
+        floatx4 orr[4], oi[4], pr[4], pi[4];
+        {  // dY rows (zero past the end) and the dP blocks (w, st <= w) in x_Q layout
+            const float f = t < valid ? 1.f : 0.f;
+            const int64_t o = b * bw.dy.s0 + h * bw.dy.s1 + (int64_t)(t0 + min(t, valid - 1)) * bw.dy.s2 + 4 * g;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                orr[q] = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(bw.dy.re) + o + 16 * q) * f;
+                oi[q] = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(bw.dy.im) + o + 16 * q) * f;
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > w) continue;
+                opbase = brec + BW_PQ + blk(w, st) * BLK + lane * 4;
+                pr[st] = *reinterpret_cast<const floatx4 *>(opbase);
+                pi[st] = *reinterpret_cast<const floatx4 *>(opbase + 256);
+            }
+        }
+        float dal = 0.f;
+        float *dqr = bw.dq.re + b * bw.dq.s0 + h * bw.dq.s1 + (int64_t)(t0 + t) * bw.dq.s2;
+        float *dqi = bw.dq.im + b * bw.dq.s0 + h * bw.dq.s1 + (int64_t)(t0 + t) * bw.dq.s2;
+#pragma unroll 1  // (unrolled, the compiler keeps every column tile's operands live and spills)
+        for (int jt = 0; jt < 4; ++jt) {
+            const int j = 16 * jt + l16;
+            // sum_s K[s][j] dP[t][s]  (k = s = 16 st + 4 g + r)
+            Gauss x;
+            gz(x);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > w) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int s = 16 * st + 4 * g + r;
+                    gstep(x, sK[s * KP + j], sK[PL + s * KP + j], pr[st][r], pi[st][r]);
+                }
+            }
+            // YS^T[j][t] = sum_i conj(S[i][j]) dY[t][i]  (k = i = 16 q + 4 g + r)
+            Gauss y;
+            gz(y);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int i = 16 * q + 4 * g + r;
+                    gstep(y, sS[i * KP + j], -sS[PL + i * KP + j], orr[q][r], oi[q][r]);
+                }
+            const floatx4 ysr = gre(y), ysi = gim(y);
+            const floatx4 qr4 = *reinterpret_cast<const floatx4 *>(sQ + t * KP + 16 * jt + 4 * g);
+            const floatx4 qi4 = *reinterpret_cast<const floatx4 *>(sQ + PL + t * KP + 16 * jt + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dal += qr4[r] * ysr[r] + qi4[r] * ysi[r];
+            if (t < valid) {
+                *reinterpret_cast<floatx4 *>(dqr + 16 * jt + 4 * g) = (gre(x) + al * ysr) * a.q_scale;
+                *reinterpret_cast<floatx4 *>(dqi + 16 * jt + 4 * g) = (gim(x) + al * ysi) * a.q_scale;
+            }
+        }
+        {  // dW rows and the dGk blocks (w, st <= w) in x_Q layout
+            const float *dw = brec + BW_W + t * D + 4 * g;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                orr[q] = *reinterpret_cast<const floatx4 *>(dw + 16 * q);
+                oi[q] = *reinterpret_cast<const floatx4 *>(dw + D * D + 16 * q);
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > w) continue;
+                opbase = brec + BW_GQ + blk(w, st) * BLK + lane * 4;
+                pr[st] = *reinterpret_cast<const floatx4 *>(opbase);
+                pi[st] = *reinterpret_cast<const floatx4 *>(opbase + 256);
+            }
+        }
+        float dk2 = 0.f;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) {
+            const int j = 16 * jt + l16;
+            Gauss x;  // sum_s K[s][j] dGk[t][s]
+            gz(x);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (st > w) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int s = 16 * st + 4 * g + r;
+                    gstep(x, sK[s * KP + j], sK[PL + s * KP + j], pr[st][r], pi[st][r]);
+                }
+            }
+            Gauss y;  // WS^T[j][t] = sum_i conj(S[i][j]) dW[t][i]
+            gz(y);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int i = 16 * q + 4 * g + r;
+                    gstep(y, sS[i * KP + j], -sS[PL + i * KP + j], orr[q][r], oi[q][r]);
+                }
+            const floatx4 wsr = gre(y), wsi = gim(y);
+            const floatx4 kr4 = *reinterpret_cast<const floatx4 *>(sK + t * KP + 16 * jt + 4 * g);
+            const floatx4 ki4 = *reinterpret_cast<const floatx4 *>(sK + PL + t * KP + 16 * jt + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dk2 += kr4[r] * wsr[r] + ki4[r] * wsi[r];
+            xkr[jt] = gre(x) - (al * bt) * wsr;
+            xki[jt] = gim(x) - (al * bt) * wsi;
+        }
+        float dba = 0.f;  // Re sum_i conj(v[t][i]) dW[t][i]
+        {
+            const int64_t o = b * a.v.s0 + h * a.v.s1 + (int64_t)(t0 + min(t, valid - 1)) * a.v.s2 + 4 * g;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const floatx4 vr4 = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(a.v.re) + o + 16 * q);
+                const floatx4 vi4 = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(a.v.im) + o + 16 * q);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dba += vr4[r] * orr[q][r] + vi4[r] * oi[q][r];
+            }
+        }
+        dal += __shfl_xor(dal, 16);
+        dal += __shfl_xor(dal, 32);
+        dk2 += __shfl_xor(dk2, 16);
+        dk2 += __shfl_xor(dk2, 32);
+        dba += __shfl_xor(dba, 16);
+        dba += __shfl_xor(dba, 32);
+        if (g == 0) {
+            sDa[t] = dal - bt * dk2;
+            sDb[t] = dba - al * dk2;
+        }
+    } else {
+        const int s = 16 * w + l16;  // this lane's step (key side)
+        const float dl = __expf(sL[CH - 1] - sL[s]);
+        float *dkr = bw.dk.re + b * bw.dk.s0 + h * bw.dk.s1 + (int64_t)(t0 + s) * bw.dk.s2;
+        float *dki = bw.dk.im + b * bw.dk.s0 + h * bw.dk.s1 + (int64_t)(t0 + s) * bw.dk.s2;
+        floatx4 urr[4], ui[4], pr[4], pi[4], hr[4], hi[4];
+        {  // U rows; dP, dGk blocks (tt >= w, w) in x_K layout
+            const float *du = rec + WS_U + s * D + 4 * g;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                urr[q] = *reinterpret_cast<const floatx4 *>(du + 16 * q);
+                ui[q] = *reinterpret_cast<const floatx4 *>(du + D * D + 16 * q);
+            }
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                if (tt < w) continue;
+                const float *p = brec + BW_PK + blk(tt, w) * BLK + lane * 4;
+                const float *q = brec + BW_GK + blk(tt, w) * BLK + lane * 4;
+                pr[tt] = *reinterpret_cast<const floatx4 *>(p);
+                pi[tt] = *reinterpret_cast<const floatx4 *>(p + 256);
+                hr[tt] = *reinterpret_cast<const floatx4 *>(q);
+                hi[tt] = *reinterpret_cast<const floatx4 *>(q + 256);
+            }
+        }
+        float ddl = 0.f;
+#pragma unroll 1  // (unrolled, the compiler keeps every column tile's operands live and spills)
+        for (int jt = 0; jt < 4; ++jt) {
+            const int j = 16 * jt + l16;
+            // sum_t q~[t][j] conj(dP[t][s]) + K[t][j] conj(dGk[t][s])  (k = t = 16 tt + 4 g + r)
+            Gauss x;
+            gz(x);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                if (tt < w) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 16 * tt + 4 * g + r;
+                    gstep(x, sQ[t * KP + j], sQ[PL + t * KP + j], pr[tt][r], -pi[tt][r]);
+                    gstep(x, sK[t * KP + j], sK[PL + t * KP + j], hr[tt][r], -hi[tt][r]);
+                }
+            }
+            // UG^T[j][s] = sum_i conj(G[i][j]) U[s][i]
+            Gauss y;
+            gz(y);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int i = 16 * q + 4 * g + r;
+                    gstep(y, sG[i * KP + j], -sG[PL + i * KP + j], urr[q][r], ui[q][r]);
+                }
+            const floatx4 ugr = gre(y), ugi = gim(y);
+            const floatx4 kr4 = *reinterpret_cast<const floatx4 *>(sK + s * KP + 16 * jt + 4 * g);
+            const floatx4 ki4 = *reinterpret_cast<const floatx4 *>(sK + PL + s * KP + 16 * jt + 4 * g);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ddl += kr4[r] * ugr[r] + ki4[r] * ugi[r];
+            if (s < valid) {  // the key side's part of dk; the query side adds its part below
+                *reinterpret_cast<floatx4 *>(dkr + 16 * jt + 4 * g) = gre(x) + dl * ugr;
+                *reinterpret_cast<floatx4 *>(dki + 16 * jt + 4 * g) = gim(x) + dl * ugi;
+            }
+        }
+        ddl += __shfl_xor(ddl, 16);
+        ddl += __shfl_xor(ddl, 32);
+        if (g == 0) sDdl[s] = ddl;
+    }
+    __syncthreads();  // the key side's dk rows are written (and visible to the block)
+    if (qside) {
+        const int t = 16 * w + l16;
+        if (t < valid) {
+            float *dkr = bw.dk.re + b * bw.dk.s0 + h * bw.dk.s1 + (int64_t)(t0 + t) * bw.dk.s2 + 4 * g;
+            float *dki = bw.dk.im + b * bw.dk.s0 + h * bw.dk.s1 + (int64_t)(t0 + t) * bw.dk.s2 + 4 * g;
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) {
+                *reinterpret_cast<floatx4 *>(dkr + 16 * jt) += xkr[jt];
+                *reinterpret_cast<floatx4 *>(dki + 16 * jt) += xki[jt];
             }
         }
     }
-    if (g.ds0_re) write_state(g.ds0_re, g.ds0_im, gs, chain, L);
-}
-
-// dq = q_scale * sum of the parts' dq~, dk, dgamma, dbeta: one thread per (chain, t, column)
-__global__ void __launch_bounds__(256) delta_reduce_kernel(qpam_delta_bwd_args g, qpam_delta_args a) {
-    const int64_t nbht = (int64_t)a.B * a.H * a.T;
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (i >= nbht * D) return;
-    const int64_t ct = i / D;
-    const int c = (int)(i - ct * D);
-    const int chain = (int)(ct / a.T), t = (int)(ct - (int64_t)chain * a.T);
-    const int b = chain / a.H, h = chain - b * a.H;
-    const floatx4 *pcol = reinterpret_cast<const floatx4 *>(static_cast<const char *>(g.workspace) + bwd_sub_bytes(a));
-    floatx4 acc = pcol[i];
+    if (wv == 4) {  // lane = step: dL, its reverse cumsum, dgamma and dbeta
+        const int t = lane;
+        const float Lt = sL[t], Llast = sL[CH - 1];
+        const float al = __expf(Lt), dl = __expf(Llast - Lt);
+        const bool tv = t < valid;
+        float x = tv ? sLp[t] + sDa[t] * al - sDdl[t] * dl : 0.f;
+        const float tot = wave_sum(tv ? sDdl[t] * dl : 0.f);
+        float dac = 0.f;
 #pragma unroll
-    for (int p = 1; p < PARTS; ++p) acc += pcol[p * nbht * D + i];
-    const int64_t qo = b * g.dq.s0 + h * g.dq.s1 + (int64_t)t * g.dq.s2 + c;
-    const int64_t ko = b * g.dk.s0 + h * g.dk.s1 + (int64_t)t * g.dk.s2 + c;
-    g.dq.re[qo] = acc.x * a.q_scale, g.dq.im[qo] = acc.y * a.q_scale;
-    g.dk.re[ko] = acc.z, g.dk.im[ko] = acc.w;
-    if (c == 0) {
-        const floatx2 *pscal = reinterpret_cast<const floatx2 *>(pcol + PARTS * nbht * D);
-        floatx2 sacc = pscal[ct];
+        for (int k = 0; k < 8; ++k) dac += sRed[k];
+        if (t == valid - 1) x += tot + dac * __expf(Llast);
 #pragma unroll
-        for (int p = 1; p < PARTS; ++p) sacc += pscal[p * nbht + ct];
-        const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)t * a.sg_t;
-        g.dgamma[go] = sacc.x;
-        g.dbeta[go] = sacc.y;
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_down(x, off);
+            if (lane + off < 64) x += y;
+        }
+        if (tv) {
+            const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)(t0 + t) * a.sg_t;
+            bw.dgamma[go] = x / (a.gamma[go] + a.gamma_eps);
+            bw.dbeta[go] = sDb[t] + sDb2[t];
+        }
     }
 }
 
@@ -967,16 +1287,10 @@ bool mview_ok(const qpam_mview &v) {
     return v.re && v.im && aligned(v.re, 16) && aligned(v.im, 16) && v.s0 % 4 == 0 && v.s1 % 4 == 0 && v.s2 % 4 == 0;
 }
 
-size_t fwd_ws(const qpam_delta_args &a) {
-    return (size_t)a.B * a.H * ((a.T + GROUP - 1) / GROUP) * STATE_FLOATS * sizeof(float);
-}
-size_t prep_bytes(const qpam_delta_args &a) {
-    return (size_t)a.B * a.H * ((a.T + CH - 1) / CH) * PREP_FLOATS * sizeof(float);
-}
-size_t bwd_ws(const qpam_delta_args &a) {
-    const size_t nbht = (size_t)a.B * a.H * a.T;
-    return bwd_sub_bytes(a) + PARTS * nbht * (D * sizeof(floatx4) + sizeof(floatx2));
-}
+size_t n_chunks_of(const qpam_delta_args &a) { return (size_t)((a.T + CH - 1) / CH); }
+size_t fwd_ws(const qpam_delta_args &a) { return (size_t)a.B * a.H * n_chunks_of(a) * WS_REC * sizeof(float); }
+size_t prep_bytes(const qpam_delta_args &a) { return (size_t)a.B * a.H * n_chunks_of(a) * PREP_FLOATS * sizeof(float); }
+size_t bwd_ws(const qpam_delta_args &a) { return (size_t)a.B * a.H * n_chunks_of(a) * BW_REC * sizeof(float); }
 
 int validate(const qpam_delta_args *a) {
     QPAM_REQUIRE(a != nullptr, "qpam_delta: null arguments");
@@ -1036,7 +1350,7 @@ extern "C" int qpam_delta_bwd(const qpam_delta_bwd_args *g, void *stream) {
     int st = validate(&a);
     if (st) return st;
     QPAM_REQUIRE(a.workspace && aligned(a.workspace, 16) && a.workspace_bytes >= fwd_ws(a),
-                 "qpam_delta_bwd: the forward's workspace (checkpoints) is required");
+                 "qpam_delta_bwd: the forward's workspace (its per-chunk records) is required");
     QPAM_REQUIRE(g->workspace && aligned(g->workspace, 16) && g->workspace_bytes >= bwd_ws(a),
                  "qpam_delta_bwd: workspace of %zu bytes needed", bwd_ws(a));
     QPAM_REQUIRE(cview_ok(g->dy) && mview_ok(g->dq) && mview_ok(g->dk) && mview_ok(g->dv),
@@ -1045,11 +1359,19 @@ extern "C" int qpam_delta_bwd(const qpam_delta_bwd_args *g, void *stream) {
     QPAM_REQUIRE((g->ds_re == nullptr) == (g->ds_im == nullptr) && (g->ds0_re == nullptr) == (g->ds0_im == nullptr),
                  "qpam_delta_bwd: ds / ds0 need both planes");
     if (a.B == 0 || a.T == 0) return QPAM_OK;
+    const int n_chunks = (a.T + CH - 1) / CH;
+    const int64_t items = (int64_t)a.B * a.H * n_chunks;
+    QPAM_REQUIRE(items < (1ll << 31), "qpam_delta_bwd: grid too large");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(delta_bwd_kernel, dim3(a.B * a.H * PARTS), dim3(BWD_THREADS), 0, s, *g, a);
-    st = launch_status("delta_bwd_kernel");
+    hipLaunchKernelGGL(delta_bwd_chain_kernel, dim3((unsigned)(a.B * a.H * ROW_BLOCKS)), dim3(256), 0, s, *g, a,
+                       n_chunks);
+    st = launch_status("delta_bwd_chain_kernel");
     if (st) return st;
-    const int64_t n = (int64_t)a.B * a.H * a.T * D;
-    hipLaunchKernelGGL(delta_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, *g, a);
-    return launch_status("delta_reduce_kernel");
+    hipLaunchKernelGGL(delta_bwd_score_kernel, dim3((unsigned)items), dim3(256), 0, s, *g, a, n_chunks);
+    st = launch_status("delta_bwd_score_kernel");
+    if (st) return st;
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)delta_bwd_grad_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)G2_SMEM));
+    hipLaunchKernelGGL(delta_bwd_grad_kernel, dim3((unsigned)items), dim3(512), G2_SMEM, s, *g, a, n_chunks);
+    return launch_status("delta_bwd_grad_kernel");
 }

@@ -103,8 +103,13 @@ def delta_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: T
     return [y_re, y_im, s_re, s_im, ws]
 
 
+# floats of one (b, h, chunk) record of the forward's workspace: entering state and U
+# (2 x 2 d^2), four triangular products of 10 blocks x 512 floats, L (64)
+_WS_REC = 4 * 64 * 64 + 4 * 10 * 512 + 64
+
+
 def _ws_bytes(B, H, T, d=64):
-    return B * H * ((T + 15) // 16) * 2 * d * d * 4
+    return B * H * ((T + 63) // 64) * _WS_REC * 4
 
 
 @delta_fwd_op.register_fake

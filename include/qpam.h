@@ -306,8 +306,11 @@ int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void *mag, cons
  * fp32 planar [B,H,T,d] (strides b, h, t); gamma, beta fp32 [B,H,T] sharing
  * strides sg_*; s0 optional fp32 planar [B,H,d,d] contiguous; y fp32 planar
  * [B,H,T,d]; s_re/s_im the final state [B,H,d,d].  The workspace (size from
- * qpam_delta_workspace_size, or NULL when no backward follows) keeps the state
- * before every 16th token.  d == 64.
+ * qpam_delta_workspace_size, or NULL when no backward follows) keeps, per
+ * 64-step chunk, the entering state, the solved U and the chunk's triangular
+ * products for the backward.  d == 64.  The chunked form follows the reference's
+ * decay matrix exp(min(L_t - L_s, 0)) and its state-write weight
+ * alpha_last / (alpha_s + 1e-12) (v11/model.py:508-510, 565-566).
  */
 typedef struct {
     int32_t B, H, T, d;
@@ -331,7 +334,7 @@ size_t qpam_delta_scratch_size(const qpam_delta_args *a);
 int qpam_delta_fwd(const qpam_delta_args *a, void *stream);
 
 /* Backward of qpam_delta_fwd (`fwd` describes the forward call; its
- * workspace still holds the checkpoints).  dy fp32 planar [B,H,T,d]; ds
+ * workspace still holds the per-chunk records).  dy fp32 planar [B,H,T,d]; ds
  * optional gradient of the final state.  Out: dq, dk, dv planar fp32; dgamma,
  * dbeta [B,H,T] with the strides of gamma; ds0 optional [B,H,d,d].
  * Deterministic (fixed-order reductions). */

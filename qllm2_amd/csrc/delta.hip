@@ -32,11 +32,15 @@ constexpr int D = 64;
 // Forward over 64-step chunks on fp32 MFMA (v_mfma_f32_16x16x4f32).  Unrolled
 // over a chunk, the recurrence is the reference's UT form: with L_t the
 // inclusive prefix of log(gamma + eps) from the chunk's start, alpha_t = e^{L_t},
-// D[t,s] = e^{L_t - L_s} and S_0 the state entering the chunk,
+// D[t,s] = e^{min(L_t - L_s, 0)} (the reference's decay matrix) and S_0 the state
+// entering the chunk,
 //     (I + M) U = W,   M[t,s] = beta_t D[t,s] (k_t . conj(k_s))  (s < t),
 //     W_t = beta_t (v_t - alpha_t S_0 k_t),
 //     y_t = alpha_t S_0 q~_t + sum_{s<=t} D[t,s] (q~_t . conj(k_s)) u_s,
-//     S_end = alpha_last S_0 + sum_s D[last,s] u_s (x) conj(k_s).
+//     S_end = alpha_last S_0 + sum_s tail_s u_s (x) conj(k_s),
+// tail_s = alpha_last / (alpha_s + 1e-12) as the reference writes the state
+// (v11/model.py:565-566; the exact ratio e^{L_last - L_s} except where alpha_s
+// nears 1e-12, and D = e^{L_t - L_s} except for gamma + eps > 1).
 // delta_prep_kernel (chunk-parallel, a block per (b, h, chunk)) forms everything
 // that does not depend on S: the Gram and query-key products, T = (I + M)^{-1}
 // (diagonal 16 x 16 blocks by forward substitution, the blocks below them as
@@ -44,8 +48,8 @@ constexpr int D = 64;
 // per chunk in the MFMA A-operand order.  delta_chunk_kernel then walks the
 // chunks of one (b, h) for 16 value rows (rows of the recurrence are
 // independent: four blocks per chain) with S^T in LDS: W = beta (V - alpha K S^T),
-// U = T W, the state update in four 16-step quarters, then Y = Ahat U + alpha
-// Q~ S^T with the chunk's entering state.
+// U = T W, the state update, then Y = Ahat U + alpha Q~ S^T with the chunk's
+// entering state.
 constexpr int CH = 64;                 // steps per chunk
 constexpr int ROW_BLOCKS = 4;          // blocks per chain in the chunk pass (16 value rows each)
 constexpr int KP = CH + 4;             // LDS pitch of [64][64] fp32 tiles read element-wise
@@ -221,7 +225,7 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * bb + 4 * g + r, s = 16 * cc + l16;
-                const float dts = s < t ? __expf(sL[t] - sL[s]) : 0.f;
+                const float dts = s < t ? __expf(fminf(sL[t] - sL[s], 0.f)) : 0.f;
                 const float m = sB[t] * dts;
                 Mb[(4 * g + r) * 16 + l16] = m * xr[r];
                 Mb[256 + (4 * g + r) * 16 + l16] = m * xi[r];
@@ -240,7 +244,7 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * bb + 4 * g + r, s = 16 * cc + l16;
-                const float dts = s <= t ? __expf(sL[t] - sL[s]) : 0.f;
+                const float dts = s <= t ? __expf(fminf(sL[t] - sL[s], 0.f)) : 0.f;
                 const int ln = (l16 & 3) * 16 + 4 * g + r, ks = l16 >> 2;
                 ar[r] = dts * xr[r];
                 ai[r] = dts * xi[r];
@@ -490,7 +494,8 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
         __syncthreads();
         const int wy = 3 - w;  // Y row tile: the wave with the most T blocks gets the fewest Ahat blocks
         ops_fetch(ops, prep + pc + PREP_A, wy, lane);  // Ahat, in flight through the state update
-        // state update, row tile w of S^T (j = 16 w + 4 g + r, i = l16), in four 16-step quarters
+        // state update, row tile w of S^T (j = 16 w + 4 g + r, i = l16):
+        // S <- alpha_last S + sum_s tail_s u_s (x) conj(k_s), tail_s = alpha_last / (alpha_s + 1e-12)
         {
             floatx4 sr, si;
 #pragma unroll
@@ -503,27 +508,19 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
                 *reinterpret_cast<floatx4 *>(ds) = sr;
                 *reinterpret_cast<floatx4 *>(ds + D * D) = si;
             }
-            float Lprev = 0.f;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const float Lq = sL[16 * q + 15];
-                const float f = __expf(Lq - Lprev);
-                sr *= f;
-                si *= f;
-                Gauss x;
-                gz(x);
-#pragma unroll
-                for (int ks = 0; ks < 4; ++ks) {
-                    const int s = 16 * q + 4 * ks + g;
-                    const float wq = __expf(Lq - sL[s]);
-                    // conj(K)^T [j][s] (A) times (D U)[s][i] (B)
-                    gstep(x, sKQr[s * KP + 16 * w + l16], -sKQi[s * KP + 16 * w + l16], sUr[s * SP + l16] * wq,
-                          sUi[s * SP + l16] * wq);
-                }
-                sr += gre(x);
-                si += gim(x);
-                Lprev = Lq;
+            const float atot = __expf(sL[CH - 1]);
+            Gauss x;
+            gz(x);
+#pragma unroll 4
+            for (int ks = 0; ks < 16; ++ks) {
+                const int s = 4 * ks + g;
+                const float wq = atot / (__expf(sL[s]) + 1e-12f);
+                // conj(K)^T [j][s] (A) times (tail U)[s][i] (B)
+                gstep(x, sKQr[s * KP + 16 * w + l16], -sKQi[s * KP + 16 * w + l16], sUr[s * SP + l16] * wq,
+                      sUi[s * SP + l16] * wq);
             }
+            sr = atot * sr + gre(x);
+            si = atot * si + gim(x);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 sSr[cur ^ 1][(16 * w + 4 * g + r) * SP + l16] = sr[r];
@@ -587,7 +584,7 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
 // a chunk and S the state entering it, the chunk's forward above differentiates to
 //     dU = Ahat^H dY + diag(dl) K G^T,   dW = T^H dU,   dv = diag(beta) dW,
 //     G_before = A_C G + (diag(alpha) dY)^T conj(Q~) - (diag(alpha beta) dW)^T conj(K)
-// (dl_s = D[last, s], A_C = e^{L_last}) and
+// (dl_s = tail_s = A_C / (alpha_s + 1e-12), A_C = alpha_last) and
 //     dAhat = dY U^H on s <= t,   dM = -dW U^H on s < t,   dP = D.dAhat,   dGk = beta_t D.dM,
 //     dq~ = dP K + diag(alpha) dY conj(S),
 //     dk  = dP^H Q~ + dGk K + dGk^H K - diag(alpha beta) dW conj(S) + diag(dl) U conj(G),
@@ -595,9 +592,11 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
 //                + Re sum_s conj(D.Gk)_ts dM_ts,
 //     dalpha_t = Re sum_j conj(q~_tj) (dY conj S)_tj - beta_t Re sum_j conj(k_tj) (dW conj S)_tj,
 //     ddl_s = Re sum_j k_sj conj(U conj G)_sj,   dA_C = Re <S, G>,
-// and the log-decay gradient dL_t = sum_s E_ts - sum_s E_st + dalpha_t alpha_t - ddl_t dl_t,
-// E = Re(conj(Ahat) dAhat) + beta_t Re(conj(D.Gk) dM), the chunk's last step also taking
-// sum_s ddl_s dl_s + dA_C A_C; dgamma_t = sum_{t' >= t} dL_t' / (gamma_t + eps).
+// and the log-decay gradient dL_t = sum_s E_ts - sum_s E_st + dalpha_t alpha_t
+// - ddl_t dl_t alpha_t / (alpha_t + 1e-12), E = (Re(conj(Ahat) dAhat) + beta_t
+// Re(conj(D.Gk) dM)) where L_t - L_s <= 0 (D's clamp passes no gradient elsewhere),
+// the chunk's last step also taking sum_s ddl_s dl_s + dA_C A_C;
+// dgamma_t = sum_{t' >= t} dL_t' / (gamma_t + eps).
 
 // the A-operand blocks (w, bb >= w) of an upper-triangular product (T^H, Ahat^H:
 // block (rows w, cols bb) stored at index blk(bb, w))
@@ -741,11 +740,12 @@ __global__ void __launch_bounds__(256, 2) delta_bwd_chain_kernel(qpam_delta_bwd_
                       sGi[j * SP + l16]);
             }
             floatx4 ur = gre(x), ui = gim(x);
+            const float atot = __expf(Llast);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float dl = __expf(Llast - sL[16 * w + 4 * g + r]);
-                ur[r] *= dl;
-                ui[r] *= dl;
+                const float tl = atot / (sA[16 * w + 4 * g + r] + 1e-12f);  // the state-write weight
+                ur[r] *= tl;
+                ui[r] *= tl;
             }
             Gauss y;
             gz(y);
@@ -919,18 +919,20 @@ __global__ void __launch_bounds__(256) delta_bwd_score_kernel(qpam_delta_bwd_arg
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * tt + 4 * g + r;
                 const bool keep = kind ? (s < t) : (s <= t);
-                const float Dv = keep ? __expf(sL[t] - Ls) : 0.f;
+                const float lx = sL[t] - Ls;
+                const float Dv = keep ? __expf(fminf(lx, 0.f)) : 0.f;
+                const float through = lx <= 0.f ? 1.f : 0.f;  // D's clamp: no gradient to L past it
                 float e;
                 if (kind == 0) {  // dP = D dAhat; E = Re(conj(Ahat) dAhat)
                     pr[r] = Dv * dr[r];
                     pi[r] = Dv * di[r];
-                    e = xr4[r] * dr[r] + xi4[r] * di[r];
+                    e = through * (xr4[r] * dr[r] + xi4[r] * di[r]);
                 } else {  // dM = -acc; dGk = beta D dM; E = beta Re(conj(D.Gk) dM)
                     const float bt = sBt[t];
                     const float e2 = -(xr4[r] * dr[r] + xi4[r] * di[r]);
                     pr[r] = -bt * Dv * dr[r];
                     pi[r] = -bt * Dv * di[r];
-                    e = bt * e2;
+                    e = through * bt * e2;
                     db2[r] += e2;
                 }
                 rowacc[kind][r] += e;
@@ -1178,7 +1180,7 @@ __global__ void __launch_bounds__(512) delta_bwd_grad_kernel(qpam_delta_bwd_args
         }
     } else {
         const int s = 16 * w + l16;  // this lane's step (key side)
-        const float dl = __expf(sL[CH - 1] - sL[s]);
+        const float dl = __expf(sL[CH - 1]) / (__expf(sL[s]) + 1e-12f);  // the state-write weight
         float *dkr = bw.dk.re + b * bw.dk.s0 + h * bw.dk.s1 + (int64_t)(t0 + s) * bw.dk.s2;
         float *dki = bw.dk.im + b * bw.dk.s0 + h * bw.dk.s1 + (int64_t)(t0 + s) * bw.dk.s2;
         floatx4 urr[4], ui[4], pr[4], pi[4], hr[4], hi[4];
@@ -1257,14 +1259,14 @@ __global__ void __launch_bounds__(512) delta_bwd_grad_kernel(qpam_delta_bwd_args
     if (wv == 4) {  // lane = step: dL, its reverse cumsum, dgamma and dbeta
         const int t = lane;
         const float Lt = sL[t], Llast = sL[CH - 1];
-        const float al = __expf(Lt), dl = __expf(Llast - Lt);
+        const float al = __expf(Lt), atot = __expf(Llast), dl = atot / (al + 1e-12f);
         const bool tv = t < valid;
-        float x = tv ? sLp[t] + sDa[t] * al - sDdl[t] * dl : 0.f;
+        float x = tv ? sLp[t] + sDa[t] * al - sDdl[t] * dl * (al / (al + 1e-12f)) : 0.f;
         const float tot = wave_sum(tv ? sDdl[t] * dl : 0.f);
         float dac = 0.f;
 #pragma unroll
         for (int k = 0; k < 8; ++k) dac += sRed[k];
-        if (t == valid - 1) x += tot + dac * __expf(Llast);
+        if (t == valid - 1) x += tot + dac * atot;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const float y = __shfl_down(x, off);

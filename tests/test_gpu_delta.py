@@ -128,3 +128,53 @@ def test_delta_long_sequence_properties(gpu_lib):
     y = torch.stack([y_re, y_im], -1)[:, :1].cpu()
     assert _rel(y, yr) < 1e-4
     assert _rel(torch.stack([s_re, s_im], -1)[:, :1].cpu(), sr) < 1e-4
+
+
+def _rel_heads(a, b):
+    """max over (batch, head) of that head's max-abs error over its own max-abs
+    reference value (floored at 1e-6 of the global one, for heads whose exact
+    gradient is zero): a head whose values are small cannot hide behind another."""
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    err = (a - b).abs().flatten(2).amax(-1)
+    ref = b.abs().flatten(2).amax(-1).clamp_min(1e-6 * b.abs().max().item() + 1e-300)
+    return (err / ref).max().item()
+
+
+def test_delta_multichunk_per_head(gpu_lib):
+    """Five chunks (T = 300, ragged last chunk) with s0 and ds, every output and
+    gradient normalised per (b, h) against the chunked oracle in float64."""
+    B, H, T, d = 2, 3, 300, 64
+    q, k, v, g, b = D.make_delta_inputs(B, H, T, d, 670)
+    gen = torch.Generator().manual_seed(671)
+    s0 = torch.randn(B, H, d, d, 2, generator=gen, dtype=torch.float64) * 0.05
+    dy = torch.randn(B, H, T, d, 2, generator=gen, dtype=torch.float64)
+    ds = torch.randn(B, H, d, d, 2, generator=gen, dtype=torch.float64) * 0.1
+    y, s, grads = _run(q, k, v, g, b, s0, dy, ds, 1e-6)
+    yr, sr, rgrads = _ref(q, k, v, g, b, s0, dy, ds, chunked=True)
+    assert _rel_heads(y, yr) < 1e-4, f"y {_rel_heads(y, yr):.2e}"
+    assert _rel_heads(s, sr) < 1e-4, f"s {_rel_heads(s, sr):.2e}"
+    for name, a, r in zip(NAMES, grads, rgrads):
+        assert _rel_heads(a, r) < 1e-4, f"{name}: {_rel_heads(a, r):.2e}"
+
+
+def test_delta_decay_regimes(gpu_lib):
+    """Per head a different regime: strong decay (gamma in (0.01, 0.3): the
+    within-chunk alpha = e^L underflows in fp32), gamma = 1 exactly (no decay),
+    beta = 0 (no write) and beta = 1 (full overwrite), over three chunks; outputs
+    and gradients per (b, h) against the chunked oracle."""
+    B, H, T, d = 1, 4, 160, 64
+    q, k, v, g, b = D.make_delta_inputs(B, H, T, d, 680)
+    gen = torch.Generator().manual_seed(681)
+    g = g.clone()
+    b = b.clone()
+    g[:, 0] = 0.01 + 0.29 * torch.rand(B, T, generator=gen, dtype=torch.float64)
+    g[:, 1] = 1.0
+    b[:, 2] = 0.0
+    b[:, 3] = 1.0
+    dy = torch.randn(B, H, T, d, 2, generator=gen, dtype=torch.float64)
+    y, s, grads = _run(q, k, v, g, b, None, dy, None, 1e-6)
+    yr, sr, rgrads = _ref(q, k, v, g, b, None, dy, None, chunked=True)
+    assert _rel_heads(y, yr) < 1e-4, f"y {_rel_heads(y, yr):.2e}"
+    assert _rel_heads(s, sr) < 1e-4, f"s {_rel_heads(s, sr):.2e}"
+    for name, a, r in zip(NAMES[:5], grads[:5], rgrads[:5]):
+        assert _rel_heads(a, r) < 1e-4, f"{name}: {_rel_heads(a, r):.2e}"

@@ -82,3 +82,46 @@ def test_chunked_gradcheck():
     q, k, v, g, b = D.make_delta_inputs(1, 1, 6, 3, 11)
     xs = [x.clone().requires_grad_(True) for x in (q, k, v, g, b)]
     assert torch.autograd.gradcheck(lambda *a: D.delta_chunked(*a, 3, 4)[0], xs, eps=1e-6, atol=1e-6)
+
+
+def test_chunked_form_edge_weights_closed_form():
+    """Where the reference's chunked form departs from the token recurrence by
+    construction (v11/model.py:508-510, 565-566), pinned by closed forms with
+    orthonormal keys (then M = 0 and U = beta V):
+    * strong decay: the state write weights u_s by alpha_last / (alpha_s + 1e-12),
+      not alpha_last / alpha_s, once alpha_s (a prefix product of gamma + 1e-6)
+      is near 1e-12;
+    * gamma = 1: log(gamma + 1e-6) > 0, and the decay matrix clamps
+      exp(min(L_t - L_s, 0)) to 1 where the recurrence grows by (1 + 1e-6)^(t-s)."""
+    d, T = 8, 6
+    qk = torch.linalg.qr(torch.randn(d, d, generator=torch.Generator().manual_seed(11)))[0]
+    keys = torch.zeros(1, 1, T, d, 2)
+    keys[0, 0, :, :, 0] = qk[:T]
+    v = torch.randn(1, 1, T, d, 2, generator=torch.Generator().manual_seed(12))
+    q = torch.randn(1, 1, T, d, 2, generator=torch.Generator().manual_seed(13))
+    beta = torch.ones(1, 1, T)
+    # strong decay: alpha runs 1e-3 .. 1e-18
+    gamma = torch.full((1, 1, T), 1e-3)
+    _, s = D.delta_chunked(q, keys, v, gamma, beta, d, 64)
+    alpha = torch.cumprod(gamma[0, 0] + D.EPS, 0)
+    tail = alpha[-1] / (alpha + 1e-12)
+    want = torch.zeros(d, d, 2)
+    for t in range(T):
+        kt = keys[0, 0, t, :, 0]
+        want[..., 0] += tail[t] * torch.outer(v[0, 0, t, :, 0], kt)
+        want[..., 1] += tail[t] * torch.outer(v[0, 0, t, :, 1], kt)
+    assert torch.allclose(s[0, 0], want, rtol=1e-10, atol=1e-300)
+    exact = alpha[-1] / alpha
+    assert (tail[4:] / exact[4:]).max() < 1e-2  # alpha_s <= 1e-15 there: the weights differ by construction
+    # gamma = 1: y_t = q~_t . sum_{s <= t} (k_s* . q~_t) v_s with unit decay (clamped)
+    gamma = torch.ones(1, 1, T)
+    y, _ = D.delta_chunked(q, keys, v, gamma, beta, d, 64)
+    qs = q[0, 0] * d ** -0.5
+    for t in range(T):
+        acc = torch.zeros(d, 2)
+        for s_ in range(t + 1):
+            w_r = (qs[t, :, 0] * keys[0, 0, s_, :, 0]).sum()  # keys are real here
+            w_i = (qs[t, :, 1] * keys[0, 0, s_, :, 0]).sum()
+            acc[:, 0] += w_r * v[0, 0, s_, :, 0] - w_i * v[0, 0, s_, :, 1]
+            acc[:, 1] += w_r * v[0, 0, s_, :, 1] + w_i * v[0, 0, s_, :, 0]
+        assert torch.allclose(y[0, 0, t], acc, rtol=1e-10, atol=1e-12)

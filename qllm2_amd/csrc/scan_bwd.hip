@@ -841,103 +841,111 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
 // unscaled; q_scale is applied where q~ enters an fp32 result.
 using U16 = unsigned short;
 
-// Gradient-state pass (reverse): PASS_SPLIT blocks of PASS_THREADS (4 waves) per
-// (state m, b, h) walk the chunks from last to first with the running dS in
-// registers (fp32, accumulator layout; block `half` owns value rows 32 half.. (dY
-// columns 32 half..), its wave w the rows 16 it.., it = 2 half + (w & 1), and
-// key-column tiles 2(w >> 1), 2(w >> 1) + 1).  Per chunk: bf16 snapshot of dS after the
-// chunk, then dS <- total dS + sum_t conj(rho_m[t]) q_scale dY_t (x) conj(q_t) on
-// MFMA.  dS0 is written when requested.  Chunk c-2's Q and gamma / rotation and
-// chunk c-1's dY (fp32; one register set) are loaded while chunk c is processed.
-// Every wave forms the chunk's weights conj(rho_m[t]) q_scale itself, and dY is
-// staged already weighted (fp32 product rounded once to bf16), so the MFMA
-// operands come straight from LDS.  Rows past the end of the sequence re-read its
-// last row: their weights are zero.
+// Gradient-state pass (reverse): PASS_SPLIT blocks of GPASS_THREADS (8 waves) per
+// (b, h) walk the chunks from last to first with the running dS of every state m
+// in registers (fp32, accumulator layout; block `half` owns value rows 32 half..
+// (dY columns 32 half..), its wave w the 16 x 16 tile (rows 16 it.., it = 2 half
+// + (w & 1); key columns 16 (w >> 1)..) of each state).  The chunk's Q and dY
+// tiles are loaded once for all states: per chunk, every state's bf16 snapshot
+// of dS after the chunk, then dS_m <- total_m dS_m + sum_t conj(rho_m[t]) q_scale
+// dY_t (x) conj(q_t) on MFMA.  dS0 is written when requested.  Chunk c-2's dY, Q,
+// gammas, rotations and totals are loaded while chunk c is processed (two register
+// sets).  Every wave forms the chunk's weights conj(rho_m[t]) q_scale itself, and
+// dY is staged once per state already weighted (fp32 product rounded once to
+// bf16), so the MFMA operands come straight from LDS.  Rows past the end of the
+// sequence re-read its last row: their weights are zero.
 constexpr int GSNAP_ROWS = 64 / PASS_SPLIT;  // dS rows of one block
+constexpr int GPASS_THREADS = 512;
+template <int M>
 constexpr size_t gpass_bf16_smem() {
     return (size_t)2 * PLANE_B * 2                 // Q [plane][64][PB]
-           + (size_t)2 * PLANE_B * 2               // weighted dY (bf16) [plane][64][PB] (this block's columns)
-           + (size_t)2 * GSNAP_ROWS * PB * 2;      // bf16 snapshot of the block's dS rows [plane][32][PB]
+           + (size_t)2 * M * PLANE_B * 2           // weighted dY (bf16) [state][plane][64][PB] (this block's columns)
+           + (size_t)2 * M * GSNAP_ROWS * PB * 2;  // bf16 snapshots of the block's dS rows [state][plane][32][PB]
 }
 
-template <bool DYBF>
-__global__ void __launch_bounds__(PASS_THREADS) __attribute__((amdgpu_waves_per_eu(3)))
-grad_pass_bf16_kernel(BwdParams p) {
-    constexpr int NT = PASS_THREADS;
+template <int M, bool DYBF>
+__global__ void __launch_bounds__(GPASS_THREADS) grad_pass_bf16_kernel(BwdParams p) {
+    constexpr int NT = GPASS_THREADS;
     extern __shared__ float smem[];
     U16 *sQ = reinterpret_cast<U16 *>(smem);  // + plane * PLANE_B
-    U16 *sG = sQ + 2 * PLANE_B;               // + plane * PLANE_B
-    U16 *sS = sG + 2 * PLANE_B;               // + plane * GSNAP_ROWS * PB
+    U16 *sG = sQ + 2 * PLANE_B;               // + (2 m + plane) * PLANE_B
+    U16 *sS = sG + 2 * M * PLANE_B;           // + (2 m + plane) * GSNAP_ROWS * PB
 
     const qpam_scan_args &a = p.a;
-    // the halves of a chain are n_chains blocks apart (same XCD when 8 | B H)
-    const int n_chains = a.M * a.B * a.H;
-    const int chain = blockIdx.x % n_chains, half = blockIdx.x / n_chains;
-    const int bh = chain % (a.B * a.H), m = chain / (a.B * a.H);
+    // the halves of a (b, h) are B H blocks apart (same XCD when 8 | B H)
+    const int n_bh = a.B * a.H;
+    const int bh = blockIdx.x % n_bh, half = blockIdx.x / n_bh;
     const int b = bh / a.H, h = bh % a.H;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int it = 2 * half + (w & 1), jh = w >> 1;
+    const int it = 2 * half + (w & 1), jt = w >> 1;
     const int yc0 = 32 * half;  // dY columns of this block's value rows
     const int n = p.n_chunks;
-    const float *gbase = a.gamma + m * a.sg_m + b * a.sg_b + h * a.sg_h;
-    const float *rbr = a.rot_re ? a.rot_re + m * a.sr_m + b * a.sr_b + h * a.sr_h : nullptr;
-    const float *rbi = a.rot_im ? a.rot_im + m * a.sr_m + b * a.sr_b + h * a.sr_h : nullptr;
     const U16 *qre = (const U16 *)a.q.re + b * a.q.s0 + h * a.q.s1, *qim = (const U16 *)a.q.im + b * a.q.s0 + h * a.q.s1;
     // dY planes: fp32, or bf16 when DYBF (the same element offsets)
     using YT = typename std::conditional<DYBF, U16, float>::type;
     const YT *yre = (const YT *)p.dy.re + b * p.dy.s0 + h * p.dy.s1;
     const YT *yim = (const YT *)p.dy.im + b * p.dy.s0 + h * p.dy.s1;
     const bool need_ds0 = p.ds0_re != nullptr;
-    // rotations are read from gamma when absent (and replaced by 1 + 0i when staged)
-    const float *rsrc_r = rbr ? rbr : gbase, *rsrc_i = rbi ? rbi : gbase;
-    const int64_t rst_r = rbr ? a.sr_t : a.sg_t, rst_i = rbi ? a.sr_t : a.sg_t;
+    const bool has_rot = a.rot_re != nullptr;
+    // rotations are read from gamma when absent (and replaced by 1 + 0i when staged):
+    // the same memory operations on every path
+    const float *rsrc_r = has_rot ? a.rot_re : a.gamma, *rsrc_i = has_rot ? a.rot_im : a.gamma;
+    const int64_t rs_m = has_rot ? a.sr_m : a.sg_m, rs_b = has_rot ? a.sr_b : a.sg_b, rs_h = has_rot ? a.sr_h : a.sg_h,
+                  rs_t = has_rot ? a.sr_t : a.sg_t;
 
-    floatx4 gR[2], gI[2];  // dS[i][j], rows 16it + 4g + r, cols 16(2jh + jj) + l16
+    floatx4 gR[M], gI[M];  // dS_m[i][j], rows 16it + 4g + r, cols 16jt + l16
 #pragma unroll
-    for (int jj = 0; jj < 2; ++jj) {
-        gR[jj] = gI[jj] = zero4();
+    for (int m = 0; m < M; ++m) {
+        gR[m] = gI[m] = zero4();
         if (p.ds_re) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                gR[jj][r] = p.ds_re[o];
-                gI[jj][r] = p.ds_im[o];
+                const int64_t o = chain_idx(p, m, b, h) * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
+                gR[m][r] = p.ds_re[o];
+                gI[m][r] = p.ds_im[o];
             }
         }
     }
 
+    // this block's dY columns of a chunk: one 16-byte piece per thread and plane
+    // (bf16: the first 256 threads' pieces; the others load clamped in-bounds
+    // duplicates and store nothing)
+    constexpr int YNT = DYBF ? 256 : NT;
+    using YRegs = typename std::conditional<DYBF, BfTileRegs<YNT, 32>, F32TileRegs<YNT, 32>>::type;
     struct ChunkRegs {
+        YRegs yr, yi;
         BfTileRegs<NT> qr, qi;
-        float gam, rr, ri, tot;
+        float gam[M], rr[M], ri[M], tot[M];
     };
     ChunkRegs cr0, cr1;
-    float tot_cur = 1.f;  // total decay of the chunk staged last (the one the next step processes)
-    // this block's dY columns of the next chunk (one set)
-    typename std::conditional<DYBF, BfTileRegs<NT, 32>, F32TileRegs<NT, 32>>::type yr, yi;
-    auto load_dy = [&](int c) {
+    float tot_cur[M];  // total decays of the chunk staged last (the one the next step processes)
+#pragma unroll
+    for (int m = 0; m < M; ++m) tot_cur[m] = 1.f;
+    auto load_chunk = [&](int c, ChunkRegs &x) {
         const int c0 = c * 64, valid = min(64, a.T - c0);
         const int64_t yo = (int64_t)c0 * p.dy.s2;
         if constexpr (DYBF) {
-            tile_load_bf<NT, 32>(yr, yre + yo, p.dy.s2, valid, yc0);
-            tile_load_bf<NT, 32>(yi, yim + yo, p.dy.s2, valid, yc0);
+            tile_load_bf<YNT, 32>(x.yr, yre + yo, p.dy.s2, valid, yc0);
+            tile_load_bf<YNT, 32>(x.yi, yim + yo, p.dy.s2, valid, yc0);
         } else {
-            tile_load_f32<NT, 32>(yr, yre + yo, p.dy.s2, valid, yc0);
-            tile_load_f32<NT, 32>(yi, yim + yo, p.dy.s2, valid, yc0);
+            tile_load_f32<YNT, 32>(x.yr, yre + yo, p.dy.s2, valid, yc0);
+            tile_load_f32<YNT, 32>(x.yi, yim + yo, p.dy.s2, valid, yc0);
         }
-    };
-    auto load_chunk = [&](int c, ChunkRegs &x) {
-        const int c0 = c * 64, valid = min(64, a.T - c0);
         const int64_t qo = (int64_t)c0 * a.q.s2;
         tile_load_bf<NT>(x.qr, qre + qo, a.q.s2, valid);
         tile_load_bf<NT>(x.qi, qim + qo, a.q.s2, valid);
         const int64_t t = c0 + min(lane, valid - 1);
-        x.gam = gbase[t * a.sg_t];
-        x.rr = rsrc_r[t * rst_r];
-        x.ri = rsrc_i[t * rst_i];
-        // a vector load (lane-dependent address; lane 0's value is taken when the
-        // chunk is staged): a scalar load would share the LDS counter, and the next
-        // LDS wait would wait for it too
-        x.tot = p.totals[chain_idx(p, m, b, h) * p.n_chunks + max(c - (lane & 1), 0)];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            x.gam[m] = a.gamma[m * a.sg_m + b * a.sg_b + h * a.sg_h + t * a.sg_t];
+            const int64_t ro = m * rs_m + b * rs_b + h * rs_h + t * rs_t;
+            x.rr[m] = rsrc_r[ro];
+            x.ri[m] = rsrc_i[ro];
+            // a vector load (lane-dependent address; lane 0's value is taken when the
+            // chunk is staged): a scalar load would share the LDS counter, and the next
+            // LDS wait would wait for it too
+            x.tot[m] = p.totals[chain_idx(p, m, b, h) * p.n_chunks + max(c - (lane & 1), 0)];
+        }
     };
     auto stage_chunk = [&](int c, const ChunkRegs &x) {
         // nothing of the staging moves above this point: its first use of the staged
@@ -945,90 +953,85 @@ grad_pass_bf16_kernel(BwdParams p) {
         // memory counter completes in order, so a use hoisted to the top of the step
         // would also wait for everything loaded one step earlier
         __builtin_amdgcn_sched_barrier(0);
-        // conj(rho[t]) q_scale = conj(r[t]) cum[t] q_scale, lane t
         const int valid = min(64, a.T - c * 64);
-        tot_cur = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x.tot)));
-        float L = (lane < valid) ? logf(x.gam + LOG_EPS) : 0.f;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float y = __shfl_up(L, off);
-            if (lane >= off) L += y;
-        }
-        const float cum = (lane < valid) ? __expf(L) * a.q_scale : 0.f;
         tile_store_bf<NT>(sQ, x.qr);
         tile_store_bf<NT>(sQ + PLANE_B, x.qi);
-        if constexpr (DYBF)
-            tile_store_bf_cmul_as_bf<NT, 32>(sG, sG + PLANE_B, yr, yi, (rbr ? x.rr : 1.f) * cum,
-                                             -(rbi ? x.ri : 0.f) * cum, yc0);
-        else
-            tile_store_f32_cmul_as_bf<NT, 32>(sG, sG + PLANE_B, yr, yi, (rbr ? x.rr : 1.f) * cum,
-                                              -(rbi ? x.ri : 0.f) * cum, yc0);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            tot_cur[m] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x.tot[m])));
+            // conj(rho_m[t]) q_scale = conj(r_m[t]) cum_m[t] q_scale, lane t
+            float L = (lane < valid) ? logf(x.gam[m] + LOG_EPS) : 0.f;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const float y = __shfl_up(L, off);
+                if (lane >= off) L += y;
+            }
+            const float cum = (lane < valid) ? __expf(L) * a.q_scale : 0.f;
+            const float wr = (has_rot ? x.rr[m] : 1.f) * cum, wi = -(has_rot ? x.ri[m] : 0.f) * cum;
+            U16 *gr = sG + 2 * m * PLANE_B, *gi = gr + PLANE_B;
+            if constexpr (DYBF) {
+                if (tid < YNT) tile_store_bf_cmul_as_bf<YNT, 32>(gr, gi, x.yr, x.yi, wr, wi, yc0);
+            } else {
+                tile_store_f32_cmul_as_bf<YNT, 32>(gr, gi, x.yr, x.yi, wr, wi, yc0);
+            }
+        }
     };
 
-    // reverse order: step k handles chunk c = n-1-k; chunk c - 2 is loaded into
-    // register set k & 1 and staged at the end of step k + 1 (one LDS buffer, staged
-    // between two barriers)
+    // reverse order: step k handles chunk c = n-1-k; chunk c - 2 (dY, Q, gammas,
+    // rotations, totals) is loaded into register set k & 1 and staged at the end of
+    // step k + 1 (one LDS buffer, staged between two barriers)
     auto step = [&](int k, ChunkRegs &mine, ChunkRegs &next) {
         const int c = n - 1 - k;
         // unconditional (chunk 0 is re-read near the end): the same memory operation
-        // count on every path keeps the compiler's waits for the staged set exact.
-        // dY first: the stage at the end of this step waits for it, and the memory
-        // counter completes in order, so Q behind it stays in flight
-        load_dy(max(c - 1, 0));
+        // count on every path keeps the compiler's waits for the staged set exact
         load_chunk(max(c - 2, 0), mine);
-        // bf16 snapshot of dS after chunk c: into LDS now, to global memory as
+        // bf16 snapshots of dS after chunk c: into LDS now, to global memory as
         // 16-byte row pieces after the next barrier
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-            acc_store_bf_pairs<PB>(sS, sS + GSNAP_ROWS * PB, gR[jj], gI[jj], 16 * (w & 1), 16 * (2 * jh + jj));
+        for (int m = 0; m < M; ++m)
+            acc_store_bf_pairs<PB>(sS + 2 * m * GSNAP_ROWS * PB, sS + (2 * m + 1) * GSNAP_ROWS * PB, gR[m], gI[m],
+                                   16 * (w & 1), 16 * jt);
         if (c > 0 || need_ds0) {
             // dG rows (value i) x cols (key j): A = (conj(rho) q_scale dY)^T, B = Q (k = t)
-            floatx4 accR[2], accI[2];
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj) accR[jj] = accI[jj] = zero4();
             const U16 *Qr = sQ, *Qi = sQ + PLANE_B;
-            const U16 *Gr = sG, *Gi = sG + PLANE_B;
 #pragma unroll
-            for (int kp = 0; kp < 2; ++kp) {
-                const int t0 = 32 * kp + 8 * g;
-                const bf16x8 ar = ld_tr(Gr, t0, t0 + 4, 16 * it), ai = ld_tr(Gi, t0, t0 + 4, 16 * it),
-                             nar = neg_bf(ar);
+            for (int m = 0; m < M; ++m) {
+                const U16 *Gr = sG + 2 * m * PLANE_B, *Gi = Gr + PLANE_B;
+                floatx4 accR = zero4(), accI = zero4();
 #pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    const int jt = 2 * jh + jj;
+                for (int kp = 0; kp < 2; ++kp) {
+                    const int t0 = 32 * kp + 8 * g;
+                    const bf16x8 ar = ld_tr(Gr, t0, t0 + 4, 16 * it), ai = ld_tr(Gi, t0, t0 + 4, 16 * it),
+                                 nar = neg_bf(ar);
                     const bf16x8 qr = ld_tr(Qr, t0, t0 + 4, 16 * jt), qi = ld_tr(Qi, t0, t0 + 4, 16 * jt);
-                    accR[jj] = mfma_bf(ar, qr, accR[jj]);
-                    accR[jj] = mfma_bf(ai, qi, accR[jj]);
-                    accI[jj] = mfma_bf(ai, qr, accI[jj]);
-                    accI[jj] = mfma_bf(nar, qi, accI[jj]);
+                    accR = mfma_bf(ar, qr, accR);
+                    accR = mfma_bf(ai, qi, accR);
+                    accI = mfma_bf(ai, qr, accI);
+                    accI = mfma_bf(nar, qi, accI);
                 }
-            }
-            const float tot = tot_cur;  // chunk c's total, loaded two steps ahead
-#pragma unroll
-            for (int jj = 0; jj < 2; ++jj)
+                const float tot = tot_cur[m];  // chunk c's total, loaded two steps ahead
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    gR[jj][r] = tot * gR[jj][r] + accR[jj][r];
-                    gI[jj][r] = tot * gI[jj][r] + accI[jj][r];
+                    gR[m][r] = tot * gR[m][r] + accR[r];
+                    gI[m][r] = tot * gI[m][r] + accI[r];
                 }
+            }
         }
-        // also unconditional: past the end, chunk 0 (which `next` and the dY registers
-        // then hold) is staged again
+        // also unconditional: past the end, chunk 0 (which `next` then holds) is
+        // staged again
         __syncthreads();
-        {  // the snapshot rows: 32 bytes per thread
-            const int pl = tid >> 7, row = (tid & 127) >> 2, q = tid & 3;
-            const uint4 *src = reinterpret_cast<const uint4 *>(sS + pl * GSNAP_ROWS * PB + row * PB + 16 * q);
-            const uint4 v0 = src[0], v1 = src[1];
-            uint4 *dst = reinterpret_cast<uint4 *>(gsnap(p, m, b, h, c) + pl * D * D + (GSNAP_ROWS * half + row) * D +
-                                                   16 * q);
-            dst[0] = v0;
-            dst[1] = v1;
+        {  // the snapshot rows: 16 bytes per thread and state
+            const int pl = tid >> 8, row = (tid & 255) >> 3, q = tid & 7;
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                const uint4 v = *reinterpret_cast<const uint4 *>(sS + (2 * m + pl) * GSNAP_ROWS * PB + row * PB + 8 * q);
+                *reinterpret_cast<uint4 *>(gsnap(p, m, b, h, c) + pl * D * D + (GSNAP_ROWS * half + row) * D + 8 * q) = v;
+            }
         }
         stage_chunk(max(c - 1, 0), next);
         __syncthreads();
     };
     load_chunk(n - 1, cr0);
-    load_dy(n - 1);
     load_chunk(max(n - 2, 0), cr1);
     stage_chunk(n - 1, cr0);
     __syncthreads();
@@ -1041,12 +1044,12 @@ grad_pass_bf16_kernel(BwdParams p) {
     if (k < n) step(k, cr0, cr1);
     if (need_ds0) {
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
+        for (int m = 0; m < M; ++m)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)chain * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * (2 * jh + jj) + l16;
-                p.ds0_re[o] = gR[jj][r];
-                p.ds0_im[o] = gI[jj][r];
+                const int64_t o = chain_idx(p, m, b, h) * D * D + (int64_t)(16 * it + 4 * g + r) * D + 16 * jt + l16;
+                p.ds0_re[o] = gR[m][r];
+                p.ds0_im[o] = gI[m][r];
             }
     }
 }
@@ -1734,19 +1737,19 @@ template <int M>
 int launch_bwd_bf16_m(const BwdParams &p, hipStream_t stream) {
     const qpam_scan_args &a = p.a;
     dim3 grid(p.n_chunks, a.H, a.B);
-    const size_t s1 = gpass_bf16_smem(), s3 = chunk_grad_bf16_smem<M>();
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel<false>,
+    const size_t s1 = gpass_bf16_smem<M>(), s3 = chunk_grad_bf16_smem<M>();
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel<M, false>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
-    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel<true>,
+    QPAM_CHECK_HIP(hipFuncSetAttribute((const void *)grad_pass_bf16_kernel<M, true>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)s1));
     const void *ck = p.dy_bf16 ? (const void *)chunk_grad_bf16_kernel<M, true>
                                : (const void *)chunk_grad_bf16_kernel<M, false>;
     QPAM_CHECK_HIP(hipFuncSetAttribute(ck, hipFuncAttributeMaxDynamicSharedMemorySize, (int)s3));
     // the gradient-state pass (sequential chains) writes dS after every chunk;
     // the chunk pass then forms every gradient of the chunk
-    const dim3 pg(PASS_SPLIT * a.M * a.B * a.H);
-    if (p.dy_bf16) hipLaunchKernelGGL(grad_pass_bf16_kernel<true>, pg, dim3(PASS_THREADS), s1, stream, p);
-    else hipLaunchKernelGGL(grad_pass_bf16_kernel<false>, pg, dim3(PASS_THREADS), s1, stream, p);
+    const dim3 pg(PASS_SPLIT * a.B * a.H);
+    if (p.dy_bf16) hipLaunchKernelGGL((grad_pass_bf16_kernel<M, true>), pg, dim3(GPASS_THREADS), s1, stream, p);
+    else hipLaunchKernelGGL((grad_pass_bf16_kernel<M, false>), pg, dim3(GPASS_THREADS), s1, stream, p);
     int st = launch_status("grad_pass_bf16_kernel");
     if (st) return st;
     if (p.dy_bf16) hipLaunchKernelGGL((chunk_grad_bf16_kernel<M, true>), grid, dim3(THREADS), s3, stream, p);

@@ -411,6 +411,22 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
     }
     TileRegs xr;
     tile_fetch(xr, a.k, b, h, 0, min(CH, a.T), tid, 1.f);
+    // V of this lane's W elements and the T blocks of the chunk: loaded one chunk ahead
+    float vr4[4], vi4[4];
+    OpRegs opT;
+    auto fetch_vt = [&](int c) {
+        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        const float *vre = static_cast<const float *>(a.v.re) + b * a.v.s0 + h * a.v.s1 + i0 + l16;
+        const float *vim = static_cast<const float *>(a.v.im) + b * a.v.s0 + h * a.v.s1 + i0 + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t o = (int64_t)(t0 + min(16 * w + 4 * g + r, valid - 1)) * a.v.s2;
+            vr4[r] = vre[o];
+            vi4[r] = vim[o];
+        }
+        ops_fetch(opT, prep + chunk_prep(chain, n_chunks, c) + PREP_T, w, lane);
+    };
+    fetch_vt(0);
     float lnext = prep[chunk_prep(chain, n_chunks, 0) + PREP_L + lane];
     float bnext = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)min(lane, a.T - 1) * a.sg_t];
     int cur = 0;
@@ -426,18 +442,6 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
         __syncthreads();
         tile_fetch(xr, a.q, b, h, t0, valid, tid, a.q_scale);  // in flight through the state work
         OpRegs ops;
-        ops_fetch(ops, prep + pc + PREP_T, w, lane);
-        float vr4[4], vi4[4];  // V of this lane's W elements
-        {
-            const float *vre = static_cast<const float *>(a.v.re) + b * a.v.s0 + h * a.v.s1 + i0 + l16;
-            const float *vim = static_cast<const float *>(a.v.im) + b * a.v.s0 + h * a.v.s1 + i0 + l16;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t o = (int64_t)(t0 + min(16 * w + 4 * g + r, valid - 1)) * a.v.s2;
-                vr4[r] = vre[o];
-                vi4[r] = vim[o];
-            }
-        }
         const int t = 16 * w + l16;  // this lane's row in A-operand reads
         // W[t][i] = beta_t (v_t[i] - alpha_t (K S^T)[t][i]), row tile w
         floatx4 ar, ai;
@@ -471,7 +475,7 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
 #pragma unroll
                 for (int ks = 0; ks < 4; ++ks) {
                     const int s = 16 * cc + 4 * ks + g;
-                    gstep(x, ops.re[cc][ks], ops.im[cc][ks], sUr[s * SP + l16], sUi[s * SP + l16]);
+                    gstep(x, opT.re[cc][ks], opT.im[cc][ks], sUr[s * SP + l16], sUi[s * SP + l16]);
                 }
             }
             ur = gre(x);
@@ -532,6 +536,7 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
         if (c + 1 < n_chunks) {
             const int v1 = min(CH, a.T - t0 - CH);
             tile_fetch(xr, a.k, b, h, t0 + CH, v1, tid, 1.f);
+            fetch_vt(c + 1);
             lnext = prep[chunk_prep(chain, n_chunks, c + 1) + PREP_L + lane];
             bnext = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)(t0 + CH + min(lane, v1 - 1)) * a.sg_t];
         }

@@ -85,11 +85,16 @@ __device__ __forceinline__ floatx4 mfma4(float a, float b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Complex 16 x 16 blocks in the prep kernel's LDS: rows of LP floats (one pad
+// float: the MFMA A-operand reads step the 16 lanes of a group over rows, which a
+// pitch of 16 would put on one bank in four), re plane then im plane (LPL apart).
+constexpr int LP = 17, LPL = 16 * LP, LBLK = 2 * LPL;
+
 __device__ __forceinline__ void blk_store(float *dst, const floatx4 &cr, const floatx4 &ci, int l16, int g) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        dst[(4 * g + r) * 16 + l16] = cr[r];
-        dst[256 + (4 * g + r) * 16 + l16] = ci[r];
+        dst[(4 * g + r) * LP + l16] = cr[r];
+        dst[LPL + (4 * g + r) * LP + l16] = ci[r];
     }
 }
 
@@ -103,7 +108,7 @@ __device__ __forceinline__ void blk_export(float *dst, const float *src, int tid
     for (int e = tid; e < 512; e += nthreads) {
         const int pl = e >> 8, idx = e & 255, ln = idx >> 2, ks = idx & 3;
         const int row = ln & 15, gg = ln >> 4;
-        dst[e] = src[pl * 256 + row * 16 + 4 * ks + gg];
+        dst[e] = src[pl * LPL + row * LP + 4 * ks + gg];
     }
 }
 
@@ -129,13 +134,13 @@ __device__ __forceinline__ void blk_mul_g(Gauss &x, const float *A, const float 
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
         const int k = 4 * ks + g;
-        gstep(x, A[l16 * 16 + k], A[256 + l16 * 16 + k], B[k * 16 + l16], B[256 + k * 16 + l16]);
+        gstep(x, A[l16 * LP + k], A[LPL + l16 * LP + k], B[k * LP + l16], B[LPL + k * LP + l16]);
     }
 }
 // element (4g + r, l16) of an LDS block, re and im
-__device__ __forceinline__ float blk_re(const float *A, int g, int r, int l16) { return A[(4 * g + r) * 16 + l16]; }
+__device__ __forceinline__ float blk_re(const float *A, int g, int r, int l16) { return A[(4 * g + r) * LP + l16]; }
 __device__ __forceinline__ float blk_im(const float *A, int g, int r, int l16) {
-    return A[256 + (4 * g + r) * 16 + l16];
+    return A[LPL + (4 * g + r) * LP + l16];
 }
 
 // The prep block's LDS: K and q_scale Q of the chunk while the Gram and
@@ -143,15 +148,15 @@ __device__ __forceinline__ float blk_im(const float *A, int g, int r, int l16) {
 // scratch blocks of the diagonal inversion, whose first three blocks later hold
 // the partial sums of the blocks below the diagonal (two blocks per CU).
 constexpr int PREP_KQ = 4 * CH * KP;
-constexpr int PREP_INV = NBLK * BLK * 2 + 16 * BLK;
+constexpr int PREP_INV = NBLK * LBLK * 2 + 16 * LBLK;
 constexpr size_t PREP_SMEM = (size_t)((PREP_KQ > PREP_INV ? PREP_KQ : PREP_INV) + 2 * CH) * sizeof(float);
 
 __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, float *prep, int n_chunks) {
     extern __shared__ float sm[];
     float *sKr = sm, *sKi = sKr + CH * KP, *sQr = sKi + CH * KP, *sQi = sQr + CH * KP;
     float *sM = sm;                // after the products: M blocks [blk][re | im][16][16] (diagonal included)
-    float *sT = sM + NBLK * BLK;   // T blocks
-    float *sX = sT + NBLK * BLK;   // four scratch blocks per wave
+    float *sT = sM + NBLK * LBLK;  // T blocks
+    float *sX = sT + NBLK * LBLK;  // four scratch blocks per wave
     float *sR = sX;                // after the inversion: three partial sums
     const int big = PREP_KQ > PREP_INV ? PREP_KQ : PREP_INV;
     float *sL = sm + big, *sB = sL + CH;
@@ -220,15 +225,15 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
         const int bb = (bk >= 1) + (bk >= 3) + (bk >= 6), cc = bk - bb * (bb + 1) / 2;
         const floatx4 xr = gre(acc[it]), xi = gim(acc[it]);
         if (kind == 0) {
-            float *Mb = sM + bk * BLK;
+            float *Mb = sM + bk * LBLK;
             floatx4 gr, gi;  // D.Gk for the backward
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 16 * bb + 4 * g + r, s = 16 * cc + l16;
                 const float dts = s < t ? __expf(fminf(sL[t] - sL[s], 0.f)) : 0.f;
                 const float m = sB[t] * dts;
-                Mb[(4 * g + r) * 16 + l16] = m * xr[r];
-                Mb[256 + (4 * g + r) * 16 + l16] = m * xi[r];
+                Mb[(4 * g + r) * LP + l16] = m * xr[r];
+                Mb[LPL + (4 * g + r) * LP + l16] = m * xi[r];
                 gr[r] = dts * xr[r];
                 gi[r] = dts * xi[r];
             }
@@ -267,18 +272,18 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
     }
     __syncthreads();
     {  // T_bb = (I + N)^{-1} = (I - N)(I + N^2)(I + N^4)(I + N^8), N = M_bb nilpotent (N^16 = 0); wave b
-        const float *N = sM + blk(w, w) * BLK;
-        float *X = sX + w * 4 * BLK;  // N^2, N^4, N^8, P1 (then P2 over N^2)
+        const float *N = sM + blk(w, w) * LBLK;
+        float *X = sX + w * 4 * LBLK;  // N^2, N^4, N^8, P1 (then P2 over N^2)
         Gauss x;
         gz(x);
         blk_mul_g(x, N, N, l16, g);
         blk_store(X, gre(x), gim(x), l16, g);
         gz(x);
         blk_mul_g(x, X, X, l16, g);
-        blk_store(X + BLK, gre(x), gim(x), l16, g);
+        blk_store(X + LBLK, gre(x), gim(x), l16, g);
         gz(x);
-        blk_mul_g(x, X + BLK, X + BLK, l16, g);
-        blk_store(X + 2 * BLK, gre(x), gim(x), l16, g);
+        blk_mul_g(x, X + LBLK, X + LBLK, l16, g);
+        blk_store(X + 2 * LBLK, gre(x), gim(x), l16, g);
         // P1 = I - N + N^2 - N N^2
         gz(x);
         blk_mul_g(x, N, X, l16, g);
@@ -289,23 +294,23 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
                 pr[r] += (4 * g + r == l16 ? 1.f : 0.f) - blk_re(N, g, r, l16) + blk_re(X, g, r, l16);
                 pi[r] += -blk_im(N, g, r, l16) + blk_im(X, g, r, l16);
             }
-            blk_store(X + 3 * BLK, pr, pi, l16, g);
+            blk_store(X + 3 * LBLK, pr, pi, l16, g);
         }
         // P2 = P1 + P1 N^4 (over N^2)
         gz(x);
-        blk_mul_g(x, X + 3 * BLK, X + BLK, l16, g);
+        blk_mul_g(x, X + 3 * LBLK, X + LBLK, l16, g);
         {
             floatx4 pr = gre(x), pi = gim(x);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                pr[r] += blk_re(X + 3 * BLK, g, r, l16);
-                pi[r] += blk_im(X + 3 * BLK, g, r, l16);
+                pr[r] += blk_re(X + 3 * LBLK, g, r, l16);
+                pi[r] += blk_im(X + 3 * LBLK, g, r, l16);
             }
             blk_store(X, pr, pi, l16, g);
         }
         // T = P2 + P2 N^8
         gz(x);
-        blk_mul_g(x, X, X + 2 * BLK, l16, g);
+        blk_mul_g(x, X, X + 2 * LBLK, l16, g);
         {
             floatx4 pr = gre(x), pi = gim(x);
 #pragma unroll
@@ -313,7 +318,7 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
                 pr[r] += blk_re(X, g, r, l16);
                 pi[r] += blk_im(X, g, r, l16);
             }
-            blk_store(sT + blk(w, w) * BLK, pr, pi, l16, g);
+            blk_store(sT + blk(w, w) * LBLK, pr, pi, l16, g);
         }
     }
     __syncthreads();
@@ -324,27 +329,27 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
         if (mine) {
             Gauss x;
             gz(x);
-            for (int k = cc; k < bb; ++k) blk_mul_g(x, sM + blk(bb, k) * BLK, sT + blk(k, cc) * BLK, l16, g);
-            blk_store(sR + w * BLK, gre(x), gim(x), l16, g);
+            for (int k = cc; k < bb; ++k) blk_mul_g(x, sM + blk(bb, k) * LBLK, sT + blk(k, cc) * LBLK, l16, g);
+            blk_store(sR + w * LBLK, gre(x), gim(x), l16, g);
         }
         __syncthreads();
         if (mine) {
             Gauss x;
             gz(x);
-            blk_mul_g(x, sT + blk(bb, bb) * BLK, sR + w * BLK, l16, g);
-            blk_store(sT + blk(bb, cc) * BLK, -gre(x), -gim(x), l16, g);
+            blk_mul_g(x, sT + blk(bb, bb) * LBLK, sR + w * LBLK, l16, g);
+            blk_store(sT + blk(bb, cc) * LBLK, -gre(x), -gim(x), l16, g);
         }
         __syncthreads();
     }
     for (int k = 0; k < NBLK; ++k)
-        blk_export(prep + chunk_prep(chain, n_chunks, c) + PREP_T + k * BLK, sT + k * BLK, tid, 256);
+        blk_export(prep + chunk_prep(chain, n_chunks, c) + PREP_T + k * BLK, sT + k * LBLK, tid, 256);
     if (wrec) {
         // T^H in A-operand order: block (rows cc, cols bb) of T^H, element (x, 4 ks + g) =
         // conj(T_(bb, cc)[4 ks + g][x]), stored at T's block index
         for (int e = tid; e < NBLK * BLK; e += 256) {
             const int k = e >> 9, pl = (e >> 8) & 1, idx = e & 255, ln = idx >> 2, ks = idx & 3;
             const int row = ln & 15, gg = ln >> 4;
-            const float v = sT[k * BLK + pl * 256 + (4 * ks + gg) * 16 + row];
+            const float v = sT[k * LBLK + pl * LPL + (4 * ks + gg) * LP + row];
             wrec[WS_TH + e] = pl ? -v : v;
         }
     }

@@ -908,9 +908,10 @@ __global__ void __launch_bounds__(GPASS_THREADS) grad_pass_bf16_kernel(BwdParams
     }
 
     // this block's dY columns of a chunk: one 16-byte piece per thread and plane
-    // (bf16: the first 256 threads' pieces; the others load clamped in-bounds
-    // duplicates and store nothing)
+    // (bf16: 256 pieces, held by threads t and t + 256 alike; the two halves of the
+    // block then stage alternate states)
     constexpr int YNT = DYBF ? 256 : NT;
+    const int ytid = tid & (YNT - 1);
     using YRegs = typename std::conditional<DYBF, BfTileRegs<YNT, 32>, F32TileRegs<YNT, 32>>::type;
     struct ChunkRegs {
         YRegs yr, yi;
@@ -925,8 +926,9 @@ __global__ void __launch_bounds__(GPASS_THREADS) grad_pass_bf16_kernel(BwdParams
         const int c0 = c * 64, valid = min(64, a.T - c0);
         const int64_t yo = (int64_t)c0 * p.dy.s2;
         if constexpr (DYBF) {
-            tile_load_bf<YNT, 32>(x.yr, yre + yo, p.dy.s2, valid, yc0);
-            tile_load_bf<YNT, 32>(x.yi, yim + yo, p.dy.s2, valid, yc0);
+            const int r = min(ytid >> 2, valid - 1), c8 = ytid & 3;
+            x.yr.v[0] = *reinterpret_cast<const uintx4 *>(yre + yo + (int64_t)r * p.dy.s2 + yc0 + 8 * c8);
+            x.yi.v[0] = *reinterpret_cast<const uintx4 *>(yim + yo + (int64_t)r * p.dy.s2 + yc0 + 8 * c8);
         } else {
             tile_load_f32<YNT, 32>(x.yr, yre + yo, p.dy.s2, valid, yc0);
             tile_load_f32<YNT, 32>(x.yi, yim + yo, p.dy.s2, valid, yc0);
@@ -957,8 +959,10 @@ __global__ void __launch_bounds__(GPASS_THREADS) grad_pass_bf16_kernel(BwdParams
         tile_store_bf<NT>(sQ, x.qr);
         tile_store_bf<NT>(sQ + PLANE_B, x.qi);
 #pragma unroll
+        for (int m = 0; m < M; ++m) tot_cur[m] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x.tot[m])));
+#pragma unroll
         for (int m = 0; m < M; ++m) {
-            tot_cur[m] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x.tot[m])));
+            if (DYBF && (tid >> 8) != (m & 1)) continue;  // (bf16: the other half stages state m)
             // conj(rho_m[t]) q_scale = conj(r_m[t]) cum_m[t] q_scale, lane t
             float L = (lane < valid) ? logf(x.gam[m] + LOG_EPS) : 0.f;
 #pragma unroll
@@ -970,7 +974,12 @@ __global__ void __launch_bounds__(GPASS_THREADS) grad_pass_bf16_kernel(BwdParams
             const float wr = (has_rot ? x.rr[m] : 1.f) * cum, wi = -(has_rot ? x.ri[m] : 0.f) * cum;
             U16 *gr = sG + 2 * m * PLANE_B, *gi = gr + PLANE_B;
             if constexpr (DYBF) {
-                if (tid < YNT) tile_store_bf_cmul_as_bf<YNT, 32>(gr, gi, x.yr, x.yi, wr, wi, yc0);
+                const int r = ytid >> 2, o = r * PB + yc0 + 8 * (ytid & 3);
+                const float wr_ = __shfl(wr, r), wi_ = __shfl(wi, r);
+                const floatx8 ya = to_f(__builtin_bit_cast(bf16x8, x.yr.v[0]));
+                const floatx8 yb = to_f(__builtin_bit_cast(bf16x8, x.yi.v[0]));
+                *reinterpret_cast<bf16x8 *>(gr + o) = to_bf(wr_ * ya - wi_ * yb);
+                *reinterpret_cast<bf16x8 *>(gi + o) = to_bf(wr_ * yb + wi_ * ya);
             } else {
                 tile_store_f32_cmul_as_bf<YNT, 32>(gr, gi, x.yr, x.yi, wr, wi, yc0);
             }

@@ -601,9 +601,10 @@ def bench_delta(steps, warmup, reference=True):
     """E2 delta rule forward + backward at the config-3 shape (one state: B=8,
     T=2048, H=12, d=64, fp32): the HIP kernels against the reference's chunked
     UT-transform steps (delta_chunk 64) run in torch on the same GPU.  The
-    kernels are a sequential recurrence per (b, h) chain: `us_per_token` is
-    the forward's time per token step, the bound that matters; achieved HBM
-    traffic (inputs, outputs, checkpoints) is reported beside it."""
+    kernels walk the chunks of each (b, h) chain in sequence (forward, and the
+    backward's state-gradient pass): `us_per_token` is the forward's time per
+    token step; achieved HBM traffic (inputs, outputs, the backward's
+    per-chunk records) is reported beside it."""
     import torch
     from qllm2_amd.pam_delta import delta_planar
     B, H, T, d = 8, 12, 2048, 64

@@ -7,7 +7,9 @@ _recur_step_delta (:967-1002).  Both compute the token recurrence
     S <- g~ S;  u = beta (v - S k);  S <- S + u (x) k*;  y = S q~
 
 with g~ = gamma + 1e-6 in the chunked form (its log(gamma + 1e-6) decays) and
-g~ = gamma in the single step; the kernels run that recurrence directly (fp32).
+g~ = gamma in the single step; the kernels compute the chunked form itself on
+fp32 MFMA, forward and backward (its clamped decay matrix and state-write
+weights included).
 
 `delta_planar` is differentiable (torch.library custom op with a registered
 autograd formula); `forward_delta` and `recur_step_delta` keep the reference
@@ -67,7 +69,7 @@ def _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale
 @torch.library.custom_op("qpam::delta_fwd", mutates_args=())
 def delta_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Tensor, v_im: Tensor,
                  gamma: Tensor, beta: Tensor, s0_re: Optional[Tensor], s0_im: Optional[Tensor], q_scale: float,
-                 gamma_eps: float, keep_checkpoints: bool) -> List[Tensor]:
+                 gamma_eps: float, keep_workspace: bool) -> List[Tensor]:
     """Returns [y_re, y_im ([B,H,T,d] fp32), s_re, s_im ([B,H,d,d]), workspace]."""
     a, keep = _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps)
     B, H, T, d = q_re.shape
@@ -79,7 +81,7 @@ def delta_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: T
     a.y = _mview(y_re, y_im)
     a.s_re, a.s_im = s_re.data_ptr(), s_im.data_ptr()
     L = _lib.lib()
-    if keep_checkpoints:
+    if keep_workspace:
         nbytes = L.qpam_delta_workspace_size(a)
         ws = torch.empty((nbytes + 3) // 4, device=dev, dtype=torch.float32)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
@@ -113,11 +115,11 @@ def _ws_bytes(B, H, T, d=64):
 
 
 @delta_fwd_op.register_fake
-def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, keep_checkpoints):
+def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, keep_workspace):
     B, H, T, d = q_re.shape
     y = q_re.new_empty(B, H, T, d, dtype=torch.float32)
     s = q_re.new_empty(B, H, d, d, dtype=torch.float32)
-    ws = q_re.new_empty(_ws_bytes(B, H, T, d) // 4 if keep_checkpoints else 0, dtype=torch.float32)
+    ws = q_re.new_empty(_ws_bytes(B, H, T, d) // 4 if keep_workspace else 0, dtype=torch.float32)
     return [y, torch.empty_like(y), s, torch.empty_like(s), ws]
 
 
@@ -174,16 +176,16 @@ def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, ga
 
 
 def _setup(ctx, inputs, output):
-    (q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, keep_ckpt) = inputs
+    (q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, keep_ws) = inputs
     ctx.save_for_backward(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, output[4])
-    ctx.q_scale, ctx.gamma_eps, ctx.keep = q_scale, gamma_eps, keep_ckpt
+    ctx.q_scale, ctx.gamma_eps, ctx.keep = q_scale, gamma_eps, keep_ws
     ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, grads):
     q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, ws = ctx.saved_tensors
     if not ctx.keep:
-        raise RuntimeError("qpam delta: the forward ran without checkpoints (keep_checkpoints=False)")
+        raise RuntimeError("qpam delta: the forward ran without its backward workspace (keep_workspace=False)")
     dy_re, dy_im, ds_re, ds_im = grads[0], grads[1], grads[2], grads[3]
     if dy_re is None:
         dy_re = torch.zeros_like(q_re, dtype=torch.float32)

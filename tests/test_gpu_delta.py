@@ -58,7 +58,7 @@ NAMES = ["dq", "dk", "dv", "dgamma", "dbeta", "ds0"]
 def test_delta_matches_chunked_oracle(gpu_lib, T, with_s0, with_ds):
     """The reference's chunked UT-transform form (delta_chunk 64) in float64
     against the kernels with gamma + 1e-6: outputs, final state, all gradients;
-    ragged T (not a multiple of the 16-token checkpoint or 4-token sub-group)."""
+    ragged T (a partial last 64-step chunk, T below one chunk)."""
     B, H, d = 2, 3, 64
     q, k, v, g, b = D.make_delta_inputs(B, H, T, d, 600 + T)
     gen = torch.Generator().manual_seed(601 + T)
@@ -114,7 +114,7 @@ def test_delta_step_matches_reference_step(gpu_lib):
 
 
 def test_delta_long_sequence_properties(gpu_lib):
-    """T = 2048 (the config-3 length, 128 checkpoint groups), B=1, H=4: output
+    """T = 2048 (the config-3 length, 32 chunks), B=1, H=4: output
     and final state of the first head against the oracle's token recurrence."""
     from qllm2_amd.pam_delta import delta_planar
     B, H, T, d = 1, 4, 2048, 64

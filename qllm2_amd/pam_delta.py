@@ -208,10 +208,25 @@ delta_fwd_op.register_autograd(_backward, setup_context=_setup)
 
 
 def delta_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, *, q_scale, gamma_eps=CHUNK_EPS, s0=None):
-    """Differentiable delta-rule scan on planar [B,H,T,64] planes (computed in
-    fp32).  gamma, beta [B,H,T]; s0 optional (re, im) [B,H,64,64].  Returns
-    (y_re, y_im, s_re, s_im)."""
+    """Differentiable delta-rule scan on planar [B,H,T,d] planes, d <= 64
+    (computed in fp32).  gamma, beta [B,H,T]; s0 optional (re, im) [B,H,d,d].
+    Returns (y_re, y_im, s_re, s_im).
+
+    d < 64 is zero-padded to 64 and sliced back, which is exact: padded key
+    columns add nothing to k.k*, S k or q.k*, and padded value rows of the
+    update (beta (v - S k)) and of the state stay zero."""
     s0_re, s0_im = s0 if s0 is not None else (None, None)
+    d = q_re.shape[-1]
+    if d < 64:
+        pad = 64 - d
+        q_re, q_im, k_re, k_im, v_re, v_im = (torch.nn.functional.pad(x, (0, pad))
+                                              for x in (q_re, q_im, k_re, k_im, v_re, v_im))
+        if s0_re is not None:
+            s0_re, s0_im = (torch.nn.functional.pad(x, (0, pad, 0, pad)) for x in (s0_re, s0_im))
+        s0p = (s0_re, s0_im) if s0_re is not None else None
+        y_re, y_im, s_re, s_im = delta_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, q_scale=q_scale,
+                                              gamma_eps=gamma_eps, s0=s0p)
+        return y_re[..., :d], y_im[..., :d], s_re[..., :d, :d], s_im[..., :d, :d]
     keep = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im))
     out = delta_fwd_op(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, float(q_scale),

@@ -36,8 +36,8 @@ every mode:
   * decode steps whose inputs need gradients (a T = 1 forward in training, a
     state-carrying call under grad mode): the reference step is differentiable
     torch code, the HIP decode step updates the state in place;
-  * head dims and state counts the scan kernels do not take (head_dim not
-    dividing 64, more than 4 states).
+  * the E2 delta write with head dims above 64 (its key dim is one 64-wide
+    tile; smaller head dims are zero-padded).
 The HIP library itself has no CPU path: the replacements raise for GPU
 tensors if it cannot load.
 """
@@ -78,9 +78,10 @@ def _original(self, name):
 
 
 def _scan_covers(t, head_dim, n_states=1):
-    """True when the HIP scan takes this call: GPU tensor, head_dim dividing 64
-    (smaller ones are zero-padded), at most 4 states."""
-    return t.is_cuda and head_dim <= 64 and 64 % head_dim == 0 and n_states <= 4
+    """True when the HIP scan takes this call: a GPU tensor (every head dim and
+    state count: head dims below 64 are zero-padded, larger ones run as 64 x 64
+    state blocks, states beyond 4 in groups)."""
+    return t.is_cuda and head_dim >= 1 and n_states >= 1
 
 
 def _needs_grad(*ts):
@@ -156,8 +157,9 @@ def forward_multistate_fused(self, x, queries, keys, values, head_dim):
 
 def forward_delta(self, queries, keys, protected_values, decay_gamma, write_beta, head_dim):
     """V11PAMLayer._forward_delta (E2 delta write, head-scalar decay): the HIP
-    delta-rule kernels; per-channel decay or other head dims keep the original."""
-    if decay_gamma.dim() != 3 or head_dim != 64 or not queries.is_cuda:
+    delta-rule kernels (head dims up to 64); per-channel decay or larger head
+    dims keep the original."""
+    if decay_gamma.dim() != 3 or head_dim > 64 or not queries.is_cuda:
         return _original(self, "_forward_delta")(self, queries, keys, protected_values, decay_gamma, write_beta,
                                                  head_dim)
     return _delta.forward_delta(queries, keys, protected_values, decay_gamma, write_beta, head_dim)
@@ -166,7 +168,7 @@ def forward_delta(self, queries, keys, protected_values, decay_gamma, write_beta
 def recur_step_delta(self, memory_state, decay_gamma, value_t, key_t, query_t, write_beta_t):
     """V11PAMLayer._recur_step_delta (one decode token of the E2 write; the HIP
     step is differentiable)."""
-    if decay_gamma.dim() != 2 or memory_state.shape[-2] != 64 or not memory_state.is_cuda:
+    if decay_gamma.dim() != 2 or memory_state.shape[-2] > 64 or not memory_state.is_cuda:
         return _original(self, "_recur_step_delta")(self, memory_state, decay_gamma, value_t, key_t, query_t,
                                                     write_beta_t)
     return _delta.recur_step_delta(memory_state, decay_gamma, value_t, key_t, query_t, write_beta_t)

@@ -312,6 +312,9 @@ def _backward(ctx, grads):
 scan_fwd_op.register_autograd(_backward, setup_context=_setup_context)
 
 
+MAX_STATES = 4  # states one kernel call carries (the E3 kernels are built for M = 1..4)
+
+
 def pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, *, q_scale, chunk=64, rot=None, s0=None,
                     y_layout="bhtd"):
     """Differentiable planar scan.  Returns (y_re, y_im, s_re, s_im); y is
@@ -322,19 +325,32 @@ def pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, *, q_scale, chunk
     64): y is rounded once from the fp32 result and the gradient is read in
     bf16, which equals rounding an fp32 y afterwards and widening a bf16 dy.
 
-    Head dims below 64 are zero-padded to 64 (exact: padded key/query columns
-    add nothing to q.k*, padded value rows stay zero) and sliced back."""
+    Any head dim and state count (the reference's layer takes any, v11/model.py:45-97):
+      * d < 64 is zero-padded to 64 and sliced back (exact: padded key/query
+        columns add nothing to q.k*, padded value rows stay zero);
+      * d > 64 is padded to a multiple of 64 and split into 64 x 64 blocks of
+        the state: block (i, j) (value rows 64 i.., key columns 64 j..) evolves
+        on its own, S_ij <- gamma S_ij + v_i (x) conj(k_j), and y_i = sum_j S_ij q_j,
+        so the blocks run as n^2 heads of the d = 64 kernels and y sums over j;
+      * more than 4 states run in groups of at most 4 (Y is the sum of the
+        states' reads, the states are independent chains)."""
     layouts = {"bhtd": 0, "bthd": 1, "bt2hd": 2, "bt2hd_bf16": 3}
     if y_layout not in layouts:
         raise ValueError(f"y_layout must be one of {list(layouts)}")
     if y_layout == "bt2hd_bf16" and (q_re.dtype != torch.bfloat16 or chunk != 64):
         raise ValueError("y_layout 'bt2hd_bf16' needs bf16 q, k, v and chunk 64")
+    if gamma.dim() == 4 and gamma.shape[0] > MAX_STATES:
+        return _scan_state_groups(q_re, q_im, k_re, k_im, v_re, v_im, gamma, q_scale, chunk, rot, s0, y_layout)
+    if q_re.shape[-1] > 64:
+        return _scan_blocks(q_re, q_im, k_re, k_im, v_re, v_im, gamma, q_scale, chunk, rot, s0, y_layout)
     rot_re, rot_im = rot if rot is not None else (None, None)
     s0_re, s0_im = s0 if s0 is not None else (None, None)
     d = q_re.shape[-1]
+    if d < 64 and y_layout in ("bt2hd", "bt2hd_bf16"):
+        y_re, y_im, s_re, s_im = pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, q_scale=q_scale,
+                                                 chunk=chunk, rot=rot, s0=s0)
+        return _to_bt2hd(y_re, y_im, y_layout), None, s_re, s_im
     if d < 64:
-        if 64 % d:
-            raise NotImplementedError(f"head_dim {d}: the HIP scan pads head dims dividing 64")
         pad = 64 - d
         q_re, q_im, k_re, k_im, v_re, v_im = (torch.nn.functional.pad(x, (0, pad))
                                               for x in (q_re, q_im, k_re, k_im, v_re, v_im))
@@ -344,12 +360,93 @@ def pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, *, q_scale, chunk
                       float(q_scale), int(chunk), layouts[y_layout])
     y_re, y_im, s_re, s_im = out[0], out[1], out[2], out[3]
     if y_layout in ("bt2hd", "bt2hd_bf16"):
-        if d < 64:
-            raise NotImplementedError(f"y_layout '{y_layout}' needs head_dim 64")
         return y_re, None, s_re, s_im
     if d < 64:
         y_re, y_im = y_re[..., :d], y_im[..., :d]
         s_re, s_im = s_re[..., :d, :d], s_im[..., :d, :d]
+    return y_re, y_im, s_re, s_im
+
+
+def _to_bt2hd(y_re, y_im, y_layout):
+    """[B,H,T,d] planes -> one [B,T,2,H,d] tensor (bf16 for 'bt2hd_bf16')."""
+    y = torch.stack([y_re.transpose(1, 2), y_im.transpose(1, 2)], dim=2)
+    return y.to(torch.bfloat16) if y_layout == "bt2hd_bf16" else y
+
+
+def _scan_state_groups(q_re, q_im, k_re, k_im, v_re, v_im, gamma, q_scale, chunk, rot, s0, y_layout):
+    """More than MAX_STATES states: near-equal groups of at most MAX_STATES,
+    one scan each; Y is summed over the groups (in fp32, rounded once for the
+    bf16 layout) and the final states are concatenated."""
+    M = gamma.shape[0]
+    n_groups = -(-M // MAX_STATES)
+    bounds = [round(i * M / n_groups) for i in range(n_groups + 1)]
+    layout = "bt2hd" if y_layout == "bt2hd_bf16" else y_layout
+    y_re = y_im = None
+    s_re, s_im = [], []
+    for m0, m1 in zip(bounds[:-1], bounds[1:]):
+        rot_g = (rot[0][m0:m1], rot[1][m0:m1]) if rot is not None else None
+        s0_g = (s0[0][m0:m1], s0[1][m0:m1]) if s0 is not None else None
+        yr, yi, sr, si = pam_scan_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma[m0:m1], q_scale=q_scale,
+                                         chunk=chunk, rot=rot_g, s0=s0_g, y_layout=layout)
+        y_re = yr if y_re is None else y_re + yr
+        if yi is not None:
+            y_im = yi if y_im is None else y_im + yi
+        s_re.append(sr)
+        s_im.append(si)
+    if y_layout == "bt2hd_bf16":
+        y_re = y_re.to(torch.bfloat16)
+    return y_re, y_im, torch.cat(s_re, 0), torch.cat(s_im, 0)
+
+
+def _scan_blocks(q_re, q_im, k_re, k_im, v_re, v_im, gamma, q_scale, chunk, rot, s0, y_layout):
+    """Head dim d > 64: d is zero-padded to 64 n and the d x d state splits into
+    n x n blocks of 64 x 64, each an independent chain with the head's decay:
+    block (i, j) reads value block i and key/query block j, and y_i = sum_j of
+    the blocks' reads.  The n^2 blocks of every head run as extra heads of one
+    d = 64 scan (q and k repeated over i, v over j, gamma and rot over both)."""
+    B, H, T, d = q_re.shape
+    M = gamma.shape[0]
+    n = -(-d // 64)
+    dp = 64 * n
+
+    def padded(x):
+        return torch.nn.functional.pad(x, (0, dp - d)) if dp != d else x
+
+    def key_side(x):  # [B,H,T,d] -> [B, H n n, T, 64], entry (i, j) = column block j
+        xb = padded(x).reshape(B, H, T, n, 64).permute(0, 1, 3, 2, 4)
+        return xb.unsqueeze(2).expand(B, H, n, n, T, 64).reshape(B, H * n * n, T, 64)
+
+    def value_side(x):  # entry (i, j) = column block i
+        xb = padded(x).reshape(B, H, T, n, 64).permute(0, 1, 3, 2, 4)
+        return xb.unsqueeze(3).expand(B, H, n, n, T, 64).reshape(B, H * n * n, T, 64)
+
+    def per_block(x):  # [M,B,H,T] -> [M, B, H n n, T]
+        return x.unsqueeze(3).expand(M, B, H, n * n, T).reshape(M, B, H * n * n, T)
+
+    def state_blocks(x):  # [M,B,H,d,d] -> [M, B, H n n, 64, 64]
+        if dp != d:
+            x = torch.nn.functional.pad(x, (0, dp - d, 0, dp - d))
+        return x.reshape(M, B, H, n, 64, n, 64).permute(0, 1, 2, 3, 5, 4, 6).reshape(M, B, H * n * n, 64, 64)
+
+    rot_b = (per_block(rot[0]), per_block(rot[1])) if rot is not None else None
+    s0_b = (state_blocks(s0[0]), state_blocks(s0[1])) if s0 is not None else None
+    y_re, y_im, s_re, s_im = pam_scan_planar(
+        key_side(q_re), key_side(q_im), key_side(k_re), key_side(k_im), value_side(v_re), value_side(v_im),
+        per_block(gamma), q_scale=q_scale, chunk=chunk, rot=rot_b, s0=s0_b)
+
+    def gather_y(y):  # [B, H n n, T, 64] -> [B,H,T,d]
+        y = y.view(B, H, n, n, T, 64).sum(3)
+        return y.permute(0, 1, 3, 2, 4).reshape(B, H, T, dp)[..., :d]
+
+    def gather_s(s):  # [M, B, H n n, 64, 64] -> [M,B,H,d,d]
+        s = s.view(M, B, H, n, n, 64, 64).permute(0, 1, 2, 3, 5, 4, 6).reshape(M, B, H, dp, dp)
+        return s[..., :d, :d]
+
+    y_re, y_im, s_re, s_im = gather_y(y_re), gather_y(y_im), gather_s(s_re), gather_s(s_im)
+    if y_layout == "bthd":
+        return y_re.transpose(1, 2), y_im.transpose(1, 2), s_re, s_im
+    if y_layout in ("bt2hd", "bt2hd_bf16"):
+        return _to_bt2hd(y_re, y_im, y_layout), None, s_re, s_im
     return y_re, y_im, s_re, s_im
 
 

@@ -18,7 +18,7 @@ def _rel(a, b):
     return ((a - b).abs().max() / (b.abs().max() + 1e-30)).item()
 
 
-def _run(q, k, v, g, b, s0, dy, ds, eps):
+def _run(q, k, v, g, b, s0, dy, ds, eps, d=64):
     from qllm2_amd.pam_delta import delta_planar
     dev = torch.device("cuda")
     planes = [x[..., i].contiguous().float().to(dev).requires_grad_(True) for x in (q, k, v) for i in (0, 1)]
@@ -26,7 +26,7 @@ def _run(q, k, v, g, b, s0, dy, ds, eps):
     s0p = None
     if s0 is not None:
         s0p = tuple(s0[..., i].contiguous().float().to(dev).requires_grad_(True) for i in (0, 1))
-    y_re, y_im, s_re, s_im = delta_planar(*planes, gg, bb, q_scale=64 ** -0.5, gamma_eps=eps, s0=s0p)
+    y_re, y_im, s_re, s_im = delta_planar(*planes, gg, bb, q_scale=d ** -0.5, gamma_eps=eps, s0=s0p)
     loss = (y_re * dy[..., 0].to(dev)).sum() + (y_im * dy[..., 1].to(dev)).sum()
     if ds is not None:
         loss = loss + (s_re * ds[..., 0].to(dev)).sum() + (s_im * ds[..., 1].to(dev)).sum()
@@ -38,13 +38,13 @@ def _run(q, k, v, g, b, s0, dy, ds, eps):
     return torch.stack([y_re, y_im], -1).detach().cpu(), torch.stack([s_re, s_im], -1).detach().cpu(), grads
 
 
-def _ref(q, k, v, g, b, s0, dy, ds, chunked):
+def _ref(q, k, v, g, b, s0, dy, ds, chunked, d=64):
     xs = [x.double().clone().requires_grad_(True) for x in (q, k, v, g, b)]
     s0r = s0.double().clone().requires_grad_(True) if s0 is not None else None
     if chunked:
-        y, s = D.delta_chunked(*xs, 64, 64, state=s0r)
+        y, s = D.delta_chunked(*xs, d, 64, state=s0r)
     else:
-        y, s = D.delta_recurrent(*xs, 64, state=s0r, eps=0.0)
+        y, s = D.delta_recurrent(*xs, d, state=s0r, eps=0.0)
     loss = (y * dy.double()).sum() + ((s * ds.double()).sum() if ds is not None else 0)
     loss.backward()
     return y.detach(), s.detach(), [x.grad for x in xs] + [s0r.grad if s0r is not None else None]
@@ -73,6 +73,27 @@ def test_delta_matches_chunked_oracle(gpu_lib, T, with_s0, with_ds):
         if a is None or r is None:
             continue
         assert math.isfinite(a.abs().sum().item()), name
+        assert _rel(a, r) < 1e-4, f"{name}: {_rel(a, r):.2e}"
+
+
+@pytest.mark.parametrize("d,T", [(32, 100), (16, 70), (48, 130)])
+def test_delta_small_head_dims(gpu_lib, d, T):
+    """Head dims below 64 (the reference's small presets use 32) run zero-padded
+    to 64 and sliced back: Y, S and every gradient against the chunked oracle
+    at the true head dim (its own query scale d^-0.5)."""
+    B, H = 2, 2
+    q, k, v, g, b = D.make_delta_inputs(B, H, T, d, 660 + d + T)
+    gen = torch.Generator().manual_seed(661 + d + T)
+    s0 = torch.randn(B, H, d, d, 2, generator=gen, dtype=torch.float64) * 0.05
+    dy = torch.randn(B, H, T, d, 2, generator=gen, dtype=torch.float64)
+    ds = torch.randn(B, H, d, d, 2, generator=gen, dtype=torch.float64) * 0.1
+    y, s, grads = _run(q, k, v, g, b, s0, dy, ds, 1e-6, d=d)
+    yr, sr, rgrads = _ref(q, k, v, g, b, s0, dy, ds, chunked=True, d=d)
+    assert y.shape == yr.shape and s.shape == sr.shape
+    assert _rel(y, yr) < 1e-4, f"y {_rel(y, yr):.2e}"
+    assert _rel(s, sr) < 1e-4, f"s {_rel(s, sr):.2e}"
+    for name, a, r in zip(NAMES, grads, rgrads):
+        assert a.shape == r.shape, name
         assert _rel(a, r) < 1e-4, f"{name}: {_rel(a, r):.2e}"
 
 

@@ -6,7 +6,8 @@ same attributes, same method names, the reference's dispatch in forward and
 _recurrent); install() rebinds a subclass of it, so the saved originals are
 the restated reference methods.  For every mode of the reference's self-test
 (v11/selftest.py:193-204: baseline, E1 per-channel, E2 delta, E3 multistate,
-E1+E3) plus the E3 K-loop, at head_dim 16 (the self-test's shape) and 64:
+E1+E3) plus the E3 K-loop, at head_dim 16 (the self-test's shape) and 64, and
+the shapes the kernels take in pieces (six states, head_dim 128 and 96):
 
   * the installed layer on the GPU (fp32) against the float64 oracle layer on
     the CPU: parallel prefill, token-by-token decode and the final state, rel
@@ -14,8 +15,9 @@ E1+E3) plus the E3 K-loop, at head_dim 16 (the self-test's shape) and 64:
   * parallel == recurrent on the GPU within the self-test's bar (atol 2e-3,
     v11/selftest.py:16-38);
   * the HIP kernels ran where they apply: counters on the saved originals show
-    the head-decay scans and decode steps never fell back (E1 and the head
-    dims the delta kernels do not take run the reference methods, by design);
+    the head-decay scans, the delta write and the decode steps never fell
+    back (E1, and decode at head dims outside 16/32/64/128, run the reference
+    methods by design);
   * grad mode: a T = 1 step carrying a state (the reference's recurrent
     branch, v11/model.py:830-832) and a prefill, every gradient (input, state,
     each parameter) against float64 autograd of the oracle layer, rel <= 1e-4.
@@ -44,6 +46,9 @@ MODES = {
     "baseline_hd64": dict(DIM64),
     "E2_hd64": dict(DIM64, write_mode="delta", delta_chunk=64),
     "E3_hd64": dict(DIM64, n_states=3, state_compete=True, gamma_floor=0.2),
+    "E3_6states": dict(DIM16, n_states=6),
+    "baseline_hd128": dict(dim=128, n_heads=1, head_dim=128, chunk_size=64),
+    "E3_hd96": dict(dim=96, n_heads=1, head_dim=96, chunk_size=32, n_states=2),
 }
 # reference methods that must not run (the HIP path covers the call) per mode
 HIP_ONLY = {
@@ -53,6 +58,10 @@ HIP_ONLY = {
     "baseline_hd64": ("_forward_chunked_head", "_recurrent", "_recur_step_additive"),
     "E2_hd64": ("_forward_delta", "_recur_step_delta"),
     "E3_hd64": ("_forward_multistate_fused", "_recurrent", "_recur_step_additive"),
+    "E2": ("_forward_delta", "_recur_step_delta"),
+    "E3_6states": ("_forward_multistate_fused", "_fused_chunk_step", "_recurrent", "_recur_step_additive"),
+    "baseline_hd128": ("_forward_chunked_head", "_recurrent", "_recur_step_additive"),
+    "E3_hd96": ("_forward_multistate_fused", "_fused_chunk_step"),
 }
 
 
@@ -135,7 +144,8 @@ def test_installed_selftest_matches_oracle(installed, mode):
         assert calls[name] == 0, f"{mode}: the reference's {name} ran {calls[name]} times"
 
 
-GRAD_MODES = ["baseline", "E1", "E3", "E1+E3", "E2_hd64", "baseline_hd64", "E3_hd64"]
+GRAD_MODES = ["baseline", "E1", "E3", "E1+E3", "E2_hd64", "baseline_hd64", "E3_hd64", "E2", "E3_6states",
+              "baseline_hd128"]
 
 
 def _grads(layer, x, step_offset, state, loss_fn):

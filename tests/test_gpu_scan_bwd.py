@@ -145,6 +145,61 @@ def test_scan_backward_strided_gamma_and_rot(gpu_lib, dtype):
         assert _rel(got, want) < tol, f"{name}: rel {_rel(got, want):.2e}"
 
 
+@pytest.mark.parametrize("M,d,T,C,dtype,with_rot,with_s0", [
+    (1, 128, 150, 64, torch.float32, False, True),   # 2 x 2 state blocks of 64 x 64
+    (2, 96, 100, 32, torch.float32, True, True),     # padded to 128
+    (1, 48, 90, 16, torch.float32, False, True),     # padded to 64 (48 does not divide 64)
+    (6, 64, 130, 64, torch.float32, True, True),     # two kernel calls of three states
+    (5, 64, 200, 64, torch.bfloat16, True, True),    # bf16 segment kernels, groups of 3 + 2 states
+    (2, 128, 200, 64, torch.bfloat16, True, False),
+    (5, 128, 70, 32, torch.float32, True, True),     # both
+])
+def test_scan_any_head_dim_and_state_count(gpu_lib, M, d, T, C, dtype, with_rot, with_s0):
+    """Head dims other than 64 and more than four states (the reference's layer
+    takes any head_dim and n_states, v11/model.py:45-97): Y, the final state
+    and every gradient against oracle autograd at the true head dim."""
+    B, H = 2, 2
+    case = _case(M, B, H, T, d, 3600 + M * 13 + d + T, with_rot, with_s0, dtype)
+    q, k, v, gamma, dy, ds, phase, routing, s0 = case
+    with torch.no_grad():
+        y_ref, s_ref = O.multistate_fused(q.double(), k.double(), v.double(), gamma.double(), phase.double(),
+                                          routing.double(), d, C,
+                                          state=s0.double() if s0 is not None else None)
+    ref = _oracle_grads(*case, d, C)
+    outs = {}
+    got = _gpu_grads(*case, d, C, dtype, with_rot, outs)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert outs["y"].shape == y_ref.shape and outs["s"].shape == s_ref.shape
+    assert _rel(outs["y"], y_ref) < tol and _rel_heads(outs["y"], y_ref, 2) < tol
+    assert _rel(outs["s"], s_ref) < tol and _rel_heads(outs["s"], s_ref, 3) < tol
+    _check(got, ref, tol)
+
+
+@pytest.mark.parametrize("M,d", [(5, 64), (2, 128), (5, 96)])
+def test_scan_head_merged_y_any_shape(gpu_lib, M, d):
+    """The head-merged layouts for shapes the kernels take in pieces: 'bt2hd'
+    holds the [B,H,T,d] planes moved into [B,T,2,H,d] (the kernels may sum in
+    another order per layout: rel 1e-6), and 'bt2hd_bf16' is that fp32 tensor
+    rounded once (the state groups are summed in fp32)."""
+    from qllm2_amd.pam_scan import pam_scan_planar
+    g = torch.Generator().manual_seed(71 + M + d)
+    B, H, T = 2, 2, 150
+    planes = [(torch.randn(B, H, T, d, generator=g) * 0.5).to(torch.bfloat16).cuda() for _ in range(6)]
+    gamma = (0.8 + 0.19 * torch.rand(M, B, H, T, generator=g)).cuda()
+    rot = tuple(torch.randn(M, B, H, T, generator=g).cuda() for _ in range(2))
+    with torch.no_grad():
+        y_re, y_im, s_re, _ = pam_scan_planar(*planes, gamma, q_scale=d ** -0.5, chunk=64, rot=rot)
+        y32, none32, s32, _ = pam_scan_planar(*planes, gamma, q_scale=d ** -0.5, chunk=64, rot=rot,
+                                              y_layout="bt2hd")
+        y16, none16, s16, _ = pam_scan_planar(*planes, gamma, q_scale=d ** -0.5, chunk=64, rot=rot,
+                                              y_layout="bt2hd_bf16")
+    assert none32 is None and none16 is None
+    assert y32.shape == (B, T, 2, H, d) and y16.dtype == torch.bfloat16
+    assert _rel(y32, torch.stack([y_re.transpose(1, 2), y_im.transpose(1, 2)], 2)) < 1e-6
+    assert torch.equal(y16, y32.to(torch.bfloat16))
+    assert _rel(s32, s_re) < 1e-6 and torch.equal(s16, s32)
+
+
 def test_scan_backward_bf16_e3(gpu_lib):
     M, B, H, T, d, C = 3, 2, 2, 512, 64, 64
     case = _case(M, B, H, T, d, 3303, False, False, torch.bfloat16)

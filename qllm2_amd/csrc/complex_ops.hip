@@ -550,6 +550,167 @@ __global__ void __launch_bounds__(THREADS) act_bwd_reg_kernel(Params p) {
     write_partials_reg<NP, G>(p, acc, lds);
 }
 
+// Row-team kernels (16-byte groups, dim / 4 a multiple of 64 up to TEAM_MAX): a
+// block of dim / 4 threads is one row wide, thread i owning columns 4 i .. 4 i + 3
+// of every row, so the parameters and the parameter-gradient column sums stay in
+// registers for the block's whole life and no wave re-reads a row; R rows are
+// loaded per iteration before any is reduced, and the ComplexNorm row sums cross
+// the block's waves through LDS (one barrier pair per R rows).  The backward
+// writes the input gradient in the form A g + B z (A, B real per element):
+//   ComplexNorm:  A = |z| sc / (rms (|z| + eps)),   B = gmag / |z| - A (g.u) / (|z| + eps)
+//   mod swish / relu: A = act / (|z| + eps),        B = dmag / |z| - A (g.u) / (|z| + eps)
+// with u = z / (|z| + eps) and gmag, dmag the gradients of the output magnitude
+// (the closed forms of the reference's autograd backward, v11/triton_kernels.py:209-345).
+constexpr int TEAM_MAX = 512;  // threads per row team (dim <= 2048)
+constexpr int TEAM_THREADS_TOTAL = 256 * 1024;  // resident threads the grid is sized for
+
+template <int R>
+__device__ __forceinline__ void team_row_sums(float (&a)[R], float (&b)[R], float *red) {
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        a[r] = wave_sum(a[r]);
+        b[r] = wave_sum(b[r]);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) red[(2 * r) * (TEAM_MAX / 64) + w] = a[r], red[(2 * r + 1) * (TEAM_MAX / 64) + w] = b[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        a[r] = b[r] = 0.f;
+        for (int k = 0; k < nw; ++k) a[r] += red[(2 * r) * (TEAM_MAX / 64) + k], b[r] += red[(2 * r + 1) * (TEAM_MAX / 64) + k];
+    }
+    __syncthreads();  // red is rewritten by the next iteration
+}
+
+// rows row0 .. row0 + R - 1 of the block's iteration (rows past the end re-read the last row)
+template <typename T, int R>
+__device__ __forceinline__ void team_load(const T *base, const Params &p, int64_t row0, float (&re)[R][4],
+                                          float (&im)[R][4]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = row0 + r < p.rows ? row0 + r : p.rows - 1;
+        CVec<T, 4>::load(base, row * p.dim + 4 * threadIdx.x, re[r], im[r]);
+    }
+}
+
+template <typename T, int R>
+__global__ void __launch_bounds__(TEAM_MAX) norm_fwd_team_kernel(Params p) {
+    __shared__ float red[2 * R * (TEAM_MAX / 64)];
+    const T *z = (const T *)p.z;
+    T *out = (T *)p.out;
+    const float4 s4 = *reinterpret_cast<const float4 *>(p.p0 + 4 * threadIdx.x);
+    const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
+    for (int64_t row0 = (int64_t)blockIdx.x * R; row0 < p.rows; row0 += (int64_t)gridDim.x * R) {
+        float re[R][4], im[R][4], ss[R], unused[R];
+        team_load<T, R>(z, p, row0, re, im);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ss[r] = unused[r] = 0.f;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float m = magnitude(re[r][k], im[r][k]);
+                ss[r] += m * m;
+            }
+        }
+        team_row_sums<R>(ss, unused, red);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (row0 + r >= p.rows) break;
+            const float inv_rms = rcp(sqrtf(ss[r] / p.dim + p.eps));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float m = magnitude(re[r][k], im[r][k]);
+                const float f = m * inv_rms * sc[k] * rcp(m + MAG_EPS);
+                re[r][k] *= f;
+                im[r][k] *= f;
+            }
+            CVec<T, 4>::store(out, (row0 + r) * p.dim + 4 * threadIdx.x, re[r], im[r]);
+        }
+    }
+}
+
+// OP 0: ComplexNorm (partial d scale), 1: mod swish (d bias, d beta), 2: mod relu (d bias)
+template <typename T, int R, int OP>
+__global__ void __launch_bounds__(TEAM_MAX) bwd_team_kernel(Params p) {
+    constexpr int NP = OP == 1 ? 2 : 1;
+    __shared__ float red[2 * R * (TEAM_MAX / 64)];
+    const T *z = (const T *)p.z, *go = (const T *)p.gout;
+    T *gz = (T *)p.gz;
+    const int c0 = 4 * threadIdx.x;
+    const float4 x0 = *reinterpret_cast<const float4 *>(p.p0 + c0);
+    const float4 x1 = OP == 1 ? *reinterpret_cast<const float4 *>(p.p1 + c0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float q0[4] = {x0.x, x0.y, x0.z, x0.w}, q1[4] = {x1.x, x1.y, x1.z, x1.w};
+    float acc[NP][4];
+#pragma unroll
+    for (int q = 0; q < NP; ++q)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[q][k] = 0.f;
+    for (int64_t row0 = (int64_t)blockIdx.x * R; row0 < p.rows; row0 += (int64_t)gridDim.x * R) {
+        float zr[R][4], zi[R][4], gr[R][4], gi[R][4];
+        team_load<T, R>(z, p, row0, zr, zi);
+        team_load<T, R>(go, p, row0, gr, gi);
+        float ss[R], sg[R];
+        if constexpr (OP == 0) {
+            // row sums: sum |z|^2 (the rms) and sum (g.u) sc |z|
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                ss[r] = sg[r] = 0.f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float m = magnitude(zr[r][k], zi[r][k]);
+                    ss[r] += m * m;
+                    sg[r] += (gr[r][k] * zr[r][k] + gi[r][k] * zi[r][k]) * rcp(m + MAG_EPS) * q0[k] * m;
+                }
+            }
+            team_row_sums<R>(ss, sg, red);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (row0 + r >= p.rows) break;
+            float inv_rms = 0.f, rms_term = 0.f;
+            if constexpr (OP == 0) {
+                const float rms = sqrtf(ss[r] / p.dim + p.eps);
+                inv_rms = rcp(rms);
+                rms_term = -sg[r] * inv_rms * inv_rms * rcp(p.dim * rms);
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float m = magnitude(zr[r][k], zi[r][k]), inv = rcp(m + MAG_EPS), rm = rcp(m);
+                const float gu = (gr[r][k] * zr[r][k] + gi[r][k] * zi[r][k]) * inv;  // g.u
+                float A, dmag;
+                if constexpr (OP == 0) {
+                    acc[0][k] += gu * m * inv_rms;
+                    dmag = gu * q0[k] * inv_rms + rms_term * m;
+                    A = m * inv_rms * q0[k] * inv;
+                } else if constexpr (OP == 1) {
+                    const float beta = q1[k], sgm = sigmoidf(beta * m + q0[k]), sd = sgm * (1.f - sgm);
+                    dmag = gu * (sgm + m * beta * sd);
+                    acc[0][k] += gu * m * sd;
+                    acc[NP - 1][k] += gu * m * m * sd;
+                    A = m * sgm * inv;
+                } else {
+                    const float x = m + q0[k];
+                    dmag = x > 0.f ? gu : 0.f;
+                    acc[0][k] += dmag;
+                    A = fmaxf(x, 0.f) * inv;
+                }
+                const float Bc = dmag * rm - A * gu * inv;
+                const float a = zr[r][k], b = zi[r][k];
+                zr[r][k] = A * gr[r][k] + Bc * a;
+                zi[r][k] = A * gi[r][k] + Bc * b;
+            }
+            CVec<T, 4>::store(gz, (row0 + r) * p.dim + c0, zr[r], zi[r]);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < NP; ++q)
+        *reinterpret_cast<float4 *>(p.part + ((int64_t)blockIdx.x * NP + q) * p.dim + c0) =
+            make_float4(acc[q][0], acc[q][1], acc[q][2], acc[q][3]);
+}
+
 // out[i] = sum over blocks of part[b][i], in a fixed order: 16 waves each sum
 // the blocks b = w, w + 16, ... (eight loads in flight), then wave 0 adds the 16
 constexpr int SUM_THREADS = 1024;
@@ -640,6 +801,16 @@ int reg_groups(int dim) {
     return g <= 1 ? 1 : g <= 2 ? 2 : g <= 4 ? 4 : g <= 8 ? 8 : 0;
 }
 
+// threads of the row team (dim / 4 when it is a multiple of 64 up to TEAM_MAX), 0 = no team path
+int team_threads(int dim) {
+    const int t = dim / 4;
+    return (t % 64 == 0 && t <= TEAM_MAX) ? t : 0;
+}
+constexpr int TEAM_ROWS_FWD = 4, TEAM_ROWS_NORM_BWD = 4, TEAM_ROWS_ACT_BWD = 2;
+int team_blocks(int64_t rows, int threads, int r) {
+    return (int)std::max<int64_t>(1, std::min<int64_t>((rows + r - 1) / r, TEAM_THREADS_TOTAL / threads));
+}
+
 template <typename T, int OP>
 int launch_act_fwd_reg(int g, int64_t rows, hipStream_t stream, const Params &p) {
     const dim3 grid(row_blocks(rows));
@@ -683,6 +854,12 @@ int fwd(const qpam_cplx_args *a, hipStream_t stream) {
     const int64_t n = a->rows * (int64_t)a->dim / V;
     switch (a->op) {
         case QPAM_CPLX_NORM:
+            if (V == 4 && team_threads(a->dim)) {
+                const int tt = team_threads(a->dim);
+                hipLaunchKernelGGL((norm_fwd_team_kernel<T, TEAM_ROWS_FWD>), dim3(team_blocks(a->rows, tt, TEAM_ROWS_FWD)),
+                                   dim3(tt), 0, stream, p);
+                break;
+            }
             if (V == 4 && reg_groups(a->dim)) {
                 const dim3 grid(row_blocks(a->rows));
                 switch (reg_groups(a->dim)) {
@@ -715,6 +892,23 @@ int bwd(const qpam_cplx_args *a, hipStream_t stream) {
     const int np = n_params(a->op);
     const int blocks = row_blocks(a->rows);
     const size_t smem = (size_t)WAVES * np * a->dim * sizeof(float);
+    if (V == 4 && team_threads(a->dim) && a->op != QPAM_CPLX_CGU_GATE) {
+        const int tt = team_threads(a->dim);
+        const int rr = a->op == QPAM_CPLX_NORM ? TEAM_ROWS_NORM_BWD : TEAM_ROWS_ACT_BWD;
+        const int tb = team_blocks(a->rows, tt, rr);
+        if (a->op == QPAM_CPLX_NORM)
+            hipLaunchKernelGGL((bwd_team_kernel<T, TEAM_ROWS_NORM_BWD, 0>), dim3(tb), dim3(tt), 0, stream, p);
+        else if (a->op == QPAM_CPLX_MOD_SWISH)
+            hipLaunchKernelGGL((bwd_team_kernel<T, TEAM_ROWS_ACT_BWD, 1>), dim3(tb), dim3(tt), 0, stream, p);
+        else
+            hipLaunchKernelGGL((bwd_team_kernel<T, TEAM_ROWS_ACT_BWD, 2>), dim3(tb), dim3(tt), 0, stream, p);
+        int st = launch_status("qpam_cplx_bwd");
+        if (st) return st;
+        const int n = np * a->dim;
+        hipLaunchKernelGGL(partial_sum_kernel, dim3((n + 63) / 64), dim3(SUM_THREADS), 0, stream,
+                           (const float *)a->workspace, tb, n, a->gp0, a->gp1, a->dim);
+        return launch_status("qpam_cplx_bwd (parameter gradients)");
+    }
     if (V == 4 && reg_groups(a->dim) && a->op != QPAM_CPLX_CGU_GATE) {
         int st = launch_bwd_reg<T>(a->op, reg_groups(a->dim), blocks, smem, stream, p);
         if (st) return st;
@@ -771,7 +965,13 @@ int bwd_t(const qpam_cplx_args *a, hipStream_t stream) { return vec4(a) ? bwd<T,
 extern "C" size_t qpam_cplx_workspace_size(const qpam_cplx_args *a) {
     using namespace qpam::cplx;
     if (!a || a->rows <= 0 || a->dim <= 0) return 0;
-    return (size_t)row_blocks(a->rows) * n_params(a->op) * a->dim * sizeof(float);
+    // partials of the kernel the call runs: the row-team grid (16-byte aligned
+    // operands) or one block per four rows; sized for the larger, so the size
+    // does not depend on the pointers
+    int blocks = row_blocks(a->rows);
+    if (const int tt = team_threads(a->dim))
+        blocks = std::max(blocks, team_blocks(a->rows, tt, std::min(TEAM_ROWS_NORM_BWD, TEAM_ROWS_ACT_BWD)));
+    return (size_t)blocks * n_params(a->op) * a->dim * sizeof(float);
 }
 
 extern "C" int qpam_cplx_fwd(const qpam_cplx_args *a, void *stream) {

@@ -69,9 +69,12 @@ def _gpu(name, z, up, gout, p0, p1):
 
 
 OPS = ["norm", "swish", "relu", "cgu"]
-# dims: 384 / 1152 / 100 / 64 take the register-row kernels (1, 2, 8 groups of four
-# columns per lane), 2304 the LDS-accumulating kernels, 7 and 50 the scalar path
-SHAPES = [(3, 128, 384), (3, 128, 1152), (5, 100), (1, 64), (2, 3, 7), (4, 2304), (6, 50)]
+# dims: 768 / 1024 / 256 / 2048 (dim / 4 a multiple of 64) take the row-team kernels
+# (row counts below, at and off a multiple of the rows per iteration, a single row);
+# 384 / 1152 / 100 / 64 the register-row kernels (1, 2, 8 groups of four columns per
+# lane), 2304 the LDS-accumulating kernels, 7 and 50 the scalar path
+SHAPES = [(3, 37, 768), (5, 26, 1024), (1, 256), (2, 2048), (3, 128, 384), (3, 128, 1152), (5, 100), (1, 64),
+          (2, 3, 7), (4, 2304), (6, 50)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -86,9 +89,10 @@ def test_complex_ops_fp32(gpu_lib, name, shape):
         assert _rel(g, r) < 1e-4, f"{name} grad {i} rel {_rel(g, r):.2e}"
 
 
+@pytest.mark.parametrize("shape", [(3, 128, 384), (3, 45, 1024)])
 @pytest.mark.parametrize("name", OPS)
-def test_complex_ops_bf16(gpu_lib, name):
-    z, up, gout, p0, p1 = _inputs((3, 128, 384), 200, torch.bfloat16)
+def test_complex_ops_bf16(gpu_lib, name, shape):
+    z, up, gout, p0, p1 = _inputs(shape, 200 + shape[-1], torch.bfloat16)
     ref_out, ref_grads = _oracle(name, z, up, gout, p0, p1)
     out, grads = _gpu(name, z, up, gout, p0, p1)
     assert _rel(out, ref_out) < 2e-2, f"{name} fwd rel {_rel(out, ref_out):.2e}"

@@ -769,6 +769,7 @@ constexpr int DH_SPLITS = 8;
 // the pipelined loads carry no conditional register initialisation.
 namespace wide {
 constexpr int TM = 256, TN = 256, WK = 64;
+constexpr float LOG2E = 1.4426950408889634f;
 constexpr int WTHREADS = 512;   // 8 waves: 4 row groups x 2 column groups, 64 x 128 each
 constexpr int WPITCH = WK + 8;  // bf16 elements per LDS row (144 bytes: conflict-free 16-byte reads)
 constexpr int WLOADS = TM * WK / 8 / WTHREADS;  // 16-byte loads per thread per operand per k-step (4)
@@ -990,6 +991,7 @@ __global__ void __launch_bounds__(WTHREADS) fwd_tile_kernel(FwdParams p) {
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const int wm = w >> 1, wn = w & 1;
     const int vl = v0 + 128 * wn + l16;  // this lane's column in tile ni: vl + 16 ni
+    const bool full = v0 + TN <= a.V;    // no column past the vocabulary: no per-element checks
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
@@ -997,16 +999,17 @@ __global__ void __launch_bounds__(WTHREADS) fwd_tile_kernel(FwdParams p) {
             float lm = -INFINITY;
 #pragma unroll
             for (int ni = 0; ni < 8; ++ni)
-                if (vl + 16 * ni < a.V) lm = fmaxf(lm, acc[mi][ni][r]);
+                if (full || vl + 16 * ni < a.V) lm = fmaxf(lm, acc[mi][ni][r]);
             const float mx = row16_max(lm);
             float s = 0.f;
             int ix = 0x7fffffff;
             if (mx > -INFINITY) {
+                const float mx2 = mx * LOG2E;  // exp(x - mx) = exp2(x log2e - mx log2e)
 #pragma unroll
                 for (int ni = 0; ni < 8; ++ni)
-                    if (vl + 16 * ni < a.V) {
+                    if (full || vl + 16 * ni < a.V) {
                         const float x = acc[mi][ni][r];
-                        s += __expf(x - mx);
+                        s += __builtin_amdgcn_exp2f(__builtin_fmaf(x, LOG2E, -mx2));
                         if (ARGMAX && x == mx) ix = min(ix, vl + 16 * ni);
                     }
             }
@@ -1082,22 +1085,34 @@ __global__ void __launch_bounds__(WTHREADS) grad_tile_kernel(BwdParams p) {
     constexpr int GT_LD = 72;   // bf16 per staged vocab row: 64 tile rows + padding against bank conflicts
     __shared__ __align__(16) U16 sEpi[8 * 16 * GT_LD];
     U16 *tw = sEpi + w * 16 * GT_LD;
+    // the 16 rows of this lane (rows 64 wm + 16 mi + 4 g + r) in registers: lse in
+    // log2 units (exp(x - lse) = exp2(x log2e - lse log2e), one fma and one exp2),
+    // +inf for rows without a gradient (their G is exp2(-inf) = 0), the scale and
+    // the target column
+    float hl[4][4], hs[4][4];
+    int ht[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int rl = 64 * wm + 16 * mi + 4 * g + r;
+            hs[mi][r] = sScale[rl];
+            hl[mi][r] = hs[mi][r] != 0.f ? sLse[rl] * LOG2E : INFINITY;
+            ht[mi][r] = sTgt[rl];
+        }
+    const bool full = v0 + TN <= a.V;  // every column of the tile is a vocabulary entry
 #pragma unroll
     for (int ni = 0; ni < 8; ++ni) {
         const int vb = v0 + 128 * wn + 16 * ni, v = vb + l16;
+        const bool vok = full || v < a.V;
 #pragma unroll
         for (int mi = 0; mi < 4; ++mi) {
             const int rl0 = 64 * wm + 16 * mi + 4 * g;
             float x[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int rl = rl0 + r;
-                x[r] = 0.f;
-                if (v < a.V && sScale[rl] != 0.f) {
-                    x[r] = __expf(acc[mi][ni][r] - sLse[rl]);
-                    if (v == sTgt[rl]) x[r] -= 1.f;
-                    x[r] *= sScale[rl];
-                }
+                const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[mi][ni][r], LOG2E, -hl[mi][r]));
+                x[r] = vok ? (e - (v == ht[mi][r] ? 1.f : 0.f)) * hs[mi][r] : 0.f;
             }
             const unsigned lo = pack_bf16x2(x[0], x[1]), hi = pack_bf16x2(x[2], x[3]);
             if (p.write_g) {

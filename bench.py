@@ -246,17 +246,21 @@ def bench_decode_e3_rope(n_steps):
             "bytes_per_step": bytes_step, "steps": n_steps}
 
 
-def bench_engine(steps, warmup):
+def bench_engine(steps, warmup, graphs=False):
     """Model-level continuous-batching decode (qllm2_amd.engine.DecodeEngine):
     16 E3 PAM layers (M=3, H=12, d=64, dim=768, fp32, RoPE, GSP, phase-routed
     states) over 256 slots, ~75% of them live per step.  A step runs every
     layer on the live rows: projection GEMM, gate GEMMs, the prologue kernel,
-    one decode launch with per-slot RoPE, the o_proj GEMM."""
+    one decode launch with per-slot RoPE, the o_proj GEMM.  With `graphs` the
+    steps replay HIP graphs (one per live-count bucket of 16 rows); the warmup
+    then runs every live set once, so every bucket is captured before timing."""
     import torch
     from qllm2_amd.engine import DecodeEngine
     S, L, H, d, M, dim = 256, 16, 12, 64, 3, 768
     layers = [_BenchPamLayer(dim, H, d, M, 16, torch.float32, seed=40 + i).mod for i in range(L)]
-    engine = DecodeEngine(layers, n_slots=S, max_len=8192)
+    engine = DecodeEngine(layers, n_slots=S, max_len=8192, graphs=graphs, graph_bucket=16)
+    if graphs:
+        warmup = max(warmup, 16)
     gen = torch.Generator().manual_seed(1015)
     for s_ in range(S):
         engine.admit(int(torch.randint(1, 4096, (1,), generator=gen)))
@@ -279,7 +283,8 @@ def bench_engine(steps, warmup):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     active = sum(len(hosts[i % 16]) for i in range(steps)) / steps
-    return {"config": "16 PAM layers E3 M=3, H=12, d=64, dim=768, fp32, 256 slots (~75% live)",
+    return {"config": "16 PAM layers E3 M=3, H=12, d=64, dim=768, fp32, 256 slots (~75% live)"
+            + (", HIP-graph replay per live-count bucket of 16" if graphs else ""),
             "ms_per_step": ms, "tokens_per_s": active / (ms * 1e-3), "active_slots": active, "steps": steps}
 
 
@@ -777,7 +782,8 @@ def main():
                                            bench_scan_fwd(args.steps, args.warmup))),
               "decode": lambda: bench_decode(args.decode_steps),
               "decode_e3": lambda: bench_decode_e3_rope(max(50, args.decode_steps // 5)),
-              "engine": lambda: bench_engine(args.steps, args.warmup),
+              "engine": lambda: {"eager": bench_engine(args.steps, args.warmup),
+                                 "graphs": bench_engine(args.steps, args.warmup, graphs=True)},
               "e3": lambda: bench_e3_fwd_bwd(args.steps, args.warmup),
               "ce": lambda: bench_ce(args.steps, args.warmup),
               "cplx": lambda: bench_complex_ops(args.steps, args.warmup),
@@ -819,6 +825,7 @@ def main():
         out["extras"] = {"decode_config4": bench_decode(args.decode_steps),
                          "decode_e3_rope_slots": bench_decode_e3_rope(max(50, args.decode_steps // 5)),
                          "decode_engine_e3_16_layers": bench_engine(20, 5),
+                         "decode_engine_e3_16_layers_graphs": bench_engine(20, 5, graphs=True),
                          # five untimed warmup steps: after two, the first timed steps still run
                          # slow (E3 0.69 vs 0.66 ms per step)
                          "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 5),

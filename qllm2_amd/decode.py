@@ -161,6 +161,15 @@ class SlotPool:
         self._free = list(range(n_slots - 1, -1, -1))
         self.live = set()
 
+    def reserve(self, count):
+        """Take the `count` highest free slot ids out of circulation for good
+        (scratch rows: a padded batch points its extra rows at them).  Returns
+        the ids."""
+        if count > len(self._free):
+            raise RuntimeError("SlotPool: not enough free slots to reserve")
+        ids, self._free = sorted(self._free[:count]), self._free[count:]
+        return ids
+
     def acquire(self, position=0, states=None):
         """Take a free slot for a sequence whose next token is at `position`.
         states: optional per-layer prefill states, each [n_states, n_heads, d, d, 2]

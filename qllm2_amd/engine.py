@@ -20,6 +20,14 @@ live sequences:
     states in the SlotPool and reads y;
   * one GEMM from the interleaved y to the interleaved o_proj output.
 
+With `graphs=True` the per-token work of all layers is captured once per
+batch-size bucket (live rows rounded up to a multiple of `graph_bucket`) in a
+HIP graph and replayed: one launch per step instead of about a dozen per
+layer, so the host's dispatch of the small GEMMs and kernels no longer sets
+the step time.  The padded rows point at reserved scratch slots (zero input,
+their states are never read).  The first step of each bucket runs eagerly
+and captures the graph; a grown RoPE table or new weights start new graphs.
+
 Prefill stays the fused layer forward (pam_layer.forward); its per-layer
 states enter the pool through `admit`.  The layers must use head-scalar decay,
 the additive write and head_dim 64 (the production presets); the engine reads
@@ -42,7 +50,7 @@ class DecodeEngine:
     """Decode state and per-step work of `layers` (V11PAMLayer modules, or any
     module with their attributes) for up to `n_slots` concurrent sequences."""
 
-    def __init__(self, layers, n_slots, *, max_len=4096):
+    def __init__(self, layers, n_slots, *, max_len=4096, graphs=False, graph_bucket=16):
         self.layers = list(layers)
         l0 = self.layers[0]
         self.n_heads, self.head_dim, self.n_states = l0.num_heads, l0.head_dim, l0.n_states
@@ -55,8 +63,17 @@ class DecodeEngine:
             if layer.head_dim != HEAD_DIM or not 1 <= layer.n_states <= 4:
                 raise NotImplementedError("DecodeEngine needs head_dim 64 and 1 to 4 states")
         device = l0.qkv_proj.weight_real.device
-        self.pool = SlotPool(n_slots, len(self.layers), self.n_heads, self.head_dim, self.n_states, device=device,
-                             max_len=max_len)
+        self.graph_bucket = int(graph_bucket) if graphs else 0
+        if graphs and self.graph_bucket < 1:
+            raise ValueError("graph_bucket must be at least 1")
+        self.n_slots = n_slots
+        self.pool = SlotPool(n_slots + max(self.graph_bucket - 1, 0), len(self.layers), self.n_heads,
+                             self.head_dim, self.n_states, device=device, max_len=max_len)
+        # scratch slots for the padded rows of a graph replay (bucket - 1 at most)
+        scratch = self.pool.reserve(max(self.graph_bucket - 1, 0))
+        self._scratch = torch.tensor(scratch, dtype=torch.int32, device=device) if scratch else None
+        self._graphs = {}
+        self._wver = 0
         self.refresh_weights()
 
     # ------------------------------------------------------------ weights
@@ -65,6 +82,8 @@ class DecodeEngine:
         changing them)."""
         h, d = self.n_heads, self.head_dim
         cols = proj_columns(h)
+        self._graphs = {}  # captured graphs hold the old weight tensors
+        self._wver += 1
         self._w = []
         with torch.no_grad():
             for layer in self.layers:
@@ -162,6 +181,13 @@ class DecodeEngine:
         y = self.pool.step(layer_idx, q, k, v, g, slots, rot=r, q_scale=d ** -0.5, compact=True)
         return F.linear(y.view(n, 2 * h * d), w["w_out"], w["b_out"]).view(n, dim, 2)
 
+    def _layers(self, x, slots, between):
+        for li in range(len(self.layers)):
+            x = self.layer_step(li, x, slots)
+            if between is not None:
+                x = between(li, x)
+        return x
+
     def step(self, x, slots, between=None, host_slots=None):
         """One token of the listed sequences through every layer in order:
         x [n, dim, 2] enters layer 0, each layer's output (passed through
@@ -169,10 +195,49 @@ class DecodeEngine:
         channel-mix work) enters the next; then the positions advance.
         slots: int32 device tensor of the live slot ids (row order of x);
         host_slots: the same ids as a host list, if the caller has them (no
-        read-back).  Returns the last layer's output."""
-        for li in range(len(self.layers)):
-            x = self.layer_step(li, x, slots)
-            if between is not None:
-                x = between(li, x)
+        read-back).  Returns the last layer's output.
+
+        With graphs, `between` is captured into the graph with the layers (it
+        must be capturable: device work only, no host reads) and the returned
+        tensor is a view of the graph's output buffer, valid until the next
+        step of the same bucket."""
+        if not self.graph_bucket:
+            x = self._layers(x, slots, between)
+            self.pool.advance(slots, host_slots)
+            return x
+        n = x.shape[0]
+        if n > self.n_slots:
+            raise ValueError(f"DecodeEngine: {n} rows for {self.n_slots} slots")
+        if host_slots is None:
+            host_slots = slots.tolist()
+        if self.pool.live:  # grow the rotary table as SlotPool.step would, before any capture or replay
+            self.pool.ensure_len(max(self.pool._host_pos[s] for s in self.pool.live))
+        nb = -(-n // self.graph_bucket) * self.graph_bucket
+        key = (nb, id(between), self.pool.rope.data_ptr(), self._wver)
+        entry = self._graphs.get(key) if n else None
+        if entry is None:
+            out = self._layers(x, slots, between)
+            if n:
+                self._graphs[key] = self._capture(nb, between)
+            self.pool.advance(slots, host_slots)
+            return out
+        entry["x"][:n].copy_(x)
+        entry["slots"][:n].copy_(slots)
+        if nb > n:
+            entry["x"][n:].zero_()
+            entry["slots"][n:].copy_(self._scratch[:nb - n])
+        entry["graph"].replay()
         self.pool.advance(slots, host_slots)
-        return x
+        return entry["out"][:n]
+
+    def _capture(self, nb, between):
+        """Capture the layers' work for `nb` rows (static input, slot-id and
+        output buffers; nothing runs during the capture)."""
+        dim = self._w[0]["dim"]
+        dev = self.pool.device
+        x = torch.zeros(nb, dim, 2, device=dev, dtype=torch.float32)
+        slots = torch.zeros(nb, device=dev, dtype=torch.int32)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = self._layers(x, slots, between)
+        return {"graph": graph, "x": x, "slots": slots, "out": out}

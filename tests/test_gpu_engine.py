@@ -33,8 +33,13 @@ def _rel(a, b):
     return ((a - b).abs().max() / (b.abs().max() + 1e-30)).item()
 
 
+@pytest.mark.parametrize("graphs", [False, True])
 @pytest.mark.parametrize("name", list(CFGS))
-def test_engine_matches_per_sequence_oracle(gpu_lib, name):
+def test_engine_matches_per_sequence_oracle(gpu_lib, name, graphs):
+    """Eager steps, and HIP-graph replays (graph_bucket 2: odd live counts pad
+    one row onto a scratch slot; each bucket is captured on its first step and
+    replayed on later ones, with admissions, releases and a RoPE-table growth
+    in between)."""
     from qllm2_amd import pam_layer
     from qllm2_amd.engine import DecodeEngine
     cfg = V.config(**CFGS[name])
@@ -42,7 +47,7 @@ def test_engine_matches_per_sequence_oracle(gpu_lib, name):
     params = [V.make_params(cfg, 800 + i) for i in range(n_layers)]
     layers = [V.V11PAMLayer(cfg, {k: v.float() for k, v in p.items()}, dtype=torch.float32).cuda().eval()
               for p in params]
-    engine = DecodeEngine(layers, n_slots=4, max_len=16)
+    engine = DecodeEngine(layers, n_slots=4, max_len=16, graphs=graphs, graph_bucket=2)
     g = torch.Generator().manual_seed(810)
     prompts = [torch.randn(1, t, dim, 2, generator=g, dtype=torch.float64) * 0.5 for t, _, _ in SEQS]
     tokens = [torch.randn(n, dim, 2, generator=g, dtype=torch.float64) * 0.5 for _, _, n in SEQS]
@@ -90,6 +95,8 @@ def test_engine_matches_per_sequence_oracle(gpu_lib, name):
                 del slot_of[si]
         step += 1
     assert engine.pool.rope.shape[0] > 16, "the RoPE table should have grown past its initial 16 rows"
+    if graphs:
+        assert len(engine._graphs) >= 2, "both buckets should have been captured"
     for si in range(len(SEQS)):
         out = torch.stack(got[si])
         assert _rel(out, ref_out[si]) < 1e-4, f"seq {si}: {_rel(out, ref_out[si]):.2e}"

@@ -50,6 +50,8 @@ class DecodeEngine:
     """Decode state and per-step work of `layers` (V11PAMLayer modules, or any
     module with their attributes) for up to `n_slots` concurrent sequences."""
 
+    MAX_GRAPHS = 64  # captured graphs kept at once (each holds its own buffers)
+
     def __init__(self, layers, n_slots, *, max_len=4096, graphs=False, graph_bucket=16):
         self.layers = list(layers)
         l0 = self.layers[0]
@@ -198,7 +200,8 @@ class DecodeEngine:
         read-back).  Returns the last layer's output.
 
         With graphs, `between` is captured into the graph with the layers (it
-        must be capturable: device work only, no host reads) and the returned
+        must be capturable: device work only, no host reads; pass the same
+        callable every step, graphs are cached per callable) and the returned
         tensor is a view of the graph's output buffer, valid until the next
         step of the same bucket."""
         if not self.graph_bucket:
@@ -213,11 +216,16 @@ class DecodeEngine:
         if self.pool.live:  # grow the rotary table as SlotPool.step would, before any capture or replay
             self.pool.ensure_len(max(self.pool._host_pos[s] for s in self.pool.live))
         nb = -(-n // self.graph_bucket) * self.graph_bucket
-        key = (nb, id(between), self.pool.rope.data_ptr(), self._wver)
+        rope = self.pool.rope.data_ptr()
+        if self._graphs and next(iter(self._graphs))[2] != rope:
+            self._graphs = {}  # graphs of the old rotary table are never replayed again
+        key = (nb, id(between), rope, self._wver)
         entry = self._graphs.get(key) if n else None
         if entry is None:
             out = self._layers(x, slots, between)
             if n:
+                if len(self._graphs) >= self.MAX_GRAPHS:  # e.g. a new `between` callable every step
+                    self._graphs = {}
                 self._graphs[key] = self._capture(nb, between)
             self.pool.advance(slots, host_slots)
             return out

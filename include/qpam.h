@@ -88,7 +88,8 @@ int qpam_event_elapsed_ms(void *ev0, void *ev1, float *ms);
  * (update before read, v11/model.py:948-964).  Slots not listed are neither
  * read nor written; ids outside [0, n_slots) are skipped.  rot may be NULL
  * (all ones).  S is interleaved complex fp32 [d][d][2]; q, k, v, y are
- * interleaved [d][2]; rot is interleaved [2].  d in {16, 32, 64, 128}.
+ * interleaved [d][2] (q, k, v optionally planar, see q_im); rot is interleaved
+ * [2].  d in {16, 32, 64, 128}.
  */
 typedef struct {
     int32_t n_slots;        /* size of the slot axis of every operand */
@@ -121,6 +122,11 @@ typedef struct {
      * are ignored / left alone).  1: they are compact, row i belonging to the
      * slot active[i] (n_active rows); S and pos stay indexed by slot id. */
     int32_t vec_by_rank;
+    /* optional planar q, k, v (ABI 7): when set (all three), q, k, v point at the
+     * real planes and these at the imaginary planes, rows of d floats with the
+     * same strides (a prologue's output planes need no interleaving copy);
+     * NULL = interleaved [d][2] rows. */
+    const float *q_im, *k_im, *v_im;
 } qpam_decode_args;
 
 int qpam_decode_step(const qpam_decode_args *a, void *stream);

@@ -53,6 +53,22 @@ struct DecodeShape {
     }
 };
 
+// Two consecutive complex features (re, im, re, im) of a q or k row: one 16-byte
+// load of the interleaved row, or two 8-byte loads of the planar row (im != null).
+template <bool PL>
+__device__ __forceinline__ float4 load_pair(const float *re, const float *im, int64_t row, int cp) {
+    if constexpr (!PL) return *reinterpret_cast<const float4 *>(re + row + 4 * cp);
+    const float2 r = *reinterpret_cast<const float2 *>(re + row + 2 * cp);
+    const float2 i = *reinterpret_cast<const float2 *>(im + row + 2 * cp);
+    return make_float4(r.x, i.x, r.y, i.y);
+}
+// complex feature `e` of a v row, interleaved or planar
+template <bool PL>
+__device__ __forceinline__ float2 load_one(const float *re, const float *im, int e) {
+    if constexpr (!PL) return *reinterpret_cast<const float2 *>(re + 2 * e);
+    return make_float2(re[e], im[e]);
+}
+
 // q and k of the slot times rope[pos[slot]] (two complex features per float4)
 template <int D>
 __device__ __forceinline__ void apply_rope(const qpam_decode_args &a, int slot, int cp, float4 &qv, float4 &kv) {
@@ -94,8 +110,9 @@ __device__ __forceinline__ void halving_reduce(float (&v)[NV], int lane, int &id
 
 // S <- gam S + v (x) conj(k) on this lane's ITERS float4 (two complex entries
 // each), streamed in place; returns the lane's partial sums of S q~ per row.
-template <typename S>
-__device__ __forceinline__ void update_state(float *st, int tid, int r0, float gam, const float *vrow, float4 kv,
+template <typename S, bool PL>
+__device__ __forceinline__ void update_state(float *st, int tid, int r0, float gam, const float *vrow,
+                                             const float *vrow_im, float4 kv,
                                              float q0r, float q0i, float q1r, float q1i, float (&part)[S::NV]) {
     floatx4 s[S::ITERS];
 #pragma unroll
@@ -104,7 +121,7 @@ __device__ __forceinline__ void update_state(float *st, int tid, int r0, float g
 #pragma unroll
     for (int it = 0; it < S::ITERS; ++it) {
         const int row = it * S::ROWS_PER_IT + r0;
-        const float2 vv = *reinterpret_cast<const float2 *>(vrow + 2 * row);
+        const float2 vv = load_one<PL>(vrow, vrow_im, row);
         // v_i conj(k_j) for the two columns
         const float o0r = vv.x * kv.x + vv.y * kv.y, o0i = vv.y * kv.x - vv.x * kv.y;
         const float o1r = vv.x * kv.z + vv.y * kv.w, o1i = vv.y * kv.z - vv.x * kv.w;
@@ -120,7 +137,7 @@ __device__ __forceinline__ void update_state(float *st, int tid, int r0, float g
 }
 
 // ------------------------------------------------ one state, no rotation --
-template <int D>
+template <int D, bool PL>
 __global__ void __launch_bounds__((DecodeShape<D, 512>::THREADS)) decode_single_kernel(qpam_decode_args a) {
     using S = DecodeShape<D, 512>;
     const int tid = threadIdx.x;
@@ -130,12 +147,13 @@ __global__ void __launch_bounds__((DecodeShape<D, 512>::THREADS)) decode_single_
     if (slot < 0 || slot >= a.n_slots) return;
     const int vr = a.vec_by_rank ? ai : slot;   // row of q, k, v, gamma, rot, y
     const int cp = tid % S::PAIRS, r0 = tid / S::PAIRS, lane = tid & 63;
-    float4 qv = *reinterpret_cast<const float4 *>(a.q + vr * a.sq_slot + g * a.sq_group + 4 * cp);
-    float4 kv = *reinterpret_cast<const float4 *>(a.k + vr * a.sk_slot + g * a.sk_group + 4 * cp);
+    float4 qv = load_pair<PL>(a.q, a.q_im, vr * a.sq_slot + g * a.sq_group, cp);
+    float4 kv = load_pair<PL>(a.k, a.k_im, vr * a.sk_slot + g * a.sk_group, cp);
     apply_rope<D>(a, slot, cp, qv, kv);
     const float gam = a.gamma[vr * a.sg_slot + g * a.sg_group];
     float part[S::NV];
-    update_state<S>(a.state + slot * a.st_slot + g * a.st_group, tid, r0, gam, a.v + vr * a.sv_slot + g * a.sv_group,
+    const int64_t vo = vr * a.sv_slot + g * a.sv_group;
+    update_state<S, PL>(a.state + slot * a.st_slot + g * a.st_group, tid, r0, gam, a.v + vo, PL ? a.v_im + vo : nullptr,
                     kv, qv.x * a.q_scale, qv.y * a.q_scale, qv.z * a.q_scale, qv.w * a.q_scale, part);
     int base, nv;
     halving_reduce<S::NV, S::PAIRS>(part, lane, base, nv);
@@ -158,7 +176,7 @@ __global__ void __launch_bounds__((DecodeShape<D, 512>::THREADS)) decode_single_
 template <int D>
 constexpr int multi_threads() { return D >= 128 ? 1024 : 512; }
 
-template <int D, int MS>
+template <int D, int MS, bool PL>
 __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS)) decode_multi_kernel(qpam_decode_args a) {
     using S = DecodeShape<D, multi_threads<D>()>;
     const int tid = threadIdx.x;
@@ -176,14 +194,15 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
         for (int it = 0; it < S::ITERS; ++it)
             s[m][it] = __builtin_nontemporal_load(
                 reinterpret_cast<const floatx4 *>(st0 + m * a.st_state + 4 * (it * S::THREADS + tid)));
-    float4 qv = *reinterpret_cast<const float4 *>(a.q + vr * a.sq_slot + g * a.sq_group + 4 * cp);
-    float4 kv = *reinterpret_cast<const float4 *>(a.k + vr * a.sk_slot + g * a.sk_group + 4 * cp);
+    float4 qv = load_pair<PL>(a.q, a.q_im, vr * a.sq_slot + g * a.sq_group, cp);
+    float4 kv = load_pair<PL>(a.k, a.k_im, vr * a.sk_slot + g * a.sk_group, cp);
     apply_rope<D>(a, slot, cp, qv, kv);
     const float q0r = qv.x * a.q_scale, q0i = qv.y * a.q_scale, q1r = qv.z * a.q_scale, q1i = qv.w * a.q_scale;
-    const float *vrow = a.v + vr * a.sv_slot + g * a.sv_group;
+    const int64_t vo = vr * a.sv_slot + g * a.sv_group;
+    const float *vrow = a.v + vo, *vrow_im = PL ? a.v_im + vo : nullptr;
     float2 vv[S::ITERS];
 #pragma unroll
-    for (int it = 0; it < S::ITERS; ++it) vv[it] = *reinterpret_cast<const float2 *>(vrow + 2 * (it * S::ROWS_PER_IT + r0));
+    for (int it = 0; it < S::ITERS; ++it) vv[it] = load_one<PL>(vrow, vrow_im, it * S::ROWS_PER_IT + r0);
     float tot[S::NV];
 #pragma unroll
     for (int j = 0; j < S::NV; ++j) tot[j] = 0.f;
@@ -230,7 +249,7 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
 template <int D>
 constexpr int general_threads() { return D >= 128 ? 1024 : 256; }  // 8 float4 of state per lane at d = 64, 128
 
-template <int D>
+template <int D, bool PL>
 __global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS)) decode_general_kernel(qpam_decode_args a) {
     using S = DecodeShape<D, general_threads<D>()>;
     __shared__ float ys[D][2];
@@ -246,16 +265,17 @@ __global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS
     const int r0 = tid / S::PAIRS;      // first row of this lane
     const int lane = tid & 63;
 
-    float4 qv = *reinterpret_cast<const float4 *>(a.q + vr * a.sq_slot + g * a.sq_group + 4 * cp);
-    float4 kv = *reinterpret_cast<const float4 *>(a.k + vr * a.sk_slot + g * a.sk_group + 4 * cp);
+    float4 qv = load_pair<PL>(a.q, a.q_im, vr * a.sq_slot + g * a.sq_group, cp);
+    float4 kv = load_pair<PL>(a.k, a.k_im, vr * a.sk_slot + g * a.sk_group, cp);
     apply_rope<D>(a, slot, cp, qv, kv);
-    const float *vrow = a.v + vr * a.sv_slot + g * a.sv_group;
+    const int64_t vo = vr * a.sv_slot + g * a.sv_group;
+    const float *vrow = a.v + vo, *vrow_im = PL ? a.v_im + vo : nullptr;
 
     float yacc_r = 0.f, yacc_i = 0.f;  // lanes tid < D accumulate row tid
     for (int m = 0; m < a.n_states; ++m) {
         const float gam = a.gamma[vr * a.sg_slot + g * a.sg_group + m * a.sg_state];
         float part[S::NV];
-        update_state<S>(a.state + slot * a.st_slot + g * a.st_group + m * a.st_state, tid, r0, gam, vrow, kv,
+        update_state<S, PL>(a.state + slot * a.st_slot + g * a.st_group + m * a.st_state, tid, r0, gam, vrow, vrow_im, kv,
                         qv.x * a.q_scale, qv.y * a.q_scale, qv.z * a.q_scale, qv.w * a.q_scale, part);
         int base, nv;
         halving_reduce<S::NV, S::PAIRS>(part, lane, base, nv);
@@ -287,12 +307,12 @@ __global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS
     }
 }
 
-template <int D>
-int launch_decode(const qpam_decode_args &a, hipStream_t stream) {
+template <int D, bool PL>
+int launch_decode_pl(const qpam_decode_args &a, hipStream_t stream) {
     const long long blocks = (long long)a.n_active * a.n_groups;
     if (blocks == 0) return QPAM_OK;
     if (a.n_states == 1 && a.rot == nullptr) {
-        hipLaunchKernelGGL(decode_single_kernel<D>, dim3((unsigned)blocks), dim3(DecodeShape<D, 512>::THREADS), 0,
+        hipLaunchKernelGGL((decode_single_kernel<D, PL>), dim3((unsigned)blocks), dim3(DecodeShape<D, 512>::THREADS), 0,
                            stream, a);
         return launch_status("decode_single_kernel");
     }
@@ -302,32 +322,38 @@ int launch_decode(const qpam_decode_args &a, hipStream_t stream) {
     constexpr int MAX_MS = D >= 128 ? 1 : 4;
     switch (a.n_states) {
         case 1:
-            hipLaunchKernelGGL((decode_multi_kernel<D, 1>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
+            hipLaunchKernelGGL((decode_multi_kernel<D, 1, PL>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
             return launch_status("decode_multi_kernel<1>");
         case 2:
             if constexpr (MAX_MS >= 2) {
-                hipLaunchKernelGGL((decode_multi_kernel<D, 2>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
+                hipLaunchKernelGGL((decode_multi_kernel<D, 2, PL>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
                 return launch_status("decode_multi_kernel<2>");
             }
             break;
         case 3:
             if constexpr (MAX_MS >= 3) {
-                hipLaunchKernelGGL((decode_multi_kernel<D, 3>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
+                hipLaunchKernelGGL((decode_multi_kernel<D, 3, PL>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
                 return launch_status("decode_multi_kernel<3>");
             }
             break;
         case 4:
             if constexpr (MAX_MS >= 4) {
-                hipLaunchKernelGGL((decode_multi_kernel<D, 4>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
+                hipLaunchKernelGGL((decode_multi_kernel<D, 4, PL>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
                 return launch_status("decode_multi_kernel<4>");
             }
             break;
         default:
             break;
     }
-    hipLaunchKernelGGL(decode_general_kernel<D>, dim3((unsigned)blocks), dim3(DecodeShape<D, general_threads<D>()>::THREADS), 0, stream,
+    hipLaunchKernelGGL((decode_general_kernel<D, PL>), dim3((unsigned)blocks), dim3(DecodeShape<D, general_threads<D>()>::THREADS), 0, stream,
                        a);
     return launch_status("decode_general_kernel");
+}
+
+// planar q, k, v (q_im set) or interleaved rows
+template <int D>
+int launch_decode(const qpam_decode_args &a, hipStream_t stream) {
+    return a.q_im ? launch_decode_pl<D, true>(a, stream) : launch_decode_pl<D, false>(a, stream);
 }
 
 bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
@@ -347,14 +373,19 @@ extern "C" int qpam_decode_step(const qpam_decode_args *a, void *stream) {
     QPAM_REQUIRE(a->rope == nullptr || (a->pos != nullptr && a->rope_len >= 1 && aligned(a->rope, 16)),
                  "qpam_decode_step: rope needs positions, rope_len >= 1 and a 16-byte aligned table");
     QPAM_REQUIRE((long long)a->n_active * a->n_groups < (1ll << 31), "qpam_decode_step: grid too large");
-    // 16-byte vector access of S, q, k and 8-byte access of v, y
-    QPAM_REQUIRE(aligned(a->state, 16) && aligned(a->q, 16) && aligned(a->k, 16) && aligned(a->v, 8) &&
+    const bool planar = a->q_im != nullptr;
+    QPAM_REQUIRE((a->k_im != nullptr) == planar && (a->v_im != nullptr) == planar,
+                 "qpam_decode_step: q_im, k_im and v_im are all set (planar q, k, v) or all NULL");
+    // 16-byte vector access of S and interleaved q, k (8-byte planar), 8-byte access of v (4-byte planar), y
+    const int qa = planar ? 8 : 16, va = planar ? 4 : 8, qs = planar ? 2 : 4, vs = planar ? 1 : 2;
+    QPAM_REQUIRE(aligned(a->state, 16) && aligned(a->q, qa) && aligned(a->k, qa) && aligned(a->v, va) &&
+                     (!planar || (aligned(a->q_im, qa) && aligned(a->k_im, qa) && aligned(a->v_im, va))) &&
                      aligned(a->y, 8),
                  "qpam_decode_step: misaligned operand");
-    QPAM_REQUIRE(a->st_slot % 4 == 0 && a->st_group % 4 == 0 && a->st_state % 4 == 0 && a->sq_slot % 4 == 0 &&
-                     a->sq_group % 4 == 0 && a->sk_slot % 4 == 0 && a->sk_group % 4 == 0 &&
-                     a->sv_slot % 2 == 0 && a->sv_group % 2 == 0 && a->sy_slot % 2 == 0 && a->sy_group % 2 == 0,
-                 "qpam_decode_step: strides must keep 16-byte (S, q, k) / 8-byte (v, y) alignment");
+    QPAM_REQUIRE(a->st_slot % 4 == 0 && a->st_group % 4 == 0 && a->st_state % 4 == 0 && a->sq_slot % qs == 0 &&
+                     a->sq_group % qs == 0 && a->sk_slot % qs == 0 && a->sk_group % qs == 0 &&
+                     a->sv_slot % vs == 0 && a->sv_group % vs == 0 && a->sy_slot % 2 == 0 && a->sy_group % 2 == 0,
+                 "qpam_decode_step: strides must keep the vector accesses of S, q, k, v and y aligned");
     hipStream_t s = (hipStream_t)stream;
     switch (a->d) {
         case 16: return launch_decode<16>(*a, s);

@@ -28,7 +28,8 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     """In-place ragged decode step over a slot pool.
 
     state  [S, G, M, d, d, 2] fp32 (G = layers*heads, M states), updated in place
-    q,k,v  [R, G, d, 2] fp32 (q unscaled; multiplied by q_scale)
+    q,k,v  [R, G, d, 2] fp32 (q unscaled; multiplied by q_scale), or all three
+           as planar (re, im) pairs of [R, G, d] fp32 tensors with equal strides
     gamma  [R, G, M] fp32 (any strides)
     active optional int32 [n] slot ids (others untouched); None = all slots
     rot    optional [R, G, M, 2] fp32 complex rotation of each state's read
@@ -39,29 +40,42 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     Returns y [R, G, d, 2] (without `compact`, rows of unlisted slots are left
     as in `out` / zero).
     """
-    _check_cuda(state, q, k, v, gamma, active, rot, rope, pos)
+    planar = isinstance(q, (tuple, list))
+    if any(isinstance(t, (tuple, list)) != planar for t in (k, v)):
+        raise ValueError("q, k and v must all be interleaved tensors or all (re, im) plane pairs")
+    planes = [x for t in (q, k, v) for x in t] if planar else [q, k, v]
+    _check_cuda(state, *planes, gamma, active, rot, rope, pos)
     if state.dim() != 6 or state.shape[-1] != 2 or state.shape[-2] != state.shape[-3]:
         raise ValueError(f"state must be [S,G,M,d,d,2], got {tuple(state.shape)}")
     n_slots, n_groups, n_states, d = state.shape[:4]
     if compact and active is None:
         raise ValueError("compact rows need the active slot list")
     rows = active.numel() if compact else n_slots
-    for name, t in (("q", q), ("k", k), ("v", v)):
-        if tuple(t.shape) != (rows, n_groups, d, 2):
-            raise ValueError(f"{name} must be [{rows},{n_groups},{d},2], got {tuple(t.shape)}")
+    want = (rows, n_groups, d) if planar else (rows, n_groups, d, 2)
+    for name, t in zip(("q_re", "q_im", "k_re", "k_im", "v_re", "v_im") if planar else ("q", "k", "v"), planes):
+        if tuple(t.shape) != want:
+            raise ValueError(f"{name} must be {list(want)}, got {tuple(t.shape)}")
     if tuple(gamma.shape) != (rows, n_groups, n_states):
         raise ValueError(f"gamma must be [{rows},{n_groups},{n_states}], got {tuple(gamma.shape)}")
-    for t in (state, q, k, v, gamma) + ((rot,) if rot is not None else ()):
+    for t in [state, gamma] + planes + ([rot] if rot is not None else []):
         if t.dtype != torch.float32:
             raise ValueError("qpam decode works on fp32 tensors")
     if state.stride()[-3:] != (2 * d, 2, 1):
         raise ValueError("state matrices must be contiguous [d, d, 2]")
-    q, k, v = (t if t.stride()[-2:] == (2, 1) else t.contiguous() for t in (q, k, v))
+    if planar:
+        pairs = []
+        for re, im in (q, k, v):
+            if re.stride(-1) != 1 or re.stride() != im.stride():
+                re, im = re.contiguous(), im.contiguous()
+            pairs.append((re, im))
+        (q, q_im), (k, k_im), (v, v_im) = pairs
+    else:
+        q, k, v = (t if t.stride()[-2:] == (2, 1) else t.contiguous() for t in (q, k, v))
     if rot is not None:
         if tuple(rot.shape) != (rows, n_groups, n_states, 2):
             raise ValueError(f"rot must be [{rows},{n_groups},{n_states},2]")
         rot = rot if rot.stride(-1) == 1 else rot.contiguous()
-    y = out if out is not None else torch.zeros_like(q)
+    y = out if out is not None else torch.zeros(rows, n_groups, d, 2, device=state.device, dtype=torch.float32)
     if active is not None:
         if active.dtype != torch.int32:
             active = active.to(torch.int32)
@@ -77,6 +91,8 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     a.state = state.data_ptr()
     a.st_slot, a.st_group, a.st_state = state.stride(0), state.stride(1), state.stride(2)
     a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    if planar:
+        a.q_im, a.k_im, a.v_im = q_im.data_ptr(), k_im.data_ptr(), v_im.data_ptr()
     a.sq_slot, a.sq_group = q.stride(0), q.stride(1)
     a.sk_slot, a.sk_group = k.stride(0), k.stride(1)
     a.sv_slot, a.sv_group = v.stride(0), v.stride(1)
@@ -207,6 +223,7 @@ class SlotPool:
 
     def step(self, layer, q, k, v, gamma, active, rot=None, q_scale=None, out=None, compact=False):
         """One token for the listed slots on one layer: q, k, v [n_slots, heads, d, 2]
+        (or planar (re, im) pairs of [n_slots, heads, d], as decode_step takes)
         (rows of unlisted slots ignored; q unscaled), gamma [n_slots, heads, states],
         rot optional [n_slots, heads, states, 2]; with `compact` the rows are those of
         the listed slots in order ([n_active, ...]).  RoPE at each slot's position; the

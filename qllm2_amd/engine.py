@@ -14,10 +14,10 @@ live sequences:
     the E3 phase / score projections (v11/model.py:230-257, 309-347);
   * the prologue kernel (qpam_prologue_fwd: decay, GSP blend, gamma floor,
     qk-norm, rotations) on that [n, 1] batch;
-  * one decode launch (qpam_decode_step, compact rows, per-slot RoPE in the
-    kernel: the rotation has unit modulus per feature, so it commutes with
-    the qk-norm the prologue applied first) that updates the live slots'
-    states in the SlotPool and reads y;
+  * one decode launch (qpam_decode_step, compact rows, planar q, k, v as the
+    prologue wrote them, per-slot RoPE in the kernel: the rotation has unit
+    modulus per feature, so it commutes with the qk-norm the prologue applied
+    first) that updates the live slots' states in the SlotPool and reads y;
   * one GEMM from the interleaved y to the interleaved o_proj output.
 
 With `graphs=True` the per-token work of all layers is captured once per
@@ -173,9 +173,8 @@ class DecodeEngine:
             phase=None if phase is None else phase.view(n, 1, h, m),
             routing=None if routing is None else routing.view(n, 1, h, m),
             rope=None, qk_norm=layer.qk_norm, gamma_floor=layer.gamma_floor or 0.0)
-        q = torch.stack([qr[:, :, 0], qi[:, :, 0]], -1)                      # [n, H, d, 2]
-        k = torch.stack([kr[:, :, 0], ki[:, :, 0]], -1)
-        v = torch.stack([vr[:, :, 0], vi[:, :, 0]], -1)
+        # the prologue's planes go to the decode kernel as they are ([n, H, d] views)
+        q, k, v = ((re[:, :, 0], im[:, :, 0]) for re, im in ((qr, qi), (kr, ki), (vr, vi)))
         g = gamma[..., 0].permute(1, 2, 0)                                    # [n, H, K] view
         r = torch.stack([rot[0][..., 0], rot[1][..., 0]], -1).permute(1, 2, 0, 3) if rot is not None else None
         if not layer.use_rope:

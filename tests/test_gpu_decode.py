@@ -187,3 +187,38 @@ def test_slot_pool_e3_continuous_batching(gpu_lib):
             s["pos"] += 1
         assert pool.pos.cpu()[active.long()].tolist() == [
             s["pos"] for s in sorted(seqs.values(), key=lambda s: s["slot"])]
+
+
+@pytest.mark.parametrize("d,M,use_rot", [(64, 1, False), (64, 3, True), (32, 5, True), (128, 1, True),
+                                         (16, 2, False)])
+def test_decode_planar_inputs_equal_interleaved(gpu_lib, d, M, use_rot):
+    """q, k, v handed over as planar (re, im) planes (the engine passes the
+    prologue's planes) give the interleaved call's y and state bit for bit: the
+    kernels read the same values, only through 8-byte instead of 16-byte loads;
+    compact rows with per-slot RoPE, every kernel variant (one state, several,
+    the general state loop)."""
+    from qllm2_amd.decode import build_rope_cache, decode_step
+    S, G = 7, 3
+    state, q, k, v, gamma, rot = _pool(S, G, M, d, 900 + d + M)
+    active = torch.tensor([6, 0, 2, 4], dtype=torch.int32).cuda()
+    n = active.numel()
+    qc, kc, vc = (x[:n].cuda() for x in (q, k, v))
+    gc, rc = gamma[:n].cuda(), rot[:n].cuda() if use_rot else None
+    rope = build_rope_cache(32, d, device="cuda")
+    pos = torch.tensor([3, 30, 1, 0, 9, 2, 17], dtype=torch.int32).cuda()
+    runs = []
+    for planar in (False, True):
+        st = state.cuda()
+        qkv = [(x[..., 0].contiguous(), x[..., 1].contiguous()) for x in (qc, kc, vc)] if planar else [qc, kc, vc]
+        y = decode_step(st, *qkv, gc, active=active, rot=rc, q_scale=d ** -0.5, rope=rope, pos=pos, compact=True)
+        torch.cuda.synchronize()
+        runs.append((y.cpu(), st.cpu()))
+    assert torch.equal(runs[0][0], runs[1][0]) and torch.equal(runs[0][1], runs[1][1])
+
+
+def test_decode_planar_inputs_rejected_when_mixed(gpu_lib):
+    from qllm2_amd.decode import decode_step
+    state, q, k, v, gamma, _ = _pool(2, 1, 1, 16, 5)
+    st, q, k, v, gamma = (x.cuda() for x in (state, q, k, v, gamma))
+    with pytest.raises(ValueError, match="plane pairs"):
+        decode_step(st, (q[..., 0], q[..., 1]), k, v, gamma)

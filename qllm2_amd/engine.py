@@ -80,8 +80,8 @@ class DecodeEngine:
 
     # ------------------------------------------------------------ weights
     def refresh_weights(self):
-        """Rebuild the GEMM weights from the layers' parameters (call after
-        changing them)."""
+        """Rebuild the GEMM weights (and the summed decay bias) from the
+        layers' parameters (call after changing them)."""
         h, d = self.n_heads, self.head_dim
         cols = proj_columns(h)
         self._graphs = {}  # captured graphs hold the old weight tensors
@@ -97,9 +97,20 @@ class DecodeEngine:
                 b_out = None
                 if getattr(layer.o_proj, "bias_real", None) is not None:
                     b_out = torch.stack([layer.o_proj.bias_real, layer.o_proj.bias_imag], 1).reshape(2 * dim)
-                self._w.append(dict(w_in=w_in.float().contiguous(), b_in=None if b_in is None else b_in.float(),
-                                    w_out=w_out.float().contiguous(),
-                                    b_out=None if b_out is None else b_out.float(), dim=dim))
+                entry = dict(w_in=w_in.float().contiguous(), b_in=None if b_in is None else b_in.float(),
+                             w_out=w_out.float().contiguous(), b_out=None if b_out is None else b_out.float(),
+                             dim=dim, w_mag=None,
+                             dt_bias=(layer.dt_bias if layer.dt_proj.bias is None
+                                      else layer.dt_bias + layer.dt_proj.bias).float().contiguous())
+                # the protect gate and the phase projection both read |x|: one GEMM for both
+                if (layer.use_gsp and not layer.gate_content_aware and self.n_states > 1
+                        and not layer.routing_content_aware):
+                    lin = (layer.protect_gate, layer.phase_proj)
+                    entry["w_mag"] = torch.cat([m.weight for m in lin], 0).float().contiguous()
+                    entry["b_mag"] = (torch.cat([m.bias if m.bias is not None else m.weight.new_zeros(m.weight.shape[0])
+                                                 for m in lin]).float()
+                                      if any(m.bias is not None for m in lin) else None)
+                self._w.append(entry)
 
     # ------------------------------------------------------------ slots
     def admit(self, position, states=None):
@@ -131,11 +142,18 @@ class DecodeEngine:
         return st.unsqueeze(1) if self.n_states > 1 else st[0].unsqueeze(0)
 
     # ------------------------------------------------------------ step
-    def _gates(self, layer, x):
+    def _gates(self, layer, x, w):
         """protect logits [n, H], phase and routing [n, H, K] of the live rows."""
         n, h, m = x.shape[0], self.n_heads, self.n_states
         mag = None
         protect = phase = routing = None
+        if w["w_mag"] is not None:  # protect gate and phase projection in one GEMM from |x|
+            mag = cabs(x)
+            gl = F.linear(mag, w["w_mag"], w["b_mag"])
+            protect, phase = gl[:, :h], gl[:, h:].reshape(n, h, m)
+            if layer.state_compete:
+                routing = F.softmax(layer.score_proj(mag).view(n, h, m), dim=-1) * m
+            return protect, phase, routing
         if layer.use_gsp:
             if layer.gate_content_aware:
                 protect = layer.protect_gate(_cat_planes(x))
@@ -165,10 +183,9 @@ class DecodeEngine:
             return x.new_zeros(0, dim, 2)
         x = x.float().contiguous()
         proj = F.linear(x.view(n, 2 * dim), w["w_in"], w["b_in"]).view(n, 1, -1)
-        protect, phase, routing = self._gates(layer, x)
-        dt_bias = layer.dt_bias if layer.dt_proj.bias is None else layer.dt_bias + layer.dt_proj.bias
+        protect, phase, routing = self._gates(layer, x, w)
         (qr, qi), (kr, ki), (vr, vi), gamma, rot = pam_prologue(
-            proj, dt_bias, n_heads=h, n_states=m, state_offset=layer.state_dt_offset if m > 1 else None,
+            proj, w["dt_bias"], n_heads=h, n_states=m, state_offset=layer.state_dt_offset if m > 1 else None,
             protect=None if protect is None else protect.view(n, 1, h),
             phase=None if phase is None else phase.view(n, 1, h, m),
             routing=None if routing is None else routing.view(n, 1, h, m),

@@ -196,7 +196,9 @@ class DecodeEngine:
         r = torch.stack([rot[0][..., 0], rot[1][..., 0]], -1).permute(1, 2, 0, 3) if rot is not None else None
         if not layer.use_rope:
             raise NotImplementedError("DecodeEngine applies RoPE per slot; layers without RoPE are not supported")
-        y = self.pool.step(layer_idx, q, k, v, g, slots, rot=r, q_scale=d ** -0.5, compact=True)
+        # every listed slot is live, so the kernel writes every row of y: no zero fill
+        y = self.pool.step(layer_idx, q, k, v, g, slots, rot=r, q_scale=d ** -0.5, compact=True,
+                           out=torch.empty(n, h, d, 2, device=x.device, dtype=torch.float32))
         return F.linear(y.view(n, 2 * h * d), w["w_out"], w["b_out"]).view(n, dim, 2)
 
     def _layers(self, x, slots, between):

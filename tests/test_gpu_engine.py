@@ -100,3 +100,36 @@ def test_engine_matches_per_sequence_oracle(gpu_lib, name, graphs):
     for si in range(len(SEQS)):
         out = torch.stack(got[si])
         assert _rel(out, ref_out[si]) < 1e-4, f"seq {si}: {_rel(out, ref_out[si]):.2e}"
+
+
+def test_engine_graph_replay_with_between_hook(gpu_lib):
+    """A `between` hook (the model's own work between layers: here a residual
+    scale and a per-feature gain, device work only) is captured into the graph
+    with the layers: graph replays over changing live sets give the eager
+    engine's outputs and states (rel 1e-6: the padded batches may run the GEMMs
+    with other tilings)."""
+    from qllm2_amd.engine import DecodeEngine
+    cfg = V.config(**CFGS["e3"])
+    dim = cfg["dim"]
+    params = [V.make_params(cfg, 830 + i) for i in range(2)]
+    layers = [V.V11PAMLayer(cfg, {k: v.float() for k, v in p.items()}, dtype=torch.float32).cuda().eval()
+              for p in params]
+    gain = torch.linspace(0.5, 1.5, dim, device="cuda").view(1, dim, 1)
+    hook = (lambda li, out: out * gain + 0.1 * li)
+    engines = [DecodeEngine(layers, n_slots=6, max_len=64, graphs=gr, graph_bucket=4) for gr in (False, True)]
+    g = torch.Generator().manual_seed(831)
+    for e in engines:
+        for pos in (3, 9, 0, 5, 12):
+            e.admit(pos)
+    live_sets = [[0, 1, 2, 3, 4], [4, 2, 0], [1, 3], [0, 1, 2, 3, 4], [3, 1], [4, 2, 0]]
+    for live in live_sets:
+        x = torch.randn(len(live), dim, 2, generator=g).cuda()
+        slots = torch.tensor(live, dtype=torch.int32, device="cuda")
+        ys = [e.step(x, slots, between=hook, host_slots=live).clone() for e in engines]
+        torch.cuda.synchronize()
+        assert _rel(ys[1], ys[0]) < 1e-6, f"live {live}: {_rel(ys[1], ys[0]):.2e}"
+    for slot in range(5):
+        for li in range(2):
+            a, b = (e.layer_state(li, slot) for e in engines)
+            assert _rel(b, a) < 1e-6
+    assert len(engines[1]._graphs) == 2  # buckets of 4 and 8 rows

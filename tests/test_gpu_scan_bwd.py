@@ -320,3 +320,37 @@ def test_bf16_head_merged_y_equals_rounded_fp32(gpu_lib, T):
     for a, b in zip(g16, g32):
         assert a.dtype == b.dtype
         assert _rel(a, b) < 1e-6
+
+
+def _random_cases(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    pick = (lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))])
+    cases = []
+    for i in range(n):
+        cases.append((pick([1, 2, 3, 4, 5, 6]), pick([16, 32, 48, 64, 80, 128]), int(torch.randint(1, 260, (1,), generator=g)),
+                      pick([16, 32, 64]), pick(["f32", "bf16"]), bool(torch.randint(2, (1,), generator=g)),
+                      bool(torch.randint(2, (1,), generator=g))))
+    return cases
+
+
+@pytest.mark.parametrize("M,d,T,C,dt,with_rot,with_s0", _random_cases(10, 4242))
+def test_scan_seeded_random_shapes(gpu_lib, M, d, T, C, dt, with_rot, with_s0):
+    """Seeded random shapes across every axis the scan takes (states 1-6, head
+    dims below, at and above 64, lengths 1-259, chunks 16/32/64, fp32 and bf16,
+    with and without rotations and a start state): Y, S and every gradient
+    against oracle autograd."""
+    dtype = torch.float32 if dt == "f32" else torch.bfloat16
+    B, H = 1, 2
+    case = _case(M, B, H, T, d, 4300 + M * 17 + d + T + C, with_rot, with_s0, dtype)
+    q, k, v, gamma, dy, ds, phase, routing, s0 = case
+    with torch.no_grad():
+        y_ref, s_ref = O.multistate_fused(q.double(), k.double(), v.double(), gamma.double(), phase.double(),
+                                          routing.double(), d, C,
+                                          state=s0.double() if s0 is not None else None)
+    ref = _oracle_grads(*case, d, C)
+    outs = {}
+    got = _gpu_grads(*case, d, C, dtype, with_rot, outs)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert _rel(outs["y"], y_ref) < tol and _rel_heads(outs["y"], y_ref, 2) < tol
+    assert _rel(outs["s"], s_ref) < tol and _rel_heads(outs["s"], s_ref, 3) < tol
+    _check(got, ref, tol)

@@ -199,3 +199,30 @@ def test_delta_decay_regimes(gpu_lib):
     assert _rel_heads(s, sr) < 1e-4, f"s {_rel_heads(s, sr):.2e}"
     for name, a, r in zip(NAMES[:5], grads[:5], rgrads[:5]):
         assert _rel_heads(a, r) < 1e-4, f"{name}: {_rel_heads(a, r):.2e}"
+
+
+def _delta_cases(n, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [([16, 32, 48, 64][int(torch.randint(4, (1,), generator=g))], int(torch.randint(1, 300, (1,), generator=g)),
+             bool(torch.randint(2, (1,), generator=g)), bool(torch.randint(2, (1,), generator=g))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("d,T,with_s0,with_ds", _delta_cases(8, 777))
+def test_delta_seeded_random_shapes(gpu_lib, d, T, with_s0, with_ds):
+    """Seeded random head dims (16-64), lengths (1-299: partial and multiple
+    chunks), start states and state gradients: Y, S and every gradient against
+    the chunked oracle."""
+    B, H = 1, 2
+    q, k, v, g, b = D.make_delta_inputs(B, H, T, d, 780 + d + T)
+    gen = torch.Generator().manual_seed(781 + d + T)
+    s0 = torch.randn(B, H, d, d, 2, generator=gen, dtype=torch.float64) * 0.05 if with_s0 else None
+    dy = torch.randn(B, H, T, d, 2, generator=gen, dtype=torch.float64)
+    ds = torch.randn(B, H, d, d, 2, generator=gen, dtype=torch.float64) * 0.1 if with_ds else None
+    y, s, grads = _run(q, k, v, g, b, s0, dy, ds, 1e-6, d=d)
+    yr, sr, rgrads = _ref(q, k, v, g, b, s0, dy, ds, chunked=True, d=d)
+    assert _rel(y, yr) < 1e-4, f"y {_rel(y, yr):.2e}"
+    assert _rel(s, sr) < 1e-4, f"s {_rel(s, sr):.2e}"
+    for name, a, r in zip(NAMES, grads, rgrads):
+        if a is None or r is None:
+            continue
+        assert _rel(a, r) < 1e-4, f"{name}: {_rel(a, r):.2e}"

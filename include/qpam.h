@@ -127,6 +127,9 @@ typedef struct {
      * same strides (a prologue's output planes need no interleaving copy);
      * NULL = interleaved [d][2] rows. */
     const float *q_im, *k_im, *v_im;
+    /* optional planar rotation (ABI 7): rot points at the real plane and rot_im at
+     * the imaginary one, same strides; NULL = interleaved [2] entries. */
+    const float *rot_im;
 } qpam_decode_args;
 
 int qpam_decode_step(const qpam_decode_args *a, void *stream);

@@ -211,9 +211,9 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
         const float gam = a.gamma[vr * a.sg_slot + g * a.sg_group + m * a.sg_state];
         float rr = 1.f, ri = 0.f;
         if (a.rot) {
-            const float *rp = a.rot + vr * a.sr_slot + g * a.sr_group + m * a.sr_state;
-            rr = rp[0];
-            ri = rp[1];
+            const int64_t ro = vr * a.sr_slot + g * a.sr_group + m * a.sr_state;
+            rr = a.rot[ro];
+            ri = a.rot_im ? a.rot_im[ro] : a.rot[ro + 1];
         }
 #pragma unroll
         for (int it = 0; it < S::ITERS; ++it) {
@@ -290,8 +290,8 @@ __global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS
         if (tid < D) {
             const float yr = ys[tid][0], yi = ys[tid][1];
             if (a.rot) {
-                const float *rp = a.rot + vr * a.sr_slot + g * a.sr_group + m * a.sr_state;
-                const float rr = rp[0], ri = rp[1];
+                const int64_t ro = vr * a.sr_slot + g * a.sr_group + m * a.sr_state;
+                const float rr = a.rot[ro], ri = a.rot_im ? a.rot_im[ro] : a.rot[ro + 1];
                 yacc_r += rr * yr - ri * yi;
                 yacc_i += rr * yi + ri * yr;
             } else {
@@ -373,6 +373,7 @@ extern "C" int qpam_decode_step(const qpam_decode_args *a, void *stream) {
     QPAM_REQUIRE(a->rope == nullptr || (a->pos != nullptr && a->rope_len >= 1 && aligned(a->rope, 16)),
                  "qpam_decode_step: rope needs positions, rope_len >= 1 and a 16-byte aligned table");
     QPAM_REQUIRE((long long)a->n_active * a->n_groups < (1ll << 31), "qpam_decode_step: grid too large");
+    QPAM_REQUIRE(a->rot_im == nullptr || a->rot != nullptr, "qpam_decode_step: rot_im without rot");
     const bool planar = a->q_im != nullptr;
     QPAM_REQUIRE((a->k_im != nullptr) == planar && (a->v_im != nullptr) == planar,
                  "qpam_decode_step: q_im, k_im and v_im are all set (planar q, k, v) or all NULL");

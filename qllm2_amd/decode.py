@@ -32,7 +32,8 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
            as planar (re, im) pairs of [R, G, d] fp32 tensors with equal strides
     gamma  [R, G, M] fp32 (any strides)
     active optional int32 [n] slot ids (others untouched); None = all slots
-    rot    optional [R, G, M, 2] fp32 complex rotation of each state's read
+    rot    optional [R, G, M, 2] fp32 complex rotation of each state's read, or a
+           planar (re, im) pair of [R, G, M] fp32 tensors with equal strides
     rope   optional [P, d, 2] fp32 rotary table (build_rope_cache) with
     pos    int32 [S] per-slot positions: q and k of slot a are rotated by rope[pos[a]]
     compact False: R = S, row a of q, k, v, gamma, rot, y belongs to slot a
@@ -44,7 +45,7 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     if any(isinstance(t, (tuple, list)) != planar for t in (k, v)):
         raise ValueError("q, k and v must all be interleaved tensors or all (re, im) plane pairs")
     planes = [x for t in (q, k, v) for x in t] if planar else [q, k, v]
-    _check_cuda(state, *planes, gamma, active, rot, rope, pos)
+    _check_cuda(state, *planes, gamma, active, *(rot if isinstance(rot, (tuple, list)) else (rot,)), rope, pos)
     if state.dim() != 6 or state.shape[-1] != 2 or state.shape[-2] != state.shape[-3]:
         raise ValueError(f"state must be [S,G,M,d,d,2], got {tuple(state.shape)}")
     n_slots, n_groups, n_states, d = state.shape[:4]
@@ -57,7 +58,9 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
             raise ValueError(f"{name} must be {list(want)}, got {tuple(t.shape)}")
     if tuple(gamma.shape) != (rows, n_groups, n_states):
         raise ValueError(f"gamma must be [{rows},{n_groups},{n_states}], got {tuple(gamma.shape)}")
-    for t in [state, gamma] + planes + ([rot] if rot is not None else []):
+    rot_pl = isinstance(rot, (tuple, list))
+    rots = list(rot) if rot_pl else ([rot] if rot is not None else [])
+    for t in [state, gamma] + planes + rots:
         if t.dtype != torch.float32:
             raise ValueError("qpam decode works on fp32 tensors")
     if state.stride()[-3:] != (2 * d, 2, 1):
@@ -71,7 +74,15 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
         (q, q_im), (k, k_im), (v, v_im) = pairs
     else:
         q, k, v = (t if t.stride()[-2:] == (2, 1) else t.contiguous() for t in (q, k, v))
-    if rot is not None:
+    rot_im = None
+    if rot_pl:
+        rot, rot_im = rots
+        for t in (rot, rot_im):
+            if tuple(t.shape) != (rows, n_groups, n_states):
+                raise ValueError(f"rot planes must be [{rows},{n_groups},{n_states}]")
+        if rot.stride() != rot_im.stride():
+            rot, rot_im = rot.contiguous(), rot_im.contiguous()
+    elif rot is not None:
         if tuple(rot.shape) != (rows, n_groups, n_states, 2):
             raise ValueError(f"rot must be [{rows},{n_groups},{n_states},2]")
         rot = rot if rot.stride(-1) == 1 else rot.contiguous()
@@ -101,6 +112,8 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     if rot is not None:
         a.rot = rot.data_ptr()
         a.sr_slot, a.sr_group, a.sr_state = rot.stride(0), rot.stride(1), rot.stride(2)
+        if rot_im is not None:
+            a.rot_im = rot_im.data_ptr()
     a.y = y.data_ptr()
     a.sy_slot, a.sy_group = y.stride(0), y.stride(1)
     if rope is not None:

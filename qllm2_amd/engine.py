@@ -193,7 +193,7 @@ class DecodeEngine:
         # the prologue's planes go to the decode kernel as they are ([n, H, d] views)
         q, k, v = ((re[:, :, 0], im[:, :, 0]) for re, im in ((qr, qi), (kr, ki), (vr, vi)))
         g = gamma[..., 0].permute(1, 2, 0)                                    # [n, H, K] view
-        r = torch.stack([rot[0][..., 0], rot[1][..., 0]], -1).permute(1, 2, 0, 3) if rot is not None else None
+        r = tuple(x[..., 0].permute(1, 2, 0) for x in rot) if rot is not None else None  # planar [n, H, K] views
         if not layer.use_rope:
             raise NotImplementedError("DecodeEngine applies RoPE per slot; layers without RoPE are not supported")
         # every listed slot is live, so the kernel writes every row of y: no zero fill

@@ -192,8 +192,9 @@ def test_slot_pool_e3_continuous_batching(gpu_lib):
 @pytest.mark.parametrize("d,M,use_rot", [(64, 1, False), (64, 3, True), (32, 5, True), (128, 1, True),
                                          (16, 2, False)])
 def test_decode_planar_inputs_equal_interleaved(gpu_lib, d, M, use_rot):
-    """q, k, v handed over as planar (re, im) planes (the engine passes the
-    prologue's planes) give the interleaved call's y and state bit for bit: the
+    """q, k, v (and the rotations) handed over as planar (re, im) planes (the
+    engine passes the prologue's planes) give the interleaved call's y and state
+    bit for bit: the
     kernels read the same values, only through 8-byte instead of 16-byte loads;
     compact rows with per-slot RoPE, every kernel variant (one state, several,
     the general state loop)."""
@@ -210,7 +211,8 @@ def test_decode_planar_inputs_equal_interleaved(gpu_lib, d, M, use_rot):
     for planar in (False, True):
         st = state.cuda()
         qkv = [(x[..., 0].contiguous(), x[..., 1].contiguous()) for x in (qc, kc, vc)] if planar else [qc, kc, vc]
-        y = decode_step(st, *qkv, gc, active=active, rot=rc, q_scale=d ** -0.5, rope=rope, pos=pos, compact=True)
+        r = (rc[..., 0].contiguous(), rc[..., 1].contiguous()) if planar and rc is not None else rc
+        y = decode_step(st, *qkv, gc, active=active, rot=r, q_scale=d ** -0.5, rope=rope, pos=pos, compact=True)
         torch.cuda.synchronize()
         runs.append((y.cpu(), st.cpu()))
     assert torch.equal(runs[0][0], runs[1][0]) and torch.equal(runs[0][1], runs[1][1])

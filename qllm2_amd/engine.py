@@ -25,8 +25,10 @@ batch-size bucket (live rows rounded up to a multiple of `graph_bucket`) in a
 HIP graph and replayed: one launch per step instead of about a dozen per
 layer, so the host's dispatch of the small GEMMs and kernels no longer sets
 the step time.  The padded rows point at reserved scratch slots (zero input,
-their states are never read).  The first step of each bucket runs eagerly
-and captures the graph; a grown RoPE table or new weights start new graphs.
+their states are never read).  The first step of each bucket runs eagerly on
+the padded batch (so library work done on a shape's first use, such as GEMM
+autotuning, happens outside the capture) and captures the graph; a grown RoPE
+table or new weights start new graphs.
 
 Prefill stays the fused layer forward (pam_layer.forward); its per-layer
 states enter the pool through `admit`.  The layers must use head-scalar decay,
@@ -240,12 +242,15 @@ class DecodeEngine:
         key = (nb, id(between), rope, self._wver)
         entry = self._graphs.get(key) if n else None
         if entry is None:
-            out = self._layers(x, slots, between)
+            if n and nb > n:  # run the padded batch eagerly: the capture then meets only shapes already run
+                x = torch.cat([x.float(), x.new_zeros(nb - n, *x.shape[1:], dtype=torch.float32)])
+                slots = torch.cat([slots.to(torch.int32), self._scratch[:nb - n]])
+            out = self._layers(x, slots, between)[:n]
             if n:
                 if len(self._graphs) >= self.MAX_GRAPHS:  # e.g. a new `between` callable every step
                     self._graphs = {}
                 self._graphs[key] = self._capture(nb, between)
-            self.pool.advance(slots, host_slots)
+            self.pool.advance(slots[:n], host_slots)
             return out
         entry["x"][:n].copy_(x)
         entry["slots"][:n].copy_(slots)

@@ -255,6 +255,48 @@ def test_fused_layer_bf16(gpu_lib):
         assert _rel(params[name].grad, pr[name].grad) < 2e-2, name
 
 
+def test_fused_layer_graph_capture(gpu_lib):
+    """The fused layer's forward and backward captured in one HIP graph: three
+    replays on new inputs (copied into the captured input buffer), with eager
+    steps and host synchronisations between them, each give the eager output,
+    dx and parameter gradients of the same input (fp32, rel 1e-6)."""
+    cfg = _layer_cfg(n_states=3)
+    dim = 48
+    p = L.make_layer_params(cfg, dim, 970)
+    layer = _Layer(cfg, p).cuda()
+    params = list(layer.parameters())
+    gen = torch.Generator().manual_seed(971)
+    dy = torch.randn(2, 128, dim, 2, generator=gen).cuda()
+
+    def eager(x):
+        xx = x.clone().requires_grad_(True)
+        y, _ = layer(xx)
+        return [y.detach()] + list(torch.autograd.grad(y, [xx] + params, dy))
+
+    static_x = torch.randn(2, 128, dim, 2, generator=gen).cuda().requires_grad_(True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            y, _ = layer(static_x)
+            torch.autograd.grad(y, [static_x] + params, dy)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_static, _ = layer(static_x)
+        g_static = torch.autograd.grad(y_static, [static_x] + params, dy)
+    for i in range(3):
+        x = torch.randn(2, 128, dim, 2, generator=gen).cuda()
+        want = eager(x)
+        torch.cuda.synchronize()
+        static_x.data.copy_(x)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [y_static] + list(g_static)
+        for a, b in zip(got, want):
+            assert _rel(a, b) < 1e-6, f"replay {i}: {_rel(a, b):.2e}"
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_cabs_matches_oracle(gpu_lib, dtype):
     """The cabs kernel (|z| with the reference's +1e-8) and its backward

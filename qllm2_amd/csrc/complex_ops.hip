@@ -745,7 +745,9 @@ __global__ void __launch_bounds__(SUM_THREADS) partial_sum_kernel(const float *p
 int n_params(int op) { return op == QPAM_CPLX_NORM || op == QPAM_CPLX_MOD_RELU ? 1 : op == QPAM_CPLX_MOD_SWISH ? 2 : 0; }
 
 int row_blocks(int64_t rows) { return (int)std::min<int64_t>((rows + WAVES - 1) / WAVES, MAX_BLOCKS); }
-int flat_blocks(int64_t n) { return (int)std::min<int64_t>((n + THREADS - 1) / THREADS, 4 * MAX_BLOCKS); }
+// flat elementwise grid: one 16-byte group per thread up to 65536 blocks (a grid-stride loop past that);
+// measured at 65536 x 1024 complex bf16: CGU gate fwd+bwd 0.386 ms with an 8192-block cap, 0.356 ms here
+int flat_blocks(int64_t n) { return (int)std::min<int64_t>((n + THREADS - 1) / THREADS, 65536); }
 
 int validate(const qpam_cplx_args *a, const char *who, bool bwd) {
     QPAM_REQUIRE(a != nullptr, "%s: null args", who);

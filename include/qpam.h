@@ -4,9 +4,15 @@
  * Plain C: POD argument structs of dimensions, strides (in elements) and
  * device pointers; every entry point launches asynchronously on the HIP
  * stream passed as `stream` (NULL = the null stream), performs no host
- * synchronisation, allocates no device memory (the caller owns every buffer,
- * workspaces included) and returns a qpam_status.  qpam_last_error() returns a
+ * synchronisation and returns a qpam_status.  qpam_last_error() returns a
  * thread-local message for the last non-zero status on the calling thread.
+ * The caller owns every input, output and workspace buffer.  The library
+ * itself holds, per device and until the process ends: a hipBLASLt handle and
+ * its plan cache (created by the first LM-head backward that uses hipBLASLt),
+ * one extra default-priority stream with two events (created by the first
+ * call that forks work onto it), and the statically allocated 64 MiB scratch
+ * array of qpam_scan_fwd_noalloc (a module-scope device array, present from
+ * load).  No other entry point allocates device memory.
  *
  * Complex tensors are planar: separate real and imaginary planes that share
  * one set of strides, innermost axis contiguous.  The decode state is the one
@@ -191,9 +197,14 @@ int qpam_scan_fwd(const qpam_scan_args *a, void *stream);
  * (qpam_scan_workspace_size) fails with QPAM_ERR_WORKSPACE before any launch;
  * 64 MiB covers one 2048-token sequence of 12 heads with up to 4 fp32 states.
  * Every call on a GPU shares that GPU's array and it keeps only the last
- * call's states: calls that overlap on one GPU (two streams or threads) race,
- * and no qpam_scan_bwd can follow (training uses qpam_scan_fwd).  The call
- * allocates nothing (no hipMalloc, no library allocation). */
+ * call's states: calls that overlap on one GPU would race, and no
+ * qpam_scan_bwd can follow (training uses qpam_scan_fwd).  Each call records
+ * an event on its stream after its launches; a call on another stream while
+ * that event is still pending fails with QPAM_ERR_ARG (checked with
+ * hipEventQuery, no host wait; not checked under HIP graph capture, where the
+ * caller orders the graph's replays).  The first call on a device sets up the
+ * symbol address and that event; no call allocates device memory (no
+ * hipMalloc, no library allocation). */
 #define QPAM_SCAN_FWD_NOALLOC_MAX_BYTES (64u << 20)
 int qpam_scan_fwd_noalloc(const qpam_scan_args *a, void *stream);
 
@@ -316,15 +327,22 @@ int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void *mag, cons
  * strides sg_*; s0 optional fp32 planar [B,H,d,d] contiguous; y fp32 planar
  * [B,H,T,d]; s_re/s_im the final state [B,H,d,d].  The workspace (size from
  * qpam_delta_workspace_size, or NULL when no backward follows) keeps, per
- * 64-step chunk, the entering state, the solved U and the chunk's triangular
- * products for the backward.  d == 64.  The chunked form follows the reference's
- * decay matrix exp(min(L_t - L_s, 0)) and its state-write weight
- * alpha_last / (alpha_s + 1e-12) (v11/model.py:508-510, 565-566).
+ * chunk, the entering state, the solved U and the chunk's triangular products
+ * for the backward.  d == 64.  The chunked form follows the reference's chunks
+ * of `chunk` steps (v11/model.py:494), its decay matrix exp(min(L_t - L_s, 0))
+ * and its state-write weight alpha_last / (alpha_s + 1e-12)
+ * (v11/model.py:508-510, 565-566); gamma + gamma_eps is kept at or above the
+ * smallest normal float.
  */
 typedef struct {
     int32_t B, H, T, d;
     float q_scale;
     float gamma_eps;
+    int32_t chunk;                         /* steps per chunk of the chunked form: the reference's
+                                              delta_chunk, 1..64 (0 = 64) */
+    int32_t exact_write;                   /* 1: state-write weight exp(L_last - L_s) (the token
+                                              recurrence, _recur_step_delta) instead of the chunked
+                                              form's alpha_last / (alpha_s + 1e-12) */
     qpam_cview q, k, v;
     const float *gamma, *beta;
     int64_t sg_b, sg_h, sg_t;

@@ -12,11 +12,13 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
 QPAM_BF16 = 1
+QPAM_OK = 0
+QPAM_ERR_ARG = 1
 QPAM_ERR_WORKSPACE = 4
 QPAM_SCAN_FWD_NOALLOC_MAX_BYTES = 64 << 20
 
@@ -116,6 +118,7 @@ class CplxArgs(ctypes.Structure):
 class DeltaArgs(ctypes.Structure):
     _fields_ = [
         ("B", c_i32), ("H", c_i32), ("T", c_i32), ("d", c_i32), ("q_scale", c_f32), ("gamma_eps", c_f32),
+        ("chunk", c_i32), ("exact_write", c_i32),
         ("q", CView), ("k", CView), ("v", CView),
         ("gamma", c_ptr), ("beta", c_ptr), ("sg_b", c_i64), ("sg_h", c_i64), ("sg_t", c_i64),
         ("s0_re", c_ptr), ("s0_im", c_ptr), ("y", MView), ("s_re", c_ptr), ("s_im", c_ptr),

@@ -50,8 +50,30 @@ constexpr int D = 64;
 // independent: four blocks per chain) with S^T in LDS: W = beta (V - alpha K S^T),
 // U = T W, the state update, then Y = Ahat U + alpha Q~ S^T with the chunk's
 // entering state.
-constexpr int CH = 64;                 // steps per chunk
+constexpr int CH = 64;                 // kernel rows per chunk
 constexpr int ROW_BLOCKS = 4;          // blocks per chain in the chunk pass (16 value rows each)
+// Steps per chunk of a call: the reference's chunk length (its delta_chunk,
+// 1..CH; 0 selects CH).  Each chunk of the call runs as one kernel chunk of CH
+// rows whose rows past the chunk's steps are zero (beta 0), exactly as a ragged
+// last chunk, so the chunk-dependent parts of the chunked form (the clamped decay
+// matrix, the state-write weight alpha_last / (alpha_s + 1e-12)) follow the
+// reference's chunk boundaries.
+__host__ __device__ __forceinline__ int chunk_len(const qpam_delta_args &a) { return a.chunk > 0 ? a.chunk : CH; }
+// log of a step's decay factor (gamma + gamma_eps, kept at or above the smallest
+// normal float so that gamma = 0 stays finite)
+__device__ __forceinline__ float decay_log(float gamma, float eps) { return logf(fmaxf(gamma + eps, 1.17549435e-38f)); }
+// The state-write weight of step s in its chunk: the reference's chunked form
+// alpha_last / (alpha_s + 1e-12), or exp(L_last - L_s) (the token recurrence's
+// weight, 1 for the last step) when the call asks for the exact write.
+__device__ __forceinline__ float write_weight(const qpam_delta_args &a, float Ls, float Llast) {
+    return a.exact_write ? __expf(Llast - Ls) : __expf(Llast) / (__expf(Ls) + 1e-12f);
+}
+// d weight / d L_s divided by -weight: alpha_s / (alpha_s + 1e-12), or 1 (exact write)
+__device__ __forceinline__ float write_weight_dl(const qpam_delta_args &a, float Ls) {
+    if (a.exact_write) return 1.f;
+    const float al = __expf(Ls);
+    return al / (al + 1e-12f);
+}
 constexpr int KP = CH + 4;             // LDS pitch of [64][64] fp32 tiles read element-wise
 constexpr int SP = 16;                 // LDS pitch of [64][16] fp32 tiles
 constexpr int NBLK = 10;               // 16 x 16 blocks on and below the diagonal of a 64 x 64 matrix
@@ -163,7 +185,7 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
     const int chain = blockIdx.x / n_chunks, c = blockIdx.x % n_chunks;
     const int b = chain / a.H, h = chain % a.H;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int t0 = c * CH, valid = min(CH, a.T - t0);
+    const int t0 = c * chunk_len(a), valid = min(chunk_len(a), a.T - t0);
     // the backward's record of this chunk (when a backward follows)
     float *wrec = a.workspace ? static_cast<float *>(a.workspace) + ((int64_t)chain * n_chunks + c) * WS_REC : nullptr;
     {  // K and q_scale Q, rows past the end zero
@@ -189,7 +211,7 @@ __global__ void __launch_bounds__(256, 2) delta_prep_kernel(qpam_delta_args a, f
     }
     if (w == 0) {  // inclusive prefix of log(gamma + eps); held past the end
         const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)(t0 + min(lane, valid - 1)) * a.sg_t;
-        float x = lane < valid ? logf(a.gamma[go] + a.gamma_eps) : 0.f;
+        float x = lane < valid ? decay_log(a.gamma[go], a.gamma_eps) : 0.f;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const float y = __shfl_up(x, off);
@@ -415,12 +437,12 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
         sSi[0][j * SP + i] = a.s0_re ? a.s0_im[o] : 0.f;
     }
     TileRegs xr;
-    tile_fetch(xr, a.k, b, h, 0, min(CH, a.T), tid, 1.f);
+    tile_fetch(xr, a.k, b, h, 0, min(chunk_len(a), a.T), tid, 1.f);
     // V of this lane's W elements and the T blocks of the chunk: loaded one chunk ahead
     float vr4[4], vi4[4];
     OpRegs opT;
     auto fetch_vt = [&](int c) {
-        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        const int t0 = c * chunk_len(a), valid = min(chunk_len(a), a.T - t0);
         const float *vre = static_cast<const float *>(a.v.re) + b * a.v.s0 + h * a.v.s1 + i0 + l16;
         const float *vim = static_cast<const float *>(a.v.im) + b * a.v.s0 + h * a.v.s1 + i0 + l16;
 #pragma unroll
@@ -437,7 +459,7 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
     int cur = 0;
     __syncthreads();
     for (int c = 0; c < n_chunks; ++c) {
-        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        const int t0 = c * chunk_len(a), valid = min(chunk_len(a), a.T - t0);
         const int64_t pc = chunk_prep(chain, n_chunks, c);
         tile_put(sKQr, sKQi, xr, tid);
         if (w == 0) {
@@ -523,7 +545,7 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
 #pragma unroll 4
             for (int ks = 0; ks < 16; ++ks) {
                 const int s = 4 * ks + g;
-                const float wq = atot / (__expf(sL[s]) + 1e-12f);
+                const float wq = write_weight(a, sL[s], sL[CH - 1]);
                 // conj(K)^T [j][s] (A) times (tail U)[s][i] (B)
                 gstep(x, sKQr[s * KP + 16 * w + l16], -sKQi[s * KP + 16 * w + l16], sUr[s * SP + l16] * wq,
                       sUi[s * SP + l16] * wq);
@@ -539,11 +561,11 @@ __global__ void __launch_bounds__(256, 2) delta_chunk_kernel(qpam_delta_args a, 
         __syncthreads();  // K no longer read
         tile_put(sKQr, sKQi, xr, tid);
         if (c + 1 < n_chunks) {
-            const int v1 = min(CH, a.T - t0 - CH);
-            tile_fetch(xr, a.k, b, h, t0 + CH, v1, tid, 1.f);
+            const int cs = chunk_len(a), v1 = min(cs, a.T - t0 - cs);
+            tile_fetch(xr, a.k, b, h, t0 + cs, v1, tid, 1.f);
             fetch_vt(c + 1);
             lnext = prep[chunk_prep(chain, n_chunks, c + 1) + PREP_L + lane];
-            bnext = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)(t0 + CH + min(lane, v1 - 1)) * a.sg_t];
+            bnext = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)(t0 + cs + min(lane, v1 - 1)) * a.sg_t];
         }
         __syncthreads();
         // Y = Ahat U + alpha Q~ S^T (entering state), row tile w
@@ -669,7 +691,7 @@ __global__ void __launch_bounds__(256, 2) delta_bwd_chain_kernel(qpam_delta_bwd_
     const int yt = tid >> 2, yc = 4 * (tid & 3);
     floatx4 dyr, dyi;
     auto fetch_dy = [&](int c) {
-        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        const int t0 = c * chunk_len(a), valid = min(chunk_len(a), a.T - t0);
         const int64_t o = b * bw.dy.s0 + h * bw.dy.s1 + (int64_t)(t0 + min(yt, valid - 1)) * bw.dy.s2 + i0 + yc;
         const float f = yt < valid ? 1.f : 0.f;
         dyr = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(bw.dy.re) + o) * f;
@@ -677,7 +699,7 @@ __global__ void __launch_bounds__(256, 2) delta_bwd_chain_kernel(qpam_delta_bwd_
     };
     float lnext = 0.f, bnext = 0.f;
     auto fetch_lb = [&](int c) {  // wave 0: L and beta of chunk c (beta 0 past the end)
-        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        const int t0 = c * chunk_len(a), valid = min(chunk_len(a), a.T - t0);
         lnext = wsf[(int64_t)c * WS_REC + WS_L + lane];
         const float bt = a.beta[b * a.sg_b + h * a.sg_h + (int64_t)(t0 + min(lane, valid - 1)) * a.sg_t];
         bnext = lane < valid ? bt : 0.f;
@@ -694,8 +716,8 @@ __global__ void __launch_bounds__(256, 2) delta_bwd_chain_kernel(qpam_delta_bwd_
         }
     };
     {
-        const int t0 = (n - 1) * CH;
-        tile_fetch(xr, a.q, b, h, t0, min(CH, a.T - t0), tid, a.q_scale);
+        const int t0 = (n - 1) * chunk_len(a);
+        tile_fetch(xr, a.q, b, h, t0, min(chunk_len(a), a.T - t0), tid, a.q_scale);
         fetch_dy(n - 1);
         if (w == 0) fetch_lb(n - 1);
     }
@@ -708,7 +730,7 @@ __global__ void __launch_bounds__(256, 2) delta_bwd_chain_kernel(qpam_delta_bwd_
     __syncthreads();
 
     for (int c = n - 1; c >= 0; --c) {
-        const int t0 = c * CH, valid = min(CH, a.T - t0);
+        const int t0 = c * chunk_len(a), valid = min(chunk_len(a), a.T - t0);
         const float *rec = wsf + (int64_t)c * WS_REC;
         float *brec = bws + (int64_t)c * BW_REC;
         {  // G after this chunk -> the record (16-byte pieces of rows i0 + l16)
@@ -733,7 +755,7 @@ __global__ void __launch_bounds__(256, 2) delta_bwd_chain_kernel(qpam_delta_bwd_
         __syncthreads();  // q~ no longer read
         tile_put(sKQr, sKQi, xr, tid);
         if (c > 0) {  // the previous (full) chunk's q~, dY, L and beta, in flight through the rest
-            tile_fetch(xr, a.q, b, h, t0 - CH, CH, tid, a.q_scale);
+            tile_fetch(xr, a.q, b, h, t0 - chunk_len(a), chunk_len(a), tid, a.q_scale);
             fetch_dy(c - 1);
             if (w == 0) fetch_lb(c - 1);
         }
@@ -753,7 +775,7 @@ __global__ void __launch_bounds__(256, 2) delta_bwd_chain_kernel(qpam_delta_bwd_
             const float atot = __expf(Llast);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float tl = atot / (sA[16 * w + 4 * g + r] + 1e-12f);  // the state-write weight
+                const float tl = write_weight(a, sL[16 * w + 4 * g + r], Llast);  // the state-write weight
                 ur[r] *= tl;
                 ui[r] *= tl;
             }
@@ -865,7 +887,7 @@ __global__ void __launch_bounds__(256) delta_bwd_score_kernel(qpam_delta_bwd_arg
     const int chain = blockIdx.x / n_chunks, c = blockIdx.x % n_chunks;
     const int b = chain / a.H, h = chain % a.H;
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
-    const int t0 = c * CH, valid = min(CH, a.T - t0);
+    const int t0 = c * chunk_len(a), valid = min(chunk_len(a), a.T - t0);
     const float *rec = static_cast<const float *>(a.workspace) + ((int64_t)chain * n_chunks + c) * WS_REC;
     float *brec = static_cast<float *>(bw.workspace) + ((int64_t)chain * n_chunks + c) * BW_REC;
     // this lane's MFMA A rows: dY of step 16 w + l16, dW of step 16 (3 - w) + l16;
@@ -1020,7 +1042,7 @@ __global__ void __launch_bounds__(512) delta_bwd_grad_kernel(qpam_delta_bwd_args
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const int w = wv & 3;
     const bool qside = wv < 4;
-    const int t0 = c * CH, valid = min(CH, a.T - t0);
+    const int t0 = c * chunk_len(a), valid = min(chunk_len(a), a.T - t0);
     const float *rec = static_cast<const float *>(a.workspace) + ((int64_t)chain * n_chunks + c) * WS_REC;
     const float *brec = static_cast<const float *>(bw.workspace) + ((int64_t)chain * n_chunks + c) * BW_REC;
     constexpr int PL = CH * KP;  // offset of the im plane in a staged tile
@@ -1190,7 +1212,7 @@ __global__ void __launch_bounds__(512) delta_bwd_grad_kernel(qpam_delta_bwd_args
         }
     } else {
         const int s = 16 * w + l16;  // this lane's step (key side)
-        const float dl = __expf(sL[CH - 1]) / (__expf(sL[s]) + 1e-12f);  // the state-write weight
+        const float dl = write_weight(a, sL[s], sL[CH - 1]);  // the state-write weight
         float *dkr = bw.dk.re + b * bw.dk.s0 + h * bw.dk.s1 + (int64_t)(t0 + s) * bw.dk.s2;
         float *dki = bw.dk.im + b * bw.dk.s0 + h * bw.dk.s1 + (int64_t)(t0 + s) * bw.dk.s2;
         floatx4 urr[4], ui[4], pr[4], pi[4], hr[4], hi[4];
@@ -1269,9 +1291,9 @@ __global__ void __launch_bounds__(512) delta_bwd_grad_kernel(qpam_delta_bwd_args
     if (wv == 4) {  // lane = step: dL, its reverse cumsum, dgamma and dbeta
         const int t = lane;
         const float Lt = sL[t], Llast = sL[CH - 1];
-        const float al = __expf(Lt), atot = __expf(Llast), dl = atot / (al + 1e-12f);
+        const float al = __expf(Lt), atot = __expf(Llast), dl = write_weight(a, Lt, Llast);
         const bool tv = t < valid;
-        float x = tv ? sLp[t] + sDa[t] * al - sDdl[t] * dl * (al / (al + 1e-12f)) : 0.f;
+        float x = tv ? sLp[t] + sDa[t] * al - sDdl[t] * dl * write_weight_dl(a, Lt) : 0.f;
         const float tot = wave_sum(tv ? sDdl[t] * dl : 0.f);
         float dac = 0.f;
 #pragma unroll
@@ -1284,7 +1306,7 @@ __global__ void __launch_bounds__(512) delta_bwd_grad_kernel(qpam_delta_bwd_args
         }
         if (tv) {
             const int64_t go = b * a.sg_b + h * a.sg_h + (int64_t)(t0 + t) * a.sg_t;
-            bw.dgamma[go] = x / (a.gamma[go] + a.gamma_eps);
+            bw.dgamma[go] = x / fmaxf(a.gamma[go] + a.gamma_eps, 1.17549435e-38f);  // as decay_log
             bw.dbeta[go] = sDb[t] + sDb2[t];
         }
     }
@@ -1299,7 +1321,7 @@ bool mview_ok(const qpam_mview &v) {
     return v.re && v.im && aligned(v.re, 16) && aligned(v.im, 16) && v.s0 % 4 == 0 && v.s1 % 4 == 0 && v.s2 % 4 == 0;
 }
 
-size_t n_chunks_of(const qpam_delta_args &a) { return (size_t)((a.T + CH - 1) / CH); }
+size_t n_chunks_of(const qpam_delta_args &a) { return (size_t)((a.T + chunk_len(a) - 1) / chunk_len(a)); }
 size_t fwd_ws(const qpam_delta_args &a) { return (size_t)a.B * a.H * n_chunks_of(a) * WS_REC * sizeof(float); }
 size_t prep_bytes(const qpam_delta_args &a) { return (size_t)a.B * a.H * n_chunks_of(a) * PREP_FLOATS * sizeof(float); }
 size_t bwd_ws(const qpam_delta_args &a) { return (size_t)a.B * a.H * n_chunks_of(a) * BW_REC * sizeof(float); }
@@ -1308,6 +1330,8 @@ int validate(const qpam_delta_args *a) {
     QPAM_REQUIRE(a != nullptr, "qpam_delta: null arguments");
     QPAM_REQUIRE(a->B >= 0 && a->H >= 1 && a->T >= 0, "qpam_delta: invalid sizes B=%d H=%d T=%d", a->B, a->H, a->T);
     QPAM_REQUIRE(a->d == D, "qpam_delta: head_dim %d unsupported (64 only)", a->d);
+    QPAM_REQUIRE(a->chunk >= 0 && a->chunk <= CH, "qpam_delta: chunk %d outside 1..%d (0 = %d)", a->chunk, CH, CH);
+    QPAM_REQUIRE(a->exact_write == 0 || a->exact_write == 1, "qpam_delta: exact_write must be 0 or 1");
     QPAM_REQUIRE(cview_ok(a->q) && cview_ok(a->k) && cview_ok(a->v),
                  "qpam_delta: q, k, v must be 16-byte aligned fp32 planes with strides multiple of 4");
     QPAM_REQUIRE(a->gamma && a->beta, "qpam_delta: gamma and beta required");
@@ -1337,7 +1361,7 @@ extern "C" int qpam_delta_fwd(const qpam_delta_args *a, void *stream) {
     QPAM_REQUIRE(a->T >= 1, "qpam_delta_fwd: T must be >= 1");
     QPAM_REQUIRE(a->scratch && aligned(a->scratch, 16) && a->scratch_bytes >= prep_bytes(*a),
                  "qpam_delta_fwd: scratch of %zu bytes needed", prep_bytes(*a));
-    const int n_chunks = (a->T + CH - 1) / CH;
+    const int n_chunks = (int)n_chunks_of(*a);
     const int64_t items = (int64_t)a->B * a->H * n_chunks;
     QPAM_REQUIRE(items < (1ll << 31) && (int64_t)a->B * a->H * ROW_BLOCKS < (1ll << 31), "qpam_delta_fwd: grid too large");
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -1371,7 +1395,7 @@ extern "C" int qpam_delta_bwd(const qpam_delta_bwd_args *g, void *stream) {
     QPAM_REQUIRE((g->ds_re == nullptr) == (g->ds_im == nullptr) && (g->ds0_re == nullptr) == (g->ds0_im == nullptr),
                  "qpam_delta_bwd: ds / ds0 need both planes");
     if (a.B == 0 || a.T == 0) return QPAM_OK;
-    const int n_chunks = (a.T + CH - 1) / CH;
+    const int n_chunks = (int)n_chunks_of(a);
     const int64_t items = (int64_t)a.B * a.H * n_chunks;
     QPAM_REQUIRE(items < (1ll << 31), "qpam_delta_bwd: grid too large");
     hipStream_t s = static_cast<hipStream_t>(stream);

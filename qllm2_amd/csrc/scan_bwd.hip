@@ -310,6 +310,10 @@ __global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
     float *sGr = sVi + D * P, *sGi = sGr + C * P;
     float *sL = sGi + C * P, *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
     float *sGL = sRi + MAX_M * 64, *sDRr = sGL + MAX_M * 64, *sDRi = sDRr + MAX_M * 64;
+    // per-wave partial log-decay gradients of the score phase [wave][m][64]: every
+    // wave adds only into its own slice, the slices are summed in wave order after
+    // it (a fixed summation order: the result does not depend on wave timing)
+    float *sGLw = sDRi + MAX_M * 64;
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -333,11 +337,12 @@ __global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
         stage_grad_and_inputs<Tin, C, 2, 6>(gd, gs, p.dy.s2, id, is, ist, isc, valid);
     }
     if (w == 0) chunk_decay_prologue(a, b, h, c0, valid, sL, sRr, sRi);
-    for (int e = tid; e < 3 * MAX_M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi
+    for (int e = tid; e < 7 * MAX_M * 64; e += THREADS) sGL[e] = 0.f;  // sGL, sDRr, sDRi, sGLw
     __syncthreads();
 
     const int tt = causal_tile(w);
     const bool active = tt < C / 16;
+    float *gl_w = sGLw + w * MAX_M * 64;  // this wave's partials
     floatx4 gqR[4], gqI[4];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) gqR[jt] = gqI[jt] = zero4();
@@ -429,7 +434,7 @@ __global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
                         float x = colp[m];
 #pragma unroll
                         for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off);
-                        if (l16 == 0) atomicAdd(&sGL[m * 64 + s], x);
+                        if (l16 == 0) gl_w[m * 64 + s] += x;
                     }
                 }
                 wr[st][r] = gwr;
@@ -446,10 +451,10 @@ __global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
                 yr += __shfl_xor(yr, 32);
                 yi += __shfl_xor(yi, 16);
                 yi += __shfl_xor(yi, 32);
-                if (g == 0) {
-                    atomicAdd(&sGL[m * 64 + t], x);
-                    atomicAdd(&sDRr[m * 64 + t], yr);
-                    atomicAdd(&sDRi[m * 64 + t], yi);
+                if (g == 0) {  // rows t are this wave's own
+                    gl_w[m * 64 + t] += x;
+                    sDRr[m * 64 + t] += yr;
+                    sDRi[m * 64 + t] += yi;
                 }
             }
         }
@@ -474,7 +479,11 @@ __global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
         }
     }
 
+    __syncthreads();
+    for (int e = tid; e < M * 64; e += THREADS)  // the waves' partials, in wave order
+        sGL[e] += ((sGLw[e] + sGLw[MAX_M * 64 + e]) + sGLw[2 * MAX_M * 64 + e]) + sGLw[3 * MAX_M * 64 + e];
     // carried read: X_m = G_Y conj(S_m); dQ~ += conj(rho_m) X_m; g_rho_m[t] = sum_j conj(q~[t,j]) X_m[t,j]
+    // (rows tr are this wave's own: plain updates)
     if (carry) {
         for (int m = 0; m < M; ++m) {
             __syncthreads();
@@ -526,9 +535,9 @@ __global__ void __launch_bounds__(THREADS) query_side_kernel(BwdParams p) {
                     pi += __shfl_xor(pi, off);
                 }
                 if (l16 == 0) {
-                    atomicAdd(&sDRr[m * 64 + tr], pr * cum);
-                    atomicAdd(&sDRi[m * 64 + tr], pi * cum);
-                    atomicAdd(&sGL[m * 64 + tr], (pr * rr + pi * ri) * cum);  // Re(g_rho conj(r)) cum
+                    sDRr[m * 64 + tr] += pr * cum;
+                    sDRi[m * 64 + tr] += pi * cum;
+                    sGL[m * 64 + tr] += (pr * rr + pi * ri) * cum;  // Re(g_rho conj(r)) cum
                 }
             }
         }
@@ -572,6 +581,7 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
     float *sL = sGi + D * P, *sRr = sL + MAX_M * 64, *sRi = sRr + MAX_M * 64;
     float *sGL = sRi + MAX_M * 64, *sDl = sGL + MAX_M * 64;
     float *sRed = sDl + MAX_M * 64;                  // [4] wave partials
+    float *sGp = sRed + 4;                           // [64] per-key decay_last terms of one state
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -781,20 +791,23 @@ __global__ void __launch_bounds__(THREADS) key_side_kernel(BwdParams p) {
                 }
 #pragma unroll
                 for (int off = 1; off < 16; off <<= 1) gdl += __shfl_xor(gdl, off);
-                if (l16 == 0 && sr_ < valid) {
+                if (l16 == 0 && sr_ < C) {  // key sr_ is this lane's own: plain updates
                     const float x = sL[m * 64 + valid - 1] - sL[m * 64 + sr_];
-                    const float gp = (x <= 0.f) ? gdl * dl : 0.f;
-                    if (sr_ != valid - 1) {
-                        atomicAdd(&sGL[m * 64 + valid - 1], gp);
-                        atomicAdd(&sGL[m * 64 + sr_], -gp);
-                    }
+                    const float gp = (sr_ < valid && sr_ != valid - 1 && x <= 0.f) ? gdl * dl : 0.f;
+                    sGL[m * 64 + sr_] -= gp;
+                    sGp[sr_] = gp;  // summed into the last step below, in a fixed order
                 }
             }
         }
         __syncthreads();
-        if (tid == 0 && carry) {
-            const float gtot = sRed[0] + sRed[1] + sRed[2] + sRed[3];
-            sGL[m * 64 + valid - 1] += gtot * __expf(sL[m * 64 + valid - 1]);
+        if (w == 0) {
+            float x = lane < C ? sGp[lane] : 0.f;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+            if (lane == 0) {
+                if (carry) x += (sRed[0] + sRed[1] + sRed[2] + sRed[3]) * __expf(sL[m * 64 + valid - 1]);
+                sGL[m * 64 + valid - 1] += x;
+            }
         }
     }
     __syncthreads();
@@ -1162,6 +1175,7 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
     float *sGL = sDqi + M * 64;
     float *sRed = sGL + M * 64;
     int *sFast = reinterpret_cast<int *>(sRed + 4);  // [M] factorisation tests
+    float *sGp = sRed + 8;                           // [64] per-key decay_last terms of one state
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -1677,18 +1691,21 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
         }
         gdl += __shfl_xor(gdl, 16);
         gdl += __shfl_xor(gdl, 32);
-        if (g == 0 && sv) {
+        if (g == 0) {  // key s is this lane's own: plain updates
             const float x = sL[m * 64 + valid - 1] - sL[m * 64 + s];
-            const float gp = (x <= 0.f) ? gdl * dls : 0.f;
-            if (s != valid - 1) {
-                atomicAdd(&sGL[m * 64 + valid - 1], gp);
-                atomicAdd(&sGL[m * 64 + s], -gp);
-            }
+            const float gp = (sv && s != valid - 1 && x <= 0.f) ? gdl * dls : 0.f;
+            sGL[m * 64 + s] -= gp;
+            sGp[s] = gp;  // summed into the last step below, in a fixed order
         }
         __syncthreads();
-        if (tid == 0 && carry) {
-            const float gtot = sRed[0] + sRed[1] + sRed[2] + sRed[3];
-            sGL[m * 64 + valid - 1] += gtot * __expf(sL[m * 64 + valid - 1]);
+        if (w == 0) {
+            float x = sGp[lane];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+            if (lane == 0) {
+                if (carry) x += (sRed[0] + sRed[1] + sRed[2] + sRed[3]) * __expf(sL[m * 64 + valid - 1]);
+                sGL[m * 64 + valid - 1] += x;
+            }
         }
     }
     __syncthreads();
@@ -1739,7 +1756,7 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
 
 // 8 bf16 planes + 10 per-step vectors: two blocks share a CU's 160 KiB LDS up to M = 3
 template <int M>
-constexpr size_t chunk_grad_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (10 * M * 64 + 8) * sizeof(float); }
+constexpr size_t chunk_grad_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (10 * M * 64 + 8 + 64) * sizeof(float); }
 static_assert(2 * chunk_grad_bf16_smem<3>() <= 160 * 1024, "LDS budget");
 
 template <int M>
@@ -1779,9 +1796,9 @@ int launch_bwd_bf16(const BwdParams &p, hipStream_t stream) {
 template <int C>
 size_t gcs_smem() { return (size_t)(4 * C * P + 3 * MAX_M * 64) * sizeof(float); }
 template <int C>
-size_t qside_smem() { return (size_t)(6 * C * P + 2 * D * P + 6 * MAX_M * 64) * sizeof(float); }
+size_t qside_smem() { return (size_t)(6 * C * P + 2 * D * P + 10 * MAX_M * 64) * sizeof(float); }
 template <int C>
-size_t kside_smem() { return (size_t)(4 * C * P + 4 * D * P + 5 * MAX_M * 64 + 4) * sizeof(float); }
+size_t kside_smem() { return (size_t)(4 * C * P + 4 * D * P + 5 * MAX_M * 64 + 4 + 64) * sizeof(float); }
 
 template <typename Tin, int C>
 int launch_bwd(const BwdParams &p, hipStream_t stream) {

@@ -459,12 +459,17 @@ __device__ __forceinline__ void pass32_dma(float *st, const qpam_scan_args &a, c
     }
 }
 
-// s_waitcnt vmcnt(16), the other counters unconstrained.  Every wave issues the
-// same operations per step: eight direct loads, then eight state stores; at
-// most 16 operations issued after the previous step's last direct load may
-// still run, and memory operations complete in order, so that step's loads
-// have landed.
-constexpr int PASS32_WAIT = waitcnt_vm(16);
+// The wait at the end of a step.  Every wave issues per step first the
+// two 16-byte stores of the entering state (re, im), then the
+// PASS32_LOADS direct loads of chunk c + 2 (pass32_dma: the decay row, the
+// total, four K and two V pieces).  Waiting until at most PASS32_LOADS
+// operations are outstanding retires everything issued before this step's
+// loads -- in particular chunk c + 1's loads, which the next step reads --
+// whether or not loads and stores complete in order relative to each other:
+// loads complete in order among themselves, so an older load still in flight
+// would keep all of this step's loads in flight too.
+constexpr int PASS32_LOADS = 8;
+constexpr int PASS32_WAIT = waitcnt_vm(PASS32_LOADS);
 
 // Decay weights of every (chain, chunk) for the state pass, all chunks at once
 // (a wave per chunk): D[C-1, s] = exp(min(L_last - L_s, 0)) (0 beyond the
@@ -520,14 +525,15 @@ __device__ __forceinline__ void state_pass_f32_body(const FwdParams &p) {
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(8));
     __builtin_amdgcn_s_barrier();
 
-    // one chunk: stream chunk c+2 into NXT, store S_in(c), dS from CUR, S <- total S + dS
+    // one chunk: store S_in(c), stream chunk c+2 into NXT, dS from CUR, S <- total S + dS
     // (the stages rotate through three unrolled steps)
 #define QPAM_PASS32_STEP(CUR, NXT)                                                                     \
     {                                                                                                  \
-        pass32_dma(NXT, a, kre, kim, vre, vim, drow, tot, min(c + 2, n - 1), i0, wv, lane);            \
         float *dst = chunk_state_ptr(p, m, b, h, c);                                                   \
         *reinterpret_cast<floatx4 *>(dst + ri * D + j0) = sr;                                          \
         *reinterpret_cast<floatx4 *>(dst + D * D + ri * D + j0) = si;                                  \
+        __builtin_amdgcn_sched_barrier(0);                                                             \
+        pass32_dma(NXT, a, kre, kim, vre, vim, drow, tot, min(c + 2, n - 1), i0, wv, lane);            \
         __builtin_amdgcn_sched_barrier(0);                                                             \
         float d_[16], vr_[16], vi_[16], kr_[16], ki_[16];                                              \
         _Pragma("unroll") for (int ks = 0; ks < 16; ++ks) {                                            \
@@ -1514,27 +1520,44 @@ extern "C" int qpam_scan_fwd(const qpam_scan_args *a, void *stream) {
 // library (one copy per GPU, alive until the process ends), instead of a
 // caller workspace.  Host code never passes the array's name to a kernel (on
 // the host it is only a stand-in for the symbol): the device address comes
-// from hipGetSymbolAddress, once per device, kept in scratch_ptr's table.
+// from hipGetSymbolAddress, once per device, kept in that device's entry.
 // The forward kernels overwrite every workspace word they later read, so no
 // part of the array has to start at zero.
+//
+// Misuse check: each call records an event on its stream after its launches;
+// a call on another stream while the previous call's event is still pending
+// (hipEventQuery, no host wait) would share the array with work in flight, and
+// is refused.  Calls on one stream are ordered by the stream and always pass.
 namespace {
 
 static __device__ __align__(256) unsigned char scratch[QPAM_SCAN_FWD_NOALLOC_MAX_BYTES];
 
-int scratch_ptr(void **out) {
+struct NoallocDevice {
+    void *ptr = nullptr;            // device address of `scratch` on this device
+    hipEvent_t done = nullptr;      // recorded after the last call's launches
+    hipStream_t last = nullptr;     // the stream of the last call
+    bool recorded = false;
+};
+
+std::mutex &noalloc_mutex() {
     static std::mutex mu;
-    static std::map<int, void *> ptrs;
+    return mu;
+}
+
+// The device's entry, set up on its first call (symbol address and event).
+int noalloc_device(NoallocDevice *&out) {
+    static std::map<int, NoallocDevice> devs;  // guarded by noalloc_mutex()
     int dev = 0;
     QPAM_CHECK_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = ptrs.find(dev);
-    if (it == ptrs.end()) {
-        void *p = nullptr;
-        QPAM_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
-        QPAM_REQUIRE(p != nullptr && ((uintptr_t)p % 256) == 0, "qpam_scan_fwd_noalloc: bad scratch address");
-        it = ptrs.emplace(dev, p).first;
+    auto it = devs.find(dev);
+    if (it == devs.end()) {
+        NoallocDevice d;
+        QPAM_CHECK_HIP(hipGetSymbolAddress(&d.ptr, HIP_SYMBOL(scratch)));
+        QPAM_REQUIRE(d.ptr != nullptr && ((uintptr_t)d.ptr % 256) == 0, "qpam_scan_fwd_noalloc: bad scratch address");
+        QPAM_CHECK_HIP(hipEventCreateWithFlags(&d.done, hipEventDisableTiming));
+        it = devs.emplace(dev, d).first;
     }
-    *out = it->second;
+    out = &it->second;
     return QPAM_OK;
 }
 
@@ -1550,11 +1573,32 @@ extern "C" int qpam_scan_fwd_noalloc(const qpam_scan_args *a, void *stream) {
                           "qpam_scan_fwd_noalloc: this call needs %zu bytes of scan state, the library's scratch "
                           "holds %zu (use qpam_scan_fwd with a caller workspace)",
                           need, (size_t)QPAM_SCAN_FWD_NOALLOC_MAX_BYTES);
-    void *ptr = nullptr;
-    int st = scratch_ptr(&ptr);
+    const hipStream_t s = (hipStream_t)stream;
+    std::lock_guard<std::mutex> lock(noalloc_mutex());
+    NoallocDevice *d = nullptr;
+    int st = noalloc_device(d);
     if (st) return st;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    QPAM_CHECK_HIP(hipStreamIsCapturing(s, &cap));
+    const bool capturing = cap != hipStreamCaptureStatusNone;
+    if (!capturing && d->recorded && d->last != s) {
+        const hipError_t q = hipEventQuery(d->done);
+        if (q == hipErrorNotReady)
+            return qpam::fail(QPAM_ERR_ARG,
+                              "qpam_scan_fwd_noalloc: the previous call on another stream is still running; calls "
+                              "that overlap on one GPU would share the library's scratch (use one stream, or "
+                              "qpam_scan_fwd with a workspace per call)");
+        if (q != hipSuccess) return qpam::fail(QPAM_ERR_HIP, "hipEventQuery failed: %s", hipGetErrorString(q));
+    }
     qpam_scan_args b = *a;
-    b.workspace = ptr;
+    b.workspace = d->ptr;
     b.workspace_bytes = (size_t)QPAM_SCAN_FWD_NOALLOC_MAX_BYTES;
-    return qpam::scan::scan_fwd(&b, (hipStream_t)stream);
+    st = qpam::scan::scan_fwd(&b, s);
+    if (st) return st;
+    if (!capturing) {  // under graph capture the graph's own replays are the caller's to order
+        QPAM_CHECK_HIP(hipEventRecord(d->done, s));
+        d->last = s;
+        d->recorded = true;
+    }
+    return QPAM_OK;
 }

@@ -241,6 +241,11 @@ class DecodeEngine:
             self._graphs = {}  # graphs of the old rotary table are never replayed again
         key = (nb, id(between), rope, self._wver)
         entry = self._graphs.get(key) if n else None
+        if entry is not None and entry["between"] is not between:
+            # an id can be reused once its object is gone; each entry holds its own
+            # callable (so the id stays taken while the entry lives), and a graph
+            # is replayed only for the very callable it captured
+            entry = None
         if entry is None:
             if n and nb > n:  # run the padded batch eagerly: the capture then meets only shapes already run
                 x = torch.cat([x.float(), x.new_zeros(nb - n, *x.shape[1:], dtype=torch.float32)])
@@ -271,4 +276,4 @@ class DecodeEngine:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             out = self._layers(x, slots, between)
-        return {"graph": graph, "x": x, "slots": slots, "out": out}
+        return {"graph": graph, "x": x, "slots": slots, "out": out, "between": between}

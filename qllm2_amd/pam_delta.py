@@ -8,8 +8,9 @@ _recur_step_delta (:967-1002).  Both compute the token recurrence
 
 with g~ = gamma + 1e-6 in the chunked form (its log(gamma + 1e-6) decays) and
 g~ = gamma in the single step; the kernels compute the chunked form itself on
-fp32 MFMA, forward and backward (its clamped decay matrix and state-write
-weights included).
+fp32 MFMA, forward and backward, over the reference's chunks of delta_chunk
+steps (its clamped decay matrix and state-write weights included); the single
+step uses the recurrence's exact write weight.
 
 `delta_planar` is differentiable (torch.library custom op with a registered
 autograd formula); `forward_delta` and `recur_step_delta` keep the reference
@@ -33,7 +34,7 @@ def _plane(t):
     return t if ok else t.contiguous()
 
 
-def _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps):
+def _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, chunk, exact_write):
     for t in (q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta):
         if not t.is_cuda:
             raise ValueError("qpam delta: tensors must be on the GPU (no CPU path in this library)")
@@ -45,9 +46,12 @@ def _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale
             raise ValueError(f"q/k/v planes must be [B,H,T,d] = {(B, H, T, d)}, got {tuple(t.shape)}")
     if tuple(gamma.shape) != (B, H, T) or gamma.shape != beta.shape:
         raise ValueError("gamma and beta must be [B, H, T]")
+    if not 1 <= chunk <= 64:
+        raise NotImplementedError(f"the HIP delta rule runs chunks of 1..64 steps, got {chunk}")
     a = _lib.DeltaArgs()
     a.B, a.H, a.T, a.d = B, H, T, d
     a.q_scale, a.gamma_eps = float(q_scale), float(gamma_eps)
+    a.chunk, a.exact_write = int(chunk), int(bool(exact_write))
     keep = []
     for name, (re, im) in (("q", (q_re, q_im)), ("k", (k_re, k_im)), ("v", (v_re, v_im))):
         view, re, im = _cview(_plane(re), _plane(im))
@@ -69,9 +73,10 @@ def _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale
 @torch.library.custom_op("qpam::delta_fwd", mutates_args=())
 def delta_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Tensor, v_im: Tensor,
                  gamma: Tensor, beta: Tensor, s0_re: Optional[Tensor], s0_im: Optional[Tensor], q_scale: float,
-                 gamma_eps: float, keep_workspace: bool) -> List[Tensor]:
+                 gamma_eps: float, chunk: int, exact_write: bool, keep_workspace: bool) -> List[Tensor]:
     """Returns [y_re, y_im ([B,H,T,d] fp32), s_re, s_im ([B,H,d,d]), workspace]."""
-    a, keep = _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps)
+    a, keep = _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, chunk,
+                    exact_write)
     B, H, T, d = q_re.shape
     dev = q_re.device
     y_re = torch.empty(B, H, T, d, device=dev, dtype=torch.float32)
@@ -110,30 +115,32 @@ def delta_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: T
 _WS_REC = 4 * 64 * 64 + 4 * 10 * 512 + 64
 
 
-def _ws_bytes(B, H, T, d=64):
-    return B * H * ((T + 63) // 64) * _WS_REC * 4
+def _ws_bytes(B, H, T, d=64, chunk=64):
+    return B * H * ((T + chunk - 1) // chunk) * _WS_REC * 4
 
 
 @delta_fwd_op.register_fake
-def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, keep_workspace):
+def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, chunk, exact_write,
+      keep_workspace):
     B, H, T, d = q_re.shape
     y = q_re.new_empty(B, H, T, d, dtype=torch.float32)
     s = q_re.new_empty(B, H, d, d, dtype=torch.float32)
-    ws = q_re.new_empty(_ws_bytes(B, H, T, d) // 4 if keep_workspace else 0, dtype=torch.float32)
+    ws = q_re.new_empty(_ws_bytes(B, H, T, d, chunk) // 4 if keep_workspace else 0, dtype=torch.float32)
     return [y, torch.empty_like(y), s, torch.empty_like(s), ws]
 
 
 @torch.library.custom_op("qpam::delta_bwd", mutates_args=())
 def delta_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Tensor, v_im: Tensor,
                  gamma: Tensor, beta: Tensor, s0_re: Optional[Tensor], s0_im: Optional[Tensor], q_scale: float,
-                 gamma_eps: float, ws: Tensor, dy_re: Tensor, dy_im: Tensor, ds_re: Optional[Tensor],
-                 ds_im: Optional[Tensor]) -> List[Tensor]:
+                 gamma_eps: float, chunk: int, exact_write: bool, ws: Tensor, dy_re: Tensor, dy_im: Tensor,
+                 ds_re: Optional[Tensor], ds_im: Optional[Tensor]) -> List[Tensor]:
     """Returns [dq_re, dq_im, dk_re, dk_im, dv_re, dv_im, dgamma, dbeta, ds0_re, ds0_im]
     (ds0 empty without s0)."""
     # the kernels write dgamma and dbeta with gamma's strides: contiguous planes,
     # matching the gradients allocated below
     gamma, beta = gamma.contiguous(), beta.contiguous()
-    a, keep = _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps)
+    a, keep = _fill(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, chunk,
+                    exact_write)
     B, H, T, d = q_re.shape
     dev = q_re.device
     a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel() * 4
@@ -165,8 +172,8 @@ def delta_bwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: T
 
 
 @delta_bwd_op.register_fake
-def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, ws, dy_re, dy_im, ds_re,
-      ds_im):
+def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, chunk, exact_write, ws,
+      dy_re, dy_im, ds_re, ds_im):
     B, H, T, d = q_re.shape
     outs = [q_re.new_empty(B, H, T, d, dtype=torch.float32) for _ in range(6)]
     dg = gamma.new_empty(B, H, T, dtype=torch.float32)
@@ -176,9 +183,11 @@ def _(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, ga
 
 
 def _setup(ctx, inputs, output):
-    (q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, keep_ws) = inputs
+    (q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, q_scale, gamma_eps, chunk, exact_write,
+     keep_ws) = inputs
     ctx.save_for_backward(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, output[4])
     ctx.q_scale, ctx.gamma_eps, ctx.keep = q_scale, gamma_eps, keep_ws
+    ctx.chunk, ctx.exact_write = chunk, exact_write
     ctx.set_materialize_grads(False)
 
 
@@ -195,21 +204,25 @@ def _backward(ctx, grads):
         ds = (None, None)
     else:
         ds = (ds_re if ds_re is not None else torch.zeros_like(ds_im), ds_im if ds_im is not None else torch.zeros_like(ds_re))
-    g = delta_bwd_op(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, ctx.q_scale, ctx.gamma_eps, ws,
-                     dy_re, dy_im, ds[0], ds[1])
+    g = delta_bwd_op(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, ctx.q_scale, ctx.gamma_eps,
+                     ctx.chunk, ctx.exact_write, ws, dy_re, dy_im, ds[0], ds[1])
     cast = (lambda x, like: x.to(like.dtype) if x.dtype != like.dtype else x)
     out = [cast(g[i], t) for i, t in enumerate((q_re, q_im, k_re, k_im, v_re, v_im))]
     out += [cast(g[6], gamma), cast(g[7], beta)]
     out += [g[8], g[9]] if s0_re is not None else [None, None]
-    return tuple(out) + (None, None, None)
+    return tuple(out) + (None, None, None, None, None)
 
 
 delta_fwd_op.register_autograd(_backward, setup_context=_setup)
 
 
-def delta_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, *, q_scale, gamma_eps=CHUNK_EPS, s0=None):
+def delta_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, *, q_scale, gamma_eps=CHUNK_EPS, s0=None,
+                 chunk=64, exact_write=False):
     """Differentiable delta-rule scan on planar [B,H,T,d] planes, d <= 64
     (computed in fp32).  gamma, beta [B,H,T]; s0 optional (re, im) [B,H,d,d].
+    `chunk` is the chunked form's chunk length (the reference's delta_chunk,
+    1..64); exact_write uses the token recurrence's state-write weight (1 on
+    the step itself) instead of the chunked form's alpha_last / (alpha_s + 1e-12).
     Returns (y_re, y_im, s_re, s_im).
 
     d < 64 is zero-padded to 64 and sliced back, which is exact: padded key
@@ -225,24 +238,25 @@ def delta_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, *, q_scale, ga
             s0_re, s0_im = (torch.nn.functional.pad(x, (0, pad, 0, pad)) for x in (s0_re, s0_im))
         s0p = (s0_re, s0_im) if s0_re is not None else None
         y_re, y_im, s_re, s_im = delta_planar(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, q_scale=q_scale,
-                                              gamma_eps=gamma_eps, s0=s0p)
+                                              gamma_eps=gamma_eps, s0=s0p, chunk=chunk, exact_write=exact_write)
         return y_re[..., :d], y_im[..., :d], s_re[..., :d, :d], s_im[..., :d, :d]
     keep = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im))
     out = delta_fwd_op(q_re, q_im, k_re, k_im, v_re, v_im, gamma, beta, s0_re, s0_im, float(q_scale),
-                       float(gamma_eps), bool(keep))
+                       float(gamma_eps), int(chunk), bool(exact_write), bool(keep))
     return out[0], out[1], out[2], out[3]
 
 
-def forward_delta(queries, keys, protected_values, decay_gamma, write_beta, head_dim, state=None):
+def forward_delta(queries, keys, protected_values, decay_gamma, write_beta, head_dim, state=None, chunk=64):
     """V11PAMLayer._forward_delta (v11/model.py:491-576) on split-real
-    [B,H,T,d,2] tensors (queries unscaled), decay_gamma / write_beta [B,H,T].
+    [B,H,T,d,2] tensors (queries unscaled), decay_gamma / write_beta [B,H,T],
+    chunks of `chunk` steps (the layer's delta_chunk, v11/model.py:494).
     Returns (output [B,H,T,d,2], memory_state [B,H,d,d,2]) in the input dtype."""
     dtype = queries.dtype
     planes = [x[..., i] for x in (queries, keys, protected_values) for i in (0, 1)]
     s0 = (state[..., 0], state[..., 1]) if state is not None else None
     y_re, y_im, s_re, s_im = delta_planar(*planes, decay_gamma, write_beta, q_scale=head_dim ** -0.5,
-                                          gamma_eps=CHUNK_EPS, s0=s0)
+                                          gamma_eps=CHUNK_EPS, s0=s0, chunk=chunk)
     return torch.stack([y_re, y_im], -1).to(dtype), torch.stack([s_re, s_im], -1).to(dtype)
 
 
@@ -250,10 +264,11 @@ def recur_step_delta(memory_state, decay_gamma, value_t, key_t, query_t, write_b
     """V11PAMLayer._recur_step_delta (v11/model.py:967-1002): one token,
     memory_state [B,H,d,d,2], decay_gamma / write_beta_t [B,H], value/key/query
     [B,H,d,2] (query already scaled).  Returns (output [B,H,d,2], new state);
-    the input state is not modified."""
+    the input state is not modified.  The step's write has weight 1 (the
+    exact recurrence) and gamma is used as given (no 1e-6 shift)."""
     dtype = memory_state.dtype
     planes = [x[..., i].unsqueeze(2) for x in (query_t, key_t, value_t) for i in (0, 1)]
     y_re, y_im, s_re, s_im = delta_planar(*planes, decay_gamma.unsqueeze(-1), write_beta_t.unsqueeze(-1),
-                                          q_scale=1.0, gamma_eps=0.0,
+                                          q_scale=1.0, gamma_eps=0.0, exact_write=True,
                                           s0=(memory_state[..., 0], memory_state[..., 1]))
     return torch.stack([y_re[:, :, 0], y_im[:, :, 0]], -1).to(dtype), torch.stack([s_re, s_im], -1).to(dtype)

@@ -157,12 +157,14 @@ def forward_multistate_fused(self, x, queries, keys, values, head_dim):
 
 def forward_delta(self, queries, keys, protected_values, decay_gamma, write_beta, head_dim):
     """V11PAMLayer._forward_delta (E2 delta write, head-scalar decay): the HIP
-    delta-rule kernels (head dims up to 64); per-channel decay or larger head
-    dims keep the original."""
-    if decay_gamma.dim() != 3 or head_dim > 64 or not queries.is_cuda:
+    delta-rule kernels (head dims up to 64) over the layer's chunks of
+    delta_chunk steps (v11/model.py:494); per-channel decay, larger head dims
+    or chunks above 64 steps keep the original."""
+    chunk = int(getattr(self, "delta_chunk", 64))
+    if decay_gamma.dim() != 3 or head_dim > 64 or not queries.is_cuda or not 1 <= chunk <= 64:
         return _original(self, "_forward_delta")(self, queries, keys, protected_values, decay_gamma, write_beta,
                                                  head_dim)
-    return _delta.forward_delta(queries, keys, protected_values, decay_gamma, write_beta, head_dim)
+    return _delta.forward_delta(queries, keys, protected_values, decay_gamma, write_beta, head_dim, chunk=chunk)
 
 
 def recur_step_delta(self, memory_state, decay_gamma, value_t, key_t, query_t, write_beta_t):

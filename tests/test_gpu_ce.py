@@ -148,26 +148,37 @@ def test_ce_per_token_and_stats(gpu_lib):
     assert corr2 == tok2 == 150
 
 
-@pytest.mark.parametrize("path", GEMM_PATHS)
-def test_ce_config5_full_size(gpu_lib, monkeypatch, path):
-    """Config 5: N=16384, d_model=512 (D=1024 real-concat), V=50261, bf16 h ~N(0,1),
-    E ~N(0, 0.02^2), 10% ignore.  Loss checked on all rows, dH on 64 sampled
-    rows, dW on 256 sampled vocab rows, against fp32 CPU math on the bf16 values."""
-    _select_gemm(monkeypatch, path)
-    N, d_model, V = 16384, 512, 50261
-    h, w, t = O.make_ce_inputs(N, d_model, V, 1005, dtype=torch.bfloat16)
-    loss, dh, dw = _gpu(h, w, t)
+_CFG5 = {}
+
+
+def _config5_reference():
+    """Config 5 inputs and the fp32 CPU row log-sum-exps on the bf16 values,
+    computed once for the module's full-size tests."""
+    if not _CFG5:
+        N, d_model, V = 16384, 512, 50261
+        h, w, t = O.make_ce_inputs(N, d_model, V, 1005, dtype=torch.bfloat16)
+        hf, wf = h.float(), w.float()
+        lse = torch.empty(N)
+        for c0 in range(0, N, 2048):
+            lse[c0:c0 + 2048] = torch.logsumexp(hf[c0:c0 + 2048] @ wf.T, dim=-1)
+        _CFG5.update(h=h, w=w, t=t, lse=lse)
+    return _CFG5
+
+
+def _check_config5(loss, dh, dw, n_rows, n_cols, seed):
+    """Loss on all rows; dH on n_rows sampled rows and dW on n_cols sampled
+    vocabulary rows, against fp32 CPU math on the bf16 values."""
+    c = _config5_reference()
+    h, w, t, lse = c["h"], c["w"], c["t"], c["lse"]
     hf, wf = h.float(), w.float()
-    lse = torch.empty(N)
-    for c0 in range(0, N, 2048):
-        lse[c0:c0 + 2048] = torch.logsumexp(hf[c0:c0 + 2048] @ wf.T, dim=-1)
+    N, V = hf.shape[0], wf.shape[0]
     valid = t != -100
     tl = (hf[valid] * wf[t[valid]]).sum(-1)
     denom = valid.sum()
     ref_loss = (lse[valid] - tl).sum() / denom
     assert _rel(loss, ref_loss) < 2e-2
-    g = torch.Generator().manual_seed(9)
-    rows = torch.randperm(N, generator=g)[:64]
+    g = torch.Generator().manual_seed(seed)
+    rows = torch.randperm(N, generator=g)[:n_rows]
     p = torch.softmax(hf[rows] @ wf.T, -1)
     tv = t[rows]
     ok = tv != -100
@@ -175,8 +186,37 @@ def test_ce_config5_full_size(gpu_lib, monkeypatch, path):
     p[~ok] = 0
     p /= denom
     assert _rel(dh[rows], p @ wf) < 2e-2
-    cols = torch.randperm(V, generator=g)[:256]
+    cols = torch.randperm(V, generator=g)[:n_cols]
     gcols = torch.exp(hf @ wf[cols].T - lse[:, None])
     onehot = (t[:, None] == cols[None, :]).float()
     gcols = (gcols - onehot) * valid[:, None].float() / denom
     assert _rel(dw[cols], gcols.T @ hf) < 2e-2
+
+
+@pytest.mark.parametrize("path", GEMM_PATHS)
+def test_ce_config5_full_size(gpu_lib, monkeypatch, path):
+    """Config 5: N=16384, d_model=512 (D=1024 real-concat), V=50261, bf16 h ~N(0,1),
+    E ~N(0, 0.02^2), 10% ignore.  Loss checked on all rows, dH on 256 sampled
+    rows, dW on 1024 sampled vocab rows, against fp32 CPU math on the bf16 values."""
+    _select_gemm(monkeypatch, path)
+    c = _config5_reference()
+    loss, dh, dw = _gpu(c["h"], c["w"], c["t"])
+    _check_config5(loss, dh, dw, 256, 1024, 9)
+
+
+def test_ce_config5_full_size_fp32_master(gpu_lib, monkeypatch):
+    """Config 5 with its stated E: an fp32 master embedding (every entry off the
+    bf16 grid by a quarter of a bf16 ulp, so its bf16 operand copy is the bf16 E
+    of the reference values), bf16 h: the loss, dH (bf16) and dE (fp32, the
+    gradient of the bf16 copy) at full size on the default backward path, dH on
+    512 sampled rows and dE on 2048 sampled vocabulary rows."""
+    _select_gemm(monkeypatch, GEMM_PATHS[0])
+    c = _config5_reference()
+    wb = c["w"].float()
+    ulp = torch.where(wb != 0, torch.exp2(torch.floor(torch.log2(wb.abs().clamp_min(1e-30))) - 7), torch.zeros_like(wb))
+    sign = torch.randint(0, 2, wb.shape, generator=torch.Generator().manual_seed(33)).float() * 2 - 1
+    master = wb + 0.25 * ulp * sign
+    assert torch.equal(master.to(torch.bfloat16), c["w"]) and not torch.equal(master, wb)
+    loss, dh, dw = _gpu(c["h"], master, c["t"])
+    assert dh.dtype == torch.bfloat16 and dw.dtype == torch.float32
+    _check_config5(loss, dh, dw, 512, 2048, 19)

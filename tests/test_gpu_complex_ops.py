@@ -116,3 +116,34 @@ def test_complex_ops_zero_rows_and_pytorch_toggle(gpu_lib):
     finally:
         tk.set_triton_enabled(True)
     assert _rel(hip, pt) < 1e-5
+
+
+@pytest.mark.parametrize("dtype,rows", [(torch.bfloat16, 70000), (torch.float32, 36000)])
+def test_cgu_gate_grid_stride_rows(gpu_lib, dtype, rows):
+    """The CGU gate's flat kernels (forward and backward) launch one 16-byte
+    group per thread up to 65536 blocks of 256 threads and loop over the rest:
+    [rows, 1024] complex tensors with more groups than that (bf16: 4 complex
+    per group, 67.1 M elements; fp32: 2 per group, 33.6 M) reach the loop.
+    Output and both gradients against the oracle on row ranges served by the
+    first pass (the first rows), around the first row the loop serves, and at
+    the end (the gate is row-local, so a slice of rows is checked exactly)."""
+    from qllm2_amd import triton_kernels as tk
+    dim = 1024
+    per_group = 4 if dtype == torch.bfloat16 else 2
+    assert rows * dim // per_group > 65536 * 256
+    first_loop_row = 65536 * 256 * per_group // dim
+    g = torch.Generator(device="cuda").manual_seed(77)
+    z = torch.randn(rows, dim, 2, device="cuda", generator=g).to(dtype).requires_grad_(True)
+    up = torch.randn(rows, dim, 2, device="cuda", generator=g).to(dtype).requires_grad_(True)
+    gout = torch.randn(rows, dim, 2, device="cuda", generator=g).to(dtype)
+    out = tk.fused_cgu_gate(z, up)
+    out.backward(gout)
+    torch.cuda.synchronize()
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    for r0, r1 in ((0, 64), (first_loop_row - 40, first_loop_row + 40), (rows - 64, rows)):
+        zs, us, gs = (x[r0:r1].detach().cpu() for x in (z, up, gout))
+        ones = torch.ones(dim)
+        ref_out, ref_grads = _oracle("cgu", zs, us, gs, ones, ones)
+        assert _rel(out[r0:r1], ref_out) < tol, f"rows {r0}..{r1}: fwd"
+        assert _rel(z.grad[r0:r1], ref_grads[0]) < max(tol, 1e-4), f"rows {r0}..{r1}: dz"
+        assert _rel(up.grad[r0:r1], ref_grads[1]) < max(tol, 1e-4), f"rows {r0}..{r1}: dup"

@@ -134,6 +134,66 @@ def test_delta_step_matches_reference_step(gpu_lib):
         assert _rel(y, yr) < 1e-4 and _rel(sc, s) < 1e-4
 
 
+@pytest.mark.parametrize("chunk", [32, 20])
+def test_delta_reference_chunk_length_strong_decay(gpu_lib, chunk):
+    """The chunked form with the reference's own chunk length (delta_chunk 32,
+    the tiny_e2 preset, v11/model.py:1326; 20, its self-test) under strong decay
+    (gamma in 0.3..0.6: over 32-64 steps the within-chunk decay falls below the
+    state-write weight's 1e-12, where the chunk boundaries change the result):
+    y, the final state and every gradient against the chunked oracle run with
+    the same chunk length, per (b, h)."""
+    from qllm2_amd.pam_delta import delta_planar
+    B, H, T, d = 2, 3, 150, 64
+    q, k, v, g, b = D.make_delta_inputs(B, H, T, d, 700 + chunk)
+    g = 0.3 + 0.3 * torch.rand(B, H, T, generator=torch.Generator().manual_seed(701), dtype=torch.float64)
+    dy = torch.randn(B, H, T, d, 2, generator=torch.Generator().manual_seed(702), dtype=torch.float64)
+    leaves = [x.clone().requires_grad_(True) for x in (q, k, v, g, b)]
+    yr, sr = D.delta_chunked(*leaves[:3], leaves[3], leaves[4], d, chunk)
+    (yr * dy).sum().backward()
+    rgrads = [x.grad for x in leaves]
+    # the 64-step form differs here (the check that the chunk length matters)
+    y64, _ = D.delta_chunked(q, k, v, g, b, d, 64)
+    assert _rel(y64, yr.detach()) > 1e-3
+    dev = torch.device("cuda")
+    planes = [x[..., i].contiguous().float().to(dev).requires_grad_(True) for x in (q, k, v) for i in (0, 1)]
+    gg, bb = g.float().to(dev).requires_grad_(True), b.float().to(dev).requires_grad_(True)
+    y_re, y_im, s_re, s_im = delta_planar(*planes, gg, bb, q_scale=d ** -0.5, gamma_eps=1e-6, chunk=chunk)
+    ((y_re * dy[..., 0].to(dev)).sum() + (y_im * dy[..., 1].to(dev)).sum()).backward()
+    assert _rel_heads(torch.stack([y_re, y_im], -1), yr) < 1e-4, "y"
+    assert _rel_heads(torch.stack([s_re, s_im], -1), sr) < 1e-4, "s"
+    for name, (re, im), r in zip(("dq", "dk", "dv"), ((planes[0], planes[1]), (planes[2], planes[3]),
+                                                       (planes[4], planes[5])), rgrads[:3]):
+        assert _rel_heads(torch.stack([re.grad, im.grad], -1), r) < 1e-4, name
+    assert _rel_heads(gg.grad, rgrads[3]) < 1e-4, "dgamma"
+    assert _rel_heads(bb.grad, rgrads[4]) < 1e-4, "dbeta"
+
+
+def test_delta_step_tiny_gamma(gpu_lib):
+    """recur_step_delta with gamma <= 1e-10 (and exactly 0): the step's write
+    keeps weight 1 as in the reference step (v11/model.py:967-1002), so the
+    state is the write alone; y, the state and the gradients of the step
+    against the reference step under autograd."""
+    from qllm2_amd.pam_delta import recur_step_delta
+    B, H, d = 2, 2, 64
+    q, k, v, g, b = D.make_delta_inputs(B, H, 1, d, 710)
+    g = torch.tensor([[1e-10, 0.0], [3e-12, 1e-10]], dtype=torch.float64)
+    s = torch.randn(B, H, d, d, 2, generator=torch.Generator().manual_seed(711), dtype=torch.float64) * 0.1
+    qt = q[:, :, 0] * d ** -0.5
+    leaves = [x.clone().requires_grad_(True) for x in (s, v[:, :, 0], k[:, :, 0], qt, b[:, :, 0])]
+    yr, sr = D.recur_step_delta(leaves[0], g, leaves[1], leaves[2], leaves[3], leaves[4])
+    gy = torch.randn(yr.shape, generator=torch.Generator().manual_seed(712), dtype=torch.float64)
+    ((yr * gy).sum() + sr.sum()).backward()
+    dev = torch.device("cuda")
+    cl = [x.detach().float().to(dev).requires_grad_(True) for x in (s, v[:, :, 0], k[:, :, 0], qt, b[:, :, 0])]
+    y, sc = recur_step_delta(cl[0], g.float().to(dev), cl[1], cl[2], cl[3], cl[4])
+    assert torch.isfinite(y).all() and torch.isfinite(sc).all()
+    assert _rel(y, yr) < 1e-4 and _rel(sc, sr) < 1e-4
+    ((y * gy.float().to(dev)).sum() + sc.sum()).backward()
+    for name, a, r in zip(("ds", "dv", "dk", "dq", "dbeta"), cl, leaves):
+        assert torch.isfinite(a.grad).all(), name
+        assert _rel(a.grad, r.grad) < 1e-4, f"{name}: {_rel(a.grad, r.grad):.2e}"
+
+
 def test_delta_long_sequence_properties(gpu_lib):
     """T = 2048 (the config-3 length, 32 chunks), B=1, H=4: output
     and final state of the first head against the oracle's token recurrence."""

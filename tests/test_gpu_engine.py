@@ -133,3 +133,30 @@ def test_engine_graph_replay_with_between_hook(gpu_lib):
             a, b = (e.layer_state(li, slot) for e in engines)
             assert _rel(b, a) < 1e-6
     assert len(engines[1]._graphs) == 2  # buckets of 4 and 8 rows
+
+
+def test_engine_graph_fresh_closure_each_step(gpu_lib):
+    """A new `between` closure every step, each with its own gain (ids of freed
+    closures are reused by CPython): every step runs its own closure's work, so
+    the graph engine matches the eager engine step by step."""
+    from qllm2_amd.engine import DecodeEngine
+    cfg = V.config(**CFGS["e3"])
+    dim = cfg["dim"]
+    params = [V.make_params(cfg, 840 + i) for i in range(2)]
+    layers = [V.V11PAMLayer(cfg, {k: v.float() for k, v in p.items()}, dtype=torch.float32).cuda().eval()
+              for p in params]
+    engines = [DecodeEngine(layers, n_slots=6, max_len=64, graphs=gr, graph_bucket=4) for gr in (False, True)]
+    g = torch.Generator().manual_seed(841)
+    for e in engines:
+        for pos in (2, 7, 4):
+            e.admit(pos)
+    live = [0, 1, 2]
+    for step in range(6):
+        x = torch.randn(len(live), dim, 2, generator=g).cuda()
+        slots = torch.tensor(live, dtype=torch.int32, device="cuda")
+        ys = []
+        for e in engines:
+            scale = torch.full((1, dim, 1), 0.5 + 0.25 * step, device="cuda")
+            ys.append(e.step(x, slots, between=(lambda li, out, s=scale: out * s), host_slots=live).clone())
+        torch.cuda.synchronize()
+        assert _rel(ys[1], ys[0]) < 1e-6, f"step {step}: {_rel(ys[1], ys[0]):.2e}"

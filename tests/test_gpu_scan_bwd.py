@@ -354,3 +354,18 @@ def test_scan_seeded_random_shapes(gpu_lib, M, d, T, C, dt, with_rot, with_s0):
     assert _rel(outs["y"], y_ref) < tol and _rel_heads(outs["y"], y_ref, 2) < tol
     assert _rel(outs["s"], s_ref) < tol and _rel_heads(outs["s"], s_ref, 3) < tol
     _check(got, ref, tol)
+
+
+@pytest.mark.parametrize("dtype,M,T,C", [(torch.bfloat16, 3, 1024, 64), (torch.float32, 2, 300, 64),
+                                         (torch.float32, 3, 200, 32)])
+def test_scan_backward_deterministic(gpu_lib, dtype, M, T, C):
+    """Two backward passes over the same inputs give bit-identical gradients
+    (the kernels' reductions run in a fixed order, no floating-point atomics):
+    the E3 bf16 path at B=4, H=12 (many blocks in flight at once) and the fp32
+    paths with 64- and 32-step chunks."""
+    B, H, d = 4, 12, 64
+    case = _case(M, B, H, T, d, 5100 + M + T + C, True, True, dtype)
+    runs = [_gpu_grads(*case, d, C, dtype, True) for _ in range(2)]
+    for name, a, b in zip(NAMES, runs[0], runs[1]):
+        if a is not None:
+            assert torch.equal(a, b), f"{name}: differs between two runs"

@@ -89,3 +89,41 @@ def test_noalloc_refuses_calls_beyond_its_scratch(gpu_lib):
     st = L.qpam_scan_fwd_noalloc(ctypes.byref(a), _lib.stream_ptr())
     assert st == _lib.QPAM_ERR_WORKSPACE
     assert b"scratch" in L.qpam_last_error()
+
+
+def test_noalloc_refuses_overlapping_call_on_another_stream(gpu_lib):
+    """A call on stream A is held behind a bounded spin kernel; a call on stream
+    B issued meanwhile would share the scratch with it and is refused
+    (QPAM_ERR_ARG) with no launch; once A has finished, the same call on B runs
+    and equals the workspace entry's result."""
+    from qllm2_amd import _lib
+    from qllm2_amd.pam_scan import _fill_args, _mview
+    planes, gamma, rr, ri, s0r, s0i = _inputs(1, 4, 512, 1, torch.float32, 377, False, False)
+    want = _run("qpam_scan_fwd", planes, gamma, rr, ri, s0r, s0i, 64)
+    L = _lib.lib()
+    M, B, H, T = gamma.shape
+
+    def args():
+        a, keep = _fill_args(*planes, gamma, None, None, None, None, 0.125, 64)
+        y_re, y_im = torch.empty(B, H, T, 64, device="cuda"), torch.empty(B, H, T, 64, device="cuda")
+        s_re, s_im = torch.empty(M, B, H, 64, 64, device="cuda"), torch.empty(M, B, H, 64, 64, device="cuda")
+        a.y = _mview(y_re, y_im)
+        a.s_re, a.s_im = s_re.data_ptr(), s_im.data_ptr()
+        return a, keep, (y_re, y_im, s_re, s_im)
+
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    aa, ka, _ = args()
+    ab, kb, outs_b = args()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(sa):
+        torch.cuda._sleep(200_000_000)  # a bounded spin (about 0.1 s) ahead of the call on A
+        assert L.qpam_scan_fwd_noalloc(ctypes.byref(aa), ctypes.c_void_p(sa.cuda_stream)) == _lib.QPAM_OK
+    st = L.qpam_scan_fwd_noalloc(ctypes.byref(ab), ctypes.c_void_p(sb.cuda_stream))
+    assert st == _lib.QPAM_ERR_ARG, st
+    assert b"another stream" in L.qpam_last_error()
+    torch.cuda.synchronize()
+    assert L.qpam_scan_fwd_noalloc(ctypes.byref(ab), ctypes.c_void_p(sb.cuda_stream)) == _lib.QPAM_OK
+    torch.cuda.synchronize()
+    for g, w in zip(outs_b, want):
+        assert torch.equal(g, w)
+    del ka, kb

@@ -1175,7 +1175,7 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
     float *sGL = sDqi + M * 64;
     float *sRed = sGL + M * 64;
     int *sFast = reinterpret_cast<int *>(sRed + 4);  // [M] factorisation tests
-    float *sGp = sRed + 8;                           // [64] per-key decay_last terms of one state
+    float *sGpw = sRed + 8;                          // [4] wave sums of the decay_last terms of one state
 
     const qpam_scan_args &a = p.a;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -1555,14 +1555,11 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
         }
     }
 
-    // q of row t in the transposed accumulator layout (unscaled), read before
-    // the q tile is overwritten
-    uint2 qq[4][2];
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        qq[jt][0] = *reinterpret_cast<const uint2 *>(sQr + t * PB + 16 * jt + 4 * g);
-        qq[jt][1] = *reinterpret_cast<const uint2 *>(sQi + t * PB + 16 * jt + 4 * g);
-    }
+    // q of row t (the q tile is overwritten by the states): re-read from global
+    // memory where the carried read needs it, in the transposed accumulator
+    // layout (held in registers through the state loop, it made the kernel spill)
+    const int64_t qrow = b * a.q.s0 + h * a.q.s1 + (int64_t)(c0 + t) * a.q.s2;
+    const U16 *qrow_r = (const U16 *)a.q.re + qrow, *qrow_i = (const U16 *)a.q.im + qrow;
     for (int m = 0; m < M; ++m) {
         __syncthreads();  // nothing reads the q tile (m = 0) or G'_{m-1} any more
         if (carry) {  // S_m natural into the q tile; this thread's share of Re<G'_m, S_m>
@@ -1619,17 +1616,19 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
                         }
                     }
     #pragma unroll
-                    for (int jj = 0; jj < 2; ++jj)
+                    for (int jj = 0; jj < 2; ++jj) {
+                        const int jt = 2 * jh + jj;
+                        const uint2 q4r = own_quad(qrow_r, jt, tv), q4i = own_quad(qrow_i, jt, tv);
     #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int jt = 2 * jh + jj;
                             const float x_r = xr[jj][r], x_i = xi[jj][r];
                             gqR[jt][r] += rhr * x_r + rhi * x_i;
                             gqI[jt][r] += rhr * x_i - rhi * x_r;
-                            const float qr = quad_elem(qq[jt][0], r), qi = quad_elem(qq[jt][1], r);
+                            const float qr = quad_elem(q4r, r), qi = quad_elem(q4i, r);
                             pr += qr * x_r + qi * x_i;
                             pi += qr * x_i - qi * x_r;
                         }
+                    }
                 }
                 pr += __shfl_xor(pr, 16);
                 pr += __shfl_xor(pr, 32);
@@ -1691,21 +1690,18 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
         }
         gdl += __shfl_xor(gdl, 16);
         gdl += __shfl_xor(gdl, 32);
-        if (g == 0) {  // key s is this lane's own: plain updates
+        {
             const float x = sL[m * 64 + valid - 1] - sL[m * 64 + s];
-            const float gp = (sv && s != valid - 1 && x <= 0.f) ? gdl * dls : 0.f;
-            sGL[m * 64 + s] -= gp;
-            sGp[s] = gp;  // summed into the last step below, in a fixed order
+            float gp = (g == 0 && sv && s != valid - 1 && x <= 0.f) ? gdl * dls : 0.f;
+            if (g == 0) sGL[m * 64 + s] -= gp;  // this lane's own key
+            gp = row16_sum(gp);                 // the wave's keys (lanes 0-15), a fixed order
+            if (lane == 0) sGpw[w] = gp;
         }
         __syncthreads();
-        if (w == 0) {
-            float x = sGp[lane];
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-            if (lane == 0) {
-                if (carry) x += (sRed[0] + sRed[1] + sRed[2] + sRed[3]) * __expf(sL[m * 64 + valid - 1]);
-                sGL[m * 64 + valid - 1] += x;
-            }
+        if (tid == 0) {  // the decay_last terms of every key, in wave order, on the last step
+            float x = ((sGpw[0] + sGpw[1]) + sGpw[2]) + sGpw[3];
+            if (carry) x += (sRed[0] + sRed[1] + sRed[2] + sRed[3]) * __expf(sL[m * 64 + valid - 1]);
+            sGL[m * 64 + valid - 1] += x;
         }
     }
     __syncthreads();
@@ -1756,7 +1752,7 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
 
 // 8 bf16 planes + 10 per-step vectors: two blocks share a CU's 160 KiB LDS up to M = 3
 template <int M>
-constexpr size_t chunk_grad_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (10 * M * 64 + 8 + 64) * sizeof(float); }
+constexpr size_t chunk_grad_bf16_smem() { return (size_t)8 * PLANE_B * 2 + (10 * M * 64 + 8 + 4) * sizeof(float); }
 static_assert(2 * chunk_grad_bf16_smem<3>() <= 160 * 1024, "LDS budget");
 
 template <int M>

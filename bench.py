@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=1000)
-    ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "engine", "e3", "ce", "cplx", "layer",
+    ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "engine", "model", "e3", "ce", "cplx", "layer",
                                        "delta", "delta_ref", "copy"], default=None,
                     help="run one workload (for profiler passes) and print its own JSON line")
     return ap.parse_args()
@@ -246,7 +246,7 @@ def bench_decode_e3_rope(n_steps):
             "bytes_per_step": bytes_step, "steps": n_steps}
 
 
-def bench_engine(steps, warmup, graphs=False):
+def bench_engine(steps, warmup, graphs=False, dtype="fp32"):
     """Model-level continuous-batching decode (qllm2_amd.engine.DecodeEngine):
     16 E3 PAM layers (M=3, H=12, d=64, dim=768, fp32, RoPE, GSP, phase-routed
     states) over 256 slots, ~75% of them live per step.  A step runs every
@@ -258,7 +258,8 @@ def bench_engine(steps, warmup, graphs=False):
     from qllm2_amd.engine import DecodeEngine
     S, L, H, d, M, dim = 256, 16, 12, 64, 3, 768
     layers = [_BenchPamLayer(dim, H, d, M, 16, torch.float32, seed=40 + i).mod for i in range(L)]
-    engine = DecodeEngine(layers, n_slots=S, max_len=8192, graphs=graphs, graph_bucket=16)
+    engine = DecodeEngine(layers, n_slots=S, max_len=8192, graphs=graphs, graph_bucket=16,
+                          dtype=torch.bfloat16 if dtype == "bf16" else torch.float32)
     if graphs:
         warmup = max(warmup, 16)
     gen = torch.Generator().manual_seed(1015)
@@ -283,8 +284,99 @@ def bench_engine(steps, warmup, graphs=False):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     active = sum(len(hosts[i % 16]) for i in range(steps)) / steps
-    return {"config": "16 PAM layers E3 M=3, H=12, d=64, dim=768, fp32, 256 slots (~75% live)"
+    return {"config": f"16 PAM layers E3 M=3, H=12, d=64, dim=768, {dtype} GEMMs, 256 slots (~75% live)"
             + (", HIP-graph replay per live-count bucket of 16" if graphs else ""),
+            "ms_per_step": ms, "tokens_per_s": active / (ms * 1e-3), "active_slots": active, "steps": steps}
+
+
+def _bench_model(L, dim, H, d, M, vocab, expand, seed=70):
+    """A V11LM-shaped module (the reference's attribute names) with random
+    weights: L blocks of ComplexNorm, a ModSwish CGU of hidden expand * dim,
+    the production E3 PAM layer of _BenchPamLayer; the tied embedding table,
+    output norm, LM-head projection and norm."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+
+    def prm(*shape, std, mean=0.0):
+        return torch.nn.Parameter((torch.randn(*shape, generator=g) * std + mean).cuda())
+
+    def clin(o, i, bias=False):
+        lin = torch.nn.Module()
+        lin.weight_real, lin.weight_imag = prm(o, i, std=(2 * i) ** -0.5), prm(o, i, std=(2 * i) ** -0.5)
+        lin.bias_real = prm(o, std=0.02) if bias else None
+        lin.bias_imag = prm(o, std=0.02) if bias else None
+        return lin
+
+    def norm(n):
+        m = torch.nn.Module()
+        m.scale, m.eps = prm(n, std=0.05, mean=1.0), 1e-6
+        return m
+
+    hid = expand * dim
+    model = torch.nn.Module()
+    model.embed = torch.nn.Module()
+    for part in ("embed_real", "embed_imag"):
+        e = torch.nn.Module()
+        e.weight = prm(vocab, dim, std=0.02)
+        setattr(model.embed, part, e)
+    model.pos_embed = None
+    model.embed_norm, model.output_norm, model.lm_head_norm = norm(dim), norm(dim), norm(dim)
+    model.lm_head_proj = clin(dim, dim, bias=True)
+    blocks = []
+    for i in range(L):
+        b = torch.nn.Module()
+        b.norm1, b.norm2 = norm(dim), norm(dim)
+        b.cgu = torch.nn.Module()
+        b.cgu.gate_proj, b.cgu.up_proj, b.cgu.down_proj = clin(hid, dim), clin(hid, dim), clin(dim, hid)
+        b.cgu.act = torch.nn.Module()
+        b.cgu.act.bias, b.cgu.act.beta = prm(hid, std=0.1), prm(hid, std=0.1, mean=1.0)
+        b.cgu_scale, b.pam_scale = prm(1, std=0.0, mean=1.0)[0], prm(1, std=0.0, mean=0.1)[0]
+        b.pam = _BenchPamLayer(dim, H, d, M, 16, torch.float32, seed=40 + i).mod
+        blocks.append(b)
+    model.blocks = blocks
+    return model
+
+
+def bench_model_decode(steps, warmup, dtype="bf16", graphs=True):
+    """Model-level continuous-batching decode (qllm2_amd.model_decode.ModelDecoder):
+    the whole V11 model per token for the live rows of 256 slots (~75% live):
+    embedding, 16 blocks (ComplexNorm -> CGU with ModSwish, hidden 3 * 768 ->
+    ComplexNorm -> E3 PAM layer M=3, H=12, d=64) and the tied LM head over the
+    50261-entry vocabulary (logits of every live row).  GEMMs in `dtype` (fp32
+    accumulation; states, norms and the decode kernel in fp32); with `graphs`
+    each live-count bucket of 16 rows is captured once and replayed."""
+    import torch
+    from qllm2_amd.model_decode import ModelDecoder
+    S, L, H, d, M, dim, V = 256, 16, 12, 64, 3, 768, 50261
+    model = _bench_model(L, dim, H, d, M, V, 3)
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    dec = ModelDecoder(model, n_slots=S, max_len=8192, dtype=dt, graphs=graphs, graph_bucket=16)
+    if graphs:
+        warmup = max(warmup, 16)
+    gen = torch.Generator().manual_seed(1017)
+    for s_ in range(S):
+        dec.engine.admit(int(torch.randint(1, 4096, (1,), generator=gen)))
+    dec.pool.state.normal_(0.0, 0.01, generator=torch.Generator(device="cuda").manual_seed(1018))
+    hosts = [torch.nonzero(torch.rand(S, generator=gen) < 0.75).flatten().tolist() for _ in range(16)]
+    masks = [torch.tensor(h, dtype=torch.int32).cuda() for h in hosts]
+    ids = [torch.randint(0, V, (len(h),), generator=gen).cuda() for h in hosts]
+
+    def step(i):
+        dec.step(ids[i % 16], masks[i % 16], host_slots=hosts[i % 16])
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    active = sum(len(hosts[i % 16]) for i in range(steps)) / steps
+    return {"config": f"V11 model decode: 16 blocks (CGU expand 3, E3 PAM M=3, H=12, d=64), dim=768, vocab {V}, "
+                      f"{dtype} GEMMs, 256 slots (~75% live)" + (", HIP-graph replay per bucket of 16" if graphs else ""),
             "ms_per_step": ms, "tokens_per_s": active / (ms * 1e-3), "active_slots": active, "steps": steps}
 
 
@@ -783,7 +875,11 @@ def main():
               "decode": lambda: bench_decode(args.decode_steps),
               "decode_e3": lambda: bench_decode_e3_rope(max(50, args.decode_steps // 5)),
               "engine": lambda: {"eager": bench_engine(args.steps, args.warmup),
-                                 "graphs": bench_engine(args.steps, args.warmup, graphs=True)},
+                                 "graphs": bench_engine(args.steps, args.warmup, graphs=True),
+                                 "graphs_bf16": bench_engine(args.steps, args.warmup, graphs=True, dtype="bf16")},
+              "model": lambda: {"bf16_graphs": bench_model_decode(args.steps, args.warmup),
+                                "fp32_graphs": bench_model_decode(args.steps, args.warmup, dtype="fp32"),
+                                "bf16_eager": bench_model_decode(args.steps, args.warmup, graphs=False)},
               "e3": lambda: bench_e3_fwd_bwd(args.steps, args.warmup),
               "ce": lambda: bench_ce(args.steps, args.warmup),
               "cplx": lambda: bench_complex_ops(args.steps, args.warmup),
@@ -826,6 +922,8 @@ def main():
                          "decode_e3_rope_slots": bench_decode_e3_rope(max(50, args.decode_steps // 5)),
                          "decode_engine_e3_16_layers": bench_engine(20, 5),
                          "decode_engine_e3_16_layers_graphs": bench_engine(20, 5, graphs=True),
+                         "decode_engine_e3_16_layers_graphs_bf16": bench_engine(20, 5, graphs=True, dtype="bf16"),
+                         "model_decode_16_blocks_bf16_graphs": bench_model_decode(20, 5),
                          # five untimed warmup steps: after two, the first timed steps still run
                          # slow (E3 0.69 vs 0.66 ms per step)
                          "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 5),

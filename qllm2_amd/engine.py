@@ -33,7 +33,10 @@ table or new weights start new graphs.
 Prefill stays the fused layer forward (pam_layer.forward); its per-layer
 states enter the pool through `admit`.  The layers must use head-scalar decay,
 the additive write and head_dim 64 (the production presets); the engine reads
-their parameters by the reference's names.  Everything runs in fp32.
+their parameters by the reference's names.  The states, the prologue and the
+decode kernel run in fp32; the projection and o_proj GEMMs run in fp32 or,
+with dtype=torch.bfloat16, on bf16 copies of the weights and inputs with fp32
+accumulation (the gates' small GEMMs stay fp32).
 """
 
 import torch
@@ -54,7 +57,10 @@ class DecodeEngine:
 
     MAX_GRAPHS = 64  # captured graphs kept at once (each holds its own buffers)
 
-    def __init__(self, layers, n_slots, *, max_len=4096, graphs=False, graph_bucket=16):
+    def __init__(self, layers, n_slots, *, max_len=4096, graphs=False, graph_bucket=16, dtype=torch.float32):
+        if dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("DecodeEngine: dtype must be float32 or bfloat16")
+        self.dtype = dtype
         self.layers = list(layers)
         l0 = self.layers[0]
         self.n_heads, self.head_dim, self.n_states = l0.num_heads, l0.head_dim, l0.n_states
@@ -99,8 +105,9 @@ class DecodeEngine:
                 b_out = None
                 if getattr(layer.o_proj, "bias_real", None) is not None:
                     b_out = torch.stack([layer.o_proj.bias_real, layer.o_proj.bias_imag], 1).reshape(2 * dim)
-                entry = dict(w_in=w_in.float().contiguous(), b_in=None if b_in is None else b_in.float(),
-                             w_out=w_out.float().contiguous(), b_out=None if b_out is None else b_out.float(),
+                dt = self.dtype  # the projection and o_proj GEMMs' dtype
+                entry = dict(w_in=w_in.to(dt).contiguous(), b_in=None if b_in is None else b_in.to(dt),
+                             w_out=w_out.to(dt).contiguous(), b_out=None if b_out is None else b_out.to(dt),
                              dim=dim, w_mag=None,
                              dt_bias=(layer.dt_bias if layer.dt_proj.bias is None
                                       else layer.dt_bias + layer.dt_proj.bias).float().contiguous())
@@ -184,7 +191,8 @@ class DecodeEngine:
         if n == 0:
             return x.new_zeros(0, dim, 2)
         x = x.float().contiguous()
-        proj = F.linear(x.view(n, 2 * dim), w["w_in"], w["b_in"]).view(n, 1, -1)
+        # the decode kernel reads fp32 planes: a bf16 projection is widened first
+        proj = F.linear(x.view(n, 2 * dim).to(self.dtype), w["w_in"], w["b_in"]).float().view(n, 1, -1)
         protect, phase, routing = self._gates(layer, x, w)
         (qr, qi), (kr, ki), (vr, vi), gamma, rot = pam_prologue(
             proj, w["dt_bias"], n_heads=h, n_states=m, state_offset=layer.state_dt_offset if m > 1 else None,
@@ -201,7 +209,7 @@ class DecodeEngine:
         # every listed slot is live, so the kernel writes every row of y: no zero fill
         y = self.pool.step(layer_idx, q, k, v, g, slots, rot=r, q_scale=d ** -0.5, compact=True,
                            out=torch.empty(n, h, d, 2, device=x.device, dtype=torch.float32))
-        return F.linear(y.view(n, 2 * h * d), w["w_out"], w["b_out"]).view(n, dim, 2)
+        return F.linear(y.view(n, 2 * h * d).to(self.dtype), w["w_out"], w["b_out"]).float().view(n, dim, 2)
 
     def _layers(self, x, slots, between):
         for li in range(len(self.layers)):

@@ -317,6 +317,15 @@ int qpam_prologue_bwd(const qpam_prologue_bwd_args *a, void *stream);
 int qpam_cabs_fwd(int32_t dtype, int64_t n, const void *z, void *mag, void *stream);
 int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void *mag, const void *gmag, void *gz, void *stream);
 
+/* Gate logits of the decode step from |x| (v11/model.py:228, 646: protect_gate
+ * and phase_proj applied to cabs(x), two nn.Linear on the same magnitudes, in
+ * one call): out[r][g] = bias[g] + sum_j w[g][j] |z[r][j]| with
+ * |z| = sqrt(re^2 + im^2 + 1e-8), z interleaved complex rows [rows][dim][2]
+ * (dtype), w fp32 [G][dim] row-major, bias fp32 [G] or NULL, out [rows][ld_out]
+ * (out_dtype).  dim <= 8192.  Inference only (no backward). */
+int qpam_mag_linear(int32_t dtype, int32_t out_dtype, int64_t rows, int32_t dim, int32_t G, const void *z,
+                    const float *w, const float *bias, void *out, int64_t ld_out, void *stream);
+
 /* ---------------------------------------------------------- E2 delta rule --
  * Gated delta-rule write, per (b, h) over t (one state, head-scalar decay):
  *   S <- (gamma_t + gamma_eps) S;  u = beta_t (v_t - S k_t);

@@ -192,6 +192,7 @@ SIGNATURES = {
     "qpam_delta_bwd_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(DeltaBwdArgs)]),
     "qpam_delta_bwd": (ctypes.c_int, [ctypes.POINTER(DeltaBwdArgs), c_ptr]),
     "qpam_cabs_bwd": (ctypes.c_int, [c_i32, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "qpam_mag_linear": (ctypes.c_int, [c_i32, c_i32, c_i64, c_i32, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
 }
 
 _LIB = None

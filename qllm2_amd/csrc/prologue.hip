@@ -423,6 +423,50 @@ int validate_outputs(const qpam_prologue_args *a) {
     return QPAM_OK;
 }
 
+
+// Gate logits from the magnitudes of the layer input, one block per row r:
+//   out[r][g] = bias[g] + sum_j w[g][j] |z[r][j]|,  |z| = sqrt(re^2 + im^2 + 1e-8)
+// (the protect gate and the phase projection both read cabs(x)).  The row's
+// magnitudes go to LDS once; wave w takes output groups of MAG_G rows of w
+// (groups w, w + 4, ...), its lanes striding over j: per step of 64 columns the
+// MAG_G coalesced row loads are all in flight before any is used, then a
+// butterfly sum per output.  Decode-time shapes (a few hundred rows, G of tens,
+// dim of hundreds) make this a latency problem: a library GEMM of that shape
+// has only a few output tiles, and a loop that uses each load as it arrives
+// waits one L2 round trip per element step.
+constexpr int MAG_THREADS = 256, MAG_MAX_DIM = 8192, MAG_G = 16;
+template <typename T, typename To>
+__global__ void __launch_bounds__(MAG_THREADS) mag_linear_kernel(int dim, int G, const void *z, const float *w,
+                                                                 const float *bias, void *out, int64_t ld_out) {
+    __shared__ float mag[MAG_MAX_DIM];
+    const int64_t r = blockIdx.x;
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    for (int j = tid; j < dim; j += MAG_THREADS) {
+        const float a = Io<T>::load1(z, (r * dim + j) * 2), b = Io<T>::load1(z, (r * dim + j) * 2 + 1);
+        mag[j] = sqrtf(a * a + b * b + 1e-8f);
+    }
+    __syncthreads();
+    for (int g0 = wv * MAG_G; g0 < G; g0 += (MAG_THREADS / 64) * MAG_G) {
+        float acc[MAG_G];
+#pragma unroll
+        for (int k = 0; k < MAG_G; ++k) acc[k] = 0.f;
+        for (int j = lane; j < dim; j += 64) {
+            float wk[MAG_G];
+#pragma unroll
+            for (int k = 0; k < MAG_G; ++k) wk[k] = (g0 + k < G) ? w[(int64_t)(g0 + k) * dim + j] : 0.f;
+            const float m = mag[j];
+#pragma unroll
+            for (int k = 0; k < MAG_G; ++k) acc[k] += wk[k] * m;
+        }
+#pragma unroll
+        for (int k = 0; k < MAG_G; ++k) {
+            float x = acc[k];
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+            if (lane == 0 && g0 + k < G) Io<To>::store1(out, r * ld_out + g0 + k, x + (bias ? bias[g0 + k] : 0.f));
+        }
+    }
+}
 }  // namespace
 }  // namespace qpam
 
@@ -506,4 +550,25 @@ extern "C" int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void
     if (dtype == QPAM_F32) hipLaunchKernelGGL(cabs_bwd_kernel<float>, grid, block, 0, s, n4, z, mag, gmag, gz);
     else hipLaunchKernelGGL(cabs_bwd_kernel<Bf16>, grid, block, 0, s, n4, z, mag, gmag, gz);
     return launch_status("cabs_bwd_kernel");
+}
+
+extern "C" int qpam_mag_linear(int32_t dtype, int32_t out_dtype, int64_t rows, int32_t dim, int32_t G, const void *z,
+                               const float *w, const float *bias, void *out, int64_t ld_out, void *stream) {
+    QPAM_REQUIRE((dtype == QPAM_F32 || dtype == QPAM_BF16) && (out_dtype == QPAM_F32 || out_dtype == QPAM_BF16),
+                 "qpam_mag_linear: dtypes must be QPAM_F32 or QPAM_BF16");
+    QPAM_REQUIRE(rows >= 0 && rows < (1ll << 31) && dim >= 1 && dim <= MAG_MAX_DIM && G >= 1 && ld_out >= G,
+                 "qpam_mag_linear: bad sizes rows=%lld dim=%d G=%d ld_out=%lld (dim <= %d)", (long long)rows, dim, G,
+                 (long long)ld_out, MAG_MAX_DIM);
+    if (rows == 0) return QPAM_OK;
+    QPAM_REQUIRE(z && w && out, "qpam_mag_linear: null z, w or out");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid((unsigned)rows), block(MAG_THREADS);
+    if (dtype == QPAM_F32) {
+        if (out_dtype == QPAM_F32) hipLaunchKernelGGL((mag_linear_kernel<float, float>), grid, block, 0, s, dim, G, z, w, bias, out, ld_out);
+        else hipLaunchKernelGGL((mag_linear_kernel<float, Bf16>), grid, block, 0, s, dim, G, z, w, bias, out, ld_out);
+    } else {
+        if (out_dtype == QPAM_F32) hipLaunchKernelGGL((mag_linear_kernel<Bf16, float>), grid, block, 0, s, dim, G, z, w, bias, out, ld_out);
+        else hipLaunchKernelGGL((mag_linear_kernel<Bf16, Bf16>), grid, block, 0, s, dim, G, z, w, bias, out, ld_out);
+    }
+    return launch_status("mag_linear_kernel");
 }

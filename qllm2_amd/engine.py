@@ -44,7 +44,7 @@ import torch.nn.functional as F
 
 from .decode import SlotPool
 from .pam_layer import _in_weight
-from .pam_prologue import HEAD_DIM, cabs, pam_prologue, proj_columns
+from .pam_prologue import HEAD_DIM, cabs, mag_linear, prologue_decode, proj_columns
 
 
 def _cat_planes(x):
@@ -156,24 +156,24 @@ class DecodeEngine:
         n, h, m = x.shape[0], self.n_heads, self.n_states
         mag = None
         protect = phase = routing = None
-        if w["w_mag"] is not None:  # protect gate and phase projection in one GEMM from |x|
-            mag = cabs(x)
-            gl = F.linear(mag, w["w_mag"], w["b_mag"])
+        if w["w_mag"] is not None:  # protect gate and phase projection from |x| in one launch
+            gl = mag_linear(x, w["w_mag"], w["b_mag"], out_dtype=self.dtype)
             protect, phase = gl[:, :h], gl[:, h:].reshape(n, h, m)
             if layer.state_compete:
-                routing = F.softmax(layer.score_proj(mag).view(n, h, m), dim=-1) * m
+                routing = F.softmax(layer.score_proj(cabs(x).float()).view(n, h, m), dim=-1) * m
             return protect, phase, routing
+        xf = x.float()
         if layer.use_gsp:
             if layer.gate_content_aware:
-                protect = layer.protect_gate(_cat_planes(x))
+                protect = layer.protect_gate(_cat_planes(xf))
             else:
-                mag = cabs(x)
+                mag = cabs(xf)
                 protect = layer.protect_gate(mag)
         if m > 1:
             if layer.routing_content_aware:
-                r_in = _cat_planes(x)
+                r_in = _cat_planes(xf)
             else:
-                r_in = mag if mag is not None else cabs(x)
+                r_in = mag if mag is not None else cabs(xf)
             phase = layer.phase_proj(r_in).view(n, h, m)
             if layer.state_compete:
                 routing = F.softmax(layer.score_proj(r_in).view(n, h, m), dim=-1) * m
@@ -182,24 +182,25 @@ class DecodeEngine:
     @torch.no_grad()
     def layer_step(self, layer_idx, x, slots):
         """One token of the listed sequences through layer `layer_idx`.
-        x [n, dim, 2] (fp32, row i belongs to slots[i]); slots: int32 device
-        tensor of n distinct live slot ids.  Updates those slots' states and
-        returns the layer's output [n, dim, 2]."""
+        x [n, dim, 2] (fp32 or bf16, row i belongs to slots[i]); slots: int32
+        device tensor of n distinct live slot ids.  Updates those slots' states
+        and returns the layer's output [n, dim, 2] in the GEMM dtype (a bf16
+        output feeds the next layer's bf16 projection with no conversion)."""
         layer, w = self.layers[layer_idx], self._w[layer_idx]
         n, dim = x.shape[0], w["dim"]
         h, d, m = self.n_heads, self.head_dim, self.n_states
         if n == 0:
             return x.new_zeros(0, dim, 2)
-        x = x.float().contiguous()
-        # the decode kernel reads fp32 planes: a bf16 projection is widened first
-        proj = F.linear(x.view(n, 2 * dim).to(self.dtype), w["w_in"], w["b_in"]).float().view(n, 1, -1)
+        x = x.contiguous() if x.dtype in (torch.float32, torch.bfloat16) else x.float().contiguous()
+        proj = F.linear(x.view(n, 2 * dim).to(self.dtype), w["w_in"], w["b_in"]).view(n, 1, -1)
         protect, phase, routing = self._gates(layer, x, w)
-        (qr, qi), (kr, ki), (vr, vi), gamma, rot = pam_prologue(
+        # the prologue writes fp32 planes (what the decode kernel reads) from a bf16 or fp32 projection
+        (qr, qi), (kr, ki), (vr, vi), gamma, rot = prologue_decode(
             proj, w["dt_bias"], n_heads=h, n_states=m, state_offset=layer.state_dt_offset if m > 1 else None,
             protect=None if protect is None else protect.view(n, 1, h),
             phase=None if phase is None else phase.view(n, 1, h, m),
             routing=None if routing is None else routing.view(n, 1, h, m),
-            rope=None, qk_norm=layer.qk_norm, gamma_floor=layer.gamma_floor or 0.0)
+            qk_norm=layer.qk_norm, gamma_floor=layer.gamma_floor or 0.0)
         # the prologue's planes go to the decode kernel as they are ([n, H, d] views)
         q, k, v = ((re[:, :, 0], im[:, :, 0]) for re, im in ((qr, qi), (kr, ki), (vr, vi)))
         g = gamma[..., 0].permute(1, 2, 0)                                    # [n, H, K] view
@@ -209,7 +210,7 @@ class DecodeEngine:
         # every listed slot is live, so the kernel writes every row of y: no zero fill
         y = self.pool.step(layer_idx, q, k, v, g, slots, rot=r, q_scale=d ** -0.5, compact=True,
                            out=torch.empty(n, h, d, 2, device=x.device, dtype=torch.float32))
-        return F.linear(y.view(n, 2 * h * d).to(self.dtype), w["w_out"], w["b_out"]).float().view(n, dim, 2)
+        return F.linear(y.view(n, 2 * h * d).to(self.dtype), w["w_out"], w["b_out"]).view(n, dim, 2)
 
     def _layers(self, x, slots, between):
         for li in range(len(self.layers)):
@@ -256,7 +257,7 @@ class DecodeEngine:
             entry = None
         if entry is None:
             if n and nb > n:  # run the padded batch eagerly: the capture then meets only shapes already run
-                x = torch.cat([x.float(), x.new_zeros(nb - n, *x.shape[1:], dtype=torch.float32)])
+                x = torch.cat([x, x.new_zeros(nb - n, *x.shape[1:])])
                 slots = torch.cat([slots.to(torch.int32), self._scratch[:nb - n]])
             out = self._layers(x, slots, between)[:n]
             if n:

@@ -240,6 +240,52 @@ def pam_prologue(proj, dt_bias, *, n_heads, n_states=1, state_offset=None, prote
     return (out[0], out[1]), (out[2], out[3]), (out[4], out[5]), out[6], rot
 
 
+def prologue_decode(proj, dt_bias, *, n_heads, n_states=1, state_offset=None, protect=None, phase=None,
+                    routing=None, qk_norm=False, gamma_floor=0.0):
+    """Inference form of pam_prologue for the decode step (no autograd, no
+    RoPE): the q, k, v planes come out in fp32 whatever proj's dtype (fp32 or
+    bf16), which is what the decode kernel reads, so a bf16 projection needs no
+    widening pass.  protect / phase / routing as in pam_prologue."""
+    cast = (lambda t: t.to(proj.dtype) if t is not None and t.dtype != proj.dtype else t)
+    f32 = (lambda t: t.float() if t is not None and t.dtype != torch.float32 else t)
+    a, keep = _fill(proj, cast(protect), cast(phase), cast(routing), f32(dt_bias), f32(state_offset), None,
+                    int(n_heads), int(n_states), 0, bool(qk_norm), float(gamma_floor))
+    a.out_dtype = _lib.QPAM_F32
+    B, T, H, M = proj.shape[0], proj.shape[1], int(n_heads), int(n_states)
+    dev = proj.device
+    outs = [torch.empty(B, H, T, HEAD_DIM, device=dev, dtype=torch.float32) for _ in range(6)]
+    a.oq_re, a.oq_im, a.ok_re, a.ok_im, a.ov_re, a.ov_im = (o.data_ptr() for o in outs)
+    gamma = torch.empty(M, B, H, T, device=dev, dtype=torch.float32)
+    a.gamma = gamma.data_ptr()
+    rot = None
+    if phase is not None:
+        rot = (torch.empty_like(gamma), torch.empty_like(gamma))
+        a.rot_re, a.rot_im = rot[0].data_ptr(), rot[1].data_ptr()
+    with torch.cuda.device(dev):
+        _lib.check(_lib.lib().qpam_prologue_fwd(a, _lib.stream_ptr(dev)), "qpam_prologue_fwd")
+    del keep
+    return (outs[0], outs[1]), (outs[2], outs[3]), (outs[4], outs[5]), gamma, rot
+
+
+def mag_linear(z, weight, bias=None, out_dtype=torch.float32):
+    """Gate logits from |z| in one launch (inference): z [n, dim, 2] (fp32 or
+    bf16, contiguous), weight fp32 [G, dim], bias fp32 [G] or None ->
+    out [n, G] = |z| weight^T + bias in out_dtype (|z| as cabs)."""
+    if not z.is_cuda:
+        raise ValueError("qpam mag_linear: tensors must be on the GPU (no CPU path in this library)")
+    z = z.contiguous()
+    n, dim = z.shape[0], z.shape[1]
+    G = weight.shape[0]
+    w = weight.float().contiguous()
+    b = bias.float().contiguous() if bias is not None else None
+    out = torch.empty(n, G, device=z.device, dtype=out_dtype)
+    with torch.cuda.device(z.device):
+        _lib.check(_lib.lib().qpam_mag_linear(_dt_code(z), _dt_code(out), n, dim, G, z.data_ptr(), w.data_ptr(),
+                                              b.data_ptr() if b is not None else None, out.data_ptr(), G,
+                                              _lib.stream_ptr(z.device)), "qpam_mag_linear")
+    return out
+
+
 @torch.library.custom_op("qpam::cabs", mutates_args=())
 def cabs_op(z: Tensor) -> Tensor:
     """|z| = sqrt(re^2 + im^2 + 1e-8) of a complex [..., 2] tensor (fp32 or bf16)."""

@@ -319,3 +319,22 @@ def test_cabs_matches_oracle(gpu_lib, dtype):
     assert m.dtype == dtype and _rel(m, mr) < tol
     assert zc.grad.dtype == dtype and _rel(zc.grad, zr.grad) < tol
     assert torch.isfinite(zc.grad.float()).all()
+
+
+@pytest.mark.parametrize("dtype,out_dtype", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                             (torch.bfloat16, torch.float32)])
+def test_mag_linear_matches_oracle(gpu_lib, dtype, out_dtype):
+    """The decode step's gate logits from |x| (qpam_mag_linear: cabs then the
+    protect-gate and phase rows in one launch) against the oracle's cabs and a
+    float64 matmul; rows of odd length, with and without bias."""
+    from qllm2_amd.pam_prologue import mag_linear
+    g = torch.Generator().manual_seed(41)
+    for n, dim, G, bias in ((193, 768, 48, True), (5, 100, 7, False), (1, 1536, 12, True)):
+        z = torch.randn(n, dim, 2, generator=g).to(dtype)
+        w = torch.randn(G, dim, generator=g) * dim ** -0.5
+        b = torch.randn(G, generator=g) if bias else None
+        ref = L.cabs(z.double()) @ w.double().T + (b.double() if bias else 0.0)
+        out = mag_linear(z.cuda(), w.cuda(), b.cuda() if bias else None, out_dtype=out_dtype)
+        assert out.dtype == out_dtype and tuple(out.shape) == (n, G)
+        tol = 1e-5 if out_dtype == torch.float32 else 1e-2
+        assert _rel(out, ref) < tol, f"n={n} dim={dim}: {_rel(out, ref):.2e}"

@@ -388,6 +388,58 @@ typedef struct {
 size_t qpam_delta_bwd_workspace_size(const qpam_delta_bwd_args *a);
 int qpam_delta_bwd(const qpam_delta_bwd_args *a, void *stream);
 
+/* ------------------------------------------------ E1 per-channel decay --
+ * The per-channel pieces of V11PAMLayer._forward_chunked_perchannel
+ * (v11/model.py:421-489); its chunk-parallel complex products are plain
+ * batched GEMMs on the caller's side.
+ *
+ * qpam_pc_fold_fwd: per chunk of `chunk` steps and key channel j, with
+ *   L_t = max(sum_{u<=t} log(max(gamma_u, 1e-6)), -30)   (v11/model.py:436-438)
+ * writes qf = q e^{L_t} q_scale, kf = k e^{-L_t}, wf = k e^{L_last - L_t}
+ * (L_last at the chunk's last step) and atot = e^{L_last}
+ * (v11/model.py:439-450, 480); rows past T are zero.  q, k interleaved complex
+ * [B,H,T,d,2] in `dtype` (element strides b, h, t; d and the pair contiguous);
+ * gamma [B,H,T,d] in `g_dtype` (strides g_*).  Outputs fp32, contiguous:
+ * qf, kf, wf [B*H][n][chunk][d][2], atot [B*H][n][d], n = ceil(T / chunk).
+ * qpam_pc_fold_bwd: from the gradients of those four (each may be NULL for
+ * zero) writes dq, dk (contiguous [B,H,T,d,2], `dtype`) and dgamma
+ * (contiguous [B,H,T,d], `g_dtype`), through both clamps as torch's
+ * clamp_min / clamp pass gradients (at or above the bound). */
+typedef struct {
+    int32_t dtype, g_dtype;
+    int64_t B, H, T, d;
+    int32_t chunk;                         /* the reference's chunk_size, 1..64 */
+    float q_scale;
+    const void *q, *k;
+    int64_t q_sb, q_sh, q_st, k_sb, k_sh, k_st;
+    const void *gamma;
+    int64_t g_sb, g_sh, g_st;
+    float *qf, *kf, *wf, *atot;            /* forward outputs */
+    const float *dqf, *dkf, *dwf, *datot;  /* backward inputs (optional) */
+    void *dq, *dk, *dgamma;                /* backward outputs */
+} qpam_pc_fold_args;
+
+int qpam_pc_fold_fwd(const qpam_pc_fold_args *a, void *stream);
+int qpam_pc_fold_bwd(const qpam_pc_fold_args *a, void *stream);
+
+/* The per-column decayed state scan of the per-channel chunks
+ * (v11/model.py:486): state S [d][d] complex per chain, column j decayed by
+ * a[c][j] at each step c; out[c] = S before step c, then S <- a[c] (.) S + x[c];
+ * fin = S after the last step.  reverse = 1 walks c from n-1 down to 0 (the
+ * gradient of the forward scan: x = the gradient of out, init = that of fin,
+ * out = the gradient of x).  fp32, contiguous: x, out [N][n][d][d][2],
+ * a [N][n][d], init, fin [N][d][d][2] (init NULL = zero, fin optional). */
+typedef struct {
+    int64_t N, n, d;
+    const float *x, *a;
+    float *out;
+    const float *init;
+    float *fin;
+    int32_t reverse;
+} qpam_pc_scan_args;
+
+int qpam_pc_scan(const qpam_pc_scan_args *a, void *stream);
+
 /* ------------------------------------------------ complex elementwise -----
  * Split-real complex tensors [rows, dim, 2] (interleaved re/im, contiguous),
  * fp32 or bf16; per-column parameters fp32 [dim].  Ops (z = gate for the CGU):

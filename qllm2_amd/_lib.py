@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -163,6 +163,26 @@ class PrologueBwdArgs(ctypes.Structure):
     ]
 
 
+class PcFoldArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_i32), ("g_dtype", c_i32), ("B", c_i64), ("H", c_i64), ("T", c_i64), ("d", c_i64),
+        ("chunk", c_i32), ("q_scale", c_f32),
+        ("q", c_ptr), ("k", c_ptr), ("q_sb", c_i64), ("q_sh", c_i64), ("q_st", c_i64),
+        ("k_sb", c_i64), ("k_sh", c_i64), ("k_st", c_i64),
+        ("gamma", c_ptr), ("g_sb", c_i64), ("g_sh", c_i64), ("g_st", c_i64),
+        ("qf", c_ptr), ("kf", c_ptr), ("wf", c_ptr), ("atot", c_ptr),
+        ("dqf", c_ptr), ("dkf", c_ptr), ("dwf", c_ptr), ("datot", c_ptr),
+        ("dq", c_ptr), ("dk", c_ptr), ("dgamma", c_ptr),
+    ]
+
+
+class PcScanArgs(ctypes.Structure):
+    _fields_ = [
+        ("N", c_i64), ("n", c_i64), ("d", c_i64), ("x", c_ptr), ("a", c_ptr), ("out", c_ptr),
+        ("init", c_ptr), ("fin", c_ptr), ("reverse", c_i32),
+    ]
+
+
 SIGNATURES = {
     "qpam_version": (ctypes.c_int, []),
     "qpam_last_error": (ctypes.c_char_p, []),
@@ -193,6 +213,9 @@ SIGNATURES = {
     "qpam_delta_bwd": (ctypes.c_int, [ctypes.POINTER(DeltaBwdArgs), c_ptr]),
     "qpam_cabs_bwd": (ctypes.c_int, [c_i32, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
     "qpam_mag_linear": (ctypes.c_int, [c_i32, c_i32, c_i64, c_i32, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "qpam_pc_fold_fwd": (ctypes.c_int, [ctypes.POINTER(PcFoldArgs), c_ptr]),
+    "qpam_pc_fold_bwd": (ctypes.c_int, [ctypes.POINTER(PcFoldArgs), c_ptr]),
+    "qpam_pc_scan": (ctypes.c_int, [ctypes.POINTER(PcScanArgs), c_ptr]),
 }
 
 _LIB = None

@@ -9,6 +9,9 @@ Reference methods replaced (v11/model.py):
   _recur_step_additive      927-965  (one decode step)
   _recurrent                845-925  (decode token loop; all K states of a
                                       token in one kernel launch)
+  _forward_chunked_perchannel 421-489 (E1 per-channel decay: the fold and the
+                                      state scan as HIP kernels, the chunk
+                                      products as batched complex GEMMs)
   _forward_delta            491-576  (E2 delta write; HIP token recurrence
                                       instead of the per-chunk solve)
   _recur_step_delta         967-1002 (one E2 decode token)
@@ -30,9 +33,8 @@ and every replacement hands a call to the saved method when the kernels do
 not cover it, so the installed layer computes what the reference computes in
 every mode:
   * CPU tensors (the reference computes on CPU through its torch code);
-  * E1 per-channel decay (decay_gamma [..., d]): the reference's
-    _forward_chunked_perchannel is not replaced, and its decode steps go to
-    the saved _recur_step_additive / _recurrent;
+  * the decode steps of E1 per-channel decay (decay_gamma [..., d]) go to the
+    saved _recur_step_additive / _recurrent;
   * decode steps whose inputs need gradients (a T = 1 forward in training, a
     state-carrying call under grad mode): the reference step is differentiable
     torch code, the HIP decode step updates the state in place;
@@ -54,6 +56,7 @@ from . import pam_delta as _delta
 from . import fused_ce as _fused_ce
 from . import flash_pam as _flash_pam
 from . import triton_kernels as _tk
+from .pam_perchannel import perchannel_chunked
 from .pam_prologue import cabs, pam_prologue, proj_columns
 from .pam_scan import chunk_for, pam_scan_interleaved, pam_scan_planar
 
@@ -177,6 +180,16 @@ def recur_step_delta(self, memory_state, decay_gamma, value_t, key_t, query_t, w
 
 
 _DECODE_DIMS = (16, 32, 64, 128)
+
+
+def forward_chunked_perchannel(self, queries, keys, protected_values, decay_gamma, head_dim):
+    """V11PAMLayer._forward_chunked_perchannel (E1, v11/model.py:421-489) on
+    the GPU (qllm2_amd/pam_perchannel.py), differentiable; CPU tensors and
+    chunk sizes outside 1..64 run the saved reference method."""
+    if not queries.is_cuda or not 1 <= int(self.chunk_size) <= 64:
+        return _original(self, "_forward_chunked_perchannel")(self, queries, keys, protected_values, decay_gamma,
+                                                              head_dim)
+    return perchannel_chunked(queries, keys, protected_values, decay_gamma, head_dim, self.chunk_size)
 
 
 def recur_step_additive(self, memory_state, decay_gamma, value_t, key_t, query_t):
@@ -418,6 +431,7 @@ _METHODS = {
     "_forward_delta": forward_delta,
     "_recur_step_delta": recur_step_delta,
     "_recurrent": recurrent,
+    "_forward_chunked_perchannel": forward_chunked_perchannel,
 }
 
 # module-level functions of the reference's v11 package that this package

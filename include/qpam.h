@@ -136,6 +136,10 @@ typedef struct {
     /* optional planar rotation (ABI 7): rot points at the real plane and rot_im at
      * the imaginary one, same strides; NULL = interleaved [2] entries. */
     const float *rot_im;
+    /* 0: one decay per (slot, group, state); 1 (ABI 9): d decays there, one per
+     * key channel j (contiguous), S[i][j] <- gamma[j] S[i][j] + v_i conj(k_j) --
+     * the per-channel branch of _recur_step_additive (v11/model.py:952-954). */
+    int32_t gamma_per_channel;
 } qpam_decode_args;
 
 int qpam_decode_step(const qpam_decode_args *a, void *stream);

@@ -4,6 +4,8 @@
 // applied per state and phase-routed/summed as in _recurrent
 // (v11/model.py:874-906):
 //     S <- gamma S + v (x) conj(k);   y = sum_m r_m (S_m @ q~)
+// with a head decay, or (gamma_per_channel) one decay per key column j, the
+// per-channel branch (v11/model.py:952-954).
 //
 // Design: one workgroup per (listed slot, group).  The d x d interleaved
 // complex state of each of the M states is streamed once with non-temporal
@@ -69,6 +71,17 @@ __device__ __forceinline__ float2 load_one(const float *re, const float *im, int
     return make_float2(re[e], im[e]);
 }
 
+// decay of this lane's key columns 2 cp, 2 cp + 1 for the state whose decay
+// entry starts at `off`: the head decay of (slot, group, state), or its two
+// per-channel decays (gamma_per_channel)
+__device__ __forceinline__ float2 lane_decay(const qpam_decode_args &a, int64_t off, int cp) {
+    if (!a.gamma_per_channel) {
+        const float g = a.gamma[off];
+        return make_float2(g, g);
+    }
+    return make_float2(a.gamma[off + 2 * cp], a.gamma[off + 2 * cp + 1]);
+}
+
 // q and k of the slot times rope[pos[slot]] (two complex features per float4)
 template <int D>
 __device__ __forceinline__ void apply_rope(const qpam_decode_args &a, int slot, int cp, float4 &qv, float4 &kv) {
@@ -111,7 +124,7 @@ __device__ __forceinline__ void halving_reduce(float (&v)[NV], int lane, int &id
 // S <- gam S + v (x) conj(k) on this lane's ITERS float4 (two complex entries
 // each), streamed in place; returns the lane's partial sums of S q~ per row.
 template <typename S, bool PL>
-__device__ __forceinline__ void update_state(float *st, int tid, int r0, float gam, const float *vrow,
+__device__ __forceinline__ void update_state(float *st, int tid, int r0, float2 gam, const float *vrow,
                                              const float *vrow_im, float4 kv,
                                              float q0r, float q0i, float q1r, float q1i, float (&part)[S::NV]) {
     floatx4 s[S::ITERS];
@@ -126,10 +139,10 @@ __device__ __forceinline__ void update_state(float *st, int tid, int r0, float g
         const float o0r = vv.x * kv.x + vv.y * kv.y, o0i = vv.y * kv.x - vv.x * kv.y;
         const float o1r = vv.x * kv.z + vv.y * kv.w, o1i = vv.y * kv.z - vv.x * kv.w;
         floatx4 n;
-        n.x = gam * s[it].x + o0r;
-        n.y = gam * s[it].y + o0i;
-        n.z = gam * s[it].z + o1r;
-        n.w = gam * s[it].w + o1i;
+        n.x = gam.x * s[it].x + o0r;
+        n.y = gam.x * s[it].y + o0i;
+        n.z = gam.y * s[it].z + o1r;
+        n.w = gam.y * s[it].w + o1i;
         __builtin_nontemporal_store(n, reinterpret_cast<floatx4 *>(st + 4 * (it * S::THREADS + tid)));
         part[2 * it] = n.x * q0r - n.y * q0i + n.z * q1r - n.w * q1i;
         part[2 * it + 1] = n.x * q0i + n.y * q0r + n.z * q1i + n.w * q1r;
@@ -150,7 +163,7 @@ __global__ void __launch_bounds__((DecodeShape<D, 512>::THREADS)) decode_single_
     float4 qv = load_pair<PL>(a.q, a.q_im, vr * a.sq_slot + g * a.sq_group, cp);
     float4 kv = load_pair<PL>(a.k, a.k_im, vr * a.sk_slot + g * a.sk_group, cp);
     apply_rope<D>(a, slot, cp, qv, kv);
-    const float gam = a.gamma[vr * a.sg_slot + g * a.sg_group];
+    const float2 gam = lane_decay(a, vr * a.sg_slot + g * a.sg_group, cp);
     float part[S::NV];
     const int64_t vo = vr * a.sv_slot + g * a.sv_group;
     update_state<S, PL>(a.state + slot * a.st_slot + g * a.st_group, tid, r0, gam, a.v + vo, PL ? a.v_im + vo : nullptr,
@@ -208,7 +221,7 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
     for (int j = 0; j < S::NV; ++j) tot[j] = 0.f;
 #pragma unroll
     for (int m = 0; m < MS; ++m) {
-        const float gam = a.gamma[vr * a.sg_slot + g * a.sg_group + m * a.sg_state];
+        const float2 gam = lane_decay(a, vr * a.sg_slot + g * a.sg_group + m * a.sg_state, cp);
         float rr = 1.f, ri = 0.f;
         if (a.rot) {
             const int64_t ro = vr * a.sr_slot + g * a.sr_group + m * a.sr_state;
@@ -220,10 +233,10 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
             const float o0r = vv[it].x * kv.x + vv[it].y * kv.y, o0i = vv[it].y * kv.x - vv[it].x * kv.y;
             const float o1r = vv[it].x * kv.z + vv[it].y * kv.w, o1i = vv[it].y * kv.z - vv[it].x * kv.w;
             floatx4 n;
-            n.x = gam * s[m][it].x + o0r;
-            n.y = gam * s[m][it].y + o0i;
-            n.z = gam * s[m][it].z + o1r;
-            n.w = gam * s[m][it].w + o1i;
+            n.x = gam.x * s[m][it].x + o0r;
+            n.y = gam.x * s[m][it].y + o0i;
+            n.z = gam.y * s[m][it].z + o1r;
+            n.w = gam.y * s[m][it].w + o1i;
             __builtin_nontemporal_store(n, reinterpret_cast<floatx4 *>(st0 + m * a.st_state + 4 * (it * S::THREADS + tid)));
             const float pr = n.x * q0r - n.y * q0i + n.z * q1r - n.w * q1i;
             const float pi = n.x * q0i + n.y * q0r + n.z * q1i + n.w * q1r;
@@ -273,7 +286,7 @@ __global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS
 
     float yacc_r = 0.f, yacc_i = 0.f;  // lanes tid < D accumulate row tid
     for (int m = 0; m < a.n_states; ++m) {
-        const float gam = a.gamma[vr * a.sg_slot + g * a.sg_group + m * a.sg_state];
+        const float2 gam = lane_decay(a, vr * a.sg_slot + g * a.sg_group + m * a.sg_state, cp);
         float part[S::NV];
         update_state<S, PL>(a.state + slot * a.st_slot + g * a.st_group + m * a.st_state, tid, r0, gam, vrow, vrow_im, kv,
                         qv.x * a.q_scale, qv.y * a.q_scale, qv.z * a.q_scale, qv.w * a.q_scale, part);
@@ -374,6 +387,8 @@ extern "C" int qpam_decode_step(const qpam_decode_args *a, void *stream) {
                  "qpam_decode_step: rope needs positions, rope_len >= 1 and a 16-byte aligned table");
     QPAM_REQUIRE((long long)a->n_active * a->n_groups < (1ll << 31), "qpam_decode_step: grid too large");
     QPAM_REQUIRE(a->rot_im == nullptr || a->rot != nullptr, "qpam_decode_step: rot_im without rot");
+    QPAM_REQUIRE(a->gamma_per_channel == 0 || a->gamma_per_channel == 1,
+                 "qpam_decode_step: gamma_per_channel must be 0 or 1");
     const bool planar = a->q_im != nullptr;
     QPAM_REQUIRE((a->k_im != nullptr) == planar && (a->v_im != nullptr) == planar,
                  "qpam_decode_step: q_im, k_im and v_im are all set (planar q, k, v) or all NULL");

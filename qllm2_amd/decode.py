@@ -30,7 +30,8 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     state  [S, G, M, d, d, 2] fp32 (G = layers*heads, M states), updated in place
     q,k,v  [R, G, d, 2] fp32 (q unscaled; multiplied by q_scale), or all three
            as planar (re, im) pairs of [R, G, d] fp32 tensors with equal strides
-    gamma  [R, G, M] fp32 (any strides)
+    gamma  [R, G, M] fp32 (any strides), or [R, G, M, d] with the last dim
+           contiguous: one decay per key channel (E1 per-channel decay)
     active optional int32 [n] slot ids (others untouched); None = all slots
     rot    optional [R, G, M, 2] fp32 complex rotation of each state's read, or a
            planar (re, im) pair of [R, G, M] fp32 tensors with equal strides
@@ -56,8 +57,12 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     for name, t in zip(("q_re", "q_im", "k_re", "k_im", "v_re", "v_im") if planar else ("q", "k", "v"), planes):
         if tuple(t.shape) != want:
             raise ValueError(f"{name} must be {list(want)}, got {tuple(t.shape)}")
-    if tuple(gamma.shape) != (rows, n_groups, n_states):
-        raise ValueError(f"gamma must be [{rows},{n_groups},{n_states}], got {tuple(gamma.shape)}")
+    per_channel = gamma.dim() == 4
+    if tuple(gamma.shape) != ((rows, n_groups, n_states, d) if per_channel else (rows, n_groups, n_states)):
+        raise ValueError(f"gamma must be [{rows},{n_groups},{n_states}] or [{rows},{n_groups},{n_states},{d}], "
+                         f"got {tuple(gamma.shape)}")
+    if per_channel and gamma.stride(-1) != 1:
+        gamma = gamma.contiguous()
     rot_pl = isinstance(rot, (tuple, list))
     rots = list(rot) if rot_pl else ([rot] if rot is not None else [])
     for t in [state, gamma] + planes + rots:
@@ -108,7 +113,8 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     a.sk_slot, a.sk_group = k.stride(0), k.stride(1)
     a.sv_slot, a.sv_group = v.stride(0), v.stride(1)
     a.gamma = gamma.data_ptr()
-    a.sg_slot, a.sg_group, a.sg_state = gamma.stride()
+    a.sg_slot, a.sg_group, a.sg_state = gamma.stride()[:3]
+    a.gamma_per_channel = int(per_channel)
     if rot is not None:
         a.rot = rot.data_ptr()
         a.sr_slot, a.sr_group, a.sr_state = rot.stride(0), rot.stride(1), rot.stride(2)
@@ -133,12 +139,14 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
 
 
 def recur_step_additive(memory_state, decay_gamma, value_t, key_t, query_t):
-    """Drop-in for V11PAMLayer._recur_step_additive (v11/model.py:927-965),
-    head-scalar decay.  memory_state [..., d, d, 2], decay_gamma [...],
-    value_t/key_t/query_t [..., d, 2] (query already scaled).
-    Returns (output [..., d, 2], new memory_state); the input is not modified."""
-    if decay_gamma.dim() != memory_state.dim() - 3:
-        raise NotImplementedError("per-channel decay (E1) is not on the HIP decode path")
+    """Drop-in for V11PAMLayer._recur_step_additive (v11/model.py:927-965).
+    memory_state [..., d, d, 2]; decay_gamma [...] (head decay) or [..., d]
+    (per-channel decay, one per key column); value_t/key_t/query_t [..., d, 2]
+    (query already scaled).  Returns (output [..., d, 2], new memory_state);
+    the input is not modified."""
+    per_channel = decay_gamma.dim() == memory_state.dim() - 2
+    if not per_channel and decay_gamma.dim() != memory_state.dim() - 3:
+        raise ValueError(f"decay_gamma must be [...] or [..., d] for a state {tuple(memory_state.shape)}")
     lead = memory_state.shape[:-3]
     d = memory_state.shape[-2]
     new_state = memory_state.to(torch.float32).contiguous().clone().view(-1, 1, 1, d, d, 2)
@@ -147,8 +155,9 @@ def recur_step_additive(memory_state, decay_gamma, value_t, key_t, query_t):
     def flat(t):
         return t.to(torch.float32).contiguous().view(n, 1, d, 2)
 
-    y = decode_step(new_state, flat(query_t), flat(key_t), flat(value_t),
-                    decay_gamma.to(torch.float32).contiguous().view(n, 1, 1), q_scale=1.0)
+    gam = decay_gamma.to(torch.float32).contiguous()
+    gam = gam.view(n, 1, 1, d) if per_channel else gam.view(n, 1, 1)
+    y = decode_step(new_state, flat(query_t), flat(key_t), flat(value_t), gam, q_scale=1.0)
     return (y.view(*lead, d, 2).to(memory_state.dtype),
             new_state.view(*lead, d, d, 2).to(memory_state.dtype))
 

@@ -33,8 +33,6 @@ and every replacement hands a call to the saved method when the kernels do
 not cover it, so the installed layer computes what the reference computes in
 every mode:
   * CPU tensors (the reference computes on CPU through its torch code);
-  * the decode steps of E1 per-channel decay (decay_gamma [..., d]) go to the
-    saved _recur_step_additive / _recurrent;
   * decode steps whose inputs need gradients (a T = 1 forward in training, a
     state-carrying call under grad mode): the reference step is differentiable
     torch code, the HIP decode step updates the state in place;
@@ -193,11 +191,11 @@ def forward_chunked_perchannel(self, queries, keys, protected_values, decay_gamm
 
 
 def recur_step_additive(self, memory_state, decay_gamma, value_t, key_t, query_t):
-    """V11PAMLayer._recur_step_additive: the HIP decode step for head-scalar
-    decay without gradients; per-channel decay (decay_gamma [..., d]), inputs
+    """V11PAMLayer._recur_step_additive: the HIP decode step for head or
+    per-channel decay (decay_gamma [...] or [..., d]) without gradients; inputs
     that need gradients, CPU tensors and head dims outside 16/32/64/128 run the
     saved reference step (v11/model.py:927-965, differentiable torch code)."""
-    if (not memory_state.is_cuda or decay_gamma.dim() != memory_state.dim() - 3
+    if (not memory_state.is_cuda or decay_gamma.dim() not in (memory_state.dim() - 3, memory_state.dim() - 2)
             or memory_state.shape[-2] not in _DECODE_DIMS
             or _needs_grad(memory_state, decay_gamma, value_t, key_t, query_t)):
         return _original(self, "_recur_step_additive")(self, memory_state, decay_gamma, value_t, key_t, query_t)
@@ -205,11 +203,12 @@ def recur_step_additive(self, memory_state, decay_gamma, value_t, key_t, query_t
 
 
 def recurrent(self, x, queries, keys, values, state, head_dim):
-    """V11PAMLayer._recurrent for the additive head-decay write: per token one
-    qpam_decode_step launch updates all K states and sums the rotated reads.
-    The E1 / E2 modes, grad mode, CPU tensors and other head dims run the saved
-    reference loop (which then calls the replaced steps where they apply)."""
-    if (self.write_mode != 'additive' or self.decay_mode == 'per_channel' or torch.is_grad_enabled()
+    """V11PAMLayer._recurrent for the additive write (head or per-channel
+    decay): per token one qpam_decode_step launch updates all K states and sums
+    the rotated reads.  The E2 mode, grad mode, CPU tensors and other head dims
+    run the saved reference loop (which then calls the replaced steps where
+    they apply)."""
+    if (self.write_mode != 'additive' or torch.is_grad_enabled()
             or not x.is_cuda or head_dim not in _DECODE_DIMS):
         return _original(self, "_recurrent")(self, x, queries, keys, values, state, head_dim)
     b, t = x.shape[0], x.shape[1]
@@ -234,7 +233,7 @@ def recurrent(self, x, queries, keys, values, state, head_dim):
             g_k, pv = self._gamma_and_vprime(tok, values[:, :, ti:ti + 1], state_offset=off)
             gam.append(g_k[:, :, 0])
             v_t = pv[:, :, 0]
-        gamma = torch.stack(gam, -1).float().contiguous()                     # [B,H,K]
+        gamma = torch.stack(gam, 2).float().contiguous()                      # [B,H,K] or [B,H,K,d]
         r = rot[:, ti].float().contiguous() if k_states > 1 else None         # [B,H,K,2]
         y = _decode.decode_step(pool, queries[:, :, ti].float().contiguous(), keys[:, :, ti].float().contiguous(),
                                 v_t.float().contiguous(), gamma, rot=r, q_scale=scale)

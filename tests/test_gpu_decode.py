@@ -224,3 +224,42 @@ def test_decode_planar_inputs_rejected_when_mixed(gpu_lib):
     st, q, k, v, gamma = (x.cuda() for x in (state, q, k, v, gamma))
     with pytest.raises(ValueError, match="plane pairs"):
         decode_step(st, (q[..., 0], q[..., 1]), k, v, gamma)
+
+
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+@pytest.mark.parametrize("M,use_rot", [(1, False), (2, True), (3, True), (5, True)])
+def test_decode_per_channel_decay_matches_textbook_recurrence(gpu_lib, d, M, use_rot):
+    """E1 per-channel decay (gamma [R, G, M, d], one per key column) through
+    every decode kernel: T steps from a zero state on two of four slots equal
+    the oracle's textbook per-channel recurrence (brute_force_perchannel,
+    complex128) per state, rotated and summed; the other slots stay zero."""
+    from qllm2_amd.decode import decode_step
+    S, G, T = 4, 3, 6
+    g = torch.Generator().manual_seed(300 + d + M)
+    q, k, v = (torch.randn(T, S, G, d, 2, generator=g, dtype=torch.float64) for _ in range(3))
+    gamma = torch.sigmoid(torch.randn(T, S, G, M, d, generator=g, dtype=torch.float64) + 1.0)
+    rot = torch.randn(T, S, G, M, 2, generator=g, dtype=torch.float64)
+    active = torch.tensor([3, 1], dtype=torch.int32)
+    scale = d ** -0.5
+    st = torch.zeros(S, G, M, d, d, 2, device="cuda")
+    ys = []
+    for t in range(T):
+        ys.append(decode_step(st, q[t].float().cuda(), k[t].float().cuda(), v[t].float().cuda(),
+                              gamma[t].float().cuda(), active=active.cuda(), q_scale=scale,
+                              rot=rot[t].float().cuda() if use_rot else None).cpu())
+    torch.cuda.synchronize()
+    for s in active.tolist():
+        y_ref = 0
+        for m in range(M):
+            y_m, s_m = O.brute_force_perchannel(O.to_complex(q[:, s]).transpose(1, 0, 2),
+                                                O.to_complex(k[:, s]).transpose(1, 0, 2),
+                                                O.to_complex(v[:, s]).transpose(1, 0, 2),
+                                                gamma[:, s, :, m].numpy().transpose(1, 0, 2), scale)
+            r = O.to_complex(rot[:, s, :, m]).T[:, :, None] if use_rot else 1.0   # [G, T, 1]
+            y_ref = y_ref + r * y_m
+            got_s = st[s, :, m].cpu()
+            assert _rel(got_s, O.from_complex(s_m)) < REL
+        got_y = torch.stack([y[s] for y in ys], 1)                    # [G, T, d, 2]
+        assert _rel(got_y, O.from_complex(y_ref)) < REL
+    for s in (0, 2):
+        assert st[s].abs().max().item() == 0.0

@@ -16,8 +16,8 @@ the shapes the kernels take in pieces (six states, head_dim 128 and 96):
     v11/selftest.py:16-38);
   * the HIP kernels ran where they apply: counters on the saved originals show
     the head-decay scans, the delta write and the decode steps never fell
-    back (E1's decode steps, and decode at head dims outside 16/32/64/128, run
-    the reference methods by design);
+    back (decode at head dims outside 16/32/64/128 runs the reference methods
+    by design);
   * grad mode: a T = 1 step carrying a state (the reference's recurrent
     branch, v11/model.py:830-832) and a prefill, every gradient (input, state,
     each parameter) against float64 autograd of the oracle layer, rel <= 1e-4.
@@ -62,8 +62,8 @@ HIP_ONLY = {
     "E3_6states": ("_forward_multistate_fused", "_fused_chunk_step", "_recurrent", "_recur_step_additive"),
     "baseline_hd128": ("_forward_chunked_head", "_recurrent", "_recur_step_additive"),
     "E3_hd96": ("_forward_multistate_fused", "_fused_chunk_step"),
-    "E1": ("_forward_chunked_perchannel",),
-    "E1+E3": ("_forward_chunked_perchannel",),
+    "E1": ("_forward_chunked_perchannel", "_recurrent", "_recur_step_additive"),
+    "E1+E3": ("_forward_chunked_perchannel", "_recurrent", "_recur_step_additive"),
 }
 
 

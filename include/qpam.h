@@ -21,6 +21,7 @@
  *
  * Reference interfaces replaced (paths relative to gowrav-vishwakarma/qllm2):
  *   qpam_decode_step    v11/model.py:927-965  V11PAMLayer._recur_step_additive
+ *   qpam_decode_step_bwd v11/model.py:927-965 its gradient (torch autograd there)
  *                       v11/model.py:845-925  V11PAMLayer._recurrent (token
  *                       step over K states with the e^{i phi} rotation)
  *   qpam_scan_fwd       v11/model.py:378-417  _forward_chunked_head,
@@ -143,6 +144,25 @@ typedef struct {
 } qpam_decode_args;
 
 int qpam_decode_step(const qpam_decode_args *a, void *stream);
+
+/* Backward of one decode step, the gradient of _recur_step_additive
+ * (v11/model.py:927-965, which the reference differentiates with torch
+ * autograd) for n independent (slot, head) states of one matrix state each:
+ *   S' = gamma (.) S + v (x) conj(k),  y = S' q   (q already scaled)
+ * with gamma one decay per state or (gamma_per_channel) one per key column.
+ * In: the state before the step `state` [n][d][d][2], gamma [n] or [n][d],
+ * q, k, v, dy [n][d][2], dstate_new [n][d][d][2] (the gradient of S'; NULL =
+ * zero).  Out: dstate (gradient of S) [n][d][d][2], dgamma (shape of gamma),
+ * dq, dk, dv [n][d][2].  fp32, contiguous; d in {16, 32, 64, 128}.
+ * Deterministic (fixed-order reductions). */
+typedef struct {
+    int64_t n;
+    int32_t d, gamma_per_channel;
+    const float *state, *gamma, *q, *k, *v, *dy, *dstate_new;
+    float *dstate, *dgamma, *dq, *dk, *dv;
+} qpam_decode_bwd_args;
+
+int qpam_decode_step_bwd(const qpam_decode_bwd_args *a, void *stream);
 
 /* ------------------------------------------------------------------ scan --
  * Chunked dual-form PAM scan with M >= 1 states per head (E3 when M > 1):

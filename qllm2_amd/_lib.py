@@ -163,6 +163,15 @@ class PrologueBwdArgs(ctypes.Structure):
     ]
 
 
+class DecodeBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("n", c_i64), ("d", c_i32), ("gamma_per_channel", c_i32),
+        ("state", c_ptr), ("gamma", c_ptr), ("q", c_ptr), ("k", c_ptr), ("v", c_ptr), ("dy", c_ptr),
+        ("dstate_new", c_ptr),
+        ("dstate", c_ptr), ("dgamma", c_ptr), ("dq", c_ptr), ("dk", c_ptr), ("dv", c_ptr),
+    ]
+
+
 class PcFoldArgs(ctypes.Structure):
     _fields_ = [
         ("dtype", c_i32), ("g_dtype", c_i32), ("B", c_i64), ("H", c_i64), ("T", c_i64), ("d", c_i64),
@@ -190,6 +199,7 @@ SIGNATURES = {
     "qpam_event_destroy": (ctypes.c_int, [c_ptr]),
     "qpam_event_elapsed_ms": (ctypes.c_int, [c_ptr, c_ptr, ctypes.POINTER(c_f32)]),
     "qpam_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeArgs), c_ptr]),
+    "qpam_decode_step_bwd": (ctypes.c_int, [ctypes.POINTER(DecodeBwdArgs), c_ptr]),
     "qpam_scan_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(ScanArgs)]),
     "qpam_scan_fwd": (ctypes.c_int, [ctypes.POINTER(ScanArgs), c_ptr]),
     "qpam_scan_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(ScanArgs), c_ptr]),

@@ -369,6 +369,109 @@ int launch_decode(const qpam_decode_args &a, hipStream_t stream) {
     return a.q_im ? launch_decode_pl<D, true>(a, stream) : launch_decode_pl<D, false>(a, stream);
 }
 
+// ------------------------------------------------ backward of one step --
+// One block per state.  Lane (r0, cp) owns key columns 2 cp, 2 cp + 1 and rows
+// r0, r0 + ROWS_PER_IT, ...: it recomputes S' from S, forms
+// G = dS' + dy conj(q) (the gradient of S'), writes dS = gamma G, and keeps its
+// partial column sums of dq = S'^H dy, dk_j = sum_i v_i conj(G_ij) and
+// dgamma_j = sum_i Re(conj(S_ij) G_ij) and its row sums of dv = G k; both are
+// summed through LDS in a fixed order.
+template <int D>
+constexpr int bwd_threads() { return (D * D / 2) < 256 ? (D * D / 2) : 256; }
+
+template <int D>
+__global__ void __launch_bounds__(bwd_threads<D>()) decode_bwd_kernel(qpam_decode_bwd_args a) {
+    using S = DecodeShape<D, bwd_threads<D>()>;
+    constexpr int NC = 10;                           // column partials: dq, dk (re, im x 2), dgamma x 2
+    __shared__ float cols[S::THREADS * NC];          // [r0][cp][NC]
+    __shared__ float rows[D * S::PAIRS * 2];         // [i][cp][re, im]
+    __shared__ float gsum[S::PAIRS];
+    const int64_t e = blockIdx.x;
+    const int tid = threadIdx.x, cp = tid % S::PAIRS, r0 = tid / S::PAIRS;
+    const float *st = a.state + e * D * D * 2;
+    const float *gst = a.dstate_new ? a.dstate_new + e * D * D * 2 : nullptr;
+    float *dst = a.dstate + e * D * D * 2;
+    const float4 q = *reinterpret_cast<const float4 *>(a.q + e * D * 2 + 4 * cp);
+    const float4 k = *reinterpret_cast<const float4 *>(a.k + e * D * 2 + 4 * cp);
+    float g0, g1;
+    if (a.gamma_per_channel) {
+        g0 = a.gamma[e * D + 2 * cp];
+        g1 = a.gamma[e * D + 2 * cp + 1];
+    } else {
+        g0 = g1 = a.gamma[e];
+    }
+    float c[NC];
+#pragma unroll
+    for (int x = 0; x < NC; ++x) c[x] = 0.f;
+#pragma unroll
+    for (int it = 0; it < S::ITERS; ++it) {
+        const int i = it * S::ROWS_PER_IT + r0;
+        const int64_t o = (int64_t)i * D * 2 + 4 * cp;
+        const float4 s = *reinterpret_cast<const float4 *>(st + o);
+        const float4 gs = gst ? *reinterpret_cast<const float4 *>(gst + o) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float2 v = *reinterpret_cast<const float2 *>(a.v + e * D * 2 + 2 * i);
+        const float2 dy = *reinterpret_cast<const float2 *>(a.dy + e * D * 2 + 2 * i);
+        // S' = gamma S + v conj(k)
+        const float p0r = g0 * s.x + v.x * k.x + v.y * k.y, p0i = g0 * s.y + v.y * k.x - v.x * k.y;
+        const float p1r = g1 * s.z + v.x * k.z + v.y * k.w, p1i = g1 * s.w + v.y * k.z - v.x * k.w;
+        // G = dS' + dy conj(q)
+        const float G0r = gs.x + dy.x * q.x + dy.y * q.y, G0i = gs.y + dy.y * q.x - dy.x * q.y;
+        const float G1r = gs.z + dy.x * q.z + dy.y * q.w, G1i = gs.w + dy.y * q.z - dy.x * q.w;
+        *reinterpret_cast<float4 *>(dst + o) = make_float4(g0 * G0r, g0 * G0i, g1 * G1r, g1 * G1i);
+        // dq_j += conj(S'_ij) dy_i
+        c[0] += p0r * dy.x + p0i * dy.y;
+        c[1] += p0r * dy.y - p0i * dy.x;
+        c[2] += p1r * dy.x + p1i * dy.y;
+        c[3] += p1r * dy.y - p1i * dy.x;
+        // dk_j += v_i conj(G_ij)
+        c[4] += v.x * G0r + v.y * G0i;
+        c[5] += v.y * G0r - v.x * G0i;
+        c[6] += v.x * G1r + v.y * G1i;
+        c[7] += v.y * G1r - v.x * G1i;
+        // dgamma_j += Re(conj(S_ij) G_ij)
+        c[8] += s.x * G0r + s.y * G0i;
+        c[9] += s.z * G1r + s.w * G1i;
+        // dv_i partial: G_i,2cp k_2cp + G_i,2cp+1 k_2cp+1
+        rows[(i * S::PAIRS + cp) * 2] = G0r * k.x - G0i * k.y + G1r * k.z - G1i * k.w;
+        rows[(i * S::PAIRS + cp) * 2 + 1] = G0r * k.y + G0i * k.x + G1r * k.w + G1i * k.z;
+    }
+#pragma unroll
+    for (int x = 0; x < NC; ++x) cols[(r0 * S::PAIRS + cp) * NC + x] = c[x];
+    __syncthreads();
+    if (tid < S::PAIRS) {  // column pair cp = tid: sum over the row groups in order
+        float t[NC];
+#pragma unroll
+        for (int x = 0; x < NC; ++x) t[x] = 0.f;
+        for (int r = 0; r < S::ROWS_PER_IT; ++r)
+#pragma unroll
+            for (int x = 0; x < NC; ++x) t[x] += cols[(r * S::PAIRS + tid) * NC + x];
+        *reinterpret_cast<float4 *>(a.dq + e * D * 2 + 4 * tid) = make_float4(t[0], t[1], t[2], t[3]);
+        *reinterpret_cast<float4 *>(a.dk + e * D * 2 + 4 * tid) = make_float4(t[4], t[5], t[6], t[7]);
+        if (a.gamma_per_channel) {
+            a.dgamma[e * D + 2 * tid] = t[8];
+            a.dgamma[e * D + 2 * tid + 1] = t[9];
+        } else {
+            gsum[tid] = t[8] + t[9];
+        }
+    }
+    if (tid < D) {  // row i = tid: sum over the column pairs in order
+        float vr = 0.f, vi = 0.f;
+        for (int p = 0; p < S::PAIRS; ++p) {
+            vr += rows[(tid * S::PAIRS + p) * 2];
+            vi += rows[(tid * S::PAIRS + p) * 2 + 1];
+        }
+        *reinterpret_cast<float2 *>(a.dv + e * D * 2 + 2 * tid) = make_float2(vr, vi);
+    }
+    if (!a.gamma_per_channel) {
+        __syncthreads();
+        if (tid == 0) {
+            float x = 0.f;
+            for (int p = 0; p < S::PAIRS; ++p) x += gsum[p];
+            a.dgamma[e] = x;
+        }
+    }
+}
+
 bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
 }  // namespace
@@ -410,4 +513,30 @@ extern "C" int qpam_decode_step(const qpam_decode_args *a, void *stream) {
         case 128: return launch_decode<128>(*a, s);
         default: return fail(QPAM_ERR_UNSUPPORTED, "qpam_decode_step: d=%d (supported 16, 32, 64, 128)", a->d);
     }
+}
+
+extern "C" int qpam_decode_step_bwd(const qpam_decode_bwd_args *a, void *stream) {
+    using namespace qpam;
+    QPAM_REQUIRE(a != nullptr, "qpam_decode_step_bwd: null args");
+    QPAM_REQUIRE(a->n >= 0 && a->n < (1ll << 31), "qpam_decode_step_bwd: bad n %lld", (long long)a->n);
+    QPAM_REQUIRE(a->gamma_per_channel == 0 || a->gamma_per_channel == 1,
+                 "qpam_decode_step_bwd: gamma_per_channel must be 0 or 1");
+    QPAM_REQUIRE(a->state && a->gamma && a->q && a->k && a->v && a->dy && a->dstate && a->dgamma && a->dq && a->dk &&
+                     a->dv,
+                 "qpam_decode_step_bwd: null pointer");
+    QPAM_REQUIRE(aligned(a->state, 16) && aligned(a->q, 16) && aligned(a->k, 16) && aligned(a->v, 8) &&
+                     aligned(a->dy, 8) && aligned(a->dstate, 16) && aligned(a->dq, 16) && aligned(a->dk, 16) &&
+                     aligned(a->dv, 8) && (a->dstate_new == nullptr || aligned(a->dstate_new, 16)),
+                 "qpam_decode_step_bwd: misaligned operand");
+    if (a->n == 0) return QPAM_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid((unsigned)a->n);
+    switch (a->d) {
+        case 16: hipLaunchKernelGGL(decode_bwd_kernel<16>, grid, dim3(bwd_threads<16>()), 0, s, *a); break;
+        case 32: hipLaunchKernelGGL(decode_bwd_kernel<32>, grid, dim3(bwd_threads<32>()), 0, s, *a); break;
+        case 64: hipLaunchKernelGGL(decode_bwd_kernel<64>, grid, dim3(bwd_threads<64>()), 0, s, *a); break;
+        case 128: hipLaunchKernelGGL(decode_bwd_kernel<128>, grid, dim3(bwd_threads<128>()), 0, s, *a); break;
+        default: return fail(QPAM_ERR_UNSUPPORTED, "qpam_decode_step_bwd: d=%d (supported 16, 32, 64, 128)", a->d);
+    }
+    return launch_status("decode_bwd_kernel");
 }

@@ -138,26 +138,55 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     return y
 
 
+class _DecodeStep(torch.autograd.Function):
+    """One decode step of n independent single-state (slot, head) rows, out of
+    place and differentiable: (state [n,d,d,2], gamma [n] or [n,d], v, k, q
+    [n,d,2], q scaled) -> (y [n,d,2], new state).  Forward: qpam_decode_step;
+    backward: qpam_decode_step_bwd."""
+
+    @staticmethod
+    def forward(ctx, state, gamma, v, k, q):
+        n, d = state.shape[0], state.shape[1]
+        per_channel = gamma.dim() == 2
+        new = state.clone()
+        y = decode_step(new.view(n, 1, 1, d, d, 2), q.view(n, 1, d, 2), k.view(n, 1, d, 2), v.view(n, 1, d, 2),
+                        gamma.view(n, 1, 1, d) if per_channel else gamma.view(n, 1, 1), q_scale=1.0)
+        ctx.save_for_backward(state, gamma, q, k, v)
+        return y.view(n, d, 2), new
+
+    @staticmethod
+    def backward(ctx, dy, dnew):
+        state, gamma, q, k, v = ctx.saved_tensors
+        dy = dy.contiguous() if dy is not None else torch.zeros_like(q)
+        dnew = dnew.contiguous() if dnew is not None else None
+        dstate, dgamma = torch.empty_like(state), torch.empty_like(gamma)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        a = _lib.DecodeBwdArgs()
+        a.n, a.d, a.gamma_per_channel = state.shape[0], state.shape[1], int(gamma.dim() == 2)
+        a.state, a.gamma, a.q, a.k, a.v, a.dy = (t.data_ptr() for t in (state, gamma, q, k, v, dy))
+        a.dstate_new = dnew.data_ptr() if dnew is not None else None
+        a.dstate, a.dgamma, a.dq, a.dk, a.dv = (t.data_ptr() for t in (dstate, dgamma, dq, dk, dv))
+        with torch.cuda.device(state.device):
+            _lib.check(_lib.lib().qpam_decode_step_bwd(a, _lib.stream_ptr(state.device)), "qpam_decode_step_bwd")
+        return dstate, dgamma, dv, dk, dq
+
+
 def recur_step_additive(memory_state, decay_gamma, value_t, key_t, query_t):
     """Drop-in for V11PAMLayer._recur_step_additive (v11/model.py:927-965).
     memory_state [..., d, d, 2]; decay_gamma [...] (head decay) or [..., d]
     (per-channel decay, one per key column); value_t/key_t/query_t [..., d, 2]
     (query already scaled).  Returns (output [..., d, 2], new memory_state);
-    the input is not modified."""
+    the input is not modified.  Differentiable in every input (the backward is
+    qpam_decode_step_bwd)."""
     per_channel = decay_gamma.dim() == memory_state.dim() - 2
     if not per_channel and decay_gamma.dim() != memory_state.dim() - 3:
         raise ValueError(f"decay_gamma must be [...] or [..., d] for a state {tuple(memory_state.shape)}")
     lead = memory_state.shape[:-3]
     d = memory_state.shape[-2]
-    new_state = memory_state.to(torch.float32).contiguous().clone().view(-1, 1, 1, d, d, 2)
-    n = new_state.shape[0]
-
-    def flat(t):
-        return t.to(torch.float32).contiguous().view(n, 1, d, 2)
-
-    gam = decay_gamma.to(torch.float32).contiguous()
-    gam = gam.view(n, 1, 1, d) if per_channel else gam.view(n, 1, 1)
-    y = decode_step(new_state, flat(query_t), flat(key_t), flat(value_t), gam, q_scale=1.0)
+    n = memory_state[..., 0, 0, 0].numel()
+    f32 = lambda t, *shape: t.to(torch.float32).contiguous().view(n, *shape)  # noqa: E731
+    y, new_state = _DecodeStep.apply(f32(memory_state, d, d, 2), f32(decay_gamma, d) if per_channel else f32(decay_gamma),
+                                     f32(value_t, d, 2), f32(key_t, d, 2), f32(query_t, d, 2))
     return (y.view(*lead, d, 2).to(memory_state.dtype),
             new_state.view(*lead, d, d, 2).to(memory_state.dtype))
 

@@ -33,9 +33,6 @@ and every replacement hands a call to the saved method when the kernels do
 not cover it, so the installed layer computes what the reference computes in
 every mode:
   * CPU tensors (the reference computes on CPU through its torch code);
-  * decode steps whose inputs need gradients (a T = 1 forward in training, a
-    state-carrying call under grad mode): the reference step is differentiable
-    torch code, the HIP decode step updates the state in place;
   * the E2 delta write with head dims above 64 (its key dim is one 64-wide
     tile; smaller head dims are zero-padded).
 The HIP library itself has no CPU path: the replacements raise for GPU
@@ -83,10 +80,6 @@ def _scan_covers(t, head_dim, n_states=1):
     state count: head dims below 64 are zero-padded, larger ones run as 64 x 64
     state blocks, states beyond 4 in groups)."""
     return t.is_cuda and head_dim >= 1 and n_states >= 1
-
-
-def _needs_grad(*ts):
-    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
 
 def dual_form_block(scaled_queries, keys, protected_values, decay_gamma, causal_mask=None):
@@ -192,12 +185,11 @@ def forward_chunked_perchannel(self, queries, keys, protected_values, decay_gamm
 
 def recur_step_additive(self, memory_state, decay_gamma, value_t, key_t, query_t):
     """V11PAMLayer._recur_step_additive: the HIP decode step for head or
-    per-channel decay (decay_gamma [...] or [..., d]) without gradients; inputs
-    that need gradients, CPU tensors and head dims outside 16/32/64/128 run the
-    saved reference step (v11/model.py:927-965, differentiable torch code)."""
+    per-channel decay (decay_gamma [...] or [..., d]), differentiable (the
+    backward is a HIP kernel as well); CPU tensors and head dims outside
+    16/32/64/128 run the saved reference step (v11/model.py:927-965)."""
     if (not memory_state.is_cuda or decay_gamma.dim() not in (memory_state.dim() - 3, memory_state.dim() - 2)
-            or memory_state.shape[-2] not in _DECODE_DIMS
-            or _needs_grad(memory_state, decay_gamma, value_t, key_t, query_t)):
+            or memory_state.shape[-2] not in _DECODE_DIMS):
         return _original(self, "_recur_step_additive")(self, memory_state, decay_gamma, value_t, key_t, query_t)
     return _decode.recur_step_additive(memory_state, decay_gamma, value_t, key_t, query_t)
 

@@ -263,3 +263,34 @@ def test_decode_per_channel_decay_matches_textbook_recurrence(gpu_lib, d, M, use
         assert _rel(got_y, O.from_complex(y_ref)) < REL
     for s in (0, 2):
         assert st[s].abs().max().item() == 0.0
+
+
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+@pytest.mark.parametrize("per_channel", [False, True])
+@pytest.mark.parametrize("with_dstate", [False, True])
+def test_decode_step_backward_matches_autograd(gpu_lib, d, per_channel, with_dstate):
+    """qpam_decode_step_bwd through recur_step_additive's autograd: the
+    gradients of the state, gamma, v, k and q for a loss on y (and on the new
+    state) equal float64 autograd of the oracle step (the reference's
+    _recur_step_additive restated) over [2, 3] (slot, head) rows."""
+    from qllm2_amd.decode import recur_step_additive
+    g = torch.Generator().manual_seed(500 + d + 7 * per_channel + with_dstate)
+    state = torch.randn(2, 3, d, d, 2, generator=g, dtype=torch.float64) * 0.1
+    gam = torch.sigmoid(torch.randn(*((2, 3, d) if per_channel else (2, 3)), generator=g, dtype=torch.float64) + 2)
+    v, k, q = (torch.randn(2, 3, d, 2, generator=g, dtype=torch.float64) for _ in range(3))
+    q = q * d ** -0.5
+    dy = torch.randn(2, 3, d, 2, generator=g, dtype=torch.float64)
+    ds = torch.randn(2, 3, d, d, 2, generator=g, dtype=torch.float64) * 0.1 if with_dstate else None
+    leaves_r = [t.clone().requires_grad_(True) for t in (state, gam, v, k, q)]
+    y_r, s_r = O.recur_step_additive(*leaves_r)
+    loss = (y_r * dy).sum() + ((s_r * ds).sum() if ds is not None else 0)
+    loss.backward()
+    leaves = [t.float().cuda().requires_grad_(True) for t in (state, gam, v, k, q)]
+    y, s = recur_step_additive(*leaves)
+    loss = (y * dy.float().cuda()).sum() + ((s * ds.float().cuda()).sum() if ds is not None else 0)
+    loss.backward()
+    torch.cuda.synchronize()
+    assert _rel(y.detach().cpu(), y_r.detach()) < REL
+    assert _rel(s.detach().cpu(), s_r.detach()) < REL
+    for name, a, b in zip(("state", "gamma", "v", "k", "q"), leaves, leaves_r):
+        assert _rel(a.grad.cpu(), b.grad) < REL, f"d{name} {_rel(a.grad.cpu(), b.grad):.2e}"

@@ -19,8 +19,9 @@ the shapes the kernels take in pieces (six states, head_dim 128 and 96):
     back (decode at head dims outside 16/32/64/128 runs the reference methods
     by design);
   * grad mode: a T = 1 step carrying a state (the reference's recurrent
-    branch, v11/model.py:830-832) and a prefill, every gradient (input, state,
-    each parameter) against float64 autograd of the oracle layer, rel <= 1e-4.
+    branch, v11/model.py:830-832; the decode step and its backward as HIP
+    kernels) and a prefill, every gradient (input, state, each parameter)
+    against float64 autograd of the oracle layer, rel <= 1e-4.
 """
 
 import collections
@@ -177,7 +178,11 @@ def test_installed_grad_mode_matches_oracle(installed, mode):
         return lambda y, s: (y * dyt).sum() + (s * s).sum()
 
     ra = _grads(ref, x[:, 33:34], 33, st_r, step_loss(dy[:, 33:34]))
+    calls = installed[1]
+    calls.clear()
     ga = _grads(gpu, x[:, 33:34].float().cuda(), 33, st_g, step_loss(dy[:, 33:34].float().cuda()))
+    if not mode.startswith("E2"):  # the additive step and its backward ran as HIP kernels
+        assert calls["_recur_step_additive"] == 0, f"{mode}: the reference step ran {calls['_recur_step_additive']} times"
     names = ["y", "state", "dx", "dstate"]
     for nm, a, b in zip(names, ga[:4], ra[:4]):
         assert _rel(a, b) < 1e-4, f"step {nm}: {_rel(a, b):.2e}"

@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--only", choices=["scan_fwd", "decode", "decode_e3", "engine", "model", "e3", "ce", "cplx", "layer",
-                                       "delta", "delta_ref", "copy"], default=None,
+                                       "delta", "delta_ref", "e1", "copy"], default=None,
                     help="run one workload (for profiler passes) and print its own JSON line")
     return ap.parse_args()
 
@@ -754,6 +754,87 @@ def bench_delta(steps, warmup, reference=True):
     return out
 
 
+def _perchannel_reference_steps(q, k, v, gamma, d, chunk):
+    """The reference's E1 chunked prefill (v11/model.py:421-489) as torch steps
+    on the GPU, for timing against the kernels: per chunk the decay fold, the
+    masked score, its read of V, the carried read and the state write.
+    Interleaved complex inputs [B,H,T,d,2], gamma [B,H,T,d]."""
+    import torch
+    B, H, T = q.shape[:3]
+    scale = d ** -0.5
+    st = q.new_zeros(B, H, d, d, 2)
+    outs = []
+    for c0 in range(0, T, chunk):
+        c1 = min(c0 + chunk, T)
+        n = c1 - c0
+        lg = torch.cumsum(torch.log(gamma[:, :, c0:c1].clamp_min(1e-6)), 2).clamp(min=-30.0)
+        a, inv, tail = torch.exp(lg), torch.exp(-lg), torch.exp(lg[:, :, -1:] - lg)
+        fq, fk = q[:, :, c0:c1] * (a * scale).unsqueeze(-1), k[:, :, c0:c1] * inv.unsqueeze(-1)
+        wr = fq[..., 0] @ fk[..., 0].transpose(-1, -2) + fq[..., 1] @ fk[..., 1].transpose(-1, -2)
+        wi = fq[..., 1] @ fk[..., 0].transpose(-1, -2) - fq[..., 0] @ fk[..., 1].transpose(-1, -2)
+        mask = torch.ones(n, n, device=q.device).tril()
+        wr, wi = wr * mask, wi * mask
+        vr, vi = v[:, :, c0:c1, :, 0], v[:, :, c0:c1, :, 1]
+        o_r, o_i = wr @ vr - wi @ vi, wr @ vi + wi @ vr
+        if c0 > 0:
+            sr, si = st[..., 0], st[..., 1]
+            o_r = o_r + fq[..., 0] @ sr.transpose(-1, -2) - fq[..., 1] @ si.transpose(-1, -2)
+            o_i = o_i + fq[..., 0] @ si.transpose(-1, -2) + fq[..., 1] @ sr.transpose(-1, -2)
+        outs.append(torch.stack([o_r, o_i], -1))
+        dk = k[:, :, c0:c1] * tail.unsqueeze(-1)
+        s_r = vr.transpose(-1, -2) @ dk[..., 0] + vi.transpose(-1, -2) @ dk[..., 1]
+        s_i = vi.transpose(-1, -2) @ dk[..., 0] - vr.transpose(-1, -2) @ dk[..., 1]
+        st = st * torch.exp(lg[:, :, -1])[:, :, None, :, None] + torch.stack([s_r, s_i], -1)
+    return torch.cat(outs, 2), st
+
+
+def bench_perchannel(steps, warmup, reference=True):
+    """E1 per-channel decay prefill forward + backward at the config-3 shape
+    (one state: B=8, T=2048, H=12, d=64, chunk 64, fp32): the HIP fold and
+    state-scan kernels around batched complex GEMMs against the reference's
+    per-chunk steps run in torch on the same GPU."""
+    import torch
+    from qllm2_amd.pam_perchannel import perchannel_chunked
+    B, H, T, d = 8, 12, 2048, 64
+    gen = torch.Generator(device="cuda").manual_seed(41)
+    q, k, v = (torch.randn(B, H, T, d, 2, device="cuda", generator=gen) * (2 * d) ** -0.5 for _ in range(3))
+    gamma = torch.sigmoid(torch.randn(B, H, T, d, device="cuda", generator=gen) + 3.0)
+    leaves = [x.requires_grad_(True) for x in (q, k, v, gamma)]
+    dy = torch.randn(B, H, T, d, 2, device="cuda", generator=gen)
+
+    def timed(fn, n):
+        for _ in range(min(warmup, n)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    def fused():
+        y, _ = perchannel_chunked(*leaves, d, 64)
+        torch.autograd.grad([y], leaves, [dy])
+
+    def fwd_only():
+        with torch.no_grad():
+            perchannel_chunked(q, k, v, gamma, d, 64)
+
+    def reference_steps():
+        y, _ = _perchannel_reference_steps(*leaves, d, 64)
+        torch.autograd.grad([y], leaves, [dy])
+
+    ms = timed(fused, steps)
+    out = {"config": "E1 per-channel decay, B=8 T=2048 H=12 d=64 chunk 64 fp32, fwd+bwd", "ms_fwd_bwd": ms,
+           "ms_fwd": timed(fwd_only, steps), "tokens_per_s": B * T / (ms * 1e-3)}
+    if reference:
+        out["reference_steps_ms_fwd_bwd"] = timed(reference_steps, max(2, steps // 5))
+        out["speedup"] = out["reference_steps_ms_fwd_bwd"] / ms
+    return out
+
+
 def _median_time(fn, reps):
     fn()
     ts = []
@@ -886,6 +967,7 @@ def main():
               "layer": lambda: bench_pam_layer(args.steps, args.warmup),
               "delta": lambda: bench_delta(args.steps, args.warmup, reference=False),
               "delta_ref": lambda: bench_delta(args.steps, args.warmup, reference="only"),
+              "e1": lambda: bench_perchannel(args.steps, args.warmup),
               "copy": copy_calibration}[args.only]
         print(json.dumps({"only": args.only, "result": fn()}), flush=True)
         return
@@ -931,7 +1013,8 @@ def main():
                          "ce_fwd_bwd_config5_fp32_master_e": bench_ce(max(3, args.steps // 4), 3, master_fp32=True),
                          "complex_elementwise": bench_complex_ops(max(3, args.steps // 2), 5),
                          "pam_layer_config3": bench_pam_layer(max(3, args.steps // 2), 5),
-                         "delta_e2_config3_shape": bench_delta(max(3, args.steps // 4), 1)}
+                         "delta_e2_config3_shape": bench_delta(max(3, args.steps // 4), 1),
+                         "perchannel_e1_config3_shape": bench_perchannel(max(3, args.steps // 4), 2)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline_scan()
         out["cpu_baselines"] = {"config3_e3_fwd_bwd": cpu_baseline_e3(), "config4_decode": cpu_baseline_decode(),

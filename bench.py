@@ -1000,15 +1000,14 @@ def main():
                            "mfma_fp32_frac": flops / (ms * 1e-3) / MFMA_FP32_PEAK},
     }
     if not args.no_extras:
-        out["extras"] = {"decode_config4": bench_decode(args.decode_steps),
+        # the north-star E3 step first, next to the headline scan, with the headline's step count
+        out["extras"] = {"e3_fwd_bwd_config3": bench_e3_fwd_bwd(args.steps, max(5, args.warmup)),
+                         "decode_config4": bench_decode(args.decode_steps),
                          "decode_e3_rope_slots": bench_decode_e3_rope(max(50, args.decode_steps // 5)),
                          "decode_engine_e3_16_layers": bench_engine(20, 5),
                          "decode_engine_e3_16_layers_graphs": bench_engine(20, 5, graphs=True),
                          "decode_engine_e3_16_layers_graphs_bf16": bench_engine(20, 5, graphs=True, dtype="bf16"),
                          "model_decode_16_blocks_bf16_graphs": bench_model_decode(20, 5),
-                         # five untimed warmup steps: after two, the first timed steps still run
-                         # slow (E3 0.69 vs 0.66 ms per step)
-                         "e3_fwd_bwd_config3": bench_e3_fwd_bwd(max(3, args.steps // 2), 5),
                          "ce_fwd_bwd_config5": bench_ce(max(3, args.steps // 4), 3),
                          "ce_fwd_bwd_config5_fp32_master_e": bench_ce(max(3, args.steps // 4), 3, master_fp32=True),
                          "complex_elementwise": bench_complex_ops(max(3, args.steps // 2), 5),

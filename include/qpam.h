@@ -141,6 +141,9 @@ typedef struct {
      * key channel j (contiguous), S[i][j] <- gamma[j] S[i][j] + v_i conj(k_j) --
      * the per-channel branch of _recur_step_additive (v11/model.py:952-954). */
     int32_t gamma_per_channel;
+    /* qpam_dtype of y (ABI 9): QPAM_F32, or QPAM_BF16 (rounded once from the fp32
+     * sums; `y` then points at bf16 elements with the same element strides) */
+    int32_t y_dtype;
 } qpam_decode_args;
 
 int qpam_decode_step(const qpam_decode_args *a, void *stream);

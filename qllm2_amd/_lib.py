@@ -40,7 +40,7 @@ class DecodeArgs(ctypes.Structure):
         ("rot", c_ptr), ("sr_slot", c_i64), ("sr_group", c_i64), ("sr_state", c_i64),
         ("y", c_ptr), ("sy_slot", c_i64), ("sy_group", c_i64),
         ("rope", c_ptr), ("pos", c_ptr), ("rope_len", c_i32), ("vec_by_rank", c_i32),
-        ("q_im", c_ptr), ("k_im", c_ptr), ("v_im", c_ptr), ("rot_im", c_ptr), ("gamma_per_channel", c_i32),
+        ("q_im", c_ptr), ("k_im", c_ptr), ("v_im", c_ptr), ("rot_im", c_ptr), ("gamma_per_channel", c_i32), ("y_dtype", c_i32),
     ]
 
 

@@ -82,6 +82,12 @@ __device__ __forceinline__ float2 lane_decay(const qpam_decode_args &a, int64_t 
     return make_float2(a.gamma[off + 2 * cp], a.gamma[off + 2 * cp + 1]);
 }
 
+// element `e` of the y row at `row` (element offset), fp32 or bf16
+__device__ __forceinline__ void store_y(const qpam_decode_args &a, int64_t row, int e, float v) {
+    if (a.y_dtype == QPAM_BF16) reinterpret_cast<unsigned short *>(a.y)[row + e] = f32_to_bf16(v);
+    else a.y[row + e] = v;
+}
+
 // q and k of the slot times rope[pos[slot]] (two complex features per float4)
 template <int D>
 __device__ __forceinline__ void apply_rope(const qpam_decode_args &a, int slot, int cp, float4 &qv, float4 &kv) {
@@ -171,12 +177,12 @@ __global__ void __launch_bounds__((DecodeShape<D, 512>::THREADS)) decode_single_
     int base, nv;
     halving_reduce<S::NV, S::PAIRS>(part, lane, base, nv);
     if ((lane & S::bfly_mask()) == 0) {
-        float *yp = a.y + vr * a.sy_slot + g * a.sy_group;
+        const int64_t yrow = vr * a.sy_slot + g * a.sy_group;
 #pragma unroll
         for (int j = 0; j < S::NV; ++j) {
             if (j < nv) {
                 const int vi = base + j;
-                yp[2 * ((vi >> 1) * S::ROWS_PER_IT + r0) + (vi & 1)] = part[j];
+                store_y(a, yrow, 2 * ((vi >> 1) * S::ROWS_PER_IT + r0) + (vi & 1), part[j]);
             }
         }
     }
@@ -247,12 +253,12 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
     int base, nv;
     halving_reduce<S::NV, S::PAIRS>(tot, lane, base, nv);
     if ((lane & S::bfly_mask()) == 0) {
-        float *yp = a.y + vr * a.sy_slot + g * a.sy_group;
+        const int64_t yrow = vr * a.sy_slot + g * a.sy_group;
 #pragma unroll
         for (int j = 0; j < S::NV; ++j) {
             if (j < nv) {
                 const int vi = base + j;
-                yp[2 * ((vi >> 1) * S::ROWS_PER_IT + r0) + (vi & 1)] = tot[j];
+                store_y(a, yrow, 2 * ((vi >> 1) * S::ROWS_PER_IT + r0) + (vi & 1), tot[j]);
             }
         }
     }
@@ -315,8 +321,13 @@ __global__ void __launch_bounds__((DecodeShape<D, general_threads<D>()>::THREADS
         __syncthreads();
     }
     if (tid < D) {
-        float *yp = a.y + vr * a.sy_slot + g * a.sy_group + 2 * tid;
-        *reinterpret_cast<float2 *>(yp) = make_float2(yacc_r, yacc_i);
+        const int64_t yrow = vr * a.sy_slot + g * a.sy_group;
+        if (a.y_dtype == QPAM_BF16) {
+            *reinterpret_cast<unsigned *>(reinterpret_cast<unsigned short *>(a.y) + yrow + 2 * tid) =
+                pack_bf16x2(yacc_r, yacc_i);
+        } else {
+            *reinterpret_cast<float2 *>(a.y + yrow + 2 * tid) = make_float2(yacc_r, yacc_i);
+        }
     }
 }
 
@@ -492,6 +503,7 @@ extern "C" int qpam_decode_step(const qpam_decode_args *a, void *stream) {
     QPAM_REQUIRE(a->rot_im == nullptr || a->rot != nullptr, "qpam_decode_step: rot_im without rot");
     QPAM_REQUIRE(a->gamma_per_channel == 0 || a->gamma_per_channel == 1,
                  "qpam_decode_step: gamma_per_channel must be 0 or 1");
+    QPAM_REQUIRE(a->y_dtype == QPAM_F32 || a->y_dtype == QPAM_BF16, "qpam_decode_step: y_dtype must be F32 or BF16");
     const bool planar = a->q_im != nullptr;
     QPAM_REQUIRE((a->k_im != nullptr) == planar && (a->v_im != nullptr) == planar,
                  "qpam_decode_step: q_im, k_im and v_im are all set (planar q, k, v) or all NULL");

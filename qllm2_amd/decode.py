@@ -39,6 +39,8 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     pos    int32 [S] per-slot positions: q and k of slot a are rotated by rope[pos[a]]
     compact False: R = S, row a of q, k, v, gamma, rot, y belongs to slot a
            True:  R = n, row i belongs to slot active[i] (the live batch of an engine)
+    out    optional y buffer [R, G, d, 2], fp32 or bf16 (the kernel rounds the fp32
+           sums once)
     Returns y [R, G, d, 2] (without `compact`, rows of unlisted slots are left
     as in `out` / zero).
     """
@@ -92,6 +94,9 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
             raise ValueError(f"rot must be [{rows},{n_groups},{n_states},2]")
         rot = rot if rot.stride(-1) == 1 else rot.contiguous()
     y = out if out is not None else torch.zeros(rows, n_groups, d, 2, device=state.device, dtype=torch.float32)
+    if y.dtype not in (torch.float32, torch.bfloat16) or tuple(y.shape) != (rows, n_groups, d, 2) \
+            or y.stride()[-2:] != (2, 1):
+        raise ValueError(f"out must be fp32 or bf16 [{rows},{n_groups},{d},2] with contiguous rows")
     if active is not None:
         if active.dtype != torch.int32:
             active = active.to(torch.int32)
@@ -122,6 +127,7 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
             a.rot_im = rot_im.data_ptr()
     a.y = y.data_ptr()
     a.sy_slot, a.sy_group = y.stride(0), y.stride(1)
+    a.y_dtype = _lib.QPAM_BF16 if y.dtype == torch.bfloat16 else _lib.QPAM_F32
     if rope is not None:
         if pos is None:
             raise ValueError("rope needs per-slot positions `pos`")

@@ -208,9 +208,10 @@ class DecodeEngine:
         if not layer.use_rope:
             raise NotImplementedError("DecodeEngine applies RoPE per slot; layers without RoPE are not supported")
         # every listed slot is live, so the kernel writes every row of y: no zero fill
+        # y in the GEMM dtype straight from the decode kernel (no conversion pass before o_proj)
         y = self.pool.step(layer_idx, q, k, v, g, slots, rot=r, q_scale=d ** -0.5, compact=True,
-                           out=torch.empty(n, h, d, 2, device=x.device, dtype=torch.float32))
-        return F.linear(y.view(n, 2 * h * d).to(self.dtype), w["w_out"], w["b_out"]).view(n, dim, 2)
+                           out=torch.empty(n, h, d, 2, device=x.device, dtype=self.dtype))
+        return F.linear(y.view(n, 2 * h * d), w["w_out"], w["b_out"]).view(n, dim, 2)
 
     def _layers(self, x, slots, between):
         for li in range(len(self.layers)):

@@ -294,3 +294,26 @@ def test_decode_step_backward_matches_autograd(gpu_lib, d, per_channel, with_dst
     assert _rel(s.detach().cpu(), s_r.detach()) < REL
     for name, a, b in zip(("state", "gamma", "v", "k", "q"), leaves, leaves_r):
         assert _rel(a.grad.cpu(), b.grad) < REL, f"d{name} {_rel(a.grad.cpu(), b.grad):.2e}"
+
+
+@pytest.mark.parametrize("d", [16, 64, 128])
+@pytest.mark.parametrize("M,use_rot", [(1, False), (3, True), (5, True)])
+def test_decode_bf16_output_equals_rounded_fp32(gpu_lib, d, M, use_rot):
+    """y written in bf16 by the kernel (y_dtype) equals the fp32 y of the same
+    step rounded to bf16, bit for bit, and the states agree exactly (single,
+    multi-state and general kernels)."""
+    from qllm2_amd.decode import decode_step
+    S, G = 5, 4
+    state, q, k, v, gamma, rot = _pool(S, G, M, d, 700 + d + M)
+    active = torch.tensor([4, 0, 2], dtype=torch.int32).cuda()
+    outs = []
+    for dt in (torch.float32, torch.bfloat16):
+        st = state.clone().cuda()
+        y = torch.empty(3, G, d, 2, device="cuda", dtype=dt)
+        decode_step(st, q[[4, 0, 2]].cuda(), k[[4, 0, 2]].cuda(), v[[4, 0, 2]].cuda(), gamma[[4, 0, 2]].cuda(),
+                    active=active, rot=rot[[4, 0, 2]].cuda() if use_rot else None, q_scale=d ** -0.5, out=y,
+                    compact=True)
+        outs.append((y, st))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[1][0], outs[0][0].to(torch.bfloat16))
+    assert torch.equal(outs[1][1], outs[0][1])

@@ -349,7 +349,7 @@ int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void *mag, cons
  * one call): out[r][g] = bias[g] + sum_j w[g][j] |z[r][j]| with
  * |z| = sqrt(re^2 + im^2 + 1e-8), z interleaved complex rows [rows][dim][2]
  * (dtype), w fp32 [G][dim] row-major, bias fp32 [G] or NULL, out [rows][ld_out]
- * (out_dtype).  dim <= 8192.  Inference only (no backward). */
+ * (out_dtype).  dim <= 4096.  Inference only (no backward). */
 int qpam_mag_linear(int32_t dtype, int32_t out_dtype, int64_t rows, int32_t dim, int32_t G, const void *z,
                     const float *w, const float *bias, void *out, int64_t ld_out, void *stream);
 

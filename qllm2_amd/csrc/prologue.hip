@@ -424,47 +424,72 @@ int validate_outputs(const qpam_prologue_args *a) {
 }
 
 
-// Gate logits from the magnitudes of the layer input, one block per row r:
+// Gate logits from the magnitudes of the layer input, one row per block:
 //   out[r][g] = bias[g] + sum_j w[g][j] |z[r][j]|,  |z| = sqrt(re^2 + im^2 + 1e-8)
-// (the protect gate and the phase projection both read cabs(x)).  The row's
+// (the protect gate and the phase projection both read cabs(x)).  The rows'
 // magnitudes go to LDS once; wave w takes output groups of MAG_G rows of w
-// (groups w, w + 4, ...), its lanes striding over j: per step of 64 columns the
-// MAG_G coalesced row loads are all in flight before any is used, then a
-// butterfly sum per output.  Decode-time shapes (a few hundred rows, G of tens,
-// dim of hundreds) make this a latency problem: a library GEMM of that shape
-// has only a few output tiles, and a loop that uses each load as it arrives
-// waits one L2 round trip per element step.
-constexpr int MAG_THREADS = 256, MAG_MAX_DIM = 8192, MAG_G = 16;
+// (groups w, w + 4, ...: the protect gate and an E3 phase projection, 12 + 36
+// outputs, are one group per wave), its lanes striding over j: per pass over
+// 12 x 64 columns (all of a 768-wide row) the 12 MAG_G coalesced loads of w
+// are all in flight before any is used; then a butterfly sum per output.
+// Decode-time shapes (a few hundred rows, G of tens, dim of hundreds) make
+// this a latency problem: a library GEMM of that shape has only a few output
+// tiles, and a loop that uses each load as it arrives waits one L2 round trip
+// per element step.  Measured at 192 rows x 48 outputs x 768: 45 us with one
+// load in flight per lane, 9.4 us with 48, 20.7 us with four rows per block
+// (a quarter of the blocks, each four times longer).
+constexpr int MAG_THREADS = 256, MAG_MAX_DIM = 4096, MAG_G = 12, MAG_U = 12, MAG_R = 1;
 template <typename T, typename To>
-__global__ void __launch_bounds__(MAG_THREADS) mag_linear_kernel(int dim, int G, const void *z, const float *w,
-                                                                 const float *bias, void *out, int64_t ld_out) {
-    __shared__ float mag[MAG_MAX_DIM];
-    const int64_t r = blockIdx.x;
+__global__ void __launch_bounds__(MAG_THREADS) mag_linear_kernel(int64_t rows, int dim, int G, const void *z,
+                                                                 const float *w, const float *bias, void *out,
+                                                                 int64_t ld_out) {
+    __shared__ float mag[MAG_R][MAG_MAX_DIM];
+    const int64_t r0 = (int64_t)blockIdx.x * MAG_R;
+    const int nr = (int)min((int64_t)MAG_R, rows - r0);
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-    for (int j = tid; j < dim; j += MAG_THREADS) {
-        const float a = Io<T>::load1(z, (r * dim + j) * 2), b = Io<T>::load1(z, (r * dim + j) * 2 + 1);
-        mag[j] = sqrtf(a * a + b * b + 1e-8f);
-    }
+    for (int rr = 0; rr < nr; ++rr)
+        for (int j = tid; j < dim; j += MAG_THREADS) {
+            const int64_t e = ((r0 + rr) * dim + j) * 2;
+            const float a = Io<T>::load1(z, e), b = Io<T>::load1(z, e + 1);
+            mag[rr][j] = sqrtf(a * a + b * b + 1e-8f);
+        }
     __syncthreads();
     for (int g0 = wv * MAG_G; g0 < G; g0 += (MAG_THREADS / 64) * MAG_G) {
-        float acc[MAG_G];
+        float acc[MAG_R][MAG_G];
 #pragma unroll
-        for (int k = 0; k < MAG_G; ++k) acc[k] = 0.f;
-        for (int j = lane; j < dim; j += 64) {
-            float wk[MAG_G];
+        for (int rr = 0; rr < MAG_R; ++rr)
 #pragma unroll
-            for (int k = 0; k < MAG_G; ++k) wk[k] = (g0 + k < G) ? w[(int64_t)(g0 + k) * dim + j] : 0.f;
-            const float m = mag[j];
+            for (int k = 0; k < MAG_G; ++k) acc[rr][k] = 0.f;
+        for (int j0 = lane; j0 < dim; j0 += 64 * MAG_U) {
+            float wk[MAG_U][MAG_G];
 #pragma unroll
-            for (int k = 0; k < MAG_G; ++k) acc[k] += wk[k] * m;
+            for (int u = 0; u < MAG_U; ++u)
+#pragma unroll
+                for (int k = 0; k < MAG_G; ++k) {
+                    const int j = j0 + 64 * u;
+                    wk[u][k] = (g0 + k < G && j < dim) ? w[(int64_t)(g0 + k) * dim + j] : 0.f;
+                }
+#pragma unroll
+            for (int u = 0; u < MAG_U; ++u) {
+                const int j = j0 + 64 * u;
+#pragma unroll
+                for (int rr = 0; rr < MAG_R; ++rr) {
+                    const float m = (j < dim && rr < nr) ? mag[rr][j] : 0.f;
+#pragma unroll
+                    for (int k = 0; k < MAG_G; ++k) acc[rr][k] += wk[u][k] * m;
+                }
+            }
         }
 #pragma unroll
-        for (int k = 0; k < MAG_G; ++k) {
-            float x = acc[k];
+        for (int rr = 0; rr < MAG_R; ++rr)
 #pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-            if (lane == 0 && g0 + k < G) Io<To>::store1(out, r * ld_out + g0 + k, x + (bias ? bias[g0 + k] : 0.f));
-        }
+            for (int k = 0; k < MAG_G; ++k) {
+                float x = acc[rr][k];
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+                if (lane == 0 && g0 + k < G && rr < nr)
+                    Io<To>::store1(out, (r0 + rr) * ld_out + g0 + k, x + (bias ? bias[g0 + k] : 0.f));
+            }
     }
 }
 }  // namespace
@@ -562,13 +587,15 @@ extern "C" int qpam_mag_linear(int32_t dtype, int32_t out_dtype, int64_t rows, i
     if (rows == 0) return QPAM_OK;
     QPAM_REQUIRE(z && w && out, "qpam_mag_linear: null z, w or out");
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)rows), block(MAG_THREADS);
+    const dim3 grid((unsigned)((rows + MAG_R - 1) / MAG_R)), block(MAG_THREADS);
     if (dtype == QPAM_F32) {
-        if (out_dtype == QPAM_F32) hipLaunchKernelGGL((mag_linear_kernel<float, float>), grid, block, 0, s, dim, G, z, w, bias, out, ld_out);
-        else hipLaunchKernelGGL((mag_linear_kernel<float, Bf16>), grid, block, 0, s, dim, G, z, w, bias, out, ld_out);
+        if (out_dtype == QPAM_F32)
+            hipLaunchKernelGGL((mag_linear_kernel<float, float>), grid, block, 0, s, rows, dim, G, z, w, bias, out, ld_out);
+        else hipLaunchKernelGGL((mag_linear_kernel<float, Bf16>), grid, block, 0, s, rows, dim, G, z, w, bias, out, ld_out);
     } else {
-        if (out_dtype == QPAM_F32) hipLaunchKernelGGL((mag_linear_kernel<Bf16, float>), grid, block, 0, s, dim, G, z, w, bias, out, ld_out);
-        else hipLaunchKernelGGL((mag_linear_kernel<Bf16, Bf16>), grid, block, 0, s, dim, G, z, w, bias, out, ld_out);
+        if (out_dtype == QPAM_F32)
+            hipLaunchKernelGGL((mag_linear_kernel<Bf16, float>), grid, block, 0, s, rows, dim, G, z, w, bias, out, ld_out);
+        else hipLaunchKernelGGL((mag_linear_kernel<Bf16, Bf16>), grid, block, 0, s, rows, dim, G, z, w, bias, out, ld_out);
     }
     return launch_status("mag_linear_kernel");
 }

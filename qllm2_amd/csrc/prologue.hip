@@ -11,9 +11,8 @@
 // the scan's planar [B,H,T,d] operands, the decays and the rotations.
 //
 // Layout: one block of 4 waves per (b, h, 64 consecutive tokens); the
-// operand planes are written with non-temporal stores (read next by other
-// kernels, not by this one: keeping them out of the caches measured 25% faster
-// than ordinary stores, which compete with the projection reads).  The per-token
+// operand planes are written with ordinary stores (see Element I/O below for
+// why not non-temporal ones).  The per-token
 // scalars (decays of the M states, protect gate, rotations) take one thread per
 // (state, token), so their [M,B,H,T] rows are written as 256-byte runs.  For
 // the vectors a token row of d = 64 complex elements is one DPP row of 16 lanes

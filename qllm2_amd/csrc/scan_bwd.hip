@@ -54,6 +54,7 @@ struct BwdParams {
     // bf16 path: entering states (forward snapshots) and dS after each chunk, bf16
     const unsigned short *snap;
     unsigned short *gsnap;
+    const float *wgr, *wgi;  // bf16 path: the forward's per-step weights conj(rho_m[t]) q_scale
     int dy_bf16;             // dy planes are bf16 (bf16 path only)
 };
 
@@ -862,11 +863,13 @@ using U16 = unsigned short;
 // tiles are loaded once for all states: per chunk, every state's bf16 snapshot
 // of dS after the chunk, then dS_m <- total_m dS_m + sum_t conj(rho_m[t]) q_scale
 // dY_t (x) conj(q_t) on MFMA.  dS0 is written when requested.  Chunk c-2's dY, Q,
-// gammas, rotations and totals are loaded while chunk c is processed (two register
-// sets).  Every wave forms the chunk's weights conj(rho_m[t]) q_scale itself, and
-// dY is staged once per state already weighted (fp32 product rounded once to
-// bf16), so the MFMA operands come straight from LDS.  Rows past the end of the
-// sequence re-read its last row: their weights are zero.
+// per-step weights and totals are loaded while chunk c is processed (two register
+// sets).  The weights conj(rho_m[t]) q_scale come from the forward's per-step
+// table (seg_decay forms them beside its decay prefixes: formed here, the
+// chunk's log-prefix scan and the cross-lane moves of its weights were 40 % of
+// every step of this sequential pass), and dY is staged once per state already
+// weighted (fp32 product rounded once to bf16), so the MFMA operands come
+// straight from LDS.  Rows past the end of the sequence carry zero weights.
 constexpr int GSNAP_ROWS = 64 / PASS_SPLIT;  // dS rows of one block
 constexpr int GPASS_THREADS = 512;
 template <int M>
@@ -899,12 +902,6 @@ __global__ void __launch_bounds__(GPASS_THREADS) grad_pass_bf16_kernel(BwdParams
     const YT *yre = (const YT *)p.dy.re + b * p.dy.s0 + h * p.dy.s1;
     const YT *yim = (const YT *)p.dy.im + b * p.dy.s0 + h * p.dy.s1;
     const bool need_ds0 = p.ds0_re != nullptr;
-    const bool has_rot = a.rot_re != nullptr;
-    // rotations are read from gamma when absent (and replaced by 1 + 0i when staged):
-    // the same memory operations on every path
-    const float *rsrc_r = has_rot ? a.rot_re : a.gamma, *rsrc_i = has_rot ? a.rot_im : a.gamma;
-    const int64_t rs_m = has_rot ? a.sr_m : a.sg_m, rs_b = has_rot ? a.sr_b : a.sg_b, rs_h = has_rot ? a.sr_h : a.sg_h,
-                  rs_t = has_rot ? a.sr_t : a.sg_t;
 
     floatx4 gR[M], gI[M];  // dS_m[i][j], rows 16it + 4g + r, cols 16jt + l16
 #pragma unroll
@@ -926,10 +923,13 @@ __global__ void __launch_bounds__(GPASS_THREADS) grad_pass_bf16_kernel(BwdParams
     constexpr int YNT = DYBF ? 256 : NT;
     const int ytid = tid & (YNT - 1);
     using YRegs = typename std::conditional<DYBF, BfTileRegs<YNT, 32>, F32TileRegs<YNT, 32>>::type;
+    // the dY row this thread stages (one 16-byte piece per plane; the weights
+    // of that row, conj(rho_m[t]) q_scale, come from the forward's per-step table)
+    const int wrow = DYBF ? (ytid >> 2) : (ytid / 8);
     struct ChunkRegs {
         YRegs yr, yi;
         BfTileRegs<NT> qr, qi;
-        float gam[M], rr[M], ri[M], tot[M];
+        float wr[M], wi[M], tot[M];
     };
     ChunkRegs cr0, cr1;
     float tot_cur[M];  // total decays of the chunk staged last (the one the next step processes)
@@ -949,13 +949,12 @@ __global__ void __launch_bounds__(GPASS_THREADS) grad_pass_bf16_kernel(BwdParams
         const int64_t qo = (int64_t)c0 * a.q.s2;
         tile_load_bf<NT>(x.qr, qre + qo, a.q.s2, valid);
         tile_load_bf<NT>(x.qi, qim + qo, a.q.s2, valid);
-        const int64_t t = c0 + min(lane, valid - 1);
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            x.gam[m] = a.gamma[m * a.sg_m + b * a.sg_b + h * a.sg_h + t * a.sg_t];
-            const int64_t ro = m * rs_m + b * rs_b + h * rs_h + t * rs_t;
-            x.rr[m] = rsrc_r[ro];
-            x.ri[m] = rsrc_i[ro];
+            // rows past the end of the sequence carry the forward's zero weights
+            const int64_t wo = chain_idx(p, m, b, h) * p.n_chunks * 64 + c0 + wrow;
+            x.wr[m] = p.wgr[wo];
+            x.wi[m] = p.wgi[wo];
             // a vector load (lane-dependent address; lane 0's value is taken when the
             // chunk is staged): a scalar load would share the LDS counter, and the next
             // LDS wait would wait for it too
@@ -976,25 +975,21 @@ __global__ void __launch_bounds__(GPASS_THREADS) grad_pass_bf16_kernel(BwdParams
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             if (DYBF && (tid >> 8) != (m & 1)) continue;  // (bf16: the other half stages state m)
-            // conj(rho_m[t]) q_scale = conj(r_m[t]) cum_m[t] q_scale, lane t
-            float L = (lane < valid) ? logf(x.gam[m] + LOG_EPS) : 0.f;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const float y = __shfl_up(L, off);
-                if (lane >= off) L += y;
-            }
-            const float cum = (lane < valid) ? __expf(L) * a.q_scale : 0.f;
-            const float wr = (has_rot ? x.rr[m] : 1.f) * cum, wi = -(has_rot ? x.ri[m] : 0.f) * cum;
+            // row wrow of dY times conj(rho_m[t]) q_scale, rounded once to bf16
+            const float wr = x.wr[m], wi = x.wi[m];
             U16 *gr = sG + 2 * m * PLANE_B, *gi = gr + PLANE_B;
             if constexpr (DYBF) {
-                const int r = ytid >> 2, o = r * PB + yc0 + 8 * (ytid & 3);
-                const float wr_ = __shfl(wr, r), wi_ = __shfl(wi, r);
+                const int o = wrow * PB + yc0 + 8 * (ytid & 3);
                 const floatx8 ya = to_f(__builtin_bit_cast(bf16x8, x.yr.v[0]));
                 const floatx8 yb = to_f(__builtin_bit_cast(bf16x8, x.yi.v[0]));
-                *reinterpret_cast<bf16x8 *>(gr + o) = to_bf(wr_ * ya - wi_ * yb);
-                *reinterpret_cast<bf16x8 *>(gi + o) = to_bf(wr_ * yb + wi_ * ya);
+                *reinterpret_cast<bf16x8 *>(gr + o) = to_bf(wr * ya - wi * yb);
+                *reinterpret_cast<bf16x8 *>(gi + o) = to_bf(wr * yb + wi * ya);
             } else {
-                tile_store_f32_cmul_as_bf<YNT, 32>(gr, gi, x.yr, x.yi, wr, wi, yc0);
+                const int o = wrow * PB + yc0 + 4 * (ytid % 8);
+                const floatx4 ya = x.yr.v[0], yb = x.yi.v[0];
+                const floatx4 pr = wr * ya - wi * yb, pi = wr * yb + wi * ya;
+                *reinterpret_cast<uint2 *>(gr + o) = make_uint2(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]));
+                *reinterpret_cast<uint2 *>(gi + o) = make_uint2(pack_bf16x2(pi[0], pi[1]), pack_bf16x2(pi[2], pi[3]));
             }
         }
     };
@@ -1909,6 +1904,9 @@ int scan_bwd(const qpam_scan_bwd_args *bw, hipStream_t stream) {
     if (uses_snapshots(*a)) {
         p.snap = reinterpret_cast<const unsigned short *>((const char *)a->workspace + fwd_snapshot_offset(*a));
         p.gsnap = reinterpret_cast<unsigned short *>((char *)bw->workspace + bwd_snapshot_offset(*a));
+        const SegLayout l = seg_layout(*a);
+        p.wgr = (const float *)a->workspace + l.wgr;
+        p.wgi = (const float *)a->workspace + l.wgi;
         return launch_bwd_bf16(p, stream);
     }
     switch (a->C) {

@@ -266,7 +266,7 @@ constexpr int SEG_THREADS = 512;  // 8 waves per segment block
 // [chains][n_segs], weights wfwd and wbwd [chains][n * 64].
 struct SegLayout {
     int n_segs;
-    int64_t segtot, wfwd, wbwd;
+    int64_t segtot, wfwd, wbwd, wgr, wgi;
 };
 SegLayout seg_layout(const qpam_scan_args &a);
 // 64-row tiles of CW columns (64, or a 32-column half at column c0) held in
@@ -318,38 +318,6 @@ __device__ __forceinline__ void tile_load_f32(F32TileRegs<NT, CW> &t, const floa
         const int idx = threadIdx.x + i * NT;
         const int r = min(idx / (CW / 4), valid - 1), c4 = idx % (CW / 4);
         t.v[i] = *reinterpret_cast<const floatx4 *>(src + (int64_t)r * st + c0 + 4 * c4);
-    }
-}
-// A complex fp32 tile (two planes) times a per-row complex weight (lane r of the
-// calling wave holds row r's (w_re, w_im)) -> two bf16 planes, rounded once.
-template <int NT, int CW = 64>
-__device__ __forceinline__ void tile_store_f32_cmul_as_bf(unsigned short *lre, unsigned short *lim,
-                                                         const F32TileRegs<NT, CW> &xr, const F32TileRegs<NT, CW> &xi,
-                                                         float w_re, float w_im, int c0 = 0) {
-#pragma unroll
-    for (int i = 0; i < 16 * CW / NT; ++i) {
-        const int idx = threadIdx.x + i * NT, r = idx / (CW / 4);
-        const float wr = __shfl(w_re, r), wi = __shfl(w_im, r);
-        const floatx4 yr = wr * xr.v[i] - wi * xi.v[i], yi = wr * xi.v[i] + wi * xr.v[i];
-        const int o = r * PB + c0 + 4 * (idx % (CW / 4));
-        *reinterpret_cast<uint2 *>(lre + o) = make_uint2(pack_bf16x2(yr[0], yr[1]), pack_bf16x2(yr[2], yr[3]));
-        *reinterpret_cast<uint2 *>(lim + o) = make_uint2(pack_bf16x2(yi[0], yi[1]), pack_bf16x2(yi[2], yi[3]));
-    }
-}
-// The same product for a complex bf16 tile (two planes as loaded by tile_load_bf):
-// widened to fp32, multiplied, rounded once to bf16.
-template <int NT, int CW = 64>
-__device__ __forceinline__ void tile_store_bf_cmul_as_bf(unsigned short *lre, unsigned short *lim,
-                                                        const BfTileRegs<NT, CW> &xr, const BfTileRegs<NT, CW> &xi,
-                                                        float w_re, float w_im, int c0 = 0) {
-#pragma unroll
-    for (int i = 0; i < 8 * CW / NT; ++i) {
-        const int idx = threadIdx.x + i * NT, r = idx / (CW / 8);
-        const float wr = __shfl(w_re, r), wi = __shfl(w_im, r);
-        const floatx8 a = to_f(__builtin_bit_cast(bf16x8, xr.v[i])), b = to_f(__builtin_bit_cast(bf16x8, xi.v[i]));
-        const int o = r * PB + c0 + 8 * (idx % (CW / 8));
-        *reinterpret_cast<bf16x8 *>(lre + o) = to_bf(wr * a - wi * b);
-        *reinterpret_cast<bf16x8 *>(lim + o) = to_bf(wr * b + wi * a);
     }
 }
 template <int NT>

@@ -42,6 +42,7 @@ struct FwdParams {
     float *segtot;  // [M][B][H][n_segs] decay total of each segment
     float *wfwd;    // [M][B][H][n*64] weight of step t in its segment's end state
     float *wbwd;    // [M][B][H][n*64] decay from its segment's start through step t
+    float *wgr, *wgi;  // [M][B][H][n*64] the backward's per-step weights conj(rho_m[t]) q_scale
 };
 
 __device__ __forceinline__ float *chunk_state_ptr(const FwdParams &p, int m, int b, int h, int c) {
@@ -814,6 +815,16 @@ __global__ void __launch_bounds__(THREADS) seg_decay_kernel(FwdParams p) {
         const int64_t o = chain * p.n_chunks * 64 + (int64_t)c * 64 + lane;
         p.wfwd[o] = lane < valid ? __expf(fminf(Llast - L, 0.f) + after) : 0.f;
         p.wbwd[o] = lane < valid ? __expf(L + before) : 0.f;
+        // the backward's weight of step t: conj(r_m[t]) e^{L_t} q_scale (L within the chunk)
+        const float cum = lane < valid ? __expf(L) * a.q_scale : 0.f;
+        float rr = 1.f, ri = 0.f;
+        if (a.rot_re && lane < valid) {
+            const int64_t ro = m * a.sr_m + b * a.sr_b + h * a.sr_h + (int64_t)(c * 64 + lane) * a.sr_t;
+            rr = a.rot_re[ro];
+            ri = a.rot_im[ro];
+        }
+        p.wgr[o] = rr * cum;
+        p.wgi[o] = -ri * cum;
         if (lane == 0) *chunk_total_ptr(p, m, b, h, c) = __expf(Llast);
     }
     if (threadIdx.x == 0) p.segtot[chain * p.n_segs + sg] = __expf(total);
@@ -1403,13 +1414,15 @@ SegLayout seg_layout(const qpam_scan_args &a) {
     l.segtot = fwd_totals_offset(a) + chains * n;
     l.wfwd = l.segtot + chains * n_segs;
     l.wbwd = l.wfwd + chains * n * 64;
+    l.wgr = l.wbwd + chains * n * 64;
+    l.wgi = l.wgr + chains * n * 64;
     return l;
 }
 
 size_t fwd_snapshot_offset(const qpam_scan_args &a) {
     const int64_t n = (a.T + a.C - 1) / a.C;
     const int64_t chains = (int64_t)a.M * a.B * a.H;
-    const int64_t floats = uses_snapshots(a) ? seg_layout(a).wbwd + chains * n * 64 : fwd_totals_offset(a) + chains * n;
+    const int64_t floats = uses_snapshots(a) ? seg_layout(a).wgi + chains * n * 64 : fwd_totals_offset(a) + chains * n;
     return ((size_t)floats * sizeof(float) + 255) & ~(size_t)255;
 }
 
@@ -1485,13 +1498,15 @@ int scan_fwd(const qpam_scan_args *a, hipStream_t stream) {
                  : nullptr;
     p.dlast = uses_dlast(*a) ? reinterpret_cast<float *>((char *)a->workspace + fwd_snapshot_offset(*a)) : nullptr;
     p.n_segs = 0;
-    p.segs = p.segtot = p.wfwd = p.wbwd = nullptr;
+    p.segs = p.segtot = p.wfwd = p.wbwd = p.wgr = p.wgi = nullptr;
     if (uses_snapshots(*a)) {
         const SegLayout l = seg_layout(*a);
         p.n_segs = l.n_segs;
         p.segtot = (float *)a->workspace + l.segtot;
         p.wfwd = (float *)a->workspace + l.wfwd;
         p.wbwd = (float *)a->workspace + l.wbwd;
+        p.wgr = (float *)a->workspace + l.wgr;
+        p.wgi = (float *)a->workspace + l.wgi;
         p.segs = reinterpret_cast<float *>((char *)a->workspace + fwd_segs_offset(*a));
     }
     QPAM_REQUIRE(p.n_chunks <= 65535 && a->H <= 65535 && a->B <= 65535, "qpam_scan_fwd: grid too large");

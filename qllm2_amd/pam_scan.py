@@ -174,7 +174,8 @@ def scan_fwd_op(q_re: Tensor, q_im: Tensor, k_re: Tensor, k_im: Tensor, v_re: Te
 def fwd_workspace_bytes(M, B, H, T, chunk, bf16, d=64):
     """Forward workspace size, as qpam_scan_workspace_size computes it: fp32
     per-chunk states (fp32 inputs) and chunk totals; with bf16 inputs and chunk
-    64 also the segment totals and two per-step segment weights, then at a
+    64 also the segment totals, two per-step segment weights and the backward's
+    per-step complex weights conj(rho_m[t]) q_scale, then at a
     256-byte aligned offset the bf16 snapshots of the entering states and the
     fp32 segment states; with fp32 inputs and chunk 64, at that offset the
     state pass's per-chunk decay weights."""
@@ -182,7 +183,7 @@ def fwd_workspace_bytes(M, B, H, T, chunk, bf16, d=64):
     snap = bf16 and chunk == 64
     if snap:
         n_segs = (n + SEG - 1) // SEG
-        floats = chains * n + chains * n_segs + 2 * chains * n * 64
+        floats = chains * n + chains * n_segs + 4 * chains * n * 64
         off = (floats * 4 + 255) & ~255
         return off + chains * n * 2 * d * d * 2 + chains * n_segs * 2 * d * d * 4
     off = ((chains * n * 2 * d * d + chains * n) * 4 + 255) & ~255

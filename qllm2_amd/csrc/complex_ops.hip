@@ -17,6 +17,7 @@
 // a [block][dim] partial, summed over blocks by a second kernel — deterministic,
 // no atomics.
 #include <algorithm>
+#include <mutex>
 
 #include "common.h"
 
@@ -562,7 +563,11 @@ __global__ void __launch_bounds__(THREADS) act_bwd_reg_kernel(Params p) {
 // with u = z / (|z| + eps) and gmag, dmag the gradients of the output magnitude
 // (the closed forms of the reference's autograd backward, v11/triton_kernels.py:209-345).
 constexpr int TEAM_MAX = 512;  // threads per row team (dim <= 2048)
-constexpr int TEAM_THREADS_TOTAL = 256 * 1024;  // resident threads the grid is sized for
+// The grid of a row-team kernel is the blocks that are resident at once (its
+// occupancy times the device's CUs: a grid beyond that runs a partly empty last
+// round), at most TEAM_RESIDENT_MAX threads, which the parameter-gradient
+// workspace is sized for.
+constexpr int64_t TEAM_RESIDENT_MAX = 256 * 2048;
 
 template <int R>
 __device__ __forceinline__ void team_row_sums(float (&a)[R], float (&b)[R], float *red) {
@@ -809,8 +814,38 @@ int team_threads(int dim) {
     return (t % 64 == 0 && t <= TEAM_MAX) ? t : 0;
 }
 constexpr int TEAM_ROWS_FWD = 4, TEAM_ROWS_NORM_BWD = 4, TEAM_ROWS_ACT_BWD = 2;
-int team_blocks(int64_t rows, int threads, int r) {
-    return (int)std::max<int64_t>(1, std::min<int64_t>((rows + r - 1) / r, TEAM_THREADS_TOTAL / threads));
+// blocks of R rows per iteration, at most TEAM_RESIDENT_MAX / threads (no kernel: the bound)
+int team_blocks(int64_t rows, int threads, int r, const void *kernel = nullptr) {
+    int64_t resident = TEAM_RESIDENT_MAX / threads;
+    if (kernel) {
+        // resident blocks per CU of (kernel, threads) on each device, looked up once
+        struct Entry {
+            const void *k;
+            int dev, threads, blocks;
+        };
+        static std::mutex mu;
+        static Entry cache[64];
+        static int n_cache = 0;
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return 0;
+        int per_cu = -1;
+        {
+            std::lock_guard<std::mutex> lock(mu);
+            for (int i = 0; i < n_cache; ++i)
+                if (cache[i].k == kernel && cache[i].dev == dev && cache[i].threads == threads) per_cu = cache[i].blocks;
+        }
+        if (per_cu < 0) {
+            int cus = 0, occ = 0;
+            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+                hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, threads, 0) != hipSuccess)
+                return 0;
+            per_cu = std::max(1, occ) * cus;
+            std::lock_guard<std::mutex> lock(mu);
+            if (n_cache < 64) cache[n_cache++] = Entry{kernel, dev, threads, per_cu};
+        }
+        resident = std::min<int64_t>(resident, per_cu);
+    }
+    return (int)std::max<int64_t>(1, std::min<int64_t>((rows + r - 1) / r, resident));
 }
 
 template <typename T, int OP>
@@ -858,8 +893,10 @@ int fwd(const qpam_cplx_args *a, hipStream_t stream) {
         case QPAM_CPLX_NORM:
             if (V == 4 && team_threads(a->dim)) {
                 const int tt = team_threads(a->dim);
-                hipLaunchKernelGGL((norm_fwd_team_kernel<T, TEAM_ROWS_FWD>), dim3(team_blocks(a->rows, tt, TEAM_ROWS_FWD)),
-                                   dim3(tt), 0, stream, p);
+                const void *k = (const void *)norm_fwd_team_kernel<T, TEAM_ROWS_FWD>;
+                const int tb = team_blocks(a->rows, tt, TEAM_ROWS_FWD, k);
+                if (tb == 0) return fail(QPAM_ERR_HIP, "qpam_cplx_fwd: occupancy query failed");
+                hipLaunchKernelGGL((norm_fwd_team_kernel<T, TEAM_ROWS_FWD>), dim3(tb), dim3(tt), 0, stream, p);
                 break;
             }
             if (V == 4 && reg_groups(a->dim)) {
@@ -897,7 +934,11 @@ int bwd(const qpam_cplx_args *a, hipStream_t stream) {
     if (V == 4 && team_threads(a->dim) && a->op != QPAM_CPLX_CGU_GATE) {
         const int tt = team_threads(a->dim);
         const int rr = a->op == QPAM_CPLX_NORM ? TEAM_ROWS_NORM_BWD : TEAM_ROWS_ACT_BWD;
-        const int tb = team_blocks(a->rows, tt, rr);
+        const void *k = a->op == QPAM_CPLX_NORM ? (const void *)bwd_team_kernel<T, TEAM_ROWS_NORM_BWD, 0>
+                        : a->op == QPAM_CPLX_MOD_SWISH ? (const void *)bwd_team_kernel<T, TEAM_ROWS_ACT_BWD, 1>
+                                                       : (const void *)bwd_team_kernel<T, TEAM_ROWS_ACT_BWD, 2>;
+        const int tb = team_blocks(a->rows, tt, rr, k);
+        if (tb == 0) return fail(QPAM_ERR_HIP, "qpam_cplx_bwd: occupancy query failed");
         if (a->op == QPAM_CPLX_NORM)
             hipLaunchKernelGGL((bwd_team_kernel<T, TEAM_ROWS_NORM_BWD, 0>), dim3(tb), dim3(tt), 0, stream, p);
         else if (a->op == QPAM_CPLX_MOD_SWISH)

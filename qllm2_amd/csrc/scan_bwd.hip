@@ -1178,8 +1178,7 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
     const bool carry = (c > 0) || (a.s0_re != nullptr);
     const float qs = a.q_scale;
-    // global loads first: decay inputs of state m = w, the Q, K, V, dY tiles and
-    // the state-0 snapshots
+    // global loads first: decay inputs of state m = w and the Q, K, V, dY tiles
     DecayIn din;
     if (w < M) din = decay_load(a, w, b, h, c0, valid);
     const int tt = causal_tile(w), st = tt;  // query tile and key tile of this wave
@@ -1218,7 +1217,6 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
             regs_load_f32<false>(rf[0], (const float *)p.dy.re + go, p.dy.s2, valid);
             regs_load_f32<false>(rf[1], (const float *)p.dy.im + go, p.dy.s2, valid);
         }
-        load_state(0);
         if (w < M) {
             const bool ok = decay_tables(din, w, valid, sL, sRr, sRi, sF, sPr, sPi);
             if (lane == 0) sFast[w] = ok ? 1 : 0;
@@ -1235,6 +1233,10 @@ __global__ void __launch_bounds__(THREADS, 2) chunk_grad_bf16_kernel(BwdParams p
         }
     }
     __syncthreads();
+    // state 0's snapshots are first read after the score phases: issued here,
+    // they do not add to the staging wait (every block of a round loads its
+    // tiles at once, so the entry is bandwidth-bound)
+    load_state(0);
 
     bool fast = true;
 #pragma unroll

@@ -55,6 +55,10 @@
  *   qpam_delta_bwd      their autograd backward
  *   qpam_cabs_fwd/_bwd  cabs (v11/complex_ops.py:86-87) feeding the gate and
  *                       phase projections (v11/model.py:228, 646)
+ *   qpam_cweight_pack   ComplexLinear's weights (v11/complex_ops.py:146-172)
+ *                       as the real operand of one GEMM: the layer's qkv_proj
+ *                       with dt_proj (v11/model.py:280, 636) and o_proj (:836)
+ *   qpam_cweight_unpack its backward (the weights' gradients)
  */
 #ifndef QPAM_H
 #define QPAM_H
@@ -343,6 +347,45 @@ int qpam_prologue_bwd(const qpam_prologue_bwd_args *a, void *stream);
  * gz[i] = gmag[i] z[i] / mag[i]. */
 int qpam_cabs_fwd(int32_t dtype, int64_t n, const void *z, void *mag, void *stream);
 int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void *mag, const void *gmag, void *gz, void *stream);
+
+/* Complex linear weights as one real GEMM operand (ComplexLinear,
+ * v11/complex_ops.py:146-172: re = Wr xr - Wi xi, im = Wi xr + Wr xi; the PAM
+ * layer's qkv_proj and dt_proj, v11/model.py:280, 636, and o_proj, :836).
+ * wr, wi [R][C] (row-major, contiguous) make W, with p the output part and q
+ * the input part (0 = re, 1 = im) and the value wr, -wi, wi, wr at
+ * (p, q) = (0,0), (0,1), (1,0), (1,1):
+ *   QPAM_CW_IN  W[p R + r][2 c + q]  (interleaved input, outputs as a real then
+ *               an imaginary block; C a multiple of 4), followed by tail_rows
+ *               real rows W[2R + h][2 c + q] = tail[h][q C + c] (an nn.Linear
+ *               over [xr | xi] reordered to the interleaved input) and
+ *               zero_rows rows of zeros;
+ *   QPAM_CW_OUT W[2 r + p][q C + c]  (input as two blocks, interleaved outputs;
+ *               C a multiple of 8, no tail or zero rows).
+ * W rows are ldw elements apart (ldw >= 2C, a multiple of 8); W, wr, wi, tail in
+ * `dtype`; every pointer 16-byte aligned.
+ * qpam_cweight_unpack is the backward: the gradient of W is the sum of `slices`
+ * W-shaped matrices in g (g_dtype, slice_stride elements apart, summed in fp32
+ * in slice order, e.g. the per-slice products of a row-sliced g^T x); it writes
+ * g_wr, g_wi [R][C] and g_tail [tail_rows][2C] in `dtype`. */
+enum { QPAM_CW_IN = 0, QPAM_CW_OUT = 1 };
+typedef struct {
+    int32_t dtype;
+    int32_t layout;
+    int64_t R, C;
+    const void *wr, *wi;
+    const void *tail;
+    int64_t tail_rows, zero_rows;
+    void *w;
+    int64_t ldw;
+    const void *g;
+    int32_t g_dtype;
+    int32_t slices;
+    int64_t slice_stride;
+    void *g_wr, *g_wi, *g_tail;
+} qpam_cweight_args;
+
+int qpam_cweight_pack(const qpam_cweight_args *a, void *stream);
+int qpam_cweight_unpack(const qpam_cweight_args *a, void *stream);
 
 /* Gate logits of the decode step from |x| (v11/model.py:228, 646: protect_gate
  * and phase_proj applied to cabs(x), two nn.Linear on the same magnitudes, in

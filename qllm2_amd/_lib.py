@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -192,6 +192,17 @@ class PcScanArgs(ctypes.Structure):
     ]
 
 
+class CWeightArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", c_i32), ("layout", c_i32), ("R", c_i64), ("C", c_i64), ("wr", c_ptr), ("wi", c_ptr),
+        ("tail", c_ptr), ("tail_rows", c_i64), ("zero_rows", c_i64), ("w", c_ptr), ("ldw", c_i64),
+        ("g", c_ptr), ("g_dtype", c_i32), ("slices", c_i32), ("slice_stride", c_i64),
+        ("g_wr", c_ptr), ("g_wi", c_ptr), ("g_tail", c_ptr),
+    ]
+
+
+QPAM_CW_IN, QPAM_CW_OUT = 0, 1
+
 SIGNATURES = {
     "qpam_version": (ctypes.c_int, []),
     "qpam_last_error": (ctypes.c_char_p, []),
@@ -226,6 +237,8 @@ SIGNATURES = {
     "qpam_pc_fold_fwd": (ctypes.c_int, [ctypes.POINTER(PcFoldArgs), c_ptr]),
     "qpam_pc_fold_bwd": (ctypes.c_int, [ctypes.POINTER(PcFoldArgs), c_ptr]),
     "qpam_pc_scan": (ctypes.c_int, [ctypes.POINTER(PcScanArgs), c_ptr]),
+    "qpam_cweight_pack": (ctypes.c_int, [ctypes.POINTER(CWeightArgs), c_ptr]),
+    "qpam_cweight_unpack": (ctypes.c_int, [ctypes.POINTER(CWeightArgs), c_ptr]),
 }
 
 _LIB = None

@@ -45,7 +45,9 @@ import sys
 import torch
 import torch.nn.functional as F
 
+from . import _lib
 from . import _reference
+from . import cproj as _cproj
 from . import decode as _decode
 from . import pam_delta as _delta
 from . import fused_ce as _fused_ce
@@ -263,6 +265,22 @@ def _in_weight(self, h, d, cols):
     return w, torch.cat([br, bi, wr.new_zeros(h + pad)])
 
 
+def _packed_in(self, x2, h, cols):
+    """proj [B,T,cols] from the packed input projection (qkv_proj, or q/k/v_proj,
+    and dt_proj's logits without its bias in one GEMM, the weight packed and its
+    gradient split on the HIP library), or None where that path does not apply
+    (projection biases, mixed dtypes, autocast)."""
+    mods = [self.qkv_proj] if self.fused_qkv else [self.q_proj, self.k_proj, self.v_proj]
+    if any(getattr(m, "bias_real", None) is not None or getattr(m, "bias_imag", None) is not None for m in mods):
+        return None
+    wr = torch.cat([m.weight_real for m in mods], 0) if len(mods) > 1 else mods[0].weight_real
+    wi = torch.cat([m.weight_imag for m in mods], 0) if len(mods) > 1 else mods[0].weight_imag
+    tail = self.dt_proj.weight
+    if tail.shape != (h, x2.shape[-1]) or not _cproj.supported(x2, wr, wi, tail, layout=_lib.QPAM_CW_IN):
+        return None
+    return _cproj.linear_in(x2, wr, wi, tail, cols)
+
+
 def _out_weight(mod):
     """Weight [2 dim, 2 inner] (and bias) of the o_proj GEMM from the
     per-token [y_re | y_im] planes to the interleaved output (re_o, im_o)."""
@@ -348,8 +366,10 @@ def forward(self, x, state=None, step_offset: int = 0):
     n = b * t
     xc = x if x.is_contiguous() else x.contiguous()
     cols = proj_columns(h)
-    w_in, b_in = _in_weight(self, h, d, cols)
-    proj = F.linear(xc.view(b, t, 2 * dim), w_in, b_in)                 # [B,T,cols]
+    proj = _packed_in(self, xc.view(b, t, 2 * dim), h, cols)
+    if proj is None:
+        w_in, b_in = _in_weight(self, h, d, cols)
+        proj = F.linear(xc.view(b, t, 2 * dim), w_in, b_in)             # [B,T,cols]
     if proj.dtype not in (torch.float32, torch.bfloat16):
         proj = proj.float()
     rope = None
@@ -394,17 +414,22 @@ def forward(self, x, state=None, step_offset: int = 0):
         proj, dt_bias, n_heads=h, n_states=m, state_offset=offsets, protect=protect, phase=phase,
         routing=routing, rope=rope, rope_offset=step_offset, qk_norm=self.qk_norm,
         gamma_floor=self.gamma_floor or 0.0)
-    w_out, b_out = _out_weight(self.o_proj)
+    o_dtype = self.o_proj.weight_real.dtype
     ck = chunk_for(self.chunk_size, t)
     # bf16 o_proj: the scan writes Y in bf16 itself (and reads its gradient in bf16)
-    y_bf16 = (qr.dtype == torch.bfloat16 and ck == 64 and w_out.dtype == torch.bfloat16
+    y_bf16 = (qr.dtype == torch.bfloat16 and ck == 64 and o_dtype == torch.bfloat16
               and not torch.is_autocast_enabled())
     y, _, s_re, s_im = pam_scan_planar(qr, qi, kr, ki, vr, vi, gamma, q_scale=d ** -0.5, chunk=ck, rot=rot,
                                        y_layout="bt2hd_bf16" if y_bf16 else "bt2hd")
     y = y.view(b, t, 2 * h * d)
-    if w_out.dtype != torch.float32 and not torch.is_autocast_enabled():
-        y = y.to(w_out.dtype)
-    out = _linear_tall_k(y, w_out, b_out).view(b, t, dim, 2)
+    if o_dtype != torch.float32 and not torch.is_autocast_enabled():
+        y = y.to(o_dtype)
+    wr_o, wi_o = self.o_proj.weight_real, self.o_proj.weight_imag
+    if getattr(self.o_proj, "bias_real", None) is None and _cproj.supported(y, wr_o, wi_o, layout=_lib.QPAM_CW_OUT):
+        out = _cproj.linear_out(y, wr_o, wi_o).view(b, t, dim, 2)
+    else:
+        w_out, b_out = _out_weight(self.o_proj)
+        out = _linear_tall_k(y, w_out, b_out).view(b, t, dim, 2)
     if self.training:
         # one keep-mask per complex value (as_complex_dropout_mask, v11/complex_ops.py:59-66)
         mask = self.dropout(torch.ones(out.shape[:-1], device=out.device, dtype=out.dtype))

@@ -616,8 +616,8 @@ def bench_pam_layer(steps, warmup):
         mag = torch.sqrt(x.detach().square().sum(-1) + 1e-8)
         prot = m.protect_gate(mag)
         phase = m.phase_proj(mag).view(B, T, H, M)
-    args = (proj, prot, phase, None, m.dt_bias.detach().float(), m.state_dt_offset.detach().float(), m.rope_cache,
-            H, M, 0, False, 0.0)
+    args = (proj, prot, phase, None, m.dt_bias.detach().float(), None, m.state_dt_offset.detach().float(),
+            m.rope_cache, H, M, 0, False, 0.0, None, -1, -1)
     outs = PP.prologue_fwd_op(*args)
     grads = [torch.randn_like(o) if o.numel() else o for o in outs]
     plane = B * T * H * d * 2                  # bytes of one bf16 plane
@@ -626,8 +626,8 @@ def bench_pam_layer(steps, warmup):
     # forward: 6 projection planes in, 6 operand planes out; dt, protect, M phases in (bf16); gamma, rot out (fp32)
     fwd_bytes = 12 * plane + (2 + M) * tok2 + 3 * M * tok
     # backward: 6 gradient planes and the 2 v planes in, 6 projection-gradient planes out; the logits in again;
-    # dgamma, drot in; dpre, dphase, dprotect out (fp32), ddt out (bf16)
-    bwd_bytes = 14 * plane + (2 + M) * tok2 + 3 * M * tok + (2 * M + 1) * tok + tok2
+    # dgamma, drot in; dphase, dprotect, ddt out (bf16); the bias gradients as per-block partial sums
+    bwd_bytes = 14 * plane + (2 + M) * tok2 + 3 * M * tok + (M + 2) * tok2
     for name, fn, nbytes in (("prologue_fwd", lambda: PP.prologue_fwd_op(*args), fwd_bytes),
                              ("prologue_bwd", lambda: PP.prologue_bwd_op(*args, grads), bwd_bytes)):
         for _ in range(3):

@@ -59,6 +59,8 @@
  *                       as the real operand of one GEMM: the layer's qkv_proj
  *                       with dt_proj (v11/model.py:280, 636) and o_proj (:836)
  *   qpam_cweight_unpack its backward (the weights' gradients)
+ *   qpam_slice_sum      the gate projections' weight gradient (v11/model.py:228,
+ *                       646) summed over row slices and cast
  */
 #ifndef QPAM_H
 #define QPAM_H
@@ -274,7 +276,7 @@ int qpam_decay_matrix(int32_t n, int32_t t, const float *gamma, int64_t ldg, flo
  * One pass from the layer's projections to the scan's inputs:
  *   q' = nrm(q * rope[rope_offset + t]),  k' = nrm(k * rope[rope_offset + t])
  *   p  = sigmoid(protect[b,t,h])                     (GSP; p = 0 without it)
- *   base_m = exp(-softplus(dt[b,t,h] + dt_bias[h] + state_offset[m]))
+ *   base_m = exp(-softplus(dt[b,t,h] + dt_bias[h] + dt_bias2[h] + state_offset[m]))
  *   base_m <- floor + (1 - floor) base_m             (only when floor > 0)
  *   gamma[m,b,h,t] = base_m (1 - p) + p,   v' = v (1 - p)
  *   rot[m,b,h,t] = routing[b,t,h,m] e^{i phase[b,t,h,m]}
@@ -287,7 +289,9 @@ int qpam_decay_matrix(int32_t n, int32_t t, const float *gamma, int64_t ldg, flo
  * q', k', v': planar [B,H,T,d] contiguous in out_dtype -- the scan's q, k, v.
  * gamma, rot: fp32 [M,B,H,T] contiguous -- the scan's gamma and rot.
  * d == 64, 1 <= M <= 4.  Rope rows past rope_len - 1 are clamped to the last
- * row (size the table to cover rope_offset + T).
+ * row (size the table to cover rope_offset + T).  dt_bias, dt_bias2 (an
+ * nn.Linear's own bias, optional) and state_offset are read in param_dtype and
+ * summed in fp32 (ABI 11; param_dtype 0 = fp32 as before).
  */
 typedef struct {
     int32_t B, T, H, d, M;
@@ -300,8 +304,8 @@ typedef struct {
     int64_t sx_b, sx_t, sx_h;
     const void *dt;                     /* [B,T,H] pre-bias decay logits */
     int64_t sd_b, sd_t, sd_h;
-    const float *dt_bias;               /* [H] fp32 */
-    const float *state_offset;          /* [M] fp32, optional (NULL = 0) */
+    const void *dt_bias;                /* [H] param_dtype */
+    const void *state_offset;           /* [M] param_dtype, optional (NULL = 0) */
     const void *protect;                /* [B,T,H] protect-gate logits, optional */
     int64_t sp_b, sp_t, sp_h;
     const void *phase;                  /* [B,T,H,M], optional (NULL = no rot) */
@@ -310,6 +314,8 @@ typedef struct {
     void *oq_re, *oq_im, *ok_re, *ok_im, *ov_re, *ov_im;
     float *gamma;
     float *rot_re, *rot_im;             /* required when phase is given */
+    int32_t param_dtype;                /* qpam_dtype of dt_bias, dt_bias2, state_offset */
+    const void *dt_bias2;               /* [H] param_dtype, optional (NULL = 0) */
 } qpam_prologue_args;
 
 int qpam_prologue_fwd(const qpam_prologue_args *a, void *stream);
@@ -323,7 +329,16 @@ int qpam_prologue_fwd(const qpam_prologue_args *a, void *stream);
  * the other axes); optionally ddt [B,T,H] (strides sdd_*, in_dtype) = the sum
  * of dpre over m, dt's gradient; dprotect [B,T,H] fp32 (when protect); dphase
  * and, optionally, drouting [B,T,H,M] fp32 (when phase) -- the layouts of the
- * logits they are the gradients of.  16 * H * (2 + 4 M) * 4 <= 65536. */
+ * logits they are the gradients of.  16 * H * (2 + 4 M) * 4 <= 65536.
+ * ABI 11: dprotect, dphase and drouting are written in dlogit_dtype (0 = fp32)
+ * with strides sdp_* (dprotect) and sdq_* (dphase, drouting), all zero meaning
+ * the contiguous layouts above (so the gradients of logits that are columns of
+ * one matrix land in that matrix's gradient directly); ddt_pad zero columns are
+ * written after ddt's H (stride sdd_h); dbias [H] and doffset [M] (param_dtype,
+ * optional) receive the sums of dpre over (b, t, m) and (b, t, h), formed in a
+ * fixed order -- dpre is then scratch (per-block partial sums) and does not
+ * hold dpre after the call.  dbias is the gradient of dt_bias and of
+ * dt_bias2 alike. */
 typedef struct {
     const qpam_prologue_args *fwd;
     const void *gq_re, *gq_im, *gk_re, *gk_im, *gv_re, *gv_im;
@@ -334,8 +349,14 @@ typedef struct {
     float *dpre;
     void *ddt;                          /* optional */
     int64_t sdd_b, sdd_t, sdd_h;
-    float *dprotect;
-    float *dphase, *drouting;
+    void *dprotect;
+    void *dphase, *drouting;
+    int32_t dlogit_dtype;
+    int32_t ddt_pad;
+    int64_t sdp_b, sdp_t, sdp_h;
+    int64_t sdq_b, sdq_t, sdq_h, sdq_m;
+    void *dbias;                        /* optional */
+    void *doffset;                      /* optional (with state_offset) */
 } qpam_prologue_bwd_args;
 
 int qpam_prologue_bwd(const qpam_prologue_bwd_args *a, void *stream);
@@ -347,6 +368,11 @@ int qpam_prologue_bwd(const qpam_prologue_bwd_args *a, void *stream);
  * gz[i] = gmag[i] z[i] / mag[i]. */
 int qpam_cabs_fwd(int32_t dtype, int64_t n, const void *z, void *mag, void *stream);
 int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void *mag, const void *gmag, void *gz, void *stream);
+/* The same backward added into gz (gz[i] += gmag[i] z[i] / mag[i]): the
+ * layer input's gradient from its projections already in gz, its gradient
+ * through the gates' magnitudes accumulated in the same pass (ABI 11). */
+int qpam_cabs_bwd_acc(int32_t dtype, int64_t n, const void *z, const void *mag, const void *gmag, void *gz,
+                      void *stream);
 
 /* Complex linear weights as one real GEMM operand (ComplexLinear,
  * v11/complex_ops.py:146-172: re = Wr xr - Wi xi, im = Wi xr + Wr xi; the PAM
@@ -386,6 +412,14 @@ typedef struct {
 
 int qpam_cweight_pack(const qpam_cweight_args *a, void *stream);
 int qpam_cweight_unpack(const qpam_cweight_args *a, void *stream);
+
+/* out[i] = sum over s < slices of in[s * stride + i], i < n (fp32, in slice
+ * order, rounded once to out_dtype): the row-sliced weight-gradient products
+ * of an nn.Linear (the layer's gate projections over |x|, v11/model.py:228,
+ * 646) reduced and cast in one pass (ABI 11).  n and stride multiples of 8,
+ * in and out 16-byte aligned. */
+int qpam_slice_sum(int32_t in_dtype, int32_t out_dtype, int32_t slices, int64_t n, int64_t stride, const void *in,
+                   void *out, void *stream);
 
 /* Gate logits of the decode step from |x| (v11/model.py:228, 646: protect_gate
  * and phase_proj applied to cabs(x), two nn.Linear on the same magnitudes, in

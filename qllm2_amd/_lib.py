@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -147,7 +147,7 @@ class PrologueArgs(ctypes.Structure):
         ("protect", c_ptr), ("sp_b", c_i64), ("sp_t", c_i64), ("sp_h", c_i64),
         ("phase", c_ptr), ("routing", c_ptr), ("sr_b", c_i64), ("sr_t", c_i64), ("sr_h", c_i64), ("sr_m", c_i64),
         ("oq_re", c_ptr), ("oq_im", c_ptr), ("ok_re", c_ptr), ("ok_im", c_ptr), ("ov_re", c_ptr), ("ov_im", c_ptr),
-        ("gamma", c_ptr), ("rot_re", c_ptr), ("rot_im", c_ptr),
+        ("gamma", c_ptr), ("rot_re", c_ptr), ("rot_im", c_ptr), ("param_dtype", c_i32), ("dt_bias2", c_ptr),
     ]
 
 
@@ -159,7 +159,10 @@ class PrologueBwdArgs(ctypes.Structure):
         ("dq_re", c_ptr), ("dq_im", c_ptr), ("dk_re", c_ptr), ("dk_im", c_ptr), ("dv_re", c_ptr), ("dv_im", c_ptr),
         ("sg_b", c_i64), ("sg_t", c_i64), ("sg_h", c_i64),
         ("dpre", c_ptr), ("ddt", c_ptr), ("sdd_b", c_i64), ("sdd_t", c_i64), ("sdd_h", c_i64),
-        ("dprotect", c_ptr), ("dphase", c_ptr), ("drouting", c_ptr),
+        ("dprotect", c_ptr), ("dphase", c_ptr), ("drouting", c_ptr), ("dlogit_dtype", c_i32), ("ddt_pad", c_i32),
+        ("sdp_b", c_i64), ("sdp_t", c_i64), ("sdp_h", c_i64),
+        ("sdq_b", c_i64), ("sdq_t", c_i64), ("sdq_h", c_i64), ("sdq_m", c_i64),
+        ("dbias", c_ptr), ("doffset", c_ptr),
     ]
 
 
@@ -239,6 +242,8 @@ SIGNATURES = {
     "qpam_pc_scan": (ctypes.c_int, [ctypes.POINTER(PcScanArgs), c_ptr]),
     "qpam_cweight_pack": (ctypes.c_int, [ctypes.POINTER(CWeightArgs), c_ptr]),
     "qpam_cweight_unpack": (ctypes.c_int, [ctypes.POINTER(CWeightArgs), c_ptr]),
+    "qpam_cabs_bwd_acc": (ctypes.c_int, [c_i32, c_i64, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "qpam_slice_sum": (ctypes.c_int, [c_i32, c_i32, c_i32, c_i64, c_i64, c_ptr, c_ptr, c_ptr]),
 }
 
 _LIB = None

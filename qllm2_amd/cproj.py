@@ -21,7 +21,13 @@ projection forward and as many backward.  Here:
     in slice order.
 
 The weight gradients are formed in fp32 from the bf16 (or fp32) GEMM outputs
-and rounded once to the weights' dtype.
+and rounded once to the weights' dtype.  linear_in can also return cabs(x)
+(the gates' input, v11/model.py:228, 646) and then adds the gradient that
+comes back through it into x's gradient in the same pass as the projection's
+(qpam_cabs_bwd_acc), instead of a separate gradient and a sum.  gate_linear
+runs the gate projections over |x| (protect_gate and phase_proj stacked) with
+their weight gradient reduced over row slices and cast by one launch
+(qpam_slice_sum) and their bias gradient as one product with a ones row.
 """
 
 import ctypes
@@ -95,33 +101,58 @@ def _unpack(layout, g, slices, wr, wi, tail, rows):
     return g_wr, g_wi, g_tail
 
 
+def _cabs(x2):
+    """|z| per complex feature of x2 [..., 2C] (qpam_cabs_fwd, cabs of
+    v11/complex_ops.py:86-87) -> [..., C] in x2's dtype."""
+    mag = torch.empty(x2.shape[:-1] + (x2.shape[-1] // 2,), device=x2.device, dtype=x2.dtype)
+    with torch.cuda.device(x2.device):
+        _lib.check(_lib.lib().qpam_cabs_fwd(_code(x2), mag.numel(), x2.data_ptr(), mag.data_ptr(),
+                                            _lib.stream_ptr(x2.device)), "qpam_cabs_fwd")
+    return mag
+
+
 class _LinearIn(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x2, wr, wi, tail, cols):
+    def forward(ctx, x2, wr, wi, tail, cols, with_mag):
         w = _pack(_lib.QPAM_CW_IN, wr, wi, tail, cols)
-        ctx.save_for_backward(x2, w, wr, wi, tail)
-        return F.linear(x2, w)
+        out = F.linear(x2, w)
+        mag = _cabs(x2) if with_mag else x2.new_empty(0)
+        ctx.save_for_backward(x2, w, wr, wi, tail, mag if with_mag else None)
+        if not with_mag:
+            ctx.mark_non_differentiable(mag)
+        return out, mag
 
     @staticmethod
-    def backward(ctx, g):
-        x2, w, wr, wi, tail = ctx.saved_tensors
+    def backward(ctx, g, g_mag):
+        x2, w, wr, wi, tail, mag = ctx.saved_tensors
         g2 = g.reshape(-1, w.shape[0])
         if not g2.is_contiguous():
             g2 = g2.contiguous()
-        gx = (g2 @ w).view(x2.shape) if ctx.needs_input_grad[0] else None
+        gx = None
+        if ctx.needs_input_grad[0]:
+            gx = (g2 @ w).view(x2.shape)
+            if mag is not None and g_mag is not None:
+                # the gradient through |x| added into the projections' in one pass
+                gm = g_mag.to(mag.dtype).contiguous()
+                with torch.cuda.device(x2.device):
+                    _lib.check(_lib.lib().qpam_cabs_bwd_acc(_code(x2), mag.numel(), x2.data_ptr(), mag.data_ptr(),
+                                                            gm.data_ptr(), gx.data_ptr(),
+                                                            _lib.stream_ptr(x2.device)), "qpam_cabs_bwd_acc")
         g_wr = g_wi = g_tail = None
         if any(ctx.needs_input_grad[1:4]):
             gw = g2.t() @ x2.reshape(-1, w.shape[1])                  # [cols, 2 dim]
             g_wr, g_wi, g_tail = _unpack(_lib.QPAM_CW_IN, gw, 1, wr, wi, tail, w.shape[0])
-        return gx, g_wr, g_wi, g_tail, None
+        return gx, g_wr, g_wi, g_tail, None, None
 
 
-def linear_in(x2, wr, wi, tail, cols):
+def linear_in(x2, wr, wi, tail, cols, with_mag=False):
     """x2 [..., 2C] (features interleaved (re, im)), complex weights wr, wi
     [R, C], tail [Tr, 2C] real rows over [xr | xi] (or None) -> [..., cols]:
     columns [0, R) the real outputs, [R, 2R) the imaginary outputs, then the
-    tail's outputs, then zeros."""
-    return _LinearIn.apply(x2, wr, wi, tail, int(cols))
+    tail's outputs, then zeros.  with_mag also returns |x| [..., C] (cabs) and
+    adds its gradient into x's own in the backward: (proj, mag)."""
+    out, mag = _LinearIn.apply(x2, wr, wi, tail, int(cols), bool(with_mag))
+    return (out, mag) if with_mag else out
 
 
 def _splits(n, out, inp):
@@ -164,3 +195,70 @@ def linear_out(y2, wr, wi):
     """y2 [..., 2C] (a real then an imaginary block of C features), complex
     weights wr, wi [R, C] -> [..., 2R] with the outputs interleaved (re, im)."""
     return _LinearOut.apply(y2, wr, wi)
+
+
+_ONES = {}
+
+
+def _ones_row(n, like):
+    key = (n, like.device, like.dtype)
+    t = _ONES.get(key)
+    if t is None:
+        if len(_ONES) > 16:
+            _ONES.clear()
+        t = _ONES[key] = torch.ones(1, n, device=like.device, dtype=like.dtype)
+    return t
+
+
+class _GateLinear(torch.autograd.Function):
+    """F.linear over the gate rows of several nn.Linear stacked: the weight
+    gradient as a batched product over row slices of N summed and cast by one
+    launch (qpam_slice_sum), the bias gradient as one product with a ones row."""
+
+    @staticmethod
+    def forward(ctx, x, n_parts, *params):
+        ws, bs = params[:n_parts], params[n_parts:]
+        w = torch.cat(ws, 0) if n_parts > 1 else ws[0]
+        b = torch.cat(bs, 0) if n_parts > 1 else bs[0]
+        ctx.save_for_backward(x, w)
+        ctx.rows = [t.shape[0] for t in ws]
+        ctx.b_dtype = b.dtype
+        return F.linear(x, w, b)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w = ctx.saved_tensors
+        out, inp = w.shape
+        g2 = g.reshape(-1, out)
+        if not g2.is_contiguous():
+            g2 = g2.contiguous()
+        n = g2.shape[0]
+        gx = (g2 @ w).view(x.shape) if ctx.needs_input_grad[0] else None
+        x2 = x.reshape(n, inp)
+        s = _splits(n, out, inp)
+        gws = torch.bmm(g2.view(s, n // s, out).transpose(1, 2), x2.view(s, n // s, inp))   # [S, out, in]
+        gw = torch.empty(out, inp, device=w.device, dtype=w.dtype)
+        with torch.cuda.device(w.device):
+            _lib.check(_lib.lib().qpam_slice_sum(_code(gws), _code(gw), s, out * inp, out * inp, gws.data_ptr(),
+                                                 gw.data_ptr(), _lib.stream_ptr(w.device)), "qpam_slice_sum")
+        gb = (_ones_row(n, g2) @ g2).view(out).to(ctx.b_dtype)
+        gws_parts = list(torch.split(gw, ctx.rows, 0))
+        gbs_parts = list(torch.split(gb, ctx.rows, 0))
+        return (gx, None, *gws_parts, *gbs_parts)
+
+
+def gate_supported(x, weights, biases):
+    """The gate path applies: biases present, one dtype (fp32 or bf16) for x,
+    weights and biases, feature counts the slice-sum vector width divides."""
+    ts = [x] + list(weights) + list(biases)
+    if any(t is None for t in biases) or torch.is_autocast_enabled():
+        return False
+    if not all(t.is_cuda and t.dtype == x.dtype for t in ts) or x.dtype not in (torch.float32, torch.bfloat16):
+        return False
+    return (sum(w.shape[0] for w in weights) * x.shape[-1]) % 8 == 0
+
+
+def gate_linear(x, weights, biases):
+    """F.linear(x, cat(weights), cat(biases)) with the weight gradients formed
+    by a sliced product reduced in one launch (see _GateLinear)."""
+    return _GateLinear.apply(x, len(weights), *weights, *biases)

@@ -141,7 +141,17 @@ __global__ void __launch_bounds__(CW_THREADS) cw_pack_kernel(CwParams p) {
 template <typename G, int N>
 __device__ __forceinline__ void g_load(const CwParams &p, int64_t row, int64_t col, float (&x)[N]) {
     V<G>::template load<N>(p.g, row * p.ldw + col, x);
-    for (int s = 1; s < p.slices; ++s) {
+    int s = 1;
+    for (; s + 2 <= p.slices; s += 2) {  // two slices' loads in flight, added in slice order
+        float y[2][N];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) V<G>::template load<N>(p.g, (s + u) * p.slice_stride + row * p.ldw + col, y[u]);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int k = 0; k < N; ++k) x[k] += y[u][k];
+    }
+    for (; s < p.slices; ++s) {
         float y[N];
         V<G>::template load<N>(p.g, s * p.slice_stride + row * p.ldw + col, y);
 #pragma unroll
@@ -196,6 +206,34 @@ __global__ void __launch_bounds__(CW_THREADS) cw_unpack_kernel(CwParams p) {
         V<T>::template store<8>(p.g_wr, r * p.C + c0, gr);
         V<T>::template store<8>(p.g_wi, r * p.C + c0, gi);
     }
+}
+
+// out[i] = sum over s of in[s * stride + i] (fp32, slice order), eight
+// consecutive elements per thread
+template <typename TI, typename TO>
+__global__ void __launch_bounds__(CW_THREADS) slice_sum_kernel(int slices, int64_t n8, int64_t stride, const void *in,
+                                                               void *out) {
+    const int64_t i = (int64_t)blockIdx.x * CW_THREADS + threadIdx.x;
+    if (i >= n8) return;
+    float x[8];
+    V<TI>::template load<8>(in, 8 * i, x);
+    int s = 1;
+    for (; s + 4 <= slices; s += 4) {  // four slices' loads in flight, added in slice order
+        float y[4][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) V<TI>::template load<8>(in, (int64_t)(s + u) * stride + 8 * i, y[u]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[k] += y[u][k];
+    }
+    for (; s < slices; ++s) {
+        float y[8];
+        V<TI>::template load<8>(in, (int64_t)s * stride + 8 * i, y);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] += y[k];
+    }
+    V<TO>::template store<8>(out, 8 * i, x);
 }
 
 bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
@@ -285,4 +323,26 @@ extern "C" int qpam_cweight_unpack(const qpam_cweight_args *a, void *stream) {
         else hipLaunchKernelGGL((cw_unpack_kernel<U, U, QPAM_CW_OUT>), grid, block, 0, s, p);
     }
     return launch_status("cw_unpack_kernel");
+}
+
+extern "C" int qpam_slice_sum(int32_t in_dtype, int32_t out_dtype, int32_t slices, int64_t n, int64_t stride,
+                              const void *in, void *out, void *stream) {
+    using namespace qpam;
+    QPAM_REQUIRE((in_dtype == QPAM_F32 || in_dtype == QPAM_BF16) && (out_dtype == QPAM_F32 || out_dtype == QPAM_BF16),
+                 "qpam_slice_sum: dtypes must be QPAM_F32 or QPAM_BF16");
+    QPAM_REQUIRE(slices >= 1 && n >= 0 && n % 8 == 0 && (slices == 1 || (stride >= n && stride % 8 == 0)),
+                 "qpam_slice_sum: slices >= 1, n a multiple of 8, stride >= n and a multiple of 8");
+    QPAM_REQUIRE(n == 0 || (in && out && aligned(in, 16) && aligned(out, 16)),
+                 "qpam_slice_sum: 16-byte aligned in and out required");
+    if (n == 0) return QPAM_OK;
+    const int64_t n8 = n / 8;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid = grid_for(n8), block(CW_THREADS);
+    using U = unsigned short;
+    const bool fi = in_dtype == QPAM_F32, fo = out_dtype == QPAM_F32;
+    if (fi && fo) hipLaunchKernelGGL((slice_sum_kernel<float, float>), grid, block, 0, s, slices, n8, stride, in, out);
+    else if (fi) hipLaunchKernelGGL((slice_sum_kernel<float, U>), grid, block, 0, s, slices, n8, stride, in, out);
+    else if (fo) hipLaunchKernelGGL((slice_sum_kernel<U, float>), grid, block, 0, s, slices, n8, stride, in, out);
+    else hipLaunchKernelGGL((slice_sum_kernel<U, U>), grid, block, 0, s, slices, n8, stride, in, out);
+    return launch_status("slice_sum_kernel");
 }

@@ -88,11 +88,24 @@ template <> struct Io<Bf16> {
 __device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 __device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
 
-// decay logit of state m: dt + dt_bias + state_offset
+// element i of a parameter vector in param_dtype
+__device__ __forceinline__ float param_at(const void *p, int32_t dtype, int i) {
+    return dtype == QPAM_BF16 ? bf16_to_f32(static_cast<const unsigned short *>(p)[i]) : static_cast<const float *>(p)[i];
+}
+
+// decay logit of state m: dt + dt_bias (+ dt_bias2) + state_offset
 template <typename TI>
 __device__ __forceinline__ float pre_sum(const qpam_prologue_args &a, int b, int t, int h, int m) {
-    return Io<TI>::load1(a.dt, b * a.sd_b + (int64_t)t * a.sd_t + h * a.sd_h) + a.dt_bias[h] +
-           (a.state_offset ? a.state_offset[m] : 0.f);
+    float bias = param_at(a.dt_bias, a.param_dtype, h);
+    if (a.dt_bias2) bias += param_at(a.dt_bias2, a.param_dtype, h);
+    return Io<TI>::load1(a.dt, b * a.sd_b + (int64_t)t * a.sd_t + h * a.sd_h) + bias +
+           (a.state_offset ? param_at(a.state_offset, a.param_dtype, m) : 0.f);
+}
+
+// a logit gradient in dlogit_dtype
+__device__ __forceinline__ void store_logit(void *p, int32_t dtype, int64_t o, float v) {
+    if (dtype == QPAM_BF16) static_cast<unsigned short *>(p)[o] = f32_to_bf16(v);
+    else static_cast<float *>(p)[o] = v;
 }
 
 // exp(-softplus(pre)) lifted onto [floor, 1) when floor > 0
@@ -334,14 +347,29 @@ __global__ void __launch_bounds__(PTHREADS) prologue_bwd_kernel(qpam_prologue_bw
         s_dpre[m * rows + r] = dpre, s_dpm[m * rows + r] = dpm, s_dph[m * rows + r] = dph, s_dro[m * rows + r] = dro;
     }
     __syncthreads();
+    const bool sums = g.dbias || g.doffset;
+    // logit-gradient strides (all zero: the contiguous layouts)
+    const bool qdef = (g.sdq_b | g.sdq_t | g.sdq_h | g.sdq_m) == 0, pdef = (g.sdp_b | g.sdp_t | g.sdp_h) == 0;
+    const int64_t qb = qdef ? (int64_t)a.T * a.H * M : g.sdq_b, qt = qdef ? (int64_t)a.H * M : g.sdq_t,
+                  qh = qdef ? M : g.sdq_h, qm = qdef ? 1 : g.sdq_m;
+    const int64_t pb = pdef ? (int64_t)a.T * a.H : g.sdp_b, pt = pdef ? a.H : g.sdp_t, ph = pdef ? 1 : g.sdp_h;
     for (int i = tid; i < items; i += PTHREADS) {   // state-fastest: contiguous [B,T,H,M] rows
         const int m = i % M, r = i / M, tt = r / a.H, h = r - tt * a.H, t = t0 + tt;
         if (t >= a.T) continue;
-        const int64_t o = (((int64_t)b * a.T + t) * a.H + h) * M + m;
-        g.dpre[o] = s_dpre[m * rows + r];
+        if (!sums) g.dpre[(((int64_t)b * a.T + t) * a.H + h) * M + m] = s_dpre[m * rows + r];
         if (a.phase) {
-            g.dphase[o] = s_dph[m * rows + r];
-            if (g.drouting) g.drouting[o] = s_dro[m * rows + r];
+            const int64_t o = b * qb + (int64_t)t * qt + h * qh + m * qm;
+            store_logit(g.dphase, g.dlogit_dtype, o, s_dph[m * rows + r]);
+            if (g.drouting) store_logit(g.drouting, g.dlogit_dtype, o, s_dro[m * rows + r]);
+        }
+    }
+    if (sums) {  // this block's sums of dpre over its tokens, per (h, m), in token order
+        const int hm = a.H * M, valid = min(BT, a.T - t0);
+        for (int j = tid; j < hm; j += PTHREADS) {
+            const int h = j / M, m = j - h * M;
+            float x = 0.f;
+            for (int tt = 0; tt < valid; ++tt) x += s_dpre[m * rows + tt * a.H + h];
+            g.dpre[(int64_t)blockIdx.x * hm + j] = x;
         }
     }
     for (int r = tid; r < rows; r += PTHREADS) {
@@ -349,12 +377,58 @@ __global__ void __launch_bounds__(PTHREADS) prologue_bwd_kernel(qpam_prologue_bw
         if (t >= a.T) continue;
         float ddt = 0.f, dp = -s_gvv[r];             // d v' / d p = -v
         for (int m = 0; m < M; ++m) ddt += s_dpre[m * rows + r], dp += s_dpm[m * rows + r];
-        if (g.ddt) Io<TI>::store1(g.ddt, b * g.sdd_b + (int64_t)t * g.sdd_t + h * g.sdd_h, ddt);
+        if (g.ddt) {
+            const int64_t o = b * g.sdd_b + (int64_t)t * g.sdd_t + h * g.sdd_h;
+            Io<TI>::store1(g.ddt, o, ddt);
+            if (h == a.H - 1)  // the padding columns after dt's
+                for (int k = 1; k <= g.ddt_pad; ++k) Io<TI>::store1(g.ddt, o + k * g.sdd_h, 0.f);
+        }
         if (a.protect) {
             const float p = 1.f - s_keep[r];
-            g.dprotect[((int64_t)b * a.T + t) * a.H + h] = dp * p * (1.f - p);
+            store_logit(g.dprotect, g.dlogit_dtype, b * pb + (int64_t)t * pt + h * ph, dp * p * (1.f - p));
         }
     }
+}
+
+// d dt_bias [H] and d state_offset [M] from the per-block partial sums
+// part[blocks][H M] of the backward, in one block: thread (group g, column j)
+// sums the rows of its group's contiguous range in row order (its loads all in
+// flight), the groups' sums are added in group order per column, then over m
+// (dbias) and over h (doffset) in index order -- a fixed order throughout
+constexpr int BIAS_THREADS = 1024;
+__global__ void __launch_bounds__(BIAS_THREADS) prologue_bias_grad_kernel(const float *part, int blocks, int H, int M,
+                                                                          int32_t dtype, void *dbias, void *doffset) {
+    extern __shared__ float red[];  // [groups][H M], then the column sums
+    const int hm = H * M, groups = max(1, BIAS_THREADS / hm), per = (blocks + groups - 1) / groups;
+    float *col = red + groups * hm;
+    for (int i = threadIdx.x; i < groups * hm; i += BIAS_THREADS) {
+        const int gr = i / hm, j = i - gr * hm, k1 = min(blocks, (gr + 1) * per);
+        float x = 0.f;
+#pragma unroll 8
+        for (int k = gr * per; k < k1; ++k) x += part[(int64_t)k * hm + j];
+        red[i] = x;
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < hm; j += BIAS_THREADS) {
+        float x = 0.f;
+        for (int gr = 0; gr < groups; ++gr) x += red[gr * hm + j];
+        col[j] = x;
+    }
+    __syncthreads();
+    for (int h = threadIdx.x; dbias && h < H; h += BIAS_THREADS) {
+        float x = 0.f;
+        for (int m = 0; m < M; ++m) x += col[h * M + m];
+        store_logit(dbias, dtype, h, x);
+    }
+    for (int m = threadIdx.x; doffset && m < M; m += BIAS_THREADS) {
+        float x = 0.f;
+        for (int h = 0; h < H; ++h) x += col[h * M + m];
+        store_logit(doffset, dtype, m, x);
+    }
+}
+size_t bias_grad_lds(int H, int M) {
+    const int hm = H * M, groups = std::max(1, BIAS_THREADS / hm);
+    return (size_t)(groups + 1) * hm * sizeof(float);
 }
 
 size_t bwd_lds_bytes(const qpam_prologue_args &a) { return (size_t)(2 + 4 * a.M) * BT * a.H * sizeof(float); }
@@ -372,7 +446,8 @@ __global__ void __launch_bounds__(256) cabs_fwd_kernel(int64_t n4, const void *z
     Io<T>::store4(mag, 4 * i, m);
 }
 
-template <typename T>
+// ACC: gz += (the gradient), the input's other gradient already in gz
+template <typename T, bool ACC>
 __global__ void __launch_bounds__(256) cabs_bwd_kernel(int64_t n4, const void *z, const void *mag, const void *gmag,
                                                        void *gz) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -385,6 +460,12 @@ __global__ void __launch_bounds__(256) cabs_bwd_kernel(int64_t n4, const void *z
     for (int j = 0; j < 4; ++j) s[j] = g[j] / m[j];
     a[0] *= s[0], a[1] *= s[0], a[2] *= s[1], a[3] *= s[1];
     b[0] *= s[2], b[1] *= s[2], b[2] *= s[3], b[3] *= s[3];
+    if constexpr (ACC) {
+        float c[4], e[4];
+        Io<T>::load4(gz, 8 * i, c), Io<T>::load4(gz, 8 * i + 4, e);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] += c[j], b[j] += e[j];
+    }
     Io<T>::store4(gz, 8 * i, a), Io<T>::store4(gz, 8 * i + 4, b);
 }
 
@@ -409,6 +490,8 @@ int validate_inputs(const qpam_prologue_args *a) {
     QPAM_REQUIRE(a->rope == nullptr || (a->rope_len >= 1 && aligned(a->rope, 16)),
                  "qpam_prologue: rope needs rope_len >= 1 and a 16-byte aligned table");
     QPAM_REQUIRE(a->routing == nullptr || a->phase, "qpam_prologue: routing needs phase");
+    QPAM_REQUIRE(a->param_dtype == QPAM_F32 || a->param_dtype == QPAM_BF16,
+                 "qpam_prologue: param_dtype must be QPAM_F32 or QPAM_BF16");
     return QPAM_OK;
 }
 
@@ -531,18 +614,34 @@ extern "C" int qpam_prologue_bwd(const qpam_prologue_bwd_args *g, void *stream) 
     QPAM_REQUIRE(a.protect == nullptr || g->dprotect != nullptr, "qpam_prologue_bwd: dprotect required with protect");
     QPAM_REQUIRE(a.phase == nullptr || (g->grot_re && g->grot_im && g->dphase),
                  "qpam_prologue_bwd: rot gradients and dphase required with phase");
+    QPAM_REQUIRE(g->dlogit_dtype == QPAM_F32 || g->dlogit_dtype == QPAM_BF16,
+                 "qpam_prologue_bwd: dlogit_dtype must be QPAM_F32 or QPAM_BF16");
+    QPAM_REQUIRE(g->ddt_pad >= 0 && (g->ddt_pad == 0 || g->ddt), "qpam_prologue_bwd: ddt_pad needs ddt");
     const size_t lds = bwd_lds_bytes(a);
     QPAM_REQUIRE(lds <= 64 * 1024, "qpam_prologue_bwd: H=%d, M=%d need %zu bytes of LDS (64 KiB max)", a.H, a.M, lds);
     const long long blocks = (long long)a.B * ((a.T + BT - 1) / BT);
-    if (blocks == 0) return QPAM_OK;
+    const bool sums = g->dbias || g->doffset;
+    QPAM_REQUIRE(!sums || bias_grad_lds(a.H, a.M) <= 64 * 1024,
+                 "qpam_prologue_bwd: H * M = %d too large for the bias gradients", a.H * a.M);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (blocks == 0) {
+        if (!sums) return QPAM_OK;
+        // no tokens: zero gradients (a fill by the same reduction over no blocks)
+        hipLaunchKernelGGL(prologue_bias_grad_kernel, dim3(1), dim3(BIAS_THREADS), bias_grad_lds(a.H, a.M), s, g->dpre,
+                           0, a.H, a.M, a.param_dtype, g->dbias, g->doffset);
+        return launch_status("prologue_bias_grad_kernel");
+    }
     const dim3 grid((unsigned)blocks), block(PTHREADS);
     const bool fi = a.in_dtype == QPAM_F32, fo = a.out_dtype == QPAM_F32;
     if (fi && fo) hipLaunchKernelGGL((prologue_bwd_kernel<float, float>), grid, block, lds, s, *g, a);
     else if (fi) hipLaunchKernelGGL((prologue_bwd_kernel<float, Bf16>), grid, block, lds, s, *g, a);
     else if (fo) hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, float>), grid, block, lds, s, *g, a);
     else hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, Bf16>), grid, block, lds, s, *g, a);
-    return launch_status("prologue_bwd_kernel");
+    int st2 = launch_status("prologue_bwd_kernel");
+    if (st2 || !sums) return st2;
+    hipLaunchKernelGGL(prologue_bias_grad_kernel, dim3(1), dim3(BIAS_THREADS), bias_grad_lds(a.H, a.M), s, g->dpre,
+                       (int)blocks, a.H, a.M, a.param_dtype, g->dbias, g->doffset);
+    return launch_status("prologue_bias_grad_kernel");
 }
 
 extern "C" int qpam_cabs_fwd(int32_t dtype, int64_t n, const void *z, void *mag, void *stream) {
@@ -571,8 +670,25 @@ extern "C" int qpam_cabs_bwd(int32_t dtype, int64_t n, const void *z, const void
     const int64_t n4 = n / 4;
     const dim3 grid((unsigned)((n4 + 255) / 256)), block(256);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (dtype == QPAM_F32) hipLaunchKernelGGL(cabs_bwd_kernel<float>, grid, block, 0, s, n4, z, mag, gmag, gz);
-    else hipLaunchKernelGGL(cabs_bwd_kernel<Bf16>, grid, block, 0, s, n4, z, mag, gmag, gz);
+    if (dtype == QPAM_F32) hipLaunchKernelGGL((cabs_bwd_kernel<float, false>), grid, block, 0, s, n4, z, mag, gmag, gz);
+    else hipLaunchKernelGGL((cabs_bwd_kernel<Bf16, false>), grid, block, 0, s, n4, z, mag, gmag, gz);
+    return launch_status("cabs_bwd_kernel");
+}
+
+extern "C" int qpam_cabs_bwd_acc(int32_t dtype, int64_t n, const void *z, const void *mag, const void *gmag, void *gz,
+                                 void *stream) {
+    QPAM_REQUIRE(dtype == QPAM_F32 || dtype == QPAM_BF16, "qpam_cabs_bwd_acc: dtype must be QPAM_F32 or QPAM_BF16");
+    QPAM_REQUIRE(n >= 0 && n % 4 == 0, "qpam_cabs_bwd_acc: element count %lld must be a multiple of 4", (long long)n);
+    const int va = dtype == QPAM_F32 ? 16 : 8;
+    QPAM_REQUIRE(n == 0 || (z && mag && gmag && gz && aligned(z, va) && aligned(mag, va) && aligned(gmag, va) &&
+                            aligned(gz, va)),
+                 "qpam_cabs_bwd_acc: %d-byte aligned buffers required", va);
+    if (n == 0) return QPAM_OK;
+    const int64_t n4 = n / 4;
+    const dim3 grid((unsigned)((n4 + 255) / 256)), block(256);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == QPAM_F32) hipLaunchKernelGGL((cabs_bwd_kernel<float, true>), grid, block, 0, s, n4, z, mag, gmag, gz);
+    else hipLaunchKernelGGL((cabs_bwd_kernel<Bf16, true>), grid, block, 0, s, n4, z, mag, gmag, gz);
     return launch_status("cabs_bwd_kernel");
 }
 

@@ -265,11 +265,23 @@ def _in_weight(self, h, d, cols):
     return w, torch.cat([br, bi, wr.new_zeros(h + pad)])
 
 
-def _packed_in(self, x2, h, cols):
+_ONES = {}
+
+
+def _ones(x):
+    """A [1,1,1,1] tensor of ones in x's device and dtype, made once."""
+    key = (x.device, x.dtype)
+    t = _ONES.get(key)
+    if t is None:
+        t = _ONES[key] = torch.ones(1, 1, 1, 1, device=x.device, dtype=x.dtype)
+    return t
+
+
+def _packed_in(self, x2, h, cols, with_mag):
     """proj [B,T,cols] from the packed input projection (qkv_proj, or q/k/v_proj,
     and dt_proj's logits without its bias in one GEMM, the weight packed and its
-    gradient split on the HIP library), or None where that path does not apply
-    (projection biases, mixed dtypes, autocast)."""
+    gradient split on the HIP library), with_mag: (proj, cabs(x)), or None where
+    that path does not apply (projection biases, mixed dtypes, autocast)."""
     mods = [self.qkv_proj] if self.fused_qkv else [self.q_proj, self.k_proj, self.v_proj]
     if any(getattr(m, "bias_real", None) is not None or getattr(m, "bias_imag", None) is not None for m in mods):
         return None
@@ -278,7 +290,7 @@ def _packed_in(self, x2, h, cols):
     tail = self.dt_proj.weight
     if tail.shape != (h, x2.shape[-1]) or not _cproj.supported(x2, wr, wi, tail, layout=_lib.QPAM_CW_IN):
         return None
-    return _cproj.linear_in(x2, wr, wi, tail, cols)
+    return _cproj.linear_in(x2, wr, wi, tail, cols, with_mag)
 
 
 def _out_weight(mod):
@@ -366,8 +378,13 @@ def forward(self, x, state=None, step_offset: int = 0):
     n = b * t
     xc = x if x.is_contiguous() else x.contiguous()
     cols = proj_columns(h)
-    proj = _packed_in(self, xc.view(b, t, 2 * dim), h, cols)
-    if proj is None:
+    need_mag = (self.use_gsp and not self.gate_content_aware) or (m > 1 and not (self.routing_content_aware
+                                                                               or self.state_compete))
+    packed = _packed_in(self, xc.view(b, t, 2 * dim), h, cols, need_mag)
+    mag = None
+    if packed is not None:
+        proj, mag = packed if need_mag else (packed, None)               # mag [B,T,dim] = cabs(x)
+    else:
         w_in, b_in = _in_weight(self, h, d, cols)
         proj = F.linear(xc.view(b, t, 2 * dim), w_in, b_in)             # [B,T,cols]
     if proj.dtype not in (torch.float32, torch.bfloat16):
@@ -379,9 +396,7 @@ def forward(self, x, state=None, step_offset: int = 0):
             self.register_buffer("rope_cache", _decode.build_rope_cache(end * 2, d, device=x.device),
                                  persistent=False)
         rope = self.rope_cache.float()
-    mag = None
-    if (self.use_gsp and not self.gate_content_aware) or (m > 1 and not (self.routing_content_aware
-                                                                         or self.state_compete)):
+    if need_mag and mag is None:
         mag = cabs(xc)                                                   # [B,T,dim]
     protect = phase = routing = offsets = None
     g_w, g_b, g_parts = [], [], []
@@ -398,22 +413,29 @@ def forward(self, x, state=None, step_offset: int = 0):
             routing = routing_w if self.state_compete else None
         else:
             g_w.append(self.phase_proj.weight), g_b.append(self.phase_proj.bias), g_parts.append("phase")
-            self._route_aux = self._route_balance_loss(x.new_ones(1, 1, 1, 1).expand(b, t, h, m))
+            self._route_aux = self._route_balance_loss(_ones(x).expand(b, t, h, m))
+    gate_kw = {}
     if g_parts:
-        gl = _linear_tall_k(mag, torch.cat(g_w, 0), torch.cat(g_b, 0))    # [B,T,H (+H K)]
-        col = 0
+        if _cproj.gate_supported(mag, g_w, g_b):
+            gl = _cproj.gate_linear(mag, g_w, g_b)                       # [B,T,H (+H K)]
+        else:
+            gl = _linear_tall_k(mag, torch.cat(g_w, 0), torch.cat(g_b, 0))
+        col, cols_of = 0, {}
         for part in g_parts:
+            cols_of[part] = col
             if part == "protect":
                 protect, col = gl[..., col:col + h], col + h
             else:
                 phase, col = gl[..., col:col + h * m].view(b, t, h, m), col + h * m
+        if routing is None and (protect is None or "protect" in cols_of) and (phase is None or "phase" in cols_of):
+            # the prologue reads the logits as columns of gl and returns gl's gradient whole
+            gate_kw = dict(gate=gl, protect_col=cols_of.get("protect", -1), phase_col=cols_of.get("phase", -1))
     if protect is not None and self.gate_surprisal_lambda > 0 and self.training:
         self._gate_prob_bt = torch.sigmoid(protect.float()).mean(dim=2)  # [B,T]
-    dt_bias = self.dt_bias if self.dt_proj.bias is None else self.dt_bias + self.dt_proj.bias
     (qr, qi), (kr, ki), (vr, vi), gamma, rot = pam_prologue(
-        proj, dt_bias, n_heads=h, n_states=m, state_offset=offsets, protect=protect, phase=phase,
-        routing=routing, rope=rope, rope_offset=step_offset, qk_norm=self.qk_norm,
-        gamma_floor=self.gamma_floor or 0.0)
+        proj, self.dt_bias, dt_bias2=self.dt_proj.bias, n_heads=h, n_states=m, state_offset=offsets,
+        protect=None if gate_kw else protect, phase=None if gate_kw else phase, routing=routing, rope=rope,
+        rope_offset=step_offset, qk_norm=self.qk_norm, gamma_floor=self.gamma_floor or 0.0, **gate_kw)
     o_dtype = self.o_proj.weight_real.dtype
     ck = chunk_for(self.chunk_size, t)
     # bf16 o_proj: the scan writes Y in bf16 itself (and reads its gradient in bf16)
@@ -434,7 +456,7 @@ def forward(self, x, state=None, step_offset: int = 0):
         # one keep-mask per complex value (as_complex_dropout_mask, v11/complex_ops.py:59-66)
         mask = self.dropout(torch.ones(out.shape[:-1], device=out.device, dtype=out.dtype))
         out = out * mask.unsqueeze(-1)
-    new_state = torch.stack([s_re, s_im], dim=-1).to(x.dtype)
+    new_state = torch.view_as_real(torch.complex(s_re, s_im)).to(x.dtype)
     return out, (new_state if m > 1 else new_state[0])
 
 

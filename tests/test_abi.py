@@ -54,7 +54,8 @@ def test_library_loads_and_exports_every_declared_symbol():
     ("qpam_decode_args", "DecodeArgs"), ("qpam_scan_args", "ScanArgs"), ("qpam_scan_bwd_args", "ScanBwdArgs"),
     ("qpam_ce_fwd_args", "CeFwdArgs"), ("qpam_ce_bwd_args", "CeBwdArgs"), ("qpam_cplx_args", "CplxArgs"),
     ("qpam_pc_fold_args", "PcFoldArgs"), ("qpam_pc_scan_args", "PcScanArgs"),
-    ("qpam_cweight_args", "CWeightArgs"),
+    ("qpam_cweight_args", "CWeightArgs"), ("qpam_prologue_args", "PrologueArgs"),
+    ("qpam_prologue_bwd_args", "PrologueBwdArgs"),
 ])
 def test_ctypes_structs_match_header(cname, pyname):
     py = [f[0] for f in getattr(_lib, pyname)._fields_]

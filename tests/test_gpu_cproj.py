@@ -153,3 +153,60 @@ def test_linear_out_matches_complex_linear(dtype, tol, N):
     assert ((out.float() - ref).abs().max() / scale(ref)) < tol
     for a, b in zip(p, q):
         assert ((a.grad.float() - b.grad).abs().max() / scale(b.grad)) < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-5), (torch.bfloat16, 2e-2)])
+def test_linear_in_with_mag(dtype, tol):
+    """proj and cabs(x) from one call; x's gradient sums the projection's and
+    the one through |x| (cabs, v11/complex_ops.py:86-87)."""
+    from qllm2_amd import cproj
+    dev = _dev()
+    B, T, C, R, H = 2, 256, 64, 48, 3
+    cols = 2 * R + H + 5
+    gen = torch.Generator(device=dev).manual_seed(8)
+    x = torch.randn(B, T, C, 2, device=dev, generator=gen)
+    wr, wi = (torch.randn(R, C, device=dev, generator=gen) * C ** -0.5 for _ in range(2))
+    tail = torch.randn(H, 2 * C, device=dev, generator=gen) * C ** -0.5
+    g1 = torch.randn(B, T, cols, device=dev, generator=gen)
+    g2 = torch.randn(B, T, C, device=dev, generator=gen)
+    p = [t.to(dtype).requires_grad_(True) for t in (x, wr, wi, tail)]
+    y, mag = cproj.linear_in(p[0].view(B, T, 2 * C), p[1], p[2], p[3], cols, with_mag=True)
+    torch.autograd.backward([y, mag], [g1.to(dtype), g2.to(dtype)])
+    q = [t.detach().float().requires_grad_(True) for t in p]
+    z = _clinear(q[0], q[1], q[2])
+    dt = torch.cat([q[0][..., 0], q[0][..., 1]], -1) @ q[3].t()
+    ref = torch.cat([z[..., 0], z[..., 1], dt, torch.zeros(B, T, cols - 2 * R - H, device=dev)], -1)
+    mref = torch.sqrt(q[0][..., 0] ** 2 + q[0][..., 1] ** 2 + 1e-8)
+    torch.autograd.backward([ref, mref], [g1.to(dtype).float(), g2.to(dtype).float()])
+    scale = lambda r: r.abs().max().clamp_min(1e-6)
+    assert ((mag.float() - mref).abs().max() / scale(mref)) < tol
+    for a, b in zip(p, q):
+        assert ((a.grad.float() - b.grad).abs().max() / scale(b.grad)) < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("parts", [1, 2])
+def test_gate_linear_matches_linear(dtype, tol, parts):
+    """Stacked nn.Linear rows over one input (N = 16384 runs 32 row slices in
+    the weight gradient) against torch autograd through F.linear."""
+    from qllm2_amd import cproj
+    dev = _dev()
+    N, D = 16384, 256
+    rows = [12, 36][:parts]
+    gen = torch.Generator(device=dev).manual_seed(parts)
+    x = torch.rand(N, D, device=dev, generator=gen)
+    ws = [torch.randn(r, D, device=dev, generator=gen) * D ** -0.5 for r in rows]
+    bs = [torch.randn(r, device=dev, generator=gen) for r in rows]
+    g = torch.randn(N, sum(rows), device=dev, generator=gen)
+    p = [t.to(dtype).requires_grad_(True) for t in [x] + ws + bs]
+    assert cproj.gate_supported(p[0], p[1:1 + parts], p[1 + parts:])
+    out = cproj.gate_linear(p[0], p[1:1 + parts], p[1 + parts:])
+    out.backward(g.to(dtype))
+    q = [t.detach().float().requires_grad_(True) for t in p]
+    ref = torch.nn.functional.linear(q[0], torch.cat(q[1:1 + parts]), torch.cat(q[1 + parts:]))
+    ref.backward(g.to(dtype).float())
+    scale = lambda r: r.abs().max().clamp_min(1e-6)
+    assert ((out.float() - ref).abs().max() / scale(ref)) < tol
+    for a, b in zip(p, q):
+        assert a.grad.dtype == a.dtype
+        assert ((a.grad.float() - b.grad).abs().max() / scale(b.grad)) < tol

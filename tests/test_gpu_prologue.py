@@ -118,6 +118,74 @@ def test_prologue_matches_oracle(gpu_lib, case, dtype):
         assert _rel(a.grad, b.grad) < tol_g, f"{name}: {_rel(a.grad, b.grad):.2e}"
 
 
+@pytest.mark.parametrize("case", [CASES[0], CASES[2], CASES[3]])
+@pytest.mark.parametrize("pdtype", [torch.float32, torch.bfloat16])
+def test_prologue_gate_matrix_and_params(gpu_lib, case, pdtype):
+    """The layer's form of the call: protect and phase as columns of one gate
+    matrix whose gradient comes back whole, the decay bias given as two
+    vectors (dt_bias and the dt projection's own bias, summed in the kernel),
+    dt_bias / dt_bias2 / state_offset in fp32 or bf16 with their gradients in
+    that dtype (formed by the in-call fixed-order reduction)."""
+    from qllm2_amd.decode import build_rope_cache
+    from qllm2_amd.pam_prologue import pam_prologue, proj_columns
+    M, offset, gsp, phase, routing, qk_norm, floor, T = case
+    B, H, d, dtype = 2, 3, 64, torch.bfloat16
+    qkv, dt, bias, off, prot, ph, ro = _inputs(M, offset is not None, gsp, phase, routing, T, 900 + M + T)
+    rnd = (lambda t: t.to(dtype).float() if t is not None else None)
+    qkv, dt, prot, ph = rnd(qkv), rnd(dt), rnd(prot), rnd(ph)
+    b1 = (0.6 * bias).to(pdtype).float()
+    b2 = (0.4 * bias).to(pdtype).float()
+    off = off.to(pdtype).float() if off is not None else None
+    rope = build_rope_cache(offset + T + 3, 64) if offset is not None else None
+    leaves, ref = _oracle(qkv, dt, b1 + b2, off, prot, ph, None, rope, offset or 0, qk_norm, floor)
+    dev = torch.device("cuda")
+    C = proj_columns(H)
+    proj = torch.cat([qkv[..., 0].reshape(B, T, 3 * H * d), qkv[..., 1].reshape(B, T, 3 * H * d), dt,
+                      torch.zeros(B, T, C - 6 * H * d - H)], -1).to(dtype).to(dev).requires_grad_(True)
+    cols = ([prot] if gsp else []) + ([ph.reshape(B, T, H * M)] if phase else [])
+    gate = torch.cat(cols, -1).to(dtype).to(dev).requires_grad_(True)
+    pcol, fcol = (0, H if gsp else 0) if phase else (0, -1)
+    if not gsp:
+        pcol = -1
+    pb1, pb2 = (x.to(pdtype).to(dev).requires_grad_(True) for x in (b1, b2))
+    poff = off.to(pdtype).to(dev).requires_grad_(True) if off is not None else None
+    q, k, v, gamma, rot = pam_prologue(proj, pb1, dt_bias2=pb2, n_heads=H, n_states=M, state_offset=poff,
+                                       gate=gate, protect_col=pcol, phase_col=fcol,
+                                       rope=rope.to(dev) if rope is not None else None, rope_offset=offset or 0,
+                                       qk_norm=qk_norm, gamma_floor=floor)
+    for name, got, want in (("q", q, ref[0]), ("k", k, ref[1]), ("v", v, ref[2])):
+        assert _rel(torch.stack([got[0].float(), got[1].float()], -1), want) < 2e-2, name
+    assert _rel(gamma, ref[3]) < 2e-2
+    g = torch.Generator().manual_seed(78)
+    cot = [torch.randn(x.shape, generator=g, dtype=torch.float64) for x in (ref[0], ref[1], ref[2], ref[3])]
+    loss_ref = sum((a * c).sum() for a, c in zip(ref[:4], cot))
+    loss = sum((torch.stack([p[0].float(), p[1].float()], -1) * c.to(dev).float()).sum()
+               for p, c in zip((q, k, v), cot[:3])) + (gamma * cot[3].to(dev).float()).sum()
+    if phase:
+        assert rot is not None and _rel(rot[0], ref[4][0]) < 2e-2
+        cr = [torch.randn(ref[4][0].shape, generator=g, dtype=torch.float64) for _ in range(2)]
+        loss_ref = loss_ref + (ref[4][0] * cr[0]).sum() + (ref[4][1] * cr[1]).sum()
+        loss = loss + (rot[0] * cr[0].to(dev).float()).sum() + (rot[1] * cr[1].to(dev).float()).sum()
+    else:
+        assert rot is None
+    loss_ref.backward()
+    loss.backward()
+    dp = proj.grad.float().cpu()
+    assert torch.all(dp[..., 6 * H * d + H:] == 0), "padding columns"
+    assert _rel(dp[..., 6 * H * d:6 * H * d + H], leaves[1].grad) < 2e-2, "ddt"
+    assert gate.grad.dtype == dtype and gate.grad.shape == gate.shape
+    gg = gate.grad.float().cpu()
+    if gsp:
+        assert _rel(gg[..., pcol:pcol + H], leaves[4].grad) < 2e-2, "dprotect"
+    if phase:
+        assert _rel(gg[..., fcol:fcol + H * M].reshape(B, T, H, M), leaves[5].grad) < 2e-2, "dphase"
+    for got in (pb1.grad, pb2.grad):
+        assert got.dtype == pdtype
+        assert _rel(got, leaves[2].grad) < 2e-2, "dbias"
+    if poff is not None:
+        assert poff.grad.dtype == pdtype and _rel(poff.grad, leaves[3].grad) < 2e-2, "doffset"
+
+
 class _Lin(torch.nn.Module):
     def __init__(self, wr, wi):
         super().__init__()

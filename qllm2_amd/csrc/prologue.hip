@@ -240,13 +240,18 @@ __device__ __forceinline__ void rope_norm_bwd(float zr, float zi, float c, float
 // projection matrix (writes of 128-byte pieces spread over the rows, as a
 // per-head block would make them, measured twice as slow).  A (token, head)
 // row of 64 complex elements is one DPP row of 16 lanes; 16 rows per pass,
-// four passes' loads issued before their arithmetic.  The per-(token, head,
+// BWD_PASSES passes' loads issued before their arithmetic.  The per-(token, head,
 // state) scalars are computed in token order (coalesced reads of the [M,B,H,T]
 // gradients), kept in LDS, and written state-fastest to the [B,T,H,M] outputs.
 constexpr int BT = 16;
+// passes of 16 rows whose loads are issued before their arithmetic: two keep the
+// kernel at four waves per SIMD (110 registers), so the 1024 blocks of a
+// B = 8, T = 2048 backward are resident at once; four (147 registers, three
+// waves per SIMD) left a third-full second round: 105 -> 96 us at that shape
+constexpr int BWD_PASSES = 2;
 
 template <typename TI, typename TO>
-__global__ void __launch_bounds__(PTHREADS) prologue_bwd_kernel(qpam_prologue_bwd_args g, qpam_prologue_args a) {
+__global__ void __launch_bounds__(PTHREADS, 4) prologue_bwd_kernel(qpam_prologue_bwd_args g, qpam_prologue_args a) {
     extern __shared__ float lds[];
     const int rows = BT * a.H, M = a.M;
     float *s_keep = lds, *s_gvv = lds + rows;
@@ -263,11 +268,11 @@ __global__ void __launch_bounds__(PTHREADS) prologue_bwd_kernel(qpam_prologue_bw
 
     const bool rope = a.rope != nullptr, norm = a.qk_norm != 0;
     const void *gplanes[6] = {g.gq_re, g.gq_im, g.gk_re, g.gk_im, g.gv_re, g.gv_im};
-    for (int r0 = 0; r0 < rows; r0 += 64) {
-        typename Io<TO>::Raw graw[4][6];
-        typename Io<TI>::Raw vraw[4][2];
+    for (int r0 = 0; r0 < rows; r0 += 16 * BWD_PASSES) {
+        typename Io<TO>::Raw graw[BWD_PASSES][6];
+        typename Io<TI>::Raw vraw[BWD_PASSES][2];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {   // rows past the tile re-read a valid row and are not stored
+        for (int k = 0; k < BWD_PASSES; ++k) {   // rows past the tile re-read a valid row and are not stored
             const int r = min(r0 + 16 * k + slot, rows - 1);
             const int tt = r / a.H, h = r - tt * a.H, t = min(t0 + tt, a.T - 1);
             const int64_t oo = (((int64_t)b * a.H + h) * a.T + t) * D + c4;
@@ -278,7 +283,7 @@ __global__ void __launch_bounds__(PTHREADS) prologue_bwd_kernel(qpam_prologue_bw
             vraw[k][1] = Io<TI>::load_raw(a.v_im, xo);
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < BWD_PASSES; ++k) {
             const int r = r0 + 16 * k + slot;
             const int tt = r / a.H, h = r - tt * a.H, t = t0 + tt;
             // a DPP row (16 lanes) shares r, so it is either all in or all out

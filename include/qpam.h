@@ -150,6 +150,29 @@ typedef struct {
     /* qpam_dtype of y (ABI 9): QPAM_F32, or QPAM_BF16 (rounded once from the fp32
      * sums; `y` then points at bf16 elements with the same element strides) */
     int32_t y_dtype;
+    /* optional (ABI 12): the decode prologue fused into the update (d = 64, head
+     * decay).  With proj set, q, k, v, gamma and rot are ignored and formed per
+     * (row, group g) from the layer's projection row proj[row][proj_ld]
+     * (proj_dtype): q, k, v real planes at columns (0, G, 2G) d + g d, their
+     * imaginary planes at (3G, 4G, 5G) d + g d, G = n_groups, the decay logit
+     * at 6 G d + g -- the layout qpam_prologue_fwd reads -- and from the gate
+     * logits gate[row][gate_ld] (proj_dtype, optional): protect at
+     * protect_col + g, phase of state m at phase_col + g M + m (-1: absent).
+     * As qpam_prologue_fwd computes them (without its RoPE, which rope / pos
+     * apply here): q, k normalised per element when qk_norm,
+     * p = sigmoid(protect), v' = v (1 - p), gamma_m = base_m (1 - p) + p with
+     * base_m = exp(-softplus(dt + dt_bias[g] + state_offset[m])) lifted onto
+     * [gamma_floor, 1) when gamma_floor > 0, rot_m = e^{i phase_m}. */
+    const void *proj;
+    int32_t proj_dtype;
+    int32_t qk_norm;
+    int64_t proj_ld;
+    const void *gate;
+    int64_t gate_ld;
+    int32_t protect_col, phase_col;
+    const float *dt_bias;               /* [G] fp32 */
+    const float *state_offset;          /* [M] fp32, optional */
+    float gamma_floor;
 } qpam_decode_args;
 
 int qpam_decode_step(const qpam_decode_args *a, void *stream);

@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -41,6 +41,9 @@ class DecodeArgs(ctypes.Structure):
         ("y", c_ptr), ("sy_slot", c_i64), ("sy_group", c_i64),
         ("rope", c_ptr), ("pos", c_ptr), ("rope_len", c_i32), ("vec_by_rank", c_i32),
         ("q_im", c_ptr), ("k_im", c_ptr), ("v_im", c_ptr), ("rot_im", c_ptr), ("gamma_per_channel", c_i32), ("y_dtype", c_i32),
+        ("proj", c_ptr), ("proj_dtype", c_i32), ("qk_norm", c_i32), ("proj_ld", c_i64),
+        ("gate", c_ptr), ("gate_ld", c_i64), ("protect_col", c_i32), ("phase_col", c_i32),
+        ("dt_bias", c_ptr), ("state_offset", c_ptr), ("gamma_floor", c_f32),
     ]
 
 

@@ -264,6 +264,128 @@ __global__ void __launch_bounds__((DecodeShape<D, multi_threads<D>()>::THREADS))
     }
 }
 
+// ------------------------------------ the decode prologue fused (d = 64) --
+// One block per (row, group g) as the multi-state kernel, with q, k, v, the
+// decays and the rotations formed from the layer's projection row and gate
+// logits instead of read: qpam_prologue_fwd's formulas in its order (q and k
+// normalised per element before the RoPE this kernel applies, as the unfused
+// engine does: |rope| = 1), so the prologue's launch and its fp32 planes go.
+template <typename TP> __device__ __forceinline__ float pld(const void *p, int64_t i);
+template <> __device__ __forceinline__ float pld<float>(const void *p, int64_t i) { return static_cast<const float *>(p)[i]; }
+template <> __device__ __forceinline__ float pld<unsigned short>(const void *p, int64_t i) {
+    return bf16_to_f32(static_cast<const unsigned short *>(p)[i]);
+}
+// elements i, i + 1 (i even)
+template <typename TP> __device__ __forceinline__ float2 pld2(const void *p, int64_t i);
+template <> __device__ __forceinline__ float2 pld2<float>(const void *p, int64_t i) {
+    return *reinterpret_cast<const float2 *>(static_cast<const float *>(p) + i);
+}
+template <> __device__ __forceinline__ float2 pld2<unsigned short>(const void *p, int64_t i) {
+    const unsigned u = *reinterpret_cast<const unsigned *>(static_cast<const unsigned short *>(p) + i);
+    return make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
+}
+__device__ __forceinline__ float p_softplus(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+__device__ __forceinline__ float p_sigmoid(float x) { return 1.f / (1.f + expf(-x)); }
+__device__ __forceinline__ void p_nrm(float &re, float &im) {
+    const float inv = 1.f / sqrtf(re * re + im * im + 1e-8f);
+    re *= inv, im *= inv;
+}
+
+template <int MS, typename TP>
+__global__ void __launch_bounds__((DecodeShape<64, multi_threads<64>()>::THREADS)) decode_proj_kernel(qpam_decode_args a) {
+    constexpr int D = 64;
+    using S = DecodeShape<D, multi_threads<D>()>;
+    const int tid = threadIdx.x;
+    const int ai = blockIdx.x / a.n_groups;
+    const int g = blockIdx.x - ai * a.n_groups;
+    const int slot = a.active ? a.active[ai] : ai;
+    if (slot < 0 || slot >= a.n_slots) return;
+    const int vr = a.vec_by_rank ? ai : slot;   // row of proj, gate, y
+    const int cp = tid % S::PAIRS, r0 = tid / S::PAIRS, lane = tid & 63;
+    float *st0 = a.state + slot * a.st_slot + g * a.st_group;
+    floatx4 s[MS][S::ITERS];
+#pragma unroll
+    for (int m = 0; m < MS; ++m)
+#pragma unroll
+        for (int it = 0; it < S::ITERS; ++it)
+            s[m][it] = __builtin_nontemporal_load(
+                reinterpret_cast<const floatx4 *>(st0 + m * a.st_state + 4 * (it * S::THREADS + tid)));
+    const int64_t GD = (int64_t)a.n_groups * D, prow = (int64_t)vr * a.proj_ld, col = (int64_t)g * D;
+    const float2 qre = pld2<TP>(a.proj, prow + col + 2 * cp), qim = pld2<TP>(a.proj, prow + 3 * GD + col + 2 * cp);
+    const float2 kre = pld2<TP>(a.proj, prow + GD + col + 2 * cp), kim = pld2<TP>(a.proj, prow + 4 * GD + col + 2 * cp);
+    float4 qv = make_float4(qre.x, qim.x, qre.y, qim.y), kv = make_float4(kre.x, kim.x, kre.y, kim.y);
+    if (a.qk_norm) {
+        p_nrm(qv.x, qv.y), p_nrm(qv.z, qv.w);
+        p_nrm(kv.x, kv.y), p_nrm(kv.z, kv.w);
+    }
+    apply_rope<D>(a, slot, cp, qv, kv);
+    const float q0r = qv.x * a.q_scale, q0i = qv.y * a.q_scale, q1r = qv.z * a.q_scale, q1i = qv.w * a.q_scale;
+    // the gates of (row, group): the protect probability, then per state the decay and rotation
+    const int64_t grow = (int64_t)vr * a.gate_ld;
+    const float p = (a.gate && a.protect_col >= 0) ? p_sigmoid(pld<TP>(a.gate, grow + a.protect_col + g)) : 0.f;
+    const float keep = 1.f - p;
+    const float dt = pld<TP>(a.proj, prow + 6 * GD + g) + a.dt_bias[g];
+    float2 vv[S::ITERS];
+#pragma unroll
+    for (int it = 0; it < S::ITERS; ++it) {
+        const int row = it * S::ROWS_PER_IT + r0;
+        vv[it] = make_float2(pld<TP>(a.proj, prow + 2 * GD + col + row) * keep,
+                             pld<TP>(a.proj, prow + 5 * GD + col + row) * keep);
+    }
+    float tot[S::NV];
+#pragma unroll
+    for (int j = 0; j < S::NV; ++j) tot[j] = 0.f;
+#pragma unroll
+    for (int m = 0; m < MS; ++m) {
+        float base = expf(-p_softplus(dt + (a.state_offset ? a.state_offset[m] : 0.f)));
+        if (a.gamma_floor > 0.f) base = a.gamma_floor + (1.f - a.gamma_floor) * base;
+        const float gam = base * (1.f - p) + p;
+        float rr = 1.f, ri = 0.f;
+        if (a.gate && a.phase_col >= 0) sincosf(pld<TP>(a.gate, grow + a.phase_col + g * MS + m), &ri, &rr);
+#pragma unroll
+        for (int it = 0; it < S::ITERS; ++it) {
+            const float o0r = vv[it].x * kv.x + vv[it].y * kv.y, o0i = vv[it].y * kv.x - vv[it].x * kv.y;
+            const float o1r = vv[it].x * kv.z + vv[it].y * kv.w, o1i = vv[it].y * kv.z - vv[it].x * kv.w;
+            floatx4 n;
+            n.x = gam * s[m][it].x + o0r;
+            n.y = gam * s[m][it].y + o0i;
+            n.z = gam * s[m][it].z + o1r;
+            n.w = gam * s[m][it].w + o1i;
+            __builtin_nontemporal_store(n, reinterpret_cast<floatx4 *>(st0 + m * a.st_state + 4 * (it * S::THREADS + tid)));
+            const float pr = n.x * q0r - n.y * q0i + n.z * q1r - n.w * q1i;
+            const float pi = n.x * q0i + n.y * q0r + n.z * q1i + n.w * q1r;
+            tot[2 * it] += rr * pr - ri * pi;
+            tot[2 * it + 1] += rr * pi + ri * pr;
+        }
+    }
+    int base, nv;
+    halving_reduce<S::NV, S::PAIRS>(tot, lane, base, nv);
+    if ((lane & S::bfly_mask()) == 0) {
+        const int64_t yrow = vr * a.sy_slot + g * a.sy_group;
+#pragma unroll
+        for (int j = 0; j < S::NV; ++j) {
+            if (j < nv) {
+                const int vi = base + j;
+                store_y(a, yrow, 2 * ((vi >> 1) * S::ROWS_PER_IT + r0) + (vi & 1), tot[j]);
+            }
+        }
+    }
+}
+
+template <typename TP>
+int launch_decode_proj(const qpam_decode_args &a, hipStream_t stream) {
+    const long long blocks = (long long)a.n_active * a.n_groups;
+    if (blocks == 0) return QPAM_OK;
+    constexpr int MT = DecodeShape<64, multi_threads<64>()>::THREADS;
+    switch (a.n_states) {
+        case 1: hipLaunchKernelGGL((decode_proj_kernel<1, TP>), dim3((unsigned)blocks), dim3(MT), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((decode_proj_kernel<2, TP>), dim3((unsigned)blocks), dim3(MT), 0, stream, a); break;
+        case 3: hipLaunchKernelGGL((decode_proj_kernel<3, TP>), dim3((unsigned)blocks), dim3(MT), 0, stream, a); break;
+        default: hipLaunchKernelGGL((decode_proj_kernel<4, TP>), dim3((unsigned)blocks), dim3(MT), 0, stream, a);
+    }
+    return launch_status("decode_proj_kernel");
+}
+
 // ------------------------------------------------ M states, rotations -----
 template <int D>
 constexpr int general_threads() { return D >= 128 ? 1024 : 256; }  // 8 float4 of state per lane at d = 64, 128
@@ -496,6 +618,28 @@ extern "C" int qpam_decode_step(const qpam_decode_args *a, void *stream) {
                  a->n_active, a->n_groups, a->n_states);
     QPAM_REQUIRE(a->active != nullptr || a->n_active <= a->n_slots,
                  "qpam_decode_step: n_active > n_slots without an active list");
+    if (a->proj) {  // the decode prologue fused (ABI 12)
+        QPAM_REQUIRE(a->state && a->y && a->dt_bias, "qpam_decode_step: state, y and dt_bias required with proj");
+        QPAM_REQUIRE(a->d == 64 && a->n_states <= 4, "qpam_decode_step: proj needs d = 64 and at most 4 states");
+        QPAM_REQUIRE(a->proj_dtype == QPAM_F32 || a->proj_dtype == QPAM_BF16,
+                     "qpam_decode_step: proj_dtype must be F32 or BF16");
+        QPAM_REQUIRE(a->y_dtype == QPAM_F32 || a->y_dtype == QPAM_BF16, "qpam_decode_step: y_dtype must be F32 or BF16");
+        QPAM_REQUIRE(a->active != nullptr || a->n_active <= a->n_slots,
+                     "qpam_decode_step: n_active > n_slots without an active list");
+        QPAM_REQUIRE(a->rope == nullptr || (a->pos != nullptr && a->rope_len >= 1 && aligned(a->rope, 16)),
+                     "qpam_decode_step: rope needs positions, rope_len >= 1 and a 16-byte aligned table");
+        QPAM_REQUIRE((long long)a->n_active * a->n_groups < (1ll << 31), "qpam_decode_step: grid too large");
+        QPAM_REQUIRE(a->gamma_per_channel == 0, "qpam_decode_step: proj takes head decays only");
+        QPAM_REQUIRE(a->proj_ld >= 6ll * a->n_groups * 64 + a->n_groups && a->proj_ld % 2 == 0 && aligned(a->proj, 8),
+                     "qpam_decode_step: proj rows of >= 6 G d + G elements, an even stride, 8-byte aligned");
+        QPAM_REQUIRE(a->gate || (a->protect_col < 0 && a->phase_col < 0),
+                     "qpam_decode_step: protect_col / phase_col need gate");
+        QPAM_REQUIRE(aligned(a->state, 16) && aligned(a->y, 8) && a->st_slot % 4 == 0 && a->st_group % 4 == 0 &&
+                         a->st_state % 4 == 0 && a->sy_slot % 2 == 0 && a->sy_group % 2 == 0,
+                     "qpam_decode_step: misaligned state or y");
+        hipStream_t s = (hipStream_t)stream;
+        return a->proj_dtype == QPAM_BF16 ? launch_decode_proj<unsigned short>(*a, s) : launch_decode_proj<float>(*a, s);
+    }
     QPAM_REQUIRE(a->state && a->q && a->k && a->v && a->gamma && a->y, "qpam_decode_step: null pointer");
     QPAM_REQUIRE(a->rope == nullptr || (a->pos != nullptr && a->rope_len >= 1 && aligned(a->rope, 16)),
                  "qpam_decode_step: rope needs positions, rope_len >= 1 and a 16-byte aligned table");

@@ -144,6 +144,76 @@ def decode_step(state, q, k, v, gamma, *, active=None, rot=None, q_scale=1.0, ou
     return y
 
 
+def decode_step_proj(state, proj, dt_bias, *, gate=None, protect_col=-1, phase_col=-1, state_offset=None,
+                     qk_norm=False, gamma_floor=0.0, active=None, q_scale=1.0, out=None, rope=None, pos=None,
+                     compact=False):
+    """decode_step with the decode prologue fused (d = 64, head decay): q, k,
+    v, the decays and the rotations of each (row, head) are formed in the kernel
+    from the layer's projection row and gate logits, as pam_prologue computes
+    them (qk-norm, GSP blend, softplus decay with floor, rotation e^{i phase}),
+    then RoPE at each slot's position and the update.
+
+    state  [S, G, M, 64, 64, 2] fp32, updated in place (G heads of one layer)
+    proj   [R, C] fp32 or bf16, the prologue's layout: q, k, v real planes
+           ([G, 64] each), their imaginary planes, G decay logits (C >= 6 G 64 + G)
+    dt_bias [G] fp32 (the summed decay biases); state_offset [M] fp32 or None
+    gate   [R, W] in proj's dtype or None: protect logits at protect_col + g,
+           phase of state m at phase_col + g M + m (-1: absent)
+    Other arguments and the return value as decode_step."""
+    _check_cuda(state, proj, dt_bias, gate, state_offset, active, rope, pos)
+    if state.dim() != 6 or state.shape[-1] != 2 or state.shape[3] != 64 or state.shape[4] != 64:
+        raise ValueError(f"state must be [S,G,M,64,64,2], got {tuple(state.shape)}")
+    n_slots, n_groups, n_states, d = state.shape[:4]
+    if compact and active is None:
+        raise ValueError("compact rows need the active slot list")
+    rows = active.numel() if compact else n_slots
+    if proj.dim() != 2 or proj.shape[0] != rows or proj.shape[1] < 6 * n_groups * d + n_groups \
+            or proj.stride(1) != 1 or proj.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"proj must be fp32/bf16 [{rows}, >= {6 * n_groups * d + n_groups}] with contiguous rows")
+    if gate is not None and (gate.dim() != 2 or gate.shape[0] != rows or gate.stride(1) != 1
+                             or gate.dtype != proj.dtype):
+        raise ValueError(f"gate must be [{rows}, W] in proj's dtype with contiguous rows")
+    if state.dtype != torch.float32 or state.stride()[-3:] != (2 * d, 2, 1):
+        raise ValueError("state must be fp32 with contiguous [d, d, 2] matrices")
+    dt_bias = dt_bias.float().contiguous()
+    state_offset = state_offset.float().contiguous() if state_offset is not None else None
+    y = out if out is not None else torch.zeros(rows, n_groups, d, 2, device=state.device, dtype=torch.float32)
+    if y.dtype not in (torch.float32, torch.bfloat16) or tuple(y.shape) != (rows, n_groups, d, 2) \
+            or y.stride()[-2:] != (2, 1):
+        raise ValueError(f"out must be fp32 or bf16 [{rows},{n_groups},{d},2] with contiguous rows")
+    if active is not None:
+        active = active.to(torch.int32).contiguous()
+    a = _lib.DecodeArgs()
+    a.n_slots, a.n_active, a.n_groups, a.n_states, a.d = n_slots, (active.numel() if active is not None else
+                                                                    n_slots), n_groups, n_states, d
+    a.vec_by_rank = int(bool(compact))
+    a.active = active.data_ptr() if active is not None else None
+    a.q_scale = float(q_scale)
+    a.state = state.data_ptr()
+    a.st_slot, a.st_group, a.st_state = state.stride(0), state.stride(1), state.stride(2)
+    a.proj, a.proj_dtype, a.proj_ld = proj.data_ptr(), _lib.QPAM_BF16 if proj.dtype == torch.bfloat16 else \
+        _lib.QPAM_F32, proj.stride(0)
+    a.qk_norm, a.gamma_floor = int(bool(qk_norm)), float(gamma_floor)
+    a.protect_col, a.phase_col = int(protect_col), int(phase_col)
+    if gate is not None:
+        a.gate, a.gate_ld = gate.data_ptr(), gate.stride(0)
+    a.dt_bias = dt_bias.data_ptr()
+    if state_offset is not None:
+        a.state_offset = state_offset.data_ptr()
+    a.y = y.data_ptr()
+    a.sy_slot, a.sy_group = y.stride(0), y.stride(1)
+    a.y_dtype = _lib.QPAM_BF16 if y.dtype == torch.bfloat16 else _lib.QPAM_F32
+    if rope is not None:
+        if pos is None:
+            raise ValueError("rope needs per-slot positions `pos`")
+        rope = rope.contiguous()
+        pos = pos.to(torch.int32).contiguous()
+        a.rope, a.pos, a.rope_len = rope.data_ptr(), pos.data_ptr(), rope.shape[0]
+    with torch.cuda.device(state.device):
+        _lib.check(_lib.lib().qpam_decode_step(a, _lib.stream_ptr(state.device)), "qpam_decode_step")
+    return y
+
+
 class _DecodeStep(torch.autograd.Function):
     """One decode step of n independent single-state (slot, head) rows, out of
     place and differentiable: (state [n,d,d,2], gamma [n] or [n,d], v, k, q
@@ -290,6 +360,17 @@ class SlotPool:
             self.ensure_len(max(self._host_pos[s] for s in self.live))
         return decode_step(self.layer_state(layer), q, k, v, gamma, active=active, rot=rot, q_scale=scale,
                            out=out, rope=self.rope, pos=self.pos, compact=compact)
+
+    def step_proj(self, layer, proj, dt_bias, active, q_scale=None, out=None, compact=False, **prologue):
+        """step with the decode prologue fused (decode_step_proj): proj
+        [rows, C] the layer's projection rows, prologue keywords as
+        decode_step_proj takes them (gate, protect_col, phase_col,
+        state_offset, qk_norm, gamma_floor)."""
+        scale = self.head_dim ** -0.5 if q_scale is None else q_scale
+        if self.live:
+            self.ensure_len(max(self._host_pos[s] for s in self.live))
+        return decode_step_proj(self.layer_state(layer), proj, dt_bias, active=active, q_scale=scale, out=out,
+                                rope=self.rope, pos=self.pos, compact=compact, **prologue)
 
     def advance(self, active, host_ids=None):
         """Move the listed slots one token on.  active: an int tensor or a list

@@ -110,7 +110,9 @@ class DecodeEngine:
                              w_out=w_out.to(dt).contiguous(), b_out=None if b_out is None else b_out.to(dt),
                              dim=dim, w_mag=None,
                              dt_bias=(layer.dt_bias if layer.dt_proj.bias is None
-                                      else layer.dt_bias + layer.dt_proj.bias).float().contiguous())
+                                      else layer.dt_bias + layer.dt_proj.bias).float().contiguous(),
+                             state_offset=(layer.state_dt_offset.float().contiguous() if self.n_states > 1
+                                           else None))
                 # the protect gate and the phase projection both read |x|: one GEMM for both
                 if (layer.use_gsp and not layer.gate_content_aware and self.n_states > 1
                         and not layer.routing_content_aware):
@@ -193,6 +195,18 @@ class DecodeEngine:
             return x.new_zeros(0, dim, 2)
         x = x.contiguous() if x.dtype in (torch.float32, torch.bfloat16) else x.float().contiguous()
         proj = F.linear(x.view(n, 2 * dim).to(self.dtype), w["w_in"], w["b_in"]).view(n, 1, -1)
+        if not layer.use_rope:
+            raise NotImplementedError("DecodeEngine applies RoPE per slot; layers without RoPE are not supported")
+        out = torch.empty(n, h, d, 2, device=x.device, dtype=self.dtype)
+        if w["w_mag"] is not None and not layer.state_compete:
+            # the gate logits from |x| in one launch, the prologue inside the decode kernel
+            gl = mag_linear(x, w["w_mag"], w["b_mag"], out_dtype=self.dtype)
+            y = self.pool.step_proj(layer_idx, proj.view(n, -1), w["dt_bias"], slots, q_scale=d ** -0.5,
+                                    compact=True, out=out, gate=gl, protect_col=0 if layer.use_gsp else -1,
+                                    phase_col=(h if layer.use_gsp else 0) if m > 1 else -1,
+                                    state_offset=w["state_offset"], qk_norm=layer.qk_norm,
+                                    gamma_floor=layer.gamma_floor or 0.0)
+            return F.linear(y.view(n, 2 * h * d), w["w_out"], w["b_out"]).view(n, dim, 2)
         protect, phase, routing = self._gates(layer, x, w)
         # the prologue writes fp32 planes (what the decode kernel reads) from a bf16 or fp32 projection
         (qr, qi), (kr, ki), (vr, vi), gamma, rot = prologue_decode(
@@ -205,12 +219,9 @@ class DecodeEngine:
         q, k, v = ((re[:, :, 0], im[:, :, 0]) for re, im in ((qr, qi), (kr, ki), (vr, vi)))
         g = gamma[..., 0].permute(1, 2, 0)                                    # [n, H, K] view
         r = tuple(x[..., 0].permute(1, 2, 0) for x in rot) if rot is not None else None  # planar [n, H, K] views
-        if not layer.use_rope:
-            raise NotImplementedError("DecodeEngine applies RoPE per slot; layers without RoPE are not supported")
         # every listed slot is live, so the kernel writes every row of y: no zero fill
         # y in the GEMM dtype straight from the decode kernel (no conversion pass before o_proj)
-        y = self.pool.step(layer_idx, q, k, v, g, slots, rot=r, q_scale=d ** -0.5, compact=True,
-                           out=torch.empty(n, h, d, 2, device=x.device, dtype=self.dtype))
+        y = self.pool.step(layer_idx, q, k, v, g, slots, rot=r, q_scale=d ** -0.5, compact=True, out=out)
         return F.linear(y.view(n, 2 * h * d), w["w_out"], w["b_out"]).view(n, dim, 2)
 
     def _layers(self, x, slots, between):

@@ -317,3 +317,47 @@ def test_decode_bf16_output_equals_rounded_fp32(gpu_lib, d, M, use_rot):
     torch.cuda.synchronize()
     assert torch.equal(outs[1][0], outs[0][0].to(torch.bfloat16))
     assert torch.equal(outs[1][1], outs[0][1])
+
+
+@pytest.mark.parametrize("M,qk_norm,floor,gsp,dtype", [(3, False, 0.0, True, torch.bfloat16), (3, True, 0.25, True, torch.float32),
+                                                       (1, False, 0.0, False, torch.bfloat16), (4, True, 0.0, False, torch.float32)])
+def test_decode_step_proj_matches_prologue_then_decode(M, qk_norm, floor, gsp, dtype):
+    """The decode prologue fused into the kernel (decode_step_proj) against the
+    separate inference prologue (prologue_decode) followed by decode_step on the
+    same projection rows, gate logits, states and positions."""
+    from qllm2_amd.decode import build_rope_cache, decode_step, decode_step_proj
+    from qllm2_amd.pam_prologue import prologue_decode, proj_columns
+    dev = "cuda"
+    S, H, d, n = 11, 5, 64, 7
+    g = torch.Generator(device=dev).manual_seed(M * 10 + int(qk_norm))
+    C = proj_columns(H)
+    proj = (torch.randn(n, C, device=dev, generator=g) * 0.5).to(dtype)
+    W = (H if gsp else 0) + (H * M if M > 1 else 0)
+    gate = (torch.randn(n, max(W, 1), device=dev, generator=g) * 1.5).to(dtype)
+    dt_bias = torch.randn(H, device=dev, generator=g) - 1.0
+    off = torch.linspace(-0.5, 0.5, M, device=dev) if M > 1 else None
+    state0 = torch.randn(S, H, M, d, d, 2, device=dev, generator=g) * 0.1
+    active = torch.tensor([9, 0, 4, 10, 2, 7, 5], device=dev, dtype=torch.int32)
+    rope = build_rope_cache(64, d, device=dev)
+    pos = torch.randint(0, 60, (S,), device=dev, generator=g, dtype=torch.int32)
+    pcol = 0 if gsp else -1
+    fcol = (H if gsp else 0) if M > 1 else -1
+    st_a = state0.clone()
+    y_a = decode_step_proj(st_a, proj, dt_bias, gate=gate if W else None, protect_col=pcol, phase_col=fcol,
+                           state_offset=off, qk_norm=qk_norm, gamma_floor=floor, active=active, q_scale=d ** -0.5,
+                           rope=rope, pos=pos, compact=True)
+    prot = gate[:, :H].view(n, 1, H) if gsp else None
+    ph = gate[:, fcol:fcol + H * M].view(n, 1, H, M) if M > 1 else None
+    (qr, qi), (kr, ki), (vr, vi), gamma, rot = prologue_decode(proj.view(n, 1, C), dt_bias, n_heads=H, n_states=M,
+                                                                state_offset=off, protect=prot, phase=ph,
+                                                                qk_norm=qk_norm, gamma_floor=floor)
+    q, k, v = ((re[:, :, 0], im[:, :, 0]) for re, im in ((qr, qi), (kr, ki), (vr, vi)))
+    gm = gamma[..., 0].permute(1, 2, 0)
+    r = tuple(x[..., 0].permute(1, 2, 0) for x in rot) if rot is not None else None
+    st_b = state0.clone()
+    y_b = decode_step(st_b, q, k, v, gm, active=active, rot=r, q_scale=d ** -0.5, rope=rope, pos=pos, compact=True)
+    scale = lambda t: t.abs().max().clamp_min(1e-6)
+    assert ((y_a - y_b).abs().max() / scale(y_b)).item() < 1e-5
+    assert ((st_a - st_b).abs().max() / scale(st_b)).item() < 1e-5
+    untouched = [s for s in range(S) if s not in active.tolist()]
+    assert torch.equal(st_a[untouched], state0[untouched])

@@ -320,11 +320,23 @@ __global__ void __launch_bounds__((DecodeShape<64, multi_threads<64>()>::THREADS
     }
     apply_rope<D>(a, slot, cp, qv, kv);
     const float q0r = qv.x * a.q_scale, q0i = qv.y * a.q_scale, q1r = qv.z * a.q_scale, q1i = qv.w * a.q_scale;
-    // the gates of (row, group): the protect probability, then per state the decay and rotation
+    // the gates of (row, group), formed once per block (lane m of wave 0: state m's
+    // decay and rotation) while the state loads are in flight, shared through LDS
+    __shared__ float sc[4][3], skeep;
     const int64_t grow = (int64_t)vr * a.gate_ld;
-    const float p = (a.gate && a.protect_col >= 0) ? p_sigmoid(pld<TP>(a.gate, grow + a.protect_col + g)) : 0.f;
-    const float keep = 1.f - p;
-    const float dt = pld<TP>(a.proj, prow + 6 * GD + g) + a.dt_bias[g];
+    if (tid < MS) {
+        const float p = (a.gate && a.protect_col >= 0) ? p_sigmoid(pld<TP>(a.gate, grow + a.protect_col + g)) : 0.f;
+        const float dt = pld<TP>(a.proj, prow + 6 * GD + g) + a.dt_bias[g];
+        float base = expf(-p_softplus(dt + (a.state_offset ? a.state_offset[tid] : 0.f)));
+        if (a.gamma_floor > 0.f) base = a.gamma_floor + (1.f - a.gamma_floor) * base;
+        sc[tid][0] = base * (1.f - p) + p;
+        float rr = 1.f, ri = 0.f;
+        if (a.gate && a.phase_col >= 0) sincosf(pld<TP>(a.gate, grow + a.phase_col + g * MS + tid), &ri, &rr);
+        sc[tid][1] = rr, sc[tid][2] = ri;
+        if (tid == 0) skeep = 1.f - p;
+    }
+    __syncthreads();
+    const float keep = skeep;
     float2 vv[S::ITERS];
 #pragma unroll
     for (int it = 0; it < S::ITERS; ++it) {
@@ -337,11 +349,7 @@ __global__ void __launch_bounds__((DecodeShape<64, multi_threads<64>()>::THREADS
     for (int j = 0; j < S::NV; ++j) tot[j] = 0.f;
 #pragma unroll
     for (int m = 0; m < MS; ++m) {
-        float base = expf(-p_softplus(dt + (a.state_offset ? a.state_offset[m] : 0.f)));
-        if (a.gamma_floor > 0.f) base = a.gamma_floor + (1.f - a.gamma_floor) * base;
-        const float gam = base * (1.f - p) + p;
-        float rr = 1.f, ri = 0.f;
-        if (a.gate && a.phase_col >= 0) sincosf(pld<TP>(a.gate, grow + a.phase_col + g * MS + m), &ri, &rr);
+        const float gam = sc[m][0], rr = sc[m][1], ri = sc[m][2];
 #pragma unroll
         for (int it = 0; it < S::ITERS; ++it) {
             const float o0r = vv[it].x * kv.x + vv[it].y * kv.y, o0i = vv[it].y * kv.x - vv[it].x * kv.y;

@@ -61,6 +61,12 @@
  *   qpam_cweight_unpack its backward (the weights' gradients)
  *   qpam_slice_sum      the gate projections' weight gradient (v11/model.py:228,
  *                       646) summed over row slices and cast
+ *   qpam_resid_norm     the decode's residual adds and pre-norms, V11Block.forward
+ *                       (v11/model.py:1039-1049) with ComplexNorm
+ *                       (v11/complex_ops.py:188-189)
+ *   qpam_cgu_mix        the CGU's activation and gate between its projections,
+ *                       ComplexGatedUnit.forward (v11/complex_ops.py:216-220;
+ *                       activations :102-143)
  */
 #ifndef QPAM_H
 #define QPAM_H
@@ -601,6 +607,66 @@ typedef struct {
 size_t qpam_cplx_workspace_size(const qpam_cplx_args *a);
 int qpam_cplx_fwd(const qpam_cplx_args *a, void *stream);
 int qpam_cplx_bwd(const qpam_cplx_args *a, void *stream);
+
+/* --------------------------------------------- decode block glue (ABI 13) --
+ * Inference only: the work between the GEMMs of a V11 block in the model-level
+ * decode, one launch each (the reference runs each as its own torch ops).
+ *
+ * qpam_resid_norm: the residual add then the next pre-norm (V11Block.forward,
+ * v11/model.py:1039-1049; ComplexNorm, v11/complex_ops.py:188-189):
+ *   x <- x + y * y_scale[0]        (when y is given; fp32 product and sum)
+ *   out = ComplexNorm(x; norm_scale, eps) in out_dtype
+ * x fp32 [rows][dim][2] (row stride ldx floats) is updated in place; y in y_dtype
+ * (row stride ldy elements); y_scale is a device fp32 scalar (the block's
+ * cgu_scale / pam_scale parameter: a captured graph follows weight updates);
+ * norm_scale fp32 [dim].  dim a multiple of 4, at most 2048; row starts 16-byte
+ * aligned.  out may not alias x or y. */
+typedef struct {
+    int64_t rows;
+    int32_t dim;
+    float eps;
+    float *x;
+    int64_t ldx;
+    const void *y;          /* NULL: no residual, out = ComplexNorm(x) */
+    int32_t y_dtype;
+    int64_t ldy;
+    const float *y_scale;
+    const float *norm_scale;
+    void *out;
+    int32_t out_dtype;
+    int64_t ldo;
+} qpam_resid_norm_args;
+
+int qpam_resid_norm(const qpam_resid_norm_args *a, void *stream);
+
+/* qpam_cgu_mix: ComplexGatedUnit.forward between its projections
+ * (v11/complex_ops.py:216-220): gu [rows][4 hid] in gu_dtype (row stride ldg
+ * elements) holds the gate projection's hid complex values (re, im
+ * interleaved) and then the up projection's;
+ *   out = cgu_gate(gate, act(up))  in out_dtype [rows][hid][2] (row stride ldo)
+ * with the formulas of qpam_cplx_fwd and act (parameters fp32 [hid]):
+ *   MOD_RELU   bias                           (beta NULL)
+ *   MOD_SWISH  bias, beta                     (phase_alpha, phase_beta NULL)
+ *   phase-modulated (PhaseModulatedActivation, v11/complex_ops.py:125-143):
+ *              bias, beta, phase_alpha, phase_beta: ModSwish's magnitude with
+ *              the phase turned by phase_alpha |u| + phase_beta.
+ * hid a multiple of 4; row starts and parameters 16-byte aligned. */
+typedef struct {
+    int64_t rows;
+    int32_t hid;
+    const void *gu;
+    int32_t gu_dtype;
+    int64_t ldg;
+    const float *bias;
+    const float *beta;
+    const float *phase_alpha;
+    const float *phase_beta;
+    void *out;
+    int32_t out_dtype;
+    int64_t ldo;
+} qpam_cgu_mix_args;
+
+int qpam_cgu_mix(const qpam_cgu_mix_args *a, void *stream);
 
 /* -------------------------------------------------------------------- CE --
  * Tied complex LM-head cross-entropy over hidden rows H [N, D] and weights

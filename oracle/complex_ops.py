@@ -7,6 +7,7 @@ ComplexNorm / ModSwish / ModReLU / CGU in v11/complex_ops.py):
   mod_swish     z / (|z| + 1e-8) * |z| * sigmoid(beta |z| + bias)
   mod_relu      z / (|z| + 1e-8) * relu(|z| + bias)
   cgu_gate      sigmoid(|g|) * (g / (|g| + 1e-8)) (x) up          (complex product)
+  phase_mod     (z / (|z| + 1e-8)) (x) e^{i (alpha |z| + beta_ph)} * |z| * sigmoid(beta |z| + bias)
 Gradients are torch autograd through these forms.  The *_backward functions
 restate the closed forms of the reference's autograd Functions
 (v11/triton_kernels.py:209-395) so that tests can check the two agree.
@@ -37,6 +38,18 @@ def mod_relu(z, bias):
     """v11/triton_kernels.py:504-508 (_pt_mod_relu)."""
     mag = _mag(z)
     return (z / (mag.unsqueeze(-1) + 1e-8)) * F.relu(mag + bias).unsqueeze(-1)
+
+
+def phase_mod(z, bias, beta, phase_alpha, phase_beta):
+    """PhaseModulatedActivation.forward (v11/complex_ops.py:135-143): ModSwish's
+    magnitude; the unit phase z / (|z| + 1e-8) turned by the angle
+    phase_alpha |z| + phase_beta (a complex product with (cos, sin))."""
+    mag = _mag(z)
+    act = mag * torch.sigmoid(beta * mag + bias)
+    pr, pi = z[..., 0] / (mag + 1e-8), z[..., 1] / (mag + 1e-8)
+    ang = phase_alpha * mag + phase_beta
+    c, s = torch.cos(ang), torch.sin(ang)
+    return torch.stack([(pr * c - pi * s) * act, (pr * s + pi * c) * act], dim=-1)
 
 
 def cgu_gate(gate, up):

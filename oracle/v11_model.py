@@ -75,6 +75,20 @@ class ModReLU(nn.Module):
         return C.mod_relu(z, self.bias)
 
 
+class PhaseModulatedActivation(nn.Module):
+    """PhaseModulatedActivation (v11/complex_ops.py:125-143)."""
+
+    def __init__(self, bias, beta, phase_alpha, phase_beta):
+        super().__init__()
+        self.bias = nn.Parameter(bias.clone())
+        self.beta = nn.Parameter(beta.clone())
+        self.phase_alpha = nn.Parameter(phase_alpha.clone())
+        self.phase_beta = nn.Parameter(phase_beta.clone())
+
+    def forward(self, z):
+        return C.phase_mod(z, self.bias, self.beta, self.phase_alpha, self.phase_beta)
+
+
 class ComplexGatedUnit(nn.Module):
     """ComplexGatedUnit (v11/complex_ops.py:200-220)."""
 
@@ -82,8 +96,12 @@ class ComplexGatedUnit(nn.Module):
         super().__init__()
         lin = lambda name: ComplexLinear(p[f"{prefix}.{name}.weight_real"], p[f"{prefix}.{name}.weight_imag"])
         self.gate_proj, self.up_proj, self.down_proj = lin("gate_proj"), lin("up_proj"), lin("down_proj")
+        # _build_activation (v11/complex_ops.py:192-197): 'swish', 'phase_mod', else ModReLU
         if activation == "swish":
             self.act = ModSwish(p[f"{prefix}.act.bias"], p[f"{prefix}.act.beta"])
+        elif activation == "phase_mod":
+            self.act = PhaseModulatedActivation(p[f"{prefix}.act.bias"], p[f"{prefix}.act.beta"],
+                                                p[f"{prefix}.act.phase_alpha"], p[f"{prefix}.act.phase_beta"])
         else:
             self.act = ModReLU(p[f"{prefix}.act.bias"])
 
@@ -158,9 +176,12 @@ def make_model_params(cfg, n_layers, vocab, seed, expand=2, activation="swish", 
         for name, (o, n_in) in (("gate_proj", (hid, dim)), ("up_proj", (hid, dim)), ("down_proj", (dim, hid))):
             p[f"{b}.cgu.{name}.weight_real"] = rn(o, n_in, std=(2 * n_in) ** -0.5)
             p[f"{b}.cgu.{name}.weight_imag"] = rn(o, n_in, std=(2 * n_in) ** -0.5)
-        p[f"{b}.cgu.act.bias"] = rn(hid, std=0.1) - (0.0 if activation == "swish" else 0.1)
-        if activation == "swish":
+        p[f"{b}.cgu.act.bias"] = rn(hid, std=0.1) - (0.0 if activation in ("swish", "phase_mod") else 0.1)
+        if activation in ("swish", "phase_mod"):
             p[f"{b}.cgu.act.beta"] = 1.0 + rn(hid, std=0.2)
+        if activation == "phase_mod":  # angles of a radian or so, so that the rotation matters
+            p[f"{b}.cgu.act.phase_alpha"] = rn(hid, std=0.5)
+            p[f"{b}.cgu.act.phase_beta"] = rn(hid, std=1.0)
         p[f"{b}.cgu_scale"] = torch.tensor(0.7, dtype=dtype)
         p[f"{b}.pam_scale"] = torch.tensor(0.6, dtype=dtype)
         for k, v in V.make_params(cfg, seed + 31 * (i + 1), dtype).items():

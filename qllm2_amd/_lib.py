@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -209,6 +209,22 @@ class CWeightArgs(ctypes.Structure):
 
 QPAM_CW_IN, QPAM_CW_OUT = 0, 1
 
+
+class ResidNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_i64), ("dim", c_i32), ("eps", c_f32), ("x", c_ptr), ("ldx", c_i64), ("y", c_ptr),
+        ("y_dtype", c_i32), ("ldy", c_i64), ("y_scale", c_ptr), ("norm_scale", c_ptr), ("out", c_ptr),
+        ("out_dtype", c_i32), ("ldo", c_i64),
+    ]
+
+
+class CguMixArgs(ctypes.Structure):
+    _fields_ = [
+        ("rows", c_i64), ("hid", c_i32), ("gu", c_ptr), ("gu_dtype", c_i32), ("ldg", c_i64), ("bias", c_ptr),
+        ("beta", c_ptr), ("phase_alpha", c_ptr), ("phase_beta", c_ptr), ("out", c_ptr), ("out_dtype", c_i32),
+        ("ldo", c_i64),
+    ]
+
 SIGNATURES = {
     "qpam_version": (ctypes.c_int, []),
     "qpam_last_error": (ctypes.c_char_p, []),
@@ -230,6 +246,8 @@ SIGNATURES = {
     "qpam_cplx_workspace_size": (ctypes.c_size_t, [ctypes.POINTER(CplxArgs)]),
     "qpam_cplx_fwd": (ctypes.c_int, [ctypes.POINTER(CplxArgs), c_ptr]),
     "qpam_cplx_bwd": (ctypes.c_int, [ctypes.POINTER(CplxArgs), c_ptr]),
+    "qpam_resid_norm": (ctypes.c_int, [ctypes.POINTER(ResidNormArgs), c_ptr]),
+    "qpam_cgu_mix": (ctypes.c_int, [ctypes.POINTER(CguMixArgs), c_ptr]),
     "qpam_prologue_fwd": (ctypes.c_int, [ctypes.POINTER(PrologueArgs), c_ptr]),
     "qpam_prologue_bwd": (ctypes.c_int, [ctypes.POINTER(PrologueBwdArgs), c_ptr]),
     "qpam_cabs_fwd": (ctypes.c_int, [c_i32, c_i64, c_ptr, c_ptr, c_ptr]),

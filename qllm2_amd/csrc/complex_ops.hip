@@ -1001,6 +1001,183 @@ int fwd_t(const qpam_cplx_args *a, hipStream_t stream) { return vec4(a) ? fwd<T,
 template <typename T>
 int bwd_t(const qpam_cplx_args *a, hipStream_t stream) { return vec4(a) ? bwd<T, 4>(a, stream) : bwd<T, 1>(a, stream); }
 
+// ------------------------------------------------ decode block glue --
+// Inference: the work between the GEMMs of a V11 block in the model-level
+// decode (a few hundred rows), one launch each instead of the casts, splits,
+// scaled adds and norms torch runs there one at a time.
+
+// four consecutive complex values, plain (cached) 16- / 32-byte accesses: the
+// outputs are read back at once by the next GEMM
+template <typename T> struct Row4;
+template <> struct Row4<float> {
+    __device__ __forceinline__ static void load(const float *p, float (&re)[4], float (&im)[4]) {
+        const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+        re[0] = a.x, im[0] = a.y, re[1] = a.z, im[1] = a.w, re[2] = b.x, im[2] = b.y, re[3] = b.z, im[3] = b.w;
+    }
+    __device__ __forceinline__ static void store(float *p, const float (&re)[4], const float (&im)[4]) {
+        *reinterpret_cast<float4 *>(p) = make_float4(re[0], im[0], re[1], im[1]);
+        *reinterpret_cast<float4 *>(p + 4) = make_float4(re[2], im[2], re[3], im[3]);
+    }
+};
+template <> struct Row4<unsigned short> {
+    __device__ __forceinline__ static void load(const unsigned short *p, float (&re)[4], float (&im)[4]) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(p);
+        const unsigned u[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) re[k] = __uint_as_float(u[k] << 16), im[k] = __uint_as_float(u[k] & 0xFFFF0000u);
+    }
+    __device__ __forceinline__ static void store(unsigned short *p, const float (&re)[4], const float (&im)[4]) {
+        *reinterpret_cast<uint4 *>(p) = make_uint4(pack_bf16x2(re[0], im[0]), pack_bf16x2(re[1], im[1]),
+                                                   pack_bf16x2(re[2], im[2]), pack_bf16x2(re[3], im[3]));
+    }
+};
+
+struct ResidNormParams {
+    int64_t rows;
+    int dim;
+    float eps;
+    float *x;
+    int64_t ldx;
+    const void *y;
+    int64_t ldy;
+    const float *y_scale;
+    const float *scale;
+    void *out;
+    int64_t ldo;
+};
+
+// One block per row, a thread per four complex columns (threads past dim / 4
+// add zero to the row sum).  x + y * s is rounded as a product and then a sum
+// (the reference's two tensor ops); the norm follows norm_fwd_team_kernel's
+// operation order (per-thread sum over its four columns, wave sums, then the
+// waves in order), so a row without y matches qpam_cplx_fwd's ComplexNorm.
+template <typename TY, typename TO>
+__global__ void __launch_bounds__(TEAM_MAX) resid_norm_kernel(ResidNormParams q) {
+    __shared__ float red[TEAM_MAX / 64];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63, nw = blockDim.x >> 6;
+    const int64_t row = blockIdx.x;
+    const int c = 4 * threadIdx.x;
+    const bool on = c < q.dim;
+    float re[4] = {0.f, 0.f, 0.f, 0.f}, im[4] = {0.f, 0.f, 0.f, 0.f};
+    float ss = 0.f;
+    if (on) {
+        float *xr = q.x + row * q.ldx + 2 * c;
+        Row4<float>::load(xr, re, im);
+        if (q.y) {
+            float yr[4], yi[4];
+            Row4<TY>::load(static_cast<const TY *>(q.y) + row * q.ldy + 2 * c, yr, yi);
+            const float s = *q.y_scale;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                // two roundings, as the reference's product and sum (no fused multiply-add)
+#pragma clang fp contract(off)
+                re[k] = re[k] + yr[k] * s;
+                im[k] = im[k] + yi[k] * s;
+            }
+            Row4<float>::store(xr, re, im);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float m = magnitude(re[k], im[k]);
+            ss += m * m;
+        }
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[w] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int k = 0; k < nw; ++k) tot += red[k];
+    if (!on) return;
+    const float inv_rms = rcp(sqrtf(tot / q.dim + q.eps));
+    const float4 s4 = *reinterpret_cast<const float4 *>(q.scale + c);
+    const float sc[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float m = magnitude(re[k], im[k]);
+        const float f = m * inv_rms * sc[k] * rcp(m + MAG_EPS);
+        re[k] *= f;
+        im[k] *= f;
+    }
+    Row4<TO>::store(static_cast<TO *>(q.out) + row * q.ldo + 2 * c, re, im);
+}
+
+struct CguMixParams {
+    int64_t rows;
+    int hid;
+    const void *gu;
+    int64_t ldg;
+    const float *bias, *beta, *pa, *pb;
+    void *out;
+    int64_t ldo;
+};
+
+// ACT 1: mod swish, 2: mod relu, 3: phase-modulated; a thread per four complex
+// columns of a row (grid-stride), the activation of up and then the gate, each
+// with pointwise_fwd_kernel's formulas
+template <typename TG, typename TO, int ACT>
+__global__ void __launch_bounds__(THREADS) cgu_mix_kernel(CguMixParams q) {
+    const int groups = q.hid / 4;
+    const int64_t n = q.rows * groups;
+    for (int64_t j = (int64_t)blockIdx.x * THREADS + threadIdx.x; j < n; j += (int64_t)gridDim.x * THREADS) {
+        const int64_t row = j / groups;
+        const int c = 4 * (int)(j - row * groups);
+        const TG *g = static_cast<const TG *>(q.gu) + row * q.ldg;
+        float gr[4], gi[4], ur[4], ui[4];
+        Row4<TG>::load(g + 2 * c, gr, gi);
+        Row4<TG>::load(g + 2 * q.hid + 2 * c, ur, ui);
+        const float4 b4 = *reinterpret_cast<const float4 *>(q.bias + c);
+        const float bs[4] = {b4.x, b4.y, b4.z, b4.w};
+        float bt[4] = {0.f, 0.f, 0.f, 0.f}, pa[4] = {0.f, 0.f, 0.f, 0.f}, pb[4] = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (ACT != 2) {
+            const float4 t4 = *reinterpret_cast<const float4 *>(q.beta + c);
+            bt[0] = t4.x, bt[1] = t4.y, bt[2] = t4.z, bt[3] = t4.w;
+        }
+        if constexpr (ACT == 3) {
+            const float4 a4 = *reinterpret_cast<const float4 *>(q.pa + c), c4 = *reinterpret_cast<const float4 *>(q.pb + c);
+            pa[0] = a4.x, pa[1] = a4.y, pa[2] = a4.z, pa[3] = a4.w;
+            pb[0] = c4.x, pb[1] = c4.y, pb[2] = c4.z, pb[3] = c4.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float m = magnitude(ur[k], ui[k]), inv = rcp(m + MAG_EPS);
+            const float act = ACT == 2 ? fmaxf(m + bs[k], 0.f) : m * sigmoidf(bt[k] * m + bs[k]);
+            if constexpr (ACT == 3) {
+                // unit phase turned by phase_alpha |u| + phase_beta, then scaled
+                float sn, cs;
+                sincosf(pa[k] * m + pb[k], &sn, &cs);
+                const float pr = ur[k] * inv, pi = ui[k] * inv;
+                ur[k] = (pr * cs - pi * sn) * act;
+                ui[k] = (pr * sn + pi * cs) * act;
+            } else {
+                ur[k] *= inv * act;
+                ui[k] *= inv * act;
+            }
+            const float mg = magnitude(gr[k], gi[k]), ig = rcp(mg + MAG_EPS), gm = sigmoidf(mg);
+            const float pr = gr[k] * ig, pi = gi[k] * ig;
+            gr[k] = (pr * ur[k] - pi * ui[k]) * gm;
+            gi[k] = (pr * ui[k] + pi * ur[k]) * gm;
+        }
+        Row4<TO>::store(static_cast<TO *>(q.out) + row * q.ldo + 2 * c, gr, gi);
+    }
+}
+
+bool al16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+int elems16(int dtype) { return dtype == QPAM_BF16 ? 8 : 4; }  // elements per 16 bytes
+
+template <typename TY, typename TO>
+void launch_resid_norm(const ResidNormParams &q, hipStream_t s) {
+    const int threads = (q.dim / 4 + 63) / 64 * 64;
+    hipLaunchKernelGGL((resid_norm_kernel<TY, TO>), dim3((unsigned)q.rows), dim3(threads), 0, s, q);
+}
+
+template <typename TG, typename TO>
+void launch_cgu_mix(const CguMixParams &q, int act, hipStream_t s) {
+    const dim3 grid(flat_blocks(q.rows * (q.hid / 4)));
+    if (act == 1) hipLaunchKernelGGL((cgu_mix_kernel<TG, TO, 1>), grid, dim3(THREADS), 0, s, q);
+    else if (act == 2) hipLaunchKernelGGL((cgu_mix_kernel<TG, TO, 2>), grid, dim3(THREADS), 0, s, q);
+    else hipLaunchKernelGGL((cgu_mix_kernel<TG, TO, 3>), grid, dim3(THREADS), 0, s, q);
+}
+
 }  // namespace
 }  // namespace cplx
 }  // namespace qpam
@@ -1039,4 +1216,59 @@ extern "C" int qpam_cplx_bwd(const qpam_cplx_args *a, void *stream) {
         return n > 0 ? qpam::launch_status("qpam_cplx_bwd (zero parameter gradients)") : QPAM_OK;
     }
     return a->dtype == QPAM_BF16 ? bwd_t<unsigned short>(a, (hipStream_t)stream) : bwd_t<float>(a, (hipStream_t)stream);
+}
+
+extern "C" int qpam_resid_norm(const qpam_resid_norm_args *a, void *stream) {
+    using namespace qpam::cplx;
+    QPAM_REQUIRE(a != nullptr, "qpam_resid_norm: null arguments");
+    QPAM_REQUIRE(a->rows >= 0 && a->rows <= INT32_MAX, "qpam_resid_norm: rows = %lld", (long long)a->rows);
+    QPAM_REQUIRE(a->dim >= 4 && a->dim % 4 == 0 && a->dim <= 4 * TEAM_MAX,
+                 "qpam_resid_norm: dim %d must be a multiple of 4 and at most %d", a->dim, 4 * TEAM_MAX);
+    QPAM_REQUIRE(a->out_dtype == QPAM_F32 || a->out_dtype == QPAM_BF16, "qpam_resid_norm: out_dtype %d", a->out_dtype);
+    QPAM_REQUIRE(a->y == nullptr || a->y_dtype == QPAM_F32 || a->y_dtype == QPAM_BF16,
+                 "qpam_resid_norm: y_dtype %d", a->y_dtype);
+    if (a->rows == 0) return QPAM_OK;
+    QPAM_REQUIRE(a->x && a->out && a->norm_scale && al16(a->x) && al16(a->out) && al16(a->norm_scale),
+                 "qpam_resid_norm: x, out and norm_scale must be set and 16-byte aligned");
+    QPAM_REQUIRE(a->ldx >= 2 * a->dim && a->ldx % 4 == 0 && a->ldo >= 2 * a->dim && a->ldo % elems16(a->out_dtype) == 0,
+                 "qpam_resid_norm: row strides must cover a row and keep 16-byte row starts");
+    QPAM_REQUIRE(a->y == nullptr || (a->y_scale && al16(a->y) && a->ldy >= 2 * a->dim && a->ldy % elems16(a->y_dtype) == 0),
+                 "qpam_resid_norm: y needs y_scale, 16-byte row starts and a row stride covering a row");
+    QPAM_REQUIRE(a->out != (void *)a->x && a->out != a->y, "qpam_resid_norm: out may not alias x or y");
+    ResidNormParams q{a->rows, a->dim, a->eps, a->x, a->ldx, a->y, a->ldy, a->y_scale, a->norm_scale, a->out, a->ldo};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool ybf = a->y && a->y_dtype == QPAM_BF16, obf = a->out_dtype == QPAM_BF16;
+    if (ybf && obf) launch_resid_norm<unsigned short, unsigned short>(q, s);
+    else if (ybf) launch_resid_norm<unsigned short, float>(q, s);
+    else if (obf) launch_resid_norm<float, unsigned short>(q, s);
+    else launch_resid_norm<float, float>(q, s);
+    return qpam::launch_status("qpam_resid_norm");
+}
+
+extern "C" int qpam_cgu_mix(const qpam_cgu_mix_args *a, void *stream) {
+    using namespace qpam::cplx;
+    QPAM_REQUIRE(a != nullptr, "qpam_cgu_mix: null arguments");
+    QPAM_REQUIRE(a->rows >= 0 && a->hid >= 4 && a->hid % 4 == 0, "qpam_cgu_mix: rows %lld, hid %d (a multiple of 4)",
+                 (long long)a->rows, a->hid);
+    QPAM_REQUIRE((a->gu_dtype == QPAM_F32 || a->gu_dtype == QPAM_BF16) && (a->out_dtype == QPAM_F32 || a->out_dtype == QPAM_BF16),
+                 "qpam_cgu_mix: gu_dtype %d / out_dtype %d", a->gu_dtype, a->out_dtype);
+    QPAM_REQUIRE((a->phase_alpha == nullptr) == (a->phase_beta == nullptr),
+                 "qpam_cgu_mix: phase_alpha and phase_beta are given together");
+    QPAM_REQUIRE(a->phase_alpha == nullptr || a->beta != nullptr, "qpam_cgu_mix: the phase-modulated activation needs beta");
+    if (a->rows == 0) return QPAM_OK;
+    QPAM_REQUIRE(a->gu && a->out && a->bias && al16(a->gu) && al16(a->out) && al16(a->bias) &&
+                     (a->beta == nullptr || al16(a->beta)) && (a->phase_alpha == nullptr || (al16(a->phase_alpha) && al16(a->phase_beta))),
+                 "qpam_cgu_mix: gu, out and the parameters must be set and 16-byte aligned");
+    QPAM_REQUIRE(a->ldg >= 4 * (int64_t)a->hid && a->ldg % elems16(a->gu_dtype) == 0 && a->ldo >= 2 * (int64_t)a->hid &&
+                     a->ldo % elems16(a->out_dtype) == 0,
+                 "qpam_cgu_mix: row strides must cover a row and keep 16-byte row starts");
+    const int act = a->beta == nullptr ? 2 : a->phase_alpha == nullptr ? 1 : 3;
+    CguMixParams q{a->rows, a->hid, a->gu, a->ldg, a->bias, a->beta, a->phase_alpha, a->phase_beta, a->out, a->ldo};
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool gbf = a->gu_dtype == QPAM_BF16, obf = a->out_dtype == QPAM_BF16;
+    if (gbf && obf) launch_cgu_mix<unsigned short, unsigned short>(q, act, s);
+    else if (gbf) launch_cgu_mix<unsigned short, float>(q, act, s);
+    else if (obf) launch_cgu_mix<float, unsigned short>(q, act, s);
+    else launch_cgu_mix<float, float>(q, act, s);
+    return qpam::launch_status("qpam_cgu_mix");
 }

@@ -9,12 +9,14 @@ step runs only the live rows:
 
   embedding rows of the tokens (the tied table, interleaved [V, dim, 2])
   -> ComplexNorm                                     (qpam_cplx_fwd)
-  -> per block (v11/model.py:1038-1049):
-       x += cgu_scale * down(cgu_gate(gate(h), act(up(h)))), h = norm1(x)
-            (gate and up in one GEMM from h; ModSwish / ModReLU, the CGU gate
-            and the norms on the HIP complex kernels)
+  -> per block (v11/model.py:1038-1049), h = norm1(x) from the step before:
+       x += cgu_scale * down(cgu_gate(gate(h), act(up(h))))
+            (gate and up in one GEMM from h; the activation and the gate in
+            one launch, qpam_cgu_mix, writing the down GEMM's input)
        x += pam_scale * PAM(norm2(x))               (DecodeEngine.layer_step:
-            projection GEMM, prologue kernel, one decode launch, o_proj GEMM)
+            projection GEMM, |x| gate kernel, one decode launch, o_proj GEMM)
+     each residual add fused with the norm that follows it (qpam_resid_norm:
+     x updated in place, the normed rows written in the GEMM dtype)
   -> output_norm -> lm_head_proj (GEMM + bias) -> lm_head_norm
   -> tied logits Re(lm . conj(E)) (one GEMM against the interleaved table).
 
@@ -34,12 +36,76 @@ pam_scale, output_norm, lm_head_proj, lm_head_norm); learned position
 embeddings (use_learned_pos) are not supported.
 """
 
+import ctypes
+
 import torch
 import torch.nn.functional as F
 
+from . import _lib
 from . import pam_layer
 from . import triton_kernels as tk
 from .engine import DecodeEngine
+
+MAX_DIM = 2048  # qpam_resid_norm: a thread per four complex columns, 512 per row
+
+
+def _code(t):
+    return _lib.QPAM_BF16 if t.dtype == torch.bfloat16 else _lib.QPAM_F32
+
+
+def _rows(t, name):
+    if not (t.is_cuda and t.dim() == 3 and t.shape[2] == 2 and t.stride(2) == 1 and t.stride(1) == 2):
+        raise ValueError(f"qpam {name}: expected a CUDA [n, dim, 2] tensor with contiguous rows")
+
+
+def resid_norm(x, scale, eps, y=None, y_scale=None, out_dtype=torch.float32):
+    """The residual add and the ComplexNorm after it in one launch
+    (qpam_resid_norm; V11Block.forward, v11/model.py:1045-1048, inference):
+    x [n, dim, 2] fp32 is updated in place to x + y * y_scale when y
+    ([n, dim, 2] fp32 or bf16; y_scale a 0-dim fp32 device tensor) is given;
+    returns ComplexNorm(x; scale fp32 [dim], eps) as [n, dim, 2] in out_dtype."""
+    _rows(x, "resid_norm")
+    if x.dtype != torch.float32:
+        raise ValueError("qpam resid_norm: x must be float32")
+    n, dim = x.shape[0], x.shape[1]
+    out = torch.empty(n, dim, 2, device=x.device, dtype=out_dtype)
+    a = _lib.ResidNormArgs()
+    a.rows, a.dim, a.eps = n, dim, float(eps)
+    a.x, a.ldx = x.data_ptr(), x.stride(0)
+    if y is not None:
+        _rows(y, "resid_norm")
+        if y.shape != x.shape or y_scale is None:
+            raise ValueError("qpam resid_norm: y must match x and come with y_scale")
+        a.y, a.y_dtype, a.ldy, a.y_scale = y.data_ptr(), _code(y), y.stride(0), y_scale.data_ptr()
+    a.norm_scale = scale.data_ptr()
+    a.out, a.out_dtype, a.ldo = out.data_ptr(), _code(out), out.stride(0)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.lib().qpam_resid_norm(ctypes.byref(a), _lib.stream_ptr(x.device)), "qpam_resid_norm")
+    return out
+
+
+def cgu_mix(gu, hid, bias, beta=None, phase_alpha=None, phase_beta=None, out_dtype=None):
+    """ComplexGatedUnit.forward between its projections in one launch
+    (qpam_cgu_mix; v11/complex_ops.py:216-220, inference): gu [n, 4 hid] (the
+    gate projection's interleaved output, then the up projection's) ->
+    cgu_gate(gate, act(up)) as [n, hid, 2] in out_dtype (default gu's); act
+    ModReLU (bias), ModSwish (bias, beta) or the phase-modulated activation
+    (bias, beta, phase_alpha, phase_beta), parameters fp32 [hid]."""
+    if not (gu.is_cuda and gu.dim() == 2 and gu.shape[1] == 4 * hid and gu.stride(1) == 1):
+        raise ValueError("qpam cgu_mix: expected a CUDA [n, 4 hid] tensor with contiguous rows")
+    n = gu.shape[0]
+    out = torch.empty(n, hid, 2, device=gu.device, dtype=out_dtype or gu.dtype)
+    a = _lib.CguMixArgs()
+    a.rows, a.hid = n, hid
+    a.gu, a.gu_dtype, a.ldg = gu.data_ptr(), _code(gu), gu.stride(0)
+    a.bias = bias.data_ptr()
+    a.beta = beta.data_ptr() if beta is not None else None
+    a.phase_alpha = phase_alpha.data_ptr() if phase_alpha is not None else None
+    a.phase_beta = phase_beta.data_ptr() if phase_beta is not None else None
+    a.out, a.out_dtype, a.ldo = out.data_ptr(), _code(out), out.stride(0)
+    with torch.cuda.device(gu.device):
+        _lib.check(_lib.lib().qpam_cgu_mix(ctypes.byref(a), _lib.stream_ptr(gu.device)), "qpam_cgu_mix")
+    return out
 
 
 def interleaved_weight(wr, wi):
@@ -89,19 +155,30 @@ class ModelDecoder:
             self._embed = e.contiguous()
             self._embed_w = e.reshape(self.vocab, 2 * self.dim).to(dt).contiguous()           # logits GEMM
             self._blk = []
+            if self.dim % 4 or self.dim > MAX_DIM:
+                raise NotImplementedError(f"ModelDecoder: dim {self.dim} (a multiple of 4 up to {MAX_DIM})")
+            prm = lambda t: t.detach().float().contiguous()
             for b in self.blocks:
                 cgu = b.cgu
                 act = cgu.act
+                hid = cgu.gate_proj.weight_real.shape[0]
+                if hid % 4:
+                    raise NotImplementedError(f"ModelDecoder: CGU width {hid} (a multiple of 4)")
                 w_gu = torch.cat([interleaved_weight(cgu.gate_proj.weight_real, cgu.gate_proj.weight_imag),
                                   interleaved_weight(cgu.up_proj.weight_real, cgu.up_proj.weight_imag)], 0)
+                # the activation by its parameters (v11/complex_ops.py:102-143): ModReLU has a
+                # bias, ModSwish a bias and beta, the phase-modulated one also phase_alpha / _beta
+                phase = hasattr(act, "phase_alpha")
                 self._blk.append(dict(
                     norm1=(b.norm1.scale.float().contiguous(), float(b.norm1.eps)),
                     norm2=(b.norm2.scale.float().contiguous(), float(b.norm2.eps)),
-                    w_gu=w_gu.to(dt).contiguous(), hid=cgu.gate_proj.weight_real.shape[0],
+                    w_gu=w_gu.to(dt).contiguous(), hid=hid,
                     w_down=interleaved_weight(cgu.down_proj.weight_real, cgu.down_proj.weight_imag).to(dt)
                     .contiguous(),
-                    act_bias=act.bias.float().contiguous(),
-                    act_beta=act.beta.float().contiguous() if hasattr(act, "beta") else None,
+                    act_bias=prm(act.bias),
+                    act_beta=prm(act.beta) if hasattr(act, "beta") else None,
+                    act_pa=prm(act.phase_alpha) if phase else None,
+                    act_pb=prm(act.phase_beta) if phase else None,
                     cgu_scale=b.cgu_scale.detach().float(), pam_scale=b.pam_scale.detach().float()))
             self._norm_e = (m.embed_norm.scale.float().contiguous(), float(m.embed_norm.eps))
             self._norm_o = (m.output_norm.scale.float().contiguous(), float(m.output_norm.eps))
@@ -112,43 +189,40 @@ class ModelDecoder:
             self._b_head = None if bh is None else bh.to(dt).contiguous()
 
     # ------------------------------------------------------------ pieces
-    def _linear(self, x, w, b=None):
-        """x [n, k] (fp32) -> fp32 [n, out] through the GEMM dtype."""
-        y = F.linear(x.to(self.dtype), w, b)
-        return y if y.dtype == torch.float32 else y.float()
-
     @staticmethod
     def _norm(x, p):
         return tk.fused_complex_norm(x, p[0], p[1])
 
     def _cgu(self, h, blk):
+        """The CGU of normed rows h [n, dim, 2] in the GEMM dtype -> its output
+        [n, dim, 2] in the GEMM dtype: gate and up in one GEMM, the activation
+        and the gate in one launch, the down GEMM."""
         n = h.shape[0]
-        hid = blk["hid"]
-        gu = self._linear(h.reshape(n, -1), blk["w_gu"])                       # [n, 4 hid]: gate, up interleaved
-        gate = gu[:, :2 * hid].reshape(n, hid, 2).contiguous()
-        up = gu[:, 2 * hid:].reshape(n, hid, 2).contiguous()
-        if blk["act_beta"] is not None:
-            up = tk.fused_mod_swish(up, blk["act_bias"], blk["act_beta"])
-        else:
-            up = tk.fused_mod_relu(up, blk["act_bias"])
-        g = tk.fused_cgu_gate(gate, up)
-        return self._linear(g.reshape(n, -1), blk["w_down"]).view(n, self.dim, 2)
+        gu = F.linear(h.reshape(n, -1), blk["w_gu"])                          # [n, 4 hid]: gate, up interleaved
+        g = cgu_mix(gu, blk["hid"], blk["act_bias"], blk["act_beta"], blk["act_pa"], blk["act_pb"])
+        return F.linear(g.view(n, -1), blk["w_down"]).view(n, self.dim, 2)
 
-    def _head(self, x):
-        n = x.shape[0]
-        x = self._norm(x, self._norm_o)
-        lm = self._linear(x.reshape(n, -1), self._w_head, self._b_head).view(n, self.dim, 2)
-        lm = self._norm(lm, self._norm_h)
-        return self._linear(lm.reshape(n, -1), self._embed_w)                  # [n, V]
+    def _head(self, h):
+        """Logits [n, V] (fp32) from output-normed rows h [n, dim, 2] (GEMM dtype)."""
+        n = h.shape[0]
+        lm = F.linear(h.reshape(n, -1), self._w_head, self._b_head).view(n, self.dim, 2)
+        lm = self._norm(lm, self._norm_h)                                      # in the GEMM dtype
+        logits = F.linear(lm.reshape(n, -1), self._embed_w)                     # [n, V]
+        return logits if logits.dtype == torch.float32 else logits.float()
+
+    def _next_norm(self, li):
+        return self._blk[li + 1]["norm1"] if li + 1 < len(self._blk) else self._norm_o
 
     def _tokens(self, ids, slots):
         """Every layer and the head for the listed rows: ids [n] int64, slots [n] int32."""
-        x = self._norm(self._embed[ids], self._norm_e)
+        dt = self.dtype
+        x = self._norm(self._embed[ids], self._norm_e)                          # fp32 residual stream
+        h = resid_norm(x, *self._blk[0]["norm1"], out_dtype=dt)
         for li, blk in enumerate(self._blk):
-            x = x + blk["cgu_scale"] * self._cgu(self._norm(x, blk["norm1"]), blk)
-            y = self.engine.layer_step(li, self._norm(x, blk["norm2"]), slots)
-            x = x + blk["pam_scale"] * y
-        return self._head(x)
+            h = resid_norm(x, *blk["norm2"], y=self._cgu(h, blk), y_scale=blk["cgu_scale"], out_dtype=dt)
+            y = self.engine.layer_step(li, h, slots)
+            h = resid_norm(x, *self._next_norm(li), y=y, y_scale=blk["pam_scale"], out_dtype=dt)
+        return self._head(h)
 
     # ------------------------------------------------------------ slots
     @torch.no_grad()
@@ -156,16 +230,17 @@ class ModelDecoder:
         """The model over one prompt (ids [T]) with the fused PAM prefill:
         (logits of its last token [V], the per-layer states)."""
         ids = prompt_ids.to(self._embed.device).long().view(1, -1)
-        t = ids.shape[1]
-        x = self._norm(self._embed[ids[0]], self._norm_e).view(1, t, self.dim, 2)
+        t, dt = ids.shape[1], self.dtype
+        x = self._norm(self._embed[ids[0]], self._norm_e)                       # [t, dim, 2] fp32
+        h = resid_norm(x, *self._blk[0]["norm1"], out_dtype=dt)
         states = []
-        for blk, b in zip(self._blk, self.blocks):
-            x = x + blk["cgu_scale"] * self._cgu(self._norm(x.view(t, self.dim, 2), blk["norm1"]), blk).view(1, t, self.dim, 2)
-            y, s = pam_layer.forward(b.pam, self._norm(x.view(t, self.dim, 2), blk["norm2"]).view(1, t, self.dim, 2),
-                                     None, 0)
+        for li, (blk, b) in enumerate(zip(self._blk, self.blocks)):
+            h2 = resid_norm(x, *blk["norm2"], y=self._cgu(h, blk), y_scale=blk["cgu_scale"])
+            y, s = pam_layer.forward(b.pam, h2.view(1, t, self.dim, 2), None, 0)
             states.append(s)
-            x = x + blk["pam_scale"] * y.float()
-        return self._head(x.view(t, self.dim, 2)[-1:])[0], states
+            h = resid_norm(x, *self._next_norm(li), y=y.reshape(t, self.dim, 2).contiguous(),
+                           y_scale=blk["pam_scale"], out_dtype=dt)
+        return self._head(h[-1:])[0], states
 
     def admit(self, prompt_ids):
         """A sequence with this prompt joins: its prefill's states enter a

@@ -55,7 +55,8 @@ def test_library_loads_and_exports_every_declared_symbol():
     ("qpam_ce_fwd_args", "CeFwdArgs"), ("qpam_ce_bwd_args", "CeBwdArgs"), ("qpam_cplx_args", "CplxArgs"),
     ("qpam_pc_fold_args", "PcFoldArgs"), ("qpam_pc_scan_args", "PcScanArgs"),
     ("qpam_cweight_args", "CWeightArgs"), ("qpam_prologue_args", "PrologueArgs"),
-    ("qpam_prologue_bwd_args", "PrologueBwdArgs"),
+    ("qpam_prologue_bwd_args", "PrologueBwdArgs"), ("qpam_resid_norm_args", "ResidNormArgs"),
+    ("qpam_cgu_mix_args", "CguMixArgs"),
 ])
 def test_ctypes_structs_match_header(cname, pyname):
     py = [f[0] for f in getattr(_lib, pyname)._fields_]

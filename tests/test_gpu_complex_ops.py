@@ -147,3 +147,87 @@ def test_cgu_gate_grid_stride_rows(gpu_lib, dtype, rows):
         assert _rel(out[r0:r1], ref_out) < tol, f"rows {r0}..{r1}: fwd"
         assert _rel(z.grad[r0:r1], ref_grads[0]) < max(tol, 1e-4), f"rows {r0}..{r1}: dz"
         assert _rel(up.grad[r0:r1], ref_grads[1]) < max(tol, 1e-4), f"rows {r0}..{r1}: dup"
+
+
+# ------------------------------------------------ decode block glue (inference)
+
+@pytest.mark.parametrize("dim,rows", [(768, 211), (64, 5), (1000, 3), (2048, 17)])
+@pytest.mark.parametrize("ydt,odt", [(None, torch.float32), (torch.float32, torch.float32),
+                                     (torch.bfloat16, torch.bfloat16), (torch.float32, torch.bfloat16)])
+def test_resid_norm_matches_add_then_norm(gpu_lib, dim, rows, ydt, odt):
+    """qpam_resid_norm: x += y * s in place (bit-equal to torch's fp32 product
+    then sum), then ComplexNorm of the new x against the float64 oracle (fp32
+    out rel <= 1e-5, bf16 out rel <= 2^-8 per element of the row scale); with no
+    y and a dim the norm's row-team path takes (768), bit-equal to
+    qpam_cplx_fwd's ComplexNorm.  x rows strided inside a wider buffer."""
+    from qllm2_amd import triton_kernels as tk
+    from qllm2_amd.model_decode import resid_norm
+    g = torch.Generator().manual_seed(dim + rows)
+    xs = (torch.randn(rows, dim + 8, 2, generator=g) * 1.5).cuda()
+    x = xs[:, :dim]
+    y = torch.randn(rows, dim, 2, generator=g).cuda().to(ydt) if ydt is not None else None
+    scale = (torch.rand(dim, generator=g) + 0.5).cuda()
+    s = torch.tensor(0.7, device="cuda")
+    x0 = x.clone()
+    want_x = x0 + y.float() * s if y is not None else x0
+    out = resid_norm(x, scale, 1e-6, y=y, y_scale=s, out_dtype=odt)
+    assert torch.equal(x, want_x)
+    assert out.dtype == odt and out.shape == (rows, dim, 2)
+    ref = O.complex_norm(want_x.double().cpu(), scale.double().cpu(), 1e-6)
+    err = (out.double().cpu() - ref).abs().amax((-1, -2)) / ref.abs().amax((-1, -2))
+    assert err.max().item() < (1e-5 if odt == torch.float32 else 2 ** -8)
+    if y is None and dim == 768:
+        assert torch.equal(out.float(), tk.fused_complex_norm(x0.contiguous(), scale, 1e-6).to(odt).float())
+
+
+@pytest.mark.parametrize("act", ["swish", "relu", "phase_mod"])
+@pytest.mark.parametrize("gdt,odt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                     (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("hid,rows", [(2304, 130), (36, 3)])
+def test_cgu_mix_matches_oracle(gpu_lib, act, gdt, odt, hid, rows):
+    """qpam_cgu_mix: cgu_gate(gate, act(up)) from the [gate | up] GEMM output
+    against the float64 oracle on the same (dtype-rounded) inputs: fp32 rel <=
+    1e-5 of each row's largest output, bf16 output rel <= 2^-8; gu rows strided
+    inside a wider buffer; the fp32 result also against the HIP ops one at a
+    time (fused_mod_* then fused_cgu_gate)."""
+    from qllm2_amd import triton_kernels as tk
+    from qllm2_amd.model_decode import cgu_mix
+    g = torch.Generator().manual_seed(hid + rows)
+    gus = (torch.randn(rows, 4 * hid + 16, generator=g) * 1.3).cuda().to(gdt)
+    gu = gus[:, :4 * hid]
+    bias = (torch.randn(hid, generator=g) * 0.3).cuda()
+    beta = (1 + torch.randn(hid, generator=g) * 0.2).cuda() if act != "relu" else None
+    pa = torch.randn(hid, generator=g).cuda() if act == "phase_mod" else None
+    pb = (torch.randn(hid, generator=g) * 2).cuda() if act == "phase_mod" else None
+    out = cgu_mix(gu, hid, bias, beta, pa, pb, out_dtype=odt)
+    assert out.dtype == odt and out.shape == (rows, hid, 2)
+    gd = gu.double().cpu()
+    gate, up = gd[:, :2 * hid].reshape(rows, hid, 2), gd[:, 2 * hid:].reshape(rows, hid, 2)
+    b64 = bias.double().cpu()
+    if act == "swish":
+        u = O.mod_swish(up, b64, beta.double().cpu())
+    elif act == "relu":
+        u = O.mod_relu(up, b64)
+    else:
+        u = O.phase_mod(up, b64, beta.double().cpu(), pa.double().cpu(), pb.double().cpu())
+    ref = O.cgu_gate(gate, u)
+    err = (out.double().cpu() - ref).abs().amax((-1, -2)) / ref.abs().amax((-1, -2))
+    assert err.max().item() < (1e-5 if odt == torch.float32 else 2 ** -8)
+    if act != "phase_mod" and gdt == torch.float32:
+        gf, uf = gu[:, :2 * hid].reshape(rows, hid, 2).contiguous(), gu[:, 2 * hid:].reshape(rows, hid, 2).contiguous()
+        ua = tk.fused_mod_swish(uf, bias, beta) if act == "swish" else tk.fused_mod_relu(uf, bias)
+        assert _rel(out, tk.fused_cgu_gate(gf, ua)) < 1e-6
+
+
+def test_block_glue_rejects_bad_arguments(gpu_lib):
+    from qllm2_amd import _lib
+    from qllm2_amd.model_decode import cgu_mix, resid_norm
+    x = torch.randn(4, 18, 2, device="cuda")
+    with pytest.raises(_lib.QpamError, match="multiple of 4"):
+        resid_norm(x, torch.ones(18, device="cuda"), 1e-6)
+    x = torch.randn(4, 4096, 2, device="cuda")
+    with pytest.raises(_lib.QpamError, match="at most"):
+        resid_norm(x, torch.ones(4096, device="cuda"), 1e-6)
+    gu = torch.randn(3, 4 * 8, device="cuda")
+    with pytest.raises(_lib.QpamError, match="given together"):
+        cgu_mix(gu, 8, torch.zeros(8, device="cuda"), torch.ones(8, device="cuda"), torch.zeros(8, device="cuda"), None)

@@ -24,6 +24,7 @@ CFGS = {
     "e3_swish": (dict(dim=128, n_heads=2, head_dim=64, n_states=3, chunk_size=64, state_compete=True,
                       gamma_floor=0.2), "swish"),
     "one_state_relu": (dict(dim=128, n_heads=2, head_dim=64, n_states=1, chunk_size=64, qk_norm=True), "relu"),
+    "one_state_phase_mod": (dict(dim=128, n_heads=2, head_dim=64, n_states=1, chunk_size=64), "phase_mod"),
 }
 VOCAB = 300
 # (prompt length, join step, tokens decoded)

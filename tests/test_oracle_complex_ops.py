@@ -69,6 +69,27 @@ def test_cgu_gate_is_a_phase_rotation_times_sigmoid_magnitude():
     assert _wrap(_angle(out) - _angle(g) - _angle(u)).abs().max() < 1e-9
 
 
+def test_phase_mod_is_mod_swish_turned_by_its_angle():
+    """The phase-modulated activation keeps ModSwish's magnitude and turns its
+    phase by alpha |z| + beta_ph: with both phase parameters zero it is ModSwish
+    exactly; otherwise the magnitudes agree and the angle difference is
+    alpha |z| + beta_ph (|z| with its 1e-8 term), checked against complex128
+    polar arithmetic."""
+    z = _z((5, 48), 11)
+    g = torch.Generator().manual_seed(12)
+    bias, beta = torch.randn(48, generator=g, dtype=torch.float64) * 0.3, 1 + torch.randn(48, generator=g, dtype=torch.float64) * 0.2
+    pa, pb = torch.randn(48, generator=g, dtype=torch.float64), torch.randn(48, generator=g, dtype=torch.float64) * 2
+    zero = torch.zeros(48, dtype=torch.float64)
+    assert torch.equal(O.phase_mod(z, bias, beta, zero, zero), O.mod_swish(z, bias, beta))
+    out = O.phase_mod(z, bias, beta, pa, pb)
+    sw = O.mod_swish(z, bias, beta)
+    assert torch.allclose(_abs(out), _abs(sw), rtol=1e-12, atol=0)
+    mag = torch.sqrt(_abs(z) ** 2 + 1e-8)
+    assert _wrap(_angle(out) - _angle(z) - (pa * mag + pb)).abs().max() < 1e-9
+    want = torch.complex(sw[..., 0], sw[..., 1]) * torch.polar(torch.ones_like(mag), pa * mag + pb)
+    assert torch.allclose(torch.view_as_real(want), out, rtol=0, atol=1e-12)
+
+
 @pytest.mark.parametrize("name", ["norm", "swish", "relu", "cgu"])
 def test_closed_form_backward_matches_autograd(name):
     torch.manual_seed(7)

@@ -77,3 +77,20 @@ def test_channel_mix_linear_in_down_projection():
                                 p["blocks.0.cgu.down_proj.weight_imag"])
     assert _rel(b, 2.5 * a) < 1e-12
     assert _rel(a, want) < 1e-12
+
+
+def test_phase_mod_block_prefill_then_decode():
+    """A model with the phase-modulated CGU activation: decode after a prefill
+    gives the logits of one prefill over the whole sequence, and its
+    activation is not ModSwish's (the phase parameters are used)."""
+    p = VM.make_model_params(CFG, 2, 60, 8, activation="phase_mod")
+    model = VM.V11LM(CFG, 2, p, activation="phase_mod").eval()
+    swish = VM.V11LM(CFG, 2, p, activation="swish").eval()
+    ids = torch.randint(0, 60, (1, 17), generator=torch.Generator().manual_seed(9))
+    with torch.no_grad():
+        full, _ = model(ids)
+        logits, states = model(ids[:, :11])
+        for t in range(11, 17):
+            step, states = model(ids[:, t:t + 1], states=states, step_offset=t)
+            assert _rel(step[:, 0], full[:, t]) < 1e-4, t
+        assert _rel(swish(ids)[0], full) > 1e-3

@@ -211,13 +211,14 @@ class ModelDecoder:
         return logits if logits.dtype == torch.float32 else logits.float()
 
     def _next_norm(self, li):
+        """The norm after block li's PAM residual (li = -1: after the embedding norm)."""
         return self._blk[li + 1]["norm1"] if li + 1 < len(self._blk) else self._norm_o
 
     def _tokens(self, ids, slots):
         """Every layer and the head for the listed rows: ids [n] int64, slots [n] int32."""
         dt = self.dtype
         x = self._norm(self._embed[ids], self._norm_e)                          # fp32 residual stream
-        h = resid_norm(x, *self._blk[0]["norm1"], out_dtype=dt)
+        h = resid_norm(x, *self._next_norm(-1), out_dtype=dt)
         for li, blk in enumerate(self._blk):
             h = resid_norm(x, *blk["norm2"], y=self._cgu(h, blk), y_scale=blk["cgu_scale"], out_dtype=dt)
             y = self.engine.layer_step(li, h, slots)
@@ -232,7 +233,7 @@ class ModelDecoder:
         ids = prompt_ids.to(self._embed.device).long().view(1, -1)
         t, dt = ids.shape[1], self.dtype
         x = self._norm(self._embed[ids[0]], self._norm_e)                       # [t, dim, 2] fp32
-        h = resid_norm(x, *self._blk[0]["norm1"], out_dtype=dt)
+        h = resid_norm(x, *self._next_norm(-1), out_dtype=dt)
         states = []
         for li, (blk, b) in enumerate(zip(self._blk, self.blocks)):
             h2 = resid_norm(x, *blk["norm2"], y=self._cgu(h, blk), y_scale=blk["cgu_scale"])

@@ -153,7 +153,8 @@ def test_cgu_gate_grid_stride_rows(gpu_lib, dtype, rows):
 
 @pytest.mark.parametrize("dim,rows", [(768, 211), (64, 5), (1000, 3), (2048, 17)])
 @pytest.mark.parametrize("ydt,odt", [(None, torch.float32), (torch.float32, torch.float32),
-                                     (torch.bfloat16, torch.bfloat16), (torch.float32, torch.bfloat16)])
+                                     (torch.bfloat16, torch.bfloat16), (torch.float32, torch.bfloat16),
+                                     (torch.bfloat16, torch.float32)])
 def test_resid_norm_matches_add_then_norm(gpu_lib, dim, rows, ydt, odt):
     """qpam_resid_norm: x += y * s in place (bit-equal to torch's fp32 product
     then sum), then ComplexNorm of the new x against the float64 oracle (fp32

@@ -9,12 +9,24 @@ rotating q and k by each slot's own RoPE position.  `SlotPool` is the decode
 engine around it (V11LM.generate, v11/model.py:1207-1245, without the batch-1
 loop): per-layer states of many sequences, joined and released between steps.
 `recur_step_additive` keeps the reference method's signature and functional
-(non-mutating) semantics.
+(non-mutating) semantics.  The kernels are built for head dims 16, 32, 64 and
+128; a smaller head dim of another size runs on the next of them with zero
+padding (the padded rows and columns of the state stay zero, since the padded
+entries of v and k are zero, and the padded columns of q add nothing to y).
 """
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
+
+KERNEL_DIMS = (16, 32, 64, 128)
+
+
+def kernel_dim(d):
+    """The kernels' head dim that runs head dim d (d itself, or the next
+    larger one with zero padding); None above 128."""
+    return next((k for k in KERNEL_DIMS if k >= d), None)
 
 
 def _check_cuda(*ts):
@@ -259,12 +271,24 @@ def recur_step_additive(memory_state, decay_gamma, value_t, key_t, query_t):
         raise ValueError(f"decay_gamma must be [...] or [..., d] for a state {tuple(memory_state.shape)}")
     lead = memory_state.shape[:-3]
     d = memory_state.shape[-2]
+    kd = kernel_dim(d)
+    if kd is None:
+        raise ValueError(f"qpam decode: head dim {d} (at most {KERNEL_DIMS[-1]})")
     n = memory_state[..., 0, 0, 0].numel()
     f32 = lambda t, *shape: t.to(torch.float32).contiguous().view(n, *shape)  # noqa: E731
-    y, new_state = _DecodeStep.apply(f32(memory_state, d, d, 2), f32(decay_gamma, d) if per_channel else f32(decay_gamma),
-                                     f32(value_t, d, 2), f32(key_t, d, 2), f32(query_t, d, 2))
-    return (y.view(*lead, d, 2).to(memory_state.dtype),
-            new_state.view(*lead, d, d, 2).to(memory_state.dtype))
+    st, gam = f32(memory_state, d, d, 2), f32(decay_gamma, d) if per_channel else f32(decay_gamma)
+    v, k, q = f32(value_t, d, 2), f32(key_t, d, 2), f32(query_t, d, 2)
+    if kd != d:  # zero padding to the kernel's head dim (differentiable: the gradients come back sliced)
+        p = kd - d
+        st = F.pad(st, (0, 0, 0, p, 0, p))
+        v, k, q = (F.pad(t, (0, 0, 0, p)) for t in (v, k, q))
+        if per_channel:
+            gam = F.pad(gam, (0, p), value=1.0)
+    y, new_state = _DecodeStep.apply(st, gam, v, k, q)
+    if kd != d:
+        y, new_state = y[:, :d], new_state[:, :d, :d]
+    return (y.reshape(*lead, d, 2).to(memory_state.dtype),
+            new_state.reshape(*lead, d, d, 2).to(memory_state.dtype))
 
 
 def build_rope_cache(max_len, head_dim, device=None):

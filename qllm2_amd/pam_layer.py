@@ -172,7 +172,7 @@ def recur_step_delta(self, memory_state, decay_gamma, value_t, key_t, query_t, w
     return _delta.recur_step_delta(memory_state, decay_gamma, value_t, key_t, query_t, write_beta_t)
 
 
-_DECODE_DIMS = (16, 32, 64, 128)
+_DECODE_MAX = _decode.KERNEL_DIMS[-1]  # head dims up to this decode on the kernels (others padded)
 
 
 def forward_chunked_perchannel(self, queries, keys, protected_values, decay_gamma, head_dim):
@@ -188,10 +188,11 @@ def forward_chunked_perchannel(self, queries, keys, protected_values, decay_gamm
 def recur_step_additive(self, memory_state, decay_gamma, value_t, key_t, query_t):
     """V11PAMLayer._recur_step_additive: the HIP decode step for head or
     per-channel decay (decay_gamma [...] or [..., d]), differentiable (the
-    backward is a HIP kernel as well); CPU tensors and head dims outside
-    16/32/64/128 run the saved reference step (v11/model.py:927-965)."""
+    backward is a HIP kernel as well; head dims other than 16/32/64/128 run
+    zero-padded to the next of them); CPU tensors and head dims above 128 run
+    the saved reference step (v11/model.py:927-965)."""
     if (not memory_state.is_cuda or decay_gamma.dim() not in (memory_state.dim() - 3, memory_state.dim() - 2)
-            or memory_state.shape[-2] not in _DECODE_DIMS):
+            or memory_state.shape[-2] > _DECODE_MAX):
         return _original(self, "_recur_step_additive")(self, memory_state, decay_gamma, value_t, key_t, query_t)
     return _decode.recur_step_additive(memory_state, decay_gamma, value_t, key_t, query_t)
 
@@ -199,14 +200,17 @@ def recur_step_additive(self, memory_state, decay_gamma, value_t, key_t, query_t
 def recurrent(self, x, queries, keys, values, state, head_dim):
     """V11PAMLayer._recurrent for the additive write (head or per-channel
     decay): per token one qpam_decode_step launch updates all K states and sums
-    the rotated reads.  The E2 mode, grad mode, CPU tensors and other head dims
-    run the saved reference loop (which then calls the replaced steps where
-    they apply)."""
+    the rotated reads (head dims other than 16/32/64/128 on the next of them,
+    the state pool and each token's q, k, v zero-padded).  The E2 mode, grad
+    mode, CPU tensors and head dims above 128 run the saved reference loop
+    (which then calls the replaced steps where they apply)."""
     if (self.write_mode != 'additive' or torch.is_grad_enabled()
-            or not x.is_cuda or head_dim not in _DECODE_DIMS):
+            or not x.is_cuda or head_dim > _DECODE_MAX):
         return _original(self, "_recurrent")(self, x, queries, keys, values, state, head_dim)
     b, t = x.shape[0], x.shape[1]
     h, k_states, d = self.num_heads, self.n_states, head_dim
+    kd = _decode.kernel_dim(d)
+    pad = (lambda z: F.pad(z, (0, 0, 0, kd - d))) if kd != d else (lambda z: z)  # [..., d, 2] -> [..., kd, 2]
     scale = head_dim ** -0.5
     if k_states > 1:
         phase, routing = self._phase_and_alpha(x)            # [B,T,H,K]
@@ -215,8 +219,9 @@ def recurrent(self, x, queries, keys, values, state, head_dim):
     if state is None:
         shape = (k_states, b, h, d, d, 2) if k_states > 1 else (b, h, d, d, 2)
         state = torch.zeros(shape, device=x.device, dtype=x.dtype)
-    # pool layout [slot=b, group=h, state=k, d, d, 2]
-    pool = (state if k_states > 1 else state.unsqueeze(0)).permute(1, 2, 0, 3, 4, 5).to(torch.float32).contiguous()
+    # pool layout [slot=b, group=h, state=k, d, d, 2] (zero-padded to the kernel's head dim)
+    pool = (state if k_states > 1 else state.unsqueeze(0)).permute(1, 2, 0, 3, 4, 5).to(torch.float32)
+    pool = (F.pad(pool, (0, 0, 0, kd - d, 0, kd - d)) if kd != d else pool).contiguous()
     ys = []
     for ti in range(t):
         tok = x[:, ti:ti + 1]
@@ -227,13 +232,16 @@ def recurrent(self, x, queries, keys, values, state, head_dim):
             g_k, pv = self._gamma_and_vprime(tok, values[:, :, ti:ti + 1], state_offset=off)
             gam.append(g_k[:, :, 0])
             v_t = pv[:, :, 0]
-        gamma = torch.stack(gam, 2).float().contiguous()                      # [B,H,K] or [B,H,K,d]
+        gamma = torch.stack(gam, 2).float()                                   # [B,H,K] or [B,H,K,d]
+        if kd != d and gamma.dim() == 4:
+            gamma = F.pad(gamma, (0, kd - d), value=1.0)  # padded key columns: any finite decay
         r = rot[:, ti].float().contiguous() if k_states > 1 else None         # [B,H,K,2]
-        y = _decode.decode_step(pool, queries[:, :, ti].float().contiguous(), keys[:, :, ti].float().contiguous(),
-                                v_t.float().contiguous(), gamma, rot=r, q_scale=scale)
-        ys.append(y.to(x.dtype))
+        y = _decode.decode_step(pool, pad(queries[:, :, ti].float()).contiguous(),
+                                pad(keys[:, :, ti].float()).contiguous(), pad(v_t.float()).contiguous(),
+                                gamma.contiguous(), rot=r, q_scale=scale)
+        ys.append(y[..., :d, :].to(x.dtype))
     out = torch.stack(ys, dim=2)
-    new_state = pool.permute(2, 0, 1, 3, 4, 5).to(x.dtype)
+    new_state = pool[..., :d, :d, :].permute(2, 0, 1, 3, 4, 5).to(x.dtype)
     return out, (new_state if k_states > 1 else new_state[0])
 
 

@@ -265,14 +265,15 @@ def test_decode_per_channel_decay_matches_textbook_recurrence(gpu_lib, d, M, use
         assert st[s].abs().max().item() == 0.0
 
 
-@pytest.mark.parametrize("d", [16, 32, 64, 128])
+@pytest.mark.parametrize("d", [16, 32, 64, 128, 24, 48, 96])
 @pytest.mark.parametrize("per_channel", [False, True])
 @pytest.mark.parametrize("with_dstate", [False, True])
 def test_decode_step_backward_matches_autograd(gpu_lib, d, per_channel, with_dstate):
     """qpam_decode_step_bwd through recur_step_additive's autograd: the
     gradients of the state, gamma, v, k and q for a loss on y (and on the new
     state) equal float64 autograd of the oracle step (the reference's
-    _recur_step_additive restated) over [2, 3] (slot, head) rows."""
+    _recur_step_additive restated) over [2, 3] (slot, head) rows.  Head dims
+    24, 48 and 96 run zero-padded on the 32-, 64- and 128-wide kernels."""
     from qllm2_amd.decode import recur_step_additive
     g = torch.Generator().manual_seed(500 + d + 7 * per_channel + with_dstate)
     state = torch.randn(2, 3, d, d, 2, generator=g, dtype=torch.float64) * 0.1

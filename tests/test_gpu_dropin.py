@@ -16,8 +16,7 @@ the shapes the kernels take in pieces (six states, head_dim 128 and 96):
     v11/selftest.py:16-38);
   * the HIP kernels ran where they apply: counters on the saved originals show
     the head-decay scans, the delta write and the decode steps never fell
-    back (decode at head dims outside 16/32/64/128 runs the reference methods
-    by design);
+    back (decode at head dim 96 runs zero-padded on the 128-wide kernels);
   * grad mode: a T = 1 step carrying a state (the reference's recurrent
     branch, v11/model.py:830-832; the decode step and its backward as HIP
     kernels) and a prefill, every gradient (input, state, each parameter)
@@ -62,7 +61,7 @@ HIP_ONLY = {
     "E2": ("_forward_delta", "_recur_step_delta"),
     "E3_6states": ("_forward_multistate_fused", "_fused_chunk_step", "_recurrent", "_recur_step_additive"),
     "baseline_hd128": ("_forward_chunked_head", "_recurrent", "_recur_step_additive"),
-    "E3_hd96": ("_forward_multistate_fused", "_fused_chunk_step"),
+    "E3_hd96": ("_forward_multistate_fused", "_fused_chunk_step", "_recurrent", "_recur_step_additive"),
     "E1": ("_forward_chunked_perchannel", "_recurrent", "_recur_step_additive"),
     "E1+E3": ("_forward_chunked_perchannel", "_recurrent", "_recur_step_additive"),
 }
@@ -148,7 +147,7 @@ def test_installed_selftest_matches_oracle(installed, mode):
 
 
 GRAD_MODES = ["baseline", "E1", "E3", "E1+E3", "E2_hd64", "baseline_hd64", "E3_hd64", "E2", "E3_6states",
-              "baseline_hd128"]
+              "baseline_hd128", "E3_hd96"]
 
 
 def _grads(layer, x, step_offset, state, loss_fn):

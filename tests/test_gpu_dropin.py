@@ -16,7 +16,8 @@ the shapes the kernels take in pieces (six states, head_dim 128 and 96):
     v11/selftest.py:16-38);
   * the HIP kernels ran where they apply: counters on the saved originals show
     the head-decay scans, the delta write and the decode steps never fell
-    back (decode at head dim 96 runs zero-padded on the 128-wide kernels);
+    back (decode at head dims 96 and 48 runs zero-padded on the 128- and
+    64-wide kernels, with per-channel decays in the E1 mode);
   * grad mode: a T = 1 step carrying a state (the reference's recurrent
     branch, v11/model.py:830-832; the decode step and its backward as HIP
     kernels) and a prefill, every gradient (input, state, each parameter)
@@ -49,6 +50,7 @@ MODES = {
     "E3_6states": dict(DIM16, n_states=6),
     "baseline_hd128": dict(dim=128, n_heads=1, head_dim=128, chunk_size=64),
     "E3_hd96": dict(dim=96, n_heads=1, head_dim=96, chunk_size=32, n_states=2),
+    "E1_hd48": dict(dim=96, n_heads=2, head_dim=48, chunk_size=32, decay_mode="per_channel"),
 }
 # reference methods that must not run (the HIP path covers the call) per mode
 HIP_ONLY = {
@@ -62,6 +64,7 @@ HIP_ONLY = {
     "E3_6states": ("_forward_multistate_fused", "_fused_chunk_step", "_recurrent", "_recur_step_additive"),
     "baseline_hd128": ("_forward_chunked_head", "_recurrent", "_recur_step_additive"),
     "E3_hd96": ("_forward_multistate_fused", "_fused_chunk_step", "_recurrent", "_recur_step_additive"),
+    "E1_hd48": ("_forward_chunked_perchannel", "_recurrent", "_recur_step_additive"),
     "E1": ("_forward_chunked_perchannel", "_recurrent", "_recur_step_additive"),
     "E1+E3": ("_forward_chunked_perchannel", "_recurrent", "_recur_step_additive"),
 }
@@ -147,7 +150,7 @@ def test_installed_selftest_matches_oracle(installed, mode):
 
 
 GRAD_MODES = ["baseline", "E1", "E3", "E1+E3", "E2_hd64", "baseline_hd64", "E3_hd64", "E2", "E3_6states",
-              "baseline_hd128", "E3_hd96"]
+              "baseline_hd128", "E3_hd96", "E1_hd48"]
 
 
 def _grads(layer, x, step_offset, state, loss_fn):

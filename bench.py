@@ -610,14 +610,14 @@ def bench_pam_layer(steps, warmup):
     from qllm2_amd import pam_layer as PL
     m = lay.mod
     with torch.no_grad():
-        cols = PP.proj_columns(H)
+        cols = PP.proj_columns(H, d)
         w_in, b_in = PL._in_weight(m, H, d, cols)
         proj = torch.nn.functional.linear(x.detach().view(B, T, 2 * dim), w_in, b_in)
         mag = torch.sqrt(x.detach().square().sum(-1) + 1e-8)
         prot = m.protect_gate(mag)
         phase = m.phase_proj(mag).view(B, T, H, M)
     args = (proj, prot, phase, None, m.dt_bias.detach().float(), None, m.state_dt_offset.detach().float(),
-            m.rope_cache, H, M, 0, False, 0.0, None, -1, -1)
+            m.rope_cache, H, M, d, 0, False, 0.0, None, -1, -1)
     outs = PP.prologue_fwd_op(*args)
     grads = [torch.randn_like(o) if o.numel() else o for o in outs]
     plane = B * T * H * d * 2                  # bytes of one bf16 plane

@@ -15,15 +15,15 @@
 // why not non-temporal ones).  The per-token
 // scalars (decays of the M states, protect gate, rotations) take one thread per
 // (state, token), so their [M,B,H,T] rows are written as 256-byte runs.  For
-// the vectors a token row of d = 64 complex elements is one DPP row of 16 lanes
-// (4 elements each: one 16-byte fp32 or 8-byte bf16 access per plane), a wave
-// covers 4 tokens per step and 16 per block slice.
+// the vectors a token row of d complex elements takes d / 4 lanes (4 elements
+// each: one 16-byte fp32 or 8-byte bf16 access per plane; d = 64: a DPP row of
+// 16 lanes, 4 tokens per wave step), and a wave covers 16 tokens of the block.
+// Head dims 16, 32, 64 and 128.
 #include "common.h"
 
 namespace qpam {
 namespace {
 
-constexpr int D = 64;
 constexpr int PT = 64;        // tokens per block
 constexpr int PTHREADS = 256;
 
@@ -128,7 +128,20 @@ __device__ __forceinline__ void rotation(const qpam_prologue_args &a, int b, int
     sincosf(Io<TI>::load1(a.phase, po), &sn, &cs);
 }
 
+// sum over the d / 4 lanes of a token row (lanes of a row are consecutive and
+// aligned): quad, half-row and row DPP steps, and a cross-row step for 32 lanes
+template <int LR> __device__ __forceinline__ float row_sum(float x) {
+    static_assert(LR == 4 || LR == 8 || LR == 16 || LR == 32, "row of 4 to 32 lanes");
+    x += dpp_f<0xB1>(x);
+    x += dpp_f<0x4E>(x);
+    if constexpr (LR >= 8) x += dpp_f<0x141>(x);
+    if constexpr (LR >= 16) x += dpp_f<0x140>(x);
+    if constexpr (LR == 32) x += __shfl_xor(x, 16);
+    return x;
+}
+
 // this lane's 4 rope factors (c, s) for the token at position rope_offset + t
+template <int D>
 __device__ __forceinline__ void rope4(const qpam_prologue_args &a, int t, int c4, float (&c)[4], float (&s)[4]) {
     const int p = min(max(a.rope_offset + t, 0), a.rope_len - 1);
     const floatx4 *rp = reinterpret_cast<const floatx4 *>(a.rope + ((int64_t)p * D + c4) * 2);
@@ -138,23 +151,24 @@ __device__ __forceinline__ void rope4(const qpam_prologue_args &a, int t, int c4
 
 __device__ __forceinline__ int64_t tile_count(const qpam_prologue_args &a) { return (a.T + PT - 1) / PT; }
 
-template <typename TI, typename TO>
+template <int D, typename TI, typename TO>
 __global__ void __launch_bounds__(PTHREADS) prologue_fwd_kernel(qpam_prologue_args a) {
+    constexpr int LR = D / 4, RW = 64 / LR, ITS = 16 / RW;  // lanes per token row, rows per wave step, steps
     __shared__ float s_keep[PT];
     const int nt = (int)tile_count(a);
     const int bh = blockIdx.x / nt, tile = blockIdx.x - bh * nt;
     const int b = bh / a.H, h = bh - b * a.H;
     const int t0 = tile * PT, tid = threadIdx.x;
-    const int w = tid >> 6, lane = tid & 63, c4 = (lane & 15) * 4;
+    const int w = tid >> 6, lane = tid & 63, c4 = (lane & (LR - 1)) * 4;
 
-    // this lane's projection elements of its 4 tokens, loaded before the
+    // this lane's projection elements of its ITS tokens, loaded before the
     // scalar work so the loads overlap it (rows past T re-read row T - 1 and
     // are not stored)
-    typename Io<TI>::Raw raw[4][6];
+    typename Io<TI>::Raw raw[ITS][6];
     const void *planes[6] = {a.q_re, a.q_im, a.k_re, a.k_im, a.v_re, a.v_im};
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int t = min(t0 + w * 16 + it * 4 + (lane >> 4), a.T - 1);
+    for (int it = 0; it < ITS; ++it) {
+        const int t = min(t0 + w * 16 + it * RW + lane / LR, a.T - 1);
         const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
 #pragma unroll
         for (int pl = 0; pl < 6; ++pl) raw[it][pl] = Io<TI>::load_raw(planes[pl], xo);
@@ -181,8 +195,8 @@ __global__ void __launch_bounds__(PTHREADS) prologue_fwd_kernel(qpam_prologue_ar
     __syncthreads();
 
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-        const int tt = w * 16 + it * 4 + (lane >> 4), t = t0 + tt;
+    for (int it = 0; it < ITS; ++it) {
+        const int tt = w * 16 + it * RW + lane / LR, t = t0 + tt;
         if (t >= a.T) continue;
         float qr[4], qi[4], kr[4], ki[4], vr[4], vi[4];
         Io<TI>::unpack(raw[it][0], qr), Io<TI>::unpack(raw[it][1], qi);
@@ -190,7 +204,7 @@ __global__ void __launch_bounds__(PTHREADS) prologue_fwd_kernel(qpam_prologue_ar
         Io<TI>::unpack(raw[it][4], vr), Io<TI>::unpack(raw[it][5], vi);
         if (a.rope) {
             float c[4], s[4];
-            rope4(a, t, c4, c, s);
+            rope4<D>(a, t, c4, c, s);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const float q0 = qr[j], k0 = kr[j];
@@ -239,8 +253,9 @@ __device__ __forceinline__ void rope_norm_bwd(float zr, float zi, float c, float
 // heads, so the projection gradients are written as whole rows of the
 // projection matrix (writes of 128-byte pieces spread over the rows, as a
 // per-head block would make them, measured twice as slow).  A (token, head)
-// row of 64 complex elements is one DPP row of 16 lanes; 16 rows per pass,
-// BWD_PASSES passes' loads issued before their arithmetic.  The per-(token, head,
+// row of d complex elements takes d / 4 lanes (d = 64: one DPP row of 16
+// lanes, 16 rows per pass), BWD_PASSES passes' loads issued before their
+// arithmetic.  The per-(token, head,
 // state) scalars are computed in token order (coalesced reads of the [M,B,H,T]
 // gradients), kept in LDS, and written state-fastest to the [B,T,H,M] outputs.
 constexpr int BT = 16;
@@ -250,15 +265,16 @@ constexpr int BT = 16;
 // waves per SIMD) left a third-full second round: 105 -> 96 us at that shape
 constexpr int BWD_PASSES = 2;
 
-template <typename TI, typename TO>
+template <int D, typename TI, typename TO>
 __global__ void __launch_bounds__(PTHREADS, 4) prologue_bwd_kernel(qpam_prologue_bwd_args g, qpam_prologue_args a) {
+    constexpr int LR = D / 4, RPP = PTHREADS / LR;  // lanes per row, rows per pass
     extern __shared__ float lds[];
     const int rows = BT * a.H, M = a.M;
     float *s_keep = lds, *s_gvv = lds + rows;
     float *s_dpre = lds + 2 * rows, *s_dpm = s_dpre + M * rows, *s_dph = s_dpm + M * rows, *s_dro = s_dph + M * rows;
     const int ntile = (a.T + BT - 1) / BT;
     const int b = blockIdx.x / ntile, t0 = (blockIdx.x - b * ntile) * BT;
-    const int tid = threadIdx.x, lane = tid & 63, c4 = (lane & 15) * 4, slot = tid >> 4;
+    const int tid = threadIdx.x, lane = tid & 63, c4 = (lane & (LR - 1)) * 4, slot = tid / LR;
 
     for (int r = tid; r < rows; r += PTHREADS) {  // row r = token-in-tile * H + head
         const int tt = r / a.H, h = r - tt * a.H, t = t0 + tt;
@@ -268,12 +284,12 @@ __global__ void __launch_bounds__(PTHREADS, 4) prologue_bwd_kernel(qpam_prologue
 
     const bool rope = a.rope != nullptr, norm = a.qk_norm != 0;
     const void *gplanes[6] = {g.gq_re, g.gq_im, g.gk_re, g.gk_im, g.gv_re, g.gv_im};
-    for (int r0 = 0; r0 < rows; r0 += 16 * BWD_PASSES) {
+    for (int r0 = 0; r0 < rows; r0 += RPP * BWD_PASSES) {
         typename Io<TO>::Raw graw[BWD_PASSES][6];
         typename Io<TI>::Raw vraw[BWD_PASSES][2];
 #pragma unroll
         for (int k = 0; k < BWD_PASSES; ++k) {   // rows past the tile re-read a valid row and are not stored
-            const int r = min(r0 + 16 * k + slot, rows - 1);
+            const int r = min(r0 + RPP * k + slot, rows - 1);
             const int tt = r / a.H, h = r - tt * a.H, t = min(t0 + tt, a.T - 1);
             const int64_t oo = (((int64_t)b * a.H + h) * a.T + t) * D + c4;
             const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
@@ -284,9 +300,9 @@ __global__ void __launch_bounds__(PTHREADS, 4) prologue_bwd_kernel(qpam_prologue
         }
 #pragma unroll
         for (int k = 0; k < BWD_PASSES; ++k) {
-            const int r = r0 + 16 * k + slot;
+            const int r = r0 + RPP * k + slot;
             const int tt = r / a.H, h = r - tt * a.H, t = t0 + tt;
-            // a DPP row (16 lanes) shares r, so it is either all in or all out
+            // the lanes of a row share r, so they are either all in or all out
             if (r >= rows || t >= a.T) continue;
             const int64_t xo = b * a.sx_b + (int64_t)t * a.sx_t + h * a.sx_h + c4;
             const int64_t go = b * g.sg_b + (int64_t)t * g.sg_t + h * g.sg_h + c4;
@@ -297,7 +313,7 @@ __global__ void __launch_bounds__(PTHREADS, 4) prologue_bwd_kernel(qpam_prologue
             Io<TI>::unpack(vraw[k][0], vr), Io<TI>::unpack(vraw[k][1], vi);
             if (rope || norm) {
                 float c[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
-                if (rope) rope4(a, t, c4, c, sn);
+                if (rope) rope4<D>(a, t, c4, c, sn);
                 float qr[4], qi[4], kr[4], ki[4];
                 if (norm) {
                     Io<TI>::load4(a.q_re, xo, qr), Io<TI>::load4(a.q_im, xo, qi);
@@ -316,8 +332,8 @@ __global__ void __launch_bounds__(PTHREADS, 4) prologue_bwd_kernel(qpam_prologue
                 dot += gvr[j] * vr[j] + gvi[j] * vi[j];
                 gvr[j] *= keep, gvi[j] *= keep;
             }
-            dot = row16_sum(dot);
-            if ((lane & 15) == 0) s_gvv[r] = dot;
+            dot = row_sum<LR>(dot);
+            if ((lane & (LR - 1)) == 0) s_gvv[r] = dot;
             Io<TI>::store4(g.dq_re, go, gqr), Io<TI>::store4(g.dq_im, go, gqi);
             Io<TI>::store4(g.dk_re, go, gkr), Io<TI>::store4(g.dk_im, go, gki);
             Io<TI>::store4(g.dv_re, go, gvr), Io<TI>::store4(g.dv_im, go, gvi);
@@ -481,7 +497,8 @@ int validate_inputs(const qpam_prologue_args *a) {
     QPAM_REQUIRE(a != nullptr, "qpam_prologue: null arguments");
     QPAM_REQUIRE(a->B >= 0 && a->T >= 0 && a->H >= 1 && a->M >= 1 && a->M <= 4,
                  "qpam_prologue: invalid sizes B=%d T=%d H=%d M=%d (1 <= M <= 4)", a->B, a->T, a->H, a->M);
-    QPAM_REQUIRE(a->d == D, "qpam_prologue: head_dim %d unsupported (64 only)", a->d);
+    QPAM_REQUIRE(a->d == 16 || a->d == 32 || a->d == 64 || a->d == 128,
+                 "qpam_prologue: head_dim %d unsupported (16, 32, 64 or 128)", a->d);
     QPAM_REQUIRE((a->in_dtype == QPAM_F32 || a->in_dtype == QPAM_BF16) &&
                      (a->out_dtype == QPAM_F32 || a->out_dtype == QPAM_BF16),
                  "qpam_prologue: dtypes must be QPAM_F32 or QPAM_BF16");
@@ -579,6 +596,26 @@ __global__ void __launch_bounds__(MAG_THREADS) mag_linear_kernel(int64_t rows, i
             }
     }
 }
+template <int D>
+void launch_fwd(const qpam_prologue_args &a, hipStream_t s) {
+    const dim3 grid((unsigned)((long long)a.B * a.H * ((a.T + PT - 1) / PT))), block(PTHREADS);
+    const bool fi = a.in_dtype == QPAM_F32, fo = a.out_dtype == QPAM_F32;
+    if (fi && fo) hipLaunchKernelGGL((prologue_fwd_kernel<D, float, float>), grid, block, 0, s, a);
+    else if (fi) hipLaunchKernelGGL((prologue_fwd_kernel<D, float, Bf16>), grid, block, 0, s, a);
+    else if (fo) hipLaunchKernelGGL((prologue_fwd_kernel<D, Bf16, float>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((prologue_fwd_kernel<D, Bf16, Bf16>), grid, block, 0, s, a);
+}
+
+template <int D>
+void launch_bwd(const qpam_prologue_bwd_args &g, const qpam_prologue_args &a, long long blocks, size_t lds,
+                hipStream_t s) {
+    const dim3 grid((unsigned)blocks), block(PTHREADS);
+    const bool fi = a.in_dtype == QPAM_F32, fo = a.out_dtype == QPAM_F32;
+    if (fi && fo) hipLaunchKernelGGL((prologue_bwd_kernel<D, float, float>), grid, block, lds, s, g, a);
+    else if (fi) hipLaunchKernelGGL((prologue_bwd_kernel<D, float, Bf16>), grid, block, lds, s, g, a);
+    else if (fo) hipLaunchKernelGGL((prologue_bwd_kernel<D, Bf16, float>), grid, block, lds, s, g, a);
+    else hipLaunchKernelGGL((prologue_bwd_kernel<D, Bf16, Bf16>), grid, block, lds, s, g, a);
+}
 }  // namespace
 }  // namespace qpam
 
@@ -591,12 +628,12 @@ extern "C" int qpam_prologue_fwd(const qpam_prologue_args *a, void *stream) {
     const long long blocks = (long long)a->B * a->H * ((a->T + PT - 1) / PT);
     if (blocks == 0) return QPAM_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)blocks), block(PTHREADS);
-    const bool fi = a->in_dtype == QPAM_F32, fo = a->out_dtype == QPAM_F32;
-    if (fi && fo) hipLaunchKernelGGL((prologue_fwd_kernel<float, float>), grid, block, 0, s, *a);
-    else if (fi) hipLaunchKernelGGL((prologue_fwd_kernel<float, Bf16>), grid, block, 0, s, *a);
-    else if (fo) hipLaunchKernelGGL((prologue_fwd_kernel<Bf16, float>), grid, block, 0, s, *a);
-    else hipLaunchKernelGGL((prologue_fwd_kernel<Bf16, Bf16>), grid, block, 0, s, *a);
+    switch (a->d) {
+        case 16: launch_fwd<16>(*a, s); break;
+        case 32: launch_fwd<32>(*a, s); break;
+        case 64: launch_fwd<64>(*a, s); break;
+        default: launch_fwd<128>(*a, s);
+    }
     return launch_status("prologue_fwd_kernel");
 }
 
@@ -636,12 +673,12 @@ extern "C" int qpam_prologue_bwd(const qpam_prologue_bwd_args *g, void *stream) 
                            0, a.H, a.M, a.param_dtype, g->dbias, g->doffset);
         return launch_status("prologue_bias_grad_kernel");
     }
-    const dim3 grid((unsigned)blocks), block(PTHREADS);
-    const bool fi = a.in_dtype == QPAM_F32, fo = a.out_dtype == QPAM_F32;
-    if (fi && fo) hipLaunchKernelGGL((prologue_bwd_kernel<float, float>), grid, block, lds, s, *g, a);
-    else if (fi) hipLaunchKernelGGL((prologue_bwd_kernel<float, Bf16>), grid, block, lds, s, *g, a);
-    else if (fo) hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, float>), grid, block, lds, s, *g, a);
-    else hipLaunchKernelGGL((prologue_bwd_kernel<Bf16, Bf16>), grid, block, lds, s, *g, a);
+    switch (a.d) {
+        case 16: launch_bwd<16>(*g, a, blocks, lds, s); break;
+        case 32: launch_bwd<32>(*g, a, blocks, lds, s); break;
+        case 64: launch_bwd<64>(*g, a, blocks, lds, s); break;
+        default: launch_bwd<128>(*g, a, blocks, lds, s);
+    }
     int st2 = launch_status("prologue_bwd_kernel");
     if (st2 || !sums) return st2;
     hipLaunchKernelGGL(prologue_bias_grad_kernel, dim3(1), dim3(BIAS_THREADS), bias_grad_lds(a.H, a.M), s, g->dpre,

@@ -32,8 +32,10 @@ table or new weights start new graphs.
 
 Prefill stays the fused layer forward (pam_layer.forward); its per-layer
 states enter the pool through `admit`.  The layers must use head-scalar decay,
-the additive write and head_dim 64 (the production presets); the engine reads
-their parameters by the reference's names.  The states, the prologue and the
+the additive write and head_dim 16, 32, 64 or 128 (64 in the production
+presets: its decode kernel forms q, k, v and the gates itself; the others run
+the prologue kernel before the decode kernel); the engine reads their
+parameters by the reference's names.  The states, the prologue and the
 decode kernel run in fp32; the projection and o_proj GEMMs run in fp32 or,
 with dtype=torch.bfloat16, on bf16 copies of the weights and inputs with fp32
 accumulation (the gates' small GEMMs stay fp32).
@@ -44,7 +46,7 @@ import torch.nn.functional as F
 
 from .decode import SlotPool
 from .pam_layer import _in_weight
-from .pam_prologue import HEAD_DIM, cabs, mag_linear, prologue_decode, proj_columns
+from .pam_prologue import HEAD_DIM, HEAD_DIMS, cabs, mag_linear, prologue_decode, proj_columns
 
 
 def _cat_planes(x):
@@ -70,8 +72,8 @@ class DecodeEngine:
             if getattr(layer, "decay_mode", "head") != "head" or getattr(layer, "write_mode", "additive") != "additive":
                 raise NotImplementedError("DecodeEngine runs the head-decay additive write (E1 / E2 layers decode "
                                           "through the reference's _recurrent)")
-            if layer.head_dim != HEAD_DIM or not 1 <= layer.n_states <= 4:
-                raise NotImplementedError("DecodeEngine needs head_dim 64 and 1 to 4 states")
+            if layer.head_dim not in HEAD_DIMS or not 1 <= layer.n_states <= 4:
+                raise NotImplementedError(f"DecodeEngine needs a head_dim in {HEAD_DIMS} and 1 to 4 states")
         device = l0.qkv_proj.weight_real.device
         self.graph_bucket = int(graph_bucket) if graphs else 0
         if graphs and self.graph_bucket < 1:
@@ -91,7 +93,7 @@ class DecodeEngine:
         """Rebuild the GEMM weights (and the summed decay bias) from the
         layers' parameters (call after changing them)."""
         h, d = self.n_heads, self.head_dim
-        cols = proj_columns(h)
+        cols = proj_columns(h, d)
         self._graphs = {}  # captured graphs hold the old weight tensors
         self._wver += 1
         self._w = []
@@ -198,7 +200,7 @@ class DecodeEngine:
         if not layer.use_rope:
             raise NotImplementedError("DecodeEngine applies RoPE per slot; layers without RoPE are not supported")
         out = torch.empty(n, h, d, 2, device=x.device, dtype=self.dtype)
-        if w["w_mag"] is not None and not layer.state_compete:
+        if w["w_mag"] is not None and not layer.state_compete and d == HEAD_DIM:
             # the gate logits from |x| in one launch, the prologue inside the decode kernel
             gl = mag_linear(x, w["w_mag"], w["b_mag"], out_dtype=self.dtype)
             y = self.pool.step_proj(layer_idx, proj.view(n, -1), w["dt_bias"], slots, q_scale=d ** -0.5,
@@ -214,7 +216,7 @@ class DecodeEngine:
             protect=None if protect is None else protect.view(n, 1, h),
             phase=None if phase is None else phase.view(n, 1, h, m),
             routing=None if routing is None else routing.view(n, 1, h, m),
-            qk_norm=layer.qk_norm, gamma_floor=layer.gamma_floor or 0.0)
+            qk_norm=layer.qk_norm, gamma_floor=layer.gamma_floor or 0.0, head_dim=d)
         # the prologue's planes go to the decode kernel as they are ([n, H, d] views)
         q, k, v = ((re[:, :, 0], im[:, :, 0]) for re, im in ((qr, qi), (kr, ki), (vr, vi)))
         g = gamma[..., 0].permute(1, 2, 0)                                    # [n, H, K] view

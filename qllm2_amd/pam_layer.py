@@ -18,7 +18,7 @@ Reference methods replaced (v11/model.py):
 
   forward                   785-843  prefill of the production modes (head
                                       decay, additive write, E3 fused or one
-                                      state, head_dim 64): projections as
+                                      state, head_dim 16/32/64/128): projections as
                                       planar GEMMs, one prologue kernel, the
                                       scan writing Y head-merged, o_proj on the
                                       planar Y; other calls go to the original
@@ -54,7 +54,7 @@ from . import fused_ce as _fused_ce
 from . import flash_pam as _flash_pam
 from . import triton_kernels as _tk
 from .pam_perchannel import perchannel_chunked
-from .pam_prologue import cabs, pam_prologue, proj_columns
+from .pam_prologue import HEAD_DIMS as _PROLOGUE_DIMS, cabs, pam_prologue, proj_columns
 from .pam_scan import chunk_for, pam_scan_interleaved, pam_scan_planar
 
 
@@ -316,7 +316,7 @@ def _out_weight(mod):
 def _fused_prefill(self, x, state):
     return (state is None and x.dim() == 4 and x.shape[1] > 1 and x.is_cuda
             and getattr(self, "decay_mode", "head") != "per_channel" and self.write_mode == "additive"
-            and self.head_dim == 64 and 1 <= self.n_states <= 4
+            and self.head_dim in _PROLOGUE_DIMS and 1 <= self.n_states <= 4
             and (self.n_states == 1 or getattr(self, "fused_e3", True)))
 
 
@@ -385,7 +385,7 @@ def forward(self, x, state=None, step_offset: int = 0):
     h, d, m = self.num_heads, self.head_dim, self.n_states
     n = b * t
     xc = x if x.is_contiguous() else x.contiguous()
-    cols = proj_columns(h)
+    cols = proj_columns(h, d)
     need_mag = (self.use_gsp and not self.gate_content_aware) or (m > 1 and not (self.routing_content_aware
                                                                                or self.state_compete))
     packed = _packed_in(self, xc.view(b, t, 2 * dim), h, cols, need_mag)
@@ -443,7 +443,7 @@ def forward(self, x, state=None, step_offset: int = 0):
     (qr, qi), (kr, ki), (vr, vi), gamma, rot = pam_prologue(
         proj, self.dt_bias, dt_bias2=self.dt_proj.bias, n_heads=h, n_states=m, state_offset=offsets,
         protect=None if gate_kw else protect, phase=None if gate_kw else phase, routing=routing, rope=rope,
-        rope_offset=step_offset, qk_norm=self.qk_norm, gamma_floor=self.gamma_floor or 0.0, **gate_kw)
+        rope_offset=step_offset, qk_norm=self.qk_norm, gamma_floor=self.gamma_floor or 0.0, head_dim=d, **gate_kw)
     o_dtype = self.o_proj.weight_real.dtype
     ck = chunk_for(self.chunk_size, t)
     # bf16 o_proj: the scan writes Y in bf16 itself (and reads its gradient in bf16)

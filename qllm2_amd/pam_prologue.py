@@ -28,12 +28,13 @@ from torch import Tensor
 
 from . import _lib
 
-HEAD_DIM = 64
+HEAD_DIM = 64                       # the layer's production head dim (the fused decode prologue's)
+HEAD_DIMS = (16, 32, 64, 128)       # head dims of the prologue kernels
 
 
-def proj_columns(n_heads):
-    """Width of `proj` for n_heads heads of 64: q, k, v planes, dt, padding to 8."""
-    return 6 * n_heads * HEAD_DIM + (n_heads + 7) // 8 * 8
+def proj_columns(n_heads, head_dim=HEAD_DIM):
+    """Width of `proj` for n_heads heads of head_dim: q, k, v planes, dt, padding to 8."""
+    return 6 * n_heads * head_dim + (n_heads + 7) // 8 * 8
 
 
 def _dt_code(t):
@@ -57,11 +58,13 @@ def _gate_views(gate, protect_col, phase_col, H, M):
     return prot, ph
 
 
-def _fill(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, rope_offset, qk_norm,
+def _fill(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, D, rope_offset, qk_norm,
           gamma_floor, gate=None, protect_col=-1, phase_col=-1):
     if not proj.is_cuda:
         raise ValueError("qpam prologue: tensors must be on the GPU (no CPU path in this library)")
-    d = HEAD_DIM
+    if D not in HEAD_DIMS:
+        raise NotImplementedError(f"the HIP prologue takes head dims {HEAD_DIMS}, not {D}")
+    d = D
     if proj.dim() != 3 or proj.shape[2] < 6 * H * d + H or proj.stride(2) != 1:
         raise ValueError(f"proj must be [B, T, >= {6 * H * d + H}] with contiguous columns, got {tuple(proj.shape)}")
     if not 1 <= M <= 4:
@@ -135,17 +138,17 @@ def _fill(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, 
 @torch.library.custom_op("qpam::prologue_fwd", mutates_args=())
 def prologue_fwd_op(proj: Tensor, protect: Optional[Tensor], phase: Optional[Tensor], routing: Optional[Tensor],
                     dt_bias: Tensor, dt_bias2: Optional[Tensor], state_offset: Optional[Tensor],
-                    rope: Optional[Tensor], H: int, M: int, rope_offset: int, qk_norm: bool, gamma_floor: float,
-                    gate: Optional[Tensor], protect_col: int, phase_col: int) -> List[Tensor]:
+                    rope: Optional[Tensor], H: int, M: int, D: int, rope_offset: int, qk_norm: bool,
+                    gamma_floor: float, gate: Optional[Tensor], protect_col: int, phase_col: int) -> List[Tensor]:
     """Returns [q_re, q_im, k_re, k_im, v_re, v_im] ([B,H,T,d], proj dtype),
     gamma [M,B,H,T] and rot_re, rot_im [M,B,H,T] (empty without phase).  With
     `gate` the protect and phase logits are its columns from protect_col /
     phase_col (-1: absent) and protect / phase / routing are None."""
-    a, keep = _fill(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, rope_offset, qk_norm,
+    a, keep = _fill(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, D, rope_offset, qk_norm,
                     gamma_floor, gate, protect_col, phase_col)
     B, T = proj.shape[0], proj.shape[1]
     dev = proj.device
-    outs = [torch.empty(B, H, T, HEAD_DIM, device=dev, dtype=proj.dtype) for _ in range(6)]
+    outs = [torch.empty(B, H, T, D, device=dev, dtype=proj.dtype) for _ in range(6)]
     a.oq_re, a.oq_im, a.ok_re, a.ok_im, a.ov_re, a.ov_im = (o.data_ptr() for o in outs)
     gamma = torch.empty(M, B, H, T, device=dev, dtype=torch.float32)
     a.gamma = gamma.data_ptr()
@@ -161,10 +164,10 @@ def prologue_fwd_op(proj: Tensor, protect: Optional[Tensor], phase: Optional[Ten
 
 
 @prologue_fwd_op.register_fake
-def _(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, rope_offset, qk_norm, gamma_floor,
+def _(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, D, rope_offset, qk_norm, gamma_floor,
       gate, protect_col, phase_col):
     B, T = proj.shape[0], proj.shape[1]
-    outs = [proj.new_empty(B, H, T, HEAD_DIM) for _ in range(6)]
+    outs = [proj.new_empty(B, H, T, D) for _ in range(6)]
     gamma = proj.new_empty(M, B, H, T, dtype=torch.float32)
     has_phase = phase is not None or (gate is not None and phase_col >= 0)
     rot = [gamma.new_empty(M, B, H, T) if has_phase else gamma.new_empty(0) for _ in range(2)]
@@ -185,14 +188,15 @@ def _gate_covered(gate, protect_col, phase_col, H, M):
 @torch.library.custom_op("qpam::prologue_bwd", mutates_args=())
 def prologue_bwd_op(proj: Tensor, protect: Optional[Tensor], phase: Optional[Tensor], routing: Optional[Tensor],
                     dt_bias: Tensor, dt_bias2: Optional[Tensor], state_offset: Optional[Tensor],
-                    rope: Optional[Tensor], H: int, M: int, rope_offset: int, qk_norm: bool, gamma_floor: float,
-                    gate: Optional[Tensor], protect_col: int, phase_col: int, grads: List[Tensor]) -> List[Tensor]:
+                    rope: Optional[Tensor], H: int, M: int, D: int, rope_offset: int, qk_norm: bool,
+                    gamma_floor: float, gate: Optional[Tensor], protect_col: int, phase_col: int,
+                    grads: List[Tensor]) -> List[Tensor]:
     """grads: the 9 output gradients (rot's empty without phase).  Returns
     [dproj ([B,T,C], padding columns zero), dprotect [B,T,H], dphase,
     drouting [B,T,H,M] (in the logits' dtype, empty where not applicable),
     dgate (gate's layout, or empty), dbias [H] (the gradient of dt_bias and of
     dt_bias2), doffset [M] (or empty), both in dt_bias's dtype]."""
-    a, keep = _fill(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, rope_offset, qk_norm,
+    a, keep = _fill(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, D, rope_offset, qk_norm,
                     gamma_floor, gate, protect_col, phase_col)
     B, T, C = proj.shape
     dev = proj.device
@@ -204,12 +208,12 @@ def prologue_bwd_op(proj: Tensor, protect: Optional[Tensor], phase: Optional[Ten
     if a.phase:
         g.grot_re, g.grot_im = gs[7].data_ptr(), gs[8].data_ptr()
     dproj = torch.empty(B, T, C, device=dev, dtype=proj.dtype)
-    used = 6 * H * HEAD_DIM + H
+    used = 6 * H * D + H
     g.ddt_pad = C - used                       # the kernel zeroes the padding columns
-    es, base, plane = dproj.element_size(), dproj.data_ptr(), H * HEAD_DIM
+    es, base, plane = dproj.element_size(), dproj.data_ptr(), H * D
     g.dq_re, g.dk_re, g.dv_re = (base + i * plane * es for i in range(3))
     g.dq_im, g.dk_im, g.dv_im = (base + (3 + i) * plane * es for i in range(3))
-    g.sg_b, g.sg_t, g.sg_h = dproj.stride(0), dproj.stride(1), HEAD_DIM
+    g.sg_b, g.sg_t, g.sg_h = dproj.stride(0), dproj.stride(1), D
     g.ddt = base + 6 * plane * es
     g.sdd_b, g.sdd_t, g.sdd_h = dproj.stride(0), dproj.stride(1), 1
     # scratch for the per-block partial sums of the decay-logit gradient
@@ -249,7 +253,7 @@ def prologue_bwd_op(proj: Tensor, protect: Optional[Tensor], phase: Optional[Ten
 
 
 @prologue_bwd_op.register_fake
-def _(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, rope_offset, qk_norm, gamma_floor,
+def _(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, D, rope_offset, qk_norm, gamma_floor,
       gate, protect_col, phase_col, grads):
     B, T, C = proj.shape
     e = proj.new_empty(0)
@@ -261,16 +265,16 @@ def _(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M
 
 
 def _setup(ctx, inputs, output):
-    (proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, rope_offset, qk_norm, gamma_floor,
+    (proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, D, rope_offset, qk_norm, gamma_floor,
      gate, protect_col, phase_col) = inputs
     ctx.save_for_backward(proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, gate)
-    ctx.cfg = (H, M, rope_offset, qk_norm, gamma_floor, protect_col, phase_col)
+    ctx.cfg = (H, M, D, rope_offset, qk_norm, gamma_floor, protect_col, phase_col)
     ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, grads):
     proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, gate = ctx.saved_tensors
-    H, M, rope_offset, qk_norm, gamma_floor, protect_col, phase_col = ctx.cfg
+    H, M, D, rope_offset, qk_norm, gamma_floor, protect_col, phase_col = ctx.cfg
     B, T = proj.shape[0], proj.shape[1]
     dev = proj.device
     has_phase = phase is not None or (gate is not None and phase_col >= 0)
@@ -279,17 +283,17 @@ def _backward(ctx, grads):
         if gr is not None:
             full.append(gr)
         elif i < 6:
-            full.append(torch.zeros(B, H, T, HEAD_DIM, device=dev, dtype=proj.dtype))
+            full.append(torch.zeros(B, H, T, D, device=dev, dtype=proj.dtype))
         elif i == 6 or has_phase:
             full.append(torch.zeros(M, B, H, T, device=dev, dtype=torch.float32))
         else:
             full.append(torch.empty(0, device=dev))
     dproj, dprotect, dphase, drouting, dgate, dbias, doffset = prologue_bwd_op(
-        proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, rope_offset, qk_norm, gamma_floor,
-        gate, protect_col, phase_col, full)
+        proj, protect, phase, routing, dt_bias, dt_bias2, state_offset, rope, H, M, D, rope_offset, qk_norm,
+        gamma_floor, gate, protect_col, phase_col, full)
     return (dproj, dprotect if protect is not None else None, dphase if phase is not None else None,
             drouting if routing is not None else None, dbias, dbias if dt_bias2 is not None else None,
-            doffset if state_offset is not None else None, None, None, None, None, None, None,
+            doffset if state_offset is not None else None, None, None, None, None, None, None, None,
             dgate if gate is not None else None, None, None)
 
 
@@ -298,7 +302,7 @@ prologue_fwd_op.register_autograd(_backward, setup_context=_setup)
 
 def pam_prologue(proj, dt_bias, *, n_heads, n_states=1, state_offset=None, protect=None, phase=None, routing=None,
                  rope=None, rope_offset=0, qk_norm=False, gamma_floor=0.0, dt_bias2=None, gate=None,
-                 protect_col=-1, phase_col=-1):
+                 protect_col=-1, phase_col=-1, head_dim=HEAD_DIM):
     """Differentiable prologue.  proj [B,T,C] (fp32 or bf16, layout above);
     protect [B,T,H] and phase, routing [B,T,H,M] (cast to proj's dtype; any
     strides), or `gate` [B,T,W] holding the protect logits in columns
@@ -306,8 +310,8 @@ def pam_prologue(proj, dt_bias, *, n_heads, n_states=1, state_offset=None, prote
     gradient then comes back as one tensor; dt_bias [H], dt_bias2 [H]
     (optional, added to dt_bias) and state_offset [M] in one dtype (fp32 or
     bf16; mixed dtypes are read in fp32); rope [P,d,2] fp32 covering
-    rope_offset + T.  Returns (q, k, v) as planar pairs [B,H,T,d],
-    gamma [M,B,H,T] and rot (re, im) [M,B,H,T] or None."""
+    rope_offset + T; head_dim 16, 32, 64 or 128.  Returns (q, k, v) as planar
+    pairs [B,H,T,d], gamma [M,B,H,T] and rot (re, im) [M,B,H,T] or None."""
     if rope is not None and rope_offset + proj.shape[1] > rope.shape[0]:
         raise ValueError(f"rope table of {rope.shape[0]} rows does not cover positions up to "
                          f"{rope_offset + proj.shape[1]}")
@@ -321,14 +325,14 @@ def pam_prologue(proj, dt_bias, *, n_heads, n_states=1, state_offset=None, prote
         if gate.stride(-1) != 1:
             gate = gate.contiguous()
     out = prologue_fwd_op(proj, cast(protect), cast(phase), cast(routing), dt_bias, dt_bias2, state_offset, rope,
-                          int(n_heads), int(n_states), int(rope_offset), bool(qk_norm), float(gamma_floor), gate,
-                          int(protect_col), int(phase_col))
+                          int(n_heads), int(n_states), int(head_dim), int(rope_offset), bool(qk_norm),
+                          float(gamma_floor), gate, int(protect_col), int(phase_col))
     rot = (out[7], out[8]) if phase is not None or (gate is not None and phase_col >= 0) else None
     return (out[0], out[1]), (out[2], out[3]), (out[4], out[5]), out[6], rot
 
 
 def prologue_decode(proj, dt_bias, *, n_heads, n_states=1, state_offset=None, protect=None, phase=None,
-                    routing=None, qk_norm=False, gamma_floor=0.0):
+                    routing=None, qk_norm=False, gamma_floor=0.0, head_dim=HEAD_DIM):
     """Inference form of pam_prologue for the decode step (no autograd, no
     RoPE): the q, k, v planes come out in fp32 whatever proj's dtype (fp32 or
     bf16), which is what the decode kernel reads, so a bf16 projection needs no
@@ -336,11 +340,11 @@ def prologue_decode(proj, dt_bias, *, n_heads, n_states=1, state_offset=None, pr
     cast = (lambda t: t.to(proj.dtype) if t is not None and t.dtype != proj.dtype else t)
     f32 = (lambda t: t.float() if t is not None and t.dtype != torch.float32 else t)
     a, keep = _fill(proj, cast(protect), cast(phase), cast(routing), f32(dt_bias), None, f32(state_offset), None,
-                    int(n_heads), int(n_states), 0, bool(qk_norm), float(gamma_floor))
+                    int(n_heads), int(n_states), int(head_dim), 0, bool(qk_norm), float(gamma_floor))
     a.out_dtype = _lib.QPAM_F32
     B, T, H, M = proj.shape[0], proj.shape[1], int(n_heads), int(n_states)
     dev = proj.device
-    outs = [torch.empty(B, H, T, HEAD_DIM, device=dev, dtype=torch.float32) for _ in range(6)]
+    outs = [torch.empty(B, H, T, int(head_dim), device=dev, dtype=torch.float32) for _ in range(6)]
     a.oq_re, a.oq_im, a.ok_re, a.ok_im, a.ov_re, a.ov_im = (o.data_ptr() for o in outs)
     gamma = torch.empty(M, B, H, T, device=dev, dtype=torch.float32)
     a.gamma = gamma.data_ptr()

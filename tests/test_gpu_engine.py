@@ -2,7 +2,9 @@
 against per-sequence float64 oracles.
 
 Two stacked PAM layers (E3 with three states, GSP, state competition, gamma
-floor; and a one-state stack with qk-norm) decode five sequences that join and
+floor; a one-state stack with qk-norm; at head dim 64, and E3 at 32 and one
+state at 128, whose steps run the prologue kernel before the decode kernel)
+decode five sequences that join and
 leave on a pool of four slots (a leaving sequence's slot is reused), in an
 unsorted live order, with prompts long enough to grow the pool's RoPE table.
 Each sequence is prefilled on the GPU by the fused layer forward
@@ -23,6 +25,8 @@ pytestmark = pytest.mark.gpu
 CFGS = {
     "e3": dict(dim=64, n_heads=2, head_dim=64, n_states=3, chunk_size=64, state_compete=True, gamma_floor=0.2),
     "one_state": dict(dim=64, n_heads=2, head_dim=64, n_states=1, chunk_size=64, qk_norm=True),
+    "e3_hd32": dict(dim=64, n_heads=2, head_dim=32, n_states=2, chunk_size=32, state_compete=True),
+    "hd128": dict(dim=128, n_heads=1, head_dim=128, n_states=1, chunk_size=64),
 }
 # (prompt length, join step, tokens decoded)
 SEQS = [(5, 0, 5), (12, 0, 9), (3, 1, 4), (20, 3, 7), (8, 6, 5)]

@@ -317,10 +317,11 @@ int qpam_decay_matrix(int32_t n, int32_t t, const float *gamma, int64_t ldg, flo
  * logits dt, protect, phase and routing are in in_dtype too (any strides).
  * q', k', v': planar [B,H,T,d] contiguous in out_dtype -- the scan's q, k, v.
  * gamma, rot: fp32 [M,B,H,T] contiguous -- the scan's gamma and rot.
- * d == 64, 1 <= M <= 4.  Rope rows past rope_len - 1 are clamped to the last
- * row (size the table to cover rope_offset + T).  dt_bias, dt_bias2 (an
- * nn.Linear's own bias, optional) and state_offset are read in param_dtype and
- * summed in fp32 (ABI 11; param_dtype 0 = fp32 as before).
+ * d in {16, 32, 64, 128}, 1 <= M <= 4.  Rope rows past rope_len - 1 are
+ * clamped to the last row (size the table to cover rope_offset + T).
+ * dt_bias, dt_bias2 (an nn.Linear's own bias, optional) and state_offset are
+ * read in param_dtype and summed in fp32 (ABI 11; param_dtype 0 = fp32 as
+ * before).
  */
 typedef struct {
     int32_t B, T, H, d, M;

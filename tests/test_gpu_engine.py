@@ -12,7 +12,10 @@ Each sequence is prefilled on the GPU by the fused layer forward
 output and each sequence's states before it leaves are compared with the
 oracle: V11PAMLayer.forward's prefill restatement (oracle/pam_layer.py
 layer_forward) and its decode form (layer_decode) chained over the layers,
-fp32 rel <= 1e-4."""
+fp32 rel <= 1e-4; with bf16 GEMMs (the projection read by the prologue in
+bf16, at head dims 64, 32 and 128) rel <= 5e-2: each decoded layer rounds to
+bf16 six times (its input, the two GEMMs' weights, the projection, y and the
+o_proj output, 2^-8 each), about 2.3e-2 to first order per layer, two layers."""
 
 import pytest
 import torch
@@ -38,8 +41,9 @@ def _rel(a, b):
 
 
 @pytest.mark.parametrize("graphs", [False, True])
-@pytest.mark.parametrize("name", list(CFGS))
-def test_engine_matches_per_sequence_oracle(gpu_lib, name, graphs):
+@pytest.mark.parametrize("name,dtype", [(n, torch.float32) for n in CFGS] +
+                         [(n, torch.bfloat16) for n in ("e3", "e3_hd32", "hd128")])
+def test_engine_matches_per_sequence_oracle(gpu_lib, name, dtype, graphs):
     """Eager steps, and HIP-graph replays (graph_bucket 2: odd live counts pad
     one row onto a scratch slot; each bucket is captured on its first step and
     replayed on later ones, with admissions, releases and a RoPE-table growth
@@ -51,7 +55,8 @@ def test_engine_matches_per_sequence_oracle(gpu_lib, name, graphs):
     params = [V.make_params(cfg, 800 + i) for i in range(n_layers)]
     layers = [V.V11PAMLayer(cfg, {k: v.float() for k, v in p.items()}, dtype=torch.float32).cuda().eval()
               for p in params]
-    engine = DecodeEngine(layers, n_slots=4, max_len=16, graphs=graphs, graph_bucket=2)
+    engine = DecodeEngine(layers, n_slots=4, max_len=16, graphs=graphs, graph_bucket=2, dtype=dtype)
+    tol = 1e-4 if dtype == torch.float32 else 5e-2
     g = torch.Generator().manual_seed(810)
     prompts = [torch.randn(1, t, dim, 2, generator=g, dtype=torch.float64) * 0.5 for t, _, _ in SEQS]
     tokens = [torch.randn(n, dim, 2, generator=g, dtype=torch.float64) * 0.5 for _, _, n in SEQS]
@@ -93,7 +98,7 @@ def test_engine_matches_per_sequence_oracle(gpu_lib, name, graphs):
                 for li in range(n_layers):
                     st = engine.layer_state(li, slot_of[si]).reshape(-1)
                     want = ref_state[si][li].reshape(-1)
-                    assert _rel(st, want) < 1e-4, f"seq {si} layer {li} state {_rel(st, want):.2e}"
+                    assert _rel(st, want) < tol, f"seq {si} layer {li} state {_rel(st, want):.2e}"
                 engine.release(slot_of[si])
                 done.add(si)
                 del slot_of[si]
@@ -103,7 +108,7 @@ def test_engine_matches_per_sequence_oracle(gpu_lib, name, graphs):
         assert len(engine._graphs) >= 2, "both buckets should have been captured"
     for si in range(len(SEQS)):
         out = torch.stack(got[si])
-        assert _rel(out, ref_out[si]) < 1e-4, f"seq {si}: {_rel(out, ref_out[si]):.2e}"
+        assert _rel(out, ref_out[si]) < tol, f"seq {si}: {_rel(out, ref_out[si]):.2e}"
 
 
 def test_engine_graph_replay_with_between_hook(gpu_lib):

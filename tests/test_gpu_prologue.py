@@ -304,11 +304,12 @@ def test_fused_layer_forward_matches_oracle(gpu_lib, over, T, offset, tol):
         assert _rel(got, ref_leaf.grad) < tol, f"{name}: {_rel(got, ref_leaf.grad):.2e}"
 
 
-def test_fused_layer_bf16(gpu_lib):
+@pytest.mark.parametrize("head_dim,n_states", [(64, 3), (32, 3), (128, 1)])
+def test_fused_layer_bf16(gpu_lib, head_dim, n_states):
     """The layer in bf16 (parameters and activations): bf16 projections, bf16
     scan operands with fp32 state; output and gradients within 2e-2 of the
     float64 oracle on the bf16-rounded parameters and input."""
-    cfg = _layer_cfg(n_states=3)
+    cfg = _layer_cfg(n_states=n_states, head_dim=head_dim)
     dim = 64
     p = {k: v.to(torch.bfloat16).double() for k, v in L.make_layer_params(cfg, dim, 950).items()}
     x = torch.randn(2, 256, dim, 2, generator=torch.Generator().manual_seed(951)).to(torch.bfloat16)
@@ -328,7 +329,8 @@ def test_fused_layer_bf16(gpu_lib):
     params = dict(layer.named_parameters())
     for name in ("qkv_proj.weight_real", "o_proj.weight_imag", "dt_bias", "state_dt_offset", "phase_proj.weight",
                  "protect_gate.weight"):
-        assert _rel(params[name].grad, pr[name].grad) < 2e-2, name
+        if name in pr:  # the one-state layer has no state offsets or phase projection
+            assert _rel(params[name].grad, pr[name].grad) < 2e-2, name
 
 
 def test_fused_layer_graph_capture(gpu_lib):

@@ -58,6 +58,12 @@ def _rows(t, name):
         raise ValueError(f"qpam {name}: expected a CUDA [n, dim, 2] tensor with contiguous rows")
 
 
+def _vec(t, n, device, name, what):
+    """A parameter vector the kernel reads n fp32 values from."""
+    if not (t.dtype == torch.float32 and t.device == device and t.numel() == n and t.is_contiguous()):
+        raise ValueError(f"qpam {name}: {what} must be a contiguous float32 tensor of {n} elements on {device}")
+
+
 def resid_norm(x, scale, eps, y=None, y_scale=None, out_dtype=torch.float32):
     """The residual add and the ComplexNorm after it in one launch
     (qpam_resid_norm; V11Block.forward, v11/model.py:1045-1048, inference):
@@ -68,6 +74,7 @@ def resid_norm(x, scale, eps, y=None, y_scale=None, out_dtype=torch.float32):
     if x.dtype != torch.float32:
         raise ValueError("qpam resid_norm: x must be float32")
     n, dim = x.shape[0], x.shape[1]
+    _vec(scale, dim, x.device, "resid_norm", "scale")
     out = torch.empty(n, dim, 2, device=x.device, dtype=out_dtype)
     a = _lib.ResidNormArgs()
     a.rows, a.dim, a.eps = n, dim, float(eps)
@@ -76,6 +83,7 @@ def resid_norm(x, scale, eps, y=None, y_scale=None, out_dtype=torch.float32):
         _rows(y, "resid_norm")
         if y.shape != x.shape or y_scale is None:
             raise ValueError("qpam resid_norm: y must match x and come with y_scale")
+        _vec(y_scale, 1, x.device, "resid_norm", "y_scale")
         a.y, a.y_dtype, a.ldy, a.y_scale = y.data_ptr(), _code(y), y.stride(0), y_scale.data_ptr()
     a.norm_scale = scale.data_ptr()
     a.out, a.out_dtype, a.ldo = out.data_ptr(), _code(out), out.stride(0)
@@ -94,6 +102,9 @@ def cgu_mix(gu, hid, bias, beta=None, phase_alpha=None, phase_beta=None, out_dty
     if not (gu.is_cuda and gu.dim() == 2 and gu.shape[1] == 4 * hid and gu.stride(1) == 1):
         raise ValueError("qpam cgu_mix: expected a CUDA [n, 4 hid] tensor with contiguous rows")
     n = gu.shape[0]
+    for what, t in (("bias", bias), ("beta", beta), ("phase_alpha", phase_alpha), ("phase_beta", phase_beta)):
+        if t is not None:
+            _vec(t, hid, gu.device, "cgu_mix", what)
     out = torch.empty(n, hid, 2, device=gu.device, dtype=out_dtype or gu.dtype)
     a = _lib.CguMixArgs()
     a.rows, a.hid = n, hid

@@ -232,3 +232,23 @@ def test_block_glue_rejects_bad_arguments(gpu_lib):
     gu = torch.randn(3, 4 * 8, device="cuda")
     with pytest.raises(_lib.QpamError, match="given together"):
         cgu_mix(gu, 8, torch.zeros(8, device="cuda"), torch.ones(8, device="cuda"), torch.zeros(8, device="cuda"), None)
+
+
+def test_block_glue_wrappers_check_parameters(gpu_lib):
+    """The host wrappers refuse parameter vectors the kernels would misread
+    (wrong length, dtype or device) before any launch."""
+    from qllm2_amd.model_decode import cgu_mix, resid_norm
+    x = torch.randn(4, 16, 2, device="cuda")
+    with pytest.raises(ValueError, match="scale"):
+        resid_norm(x, torch.ones(8, device="cuda"), 1e-6)
+    with pytest.raises(ValueError, match="scale"):
+        resid_norm(x, torch.ones(16, device="cuda", dtype=torch.bfloat16), 1e-6)
+    with pytest.raises(ValueError, match="scale"):
+        resid_norm(x, torch.ones(16), 1e-6)
+    with pytest.raises(ValueError, match="y_scale"):
+        resid_norm(x, torch.ones(16, device="cuda"), 1e-6, y=x.clone(), y_scale=torch.ones(2, device="cuda"))
+    gu = torch.randn(3, 4 * 8, device="cuda")
+    with pytest.raises(ValueError, match="bias"):
+        cgu_mix(gu, 8, torch.zeros(4, device="cuda"))
+    with pytest.raises(ValueError, match="beta"):
+        cgu_mix(gu, 8, torch.zeros(8, device="cuda"), torch.ones(8, device="cuda", dtype=torch.float64))

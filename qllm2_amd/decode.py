@@ -187,6 +187,15 @@ def decode_step_proj(state, proj, dt_bias, *, gate=None, protect_col=-1, phase_c
         raise ValueError(f"gate must be [{rows}, W] in proj's dtype with contiguous rows")
     if state.dtype != torch.float32 or state.stride()[-3:] != (2 * d, 2, 1):
         raise ValueError("state must be fp32 with contiguous [d, d, 2] matrices")
+    # the gate columns the kernel reads must lie inside the gate matrix
+    width = gate.shape[1] if gate is not None else 0
+    if protect_col >= 0 and protect_col + n_groups > width:
+        raise ValueError(f"protect columns {protect_col}..{protect_col + n_groups - 1} outside the gate's {width}")
+    if phase_col >= 0 and phase_col + n_groups * n_states > width:
+        raise ValueError(f"phase columns {phase_col}..{phase_col + n_groups * n_states - 1} outside the gate's "
+                         f"{width}")
+    if dt_bias.numel() != n_groups or (state_offset is not None and state_offset.numel() != n_states):
+        raise ValueError(f"dt_bias must have {n_groups} elements and state_offset {n_states}")
     dt_bias = dt_bias.float().contiguous()
     state_offset = state_offset.float().contiguous() if state_offset is not None else None
     y = out if out is not None else torch.zeros(rows, n_groups, d, 2, device=state.device, dtype=torch.float32)
@@ -218,8 +227,12 @@ def decode_step_proj(state, proj, dt_bias, *, gate=None, protect_col=-1, phase_c
     if rope is not None:
         if pos is None:
             raise ValueError("rope needs per-slot positions `pos`")
+        if rope.dtype != torch.float32 or tuple(rope.shape[1:]) != (d, 2):
+            raise ValueError(f"rope must be fp32 [P, {d}, 2], got {rope.dtype} {tuple(rope.shape)}")
         rope = rope.contiguous()
         pos = pos.to(torch.int32).contiguous()
+        if pos.numel() != n_slots:
+            raise ValueError(f"pos must hold one position per slot ({n_slots}), got {pos.numel()}")
         a.rope, a.pos, a.rope_len = rope.data_ptr(), pos.data_ptr(), rope.shape[0]
     with torch.cuda.device(state.device):
         _lib.check(_lib.lib().qpam_decode_step(a, _lib.stream_ptr(state.device)), "qpam_decode_step")

@@ -364,9 +364,15 @@ def mag_linear(z, weight, bias=None, out_dtype=torch.float32):
     out [n, G] = |z| weight^T + bias in out_dtype (|z| as cabs)."""
     if not z.is_cuda:
         raise ValueError("qpam mag_linear: tensors must be on the GPU (no CPU path in this library)")
+    if not (z.dim() == 3 and z.shape[2] == 2 and z.dtype in (torch.float32, torch.bfloat16)):
+        raise ValueError("qpam mag_linear: z must be a float32 or bfloat16 [n, dim, 2] tensor")
     z = z.contiguous()
     n, dim = z.shape[0], z.shape[1]
+    if not (weight.dim() == 2 and weight.shape[1] == dim and weight.device == z.device):
+        raise ValueError(f"qpam mag_linear: weight must be [G, {dim}] on {z.device}")
     G = weight.shape[0]
+    if bias is not None and not (bias.numel() == G and bias.device == z.device):
+        raise ValueError(f"qpam mag_linear: bias must have {G} elements on {z.device}")
     w = weight.float().contiguous()
     b = bias.float().contiguous() if bias is not None else None
     out = torch.empty(n, G, device=z.device, dtype=out_dtype)

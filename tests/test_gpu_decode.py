@@ -362,3 +362,32 @@ def test_decode_step_proj_matches_prologue_then_decode(M, qk_norm, floor, gsp, d
     assert ((st_a - st_b).abs().max() / scale(st_b)).item() < 1e-5
     untouched = [s for s in range(S) if s not in active.tolist()]
     assert torch.equal(st_a[untouched], state0[untouched])
+
+
+def test_decode_step_proj_checks_arguments(gpu_lib):
+    """The fused-prologue decode wrapper refuses gate columns outside the gate
+    matrix, decay-bias / state-offset vectors of the wrong length and a RoPE
+    table of another head dim, before any launch."""
+    from qllm2_amd.decode import decode_step_proj
+    S, G, M, d = 2, 2, 2, 64
+    state = torch.zeros(S, G, M, d, d, 2, device="cuda")
+    proj = torch.zeros(S, 6 * G * d + G, device="cuda")
+    gate = torch.zeros(S, G + G * M, device="cuda")
+    dt_bias, off = torch.zeros(G, device="cuda"), torch.zeros(M, device="cuda")
+    ok = dict(gate=gate, protect_col=0, phase_col=G, state_offset=off)
+    with pytest.raises(ValueError, match="protect columns"):
+        decode_step_proj(state, proj, dt_bias, **{**ok, "protect_col": G + G * M - 1})
+    with pytest.raises(ValueError, match="phase columns"):
+        decode_step_proj(state, proj, dt_bias, **{**ok, "phase_col": G + 1})
+    with pytest.raises(ValueError, match="phase columns"):
+        decode_step_proj(state, proj, dt_bias, phase_col=0)  # no gate matrix at all
+    with pytest.raises(ValueError, match="dt_bias"):
+        decode_step_proj(state, proj, torch.zeros(G + 1, device="cuda"), **ok)
+    with pytest.raises(ValueError, match="state_offset"):
+        decode_step_proj(state, proj, dt_bias, **{**ok, "state_offset": torch.zeros(M + 1, device="cuda")})
+    with pytest.raises(ValueError, match="rope"):
+        decode_step_proj(state, proj, dt_bias, **ok, rope=torch.zeros(8, 32, 2, device="cuda"),
+                         pos=torch.zeros(S, dtype=torch.int32, device="cuda"))
+    y = decode_step_proj(state, proj, dt_bias, **ok)  # the valid call runs
+    torch.cuda.synchronize()
+    assert y.shape == (S, G, d, 2)

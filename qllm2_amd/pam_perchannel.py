@@ -63,6 +63,9 @@ class _Fold(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, gamma, chunk, q_scale):
+        if q.dim() != 5 or q.shape[-1] != 2 or k.shape != q.shape or gamma.shape != q.shape[:4]:
+            raise ValueError(f"qpam per-channel fold: q, k [B,H,T,d,2] and gamma [B,H,T,d] expected, got "
+                             f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(gamma.shape)}")
         q, k = _pairs(q), _pairs(k.to(q.dtype))
         gamma = gamma if gamma.stride(-1) == 1 else gamma.contiguous()
         B, H, T, d = q.shape[:4]
@@ -122,6 +125,9 @@ class _Scan(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, a):
+        if a.dim() != 3 or x.shape != (*a.shape, a.shape[2], 2):
+            raise ValueError(f"qpam per-channel scan: x [N,n,d,d,2] and a [N,n,d] expected, got "
+                             f"{tuple(x.shape)}, {tuple(a.shape)}")
         x, a = x.contiguous(), a.contiguous()
         N, n, d = a.shape
         out = torch.empty_like(x)

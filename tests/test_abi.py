@@ -88,6 +88,24 @@ def test_complex_op_argument_errors_without_gpu():
     assert lib.qpam_cplx_workspace_size(ctypes.byref(a)) == 1 * 1 * 8 * 4  # one block, one parameter
 
 
+@pytest.mark.parametrize("d", [8, 24, 48, 96, 256])
+def test_prologue_refuses_head_dims_outside_its_kernels(d):
+    """The prologue's C entry points take exactly the head dims the Python side
+    dispatches to them (pam_prologue.HEAD_DIMS); any other is an error before
+    any launch, forward and backward."""
+    from qllm2_amd.pam_prologue import HEAD_DIMS
+    assert HEAD_DIMS == (16, 32, 64, 128)
+    lib = _lib.lib()
+    a = _lib.PrologueArgs()
+    a.B, a.T, a.H, a.M, a.d = 1, 1, 1, 1, d
+    assert lib.qpam_prologue_fwd(ctypes.byref(a), None) != 0
+    assert b"head_dim %d unsupported" % d in lib.qpam_last_error()
+    g = _lib.PrologueBwdArgs()
+    g.fwd = ctypes.pointer(a)
+    assert lib.qpam_prologue_bwd(ctypes.byref(g), None) != 0
+    assert b"head_dim %d unsupported" % d in lib.qpam_last_error()
+
+
 def test_cpu_tensors_are_refused():
     from qllm2_amd import decode, pam_scan
     s = torch.zeros(1, 1, 1, 4, 4, 2)

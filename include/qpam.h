@@ -712,7 +712,8 @@ typedef struct {
     const float *lse;              /* from qpam_ce_fwd */
     const float *grad_scale;       /* device scalar: grad_output / denom */
     void *dh; int64_t lddh;        /* dtype of h */
-    float *dw; int64_t lddw;       /* fp32, accumulated (caller zeroes) */
+    void *dw; int64_t lddw;        /* dw_out 0: fp32, accumulated (the caller zeroes it);
+                                      dw_out 1: written, in dtype */
     int32_t chunk;                 /* the reference's row chunk: one pass covers as many rows
                                       as fit the bytes the reference keeps alive for `chunk`
                                       rows (fp32 logits and softmax): 4 chunk rows with bf16
@@ -720,6 +721,10 @@ typedef struct {
                                       with the hand-written GEMMs (G and G^T), chunk rows fp32 */
     void *workspace;
     size_t workspace_bytes;
+    int32_t dw_out;                /* ABI 14: 0 = dw accumulated in fp32 as above; 1 = dw written
+                                      (not accumulated) in dtype -- with bf16 inputs the weight
+                                      gradient leaves in bf16 from the fp32 sums, with no
+                                      conversion pass after the call */
 } qpam_ce_bwd_args;
 
 size_t qpam_ce_bwd_workspace_size(const qpam_ce_bwd_args *a);

@@ -12,7 +12,7 @@ import os
 import torch  # noqa: F401  (must be loaded before the HIP library)
 
 LIB_NAME = "libqpam.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 _HERE = os.path.dirname(os.path.abspath(__file__))
 
 QPAM_F32 = 0
@@ -102,6 +102,7 @@ class CeBwdArgs(ctypes.Structure):
         ("dh", c_ptr), ("lddh", c_i64), ("dw", c_ptr), ("lddw", c_i64),
         ("chunk", c_i32),
         ("workspace", c_ptr), ("workspace_bytes", ctypes.c_size_t),
+        ("dw_out", c_i32),
     ]
 
 

@@ -45,7 +45,7 @@ int side_stream(SideStream *&out) {
 }
 }  // namespace qpam
 
-extern "C" int qpam_version(void) { return 13; }
+extern "C" int qpam_version(void) { return 14; }
 
 extern "C" const char *qpam_last_error(void) { return qpam::last_error_slot().c_str(); }
 

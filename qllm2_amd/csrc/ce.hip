@@ -711,7 +711,7 @@ __global__ void __launch_bounds__(THREADS, 2) dw_gemm_kernel(GroupParams q) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + 128 * wm + 16 * mi + 4 * g + r, n = n0 + 64 * wn + 16 * ni + l16;
-                if (m < a.V && n < a.D) a.dw[(int64_t)m * a.lddw + n] += acc[mi][ni][r];
+                if (m < a.V && n < a.D) static_cast<float *>(a.dw)[(int64_t)m * a.lddw + n] += acc[mi][ni][r];
             }
 }
 
@@ -1171,7 +1171,7 @@ int pass_rows(const qpam_ce_bwd_args &a) {
 }
 
 template <typename T>
-size_t bwd_ws(const qpam_ce_bwd_args &a) {
+size_t bwd_ws_base(const qpam_ce_bwd_args &a) {
     const int64_t Vp = round_up(a.V, vocab_pad<T>()), chunk = pass_rows(a);
     const int64_t Rp = round_up((int)chunk, row_tile<T>());
     if (is_bf<T>() && blas::enabled())  // G^T and the library GEMMs' workspace
@@ -1182,6 +1182,38 @@ size_t bwd_ws(const qpam_ce_bwd_args &a) {
     // bf16: split-K partials of the hand-written dH GEMM
     if (is_bf<T>()) bytes += std::max((size_t)big::DH_SPLITS * chunk * a.D * sizeof(float), blas::WS_BYTES) + 256;
     return bytes;
+}
+
+// dw_out 1 with bf16 inputs, the library GEMMs and one pass over the rows: the
+// dW GEMM writes the bf16 gradient itself (beta 0), from its fp32 sums
+bool dw_direct(const qpam_ce_bwd_args &a) {
+    return a.dw_out == 1 && a.dtype == QPAM_BF16 && blas::enabled() && pass_rows(a) >= a.N;
+}
+
+// dw_out 1 otherwise: bf16 inputs accumulate dW in fp32 after the passes' own
+// workspace (V x D, 256-byte aligned) and convert it once at the end
+template <typename T>
+size_t bwd_ws(const qpam_ce_bwd_args &a) {
+    const size_t base = bwd_ws_base<T>(a);
+    if (a.dw_out != 1 || !is_bf<T>() || dw_direct(a)) return base;
+    return base + 256 + (size_t)a.V * a.D * sizeof(float);
+}
+
+__global__ void __launch_bounds__(THREADS) dw_fill_kernel(float *p, int64_t rows, int cols, int64_t ld) {
+    const int64_t n = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * THREADS) {
+        const int64_t r = i / cols;
+        p[r * ld + (i - r * cols)] = 0.f;
+    }
+}
+
+__global__ void __launch_bounds__(THREADS) dw_cast_kernel(const float *src, int64_t lds, unsigned short *dst,
+                                                          int64_t ldd, int64_t rows, int cols) {
+    const int64_t n = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * THREADS + threadIdx.x; i < n; i += (int64_t)gridDim.x * THREADS) {
+        const int64_t r = i / cols, c = i - r * cols;
+        dst[r * ldd + c] = f32_to_bf16(src[r * lds + c]);
+    }
 }
 
 template <typename T>
@@ -1232,7 +1264,8 @@ int run_fwd(const qpam_ce_fwd_args &a, hipStream_t stream) {
     return st;
 }
 
-int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
+// dw_bf16: dW written in bf16 by the library GEMM (beta 0; one pass over the rows)
+int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream, bool dw_bf16 = false) {
     using U = unsigned short;
     big::GroupParams q;
     BwdParams &p = q.p;
@@ -1272,7 +1305,8 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream) {
             int st = launch_grad();
             if (st) return st;
             st = blas::gemm_bf16(false, false, a.D, a.V, p.rows, (const U *)a.h + (int64_t)r0 * a.ldh, a.ldh,
-                                 p.gtbuf, p.Rp, 1.f, a.dw, a.lddw, true, q.dh_part, blas_ws, stream);
+                                 p.gtbuf, p.Rp, dw_bf16 ? 0.f : 1.f, a.dw, a.lddw, !dw_bf16, q.dh_part, blas_ws,
+                                 stream);
             if (st) return st;
             st = blas::gemm_bf16(false, true, a.D, p.rows, a.V, a.w, a.ldw, p.gtbuf, p.Rp, 0.f,
                                  (U *)a.dh + (int64_t)r0 * a.lddh, a.lddh, false, q.dh_part, blas_ws, stream);
@@ -1434,9 +1468,32 @@ extern "C" int qpam_ce_bwd(const qpam_ce_bwd_args *a, void *stream) {
     QPAM_REQUIRE(a->lse && a->grad_scale && a->dh && a->dw, "qpam_ce_bwd: null lse/grad_scale/dh/dw");
     QPAM_REQUIRE(a->chunk >= 1, "qpam_ce_bwd: chunk must be >= 1");
     QPAM_REQUIRE(a->lddh >= a->D && a->lddw >= a->D, "qpam_ce_bwd: output leading dims must be >= D");
+    QPAM_REQUIRE(a->dw_out == 0 || a->dw_out == 1, "qpam_ce_bwd: dw_out must be 0 or 1");
     const size_t need = qpam_ce_bwd_workspace_size(a);
     QPAM_REQUIRE(a->workspace && a->workspace_bytes >= need && ((uintptr_t)a->workspace % 16) == 0,
                  "qpam_ce_bwd: workspace needs %zu bytes (got %zu)", need, a->workspace_bytes);
-    return a->dtype == QPAM_BF16 ? run_bwd<unsigned short>(*a, (hipStream_t)stream)
-                                 : run_bwd<float>(*a, (hipStream_t)stream);
+    hipStream_t s = (hipStream_t)stream;
+    if (a->dw_out == 0) return a->dtype == QPAM_BF16 ? run_bwd<unsigned short>(*a, s) : run_bwd<float>(*a, s);
+    if (dw_direct(*a)) return run_bwd_bf16(*a, s, true);
+    // dW accumulated in fp32 -- dw itself for fp32 inputs, else the workspace's tail -- from zero
+    qpam_ce_bwd_args b = *a;
+    b.dw_out = 0;
+    float *acc = static_cast<float *>(a->dw);
+    int64_t ld = a->lddw;
+    if (a->dtype == QPAM_BF16) {
+        acc = (float *)(((uintptr_t)a->workspace + bwd_ws_base<unsigned short>(b) + 255) & ~(uintptr_t)255);
+        ld = a->D;
+    }
+    const int64_t n = (int64_t)a->V * a->D;
+    const dim3 grid((unsigned)std::min<int64_t>((n + THREADS - 1) / THREADS, 65536));
+    hipLaunchKernelGGL(dw_fill_kernel, grid, dim3(THREADS), 0, s, acc, (int64_t)a->V, a->D, ld);
+    st = launch_status("ce dw_fill_kernel");
+    if (st) return st;
+    b.dw = acc;
+    b.lddw = ld;
+    st = a->dtype == QPAM_BF16 ? run_bwd<unsigned short>(b, s) : run_bwd<float>(b, s);
+    if (st || a->dtype != QPAM_BF16) return st;
+    hipLaunchKernelGGL(dw_cast_kernel, grid, dim3(THREADS), 0, s, (const float *)acc, ld, (unsigned short *)a->dw,
+                       a->lddw, (int64_t)a->V, a->D);
+    return launch_status("ce dw_cast_kernel");
 }

@@ -112,7 +112,12 @@ def ce_bwd_op(hidden_rows: Tensor, weight_matrix: Tensor, targets: Tensor, mask:
     targets, mask = _prep_targets(targets, mask, h.shape[0])
     dev = h.device
     dh = torch.empty_like(h)
-    dw = torch.zeros(w.shape, device=dev, dtype=torch.float32)
+    # the weight's own dtype is the working one: the library writes dW in it (no
+    # zero fill, no conversion pass); an fp32 master weight run on its bf16 copy
+    # keeps the fp32 accumulation
+    write_dw = weight_matrix.dtype == w.dtype
+    dw = (torch.empty(w.shape, device=dev, dtype=w.dtype) if write_dw
+          else torch.zeros(w.shape, device=dev, dtype=torch.float32))
     gs = grad_scale.to(torch.float32).reshape(1).contiguous()
     a = _lib.CeBwdArgs()
     a.N, a.V, a.D, a.dtype = h.shape[0], w.shape[0], h.shape[1], dtype
@@ -123,6 +128,7 @@ def ce_bwd_op(hidden_rows: Tensor, weight_matrix: Tensor, targets: Tensor, mask:
     a.lse, a.grad_scale = lse.data_ptr(), gs.data_ptr()
     a.dh, a.lddh, a.dw, a.lddw = dh.data_ptr(), dh.stride(0), dw.data_ptr(), dw.stride(0)
     a.chunk = int(max(1, min(chunk, h.shape[0])))
+    a.dw_out = 1 if write_dw else 0
     L = _lib.lib()
     nbytes = L.qpam_ce_bwd_workspace_size(a)
     ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)

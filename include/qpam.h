@@ -713,7 +713,7 @@ typedef struct {
     const float *grad_scale;       /* device scalar: grad_output / denom */
     void *dh; int64_t lddh;        /* dtype of h */
     void *dw; int64_t lddw;        /* dw_out 0: fp32, accumulated (the caller zeroes it);
-                                      dw_out 1: written, in dtype */
+                                      1: written, in dtype; 2: written, fp32 */
     int32_t chunk;                 /* the reference's row chunk: one pass covers as many rows
                                       as fit the bytes the reference keeps alive for `chunk`
                                       rows (fp32 logits and softmax): 4 chunk rows with bf16
@@ -724,7 +724,8 @@ typedef struct {
     int32_t dw_out;                /* ABI 14: 0 = dw accumulated in fp32 as above; 1 = dw written
                                       (not accumulated) in dtype -- with bf16 inputs the weight
                                       gradient leaves in bf16 from the fp32 sums, with no
-                                      conversion pass after the call */
+                                      conversion pass after the call; 2 = dw written in fp32 (an
+                                      fp32 master weight run on its bf16 copy), no zero fill */
 } qpam_ce_bwd_args;
 
 size_t qpam_ce_bwd_workspace_size(const qpam_ce_bwd_args *a);

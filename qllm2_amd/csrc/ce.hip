@@ -1184,10 +1184,11 @@ size_t bwd_ws_base(const qpam_ce_bwd_args &a) {
     return bytes;
 }
 
-// dw_out 1 with bf16 inputs, the library GEMMs and one pass over the rows: the
-// dW GEMM writes the bf16 gradient itself (beta 0), from its fp32 sums
+// dw_out 1 or 2 with bf16 inputs, the library GEMMs and one pass over the rows:
+// the dW GEMM writes the gradient itself (beta 0) from its fp32 sums, in bf16
+// or fp32
 bool dw_direct(const qpam_ce_bwd_args &a) {
-    return a.dw_out == 1 && a.dtype == QPAM_BF16 && blas::enabled() && pass_rows(a) >= a.N;
+    return a.dw_out != 0 && a.dtype == QPAM_BF16 && blas::enabled() && pass_rows(a) >= a.N;
 }
 
 // dw_out 1 otherwise: bf16 inputs accumulate dW in fp32 after the passes' own
@@ -1264,8 +1265,9 @@ int run_fwd(const qpam_ce_fwd_args &a, hipStream_t stream) {
     return st;
 }
 
-// dw_bf16: dW written in bf16 by the library GEMM (beta 0; one pass over the rows)
-int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream, bool dw_bf16 = false) {
+// dw_write: dW written (beta 0; one pass over the rows) by the library GEMM, in
+// bf16 (dw_out 1) or fp32 (dw_out 2); otherwise added into the fp32 dW
+int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream, bool dw_write = false) {
     using U = unsigned short;
     big::GroupParams q;
     BwdParams &p = q.p;
@@ -1305,8 +1307,8 @@ int run_bwd_bf16(const qpam_ce_bwd_args &a, hipStream_t stream, bool dw_bf16 = f
             int st = launch_grad();
             if (st) return st;
             st = blas::gemm_bf16(false, false, a.D, a.V, p.rows, (const U *)a.h + (int64_t)r0 * a.ldh, a.ldh,
-                                 p.gtbuf, p.Rp, dw_bf16 ? 0.f : 1.f, a.dw, a.lddw, !dw_bf16, q.dh_part, blas_ws,
-                                 stream);
+                                 p.gtbuf, p.Rp, dw_write ? 0.f : 1.f, a.dw, a.lddw, !(dw_write && a.dw_out == 1),
+                                 q.dh_part, blas_ws, stream);
             if (st) return st;
             st = blas::gemm_bf16(false, true, a.D, p.rows, a.V, a.w, a.ldw, p.gtbuf, p.Rp, 0.f,
                                  (U *)a.dh + (int64_t)r0 * a.lddh, a.lddh, false, q.dh_part, blas_ws, stream);
@@ -1468,19 +1470,20 @@ extern "C" int qpam_ce_bwd(const qpam_ce_bwd_args *a, void *stream) {
     QPAM_REQUIRE(a->lse && a->grad_scale && a->dh && a->dw, "qpam_ce_bwd: null lse/grad_scale/dh/dw");
     QPAM_REQUIRE(a->chunk >= 1, "qpam_ce_bwd: chunk must be >= 1");
     QPAM_REQUIRE(a->lddh >= a->D && a->lddw >= a->D, "qpam_ce_bwd: output leading dims must be >= D");
-    QPAM_REQUIRE(a->dw_out == 0 || a->dw_out == 1, "qpam_ce_bwd: dw_out must be 0 or 1");
+    QPAM_REQUIRE(a->dw_out >= 0 && a->dw_out <= 2, "qpam_ce_bwd: dw_out must be 0, 1 or 2");
     const size_t need = qpam_ce_bwd_workspace_size(a);
     QPAM_REQUIRE(a->workspace && a->workspace_bytes >= need && ((uintptr_t)a->workspace % 16) == 0,
                  "qpam_ce_bwd: workspace needs %zu bytes (got %zu)", need, a->workspace_bytes);
     hipStream_t s = (hipStream_t)stream;
     if (a->dw_out == 0) return a->dtype == QPAM_BF16 ? run_bwd<unsigned short>(*a, s) : run_bwd<float>(*a, s);
     if (dw_direct(*a)) return run_bwd_bf16(*a, s, true);
-    // dW accumulated in fp32 -- dw itself for fp32 inputs, else the workspace's tail -- from zero
+    // dW accumulated in fp32 -- dw itself when it is fp32, else the workspace's tail -- from zero
     qpam_ce_bwd_args b = *a;
     b.dw_out = 0;
     float *acc = static_cast<float *>(a->dw);
     int64_t ld = a->lddw;
-    if (a->dtype == QPAM_BF16) {
+    const bool convert = a->dw_out == 1 && a->dtype == QPAM_BF16;
+    if (convert) {
         acc = (float *)(((uintptr_t)a->workspace + bwd_ws_base<unsigned short>(b) + 255) & ~(uintptr_t)255);
         ld = a->D;
     }
@@ -1492,7 +1495,7 @@ extern "C" int qpam_ce_bwd(const qpam_ce_bwd_args *a, void *stream) {
     b.dw = acc;
     b.lddw = ld;
     st = a->dtype == QPAM_BF16 ? run_bwd<unsigned short>(b, s) : run_bwd<float>(b, s);
-    if (st || a->dtype != QPAM_BF16) return st;
+    if (st || !convert) return st;
     hipLaunchKernelGGL(dw_cast_kernel, grid, dim3(THREADS), 0, s, (const float *)acc, ld, (unsigned short *)a->dw,
                        a->lddw, (int64_t)a->V, a->D);
     return launch_status("ce dw_cast_kernel");

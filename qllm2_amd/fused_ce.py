@@ -106,8 +106,10 @@ def _(hidden_rows, weight_matrix, targets, mask, ignore_index):
 
 @torch.library.custom_op("qpam::ce_bwd", mutates_args=())
 def ce_bwd_op(hidden_rows: Tensor, weight_matrix: Tensor, targets: Tensor, mask: Optional[Tensor],
-              ignore_index: int, lse: Tensor, grad_scale: Tensor, chunk: int) -> List[Tensor]:
-    """Returns [d hidden_rows, d weight_matrix] in the input dtypes."""
+              ignore_index: int, lse: Tensor, grad_scale: Tensor, chunk: int, dw_fp32: bool = False) -> List[Tensor]:
+    """Returns [d hidden_rows, d weight_matrix] in the input dtypes (d
+    weight_matrix in fp32 with dw_fp32: the gradient of an fp32 master weight
+    whose bf16 copy is weight_matrix)."""
     h, w, dtype = _operands(hidden_rows, weight_matrix)
     targets, mask = _prep_targets(targets, mask, h.shape[0])
     dev = h.device
@@ -115,9 +117,10 @@ def ce_bwd_op(hidden_rows: Tensor, weight_matrix: Tensor, targets: Tensor, mask:
     # the weight's own dtype is the working one: the library writes dW in it (no
     # zero fill, no conversion pass); an fp32 master weight run on its bf16 copy
     # keeps the fp32 accumulation
-    write_dw = weight_matrix.dtype == w.dtype
-    dw = (torch.empty(w.shape, device=dev, dtype=w.dtype) if write_dw
-          else torch.zeros(w.shape, device=dev, dtype=torch.float32))
+    # fp32 dW written (no zero fill) for an fp32 master weight: dw_fp32, or an fp32
+    # weight_matrix run on its bf16 copy here
+    fp32_dw = dw_fp32 or weight_matrix.dtype != w.dtype
+    dw = torch.empty(w.shape, device=dev, dtype=torch.float32 if fp32_dw else w.dtype)
     gs = grad_scale.to(torch.float32).reshape(1).contiguous()
     a = _lib.CeBwdArgs()
     a.N, a.V, a.D, a.dtype = h.shape[0], w.shape[0], h.shape[1], dtype
@@ -128,19 +131,20 @@ def ce_bwd_op(hidden_rows: Tensor, weight_matrix: Tensor, targets: Tensor, mask:
     a.lse, a.grad_scale = lse.data_ptr(), gs.data_ptr()
     a.dh, a.lddh, a.dw, a.lddw = dh.data_ptr(), dh.stride(0), dw.data_ptr(), dw.stride(0)
     a.chunk = int(max(1, min(chunk, h.shape[0])))
-    a.dw_out = 1 if write_dw else 0
+    a.dw_out = 2 if fp32_dw else 1
     L = _lib.lib()
     nbytes = L.qpam_ce_bwd_workspace_size(a)
     ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
     a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
     with torch.cuda.device(dev):
         _lib.check(L.qpam_ce_bwd(a, _lib.stream_ptr(dev)), "qpam_ce_bwd")
-    return [dh.to(hidden_rows.dtype), dw.to(weight_matrix.dtype)]
+    return [dh.to(hidden_rows.dtype), dw if fp32_dw else dw.to(weight_matrix.dtype)]
 
 
 @ce_bwd_op.register_fake
-def _(hidden_rows, weight_matrix, targets, mask, ignore_index, lse, grad_scale, chunk):
-    return [torch.empty_like(hidden_rows), torch.empty_like(weight_matrix)]
+def _(hidden_rows, weight_matrix, targets, mask, ignore_index, lse, grad_scale, chunk, dw_fp32=False):
+    return [torch.empty_like(hidden_rows),
+            torch.empty_like(weight_matrix, dtype=torch.float32 if dw_fp32 else weight_matrix.dtype)]
 
 
 class _FusedLinearCE(torch.autograd.Function):
@@ -148,16 +152,20 @@ class _FusedLinearCE(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, hidden_rows, weight_matrix, targets, mask, chunk, ignore_index):
-        loss, lse, denom = ce_fwd_op(hidden_rows, weight_matrix, targets, mask, ignore_index)
-        ctx.save_for_backward(hidden_rows, weight_matrix, targets, mask, lse, denom)
-        ctx.chunk, ctx.ignore_index = chunk, ignore_index
+        # an fp32 master weight with bf16 rows: one bf16 copy serves the forward and the backward
+        master = weight_matrix.dtype == torch.float32 and hidden_rows.dtype == torch.bfloat16
+        w_op = weight_matrix.to(torch.bfloat16) if master else weight_matrix
+        loss, lse, denom = ce_fwd_op(hidden_rows, w_op, targets, mask, ignore_index)
+        ctx.save_for_backward(hidden_rows, w_op, targets, mask, lse, denom)
+        ctx.chunk, ctx.ignore_index, ctx.master = chunk, ignore_index, master
         return loss
 
     @staticmethod
     def backward(ctx, grad_output):
-        hidden_rows, weight_matrix, targets, mask, lse, denom = ctx.saved_tensors
+        hidden_rows, w_op, targets, mask, lse, denom = ctx.saved_tensors
         grad_scale = grad_output.to(torch.float32) / denom
-        dh, dw = ce_bwd_op(hidden_rows, weight_matrix, targets, mask, ctx.ignore_index, lse, grad_scale, ctx.chunk)
+        dh, dw = ce_bwd_op(hidden_rows, w_op, targets, mask, ctx.ignore_index, lse, grad_scale, ctx.chunk,
+                           ctx.master)
         return dh, dw, None, None, None, None
 
 
